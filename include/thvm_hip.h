@@ -1,0 +1,93 @@
+/*
+ * thvm_hip.h - C ABI of the MI355X (gfx950) HIP backend for TinyHVM.
+ *
+ * The drop-in is the vtable `hip_backend`, a `Backend` exactly like the
+ * engine's `cpu_backend` (src/backend/cpu/_.c:21) and `metal_backend`
+ * (src/backend/metal/_.m:30); the engine registers it from thvm_init
+ * (src/ctx/init.c:17-35). The flat thvm_hip_* functions below are the same
+ * slots under plain names, for FFI callers (ctypes) that do not walk a vtable.
+ *
+ * All calls come from one host thread in dependency order (the engine's
+ * contract, src/schedule/_.c:2005-2043). Work is enqueued on one HIP stream;
+ * only buf_read (and large buf_writes) block.
+ */
+#ifndef THVM_HIP_H
+#define THVM_HIP_H
+
+#include "thvm_abi.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* The vtable. Replaces cpu_backend / metal_backend (src/tinyhvm.h:988-1046). */
+extern Backend hip_backend;
+
+/* Backend.init / .shutdown (src/tinyhvm.h:990-991). init returns 0 on success
+ * and -1 without a usable gfx950 device (the engine then stays on the CPU,
+ * src/ctx/init.c:26-33). */
+int  thvm_hip_init(void);
+void thvm_hip_shutdown(void);
+
+/* Backend.buf_alloc (src/tinyhvm.h:994): nonzero id, 0 on failure. */
+u32  thvm_hip_buf_alloc(u64 bytes);
+/* Backend.buf_free (src/tinyhvm.h:995): idempotent. */
+void thvm_hip_buf_free(u32 id);
+/* Backend.buf_incref / buf_decref (src/tinyhvm.h:996-997). */
+void thvm_hip_buf_incref(u32 id);
+void thvm_hip_buf_decref(u32 id);
+/* Backend.buf_write (src/tinyhvm.h:1000): the host buffer may be reused on return. */
+void thvm_hip_buf_write(u32 id, const void *data, u64 bytes);
+/* Backend.buf_read (src/tinyhvm.h:1001): waits for all enqueued work. */
+void thvm_hip_buf_read(u32 id, void *out, u64 bytes);
+/* Backend.buf_read_nosync (src/tinyhvm.h:1032): serves host-written metadata
+ * without a device sync when no kernel has written the buffer since. */
+void thvm_hip_buf_read_nosync(u32 id, void *out, u64 bytes);
+
+/* Backend.dispatch_uop_kernel (src/tinyhvm.h:1027-1029), called from
+ * thvm_sched_dispatch_kernel (src/schedule/_.c:2370-2371). */
+void thvm_hip_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
+                                  const UOpKernel *kernel, u64 cache_key);
+/* Backend.dispatch_kernel_rs (src/tinyhvm.h:1020-1026), the fallback the
+ * scheduler uses when lowering fails (src/schedule/_.c:2372-2379). */
+void thvm_hip_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **leaf_views,
+                                 const ShapeTracker *const *leaf_sts, u32 n_leaves,
+                                 FusedOp *ops, u32 n_ops, const Shape *full_shape,
+                                 const ReduceSpec *reduce, u32 *side_bufs,
+                                 const u32 *side_op_indices, u32 n_side_outputs,
+                                 const u32 *leaf_dtypes, u32 out_dtype);
+/* Backend.contiguify / buf_copy (src/tinyhvm.h:1030-1031), used by ASSIGN
+ * (src/interact/tensor_ops.c:113-120). */
+void thvm_hip_contiguify(u32 dst_buf, u32 numel, u32 src_buf, const View *src_view);
+void thvm_hip_buf_copy(u32 dst_buf, u32 src_buf, u64 nbytes);
+/* Backend.pool_reset / pool_set_persistent (src/tinyhvm.h:1039-1040). */
+void thvm_hip_pool_reset(u32 keep);
+void thvm_hip_pool_set_persistent(u32 max_buf);
+/* Backend.profile_report / profile_reset (src/tinyhvm.h:1044-1045). */
+void thvm_hip_profile_report(void);
+void thvm_hip_profile_reset(void);
+
+/* ---- additions with no counterpart in the engine ---- */
+
+/* Wait for all enqueued work; returns 0, or -1 on a device error. */
+int  thvm_hip_synchronize(void);
+/* The hipStream_t all work is ordered on (for timing with events). */
+void *thvm_hip_stream(void);
+/* Device address of a buffer (for tests and timing harnesses). */
+void *thvm_hip_buf_device_ptr(u32 id);
+/* The vtable, for callers that cannot read exported data symbols. */
+const Backend *thvm_hip_backend(void);
+/* sizeof(View), sizeof(ShapeTracker), sizeof(UOpKernel), sizeof(Backend). */
+int  thvm_hip_abi_sizes(u32 *out, u32 n);
+/* Generated HIP source for a kernel (no device needed). Returns its length,
+ * or -1 with the reason in buf. mode: 0 serial, 1 group; vec: lanes per thread. */
+int  thvm_hip_kernel_source(const UOpKernel *kernel, char *buf, u64 buflen, u32 *mode, u32 *vec);
+/* Generate and compile with hipRTC for gfx950, without loading (no device
+ * needed). Returns the code-object size, or -1 with the reason in errbuf. */
+int  thvm_hip_compile_check(const UOpKernel *kernel, char *errbuf, u64 errlen);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* THVM_HIP_H */

@@ -1,0 +1,543 @@
+/*
+ * oracle.c - CPU restatement of the TinyHVM CPU backend's kernel semantics.
+ *
+ * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load this library, and only as the checker
+ * (or as the timed CPU baseline). The product path (tinyhvm_amd) never calls it.
+ *
+ * It exports a host-memory Backend vtable (`oracle_backend`) so that kernel
+ * traces can be replayed through it exactly as through the GPU backend.
+ *
+ * Functions and the reference code they restate:
+ *   ora_h2f / ora_f2h ............ src/tinyhvm.h:433-486 (f16 with the engine's
+ *                                  round-half-up on the first dropped bit)
+ *   ora_load / ora_store / cast .. src/tinyhvm.h:488-526
+ *   ora_alu ...................... src/backend/cpu/dispatch.c:5-21
+ *   ora_uop_exec / ora_dispatch_uop
+ *                                  src/backend/cpu/uop.c:3-155
+ *   ora_view_read / ora_st_read / ora_dispatch_rs
+ *                                  src/backend/cpu/dispatch.c:23-282
+ *   ora_contiguify ............... strided masked copy, src/ops/_.c:338-357
+ *   pool (alloc ids, reset) ...... src/backend/cpu/pool.c:6-26
+ *
+ * Deliberate difference from the reference: every load and store is checked
+ * against the buffer size (out-of-range loads read 0, stores are dropped).
+ * The reference reads out of range for masked pad positions and faults there
+ * (its LOAD runs before the MASK select); masked values are discarded, so the
+ * results are identical wherever the reference does not fault.
+ *
+ * Parity pins (tests/): bit-exact against the reference CPU backend's own
+ * outputs recorded in tests/golden/*.trc (SNAPSHOT records), and against
+ * closed forms in f64 for the fused, matmul, conv, pooling and softmax
+ * workloads.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "thvm_abi.h"
+
+/* ---------------- dtype helpers ---------------- */
+f32 ora_h2f(u16 h) {
+    u32 sign = ((u32)h & 0x8000u) << 16;
+    u32 ex = ((u32)h >> 10) & 0x1Fu;
+    u32 man = (u32)h & 0x03FFu;
+    u32 bits;
+    if (ex == 0) {
+        if (man == 0) bits = sign;
+        else {
+            ex = 1;
+            while ((man & 0x0400u) == 0) { man <<= 1; ex -= 1; }
+            man &= 0x03FFu;
+            bits = sign | ((ex + 127 - 15) << 23) | (man << 13);
+        }
+    } else if (ex == 0x1Fu) {
+        bits = sign | 0x7F800000u | (man << 13);
+    } else {
+        bits = sign | ((ex + 127 - 15) << 23) | (man << 13);
+    }
+    f32 out;
+    memcpy(&out, &bits, 4);
+    return out;
+}
+
+u16 ora_f2h(f32 f) {
+    u32 x;
+    memcpy(&x, &f, 4);
+    u32 sign = (x >> 16) & 0x8000u;
+    i32 ex = (i32)((x >> 23) & 0xFFu) - 127 + 15;
+    u32 man = x & 0x7FFFFFu;
+    if (ex <= 0) {
+        if (ex < -10) return (u16)sign;
+        man = (man | 0x800000u) >> (1 - ex);
+        if (man & 0x1000u) man += 0x2000u;
+        return (u16)(sign | (man >> 13));
+    }
+    if (ex >= 31) return (u16)(sign | 0x7C00u | (man ? 0x0200u : 0));
+    if (man & 0x1000u) {
+        man += 0x2000u;
+        if (man & 0x800000u) {
+            man = 0;
+            ex += 1;
+            if (ex >= 31) return (u16)(sign | 0x7C00u);
+        }
+    }
+    return (u16)(sign | ((u32)ex << 10) | (man >> 13));
+}
+
+static u32 dt_size(u32 dt) { return dt == DTYPE_F16 ? 2u : 4u; }
+
+/* Host C conversions on x86-64: the same instructions the reference build uses. */
+f32 ora_load(const void *base, u64 nbytes, u32 dt, u32 i) {
+    if (!base || (u64)i * dt_size(dt) + dt_size(dt) > nbytes) return 0.0f;
+    switch (dt) {
+    case DTYPE_F32: return ((const f32 *)base)[i];
+    case DTYPE_F16: return ora_h2f(((const u16 *)base)[i]);
+    case DTYPE_I32: return (f32)((const i32 *)base)[i];
+    case DTYPE_U32: return (f32)((const u32 *)base)[i];
+    default: return 0.0f;
+    }
+}
+
+void ora_store(void *base, u64 nbytes, u32 dt, u32 i, f32 v) {
+    if (!base || (u64)i * dt_size(dt) + dt_size(dt) > nbytes) return;
+    switch (dt) {
+    case DTYPE_F32: ((f32 *)base)[i] = v; break;
+    case DTYPE_F16: ((u16 *)base)[i] = ora_f2h(v); break;
+    case DTYPE_I32: ((i32 *)base)[i] = (i32)v; break;
+    case DTYPE_U32: ((u32 *)base)[i] = (u32)v; break;
+    default: break;
+    }
+}
+
+f32 ora_cast(f32 v, u32 dt) {
+    switch (dt) {
+    case DTYPE_F32: return v;
+    case DTYPE_F16: return ora_h2f(ora_f2h(v));
+    case DTYPE_I32: return (f32)(i32)v;
+    case DTYPE_U32: return (f32)(u32)v;
+    default: return v;
+    }
+}
+
+f32 ora_alu(u32 uop, u32 aux, f32 a, f32 b) {
+    switch (uop) {
+    case UOP_ADD: return a + b;
+    case UOP_MUL: return a * b;
+    case UOP_DIV: return b != 0.f ? a / b : 0.f;
+    case UOP_SUB: return a - b;
+    case UOP_MAX: return a > b ? a : b;
+    case UOP_CMP: return a > b ? 1.f : 0.f;
+    case UOP_NEG: return -a;
+    case UOP_RELU: return a > 0.f ? a : 0.f;
+    case UOP_EXP: return expf(a);
+    case UOP_LOG: return logf(a);
+    case UOP_SQRT: return sqrtf(a);
+    case UOP_CAST: return ora_cast(a, aux);
+    default: return a;
+    }
+}
+
+/* ---------------- KOp interpreter ---------------- */
+typedef struct {
+    const UOpKernel *k;
+    const u32 *range_end;
+    void *out;
+    u64 out_bytes;
+    const void **leaf;
+    const u64 *leaf_bytes;
+    u32 n_leaf_ptrs;
+    u32 *uv;
+    f32 *fv;
+} OraCtx;
+
+static int is_ftype(const UOpKernel *k, u32 id) {
+    if (id >= k->n_ops) return 0;
+    switch (k->ops[id].type) {
+    case KOP_CONST_F: case KOP_LOAD: case KOP_ALU: case KOP_ACC_INIT: case KOP_MASK: return 1;
+    default: return 0;
+    }
+}
+static u32 as_u(const OraCtx *c, u32 id) {
+    if (id >= c->k->n_ops) return 0;
+    return is_ftype(c->k, id) ? (u32)c->fv[id] : c->uv[id];
+}
+static f32 as_f(const OraCtx *c, u32 id) {
+    if (id >= c->k->n_ops) return 0.0f;
+    return is_ftype(c->k, id) ? c->fv[id] : (f32)c->uv[id];
+}
+
+/* Returns 0 where the reference interpreter would abandon the dispatch. */
+static int ora_uop_exec(OraCtx *c, u32 start, u32 stop, u32 gid) {
+    const UOpKernel *k = c->k;
+    for (u32 i = start; i < stop; i++) {
+        const KOp *op = &k->ops[i];
+        switch (op->type) {
+        case KOP_GID: c->uv[i] = gid; break;
+        case KOP_CONST_U: c->uv[i] = op->imm.u; break;
+        case KOP_CONST_F: c->fv[i] = op->imm.f; break;
+        case KOP_MOD: c->uv[i] = op->imm.u ? as_u(c, op->arg[0]) % op->imm.u : 0; break;
+        case KOP_DIV: c->uv[i] = op->imm.u ? as_u(c, op->arg[0]) / op->imm.u : 0; break;
+        case KOP_IDX: c->uv[i] = as_u(c, op->arg[0]) * op->imm.u + as_u(c, op->arg[1]); break;
+        case KOP_LOAD: {
+            u32 bi = op->imm.u;
+            if (bi == 0) c->fv[i] = ora_load(c->out, c->out_bytes, k->out_dtype, as_u(c, op->arg[0]));
+            else if (bi - 1 < k->n_leaves && bi - 1 < c->n_leaf_ptrs)
+                c->fv[i] = ora_load(c->leaf[bi - 1], c->leaf_bytes[bi - 1], k->leaf_dtypes[bi - 1],
+                                    as_u(c, op->arg[0]));
+            else c->fv[i] = 0.0f;
+            break;
+        }
+        case KOP_MASK: c->fv[i] = as_f(c, op->arg[0]) != 0.0f ? as_f(c, op->arg[1]) : 0.0f; break;
+        case KOP_ALU: c->fv[i] = ora_alu(op->imm.u, op->arg[2], as_f(c, op->arg[0]), as_f(c, op->arg[1])); break;
+        case KOP_ACC_INIT: c->fv[i] = op->imm.f; break;
+        case KOP_ACC: {
+            u32 a = op->arg[0];
+            f32 v = as_f(c, op->arg[1]);
+            if (a < k->n_ops) c->fv[a] = (op->imm.u == UOP_RMAX) ? (c->fv[a] > v ? c->fv[a] : v) : (c->fv[a] + v);
+            break;
+        }
+        case KOP_RANGE: {
+            u32 end = c->range_end[i];
+            if (end == 0xFFFFFFFFu || end <= i) return 0;
+            for (u32 r = 0; r < op->imm.u; r++) {
+                c->uv[i] = r;
+                if (!ora_uop_exec(c, i + 1, end, gid)) return 0;
+            }
+            i = end;
+            break;
+        }
+        case KOP_ENDRANGE: break;
+        case KOP_STORE: ora_store(c->out, c->out_bytes, k->out_dtype, as_u(c, op->arg[0]), as_f(c, op->arg[1])); break;
+        default: return 0;
+        }
+    }
+    return 1;
+}
+
+void ora_dispatch_uop(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, u32 n_leaves,
+                      const UOpKernel *k) {
+    if (!k || !out || k->n_ops > KOP_MAX) return;
+    u32 range_end[KOP_MAX], stack[KOP_MAX], sp = 0;
+    for (u32 i = 0; i < KOP_MAX; i++) range_end[i] = 0xFFFFFFFFu;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        if (k->ops[i].type == KOP_RANGE) stack[sp++] = i;
+        else if (k->ops[i].type == KOP_ENDRANGE) {
+            if (sp == 0) return;
+            range_end[stack[--sp]] = i;
+        }
+    }
+    if (sp != 0) return;
+    u32 uv[KOP_MAX];
+    f32 fv[KOP_MAX];
+    OraCtx c = {k, range_end, out, out_bytes, leaf, leaf_bytes, n_leaves, uv, fv};
+    u32 total = k->local_size > 0 ? k->grid[0] : k->grid[0] * k->grid[1] * k->grid[2];
+    for (u32 gid = 0; gid < total; gid++) {
+        memset(uv, 0, sizeof uv);
+        memset(fv, 0, sizeof fv);
+        if (!ora_uop_exec(&c, 0, k->n_ops, gid)) return;
+    }
+}
+
+/* ---------------- FusedOp interpreter ---------------- */
+static f32 ora_st_read(const void *buf, u64 nb, u32 dt, const ShapeTracker *st, const u32 *coords, u32 rank,
+                       const u32 *full_dims) {
+    if (!st || st->n_views <= 1) return 0.f;
+    u32 si = 0;
+    {
+        u32 stride = 1;
+        for (i32 d = (i32)rank - 1; d >= 0; d--) {
+            si += coords[d] * stride;
+            stride *= full_dims[d];
+        }
+    }
+    for (i32 vi = (i32)st->n_views - 2; vi >= 0; vi--) {
+        const View *vw = &st->views[vi];
+        const View *outer = &st->views[vi + 1];
+        u32 outer_flat = 0;
+        {
+            u32 udiv = 1, ostr[MAX_DIM];
+            u32 orank = outer->shape.rank < MAX_DIM ? outer->shape.rank : MAX_DIM;
+            if (orank > 0) {
+                ostr[orank - 1] = 1;
+                for (i32 d = (i32)orank - 2; d >= 0; d--) ostr[d] = ostr[d + 1] * outer->shape.dims[d + 1];
+            }
+            for (i32 d = (i32)orank - 1; d >= 0; d--) {
+                u32 dim = outer->shape.dims[d];
+                if (dim <= 1) { udiv *= dim; continue; }
+                u32 cc = udiv ? (si / udiv) % dim : 0;
+                outer_flat += cc * ostr[d];
+                udiv *= dim;
+            }
+        }
+        i32 idx = vw->offset;
+        {
+            u32 rem = outer_flat, istr[MAX_DIM];
+            u32 irank = vw->shape.rank < MAX_DIM ? vw->shape.rank : MAX_DIM;
+            if (irank > 0) {
+                istr[irank - 1] = 1;
+                for (i32 d = (i32)irank - 2; d >= 0; d--) istr[d] = istr[d + 1] * vw->shape.dims[d + 1];
+            }
+            for (u32 d = 0; d < irank; d++) {
+                u32 cc = istr[d] ? rem / istr[d] : 0;
+                rem = istr[d] ? rem % istr[d] : rem;
+                if (vw->has_mask && (cc < vw->mask_begin[d] || cc >= vw->mask_end[d])) return 0.f;
+                if (vw->strides[d] != 0) idx = (i32)((u32)idx + cc * (u32)vw->strides[d]);
+            }
+        }
+        if (idx < 0) return 0.f;
+        si = (u32)idx;
+    }
+    return ora_load(buf, nb, dt, si);
+}
+
+static f32 ora_view_read(const void *buf, u64 nb, u32 dt, const View *v, const u32 *coords, u32 rank) {
+    if (v->has_mask) {
+        for (u32 d = 0; d < rank && d < v->shape.rank; d++)
+            if (coords[d] < v->mask_begin[d] || coords[d] >= v->mask_end[d]) return 0.f;
+        for (u32 cm = 0; cm < v->n_compound_masks; cm++) {
+            u32 da = v->compound_masks[cm].dim_a, db = v->compound_masks[cm].dim_b;
+            if (da >= MAX_DIM || db >= MAX_DIM) return 0.f;
+            i32 composed = (i32)coords[da] * v->compound_masks[cm].stride_a + (i32)coords[db];
+            if (composed < (i32)v->compound_masks[cm].begin || composed >= (i32)v->compound_masks[cm].end)
+                return 0.f;
+        }
+    }
+    i32 idx = v->offset;
+    for (u32 d = 0; d < rank && d < v->shape.rank; d++) {
+        u32 dim = v->shape.dims[d];
+        u32 cc = dim ? coords[d] % dim : 0;
+        idx = (i32)((u32)idx + cc * (u32)v->strides[d]);
+    }
+    if (idx < 0) return 0.f;
+    return ora_load(buf, nb, dt, (u32)idx);
+}
+
+void ora_dispatch_rs(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, const View **views,
+                     const ShapeTracker *const *sts, u32 n_leaves, const FusedOp *ops, u32 n_ops,
+                     const Shape *full, const ReduceSpec *reduce, const u32 *leaf_dtypes, u32 out_dtype) {
+    u32 rank = full->rank ? full->rank : 1;
+    if (rank > MAX_DIM) return;
+    int has_reduce = reduce && reduce->reduce_type;
+    u32 out_numel = 1, full_numel = 1, out_shape[MAX_DIM];
+    for (u32 d = 0; d < rank; d++) {
+        full_numel *= full->dims[d];
+        out_shape[d] = (has_reduce && reduce->is_reduce[d]) ? 1 : full->dims[d];
+        out_numel *= out_shape[d];
+    }
+    if (has_reduce) {
+        f32 init = reduce->reduce_type == UOP_RMAX ? -1e30f : 0.f;
+        for (u32 i = 0; i < out_numel; i++) ora_store(out, out_bytes, out_dtype, i, init);
+    }
+    u32 fs[MAX_DIM], os[MAX_DIM];
+    fs[rank - 1] = 1;
+    os[rank - 1] = 1;
+    for (i32 d = (i32)rank - 2; d >= 0; d--) {
+        fs[d] = fs[d + 1] * full->dims[d + 1];
+        os[d] = os[d + 1] * out_shape[d + 1];
+    }
+    f32 vals[FUSE_MAX_LEAVES + FUSE_MAX_OPS];
+    memset(vals, 0, sizeof vals);
+    for (u32 flat = 0; flat < full_numel; flat++) {
+        u32 coords[MAX_DIM], rem = flat;
+        for (u32 d = 0; d < rank; d++) {
+            coords[d] = fs[d] ? rem / fs[d] : 0;
+            rem = fs[d] ? rem % fs[d] : rem;
+        }
+        for (u32 i = 0; i < n_leaves; i++) {
+            u32 dt = leaf_dtypes ? leaf_dtypes[i] : DTYPE_F32;
+            if (sts && sts[i] && sts[i]->n_views >= 2)
+                vals[i] = ora_st_read(leaf[i], leaf_bytes[i], dt, sts[i], coords, rank, full->dims);
+            else
+                vals[i] = ora_view_read(leaf[i], leaf_bytes[i], dt, views[i], coords, rank);
+        }
+        u32 en = (has_reduce && reduce->post_reduce_start) ? reduce->post_reduce_start : n_ops;
+        for (u32 i = 0; i < en; i++) {
+            u32 aa = ops[i].arg_a, bb = ops[i].arg_b;
+            if (aa >= n_leaves + en || bb >= n_leaves + en) break;
+            vals[n_leaves + i] = ora_alu(ops[i].uop, ops[i].aux, vals[aa], vals[bb]);
+        }
+        f32 result = en > 0 ? vals[n_leaves + en - 1] : vals[0];
+        if (has_reduce) {
+            u32 oi = 0;
+            for (u32 d = 0; d < rank; d++) if (!reduce->is_reduce[d]) oi += coords[d] * os[d];
+            f32 cur = ora_load(out, out_bytes, out_dtype, oi);
+            if (reduce->reduce_type == UOP_SUM) ora_store(out, out_bytes, out_dtype, oi, cur + result);
+            else if (reduce->reduce_type == UOP_RMAX) ora_store(out, out_bytes, out_dtype, oi, result > cur ? result : cur);
+        } else {
+            ora_store(out, out_bytes, out_dtype, flat, result);
+        }
+    }
+    if (has_reduce && reduce->post_reduce_start && reduce->post_reduce_start < n_ops) {
+        u32 ps = reduce->post_reduce_start;
+        u32 zero_dims[MAX_DIM] = {0};
+        const u32 LIM = FUSE_MAX_LEAVES + FUSE_MAX_OPS;
+        for (u32 oi = 0; oi < out_numel; oi++) {
+            u32 coords[MAX_DIM], rem = oi;
+            for (u32 d = 0; d < rank; d++) {
+                coords[d] = os[d] ? rem / os[d] : 0;
+                rem = os[d] ? rem % os[d] : rem;
+            }
+            f32 rr = ora_load(out, out_bytes, out_dtype, oi);
+            u32 npre = n_leaves - reduce->n_post_leaves;
+            for (u32 i = 0; i < n_leaves; i++) {
+                if (i < npre) { vals[i] = 0; continue; }
+                u32 dt = leaf_dtypes ? leaf_dtypes[i] : DTYPE_F32;
+                if (sts && sts[i] && sts[i]->n_views >= 2)
+                    vals[i] = ora_st_read(leaf[i], leaf_bytes[i], dt, sts[i], coords, rank, zero_dims);
+                else
+                    vals[i] = ora_view_read(leaf[i], leaf_bytes[i], dt, views[i], coords, rank);
+            }
+            if (ps > 0 && n_leaves + ps - 1 < LIM) vals[n_leaves + ps - 1] = rr;
+            for (u32 i = ps; i < n_ops; i++) {
+                u32 aa = ops[i].arg_a, bb = ops[i].arg_b;
+                f32 a = aa < LIM ? vals[aa] : 0.f, b = bb < LIM ? vals[bb] : 0.f;
+                vals[n_leaves + i] = ora_alu(ops[i].uop, ops[i].aux, a, b);
+            }
+            ora_store(out, out_bytes, out_dtype, oi, vals[n_leaves + n_ops - 1]);
+        }
+    }
+}
+
+void ora_contiguify(u32 *dst, u64 dst_bytes, const u32 *src, u64 src_bytes, u32 numel, const View *v) {
+    for (u32 t = 0; t < numel && (u64)t * 4 + 4 <= dst_bytes; t++) {
+        u32 rem = t, coords[MAX_DIM];
+        i32 idx = v->offset;
+        int masked = 0;
+        for (i32 d = (i32)v->shape.rank - 1; d >= 0; d--) {
+            u32 dim = v->shape.dims[d];
+            u32 cc = dim ? rem % dim : 0;
+            rem = dim ? rem / dim : 0;
+            coords[d] = cc;
+            if (v->has_mask && (cc < v->mask_begin[d] || cc >= v->mask_end[d])) masked = 1;
+            idx = (i32)((u32)idx + cc * (u32)v->strides[d]);
+        }
+        if (v->has_mask && !masked) {
+            for (u32 cm = 0; cm < v->n_compound_masks && cm < 2; cm++) {
+                u32 da = v->compound_masks[cm].dim_a, db = v->compound_masks[cm].dim_b;
+                if (da >= MAX_DIM || db >= MAX_DIM) { masked = 1; break; }
+                i32 cc = (i32)coords[da] * v->compound_masks[cm].stride_a + (i32)coords[db];
+                if (cc < (i32)v->compound_masks[cm].begin || cc >= (i32)v->compound_masks[cm].end) masked = 1;
+            }
+        }
+        dst[t] = (masked || idx < 0 || (u64)(u32)idx * 4 + 4 > src_bytes) ? 0u : src[(u32)idx];
+    }
+}
+
+/* ---------------- host-memory Backend ---------------- */
+static struct {
+    void **bufs;
+    u64 *sizes;
+    u32 cap, count;
+} OP;
+
+static int ob_init(void) {
+    free(OP.bufs);
+    free(OP.sizes);
+    OP.cap = 1024;
+    OP.bufs = calloc(OP.cap, sizeof(void *));
+    OP.sizes = calloc(OP.cap, sizeof(u64));
+    OP.count = 1;
+    return (OP.bufs && OP.sizes) ? 0 : -1;
+}
+static void ob_shutdown(void) {
+    for (u32 i = 1; i < OP.count; i++) free(OP.bufs[i]);
+    free(OP.bufs);
+    free(OP.sizes);
+    memset(&OP, 0, sizeof OP);
+}
+static u32 ob_alloc(u64 b) {
+    if (!OP.bufs && ob_init() != 0) return 0;
+    if (OP.count >= OP.cap) {
+        u32 nc = OP.cap * 2;
+        void **nb = realloc(OP.bufs, nc * sizeof(void *));
+        u64 *ns = realloc(OP.sizes, nc * sizeof(u64));
+        if (!nb || !ns) return 0;
+        memset(nb + OP.cap, 0, (nc - OP.cap) * sizeof(void *));
+        memset(ns + OP.cap, 0, (nc - OP.cap) * sizeof(u64));
+        OP.bufs = nb;
+        OP.sizes = ns;
+        OP.cap = nc;
+    }
+    u32 id = OP.count++;
+    OP.bufs[id] = calloc(1, b ? b : 4);
+    OP.sizes[id] = b;
+    return OP.bufs[id] ? id : 0;
+}
+static void *ob_ptr(u32 id) { return (id && id < OP.count) ? OP.bufs[id] : NULL; }
+static u64 ob_size(u32 id) { return (id && id < OP.count && OP.bufs[id]) ? OP.sizes[id] : 0; }
+static void ob_free(u32 id) {
+    if (id && id < OP.count) {
+        free(OP.bufs[id]);
+        OP.bufs[id] = NULL;
+        OP.sizes[id] = 0;
+    }
+}
+static void ob_write(u32 id, const void *d, u64 b) {
+    void *p = ob_ptr(id);
+    if (p && d) memcpy(p, d, b < ob_size(id) ? b : ob_size(id));
+}
+static void ob_read(u32 id, void *o, u64 b) {
+    void *p = ob_ptr(id);
+    u64 n = b < ob_size(id) ? b : ob_size(id);
+    if (p) memcpy(o, p, n);
+    if (n < b) memset((u8 *)o + n, 0, b - n);
+}
+static void ob_reset(u32 keep) {
+    u32 first = keep + 1;
+    for (u32 i = first; i < OP.count; i++) ob_free(i);
+    if (first < OP.count) OP.count = first;
+}
+static void ob_uop(u32 out, const u32 *leaves, u32 n, const UOpKernel *k, u64 key) {
+    (void)key;
+    const void *lp[FUSE_MAX_LEAVES];
+    u64 lb[FUSE_MAX_LEAVES];
+    for (u32 i = 0; i < n && i < FUSE_MAX_LEAVES; i++) {
+        lp[i] = ob_ptr(leaves[i]);
+        lb[i] = ob_size(leaves[i]);
+    }
+    ora_dispatch_uop(ob_ptr(out), ob_size(out), lp, lb, n < FUSE_MAX_LEAVES ? n : FUSE_MAX_LEAVES, k);
+}
+static void ob_rs(u32 out, u32 *leaves, const View **views, const ShapeTracker *const *sts, u32 n, FusedOp *ops,
+                  u32 n_ops, const Shape *full, const ReduceSpec *reduce, u32 *sb, const u32 *si, u32 ns,
+                  const u32 *dts, u32 odt) {
+    (void)sb; (void)si; (void)ns;
+    const void *lp[FUSE_MAX_LEAVES];
+    u64 lb[FUSE_MAX_LEAVES];
+    for (u32 i = 0; i < n && i < FUSE_MAX_LEAVES; i++) {
+        lp[i] = ob_ptr(leaves[i]);
+        lb[i] = ob_size(leaves[i]);
+    }
+    ora_dispatch_rs(ob_ptr(out), ob_size(out), lp, lb, views, sts, n, ops, n_ops, full, reduce, dts, odt);
+}
+static void ob_copy(u32 d, u32 s, u64 b) {
+    void *dp = ob_ptr(d), *sp = ob_ptr(s);
+    u64 n = b;
+    if (n > ob_size(d)) n = ob_size(d);
+    if (n > ob_size(s)) n = ob_size(s);
+    if (dp && sp) memmove(dp, sp, n);
+}
+static void ob_contig(u32 d, u32 numel, u32 s, const View *v) {
+    if (ob_ptr(d) && v) ora_contiguify(ob_ptr(d), ob_size(d), ob_ptr(s), ob_size(s), numel, v);
+}
+
+Backend oracle_backend = {
+    .init = ob_init,
+    .shutdown = ob_shutdown,
+    .buf_alloc = ob_alloc,
+    .buf_free = ob_free,
+    .buf_write = ob_write,
+    .buf_read = ob_read,
+    .buf_read_nosync = ob_read,
+    .dispatch_kernel_rs = ob_rs,
+    .dispatch_uop_kernel = ob_uop,
+    .contiguify = ob_contig,
+    .buf_copy = ob_copy,
+    .pool_reset = ob_reset,
+};
+
+const Backend *oracle_backend_ptr(void) { return &oracle_backend; }
+void *oracle_buf_ptr(u32 id) { return ob_ptr(id); }
+u64 oracle_buf_size(u32 id) { return ob_size(id); }

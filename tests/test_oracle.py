@@ -1,0 +1,72 @@
+"""The oracle (oracle/oracle.c) against the golden vectors: every SNAPSHOT in
+the committed kernel traces holds the reference CPU backend's output for the
+dispatch before it; replaying the trace through the oracle must reproduce
+them bit for bit. Plus closed-form checks that do not depend on the traces."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from tests import tracetools as tt
+from tinyhvm_amd import trace
+
+
+@pytest.mark.parametrize("path", tt.fixtures(), ids=lambda p: p.split("/")[-1])
+def test_oracle_reproduces_reference_snapshots(path):
+    ora = tt.oracle()
+    be = ora.oracle_backend_ptr()
+    be.contents.init()
+    rp = tt.Replay(path, be)
+    n_snap = 0
+    try:
+        for i in range(rp.n):
+            if rp.tag(i) == tt.TRC_SNAPSHOT:
+                tid, ref = rp.snapshot(i)
+                live = rp.live(tid)
+                p = ora.oracle_buf_ptr(live)
+                got = C.string_at(p, len(ref))
+                assert got == ref, "%s: snapshot %d differs from the reference" % (path, i)
+                n_snap += 1
+            else:
+                rp.run(i, i + 1)
+    finally:
+        rp.close()
+        be.contents.shutdown()
+    assert n_snap > 0
+
+
+def _fused_closed_form(path):
+    recs = trace.read_trace(path)
+    gens = [r for r in recs if r.tag == trace.WRITE and r.f["enc"] == trace.ENC_GEN]
+    assert len(gens) == 3
+    ups = [r for r in recs if r.tag == trace.UOP]
+    R, Cc = ups[0].f["full_dims"][:2]
+    a, b, c = [np.frombuffer(trace.gen_data(g.f["dist"], g.f["dtype"], g.f["seed"], g.f["p0"],
+                                            g.f["p1"], g.f["bytes"]), dtype=np.float32).reshape(R, Cc)
+               for g in gens]
+    snaps = [r for r in recs if r.tag == trace.SNAPSHOT]
+    return a, b, c, snaps
+
+
+@pytest.mark.parametrize("path", tt.fixtures("fused_*.trc"), ids=lambda p: p.split("/")[-1])
+def test_fused_snapshots_match_closed_form(path):
+    """y = sum(relu(a*b + c), -1) in f64 (within 1e-5 of the f32 sequential
+    sum) and dA = (a*b + c > 0) * b (exact: the mask and one f32 product)."""
+    a, b, c, snaps = _fused_closed_form(path)
+    y_ref = np.maximum(a.astype(np.float64) * b + c, 0).sum(axis=1)
+    y = np.frombuffer(snaps[0].f["data"], dtype=np.float32)
+    ok, msg = tt.close(y, y_ref, 1e-5)
+    assert ok, msg
+    pre = (a * b) + c  # f32, same two roundings as the kernel
+    da_ref = np.where(pre > 0, 1.0, 0.0).astype(np.float32) * b
+    da = np.frombuffer(snaps[1].f["data"], dtype=np.float32).reshape(a.shape)
+    assert np.array_equal(da, da_ref)
+
+
+def test_planted_mistake_is_caught():
+    """A wrong sign in the closed form must fail the same comparison."""
+    a, b, c, snaps = _fused_closed_form(tt.fixtures("fused_64x256.trc")[0])
+    y_wrong = np.maximum(a.astype(np.float64) * b - c, 0).sum(axis=1)
+    y = np.frombuffer(snaps[0].f["data"], dtype=np.float32)
+    ok, _ = tt.close(y, y_wrong, 1e-5)
+    assert not ok

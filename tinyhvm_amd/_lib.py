@@ -1,0 +1,116 @@
+"""ctypes binding of libthvm_hip.so (include/thvm_hip.h, include/thvm_replay.h).
+
+Loading fails loudly when the library has not been built: there is no CPU
+fallback behind these entry points.
+"""
+import ctypes as C
+import os
+
+from . import abi
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libthvm_hip.so")
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError("libthvm_hip.so is not built (run __graft_entry__.build() "
+                           "or python -m tinyhvm_amd.build)")
+    L = C.CDLL(LIB_PATH)
+    u32, u64, f32, vp, cp = C.c_uint32, C.c_uint64, C.c_float, C.c_void_p, C.c_char_p
+    PU32 = C.POINTER(u32)
+    sigs = {
+        "thvm_hip_init": (C.c_int, []),
+        "thvm_hip_shutdown": (None, []),
+        "thvm_hip_buf_alloc": (u32, [u64]),
+        "thvm_hip_buf_free": (None, [u32]),
+        "thvm_hip_buf_incref": (None, [u32]),
+        "thvm_hip_buf_decref": (None, [u32]),
+        "thvm_hip_buf_write": (None, [u32, vp, u64]),
+        "thvm_hip_buf_read": (None, [u32, vp, u64]),
+        "thvm_hip_buf_read_nosync": (None, [u32, vp, u64]),
+        "thvm_hip_dispatch_uop_kernel": (None, [u32, PU32, u32, C.POINTER(abi.UOpKernel), u64]),
+        "thvm_hip_dispatch_kernel_rs": (None, [u32, PU32, C.POINTER(C.POINTER(abi.View)),
+                                               C.POINTER(C.POINTER(abi.ShapeTracker)), u32,
+                                               C.POINTER(abi.FusedOp), u32, C.POINTER(abi.Shape),
+                                               C.POINTER(abi.ReduceSpec), PU32, PU32, u32, PU32,
+                                               u32]),
+        "thvm_hip_contiguify": (None, [u32, u32, u32, C.POINTER(abi.View)]),
+        "thvm_hip_buf_copy": (None, [u32, u32, u64]),
+        "thvm_hip_pool_reset": (None, [u32]),
+        "thvm_hip_pool_set_persistent": (None, [u32]),
+        "thvm_hip_profile_report": (None, []),
+        "thvm_hip_profile_reset": (None, []),
+        "thvm_hip_synchronize": (C.c_int, []),
+        "thvm_hip_stream": (vp, []),
+        "thvm_hip_buf_device_ptr": (vp, [u32]),
+        "thvm_hip_backend": (C.POINTER(abi.Backend), []),
+        "thvm_hip_abi_sizes": (C.c_int, [PU32, u32]),
+        "thvm_hip_kernel_source": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64, PU32, PU32]),
+        "thvm_hip_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
+        "thvm_trace_load": (vp, [cp]),
+        "thvm_trace_free": (None, [vp]),
+        "thvm_trace_count": (u32, [vp]),
+        "thvm_trace_tag": (u32, [vp, u32]),
+        "thvm_trace_rec_id": (u32, [vp, u32]),
+        "thvm_trace_rec_bytes": (u64, [vp, u32]),
+        "thvm_trace_rec_data": (vp, [vp, u32]),
+        "thvm_trace_rec_kernel": (C.POINTER(abi.UOpKernel), [vp, u32]),
+        "thvm_trace_find_mark": (C.c_int, [vp, cp, u32]),
+        "thvm_trace_replay": (C.c_int, [vp, C.POINTER(abi.Backend), u32, u32, u32]),
+        "thvm_trace_live_id": (u32, [vp, u32]),
+        "thvm_trace_release": (None, [vp, C.POINTER(abi.Backend)]),
+        "thvm_trace_drop_gen_cache": (None, [vp]),
+        "thvm_gen_fill_parallel": (None, [vp, u32, u32, u64, f32, f32, u64, u32]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+EXPORTED = ["hip_backend"] + [
+    "thvm_hip_init", "thvm_hip_shutdown", "thvm_hip_buf_alloc", "thvm_hip_buf_free",
+    "thvm_hip_buf_incref", "thvm_hip_buf_decref", "thvm_hip_buf_write", "thvm_hip_buf_read",
+    "thvm_hip_buf_read_nosync", "thvm_hip_dispatch_uop_kernel", "thvm_hip_dispatch_kernel_rs",
+    "thvm_hip_contiguify", "thvm_hip_buf_copy", "thvm_hip_pool_reset",
+    "thvm_hip_pool_set_persistent", "thvm_hip_profile_report", "thvm_hip_profile_reset",
+    "thvm_hip_synchronize", "thvm_hip_stream", "thvm_hip_buf_device_ptr", "thvm_hip_backend",
+    "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_compile_check",
+    "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
+    "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
+    "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",
+    "thvm_trace_drop_gen_cache", "thvm_gen_fill_parallel",
+]
+
+
+def gen_bytes(dist, dtype, seed, p0, p1, nbytes):
+    n = nbytes // 4
+    buf = (C.c_uint8 * max(nbytes, 4))()
+    lib().thvm_gen_fill_parallel(C.cast(buf, C.c_void_p), dtype, dist, seed, p0, p1, n, 0)
+    return bytes(buf)[:nbytes]
+
+
+def kernel_source(k: abi.UOpKernel):
+    buf = C.create_string_buffer(1 << 20)
+    mode, vec = C.c_uint32(), C.c_uint32()
+    n = lib().thvm_hip_kernel_source(C.byref(k), buf, len(buf), C.byref(mode), C.byref(vec))
+    text = buf.value.decode()
+    if n < 0:
+        raise ValueError(text)
+    return text, mode.value, vec.value
+
+
+def compile_check(k: abi.UOpKernel):
+    err = C.create_string_buffer(512)
+    n = lib().thvm_hip_compile_check(C.byref(k), err, len(err))
+    if n < 0:
+        raise RuntimeError(err.value.decode())
+    return n

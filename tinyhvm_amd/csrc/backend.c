@@ -1,0 +1,397 @@
+/*
+ * backend.c - the HIP Backend vtable (drop-in for cpu_backend / metal_backend,
+ * src/backend/cpu/_.c:21-35, src/backend/metal/_.m:30-57) and its dispatch.
+ *
+ * Everything runs on one device and one in-order HIP stream; the only calls
+ * that block the host are buf_read (the engine's sync point), large pageable
+ * buf_writes, and pool_reset when device memory must be returned.
+ *
+ * dispatch_uop_kernel: dense recognizers first (matmul / conv / pooling
+ * shapes routed to hand-written kernels), else the hipRTC-generated kernel
+ * for the KOp program, compiled once per program and cached.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "hipb.h"
+#include "thvm_hip.h"
+#include "kargs.h"
+
+HipbState hipb;
+
+static int env_flag(const char *name) {
+    const char *v = getenv(name);
+    return v && v[0] && strcmp(v, "0") != 0;
+}
+
+static int hb_init(void) {
+    if (hipb.initialized) return 0;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
+        (void)hipGetLastError();
+        fprintf(stderr, "tinyhvm-hip: no HIP device\n");
+        return -1;
+    }
+    memset(&hipb, 0, sizeof(hipb));
+    const char *dev = getenv("THVM_HIP_DEVICE");
+    hipb.device = dev ? atoi(dev) : 0;
+    if (hipSetDevice(hipb.device) != hipSuccess) {
+        fprintf(stderr, "tinyhvm-hip: hipSetDevice(%d) failed\n", hipb.device);
+        return -1;
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, hipb.device) == hipSuccess &&
+        strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        fprintf(stderr, "tinyhvm-hip: device is %s; kernels are built for gfx950\n", prop.gcnArchName);
+        return -1;
+    }
+    if (hipStreamCreateWithFlags(&hipb.stream, hipStreamNonBlocking) != hipSuccess) return -1;
+    hipb.sync_each = env_flag("THVM_HIP_SYNC");
+    hipb.dump_src = env_flag("THVM_HIP_DUMP");
+    hipb.no_dense = env_flag("THVM_HIP_NO_DENSE");
+    hipb.verbose = env_flag("THVM_HIP_VERBOSE");
+    if (pool_init() != 0) return -1;
+    if (rtc_init() != 0) return -1;
+    hipb.initialized = 1;
+    return 0;
+}
+
+static void hb_shutdown(void) {
+    if (!hipb.initialized) return;
+    HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    rtc_shutdown();
+    pool_shutdown();
+    HIPB_CHECK(hipStreamDestroy(hipb.stream));
+    hipb.initialized = 0;
+}
+
+static u32 hb_buf_alloc(u64 bytes) { return pool_alloc(bytes); }
+static void hb_buf_free(u32 id) { pool_free(id); }
+static void hb_buf_incref(u32 id) { pool_incref(id); }
+static void hb_buf_decref(u32 id) { pool_decref(id); }
+static void hb_buf_write(u32 id, const void *data, u64 bytes) { pool_write(id, data, bytes); }
+static void hb_buf_read(u32 id, void *out, u64 bytes) { pool_read(id, out, bytes, 0); }
+static void hb_buf_read_nosync(u32 id, void *out, u64 bytes) { pool_read(id, out, bytes, 1); }
+static void hb_mem_checkpoint(u32 *ids, u32 n) { (void)ids; (void)n; }
+static void hb_buf_mark_use(u32 id) { (void)id; }
+static void hb_pool_reset(u32 keep) { pool_reset(keep); }
+static void hb_pool_set_persistent(u32 max_buf) { pool_set_persistent(max_buf); }
+static void hb_begin_batch(void) {}
+static void hb_end_batch(void) {}
+
+static u32 dtype_bytes(u32 dt) { return dt == DTYPE_F16 ? 2u : 4u; }
+
+static u32 elem_count(u32 id, u32 dt) {
+    u64 b = pool_bytes(id);
+    u64 n = b / dtype_bytes(dt);
+    return n > 0xFFFFFFFFull ? 0xFFFFFFFFu : (u32)n;
+}
+
+int hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params) {
+    hipError_t e = hipModuleLaunchKernel(fn, gx, gy, gz, bx, 1, 1, 0, hipb.stream, params, NULL);
+    if (e != hipSuccess) {
+        fprintf(stderr, "tinyhvm-hip: launch failed: %s\n", hipGetErrorString(e));
+        return 0;
+    }
+    if (hipb.sync_each) {
+        e = hipStreamSynchronize(hipb.stream);
+        if (e != hipSuccess) {
+            fprintf(stderr, "tinyhvm-hip: kernel failed: %s\n", hipGetErrorString(e));
+            return 0;
+        }
+    }
+    return 1;
+}
+
+/* Grid for `blocks` workgroups of `bx` lanes: x holds up to 2^16 groups when
+ * the work-item count would not fit 32 bits; the kernels fold y back in. */
+static void grid_for(u64 blocks, u32 bx, u32 *gx, u32 *gy) {
+    if (blocks * bx < (1ull << 32)) {
+        *gx = (u32)blocks;
+        *gy = 1;
+    } else {
+        *gx = 65536;
+        *gy = (u32)((blocks + 65535) / 65536);
+    }
+}
+
+static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
+                                   const UOpKernel *k, u64 cache_key) {
+    (void)cache_key;
+    if (!hipb.initialized || !k) return;
+    HipbBuf *ob = pool_get(out_buf);
+    if (!ob) {
+        fprintf(stderr, "tinyhvm-hip: dispatch into unknown buffer %u\n", out_buf);
+        return;
+    }
+    hipb.n_dispatch++;
+    if (!hipb.no_dense && dense_try_dispatch(out_buf, leaf_bufs, n_leaves, k)) {
+        pool_mark_device_write(out_buf);
+        hipb.n_dense++;
+        return;
+    }
+    u64 key = uop_signature(k);
+    KCacheEntry *e = rtc_lookup(key, k);
+    if (e) hipb.n_cache_hit++;
+    else e = rtc_compile_uop(key, k);
+    if (!e) return;
+    if (e->total == 0) return;
+
+    /* kernel parameters: p0..pN (buffer pointers), then c0..cN (element counts) */
+    u32 nb = k->n_leaves + 1;
+    void *ptrs[FUSE_MAX_LEAVES + 1];
+    u32 counts[FUSE_MAX_LEAVES + 1];
+    void *params[2 * (FUSE_MAX_LEAVES + 1)];
+    ptrs[0] = ob->ptr;
+    counts[0] = elem_count(out_buf, k->out_dtype);
+    for (u32 i = 0; i < k->n_leaves; i++) {
+        void *lp = (i < n_leaves) ? pool_ptr(leaf_bufs[i]) : NULL;
+        ptrs[i + 1] = lp;
+        counts[i + 1] = lp ? elem_count(leaf_bufs[i], k->leaf_dtypes[i]) : 0u;
+    }
+    for (u32 b = 0; b < nb; b++) {
+        params[b] = &ptrs[b];
+        params[nb + b] = &counts[b];
+    }
+    u32 gx, gy;
+    if (e->mode == KG_MODE_GROUP) grid_for(e->total, e->block, &gx, &gy);
+    else grid_for((e->n_threads + e->block - 1) / e->block, e->block, &gx, &gy);
+    hipb_launch(e->fn, gx, gy, 1, e->block, params);
+    pool_mark_device_write(out_buf);
+}
+
+/* ---- dispatch_kernel_rs: static interpreter ---- */
+static void hb_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **leaf_views,
+                                  const ShapeTracker *const *leaf_sts, u32 n_leaves,
+                                  FusedOp *ops, u32 n_ops, const Shape *full_shape,
+                                  const ReduceSpec *reduce, u32 *side_bufs, const u32 *side_idx,
+                                  u32 n_side, const u32 *leaf_dtypes, u32 out_dtype) {
+    (void)side_bufs; (void)side_idx; (void)n_side;
+    if (!hipb.initialized || !full_shape) return;
+    HipbBuf *ob = pool_get(out_buf);
+    if (!ob) return;
+    if (n_leaves > FUSE_MAX_LEAVES || n_ops > FUSE_MAX_OPS || out_dtype >= DTYPE_COUNT) {
+        fprintf(stderr, "tinyhvm-hip: dispatch_kernel_rs: unsupported kernel size\n");
+        return;
+    }
+    u32 n_st = 0;
+    for (u32 i = 0; i < n_leaves; i++)
+        if (leaf_sts && leaf_sts[i] && leaf_sts[i]->n_views >= 2) n_st++;
+    size_t psize = sizeof(RsParams) + (n_st ? (n_st - 1) : 0) * sizeof(ShapeTracker);
+    RsParams *P = calloc(1, psize);
+    if (!P) return;
+    u32 rank = full_shape->rank ? full_shape->rank : 1;
+    if (rank > MAX_DIM) rank = MAX_DIM;
+    P->rank = rank;
+    P->has_reduce = (reduce && reduce->reduce_type) ? 1u : 0u;
+    P->reduce_type = P->has_reduce ? reduce->reduce_type : 0;
+    P->post_start = P->has_reduce ? reduce->post_reduce_start : 0;
+    P->n_post_leaves = P->has_reduce ? reduce->n_post_leaves : 0;
+    u32 full_numel = 1, out_numel = 1, red_numel = 1;
+    for (u32 d = 0; d < rank; d++) {
+        P->dims[d] = full_shape->dims[d];
+        P->is_reduce[d] = (P->has_reduce && reduce->is_reduce[d]) ? 1u : 0u;
+        P->out_shape[d] = P->is_reduce[d] ? 1u : full_shape->dims[d];
+        full_numel *= full_shape->dims[d];
+        out_numel *= P->out_shape[d];
+        if (P->is_reduce[d]) red_numel *= full_shape->dims[d];
+    }
+    P->full_numel = full_numel;
+    P->out_numel = out_numel;
+    P->reduce_numel = red_numel;
+    P->n_leaves = n_leaves;
+    P->n_ops = n_ops;
+    P->out_dtype = out_dtype;
+    P->out_n = elem_count(out_buf, out_dtype);
+    P->out_ptr = (u64)(uintptr_t)ob->ptr;
+    u32 si = 0;
+    for (u32 i = 0; i < n_leaves; i++) {
+        u32 dt = leaf_dtypes ? leaf_dtypes[i] : DTYPE_F32;
+        if (dt >= DTYPE_COUNT) dt = DTYPE_F32;
+        P->leaf_dtype[i] = dt;
+        void *lp = pool_ptr(leaf_bufs[i]);
+        P->leaf_ptr[i] = (u64)(uintptr_t)lp;
+        P->leaf_n[i] = lp ? elem_count(leaf_bufs[i], dt) : 0;
+        if (leaf_views && leaf_views[i]) P->views[i] = *leaf_views[i];
+        if (leaf_sts && leaf_sts[i] && leaf_sts[i]->n_views >= 2) {
+            P->sts[si] = *leaf_sts[i];
+            P->leaf_st[i] = si++;
+        } else {
+            P->leaf_st[i] = 0xFFFFFFFFu;
+        }
+    }
+    for (u32 i = 0; i < n_ops; i++) P->ops[i] = ops[i];
+
+    hipFunction_t fn = rtc_static_fn("thvm_rs");
+    u32 pbuf = pool_alloc(psize);
+    if (!fn || !pbuf) {
+        free(P);
+        if (pbuf) pool_free(pbuf);
+        return;
+    }
+    pool_write(pbuf, P, psize);
+    void *dp = pool_ptr(pbuf);
+    u32 threads = P->has_reduce ? out_numel : full_numel;
+    u32 phase0 = 0, phase1 = 1;
+    void *a0[] = {&dp, &phase0};
+    void *a1[] = {&dp, &phase1};
+    if (threads) hipb_launch(fn, (threads + 63) / 64, 1, 1, 64, a0);
+    if (P->has_reduce && P->post_start && P->post_start < n_ops && out_numel)
+        hipb_launch(fn, (out_numel + 63) / 64, 1, 1, 64, a1);
+    pool_free(pbuf);   /* stream order keeps the block alive for the kernels above */
+    pool_mark_device_write(out_buf);
+    free(P);
+    hipb.n_dispatch++;
+}
+
+static void hb_contiguify(u32 dst_buf, u32 numel, u32 src_buf, const View *src_view) {
+    if (!hipb.initialized || !src_view || numel == 0) return;
+    HipbBuf *d = pool_get(dst_buf), *s = pool_get(src_buf);
+    if (!d) return;
+    hipFunction_t fn = rtc_static_fn("thvm_contiguify");
+    if (!fn) return;
+    ContigArgs a;
+    memset(&a, 0, sizeof a);
+    a.dst = (u64)(uintptr_t)d->ptr;
+    a.dst_n = (u32)(d->bytes / 4);
+    a.src = s ? (u64)(uintptr_t)s->ptr : 0;
+    a.src_n = s ? (u32)(s->bytes / 4) : 0;
+    a.v = *src_view;
+    a.numel = numel;
+    void *params[] = {&a};
+    hipb_launch(fn, (numel + 255) / 256, 1, 1, 256, params);
+    pool_mark_device_write(dst_buf);
+}
+
+static void hb_buf_copy(u32 dst_buf, u32 src_buf, u64 nbytes) {
+    HipbBuf *d = pool_get(dst_buf), *s = pool_get(src_buf);
+    if (!d || !s || nbytes == 0) return;
+    u64 n = nbytes;
+    if (n > d->cap) n = d->cap;
+    if (n > s->cap) n = s->cap;
+    HIPB_CHECK(hipMemcpyAsync(d->ptr, s->ptr, n, hipMemcpyDeviceToDevice, hipb.stream));
+    pool_mark_device_write(dst_buf);
+}
+
+static void hb_profile_report(void) {
+    u64 live, cached, mallocs;
+    pool_stats(&live, &cached, &mallocs);
+    fprintf(stderr,
+            "tinyhvm-hip: dispatches=%llu dense=%llu compiled=%llu cache_hits=%llu "
+            "live=%.1fMB cached=%.1fMB hipMalloc=%llu\n",
+            (unsigned long long)hipb.n_dispatch, (unsigned long long)hipb.n_dense,
+            (unsigned long long)hipb.n_compile, (unsigned long long)hipb.n_cache_hit,
+            live / 1e6, cached / 1e6, (unsigned long long)mallocs);
+}
+
+static void hb_profile_reset(void) {
+    hipb.n_dispatch = hipb.n_compile = hipb.n_cache_hit = hipb.n_dense = 0;
+}
+
+Backend hip_backend = {
+    .init = hb_init,
+    .shutdown = hb_shutdown,
+    .buf_alloc = hb_buf_alloc,
+    .buf_free = hb_buf_free,
+    .buf_incref = hb_buf_incref,
+    .buf_decref = hb_buf_decref,
+    .mem_checkpoint = hb_mem_checkpoint,
+    .buf_mark_use = hb_buf_mark_use,
+    .buf_write = hb_buf_write,
+    .buf_read = hb_buf_read,
+    .op_unary = NULL,
+    .op_binary = NULL,
+    .op_mm = NULL,
+    .op_reduce = NULL,
+    .dispatch_kernel_rs = hb_dispatch_kernel_rs,
+    .dispatch_uop_kernel = hb_dispatch_uop_kernel,
+    .contiguify = hb_contiguify,
+    .buf_copy = hb_buf_copy,
+    .buf_read_nosync = hb_buf_read_nosync,
+    .adam_step = NULL,
+    .pool_reset = hb_pool_reset,
+    .pool_set_persistent = hb_pool_set_persistent,
+    .begin_batch = hb_begin_batch,
+    .end_batch = hb_end_batch,
+    .profile_report = hb_profile_report,
+    .profile_reset = hb_profile_reset,
+};
+
+/* ---- flat C entry points (same behaviour as the vtable slots) ---- */
+int  thvm_hip_init(void) { return hb_init(); }
+void thvm_hip_shutdown(void) { hb_shutdown(); }
+u32  thvm_hip_buf_alloc(u64 bytes) { return hb_buf_alloc(bytes); }
+void thvm_hip_buf_free(u32 id) { hb_buf_free(id); }
+void thvm_hip_buf_incref(u32 id) { hb_buf_incref(id); }
+void thvm_hip_buf_decref(u32 id) { hb_buf_decref(id); }
+void thvm_hip_buf_write(u32 id, const void *data, u64 bytes) { hb_buf_write(id, data, bytes); }
+void thvm_hip_buf_read(u32 id, void *out, u64 bytes) { hb_buf_read(id, out, bytes); }
+void thvm_hip_buf_read_nosync(u32 id, void *out, u64 bytes) { hb_buf_read_nosync(id, out, bytes); }
+void thvm_hip_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
+                                  const UOpKernel *k, u64 cache_key) {
+    hb_dispatch_uop_kernel(out_buf, leaf_bufs, n_leaves, k, cache_key);
+}
+void thvm_hip_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **leaf_views,
+                                 const ShapeTracker *const *leaf_sts, u32 n_leaves,
+                                 FusedOp *ops, u32 n_ops, const Shape *full_shape,
+                                 const ReduceSpec *reduce, u32 *side_bufs, const u32 *side_idx,
+                                 u32 n_side, const u32 *leaf_dtypes, u32 out_dtype) {
+    hb_dispatch_kernel_rs(out_buf, leaf_bufs, leaf_views, leaf_sts, n_leaves, ops, n_ops, full_shape,
+                          reduce, side_bufs, side_idx, n_side, leaf_dtypes, out_dtype);
+}
+void thvm_hip_contiguify(u32 dst, u32 numel, u32 src, const View *v) { hb_contiguify(dst, numel, src, v); }
+void thvm_hip_buf_copy(u32 dst, u32 src, u64 n) { hb_buf_copy(dst, src, n); }
+void thvm_hip_pool_reset(u32 keep) { hb_pool_reset(keep); }
+void thvm_hip_pool_set_persistent(u32 max_buf) { hb_pool_set_persistent(max_buf); }
+void thvm_hip_profile_report(void) { hb_profile_report(); }
+void thvm_hip_profile_reset(void) { hb_profile_reset(); }
+
+int thvm_hip_synchronize(void) {
+    if (!hipb.initialized) return -1;
+    hipError_t e = hipStreamSynchronize(hipb.stream);
+    if (e != hipSuccess) {
+        fprintf(stderr, "tinyhvm-hip: stream error: %s\n", hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+void *thvm_hip_stream(void) { return hipb.initialized ? (void *)hipb.stream : NULL; }
+void *thvm_hip_buf_device_ptr(u32 id) { return pool_ptr(id); }
+
+const Backend *thvm_hip_backend(void) { return &hip_backend; }
+
+int thvm_hip_abi_sizes(u32 *out, u32 n) {
+    u32 v[4] = {(u32)sizeof(View), (u32)sizeof(ShapeTracker), (u32)sizeof(UOpKernel), (u32)sizeof(Backend)};
+    for (u32 i = 0; i < n && i < 4; i++) out[i] = v[i];
+    return 4;
+}
+
+int thvm_hip_kernel_source(const UOpKernel *k, char *buf, u64 buflen, u32 *mode, u32 *vec) {
+    char err[256] = {0};
+    KGenResult g;
+    if (!kgen_uop(k, &g, err, sizeof err)) {
+        if (buf && buflen) snprintf(buf, buflen, "error: %s", err);
+        return -1;
+    }
+    size_t n = strlen(g.src);
+    if (buf && buflen) {
+        size_t c = n < buflen - 1 ? n : buflen - 1;
+        memcpy(buf, g.src, c);
+        buf[c] = 0;
+    }
+    if (mode) *mode = (u32)g.mode;
+    if (vec) *vec = g.vec;
+    kgen_free(&g);
+    return (int)n;
+}
+
+int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t errlen);
+
+int thvm_hip_compile_check(const UOpKernel *k, char *errbuf, u64 errlen) {
+    size_t cl = 0;
+    char err[256] = {0};
+    int ok = rtc_compile_check(k, &cl, err, sizeof err);
+    if (!ok && errbuf && errlen) snprintf(errbuf, errlen, "%s", err);
+    return ok ? (int)cl : -1;
+}

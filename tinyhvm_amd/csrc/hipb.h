@@ -1,0 +1,118 @@
+/*
+ * hipb.h - internal interfaces of the HIP backend (plain C, HIP runtime C API).
+ *
+ * Components:
+ *   pool.c     device buffer pool: u32 ids -> device blocks, size classes,
+ *              refcounts, persistent floor, pinned staging for host copies
+ *   kgen.c     KOp program analysis and HIP source generation
+ *   rtc.c      hipRTC compilation and the module cache
+ *   dense.c    recognizers that route dense UOpKernels to hand-written kernels
+ *   backend.c  the Backend vtable (hip_backend) and dispatch
+ *   replay.c   kernel-trace replay
+ */
+#ifndef HIPB_H
+#define HIPB_H
+
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <hip/hip_runtime_api.h>
+
+#include "thvm_abi.h"
+
+#define HIPB_CHECK(expr)                                                         \
+    do {                                                                         \
+        hipError_t e_ = (expr);                                                  \
+        if (e_ != hipSuccess) {                                                  \
+            fprintf(stderr, "tinyhvm-hip: %s failed: %s (%s:%d)\n", #expr,      \
+                    hipGetErrorString(e_), __FILE__, __LINE__);                  \
+        }                                                                        \
+    } while (0)
+
+/* ---------------- global state ---------------- */
+typedef struct {
+    int initialized;
+    int device;
+    hipStream_t stream;
+    int sync_each;           /* THVM_HIP_SYNC: synchronize after every dispatch */
+    int dump_src;            /* THVM_HIP_DUMP: print generated HIP source */
+    int no_dense;            /* THVM_HIP_NO_DENSE: skip dense recognizers */
+    int verbose;             /* THVM_HIP_VERBOSE */
+    u64 n_dispatch, n_compile, n_cache_hit, n_dense;
+    hipModule_t static_mod;  /* precompiled kernels */
+} HipbState;
+
+extern HipbState hipb;
+
+/* ---------------- pool ---------------- */
+typedef struct {
+    void *ptr;        /* device pointer, NULL if free */
+    u64 bytes;        /* requested bytes */
+    u64 cap;          /* capacity of the block (size class) */
+    u32 refcount;
+    u8  live;
+    u8  host_valid;   /* host mirror holds the current contents */
+    void *host_mirror;
+} HipbBuf;
+
+int   pool_init(void);
+void  pool_shutdown(void);
+u32   pool_alloc(u64 bytes);
+void  pool_free(u32 id);
+void  pool_incref(u32 id);
+void  pool_decref(u32 id);
+void  pool_reset(u32 keep);
+void  pool_set_persistent(u32 max_buf);
+HipbBuf *pool_get(u32 id);
+void *pool_ptr(u32 id);
+u64   pool_bytes(u32 id);
+void  pool_mark_device_write(u32 id);
+void  pool_write(u32 id, const void *data, u64 bytes);
+void  pool_read(u32 id, void *out, u64 bytes, int nosync);
+void  pool_stats(u64 *live_bytes, u64 *cached_bytes, u64 *n_mallocs);
+
+/* ---------------- code generation ---------------- */
+enum { KG_MODE_SERIAL = 0, KG_MODE_GROUP = 1 };
+
+typedef struct {
+    char *src;            /* generated HIP source (malloc'd) */
+    char name[32];        /* entry symbol */
+    int mode;             /* KG_MODE_* */
+    u32 vec;              /* elements per thread-vector (1 or 4) */
+    u32 block;            /* threads per workgroup */
+    u64 total;            /* serial: gids; group: outputs */
+    u64 n_threads;        /* serial: number of vector lanes (ceil(total/vec)) */
+} KGenResult;
+
+int  kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen);
+void kgen_free(KGenResult *r);
+int  kgen_validate(const UOpKernel *k, char *err, size_t errlen);
+
+/* ---------------- rtc / cache ---------------- */
+typedef struct {
+    u64 key;
+    hipModule_t mod;
+    hipFunction_t fn;
+    int mode;
+    u32 vec, block;
+    u64 total, n_threads;
+    u32 n_ops, n_leaves;
+    KOp *ops;             /* copy for collision checks */
+    u32 meta[5 + FUSE_MAX_LEAVES]; /* grid, local_size, out_dtype, leaf dtypes */
+} KCacheEntry;
+
+int  rtc_init(void);
+void rtc_shutdown(void);
+KCacheEntry *rtc_lookup(u64 key, const UOpKernel *k);
+KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k);
+hipFunction_t rtc_static_fn(const char *name);
+u64  uop_signature(const UOpKernel *k);
+
+/* ---------------- dense paths ---------------- */
+int  dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
+void dense_reset_stats(void);
+
+/* ---------------- launch helpers ---------------- */
+int  hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params);
+
+#endif /* HIPB_H */

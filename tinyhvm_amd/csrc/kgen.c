@@ -1,0 +1,948 @@
+/*
+ * kgen.c - lowers a UOpKernel (the engine's linear KOp program) to HIP source
+ * for hipRTC.
+ *
+ * Semantics follow the engine's CPU interpreter (src/backend/cpu/uop.c:1-155)
+ * and its ALU (src/backend/cpu/dispatch.c:5-21), with the storage helpers of
+ * src/tinyhvm.h:433-526:
+ *   - ops are SSA values; CONST_F, LOAD, ALU, ACC_INIT and MASK are float
+ *     valued, the rest u32 valued; a u32 value read as float is (float)u and
+ *     a float read as u32 is the x86-64 conversion (u32)(int64)trunc(f);
+ *   - index arithmetic wraps modulo 2^32, MOD/DIV by 0 give 0;
+ *   - RANGE..ENDRANGE is a loop over [0, imm); ACC folds SUM (a+b) or RMAX
+ *     (a > b ? a : b) into the accumulator op named by arg[0];
+ *   - a launch covers grid[0] outputs when local_size > 0, else the product
+ *     of the grid.
+ * Deliberate difference: every LOAD and STORE is bounds-checked against the
+ * buffer's size (out of range loads read 0, stores are dropped). The CPU
+ * interpreter reads out of range for masked pad positions; masked values are
+ * discarded by MASK, so results agree wherever the CPU does not fault.
+ *
+ * Two execution shapes:
+ *   SERIAL  one thread runs the whole program for V consecutive gids (V = 4 or
+ *           1); loops run sequentially, so SUM order matches the CPU exactly.
+ *   GROUP   (local_size > 0) one workgroup per output; the lanes split each
+ *           top-level reduce loop, keep per-lane partials, and combine them
+ *           with wavefront shuffles and LDS. SUM order differs from the CPU.
+ *
+ * Vectorization: inside the vector variable's scope (gid in SERIAL, the loop
+ * counter in GROUP) each u32 op is classified as invariant (INV), linear
+ * (value at lane v = base + v*step, with a known power-of-two alignment of
+ * base) or varying. Loads whose index is linear with step 1 and aligned to 4
+ * become one 128-bit load; linear step-1 stores become one 128-bit store.
+ * In GROUP mode, loads whose index is affine in the loop counter over the
+ * whole loop are range-checked once per workgroup and then loaded unchecked.
+ */
+#include <stdarg.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "hipb.h"
+
+/* ---------------- string builder ---------------- */
+typedef struct { char *p; size_t n, cap; } SB;
+
+static void sb_put(SB *s, const char *fmt, ...) {
+    va_list ap;
+    for (;;) {
+        size_t room = s->cap - s->n;
+        va_start(ap, fmt);
+        int w = vsnprintf(s->p ? s->p + s->n : NULL, s->p ? room : 0, fmt, ap);
+        va_end(ap);
+        if (w < 0) return;
+        if (s->p && (size_t)w < room) {
+            s->n += (size_t)w;
+            return;
+        }
+        size_t nc = s->cap ? s->cap * 2 : 16384;
+        while (nc < s->n + (size_t)w + 1) nc *= 2;
+        char *np = realloc(s->p, nc);
+        if (!np) return;
+        s->p = np;
+        s->cap = nc;
+    }
+}
+
+/* ---------------- analysis ---------------- */
+enum { K_INV = 0, K_LIN = 1, K_VAR = 2 };
+enum { G_INV = 0, G_LIN = 1, G_NOT = 2 };
+
+typedef struct {
+    u8  ft;        /* float valued */
+    u8  kind;      /* K_* w.r.t. the vector variable */
+    u32 step;      /* K_LIN: value(v) = value(0) + v*step */
+    u32 align;     /* power of two dividing value(0); 0 means "value is 0" */
+    u8  gk;        /* G_* w.r.t. the enclosing parallel loop counter */
+    u32 gs;        /* G_LIN slope */
+    u8  pure;      /* value equals the parallel loop counter */
+    i32 depth;     /* loop nesting depth at this op */
+    i32 ploop;     /* enclosing parallel (top-level) loop RANGE op, or -1 */
+    u32 end;       /* RANGE: index of its ENDRANGE */
+    u8  acc_tgt;   /* target of ACC ops inside a parallel loop */
+    u32 acc_type;  /* UOP_SUM / UOP_RMAX */
+    u8  used_after;/* referenced after its enclosing top-level loop ends */
+} OpI;
+
+typedef struct {
+    const UOpKernel *k;
+    OpI *oi;
+    int mode;
+    u32 V;
+    u32 block;
+    u32 total;
+    u32 gx;            /* GROUP: workgroups per grid row */
+    SB sb;
+    char err[256];
+} Gen;
+
+static int op_is_float(KOpType t) {
+    return t == KOP_CONST_F || t == KOP_LOAD || t == KOP_ALU || t == KOP_ACC_INIT || t == KOP_MASK;
+}
+
+static int op_nargs(KOpType t) {
+    switch (t) {
+    case KOP_MOD: case KOP_DIV: case KOP_LOAD: case KOP_ENDRANGE: return 1;
+    case KOP_IDX: case KOP_MASK: case KOP_ACC: case KOP_STORE: case KOP_ALU: return 2;
+    default: return 0;
+    }
+}
+
+static int alu_is_unary(u32 uop) {
+    return uop == UOP_NEG || uop == UOP_EXP || uop == UOP_LOG || uop == UOP_RELU ||
+           uop == UOP_CAST || uop == UOP_SQRT;
+}
+
+static u32 pow2_of(u32 x) {
+    if (x == 0) return 0; /* zero: divisible by anything */
+    return x & (~x + 1u);
+}
+static u32 align_min(u32 a, u32 b) {
+    if (a == 0) return b;
+    if (b == 0) return a;
+    return a < b ? a : b;
+}
+static u32 align_mul(u32 a, u32 s) {
+    /* alignment of (value * s) where value is divisible by a */
+    if (s == 0 || a == 0) return 0;
+    u64 r = (u64)a * (u64)pow2_of(s);
+    return r >= (1ull << 31) ? (1u << 31) : (u32)r;
+}
+
+int kgen_validate(const UOpKernel *k, char *err, size_t errlen) {
+    if (!k) { snprintf(err, errlen, "null kernel"); return 0; }
+    if (k->n_ops == 0 || k->n_ops > KOP_MAX) { snprintf(err, errlen, "bad n_ops %u", k->n_ops); return 0; }
+    if (k->n_leaves > FUSE_MAX_LEAVES) { snprintf(err, errlen, "bad n_leaves %u", k->n_leaves); return 0; }
+    if (k->out_dtype >= DTYPE_COUNT) { snprintf(err, errlen, "bad out dtype %u", k->out_dtype); return 0; }
+    for (u32 i = 0; i < k->n_leaves; i++)
+        if (k->leaf_dtypes[i] >= DTYPE_COUNT) { snprintf(err, errlen, "bad leaf dtype"); return 0; }
+    i32 stack[KOP_MAX];
+    int sp = 0;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        if (op->type <= KOP_NOOP || op->type > KOP_MASK) {
+            snprintf(err, errlen, "op %u: unsupported type %d", i, (int)op->type);
+            return 0;
+        }
+        int na = op_nargs(op->type);
+        for (int a = 0; a < na; a++) {
+            if (op->type == KOP_ENDRANGE) break;
+            if (op->arg[a] >= i) {
+                snprintf(err, errlen, "op %u: arg %d = %u is not an earlier op", i, a, op->arg[a]);
+                return 0;
+            }
+        }
+        if (op->type == KOP_ACC && k->ops[op->arg[0]].type != KOP_ACC_INIT) {
+            snprintf(err, errlen, "op %u: accumulator %u is not an ACC_INIT op", i, op->arg[0]);
+            return 0;
+        }
+        if (op->type == KOP_RANGE) stack[sp++] = (i32)i;
+        if (op->type == KOP_ENDRANGE) {
+            if (sp == 0) { snprintf(err, errlen, "op %u: ENDRANGE without RANGE", i); return 0; }
+            sp--;
+        }
+    }
+    if (sp != 0) { snprintf(err, errlen, "unterminated RANGE"); return 0; }
+    return 1;
+}
+
+/* Structure: loop ends, depths, enclosing top-level loop. */
+static void analyze_structure(Gen *g) {
+    const UOpKernel *k = g->k;
+    i32 stack[KOP_MAX];
+    int sp = 0;
+    i32 top = -1;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        OpI *o = &g->oi[i];
+        o->ft = (u8)op_is_float(k->ops[i].type);
+        o->ploop = top;
+        o->depth = sp;
+        if (k->ops[i].type == KOP_RANGE) {
+            if (sp == 0) top = (i32)i;
+            o->ploop = (sp == 0) ? (i32)i : top;
+            stack[sp++] = (i32)i;
+        } else if (k->ops[i].type == KOP_ENDRANGE) {
+            i32 r = stack[--sp];
+            g->oi[r].end = i;
+            o->depth = sp;
+            o->ploop = top;
+            if (sp == 0) top = -1;
+        }
+    }
+    /* references that escape a top-level loop */
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        int na = op_nargs(op->type);
+        if (op->type == KOP_ENDRANGE) na = 0;
+        for (int a = 0; a < na; a++) {
+            u32 j = op->arg[a];
+            i32 lj = g->oi[j].ploop;
+            if (lj >= 0 && g->oi[j].depth > 0 && (u32)lj != (u32)g->oi[i].ploop)
+                g->oi[j].used_after = 1;
+            if (lj >= 0 && (u32)lj == j && g->oi[i].ploop != lj) g->oi[j].used_after = 1;
+        }
+    }
+}
+
+/* May the top-level loops be split across the lanes of a workgroup? */
+static int group_ok(Gen *g, char *why, size_t wlen) {
+    const UOpKernel *k = g->k;
+    int n_loops = 0;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        if (k->ops[i].type != KOP_RANGE || g->oi[i].depth != 0) continue;
+        n_loops++;
+        u32 e = g->oi[i].end;
+        if (g->oi[i].used_after) { snprintf(why, wlen, "loop counter used after loop"); return 0; }
+        for (u32 j = i + 1; j < e; j++) {
+            const KOp *op = &k->ops[j];
+            if (op->type == KOP_STORE) { snprintf(why, wlen, "store inside loop"); return 0; }
+            if (g->oi[j].used_after && op->type != KOP_ACC_INIT) {
+                snprintf(why, wlen, "op %u used after its loop", j);
+                return 0;
+            }
+            if (op->type == KOP_ACC) {
+                u32 t = op->arg[0];
+                if (k->ops[t].type != KOP_ACC_INIT || t > i || g->oi[t].depth != 0) {
+                    snprintf(why, wlen, "accumulator %u not initialised outside the loop", t);
+                    return 0;
+                }
+                u32 ty = op->imm.u == UOP_RMAX ? UOP_RMAX : UOP_SUM;
+                if (g->oi[t].acc_tgt && g->oi[t].acc_type != ty) {
+                    snprintf(why, wlen, "mixed reductions on one accumulator");
+                    return 0;
+                }
+                g->oi[t].acc_tgt = 1;
+                g->oi[t].acc_type = ty;
+            }
+        }
+        /* an accumulator may only be read by its ACC ops inside the loop */
+        for (u32 j = i + 1; j < e; j++) {
+            const KOp *op = &k->ops[j];
+            int na = op_nargs(op->type);
+            if (op->type == KOP_ENDRANGE) na = 0;
+            for (int a = 0; a < na; a++) {
+                u32 t = op->arg[a];
+                if (!(op->type == KOP_ACC && a == 0) && g->oi[t].acc_tgt && t < i) {
+                    snprintf(why, wlen, "accumulator %u read inside its loop", t);
+                    return 0;
+                }
+            }
+        }
+    }
+    if (n_loops == 0) { snprintf(why, wlen, "no reduce loop"); return 0; }
+    return 1;
+}
+
+/* Vector classification. In SERIAL mode the vector variable is the gid; in
+ * GROUP mode it is the counter of the enclosing top-level loop, and ops
+ * outside top-level loops are uniform. */
+static void analyze_vector(Gen *g) {
+    const UOpKernel *k = g->k;
+    u32 V = g->V;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        OpI *o = &g->oi[i];
+        o->kind = K_VAR;
+        o->step = 0;
+        o->align = 1;
+        int inscope = (g->mode == KG_MODE_SERIAL) || (o->ploop >= 0 && o->depth > 0) ||
+                      op->type == KOP_RANGE;
+        if (g->mode == KG_MODE_GROUP && !inscope) {
+            /* uniform across the workgroup */
+            o->kind = K_INV;
+            if (op->type == KOP_CONST_U) o->align = pow2_of(op->imm.u);
+            continue;
+        }
+        if (V == 1) {
+            o->kind = K_INV;
+            if (op->type == KOP_CONST_U) o->align = pow2_of(op->imm.u);
+            continue;
+        }
+        switch (op->type) {
+        case KOP_GID:
+            if (g->mode == KG_MODE_SERIAL) { o->kind = K_LIN; o->step = 1; o->align = V; }
+            else { o->kind = K_INV; o->align = 1; }
+            break;
+        case KOP_CONST_U:
+            o->kind = K_INV; o->align = pow2_of(op->imm.u);
+            break;
+        case KOP_CONST_F:
+            o->kind = K_INV;
+            break;
+        case KOP_RANGE:
+            if (g->mode == KG_MODE_GROUP && o->depth == 0) { o->kind = K_LIN; o->step = 1; o->align = V; }
+            else { o->kind = K_INV; o->align = 1; }
+            break;
+        case KOP_IDX: {
+            const OpI *a = &g->oi[op->arg[0]], *b = &g->oi[op->arg[1]];
+            if (a->ft || b->ft) {
+                o->kind = (a->kind == K_INV && b->kind == K_INV) ? K_INV : K_VAR;
+                o->align = 1;
+                break;
+            }
+            if (a->kind == K_VAR || b->kind == K_VAR) { o->kind = K_VAR; break; }
+            u32 st = a->step * op->imm.u + b->step;
+            o->kind = st ? K_LIN : K_INV;
+            o->step = st;
+            o->align = align_min(align_mul(a->align, op->imm.u), b->align);
+            break;
+        }
+        case KOP_MOD: {
+            const OpI *a = &g->oi[op->arg[0]];
+            u32 m = op->imm.u;
+            if (m == 0) { o->kind = K_INV; o->align = 0; break; }
+            if (a->ft) { o->kind = a->kind == K_INV ? K_INV : K_VAR; break; }
+            if (a->kind == K_INV) { o->kind = K_INV; o->align = align_min(a->align, pow2_of(m)); break; }
+            if (a->kind == K_LIN && a->step == 1 && (a->align == 0 || a->align >= V) && pow2_of(m) >= V) {
+                o->kind = K_LIN; o->step = 1; o->align = align_min(a->align, pow2_of(m));
+                break;
+            }
+            o->kind = K_VAR;
+            break;
+        }
+        case KOP_DIV: {
+            const OpI *a = &g->oi[op->arg[0]];
+            u32 d = op->imm.u;
+            if (d == 0) { o->kind = K_INV; o->align = 0; break; }
+            if (a->ft) { o->kind = a->kind == K_INV ? K_INV : K_VAR; break; }
+            if (a->kind == K_INV) { o->kind = K_INV; o->align = d == 1 ? a->align : 1; break; }
+            if (d == 1) { o->kind = a->kind; o->step = a->step; o->align = a->align; break; }
+            if (a->kind == K_LIN && a->step == 1 && (a->align == 0 || a->align >= V) && pow2_of(d) >= V) {
+                o->kind = K_INV; o->align = 1;
+                break;
+            }
+            o->kind = K_VAR;
+            break;
+        }
+        case KOP_LOAD:
+            o->kind = g->oi[op->arg[0]].kind == K_INV ? K_INV : K_VAR;
+            break;
+        case KOP_MASK:
+        case KOP_ALU: {
+            const OpI *a = &g->oi[op->arg[0]], *b = &g->oi[op->arg[1]];
+            int unary = op->type == KOP_ALU && alu_is_unary(op->imm.u);
+            o->kind = (a->kind == K_INV && (unary || b->kind == K_INV)) ? K_INV : K_VAR;
+            break;
+        }
+        case KOP_ACC_INIT:
+            o->kind = (g->mode == KG_MODE_GROUP) ? K_INV : K_VAR;
+            break;
+        default:
+            o->kind = K_INV;
+            break;
+        }
+    }
+}
+
+/* Global affine analysis of u32 ops inside GROUP parallel loops, w.r.t. the
+ * loop counter over its whole range [0, trip). */
+static void analyze_global(Gen *g) {
+    const UOpKernel *k = g->k;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        OpI *o = &g->oi[i];
+        o->gk = G_NOT; o->gs = 0; o->pure = 0;
+        if (g->mode != KG_MODE_GROUP) continue;
+        int inloop = o->ploop >= 0 && o->depth > 0;
+        if (!inloop) {
+            if (op->type == KOP_RANGE && o->depth == 0) { o->gk = G_LIN; o->gs = 1; o->pure = 1; }
+            else o->gk = o->ft ? G_NOT : G_INV;
+            continue;
+        }
+        u32 trip = k->ops[o->ploop].imm.u;
+        switch (op->type) {
+        case KOP_CONST_U: case KOP_GID: o->gk = G_INV; break;
+        case KOP_RANGE: o->gk = G_NOT; break;  /* nested loop counter */
+        case KOP_IDX: {
+            const OpI *a = &g->oi[op->arg[0]], *b = &g->oi[op->arg[1]];
+            if (a->gk == G_NOT || b->gk == G_NOT) break;
+            u64 s = (u64)a->gs * op->imm.u + b->gs;
+            if (s * (u64)(trip ? trip - 1 : 0) >= (1ull << 31)) break;
+            o->gs = (u32)s;
+            o->gk = s ? G_LIN : G_INV;
+            o->pure = (a->pure && op->imm.u == 1 && b->gk == G_INV && k->ops[op->arg[1]].type == KOP_CONST_U &&
+                       k->ops[op->arg[1]].imm.u == 0) ||
+                      (b->pure && a->gk == G_INV && k->ops[op->arg[0]].type == KOP_CONST_U &&
+                       k->ops[op->arg[0]].imm.u == 0);
+            break;
+        }
+        case KOP_MOD: {
+            const OpI *a = &g->oi[op->arg[0]];
+            if (op->imm.u == 0) { o->gk = G_INV; break; }
+            if (a->gk == G_INV) { o->gk = G_INV; break; }
+            if (a->pure && op->imm.u >= trip) { o->gk = G_LIN; o->gs = 1; o->pure = 1; }
+            break;
+        }
+        case KOP_DIV: {
+            const OpI *a = &g->oi[op->arg[0]];
+            if (op->imm.u == 0) { o->gk = G_INV; break; }
+            if (a->gk == G_INV) { o->gk = G_INV; break; }
+            if (op->imm.u == 1) { o->gk = a->gk; o->gs = a->gs; o->pure = a->pure; break; }
+            if (a->pure && op->imm.u >= trip) { o->gk = G_INV; }
+            break;
+        }
+        default: break;
+        }
+    }
+}
+
+/* ---------------- expression accessors ---------------- */
+static const char *U(Gen *g, u32 j, u32 v, char *buf);
+
+static const char *Fx(Gen *g, u32 j, u32 v, char *buf) {
+    const OpI *o = &g->oi[j];
+    if (o->ft) {
+        if (o->kind == K_INV || g->V == 1) snprintf(buf, 64, "f%u", j);
+        else snprintf(buf, 64, "f%u_%u", j, v);
+    } else {
+        char t[64];
+        snprintf(buf, 96, "((float)%s)", U(g, j, v, t));
+    }
+    return buf;
+}
+
+static const char *U(Gen *g, u32 j, u32 v, char *buf) {
+    const OpI *o = &g->oi[j];
+    if (o->ft) {
+        char t[96];
+        snprintf(buf, 128, "f2u(%s)", Fx(g, j, v, t));
+        return buf;
+    }
+    if (o->kind == K_INV || g->V == 1) snprintf(buf, 64, "u%u", j);
+    else if (o->kind == K_LIN) {
+        if (v == 0) snprintf(buf, 64, "u%u", j);
+        else snprintf(buf, 64, "(u%u+%uu)", j, v * o->step);
+    } else snprintf(buf, 64, "u%u_%u", j, v);
+    return buf;
+}
+
+/* Value of u32 op j at loop counter 0 (GROUP range-check prologue). */
+static const char *G0(Gen *g, u32 j, i32 loop, char *buf) {
+    const OpI *o = &g->oi[j];
+    if ((i32)j == loop) snprintf(buf, 64, "0u");
+    else if (o->ploop == loop && o->depth > 0) snprintf(buf, 64, "g%u", j);
+    else snprintf(buf, 64, "u%u", j);
+    return buf;
+}
+
+static const char *dt_ld(u32 dt) {
+    switch (dt) {
+    case DTYPE_F16: return "ld_f16";
+    case DTYPE_I32: return "ld_i32";
+    case DTYPE_U32: return "ld_u32";
+    default: return "ld_f32";
+    }
+}
+static const char *dt_st(u32 dt) {
+    switch (dt) {
+    case DTYPE_F16: return "st_f16";
+    case DTYPE_I32: return "st_i32";
+    case DTYPE_U32: return "st_u32";
+    default: return "st_f32";
+    }
+}
+
+static void fmt_float(char *buf, f32 f) {
+    u32 bits;
+    memcpy(&bits, &f, 4);
+    snprintf(buf, 64, "__uint_as_float(0x%08xu)", bits);
+}
+
+/* Declare every op variable once, zero-initialised (the CPU interpreter
+ * clears its value arrays for each gid). */
+static void emit_decls(Gen *g) {
+    const UOpKernel *k = g->k;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const OpI *o = &g->oi[i];
+        KOpType t = k->ops[i].type;
+        if (t == KOP_ENDRANGE || t == KOP_STORE || t == KOP_ACC) continue;
+        const char *ty = o->ft ? "float" : "u32";
+        const char *z = o->ft ? "0.0f" : "0u";
+        char pf = o->ft ? 'f' : 'u';
+        if (o->kind == K_VAR && g->V > 1) {
+            sb_put(&g->sb, "  %s", ty);
+            for (u32 v = 0; v < g->V; v++) sb_put(&g->sb, "%s %c%u_%u = %s", v ? "," : "", pf, i, v, z);
+            sb_put(&g->sb, ";\n");
+        } else {
+            sb_put(&g->sb, "  %s %c%u = %s;\n", ty, pf, i, z);
+        }
+    }
+}
+
+static void emit_alu(Gen *g, const KOp *op, u32 i, u32 v) {
+    char a[128], b[128], d[64];
+    Fx(g, op->arg[0], v, a);
+    Fx(g, op->arg[1], v, b);
+    const OpI *o = &g->oi[i];
+    if (o->kind == K_VAR && g->V > 1) snprintf(d, sizeof d, "f%u_%u", i, v);
+    else snprintf(d, sizeof d, "f%u", i);
+    switch (op->imm.u) {
+    case UOP_ADD:  sb_put(&g->sb, "    %s = %s + %s;\n", d, a, b); break;
+    case UOP_SUB:  sb_put(&g->sb, "    %s = %s - %s;\n", d, a, b); break;
+    case UOP_MUL:  sb_put(&g->sb, "    %s = %s * %s;\n", d, a, b); break;
+    case UOP_DIV:  sb_put(&g->sb, "    %s = (%s != 0.0f) ? (%s / %s) : 0.0f;\n", d, b, a, b); break;
+    case UOP_MAX:  sb_put(&g->sb, "    %s = (%s > %s) ? %s : %s;\n", d, a, b, a, b); break;
+    case UOP_CMP:  sb_put(&g->sb, "    %s = (%s > %s) ? 1.0f : 0.0f;\n", d, a, b); break;
+    case UOP_NEG:  sb_put(&g->sb, "    %s = -%s;\n", d, a); break;
+    case UOP_RELU: sb_put(&g->sb, "    %s = (%s > 0.0f) ? %s : 0.0f;\n", d, a, a); break;
+    case UOP_EXP:  sb_put(&g->sb, "    %s = expf(%s);\n", d, a); break;
+    case UOP_LOG:  sb_put(&g->sb, "    %s = logf(%s);\n", d, a); break;
+    case UOP_SQRT: sb_put(&g->sb, "    %s = sqrtf(%s);\n", d, a); break;
+    case UOP_CAST: sb_put(&g->sb, "    %s = cast_f(%s, %uu);\n", d, a, op->arg[2]); break;
+    default:       sb_put(&g->sb, "    %s = %s;\n", d, a); break;
+    }
+}
+
+/* Emit one op (all vector lanes). `fast` selects unchecked loads for indices
+ * proven in range by the GROUP prologue. `ploop_active`: inside a parallel loop. */
+static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
+    const UOpKernel *k = g->k;
+    const KOp *op = &k->ops[i];
+    const OpI *o = &g->oi[i];
+    u32 V = g->V;
+    int single = (o->kind != K_VAR) || V == 1;
+    char a[128], b[128], fb[64];
+    switch (op->type) {
+    case KOP_GID:
+        if (g->mode == KG_MODE_SERIAL) sb_put(&g->sb, "    u%u = X0;\n", i);
+        else sb_put(&g->sb, "    u%u = gid;\n", i);
+        break;
+    case KOP_CONST_U:
+        sb_put(&g->sb, "    u%u = %uu;\n", i, op->imm.u);
+        break;
+    case KOP_CONST_F:
+        fmt_float(fb, op->imm.f);
+        sb_put(&g->sb, "    f%u = %s;\n", i, fb);
+        break;
+    case KOP_MOD: case KOP_DIV: case KOP_IDX: {
+        u32 nv = single ? 1 : V;
+        for (u32 v = 0; v < nv; v++) {
+            char d[32];
+            if (single) snprintf(d, sizeof d, "u%u", i);
+            else snprintf(d, sizeof d, "u%u_%u", i, v);
+            U(g, op->arg[0], v, a);
+            if (op->type == KOP_IDX) {
+                U(g, op->arg[1], v, b);
+                sb_put(&g->sb, "    %s = %s * %uu + %s;\n", d, a, op->imm.u, b);
+            } else if (op->imm.u == 0) {
+                sb_put(&g->sb, "    %s = 0u;\n", d);
+            } else {
+                sb_put(&g->sb, "    %s = %s %c %uu;\n", d, a, op->type == KOP_MOD ? '%' : '/', op->imm.u);
+            }
+        }
+        break;
+    }
+    case KOP_LOAD: {
+        u32 bi = op->imm.u;
+        if (bi > k->n_leaves) {
+            if (single) sb_put(&g->sb, "    f%u = 0.0f;\n", i);
+            else for (u32 v = 0; v < V; v++) sb_put(&g->sb, "    f%u_%u = 0.0f;\n", i, v);
+            break;
+        }
+        u32 dt = bi == 0 ? k->out_dtype : k->leaf_dtypes[bi - 1];
+        const OpI *ix = &g->oi[op->arg[0]];
+        int unchecked = fast && ix->gk != G_NOT && !ix->ft && o->depth == 1;
+        if (single) {
+            U(g, op->arg[0], 0, a);
+            if (unchecked) sb_put(&g->sb, "    f%u = %s_u(p%u, %s);\n", i, dt_ld(dt), bi, a);
+            else sb_put(&g->sb, "    f%u = %s(p%u, c%u, %s);\n", i, dt_ld(dt), bi, bi, a);
+        } else if (V == 4 && ix->kind == K_LIN && ix->step == 1 && !ix->ft &&
+                   (ix->align == 0 || ix->align % 4 == 0) && dt == DTYPE_F32) {
+            U(g, op->arg[0], 0, a);
+            if (unchecked)
+                sb_put(&g->sb, "    { float4 t_ = ld4_u(p%u, %s); f%u_0 = t_.x; f%u_1 = t_.y; f%u_2 = t_.z; f%u_3 = t_.w; }\n",
+                       bi, a, i, i, i, i);
+            else
+                sb_put(&g->sb, "    { float4 t_ = ld4(p%u, c%u, %s); f%u_0 = t_.x; f%u_1 = t_.y; f%u_2 = t_.z; f%u_3 = t_.w; }\n",
+                       bi, bi, a, i, i, i, i);
+        } else {
+            for (u32 v = 0; v < V; v++) {
+                U(g, op->arg[0], v, a);
+                if (unchecked) sb_put(&g->sb, "    f%u_%u = %s_u(p%u, %s);\n", i, v, dt_ld(dt), bi, a);
+                else sb_put(&g->sb, "    f%u_%u = %s(p%u, c%u, %s);\n", i, v, dt_ld(dt), bi, bi, a);
+            }
+        }
+        break;
+    }
+    case KOP_MASK: {
+        u32 nv = single ? 1 : V;
+        for (u32 v = 0; v < nv; v++) {
+            Fx(g, op->arg[0], v, a);
+            Fx(g, op->arg[1], v, b);
+            if (single) sb_put(&g->sb, "    f%u = (%s != 0.0f) ? %s : 0.0f;\n", i, a, b);
+            else sb_put(&g->sb, "    f%u_%u = (%s != 0.0f) ? %s : 0.0f;\n", i, v, a, b);
+        }
+        break;
+    }
+    case KOP_ALU: {
+        u32 nv = single ? 1 : V;
+        for (u32 v = 0; v < nv; v++) emit_alu(g, op, i, v);
+        break;
+    }
+    case KOP_ACC_INIT:
+        fmt_float(fb, op->imm.f);
+        if (single) sb_put(&g->sb, "    f%u = %s;\n", i, fb);
+        else for (u32 v = 0; v < V; v++) sb_put(&g->sb, "    f%u_%u = %s;\n", i, v, fb);
+        break;
+    case KOP_ACC: {
+        /* SERIAL: one accumulator per vector lane (per gid). GROUP inside a
+         * parallel loop: per-lane partials p<t>_<v>. V == 1: a single one. */
+        u32 t = op->arg[0];
+        int rmax = op->imm.u == UOP_RMAX;
+        int group = in_ploop && g->mode == KG_MODE_GROUP;
+        u32 nv = (group || g->oi[t].kind == K_VAR) ? V : 1;
+        for (u32 v = 0; v < nv; v++) {
+            char d[32];
+            if (group) snprintf(d, sizeof d, "p%u_%u", t, v);
+            else if (nv > 1) snprintf(d, sizeof d, "f%u_%u", t, v);
+            else snprintf(d, sizeof d, "f%u", t);
+            Fx(g, op->arg[1], v, a);
+            if (rmax) sb_put(&g->sb, "    %s = (%s > %s) ? %s : %s;\n", d, d, a, d, a);
+            else sb_put(&g->sb, "    %s = %s + %s;\n", d, d, a);
+        }
+        break;
+    }
+    case KOP_STORE: {
+        const OpI *ix = &g->oi[op->arg[0]];
+        if (g->mode == KG_MODE_GROUP) {
+            U(g, op->arg[0], 0, a);
+            Fx(g, op->arg[1], 0, b);
+            sb_put(&g->sb, "    if (lane == 0) %s(p0, c0, %s, %s);\n", dt_st(k->out_dtype), a, b);
+            break;
+        }
+        if (V == 4 && ix->kind == K_LIN && ix->step == 1 && !ix->ft &&
+            (ix->align == 0 || ix->align % 4 == 0) && k->out_dtype == DTYPE_F32) {
+            char b1[128], b2[128], b3[128];
+            U(g, op->arg[0], 0, a);
+            Fx(g, op->arg[1], 0, b);
+            Fx(g, op->arg[1], 1, b1);
+            Fx(g, op->arg[1], 2, b2);
+            Fx(g, op->arg[1], 3, b3);
+            sb_put(&g->sb, "    if (X0 + 3u < TOTAL) st4(p0, c0, %s, make_float4(%s, %s, %s, %s));\n", a, b, b1, b2, b3);
+            sb_put(&g->sb, "    else {\n");
+            for (u32 v = 0; v < V; v++) {
+                U(g, op->arg[0], v, a);
+                Fx(g, op->arg[1], v, b);
+                sb_put(&g->sb, "      if (X0 + %uu < TOTAL) %s(p0, c0, %s, %s);\n", v, dt_st(k->out_dtype), a, b);
+            }
+            sb_put(&g->sb, "    }\n");
+        } else {
+            for (u32 v = 0; v < V; v++) {
+                U(g, op->arg[0], v, a);
+                Fx(g, op->arg[1], v, b);
+                sb_put(&g->sb, "    if (X0 + %uu < TOTAL) %s(p0, c0, %s, %s);\n", v, dt_st(k->out_dtype), a, b);
+            }
+        }
+        break;
+    }
+    default:
+        break;
+    }
+}
+
+/* Emit ops [lo, hi) sequentially; nested RANGEs become sequential loops. */
+static void emit_range_seq(Gen *g, u32 lo, u32 hi, int fast, int in_ploop);
+
+static void emit_seq_loop(Gen *g, u32 r, int fast, int in_ploop) {
+    const KOp *op = &g->k->ops[r];
+    u32 e = g->oi[r].end;
+    sb_put(&g->sb, "    for (u32 r%u = 0u; r%u < %uu; r%u++) {\n    u%u = r%u;\n", r, r, op->imm.u, r, r, r);
+    emit_range_seq(g, r + 1, e, fast, in_ploop);
+    sb_put(&g->sb, "    }\n");
+}
+
+static void emit_range_seq(Gen *g, u32 lo, u32 hi, int fast, int in_ploop) {
+    for (u32 i = lo; i < hi; i++) {
+        const KOp *op = &g->k->ops[i];
+        if (op->type == KOP_RANGE) {
+            emit_seq_loop(g, i, fast, in_ploop);
+            i = g->oi[i].end;
+            continue;
+        }
+        if (op->type == KOP_ENDRANGE) continue;
+        emit_op(g, i, fast, in_ploop);
+    }
+}
+
+static const char *PRELUDE =
+"typedef unsigned int u32;\n"
+"typedef unsigned short u16;\n"
+"/* f16 decode (exact) */\n"
+"__device__ __forceinline__ float h2f(u32 h) {\n"
+"  u32 sign = (h & 0x8000u) << 16, ex = (h >> 10) & 0x1Fu, man = h & 0x3FFu, bits;\n"
+"  if (ex == 0u) {\n"
+"    if (man == 0u) bits = sign;\n"
+"    else { ex = 1u; while ((man & 0x400u) == 0u) { man <<= 1; ex -= 1u; } man &= 0x3FFu;\n"
+"           bits = sign | ((ex + 112u) << 23) | (man << 13); }\n"
+"  } else if (ex == 0x1Fu) bits = sign | 0x7F800000u | (man << 13);\n"
+"  else bits = sign | ((ex + 112u) << 23) | (man << 13);\n"
+"  return __uint_as_float(bits);\n"
+"}\n"
+"/* f16 encode: round half up on the first dropped bit (engine rule) */\n"
+"__device__ __forceinline__ u32 f2h(float f) {\n"
+"  u32 x = __float_as_uint(f), sign = (x >> 16) & 0x8000u, man = x & 0x7FFFFFu;\n"
+"  int ex = (int)((x >> 23) & 0xFFu) - 112;\n"
+"  if (ex <= 0) { if (ex < -10) return sign; man = (man | 0x800000u) >> (1 - ex);\n"
+"                 if (man & 0x1000u) man += 0x2000u; return sign | (man >> 13); }\n"
+"  if (ex >= 31) return sign | 0x7C00u | (man ? 0x200u : 0u);\n"
+"  if (man & 0x1000u) { man += 0x2000u; if (man & 0x800000u) { man = 0u; ex += 1; if (ex >= 31) return sign | 0x7C00u; } }\n"
+"  return sign | ((u32)ex << 10) | (man >> 13);\n"
+"}\n"
+"/* x86-64 conversions: (u32)f goes through a 64-bit truncation; (i32)f gives INT_MIN out of range */\n"
+"__device__ __forceinline__ u32 f2u(float f) {\n"
+"  if (!(fabsf(f) < 9.2233720368547758e18f)) return 0u;\n"
+"  return (u32)(unsigned long long)(long long)f;\n"
+"}\n"
+"__device__ __forceinline__ int f2i(float f) {\n"
+"  if (!(f >= -2147483648.0f && f < 2147483648.0f)) return (int)0x80000000u;\n"
+"  return (int)f;\n"
+"}\n"
+"__device__ __forceinline__ float cast_f(float v, u32 dt) {\n"
+"  if (dt == 1u) return h2f(f2h(v));\n"
+"  if (dt == 2u) return (float)f2i(v);\n"
+"  if (dt == 3u) return (float)f2u(v);\n"
+"  return v;\n"
+"}\n"
+"__device__ __forceinline__ float ld_f32(const char* p, u32 n, u32 i) { return i < n ? ((const float*)p)[i] : 0.0f; }\n"
+"__device__ __forceinline__ float ld_f16(const char* p, u32 n, u32 i) { return i < n ? h2f(((const u16*)p)[i]) : 0.0f; }\n"
+"__device__ __forceinline__ float ld_i32(const char* p, u32 n, u32 i) { return i < n ? (float)((const int*)p)[i] : 0.0f; }\n"
+"__device__ __forceinline__ float ld_u32(const char* p, u32 n, u32 i) { return i < n ? (float)((const u32*)p)[i] : 0.0f; }\n"
+"__device__ __forceinline__ float ld_f32_u(const char* p, u32 i) { return ((const float*)p)[i]; }\n"
+"__device__ __forceinline__ float ld_f16_u(const char* p, u32 i) { return h2f(((const u16*)p)[i]); }\n"
+"__device__ __forceinline__ float ld_i32_u(const char* p, u32 i) { return (float)((const int*)p)[i]; }\n"
+"__device__ __forceinline__ float ld_u32_u(const char* p, u32 i) { return (float)((const u32*)p)[i]; }\n"
+"__device__ __forceinline__ float4 ld4_u(const char* p, u32 i) { return *(const float4*)((const float*)p + i); }\n"
+"__device__ __forceinline__ float4 ld4(const char* p, u32 n, u32 i) {\n"
+"  if (i + 3u < n && i + 3u >= i) return *(const float4*)((const float*)p + i);\n"
+"  return make_float4(ld_f32(p, n, i), ld_f32(p, n, i + 1u), ld_f32(p, n, i + 2u), ld_f32(p, n, i + 3u));\n"
+"}\n"
+"__device__ __forceinline__ void st_f32(char* p, u32 n, u32 i, float v) { if (i < n) ((float*)p)[i] = v; }\n"
+"__device__ __forceinline__ void st_f16(char* p, u32 n, u32 i, float v) { if (i < n) ((u16*)p)[i] = (u16)f2h(v); }\n"
+"__device__ __forceinline__ void st_i32(char* p, u32 n, u32 i, float v) { if (i < n) ((int*)p)[i] = f2i(v); }\n"
+"__device__ __forceinline__ void st_u32(char* p, u32 n, u32 i, float v) { if (i < n) ((u32*)p)[i] = f2u(v); }\n"
+"__device__ __forceinline__ void st4(char* p, u32 n, u32 i, float4 v) {\n"
+"  if (i + 3u < n && i + 3u >= i) { *(float4*)((float*)p + i) = v; return; }\n"
+"  st_f32(p, n, i, v.x); st_f32(p, n, i + 1u, v.y); st_f32(p, n, i + 2u, v.z); st_f32(p, n, i + 3u, v.w);\n"
+"}\n"
+"__device__ __forceinline__ float wsum(float x) {\n"
+"  for (int o = 32; o > 0; o >>= 1) x = x + __shfl_xor(x, o, 64);\n"
+"  return x;\n"
+"}\n"
+"__device__ __forceinline__ float wmax(float x) {\n"
+"  for (int o = 32; o > 0; o >>= 1) { float y = __shfl_xor(x, o, 64); x = (x > y) ? x : y; }\n"
+"  return x;\n"
+"}\n"
+"__device__ __forceinline__ float bsum(float x, float* red) {\n"
+"  x = wsum(x);\n"
+"  __syncthreads();\n"
+"  if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = x;\n"
+"  __syncthreads();\n"
+"  float s = red[0];\n"
+"  for (u32 w = 1u; w < (blockDim.x >> 6); w++) s = s + red[w];\n"
+"  return s;\n"
+"}\n"
+"__device__ __forceinline__ float bmax(float x, float* red) {\n"
+"  x = wmax(x);\n"
+"  __syncthreads();\n"
+"  if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = x;\n"
+"  __syncthreads();\n"
+"  float s = red[0];\n"
+"  for (u32 w = 1u; w < (blockDim.x >> 6); w++) { float y = red[w]; s = (s > y) ? s : y; }\n"
+"  return s;\n"
+"}\n";
+
+static void emit_params(Gen *g) {
+    u32 nb = g->k->n_leaves + 1;
+    for (u32 b = 0; b < nb; b++) sb_put(&g->sb, "%schar* p%u", b ? ", " : "", b);
+    for (u32 b = 0; b < nb; b++) sb_put(&g->sb, ", u32 c%u", b);
+}
+
+/* One parallel loop of GROUP mode. */
+static void emit_group_loop(Gen *g, u32 r) {
+    const UOpKernel *k = g->k;
+    u32 e = g->oi[r].end;
+    u32 trip = k->ops[r].imm.u;
+    u32 V = g->V;
+    char a[128], b[128];
+    sb_put(&g->sb, "  {\n");
+    /* partials */
+    for (u32 t = 0; t < r; t++) {
+        if (!g->oi[t].acc_tgt) continue;
+        int used = 0;
+        for (u32 j = r + 1; j < e; j++)
+            if (k->ops[j].type == KOP_ACC && k->ops[j].arg[0] == t) used = 1;
+        if (!used) continue;
+        for (u32 v = 0; v < V; v++) {
+            if (g->oi[t].acc_type == UOP_RMAX) sb_put(&g->sb, "    float p%u_%u = f%u;\n", t, v, t);
+            else sb_put(&g->sb, "    float p%u_%u = 0.0f;\n", t, v);
+        }
+    }
+    /* prologue: index values at counter 0 and the one-time range check */
+    sb_put(&g->sb, "    bool ok_ = true;\n");
+    for (u32 j = r + 1; j < e; j++) {
+        const OpI *o = &g->oi[j];
+        const KOp *op = &k->ops[j];
+        if (o->ft || o->gk == G_NOT || o->depth != 1) continue;
+        if (op->type == KOP_CONST_U) { sb_put(&g->sb, "    const u32 g%u = %uu;\n", j, op->imm.u); continue; }
+        if (op->type == KOP_GID) { sb_put(&g->sb, "    const u32 g%u = gid;\n", j); continue; }
+        G0(g, op->arg[0], (i32)r, a);
+        if (op->type == KOP_IDX) {
+            G0(g, op->arg[1], (i32)r, b);
+            sb_put(&g->sb, "    const u32 g%u = %s * %uu + %s;\n", j, a, op->imm.u, b);
+        } else if (op->imm.u == 0) {
+            sb_put(&g->sb, "    const u32 g%u = 0u;\n", j);
+        } else {
+            sb_put(&g->sb, "    const u32 g%u = %s %c %uu;\n", j, a, op->type == KOP_MOD ? '%' : '/', op->imm.u);
+        }
+    }
+    for (u32 j = r + 1; j < e; j++) {
+        const KOp *op = &k->ops[j];
+        if (op->type != KOP_LOAD || g->oi[j].depth != 1) continue;
+        const OpI *ix = &g->oi[op->arg[0]];
+        if (ix->ft || ix->gk == G_NOT) continue;
+        u32 bi = op->imm.u;
+        if (bi > k->n_leaves) continue;
+        char gv[64];
+        G0(g, op->arg[0], (i32)r, gv);
+        u64 span = (u64)ix->gs * (u64)(trip ? trip - 1 : 0);
+        sb_put(&g->sb, "    ok_ = ok_ && (%s + %lluu >= %s) && (%s + %lluu < c%u);\n", gv,
+               (unsigned long long)span, gv, gv, (unsigned long long)span, bi);
+    }
+    u32 nq = trip / V;
+    for (int pass = 0; pass < 2; pass++) {
+        sb_put(&g->sb, pass == 0 ? "    if (ok_) {\n" : "    } else {\n");
+        sb_put(&g->sb, "    for (u32 q_ = lane; q_ < %uu; q_ += %uu) {\n    u%u = q_ * %uu;\n", nq, g->block, r, V);
+        emit_range_seq(g, r + 1, e, pass == 0, 1);
+        sb_put(&g->sb, "    }\n");
+    }
+    sb_put(&g->sb, "    }\n");
+    /* combine partials across the workgroup */
+    for (u32 t = 0; t < r; t++) {
+        if (!g->oi[t].acc_tgt) continue;
+        int used = 0;
+        for (u32 j = r + 1; j < e; j++)
+            if (k->ops[j].type == KOP_ACC && k->ops[j].arg[0] == t) used = 1;
+        if (!used) continue;
+        if (g->oi[t].acc_type == UOP_RMAX) {
+            sb_put(&g->sb, "    { float t_ = p%u_0;\n", t);
+            for (u32 v = 1; v < V; v++) sb_put(&g->sb, "      t_ = (t_ > p%u_%u) ? t_ : p%u_%u;\n", t, v, t, v);
+            sb_put(&g->sb, "      f%u = bmax(t_, red_); }\n", t);
+        } else {
+            if (V == 4) sb_put(&g->sb, "    { float t_ = (p%u_0 + p%u_1) + (p%u_2 + p%u_3);\n", t, t, t, t);
+            else {
+                sb_put(&g->sb, "    { float t_ = p%u_0;\n", t);
+                for (u32 v = 1; v < V; v++) sb_put(&g->sb, "      t_ = t_ + p%u_%u;\n", t, v);
+            }
+            sb_put(&g->sb, "      f%u = f%u + bsum(t_, red_); }\n", t, t);
+        }
+    }
+    sb_put(&g->sb, "  }\n");
+}
+
+int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
+    memset(out, 0, sizeof(*out));
+    if (!kgen_validate(k, err, errlen)) return 0;
+    Gen G;
+    memset(&G, 0, sizeof(G));
+    G.k = k;
+    G.oi = calloc(k->n_ops, sizeof(OpI));
+    if (!G.oi) { snprintf(err, errlen, "oom"); return 0; }
+    analyze_structure(&G);
+
+    u32 total = k->local_size > 0 ? k->grid[0] : k->grid[0] * k->grid[1] * k->grid[2];
+    G.total = total;
+    char why[128] = {0};
+    G.mode = KG_MODE_SERIAL;
+    if (k->local_size > 0 && group_ok(&G, why, sizeof why)) G.mode = KG_MODE_GROUP;
+    if (G.mode == KG_MODE_SERIAL) {
+        for (u32 i = 0; i < k->n_ops; i++) { G.oi[i].acc_tgt = 0; G.oi[i].acc_type = 0; }
+    }
+
+    if (G.mode == KG_MODE_GROUP) {
+        u32 min_trip = 0xFFFFFFFFu;
+        int all4 = 1;
+        for (u32 i = 0; i < k->n_ops; i++) {
+            if (k->ops[i].type == KOP_RANGE && G.oi[i].depth == 0) {
+                u32 t = k->ops[i].imm.u;
+                if (t < min_trip) min_trip = t;
+                if (t % 4 != 0) all4 = 0;
+            }
+        }
+        G.V = (all4 && min_trip >= 64) ? 4 : 1;
+        u32 nq = min_trip / G.V;
+        G.block = 64;
+        while (G.block < 256 && G.block < nq) G.block *= 2;
+    } else {
+        G.V = (total >= 1024 && k->n_ops <= 256) ? 4 : 1;
+        G.block = 256;
+    }
+    analyze_vector(&G);
+    analyze_global(&G);
+
+    SB *s = &G.sb;
+    sb_put(s, "%s\n", PRELUDE);
+    snprintf(out->name, sizeof out->name, "thvm_k");
+    sb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void thvm_k(", G.block);
+    emit_params(&G);
+    sb_put(s, ") {\n");
+    if (G.mode == KG_MODE_SERIAL) {
+        u64 nthreads = ((u64)total + G.V - 1) / G.V;
+        sb_put(s, "  const u32 TOTAL = %uu;\n", total);
+        sb_put(s, "  const unsigned long long t_ = ((unsigned long long)blockIdx.y * gridDim.x + blockIdx.x) * %uull + threadIdx.x;\n", G.block);
+        sb_put(s, "  if (t_ >= %lluull) return;\n", (unsigned long long)nthreads);
+        sb_put(s, "  const u32 X0 = (u32)t_ * %uu;\n", G.V);
+        emit_decls(&G);
+        emit_range_seq(&G, 0, k->n_ops, 0, 0);
+        out->n_threads = nthreads;
+    } else {
+        sb_put(s, "  const u32 gid = blockIdx.y * gridDim.x + blockIdx.x;\n");
+        sb_put(s, "  if (gid >= %uu) return;\n", total);
+        sb_put(s, "  const u32 lane = threadIdx.x;\n");
+        sb_put(s, "  __shared__ float red_[%u];\n", G.block / 64);
+        emit_decls(&G);
+        for (u32 i = 0; i < k->n_ops; i++) {
+            const KOp *op = &k->ops[i];
+            if (op->type == KOP_RANGE && G.oi[i].depth == 0) {
+                emit_group_loop(&G, i);
+                i = G.oi[i].end;
+                continue;
+            }
+            if (op->type == KOP_ENDRANGE) continue;
+            emit_op(&G, i, 0, 0);
+        }
+        out->n_threads = total;
+    }
+    sb_put(s, "}\n");
+    free(G.oi);
+    if (!s->p) { snprintf(err, errlen, "oom"); return 0; }
+    out->src = s->p;
+    out->mode = G.mode;
+    out->vec = G.V;
+    out->block = G.block;
+    out->total = total;
+    return 1;
+}
+
+void kgen_free(KGenResult *r) {
+    if (r && r->src) free(r->src);
+    if (r) r->src = NULL;
+}

@@ -1,0 +1,310 @@
+/*
+ * pool.c - device buffer pool behind the Backend buffer slots.
+ *
+ * Contract (src/tinyhvm.h:992-1000, CPU pool src/backend/cpu/pool.c:6-26,
+ * Metal pool src/backend/metal/pool.m:46-223):
+ *   - ids are nonzero u32, handed out in increasing order; 0 means failure;
+ *   - buf_free may be called repeatedly for the same id (views alias ids);
+ *   - pool_reset(keep) releases ids >= keep+1 and restarts numbering there;
+ *   - decref on an id at or below the persistent floor is ignored.
+ *
+ * Device memory: every block comes from hipMalloc in a size class (256 B,
+ * then quarter-power-of-two steps) and returns to its class free list when
+ * its id dies. All device work is ordered on one stream, so a block freed
+ * by the host may be handed to a later dispatch without waiting: the stream
+ * orders the old readers before the new writer.
+ *
+ * Host copies: writes up to one staging segment go through a pinned ring
+ * (memcpy, then an async copy on the stream), so buf_write returns as soon as
+ * the caller's memory has been consumed and never blocks on the GPU unless
+ * the ring wraps onto a segment still in flight. Small writes also keep a
+ * host mirror that buf_read_nosync serves until a kernel writes the buffer.
+ */
+#include <stdlib.h>
+#include <string.h>
+
+#include "hipb.h"
+
+#define POOL_MIN_CLASS_BYTES 256ull
+#define POOL_N_CLASSES 256
+#define POOL_MIRROR_MAX 4096ull
+#define STAGE_SEGMENTS 4
+#define STAGE_SEG_BYTES (16ull << 20)
+
+typedef struct {
+    void **ptrs;
+    u32 n, cap;
+} FreeList;
+
+static struct {
+    HipbBuf *bufs;
+    u32 cap;
+    u32 count;            /* next id */
+    u32 persistent_floor;
+    FreeList free[POOL_N_CLASSES];
+    u64 live_bytes, cached_bytes, n_mallocs;
+    /* pinned staging ring */
+    u8 *stage;
+    hipEvent_t seg_done[STAGE_SEGMENTS];
+    u8 seg_pending[STAGE_SEGMENTS];
+    u32 seg;
+    u64 seg_off;
+} P;
+
+/* Size class of a byte count: 256 B minimum, then 4 classes per octave. */
+static u32 size_class(u64 bytes, u64 *cap_out) {
+    if (bytes <= POOL_MIN_CLASS_BYTES) {
+        *cap_out = POOL_MIN_CLASS_BYTES;
+        return 0;
+    }
+    u32 lg = 63 - (u32)__builtin_clzll(bytes - 1);   /* 2^lg < bytes <= 2^(lg+1) */
+    u64 base = 1ull << lg;
+    u64 quarter = base >> 2;
+    u32 sub = (u32)((bytes - base + quarter - 1) / quarter); /* 1..4 */
+    *cap_out = base + (u64)sub * quarter;
+    u32 c = (lg - 8) * 4 + sub;
+    return c < POOL_N_CLASSES ? c : POOL_N_CLASSES - 1;
+}
+
+static int fl_push(FreeList *f, void *p) {
+    if (f->n == f->cap) {
+        u32 nc = f->cap ? f->cap * 2 : 16;
+        void **np = realloc(f->ptrs, nc * sizeof(void *));
+        if (!np) return 0;
+        f->ptrs = np;
+        f->cap = nc;
+    }
+    f->ptrs[f->n++] = p;
+    return 1;
+}
+
+static void release_cache(void) {
+    HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    for (u32 c = 0; c < POOL_N_CLASSES; c++) {
+        for (u32 i = 0; i < P.free[c].n; i++) HIPB_CHECK(hipFree(P.free[c].ptrs[i]));
+        P.free[c].n = 0;
+    }
+    P.cached_bytes = 0;
+}
+
+int pool_init(void) {
+    memset(&P, 0, sizeof(P));
+    P.cap = 1024;
+    P.bufs = calloc(P.cap, sizeof(HipbBuf));
+    if (!P.bufs) return -1;
+    P.count = 1;
+    if (hipHostMalloc((void **)&P.stage, STAGE_SEGMENTS * STAGE_SEG_BYTES, 0) != hipSuccess) {
+        fprintf(stderr, "tinyhvm-hip: pinned staging allocation failed\n");
+        P.stage = NULL;
+        return -1;
+    }
+    for (u32 s = 0; s < STAGE_SEGMENTS; s++) {
+        if (hipEventCreateWithFlags(&P.seg_done[s], hipEventDisableTiming) != hipSuccess) return -1;
+    }
+    return 0;
+}
+
+void pool_shutdown(void) {
+    if (!P.bufs) return;
+    HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    for (u32 i = 1; i < P.count; i++) {
+        if (P.bufs[i].live && P.bufs[i].ptr) HIPB_CHECK(hipFree(P.bufs[i].ptr));
+        free(P.bufs[i].host_mirror);
+    }
+    release_cache();
+    for (u32 c = 0; c < POOL_N_CLASSES; c++) free(P.free[c].ptrs);
+    for (u32 s = 0; s < STAGE_SEGMENTS; s++) HIPB_CHECK(hipEventDestroy(P.seg_done[s]));
+    if (P.stage) HIPB_CHECK(hipHostFree(P.stage));
+    free(P.bufs);
+    memset(&P, 0, sizeof(P));
+}
+
+static int ensure_cap(u32 id) {
+    if (id < P.cap) return 1;
+    u32 nc = P.cap;
+    while (nc <= id) nc *= 2;
+    HipbBuf *nb = realloc(P.bufs, (size_t)nc * sizeof(HipbBuf));
+    if (!nb) return 0;
+    memset(nb + P.cap, 0, (size_t)(nc - P.cap) * sizeof(HipbBuf));
+    P.bufs = nb;
+    P.cap = nc;
+    return 1;
+}
+
+u32 pool_alloc(u64 bytes) {
+    if (!hipb.initialized) return 0;
+    u64 cap = 0;
+    u32 c = size_class(bytes ? bytes : 4, &cap);
+    void *ptr = NULL;
+    if (P.free[c].n > 0) {
+        ptr = P.free[c].ptrs[--P.free[c].n];
+        P.cached_bytes -= cap;
+    } else {
+        if (hipMalloc(&ptr, cap) != hipSuccess) {
+            (void)hipGetLastError();
+            release_cache();
+            if (hipMalloc(&ptr, cap) != hipSuccess) {
+                (void)hipGetLastError();
+                fprintf(stderr, "tinyhvm-hip: out of device memory (%llu bytes)\n",
+                        (unsigned long long)cap);
+                return 0;
+            }
+        }
+        P.n_mallocs++;
+    }
+    u32 id = P.count;
+    if (!ensure_cap(id)) {
+        fl_push(&P.free[c], ptr);
+        P.cached_bytes += cap;
+        return 0;
+    }
+    P.count++;
+    HipbBuf *b = &P.bufs[id];
+    free(b->host_mirror);
+    memset(b, 0, sizeof(*b));
+    b->ptr = ptr;
+    b->bytes = bytes;
+    b->cap = cap;
+    b->refcount = 1;
+    b->live = 1;
+    P.live_bytes += cap;
+    return id;
+}
+
+static void release_block(HipbBuf *b) {
+    u64 cap = 0;
+    u32 c = size_class(b->cap, &cap);
+    if (fl_push(&P.free[c], b->ptr)) {
+        P.cached_bytes += b->cap;
+    } else {
+        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+        HIPB_CHECK(hipFree(b->ptr));
+    }
+    P.live_bytes -= b->cap;
+    b->ptr = NULL;
+    b->live = 0;
+    b->refcount = 0;
+    b->host_valid = 0;
+    free(b->host_mirror);
+    b->host_mirror = NULL;
+}
+
+void pool_free(u32 id) {
+    if (id == 0 || id >= P.count || !P.bufs[id].live) return;
+    release_block(&P.bufs[id]);
+}
+
+void pool_incref(u32 id) {
+    if (id == 0 || id >= P.count || !P.bufs[id].live) return;
+    P.bufs[id].refcount++;
+}
+
+void pool_decref(u32 id) {
+    if (id == 0 || id >= P.count || !P.bufs[id].live) return;
+    if (id <= P.persistent_floor) return;
+    if (P.bufs[id].refcount > 0) P.bufs[id].refcount--;
+    if (P.bufs[id].refcount == 0) release_block(&P.bufs[id]);
+}
+
+void pool_reset(u32 keep) {
+    u32 first = keep + 1;
+    if (first < 1) first = 1;
+    for (u32 i = first; i < P.count; i++)
+        if (P.bufs[i].live) release_block(&P.bufs[i]);
+    if (first < P.count) P.count = first;
+}
+
+void pool_set_persistent(u32 max_buf) { P.persistent_floor = max_buf; }
+
+HipbBuf *pool_get(u32 id) {
+    if (id == 0 || id >= P.count || !P.bufs[id].live) return NULL;
+    return &P.bufs[id];
+}
+
+void *pool_ptr(u32 id) {
+    HipbBuf *b = pool_get(id);
+    return b ? b->ptr : NULL;
+}
+
+u64 pool_bytes(u32 id) {
+    HipbBuf *b = pool_get(id);
+    return b ? b->bytes : 0;
+}
+
+void pool_mark_device_write(u32 id) {
+    HipbBuf *b = pool_get(id);
+    if (b) b->host_valid = 0;
+}
+
+/* Reserve n bytes of pinned staging; waits only if the ring wraps onto a
+ * segment whose copies are still in flight. */
+static u8 *stage_reserve(u64 n) {
+    if (P.seg_off + n > STAGE_SEG_BYTES) {
+        HIPB_CHECK(hipEventRecord(P.seg_done[P.seg], hipb.stream));
+        P.seg_pending[P.seg] = 1;
+        P.seg = (P.seg + 1) % STAGE_SEGMENTS;
+        if (P.seg_pending[P.seg]) {
+            HIPB_CHECK(hipEventSynchronize(P.seg_done[P.seg]));
+            P.seg_pending[P.seg] = 0;
+        }
+        P.seg_off = 0;
+    }
+    u8 *p = P.stage + (u64)P.seg * STAGE_SEG_BYTES + P.seg_off;
+    P.seg_off += (n + 255) & ~255ull;
+    return p;
+}
+
+void pool_write(u32 id, const void *data, u64 bytes) {
+    HipbBuf *b = pool_get(id);
+    if (!b || !data || bytes == 0) return;
+    if (bytes > b->cap) {
+        fprintf(stderr, "tinyhvm-hip: buf_write of %llu bytes into buffer %u of %llu bytes; truncated\n",
+                (unsigned long long)bytes, id, (unsigned long long)b->cap);
+        bytes = b->cap;
+    }
+    if (bytes <= STAGE_SEG_BYTES) {
+        u8 *s = stage_reserve(bytes);
+        memcpy(s, data, bytes);
+        HIPB_CHECK(hipMemcpyAsync(b->ptr, s, bytes, hipMemcpyHostToDevice, hipb.stream));
+    } else {
+        HIPB_CHECK(hipMemcpyAsync(b->ptr, data, bytes, hipMemcpyHostToDevice, hipb.stream));
+        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    }
+    if (bytes <= POOL_MIRROR_MAX && bytes == b->bytes) {
+        if (!b->host_mirror) b->host_mirror = malloc(POOL_MIRROR_MAX);
+        if (b->host_mirror) {
+            memcpy(b->host_mirror, data, bytes);
+            b->host_valid = 1;
+        }
+    } else {
+        b->host_valid = 0;
+    }
+}
+
+void pool_read(u32 id, void *out, u64 bytes, int nosync) {
+    HipbBuf *b = pool_get(id);
+    if (!out || bytes == 0) return;
+    if (!b) {
+        memset(out, 0, bytes);
+        return;
+    }
+    u64 n = bytes < b->bytes ? bytes : b->bytes;
+    if (nosync && b->host_valid && n <= POOL_MIRROR_MAX) {
+        memcpy(out, b->host_mirror, n);
+    } else if (n <= STAGE_SEG_BYTES) {
+        u8 *s = stage_reserve(n);
+        HIPB_CHECK(hipMemcpyAsync(s, b->ptr, n, hipMemcpyDeviceToHost, hipb.stream));
+        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+        memcpy(out, s, n);
+    } else {
+        HIPB_CHECK(hipMemcpyAsync(out, b->ptr, n, hipMemcpyDeviceToHost, hipb.stream));
+        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    }
+    if (n < bytes) memset((u8 *)out + n, 0, bytes - n);
+}
+
+void pool_stats(u64 *live_bytes, u64 *cached_bytes, u64 *n_mallocs) {
+    if (live_bytes) *live_bytes = P.live_bytes;
+    if (cached_bytes) *cached_bytes = P.cached_bytes;
+    if (n_mallocs) *n_mallocs = P.n_mallocs;
+}

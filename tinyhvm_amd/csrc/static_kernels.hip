@@ -1,0 +1,303 @@
+// static_kernels.hip - precompiled gfx950 kernels loaded once at init:
+//   thvm_rs          FusedOp/ReduceSpec interpreter (dispatch_kernel_rs fallback)
+//   thvm_contiguify  strided, masked view -> dense copy (4-byte elements)
+//   thvm_fill_u32    fill a buffer with a 32-bit pattern (graph-safe clear)
+//
+// The rs interpreter restates the engine's CPU fallback
+// (src/backend/cpu/dispatch.c:23-282): leaves are read through their view
+// (mask and compound masks checked before the read, broadcast by coord %
+// dim, negative index reads 0) or through a multi-view ShapeTracker; the
+// FusedOp DAG is evaluated with the engine ALU; SUM/RMAX accumulate in the
+// output's storage dtype in flat iteration order. Each thread owns one output
+// element and walks its reduce sub-domain in the same row-major order as the
+// CPU's flat loop, so results are bit-identical, f16 rounding included.
+#include <hip/hip_runtime.h>
+#include "thvm_abi.h"
+
+#include "kargs.h"
+
+__device__ __forceinline__ float h2f(u32 h) {
+    u32 sign = (h & 0x8000u) << 16, ex = (h >> 10) & 0x1Fu, man = h & 0x3FFu, bits;
+    if (ex == 0u) {
+        if (man == 0u) bits = sign;
+        else {
+            ex = 1u;
+            while ((man & 0x400u) == 0u) { man <<= 1; ex -= 1u; }
+            man &= 0x3FFu;
+            bits = sign | ((ex + 112u) << 23) | (man << 13);
+        }
+    } else if (ex == 0x1Fu) bits = sign | 0x7F800000u | (man << 13);
+    else bits = sign | ((ex + 112u) << 23) | (man << 13);
+    return __uint_as_float(bits);
+}
+
+__device__ __forceinline__ u32 f2h(float f) {
+    u32 x = __float_as_uint(f), sign = (x >> 16) & 0x8000u, man = x & 0x7FFFFFu;
+    int ex = (int)((x >> 23) & 0xFFu) - 112;
+    if (ex <= 0) {
+        if (ex < -10) return sign;
+        man = (man | 0x800000u) >> (1 - ex);
+        if (man & 0x1000u) man += 0x2000u;
+        return sign | (man >> 13);
+    }
+    if (ex >= 31) return sign | 0x7C00u | (man ? 0x200u : 0u);
+    if (man & 0x1000u) {
+        man += 0x2000u;
+        if (man & 0x800000u) { man = 0u; ex += 1; if (ex >= 31) return sign | 0x7C00u; }
+    }
+    return sign | ((u32)ex << 10) | (man >> 13);
+}
+
+__device__ __forceinline__ u32 f2u(float f) {
+    if (!(fabsf(f) < 9.2233720368547758e18f)) return 0u;
+    return (u32)(unsigned long long)(long long)f;
+}
+__device__ __forceinline__ int f2i(float f) {
+    if (!(f >= -2147483648.0f && f < 2147483648.0f)) return (int)0x80000000u;
+    return (int)f;
+}
+__device__ __forceinline__ float cast_f(float v, u32 dt) {
+    if (dt == DTYPE_F16) return h2f(f2h(v));
+    if (dt == DTYPE_I32) return (float)f2i(v);
+    if (dt == DTYPE_U32) return (float)f2u(v);
+    return v;
+}
+
+__device__ __forceinline__ float load_as_f32(const void *p, u32 dt, u32 n, u32 i) {
+    if (!p || i >= n) return 0.0f;
+    switch (dt) {
+    case DTYPE_F16: return h2f(((const unsigned short *)p)[i]);
+    case DTYPE_I32: return (float)((const int *)p)[i];
+    case DTYPE_U32: return (float)((const u32 *)p)[i];
+    default: return ((const float *)p)[i];
+    }
+}
+
+__device__ __forceinline__ void store_from_f32(void *p, u32 dt, u32 n, u32 i, float v) {
+    if (!p || i >= n) return;
+    switch (dt) {
+    case DTYPE_F16: ((unsigned short *)p)[i] = (unsigned short)f2h(v); break;
+    case DTYPE_I32: ((int *)p)[i] = f2i(v); break;
+    case DTYPE_U32: ((u32 *)p)[i] = f2u(v); break;
+    default: ((float *)p)[i] = v; break;
+    }
+}
+
+__device__ __forceinline__ float alu(u32 uop, u32 aux, float a, float b) {
+    switch (uop) {
+    case UOP_ADD: return a + b;
+    case UOP_MUL: return a * b;
+    case UOP_DIV: return b != 0.0f ? a / b : 0.0f;
+    case UOP_SUB: return a - b;
+    case UOP_MAX: return a > b ? a : b;
+    case UOP_CMP: return a > b ? 1.0f : 0.0f;
+    case UOP_NEG: return -a;
+    case UOP_RELU: return a > 0.0f ? a : 0.0f;
+    case UOP_EXP: return expf(a);
+    case UOP_LOG: return logf(a);
+    case UOP_SQRT: return sqrtf(a);
+    case UOP_CAST: return cast_f(a, aux);
+    default: return a;
+    }
+}
+
+// Read through one view; coords are in the iteration domain.
+__device__ float view_read(const void *buf, u32 dt, u32 n, const View *v, const u32 *coords, u32 rank) {
+    if (v->has_mask) {
+        for (u32 d = 0; d < rank && d < v->shape.rank; d++)
+            if (coords[d] < v->mask_begin[d] || coords[d] >= v->mask_end[d]) return 0.0f;
+        for (u32 cm = 0; cm < v->n_compound_masks; cm++) {
+            u32 da = v->compound_masks[cm].dim_a, db = v->compound_masks[cm].dim_b;
+            if (da >= MAX_DIM || db >= MAX_DIM) return 0.0f;
+            int composed = (int)coords[da] * v->compound_masks[cm].stride_a + (int)coords[db];
+            if (composed < (int)v->compound_masks[cm].begin || composed >= (int)v->compound_masks[cm].end)
+                return 0.0f;
+        }
+    }
+    int idx = v->offset;
+    for (u32 d = 0; d < rank && d < v->shape.rank; d++) {
+        u32 dim = v->shape.dims[d];
+        u32 c = dim ? coords[d] % dim : 0u;
+        idx = (int)((u32)idx + c * (u32)v->strides[d]);
+    }
+    if (idx < 0) return 0.0f;
+    return load_as_f32(buf, dt, n, (u32)idx);
+}
+
+// Read through a stacked ShapeTracker (src/backend/cpu/dispatch.c:26-83).
+__device__ float st_read(const void *buf, u32 dt, u32 n, const ShapeTracker *st, const u32 *coords,
+                         u32 rank, const u32 *full_dims) {
+    if (st->n_views <= 1) return 0.0f;
+    u32 si = 0;
+    {
+        u32 stride = 1;
+        for (int d = (int)rank - 1; d >= 0; d--) {
+            si += coords[d] * stride;
+            stride *= full_dims[d];
+        }
+    }
+    for (int vi = (int)st->n_views - 2; vi >= 0; vi--) {
+        const View *vw = &st->views[vi];
+        const View *outer = &st->views[vi + 1];
+        u32 outer_flat = 0;
+        {
+            u32 udiv = 1;
+            u32 ostr[MAX_DIM];
+            u32 orank = outer->shape.rank < MAX_DIM ? outer->shape.rank : MAX_DIM;
+            if (orank > 0) {
+                ostr[orank - 1] = 1;
+                for (int d = (int)orank - 2; d >= 0; d--) ostr[d] = ostr[d + 1] * outer->shape.dims[d + 1];
+            }
+            for (int d = (int)orank - 1; d >= 0; d--) {
+                u32 dim = outer->shape.dims[d];
+                if (dim <= 1) { udiv *= dim; continue; }
+                u32 c = udiv ? (si / udiv) % dim : 0u;
+                outer_flat += c * ostr[d];
+                udiv *= dim;
+            }
+        }
+        int idx = vw->offset;
+        {
+            u32 rem = outer_flat;
+            u32 istr[MAX_DIM];
+            u32 irank = vw->shape.rank < MAX_DIM ? vw->shape.rank : MAX_DIM;
+            if (irank > 0) {
+                istr[irank - 1] = 1;
+                for (int d = (int)irank - 2; d >= 0; d--) istr[d] = istr[d + 1] * vw->shape.dims[d + 1];
+            }
+            for (u32 d = 0; d < irank; d++) {
+                u32 c = istr[d] ? rem / istr[d] : 0u;
+                rem = istr[d] ? rem % istr[d] : rem;
+                if (vw->has_mask && (c < vw->mask_begin[d] || c >= vw->mask_end[d])) return 0.0f;
+                if (vw->strides[d] != 0) idx = (int)((u32)idx + c * (u32)vw->strides[d]);
+            }
+        }
+        if (idx < 0) return 0.0f;
+        si = (u32)idx;
+    }
+    return load_as_f32(buf, dt, n, si);
+}
+
+__device__ float read_leaf(const RsParams *P, u32 i, const u32 *coords, u32 rank, const u32 *full_dims) {
+    const void *p = (const void *)(uintptr_t)P->leaf_ptr[i];
+    if (P->leaf_st[i] != 0xFFFFFFFFu)
+        return st_read(p, P->leaf_dtype[i], P->leaf_n[i], &P->sts[P->leaf_st[i]], coords, rank, full_dims);
+    return view_read(p, P->leaf_dtype[i], P->leaf_n[i], &P->views[i], coords, rank);
+}
+
+// Evaluates ops [lo, hi) over vals; returns 0 if an arg is out of range
+// (the CPU stops evaluating at that op).
+__device__ void eval_ops(const RsParams *P, float *vals, u32 lo, u32 hi, u32 limit) {
+    for (u32 i = lo; i < hi; i++) {
+        u32 aa = P->ops[i].arg_a, bb = P->ops[i].arg_b;
+        if (aa >= limit || bb >= limit) break;
+        vals[P->n_leaves + i] = alu(P->ops[i].uop, P->ops[i].aux, vals[aa], vals[bb]);
+    }
+}
+
+extern "C" __global__ __launch_bounds__(64) void thvm_rs(const RsParams *P, u32 phase) {
+    const u32 t = blockIdx.x * 64u + threadIdx.x;
+    const u32 rank = P->rank;
+    float vals[FUSE_MAX_LEAVES + FUSE_MAX_OPS];
+    u32 coords[MAX_DIM];
+    u32 n_ops = P->n_ops, n_leaves = P->n_leaves;
+    void *out = (void *)(uintptr_t)P->out_ptr;
+    if (phase == 0) {
+        if (!P->has_reduce) {
+            if (t >= P->full_numel) return;
+            u32 rem = t;
+            for (int d = (int)rank - 1; d >= 0; d--) {
+                coords[d] = P->dims[d] ? rem % P->dims[d] : 0u;
+                rem = P->dims[d] ? rem / P->dims[d] : 0u;
+            }
+            for (u32 i = 0; i < n_leaves; i++) vals[i] = read_leaf(P, i, coords, rank, P->dims);
+            eval_ops(P, vals, 0, n_ops, n_leaves + n_ops);
+            float result = n_ops > 0 ? vals[n_leaves + n_ops - 1] : vals[0];
+            store_from_f32(out, P->out_dtype, P->out_n, t, result);
+            return;
+        }
+        if (t >= P->out_numel) return;
+        // output coords from t over out_shape
+        u32 rem = t;
+        for (int d = (int)rank - 1; d >= 0; d--) {
+            u32 od = P->out_shape[d];
+            coords[d] = od ? rem % od : 0u;
+            rem = od ? rem / od : 0u;
+        }
+        u32 eval_n = P->post_start ? P->post_start : n_ops;
+        float acc = cast_f(P->reduce_type == UOP_RMAX ? -1e30f : 0.0f, P->out_dtype);
+        for (u32 r = 0; r < P->reduce_numel; r++) {
+            u32 rr = r;
+            for (int d = (int)rank - 1; d >= 0; d--) {
+                if (!P->is_reduce[d]) continue;
+                coords[d] = P->dims[d] ? rr % P->dims[d] : 0u;
+                rr = P->dims[d] ? rr / P->dims[d] : 0u;
+            }
+            for (u32 i = 0; i < n_leaves; i++) vals[i] = read_leaf(P, i, coords, rank, P->dims);
+            eval_ops(P, vals, 0, eval_n, n_leaves + eval_n);
+            float result = eval_n > 0 ? vals[n_leaves + eval_n - 1] : vals[0];
+            if (P->reduce_type == UOP_SUM) acc = cast_f(acc + result, P->out_dtype);
+            else if (P->reduce_type == UOP_RMAX) acc = cast_f(result > acc ? result : acc, P->out_dtype);
+        }
+        store_from_f32(out, P->out_dtype, P->out_n, t, acc);
+        return;
+    }
+    // phase 1: post-reduce ops over the reduced output
+    if (t >= P->out_numel) return;
+    u32 rem = t;
+    for (int d = (int)rank - 1; d >= 0; d--) {
+        u32 od = P->out_shape[d];
+        coords[d] = od ? rem % od : 0u;
+        rem = od ? rem / od : 0u;
+    }
+    float reduce_result = load_as_f32(out, P->out_dtype, P->out_n, t);
+    u32 n_pre = n_leaves - P->n_post_leaves;
+    u32 zero_dims[MAX_DIM] = {0, 0, 0, 0, 0, 0, 0, 0};
+    for (u32 i = 0; i < n_leaves; i++)
+        vals[i] = i < n_pre ? 0.0f : read_leaf(P, i, coords, rank, zero_dims);
+    u32 ps = P->post_start;
+    const u32 LIM = FUSE_MAX_LEAVES + FUSE_MAX_OPS;
+    if (ps > 0 && n_leaves + ps - 1 < LIM) vals[n_leaves + ps - 1] = reduce_result;
+    for (u32 i = ps; i < n_ops; i++) {
+        u32 aa = P->ops[i].arg_a, bb = P->ops[i].arg_b;
+        float a = aa < LIM ? vals[aa] : 0.0f, b = bb < LIM ? vals[bb] : 0.0f;
+        vals[n_leaves + i] = alu(P->ops[i].uop, P->ops[i].aux, a, b);
+    }
+    store_from_f32(out, P->out_dtype, P->out_n, t, vals[n_leaves + n_ops - 1]);
+}
+
+// Dense copy of a strided, masked view of 4-byte elements.
+extern "C" __global__ __launch_bounds__(256) void thvm_contiguify(ContigArgs A) {
+    const u32 t = blockIdx.x * 256u + threadIdx.x;
+    const View &v = A.v;
+    const u32 numel = A.numel, dst_n = A.dst_n, src_n = A.src_n;
+    u32 *dst = (u32 *)(uintptr_t)A.dst;
+    const u32 *src = (const u32 *)(uintptr_t)A.src;
+    if (t >= numel || t >= dst_n) return;
+    u32 rem = t;
+    int idx = v.offset;
+    int masked = 0;
+    u32 coords[MAX_DIM];
+    for (int d = (int)v.shape.rank - 1; d >= 0; d--) {
+        u32 dim = v.shape.dims[d];
+        u32 c = dim ? rem % dim : 0u;
+        rem = dim ? rem / dim : 0u;
+        coords[d] = c;
+        if (v.has_mask && (c < v.mask_begin[d] || c >= v.mask_end[d])) masked = 1;
+        idx = (int)((u32)idx + c * (u32)v.strides[d]);
+    }
+    if (v.has_mask && !masked) {
+        for (u32 cm = 0; cm < v.n_compound_masks && cm < 2; cm++) {
+            u32 da = v.compound_masks[cm].dim_a, db = v.compound_masks[cm].dim_b;
+            if (da >= MAX_DIM || db >= MAX_DIM) { masked = 1; break; }
+            int c = (int)coords[da] * v.compound_masks[cm].stride_a + (int)coords[db];
+            if (c < (int)v.compound_masks[cm].begin || c >= (int)v.compound_masks[cm].end) masked = 1;
+        }
+    }
+    dst[t] = (masked || idx < 0 || (u32)idx >= src_n) ? 0u : src[(u32)idx];
+}
+
+extern "C" __global__ __launch_bounds__(256) void thvm_fill_u32(u32 *dst, u32 n, u32 value) {
+    const u32 t = blockIdx.x * 256u + threadIdx.x;
+    if (t < n) dst[t] = value;
+}
