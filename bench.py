@@ -42,6 +42,7 @@ WORKLOADS = {
         "config": {"workload": "fused elementwise+reduce f32: y = sum(relu(a*b+c), -1) and dA",
                    "shape": [8192, 8192], "dist": "N(0,1)"},
         "cpu_sample": "full fused fwd+bwd step at [8192,8192], 1 replay",
+        "profile": "fused_8192x8192.md",
     },
 }
 
@@ -73,6 +74,19 @@ class Hip:
         return out.value
 
 
+def measured_traffic(profile, kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 summary
+    (its ```json block), or None when no counter run has been recorded."""
+    path = os.path.join(ROOT, "profiles", profile)
+    if not os.path.exists(path):
+        return None
+    text = open(path).read()
+    if "```json" not in text:
+        return None
+    block = text.split("```json", 1)[1].split("```", 1)[0]
+    return json.loads(block).get("traffic_bytes", {}).get(kernel)
+
+
 def find_mark(L, t, text, start=0):
     return L.thvm_trace_find_mark(t, text.encode(), start)
 
@@ -94,6 +108,40 @@ def cpu_baseline(wl, lo_mark):
             "kind": "reference", "sample": wl["cpu_sample"], "seconds": res["per_rep"]}
 
 
+def copy_calibration(nbytes=256 << 20, reps=5):
+    """A plain copy kernel of known size through the same generated-kernel
+    path (out[i] = src[i]): the reference reading for the HBM byte counters."""
+    from tinyhvm_amd import abi
+    L = _lib.lib()
+    if L.thvm_hip_init() != 0:
+        raise SystemExit("HIP backend failed to initialise")
+    n = nbytes // 4
+    k = abi.UOpKernel()
+    k.n_ops, k.n_leaves, k.n_bufs, k.rank = 3, 1, 2, 1
+    k.full_shape.rank, k.full_shape.dims[0] = 1, n
+    k.grid[0], k.grid[1], k.grid[2] = n, 1, 1
+    k.ops[0].type = abi.KOP_GID
+    k.ops[1].type = abi.KOP_LOAD
+    k.ops[1].arg[0], k.ops[1].imm.u = 0, 1
+    k.ops[2].type = abi.KOP_STORE
+    k.ops[2].arg[0], k.ops[2].arg[1] = 0, 1
+    src, dst = L.thvm_hip_buf_alloc(nbytes), L.thvm_hip_buf_alloc(nbytes)
+    leaves = (C.c_uint32 * 1)(src)
+    L.thvm_hip_dispatch_uop_kernel(dst, leaves, 1, C.byref(k), 0)
+    assert L.thvm_hip_synchronize() == 0
+    hip = Hip(L.thvm_hip_stream())
+    e0, e1 = hip.event(), hip.event()
+    hip.record(e0)
+    for _ in range(reps):
+        L.thvm_hip_dispatch_uop_kernel(dst, leaves, 1, C.byref(k), 0)
+    hip.record(e1)
+    ms = hip.ms(e0, e1) / reps
+    assert L.thvm_hip_synchronize() == 0
+    L.thvm_hip_shutdown()
+    print(json.dumps({"copy_calibration_bytes_read": nbytes, "bytes_written": nbytes, "reps": reps,
+                      "ms_per_copy": round(ms, 4), "GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -101,7 +149,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="fused")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="run only a 256 MiB copy kernel (HBM counter calibration)")
     args = ap.parse_args()
+    if args.calibrate_copy:
+        copy_calibration()
+        return
     if args.gpus != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(use --gpus 1)", file=sys.stderr)
@@ -144,16 +197,22 @@ def main():
     # pass 2: the same steps split at the workload's marks, with events around
     # each kernel's records on the backend stream
     marks = sorted((find_mark(L, t, m, lo), m) for m in wl["kernels"])
-    bounds = [(marks[i][0], marks[i + 1][0] if i + 1 < len(marks) else hi, marks[i][1])
-              for i in range(len(marks))]
+    bounds = []
+    for i in range(len(marks)):
+        a = marks[i][0]
+        b = marks[i + 1][0] if i + 1 < len(marks) else hi
+        u = next(j for j in range(a, b) if L.thvm_trace_tag(t, j) in (7, 8))  # the dispatch
+        bounds.append((a, u, b, marks[i][1]))
     ev = [(hip.event(), hip.event()) for _ in bounds]
     k_ms = {m: 0.0 for m in wl["kernels"]}
     for _ in range(args.steps):
-        for (a, b, m), (ea, eb) in zip(bounds, ev):
+        for (a, u, b, m), (ea, eb) in zip(bounds, ev):
+            L.thvm_trace_replay(t, be, a, u, SKIP_READS)
             hip.record(ea)
-            L.thvm_trace_replay(t, be, a, b, SKIP_READS)
+            L.thvm_trace_replay(t, be, u, u + 1, SKIP_READS)
             hip.record(eb)
-        for (a, b, m), (ea, eb) in zip(bounds, ev):
+            L.thvm_trace_replay(t, be, u + 1, b, SKIP_READS)
+        for (a, u, b, m), (ea, eb) in zip(bounds, ev):
             k_ms[m] += hip.ms(ea, eb)
     assert L.thvm_hip_synchronize() == 0
     step_s = wall / args.steps
@@ -177,7 +236,8 @@ def main():
         "data": "synthetic",
         "config": wl["config"],
         "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": measured_traffic(wl["profile"], dom),
                      "kernel": dom},
         "kernels_ms": {m: round(v / args.steps, 4) for m, v in k_ms.items()},
         "gpu_ms_per_step": round(gpu_ms / args.steps, 4),

@@ -91,6 +91,11 @@ typedef struct {
     u32 block;
     u32 total;
     u32 gx;            /* GROUP: workgroups per grid row */
+    u32 unroll;        /* GROUP: unroll depth of the parallel loop */
+    int nt;            /* streaming (non-temporal) 128-bit loads/stores */
+    u32 per_thread;    /* SERIAL: thread-vectors per thread */
+    u32 ew_block;      /* SERIAL: workgroup size (0: chosen by size) */
+    u32 red_block;     /* GROUP: largest workgroup size */
     SB sb;
     char err[256];
 } Gen;
@@ -568,12 +573,13 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
         } else if (V == 4 && ix->kind == K_LIN && ix->step == 1 && !ix->ft &&
                    (ix->align == 0 || ix->align % 4 == 0) && dt == DTYPE_F32) {
             U(g, op->arg[0], 0, a);
+            const char *sfx = (g->nt & 1) ? "nt" : "";
             if (unchecked)
-                sb_put(&g->sb, "    { float4 t_ = ld4_u(p%u, %s); f%u_0 = t_.x; f%u_1 = t_.y; f%u_2 = t_.z; f%u_3 = t_.w; }\n",
-                       bi, a, i, i, i, i);
+                sb_put(&g->sb, "    { float4 t_ = ld4%s_u(p%u, %s); f%u_0 = t_.x; f%u_1 = t_.y; f%u_2 = t_.z; f%u_3 = t_.w; }\n",
+                       sfx, bi, a, i, i, i, i);
             else
-                sb_put(&g->sb, "    { float4 t_ = ld4(p%u, c%u, %s); f%u_0 = t_.x; f%u_1 = t_.y; f%u_2 = t_.z; f%u_3 = t_.w; }\n",
-                       bi, bi, a, i, i, i, i);
+                sb_put(&g->sb, "    { float4 t_ = ld4%s(p%u, c%u, %s); f%u_0 = t_.x; f%u_1 = t_.y; f%u_2 = t_.z; f%u_3 = t_.w; }\n",
+                       sfx, bi, bi, a, i, i, i, i);
         } else {
             for (u32 v = 0; v < V; v++) {
                 U(g, op->arg[0], v, a);
@@ -637,7 +643,8 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
             Fx(g, op->arg[1], 1, b1);
             Fx(g, op->arg[1], 2, b2);
             Fx(g, op->arg[1], 3, b3);
-            sb_put(&g->sb, "    if (X0 + 3u < TOTAL) st4(p0, c0, %s, make_float4(%s, %s, %s, %s));\n", a, b, b1, b2, b3);
+            sb_put(&g->sb, "    if (X0 + 3u < TOTAL) st4%s(p0, c0, %s, make_float4(%s, %s, %s, %s));\n",
+                   (g->nt & 2) ? "nt" : "", a, b, b1, b2, b3);
             sb_put(&g->sb, "    else {\n");
             for (u32 v = 0; v < V; v++) {
                 U(g, op->arg[0], v, a);
@@ -735,12 +742,24 @@ static const char *PRELUDE =
 "  if (i + 3u < n && i + 3u >= i) return *(const float4*)((const float*)p + i);\n"
 "  return make_float4(ld_f32(p, n, i), ld_f32(p, n, i + 1u), ld_f32(p, n, i + 2u), ld_f32(p, n, i + 3u));\n"
 "}\n"
+"typedef float v4f_ __attribute__((ext_vector_type(4)));\n"
+"__device__ __forceinline__ float4 ld4nt_u(const char* p, u32 i) {\n"
+"  v4f_ t = __builtin_nontemporal_load((const v4f_*)((const float*)p + i)); return make_float4(t.x, t.y, t.z, t.w);\n"
+"}\n"
+"__device__ __forceinline__ float4 ld4nt(const char* p, u32 n, u32 i) {\n"
+"  if (i + 3u < n && i + 3u >= i) return ld4nt_u(p, i);\n"
+"  return make_float4(ld_f32(p, n, i), ld_f32(p, n, i + 1u), ld_f32(p, n, i + 2u), ld_f32(p, n, i + 3u));\n"
+"}\n"
 "__device__ __forceinline__ void st_f32(char* p, u32 n, u32 i, float v) { if (i < n) ((float*)p)[i] = v; }\n"
 "__device__ __forceinline__ void st_f16(char* p, u32 n, u32 i, float v) { if (i < n) ((u16*)p)[i] = (u16)f2h(v); }\n"
 "__device__ __forceinline__ void st_i32(char* p, u32 n, u32 i, float v) { if (i < n) ((int*)p)[i] = f2i(v); }\n"
 "__device__ __forceinline__ void st_u32(char* p, u32 n, u32 i, float v) { if (i < n) ((u32*)p)[i] = f2u(v); }\n"
 "__device__ __forceinline__ void st4(char* p, u32 n, u32 i, float4 v) {\n"
 "  if (i + 3u < n && i + 3u >= i) { *(float4*)((float*)p + i) = v; return; }\n"
+"  st_f32(p, n, i, v.x); st_f32(p, n, i + 1u, v.y); st_f32(p, n, i + 2u, v.z); st_f32(p, n, i + 3u, v.w);\n"
+"}\n"
+"__device__ __forceinline__ void st4nt(char* p, u32 n, u32 i, float4 v) {\n"
+"  if (i + 3u < n && i + 3u >= i) { v4f_ t = {v.x, v.y, v.z, v.w}; __builtin_nontemporal_store(t, (v4f_*)((float*)p + i)); return; }\n"
 "  st_f32(p, n, i, v.x); st_f32(p, n, i + 1u, v.y); st_f32(p, n, i + 2u, v.z); st_f32(p, n, i + 3u, v.w);\n"
 "}\n"
 "__device__ __forceinline__ float wsum(float x) {\n"
@@ -830,6 +849,7 @@ static void emit_group_loop(Gen *g, u32 r) {
     u32 nq = trip / V;
     for (int pass = 0; pass < 2; pass++) {
         sb_put(&g->sb, pass == 0 ? "    if (ok_) {\n" : "    } else {\n");
+        if (g->unroll > 1) sb_put(&g->sb, "    #pragma unroll %u\n", g->unroll);
         sb_put(&g->sb, "    for (u32 q_ = lane; q_ < %uu; q_ += %uu) {\n    u%u = q_ * %uu;\n", nq, g->block, r, V);
         emit_range_seq(g, r + 1, e, pass == 0, 1);
         sb_put(&g->sb, "    }\n");
@@ -867,6 +887,20 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
     G.oi = calloc(k->n_ops, sizeof(OpI));
     if (!G.oi) { snprintf(err, errlen, "oom"); return 0; }
     analyze_structure(&G);
+    {
+        const char *e;
+        G.unroll = (e = getenv("THVM_HIP_UNROLL")) ? (u32)atoi(e) : 1;
+        G.nt = (e = getenv("THVM_HIP_NT")) ? atoi(e) : 1;   /* bit 0: loads, bit 1: stores */
+        G.ew_block = (e = getenv("THVM_HIP_EW_BLOCK")) ? (u32)atoi(e) : 0;   /* 0: by size */
+        if (G.ew_block != 0 && G.ew_block != 128 && G.ew_block != 256 && G.ew_block != 512 &&
+            G.ew_block != 1024) G.ew_block = 0;
+        G.red_block = (e = getenv("THVM_HIP_RED_BLOCK")) ? (u32)atoi(e) : 256;
+        if (G.red_block != 64 && G.red_block != 128 && G.red_block != 512 && G.red_block != 1024)
+            G.red_block = 256;
+        G.per_thread = (e = getenv("THVM_HIP_EW_PER_THREAD")) ? (u32)atoi(e) : 1;
+        if (G.per_thread < 1) G.per_thread = 1;
+        if (G.per_thread > 8) G.per_thread = 8;
+    }
 
     u32 total = k->local_size > 0 ? k->grid[0] : k->grid[0] * k->grid[1] * k->grid[2];
     G.total = total;
@@ -890,28 +924,48 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
         G.V = (all4 && min_trip >= 64) ? 4 : 1;
         u32 nq = min_trip / G.V;
         G.block = 64;
-        while (G.block < 256 && G.block < nq) G.block *= 2;
+        while (G.block < G.red_block && G.block < nq) G.block *= 2;
     } else {
         G.V = (total >= 1024 && k->n_ops <= 256) ? 4 : 1;
-        G.block = 256;
+        /* Streaming kernels over >= 4M thread-vectors run best with 1024-lane
+         * workgroups (fewer, longer-lived groups); smaller grids keep 256 so
+         * every CU still gets work. */
+        u64 nv = ((u64)total + G.V - 1) / G.V;
+        G.block = G.ew_block ? G.ew_block : (nv >= (4ull << 20) ? 1024 : 256);
     }
     analyze_vector(&G);
     analyze_global(&G);
 
     SB *s = &G.sb;
     sb_put(s, "%s\n", PRELUDE);
-    snprintf(out->name, sizeof out->name, "thvm_k");
-    sb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void thvm_k(", G.block);
+    {
+        int has_loop = 0;
+        for (u32 i = 0; i < k->n_ops; i++) if (k->ops[i].type == KOP_RANGE) has_loop = 1;
+        const char *kind = G.mode == KG_MODE_GROUP ? "red" : (has_loop ? "loop" : "ew");
+        snprintf(out->name, sizeof out->name, "thvm_%s_%08x", kind, (u32)(uop_signature(k) & 0xFFFFFFFFu));
+    }
+    sb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", G.block, out->name);
     emit_params(&G);
     sb_put(s, ") {\n");
     if (G.mode == KG_MODE_SERIAL) {
-        u64 nthreads = ((u64)total + G.V - 1) / G.V;
+        u64 nvec = ((u64)total + G.V - 1) / G.V;          /* thread-vectors */
+        u32 W = G.per_thread;
+        if (nvec < (u64)W * G.block * 256) W = 1;
+        u64 nthreads = (nvec + W - 1) / W;
         sb_put(s, "  const u32 TOTAL = %uu;\n", total);
         sb_put(s, "  const unsigned long long t_ = ((unsigned long long)blockIdx.y * gridDim.x + blockIdx.x) * %uull + threadIdx.x;\n", G.block);
         sb_put(s, "  if (t_ >= %lluull) return;\n", (unsigned long long)nthreads);
-        sb_put(s, "  const u32 X0 = (u32)t_ * %uu;\n", G.V);
+        if (W > 1) {
+            sb_put(s, "  #pragma unroll\n  for (u32 w_ = 0; w_ < %uu; w_++) {\n", W);
+            sb_put(s, "  const unsigned long long v_ = t_ + (unsigned long long)w_ * %lluull;\n", (unsigned long long)nthreads);
+            sb_put(s, "  if (v_ >= %lluull) break;\n", (unsigned long long)nvec);
+            sb_put(s, "  const u32 X0 = (u32)v_ * %uu;\n", G.V);
+        } else {
+            sb_put(s, "  const u32 X0 = (u32)t_ * %uu;\n", G.V);
+        }
         emit_decls(&G);
         emit_range_seq(&G, 0, k->n_ops, 0, 0);
+        if (W > 1) sb_put(s, "  }\n");
         out->n_threads = nthreads;
     } else {
         sb_put(s, "  const u32 gid = blockIdx.y * gridDim.x + blockIdx.x;\n");
