@@ -41,8 +41,10 @@
  *   CONTIG    dst, numel, src, VIEW
  *   RESET     keep
  *   PERSIST   max_buf
- *   SNAPSHOT  id, pad, u64 bytes, data   (buffer contents after the
- *             preceding dispatch, as the reference CPU backend produced them)
+ *   SNAPSHOT  id, source, u64 bytes, data   (buffer contents after the
+ *             preceding dispatch: source 0 = produced by the engine's CPU
+ *             backend; 1 = produced by the oracle because the engine's
+ *             interpreter would read out of bounds for that kernel)
  *   MARK      n, n bytes of text (annotation: phase names, config)
  */
 #ifndef THVM_TRACE_H

@@ -89,9 +89,16 @@ u16 ora_f2h(f32 f) {
 
 static u32 dt_size(u32 dt) { return dt == DTYPE_F16 ? 2u : 4u; }
 
+/* Loads that fell outside their buffer since the counter was last cleared
+ * (where the reference interpreter would have read out of bounds). */
+u64 ora_oob_loads;
+
 /* Host C conversions on x86-64: the same instructions the reference build uses. */
 f32 ora_load(const void *base, u64 nbytes, u32 dt, u32 i) {
-    if (!base || (u64)i * dt_size(dt) + dt_size(dt) > nbytes) return 0.0f;
+    if (!base || (u64)i * dt_size(dt) + dt_size(dt) > nbytes) {
+        ora_oob_loads++;
+        return 0.0f;
+    }
     switch (dt) {
     case DTYPE_F32: return ((const f32 *)base)[i];
     case DTYPE_F16: return ora_h2f(((const u16 *)base)[i]);

@@ -17,12 +17,22 @@
  * Usage: capture [-n] <workload> <out.trc> [size args...]
  */
 #include "tinyhvm.c"
+#include "nn/_.c"
 #include "backend/cpu/_.c"
 #include "thvm_trace.h"
 #include "thvm_gen.h"
 
+/* The oracle (oracle/oracle.c, compiled separately against the same layouts). */
+extern u64 ora_oob_loads;
+void ora_dispatch_rs(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, const View **views,
+                     const ShapeTracker *const *sts, u32 n_leaves, const FusedOp *ops, u32 n_ops,
+                     const Shape *full, const ReduceSpec *reduce, const u32 *leaf_dtypes, u32 out_dtype);
+void ora_dispatch_uop(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, u32 n_leaves,
+                      const UOpKernel *k);
+
 static FILE *g_out;
 static int g_exec = 1;
+static int g_read_data = 0;   /* -r: keep READ payloads (the SNAPSHOTs already hold them) */
 static Backend g_orig;
 
 typedef struct { u8 *p; size_t n, cap; } RecBuf;
@@ -91,11 +101,16 @@ static void rec_mark(const char *text) {
     rb_emit(TRC_MARK);
 }
 
+/* Source of a SNAPSHOT: 0 = the engine's CPU backend, 1 = the oracle, used
+ * where the engine's interpreter would read out of bounds (masked pad loads,
+ * src/backend/cpu/uop.c:55-71) and fault. */
+static u32 g_snap_source;
+
 static void rec_snapshot(u32 id) {
     if (!g_exec || id == 0 || id >= MAX_BUFS || !cpu_pool.bufs[id]) return;
     rb_begin();
     rb_u32(id);
-    rb_u32(0);
+    rb_u32(g_snap_source);
     rb_u64(cpu_pool.sizes[id]);
     rb_bytes(cpu_pool.bufs[id], cpu_pool.sizes[id]);
     rb_emit(TRC_SNAPSHOT);
@@ -134,8 +149,9 @@ static void cap_buf_write(u32 id, const void *data, u64 bytes) {
 }
 static void cap_buf_read(u32 id, void *out, u64 bytes) {
     g_orig.buf_read(id, out, bytes);
-    rb_begin(); rb_u32(id); rb_u32(g_exec ? 1 : 0); rb_u64(bytes);
-    if (g_exec) rb_bytes(out, bytes);
+    int keep = g_exec && g_read_data;
+    rb_begin(); rb_u32(id); rb_u32(keep ? 1 : 0); rb_u64(bytes);
+    if (keep) rb_bytes(out, bytes);
     rb_emit(TRC_READ);
 }
 static void cap_pool_reset(u32 keep) {
@@ -164,8 +180,31 @@ static void cap_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_lea
     for (u32 i = 0; i < n_leaves; i++) rb_view(&k->leaf_views[i]);
     for (u32 i = 0; i < n_leaves; i++) rb_u32(k->leaf_dtypes[i]);
     rb_emit(TRC_UOP);
-    if (g_exec) g_orig.dispatch_uop_kernel(out_buf, leaf_bufs, n_leaves, k, cache_key);
+    g_snap_source = 0;
+    if (g_exec) {
+        /* dry run through the oracle into a scratch copy to see whether any
+         * load leaves its buffer */
+        const void *lp[FUSE_MAX_LEAVES];
+        u64 lb[FUSE_MAX_LEAVES];
+        for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) {
+            lp[i] = cpu_pool.bufs[leaf_bufs[i]];
+            lb[i] = cpu_pool.bufs[leaf_bufs[i]] ? cpu_pool.sizes[leaf_bufs[i]] : 0;
+        }
+        u64 ob = cpu_pool.sizes[out_buf];
+        void *scratch = malloc(ob ? ob : 4);
+        memcpy(scratch, cpu_pool.bufs[out_buf], ob);
+        ora_oob_loads = 0;
+        ora_dispatch_uop(scratch, ob, lp, lb, n_leaves, k);
+        if (ora_oob_loads) {
+            memcpy(cpu_pool.bufs[out_buf], scratch, ob);
+            g_snap_source = 1;
+        } else {
+            g_orig.dispatch_uop_kernel(out_buf, leaf_bufs, n_leaves, k, cache_key);
+        }
+        free(scratch);
+    }
     rec_snapshot(out_buf);
+    g_snap_source = 0;
 }
 
 static void cap_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **leaf_views,
@@ -201,11 +240,32 @@ static void cap_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **lea
     if (leaf_dtypes) for (u32 i = 0; i < n_leaves; i++) rb_u32(leaf_dtypes[i]);
     rb_u32(out_dtype);
     rb_emit(TRC_RS);
-    if (g_exec)
-        g_orig.dispatch_kernel_rs(out_buf, leaf_bufs, leaf_views, leaf_sts, n_leaves, ops, n_ops,
-                                  full_shape, reduce, side_bufs, side_idx, n_side,
-                                  leaf_dtypes, out_dtype);
+    g_snap_source = 0;
+    if (g_exec) {
+        const void *lp[FUSE_MAX_LEAVES];
+        u64 lb[FUSE_MAX_LEAVES];
+        for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) {
+            lp[i] = cpu_pool.bufs[leaf_bufs[i]];
+            lb[i] = cpu_pool.bufs[leaf_bufs[i]] ? cpu_pool.sizes[leaf_bufs[i]] : 0;
+        }
+        u64 ob = cpu_pool.sizes[out_buf];
+        void *scratch = malloc(ob ? ob : 4);
+        memcpy(scratch, cpu_pool.bufs[out_buf], ob);
+        ora_oob_loads = 0;
+        ora_dispatch_rs(scratch, ob, lp, lb, leaf_views, leaf_sts, n_leaves, ops, n_ops, full_shape, reduce,
+                        leaf_dtypes, out_dtype);
+        if (ora_oob_loads) {
+            memcpy(cpu_pool.bufs[out_buf], scratch, ob);
+            g_snap_source = 1;
+        } else {
+            g_orig.dispatch_kernel_rs(out_buf, leaf_bufs, leaf_views, leaf_sts, n_leaves, ops, n_ops,
+                                      full_shape, reduce, side_bufs, side_idx, n_side,
+                                      leaf_dtypes, out_dtype);
+        }
+        free(scratch);
+    }
     rec_snapshot(out_buf);
+    g_snap_source = 0;
 }
 
 static void cap_legacy_unary(u32 uop, u32 dst, const View *dv, u32 dd, u32 src,
@@ -228,6 +288,42 @@ static void cap_legacy_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn,
     g_orig.op_reduce(uop, dst, dn, dd, src, sn, sd, rd);
 }
 
+/* The engine's CPU backend has no buf_copy/contiguify, so ASSIGN would fall
+ * back to a host round trip (src/interact/tensor_ops.c:113-137). Giving the
+ * recorded backend both slots makes the engine take the device-copy path a
+ * GPU backend gets. */
+static void cap_buf_copy(u32 dst, u32 src, u64 nbytes) {
+    rb_begin(); rb_u32(dst); rb_u32(src); rb_u64(nbytes); rb_emit(TRC_COPY);
+    if (cpu_pool.bufs[dst] && cpu_pool.bufs[src]) {
+        u64 n = nbytes;
+        if (n > cpu_pool.sizes[dst]) n = cpu_pool.sizes[dst];
+        if (n > cpu_pool.sizes[src]) n = cpu_pool.sizes[src];
+        memmove(cpu_pool.bufs[dst], cpu_pool.bufs[src], n);
+    }
+    rec_snapshot(dst);
+}
+static void cap_contiguify(u32 dst, u32 numel, u32 src, const View *v) {
+    rb_begin(); rb_u32(dst); rb_u32(numel); rb_u32(src); rb_view(v); rb_emit(TRC_CONTIG);
+    if (g_exec && cpu_pool.bufs[dst] && cpu_pool.bufs[src]) {
+        u32 *d = cpu_pool.bufs[dst];
+        const u32 *sp = cpu_pool.bufs[src];
+        for (u32 t = 0; t < numel && (u64)t * 4 + 4 <= cpu_pool.sizes[dst]; t++) {
+            u32 rem = t;
+            i32 idx = v->offset;
+            int masked = 0;
+            for (i32 dd = (i32)v->shape.rank - 1; dd >= 0; dd--) {
+                u32 dim = v->shape.dims[dd];
+                u32 c = dim ? rem % dim : 0;
+                rem = dim ? rem / dim : 0;
+                if (v->has_mask && (c < v->mask_begin[dd] || c >= v->mask_end[dd])) masked = 1;
+                idx = (i32)((u32)idx + c * (u32)v->strides[dd]);
+            }
+            d[t] = (masked || idx < 0 || (u64)(u32)idx * 4 + 4 > cpu_pool.sizes[src]) ? 0u : sp[(u32)idx];
+        }
+    }
+    rec_snapshot(dst);
+}
+
 static void install_recorder(void) {
     g_orig = cpu_backend;
     cpu_backend.init = cap_init;
@@ -243,6 +339,8 @@ static void install_recorder(void) {
     cpu_backend.op_binary = cap_legacy_binary;
     cpu_backend.op_mm = cap_legacy_mm;
     cpu_backend.op_reduce = cap_legacy_reduce;
+    cpu_backend.buf_copy = cap_buf_copy;
+    cpu_backend.contiguify = cap_contiguify;
 }
 
 /* ---- workload helpers ---- */
@@ -275,7 +373,43 @@ static Term gen_tensor(TinyHVM *ctx, Shape s, u32 dtype, u32 dist, u64 seed, f32
 static Term unary(TinyHVM *ctx, u32 uop, Term a) { return thvm_op(ctx, uop, a, term_era()); }
 static Term binary(TinyHVM *ctx, u32 uop, Term a, Term b) { return thvm_op(ctx, uop, a, b); }
 
-static Term realize(TinyHVM *ctx, Term t) { return thvm_eval(ctx, t); }
+static Term realize(TinyHVM *ctx, Term t) {
+    Term r = thvm_eval(ctx, t);
+    if (getenv("CAP_DEBUG")) {
+        const View *v = term_view(ctx, r);
+        fprintf(stderr, "realize -> tag %u shape [", term_tag(r));
+        for (u32 d = 0; v && d < v->shape.rank; d++) fprintf(stderr, "%u%s", v->shape.dims[d], d + 1 < v->shape.rank ? "," : "");
+        fprintf(stderr, "]\n");
+    }
+    return r;
+}
+
+/* An eager view alias of a realized tensor with another shape (no kernel). */
+static Term alias_as(TinyHVM *ctx, Term r, Shape s) {
+    u8 saved = ctx->no_grad_alloc;
+    ctx->no_grad_alloc = 0;
+    Term a = thvm_reshape(ctx, r, s);
+    ctx->no_grad_alloc = saved;
+    return a;
+}
+
+/* Realize, then view the result with the intended shape. On this engine
+ * snapshot thvm_eval can return a reduce kernel's raw output ([M,1,N] for a
+ * matmul) without the trailing reshape, which later broadcasts wrongly. */
+static Term realize_as(TinyHVM *ctx, Term t, Shape s) {
+    Term r = realize(ctx, t);
+    const View *v = term_view(ctx, r);
+    int same = v && v->shape.rank == s.rank;
+    for (u32 d = 0; same && d < s.rank; d++) same = v->shape.dims[d] == s.dims[d];
+    if (same) return r;
+    /* an eager view alias of the realized buffer (src/ctx/init.c:626-653):
+     * a real tensor with the intended shape, no kernel */
+    u8 saved = ctx->no_grad_alloc;
+    ctx->no_grad_alloc = 0;
+    Term a = thvm_reshape(ctx, r, s);
+    ctx->no_grad_alloc = saved;
+    return a;
+}
 
 static void readback(TinyHVM *ctx, Term t) {
     f32 *h = thvm_to_host(ctx, t);
@@ -307,9 +441,395 @@ static void wl_fused(TinyHVM *ctx, u32 R, u32 C, int fwd, int bwd) {
     }
 }
 
+/* Dense matmul + bias + relu (linear_forward, src/nn/tensor_api.c:93-97 via
+ * thvm_tg_linear, src/nn/tg_tensor.c:34-66): y = relu(X @ W + b), X [M,K],
+ * W [K,N], b [N], all U(-1,1). Backward with the ones cotangent on y:
+ * G = (y > 0), dX = G @ W^T, dW = X^T @ G (transposes are permute views). */
+static void wl_linear(TinyHVM *ctx, u32 M, u32 K, u32 N, int bwd) {
+    Term X = gen_tensor(ctx, SHAPE(M, K), DTYPE_F32, TRC_GEN_UNIFORM, 3001, -1.f, 1.f);
+    Term W = gen_tensor(ctx, SHAPE(K, N), DTYPE_F32, TRC_GEN_UNIFORM, 3002, -1.f, 1.f);
+    Term b = gen_tensor(ctx, SHAPE(N), DTYPE_F32, TRC_GEN_UNIFORM, 3003, -1.f, 1.f);
+    rec_mark("linear.fwd");
+    Term y = unary(ctx, UOP_RELU, thvm_tg_linear(ctx, X, W, &b));
+    y = realize(ctx, y);
+    readback(ctx, y);
+    if (!bwd) return;
+    rec_mark("linear.bwd.dx");
+    Term G = binary(ctx, UOP_CMP, y, term_num_f32(0.0f));
+    Term dX = thvm_mm(ctx, G, thvm_permute(ctx, W, (u32[]){1, 0}, 2));
+    dX = realize(ctx, dX);
+    readback(ctx, dX);
+    rec_mark("linear.bwd.dw");
+    Term G2 = binary(ctx, UOP_CMP, y, term_num_f32(0.0f));
+    Term dW = thvm_mm(ctx, thvm_permute(ctx, X, (u32[]){1, 0}, 2), G2);
+    dW = realize(ctx, dW);
+    readback(ctx, dW);
+}
+
+/* ---- shared pieces of the network workloads ---- */
+
+/* Kaiming-uniform U(-sqrt(6/fan_in), +sqrt(6/fan_in)). */
+static Term kaiming_u(TinyHVM *ctx, Shape s, u32 fan_in, u64 seed) {
+    f32 bound = sqrtf(6.0f / (f32)fan_in);
+    return gen_tensor(ctx, s, DTYPE_F32, TRC_GEN_UNIFORM, seed, -bound, bound);
+}
+static Term zeros(TinyHVM *ctx, Shape s, u64 seed) {
+    return gen_tensor(ctx, s, DTYPE_F32, TRC_GEN_CONST, seed, 0.f, 0.f);
+}
+static u8 *labels_u8(u32 B, u64 seed) {
+    u8 *lab = malloc(B);
+    for (u32 i = 0; i < B; i++) lab[i] = (u8)thvm_gen_i32(TRC_GEN_INT, seed, i, 0.f, 10.f);
+    return lab;
+}
+static Term onehot_tensor(TinyHVM *ctx, const u8 *lab, u32 B, u32 C) {
+    f32 *oh = calloc((size_t)B * C, sizeof(f32));
+    for (u32 i = 0; i < B; i++) oh[i * C + lab[i]] = 1.0f;
+    Term t = thvm_tensor(ctx, oh, SHAPE(B, C));
+    free(oh);
+    return t;
+}
+static Term scalar_t(TinyHVM *ctx, f32 v) { return term_num_f32(v); }
+
+/* x [B,in] @ W [in,out] + b, then optional relu; realized. */
+static Term dense(TinyHVM *ctx, Term x, Term W, Term b, int relu, u32 B, u32 out) {
+    /* thvm_tg_linear's composition (src/nn/tg_tensor.c:56-66): mm, then the
+     * bias reshaped to [1,N] and expanded to [B,N]; it needs realized inputs
+     * to read shapes, so it is spelled out here for view inputs. */
+    Term y = thvm_mm(ctx, x, W);
+    y = binary(ctx, UOP_ADD, y, thvm_expand(ctx, thvm_reshape(ctx, b, SHAPE(1, out)), SHAPE(B, out)));
+    if (relu) y = unary(ctx, UOP_RELU, y);
+    return realize_as(ctx, y, SHAPE(B, out));
+}
+
+/* sum over axis 0 of [B,N] -> [N] */
+static Term colsum(TinyHVM *ctx, Term g, u32 N) {
+    return realize_as(ctx, thvm_sum_axes(ctx, g, (u32[]){0}, 1), SHAPE(N));
+}
+
+/* a [M,K] @ b [K,N], realized as [M,N] */
+static Term mm_as(TinyHVM *ctx, Term a, Term b, u32 M, u32 N) {
+    return realize_as(ctx, thvm_mm(ctx, a, b), SHAPE(M, N));
+}
+
+/* Backward of y = act(x @ W + b) for the ones-free chain: given dz (the grad
+ * of the pre-activation), dW = x^T @ dz, db = colsum(dz), dx = dz @ W^T. */
+typedef struct { Term dW, db, dx; } DenseGrads;
+static DenseGrads dense_bwd(TinyHVM *ctx, Term x, Term W, Term dz, u32 B, u32 in, u32 out, int need_dx) {
+    DenseGrads g;
+    g.dW = mm_as(ctx, thvm_permute(ctx, x, (u32[]){1, 0}, 2), dz, in, out);
+    g.db = colsum(ctx, dz, out);
+    g.dx = need_dx ? mm_as(ctx, dz, thvm_permute(ctx, W, (u32[]){1, 0}, 2), B, in) : term_era();
+    return g;
+}
+
+/* softmax(logits) as src/nn/softmax.c:3-23 composes it (row max, subtract,
+ * exp, row sum, divide), on realized tensors so no DUP is needed. */
+static Term softmax_rows(TinyHVM *ctx, Term logits, u32 B, u32 C) {
+    Term m = realize_as(ctx, thvm_rmax_axes(ctx, logits, (u32[]){1}, 1), SHAPE(B, 1));
+    Term e = realize_as(ctx, unary(ctx, UOP_EXP, binary(ctx, UOP_SUB, logits, thvm_expand(ctx, m, SHAPE(B, C)))),
+                        SHAPE(B, C));
+    Term ssum = realize_as(ctx, thvm_sum_axes(ctx, e, (u32[]){1}, 1), SHAPE(B, 1));
+    return realize_as(ctx, binary(ctx, UOP_DIV, e, thvm_expand(ctx, ssum, SHAPE(B, C))), SHAPE(B, C));
+}
+
+/* softmax cross-entropy gradient: (softmax(logits) - onehot) / B */
+static Term ce_grad(TinyHVM *ctx, Term logits, Term onehot, u32 B, u32 C) {
+    Term p = softmax_rows(ctx, logits, B, C);
+    Term d = binary(ctx, UOP_SUB, p, onehot);
+    return realize_as(ctx, binary(ctx, UOP_MUL, d, scalar_t(ctx, 1.0f / (f32)B)), SHAPE(B, C));
+}
+
+/* Nearest 2x upsample of [B,C,H,W] to [B,C,2H,2W] (view chain). */
+static Term up2(TinyHVM *ctx, Term t, u32 B, u32 C, u32 H, u32 W) {
+    Term r = thvm_reshape(ctx, t, shape_of((u32[]){B, C, H, 1, W, 1}, 6));
+    r = thvm_expand(ctx, r, shape_of((u32[]){B, C, H, 2, W, 2}, 6));
+    return thvm_reshape(ctx, r, shape_of((u32[]){B, C, 2 * H, 2 * W}, 4));
+}
+
+/* Max-pool 2x2 backward with the engine's routing rule (every tied maximum
+ * receives the gradient, src/interact/grad.c:405-425) fused with the relu
+ * mask of the pooled activation a: dz = up(dp) * (1 - (up(pool) > a)) * (a > 0). */
+static Term pool_relu_bwd(TinyHVM *ctx, Term dp, Term pooled, Term a, u32 B, u32 C, u32 H, u32 W) {
+    Term routed = binary(ctx, UOP_SUB, scalar_t(ctx, 1.0f),
+                         binary(ctx, UOP_CMP, up2(ctx, pooled, B, C, H / 2, W / 2), a));
+    Term g = binary(ctx, UOP_MUL, up2(ctx, dp, B, C, H / 2, W / 2), routed);
+    g = binary(ctx, UOP_MUL, g, binary(ctx, UOP_CMP, a, scalar_t(ctx, 0.0f)));
+    return realize_as(ctx, g, shape_of((u32[]){B, C, H, W}, 4));
+}
+
+/* Weight gradient of a stride-1 conv as one contraction:
+ * dW[co,ci,kh,kw] = sum_{b,oy,ox} xp[b,ci,oy+kh,ox+kw] * dz[b,co,oy,ox],
+ * with xp = x padded by `pad` (a masked pool view, src/nn/conv.c:20-388). */
+static Term conv_dw(TinyHVM *ctx, Term x, Term dz, u32 B, u32 Ci, u32 Co, u32 K, u32 pad, u32 OY, u32 OX) {
+    Term xp = x;
+    if (pad) xp = thvm_pad(ctx, x, (u32[]){0, 0, 0, 0, pad, pad, pad, pad}, 4);
+    Term P = thvm_pool(ctx, xp, (u32[]){K, K}, (u32[]){1, 1}, 2);          /* [B,Ci,OY,OX,K,K] */
+    P = thvm_permute(ctx, P, (u32[]){1, 4, 5, 0, 2, 3}, 6);                  /* [Ci,K,K,B,OY,OX] */
+    P = thvm_reshape(ctx, P, shape_of((u32[]){1, Ci, K, K, B, OY, OX}, 7));
+    P = thvm_expand(ctx, P, shape_of((u32[]){Co, Ci, K, K, B, OY, OX}, 7));
+    Term G = thvm_permute(ctx, dz, (u32[]){1, 0, 2, 3}, 4);                  /* [Co,B,OY,OX] */
+    G = thvm_reshape(ctx, G, shape_of((u32[]){Co, 1, 1, 1, B, OY, OX}, 7));
+    G = thvm_expand(ctx, G, shape_of((u32[]){Co, Ci, K, K, B, OY, OX}, 7));
+    Term s = thvm_sum_axes(ctx, binary(ctx, UOP_MUL, P, G), (u32[]){4, 5, 6}, 3);
+    return realize_as(ctx, s, shape_of((u32[]){Co, Ci, K, K}, 4));
+}
+
+/* The KxK spatial flip of W [Co,Ci,K,K] transposed to [Ci,Co,K,K]: an exact
+ * matmul with the exchange matrix (the engine has no flip view). */
+static Term flip_t(TinyHVM *ctx, Term W, u32 Co, u32 Ci, u32 K) {
+    u32 KK = K * K;
+    f32 *J = calloc((size_t)KK * KK, sizeof(f32));
+    for (u32 p = 0; p < KK; p++) J[(KK - 1 - p) * KK + p] = 1.0f;
+    Term Jt = thvm_tensor(ctx, J, SHAPE(KK, KK));
+    free(J);
+    Term Wf = mm_as(ctx, thvm_reshape(ctx, W, SHAPE(Co * Ci, KK)), Jt, Co * Ci, KK);
+    Term Wt = thvm_permute(ctx, thvm_reshape(ctx, Wf, shape_of((u32[]){Co, Ci, K, K}, 4)),
+                           (u32[]){1, 0, 2, 3}, 4);
+    return realize_as(ctx, Wt, shape_of((u32[]){Ci, Co, K, K}, 4));
+}
+
+/* Input gradient of a stride-1 conv with padding `pad`: the conv of dz with
+ * the flipped, transposed kernel and padding K-1-pad. */
+static Term conv_dx(TinyHVM *ctx, Term dz, Term W, u32 B, u32 Co, u32 Ci, u32 K, u32 pad, u32 H, u32 W_) {
+    Term Wt = flip_t(ctx, W, Co, Ci, K);
+    u32 p = K - 1 - pad;
+    return realize_as(ctx, thvm_conv2d(ctx, dz, Wt, term_era(), 1, (u32[]){1, 1}, (u32[]){p, p, p, p}),
+                      shape_of((u32[]){B, Ci, H, W_}, 4));
+}
+
+/* per-channel sum over [0,2,3] of [B,C,H,W] -> [C] */
+static Term chansum(TinyHVM *ctx, Term g, u32 C) {
+    return realize_as(ctx, thvm_sum_axes(ctx, g, (u32[]){0, 2, 3}, 3), SHAPE(C));
+}
+
+/* SGD through the engine's ASSIGN: p <- p - lr * g for every parameter. */
+static void sgd(TinyHVM *ctx, Term *params, Term *grads, u32 n, f32 lr) {
+    Term chain = term_era();
+    for (u32 i = 0; i < n; i++) {
+        Term upd = binary(ctx, UOP_SUB, params[i], binary(ctx, UOP_MUL, grads[i], scalar_t(ctx, lr)));
+        Term a = thvm_assign(ctx, params[i], upd);
+        chain = (i == 0) ? a : thvm_seq(ctx, chain, a);
+    }
+    thvm_eval(ctx, chain);
+}
+
+/* 2-layer MLP: x [B,784] ~ N(0,1), W1 [784,H], W2 [H,10] Kaiming-uniform, b = 0,
+ * relu, softmax cross-entropy (src/nn/loss.c:8-44); outputs loss, dW1, dW2. */
+static void wl_mlp(TinyHVM *ctx, u32 B, u32 IN, u32 H, u32 C) {
+    Term x = gen_tensor(ctx, SHAPE(B, IN), DTYPE_F32, TRC_GEN_NORMAL, 1001, 0.f, 1.f);
+    Term W1 = kaiming_u(ctx, SHAPE(IN, H), IN, 1002);
+    Term b1 = zeros(ctx, SHAPE(H), 1003);
+    Term W2 = kaiming_u(ctx, SHAPE(H, C), H, 1004);
+    Term b2 = zeros(ctx, SHAPE(C), 1005);
+    u8 *lab = labels_u8(B, 1006);
+    Term onehot = onehot_tensor(ctx, lab, B, C);
+    rec_mark("mlp.fwd");
+    Term h = dense(ctx, x, W1, b1, 1, B, H);
+    Term logits = dense(ctx, h, W2, b2, 0, B, C);
+    Term loss = realize(ctx, cross_entropy_loss(ctx, logits, lab, B, C));
+    readback(ctx, loss);
+    rec_mark("mlp.bwd");
+    Term d2 = ce_grad(ctx, logits, onehot, B, C);
+    DenseGrads g2 = dense_bwd(ctx, h, W2, d2, B, H, C, 1);
+    Term dz1 = realize_as(ctx, binary(ctx, UOP_MUL, g2.dx, binary(ctx, UOP_CMP, h, scalar_t(ctx, 0.0f))),
+                          SHAPE(B, H));
+    DenseGrads g1 = dense_bwd(ctx, x, W1, dz1, B, IN, H, 0);
+    readback(ctx, g1.dW);
+    readback(ctx, g2.dW);
+    free(lab);
+}
+
+/* LeNet-5 training step: x [B,1,28,28] ~ U(0,1); conv5x5 -> 6 (pad 2, so that
+ * the flatten is 16*5*5 = 400), relu, maxpool 2, conv5x5 -> 16, relu,
+ * maxpool 2, fc 400 -> 120 -> 84 -> 10, softmax cross-entropy; backward and
+ * SGD (lr 0.01) through ASSIGN. */
+static void wl_lenet(TinyHVM *ctx, u32 B, int steps) {
+    Term x = gen_tensor(ctx, shape_of((u32[]){B, 1, 28, 28}, 4), DTYPE_F32, TRC_GEN_UNIFORM, 4001, 0.f, 1.f);
+    Term W1 = kaiming_u(ctx, shape_of((u32[]){6, 1, 5, 5}, 4), 25, 4002);
+    Term b1 = zeros(ctx, SHAPE(6), 4003);
+    Term W2 = kaiming_u(ctx, shape_of((u32[]){16, 6, 5, 5}, 4), 150, 4004);
+    Term b2 = zeros(ctx, SHAPE(16), 4005);
+    Term W3 = kaiming_u(ctx, SHAPE(400, 120), 400, 4006);
+    Term b3 = zeros(ctx, SHAPE(120), 4007);
+    Term W4 = kaiming_u(ctx, SHAPE(120, 84), 120, 4008);
+    Term b4 = zeros(ctx, SHAPE(84), 4009);
+    Term W5 = kaiming_u(ctx, SHAPE(84, 10), 84, 4010);
+    Term b5 = zeros(ctx, SHAPE(10), 4011);
+    u8 *lab = labels_u8(B, 4012);
+    Term onehot = onehot_tensor(ctx, lab, B, 10);
+    Term params[10] = {W1, b1, W2, b2, W3, b3, W4, b4, W5, b5};
+    u32 keep = ctx->tensor_count;
+    for (int st = 0; st < steps; st++) {
+        rec_mark("lenet.step");
+        rec_mark("lenet.fwd");
+        Term a1 = realize_as(ctx, unary(ctx, UOP_RELU,
+                             thvm_conv2d(ctx, x, W1, b1, 1, (u32[]){1, 1}, (u32[]){2, 2, 2, 2})),
+                             shape_of((u32[]){B, 6, 28, 28}, 4));
+        Term p1 = realize_as(ctx, thvm_maxpool2d(ctx, a1, (u32[]){2, 2}, (u32[]){2, 2}),
+                             shape_of((u32[]){B, 6, 14, 14}, 4));
+        Term a2 = realize_as(ctx, unary(ctx, UOP_RELU,
+                             thvm_conv2d(ctx, p1, W2, b2, 1, (u32[]){1, 1}, (u32[]){0, 0, 0, 0})),
+                             shape_of((u32[]){B, 16, 10, 10}, 4));
+        Term p2 = realize_as(ctx, thvm_maxpool2d(ctx, a2, (u32[]){2, 2}, (u32[]){2, 2}),
+                             shape_of((u32[]){B, 16, 5, 5}, 4));
+        Term f = alias_as(ctx, p2, SHAPE(B, 400));
+        Term h3 = dense(ctx, f, W3, b3, 1, B, 120);
+        Term h4 = dense(ctx, h3, W4, b4, 1, B, 84);
+        Term logits = dense(ctx, h4, W5, b5, 0, B, 10);
+        Term loss = realize(ctx, cross_entropy_loss(ctx, logits, lab, B, 10));
+        readback(ctx, loss);
+        rec_mark("lenet.bwd");
+        Term d5 = ce_grad(ctx, logits, onehot, B, 10);
+        DenseGrads g5 = dense_bwd(ctx, h4, W5, d5, B, 84, 10, 1);
+        Term dz4 = realize_as(ctx, binary(ctx, UOP_MUL, g5.dx, binary(ctx, UOP_CMP, h4, scalar_t(ctx, 0.0f))),
+                              SHAPE(B, 84));
+        DenseGrads g4 = dense_bwd(ctx, h3, W4, dz4, B, 120, 84, 1);
+        Term dz3 = realize_as(ctx, binary(ctx, UOP_MUL, g4.dx, binary(ctx, UOP_CMP, h3, scalar_t(ctx, 0.0f))),
+                              SHAPE(B, 120));
+        DenseGrads g3 = dense_bwd(ctx, f, W3, dz3, B, 400, 120, 1);
+        Term dp2 = alias_as(ctx, g3.dx, shape_of((u32[]){B, 16, 5, 5}, 4));
+        Term dz2 = pool_relu_bwd(ctx, dp2, p2, a2, B, 16, 10, 10);
+        Term dW2 = conv_dw(ctx, p1, dz2, B, 6, 16, 5, 0, 10, 10);
+        Term db2 = chansum(ctx, dz2, 16);
+        Term dp1 = conv_dx(ctx, dz2, W2, B, 16, 6, 5, 0, 14, 14);
+        Term dz1 = pool_relu_bwd(ctx, dp1, p1, a1, B, 6, 28, 28);
+        Term dW1 = conv_dw(ctx, x, dz1, B, 1, 6, 5, 2, 28, 28);
+        Term db1 = chansum(ctx, dz1, 6);
+        rec_mark("lenet.sgd");
+        Term grads[10] = {dW1, db1, dW2, db2, g3.dW, g3.db, g4.dW, g4.db, g5.dW, g5.db};
+        sgd(ctx, params, grads, 10, 0.01f);
+        rec_mark("lenet.end");
+        for (u32 i = 0; i < 10; i++) readback(ctx, params[i]);
+        thvm_reset(ctx, keep);
+    }
+    free(lab);
+}
+
+/* Conv block: x [B,C,H,W] ~ N(0,1), conv3x3 C->C pad 1 (Kaiming-normal
+ * N(0, 2/(9C))), batchnorm train mode (gamma 1, beta 0, eps 1e-5,
+ * src/nn/batchnorm.c:35-87), relu, maxpool 2, loss = sum; backward dW and dX. */
+static void wl_convblock(TinyHVM *ctx, u32 B, u32 C, u32 H) {
+    u32 W_ = H;
+    Term x = gen_tensor(ctx, shape_of((u32[]){B, C, H, W_}, 4), DTYPE_F32, TRC_GEN_NORMAL, 5001, 0.f, 1.f);
+    Term Wc = gen_tensor(ctx, shape_of((u32[]){C, C, 3, 3}, 4), DTYPE_F32, TRC_GEN_NORMAL, 5002, 0.f,
+                         sqrtf(2.0f / (f32)(9 * C)));
+    Term gamma = gen_tensor(ctx, SHAPE(C), DTYPE_F32, TRC_GEN_CONST, 5003, 1.f, 1.f);
+    Term beta = zeros(ctx, SHAPE(C), 5004);
+    Term rmean = zeros(ctx, SHAPE(C), 5005);
+    Term rvar = gen_tensor(ctx, SHAPE(C), DTYPE_F32, TRC_GEN_CONST, 5006, 1.f, 1.f);
+    u32 N = B * H * W_;
+    rec_mark("conv.fwd");
+    Shape full = shape_of((u32[]){B, C, H, W_}, 4);
+    Shape cshape = shape_of((u32[]){1, C, 1, 1}, 4);
+    Term c = realize_as(ctx, thvm_conv2d(ctx, x, Wc, term_era(), 1, (u32[]){1, 1}, (u32[]){1, 1, 1, 1}), full);
+    /* batchnorm, train mode, as src/nn/batchnorm.c:35-87 computes it (mean and
+     * biased variance over [0,2,3], eps 1e-5, momentum 0.1, unbiased running
+     * variance), on realized tensors: the engine's own variance composition
+     * shares one lazy term on both sides of a MUL and does not terminate. */
+    f32 inv_n = 1.0f / (f32)N;
+    Term mean = realize_as(ctx, binary(ctx, UOP_MUL, thvm_sum_axes(ctx, c, (u32[]){0, 2, 3}, 3), scalar_t(ctx, inv_n)),
+                           cshape);
+    Term cen = realize_as(ctx, binary(ctx, UOP_SUB, c, thvm_expand(ctx, mean, full)), full);
+    Term var = realize_as(ctx, binary(ctx, UOP_MUL, thvm_sum_axes(ctx, binary(ctx, UOP_MUL, cen, cen), (u32[]){0, 2, 3}, 3),
+                                      scalar_t(ctx, inv_n)), cshape);
+    Term invstd = realize_as(ctx, binary(ctx, UOP_DIV, scalar_t(ctx, 1.0f),
+                                         unary(ctx, UOP_SQRT, binary(ctx, UOP_ADD, var, scalar_t(ctx, 1e-5f)))), cshape);
+    Term g4 = thvm_expand(ctx, thvm_reshape(ctx, gamma, cshape), full);
+    Term b4 = thvm_expand(ctx, thvm_reshape(ctx, beta, cshape), full);
+    Term xhat = realize_as(ctx, binary(ctx, UOP_MUL, cen, thvm_expand(ctx, invstd, full)), full);
+    Term yb = realize_as(ctx, binary(ctx, UOP_ADD, binary(ctx, UOP_MUL, xhat, g4), b4), full);
+    {
+        f32 mom = 0.1f, bessel = (f32)N / (f32)(N - 1);
+        Term m1 = alias_as(ctx, mean, SHAPE(C));
+        Term v1 = alias_as(ctx, var, SHAPE(C));
+        Term nrm = binary(ctx, UOP_ADD, binary(ctx, UOP_MUL, rmean, scalar_t(ctx, 1.0f - mom)),
+                          binary(ctx, UOP_MUL, m1, scalar_t(ctx, mom)));
+        Term nrv = binary(ctx, UOP_ADD, binary(ctx, UOP_MUL, rvar, scalar_t(ctx, 1.0f - mom)),
+                          binary(ctx, UOP_MUL, v1, scalar_t(ctx, mom * bessel)));
+        thvm_eval(ctx, thvm_seq(ctx, thvm_assign(ctx, rmean, nrm), thvm_assign(ctx, rvar, nrv)));
+    }
+    Term a = realize_as(ctx, unary(ctx, UOP_RELU, yb), full);
+    Term p = realize_as(ctx, thvm_maxpool2d(ctx, a, (u32[]){2, 2}, (u32[]){2, 2}),
+                        shape_of((u32[]){B, C, H / 2, W_ / 2}, 4));
+    Term loss = realize(ctx, thvm_sum_axes(ctx, p, (u32[]){0, 1, 2, 3}, 4));
+    readback(ctx, loss);
+    rec_mark("conv.bwd");
+    /* d loss / d p = 1; pool + relu backward */
+    Term ones = gen_tensor(ctx, shape_of((u32[]){B, C, H / 2, W_ / 2}, 4), DTYPE_F32, TRC_GEN_CONST, 5007, 1.f, 1.f);
+    Term dya = pool_relu_bwd(ctx, ones, p, a, B, C, H, W_);
+    /* batchnorm backward (gamma = g):
+     *   xhat = (c - mean) * invstd, dxhat = dy * g
+     *   dc = invstd / N * (N * dxhat - sum(dxhat) - xhat * sum(dxhat * xhat)) */
+    /* lazy terms are consumed by the eval that uses them: a fresh gamma view */
+    Term g4b = thvm_expand(ctx, thvm_reshape(ctx, gamma, cshape), full);
+    Term dxhat = realize_as(ctx, binary(ctx, UOP_MUL, dya, g4b), full);
+    Term s1 = realize_as(ctx, thvm_sum_axes(ctx, dxhat, (u32[]){0, 2, 3}, 3), cshape);
+    Term s2 = realize_as(ctx, thvm_sum_axes(ctx, binary(ctx, UOP_MUL, dxhat, xhat), (u32[]){0, 2, 3}, 3), cshape);
+    Term t = binary(ctx, UOP_SUB, binary(ctx, UOP_MUL, dxhat, scalar_t(ctx, (f32)N)), thvm_expand(ctx, s1, full));
+    t = binary(ctx, UOP_SUB, t, binary(ctx, UOP_MUL, xhat, thvm_expand(ctx, s2, full)));
+    Term dc = realize_as(ctx, binary(ctx, UOP_MUL, t,
+                                     thvm_expand(ctx, binary(ctx, UOP_MUL, invstd, scalar_t(ctx, 1.0f / (f32)N)), full)),
+                         full);
+    Term dgamma = realize_as(ctx, thvm_sum_axes(ctx, binary(ctx, UOP_MUL, dya, xhat), (u32[]){0, 2, 3}, 3), cshape);
+    Term dbeta = chansum(ctx, dya, C);
+    Term dW = conv_dw(ctx, x, dc, B, C, C, 3, 1, H, W_);
+    Term dx = conv_dx(ctx, dc, Wc, B, C, C, 3, 1, H, W_);
+    readback(ctx, dW);
+    readback(ctx, dx);
+    (void)dgamma; (void)dbeta;
+}
+
+/* Storage dtypes and casts (the operations of the engine's own dtype test,
+ * test/archive/test_dtype_cast.m, at edge values): f32 -> i32/u32/f16 casts
+ * (truncation, out-of-range, negative, NaN, f16 ties and overflow), i32/u32
+ * arithmetic and sums, f16 tensors in arithmetic and reductions. */
+static void wl_dtypes(TinyHVM *ctx) {
+    f32 xf[16] = {1.9f, -2.1f, 3.0f, 2147483648.0f, -3e9f, 1e19f, -1.0f, 4e9f,
+                  2049.0f, 65520.0f, 1e-6f, -0.0f, 0.5f, 1.00048828125f, 3.0e-5f, 0.0f};
+    xf[15] = nanf("");
+    Term x = thvm_tensor(ctx, xf, SHAPE(16));
+    rec_mark("dtypes.cast_i32");
+    readback(ctx, realize(ctx, thvm_cast(ctx, x, DTYPE_I32)));
+    rec_mark("dtypes.cast_u32");
+    readback(ctx, realize(ctx, thvm_cast(ctx, x, DTYPE_U32)));
+    rec_mark("dtypes.cast_f16");
+    readback(ctx, realize(ctx, thvm_cast(ctx, x, DTYPE_F16)));
+    i32 iv[4] = {3, -4, 100000, -7};
+    Term ti = thvm_tensor_i32(ctx, iv, SHAPE(4));
+    rec_mark("dtypes.i32");
+    readback(ctx, realize(ctx, thvm_cast(ctx, ti, DTYPE_F32)));
+    i32 bb[4] = {-3, 4, 5, 9};
+    Term tb = thvm_tensor_i32(ctx, bb, SHAPE(4));
+    readback(ctx, realize(ctx, binary(ctx, UOP_ADD, ti, tb)));
+    readback(ctx, realize(ctx, thvm_sum_axes(ctx, ti, (u32[]){0}, 1)));
+    i32 ones[16];
+    for (int i = 0; i < 16; i++) ones[i] = 1;
+    Term tones = thvm_tensor_i32(ctx, ones, SHAPE(16));
+    readback(ctx, realize(ctx, binary(ctx, UOP_ADD, thvm_cast(ctx, x, DTYPE_I32), tones)));
+    rec_mark("dtypes.u32");
+    u32 uv[4] = {7, 4000000000u, 0, 123};
+    Term tu = thvm_tensor_u32(ctx, uv, SHAPE(4));
+    readback(ctx, realize(ctx, binary(ctx, UOP_MUL, tu, scalar_t(ctx, 2.0f))));
+    readback(ctx, realize(ctx, thvm_sum_axes(ctx, tu, (u32[]){0}, 1)));
+    rec_mark("dtypes.f16");
+    u16 hv[300];
+    for (int i = 0; i < 300; i++) hv[i] = f32_to_f16_bits(0.01f * (f32)(i - 150));
+    Term th = thvm_tensor_typed(ctx, hv, SHAPE(300), DTYPE_F16);
+    readback(ctx, realize(ctx, binary(ctx, UOP_MUL, th, scalar_t(ctx, 3.0f))));
+    readback(ctx, realize(ctx, thvm_sum_axes(ctx, th, (u32[]){0}, 1)));
+    readback(ctx, realize(ctx, thvm_rmax_axes(ctx, th, (u32[]){0}, 1)));
+    readback(ctx, realize(ctx, thvm_cast(ctx, th, DTYPE_F32)));
+    Term seed = thvm_scalar_typed(ctx, 1.0f, DTYPE_F16);
+    readback(ctx, seed);
+}
+
 int main(int argc, char **argv) {
     int ai = 1;
-    if (ai < argc && strcmp(argv[ai], "-n") == 0) { g_exec = 0; ai++; }
+    while (ai < argc && argv[ai][0] == '-') {
+        if (strcmp(argv[ai], "-n") == 0) g_exec = 0;
+        else if (strcmp(argv[ai], "-r") == 0) g_read_data = 1;
+        ai++;
+    }
     if (argc - ai < 2) {
         fprintf(stderr, "usage: capture [-n] <workload> <out.trc> [sizes...]\n");
         return 2;
@@ -335,6 +855,16 @@ int main(int argc, char **argv) {
         wl_fused(ctx, nsz > 0 ? sz[0] : 64, nsz > 1 ? sz[1] : 256, 1, 0);
     } else if (strcmp(wl, "fused_bwd") == 0) {
         wl_fused(ctx, nsz > 0 ? sz[0] : 64, nsz > 1 ? sz[1] : 256, 0, 1);
+    } else if (strcmp(wl, "mlp") == 0) {
+        wl_mlp(ctx, nsz > 0 ? sz[0] : 64, nsz > 1 ? sz[1] : 784, nsz > 2 ? sz[2] : 128, nsz > 3 ? sz[3] : 10);
+    } else if (strcmp(wl, "lenet") == 0) {
+        wl_lenet(ctx, nsz > 0 ? sz[0] : 256, nsz > 1 ? (int)sz[1] : 1);
+    } else if (strcmp(wl, "convblock") == 0) {
+        wl_convblock(ctx, nsz > 0 ? sz[0] : 64, nsz > 1 ? sz[1] : 64, nsz > 2 ? sz[2] : 56);
+    } else if (strcmp(wl, "dtypes") == 0) {
+        wl_dtypes(ctx);
+    } else if (strcmp(wl, "linear") == 0) {
+        wl_linear(ctx, nsz > 0 ? sz[0] : 64, nsz > 1 ? sz[1] : 64, nsz > 2 ? sz[2] : 64, 1);
     } else {
         fprintf(stderr, "unknown workload %s\n", wl);
         return 2;

@@ -1,18 +1,35 @@
 #!/bin/sh
 # Regenerates the kernel-trace fixtures in this directory from the TinyHVM
-# engine (its CPU backend is the reference). Needs the engine sources at
+# engine, whose CPU backend is the reference. Needs the engine sources at
 # $REF (default /root/reference/src); builds oracle/_ref/capture first.
-#   exec mode (-x): kernels run on the engine's CPU backend; SNAPSHOT records
-#                   hold its outputs (the golden vectors).
-#   record mode:    kernels are recorded only (full-size workloads); inputs
-#                   are generator specs.
+# Exec mode: kernels run on the engine's CPU backend and each dispatch is
+# followed by a SNAPSHOT of its output (the golden vectors). Dispatches the
+# engine's interpreter cannot run without reading out of bounds (padded
+# convolutions) take their SNAPSHOT from the oracle and are marked so.
 set -e
 HERE=$(cd "$(dirname "$0")" && pwd)
 ROOT=$(cd "$HERE/../.." && pwd)
 make -s -C "$ROOT/oracle" ref
 CAP="$ROOT/oracle/_ref/capture"
 cd "$HERE"
-# fused elementwise + reduce: sum(relu(a*b+c), -1) and dA = (a*b+c > 0) * b
+rm -f ./*.trc
+# fused elementwise + reduce: y = sum(relu(a*b+c), -1), dA = (a*b+c > 0) * b
 $CAP fused fused_64x256.trc 64 256
 $CAP fused fused_3x1000.trc 3 1000
 $CAP fused fused_5x7.trc 5 7
+# dense matmul + bias + relu, backward dX and dW (K >= 256 takes the group reduce)
+$CAP linear linear_8x16x12.trc 8 16 12
+$CAP linear linear_33x300x40.trc 33 300 40
+# 2-layer MLP forward + backward at the benchmark's own size
+$CAP mlp mlp_64x784x128x10.trc 64 784 128 10
+# LeNet-5 training step (forward, backward, SGD through ASSIGN)
+$CAP lenet lenet_b2.trc 2 1
+# conv3x3 + batchnorm(train) + relu + maxpool block, forward + backward
+$CAP convblock convblock_2x4x8.trc 2 4 8
+# storage dtypes and casts
+$CAP dtypes dtypes.trc
+# the engine's FusedOp fallback path (lowering disabled)
+THVM_NO_LOWER=1 $CAP fused rs_fused_16x300.trc 16 300
+THVM_NO_LOWER=1 $CAP linear rs_linear_8x16x12.trc 8 16 12
+THVM_NO_LOWER=1 $CAP dtypes rs_dtypes.trc
+THVM_NO_LOWER=1 $CAP convblock rs_convblock_2x4x8.trc 2 4 8

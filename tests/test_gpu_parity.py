@@ -1,22 +1,31 @@
-"""GPU parity: every committed kernel trace is replayed through the HIP
-backend's C ABI and each dispatch's output is compared with the reference CPU
-backend's output recorded in the trace.
+"""GPU parity, through the HIP backend's C ABI, for every committed kernel trace.
 
-Tolerances: bit-exact for kernels that run in the
-reference's own order (serial mode: elementwise, index/view work, RMAX, and
-reductions a single lane walks in order) except for EXP/LOG, 1e-6 relative for
-those, and 1e-4 relative (with a floor at 1e-3 of the output's max) for
-reductions split across a workgroup, whose summation order differs."""
+Kernel-boundary parity: before each dispatch the GPU's actual input buffers
+are read back and the oracle (oracle/oracle.c, the CPU restatement of the
+engine's interpreter) runs the same kernel on them; the GPU output must match
+the oracle's under the kernel's tolerance class (the BASELINE north star):
+  - bit-exact: kernels a single lane evaluates in the reference's own order
+    (elementwise, index/view work, casts, RMAX), the FusedOp fallback and
+    buffer copies;
+  - 1e-6 relative per element (floor 1e-3 of the output's max): the same with
+    EXP or LOG, whose last bit may differ between GPU and host libm;
+  - 1e-4 normwise (max |x - y| <= 1e-4 max |y|): sums whose order differs
+    (split across a workgroup, or accumulated by matrix cores).
+End-to-end: the outputs the trace recorded from the reference CPU backend
+(SNAPSHOT records) must match the GPU run within 1e-3 normwise, the GPU's
+reordered sums propagating through whole training steps.
+"""
 import ctypes as C
-import sys
 
 import numpy as np
 import pytest
 
 from tests import tracetools as tt
-from tinyhvm_amd import _lib, abi
+from tinyhvm_amd import _lib, abi, trace
 
 pytestmark = pytest.mark.gpu
+
+DT = {0: np.float32, 1: np.uint16, 2: np.int32, 3: np.uint32}
 
 
 @pytest.fixture(scope="module")
@@ -27,67 +36,172 @@ def hip():
     L.thvm_hip_shutdown()
 
 
-def _has_transcendental(k):
+def _oracle():
+    ora = tt.oracle()
+    u64, vp = C.c_uint64, C.c_void_p
+    ora.ora_dispatch_uop.argtypes = [vp, u64, C.POINTER(vp), C.POINTER(u64), C.c_uint32,
+                                     C.POINTER(abi.UOpKernel)]
+    ora.ora_dispatch_rs.argtypes = [vp, u64, C.POINTER(vp), C.POINTER(u64),
+                                    C.POINTER(C.POINTER(abi.View)),
+                                    C.POINTER(C.POINTER(abi.ShapeTracker)), C.c_uint32,
+                                    C.POINTER(abi.FusedOp), C.c_uint32, C.POINTER(abi.Shape),
+                                    C.POINTER(abi.ReduceSpec), C.POINTER(C.c_uint32), C.c_uint32]
+    return ora
+
+
+def _has_transcendental_uop(k):
     return any(k.ops[i].type == abi.KOP_ALU and k.ops[i].imm.u in (abi.UOP_EXP, abi.UOP_LOG)
                for i in range(k.n_ops))
 
 
-def _kernel_tolerance(k):
+def uop_tolerance(k):
+    """(kind, rtol) for a lowered kernel, from how the backend runs it."""
     _src, mode, _vec = _lib.kernel_source(k)
-    if mode == 1:
-        has_sum = any(k.ops[i].type == abi.KOP_ACC and k.ops[i].imm.u != abi.UOP_RMAX
-                      for i in range(k.n_ops))
-        if has_sum:
-            return 1e-4
-    return 1e-6 if _has_transcendental(k) else 0.0
+    has_sum = any(k.ops[i].type == abi.KOP_ACC and k.ops[i].imm.u != abi.UOP_RMAX
+                  for i in range(k.n_ops))
+    if mode == 1 and has_sum:
+        return "norm", 1e-4
+    if _has_transcendental_uop(k):
+        return "elem", 1e-6
+    return "exact", 0.0
 
 
-def replay_and_compare(L, path):
-    be = L.thvm_hip_backend()
-    rp = tt.Replay(path, be)
-    results = []
-    last_kernel = None
-    last_rs = False
+def compare(got, want, dtype, kind, rtol):
+    if kind == "exact" or dtype != 0:
+        if got == want:
+            return True, "bit-exact"
+        g = np.frombuffer(got, dtype=np.uint8)
+        w = np.frombuffer(want, dtype=np.uint8)
+        return False, "differs in %d of %d bytes" % (int(np.sum(g != w)), len(w))
+    x = np.frombuffer(got, dtype=np.float32).astype(np.float64)
+    y = np.frombuffer(want, dtype=np.float32).astype(np.float64)
+    both_nan = np.isnan(x) & np.isnan(y)
+    x, y = np.where(both_nan, 0, x), np.where(both_nan, 0, y)
+    ymax = float(np.max(np.abs(y))) if y.size else 0.0
+    if kind == "norm":
+        err = float(np.max(np.abs(x - y))) / max(ymax, 1e-30)
+        return err <= rtol, "normwise %.2e (tol %.0e)" % (err, rtol)
+    scale = np.maximum(np.abs(y), 1e-3 * max(ymax, 1e-30))
+    err = float(np.max(np.abs(x - y) / scale)) if y.size else 0.0
+    return err <= rtol, "elementwise %.2e (tol %.0e)" % (err, rtol)
+
+
+class Host:
+    """Host copies of the device's buffers, read just before a dispatch."""
+
+    def __init__(self, read_fn, rp, sizes):
+        self.read_fn, self.rp, self.sizes = read_fn, rp, sizes
+
+    def read(self, trace_id):
+        live = self.rp.live(trace_id)
+        n = self.sizes.get(trace_id, 0)
+        buf = (C.c_uint8 * max(n, 4))()
+        if live and n:
+            self.read_fn(live, buf, n)
+        return buf, n if live else 0
+
+
+def _rs_args(r):
+    f = r.f
+    n = f["n_leaves"]
+    views = [v.to_c() for v in f["views"]]
+    sts = []
+    for s in f["sts"]:
+        if s is None:
+            sts.append(None)
+            continue
+        st = abi.ShapeTracker()
+        st.n_views = len(s)
+        for j, v in enumerate(s):
+            v.to_c(st.views[j])
+        sts.append(st)
+    vptr = (C.POINTER(abi.View) * max(n, 1))(*[C.pointer(v) for v in views])
+    sptr = (C.POINTER(abi.ShapeTracker) * max(n, 1))(*[C.pointer(s) if s is not None else None
+                                                      for s in sts])
+    ops = (abi.FusedOp * max(len(f["ops"]), 1))()
+    for j, (u, a, b, aux) in enumerate(f["ops"]):
+        ops[j].uop, ops[j].arg_a, ops[j].arg_b, ops[j].aux = u, a, b, aux
+    full = abi.Shape()
+    full.rank = f["full_rank"]
+    for d in range(8):
+        full.dims[d] = f["full_dims"][d]
+    red = None
+    if f["has_reduce"]:
+        red = abi.ReduceSpec()
+        rr = f["reduce"]
+        for d in range(8):
+            red.is_reduce[d] = rr["is_reduce"][d]
+            red.is_reduce2[d] = rr["is_reduce2"][d]
+        red.reduce_type, red.post_reduce_start = rr["reduce_type"], rr["post_reduce_start"]
+        red.n_post_leaves, red.reduce2_type = rr["n_post_leaves"], rr["reduce2_type"]
+        red.reduce2_start = rr["reduce2_start"]
+    dts = (C.c_uint32 * max(n, 1))(*f["leaf_dtypes"]) if f["has_dtypes"] else None
+    keep = (views, sts)
+    return keep, vptr, sptr, ops, full, red, dts
+
+
+def kernel_parity(backend, read_fn, sync_fn, ora, path, tol_fn=None):
+    """Replays `path` against `backend`, checking every dispatch against the
+    oracle on the same inputs and every SNAPSHOT against the reference."""
+    tol_fn = tol_fn or uop_tolerance
+    recs = trace.read_trace(path)
+    rp = tt.Replay(path, backend)
+    host = Host(read_fn, rp, {})
+    dtype_of = {}
+    kernel_results, e2e = [], []
     try:
-        for i in range(rp.n):
-            tag = rp.tag(i)
-            if tag == tt.TRC_SNAPSHOT:
-                tid, ref = rp.snapshot(i)
-                live = rp.live(tid)
-                buf = (C.c_uint8 * len(ref))()
-                L.thvm_hip_buf_read(live, buf, len(ref))
-                got = bytes(buf)
-                if last_rs or last_kernel is None:
-                    tol = 0.0
-                    dt = np.float32
+        for i, r in enumerate(recs):
+            if r.tag == trace.ALLOC:
+                host.sizes[r.f["id"]] = r.f["bytes"]
+            if r.tag in (trace.UOP, trace.RS):
+                out_id = r.f["out"]
+                out_buf, out_n = host.read(out_id)
+                leaves = [host.read(t) for t in r.f["leaf_bufs"]]
+                n = len(leaves)
+                lp = (C.c_void_p * max(n, 1))(*[C.cast(b, C.c_void_p) if m else None for b, m in leaves])
+                lb = (C.c_uint64 * max(n, 1))(*[m for _b, m in leaves])
+                if r.tag == trace.UOP:
+                    k = trace.to_uop_kernel(r)
+                    ora.ora_dispatch_uop(C.cast(out_buf, C.c_void_p), out_n, lp, lb, n, C.byref(k))
+                    kind, rtol = tol_fn(k)
+                    dtype = k.out_dtype
                 else:
-                    tol = _kernel_tolerance(last_kernel)
-                    dt = tt.dtype_of_kernel(last_kernel)
-                if tol == 0.0:
-                    ok = got == ref
-                    msg = "bit-exact" if ok else "differs (%d of %d bytes)" % (
-                        sum(a != b for a, b in zip(got, ref)), len(ref))
-                else:
-                    ok, msg = tt.close(np.frombuffer(got, dtype=dt), np.frombuffer(ref, dtype=dt), tol)
-                results.append((i, ok, msg))
-                print("  %s record %d: %s" % (path.split("/")[-1], i, msg), flush=True)
-            else:
-                if tag == tt.TRC_UOP:
-                    last_kernel = rp.kernel(i)
-                    last_rs = False
-                elif tag == tt.TRC_RS:
-                    last_rs = True
-                print("  %s record %d tag %d" % (path.split("/")[-1], i, tag), file=sys.stderr, flush=True)
+                    keep, vptr, sptr, ops, full, red, dts = _rs_args(r)
+                    ora.ora_dispatch_rs(C.cast(out_buf, C.c_void_p), out_n, lp, lb, vptr, sptr, n, ops,
+                                        len(r.f["ops"]), C.byref(full),
+                                        C.byref(red) if red is not None else None, dts,
+                                        r.f["out_dtype"])
+                    has_tr = any(o[0] in (abi.UOP_EXP, abi.UOP_LOG) for o in r.f["ops"])
+                    kind, rtol = ("elem", 1e-6) if has_tr else ("exact", 0.0)
+                    dtype = r.f["out_dtype"]
                 rp.run(i, i + 1)
-        assert L.thvm_hip_synchronize() == 0
+                dtype_of[out_id] = dtype
+                got, _ = host.read(out_id)
+                ok, msg = compare(bytes(got)[:out_n], bytes(out_buf)[:out_n], dtype, kind, rtol)
+                kernel_results.append((i, ok, msg))
+                print("  %s dispatch %d (%s): %s" % (path.split("/")[-1], i, kind, msg), flush=True)
+            elif r.tag == trace.SNAPSHOT:
+                got, n = host.read(r.f["id"])
+                dt = dtype_of.get(r.f["id"], 0)
+                ok, msg = compare(bytes(got)[:n], r.f["data"][:n], dt, "norm", 1e-3)
+                e2e.append((i, ok, msg))
+            else:
+                if r.tag == trace.COPY:
+                    dtype_of[r.f["dst"]] = dtype_of.get(r.f["src"], 0)
+                rp.run(i, i + 1)
+        assert sync_fn() == 0
     finally:
         rp.close()
-    return results
+    return kernel_results, e2e
 
 
 @pytest.mark.parametrize("path", tt.fixtures(), ids=lambda p: p.split("/")[-1])
 def test_trace_parity(hip, path):
-    res = replay_and_compare(hip, path)
-    assert res, "trace has no snapshots"
-    bad = [r for r in res if not r[1]]
-    assert not bad, bad
+    ora = _oracle()
+    kr, e2e = kernel_parity(hip.thvm_hip_backend(), hip.thvm_hip_buf_read, hip.thvm_hip_synchronize,
+                            ora, path)
+    assert kr, "trace has no dispatches"
+    bad = [r for r in kr if not r[1]]
+    assert not bad, "kernel parity: %s" % bad
+    bad_e2e = [r for r in e2e if not r[1]]
+    assert not bad_e2e, "end-to-end vs reference: %s" % bad_e2e

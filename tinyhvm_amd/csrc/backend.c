@@ -125,6 +125,8 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         return;
     }
     hipb.n_dispatch++;
+    pool_sync_device(out_buf);
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     if (!hipb.no_dense && dense_try_dispatch(out_buf, leaf_bufs, n_leaves, k)) {
         pool_mark_device_write(out_buf);
         hipb.n_dense++;
@@ -170,6 +172,8 @@ static void hb_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **leaf
     if (!hipb.initialized || !full_shape) return;
     HipbBuf *ob = pool_get(out_buf);
     if (!ob) return;
+    pool_sync_device(out_buf);
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     if (n_leaves > FUSE_MAX_LEAVES || n_ops > FUSE_MAX_OPS || out_dtype >= DTYPE_COUNT) {
         fprintf(stderr, "tinyhvm-hip: dispatch_kernel_rs: unsupported kernel size\n");
         return;
@@ -248,6 +252,8 @@ static void hb_contiguify(u32 dst_buf, u32 numel, u32 src_buf, const View *src_v
     if (!hipb.initialized || !src_view || numel == 0) return;
     HipbBuf *d = pool_get(dst_buf), *s = pool_get(src_buf);
     if (!d) return;
+    pool_sync_device(dst_buf);
+    pool_sync_device(src_buf);
     hipFunction_t fn = rtc_static_fn("thvm_contiguify");
     if (!fn) return;
     ContigArgs a;
@@ -266,6 +272,8 @@ static void hb_contiguify(u32 dst_buf, u32 numel, u32 src_buf, const View *src_v
 static void hb_buf_copy(u32 dst_buf, u32 src_buf, u64 nbytes) {
     HipbBuf *d = pool_get(dst_buf), *s = pool_get(src_buf);
     if (!d || !s || nbytes == 0) return;
+    pool_sync_device(dst_buf);
+    pool_sync_device(src_buf);
     u64 n = nbytes;
     if (n > d->cap) n = d->cap;
     if (n > s->cap) n = s->cap;

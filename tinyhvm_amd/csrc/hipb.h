@@ -52,6 +52,8 @@ typedef struct {
     u32 refcount;
     u8  live;
     u8  host_valid;   /* host mirror holds the current contents */
+    u8  dev_stale;    /* the mirror has not been copied to the device yet */
+    u32 mirror_bytes; /* bytes of the mirror that were written */
     void *host_mirror;
 } HipbBuf;
 
@@ -67,6 +69,7 @@ HipbBuf *pool_get(u32 id);
 void *pool_ptr(u32 id);
 u64   pool_bytes(u32 id);
 void  pool_mark_device_write(u32 id);
+void  pool_sync_device(u32 id);
 void  pool_write(u32 id, const void *data, u64 bytes);
 void  pool_read(u32 id, void *out, u64 bytes, int nosync);
 void  pool_stats(u64 *live_bytes, u64 *cached_bytes, u64 *n_mallocs);

@@ -432,11 +432,11 @@ static const char *U(Gen *g, u32 j, u32 v, char *buf) {
         snprintf(buf, 128, "f2u(%s)", Fx(g, j, v, t));
         return buf;
     }
-    if (o->kind == K_INV || g->V == 1) snprintf(buf, 64, "u%u", j);
+    if (o->kind == K_INV || g->V == 1) snprintf(buf, 64, "n%u", j);
     else if (o->kind == K_LIN) {
-        if (v == 0) snprintf(buf, 64, "u%u", j);
-        else snprintf(buf, 64, "(u%u+%uu)", j, v * o->step);
-    } else snprintf(buf, 64, "u%u_%u", j, v);
+        if (v == 0) snprintf(buf, 64, "n%u", j);
+        else snprintf(buf, 64, "(n%u+%uu)", j, v * o->step);
+    } else snprintf(buf, 64, "n%u_%u", j, v);
     return buf;
 }
 
@@ -445,7 +445,7 @@ static const char *G0(Gen *g, u32 j, i32 loop, char *buf) {
     const OpI *o = &g->oi[j];
     if ((i32)j == loop) snprintf(buf, 64, "0u");
     else if (o->ploop == loop && o->depth > 0) snprintf(buf, 64, "g%u", j);
-    else snprintf(buf, 64, "u%u", j);
+    else snprintf(buf, 64, "n%u", j);
     return buf;
 }
 
@@ -482,7 +482,7 @@ static void emit_decls(Gen *g) {
         if (t == KOP_ENDRANGE || t == KOP_STORE || t == KOP_ACC) continue;
         const char *ty = o->ft ? "float" : "u32";
         const char *z = o->ft ? "0.0f" : "0u";
-        char pf = o->ft ? 'f' : 'u';
+        char pf = o->ft ? 'f' : 'n';
         if (o->kind == K_VAR && g->V > 1) {
             sb_put(&g->sb, "  %s", ty);
             for (u32 v = 0; v < g->V; v++) sb_put(&g->sb, "%s %c%u_%u = %s", v ? "," : "", pf, i, v, z);
@@ -528,11 +528,11 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
     char a[128], b[128], fb[64];
     switch (op->type) {
     case KOP_GID:
-        if (g->mode == KG_MODE_SERIAL) sb_put(&g->sb, "    u%u = X0;\n", i);
-        else sb_put(&g->sb, "    u%u = gid;\n", i);
+        if (g->mode == KG_MODE_SERIAL) sb_put(&g->sb, "    n%u = X0;\n", i);
+        else sb_put(&g->sb, "    n%u = gid;\n", i);
         break;
     case KOP_CONST_U:
-        sb_put(&g->sb, "    u%u = %uu;\n", i, op->imm.u);
+        sb_put(&g->sb, "    n%u = %uu;\n", i, op->imm.u);
         break;
     case KOP_CONST_F:
         fmt_float(fb, op->imm.f);
@@ -542,8 +542,8 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
         u32 nv = single ? 1 : V;
         for (u32 v = 0; v < nv; v++) {
             char d[32];
-            if (single) snprintf(d, sizeof d, "u%u", i);
-            else snprintf(d, sizeof d, "u%u_%u", i, v);
+            if (single) snprintf(d, sizeof d, "n%u", i);
+            else snprintf(d, sizeof d, "n%u_%u", i, v);
             U(g, op->arg[0], v, a);
             if (op->type == KOP_IDX) {
                 U(g, op->arg[1], v, b);
@@ -672,7 +672,7 @@ static void emit_range_seq(Gen *g, u32 lo, u32 hi, int fast, int in_ploop);
 static void emit_seq_loop(Gen *g, u32 r, int fast, int in_ploop) {
     const KOp *op = &g->k->ops[r];
     u32 e = g->oi[r].end;
-    sb_put(&g->sb, "    for (u32 r%u = 0u; r%u < %uu; r%u++) {\n    u%u = r%u;\n", r, r, op->imm.u, r, r, r);
+    sb_put(&g->sb, "    for (u32 r%u = 0u; r%u < %uu; r%u++) {\n    n%u = r%u;\n", r, r, op->imm.u, r, r, r);
     emit_range_seq(g, r + 1, e, fast, in_ploop);
     sb_put(&g->sb, "    }\n");
 }
@@ -850,7 +850,7 @@ static void emit_group_loop(Gen *g, u32 r) {
     for (int pass = 0; pass < 2; pass++) {
         sb_put(&g->sb, pass == 0 ? "    if (ok_) {\n" : "    } else {\n");
         if (g->unroll > 1) sb_put(&g->sb, "    #pragma unroll %u\n", g->unroll);
-        sb_put(&g->sb, "    for (u32 q_ = lane; q_ < %uu; q_ += %uu) {\n    u%u = q_ * %uu;\n", nq, g->block, r, V);
+        sb_put(&g->sb, "    for (u32 q_ = lane; q_ < %uu; q_ += %uu) {\n    n%u = q_ * %uu;\n", nq, g->block, r, V);
         emit_range_seq(g, r + 1, e, pass == 0, 1);
         sb_put(&g->sb, "    }\n");
     }

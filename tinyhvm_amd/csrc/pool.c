@@ -14,11 +14,14 @@
  * by the host may be handed to a later dispatch without waiting: the stream
  * orders the old readers before the new writer.
  *
- * Host copies: writes up to one staging segment go through a pinned ring
- * (memcpy, then an async copy on the stream), so buf_write returns as soon as
- * the caller's memory has been consumed and never blocks on the GPU unless
- * the ring wraps onto a segment still in flight. Small writes also keep a
- * host mirror that buf_read_nosync serves until a kernel writes the buffer.
+ * Host copies: writes of at most 4 KiB are kept in a host mirror and reach
+ * the device only when something on the device first needs the buffer (a
+ * dispatch reading or writing it, a copy, a synchronous read): the engine
+ * writes many small metadata buffers (shape and axis tensors, scalars) that
+ * no kernel reads. Larger writes up to one staging segment go through a
+ * pinned ring (memcpy, then an async copy on the stream), so buf_write
+ * returns as soon as the caller's memory has been consumed and never blocks
+ * unless the ring wraps onto a segment still in flight.
  */
 #include <stdlib.h>
 #include <string.h>
@@ -167,6 +170,8 @@ u32 pool_alloc(u64 bytes) {
     b->cap = cap;
     b->refcount = 1;
     b->live = 1;
+    b->dev_stale = 0;
+    b->mirror_bytes = 0;
     P.live_bytes += cap;
     return id;
 }
@@ -185,6 +190,7 @@ static void release_block(HipbBuf *b) {
     b->live = 0;
     b->refcount = 0;
     b->host_valid = 0;
+    b->dev_stale = 0;
     free(b->host_mirror);
     b->host_mirror = NULL;
 }
@@ -236,6 +242,18 @@ void pool_mark_device_write(u32 id) {
     if (b) b->host_valid = 0;
 }
 
+static u8 *stage_reserve(u64 n);
+
+/* Copy a pending host mirror to the device (stream ordered). */
+void pool_sync_device(u32 id) {
+    HipbBuf *b = pool_get(id);
+    if (!b || !b->dev_stale) return;
+    u8 *st = stage_reserve(b->mirror_bytes);
+    memcpy(st, b->host_mirror, b->mirror_bytes);
+    HIPB_CHECK(hipMemcpyAsync(b->ptr, st, b->mirror_bytes, hipMemcpyHostToDevice, hipb.stream));
+    b->dev_stale = 0;
+}
+
 /* Reserve n bytes of pinned staging; waits only if the ring wraps onto a
  * segment whose copies are still in flight. */
 static u8 *stage_reserve(u64 n) {
@@ -262,6 +280,21 @@ void pool_write(u32 id, const void *data, u64 bytes) {
                 (unsigned long long)bytes, id, (unsigned long long)b->cap);
         bytes = b->cap;
     }
+    /* Defer small writes when the mirror then holds the whole buffer: a full
+     * overwrite, or a partial one over contents the mirror already holds. */
+    if (bytes <= POOL_MIRROR_MAX && (bytes >= b->bytes || b->host_valid)) {
+        if (!b->host_mirror) b->host_mirror = malloc(POOL_MIRROR_MAX);
+        if (b->host_mirror) {
+            memcpy(b->host_mirror, data, bytes);
+            if (bytes >= b->bytes) b->mirror_bytes = (u32)bytes;
+            b->host_valid = 1;
+            b->dev_stale = 1;
+            return;
+        }
+    }
+    pool_sync_device(id);
+    b->dev_stale = 0;
+    b->host_valid = 0;
     if (bytes <= STAGE_SEG_BYTES) {
         u8 *s = stage_reserve(bytes);
         memcpy(s, data, bytes);
@@ -269,15 +302,6 @@ void pool_write(u32 id, const void *data, u64 bytes) {
     } else {
         HIPB_CHECK(hipMemcpyAsync(b->ptr, data, bytes, hipMemcpyHostToDevice, hipb.stream));
         HIPB_CHECK(hipStreamSynchronize(hipb.stream));
-    }
-    if (bytes <= POOL_MIRROR_MAX && bytes == b->bytes) {
-        if (!b->host_mirror) b->host_mirror = malloc(POOL_MIRROR_MAX);
-        if (b->host_mirror) {
-            memcpy(b->host_mirror, data, bytes);
-            b->host_valid = 1;
-        }
-    } else {
-        b->host_valid = 0;
     }
 }
 
@@ -289,14 +313,18 @@ void pool_read(u32 id, void *out, u64 bytes, int nosync) {
         return;
     }
     u64 n = bytes < b->bytes ? bytes : b->bytes;
-    if (nosync && b->host_valid && n <= POOL_MIRROR_MAX) {
+    (void)nosync;
+    if (b->host_valid && n <= b->mirror_bytes) {
+        /* no device write since the host wrote it: the mirror is current */
         memcpy(out, b->host_mirror, n);
     } else if (n <= STAGE_SEG_BYTES) {
+        pool_sync_device(id);
         u8 *s = stage_reserve(n);
         HIPB_CHECK(hipMemcpyAsync(s, b->ptr, n, hipMemcpyDeviceToHost, hipb.stream));
         HIPB_CHECK(hipStreamSynchronize(hipb.stream));
         memcpy(out, s, n);
     } else {
+        pool_sync_device(id);
         HIPB_CHECK(hipMemcpyAsync(out, b->ptr, n, hipMemcpyDeviceToHost, hipb.stream));
         HIPB_CHECK(hipStreamSynchronize(hipb.stream));
     }

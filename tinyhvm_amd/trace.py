@@ -200,7 +200,7 @@ def _parse_payload(tag, p: bytes) -> dict:
     elif tag == PERSIST:
         f["max_buf"] = c.u32()
     elif tag == SNAPSHOT:
-        f["id"] = c.u32(); c.u32(); f["bytes"] = c.u64()
+        f["id"] = c.u32(); f["source"] = c.u32(); f["bytes"] = c.u64()
         f["data"] = c.raw(f["bytes"])
     elif tag == MARK:
         n = c.u32()
