@@ -1,0 +1,47 @@
+"""Matrix-core (f32 MFMA) contraction kernels on the GPU: every committed trace
+replayed with every contraction forced onto the matrix-core path (the
+fixtures are below the size heuristics) and with K split over 2 workgroups,
+under the same kernel-boundary parity as tests/test_gpu_parity.py; the
+matrix-core kernels fall in the 1e-4 normwise class."""
+import os
+
+import pytest
+
+from tests import tracetools as tt
+from tests.test_gpu_parity import _oracle, kernel_parity, uop_tolerance
+from tinyhvm_amd import _lib
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", params=["1", "2"], ids=["whole-K", "split-K"])
+def hip_dense(request):
+    saved = {k: os.environ.get(k) for k in ("THVM_HIP_DENSE_FORCE", "THVM_HIP_DENSE_SPLITS")}
+    os.environ["THVM_HIP_DENSE_FORCE"] = "1"
+    os.environ["THVM_HIP_DENSE_SPLITS"] = request.param
+    L = _lib.lib()
+    assert L.thvm_hip_init() == 0
+    yield L
+    L.thvm_hip_shutdown()
+    for k, v in saved.items():
+        if v is None:
+            os.environ.pop(k, None)
+        else:
+            os.environ[k] = v
+
+
+def dense_tolerance(k):
+    if _lib.dense_analyze(k):
+        return "norm", 1e-4
+    return uop_tolerance(k)
+
+
+@pytest.mark.parametrize("path", tt.fixtures(), ids=lambda p: p.split("/")[-1])
+def test_trace_parity_matrix_cores(hip_dense, path):
+    L = hip_dense
+    kr, e2e = kernel_parity(L.thvm_hip_backend(), L.thvm_hip_buf_read, L.thvm_hip_synchronize,
+                            _oracle(), path, tol_fn=dense_tolerance)
+    bad = [r for r in kr if not r[1]]
+    assert not bad, "kernel parity: %s" % bad
+    bad_e2e = [r for r in e2e if not r[1]]
+    assert not bad_e2e, "end-to-end vs reference: %s" % bad_e2e

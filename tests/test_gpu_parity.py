@@ -16,6 +16,7 @@ End-to-end: the outputs the trace recorded from the reference CPU backend
 reordered sums propagating through whole training steps.
 """
 import ctypes as C
+import os
 
 import numpy as np
 import pytest
@@ -30,10 +31,14 @@ DT = {0: np.float32, 1: np.uint16, 2: np.int32, 3: np.uint32}
 
 @pytest.fixture(scope="module")
 def hip():
+    # default heuristics: small contractions stay on the generated kernels
+    saved = os.environ.pop("THVM_HIP_DENSE_FORCE", None)
     L = _lib.lib()
     assert L.thvm_hip_init() == 0, "HIP backend failed to initialise"
     yield L
     L.thvm_hip_shutdown()
+    if saved is not None:
+        os.environ["THVM_HIP_DENSE_FORCE"] = saved
 
 
 def _oracle():
@@ -56,6 +61,8 @@ def _has_transcendental_uop(k):
 
 def uop_tolerance(k):
     """(kind, rtol) for a lowered kernel, from how the backend runs it."""
+    if _lib.dense_analyze(k):
+        return "norm", 1e-4
     _src, mode, _vec = _lib.kernel_source(k)
     has_sum = any(k.ops[i].type == abi.KOP_ACC and k.ops[i].imm.u != abi.UOP_RMAX
                   for i in range(k.n_ops))

@@ -50,6 +50,11 @@ static int hb_init(void) {
     hipb.dump_src = env_flag("THVM_HIP_DUMP");
     hipb.no_dense = env_flag("THVM_HIP_NO_DENSE");
     hipb.verbose = env_flag("THVM_HIP_VERBOSE");
+    hipb.dense_force = env_flag("THVM_HIP_DENSE_FORCE");
+    {
+        const char *e = getenv("THVM_HIP_DENSE_SPLITS");
+        hipb.dense_splits = e ? (u32)atoi(e) : 0;
+    }
     if (pool_init() != 0) return -1;
     if (rtc_init() != 0) return -1;
     hipb.initialized = 1;
@@ -59,6 +64,7 @@ static int hb_init(void) {
 static void hb_shutdown(void) {
     if (!hipb.initialized) return;
     HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    dense_shutdown();
     rtc_shutdown();
     pool_shutdown();
     HIPB_CHECK(hipStreamDestroy(hipb.stream));
@@ -101,6 +107,14 @@ int hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params)
         }
     }
     return 1;
+}
+
+int hipb_launch_grid(hipFunction_t fn, u32 gx, u32 gy, u32 bx, void **params) {
+    if ((u64)gx * bx >= (1ull << 32)) {
+        fprintf(stderr, "tinyhvm-hip: grid of %u groups exceeds the launch limit\n", gx);
+        return 0;
+    }
+    return hipb_launch(fn, gx, gy, 1, bx, params);
 }
 
 /* Grid for `blocks` workgroups of `bx` lanes: x holds up to 2^16 groups when
@@ -395,6 +409,30 @@ int thvm_hip_kernel_source(const UOpKernel *k, char *buf, u64 buflen, u32 *mode,
 }
 
 int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t errlen);
+
+int thvm_hip_dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits) {
+    static int env_read = 0;
+    if (!hipb.initialized && !env_read) {
+        hipb.dense_force = env_flag("THVM_HIP_DENSE_FORCE");
+        const char *e = getenv("THVM_HIP_DENSE_SPLITS");
+        hipb.dense_splits = e ? (u32)atoi(e) : 0;
+        env_read = 1;
+    }
+    return dense_analyze(k, M, N, K, splits);
+}
+
+int thvm_hip_dense_compile_check(const UOpKernel *k, char *errbuf, u64 errlen) {
+    char *src = dense_source(k);
+    if (!src) {
+        if (errbuf && errlen) snprintf(errbuf, errlen, "not a matrix-core contraction");
+        return -1;
+    }
+    char err[256] = {0};
+    long n = rtc_compile_only(src, err, sizeof err);
+    free(src);
+    if (n < 0 && errbuf && errlen) snprintf(errbuf, errlen, "%s", err);
+    return (int)n;
+}
 
 int thvm_hip_compile_check(const UOpKernel *k, char *errbuf, u64 errlen) {
     size_t cl = 0;

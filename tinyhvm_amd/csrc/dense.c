@@ -1,11 +1,802 @@
 /*
- * dense.c - recognizers that route dense UOpKernels to hand-written kernels.
+ * dense.c - routes contraction-shaped UOpKernels to f32 matrix-core kernels.
+ *
+ * The engine has no matmul or convolution op on this path: a matmul is
+ * EXPAND+MUL+SUM over [M,K,N] (src/ctx/init.c:555-612) and a convolution is
+ * a pool view times the weight, summed over (ci,kh,kw) of an 8-D domain
+ * (src/nn/conv.c:390-481). Both reach the backend as a KOp program of the
+ * form
+ *     acc = 0;  for r in [0,K): acc += P(gid, r) * Q(gid, r);  out[gid] = acc
+ * This file proves that shape and splits the output index into M and N.
+ *
+ * Digit analysis. Every index op of the program is rewritten as
+ *     c + sum_i a_i * digit_i,   digit = (x / div) % mod   (mod 0: none)
+ * of x = gid (range [0, total)) or x = r (range [0, K)). The lowerer builds
+ * coordinates exactly this way (MOD/DIV chains over GID and the RANGE
+ * counter, src/lower/_.c:828-876) and leaf indices as strided sums of them
+ * (src/lower/_.c:435-494). A program is a contraction when
+ *   - the loop body is one SUM ACC of MUL(P, Q), and nothing else escapes;
+ *   - the gid digits P depends on and the gid digits Q depends on are
+ *     disjoint, and together tile gid exactly (a mixed-radix decomposition);
+ *   - the output index is gid itself.
+ * Then out[gid_m(m) + gid_n(n)] = init + sum_r P(gid_m(m), r) * Q(gid_n(n), r)
+ * for m in [0,M), n in [0,N): a GEMM whose operands are *evaluated*, not
+ * loaded: the generated kernel runs P's and Q's own KOp code per element
+ * (bounds-checked loads, pad masks, fused elementwise prologues), so the
+ * operand values are exactly the engine's; only the summation order differs
+ * (matrix-core accumulation, tolerance 1e-4 normwise).
+ *
+ * Kernel: 256 lanes, 128x128 output tile, K staged 16 at a time through
+ * double-buffered LDS, each wavefront accumulating 64x64 with
+ * v_mfma_f32_32x32x2_f32 (2x2 blocks). Operand tiles are loaded with the
+ * lane order that is contiguous in memory for that operand (found from the
+ * digit form of its first load). Tiles are assigned so that each XCD works on
+ * a compact block of the tile grid (L2 reuse); long reductions are split
+ * over K across workgroups and summed in a second, fixed-order pass.
  */
+#include <stdlib.h>
+#include <string.h>
+
 #include "hipb.h"
 
+#define DG_MAX 8
+#define DENSE_MIN_MN 32
+#define DENSE_MIN_K 32
+#define DENSE_MIN_WORK (1ull << 21)
+
+static int op_type_is_float(KOpType t) {
+    return t == KOP_CONST_F || t == KOP_LOAD || t == KOP_ALU || t == KOP_ACC_INIT || t == KOP_MASK;
+}
+
+typedef struct { u8 var; u32 div, mod; } Digit;      /* var 0: gid, 1: r */
+typedef struct {
+    int ok;
+    u32 cst;
+    u32 n;
+    Digit d[DG_MAX];
+    u32 coef[DG_MAX];
+} Aff;
+
+typedef struct {
+    const UOpKernel *k;
+    u32 total, trip;
+    i32 range_op;
+    Aff *aff;
+} DCtx;
+
+static u64 var_range(const DCtx *c, u8 var) { return var ? c->trip : c->total; }
+
+static void digit_norm(const DCtx *c, Digit *d, int *is_zero) {
+    u64 r = var_range(c, d->var);
+    *is_zero = 0;
+    if ((u64)d->div >= r) { *is_zero = 1; return; }
+    if (d->mod && (u64)d->div * d->mod >= r) d->mod = 0;
+}
+
+static int aff_add_term(Aff *a, Digit d, u32 coef) {
+    if (coef == 0) return 1;
+    for (u32 i = 0; i < a->n; i++) {
+        if (a->d[i].var == d.var && a->d[i].div == d.div && a->d[i].mod == d.mod) {
+            a->coef[i] += coef;
+            if (a->coef[i] == 0) {
+                a->d[i] = a->d[a->n - 1];
+                a->coef[i] = a->coef[a->n - 1];
+                a->n--;
+            }
+            return 1;
+        }
+    }
+    if (a->n >= DG_MAX) return 0;
+    a->d[a->n] = d;
+    a->coef[a->n] = coef;
+    a->n++;
+    return 1;
+}
+
+static int is_single_digit(const Aff *a) { return a->ok && a->cst == 0 && a->n == 1 && a->coef[0] == 1; }
+
+static void analyze_aff(DCtx *c) {
+    const UOpKernel *k = c->k;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        Aff *o = &c->aff[i];
+        memset(o, 0, sizeof *o);
+        switch (op->type) {
+        case KOP_GID: {
+            Digit d = {0, 1, 0};
+            int z;
+            digit_norm(c, &d, &z);
+            o->ok = 1;
+            if (!z) aff_add_term(o, d, 1);
+            break;
+        }
+        case KOP_RANGE: {
+            if ((i32)i != c->range_op) break;
+            Digit d = {1, 1, 0};
+            int z;
+            digit_norm(c, &d, &z);
+            o->ok = 1;
+            if (!z) aff_add_term(o, d, 1);
+            break;
+        }
+        case KOP_CONST_U:
+            o->ok = 1;
+            o->cst = op->imm.u;
+            break;
+        case KOP_IDX: {
+            const Aff *a = &c->aff[op->arg[0]], *b = &c->aff[op->arg[1]];
+            if (!a->ok || !b->ok) break;
+            u32 s = op->imm.u;
+            o->ok = 1;
+            o->cst = a->cst * s + b->cst;
+            for (u32 t = 0; t < a->n && o->ok; t++) o->ok = aff_add_term(o, a->d[t], a->coef[t] * s);
+            for (u32 t = 0; t < b->n && o->ok; t++) o->ok = aff_add_term(o, b->d[t], b->coef[t]);
+            break;
+        }
+        case KOP_MOD: case KOP_DIV: {
+            const Aff *a = &c->aff[op->arg[0]];
+            u32 q = op->imm.u;
+            if (!a->ok) break;
+            if (q == 0) { o->ok = 1; break; }
+            if (a->n == 0) {
+                o->ok = 1;
+                o->cst = op->type == KOP_MOD ? a->cst % q : a->cst / q;
+                break;
+            }
+            if (!is_single_digit(a)) break;
+            Digit d = a->d[0];
+            if (op->type == KOP_MOD) {
+                if (d.mod == 0 || d.mod % q == 0) d.mod = q;
+                else if (q % d.mod == 0) { /* already smaller */ }
+                else break;
+            } else {
+                if (q == 1) { *o = *a; break; }
+                if (d.mod == 0) d.div *= q;
+                else if (d.mod % q == 0) { d.div *= q; d.mod /= q; }
+                else break;
+            }
+            int z;
+            digit_norm(c, &d, &z);
+            o->ok = 1;
+            if (!z) aff_add_term(o, d, 1);
+            break;
+        }
+        default:
+            break;
+        }
+    }
+}
+
+/* Marks the cone of op `root` (all ops it depends on). */
+static void mark_cone(const UOpKernel *k, u32 root, u8 *cone) {
+    u32 stack[KOP_MAX];
+    u32 sp = 0;
+    stack[sp++] = root;
+    while (sp) {
+        u32 i = stack[--sp];
+        if (cone[i]) continue;
+        cone[i] = 1;
+        const KOp *op = &k->ops[i];
+        int na = 0;
+        switch (op->type) {
+        case KOP_MOD: case KOP_DIV: case KOP_LOAD: na = 1; break;
+        case KOP_IDX: case KOP_MASK: case KOP_ALU: na = 2; break;
+        default: na = 0; break;
+        }
+        if (op->type == KOP_ALU) {
+            u32 u = op->imm.u;
+            if (u == UOP_NEG || u == UOP_EXP || u == UOP_LOG || u == UOP_RELU || u == UOP_CAST || u == UOP_SQRT)
+                na = 1;
+        }
+        for (int a = 0; a < na; a++)
+            if (op->arg[a] < i && sp < KOP_MAX) stack[sp++] = op->arg[a];
+    }
+}
+
+typedef struct {
+    int ok;
+    u32 M, N, K;
+    f32 init;
+    u8 coneP[KOP_MAX], coneQ[KOP_MAX];
+    u32 rootP, rootQ;
+    /* gid digits of each side, sorted by div descending */
+    u32 np, nq;
+    u32 pdiv[DG_MAX], pext[DG_MAX], qdiv[DG_MAX], qext[DG_MAX];
+    int p_kmajor, q_kmajor;       /* lanes along k when loading the tile */
+} Contraction;
+
+/* The gid digits an operand consumes: those of the integer values its float
+ * ops read (load indices, integers converted for ALU/MASK). Intermediate
+ * index ops (the raw GID, partial MOD/DIV chains) do not count. */
+static int add_digits(const DCtx *c, u32 arg, Digit *out, u32 *n, int *uses_r) {
+    if (op_type_is_float(c->k->ops[arg].type)) return 1;
+    const Aff *a = &c->aff[arg];
+    if (!a->ok) return 0;
+    for (u32 t = 0; t < a->n; t++) {
+        if (a->d[t].var == 1) { *uses_r = 1; continue; }
+        int dup = 0;
+        for (u32 j = 0; j < *n; j++)
+            if (out[j].div == a->d[t].div && out[j].mod == a->d[t].mod) dup = 1;
+        if (!dup) {
+            if (*n >= DG_MAX) return 0;
+            out[(*n)++] = a->d[t];
+        }
+    }
+    return 1;
+}
+
+static int collect_gdigits(const DCtx *c, const u8 *cone, Digit *out, u32 *n, int *uses_r) {
+    *n = 0;
+    *uses_r = 0;
+    for (u32 i = 0; i < c->k->n_ops; i++) {
+        if (!cone[i]) continue;
+        const KOp *op = &c->k->ops[i];
+        switch (op->type) {
+        case KOP_LOAD:
+            if (!add_digits(c, op->arg[0], out, n, uses_r)) return 0;
+            break;
+        case KOP_MASK:
+        case KOP_ALU:
+            if (!add_digits(c, op->arg[0], out, n, uses_r)) return 0;
+            if (!add_digits(c, op->arg[1], out, n, uses_r)) return 0;
+            break;
+        default:
+            break;
+        }
+    }
+    return 1;
+}
+
+/* Is the first load of the cone contiguous along r (k) rather than gid? */
+static int cone_kmajor(const DCtx *c, const u8 *cone) {
+    for (u32 i = 0; i < c->k->n_ops; i++) {
+        if (!cone[i] || c->k->ops[i].type != KOP_LOAD) continue;
+        const Aff *a = &c->aff[c->k->ops[i].arg[0]];
+        if (!a->ok) return 1;
+        u32 coef_r = 0, coef_g = 0, best_r = 0xFFFFFFFFu, best_g = 0xFFFFFFFFu;
+        for (u32 t = 0; t < a->n; t++) {
+            if (a->d[t].var == 1 && a->d[t].div < best_r) { best_r = a->d[t].div; coef_r = a->coef[t]; }
+            if (a->d[t].var == 0 && a->d[t].div < best_g) { best_g = a->d[t].div; coef_g = a->coef[t]; }
+        }
+        if (coef_r == 1) return 1;
+        if (coef_g == 1) return 0;
+        return 1;
+    }
+    return 1;
+}
+
+static int cmp_digit_div_desc(const void *x, const void *y) {
+    const Digit *a = x, *b = y;
+    return a->div < b->div ? 1 : (a->div > b->div ? -1 : 0);
+}
+
+static int dense_debug(void) {
+    static int v = -1;
+    if (v < 0) { const char *e = getenv("THVM_HIP_DENSE_DEBUG"); v = e && e[0] == '1'; }
+    return v;
+}
+#define REJECT(why) do { if (dense_debug()) fprintf(stderr, "dense: not a contraction: %s\n", why); return 0; } while (0)
+
+static int recognize(const UOpKernel *k, Contraction *ct) {
+    memset(ct, 0, sizeof *ct);
+    if (k->n_ops == 0 || k->n_ops > KOP_MAX) REJECT("line 2");
+    /* one top-level loop, no nesting */
+    i32 R = -1;
+    u32 E = 0;
+    int depth = 0;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        if (k->ops[i].type == KOP_RANGE) {
+            if (depth || R >= 0) REJECT("line 9");
+            R = (i32)i;
+            depth = 1;
+        } else if (k->ops[i].type == KOP_ENDRANGE) {
+            if (!depth) REJECT("line 13");
+            depth = 0;
+            E = i;
+        }
+    }
+    if (R < 0 || depth) REJECT("line 18");
+    /* the body: exactly one ACC, SUM, of a MUL */
+    i32 acc_op = -1;
+    for (u32 i = (u32)R + 1; i < E; i++) {
+        const KOp *op = &k->ops[i];
+        if (op->type == KOP_STORE || op->type == KOP_ACC_INIT) REJECT("line 23");
+        if (op->type == KOP_ACC) {
+            if (acc_op >= 0 || op->imm.u == UOP_RMAX) REJECT("line 25");
+            acc_op = (i32)i;
+        }
+    }
+    if (acc_op < 0) REJECT("line 29");
+    u32 tgt = k->ops[acc_op].arg[0];
+    if (k->ops[tgt].type != KOP_ACC_INIT || tgt > (u32)R) REJECT("line 31");
+    const KOp *mul = &k->ops[k->ops[acc_op].arg[1]];
+    if (mul->type != KOP_ALU || mul->imm.u != UOP_MUL) REJECT("line 33");
+    ct->rootP = mul->arg[0];
+    ct->rootQ = mul->arg[1];
+    ct->init = k->ops[tgt].imm.f;
+    /* after the loop: one STORE of the accumulator at index gid; no other
+     * side effects anywhere */
+    i32 store = -1;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        if (k->ops[i].type == KOP_STORE) {
+            if (store >= 0 || i < E) REJECT("line 42");
+            store = (i32)i;
+        }
+    }
+    if (store < 0 || k->ops[store].arg[1] != tgt) REJECT("line 46");
+
+    DCtx c = {k, k->local_size > 0 ? k->grid[0] : k->grid[0] * k->grid[1] * k->grid[2],
+              k->ops[R].imm.u, R, NULL};
+    if (c.total == 0 || c.trip == 0) REJECT("line 50");
+    Aff aff[KOP_MAX];
+    c.aff = aff;
+    analyze_aff(&c);
+    /* output index must be exactly gid */
+    const Aff *sa = &aff[k->ops[store].arg[0]];
+    if (!sa->ok || sa->cst != 0 || sa->n != 1 || sa->coef[0] != 1 || sa->d[0].var != 0 ||
+        sa->d[0].div != 1 || sa->d[0].mod != 0)
+        REJECT("line 58");
+    mark_cone(k, ct->rootP, ct->coneP);
+    mark_cone(k, ct->rootQ, ct->coneQ);
+    /* every op of the loop body belongs to P, Q, or is the MUL/ACC */
+    for (u32 i = (u32)R + 1; i < E; i++) {
+        if ((i32)i == acc_op || &k->ops[i] == mul) continue;
+        if (!ct->coneP[i] && !ct->coneQ[i]) REJECT("line 64");
+    }
+    /* no float op is shared between the operands */
+    for (u32 i = 0; i < k->n_ops; i++)
+        if (ct->coneP[i] && ct->coneQ[i] && op_type_is_float(k->ops[i].type)) REJECT("line 68");
+    /* the accumulator itself must not feed the operands */
+    if (ct->coneP[tgt] || ct->coneQ[tgt]) REJECT("line 70");
+    Digit gp[DG_MAX], gq[DG_MAX];
+    u32 np = 0, nq = 0;
+    int pr = 0, qr = 0;
+    if (!collect_gdigits(&c, ct->coneP, gp, &np, &pr)) REJECT("line 74");
+    if (!collect_gdigits(&c, ct->coneQ, gq, &nq, &qr)) REJECT("line 75");
+    if (np == 0 || nq == 0) REJECT("line 76");
+    /* disjoint, and together a mixed-radix tiling of [0,total) */
+    Digit all[2 * DG_MAX];
+    u32 na = 0;
+    for (u32 i = 0; i < np; i++) all[na++] = gp[i];
+    for (u32 i = 0; i < nq; i++) {
+        for (u32 j = 0; j < np; j++)
+            if (gp[j].div == gq[i].div) REJECT("line 83");
+        all[na++] = gq[i];
+    }
+    qsort(all, na, sizeof(Digit), cmp_digit_div_desc);
+    u64 expect_div = 1;
+    for (i32 i = (i32)na - 1; i >= 0; i--) {
+        if (all[i].div != expect_div) REJECT("line 89");
+        if (i > 0) {
+            if (all[i].mod == 0) REJECT("line 91");
+            expect_div *= all[i].mod;
+        } else if (all[i].mod != 0) {
+            REJECT("line 94");
+        }
+    }
+    qsort(gp, np, sizeof(Digit), cmp_digit_div_desc);
+    qsort(gq, nq, sizeof(Digit), cmp_digit_div_desc);
+    u64 M = 1, N = 1;
+    for (u32 i = 0; i < np; i++) {
+        u32 e = gp[i].mod ? gp[i].mod : (u32)((c.total + gp[i].div - 1) / gp[i].div);
+        ct->pdiv[i] = gp[i].div;
+        ct->pext[i] = e;
+        M *= e;
+    }
+    for (u32 i = 0; i < nq; i++) {
+        u32 e = gq[i].mod ? gq[i].mod : (u32)((c.total + gq[i].div - 1) / gq[i].div);
+        ct->qdiv[i] = gq[i].div;
+        ct->qext[i] = e;
+        N *= e;
+    }
+    if (M * N != c.total || M > 0xFFFFFFFFull || N > 0xFFFFFFFFull) REJECT("line 112");
+    ct->np = np;
+    ct->nq = nq;
+    ct->M = (u32)M;
+    ct->N = (u32)N;
+    ct->K = c.trip;
+    ct->p_kmajor = cone_kmajor(&c, ct->coneP);
+    ct->q_kmajor = cone_kmajor(&c, ct->coneQ);
+    ct->ok = 1;
+    return 1;
+}
+
+/* ---------------- code generation ---------------- */
+
+typedef struct { char *p; size_t n, cap; } DSB;
+static void dsb_put(DSB *s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+#include <stdarg.h>
+static void dsb_put(DSB *s, const char *fmt, ...) {
+    va_list ap;
+    for (;;) {
+        size_t room = s->cap - s->n;
+        va_start(ap, fmt);
+        int w = vsnprintf(s->p ? s->p + s->n : NULL, s->p ? room : 0, fmt, ap);
+        va_end(ap);
+        if (w < 0) return;
+        if (s->p && (size_t)w < room) { s->n += (size_t)w; return; }
+        size_t nc = s->cap ? s->cap * 2 : 32768;
+        while (nc < s->n + (size_t)w + 1) nc *= 2;
+        char *np = realloc(s->p, nc);
+        if (!np) return;
+        s->p = np;
+        s->cap = nc;
+    }
+}
+
+static void emit_params(DSB *s, u32 n_leaves) {
+    for (u32 b = 0; b <= n_leaves; b++) dsb_put(s, "%schar* p%u", b ? ", " : "", b);
+    for (u32 b = 0; b <= n_leaves; b++) dsb_put(s, ", u32 c%u", b);
+}
+static void emit_args(DSB *s, u32 n_leaves) {
+    for (u32 b = 0; b <= n_leaves; b++) dsb_put(s, "%sp%u", b ? ", " : "", b);
+    for (u32 b = 0; b <= n_leaves; b++) dsb_put(s, ", c%u", b);
+}
+
+/* flat index over one side's digits -> the gid contribution */
+static void emit_gid_fn(DSB *s, const char *name, u32 n, const u32 *div, const u32 *ext) {
+    dsb_put(s, "__device__ __forceinline__ u32 %s(u32 x) {\n  u32 g = 0u;\n", name);
+    for (i32 i = (i32)n - 1; i >= 0; i--) {
+        if (i > 0) dsb_put(s, "  g += (x %% %uu) * %uu; x /= %uu;\n", ext[i], div[i], ext[i]);
+        else dsb_put(s, "  g += x * %uu;\n", div[i]);
+    }
+    dsb_put(s, "  return g;\n}\n");
+}
+
+typedef struct {
+    char name[48];
+    u32 splits;
+    u32 kchunk;
+    u32 tiles_m, tiles_n;
+} GemmPlan;
+
+#define BM 128
+#define BN 128
+#define BK 16
+
+static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const GemmPlan *pl, char *err,
+                             size_t errlen) {
+    DSB s = {0};
+    dsb_put(&s, "%s\n", kgen_prelude());
+    dsb_put(&s, "typedef float f32x16 __attribute__((ext_vector_type(16)));\n");
+    emit_gid_fn(&s, "gid_m", ct->np, ct->pdiv, ct->pext);
+    emit_gid_fn(&s, "gid_n", ct->nq, ct->qdiv, ct->qext);
+    static char body[1 << 16];
+    for (int side = 0; side < 2; side++) {
+        const u8 *cone = side ? ct->coneQ : ct->coneP;
+        u32 root = side ? ct->rootQ : ct->rootP;
+        if (kgen_emit_cone(k, cone, "gid", "r", body, sizeof body) < 0) {
+            snprintf(err, errlen, "operand cone cannot be emitted");
+            free(s.p);
+            return NULL;
+        }
+        dsb_put(&s, "__device__ __forceinline__ float operand_%c(u32 gid, u32 r, ", side ? 'q' : 'p');
+        emit_params(&s, k->n_leaves);
+        dsb_put(&s, ") {\n%s", body);
+        if (op_type_is_float(k->ops[root].type)) dsb_put(&s, "  return f%u;\n}\n", root);
+        else dsb_put(&s, "  return (float)n%u;\n}\n", root);
+    }
+    const u32 M = ct->M, N = ct->N, K = ct->K;
+    const u32 tiles = pl->tiles_m * pl->tiles_n;
+    dsb_put(&s,
+            "extern \"C\" __global__ __launch_bounds__(256) void %s(", pl->name);
+    emit_params(&s, k->n_leaves);
+    dsb_put(&s, ", float* ws) {\n");
+    dsb_put(&s,
+            "  constexpr u32 BM = %u, BN = %u, BK = %u, LDA = BM + 4, LDB = BN + 4;\n"
+            "  constexpr u32 M = %uu, N = %uu, K = %uu, TM = %uu, TN = %uu, TILES = %uu, KCH = %uu;\n",
+            BM, BN, BK, M, N, K, pl->tiles_m, pl->tiles_n, tiles, pl->kchunk);
+    dsb_put(&s,
+            "  __shared__ float As[2][BK * LDA];\n"
+            "  __shared__ float Bs[2][BK * LDB];\n"
+            "  const u32 tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;\n"
+            "  /* XCD-aware tile order: workgroups go round-robin over 8 XCDs; give\n"
+            "   * each XCD a compact block of tiles so their operand panels share L2 */\n"
+            "  u32 bid = blockIdx.x, tile = bid;\n"
+            "  if (TILES %% 8u == 0u) tile = (bid %% 8u) * (TILES / 8u) + bid / 8u;\n"
+            "  u32 tm, tn;\n"
+            "  { const u32 G = 8u; const u32 grp = tile / (G * TN), first = grp * G;\n"
+            "    const u32 gsz = (TM - first) < G ? (TM - first) : G;\n"
+            "    tm = first + (tile %% (G * TN)) %% gsz; tn = (tile %% (G * TN)) / gsz; }\n"
+            "  const u32 m0 = tm * BM, n0 = tn * BN;\n"
+            "  const u32 kbeg = blockIdx.y * KCH;\n"
+            "  const u32 kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
+            "  float ra[8], rb[8];\n");
+    /* loader maps: 8 elements per thread of a 128x16 tile */
+    const char *map_p = ct->p_kmajor
+        ? "const u32 kk = tid & 15u, mm = (tid >> 4) + e * 16u;"
+        : "const u32 mm = tid & 127u, kk = (tid >> 7) + e * 2u;";
+    const char *map_q = ct->q_kmajor
+        ? "const u32 kk = tid & 15u, nn = (tid >> 4) + e * 16u;"
+        : "const u32 nn = tid & 127u, kk = (tid >> 7) + e * 2u;";
+    dsb_put(&s, "  auto loadA = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < 8u; e++) { %s\n"
+                "      const u32 m = m0 + mm, k = k0 + kk;\n"
+                "      ra[e] = (m < M && k < kend) ? operand_p(gid_m(m), k, ", map_p);
+    emit_args(&s, k->n_leaves);
+    dsb_put(&s, ") : 0.0f; }\n  };\n");
+    dsb_put(&s, "  auto loadB = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < 8u; e++) { %s\n"
+                "      const u32 n = n0 + nn, k = k0 + kk;\n"
+                "      rb[e] = (n < N && k < kend) ? operand_q(gid_n(n), k, ", map_q);
+    emit_args(&s, k->n_leaves);
+    dsb_put(&s, ") : 0.0f; }\n  };\n");
+    dsb_put(&s, "  auto storeA = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < 8u; e++) { %s As[buf][kk * LDA + mm] = ra[e]; }\n  };\n", map_p);
+    dsb_put(&s, "  auto storeB = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < 8u; e++) { %s Bs[buf][kk * LDB + nn] = rb[e]; }\n  };\n", map_q);
+    dsb_put(&s,
+            "  f32x16 acc00 = {0}, acc01 = {0}, acc10 = {0}, acc11 = {0};\n"
+            "  const u32 wm = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;\n"
+            "  const u32 nst = (kend > kbeg) ? (kend - kbeg + BK - 1u) / BK : 0u;\n"
+            "  if (nst > 0u) { loadA(kbeg); loadB(kbeg); storeA(0u); storeB(0u); }\n"
+            "  __syncthreads();\n"
+            "  for (u32 st = 0; st < nst; st++) {\n"
+            "    const u32 cur = st & 1u;\n"
+            "    if (st + 1u < nst) { loadA(kbeg + (st + 1u) * BK); loadB(kbeg + (st + 1u) * BK); }\n"
+            "    const float* A = As[cur];\n"
+            "    const float* B = Bs[cur];\n"
+            "    #pragma unroll\n"
+            "    for (u32 kk = 0; kk < BK; kk += 2u) {\n"
+            "      const u32 kr = kk + (lane >> 5);\n"
+            "      const float a0 = A[kr * LDA + wm + (lane & 31u)];\n"
+            "      const float a1 = A[kr * LDA + wm + 32u + (lane & 31u)];\n"
+            "      const float b0 = B[kr * LDB + wn + (lane & 31u)];\n"
+            "      const float b1 = B[kr * LDB + wn + 32u + (lane & 31u)];\n"
+            "      acc00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc00, 0, 0, 0);\n"
+            "      acc01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc01, 0, 0, 0);\n"
+            "      acc10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc10, 0, 0, 0);\n"
+            "      acc11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc11, 0, 0, 0);\n"
+            "    }\n"
+            "    if (st + 1u < nst) { storeA(cur ^ 1u); storeB(cur ^ 1u); }\n"
+            "    __syncthreads();\n"
+            "  }\n");
+    /* epilogue: D[i][j] of a 32x32 block sits in lane j + 32*((i/4)%%2), register (i%%4) + 4*(i/8) */
+    dsb_put(&s,
+            "  #pragma unroll\n"
+            "  for (u32 blk = 0; blk < 4u; blk++) {\n"
+            "    const f32x16 c = blk == 0u ? acc00 : (blk == 1u ? acc01 : (blk == 2u ? acc10 : acc11));\n"
+            "    const u32 bm = wm + (blk >> 1) * 32u, bn = wn + (blk & 1u) * 32u;\n"
+            "    const u32 n = n0 + bn + (lane & 31u);\n"
+            "    #pragma unroll\n"
+            "    for (u32 v = 0; v < 16u; v++) {\n"
+            "      const u32 m = m0 + bm + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3u);\n"
+            "      if (m < M && n < N) {\n");
+    if (pl->splits > 1) {
+        dsb_put(&s, "        ws[((unsigned long long)blockIdx.y * M + m) * N + n] = c[v];\n");
+    } else {
+        char fb[64];
+        u32 bits;
+        memcpy(&bits, &ct->init, 4);
+        snprintf(fb, sizeof fb, "__uint_as_float(0x%08xu)", bits);
+        const char *st = k->out_dtype == DTYPE_F16 ? "st_f16" : k->out_dtype == DTYPE_I32 ? "st_i32"
+                         : k->out_dtype == DTYPE_U32 ? "st_u32" : "st_f32";
+        dsb_put(&s, "        %s(p0, c0, gid_m(m) + gid_n(n), %s + c[v]);\n", st, fb);
+    }
+    dsb_put(&s, "      }\n    }\n  }\n}\n");
+    if (pl->splits > 1) {
+        char fb[64];
+        u32 bits;
+        memcpy(&bits, &ct->init, 4);
+        snprintf(fb, sizeof fb, "__uint_as_float(0x%08xu)", bits);
+        const char *st = k->out_dtype == DTYPE_F16 ? "st_f16" : k->out_dtype == DTYPE_I32 ? "st_i32"
+                         : k->out_dtype == DTYPE_U32 ? "st_u32" : "st_f32";
+        dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
+                    "  const unsigned long long t = (unsigned long long)blockIdx.x * 256u + threadIdx.x;\n"
+                    "  if (t >= %lluull) return;\n"
+                    "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
+                    "  float a = 0.0f;\n"
+                    "  for (u32 s = 0; s < %uu; s++) a = a + ws[(unsigned long long)s * %lluull + t];\n"
+                    "  %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
+                pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
+    }
+    return s.p;
+}
+
+/* ---------------- plan cache and dispatch ---------------- */
+
+typedef struct {
+    u64 key;
+    KOp *ops;
+    u32 n_ops, n_leaves;
+    u32 meta[5 + FUSE_MAX_LEAVES];
+    int is_dense;                 /* 0: not a contraction (negative cache) */
+    hipModule_t mod;
+    hipFunction_t fn, fn_sum;
+    GemmPlan plan;
+    u32 M, N;
+} DenseEntry;
+
+static struct {
+    DenseEntry *tab;
+    u32 cap, n;
+    u32 ws_buf;
+    u64 ws_bytes;
+} D;
+
+static void meta_of(const UOpKernel *k, u32 *m) {
+    memset(m, 0, (5 + FUSE_MAX_LEAVES) * sizeof(u32));
+    m[0] = k->grid[0]; m[1] = k->grid[1]; m[2] = k->grid[2];
+    m[3] = k->local_size; m[4] = k->out_dtype;
+    for (u32 i = 0; i < k->n_leaves && i < FUSE_MAX_LEAVES; i++) m[5 + i] = k->leaf_dtypes[i];
+}
+
+static DenseEntry *lookup(u64 key, const UOpKernel *k) {
+    if (!D.tab) return NULL;
+    u32 mk = D.cap - 1;
+    for (u32 p = (u32)key & mk, probes = 0; probes < D.cap; p = (p + 1) & mk, probes++) {
+        DenseEntry *e = &D.tab[p];
+        if (!e->key) return NULL;
+        if (e->key != key || e->n_ops != k->n_ops || e->n_leaves != k->n_leaves) continue;
+        u32 m[5 + FUSE_MAX_LEAVES];
+        meta_of(k, m);
+        if (memcmp(m, e->meta, sizeof m) == 0 && memcmp(e->ops, k->ops, (size_t)k->n_ops * sizeof(KOp)) == 0)
+            return e;
+    }
+    return NULL;
+}
+
+static DenseEntry *insert(u64 key, const UOpKernel *k) {
+    if (!D.tab || (D.n + 1) * 2 > D.cap) {
+        u32 nc = D.cap ? D.cap * 2 : 256;
+        DenseEntry *nt = calloc(nc, sizeof(DenseEntry));
+        if (!nt) return NULL;
+        for (u32 i = 0; i < D.cap; i++) {
+            if (!D.tab[i].key) continue;
+            u32 p = (u32)D.tab[i].key & (nc - 1);
+            while (nt[p].key) p = (p + 1) & (nc - 1);
+            nt[p] = D.tab[i];
+        }
+        free(D.tab);
+        D.tab = nt;
+        D.cap = nc;
+    }
+    u32 p = (u32)key & (D.cap - 1);
+    while (D.tab[p].key) p = (p + 1) & (D.cap - 1);
+    DenseEntry *e = &D.tab[p];
+    memset(e, 0, sizeof *e);
+    e->key = key;
+    e->n_ops = k->n_ops;
+    e->n_leaves = k->n_leaves;
+    meta_of(k, e->meta);
+    e->ops = malloc((size_t)k->n_ops * sizeof(KOp));
+    if (e->ops) memcpy(e->ops, k->ops, (size_t)k->n_ops * sizeof(KOp));
+    D.n++;
+    return e;
+}
+
+static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
+    memset(pl, 0, sizeof *pl);
+    pl->tiles_m = (ct->M + BM - 1) / BM;
+    pl->tiles_n = (ct->N + BN - 1) / BN;
+    u32 tiles = pl->tiles_m * pl->tiles_n;
+    /* split K until the grid covers the 256 CUs about twice, keeping at
+     * least 512 elements of K per split */
+    u32 splits = 1;
+    while (tiles * splits < 512 && ct->K / (splits * 2) >= 512 && splits < 256) splits *= 2;
+    if (hipb.dense_splits) splits = hipb.dense_splits;
+    pl->splits = splits;
+    u32 kch = (ct->K + splits - 1) / splits;
+    kch = (kch + BK - 1) / BK * BK;
+    pl->kchunk = kch;
+    pl->splits = (ct->K + kch - 1) / kch;
+    snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));
+}
+
+/* Contraction analysis without a device: returns 1 and fills M/N/K when the
+ * kernel would take the matrix-core path. */
+int dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits) {
+    Contraction ct;
+    if (!recognize(k, &ct)) return 0;
+    GemmPlan pl;
+    make_plan(&ct, &pl, 0);
+    /* Matrix cores pay off for reasonably sized operands spread over at
+     * least a quarter of the CUs; smaller contractions stay on the
+     * generated reduce kernels (one workgroup or lane per output). */
+    if (!hipb.dense_force &&
+        (ct.M < DENSE_MIN_MN || ct.N < DENSE_MIN_MN || ct.K < DENSE_MIN_K ||
+         (u64)ct.M * ct.N * ct.K < DENSE_MIN_WORK || pl.tiles_m * pl.tiles_n * pl.splits < 64))
+        return 0;
+    if (M) *M = ct.M;
+    if (N) *N = ct.N;
+    if (K) *K = ct.K;
+    if (splits) *splits = pl.splits;
+    return 1;
+}
+
+/* Generated source of the matrix-core kernel (no device needed). */
+char *dense_source(const UOpKernel *k) {
+    Contraction ct;
+    if (!dense_analyze(k, NULL, NULL, NULL, NULL) || !recognize(k, &ct)) return NULL;
+    GemmPlan pl;
+    make_plan(&ct, &pl, uop_signature(k));
+    char err[128];
+    return gen_gemm_source(k, &ct, &pl, err, sizeof err);
+}
+
 int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
-    (void)out_buf; (void)leaf_bufs; (void)n_leaves; (void)k;
-    return 0;
+    u64 key = uop_signature(k) ^ 0xD5E5E5E5D5E5E5E5ull;
+    if (!key) key = 1;
+    DenseEntry *e = lookup(key, k);
+    if (!e) {
+        e = insert(key, k);
+        if (!e) return 0;
+        Contraction ct;
+        u32 M, N, K, sp;
+        if (!dense_analyze(k, &M, &N, &K, &sp) || !recognize(k, &ct)) return 0;
+        make_plan(&ct, &e->plan, uop_signature(k));
+        char err[256] = {0};
+        char *src = gen_gemm_source(k, &ct, &e->plan, err, sizeof err);
+        if (!src) {
+            fprintf(stderr, "tinyhvm-hip: dense kernel generation failed: %s\n", err);
+            return 0;
+        }
+        if (hipb.dump_src) fprintf(stderr, "---- dense kernel ----\n%s\n", src);
+        if (!rtc_build_module(src, &e->mod, err, sizeof err)) {
+            fprintf(stderr, "tinyhvm-hip: dense kernel build failed: %s\n", err);
+            free(src);
+            return 0;
+        }
+        free(src);
+        if (hipModuleGetFunction(&e->fn, e->mod, e->plan.name) != hipSuccess) return 0;
+        if (e->plan.splits > 1) {
+            char nm[64];
+            snprintf(nm, sizeof nm, "%s_sum", e->plan.name);
+            if (hipModuleGetFunction(&e->fn_sum, e->mod, nm) != hipSuccess) return 0;
+        }
+        e->M = ct.M;
+        e->N = ct.N;
+        e->is_dense = 1;
+        if (hipb.verbose)
+            fprintf(stderr, "tinyhvm-hip: dense %s M=%u N=%u K=%u splits=%u\n", e->plan.name, ct.M, ct.N,
+                    ct.K, e->plan.splits);
+    }
+    if (!e->is_dense) return 0;
+    /* split-K workspace */
+    float *ws = NULL;
+    if (e->plan.splits > 1) {
+        u64 need = (u64)e->plan.splits * e->M * e->N * sizeof(float);
+        if (need > D.ws_bytes) {
+            if (D.ws_buf) pool_free(D.ws_buf);
+            D.ws_buf = pool_alloc(need);
+            D.ws_bytes = D.ws_buf ? need : 0;
+            if (!D.ws_buf) return 0;
+        }
+        ws = pool_ptr(D.ws_buf);
+    }
+    void *ptrs[FUSE_MAX_LEAVES + 1];
+    u32 counts[FUSE_MAX_LEAVES + 1];
+    void *params[2 * (FUSE_MAX_LEAVES + 1) + 1];
+    u32 nb = k->n_leaves + 1;
+    ptrs[0] = pool_ptr(out_buf);
+    counts[0] = (u32)(pool_bytes(out_buf) / (k->out_dtype == DTYPE_F16 ? 2 : 4));
+    for (u32 i = 0; i < k->n_leaves; i++) {
+        void *lp = i < n_leaves ? pool_ptr(leaf_bufs[i]) : NULL;
+        ptrs[i + 1] = lp;
+        u64 b = lp ? pool_bytes(leaf_bufs[i]) : 0;
+        counts[i + 1] = (u32)(b / (k->leaf_dtypes[i] == DTYPE_F16 ? 2 : 4));
+    }
+    for (u32 b = 0; b < nb; b++) {
+        params[b] = &ptrs[b];
+        params[nb + b] = &counts[b];
+    }
+    params[2 * nb] = &ws;
+    u32 tiles = e->plan.tiles_m * e->plan.tiles_n;
+    if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, 256, params)) return 0;
+    if (e->plan.splits > 1) {
+        void *p2[] = {&ptrs[0], &counts[0], &ws};
+        u64 mn = (u64)e->M * e->N;
+        if (!hipb_launch_grid(e->fn_sum, (u32)((mn + 255) / 256), 1, 256, p2)) return 0;
+    }
+    return 1;
 }
 
 void dense_reset_stats(void) {}
+
+void dense_shutdown(void) {
+    if (D.tab) {
+        for (u32 i = 0; i < D.cap; i++) {
+            if (!D.tab[i].key) continue;
+            if (D.tab[i].is_dense) HIPB_CHECK(hipModuleUnload(D.tab[i].mod));
+            free(D.tab[i].ops);
+        }
+        free(D.tab);
+    }
+    memset(&D, 0, sizeof D);
+}

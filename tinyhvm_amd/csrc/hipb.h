@@ -38,6 +38,8 @@ typedef struct {
     int dump_src;            /* THVM_HIP_DUMP: print generated HIP source */
     int no_dense;            /* THVM_HIP_NO_DENSE: skip dense recognizers */
     int verbose;             /* THVM_HIP_VERBOSE */
+    int dense_force;         /* THVM_HIP_DENSE_FORCE: matrix cores for every contraction */
+    u32 dense_splits;        /* THVM_HIP_DENSE_SPLITS: fixed split-K factor (0: chosen) */
     u64 n_dispatch, n_compile, n_cache_hit, n_dense;
     hipModule_t static_mod;  /* precompiled kernels */
 } HipbState;
@@ -90,6 +92,9 @@ typedef struct {
 int  kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen);
 void kgen_free(KGenResult *r);
 int  kgen_validate(const UOpKernel *k, char *err, size_t errlen);
+const char *kgen_prelude(void);
+int  kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
+                    char *out, size_t outlen);
 
 /* ---------------- rtc / cache ---------------- */
 typedef struct {
@@ -109,13 +114,22 @@ void rtc_shutdown(void);
 KCacheEntry *rtc_lookup(u64 key, const UOpKernel *k);
 KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k);
 hipFunction_t rtc_static_fn(const char *name);
+/* Compile HIP source and load it; returns the module (0 on failure). */
+int  rtc_build_module(const char *src, hipModule_t *mod, char *err, size_t errlen);
+/* Compile only (no device needed); returns the code size or -1. */
+long rtc_compile_only(const char *src, char *err, size_t errlen);
 u64  uop_signature(const UOpKernel *k);
 
 /* ---------------- dense paths ---------------- */
 int  dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
+int  dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits);
+char *dense_source(const UOpKernel *k);
 void dense_reset_stats(void);
+void dense_shutdown(void);
 
 /* ---------------- launch helpers ---------------- */
 int  hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params);
+/* gx*gy workgroups of bx lanes; gx may exceed the 32-bit work-item limit */
+int  hipb_launch_grid(hipFunction_t fn, u32 gx, u32 gy, u32 bx, void **params);
 
 #endif /* HIPB_H */

@@ -789,6 +789,91 @@ static const char *PRELUDE =
 "  return s;\n"
 "}\n";
 
+const char *kgen_prelude(void) { return PRELUDE; }
+
+/* Scalar straight-line code for the ops flagged in `cone` (in op order), as
+ * the body of a device function: GID reads `gid_expr`, the top-level RANGE
+ * reads `r_expr`. Buffers are the kernel parameters p<i>/c<i>. Returns the
+ * number of bytes written, or -1 if an op cannot be emitted this way. */
+int kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
+                   char *out, size_t outlen) {
+    SB sb = {0};
+    char a[96], b[96], fb[64];
+    for (u32 i = 0; i < k->n_ops; i++) {
+        if (!cone[i]) continue;
+        const KOp *op = &k->ops[i];
+        int fa = op_is_float(k->ops[op->arg[0]].type), fbt = op_is_float(k->ops[op->arg[1]].type);
+#define UA(x, ft) ((ft) ? (snprintf(a, sizeof a, "f2u(f%u)", (x)), a) : (snprintf(a, sizeof a, "n%u", (x)), a))
+        switch (op->type) {
+        case KOP_GID: sb_put(&sb, "  const u32 n%u = %s;\n", i, gid_expr); break;
+        case KOP_RANGE: sb_put(&sb, "  const u32 n%u = %s;\n", i, r_expr); break;
+        case KOP_CONST_U: sb_put(&sb, "  const u32 n%u = %uu;\n", i, op->imm.u); break;
+        case KOP_CONST_F: fmt_float(fb, op->imm.f); sb_put(&sb, "  const float f%u = %s;\n", i, fb); break;
+        case KOP_MOD: case KOP_DIV:
+            if (op->imm.u == 0) sb_put(&sb, "  const u32 n%u = 0u;\n", i);
+            else sb_put(&sb, "  const u32 n%u = %s %c %uu;\n", i, UA(op->arg[0], fa),
+                        op->type == KOP_MOD ? '%' : '/', op->imm.u);
+            break;
+        case KOP_IDX: {
+            char t[96];
+            snprintf(t, sizeof t, "%s", UA(op->arg[0], fa));
+            if (fbt) snprintf(b, sizeof b, "f2u(f%u)", op->arg[1]);
+            else snprintf(b, sizeof b, "n%u", op->arg[1]);
+            sb_put(&sb, "  const u32 n%u = %s * %uu + %s;\n", i, t, op->imm.u, b);
+            break;
+        }
+        case KOP_LOAD: {
+            u32 bi = op->imm.u;
+            if (bi > k->n_leaves) { sb_put(&sb, "  const float f%u = 0.0f;\n", i); break; }
+            u32 dt = bi == 0 ? k->out_dtype : k->leaf_dtypes[bi - 1];
+            sb_put(&sb, "  const float f%u = %s(p%u, c%u, %s);\n", i, dt_ld(dt), bi, bi, UA(op->arg[0], fa));
+            break;
+        }
+        case KOP_MASK: {
+            char x[96], y[96];
+            if (fa) snprintf(x, sizeof x, "f%u", op->arg[0]); else snprintf(x, sizeof x, "(float)n%u", op->arg[0]);
+            if (fbt) snprintf(y, sizeof y, "f%u", op->arg[1]); else snprintf(y, sizeof y, "(float)n%u", op->arg[1]);
+            sb_put(&sb, "  const float f%u = (%s != 0.0f) ? %s : 0.0f;\n", i, x, y);
+            break;
+        }
+        case KOP_ALU: {
+            char x[96], y[96];
+            if (fa) snprintf(x, sizeof x, "f%u", op->arg[0]); else snprintf(x, sizeof x, "((float)n%u)", op->arg[0]);
+            if (fbt) snprintf(y, sizeof y, "f%u", op->arg[1]); else snprintf(y, sizeof y, "((float)n%u)", op->arg[1]);
+            switch (op->imm.u) {
+            case UOP_ADD: sb_put(&sb, "  const float f%u = %s + %s;\n", i, x, y); break;
+            case UOP_SUB: sb_put(&sb, "  const float f%u = %s - %s;\n", i, x, y); break;
+            case UOP_MUL: sb_put(&sb, "  const float f%u = %s * %s;\n", i, x, y); break;
+            case UOP_DIV: sb_put(&sb, "  const float f%u = (%s != 0.0f) ? (%s / %s) : 0.0f;\n", i, y, x, y); break;
+            case UOP_MAX: sb_put(&sb, "  const float f%u = (%s > %s) ? %s : %s;\n", i, x, y, x, y); break;
+            case UOP_CMP: sb_put(&sb, "  const float f%u = (%s > %s) ? 1.0f : 0.0f;\n", i, x, y); break;
+            case UOP_NEG: sb_put(&sb, "  const float f%u = -%s;\n", i, x); break;
+            case UOP_RELU: sb_put(&sb, "  const float f%u = (%s > 0.0f) ? %s : 0.0f;\n", i, x, x); break;
+            case UOP_EXP: sb_put(&sb, "  const float f%u = expf(%s);\n", i, x); break;
+            case UOP_LOG: sb_put(&sb, "  const float f%u = logf(%s);\n", i, x); break;
+            case UOP_SQRT: sb_put(&sb, "  const float f%u = sqrtf(%s);\n", i, x); break;
+            case UOP_CAST: sb_put(&sb, "  const float f%u = cast_f(%s, %uu);\n", i, x, op->arg[2]); break;
+            default: sb_put(&sb, "  const float f%u = %s;\n", i, x); break;
+            }
+            break;
+        }
+        default:
+            free(sb.p);
+            return -1;
+        }
+#undef UA
+    }
+    if (!sb.p) {
+        if (outlen) out[0] = 0;
+        return 0;
+    }
+    size_t n = strlen(sb.p);
+    if (n + 1 > outlen) { free(sb.p); return -1; }
+    memcpy(out, sb.p, n + 1);
+    free(sb.p);
+    return (int)n;
+}
+
 static void emit_params(Gen *g) {
     u32 nb = g->k->n_leaves + 1;
     for (u32 b = 0; b < nb; b++) sb_put(&g->sb, "%schar* p%u", b ? ", " : "", b);

@@ -174,6 +174,28 @@ static char *compile_source(const char *src, size_t *code_len, char *err, size_t
     return code;
 }
 
+int rtc_build_module(const char *src, hipModule_t *mod, char *err, size_t errlen) {
+    size_t cs = 0;
+    char *code = compile_source(src, &cs, err, errlen);
+    if (!code) return 0;
+    hipError_t he = hipModuleLoadData(mod, code);
+    free(code);
+    if (he != hipSuccess) {
+        snprintf(err, errlen, "hipModuleLoadData: %s", hipGetErrorString(he));
+        return 0;
+    }
+    hipb.n_compile++;
+    return 1;
+}
+
+long rtc_compile_only(const char *src, char *err, size_t errlen) {
+    size_t cs = 0;
+    char *code = compile_source(src, &cs, err, errlen);
+    if (!code) return -1;
+    free(code);
+    return (long)cs;
+}
+
 /* Generate and compile without loading: usable without a GPU. */
 int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t errlen) {
     KGenResult g;
