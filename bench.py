@@ -1,15 +1,24 @@
-"""Benchmark of the HIP backend on the TinyHVM kernel-dispatch hot path.
+"""Benchmark of the HIP backend on TinyHVM's kernel-dispatch hot path.
 
-A step is one replay of the engine's recorded Backend calls for the workload
-(kernel trace, inputs already resident in HBM): for the fused workload that is
-y = sum(relu(a*b + c), -1) (one group-reduce kernel) and its gradient
-dA = (a*b + c > 0) * b (one elementwise kernel), a/b/c ~ N(0,1) of [8192,8192] f32.
+A step is one replay of the engine's recorded Backend calls for a workload
+(a kernel trace; inputs already resident in HBM, results not read back):
 
-value  = algorithmic HBM bytes of one step / time per step (GB/s).
-roofline: the dominant kernel's algorithmic bytes per launch / its average
-          launch time, from HIP events recorded on the backend's stream.
+  fused   y = sum(relu(a*b + c), -1) and dA = (a*b + c > 0) * b, a/b/c ~ N(0,1)
+          [8192,8192] f32 (one group-reduce kernel + one elementwise kernel).
+          This is the headline: `value` = algorithmic HBM bytes / step time.
+  matmul  y = relu(X @ W + b), dX = G @ W^T, dW = X^T @ G at 4096^3 f32
+          (three matrix-core contractions + three elementwise kernels):
+          TFLOP/s = GEMM FLOPs / step time.
+  lenet   one LeNet-5 training step at batch 256 (forward, backward, SGD
+          through ASSIGN: 51 kernels): steps/s.
+
+roofline: the dominant kernel's algorithmic bytes (or FLOPs) per launch / its
+average duration, from HIP events on the backend's stream around that one
+dispatch; `traffic` comes from the committed rocprofv3 counter summary.
 cpu_baseline: the engine's own CPU backend (oracle/_ref/ref_replay, built from
-          the engine sources) replaying the same trace on one host core.
+the engine sources) on one host core, on the same trace or a stated slice;
+for LeNet the engine's interpreter faults on the padded convolution, so the
+oracle (oracle/ora_replay, the CPU restatement) is timed instead.
 """
 import argparse
 import ctypes as C
@@ -28,21 +37,58 @@ from tinyhvm_amd import _lib  # noqa: E402
 HBM_PEAK_GBS = 8000.0
 MFMA_F32_PEAK_TFLOPS = 157.3
 METRIC = "fused-kernel HBM GB/s (% peak); f32 matmul TFLOPS; LeNet-5 train steps/sec"
+WL = os.path.join(ROOT, "tinyhvm_amd", "workloads")
+F4096 = 2 * 4096 ** 3
+TAG_UOP, TAG_RS = 7, 8
+SKIP_READS = 1
 
 WORKLOADS = {
     "fused": {
-        "trace": os.path.join(ROOT, "tinyhvm_amd", "workloads", "fused_8192x8192.trc"),
-        "step_marks": ("fused.fwd", None),
-        "kernels": {
-            # mark -> algorithmic HBM bytes of the kernel that follows it
-            "fused.fwd": 3 * 8192 * 8192 * 4 + 8192 * 4,
-            "fused.bwd": 4 * 8192 * 8192 * 4,
-        },
-        "dominant": "fused.bwd",
-        "config": {"workload": "fused elementwise+reduce f32: y = sum(relu(a*b+c), -1) and dA",
-                   "shape": [8192, 8192], "dist": "N(0,1)"},
-        "cpu_sample": "full fused fwd+bwd step at [8192,8192], 1 replay",
+        "trace": os.path.join(WL, "fused_8192x8192.trc"),
+        "step": ("fused.fwd", None),
+        # dispatch ordinal within the step -> (name, algorithmic bytes or FLOPs)
+        "kernels": {0: ("fused.fwd", 3 * 8192 * 8192 * 4 + 8192 * 4),
+                    1: ("fused.bwd", 4 * 8192 * 8192 * 4)},
+        "unit": "GB/s", "bound": "hbm", "dominant": "fused.bwd",
+        "config": {"workload": "fused elementwise+reduce f32: y = sum(relu(a*b+c), -1) and its "
+                               "gradient dA = (a*b+c > 0) * b", "shape": [8192, 8192],
+                   "dist": "N(0,1)", "kernels_per_step": 2},
         "profile": "fused_8192x8192.md",
+        "cpu": {"exe": "oracle/_ref/ref_replay", "kind": "reference",
+                "trace": os.path.join(WL, "fused_8192x8192.trc"), "marks": ("fused.fwd", "-"),
+                "sample": "the full step (fwd+bwd) at [8192,8192], 1 replay"},
+    },
+    "matmul": {
+        "trace": os.path.join(WL, "linear_4096.trc"),
+        "step": ("linear.fwd", None),
+        "kernels": {0: ("gemm.fwd", F4096), 3: ("gemm.dx", F4096), 5: ("gemm.dw", F4096)},
+        "unit": "TFLOP/s", "bound": "mfma", "dominant": "gemm.fwd",
+        "config": {"workload": "dense f32 matmul + bias + relu (linear forward) and backward "
+                               "dX, dW", "shape": [4096, 4096, 4096], "dist": "U(-1,1)",
+                   "kernels_per_step": 6},
+        "profile": "matmul_4096.md",
+        "cpu": {"exe": "oracle/_ref/ref_replay", "kind": "reference",
+                "trace": os.path.join(WL, "linear_8x4096x4096.trc"),
+                "marks": ("linear.fwd", "linear.bwd.dx"), "flops": 2 * 8 * 4096 * 4096,
+                "sample": "forward (GEMM + bias + relu) on an 8-row slice of X (8x4096 @ 4096x4096), "
+                          "the same kernels; GEMM throughput is linear in the rows"},
+    },
+    "lenet": {
+        "trace": os.path.join(WL, "lenet_b256.trc"),
+        "step": ("lenet.step", "lenet.end"),
+        "kernels": {},
+        "unit": "steps/s", "bound": None, "dominant": None,
+        "config": {"workload": "LeNet-5 training step f32 (conv5x5 pad2 -> 6, relu, maxpool2, "
+                               "conv5x5 -> 16, relu, maxpool2, fc 400-120-84-10, softmax CE, "
+                               "backward, SGD via ASSIGN)", "batch": 256,
+                   "input": "U(0,1) [256,1,28,28]", "kernels_per_step": 51},
+        "cpu": {"exe": "oracle/ora_replay", "kind": "port",
+                "trace": os.path.join(WL, "lenet_b64.trc"), "marks": ("lenet.step", "lenet.end"),
+                "batch_scale": 256 / 64,
+                "sample": "one training step at batch 64 (the same kernels at 1/4 the batch), "
+                          "time scaled by 4; the engine's own CPU interpreter faults on the "
+                          "padded convolution, so the oracle's restatement of it is timed "
+                          "(1.4x slower than the engine's interpreter on the fused step)"},
     },
 }
 
@@ -57,7 +103,6 @@ class Hip:
         self.h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
         self.h.hipEventSynchronize.argtypes = [C.c_void_p]
         self.h.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
-        self.h.hipEventDestroy.argtypes = [C.c_void_p]
 
     def event(self):
         e = C.c_void_p()
@@ -77,6 +122,8 @@ class Hip:
 def measured_traffic(profile, kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 summary
     (its ```json block), or None when no counter run has been recorded."""
+    if not profile:
+        return None
     path = os.path.join(ROOT, "profiles", profile)
     if not os.path.exists(path):
         return None
@@ -87,25 +134,109 @@ def measured_traffic(profile, kernel):
     return json.loads(block).get("traffic_bytes", {}).get(kernel)
 
 
-def find_mark(L, t, text, start=0):
-    return L.thvm_trace_find_mark(t, text.encode(), start)
-
-
-def cpu_baseline(wl, lo_mark):
-    exe = os.path.join(ROOT, "oracle", "_ref", "ref_replay")
+def cpu_baseline(spec, wl):
+    exe = os.path.join(ROOT, spec["exe"])
     if not os.path.exists(exe):
+        print("cpu baseline: %s is not built" % spec["exe"], file=sys.stderr)
         return None
-    cmd = [exe, wl["trace"], lo_mark, "-", "1"]
+    cmd = [exe, spec["trace"], spec["marks"][0], spec["marks"][1], "1"]
     if shutil.which("taskset"):
         cmd = ["taskset", "-c", "0"] + cmd
-    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    print("cpu baseline: %s" % " ".join(cmd), file=sys.stderr, flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
     if r.returncode != 0:
         sys.stderr.write(r.stderr)
         return None
-    res = json.loads(r.stdout.strip().splitlines()[-1])
-    step_bytes = sum(wl["kernels"].values())
-    return {"value": step_bytes / res["per_rep"] / 1e9, "unit": "GB/s", "cores": 1,
-            "kind": "reference", "sample": wl["cpu_sample"], "seconds": res["per_rep"]}
+    sec = json.loads(r.stdout.strip().splitlines()[-1])["per_rep"]
+    out = {"unit": wl["unit"], "cores": 1, "kind": spec["kind"], "sample": spec["sample"],
+           "seconds": round(sec, 3)}
+    if wl["unit"] == "GB/s":
+        out["value"] = round(sum(b for _n, b in wl["kernels"].values()) / sec / 1e9, 4)
+    elif wl["unit"] == "TFLOP/s":
+        out["value"] = round(spec["flops"] / sec / 1e12, 6)
+    else:
+        out["value"] = round(1.0 / (sec * spec.get("batch_scale", 1.0)), 5)
+    return out
+
+
+def run_workload(L, name, steps, warmup, want_cpu):
+    wl = WORKLOADS[name]
+    be = L.thvm_hip_backend()
+    t = L.thvm_trace_load(wl["trace"].encode())
+    if not t:
+        raise SystemExit("cannot load %s" % wl["trace"])
+    n = L.thvm_trace_count(t)
+    lo = L.thvm_trace_find_mark(t, wl["step"][0].encode(), 0)
+    hi = n if wl["step"][1] is None else L.thvm_trace_find_mark(t, wl["step"][1].encode(), lo)
+    assert 0 <= lo < hi <= n
+    L.thvm_trace_replay(t, be, 0, lo, 0)           # inputs: allocate and upload (untimed)
+    L.thvm_trace_drop_gen_cache(t)
+    assert L.thvm_hip_synchronize() == 0
+    t_c = time.perf_counter()
+    for _ in range(max(warmup, 1)):                # the first replay compiles every kernel
+        L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
+    assert L.thvm_hip_synchronize() == 0
+    print("%s: setup + warmup %.1fs, step = records [%d, %d)" % (name, time.perf_counter() - t_c, lo, hi),
+          file=sys.stderr, flush=True)
+    hip = Hip(L.thvm_hip_stream())
+    # pass 1: whole steps (the reported throughput)
+    e0, e1 = hip.event(), hip.event()
+    t0 = time.perf_counter()
+    hip.record(e0)
+    for _ in range(steps):
+        L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
+    hip.record(e1)
+    assert L.thvm_hip_synchronize() == 0
+    wall = time.perf_counter() - t0
+    gpu_ms = hip.ms(e0, e1)
+    step_s = wall / steps
+    # pass 2: events around each listed dispatch on the backend stream
+    disp = [j for j in range(lo, hi) if L.thvm_trace_tag(t, j) in (TAG_UOP, TAG_RS)]
+    k_ms = {}
+    if wl["kernels"]:
+        ev = {o: (hip.event(), hip.event()) for o in wl["kernels"]}
+        for _ in range(steps):
+            prev = lo
+            for o in sorted(ev):
+                u = disp[o]
+                L.thvm_trace_replay(t, be, prev, u, SKIP_READS)
+                hip.record(ev[o][0])
+                L.thvm_trace_replay(t, be, u, u + 1, SKIP_READS)
+                hip.record(ev[o][1])
+                prev = u + 1
+            L.thvm_trace_replay(t, be, prev, hi, SKIP_READS)
+            for o, (ea, eb) in ev.items():
+                nm = wl["kernels"][o][0]
+                k_ms[nm] = k_ms.get(nm, 0.0) + hip.ms(ea, eb)
+        k_ms = {k: v / steps for k, v in k_ms.items()}
+    assert L.thvm_hip_synchronize() == 0
+    L.thvm_trace_release(t, be)
+    L.thvm_trace_free(t)
+    L.thvm_hip_pool_reset(0)
+    res = {"value": None, "unit": wl["unit"], "ms_per_step": round(step_s * 1e3, 4),
+           "gpu_ms_per_step": round(gpu_ms / steps, 4), "config": wl["config"],
+           "kernels_ms": {k: round(v, 4) for k, v in k_ms.items()}}
+    work = sum(w for _n, w in wl["kernels"].values())
+    if wl["unit"] == "GB/s":
+        res["value"] = round(work / step_s / 1e9, 2)
+    elif wl["unit"] == "TFLOP/s":
+        res["value"] = round(work / step_s / 1e12, 3)
+    else:
+        res["value"] = round(1.0 / step_s, 3)
+    if wl["dominant"]:
+        dom = wl["dominant"]
+        dom_w = next(w for nm, w in wl["kernels"].values() if nm == dom)
+        if wl["bound"] == "hbm":
+            ach, peak, unit = dom_w / (k_ms[dom] * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
+        else:
+            ach, peak, unit = dom_w / (k_ms[dom] * 1e-3) / 1e12, MFMA_F32_PEAK_TFLOPS, "TFLOP/s"
+        res["roofline"] = {"bound": wl["bound"], "achieved": round(ach, 2), "peak": peak,
+                           "unit": unit, "frac": round(ach / peak, 4),
+                           "traffic": measured_traffic(wl.get("profile"), dom), "kernel": dom}
+    if want_cpu and wl.get("cpu"):
+        res["cpu_baseline"] = cpu_baseline(wl["cpu"], wl)
+    print("%s: %s" % (name, json.dumps(res)), file=sys.stderr, flush=True)
+    return res
 
 
 def copy_calibration(nbytes=256 << 20, reps=5):
@@ -147,8 +278,9 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workload", default="fused")
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--workloads", default="fused,matmul,lenet",
+                    help="comma list; the first one gives the headline value")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 256 MiB copy kernel (HBM counter calibration)")
     args = ap.parse_args()
@@ -159,94 +291,35 @@ def main():
         print("bench.py measures one GPU: this build has no multi-GPU path "
               "(use --gpus 1)", file=sys.stderr)
         sys.exit(2)
-    wl = WORKLOADS[args.workload]
+    names = [w for w in args.workloads.split(",") if w]
+    for nm in names:
+        if nm not in WORKLOADS:
+            raise SystemExit("unknown workload %r (have %s)" % (nm, ", ".join(WORKLOADS)))
     L = _lib.lib()
     if L.thvm_hip_init() != 0:
         raise SystemExit("HIP backend failed to initialise")
-    be = L.thvm_hip_backend()
-    t = L.thvm_trace_load(wl["trace"].encode())
-    if not t:
-        raise SystemExit("cannot load %s" % wl["trace"])
-    n = L.thvm_trace_count(t)
-    lo = find_mark(L, t, wl["step_marks"][0])
-    hi = n if wl["step_marks"][1] is None else find_mark(L, t, wl["step_marks"][1], lo)
-    SKIP_READS = 1
-    # setup: allocate and upload the inputs (not timed)
-    L.thvm_trace_replay(t, be, 0, lo, 0)
-    L.thvm_trace_drop_gen_cache(t)
-    assert L.thvm_hip_synchronize() == 0
-    print("setup done: %d records, step = records [%d, %d)" % (n, lo, hi), file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
-        L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
-    assert L.thvm_hip_synchronize() == 0
-
-    hip = Hip(L.thvm_hip_stream())
-    # pass 1: whole steps, no per-kernel events (the reported value)
-    e0, e1 = hip.event(), hip.event()
-    assert L.thvm_hip_synchronize() == 0
-    t0 = time.perf_counter()
-    hip.record(e0)
-    for _ in range(args.steps):
-        L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
-    hip.record(e1)
-    assert L.thvm_hip_synchronize() == 0
-    wall = time.perf_counter() - t0
-    gpu_ms = hip.ms(e0, e1)
-    print("timed %d steps: %.3f ms/step wall, %.3f ms/step on the stream"
-          % (args.steps, wall / args.steps * 1e3, gpu_ms / args.steps), file=sys.stderr, flush=True)
-    # pass 2: the same steps split at the workload's marks, with events around
-    # each kernel's records on the backend stream
-    marks = sorted((find_mark(L, t, m, lo), m) for m in wl["kernels"])
-    bounds = []
-    for i in range(len(marks)):
-        a = marks[i][0]
-        b = marks[i + 1][0] if i + 1 < len(marks) else hi
-        u = next(j for j in range(a, b) if L.thvm_trace_tag(t, j) in (7, 8))  # the dispatch
-        bounds.append((a, u, b, marks[i][1]))
-    ev = [(hip.event(), hip.event()) for _ in bounds]
-    k_ms = {m: 0.0 for m in wl["kernels"]}
-    for _ in range(args.steps):
-        for (a, u, b, m), (ea, eb) in zip(bounds, ev):
-            L.thvm_trace_replay(t, be, a, u, SKIP_READS)
-            hip.record(ea)
-            L.thvm_trace_replay(t, be, u, u + 1, SKIP_READS)
-            hip.record(eb)
-            L.thvm_trace_replay(t, be, u + 1, b, SKIP_READS)
-        for (a, u, b, m), (ea, eb) in zip(bounds, ev):
-            k_ms[m] += hip.ms(ea, eb)
-    assert L.thvm_hip_synchronize() == 0
-    step_s = wall / args.steps
-    step_bytes = sum(wl["kernels"].values())
-    value = step_bytes / step_s / 1e9
-    dom = wl["dominant"]
-    dom_ms = k_ms[dom] / args.steps
-    achieved = wl["kernels"][dom] / (dom_ms * 1e-3) / 1e9
+    results = {nm: run_workload(L, nm, args.steps, args.warmup, not args.no_cpu) for nm in names}
+    L.thvm_hip_shutdown()
+    head = results[names[0]]
     out = {
         "metric": METRIC,
-        "value": round(value, 2),
-        "unit": "GB/s",
+        "value": head["value"],
+        "unit": head["unit"],
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(step_s * 1e3, 4),
+        "ms_per_step": head["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32",
         "data": "synthetic",
-        "config": wl["config"],
-        "roofline": {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS,
-                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": measured_traffic(wl["profile"], dom),
-                     "kernel": dom},
-        "kernels_ms": {m: round(v / args.steps, 4) for m, v in k_ms.items()},
-        "gpu_ms_per_step": round(gpu_ms / args.steps, 4),
+        "config": head["config"],
+        "roofline": head.get("roofline"),
+        "cpu_baseline": head.get("cpu_baseline"),
+        "kernels_ms": head.get("kernels_ms"),
+        "workloads": {nm: r for nm, r in results.items() if nm != names[0]},
     }
-    L.thvm_trace_release(t, be)
-    L.thvm_trace_free(t)
-    L.thvm_hip_shutdown()
-    if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline(wl, wl["step_marks"][0])
     print(json.dumps(out))
 
 
