@@ -10,7 +10,7 @@ A step is one replay of the engine's recorded Backend calls for a workload
           (three matrix-core contractions + three elementwise kernels):
           TFLOP/s = GEMM FLOPs / step time.
   lenet   one LeNet-5 training step at batch 256 (forward, backward, SGD
-          through ASSIGN: 51 kernels): steps/s.
+          through ASSIGN: 54 kernels): steps/s.
 
 roofline: the dominant kernel's algorithmic bytes (or FLOPs) per launch / its
 average duration, from HIP events on the backend's stream around that one
@@ -81,7 +81,7 @@ WORKLOADS = {
         "config": {"workload": "LeNet-5 training step f32 (conv5x5 pad2 -> 6, relu, maxpool2, "
                                "conv5x5 -> 16, relu, maxpool2, fc 400-120-84-10, softmax CE, "
                                "backward, SGD via ASSIGN)", "batch": 256,
-                   "input": "U(0,1) [256,1,28,28]", "kernels_per_step": 51},
+                   "input": "U(0,1) [256,1,28,28]", "kernels_per_step": 54},
         "cpu": {"exe": "oracle/ora_replay", "kind": "port",
                 "trace": os.path.join(WL, "lenet_b64.trc"), "marks": ("lenet.step", "lenet.end"),
                 "batch_scale": 256 / 64,

@@ -43,8 +43,10 @@
  *   PERSIST   max_buf
  *   SNAPSHOT  id, source, u64 bytes, data   (buffer contents after the
  *             preceding dispatch: source 0 = produced by the engine's CPU
- *             backend; 1 = produced by the oracle because the engine's
- *             interpreter would read out of bounds for that kernel)
+ *             backend; 2 = produced by the engine's CPU backend with its
+ *             leaves in zero-filled guard memory, because its interpreter
+ *             loads masked elements outside the buffer before discarding
+ *             them; 1 = produced by the oracle, where neither could run)
  *   MARK      n, n bytes of text (annotation: phase names, config)
  */
 #ifndef THVM_TRACE_H

@@ -22,6 +22,8 @@
 #include "thvm_trace.h"
 #include "thvm_gen.h"
 
+#include <sys/mman.h>
+
 /* The oracle (oracle/oracle.c, compiled separately against the same layouts). */
 extern u64 ora_oob_loads;
 void ora_dispatch_rs(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, const View **views,
@@ -101,10 +103,58 @@ static void rec_mark(const char *text) {
     rb_emit(TRC_MARK);
 }
 
-/* Source of a SNAPSHOT: 0 = the engine's CPU backend, 1 = the oracle, used
- * where the engine's interpreter would read out of bounds (masked pad loads,
- * src/backend/cpu/uop.c:55-71) and fault. */
+/* Source of a SNAPSHOT: 0 = the engine's CPU backend; 2 = the engine's CPU
+ * backend run over zero-guarded leaves (below), for kernels whose masked loads
+ * fall outside their buffer; 1 = the oracle, only if the guarded run is not
+ * possible (the mapping fails). */
 static u32 g_snap_source;
+
+/* The engine's interpreter loads a leaf element before applying the mask that
+ * discards it (src/backend/cpu/uop.c:55-72), so a zero-padded view reads
+ * outside its buffer at the masked positions (u32 index arithmetic wraps a
+ * negative pad offset to a large index) and faults. Such a kernel is run by the
+ * engine itself with every leaf copied to the start of a lazily mapped,
+ * zero-filled region that spans every u32 element index of a 4-byte type: the
+ * stray loads read zeros, the masks discard them, and the output is the
+ * engine's own. */
+#define GUARD_SPAN (((u64)1 << 34) + 65536)
+
+typedef struct { u32 id; void *saved; void *guard; } Guarded;
+
+static u32 guard_leaves(const u32 *leaf_bufs, u32 n_leaves, Guarded *g) {
+    u32 ng = 0;
+    for (u32 i = 0; i < n_leaves; i++) {
+        u32 id = leaf_bufs[i];
+        if (!id || id >= MAX_BUFS || !cpu_pool.bufs[id]) continue;
+        int seen = 0;
+        for (u32 j = 0; j < ng; j++) seen |= g[j].id == id;
+        if (seen) continue;
+        void *m = mmap(NULL, GUARD_SPAN, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE,
+                       -1, 0);
+        if (m == MAP_FAILED) {
+            for (u32 j = 0; j < ng; j++) {
+                cpu_pool.bufs[g[j].id] = g[j].saved;
+                munmap(g[j].guard, GUARD_SPAN);
+            }
+            return (u32)-1;
+        }
+        memcpy(m, cpu_pool.bufs[id], cpu_pool.sizes[id]);
+        g[ng].id = id;
+        g[ng].saved = cpu_pool.bufs[id];
+        g[ng].guard = m;
+        cpu_pool.bufs[id] = m;
+        ng++;
+    }
+    return ng;
+}
+
+static void unguard_leaves(Guarded *g, u32 ng, u32 out_buf) {
+    for (u32 j = 0; j < ng; j++) {
+        if (g[j].id == out_buf) memcpy(g[j].saved, g[j].guard, cpu_pool.sizes[out_buf]);
+        cpu_pool.bufs[g[j].id] = g[j].saved;
+        munmap(g[j].guard, GUARD_SPAN);
+    }
+}
 
 static void rec_snapshot(u32 id) {
     if (!g_exec || id == 0 || id >= MAX_BUFS || !cpu_pool.bufs[id]) return;
@@ -196,8 +246,18 @@ static void cap_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_lea
         ora_oob_loads = 0;
         ora_dispatch_uop(scratch, ob, lp, lb, n_leaves, k);
         if (ora_oob_loads) {
-            memcpy(cpu_pool.bufs[out_buf], scratch, ob);
-            g_snap_source = 1;
+            Guarded g[FUSE_MAX_LEAVES];
+            u32 ng = guard_leaves(leaf_bufs, n_leaves, g);
+            if (ng == (u32)-1) {
+                memcpy(cpu_pool.bufs[out_buf], scratch, ob);
+                g_snap_source = 1;
+            } else {
+                g_orig.dispatch_uop_kernel(out_buf, leaf_bufs, n_leaves, k, cache_key);
+                unguard_leaves(g, ng, out_buf);
+                g_snap_source = 2;
+                if (memcmp(cpu_pool.bufs[out_buf], scratch, ob) != 0)
+                    fprintf(stderr, "capture: oracle differs from the engine on a guarded kernel\n");
+            }
         } else {
             g_orig.dispatch_uop_kernel(out_buf, leaf_bufs, n_leaves, k, cache_key);
         }
@@ -254,13 +314,21 @@ static void cap_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **lea
         ora_oob_loads = 0;
         ora_dispatch_rs(scratch, ob, lp, lb, leaf_views, leaf_sts, n_leaves, ops, n_ops, full_shape, reduce,
                         leaf_dtypes, out_dtype);
-        if (ora_oob_loads) {
+        Guarded g[FUSE_MAX_LEAVES];
+        u32 ng = ora_oob_loads ? guard_leaves(leaf_bufs, n_leaves, g) : 0;
+        if (ng == (u32)-1) {
             memcpy(cpu_pool.bufs[out_buf], scratch, ob);
             g_snap_source = 1;
         } else {
             g_orig.dispatch_kernel_rs(out_buf, leaf_bufs, leaf_views, leaf_sts, n_leaves, ops, n_ops,
                                       full_shape, reduce, side_bufs, side_idx, n_side,
                                       leaf_dtypes, out_dtype);
+            if (ora_oob_loads) {
+                unguard_leaves(g, ng, out_buf);
+                g_snap_source = 2;
+                if (memcmp(cpu_pool.bufs[out_buf], scratch, ob) != 0)
+                    fprintf(stderr, "capture: oracle differs from the engine on a guarded kernel\n");
+            }
         }
         free(scratch);
     }
@@ -539,30 +607,40 @@ static Term ce_grad(TinyHVM *ctx, Term logits, Term onehot, u32 B, u32 C) {
     return realize_as(ctx, binary(ctx, UOP_MUL, d, scalar_t(ctx, 1.0f / (f32)B)), SHAPE(B, C));
 }
 
-/* Nearest 2x upsample of [B,C,H,W] to [B,C,2H,2W] (view chain). */
-static Term up2(TinyHVM *ctx, Term t, u32 B, u32 C, u32 H, u32 W) {
-    Term r = thvm_reshape(ctx, t, shape_of((u32[]){B, C, H, 1, W, 1}, 6));
-    r = thvm_expand(ctx, r, shape_of((u32[]){B, C, H, 2, W, 2}, 6));
-    return thvm_reshape(ctx, r, shape_of((u32[]){B, C, 2 * H, 2 * W}, 4));
+/* Zero padding of the two spatial dims of [B,C,H,W] by p, realized on its
+ * own. The engine lowers a lone pad view with its mask; composed with the
+ * conv's pool view (src/nn/conv.c:390-481) the mask is lost and the kernel
+ * reads the neighbouring rows at the borders and runs off the buffer at the
+ * ends, so the workloads pad explicitly and convolve without padding. */
+static Term pad_exact(TinyHVM *ctx, Term x, u32 B, u32 C, u32 H, u32 W, u32 p) {
+    /* times 1 (exact): a bare view would be folded into its consumer */
+    Term t = binary(ctx, UOP_MUL, thvm_pad(ctx, x, (u32[]){0, 0, 0, 0, p, p, p, p}, 4), scalar_t(ctx, 1.0f));
+    return realize_as(ctx, t, shape_of((u32[]){B, C, H + 2 * p, W + 2 * p}, 4));
 }
 
 /* Max-pool 2x2 backward with the engine's routing rule (every tied maximum
  * receives the gradient, src/interact/grad.c:405-425) fused with the relu
- * mask of the pooled activation a: dz = up(dp) * (1 - (up(pool) > a)) * (a > 0). */
+ * mask of the pooled activation a: dz = up(dp) * (1 - (up(pool) > a)) * (a > 0).
+ * Computed in the 6-D layout [B,C,H/2,2,W/2,2] (the same memory order as
+ * [B,C,H,W]) where the upsample is a plain stride-0 expand: a reshape of the
+ * expanded [B,C,H/2,2,W/2,2] back to [B,C,H,W] is not a strided view and the
+ * engine lowers it as a dense [B,C,H,W] read of the small tensor. */
 static Term pool_relu_bwd(TinyHVM *ctx, Term dp, Term pooled, Term a, u32 B, u32 C, u32 H, u32 W) {
+    Shape s6 = shape_of((u32[]){B, C, H / 2, 2, W / 2, 2}, 6);
+    Shape s1 = shape_of((u32[]){B, C, H / 2, 1, W / 2, 1}, 6);
+    Term pu = thvm_expand(ctx, thvm_reshape(ctx, pooled, s1), s6);
+    Term du = thvm_expand(ctx, thvm_reshape(ctx, dp, s1), s6);
     Term routed = binary(ctx, UOP_SUB, scalar_t(ctx, 1.0f),
-                         binary(ctx, UOP_CMP, up2(ctx, pooled, B, C, H / 2, W / 2), a));
-    Term g = binary(ctx, UOP_MUL, up2(ctx, dp, B, C, H / 2, W / 2), routed);
-    g = binary(ctx, UOP_MUL, g, binary(ctx, UOP_CMP, a, scalar_t(ctx, 0.0f)));
+                         binary(ctx, UOP_CMP, pu, thvm_reshape(ctx, a, s6)));
+    Term g = binary(ctx, UOP_MUL, du, routed);
+    g = binary(ctx, UOP_MUL, g, binary(ctx, UOP_CMP, thvm_reshape(ctx, a, s6), scalar_t(ctx, 0.0f)));
     return realize_as(ctx, g, shape_of((u32[]){B, C, H, W}, 4));
 }
 
 /* Weight gradient of a stride-1 conv as one contraction:
  * dW[co,ci,kh,kw] = sum_{b,oy,ox} xp[b,ci,oy+kh,ox+kw] * dz[b,co,oy,ox],
- * with xp = x padded by `pad` (a masked pool view, src/nn/conv.c:20-388). */
-static Term conv_dw(TinyHVM *ctx, Term x, Term dz, u32 B, u32 Ci, u32 Co, u32 K, u32 pad, u32 OY, u32 OX) {
-    Term xp = x;
-    if (pad) xp = thvm_pad(ctx, x, (u32[]){0, 0, 0, 0, pad, pad, pad, pad}, 4);
+ * with xp the already padded input (a pool view, src/nn/conv.c:20-388). */
+static Term conv_dw(TinyHVM *ctx, Term xp, Term dz, u32 B, u32 Ci, u32 Co, u32 K, u32 OY, u32 OX) {
     Term P = thvm_pool(ctx, xp, (u32[]){K, K}, (u32[]){1, 1}, 2);          /* [B,Ci,OY,OX,K,K] */
     P = thvm_permute(ctx, P, (u32[]){1, 4, 5, 0, 2, 3}, 6);                  /* [Ci,K,K,B,OY,OX] */
     P = thvm_reshape(ctx, P, shape_of((u32[]){1, Ci, K, K, B, OY, OX}, 7));
@@ -585,7 +663,8 @@ static Term flip_t(TinyHVM *ctx, Term W, u32 Co, u32 Ci, u32 K) {
     Term Wf = mm_as(ctx, thvm_reshape(ctx, W, SHAPE(Co * Ci, KK)), Jt, Co * Ci, KK);
     Term Wt = thvm_permute(ctx, thvm_reshape(ctx, Wf, shape_of((u32[]){Co, Ci, K, K}, 4)),
                            (u32[]){1, 0, 2, 3}, 4);
-    return realize_as(ctx, Wt, shape_of((u32[]){Ci, Co, K, K}, 4));
+    /* times 1 (exact) materializes the transpose, so the conv reads a dense kernel */
+    return realize_as(ctx, binary(ctx, UOP_MUL, Wt, scalar_t(ctx, 1.0f)), shape_of((u32[]){Ci, Co, K, K}, 4));
 }
 
 /* Input gradient of a stride-1 conv with padding `pad`: the conv of dz with
@@ -593,7 +672,8 @@ static Term flip_t(TinyHVM *ctx, Term W, u32 Co, u32 Ci, u32 K) {
 static Term conv_dx(TinyHVM *ctx, Term dz, Term W, u32 B, u32 Co, u32 Ci, u32 K, u32 pad, u32 H, u32 W_) {
     Term Wt = flip_t(ctx, W, Co, Ci, K);
     u32 p = K - 1 - pad;
-    return realize_as(ctx, thvm_conv2d(ctx, dz, Wt, term_era(), 1, (u32[]){1, 1}, (u32[]){p, p, p, p}),
+    Term dzp = pad_exact(ctx, dz, B, Co, H + 2 * pad - K + 1, W_ + 2 * pad - K + 1, p);
+    return realize_as(ctx, thvm_conv2d(ctx, dzp, Wt, term_era(), 1, (u32[]){1, 1}, (u32[]){0, 0, 0, 0}),
                       shape_of((u32[]){B, Ci, H, W_}, 4));
 }
 
@@ -662,8 +742,9 @@ static void wl_lenet(TinyHVM *ctx, u32 B, int steps) {
     for (int st = 0; st < steps; st++) {
         rec_mark("lenet.step");
         rec_mark("lenet.fwd");
+        Term xp = pad_exact(ctx, x, B, 1, 28, 28, 2);
         Term a1 = realize_as(ctx, unary(ctx, UOP_RELU,
-                             thvm_conv2d(ctx, x, W1, b1, 1, (u32[]){1, 1}, (u32[]){2, 2, 2, 2})),
+                             thvm_conv2d(ctx, xp, W1, b1, 1, (u32[]){1, 1}, (u32[]){0, 0, 0, 0})),
                              shape_of((u32[]){B, 6, 28, 28}, 4));
         Term p1 = realize_as(ctx, thvm_maxpool2d(ctx, a1, (u32[]){2, 2}, (u32[]){2, 2}),
                              shape_of((u32[]){B, 6, 14, 14}, 4));
@@ -689,11 +770,11 @@ static void wl_lenet(TinyHVM *ctx, u32 B, int steps) {
         DenseGrads g3 = dense_bwd(ctx, f, W3, dz3, B, 400, 120, 1);
         Term dp2 = alias_as(ctx, g3.dx, shape_of((u32[]){B, 16, 5, 5}, 4));
         Term dz2 = pool_relu_bwd(ctx, dp2, p2, a2, B, 16, 10, 10);
-        Term dW2 = conv_dw(ctx, p1, dz2, B, 6, 16, 5, 0, 10, 10);
+        Term dW2 = conv_dw(ctx, p1, dz2, B, 6, 16, 5, 10, 10);
         Term db2 = chansum(ctx, dz2, 16);
         Term dp1 = conv_dx(ctx, dz2, W2, B, 16, 6, 5, 0, 14, 14);
         Term dz1 = pool_relu_bwd(ctx, dp1, p1, a1, B, 6, 28, 28);
-        Term dW1 = conv_dw(ctx, x, dz1, B, 1, 6, 5, 2, 28, 28);
+        Term dW1 = conv_dw(ctx, xp, dz1, B, 1, 6, 5, 28, 28);
         Term db1 = chansum(ctx, dz1, 6);
         rec_mark("lenet.sgd");
         Term grads[10] = {dW1, db1, dW2, db2, g3.dW, g3.db, g4.dW, g4.db, g5.dW, g5.db};
@@ -721,7 +802,8 @@ static void wl_convblock(TinyHVM *ctx, u32 B, u32 C, u32 H) {
     rec_mark("conv.fwd");
     Shape full = shape_of((u32[]){B, C, H, W_}, 4);
     Shape cshape = shape_of((u32[]){1, C, 1, 1}, 4);
-    Term c = realize_as(ctx, thvm_conv2d(ctx, x, Wc, term_era(), 1, (u32[]){1, 1}, (u32[]){1, 1, 1, 1}), full);
+    Term xp = pad_exact(ctx, x, B, C, H, W_, 1);
+    Term c = realize_as(ctx, thvm_conv2d(ctx, xp, Wc, term_era(), 1, (u32[]){1, 1}, (u32[]){0, 0, 0, 0}), full);
     /* batchnorm, train mode, as src/nn/batchnorm.c:35-87 computes it (mean and
      * biased variance over [0,2,3], eps 1e-5, momentum 0.1, unbiased running
      * variance), on realized tensors: the engine's own variance composition
@@ -772,7 +854,7 @@ static void wl_convblock(TinyHVM *ctx, u32 B, u32 C, u32 H) {
                          full);
     Term dgamma = realize_as(ctx, thvm_sum_axes(ctx, binary(ctx, UOP_MUL, dya, xhat), (u32[]){0, 2, 3}, 3), cshape);
     Term dbeta = chansum(ctx, dya, C);
-    Term dW = conv_dw(ctx, x, dc, B, C, C, 3, 1, H, W_);
+    Term dW = conv_dw(ctx, xp, dc, B, C, C, 3, H, W_);
     Term dx = conv_dx(ctx, dc, Wc, B, C, C, 3, 1, H, W_);
     readback(ctx, dW);
     readback(ctx, dx);

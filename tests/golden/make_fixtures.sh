@@ -3,9 +3,9 @@
 # engine, whose CPU backend is the reference. Needs the engine sources at
 # $REF (default /root/reference/src); builds oracle/_ref/capture first.
 # Exec mode: kernels run on the engine's CPU backend and each dispatch is
-# followed by a SNAPSHOT of its output (the golden vectors). Dispatches the
-# engine's interpreter cannot run without reading out of bounds (padded
-# convolutions) take their SNAPSHOT from the oracle and are marked so.
+# followed by a SNAPSHOT of its output (the golden vectors). Dispatches whose
+# masked loads fall outside their buffer (zero padding) are run by the engine
+# with its leaves in zero-filled guard memory and marked so (source 2).
 set -e
 HERE=$(cd "$(dirname "$0")" && pwd)
 ROOT=$(cd "$HERE/../.." && pwd)
