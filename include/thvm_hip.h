@@ -63,6 +63,18 @@ void thvm_hip_buf_copy(u32 dst_buf, u32 src_buf, u64 nbytes);
 /* Backend.pool_reset / pool_set_persistent (src/tinyhvm.h:1039-1040). */
 void thvm_hip_pool_reset(u32 keep);
 void thvm_hip_pool_set_persistent(u32 max_buf);
+/* Backend.op_unary / op_binary / op_mm / op_reduce (src/tinyhvm.h:1004-1016),
+ * the legacy per-op slots of the ENSURE/materialize path
+ * (src/fuse/materialize.c:195,672,683,700); semantics of
+ * src/backend/cpu/ops.c. */
+void thvm_hip_op_unary(u32 uop, u32 dst, const View *dst_view, u32 dst_dtype, u32 src,
+                       const View *src_view, u32 src_dtype);
+void thvm_hip_op_binary(u32 uop, u32 dst, const View *dst_view, u32 dst_dtype, u32 a, const View *a_view,
+                        u32 a_dtype, u32 b, const View *b_view, u32 b_dtype);
+void thvm_hip_op_mm(u32 dst, u32 dst_dtype, u32 a, const View *a_view, u32 a_dtype, u32 b,
+                    const View *b_view, u32 b_dtype, u32 M, u32 K, u32 N);
+void thvm_hip_op_reduce(u32 uop, u32 dst, u32 dst_numel, u32 dst_dtype, u32 src, u32 src_numel,
+                        u32 src_dtype, u32 reduce_dim);
 /* Backend.profile_report / profile_reset (src/tinyhvm.h:1044-1045). */
 void thvm_hip_profile_report(void);
 void thvm_hip_profile_reset(void);

@@ -48,6 +48,15 @@
  *             loads masked elements outside the buffer before discarding
  *             them; 1 = produced by the oracle, where neither could run)
  *   MARK      n, n bytes of text (annotation: phase names, config)
+ *   OPUN      uop, dst, dst_dtype, VIEW dst_view, src, src_dtype, VIEW src_view
+ *   OPBIN     uop, dst, dst_dtype, VIEW dst_view, a, a_dtype, VIEW a_view,
+ *             b, b_dtype, VIEW b_view
+ *   OPMM      dst, dst_dtype, a, a_dtype, VIEW a_view, b, b_dtype, VIEW b_view,
+ *             M, K, N
+ *   OPRED     uop, dst, dst_numel, dst_dtype, src, src_numel, src_dtype,
+ *             reduce_dim
+ *   (the OP* records are the legacy per-op slots op_unary, op_binary, op_mm,
+ *   op_reduce, src/tinyhvm.h:1004-1016)
  */
 #ifndef THVM_TRACE_H
 #define THVM_TRACE_H
@@ -68,7 +77,11 @@ enum {
     TRC_RESET = 11,
     TRC_PERSIST = 12,
     TRC_SNAPSHOT = 13,
-    TRC_MARK = 14
+    TRC_MARK = 14,
+    TRC_OPUN = 15,
+    TRC_OPBIN = 16,
+    TRC_OPMM = 17,
+    TRC_OPRED = 18
 };
 
 enum { TRC_ENC_RAW = 0, TRC_ENC_GEN = 1 };

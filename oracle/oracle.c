@@ -18,6 +18,7 @@
  *   ora_view_read / ora_st_read / ora_dispatch_rs
  *                                  src/backend/cpu/dispatch.c:23-282
  *   ora_contiguify ............... strided masked copy, src/ops/_.c:338-357
+ *   ora_op_unary/binary/mm/reduce  legacy per-op slots, src/backend/cpu/ops.c:1-130
  *   pool (alloc ids, reset) ...... src/backend/cpu/pool.c:6-26
  *
  * Deliberate difference from the reference: every load and store is checked
@@ -27,9 +28,10 @@
  * results are identical wherever the reference does not fault.
  *
  * Parity pins (tests/): bit-exact against the reference CPU backend's own
- * outputs recorded in tests/golden/*.trc (SNAPSHOT records), and against
- * closed forms in f64 for the fused, matmul, conv, pooling and softmax
- * workloads.
+ * outputs recorded in tests/golden/*.trc (SNAPSHOT records; for kernels whose
+ * masked loads leave their buffer, the reference run over zero-filled guard
+ * memory); the fused workload's closed form in f64; textbook restatements of
+ * the convolution, padding and pool-backward kernels.
  */
 #include <math.h>
 #include <stdint.h>
@@ -408,28 +410,108 @@ void ora_dispatch_rs(void *out, u64 out_bytes, const void **leaf, const u64 *lea
     }
 }
 
-void ora_contiguify(u32 *dst, u64 dst_bytes, const u32 *src, u64 src_bytes, u32 numel, const View *v) {
-    for (u32 t = 0; t < numel && (u64)t * 4 + 4 <= dst_bytes; t++) {
-        u32 rem = t, coords[MAX_DIM];
+/* ASSIGN from a strided view into a dense buffer. The engine's CPU backend
+ * has no contiguify slot; without it ASSIGN reads the source to the host
+ * (thvm_to_host_raw, src/ops/_.c:338-357) and writes it back, so that read is
+ * the semantics: per-dim mask checked, strides below 0 counted as 0 (:348),
+ * compound masks not consulted, element size from the dtype. esize is the
+ * destination's bytes per element (dtypes agree, src/interact/tensor_ops.c:116). */
+void ora_contiguify(void *dst, u64 dst_bytes, const void *src, u64 src_bytes, u32 numel, const View *v,
+                    u32 esize) {
+    for (u32 t = 0; t < numel && (u64)(t + 1) * esize <= dst_bytes; t++) {
+        u32 rem = t;
         i32 idx = v->offset;
         int masked = 0;
         for (i32 d = (i32)v->shape.rank - 1; d >= 0; d--) {
             u32 dim = v->shape.dims[d];
             u32 cc = dim ? rem % dim : 0;
             rem = dim ? rem / dim : 0;
-            coords[d] = cc;
             if (v->has_mask && (cc < v->mask_begin[d] || cc >= v->mask_end[d])) masked = 1;
-            idx = (i32)((u32)idx + cc * (u32)v->strides[d]);
+            idx += (i32)cc * (v->strides[d] > 0 ? v->strides[d] : 0);
         }
-        if (v->has_mask && !masked) {
-            for (u32 cm = 0; cm < v->n_compound_masks && cm < 2; cm++) {
-                u32 da = v->compound_masks[cm].dim_a, db = v->compound_masks[cm].dim_b;
-                if (da >= MAX_DIM || db >= MAX_DIM) { masked = 1; break; }
-                i32 cc = (i32)coords[da] * v->compound_masks[cm].stride_a + (i32)coords[db];
-                if (cc < (i32)v->compound_masks[cm].begin || cc >= (i32)v->compound_masks[cm].end) masked = 1;
+        int ok = !masked && idx >= 0 && (u64)((u32)idx + 1) * esize <= src_bytes;
+        if (esize == 2) ((u16 *)dst)[t] = ok ? ((const u16 *)src)[(u32)idx] : 0;
+        else ((u32 *)dst)[t] = ok ? ((const u32 *)src)[(u32)idx] : 0;
+    }
+}
+
+/* ---------------- legacy per-op slots (src/backend/cpu/ops.c) ---------------- */
+
+/* strided_index, src/backend/cpu/ops.c:3-13: u32 arithmetic, no masks. */
+static u32 ora_strided_index(u32 flat, const View *v) {
+    u32 idx = (u32)v->offset, rem = flat;
+    for (i32 d = (i32)v->shape.rank - 1; d >= 0; d--) {
+        u32 dim = v->shape.dims[d];
+        u32 coord = dim ? rem % dim : 0;
+        rem = dim ? rem / dim : 0;
+        idx += coord * (u32)v->strides[d];
+    }
+    return idx;
+}
+
+/* cpu_op_unary, src/backend/cpu/ops.c:15-33 */
+void ora_op_unary(u32 uop, void *dst, u64 dst_bytes, const View *dv, u32 dd, const void *src, u64 src_bytes,
+                  const View *sv, u32 sd) {
+    for (u32 i = 0; i < dv->numel; i++) {
+        f32 val = ora_load(src, src_bytes, sd, ora_strided_index(i, sv));
+        switch (uop) {
+        case UOP_NEG: val = -val; break;
+        case UOP_RELU: val = val > 0.0f ? val : 0.0f; break;
+        case UOP_EXP: val = expf(val); break;
+        case UOP_LOG: val = logf(val); break;
+        case UOP_SQRT: val = sqrtf(val); break;
+        default: break;
+        }
+        ora_store(dst, dst_bytes, dd, i, val);
+    }
+}
+
+/* cpu_op_binary, src/backend/cpu/ops.c:35-60 */
+void ora_op_binary(u32 uop, void *dst, u64 dst_bytes, const View *dv, u32 dd, const void *a, u64 a_bytes,
+                   const View *av, u32 ad, const void *b, u64 b_bytes, const View *bv, u32 bd) {
+    for (u32 i = 0; i < dv->numel; i++) {
+        f32 va = ora_load(a, a_bytes, ad, ora_strided_index(i, av));
+        f32 vb = ora_load(b, b_bytes, bd, ora_strided_index(i, bv));
+        f32 vr;
+        switch (uop) {
+        case UOP_ADD: vr = va + vb; break;
+        case UOP_MUL: vr = va * vb; break;
+        case UOP_DIV: vr = vb != 0.0f ? va / vb : 0.0f; break;
+        case UOP_SUB: vr = va - vb; break;
+        case UOP_MAX: vr = va > vb ? va : vb; break;
+        case UOP_CMP: vr = va > vb ? 1.0f : 0.0f; break;
+        default: vr = va; break;
+        }
+        ora_store(dst, dst_bytes, dd, i, vr);
+    }
+}
+
+/* cpu_op_mm without BLAS, src/backend/cpu/ops.c:80-113: k innermost, in order */
+void ora_op_mm(void *dst, u64 dst_bytes, u32 dd, const void *a, u64 a_bytes, const View *av, u32 ad,
+               const void *b, u64 b_bytes, const View *bv, u32 bd, u32 M, u32 K, u32 N) {
+    for (u32 i = 0; i < M; i++)
+        for (u32 j = 0; j < N; j++) {
+            f32 acc = 0;
+            for (u32 k = 0; k < K; k++) {
+                f32 va = ora_load(a, a_bytes, ad, ora_strided_index(i * K + k, av));
+                f32 vb = ora_load(b, b_bytes, bd, ora_strided_index(k * N + j, bv));
+                acc += va * vb;
             }
+            ora_store(dst, dst_bytes, dd, i * N + j, acc);
         }
-        dst[t] = (masked || idx < 0 || (u64)(u32)idx * 4 + 4 > src_bytes) ? 0u : src[(u32)idx];
+}
+
+/* cpu_op_reduce, src/backend/cpu/ops.c:115-130: innermost reduce_dim elements */
+void ora_op_reduce(u32 uop, void *dst, u64 dst_bytes, u32 dst_numel, u32 dd, const void *src, u64 src_bytes,
+                   u32 sd, u32 reduce_dim) {
+    for (u32 o = 0; o < dst_numel; o++) {
+        f32 acc = uop == UOP_RMAX ? -1e30f : 0.0f;
+        for (u32 r = 0; r < reduce_dim; r++) {
+            f32 v = ora_load(src, src_bytes, sd, o * reduce_dim + r);
+            if (uop == UOP_SUM) acc += v;
+            else if (uop == UOP_RMAX) acc = v > acc ? v : acc;
+        }
+        ora_store(dst, dst_bytes, dd, o, acc);
     }
 }
 
@@ -527,7 +609,27 @@ static void ob_copy(u32 d, u32 s, u64 b) {
     if (dp && sp) memmove(dp, sp, n);
 }
 static void ob_contig(u32 d, u32 numel, u32 s, const View *v) {
-    if (ob_ptr(d) && v) ora_contiguify(ob_ptr(d), ob_size(d), ob_ptr(s), ob_size(s), numel, v);
+    if (ob_ptr(d) && v)
+        ora_contiguify(ob_ptr(d), ob_size(d), ob_ptr(s), ob_size(s), numel, v,
+                       ob_size(d) == (u64)numel * 2 ? 2 : 4);
+}
+
+static void ob_op_unary(u32 uop, u32 dst, const View *dv, u32 dd, u32 src, const View *sv, u32 sd) {
+    ora_op_unary(uop, ob_ptr(dst), ob_size(dst), dv, dd, ob_ptr(src), ob_size(src), sv, sd);
+}
+static void ob_op_binary(u32 uop, u32 dst, const View *dv, u32 dd, u32 a, const View *av, u32 ad, u32 b,
+                         const View *bv, u32 bd) {
+    ora_op_binary(uop, ob_ptr(dst), ob_size(dst), dv, dd, ob_ptr(a), ob_size(a), av, ad, ob_ptr(b), ob_size(b),
+                  bv, bd);
+}
+static void ob_op_mm(u32 dst, u32 dd, u32 a, const View *av, u32 ad, u32 b, const View *bv, u32 bd, u32 M,
+                     u32 K, u32 N) {
+    ora_op_mm(ob_ptr(dst), ob_size(dst), dd, ob_ptr(a), ob_size(a), av, ad, ob_ptr(b), ob_size(b), bv, bd, M, K,
+              N);
+}
+static void ob_op_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn, u32 sd, u32 rdim) {
+    (void)sn;
+    ora_op_reduce(uop, ob_ptr(dst), ob_size(dst), dn, dd, ob_ptr(src), ob_size(src), sd, rdim);
 }
 
 Backend oracle_backend = {
@@ -538,6 +640,10 @@ Backend oracle_backend = {
     .buf_write = ob_write,
     .buf_read = ob_read,
     .buf_read_nosync = ob_read,
+    .op_unary = ob_op_unary,
+    .op_binary = ob_op_binary,
+    .op_mm = ob_op_mm,
+    .op_reduce = ob_op_reduce,
     .dispatch_kernel_rs = ob_rs,
     .dispatch_uop_kernel = ob_uop,
     .contiguify = ob_contig,

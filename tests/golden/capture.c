@@ -336,24 +336,42 @@ static void cap_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **lea
     g_snap_source = 0;
 }
 
+/* The legacy per-op slots (src/tinyhvm.h:1004-1016), reached only from the
+ * engine's ENSURE/materialize path (src/fuse/materialize.c:195,672,683,700):
+ * recorded, run on the engine's CPU backend (src/backend/cpu/ops.c), and
+ * followed by a SNAPSHOT of the destination. */
 static void cap_legacy_unary(u32 uop, u32 dst, const View *dv, u32 dd, u32 src,
                              const View *sv, u32 sd) {
-    fprintf(stderr, "capture: legacy op_unary reached (uop %u)\n", uop);
-    g_orig.op_unary(uop, dst, dv, dd, src, sv, sd);
+    rb_begin();
+    rb_u32(uop); rb_u32(dst); rb_u32(dd); rb_view(dv); rb_u32(src); rb_u32(sd); rb_view(sv);
+    rb_emit(TRC_OPUN);
+    if (g_exec) g_orig.op_unary(uop, dst, dv, dd, src, sv, sd);
+    rec_snapshot(dst);
 }
 static void cap_legacy_binary(u32 uop, u32 dst, const View *dv, u32 dd, u32 a, const View *av,
                               u32 ad, u32 b, const View *bv, u32 bd) {
-    fprintf(stderr, "capture: legacy op_binary reached (uop %u)\n", uop);
-    g_orig.op_binary(uop, dst, dv, dd, a, av, ad, b, bv, bd);
+    rb_begin();
+    rb_u32(uop); rb_u32(dst); rb_u32(dd); rb_view(dv);
+    rb_u32(a); rb_u32(ad); rb_view(av); rb_u32(b); rb_u32(bd); rb_view(bv);
+    rb_emit(TRC_OPBIN);
+    if (g_exec) g_orig.op_binary(uop, dst, dv, dd, a, av, ad, b, bv, bd);
+    rec_snapshot(dst);
 }
 static void cap_legacy_mm(u32 dst, u32 dd, u32 a, const View *av, u32 ad, u32 b,
                           const View *bv, u32 bd, u32 M, u32 K, u32 N) {
-    fprintf(stderr, "capture: legacy op_mm reached\n");
-    g_orig.op_mm(dst, dd, a, av, ad, b, bv, bd, M, K, N);
+    rb_begin();
+    rb_u32(dst); rb_u32(dd); rb_u32(a); rb_u32(ad); rb_view(av); rb_u32(b); rb_u32(bd); rb_view(bv);
+    rb_u32(M); rb_u32(K); rb_u32(N);
+    rb_emit(TRC_OPMM);
+    if (g_exec) g_orig.op_mm(dst, dd, a, av, ad, b, bv, bd, M, K, N);
+    rec_snapshot(dst);
 }
 static void cap_legacy_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn, u32 sd, u32 rd) {
-    fprintf(stderr, "capture: legacy op_reduce reached (uop %u)\n", uop);
-    g_orig.op_reduce(uop, dst, dn, dd, src, sn, sd, rd);
+    rb_begin();
+    rb_u32(uop); rb_u32(dst); rb_u32(dn); rb_u32(dd); rb_u32(src); rb_u32(sn); rb_u32(sd); rb_u32(rd);
+    rb_emit(TRC_OPRED);
+    if (g_exec) g_orig.op_reduce(uop, dst, dn, dd, src, sn, sd, rd);
+    rec_snapshot(dst);
 }
 
 /* The engine's CPU backend has no buf_copy/contiguify, so ASSIGN would fall
@@ -370,25 +388,26 @@ static void cap_buf_copy(u32 dst, u32 src, u64 nbytes) {
     }
     rec_snapshot(dst);
 }
+/* contiguify's golden output. The engine's CPU backend has no contiguify
+ * slot; without one, ASSIGN reads the source view to the host
+ * (thvm_to_host_raw, src/ops/_.c:304-359) and writes the result back
+ * (src/interact/tensor_ops.c:121-136). The assign workload runs each case that
+ * way first and keeps the engine's result here; the recorded contiguify call
+ * of the same case then produces exactly those bytes (SNAPSHOT source 0). */
+static u8 *g_contig_expect;
+static u64 g_contig_expect_n;
+
 static void cap_contiguify(u32 dst, u32 numel, u32 src, const View *v) {
     rb_begin(); rb_u32(dst); rb_u32(numel); rb_u32(src); rb_view(v); rb_emit(TRC_CONTIG);
-    if (g_exec && cpu_pool.bufs[dst] && cpu_pool.bufs[src]) {
-        u32 *d = cpu_pool.bufs[dst];
-        const u32 *sp = cpu_pool.bufs[src];
-        for (u32 t = 0; t < numel && (u64)t * 4 + 4 <= cpu_pool.sizes[dst]; t++) {
-            u32 rem = t;
-            i32 idx = v->offset;
-            int masked = 0;
-            for (i32 dd = (i32)v->shape.rank - 1; dd >= 0; dd--) {
-                u32 dim = v->shape.dims[dd];
-                u32 c = dim ? rem % dim : 0;
-                rem = dim ? rem / dim : 0;
-                if (v->has_mask && (c < v->mask_begin[dd] || c >= v->mask_end[dd])) masked = 1;
-                idx = (i32)((u32)idx + c * (u32)v->strides[dd]);
-            }
-            d[t] = (masked || idx < 0 || (u64)(u32)idx * 4 + 4 > cpu_pool.sizes[src]) ? 0u : sp[(u32)idx];
+    (void)src;
+    if (g_exec && cpu_pool.bufs[dst]) {
+        if (!g_contig_expect || g_contig_expect_n != cpu_pool.sizes[dst]) {
+            fprintf(stderr, "capture: contiguify outside the assign workload has no golden output\n");
+            exit(1);
         }
+        memcpy(cpu_pool.bufs[dst], g_contig_expect, g_contig_expect_n);
     }
+    (void)numel;
     rec_snapshot(dst);
 }
 
@@ -861,6 +880,182 @@ static void wl_convblock(TinyHVM *ctx, u32 B, u32 C, u32 H) {
     (void)dgamma; (void)dbeta;
 }
 
+/* ASSIGN from strided views, the engine's use of contiguify
+ * (src/interact/tensor_ops.c:113-120): a transpose, a broadcast, a zero-padded
+ * (masked) view, a 3-D permute of i32 and a transpose of f16. Each case runs
+ * twice: without a contiguify slot (the engine's host round trip gives the
+ * golden bytes) and with it (the recorded call). */
+typedef Term (*ViewFn)(TinyHVM *ctx, Term src);
+/* Views are made eagerly (an aliasing tensor with a strided view, as
+ * no_grad_alloc = 0 gives): ASSIGN waits for a tensor source, and a lazy
+ * movement term is left to a scheduler pass that never comes for it. */
+static Term eager_view(TinyHVM *ctx, Term t, int kind) {
+    u8 saved = ctx->no_grad_alloc;
+    ctx->no_grad_alloc = 0;
+    Term v = kind == 0 ? thvm_permute(ctx, t, (u32[]){1, 0}, 2)
+           : kind == 1 ? thvm_expand(ctx, t, SHAPE(4, 7))
+           : kind == 2 ? thvm_pad(ctx, t, (u32[]){1, 1, 2, 0}, 2)
+                       : thvm_permute(ctx, t, (u32[]){2, 0, 1}, 3);
+    ctx->no_grad_alloc = saved;
+    return v;
+}
+static Term v_transpose(TinyHVM *ctx, Term t) { return eager_view(ctx, t, 0); }
+static Term v_bcast(TinyHVM *ctx, Term t) { return eager_view(ctx, t, 1); }
+static Term v_pad(TinyHVM *ctx, Term t) { return eager_view(ctx, t, 2); }
+static Term v_perm3(TinyHVM *ctx, Term t) { return eager_view(ctx, t, 3); }
+
+static void assign_case(TinyHVM *ctx, const char *name, Shape ss, Shape ds, u32 dtype, ViewFn vf, u64 seed) {
+    char mk[64];
+    snprintf(mk, sizeof mk, "assign.%s", name);
+    rec_mark(mk);
+    u32 dist = dtype == DTYPE_F32 || dtype == DTYPE_F16 ? TRC_GEN_NORMAL : TRC_GEN_INT;
+    f32 p0 = dist == TRC_GEN_INT ? -1000.f : 0.f, p1 = dist == TRC_GEN_INT ? 1000.f : 1.f;
+    Term src = gen_tensor(ctx, ss, dtype, dist, seed, p0, p1);
+    Term dst_host = gen_tensor(ctx, ds, dtype, TRC_GEN_CONST, seed + 1, 0.f, 0.f);
+    Term dst_dev = gen_tensor(ctx, ds, dtype, TRC_GEN_CONST, seed + 2, 0.f, 0.f);
+    u32 hid = ctx->tensors[(u32)term_val(dst_host)].buf_id;
+    u64 nb = cpu_pool.sizes[hid];
+    /* pass 1: no contiguify slot, the engine's host path */
+    cpu_backend.contiguify = NULL;
+    thvm_eval(ctx, thvm_assign(ctx, dst_host, vf(ctx, src)));
+    g_contig_expect = malloc(nb);
+    g_contig_expect_n = nb;
+    memcpy(g_contig_expect, cpu_pool.bufs[hid], nb);
+    /* pass 2: the recorded contiguify call */
+    cpu_backend.contiguify = cap_contiguify;
+    thvm_eval(ctx, thvm_assign(ctx, dst_dev, vf(ctx, src)));
+    free(g_contig_expect);
+    g_contig_expect = NULL;
+    readback(ctx, dst_dev);
+}
+
+static void wl_assign(TinyHVM *ctx) {
+    assign_case(ctx, "transpose_f32", SHAPE(5, 7), SHAPE(7, 5), DTYPE_F32, v_transpose, 6001);
+    assign_case(ctx, "broadcast_f32", SHAPE(1, 7), SHAPE(4, 7), DTYPE_F32, v_bcast, 6011);
+    assign_case(ctx, "pad_f32", SHAPE(5, 7), SHAPE(7, 9), DTYPE_F32, v_pad, 6021);
+    assign_case(ctx, "permute3_i32", shape_of((u32[]){3, 4, 2}, 3), shape_of((u32[]){2, 3, 4}, 3), DTYPE_I32,
+                v_perm3, 6031);
+    assign_case(ctx, "transpose_f16", SHAPE(6, 3), SHAPE(3, 6), DTYPE_F16, v_transpose, 6041);
+}
+
+/* The legacy per-op slots, called directly on the recorded backend with the
+ * argument shapes the materialize path produces: strided, broadcast and
+ * transposed views, mixed storage dtypes, every unary/binary ALU op the CPU
+ * backend implements (src/backend/cpu/ops.c:16-60), a strided matmul
+ * (:80-113) and SUM/RMAX over the innermost dim (:115-130). */
+static u32 gen_buf(u32 n, u32 dtype, u32 dist, u64 seed, f32 p0, f32 p1) {
+    u64 bytes = (u64)n * dtype_size(dtype);
+    u32 id = cpu_backend.buf_alloc(bytes);
+    void *data = NULL;
+    if (g_exec) {
+        data = malloc((size_t)n * 4 + 4);
+        thvm_gen_fill(data, dtype, dist, seed, p0, p1, 0, n);
+    }
+    g_gen.active = 1; g_gen.dist = dist; g_gen.dtype = dtype; g_gen.seed = seed;
+    g_gen.p0 = p0; g_gen.p1 = p1;
+    cpu_backend.buf_write(id, data, bytes);
+    g_gen.active = 0;
+    free(data);
+    return id;
+}
+
+static View mkview(u32 rank, const u32 *dims, const i32 *strides, i32 offset) {
+    View v;
+    memset(&v, 0, sizeof v);
+    v.shape.rank = rank;
+    u32 n = 1, contig = offset == 0;
+    i32 expect = 1;
+    for (i32 d = (i32)rank - 1; d >= 0; d--) {
+        v.shape.dims[d] = dims[d];
+        v.strides[d] = strides[d];
+        n *= dims[d];
+        if (dims[d] != 1 && strides[d] != expect) contig = 0;
+        expect *= (i32)dims[d];
+    }
+    v.offset = offset;
+    v.numel = n;
+    v.contiguous = contig;
+    return v;
+}
+
+static void wl_legacy(void) {
+    Backend *be = &cpu_backend;
+    /* unary: every op on a contiguous f32 vector; a transposed source into f16
+     * and i32 destinations; an op id the CPU treats as a plain copy */
+    rec_mark("legacy.unary");
+    {
+        u32 n = 37;
+        View v1 = mkview(1, (u32[]){n}, (i32[]){1}, 0);
+        u32 x = gen_buf(n, DTYPE_F32, TRC_GEN_NORMAL, 7001, 0.f, 2.f);
+        u32 xp = gen_buf(n, DTYPE_F32, TRC_GEN_UNIFORM, 7002, 0.01f, 9.f);
+        u32 ops[5] = {UOP_NEG, UOP_RELU, UOP_EXP, UOP_LOG, UOP_SQRT};
+        for (u32 i = 0; i < 5; i++) {
+            u32 out = be->buf_alloc(n * 4);
+            u32 src = (ops[i] == UOP_LOG || ops[i] == UOP_SQRT) ? xp : x;
+            be->op_unary(ops[i], out, &v1, DTYPE_F32, src, &v1, DTYPE_F32);
+        }
+        /* LOG and SQRT of negative inputs: NaN */
+        u32 o1 = be->buf_alloc(n * 4), o2 = be->buf_alloc(n * 4);
+        be->op_unary(UOP_LOG, o1, &v1, DTYPE_F32, x, &v1, DTYPE_F32);
+        be->op_unary(UOP_SQRT, o2, &v1, DTYPE_F32, x, &v1, DTYPE_F32);
+        u32 a = gen_buf(35, DTYPE_F32, TRC_GEN_NORMAL, 7003, 0.f, 100.f);
+        View dv = mkview(2, (u32[]){7, 5}, (i32[]){5, 1}, 0);
+        View tv = mkview(2, (u32[]){7, 5}, (i32[]){1, 7}, 0);
+        u32 h = be->buf_alloc(35 * 2), i32b = be->buf_alloc(35 * 4);
+        be->op_unary(UOP_RELU, h, &dv, DTYPE_F16, a, &tv, DTYPE_F32);
+        be->op_unary(UOP_NEG, i32b, &dv, DTYPE_I32, a, &tv, DTYPE_F32);
+        u32 cpy = be->buf_alloc(35 * 4);
+        be->op_unary(UOP_ADD, cpy, &dv, DTYPE_U32, a, &tv, DTYPE_F32);
+    }
+    /* binary: every op, b broadcast along rows (stride 0), b with zeros for
+     * DIV, mixed source dtypes */
+    rec_mark("legacy.binary");
+    {
+        u32 R = 6, Cn = 9;
+        View dv = mkview(2, (u32[]){R, Cn}, (i32[]){(i32)Cn, 1}, 0);
+        View row = mkview(2, (u32[]){R, Cn}, (i32[]){0, 1}, 0);
+        u32 a = gen_buf(R * Cn, DTYPE_F32, TRC_GEN_NORMAL, 7011, 0.f, 1.f);
+        u32 b = gen_buf(Cn, DTYPE_F32, TRC_GEN_INT, 7012, -2.f, 3.f);   /* integers: zeros for DIV */
+        u32 ops[6] = {UOP_ADD, UOP_SUB, UOP_MUL, UOP_DIV, UOP_MAX, UOP_CMP};
+        for (u32 i = 0; i < 6; i++) {
+            u32 out = be->buf_alloc(R * Cn * 4);
+            be->op_binary(ops[i], out, &dv, DTYPE_F32, a, &dv, DTYPE_F32, b, &row, DTYPE_F32);
+        }
+        u32 ai = gen_buf(R * Cn, DTYPE_I32, TRC_GEN_INT, 7013, -50.f, 50.f);
+        u32 bh = gen_buf(R * Cn, DTYPE_F16, TRC_GEN_NORMAL, 7014, 0.f, 4.f);
+        View tv = mkview(2, (u32[]){R, Cn}, (i32[]){1, (i32)R}, 0);
+        u32 o = be->buf_alloc(R * Cn * 4), oh = be->buf_alloc(R * Cn * 2);
+        be->op_binary(UOP_MUL, o, &dv, DTYPE_F32, ai, &dv, DTYPE_I32, bh, &tv, DTYPE_F16);
+        be->op_binary(UOP_ADD, oh, &dv, DTYPE_F16, a, &tv, DTYPE_F32, ai, &dv, DTYPE_I32);
+    }
+    /* matmul: contiguous f32; A as a transposed view; f16 B into f16 */
+    rec_mark("legacy.mm");
+    {
+        u32 M = 13, K = 17, N = 11;
+        View av = mkview(2, (u32[]){M, K}, (i32[]){(i32)K, 1}, 0);
+        View bv = mkview(2, (u32[]){K, N}, (i32[]){(i32)N, 1}, 0);
+        View at = mkview(2, (u32[]){M, K}, (i32[]){1, (i32)M}, 0);
+        u32 A = gen_buf(M * K, DTYPE_F32, TRC_GEN_UNIFORM, 7021, -1.f, 1.f);
+        u32 B = gen_buf(K * N, DTYPE_F32, TRC_GEN_UNIFORM, 7022, -1.f, 1.f);
+        u32 Bh = gen_buf(K * N, DTYPE_F16, TRC_GEN_UNIFORM, 7023, -1.f, 1.f);
+        u32 o1 = be->buf_alloc(M * N * 4), o2 = be->buf_alloc(M * N * 4), o3 = be->buf_alloc(M * N * 2);
+        be->op_mm(o1, DTYPE_F32, A, &av, DTYPE_F32, B, &bv, DTYPE_F32, M, K, N);
+        be->op_mm(o2, DTYPE_F32, A, &at, DTYPE_F32, B, &bv, DTYPE_F32, M, K, N);
+        be->op_mm(o3, DTYPE_F16, A, &av, DTYPE_F32, Bh, &bv, DTYPE_F16, M, K, N);
+    }
+    /* reduce: SUM and RMAX over the innermost dim, f32 and i32 sources */
+    rec_mark("legacy.reduce");
+    {
+        u32 O = 9, Rn = 33;
+        u32 x = gen_buf(O * Rn, DTYPE_F32, TRC_GEN_NORMAL, 7031, 0.f, 1.f);
+        u32 xi = gen_buf(O * Rn, DTYPE_I32, TRC_GEN_INT, 7032, -1000.f, 1000.f);
+        u32 s1 = be->buf_alloc(O * 4), s2 = be->buf_alloc(O * 4), s3 = be->buf_alloc(O * 4);
+        be->op_reduce(UOP_SUM, s1, O, DTYPE_F32, x, O * Rn, DTYPE_F32, Rn);
+        be->op_reduce(UOP_RMAX, s2, O, DTYPE_F32, x, O * Rn, DTYPE_F32, Rn);
+        be->op_reduce(UOP_SUM, s3, O, DTYPE_I32, xi, O * Rn, DTYPE_I32, Rn);
+    }
+}
+
 /* Storage dtypes and casts (the operations of the engine's own dtype test,
  * test/archive/test_dtype_cast.m, at edge values): f32 -> i32/u32/f16 casts
  * (truncation, out-of-range, negative, NaN, f16 ties and overflow), i32/u32
@@ -945,6 +1140,10 @@ int main(int argc, char **argv) {
         wl_convblock(ctx, nsz > 0 ? sz[0] : 64, nsz > 1 ? sz[1] : 64, nsz > 2 ? sz[2] : 56);
     } else if (strcmp(wl, "dtypes") == 0) {
         wl_dtypes(ctx);
+    } else if (strcmp(wl, "assign") == 0) {
+        wl_assign(ctx);
+    } else if (strcmp(wl, "legacy") == 0) {
+        wl_legacy();
     } else if (strcmp(wl, "linear") == 0) {
         wl_linear(ctx, nsz > 0 ? sz[0] : 64, nsz > 1 ? sz[1] : 64, nsz > 2 ? sz[2] : 64, 1);
     } else {

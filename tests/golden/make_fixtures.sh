@@ -28,6 +28,10 @@ $CAP lenet lenet_b2.trc 2 1
 $CAP convblock convblock_2x4x8.trc 2 4 8
 # storage dtypes and casts
 $CAP dtypes dtypes.trc
+# ASSIGN from strided views (the contiguify slot)
+$CAP assign assign.trc
+# the legacy per-op slots (op_unary / op_binary / op_mm / op_reduce)
+$CAP legacy legacy.trc
 # the engine's FusedOp fallback path (lowering disabled)
 THVM_NO_LOWER=1 $CAP fused rs_fused_16x300.trc 16 300
 THVM_NO_LOWER=1 $CAP linear rs_linear_8x16x12.trc 8 16 12

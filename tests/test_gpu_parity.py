@@ -5,8 +5,8 @@ are read back and the oracle (oracle/oracle.c, the CPU restatement of the
 engine's interpreter) runs the same kernel on them; the GPU output must match
 the oracle's under the kernel's tolerance class (the BASELINE north star):
   - bit-exact: kernels a single lane evaluates in the reference's own order
-    (elementwise, index/view work, casts, RMAX), the FusedOp fallback and
-    buffer copies;
+    (elementwise, index/view work, casts, RMAX), the FusedOp fallback, the
+    legacy per-op slots, strided copies (contiguify) and buffer copies;
   - 1e-6 relative per element (floor 1e-3 of the output's max): the same with
     EXP or LOG, whose last bit may differ between GPU and host libm;
   - 1e-4 normwise (max |x - y| <= 1e-4 max |y|): sums whose order differs
@@ -51,7 +51,47 @@ def _oracle():
                                     C.POINTER(C.POINTER(abi.ShapeTracker)), C.c_uint32,
                                     C.POINTER(abi.FusedOp), C.c_uint32, C.POINTER(abi.Shape),
                                     C.POINTER(abi.ReduceSpec), C.POINTER(C.c_uint32), C.c_uint32]
+    u32, PV = C.c_uint32, C.POINTER(abi.View)
+    ora.ora_contiguify.argtypes = [vp, u64, vp, u64, u32, PV, u32]
+    ora.ora_op_unary.argtypes = [u32, vp, u64, PV, u32, vp, u64, PV, u32]
+    ora.ora_op_binary.argtypes = [u32, vp, u64, PV, u32, vp, u64, PV, u32, vp, u64, PV, u32]
+    ora.ora_op_mm.argtypes = [vp, u64, u32, vp, u64, PV, u32, vp, u64, PV, u32, u32, u32, u32]
+    ora.ora_op_reduce.argtypes = [u32, vp, u64, u32, u32, vp, u64, u32, u32]
     return ora
+
+
+def _legacy_oracle(ora, r, host):
+    """Runs a CONTIG or legacy per-op record through the oracle on the GPU's
+    inputs; returns (expected bytes, output dtype, tolerance kind, rtol)."""
+    f = r.f
+    cast = lambda b: C.cast(b, C.c_void_p)  # noqa: E731
+    if r.tag == trace.CONTIG:
+        out, n = host.read(f["dst"])
+        src, sn = host.read(f["src"])
+        esize = 2 if n == f["numel"] * 2 else 4
+        v = f["view"].to_c()
+        ora.ora_contiguify(cast(out), n, cast(src), sn, f["numel"], C.byref(v), esize)
+        return out, n, {2: 1, 4: 0}[esize], "exact", 0.0
+    out, n = host.read(f["dst"])
+    a, an = host.read(f["a"])
+    tr = f.get("uop") in (abi.UOP_EXP, abi.UOP_LOG)
+    kind, rtol = ("elem", 1e-6) if tr and r.tag != trace.OPRED else ("exact", 0.0)
+    if r.tag == trace.OPUN:
+        dv, av = f["dv"].to_c(), f["av"].to_c()
+        ora.ora_op_unary(f["uop"], cast(out), n, C.byref(dv), f["dd"], cast(a), an, C.byref(av), f["ad"])
+    elif r.tag == trace.OPBIN:
+        b, bn = host.read(f["b"])
+        dv, av, bv = f["dv"].to_c(), f["av"].to_c(), f["bv"].to_c()
+        ora.ora_op_binary(f["uop"], cast(out), n, C.byref(dv), f["dd"], cast(a), an, C.byref(av), f["ad"],
+                          cast(b), bn, C.byref(bv), f["bd"])
+    elif r.tag == trace.OPMM:
+        b, bn = host.read(f["b"])
+        av, bv = f["av"].to_c(), f["bv"].to_c()
+        ora.ora_op_mm(cast(out), n, f["dd"], cast(a), an, C.byref(av), f["ad"], cast(b), bn, C.byref(bv),
+                      f["bd"], f["M"], f["K"], f["N"])
+    else:
+        ora.ora_op_reduce(f["uop"], cast(out), n, f["dn"], f["dd"], cast(a), an, f["ad"], f["rdim"])
+    return out, n, f["dd"], kind, rtol
 
 
 def _has_transcendental_uop(k):
@@ -160,6 +200,8 @@ def kernel_parity(backend, read_fn, sync_fn, ora, path, tol_fn=None):
         for i, r in enumerate(recs):
             if r.tag == trace.ALLOC:
                 host.sizes[r.f["id"]] = r.f["bytes"]
+            if r.tag == trace.WRITE and r.f["enc"] == trace.ENC_GEN:
+                dtype_of[r.f["id"]] = r.f["dtype"]
             if r.tag in (trace.UOP, trace.RS):
                 out_id = r.f["out"]
                 out_buf, out_n = host.read(out_id)
@@ -187,6 +229,16 @@ def kernel_parity(backend, read_fn, sync_fn, ora, path, tol_fn=None):
                 ok, msg = compare(bytes(got)[:out_n], bytes(out_buf)[:out_n], dtype, kind, rtol)
                 kernel_results.append((i, ok, msg))
                 print("  %s dispatch %d (%s): %s" % (path.split("/")[-1], i, kind, msg), flush=True)
+            elif r.tag == trace.CONTIG or r.tag in trace.LEGACY:
+                want, n, dtype, kind, rtol = _legacy_oracle(ora, r, host)
+                rp.run(i, i + 1)
+                dst = r.f["dst"]
+                dtype_of[dst] = dtype
+                got, _ = host.read(dst)
+                ok, msg = compare(bytes(got)[:n], bytes(want)[:n], dtype, kind, rtol)
+                kernel_results.append((i, ok, msg))
+                print("  %s %s %d (%s): %s" % (path.split("/")[-1], trace.TAG_NAMES[r.tag], i, kind, msg),
+                      flush=True)
             elif r.tag == trace.SNAPSHOT:
                 got, n = host.read(r.f["id"])
                 dt = dtype_of.get(r.f["id"], 0)

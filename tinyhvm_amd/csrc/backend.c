@@ -270,17 +270,99 @@ static void hb_contiguify(u32 dst_buf, u32 numel, u32 src_buf, const View *src_v
     pool_sync_device(src_buf);
     hipFunction_t fn = rtc_static_fn("thvm_contiguify");
     if (!fn) return;
+    /* The engine calls this only when source and destination dtypes agree
+     * (src/interact/tensor_ops.c:113-116) and allocates numel * dtype size
+     * bytes, so the element size is the destination's bytes per element. */
     ContigArgs a;
     memset(&a, 0, sizeof a);
+    a.esize = d->bytes == (u64)numel * 2 ? 2u : 4u;
     a.dst = (u64)(uintptr_t)d->ptr;
-    a.dst_n = (u32)(d->bytes / 4);
+    a.dst_n = (u32)(d->bytes / a.esize);
     a.src = s ? (u64)(uintptr_t)s->ptr : 0;
-    a.src_n = s ? (u32)(s->bytes / 4) : 0;
+    a.src_n = s ? (u32)(s->bytes / a.esize) : 0;
     a.v = *src_view;
     a.numel = numel;
     void *params[] = {&a};
     hipb_launch(fn, (numel + 255) / 256, 1, 1, 256, params);
     pool_mark_device_write(dst_buf);
+}
+
+/* ---- legacy per-op slots (src/tinyhvm.h:1004-1016) ----
+ * Reached only from the engine's ENSURE/materialize path
+ * (src/fuse/materialize.c:195,672,683,700). One lane per output in the CPU
+ * backend's order (src/backend/cpu/ops.c), so results are bit-identical. */
+static u32 elems_of(const HipbBuf *b, u32 dt) { return b ? (u32)(b->bytes / (dt == DTYPE_F16 ? 2u : 4u)) : 0u; }
+
+static void legacy_launch(const char *name, LegacyArgs *a, u32 dst) {
+    hipFunction_t fn = rtc_static_fn(name);
+    if (fn && a->n) {
+        void *params[] = {a};
+        hipb_launch(fn, (a->n + 255u) / 256u, 1, 1, 256, params);
+    }
+    pool_mark_device_write(dst);
+}
+
+static void hb_op_unary(u32 uop, u32 dst, const View *dv, u32 dd, u32 src, const View *sv, u32 sd) {
+    HipbBuf *d = pool_get(dst), *s = pool_get(src);
+    if (!hipb.initialized || !d || !dv || !sv) return;
+    pool_sync_device(dst);
+    pool_sync_device(src);
+    LegacyArgs a;
+    memset(&a, 0, sizeof a);
+    a.dst = (u64)(uintptr_t)d->ptr; a.dst_n = elems_of(d, dd); a.dd = dd;
+    a.a = s ? (u64)(uintptr_t)s->ptr : 0; a.a_n = elems_of(s, sd); a.ad = sd; a.av = *sv;
+    a.n = dv->numel; a.uop = uop; a.binary = 0;
+    legacy_launch("thvm_op_ew", &a, dst);
+}
+
+static void hb_op_binary(u32 uop, u32 dst, const View *dv, u32 dd, u32 ab, const View *av, u32 ad, u32 bb,
+                         const View *bv, u32 bd) {
+    HipbBuf *d = pool_get(dst), *x = pool_get(ab), *y = pool_get(bb);
+    if (!hipb.initialized || !d || !dv || !av || !bv) return;
+    pool_sync_device(dst);
+    pool_sync_device(ab);
+    pool_sync_device(bb);
+    LegacyArgs a;
+    memset(&a, 0, sizeof a);
+    a.dst = (u64)(uintptr_t)d->ptr; a.dst_n = elems_of(d, dd); a.dd = dd;
+    a.a = x ? (u64)(uintptr_t)x->ptr : 0; a.a_n = elems_of(x, ad); a.ad = ad; a.av = *av;
+    a.b = y ? (u64)(uintptr_t)y->ptr : 0; a.b_n = elems_of(y, bd); a.bd = bd; a.bv = *bv;
+    a.n = dv->numel; a.uop = uop; a.binary = 1;
+    legacy_launch("thvm_op_ew", &a, dst);
+}
+
+static void hb_op_mm(u32 dst, u32 dd, u32 ab, const View *av, u32 ad, u32 bb, const View *bv, u32 bd, u32 M,
+                     u32 K, u32 N) {
+    HipbBuf *d = pool_get(dst), *x = pool_get(ab), *y = pool_get(bb);
+    if (!hipb.initialized || !d || !av || !bv) return;
+    if ((u64)M * N > 0xFFFFFFFFull) {
+        fprintf(stderr, "tinyhvm-hip: op_mm %ux%u output exceeds u32 indexing\n", M, N);
+        return;
+    }
+    pool_sync_device(dst);
+    pool_sync_device(ab);
+    pool_sync_device(bb);
+    LegacyArgs a;
+    memset(&a, 0, sizeof a);
+    a.dst = (u64)(uintptr_t)d->ptr; a.dst_n = elems_of(d, dd); a.dd = dd;
+    a.a = x ? (u64)(uintptr_t)x->ptr : 0; a.a_n = elems_of(x, ad); a.ad = ad; a.av = *av;
+    a.b = y ? (u64)(uintptr_t)y->ptr : 0; a.b_n = elems_of(y, bd); a.bd = bd; a.bv = *bv;
+    a.M = M; a.K = K; a.N = N; a.n = M * N;
+    legacy_launch("thvm_op_mm", &a, dst);
+}
+
+static void hb_op_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn, u32 sd, u32 rdim) {
+    HipbBuf *d = pool_get(dst), *s = pool_get(src);
+    (void)sn;
+    if (!hipb.initialized || !d) return;
+    pool_sync_device(dst);
+    pool_sync_device(src);
+    LegacyArgs a;
+    memset(&a, 0, sizeof a);
+    a.dst = (u64)(uintptr_t)d->ptr; a.dst_n = elems_of(d, dd); a.dd = dd;
+    a.a = s ? (u64)(uintptr_t)s->ptr : 0; a.a_n = elems_of(s, sd); a.ad = sd;
+    a.n = dn; a.uop = uop; a.K = rdim;
+    legacy_launch("thvm_op_reduce", &a, dst);
 }
 
 static void hb_buf_copy(u32 dst_buf, u32 src_buf, u64 nbytes) {
@@ -321,10 +403,10 @@ Backend hip_backend = {
     .buf_mark_use = hb_buf_mark_use,
     .buf_write = hb_buf_write,
     .buf_read = hb_buf_read,
-    .op_unary = NULL,
-    .op_binary = NULL,
-    .op_mm = NULL,
-    .op_reduce = NULL,
+    .op_unary = hb_op_unary,
+    .op_binary = hb_op_binary,
+    .op_mm = hb_op_mm,
+    .op_reduce = hb_op_reduce,
     .dispatch_kernel_rs = hb_dispatch_kernel_rs,
     .dispatch_uop_kernel = hb_dispatch_uop_kernel,
     .contiguify = hb_contiguify,
@@ -341,6 +423,20 @@ Backend hip_backend = {
 
 /* ---- flat C entry points (same behaviour as the vtable slots) ---- */
 int  thvm_hip_init(void) { return hb_init(); }
+void thvm_hip_op_unary(u32 uop, u32 dst, const View *dv, u32 dd, u32 src, const View *sv, u32 sd) {
+    hb_op_unary(uop, dst, dv, dd, src, sv, sd);
+}
+void thvm_hip_op_binary(u32 uop, u32 dst, const View *dv, u32 dd, u32 a, const View *av, u32 ad, u32 b,
+                        const View *bv, u32 bd) {
+    hb_op_binary(uop, dst, dv, dd, a, av, ad, b, bv, bd);
+}
+void thvm_hip_op_mm(u32 dst, u32 dd, u32 a, const View *av, u32 ad, u32 b, const View *bv, u32 bd, u32 M, u32 K,
+                    u32 N) {
+    hb_op_mm(dst, dd, a, av, ad, b, bv, bd, M, K, N);
+}
+void thvm_hip_op_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn, u32 sd, u32 rdim) {
+    hb_op_reduce(uop, dst, dn, dd, src, sn, sd, rdim);
+}
 void thvm_hip_shutdown(void) { hb_shutdown(); }
 u32  thvm_hip_buf_alloc(u64 bytes) { return hb_buf_alloc(bytes); }
 void thvm_hip_buf_free(u32 id) { hb_buf_free(id); }

@@ -27,15 +27,29 @@ typedef struct {
     ShapeTracker sts[1];              /* one per leaf with a stacked tracker */
 } RsParams;
 
-/* contiguify: passed by value as the kernel's only argument. */
+/* contiguify: passed by value as the kernel's only argument. dst_n/src_n
+ * are capacities in elements of esize (2 or 4) bytes. */
 typedef struct {
     u64 dst;
     u64 src;
     u32 dst_n;
     u32 src_n;
     u32 numel;
-    u32 pad;
+    u32 esize;
     View v;
 } ContigArgs;
+
+/* legacy per-op slots (op_unary / op_binary / op_mm / op_reduce): passed by
+ * value. Capacities are in elements of each buffer's dtype. */
+typedef struct {
+    u64 dst, a, b;
+    u32 dst_n, a_n, b_n;
+    u32 n;                 /* outputs: dst numel, or M*N for mm */
+    u32 uop, binary;
+    u32 dd, ad, bd;        /* dtypes */
+    u32 M, K, N;           /* mm; K doubles as reduce_dim for reduce */
+    u32 pad;
+    View av, bv;
+} LegacyArgs;
 
 #endif

@@ -53,6 +53,9 @@ typedef struct {
     u32 out_dtype;
     View cview;            /* CONTIG */
     u32 numel;
+    /* OPUN / OPBIN / OPMM / OPRED (id = dst, id2 = a or src, id3 = b) */
+    u32 uop, id3, dd, ad, bd, mm_m, mm_k, mm_n, dn, sn, rdim;
+    View *lv;              /* dst, a, b views */
     char *text;            /* MARK */
     void *gen_cache;       /* materialized GEN data */
 } TRec;
@@ -238,6 +241,26 @@ static int parse_rec(ThvmTrace *t, TRec *r, u32 tag, const u8 *p, u64 len) {
         r->id = c_u32(&c); c_u32(&c); r->bytes = c_u64(&c);
         r->data = c_raw(&c, r->bytes);
         break;
+    case TRC_OPUN:
+    case TRC_OPBIN:
+    case TRC_OPMM:
+        r->lv = calloc(3, sizeof(View));
+        if (!r->lv) return 0;
+        if (tag == TRC_OPMM) {
+            r->id = c_u32(&c); r->dd = c_u32(&c);
+            r->id2 = c_u32(&c); r->ad = c_u32(&c); c_view(&c, &r->lv[1]);
+            r->id3 = c_u32(&c); r->bd = c_u32(&c); c_view(&c, &r->lv[2]);
+            r->mm_m = c_u32(&c); r->mm_k = c_u32(&c); r->mm_n = c_u32(&c);
+        } else {
+            r->uop = c_u32(&c); r->id = c_u32(&c); r->dd = c_u32(&c); c_view(&c, &r->lv[0]);
+            r->id2 = c_u32(&c); r->ad = c_u32(&c); c_view(&c, &r->lv[1]);
+            if (tag == TRC_OPBIN) { r->id3 = c_u32(&c); r->bd = c_u32(&c); c_view(&c, &r->lv[2]); }
+        }
+        break;
+    case TRC_OPRED:
+        r->uop = c_u32(&c); r->id = c_u32(&c); r->dn = c_u32(&c); r->dd = c_u32(&c);
+        r->id2 = c_u32(&c); r->sn = c_u32(&c); r->ad = c_u32(&c); r->rdim = c_u32(&c);
+        break;
     case TRC_MARK: {
         u32 n = c_u32(&c);
         const u8 *s = c_raw(&c, n);
@@ -302,7 +325,7 @@ void thvm_trace_free(ThvmTrace *t) {
     for (u32 i = 0; i < t->n; i++) {
         TRec *r = &t->recs[i];
         free(r->leaf_ids); free(r->uk); free(r->views); free(r->sts); free(r->has_st);
-        free(r->ops); free(r->leaf_dtypes); free(r->text); free(r->gen_cache);
+        free(r->ops); free(r->leaf_dtypes); free(r->text); free(r->gen_cache); free(r->lv);
     }
     free(t->recs);
     free(t->live);
@@ -457,6 +480,26 @@ int thvm_trace_replay(ThvmTrace *t, const Backend *be, u32 lo, u32 hi, u32 flags
             break;
         case TRC_CONTIG:
             if (be->contiguify) be->contiguify(L(t, r->id), r->numel, L(t, r->id2), &r->cview);
+            break;
+        case TRC_OPUN:
+            if (be->op_unary) be->op_unary(r->uop, L(t, r->id), &r->lv[0], r->dd, L(t, r->id2), &r->lv[1], r->ad);
+            dispatched++;
+            break;
+        case TRC_OPBIN:
+            if (be->op_binary)
+                be->op_binary(r->uop, L(t, r->id), &r->lv[0], r->dd, L(t, r->id2), &r->lv[1], r->ad,
+                              L(t, r->id3), &r->lv[2], r->bd);
+            dispatched++;
+            break;
+        case TRC_OPMM:
+            if (be->op_mm)
+                be->op_mm(L(t, r->id), r->dd, L(t, r->id2), &r->lv[1], r->ad, L(t, r->id3), &r->lv[2], r->bd,
+                          r->mm_m, r->mm_k, r->mm_n);
+            dispatched++;
+            break;
+        case TRC_OPRED:
+            if (be->op_reduce) be->op_reduce(r->uop, L(t, r->id), r->dn, r->dd, L(t, r->id2), r->sn, r->ad, r->rdim);
+            dispatched++;
             break;
         case TRC_RESET:
             /* ids are remapped; the target's own pool keeps its numbering */

@@ -1,6 +1,9 @@
 // static_kernels.hip - precompiled gfx950 kernels loaded once at init:
 //   thvm_rs          FusedOp/ReduceSpec interpreter (dispatch_kernel_rs fallback)
-//   thvm_contiguify  strided, masked view -> dense copy (4-byte elements)
+//   thvm_contiguify  strided, masked view -> dense copy (2- or 4-byte elements),
+//                    as the engine's host read src/ops/_.c:338-357
+//   thvm_op_ew / thvm_op_mm / thvm_op_reduce
+//                    the legacy per-op slots (src/backend/cpu/ops.c)
 //   thvm_fill_u32    fill a buffer with a 32-bit pattern (graph-safe clear)
 //
 // The rs interpreter restates the engine's CPU fallback
@@ -270,31 +273,99 @@ extern "C" __global__ __launch_bounds__(64) void thvm_rs(const RsParams *P, u32 
 extern "C" __global__ __launch_bounds__(256) void thvm_contiguify(ContigArgs A) {
     const u32 t = blockIdx.x * 256u + threadIdx.x;
     const View &v = A.v;
-    const u32 numel = A.numel, dst_n = A.dst_n, src_n = A.src_n;
-    u32 *dst = (u32 *)(uintptr_t)A.dst;
-    const u32 *src = (const u32 *)(uintptr_t)A.src;
-    if (t >= numel || t >= dst_n) return;
+    if (t >= A.numel || t >= A.dst_n) return;
     u32 rem = t;
     int idx = v.offset;
     int masked = 0;
-    u32 coords[MAX_DIM];
     for (int d = (int)v.shape.rank - 1; d >= 0; d--) {
-        u32 dim = v.shape.dims[d];
-        u32 c = dim ? rem % dim : 0u;
+        const u32 dim = v.shape.dims[d];
+        const u32 c = dim ? rem % dim : 0u;
         rem = dim ? rem / dim : 0u;
-        coords[d] = c;
         if (v.has_mask && (c < v.mask_begin[d] || c >= v.mask_end[d])) masked = 1;
-        idx = (int)((u32)idx + c * (u32)v.strides[d]);
+        idx += (int)c * (v.strides[d] > 0 ? v.strides[d] : 0);
     }
-    if (v.has_mask && !masked) {
-        for (u32 cm = 0; cm < v.n_compound_masks && cm < 2; cm++) {
-            u32 da = v.compound_masks[cm].dim_a, db = v.compound_masks[cm].dim_b;
-            if (da >= MAX_DIM || db >= MAX_DIM) { masked = 1; break; }
-            int c = (int)coords[da] * v.compound_masks[cm].stride_a + (int)coords[db];
-            if (c < (int)v.compound_masks[cm].begin || c >= (int)v.compound_masks[cm].end) masked = 1;
+    const int ok = !masked && idx >= 0 && (u32)idx < A.src_n;
+    if (A.esize == 2u) {
+        const unsigned short *src = (const unsigned short *)(uintptr_t)A.src;
+        ((unsigned short *)(uintptr_t)A.dst)[t] = ok ? src[(u32)idx] : (unsigned short)0;
+    } else {
+        const u32 *src = (const u32 *)(uintptr_t)A.src;
+        ((u32 *)(uintptr_t)A.dst)[t] = ok ? src[(u32)idx] : 0u;
+    }
+}
+
+// ---- legacy per-op slots (src/backend/cpu/ops.c) ----
+// One lane per output, each in the CPU's order of operations, so results are
+// bit-identical (EXP/LOG aside). Index arithmetic is strided_index
+// (src/backend/cpu/ops.c:3-13): u32, no masks; loads out of range read 0.
+__device__ __forceinline__ u32 strided_index(u32 flat, const View &v) {
+    u32 idx = (u32)v.offset, rem = flat;
+    for (int d = (int)v.shape.rank - 1; d >= 0; d--) {
+        const u32 dim = v.shape.dims[d];
+        const u32 c = dim ? rem % dim : 0u;
+        rem = dim ? rem / dim : 0u;
+        idx += c * (u32)v.strides[d];
+    }
+    return idx;
+}
+
+extern "C" __global__ __launch_bounds__(256) void thvm_op_ew(LegacyArgs A) {
+    const u32 t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= A.n) return;
+    const float va = load_as_f32((const void *)(uintptr_t)A.a, A.ad, A.a_n, strided_index(t, A.av));
+    float vr = va;
+    if (A.binary) {
+        const float vb = load_as_f32((const void *)(uintptr_t)A.b, A.bd, A.b_n, strided_index(t, A.bv));
+        switch (A.uop) {
+        case UOP_ADD: vr = va + vb; break;
+        case UOP_MUL: vr = va * vb; break;
+        case UOP_DIV: vr = vb != 0.0f ? va / vb : 0.0f; break;
+        case UOP_SUB: vr = va - vb; break;
+        case UOP_MAX: vr = va > vb ? va : vb; break;
+        case UOP_CMP: vr = va > vb ? 1.0f : 0.0f; break;
+        default: break;
+        }
+    } else {
+        switch (A.uop) {
+        case UOP_NEG: vr = -va; break;
+        case UOP_RELU: vr = va > 0.0f ? va : 0.0f; break;
+        case UOP_EXP: vr = expf(va); break;
+        case UOP_LOG: vr = logf(va); break;
+        case UOP_SQRT: vr = sqrtf(va); break;
+        default: break;
         }
     }
-    dst[t] = (masked || idx < 0 || (u32)idx >= src_n) ? 0u : src[(u32)idx];
+    store_from_f32((void *)(uintptr_t)A.dst, A.dd, A.dst_n, t, vr);
+}
+
+// C[i][j] = sum_k A[i*K+k] * B[k*N+j] through the operand views, k in order
+// (src/backend/cpu/ops.c:80-113, the path without BLAS).
+extern "C" __global__ __launch_bounds__(256) void thvm_op_mm(LegacyArgs A) {
+    const u32 t = blockIdx.x * 256u + threadIdx.x;
+    if (t >= A.n) return;
+    const u32 i = t / A.N, j = t % A.N;
+    const void *pa = (const void *)(uintptr_t)A.a, *pb = (const void *)(uintptr_t)A.b;
+    float acc = 0.0f;
+    for (u32 k = 0; k < A.K; k++) {
+        const float va = load_as_f32(pa, A.ad, A.a_n, strided_index(i * A.K + k, A.av));
+        const float vb = load_as_f32(pb, A.bd, A.b_n, strided_index(k * A.N + j, A.bv));
+        acc = acc + va * vb;
+    }
+    store_from_f32((void *)(uintptr_t)A.dst, A.dd, A.dst_n, i * A.N + j, acc);
+}
+
+// out[o] = SUM / RMAX of src[o*R .. o*R+R) in order (src/backend/cpu/ops.c:115-130); R = A.K.
+extern "C" __global__ __launch_bounds__(256) void thvm_op_reduce(LegacyArgs A) {
+    const u32 o = blockIdx.x * 256u + threadIdx.x;
+    if (o >= A.n) return;
+    const void *ps = (const void *)(uintptr_t)A.a;
+    float acc = A.uop == UOP_RMAX ? -1e30f : 0.0f;
+    for (u32 r = 0; r < A.K; r++) {
+        const float v = load_as_f32(ps, A.ad, A.a_n, o * A.K + r);
+        if (A.uop == UOP_SUM) acc = acc + v;
+        else if (A.uop == UOP_RMAX) acc = v > acc ? v : acc;
+    }
+    store_from_f32((void *)(uintptr_t)A.dst, A.dd, A.dst_n, o, acc);
 }
 
 extern "C" __global__ __launch_bounds__(256) void thvm_fill_u32(u32 *dst, u32 n, u32 value) {

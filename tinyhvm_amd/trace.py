@@ -15,12 +15,14 @@ from . import abi
 
 MAGIC = b"THVMTRC1"
 (ALLOC, FREE, INCREF, DECREF, WRITE, READ, UOP, RS, COPY, CONTIG, RESET, PERSIST,
- SNAPSHOT, MARK) = range(1, 15)
+ SNAPSHOT, MARK, OPUN, OPBIN, OPMM, OPRED) = range(1, 19)
+LEGACY = (OPUN, OPBIN, OPMM, OPRED)
 ENC_RAW, ENC_GEN = 0, 1
 GEN_UNIFORM, GEN_NORMAL, GEN_INT, GEN_CONST = 1, 2, 3, 4
 TAG_NAMES = {ALLOC: "ALLOC", FREE: "FREE", INCREF: "INCREF", DECREF: "DECREF", WRITE: "WRITE",
              READ: "READ", UOP: "UOP", RS: "RS", COPY: "COPY", CONTIG: "CONTIG",
-             RESET: "RESET", PERSIST: "PERSIST", SNAPSHOT: "SNAPSHOT", MARK: "MARK"}
+             RESET: "RESET", PERSIST: "PERSIST", SNAPSHOT: "SNAPSHOT", MARK: "MARK",
+             OPUN: "OPUN", OPBIN: "OPBIN", OPMM: "OPMM", OPRED: "OPRED"}
 
 
 @dataclass
@@ -205,6 +207,24 @@ def _parse_payload(tag, p: bytes) -> dict:
     elif tag == MARK:
         n = c.u32()
         f["text"] = c.raw(n).decode()
+    elif tag in (OPUN, OPBIN):
+        f["uop"], f["dst"], f["dd"] = c.u32(), c.u32(), c.u32()
+        f["dv"] = c.view()
+        f["a"], f["ad"] = c.u32(), c.u32()
+        f["av"] = c.view()
+        if tag == OPBIN:
+            f["b"], f["bd"] = c.u32(), c.u32()
+            f["bv"] = c.view()
+    elif tag == OPMM:
+        f["dst"], f["dd"] = c.u32(), c.u32()
+        f["a"], f["ad"] = c.u32(), c.u32()
+        f["av"] = c.view()
+        f["b"], f["bd"] = c.u32(), c.u32()
+        f["bv"] = c.view()
+        f["M"], f["K"], f["N"] = c.u32(), c.u32(), c.u32()
+    elif tag == OPRED:
+        f["uop"], f["dst"], f["dn"], f["dd"] = c.u32(), c.u32(), c.u32(), c.u32()
+        f["a"], f["sn"], f["ad"], f["rdim"] = c.u32(), c.u32(), c.u32(), c.u32()
     return f
 
 
