@@ -102,7 +102,7 @@ EXPORTED = ["hip_backend"] + [
 
 
 def gen_bytes(dist, dtype, seed, p0, p1, nbytes):
-    n = nbytes // 4
+    n = nbytes // (2 if dtype == abi.DTYPE_F16 else 4)
     buf = (C.c_uint8 * max(nbytes, 4))()
     lib().thvm_gen_fill_parallel(C.cast(buf, C.c_void_p), dtype, dist, seed, p0, p1, n, 0)
     return bytes(buf)[:nbytes]

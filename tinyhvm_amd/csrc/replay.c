@@ -394,7 +394,8 @@ static const void *write_payload(TRec *r) {
     if (!r->gen_cache) {
         r->gen_cache = malloc(r->bytes ? r->bytes : 4);
         if (!r->gen_cache) return NULL;
-        thvm_gen_fill_parallel(r->gen_cache, r->dtype, r->dist, r->seed, r->p0, r->p1, r->bytes / 4, 0);
+        thvm_gen_fill_parallel(r->gen_cache, r->dtype, r->dist, r->seed, r->p0, r->p1,
+                               r->bytes / thvm_gen_esize(r->dtype), 0);
     }
     return r->gen_cache;
 }
