@@ -1,8 +1,10 @@
 """Matrix-core (f32 MFMA) contraction kernels on the GPU: every committed trace
-replayed with every contraction forced onto the matrix-core path (the
-fixtures are below the size heuristics) and with K split over 2 workgroups,
-under the same kernel-boundary parity as tests/test_gpu_parity.py; the
-matrix-core kernels fall in the 1e-4 normwise class."""
+replayed with every contraction forced onto the matrix-core path (most
+fixtures are below the size heuristics), once with the tile shape and split-K
+chosen by size, and once per tile shape (128x128, 64x64, 256x32, 32x256) with
+fixed split-K factors, under the same kernel-boundary parity as
+tests/test_gpu_parity.py; the matrix-core kernels fall in the 1e-4 normwise
+class."""
 import os
 
 import pytest
@@ -14,11 +16,19 @@ from tinyhvm_amd import _lib
 pytestmark = pytest.mark.gpu
 
 
-@pytest.fixture(scope="module", params=["1", "2"], ids=["whole-K", "split-K"])
+# (split-K factor, tile shape): 0 = chosen by size, 1 = 128x128, 2 = 64x64,
+# 3 = 256x32, 4 = 32x256
+CONFIGS = [("1", "0"), ("2", "0"), ("1", "1"), ("3", "2"), ("1", "3"), ("2", "4")]
+
+
+@pytest.fixture(scope="module", params=CONFIGS,
+                ids=["whole-K", "split-K", "tile128x128", "tile64x64-split3", "tile256x32",
+                     "tile32x256-split2"])
 def hip_dense(request):
-    saved = {k: os.environ.get(k) for k in ("THVM_HIP_DENSE_FORCE", "THVM_HIP_DENSE_SPLITS")}
+    saved = {k: os.environ.get(k) for k in ("THVM_HIP_DENSE_FORCE", "THVM_HIP_DENSE_SPLITS",
+                                             "THVM_HIP_DENSE_TILE")}
     os.environ["THVM_HIP_DENSE_FORCE"] = "1"
-    os.environ["THVM_HIP_DENSE_SPLITS"] = request.param
+    os.environ["THVM_HIP_DENSE_SPLITS"], os.environ["THVM_HIP_DENSE_TILE"] = request.param
     L = _lib.lib()
     assert L.thvm_hip_init() == 0
     yield L

@@ -24,6 +24,17 @@ static int env_flag(const char *name) {
     return v && v[0] && strcmp(v, "0") != 0;
 }
 
+/* Matrix-core routing knobs (read at init, or before the first device-free
+ * analysis call). */
+static void read_dense_env(void) {
+    hipb.dense_force = env_flag("THVM_HIP_DENSE_FORCE");
+    const char *e = getenv("THVM_HIP_DENSE_SPLITS");
+    hipb.dense_splits = e ? (u32)atoi(e) : 0;
+    e = getenv("THVM_HIP_DENSE_TILE");
+    hipb.dense_tile = e ? (u32)atoi(e) : 0;
+    if (hipb.dense_tile > 4) hipb.dense_tile = 0;
+}
+
 static int hb_init(void) {
     if (hipb.initialized) return 0;
     int n = 0;
@@ -50,11 +61,7 @@ static int hb_init(void) {
     hipb.dump_src = env_flag("THVM_HIP_DUMP");
     hipb.no_dense = env_flag("THVM_HIP_NO_DENSE");
     hipb.verbose = env_flag("THVM_HIP_VERBOSE");
-    hipb.dense_force = env_flag("THVM_HIP_DENSE_FORCE");
-    {
-        const char *e = getenv("THVM_HIP_DENSE_SPLITS");
-        hipb.dense_splits = e ? (u32)atoi(e) : 0;
-    }
+    read_dense_env();
     if (pool_init() != 0) return -1;
     if (rtc_init() != 0) return -1;
     hipb.initialized = 1;
@@ -509,9 +516,7 @@ int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t er
 int thvm_hip_dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits) {
     static int env_read = 0;
     if (!hipb.initialized && !env_read) {
-        hipb.dense_force = env_flag("THVM_HIP_DENSE_FORCE");
-        const char *e = getenv("THVM_HIP_DENSE_SPLITS");
-        hipb.dense_splits = e ? (u32)atoi(e) : 0;
+        read_dense_env();
         env_read = 1;
     }
     return dense_analyze(k, M, N, K, splits);

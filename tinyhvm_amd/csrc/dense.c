@@ -40,9 +40,8 @@
 #include "hipb.h"
 
 #define DG_MAX 8
-#define DENSE_MIN_MN 32
-#define DENSE_MIN_K 32
-#define DENSE_MIN_WORK (1ull << 21)
+#define DENSE_MIN_K 16
+#define DENSE_MIN_WORK (1ull << 16)
 
 static int op_type_is_float(KOpType t) {
     return t == KOP_CONST_F || t == KOP_LOAD || t == KOP_ALU || t == KOP_ACC_INIT || t == KOP_MASK;
@@ -443,20 +442,47 @@ static void emit_gid_fn(DSB *s, const char *name, u32 n, const u32 *div, const u
     dsb_put(s, "  return g;\n}\n");
 }
 
+/* Tile shapes. Every shape uses v_mfma_f32_32x32x2f32 blocks and 4 waves:
+ * a wave owns wm_b x wn_b blocks (32x32 each); the waves form a gm x gn grid. */
+typedef struct {
+    u32 bm, bn;
+    u32 wm_b, wn_b;
+    u32 gm, gn;
+    const char *tag;
+} TileCfg;
+
+static const TileCfg CFG_BIG = {128, 128, 2, 2, 2, 2, "128x128"};   /* large square GEMMs */
+static const TileCfg CFG_MID = {64, 64, 1, 1, 2, 2, "64x64"};       /* small GEMMs: more tiles */
+static const TileCfg CFG_TALL = {256, 32, 2, 1, 4, 1, "256x32"};    /* N <= 32 (conv channels) */
+static const TileCfg CFG_WIDE = {32, 256, 1, 2, 1, 4, "32x256"};    /* M <= 32 */
+
 typedef struct {
     char name[48];
+    TileCfg cfg;
     u32 splits;
     u32 kchunk;
     u32 tiles_m, tiles_n;
 } GemmPlan;
 
-#define BM 128
-#define BN 128
 #define BK 16
+#define GEMM_THREADS 256
+
+/* Loader lane map for one operand: x in [0, BX) along the tile's M or N side,
+ * k in [0, BK). k-major operands put 16 consecutive lanes on consecutive k,
+ * the others put consecutive lanes on consecutive x (coalesced either way). */
+static void emit_map(DSB *s, int kmajor, u32 bx, const char *xname) {
+    if (kmajor)
+        dsb_put(s, "const u32 kk = tid & 15u, %s = (tid >> 4) + e * 16u;", xname);
+    else if (bx >= GEMM_THREADS)
+        dsb_put(s, "const u32 %s = tid, kk = e;", xname);
+    else
+        dsb_put(s, "const u32 %s = tid %% %uu, kk = tid / %uu + e * %uu;", xname, bx, bx, GEMM_THREADS / bx);
+}
 
 static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const GemmPlan *pl, char *err,
                              size_t errlen) {
     DSB s = {0};
+    const TileCfg *cf = &pl->cfg;
     dsb_put(&s, "%s\n", kgen_prelude());
     dsb_put(&s, "typedef float f32x16 __attribute__((ext_vector_type(16)));\n");
     emit_gid_fn(&s, "gid_m", ct->np, ct->pdiv, ct->pext);
@@ -478,14 +504,17 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
     }
     const u32 M = ct->M, N = ct->N, K = ct->K;
     const u32 tiles = pl->tiles_m * pl->tiles_n;
-    dsb_put(&s,
-            "extern \"C\" __global__ __launch_bounds__(256) void %s(", pl->name);
+    const u32 EA = cf->bm * BK / GEMM_THREADS, EB = cf->bn * BK / GEMM_THREADS;
+    const u32 NB = cf->wm_b * cf->wn_b;
+    dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", GEMM_THREADS, pl->name);
     emit_params(&s, k->n_leaves);
     dsb_put(&s, ", float* ws) {\n");
     dsb_put(&s,
             "  constexpr u32 BM = %u, BN = %u, BK = %u, LDA = BM + 4, LDB = BN + 4;\n"
-            "  constexpr u32 M = %uu, N = %uu, K = %uu, TM = %uu, TN = %uu, TILES = %uu, KCH = %uu;\n",
-            BM, BN, BK, M, N, K, pl->tiles_m, pl->tiles_n, tiles, pl->kchunk);
+            "  constexpr u32 M = %uu, N = %uu, K = %uu, TM = %uu, TN = %uu, TILES = %uu, KCH = %uu;\n"
+            "  constexpr u32 WM = %uu, WN = %uu, GN = %uu;\n",
+            cf->bm, cf->bn, BK, M, N, K, pl->tiles_m, pl->tiles_n, tiles, pl->kchunk,
+            cf->wm_b * 32, cf->wn_b * 32, cf->gn);
     dsb_put(&s,
             "  __shared__ float As[2][BK * LDA];\n"
             "  __shared__ float Bs[2][BK * LDB];\n"
@@ -501,29 +530,29 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
             "  const u32 m0 = tm * BM, n0 = tn * BN;\n"
             "  const u32 kbeg = blockIdx.y * KCH;\n"
             "  const u32 kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
-            "  float ra[8], rb[8];\n");
-    /* loader maps: 8 elements per thread of a 128x16 tile */
-    const char *map_p = ct->p_kmajor
-        ? "const u32 kk = tid & 15u, mm = (tid >> 4) + e * 16u;"
-        : "const u32 mm = tid & 127u, kk = (tid >> 7) + e * 2u;";
-    const char *map_q = ct->q_kmajor
-        ? "const u32 kk = tid & 15u, nn = (tid >> 4) + e * 16u;"
-        : "const u32 nn = tid & 127u, kk = (tid >> 7) + e * 2u;";
-    dsb_put(&s, "  auto loadA = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < 8u; e++) { %s\n"
-                "      const u32 m = m0 + mm, k = k0 + kk;\n"
-                "      ra[e] = (m < M && k < kend) ? operand_p(gid_m(m), k, ", map_p);
+            "  float ra[%u], rb[%u];\n", EA, EB);
+    dsb_put(&s, "  auto loadA = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
+    emit_map(&s, ct->p_kmajor, cf->bm, "mm");
+    dsb_put(&s, "\n      const u32 m = m0 + mm, k = k0 + kk;\n"
+                "      ra[e] = (m < M && k < kend) ? operand_p(gid_m(m), k, ");
     emit_args(&s, k->n_leaves);
     dsb_put(&s, ") : 0.0f; }\n  };\n");
-    dsb_put(&s, "  auto loadB = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < 8u; e++) { %s\n"
-                "      const u32 n = n0 + nn, k = k0 + kk;\n"
-                "      rb[e] = (n < N && k < kend) ? operand_q(gid_n(n), k, ", map_q);
+    dsb_put(&s, "  auto loadB = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EB);
+    emit_map(&s, ct->q_kmajor, cf->bn, "nn");
+    dsb_put(&s, "\n      const u32 n = n0 + nn, k = k0 + kk;\n"
+                "      rb[e] = (n < N && k < kend) ? operand_q(gid_n(n), k, ");
     emit_args(&s, k->n_leaves);
     dsb_put(&s, ") : 0.0f; }\n  };\n");
-    dsb_put(&s, "  auto storeA = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < 8u; e++) { %s As[buf][kk * LDA + mm] = ra[e]; }\n  };\n", map_p);
-    dsb_put(&s, "  auto storeB = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < 8u; e++) { %s Bs[buf][kk * LDB + nn] = rb[e]; }\n  };\n", map_q);
+    dsb_put(&s, "  auto storeA = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
+    emit_map(&s, ct->p_kmajor, cf->bm, "mm");
+    dsb_put(&s, " As[buf][kk * LDA + mm] = ra[e]; }\n  };\n");
+    dsb_put(&s, "  auto storeB = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EB);
+    emit_map(&s, ct->q_kmajor, cf->bn, "nn");
+    dsb_put(&s, " Bs[buf][kk * LDB + nn] = rb[e]; }\n  };\n");
     dsb_put(&s,
-            "  f32x16 acc00 = {0}, acc01 = {0}, acc10 = {0}, acc11 = {0};\n"
-            "  const u32 wm = (wave >> 1) * 64u, wn = (wave & 1u) * 64u;\n"
+            "  f32x16 acc[%u];\n"
+            "  #pragma unroll\n  for (u32 b = 0; b < %uu; b++) acc[b] = (f32x16){0};\n"
+            "  const u32 wm = (wave / GN) * WM, wn = (wave %% GN) * WN;\n"
             "  const u32 nst = (kend > kbeg) ? (kend - kbeg + BK - 1u) / BK : 0u;\n"
             "  if (nst > 0u) { loadA(kbeg); loadB(kbeg); storeA(0u); storeB(0u); }\n"
             "  __syncthreads();\n"
@@ -535,29 +564,32 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
             "    #pragma unroll\n"
             "    for (u32 kk = 0; kk < BK; kk += 2u) {\n"
             "      const u32 kr = kk + (lane >> 5);\n"
-            "      const float a0 = A[kr * LDA + wm + (lane & 31u)];\n"
-            "      const float a1 = A[kr * LDA + wm + 32u + (lane & 31u)];\n"
-            "      const float b0 = B[kr * LDB + wn + (lane & 31u)];\n"
-            "      const float b1 = B[kr * LDB + wn + 32u + (lane & 31u)];\n"
-            "      acc00 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, acc00, 0, 0, 0);\n"
-            "      acc01 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, acc01, 0, 0, 0);\n"
-            "      acc10 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, acc10, 0, 0, 0);\n"
-            "      acc11 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, acc11, 0, 0, 0);\n"
+            "      float a[%u], b[%u];\n"
+            "      #pragma unroll\n"
+            "      for (u32 i = 0; i < %uu; i++) a[i] = A[kr * LDA + wm + i * 32u + (lane & 31u)];\n"
+            "      #pragma unroll\n"
+            "      for (u32 j = 0; j < %uu; j++) b[j] = B[kr * LDB + wn + j * 32u + (lane & 31u)];\n"
+            "      #pragma unroll\n"
+            "      for (u32 i = 0; i < %uu; i++)\n"
+            "        #pragma unroll\n"
+            "        for (u32 j = 0; j < %uu; j++)\n"
+            "          acc[i * %uu + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i * %uu + j], 0, 0, 0);\n"
             "    }\n"
             "    if (st + 1u < nst) { storeA(cur ^ 1u); storeB(cur ^ 1u); }\n"
             "    __syncthreads();\n"
-            "  }\n");
+            "  }\n",
+            NB, NB, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wn_b, cf->wn_b);
     /* epilogue: D[i][j] of a 32x32 block sits in lane j + 32*((i/4)%%2), register (i%%4) + 4*(i/8) */
     dsb_put(&s,
             "  #pragma unroll\n"
-            "  for (u32 blk = 0; blk < 4u; blk++) {\n"
-            "    const f32x16 c = blk == 0u ? acc00 : (blk == 1u ? acc01 : (blk == 2u ? acc10 : acc11));\n"
-            "    const u32 bm = wm + (blk >> 1) * 32u, bn = wn + (blk & 1u) * 32u;\n"
+            "  for (u32 blk = 0; blk < %uu; blk++) {\n"
+            "    const f32x16 c = acc[blk];\n"
+            "    const u32 bm = wm + (blk / %uu) * 32u, bn = wn + (blk %% %uu) * 32u;\n"
             "    const u32 n = n0 + bn + (lane & 31u);\n"
             "    #pragma unroll\n"
             "    for (u32 v = 0; v < 16u; v++) {\n"
             "      const u32 m = m0 + bm + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3u);\n"
-            "      if (m < M && n < N) {\n");
+            "      if (m < M && n < N) {\n", NB, cf->wn_b, cf->wn_b);
     if (pl->splits > 1) {
         dsb_put(&s, "        ws[((unsigned long long)blockIdx.y * M + m) * N + n] = c[v];\n");
     } else {
@@ -661,17 +693,27 @@ static DenseEntry *insert(u64 key, const UOpKernel *k) {
     return e;
 }
 
+static TileCfg pick_cfg(u32 M, u32 N) {
+    if (N <= 32 && M >= 256) return CFG_TALL;
+    if (M <= 32 && N >= 256) return CFG_WIDE;
+    u64 big_tiles = (u64)((M + 127) / 128) * ((N + 127) / 128);
+    return big_tiles >= 128 ? CFG_BIG : CFG_MID;
+}
+
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
+    static const TileCfg *forced[5] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE};
     memset(pl, 0, sizeof *pl);
-    pl->tiles_m = (ct->M + BM - 1) / BM;
-    pl->tiles_n = (ct->N + BN - 1) / BN;
+    pl->cfg = hipb.dense_tile ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N);
+    pl->tiles_m = (ct->M + pl->cfg.bm - 1) / pl->cfg.bm;
+    pl->tiles_n = (ct->N + pl->cfg.bn - 1) / pl->cfg.bn;
     u32 tiles = pl->tiles_m * pl->tiles_n;
-    /* split K until the grid covers the 256 CUs about twice, keeping at
-     * least 512 elements of K per split */
+    /* split K until the grid covers the 256 CUs about twice, keeping each
+     * split at least min_chunk long (512 for the big tiles, whose per-tile
+     * setup is larger; 64 otherwise) */
+    u32 min_chunk = pl->cfg.bm == 128 ? 512 : 64;
     u32 splits = 1;
-    while (tiles * splits < 512 && ct->K / (splits * 2) >= 512 && splits < 256) splits *= 2;
+    while ((u64)tiles * splits < 512 && ct->K / (splits * 2) >= min_chunk && splits < 512) splits *= 2;
     if (hipb.dense_splits) splits = hipb.dense_splits;
-    pl->splits = splits;
     u32 kch = (ct->K + splits - 1) / splits;
     kch = (kch + BK - 1) / BK * BK;
     pl->kchunk = kch;
@@ -686,12 +728,13 @@ int dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits) {
     if (!recognize(k, &ct)) return 0;
     GemmPlan pl;
     make_plan(&ct, &pl, 0);
-    /* Matrix cores pay off for reasonably sized operands spread over at
-     * least a quarter of the CUs; smaller contractions stay on the
-     * generated reduce kernels (one workgroup or lane per output). */
+    /* Matrix cores pay off once the contraction is more than a few hundred
+     * thousand multiply-adds with a reduction of at least one K step: the
+     * tile loaders then evaluate each operand element once instead of once
+     * per output, and split-K spreads short outputs over the CUs. Smaller
+     * ones stay on the generated kernels (one lane or workgroup per output). */
     if (!hipb.dense_force &&
-        (ct.M < DENSE_MIN_MN || ct.N < DENSE_MIN_MN || ct.K < DENSE_MIN_K ||
-         (u64)ct.M * ct.N * ct.K < DENSE_MIN_WORK || pl.tiles_m * pl.tiles_n * pl.splits < 64))
+        (ct.M < 2 || ct.N < 2 || ct.K < DENSE_MIN_K || (u64)ct.M * ct.N * ct.K < DENSE_MIN_WORK))
         return 0;
     if (M) *M = ct.M;
     if (N) *N = ct.N;
@@ -744,8 +787,8 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         e->N = ct.N;
         e->is_dense = 1;
         if (hipb.verbose)
-            fprintf(stderr, "tinyhvm-hip: dense %s M=%u N=%u K=%u splits=%u\n", e->plan.name, ct.M, ct.N,
-                    ct.K, e->plan.splits);
+            fprintf(stderr, "tinyhvm-hip: dense %s M=%u N=%u K=%u tile %s splits=%u\n", e->plan.name, ct.M,
+                    ct.N, ct.K, e->plan.cfg.tag, e->plan.splits);
     }
     if (!e->is_dense) return 0;
     /* split-K workspace */
@@ -778,7 +821,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     }
     params[2 * nb] = &ws;
     u32 tiles = e->plan.tiles_m * e->plan.tiles_n;
-    if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, 256, params)) return 0;
+    if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, GEMM_THREADS, params)) return 0;
     if (e->plan.splits > 1) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};
         u64 mn = (u64)e->M * e->N;
