@@ -1056,6 +1056,21 @@ static void wl_legacy(void) {
     }
 }
 
+/* Reductions with few outputs over long axes (a row sum and row max of
+ * [R, C], and a per-channel sum over [B, Ch, H, W] axes 0, 2, 3), the shape of
+ * batchnorm statistics and bias gradients. */
+static void wl_longreduce(TinyHVM *ctx, u32 R, u32 Cn) {
+    Term x = gen_tensor(ctx, SHAPE(R, Cn), DTYPE_F32, TRC_GEN_NORMAL, 8001, 0.f, 1.f);
+    rec_mark("longreduce.sum");
+    readback(ctx, realize_as(ctx, thvm_sum_axes(ctx, binary(ctx, UOP_MUL, x, scalar_t(ctx, 0.5f)), (u32[]){1}, 1),
+                             SHAPE(R)));
+    rec_mark("longreduce.max");
+    readback(ctx, realize_as(ctx, thvm_rmax_axes(ctx, x, (u32[]){1}, 1), SHAPE(R)));
+    Term g = gen_tensor(ctx, shape_of((u32[]){8, 3, 40, 40}, 4), DTYPE_F32, TRC_GEN_UNIFORM, 8002, -1.f, 1.f);
+    rec_mark("longreduce.chansum");
+    readback(ctx, chansum(ctx, g, 3));
+}
+
 /* Storage dtypes and casts (the operations of the engine's own dtype test,
  * test/archive/test_dtype_cast.m, at edge values): f32 -> i32/u32/f16 casts
  * (truncation, out-of-range, negative, NaN, f16 ties and overflow), i32/u32
@@ -1144,6 +1159,8 @@ int main(int argc, char **argv) {
         wl_assign(ctx);
     } else if (strcmp(wl, "legacy") == 0) {
         wl_legacy();
+    } else if (strcmp(wl, "longreduce") == 0) {
+        wl_longreduce(ctx, nsz > 0 ? sz[0] : 4, nsz > 1 ? sz[1] : 20000);
     } else if (strcmp(wl, "linear") == 0) {
         wl_linear(ctx, nsz > 0 ? sz[0] : 64, nsz > 1 ? sz[1] : 64, nsz > 2 ? sz[2] : 64, 1);
     } else {

@@ -32,6 +32,8 @@ $CAP dtypes dtypes.trc
 $CAP assign assign.trc
 # the legacy per-op slots (op_unary / op_binary / op_mm / op_reduce)
 $CAP legacy legacy.trc
+# few outputs over long axes (split group reductions)
+$CAP longreduce longreduce_4x20000.trc 4 20000
 # the engine's FusedOp fallback path (lowering disabled)
 THVM_NO_LOWER=1 $CAP fused rs_fused_16x300.trc 16 300
 THVM_NO_LOWER=1 $CAP linear rs_linear_8x16x12.trc 8 16 12

@@ -19,6 +19,10 @@
 
 HipbState hipb;
 
+/* Workspace of split group reductions: grown on demand and reused by every
+ * dispatch (the stream orders the users). */
+static Scratch red_ws;
+
 static int env_flag(const char *name) {
     const char *v = getenv(name);
     return v && v[0] && strcmp(v, "0") != 0;
@@ -73,6 +77,7 @@ static void hb_shutdown(void) {
     HIPB_CHECK(hipStreamSynchronize(hipb.stream));
     dense_shutdown();
     rtc_shutdown();
+    scratch_release(&red_ws);
     pool_shutdown();
     HIPB_CHECK(hipStreamDestroy(hipb.stream));
     hipb.initialized = 0;
@@ -136,6 +141,8 @@ static void grid_for(u64 blocks, u32 bx, u32 *gx, u32 *gy) {
     }
 }
 
+static float *reduce_workspace(u64 bytes) { return scratch_reserve(&red_ws, bytes); }
+
 static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
                                    const UOpKernel *k, u64 cache_key) {
     (void)cache_key;
@@ -164,7 +171,7 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     u32 nb = k->n_leaves + 1;
     void *ptrs[FUSE_MAX_LEAVES + 1];
     u32 counts[FUSE_MAX_LEAVES + 1];
-    void *params[2 * (FUSE_MAX_LEAVES + 1)];
+    void *params[2 * (FUSE_MAX_LEAVES + 1) + 1];
     ptrs[0] = ob->ptr;
     counts[0] = elem_count(out_buf, k->out_dtype);
     for (u32 i = 0; i < k->n_leaves; i++) {
@@ -177,6 +184,18 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         params[nb + b] = &counts[b];
     }
     u32 gx, gy;
+    if (e->splits > 1) {
+        /* split group reduce: partials into the workspace, then the combine */
+        float *ws = reduce_workspace((u64)e->total * e->splits * sizeof(float));
+        if (!ws) return;
+        params[2 * nb] = &ws;
+        grid_for(e->total * e->splits, e->block, &gx, &gy);
+        hipb_launch(e->fn, gx, gy, 1, e->block, params);
+        void *p2[] = {&ptrs[0], &counts[0], &ws};
+        hipb_launch(e->fn_fin, (u32)((e->total + 255) / 256), 1, 1, 256, p2);
+        pool_mark_device_write(out_buf);
+        return;
+    }
     if (e->mode == KG_MODE_GROUP) grid_for(e->total, e->block, &gx, &gy);
     else grid_for((e->n_threads + e->block - 1) / e->block, e->block, &gx, &gy);
     hipb_launch(e->fn, gx, gy, 1, e->block, params);
@@ -248,14 +267,13 @@ static void hb_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **leaf
     for (u32 i = 0; i < n_ops; i++) P->ops[i] = ops[i];
 
     hipFunction_t fn = rtc_static_fn("thvm_rs");
-    u32 pbuf = pool_alloc(psize);
-    if (!fn || !pbuf) {
+    u64 pcap = 0;
+    void *dp = fn ? pool_block_get(psize, &pcap) : NULL;
+    if (!dp) {
         free(P);
-        if (pbuf) pool_free(pbuf);
         return;
     }
-    pool_write(pbuf, P, psize);
-    void *dp = pool_ptr(pbuf);
+    pool_upload(dp, P, psize);
     u32 threads = P->has_reduce ? out_numel : full_numel;
     u32 phase0 = 0, phase1 = 1;
     void *a0[] = {&dp, &phase0};
@@ -263,7 +281,7 @@ static void hb_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **leaf
     if (threads) hipb_launch(fn, (threads + 63) / 64, 1, 1, 64, a0);
     if (P->has_reduce && P->post_start && P->post_start < n_ops && out_numel)
         hipb_launch(fn, (out_numel + 63) / 64, 1, 1, 64, a1);
-    pool_free(pbuf);   /* stream order keeps the block alive for the kernels above */
+    pool_block_put(dp, pcap);   /* stream order keeps the block alive for the kernels above */
     pool_mark_device_write(out_buf);
     free(P);
     hipb.n_dispatch++;

@@ -41,7 +41,7 @@
 
 #define DG_MAX 8
 #define DENSE_MIN_K 16
-#define DENSE_MIN_WORK (1ull << 16)
+#define DENSE_MIN_WORK (1ull << 12)
 
 static int op_type_is_float(KOpType t) {
     return t == KOP_CONST_F || t == KOP_LOAD || t == KOP_ALU || t == KOP_ACC_INIT || t == KOP_MASK;
@@ -466,6 +466,7 @@ typedef struct {
 
 #define BK 16
 #define GEMM_THREADS 256
+#define SUM_WAVE_MIN_SPLITS 16   /* split-K sums this long use a wavefront per output */
 
 /* Loader lane map for one operand: x in [0, BX) along the tile's M or N side,
  * k in [0, BK). k-major operands put 16 consecutive lanes on consecutive k,
@@ -609,14 +610,29 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
         snprintf(fb, sizeof fb, "__uint_as_float(0x%08xu)", bits);
         const char *st = k->out_dtype == DTYPE_F16 ? "st_f16" : k->out_dtype == DTYPE_I32 ? "st_i32"
                          : k->out_dtype == DTYPE_U32 ? "st_u32" : "st_f32";
-        dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
-                    "  const unsigned long long t = (unsigned long long)blockIdx.x * 256u + threadIdx.x;\n"
-                    "  if (t >= %lluull) return;\n"
-                    "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
-                    "  float a = 0.0f;\n"
-                    "  for (u32 s = 0; s < %uu; s++) a = a + ws[(unsigned long long)s * %lluull + t];\n"
-                    "  %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
-                pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
+        if (pl->splits >= SUM_WAVE_MIN_SPLITS) {
+            /* many splits: one wavefront per output; lane l adds splits l, l+64, ...
+             * in order, then a fixed shuffle tree (deterministic) */
+            dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
+                        "  const unsigned long long t = (unsigned long long)blockIdx.x * 4u + (threadIdx.x >> 6);\n"
+                        "  const u32 lane = threadIdx.x & 63u;\n"
+                        "  if (t >= %lluull) return;\n"
+                        "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
+                        "  float a = 0.0f;\n"
+                        "  for (u32 s = lane; s < %uu; s += 64u) a = a + ws[(unsigned long long)s * %lluull + t];\n"
+                        "  a = wsum(a);\n"
+                        "  if (lane == 0u) %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
+                    pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
+        } else {
+            dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
+                        "  const unsigned long long t = (unsigned long long)blockIdx.x * 256u + threadIdx.x;\n"
+                        "  if (t >= %lluull) return;\n"
+                        "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
+                        "  float a = 0.0f;\n"
+                        "  for (u32 s = 0; s < %uu; s++) a = a + ws[(unsigned long long)s * %lluull + t];\n"
+                        "  %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
+                    pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
+        }
     }
     return s.p;
 }
@@ -638,8 +654,7 @@ typedef struct {
 static struct {
     DenseEntry *tab;
     u32 cap, n;
-    u32 ws_buf;
-    u64 ws_bytes;
+    Scratch ws;            /* split-K partial sums */
 } D;
 
 static void meta_of(const UOpKernel *k, u32 *m) {
@@ -794,14 +809,8 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     /* split-K workspace */
     float *ws = NULL;
     if (e->plan.splits > 1) {
-        u64 need = (u64)e->plan.splits * e->M * e->N * sizeof(float);
-        if (need > D.ws_bytes) {
-            if (D.ws_buf) pool_free(D.ws_buf);
-            D.ws_buf = pool_alloc(need);
-            D.ws_bytes = D.ws_buf ? need : 0;
-            if (!D.ws_buf) return 0;
-        }
-        ws = pool_ptr(D.ws_buf);
+        ws = scratch_reserve(&D.ws, (u64)e->plan.splits * e->M * e->N * sizeof(float));
+        if (!ws) return 0;
     }
     void *ptrs[FUSE_MAX_LEAVES + 1];
     u32 counts[FUSE_MAX_LEAVES + 1];
@@ -825,7 +834,8 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     if (e->plan.splits > 1) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};
         u64 mn = (u64)e->M * e->N;
-        if (!hipb_launch_grid(e->fn_sum, (u32)((mn + 255) / 256), 1, 256, p2)) return 0;
+        u64 per_block = e->plan.splits >= SUM_WAVE_MIN_SPLITS ? 4 : 256;
+        if (!hipb_launch_grid(e->fn_sum, (u32)((mn + per_block - 1) / per_block), 1, 256, p2)) return 0;
     }
     return 1;
 }
@@ -841,5 +851,6 @@ void dense_shutdown(void) {
         }
         free(D.tab);
     }
+    scratch_release(&D.ws);
     memset(&D, 0, sizeof D);
 }

@@ -63,6 +63,13 @@ typedef struct {
 int   pool_init(void);
 void  pool_shutdown(void);
 u32   pool_alloc(u64 bytes);
+/* device blocks outside the engine's id space */
+typedef struct { void *ptr; u64 cap; } Scratch;
+void *pool_block_get(u64 bytes, u64 *cap_out);
+void  pool_block_put(void *ptr, u64 cap);
+void *scratch_reserve(Scratch *sc, u64 bytes);
+void  scratch_release(Scratch *sc);
+void  pool_upload(void *dst, const void *src, u64 bytes);
 void  pool_free(u32 id);
 void  pool_incref(u32 id);
 void  pool_decref(u32 id);
@@ -88,6 +95,7 @@ typedef struct {
     u32 block;            /* threads per workgroup */
     u64 total;            /* serial: gids; group: outputs */
     u64 n_threads;        /* serial: number of vector lanes (ceil(total/vec)) */
+    u32 splits;           /* group: workgroups per output; > 1 adds a <name>_fin combine kernel */
 } KGenResult;
 
 int  kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen);
@@ -102,6 +110,8 @@ typedef struct {
     u64 key;
     hipModule_t mod;
     hipFunction_t fn;
+    hipFunction_t fn_fin;  /* split group reduce: combine kernel */
+    u32 splits;
     int mode;
     u32 vec, block;
     u64 total, n_threads;

@@ -96,6 +96,8 @@ typedef struct {
     u32 per_thread;    /* SERIAL: thread-vectors per thread */
     u32 ew_block;      /* SERIAL: workgroup size (0: chosen by size) */
     u32 red_block;     /* GROUP: largest workgroup size */
+    u32 splits;        /* GROUP: workgroups per output (1: whole loop in one) */
+    u32 split_acc;     /* GROUP split: the accumulator op */
     SB sb;
     char err[256];
 } Gen;
@@ -140,8 +142,7 @@ int kgen_validate(const UOpKernel *k, char *err, size_t errlen) {
     if (k->out_dtype >= DTYPE_COUNT) { snprintf(err, errlen, "bad out dtype %u", k->out_dtype); return 0; }
     for (u32 i = 0; i < k->n_leaves; i++)
         if (k->leaf_dtypes[i] >= DTYPE_COUNT) { snprintf(err, errlen, "bad leaf dtype"); return 0; }
-    i32 stack[KOP_MAX];
-    int sp = 0;
+    int sp = 0;   /* open RANGEs; ENDRANGE closes the innermost, as the interpreter pairs them */
     for (u32 i = 0; i < k->n_ops; i++) {
         const KOp *op = &k->ops[i];
         if (op->type <= KOP_NOOP || op->type > KOP_MASK) {
@@ -160,7 +161,7 @@ int kgen_validate(const UOpKernel *k, char *err, size_t errlen) {
             snprintf(err, errlen, "op %u: accumulator %u is not an ACC_INIT op", i, op->arg[0]);
             return 0;
         }
-        if (op->type == KOP_RANGE) stack[sp++] = (i32)i;
+        if (op->type == KOP_RANGE) sp++;
         if (op->type == KOP_ENDRANGE) {
             if (sp == 0) { snprintf(err, errlen, "op %u: ENDRANGE without RANGE", i); return 0; }
             sp--;
@@ -880,6 +881,44 @@ static void emit_params(Gen *g) {
     for (u32 b = 0; b < nb; b++) sb_put(&g->sb, ", u32 c%u", b);
 }
 
+/* GROUP kernels with few outputs and a long reduction (per-channel sums of
+ * a whole batch: a handful of outputs over 10^5 elements) would leave most
+ * CUs idle with one workgroup per output. When the program is a single
+ * reduce loop whose accumulator is stored as is at gid, each output is split
+ * over several workgroups: each writes its partial to a workspace, and a
+ * second kernel combines the partials of an output in a fixed order
+ * (SUM: init + p0 + p1 + ..., RMAX: the engine's a > b ? a : b). */
+#define SPLIT_MAX_OUTPUTS 256u
+#define SPLIT_MIN_TRIP 8192u
+#define SPLIT_MIN_CHUNK 2048u
+
+static void group_split_plan(Gen *g) {
+    const UOpKernel *k = g->k;
+    i32 r = -1;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        if (k->ops[i].type == KOP_RANGE && g->oi[i].depth == 0) {
+            if (r >= 0) return;                       /* more than one loop */
+            r = (i32)i;
+        }
+    }
+    if (r < 0) return;
+    u32 e = g->oi[r].end, trip = k->ops[r].imm.u;
+    if (g->total > SPLIT_MAX_OUTPUTS || trip < SPLIT_MIN_TRIP) return;
+    /* after the loop: exactly STORE(gid op, accumulator) */
+    if (e + 2 != k->n_ops) return;
+    const KOp *st = &k->ops[e + 1];
+    if (st->type != KOP_STORE || k->ops[st->arg[0]].type != KOP_GID) return;
+    u32 t = st->arg[1];
+    if (k->ops[t].type != KOP_ACC_INIT || !g->oi[t].acc_tgt) return;
+    for (u32 i = 0; i < k->n_ops; i++)
+        if (i != t && g->oi[i].acc_tgt) return;       /* one accumulator */
+    u32 S = 1;
+    while (g->total * S < 512u && trip / (S * 2) >= SPLIT_MIN_CHUNK && S < 64u) S *= 2;
+    if (S < 2) return;
+    g->splits = S;
+    g->split_acc = t;
+}
+
 /* One parallel loop of GROUP mode. */
 static void emit_group_loop(Gen *g, u32 r) {
     const UOpKernel *k = g->k;
@@ -932,10 +971,17 @@ static void emit_group_loop(Gen *g, u32 r) {
                (unsigned long long)span, gv, gv, (unsigned long long)span, bi);
     }
     u32 nq = trip / V;
+    if (g->splits > 1) {
+        u32 cq = (nq + g->splits - 1) / g->splits;
+        sb_put(&g->sb, "    const u32 qlo_ = sp_ * %uu, qhi_ = (qlo_ + %uu < %uu) ? qlo_ + %uu : %uu;\n", cq, cq, nq,
+               cq, nq);
+    } else {
+        sb_put(&g->sb, "    const u32 qlo_ = 0u, qhi_ = %uu;\n", nq);
+    }
     for (int pass = 0; pass < 2; pass++) {
         sb_put(&g->sb, pass == 0 ? "    if (ok_) {\n" : "    } else {\n");
         if (g->unroll > 1) sb_put(&g->sb, "    #pragma unroll %u\n", g->unroll);
-        sb_put(&g->sb, "    for (u32 q_ = lane; q_ < %uu; q_ += %uu) {\n    n%u = q_ * %uu;\n", nq, g->block, r, V);
+        sb_put(&g->sb, "    for (u32 q_ = qlo_ + lane; q_ < qhi_; q_ += %uu) {\n    n%u = q_ * %uu;\n", g->block, r, V);
         emit_range_seq(g, r + 1, e, pass == 0, 1);
         sb_put(&g->sb, "    }\n");
     }
@@ -950,14 +996,22 @@ static void emit_group_loop(Gen *g, u32 r) {
         if (g->oi[t].acc_type == UOP_RMAX) {
             sb_put(&g->sb, "    { float t_ = p%u_0;\n", t);
             for (u32 v = 1; v < V; v++) sb_put(&g->sb, "      t_ = (t_ > p%u_%u) ? t_ : p%u_%u;\n", t, v, t, v);
-            sb_put(&g->sb, "      f%u = bmax(t_, red_); }\n", t);
+            if (g->splits > 1)
+                sb_put(&g->sb, "      t_ = bmax(t_, red_);\n"
+                               "      if (lane == 0) ws_[(unsigned long long)gid * %uu + sp_] = t_; }\n", g->splits);
+            else
+                sb_put(&g->sb, "      f%u = bmax(t_, red_); }\n", t);
         } else {
             if (V == 4) sb_put(&g->sb, "    { float t_ = (p%u_0 + p%u_1) + (p%u_2 + p%u_3);\n", t, t, t, t);
             else {
                 sb_put(&g->sb, "    { float t_ = p%u_0;\n", t);
                 for (u32 v = 1; v < V; v++) sb_put(&g->sb, "      t_ = t_ + p%u_%u;\n", t, v);
             }
-            sb_put(&g->sb, "      f%u = f%u + bsum(t_, red_); }\n", t, t);
+            if (g->splits > 1)
+                sb_put(&g->sb, "      t_ = bsum(t_, red_);\n"
+                               "      if (lane == 0) ws_[(unsigned long long)gid * %uu + sp_] = t_; }\n", g->splits);
+            else
+                sb_put(&g->sb, "      f%u = f%u + bsum(t_, red_); }\n", t, t);
         }
     }
     sb_put(&g->sb, "  }\n");
@@ -1018,6 +1072,8 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
         u64 nv = ((u64)total + G.V - 1) / G.V;
         G.block = G.ew_block ? G.ew_block : (nv >= (4ull << 20) ? 1024 : 256);
     }
+    G.splits = 1;
+    if (G.mode == KG_MODE_GROUP) group_split_plan(&G);
     analyze_vector(&G);
     analyze_global(&G);
 
@@ -1031,6 +1087,7 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
     }
     sb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", G.block, out->name);
     emit_params(&G);
+    if (G.splits > 1) sb_put(s, ", float* ws_");
     sb_put(s, ") {\n");
     if (G.mode == KG_MODE_SERIAL) {
         u64 nvec = ((u64)total + G.V - 1) / G.V;          /* thread-vectors */
@@ -1053,7 +1110,12 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
         if (W > 1) sb_put(s, "  }\n");
         out->n_threads = nthreads;
     } else {
-        sb_put(s, "  const u32 gid = blockIdx.y * gridDim.x + blockIdx.x;\n");
+        if (G.splits > 1) {
+            sb_put(s, "  const u32 bid_ = blockIdx.y * gridDim.x + blockIdx.x;\n");
+            sb_put(s, "  const u32 gid = bid_ / %uu, sp_ = bid_ %% %uu;\n", G.splits, G.splits);
+        } else {
+            sb_put(s, "  const u32 gid = blockIdx.y * gridDim.x + blockIdx.x;\n");
+        }
         sb_put(s, "  if (gid >= %uu) return;\n", total);
         sb_put(s, "  const u32 lane = threadIdx.x;\n");
         sb_put(s, "  __shared__ float red_[%u];\n", G.block / 64);
@@ -1063,6 +1125,7 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
             if (op->type == KOP_RANGE && G.oi[i].depth == 0) {
                 emit_group_loop(&G, i);
                 i = G.oi[i].end;
+                if (G.splits > 1) break;      /* the store happens in the combine kernel */
                 continue;
             }
             if (op->type == KOP_ENDRANGE) continue;
@@ -1071,6 +1134,22 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
         out->n_threads = total;
     }
     sb_put(s, "}\n");
+    if (G.splits > 1) {
+        const KOp *init = &k->ops[G.split_acc];
+        u32 bits = init->imm.u;
+        int rmax = G.oi[G.split_acc].acc_type == UOP_RMAX;
+        sb_put(s, "extern \"C\" __global__ __launch_bounds__(256) void %s_fin(char* p0, u32 c0, const float* ws_) {\n"
+                  "  const u32 o = blockIdx.x * 256u + threadIdx.x;\n"
+                  "  if (o >= %uu) return;\n"
+                  "  float f = __uint_as_float(0x%08xu);\n"
+                  "  for (u32 s = 0; s < %uu; s++) {\n"
+                  "    const float w = ws_[(unsigned long long)o * %uu + s];\n"
+                  "    %s\n"
+                  "  }\n"
+                  "  %s(p0, c0, o, f);\n}\n",
+               out->name, total, bits, G.splits, G.splits, rmax ? "f = (f > w) ? f : w;" : "f = f + w;",
+               dt_st(k->out_dtype));
+    }
     free(G.oi);
     if (!s->p) { snprintf(err, errlen, "oom"); return 0; }
     out->src = s->p;
@@ -1078,6 +1157,7 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
     out->vec = G.V;
     out->block = G.block;
     out->total = total;
+    out->splits = G.splits;
     return 1;
 }
 

@@ -134,8 +134,9 @@ static int ensure_cap(u32 id) {
     return 1;
 }
 
-u32 pool_alloc(u64 bytes) {
-    if (!hipb.initialized) return 0;
+/* A device block of at least `bytes` from its size class's free list, or
+ * hipMalloc (after releasing the cached blocks on failure). */
+void *pool_block_get(u64 bytes, u64 *cap_out) {
     u64 cap = 0;
     u32 c = size_class(bytes ? bytes : 4, &cap);
     void *ptr = NULL;
@@ -150,15 +151,50 @@ u32 pool_alloc(u64 bytes) {
                 (void)hipGetLastError();
                 fprintf(stderr, "tinyhvm-hip: out of device memory (%llu bytes)\n",
                         (unsigned long long)cap);
-                return 0;
+                return NULL;
             }
         }
         P.n_mallocs++;
     }
+    *cap_out = cap;
+    return ptr;
+}
+
+/* Returns a block to its free list. The stream orders its last users before
+ * any later owner's work. */
+void pool_block_put(void *ptr, u64 cap) {
+    if (!ptr) return;
+    u64 c2 = 0;
+    u32 c = size_class(cap, &c2);
+    if (fl_push(&P.free[c], ptr)) P.cached_bytes += c2;
+    else HIPB_CHECK(hipFree(ptr));
+}
+
+/* Device scratch outside the engine's buffer ids (kernel workspaces): grown
+ * on demand, kept until released. Engine ids are never used for it, so
+ * pool_reset cannot free it and the engine's id numbering is untouched. */
+void *scratch_reserve(Scratch *sc, u64 bytes) {
+    if (bytes <= sc->cap && sc->ptr) return sc->ptr;
+    pool_block_put(sc->ptr, sc->cap);
+    sc->ptr = pool_block_get(bytes, &sc->cap);
+    if (!sc->ptr) sc->cap = 0;
+    return sc->ptr;
+}
+
+void scratch_release(Scratch *sc) {
+    pool_block_put(sc->ptr, sc->cap);
+    sc->ptr = NULL;
+    sc->cap = 0;
+}
+
+u32 pool_alloc(u64 bytes) {
+    if (!hipb.initialized) return 0;
+    u64 cap = 0;
+    void *ptr = pool_block_get(bytes, &cap);
+    if (!ptr) return 0;
     u32 id = P.count;
     if (!ensure_cap(id)) {
-        fl_push(&P.free[c], ptr);
-        P.cached_bytes += cap;
+        pool_block_put(ptr, cap);
         return 0;
     }
     P.count++;
@@ -301,6 +337,20 @@ void pool_write(u32 id, const void *data, u64 bytes) {
         HIPB_CHECK(hipMemcpyAsync(b->ptr, s, bytes, hipMemcpyHostToDevice, hipb.stream));
     } else {
         HIPB_CHECK(hipMemcpyAsync(b->ptr, data, bytes, hipMemcpyHostToDevice, hipb.stream));
+        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    }
+}
+
+/* Host bytes to device memory on the stream (through the staging ring, so
+ * the caller's memory may be reused on return). */
+void pool_upload(void *dst, const void *src, u64 bytes) {
+    if (!dst || !src || bytes == 0) return;
+    if (bytes <= STAGE_SEG_BYTES) {
+        u8 *s = stage_reserve(bytes);
+        memcpy(s, src, bytes);
+        HIPB_CHECK(hipMemcpyAsync(dst, s, bytes, hipMemcpyHostToDevice, hipb.stream));
+    } else {
+        HIPB_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, hipb.stream));
         HIPB_CHECK(hipStreamSynchronize(hipb.stream));
     }
 }

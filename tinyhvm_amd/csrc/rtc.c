@@ -229,8 +229,11 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
         kgen_free(&g);
         return NULL;
     }
-    hipFunction_t fn;
-    if (hipModuleGetFunction(&fn, mod, g.name) != hipSuccess) {
+    hipFunction_t fn, fn_fin = NULL;
+    char fin_name[48];
+    snprintf(fin_name, sizeof fin_name, "%s_fin", g.name);
+    if (hipModuleGetFunction(&fn, mod, g.name) != hipSuccess ||
+        (g.splits > 1 && hipModuleGetFunction(&fn_fin, mod, fin_name) != hipSuccess)) {
         fprintf(stderr, "tinyhvm-hip: kernel symbol missing\n");
         HIPB_CHECK(hipModuleUnload(mod));
         kgen_free(&g);
@@ -245,6 +248,8 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
     e->key = key;
     e->mod = mod;
     e->fn = fn;
+    e->fn_fin = fn_fin;
+    e->splits = g.splits > 1 ? g.splits : 1;
     e->mode = g.mode;
     e->vec = g.vec;
     e->block = g.block;
