@@ -23,6 +23,53 @@ HipbState hipb;
  * dispatch (the stream orders the users). */
 static Scratch red_ws;
 
+/* ASSIGN's buf_copy calls are queued and issued together as one batched copy
+ * kernel: an SGD step copies every updated parameter back, one copy after
+ * each update kernel, and none of those kernels touches an earlier copy's
+ * buffers. Anything that does touch a queued buffer (a dispatch reading or
+ * writing it, a host read or write, a free) issues the queue first, so the
+ * stream still sees every copy before any later use of its buffers. */
+static struct {
+    CopyBatch b;
+    u32 dst_id[COPY_BATCH_MAX], src_id[COPY_BATCH_MAX];
+} CQ;
+
+static void copyq_flush(void) {
+    if (CQ.b.n == 0) return;
+    hipFunction_t fn = rtc_static_fn("thvm_copy_batch");
+    if (fn) {
+        u64 mx = 0;
+        for (u32 i = 0; i < CQ.b.n; i++) if (CQ.b.bytes[i] > mx) mx = CQ.b.bytes[i];
+        u64 gx = (mx + 4095) / 4096;
+        if (gx < 1) gx = 1;
+        if (gx > 256) gx = 256;
+        void *params[] = {&CQ.b};
+        hipb_launch(fn, (u32)gx, CQ.b.n, 1, 256, params);
+    } else {
+        for (u32 i = 0; i < CQ.b.n; i++)
+            HIPB_CHECK(hipMemcpyAsync((void *)(uintptr_t)CQ.b.dst[i], (const void *)(uintptr_t)CQ.b.src[i],
+                                      CQ.b.bytes[i], hipMemcpyDeviceToDevice, hipb.stream));
+    }
+    CQ.b.n = 0;
+}
+
+static int copyq_uses(u32 id) {
+    for (u32 i = 0; i < CQ.b.n; i++)
+        if (CQ.dst_id[i] == id || CQ.src_id[i] == id) return 1;
+    return 0;
+}
+
+/* issue the queue if buffer id takes part in it */
+static void copyq_guard(u32 id) {
+    if (CQ.b.n && id && copyq_uses(id)) copyq_flush();
+}
+
+static void copyq_guard_dispatch(u32 out, const u32 *leaves, u32 n) {
+    if (!CQ.b.n) return;
+    copyq_guard(out);
+    for (u32 i = 0; i < n && CQ.b.n; i++) copyq_guard(leaves[i]);
+}
+
 static int env_flag(const char *name) {
     const char *v = getenv(name);
     return v && v[0] && strcmp(v, "0") != 0;
@@ -74,6 +121,7 @@ static int hb_init(void) {
 
 static void hb_shutdown(void) {
     if (!hipb.initialized) return;
+    copyq_flush();
     HIPB_CHECK(hipStreamSynchronize(hipb.stream));
     dense_shutdown();
     rtc_shutdown();
@@ -84,15 +132,15 @@ static void hb_shutdown(void) {
 }
 
 static u32 hb_buf_alloc(u64 bytes) { return pool_alloc(bytes); }
-static void hb_buf_free(u32 id) { pool_free(id); }
+static void hb_buf_free(u32 id) { copyq_guard(id); pool_free(id); }
 static void hb_buf_incref(u32 id) { pool_incref(id); }
-static void hb_buf_decref(u32 id) { pool_decref(id); }
-static void hb_buf_write(u32 id, const void *data, u64 bytes) { pool_write(id, data, bytes); }
-static void hb_buf_read(u32 id, void *out, u64 bytes) { pool_read(id, out, bytes, 0); }
-static void hb_buf_read_nosync(u32 id, void *out, u64 bytes) { pool_read(id, out, bytes, 1); }
+static void hb_buf_decref(u32 id) { copyq_guard(id); pool_decref(id); }
+static void hb_buf_write(u32 id, const void *data, u64 bytes) { copyq_guard(id); pool_write(id, data, bytes); }
+static void hb_buf_read(u32 id, void *out, u64 bytes) { copyq_guard(id); pool_read(id, out, bytes, 0); }
+static void hb_buf_read_nosync(u32 id, void *out, u64 bytes) { copyq_guard(id); pool_read(id, out, bytes, 1); }
 static void hb_mem_checkpoint(u32 *ids, u32 n) { (void)ids; (void)n; }
 static void hb_buf_mark_use(u32 id) { (void)id; }
-static void hb_pool_reset(u32 keep) { pool_reset(keep); }
+static void hb_pool_reset(u32 keep) { copyq_flush(); pool_reset(keep); }
 static void hb_pool_set_persistent(u32 max_buf) { pool_set_persistent(max_buf); }
 static void hb_begin_batch(void) {}
 static void hb_end_batch(void) {}
@@ -153,8 +201,8 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         return;
     }
     hipb.n_dispatch++;
+    copyq_guard_dispatch(out_buf, leaf_bufs, n_leaves < FUSE_MAX_LEAVES ? n_leaves : FUSE_MAX_LEAVES);
     pool_sync_device(out_buf);
-    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     if (!hipb.no_dense && dense_try_dispatch(out_buf, leaf_bufs, n_leaves, k)) {
         pool_mark_device_write(out_buf);
         hipb.n_dense++;
@@ -164,14 +212,36 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     KCacheEntry *e = rtc_lookup(key, k);
     if (e) hipb.n_cache_hit++;
     else e = rtc_compile_uop(key, k);
-    if (!e) return;
+    if (!e) {
+        for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
+        return;
+    }
+
+    /* constant-index loads of host-held leaves take their value inline; a
+     * leaf read only that way is not uploaded */
+    u32 sm = 0;
+    float sv[KGEN_MAX_SCALARS];
+    for (u32 j = 0; j < e->n_scal; j++) {
+        u32 leaf = e->scal_leaf[j];
+        u32 id = leaf < n_leaves ? leaf_bufs[leaf] : 0;
+        sv[j] = 0.0f;
+        if (id && id != out_buf && pool_host_value(id, k->leaf_dtypes[leaf], e->scal_index[j], &sv[j]))
+            sm |= 1u << j;
+    }
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) {
+        int inline_only = i < 32 && ((e->scal_only_leaves >> i) & 1u);
+        for (u32 j = 0; j < e->n_scal && inline_only; j++)
+            if (e->scal_leaf[j] == i && !((sm >> j) & 1u)) inline_only = 0;
+        if (!inline_only) pool_sync_device(leaf_bufs[i]);
+    }
     if (e->total == 0) return;
 
-    /* kernel parameters: p0..pN (buffer pointers), then c0..cN (element counts) */
+    /* kernel parameters: p0..pN (buffer pointers), c0..cN (element counts),
+     * then sm_ and the inline scalars, then the split-reduce workspace */
     u32 nb = k->n_leaves + 1;
     void *ptrs[FUSE_MAX_LEAVES + 1];
     u32 counts[FUSE_MAX_LEAVES + 1];
-    void *params[2 * (FUSE_MAX_LEAVES + 1) + 1];
+    void *params[2 * (FUSE_MAX_LEAVES + 1) + 2 + KGEN_MAX_SCALARS];
     ptrs[0] = ob->ptr;
     counts[0] = elem_count(out_buf, k->out_dtype);
     for (u32 i = 0; i < k->n_leaves; i++) {
@@ -183,12 +253,17 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         params[b] = &ptrs[b];
         params[nb + b] = &counts[b];
     }
+    u32 np = 2 * nb;
+    if (e->n_scal) {
+        params[np++] = &sm;
+        for (u32 j = 0; j < e->n_scal; j++) params[np++] = &sv[j];
+    }
     u32 gx, gy;
     if (e->splits > 1) {
         /* split group reduce: partials into the workspace, then the combine */
         float *ws = reduce_workspace((u64)e->total * e->splits * sizeof(float));
         if (!ws) return;
-        params[2 * nb] = &ws;
+        params[np] = &ws;
         grid_for(e->total * e->splits, e->block, &gx, &gy);
         hipb_launch(e->fn, gx, gy, 1, e->block, params);
         void *p2[] = {&ptrs[0], &counts[0], &ws};
@@ -212,6 +287,7 @@ static void hb_dispatch_kernel_rs(u32 out_buf, u32 *leaf_bufs, const View **leaf
     if (!hipb.initialized || !full_shape) return;
     HipbBuf *ob = pool_get(out_buf);
     if (!ob) return;
+    copyq_guard_dispatch(out_buf, leaf_bufs, n_leaves < FUSE_MAX_LEAVES ? n_leaves : FUSE_MAX_LEAVES);
     pool_sync_device(out_buf);
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     if (n_leaves > FUSE_MAX_LEAVES || n_ops > FUSE_MAX_OPS || out_dtype >= DTYPE_COUNT) {
@@ -291,6 +367,8 @@ static void hb_contiguify(u32 dst_buf, u32 numel, u32 src_buf, const View *src_v
     if (!hipb.initialized || !src_view || numel == 0) return;
     HipbBuf *d = pool_get(dst_buf), *s = pool_get(src_buf);
     if (!d) return;
+    copyq_guard(dst_buf);
+    copyq_guard(src_buf);
     pool_sync_device(dst_buf);
     pool_sync_device(src_buf);
     hipFunction_t fn = rtc_static_fn("thvm_contiguify");
@@ -318,6 +396,12 @@ static void hb_contiguify(u32 dst_buf, u32 numel, u32 src_buf, const View *src_v
  * backend's order (src/backend/cpu/ops.c), so results are bit-identical. */
 static u32 elems_of(const HipbBuf *b, u32 dt) { return b ? (u32)(b->bytes / (dt == DTYPE_F16 ? 2u : 4u)) : 0u; }
 
+static void legacy_guard(u32 dst, u32 a, u32 b) {
+    copyq_guard(dst);
+    copyq_guard(a);
+    copyq_guard(b);
+}
+
 static void legacy_launch(const char *name, LegacyArgs *a, u32 dst) {
     hipFunction_t fn = rtc_static_fn(name);
     if (fn && a->n) {
@@ -330,6 +414,7 @@ static void legacy_launch(const char *name, LegacyArgs *a, u32 dst) {
 static void hb_op_unary(u32 uop, u32 dst, const View *dv, u32 dd, u32 src, const View *sv, u32 sd) {
     HipbBuf *d = pool_get(dst), *s = pool_get(src);
     if (!hipb.initialized || !d || !dv || !sv) return;
+    legacy_guard(dst, src, 0);
     pool_sync_device(dst);
     pool_sync_device(src);
     LegacyArgs a;
@@ -344,6 +429,7 @@ static void hb_op_binary(u32 uop, u32 dst, const View *dv, u32 dd, u32 ab, const
                          const View *bv, u32 bd) {
     HipbBuf *d = pool_get(dst), *x = pool_get(ab), *y = pool_get(bb);
     if (!hipb.initialized || !d || !dv || !av || !bv) return;
+    legacy_guard(dst, ab, bb);
     pool_sync_device(dst);
     pool_sync_device(ab);
     pool_sync_device(bb);
@@ -364,6 +450,7 @@ static void hb_op_mm(u32 dst, u32 dd, u32 ab, const View *av, u32 ad, u32 bb, co
         fprintf(stderr, "tinyhvm-hip: op_mm %ux%u output exceeds u32 indexing\n", M, N);
         return;
     }
+    legacy_guard(dst, ab, bb);
     pool_sync_device(dst);
     pool_sync_device(ab);
     pool_sync_device(bb);
@@ -380,6 +467,7 @@ static void hb_op_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn, u32 
     HipbBuf *d = pool_get(dst), *s = pool_get(src);
     (void)sn;
     if (!hipb.initialized || !d) return;
+    legacy_guard(dst, src, 0);
     pool_sync_device(dst);
     pool_sync_device(src);
     LegacyArgs a;
@@ -393,12 +481,25 @@ static void hb_op_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn, u32 
 static void hb_buf_copy(u32 dst_buf, u32 src_buf, u64 nbytes) {
     HipbBuf *d = pool_get(dst_buf), *s = pool_get(src_buf);
     if (!d || !s || nbytes == 0) return;
+    /* a queued copy that writes this copy's source or touches its
+     * destination must land first */
+    for (u32 i = 0; i < CQ.b.n; i++)
+        if (CQ.dst_id[i] == src_buf || CQ.dst_id[i] == dst_buf || CQ.src_id[i] == dst_buf) {
+            copyq_flush();
+            break;
+        }
     pool_sync_device(dst_buf);
     pool_sync_device(src_buf);
     u64 n = nbytes;
     if (n > d->cap) n = d->cap;
     if (n > s->cap) n = s->cap;
-    HIPB_CHECK(hipMemcpyAsync(d->ptr, s->ptr, n, hipMemcpyDeviceToDevice, hipb.stream));
+    if (CQ.b.n == COPY_BATCH_MAX) copyq_flush();
+    u32 q = CQ.b.n++;
+    CQ.b.dst[q] = (u64)(uintptr_t)d->ptr;
+    CQ.b.src[q] = (u64)(uintptr_t)s->ptr;
+    CQ.b.bytes[q] = n;
+    CQ.dst_id[q] = dst_buf;
+    CQ.src_id[q] = src_buf;
     pool_mark_device_write(dst_buf);
 }
 
@@ -491,6 +592,7 @@ void thvm_hip_profile_reset(void) { hb_profile_reset(); }
 
 int thvm_hip_synchronize(void) {
     if (!hipb.initialized) return -1;
+    copyq_flush();
     hipError_t e = hipStreamSynchronize(hipb.stream);
     if (e != hipSuccess) {
         fprintf(stderr, "tinyhvm-hip: stream error: %s\n", hipGetErrorString(e));

@@ -806,6 +806,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
                     ct.N, ct.K, e->plan.cfg.tag, e->plan.splits);
     }
     if (!e->is_dense) return 0;
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     /* split-K workspace */
     float *ws = NULL;
     if (e->plan.splits > 1) {

@@ -80,12 +80,14 @@ void *pool_ptr(u32 id);
 u64   pool_bytes(u32 id);
 void  pool_mark_device_write(u32 id);
 void  pool_sync_device(u32 id);
+int   pool_host_value(u32 id, u32 dtype, u32 idx, float *out);
 void  pool_write(u32 id, const void *data, u64 bytes);
 void  pool_read(u32 id, void *out, u64 bytes, int nosync);
 void  pool_stats(u64 *live_bytes, u64 *cached_bytes, u64 *n_mallocs);
 
 /* ---------------- code generation ---------------- */
 enum { KG_MODE_SERIAL = 0, KG_MODE_GROUP = 1 };
+#define KGEN_MAX_SCALARS 16
 
 typedef struct {
     char *src;            /* generated HIP source (malloc'd) */
@@ -96,6 +98,9 @@ typedef struct {
     u64 total;            /* serial: gids; group: outputs */
     u64 n_threads;        /* serial: number of vector lanes (ceil(total/vec)) */
     u32 splits;           /* group: workgroups per output; > 1 adds a <name>_fin combine kernel */
+    u32 n_scal;           /* constant-index leaf loads that take an inline value (sm_, sv*) */
+    u32 scal_leaf[KGEN_MAX_SCALARS], scal_index[KGEN_MAX_SCALARS];
+    u32 scal_only_leaves; /* bit b: every load of leaf b is such a load */
 } KGenResult;
 
 int  kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen);
@@ -112,6 +117,7 @@ typedef struct {
     hipFunction_t fn;
     hipFunction_t fn_fin;  /* split group reduce: combine kernel */
     u32 splits;
+    u32 n_scal, scal_leaf[KGEN_MAX_SCALARS], scal_index[KGEN_MAX_SCALARS], scal_only_leaves;
     int mode;
     u32 vec, block;
     u64 total, n_threads;

@@ -52,4 +52,11 @@ typedef struct {
     View av, bv;
 } LegacyArgs;
 
+/* batched buffer-to-buffer copies: passed by value */
+#define COPY_BATCH_MAX 32
+typedef struct {
+    u32 n, pad;
+    u64 dst[COPY_BATCH_MAX], src[COPY_BATCH_MAX], bytes[COPY_BATCH_MAX];
+} CopyBatch;
+
 #endif

@@ -98,6 +98,8 @@ typedef struct {
     u32 red_block;     /* GROUP: largest workgroup size */
     u32 splits;        /* GROUP: workgroups per output (1: whole loop in one) */
     u32 split_acc;     /* GROUP split: the accumulator op */
+    i32 *scal;         /* per op: index into the inline scalar list, or -1 */
+    u32 n_scal;
     SB sb;
     char err[256];
 } Gen;
@@ -567,6 +569,18 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
         u32 dt = bi == 0 ? k->out_dtype : k->leaf_dtypes[bi - 1];
         const OpI *ix = &g->oi[op->arg[0]];
         int unchecked = fast && ix->gk != G_NOT && !ix->ft && o->depth == 1;
+        if (g->scal && g->scal[i] >= 0) {
+            u32 j = (u32)g->scal[i];
+            U(g, op->arg[0], 0, a);
+            if (single)
+                sb_put(&g->sb, "    f%u = ((sm_ >> %uu) & 1u) ? sv%u : %s(p%u, c%u, %s);\n", i, j, j, dt_ld(dt), bi,
+                       bi, a);
+            else
+                for (u32 v = 0; v < V; v++)
+                    sb_put(&g->sb, "    f%u_%u = ((sm_ >> %uu) & 1u) ? sv%u : %s(p%u, c%u, %s);\n", i, v, j, j,
+                           dt_ld(dt), bi, bi, a);
+            break;
+        }
         if (single) {
             U(g, op->arg[0], 0, a);
             if (unchecked) sb_put(&g->sb, "    f%u = %s_u(p%u, %s);\n", i, dt_ld(dt), bi, a);
@@ -879,6 +893,39 @@ static void emit_params(Gen *g) {
     u32 nb = g->k->n_leaves + 1;
     for (u32 b = 0; b < nb; b++) sb_put(&g->sb, "%schar* p%u", b ? ", " : "", b);
     for (u32 b = 0; b < nb; b++) sb_put(&g->sb, ", u32 c%u", b);
+    if (g->n_scal) {
+        sb_put(&g->sb, ", u32 sm_");
+        for (u32 j = 0; j < g->n_scal; j++) sb_put(&g->sb, ", float sv%u", j);
+    }
+}
+
+/* Loads of a leaf element at a constant index (the engine's scalar leaves:
+ * learning rates, constants, counts) can take their value from a kernel
+ * argument: when the host still holds the leaf's contents (written by the
+ * host, not by a kernel since), it passes the value and sets bit j of sm_,
+ * and the leaf need not be uploaded at all. */
+static void plan_inline_scalars(Gen *g, KGenResult *out) {
+    const UOpKernel *k = g->k;
+    u32 scal_only = 0, other = 0;
+    g->n_scal = 0;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        g->scal[i] = -1;
+        const KOp *op = &k->ops[i];
+        if (op->type != KOP_LOAD) continue;
+        u32 bi = op->imm.u;
+        if (bi == 0 || bi > k->n_leaves) continue;
+        u32 bit = bi <= 32 ? 1u << (bi - 1) : 0u;
+        if (k->ops[op->arg[0]].type == KOP_CONST_U && g->n_scal < KGEN_MAX_SCALARS) {
+            out->scal_leaf[g->n_scal] = bi - 1;
+            out->scal_index[g->n_scal] = k->ops[op->arg[0]].imm.u;
+            g->scal[i] = (i32)g->n_scal++;
+            scal_only |= bit;
+        } else {
+            other |= bit;
+        }
+    }
+    out->n_scal = g->n_scal;
+    out->scal_only_leaves = scal_only & ~other;
 }
 
 /* GROUP kernels with few outputs and a long reduction (per-channel sums of
@@ -1074,6 +1121,9 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
     }
     G.splits = 1;
     if (G.mode == KG_MODE_GROUP) group_split_plan(&G);
+    G.scal = malloc(k->n_ops * sizeof(i32));
+    if (!G.scal) { free(G.oi); snprintf(err, errlen, "oom"); return 0; }
+    plan_inline_scalars(&G, out);
     analyze_vector(&G);
     analyze_global(&G);
 
@@ -1151,6 +1201,7 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
                dt_st(k->out_dtype));
     }
     free(G.oi);
+    free(G.scal);
     if (!s->p) { snprintf(err, errlen, "oom"); return 0; }
     out->src = s->p;
     out->mode = G.mode;

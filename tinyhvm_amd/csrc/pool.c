@@ -273,6 +273,39 @@ u64 pool_bytes(u32 id) {
     return b ? b->bytes : 0;
 }
 
+/* Element idx of a buffer from its host mirror, as the device loads read it
+ * (f16 widened exactly, integers converted to float; past the end reads 0).
+ * Returns 0 when the host does not hold the buffer's current contents. */
+int pool_host_value(u32 id, u32 dtype, u32 idx, float *out) {
+    HipbBuf *b = pool_get(id);
+    if (!b || !b->host_valid || !b->host_mirror) return 0;
+    u64 es = dtype == DTYPE_F16 ? 2 : 4;
+    if ((u64)idx * es + es > b->bytes) { *out = 0.0f; return 1; }
+    if ((u64)idx * es + es > b->mirror_bytes) return 0;
+    const u8 *p = (const u8 *)b->host_mirror + (u64)idx * es;
+    switch (dtype) {
+    case DTYPE_F16: {
+        u16 h;
+        memcpy(&h, p, 2);
+        u32 sign = ((u32)h & 0x8000u) << 16, ex = ((u32)h >> 10) & 0x1Fu, man = (u32)h & 0x3FFu, bits;
+        if (ex == 0) {
+            if (man == 0) bits = sign;
+            else {
+                ex = 1;
+                while (!(man & 0x400u)) { man <<= 1; ex -= 1; }
+                bits = sign | ((ex + 112u) << 23) | ((man & 0x3FFu) << 13);
+            }
+        } else if (ex == 0x1Fu) bits = sign | 0x7F800000u | (man << 13);
+        else bits = sign | ((ex + 112u) << 23) | (man << 13);
+        memcpy(out, &bits, 4);
+        return 1;
+    }
+    case DTYPE_I32: { i32 v; memcpy(&v, p, 4); *out = (float)v; return 1; }
+    case DTYPE_U32: { u32 v; memcpy(&v, p, 4); *out = (float)v; return 1; }
+    default: memcpy(out, p, 4); return 1;
+    }
+}
+
 void pool_mark_device_write(u32 id) {
     HipbBuf *b = pool_get(id);
     if (b) b->host_valid = 0;

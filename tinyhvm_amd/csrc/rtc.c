@@ -250,6 +250,10 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
     e->fn = fn;
     e->fn_fin = fn_fin;
     e->splits = g.splits > 1 ? g.splits : 1;
+    e->n_scal = g.n_scal;
+    memcpy(e->scal_leaf, g.scal_leaf, sizeof e->scal_leaf);
+    memcpy(e->scal_index, g.scal_index, sizeof e->scal_index);
+    e->scal_only_leaves = g.scal_only_leaves;
     e->mode = g.mode;
     e->vec = g.vec;
     e->block = g.block;

@@ -4,6 +4,7 @@
 //                    as the engine's host read src/ops/_.c:338-357
 //   thvm_op_ew / thvm_op_mm / thvm_op_reduce
 //                    the legacy per-op slots (src/backend/cpu/ops.c)
+//   thvm_copy_batch  several buffer-to-buffer copies in one launch
 //   thvm_fill_u32    fill a buffer with a 32-bit pattern (graph-safe clear)
 //
 // The rs interpreter restates the engine's CPU fallback
@@ -366,6 +367,24 @@ extern "C" __global__ __launch_bounds__(256) void thvm_op_reduce(LegacyArgs A) {
         else if (A.uop == UOP_RMAX) acc = v > acc ? v : acc;
     }
     store_from_f32((void *)(uintptr_t)A.dst, A.dd, A.dst_n, o, acc);
+}
+
+// Batched device copies (ASSIGN's buf_copy): blockIdx.y picks the copy; the
+// blocks of a row stride over it in 16-byte words, then the byte tail.
+extern "C" __global__ __launch_bounds__(256) void thvm_copy_batch(CopyBatch B) {
+    const u32 c = blockIdx.y;
+    if (c >= B.n) return;
+    char *d = (char *)(uintptr_t)B.dst[c];
+    const char *s = (const char *)(uintptr_t)B.src[c];
+    const unsigned long long nb = B.bytes[c], n16 = nb / 16u;
+    const unsigned long long t0 = (unsigned long long)blockIdx.x * 256u + threadIdx.x;
+    const unsigned long long step = (unsigned long long)gridDim.x * 256u;
+    if (((uintptr_t)d % 16u) == 0u && ((uintptr_t)s % 16u) == 0u) {
+        for (unsigned long long i = t0; i < n16; i += step) ((uint4 *)d)[i] = ((const uint4 *)s)[i];
+        for (unsigned long long i = n16 * 16u + t0; i < nb; i += step) d[i] = s[i];
+    } else {
+        for (unsigned long long i = t0; i < nb; i += step) d[i] = s[i];
+    }
 }
 
 extern "C" __global__ __launch_bounds__(256) void thvm_fill_u32(u32 *dst, u32 n, u32 value) {
