@@ -202,6 +202,12 @@ typedef struct {
     u32 np, nq;
     u32 pdiv[DG_MAX], pext[DG_MAX], qdiv[DG_MAX], qext[DG_MAX];
     int p_kmajor, q_kmajor;       /* lanes along k when loading the tile */
+    /* separable operands: the side is one LOAD whose index is f(gid) + g(r)
+     * (no digit mixes gid and r); the loader then adds a per-row base and a
+     * per-k offset instead of evaluating the operand's program per element */
+    int sep[2];
+    u32 sep_buf[2], sep_dt[2];
+    Aff sep_aff[2];
 } Contraction;
 
 /* The gid digits an operand consumes: those of the integer values its float
@@ -396,6 +402,14 @@ static int recognize(const UOpKernel *k, Contraction *ct) {
     ct->K = c.trip;
     ct->p_kmajor = cone_kmajor(&c, ct->coneP);
     ct->q_kmajor = cone_kmajor(&c, ct->coneQ);
+    for (int side = 0; side < 2; side++) {
+        const KOp *ld = &k->ops[side ? ct->rootQ : ct->rootP];
+        if (ld->type != KOP_LOAD || ld->imm.u > k->n_leaves || !c.aff[ld->arg[0]].ok) continue;
+        ct->sep[side] = 1;
+        ct->sep_buf[side] = ld->imm.u;
+        ct->sep_dt[side] = ld->imm.u == 0 ? k->out_dtype : k->leaf_dtypes[ld->imm.u - 1];
+        ct->sep_aff[side] = c.aff[ld->arg[0]];
+    }
     ct->ok = 1;
     return 1;
 }
@@ -445,16 +459,18 @@ static void emit_gid_fn(DSB *s, const char *name, u32 n, const u32 *div, const u
 /* Tile shapes. Every shape uses v_mfma_f32_32x32x2f32 blocks and 4 waves:
  * a wave owns wm_b x wn_b blocks (32x32 each); the waves form a gm x gn grid. */
 typedef struct {
-    u32 bm, bn;
+    u32 bm, bn, bk;
     u32 wm_b, wn_b;
     u32 gm, gn;
     const char *tag;
 } TileCfg;
 
-static const TileCfg CFG_BIG = {128, 128, 2, 2, 2, 2, "128x128"};   /* large square GEMMs */
-static const TileCfg CFG_MID = {64, 64, 1, 1, 2, 2, "64x64"};       /* small GEMMs: more tiles */
-static const TileCfg CFG_TALL = {256, 32, 2, 1, 4, 1, "256x32"};    /* N <= 32 (conv channels) */
-static const TileCfg CFG_WIDE = {32, 256, 1, 2, 1, 4, "32x256"};    /* M <= 32 */
+/* bk: K per LDS stage. The small tile stages 32 so that long, split
+ * reductions take half as many load-latency-bound steps. */
+static const TileCfg CFG_BIG = {128, 128, 16, 2, 2, 2, 2, "128x128"};   /* large square GEMMs */
+static const TileCfg CFG_MID = {64, 64, 32, 1, 1, 2, 2, "64x64"};       /* small GEMMs: more tiles */
+static const TileCfg CFG_TALL = {256, 32, 16, 2, 1, 4, 1, "256x32"};    /* N <= 32 (conv channels) */
+static const TileCfg CFG_WIDE = {32, 256, 16, 1, 2, 1, 4, "32x256"};    /* M <= 32 */
 
 typedef struct {
     char name[48];
@@ -464,20 +480,39 @@ typedef struct {
     u32 tiles_m, tiles_n;
 } GemmPlan;
 
-#define BK 16
 #define GEMM_THREADS 256
 #define SUM_WAVE_MIN_SPLITS 16   /* split-K sums this long use a wavefront per output */
+
+/* f(gid) (var 0) or g(r) (var 1) part of a separable operand index */
+static void emit_sep_fn(DSB *s, const char *name, const Aff *a, u8 var) {
+    dsb_put(s, "__device__ __forceinline__ u32 %s(u32 x) {\n  return %uu", name, var == 0 ? a->cst : 0u);
+    for (u32 t = 0; t < a->n; t++) {
+        if (a->d[t].var != var) continue;
+        if (a->d[t].mod) dsb_put(s, " + ((x / %uu) %% %uu) * %uu", a->d[t].div, a->d[t].mod, a->coef[t]);
+        else dsb_put(s, " + (x / %uu) * %uu", a->d[t].div, a->coef[t]);
+    }
+    dsb_put(s, ";\n}\n");
+}
+
+static const char *ld_name(u32 dt) {
+    return dt == DTYPE_F16 ? "ld_f16" : dt == DTYPE_I32 ? "ld_i32" : dt == DTYPE_U32 ? "ld_u32" : "ld_f32";
+}
 
 /* Loader lane map for one operand: x in [0, BX) along the tile's M or N side,
  * k in [0, BK). k-major operands put 16 consecutive lanes on consecutive k,
  * the others put consecutive lanes on consecutive x (coalesced either way). */
-static void emit_map(DSB *s, int kmajor, u32 bx, const char *xname) {
-    if (kmajor)
-        dsb_put(s, "const u32 kk = tid & 15u, %s = (tid >> 4) + e * 16u;", xname);
-    else if (bx >= GEMM_THREADS)
+static void emit_map(DSB *s, int kmajor, u32 bx, u32 bk, const char *xname) {
+    if (kmajor) {
+        if (bk == 16)
+            dsb_put(s, "const u32 kk = tid & 15u, %s = (tid >> 4) + e * 16u;", xname);
+        else
+            dsb_put(s, "const u32 kk = (tid & 15u) + (e %% %uu) * 16u, %s = (tid >> 4) + (e / %uu) * 16u;", bk / 16,
+                    xname, bk / 16);
+    } else if (bx >= GEMM_THREADS) {
         dsb_put(s, "const u32 %s = tid, kk = e;", xname);
-    else
+    } else {
         dsb_put(s, "const u32 %s = tid %% %uu, kk = tid / %uu + e * %uu;", xname, bx, bx, GEMM_THREADS / bx);
+    }
 }
 
 static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const GemmPlan *pl, char *err,
@@ -488,6 +523,11 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
     dsb_put(&s, "typedef float f32x16 __attribute__((ext_vector_type(16)));\n");
     emit_gid_fn(&s, "gid_m", ct->np, ct->pdiv, ct->pext);
     emit_gid_fn(&s, "gid_n", ct->nq, ct->qdiv, ct->qext);
+    for (int side = 0; side < 2; side++) {
+        if (!ct->sep[side]) continue;
+        emit_sep_fn(&s, side ? "rowb_q" : "rowb_p", &ct->sep_aff[side], 0);
+        emit_sep_fn(&s, side ? "koff_q" : "koff_p", &ct->sep_aff[side], 1);
+    }
     static char body[1 << 16];
     for (int side = 0; side < 2; side++) {
         const u8 *cone = side ? ct->coneQ : ct->coneP;
@@ -505,6 +545,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
     }
     const u32 M = ct->M, N = ct->N, K = ct->K;
     const u32 tiles = pl->tiles_m * pl->tiles_n;
+    const u32 BK = cf->bk;
     const u32 EA = cf->bm * BK / GEMM_THREADS, EB = cf->bn * BK / GEMM_THREADS;
     const u32 NB = cf->wm_b * cf->wn_b;
     dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", GEMM_THREADS, pl->name);
@@ -532,23 +573,44 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
             "  const u32 kbeg = blockIdx.y * KCH;\n"
             "  const u32 kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
             "  float ra[%u], rb[%u];\n", EA, EB);
+    /* separable operands: per-row index bases, once per tile */
+    if (ct->sep[0]) {
+        dsb_put(&s, "  u32 bA[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", EA, EA);
+        emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
+        dsb_put(&s, " (void)kk; bA[e] = rowb_p(gid_m(m0 + mm)); }\n");
+    }
+    if (ct->sep[1]) {
+        dsb_put(&s, "  u32 bB[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", EB, EB);
+        emit_map(&s, ct->q_kmajor, cf->bn, cf->bk, "nn");
+        dsb_put(&s, " (void)kk; bB[e] = rowb_q(gid_n(n0 + nn)); }\n");
+    }
     dsb_put(&s, "  auto loadA = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
-    emit_map(&s, ct->p_kmajor, cf->bm, "mm");
-    dsb_put(&s, "\n      const u32 m = m0 + mm, k = k0 + kk;\n"
-                "      ra[e] = (m < M && k < kend) ? operand_p(gid_m(m), k, ");
-    emit_args(&s, k->n_leaves);
-    dsb_put(&s, ") : 0.0f; }\n  };\n");
+    emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
+    dsb_put(&s, "\n      const u32 m = m0 + mm, k = k0 + kk;\n");
+    if (ct->sep[0]) {
+        dsb_put(&s, "      ra[e] = (m < M && k < kend) ? %s(p%u, c%u, bA[e] + koff_p(k)) : 0.0f; }\n  };\n",
+                ld_name(ct->sep_dt[0]), ct->sep_buf[0], ct->sep_buf[0]);
+    } else {
+        dsb_put(&s, "      ra[e] = (m < M && k < kend) ? operand_p(gid_m(m), k, ");
+        emit_args(&s, k->n_leaves);
+        dsb_put(&s, ") : 0.0f; }\n  };\n");
+    }
     dsb_put(&s, "  auto loadB = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EB);
-    emit_map(&s, ct->q_kmajor, cf->bn, "nn");
-    dsb_put(&s, "\n      const u32 n = n0 + nn, k = k0 + kk;\n"
-                "      rb[e] = (n < N && k < kend) ? operand_q(gid_n(n), k, ");
-    emit_args(&s, k->n_leaves);
-    dsb_put(&s, ") : 0.0f; }\n  };\n");
+    emit_map(&s, ct->q_kmajor, cf->bn, cf->bk, "nn");
+    dsb_put(&s, "\n      const u32 n = n0 + nn, k = k0 + kk;\n");
+    if (ct->sep[1]) {
+        dsb_put(&s, "      rb[e] = (n < N && k < kend) ? %s(p%u, c%u, bB[e] + koff_q(k)) : 0.0f; }\n  };\n",
+                ld_name(ct->sep_dt[1]), ct->sep_buf[1], ct->sep_buf[1]);
+    } else {
+        dsb_put(&s, "      rb[e] = (n < N && k < kend) ? operand_q(gid_n(n), k, ");
+        emit_args(&s, k->n_leaves);
+        dsb_put(&s, ") : 0.0f; }\n  };\n");
+    }
     dsb_put(&s, "  auto storeA = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
-    emit_map(&s, ct->p_kmajor, cf->bm, "mm");
+    emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
     dsb_put(&s, " As[buf][kk * LDA + mm] = ra[e]; }\n  };\n");
     dsb_put(&s, "  auto storeB = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EB);
-    emit_map(&s, ct->q_kmajor, cf->bn, "nn");
+    emit_map(&s, ct->q_kmajor, cf->bn, cf->bk, "nn");
     dsb_put(&s, " Bs[buf][kk * LDB + nn] = rb[e]; }\n  };\n");
     dsb_put(&s,
             "  f32x16 acc[%u];\n"
@@ -730,7 +792,7 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     while ((u64)tiles * splits < 512 && ct->K / (splits * 2) >= min_chunk && splits < 512) splits *= 2;
     if (hipb.dense_splits) splits = hipb.dense_splits;
     u32 kch = (ct->K + splits - 1) / splits;
-    kch = (kch + BK - 1) / BK * BK;
+    kch = (kch + pl->cfg.bk - 1) / pl->cfg.bk * pl->cfg.bk;
     pl->kchunk = kch;
     pl->splits = (ct->K + kch - 1) / kch;
     snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));
