@@ -1,7 +1,8 @@
 """Matrix-core (f32 MFMA) contraction kernels on the GPU: every committed trace
 replayed with every contraction forced onto the matrix-core path (most
 fixtures are below the size heuristics), once with the tile shape and split-K
-chosen by size, and once per tile shape (128x128, 64x64, 256x32, 32x256) with
+chosen by size, and once per tile shape (128x128, 64x64, 256x32, 32x256,
+and the direct per-wave kernel) with
 fixed split-K factors, under the same kernel-boundary parity as
 tests/test_gpu_parity.py; the matrix-core kernels fall in the 1e-4 normwise
 class."""
@@ -17,13 +18,13 @@ pytestmark = pytest.mark.gpu
 
 
 # (split-K factor, tile shape): 0 = chosen by size, 1 = 128x128, 2 = 64x64,
-# 3 = 256x32, 4 = 32x256
-CONFIGS = [("1", "0"), ("2", "0"), ("1", "1"), ("3", "2"), ("1", "3"), ("2", "4")]
+# 3 = 256x32, 4 = 32x256, 5 = direct (per-wave 32x32 blocks, no LDS)
+CONFIGS = [("1", "0"), ("2", "0"), ("1", "1"), ("3", "2"), ("1", "3"), ("2", "4"), ("1", "5"), ("3", "5")]
 
 
 @pytest.fixture(scope="module", params=CONFIGS,
                 ids=["whole-K", "split-K", "tile128x128", "tile64x64-split3", "tile256x32",
-                     "tile32x256-split2"])
+                     "tile32x256-split2", "direct", "direct-split3"])
 def hip_dense(request):
     saved = {k: os.environ.get(k) for k in ("THVM_HIP_DENSE_FORCE", "THVM_HIP_DENSE_SPLITS",
                                              "THVM_HIP_DENSE_TILE")}

@@ -83,7 +83,7 @@ static void read_dense_env(void) {
     hipb.dense_splits = e ? (u32)atoi(e) : 0;
     e = getenv("THVM_HIP_DENSE_TILE");
     hipb.dense_tile = e ? (u32)atoi(e) : 0;
-    if (hipb.dense_tile > 4) hipb.dense_tile = 0;
+    if (hipb.dense_tile > 5) hipb.dense_tile = 0;
 }
 
 static int hb_init(void) {

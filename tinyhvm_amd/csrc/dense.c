@@ -463,6 +463,7 @@ typedef struct {
     u32 wm_b, wn_b;
     u32 gm, gn;
     const char *tag;
+    int direct;    /* no LDS: each wave owns one 32x32 block and loads its MFMA operands itself */
 } TileCfg;
 
 /* bk: K per LDS stage. The small tile stages 32 so that long, split
@@ -471,6 +472,12 @@ static const TileCfg CFG_BIG = {128, 128, 16, 2, 2, 2, 2, "128x128"};   /* large
 static const TileCfg CFG_MID = {64, 64, 32, 1, 1, 2, 2, "64x64"};       /* small GEMMs: more tiles */
 static const TileCfg CFG_TALL = {256, 32, 16, 2, 1, 4, 1, "256x32"};    /* N <= 32 (conv channels) */
 static const TileCfg CFG_WIDE = {32, 256, 16, 1, 2, 1, 4, "32x256"};    /* M <= 32 */
+/* Small and skinny contractions (conv channels, fc layers, weight gradients):
+ * with operands that fit in L2 there is little to gain from sharing tiles
+ * through LDS, and everything to gain from keeping many independent loads in
+ * flight without barriers. Each wave computes one 32x32 block, loading 32 K
+ * of both MFMA operands per iteration straight into registers. */
+static const TileCfg CFG_DIRECT = {32, 32, 32, 1, 1, 1, 1, "direct32", 1};
 
 typedef struct {
     char name[48];
@@ -515,6 +522,111 @@ static void emit_map(DSB *s, int kmajor, u32 bx, u32 bk, const char *xname) {
     }
 }
 
+static void out_store_fn(const UOpKernel *k, const Contraction *ct, char *fb, size_t fblen, const char **st) {
+    u32 bits;
+    memcpy(&bits, &ct->init, 4);
+    snprintf(fb, fblen, "__uint_as_float(0x%08xu)", bits);
+    *st = k->out_dtype == DTYPE_F16 ? "st_f16" : k->out_dtype == DTYPE_I32 ? "st_i32"
+          : k->out_dtype == DTYPE_U32 ? "st_u32" : "st_f32";
+}
+
+/* Closes the epilogue opened by the caller (inside `if (m < M && n < N) {`
+ * with the accumulator value c[v]): stores the result (or the split's partial
+ * into the workspace), closes the kernel, and emits the split-K sum kernel. */
+static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
+    DSB *s_ = sp;
+    char fb[64];
+    const char *st;
+    out_store_fn(k, ct, fb, sizeof fb, &st);
+    const u32 M = ct->M, N = ct->N;
+    if (pl->splits > 1)
+        dsb_put(s_, "        ws[((unsigned long long)blockIdx.y * M + m) * N + n] = c[v];\n");
+    else
+        dsb_put(s_, "        %s(p0, c0, gid_m(m) + gid_n(n), %s + c[v]);\n", st, fb);
+    dsb_put(s_, "      }\n    }\n  }\n}\n");
+    if (pl->splits <= 1) return;
+    if (pl->splits >= SUM_WAVE_MIN_SPLITS) {
+        /* many splits: one wavefront per output; lane l adds splits l, l+64, ...
+         * in order, then a fixed shuffle tree (deterministic) */
+        dsb_put(s_, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
+                    "  const unsigned long long t = (unsigned long long)blockIdx.x * 4u + (threadIdx.x >> 6);\n"
+                    "  const u32 lane = threadIdx.x & 63u;\n"
+                    "  if (t >= %lluull) return;\n"
+                    "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
+                    "  float a = 0.0f;\n"
+                    "  for (u32 s = lane; s < %uu; s += 64u) a = a + ws[(unsigned long long)s * %lluull + t];\n"
+                    "  a = wsum(a);\n"
+                    "  if (lane == 0u) %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
+                pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
+    } else {
+        dsb_put(s_, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
+                    "  const unsigned long long t = (unsigned long long)blockIdx.x * 256u + threadIdx.x;\n"
+                    "  if (t >= %lluull) return;\n"
+                    "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
+                    "  float a = 0.0f;\n"
+                    "  for (u32 s = 0; s < %uu; s++) a = a + ws[(unsigned long long)s * %lluull + t];\n"
+                    "  %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
+                pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
+    }
+}
+
+/* Operand element (m, k) of one side: separable loads add a row base and a
+ * k offset; other operands run their own KOp program. */
+static void emit_operand_expr(DSB *s, const UOpKernel *k, const Contraction *ct, int side, const char *base,
+                              const char *x, const char *kv) {
+    if (ct->sep[side]) {
+        dsb_put(s, "%s(p%u, c%u, %s + koff_%c(%s))", ld_name(ct->sep_dt[side]), ct->sep_buf[side], ct->sep_buf[side],
+                base, side ? 'q' : 'p', kv);
+    } else {
+        dsb_put(s, "operand_%c(gid_%c(%s), %s, ", side ? 'q' : 'p', side ? 'n' : 'm', x, kv);
+        emit_args(s, k->n_leaves);
+        dsb_put(s, ")");
+    }
+}
+
+static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
+    const u32 M = ct->M, N = ct->N, K = ct->K, KU = pl->cfg.bk;
+    const u32 blocks = pl->tiles_m * pl->tiles_n;
+    dsb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", GEMM_THREADS, pl->name);
+    emit_params(s, k->n_leaves);
+    dsb_put(s, ", float* ws) {\n");
+    dsb_put(s,
+            "  constexpr u32 M = %uu, N = %uu, K = %uu, TN = %uu, BLOCKS = %uu, KCH = %uu, KU = %uu;\n"
+            "  const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;\n"
+            "  const u32 blk = blockIdx.x * %uu + wave;\n"
+            "  if (blk >= BLOCKS) return;\n"
+            "  const u32 m0 = (blk / TN) * 32u, n0 = (blk %% TN) * 32u;\n"
+            "  const u32 kbeg = blockIdx.y * KCH;\n"
+            "  const u32 kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
+            "  const u32 i = lane & 31u, kh = lane >> 5;\n"
+            "  const u32 ma = m0 + i, nb = n0 + i;\n",
+            M, N, K, pl->tiles_n, blocks, pl->kchunk, KU, GEMM_THREADS / 64);
+    if (ct->sep[0]) dsb_put(s, "  const u32 bA = ma < M ? rowb_p(gid_m(ma)) : 0u;\n");
+    if (ct->sep[1]) dsb_put(s, "  const u32 bB = nb < N ? rowb_q(gid_n(nb)) : 0u;\n");
+    dsb_put(s,
+            "  f32x16 acc = {0};\n"
+            "  for (u32 k0 = kbeg; k0 < kend; k0 += KU) {\n"
+            "    float a[KU / 2u], b[KU / 2u];\n"
+            "    #pragma unroll\n"
+            "    for (u32 q = 0; q < KU / 2u; q++) {\n"
+            "      const u32 k = k0 + 2u * q + kh;\n"
+            "      a[q] = (ma < M && k < kend) ? ");
+    emit_operand_expr(s, k, ct, 0, "bA", "ma", "k");
+    dsb_put(s, " : 0.0f;\n      b[q] = (nb < N && k < kend) ? ");
+    emit_operand_expr(s, k, ct, 1, "bB", "nb", "k");
+    dsb_put(s, " : 0.0f;\n    }\n"
+               "    #pragma unroll\n"
+               "    for (u32 q = 0; q < KU / 2u; q++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q], b[q], acc, 0, 0, 0);\n"
+               "  }\n"
+               "  {\n"
+               "    const f32x16 c = acc;\n"
+               "    const u32 n = n0 + (lane & 31u);\n"
+               "    #pragma unroll\n"
+               "    for (u32 v = 0; v < 16u; v++) {\n"
+               "      const u32 m = m0 + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3u);\n"
+               "      if (m < M && n < N) {\n");
+}
+
 static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const GemmPlan *pl, char *err,
                              size_t errlen) {
     DSB s = {0};
@@ -545,6 +657,11 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
     }
     const u32 M = ct->M, N = ct->N, K = ct->K;
     const u32 tiles = pl->tiles_m * pl->tiles_n;
+    if (cf->direct) {
+        emit_direct_kernel(&s, k, ct, pl);
+        emit_store_tail(&s, k, ct, pl);
+        return s.p;
+    }
     const u32 BK = cf->bk;
     const u32 EA = cf->bm * BK / GEMM_THREADS, EB = cf->bn * BK / GEMM_THREADS;
     const u32 NB = cf->wm_b * cf->wn_b;
@@ -653,49 +770,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
             "    for (u32 v = 0; v < 16u; v++) {\n"
             "      const u32 m = m0 + bm + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3u);\n"
             "      if (m < M && n < N) {\n", NB, cf->wn_b, cf->wn_b);
-    if (pl->splits > 1) {
-        dsb_put(&s, "        ws[((unsigned long long)blockIdx.y * M + m) * N + n] = c[v];\n");
-    } else {
-        char fb[64];
-        u32 bits;
-        memcpy(&bits, &ct->init, 4);
-        snprintf(fb, sizeof fb, "__uint_as_float(0x%08xu)", bits);
-        const char *st = k->out_dtype == DTYPE_F16 ? "st_f16" : k->out_dtype == DTYPE_I32 ? "st_i32"
-                         : k->out_dtype == DTYPE_U32 ? "st_u32" : "st_f32";
-        dsb_put(&s, "        %s(p0, c0, gid_m(m) + gid_n(n), %s + c[v]);\n", st, fb);
-    }
-    dsb_put(&s, "      }\n    }\n  }\n}\n");
-    if (pl->splits > 1) {
-        char fb[64];
-        u32 bits;
-        memcpy(&bits, &ct->init, 4);
-        snprintf(fb, sizeof fb, "__uint_as_float(0x%08xu)", bits);
-        const char *st = k->out_dtype == DTYPE_F16 ? "st_f16" : k->out_dtype == DTYPE_I32 ? "st_i32"
-                         : k->out_dtype == DTYPE_U32 ? "st_u32" : "st_f32";
-        if (pl->splits >= SUM_WAVE_MIN_SPLITS) {
-            /* many splits: one wavefront per output; lane l adds splits l, l+64, ...
-             * in order, then a fixed shuffle tree (deterministic) */
-            dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
-                        "  const unsigned long long t = (unsigned long long)blockIdx.x * 4u + (threadIdx.x >> 6);\n"
-                        "  const u32 lane = threadIdx.x & 63u;\n"
-                        "  if (t >= %lluull) return;\n"
-                        "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
-                        "  float a = 0.0f;\n"
-                        "  for (u32 s = lane; s < %uu; s += 64u) a = a + ws[(unsigned long long)s * %lluull + t];\n"
-                        "  a = wsum(a);\n"
-                        "  if (lane == 0u) %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
-                    pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
-        } else {
-            dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
-                        "  const unsigned long long t = (unsigned long long)blockIdx.x * 256u + threadIdx.x;\n"
-                        "  if (t >= %lluull) return;\n"
-                        "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
-                        "  float a = 0.0f;\n"
-                        "  for (u32 s = 0; s < %uu; s++) a = a + ws[(unsigned long long)s * %lluull + t];\n"
-                        "  %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
-                    pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
-        }
-    }
+    emit_store_tail(&s, k, ct, pl);
     return s.p;
 }
 
@@ -771,14 +846,12 @@ static DenseEntry *insert(u64 key, const UOpKernel *k) {
 }
 
 static TileCfg pick_cfg(u32 M, u32 N) {
-    if (N <= 32 && M >= 256) return CFG_TALL;
-    if (M <= 32 && N >= 256) return CFG_WIDE;
     u64 big_tiles = (u64)((M + 127) / 128) * ((N + 127) / 128);
-    return big_tiles >= 128 ? CFG_BIG : CFG_MID;
+    return big_tiles >= 128 ? CFG_BIG : CFG_DIRECT;
 }
 
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
-    static const TileCfg *forced[5] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE};
+    static const TileCfg *forced[6] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT};
     memset(pl, 0, sizeof *pl);
     pl->cfg = hipb.dense_tile ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N);
     pl->tiles_m = (ct->M + pl->cfg.bm - 1) / pl->cfg.bm;
@@ -787,9 +860,10 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     /* split K until the grid covers the 256 CUs about twice, keeping each
      * split at least min_chunk long (512 for the big tiles, whose per-tile
      * setup is larger; 64 otherwise) */
-    u32 min_chunk = pl->cfg.bm == 128 ? 512 : 64;
+    u32 min_chunk = pl->cfg.bm == 128 ? 512 : pl->cfg.direct ? 128 : 64;
+    u64 target = pl->cfg.direct ? 2048 : 512;   /* workgroups, or waves for the direct kernel */
     u32 splits = 1;
-    while ((u64)tiles * splits < 512 && ct->K / (splits * 2) >= min_chunk && splits < 512) splits *= 2;
+    while ((u64)tiles * splits < target && ct->K / (splits * 2) >= min_chunk && splits < 1024) splits *= 2;
     if (hipb.dense_splits) splits = hipb.dense_splits;
     u32 kch = (ct->K + splits - 1) / splits;
     kch = (kch + pl->cfg.bk - 1) / pl->cfg.bk * pl->cfg.bk;
@@ -893,6 +967,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     }
     params[2 * nb] = &ws;
     u32 tiles = e->plan.tiles_m * e->plan.tiles_n;
+    if (e->plan.cfg.direct) tiles = (tiles + GEMM_THREADS / 64 - 1) / (GEMM_THREADS / 64);   /* 4 waves per group */
     if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, GEMM_THREADS, params)) return 0;
     if (e->plan.splits > 1) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};
