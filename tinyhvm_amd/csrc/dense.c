@@ -584,6 +584,11 @@ static void emit_operand_expr(DSB *s, const UOpKernel *k, const Contraction *ct,
     }
 }
 
+/* Direct kernel: a workgroup of 4 waves owns one 32x32 output block; the
+ * waves take alternate KU-long steps of the workgroup's K range, each wave
+ * keeping 4 independent accumulator chains and loading the next step's
+ * operands before it multiplies the current ones. The 4 waves' partial blocks
+ * are summed through LDS in a fixed order. */
 static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
     const u32 M = ct->M, N = ct->N, K = ct->K, KU = pl->cfg.bk;
     const u32 blocks = pl->tiles_m * pl->tiles_n;
@@ -591,9 +596,9 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
     emit_params(s, k->n_leaves);
     dsb_put(s, ", float* ws) {\n");
     dsb_put(s,
-            "  constexpr u32 M = %uu, N = %uu, K = %uu, TN = %uu, BLOCKS = %uu, KCH = %uu, KU = %uu;\n"
+            "  constexpr u32 M = %uu, N = %uu, K = %uu, TN = %uu, BLOCKS = %uu, KCH = %uu, KU = %uu, NW = %uu;\n"
             "  const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;\n"
-            "  const u32 blk = blockIdx.x * %uu + wave;\n"
+            "  const u32 blk = blockIdx.x;\n"
             "  if (blk >= BLOCKS) return;\n"
             "  const u32 m0 = (blk / TN) * 32u, n0 = (blk %% TN) * 32u;\n"
             "  const u32 kbeg = blockIdx.y * KCH;\n"
@@ -604,9 +609,8 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
     if (ct->sep[0]) dsb_put(s, "  const u32 bA = ma < M ? rowb_p(gid_m(ma)) : 0u;\n");
     if (ct->sep[1]) dsb_put(s, "  const u32 bB = nb < N ? rowb_q(gid_n(nb)) : 0u;\n");
     dsb_put(s,
-            "  f32x16 acc = {0};\n"
-            "  for (u32 k0 = kbeg; k0 < kend; k0 += KU) {\n"
-            "    float a[KU / 2u], b[KU / 2u];\n"
+            "  float a[KU / 2u], b[KU / 2u];\n"
+            "  auto fetch = [&](u32 k0) {\n"
             "    #pragma unroll\n"
             "    for (u32 q = 0; q < KU / 2u; q++) {\n"
             "      const u32 k = k0 + 2u * q + kh;\n"
@@ -614,10 +618,37 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
     emit_operand_expr(s, k, ct, 0, "bA", "ma", "k");
     dsb_put(s, " : 0.0f;\n      b[q] = (nb < N && k < kend) ? ");
     emit_operand_expr(s, k, ct, 1, "bB", "nb", "k");
-    dsb_put(s, " : 0.0f;\n    }\n"
+    dsb_put(s, " : 0.0f;\n    }\n  };\n"
+               "  f32x16 acc0 = {0}, acc1 = {0}, acc2 = {0}, acc3 = {0};\n"
+               "  u32 k0 = kbeg + wave * KU;\n"
+               "  if (k0 < kend) fetch(k0);\n"
+               "  while (k0 < kend) {\n"
+               "    float ca[KU / 2u], cb[KU / 2u];\n"
                "    #pragma unroll\n"
-               "    for (u32 q = 0; q < KU / 2u; q++) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[q], b[q], acc, 0, 0, 0);\n"
+               "    for (u32 q = 0; q < KU / 2u; q++) { ca[q] = a[q]; cb[q] = b[q]; }\n"
+               "    const u32 kn = k0 + NW * KU;\n"
+               "    if (kn < kend) fetch(kn);\n"
+               "    #pragma unroll\n"
+               "    for (u32 q = 0; q < KU / 2u; q += 4u) {\n"
+               "      acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[q], cb[q], acc0, 0, 0, 0);\n"
+               "      acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[q + 1u], cb[q + 1u], acc1, 0, 0, 0);\n"
+               "      acc2 = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[q + 2u], cb[q + 2u], acc2, 0, 0, 0);\n"
+               "      acc3 = __builtin_amdgcn_mfma_f32_32x32x2f32(ca[q + 3u], cb[q + 3u], acc3, 0, 0, 0);\n"
+               "    }\n"
+               "    k0 = kn;\n"
                "  }\n"
+               "  f32x16 acc = (acc0 + acc1) + (acc2 + acc3);\n"
+               "  __shared__ float part_[NW - 1u][16][64];\n"
+               "  if (wave > 0u) {\n"
+               "    #pragma unroll\n"
+               "    for (u32 v = 0; v < 16u; v++) part_[wave - 1u][v][lane] = acc[v];\n"
+               "  }\n"
+               "  __syncthreads();\n"
+               "  if (wave > 0u) return;\n"
+               "  #pragma unroll\n"
+               "  for (u32 w = 0; w < NW - 1u; w++)\n"
+               "    #pragma unroll\n"
+               "    for (u32 v = 0; v < 16u; v++) acc[v] = acc[v] + part_[w][v][lane];\n"
                "  {\n"
                "    const f32x16 c = acc;\n"
                "    const u32 n = n0 + (lane & 31u);\n"
@@ -847,7 +878,8 @@ static DenseEntry *insert(u64 key, const UOpKernel *k) {
 
 static TileCfg pick_cfg(u32 M, u32 N) {
     u64 big_tiles = (u64)((M + 127) / 128) * ((N + 127) / 128);
-    return big_tiles >= 128 ? CFG_BIG : CFG_DIRECT;
+    if (M >= 128 && N >= 128 && big_tiles >= 128) return CFG_BIG;
+    return CFG_DIRECT;
 }
 
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
@@ -860,8 +892,10 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     /* split K until the grid covers the 256 CUs about twice, keeping each
      * split at least min_chunk long (512 for the big tiles, whose per-tile
      * setup is larger; 64 otherwise) */
-    u32 min_chunk = pl->cfg.bm == 128 ? 512 : pl->cfg.direct ? 128 : 64;
-    u64 target = pl->cfg.direct ? 2048 : 512;   /* workgroups, or waves for the direct kernel */
+    /* direct: 4 waves per block share its K range, so a split of c gives
+     * each wave c/4; keep that >= 64 and aim for ~2048 waves */
+    u32 min_chunk = pl->cfg.bm == 128 ? 512 : pl->cfg.direct ? 256 : 64;
+    u64 target = pl->cfg.direct ? 512 : 512;    /* workgroups */
     u32 splits = 1;
     while ((u64)tiles * splits < target && ct->K / (splits * 2) >= min_chunk && splits < 1024) splits *= 2;
     if (hipb.dense_splits) splits = hipb.dense_splits;
@@ -967,7 +1001,6 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     }
     params[2 * nb] = &ws;
     u32 tiles = e->plan.tiles_m * e->plan.tiles_n;
-    if (e->plan.cfg.direct) tiles = (tiles + GEMM_THREADS / 64 - 1) / (GEMM_THREADS / 64);   /* 4 waves per group */
     if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, GEMM_THREADS, params)) return 0;
     if (e->plan.splits > 1) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};
