@@ -102,6 +102,9 @@ int  thvm_hip_compile_check(const UOpKernel *kernel, char *errbuf, u64 errlen);
  * GEMM shape (no device needed). Reads THVM_HIP_DENSE_FORCE /
  * THVM_HIP_DENSE_SPLITS before init. Returns 1 if so, else 0. */
 int  thvm_hip_dense_analyze(const UOpKernel *kernel, u32 *M, u32 *N, u32 *K, u32 *splits);
+/* Generated HIP source of that matrix-core kernel (no device needed); returns
+ * its length, or -1 with the reason in buf. */
+int  thvm_hip_dense_source(const UOpKernel *kernel, char *buf, u64 buflen);
 /* Generate and compile that matrix-core kernel without loading it; returns the
  * code-object size, or -1 with the reason in errbuf. */
 int  thvm_hip_dense_compile_check(const UOpKernel *kernel, char *errbuf, u64 errlen);

@@ -61,6 +61,7 @@ def lib():
         "thvm_hip_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
         "thvm_hip_dense_analyze": (C.c_int, [C.POINTER(abi.UOpKernel), PU32, PU32, PU32, PU32]),
         "thvm_hip_dense_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
+        "thvm_hip_dense_source": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
         "thvm_trace_load": (vp, [cp]),
         "thvm_trace_free": (None, [vp]),
         "thvm_trace_count": (u32, [vp]),
@@ -93,7 +94,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_pool_set_persistent", "thvm_hip_profile_report", "thvm_hip_profile_reset",
     "thvm_hip_synchronize", "thvm_hip_stream", "thvm_hip_buf_device_ptr", "thvm_hip_backend",
     "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_compile_check",
-    "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check",
+    "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
     "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",
@@ -124,6 +125,14 @@ def dense_analyze(k: abi.UOpKernel):
     if lib().thvm_hip_dense_analyze(C.byref(k), C.byref(M), C.byref(N), C.byref(K), C.byref(S)):
         return M.value, N.value, K.value, S.value
     return None
+
+
+def dense_source(k: abi.UOpKernel):
+    buf = C.create_string_buffer(1 << 20)
+    n = lib().thvm_hip_dense_source(C.byref(k), buf, len(buf))
+    if n < 0:
+        raise ValueError(buf.value.decode())
+    return buf.value.decode()
 
 
 def dense_compile_check(k: abi.UOpKernel):

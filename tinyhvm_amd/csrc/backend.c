@@ -79,6 +79,7 @@ static int env_flag(const char *name) {
  * analysis call). */
 static void read_dense_env(void) {
     hipb.dense_force = env_flag("THVM_HIP_DENSE_FORCE");
+    hipb.dense_nosep = env_flag("THVM_HIP_DENSE_NOSEP");
     const char *e = getenv("THVM_HIP_DENSE_SPLITS");
     hipb.dense_splits = e ? (u32)atoi(e) : 0;
     e = getenv("THVM_HIP_DENSE_TILE");
@@ -114,6 +115,8 @@ static int hb_init(void) {
     hipb.verbose = env_flag("THVM_HIP_VERBOSE");
     read_dense_env();
     if (pool_init() != 0) return -1;
+    hipb.dummy = pool_block_get(256, &hipb.dummy_cap);
+    if (!hipb.dummy || hipMemset(hipb.dummy, 0, 256) != hipSuccess) return -1;
     if (rtc_init() != 0) return -1;
     hipb.initialized = 1;
     return 0;
@@ -126,6 +129,8 @@ static void hb_shutdown(void) {
     dense_shutdown();
     rtc_shutdown();
     scratch_release(&red_ws);
+    pool_block_put(hipb.dummy, hipb.dummy_cap);
+    hipb.dummy = NULL;
     pool_shutdown();
     HIPB_CHECK(hipStreamDestroy(hipb.stream));
     hipb.initialized = 0;
@@ -246,7 +251,7 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     counts[0] = elem_count(out_buf, k->out_dtype);
     for (u32 i = 0; i < k->n_leaves; i++) {
         void *lp = (i < n_leaves) ? pool_ptr(leaf_bufs[i]) : NULL;
-        ptrs[i + 1] = lp;
+        ptrs[i + 1] = lp ? lp : hipb.dummy;   /* loads index an absent buffer's element 0 */
         counts[i + 1] = lp ? elem_count(leaf_bufs[i], k->leaf_dtypes[i]) : 0u;
     }
     for (u32 b = 0; b < nb; b++) {
@@ -640,6 +645,18 @@ int thvm_hip_dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *spli
         env_read = 1;
     }
     return dense_analyze(k, M, N, K, splits);
+}
+
+int thvm_hip_dense_source(const UOpKernel *k, char *buf, u64 buflen) {
+    char *src = dense_source(k);
+    if (!src) {
+        if (buf && buflen) snprintf(buf, buflen, "not a matrix-core contraction");
+        return -1;
+    }
+    size_t n = strlen(src);
+    if (buf && buflen) snprintf(buf, buflen, "%s", src);
+    free(src);
+    return (int)n;
 }
 
 int thvm_hip_dense_compile_check(const UOpKernel *k, char *errbuf, u64 errlen) {

@@ -402,7 +402,7 @@ static int recognize(const UOpKernel *k, Contraction *ct) {
     ct->K = c.trip;
     ct->p_kmajor = cone_kmajor(&c, ct->coneP);
     ct->q_kmajor = cone_kmajor(&c, ct->coneQ);
-    for (int side = 0; side < 2; side++) {
+    for (int side = 0; side < 2 && !hipb.dense_nosep; side++) {
         const KOp *ld = &k->ops[side ? ct->rootQ : ct->rootP];
         if (ld->type != KOP_LOAD || ld->imm.u > k->n_leaves || !c.aff[ld->arg[0]].ok) continue;
         ct->sep[side] = 1;
@@ -614,11 +614,12 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
             "    #pragma unroll\n"
             "    for (u32 q = 0; q < KU / 2u; q++) {\n"
             "      const u32 k = k0 + 2u * q + kh;\n"
-            "      a[q] = (ma < M && k < kend) ? ");
+            "      const float va = ");
     emit_operand_expr(s, k, ct, 0, "bA", "ma", "k");
-    dsb_put(s, " : 0.0f;\n      b[q] = (nb < N && k < kend) ? ");
+    dsb_put(s, ";\n      const float vb = ");
     emit_operand_expr(s, k, ct, 1, "bB", "nb", "k");
-    dsb_put(s, " : 0.0f;\n    }\n  };\n"
+    dsb_put(s, ";\n      a[q] = __uint_as_float(__float_as_uint(va) & ((ma < M && k < kend) ? 0xFFFFFFFFu : 0u));\n"
+               "      b[q] = __uint_as_float(__float_as_uint(vb) & ((nb < N && k < kend) ? 0xFFFFFFFFu : 0u));\n    }\n  };\n"
                "  f32x16 acc0 = {0}, acc1 = {0}, acc2 = {0}, acc3 = {0};\n"
                "  u32 k0 = kbeg + wave * KU;\n"
                "  if (k0 < kend) fetch(k0);\n"
@@ -658,8 +659,13 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
                "      if (m < M && n < N) {\n");
 }
 
-static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const GemmPlan *pl, char *err,
+static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const GemmPlan *pl, char *err,
                              size_t errlen) {
+    /* the big tile evaluates its operands in place: separable row bases would
+     * hold 16 more registers across its whole K loop (measured slower) */
+    Contraction ctl = *ct_in;
+    if (pl->cfg.bm == 128) ctl.sep[0] = ctl.sep[1] = 0;
+    const Contraction *ct = &ctl;
     DSB s = {0};
     const TileCfg *cf = &pl->cfg;
     dsb_put(&s, "%s\n", kgen_prelude());
@@ -734,26 +740,39 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
     }
     dsb_put(&s, "  auto loadA = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
     emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
+    /* operands are evaluated unconditionally (every load is range-checked,
+     * so any (m, k) is safe) and masked after: no divergent branches */
     dsb_put(&s, "\n      const u32 m = m0 + mm, k = k0 + kk;\n");
+    /* the mask is applied to the bits (a select would let the compiler move
+     * the load under a branch and wait for each load in turn); it is left out
+     * where the tile grid and K split divide the problem exactly */
+    const int full_k = (K % pl->kchunk == 0) && (pl->kchunk % BK == 0);
+    const char *gm = (M % cf->bm == 0) ? "true" : "(m < M)";
+    const char *gn = (N % cf->bn == 0) ? "true" : "(n < N)";
+    const char *gk = full_k ? "true" : "(k < kend)";
     if (ct->sep[0]) {
-        dsb_put(&s, "      ra[e] = (m < M && k < kend) ? %s(p%u, c%u, bA[e] + koff_p(k)) : 0.0f; }\n  };\n",
+        dsb_put(&s, "      const float v = %s(p%u, c%u, bA[e] + koff_p(k));\n",
                 ld_name(ct->sep_dt[0]), ct->sep_buf[0], ct->sep_buf[0]);
     } else {
-        dsb_put(&s, "      ra[e] = (m < M && k < kend) ? operand_p(gid_m(m), k, ");
+        dsb_put(&s, "      const float v = operand_p(gid_m(m), k, ");
         emit_args(&s, k->n_leaves);
-        dsb_put(&s, ") : 0.0f; }\n  };\n");
+        dsb_put(&s, ");\n");
     }
+    dsb_put(&s, "      ra[e] = __uint_as_float(__float_as_uint(v) & ((%s && %s) ? 0xFFFFFFFFu : 0u)); }\n  };\n", gm,
+            gk);
     dsb_put(&s, "  auto loadB = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EB);
     emit_map(&s, ct->q_kmajor, cf->bn, cf->bk, "nn");
     dsb_put(&s, "\n      const u32 n = n0 + nn, k = k0 + kk;\n");
     if (ct->sep[1]) {
-        dsb_put(&s, "      rb[e] = (n < N && k < kend) ? %s(p%u, c%u, bB[e] + koff_q(k)) : 0.0f; }\n  };\n",
+        dsb_put(&s, "      const float v = %s(p%u, c%u, bB[e] + koff_q(k));\n",
                 ld_name(ct->sep_dt[1]), ct->sep_buf[1], ct->sep_buf[1]);
     } else {
-        dsb_put(&s, "      rb[e] = (n < N && k < kend) ? operand_q(gid_n(n), k, ");
+        dsb_put(&s, "      const float v = operand_q(gid_n(n), k, ");
         emit_args(&s, k->n_leaves);
-        dsb_put(&s, ") : 0.0f; }\n  };\n");
+        dsb_put(&s, ");\n");
     }
+    dsb_put(&s, "      rb[e] = __uint_as_float(__float_as_uint(v) & ((%s && %s) ? 0xFFFFFFFFu : 0u)); }\n  };\n", gn,
+            gk);
     dsb_put(&s, "  auto storeA = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
     emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
     dsb_put(&s, " As[buf][kk * LDA + mm] = ra[e]; }\n  };\n");
@@ -770,22 +789,29 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct, const Ge
             "  for (u32 st = 0; st < nst; st++) {\n"
             "    const u32 cur = st & 1u;\n"
             "    if (st + 1u < nst) { loadA(kbeg + (st + 1u) * BK); loadB(kbeg + (st + 1u) * BK); }\n"
+
             "    const float* A = As[cur];\n"
             "    const float* B = Bs[cur];\n"
+            "    /* all of the stage's fragments first, so LDS latency overlaps MFMAs */\n"
+            "    float a[BK / 2u][%u], b[BK / 2u][%u];\n"
             "    #pragma unroll\n"
             "    for (u32 kk = 0; kk < BK; kk += 2u) {\n"
             "      const u32 kr = kk + (lane >> 5);\n"
-            "      float a[%u], b[%u];\n"
             "      #pragma unroll\n"
-            "      for (u32 i = 0; i < %uu; i++) a[i] = A[kr * LDA + wm + i * 32u + (lane & 31u)];\n"
+            "      for (u32 i = 0; i < %uu; i++) a[kk / 2u][i] = A[kr * LDA + wm + i * 32u + (lane & 31u)];\n"
             "      #pragma unroll\n"
-            "      for (u32 j = 0; j < %uu; j++) b[j] = B[kr * LDB + wn + j * 32u + (lane & 31u)];\n"
+            "      for (u32 j = 0; j < %uu; j++) b[kk / 2u][j] = B[kr * LDB + wn + j * 32u + (lane & 31u)];\n"
+            "    }\n"
+            "    #pragma unroll\n"
+            "    for (u32 kk = 0; kk < BK / 2u; kk++)\n"
             "      #pragma unroll\n"
             "      for (u32 i = 0; i < %uu; i++)\n"
             "        #pragma unroll\n"
             "        for (u32 j = 0; j < %uu; j++)\n"
-            "          acc[i * %uu + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[i], b[j], acc[i * %uu + j], 0, 0, 0);\n"
-            "    }\n"
+            "          acc[i * %uu + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][i], b[kk][j], acc[i * %uu + j], 0, 0, 0);\n"
+            "    /* the next stage's global loads stay in flight across the MFMAs: the\n"
+            "     * LDS stores (which need them) may not move above the math */\n"
+            "    __builtin_amdgcn_sched_barrier(0);\n"
             "    if (st + 1u < nst) { storeA(cur ^ 1u); storeB(cur ^ 1u); }\n"
             "    __syncthreads();\n"
             "  }\n",
@@ -876,9 +902,16 @@ static DenseEntry *insert(u64 key, const UOpKernel *k) {
     return e;
 }
 
+/* Measured on MI355X over the LeNet-5 and 4096^3 contractions: big tiles
+ * when both sides are large; the LDS-staged 256x32 (32x256) tile for very
+ * tall (wide) and thin operands such as convolutions over a batch of images,
+ * where its four waves share each operand stage; the direct kernel for the
+ * rest (fully connected layers, weight gradients). */
 static TileCfg pick_cfg(u32 M, u32 N) {
     u64 big_tiles = (u64)((M + 127) / 128) * ((N + 127) / 128);
     if (M >= 128 && N >= 128 && big_tiles >= 128) return CFG_BIG;
+    if (N <= 32 && M >= 4096) return CFG_TALL;
+    if (M <= 32 && N >= 4096) return CFG_WIDE;
     return CFG_DIRECT;
 }
 
@@ -991,7 +1024,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     counts[0] = (u32)(pool_bytes(out_buf) / (k->out_dtype == DTYPE_F16 ? 2 : 4));
     for (u32 i = 0; i < k->n_leaves; i++) {
         void *lp = i < n_leaves ? pool_ptr(leaf_bufs[i]) : NULL;
-        ptrs[i + 1] = lp;
+        ptrs[i + 1] = lp ? lp : hipb.dummy;   /* loads index an absent buffer's element 0 */
         u64 b = lp ? pool_bytes(leaf_bufs[i]) : 0;
         counts[i + 1] = (u32)(b / (k->leaf_dtypes[i] == DTYPE_F16 ? 2 : 4));
     }

@@ -744,10 +744,21 @@ static const char *PRELUDE =
 "  if (dt == 3u) return (float)f2u(v);\n"
 "  return v;\n"
 "}\n"
-"__device__ __forceinline__ float ld_f32(const char* p, u32 n, u32 i) { return i < n ? ((const float*)p)[i] : 0.0f; }\n"
-"__device__ __forceinline__ float ld_f16(const char* p, u32 n, u32 i) { return i < n ? h2f(((const u16*)p)[i]) : 0.0f; }\n"
-"__device__ __forceinline__ float ld_i32(const char* p, u32 n, u32 i) { return i < n ? (float)((const int*)p)[i] : 0.0f; }\n"
-"__device__ __forceinline__ float ld_u32(const char* p, u32 n, u32 i) { return i < n ? (float)((const u32*)p)[i] : 0.0f; }\n"
+"/* checked loads without branches: an out-of-range index loads element 0\n"
+" * instead and the value is replaced by 0 (every pointer argument points at\n"
+" * least 4 valid bytes, also for empty or absent buffers) */\n"
+"__device__ __forceinline__ float ld_f32(const char* p, u32 n, u32 i) {\n"
+"  const float v = ((const float*)p)[i < n ? i : 0u]; return i < n ? v : 0.0f;\n"
+"}\n"
+"__device__ __forceinline__ float ld_f16(const char* p, u32 n, u32 i) {\n"
+"  const float v = h2f(((const u16*)p)[i < n ? i : 0u]); return i < n ? v : 0.0f;\n"
+"}\n"
+"__device__ __forceinline__ float ld_i32(const char* p, u32 n, u32 i) {\n"
+"  const float v = (float)((const int*)p)[i < n ? i : 0u]; return i < n ? v : 0.0f;\n"
+"}\n"
+"__device__ __forceinline__ float ld_u32(const char* p, u32 n, u32 i) {\n"
+"  const float v = (float)((const u32*)p)[i < n ? i : 0u]; return i < n ? v : 0.0f;\n"
+"}\n"
 "__device__ __forceinline__ float ld_f32_u(const char* p, u32 i) { return ((const float*)p)[i]; }\n"
 "__device__ __forceinline__ float ld_f16_u(const char* p, u32 i) { return h2f(((const u16*)p)[i]); }\n"
 "__device__ __forceinline__ float ld_i32_u(const char* p, u32 i) { return (float)((const int*)p)[i]; }\n"
