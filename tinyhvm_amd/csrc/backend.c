@@ -82,6 +82,12 @@ static void read_dense_env(void) {
     hipb.dense_nosep = env_flag("THVM_HIP_DENSE_NOSEP");
     const char *e = getenv("THVM_HIP_DENSE_SPLITS");
     hipb.dense_splits = e ? (u32)atoi(e) : 0;
+    e = getenv("THVM_HIP_GEMM_PAD");
+    hipb.gemm_pad_k = e ? (u32)atoi(e) : 4;
+    if (hipb.gemm_pad_k > 8) hipb.gemm_pad_k = 4;
+    e = getenv("THVM_HIP_GEMM_BK");
+    hipb.gemm_bk = e ? (u32)atoi(e) : 0;
+    if (hipb.gemm_bk != 16 && hipb.gemm_bk != 32) hipb.gemm_bk = 0;
     e = getenv("THVM_HIP_DENSE_TILE");
     hipb.dense_tile = e ? (u32)atoi(e) : 0;
     if (hipb.dense_tile > 5) hipb.dense_tile = 0;
@@ -638,16 +644,23 @@ int thvm_hip_kernel_source(const UOpKernel *k, char *buf, u64 buflen, u32 *mode,
 
 int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t errlen);
 
-int thvm_hip_dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits) {
+/* The device-free entry points read the routing and tuning knobs once, as
+ * init would. */
+static void ensure_env(void) {
     static int env_read = 0;
     if (!hipb.initialized && !env_read) {
         read_dense_env();
         env_read = 1;
     }
+}
+
+int thvm_hip_dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits) {
+    ensure_env();
     return dense_analyze(k, M, N, K, splits);
 }
 
 int thvm_hip_dense_source(const UOpKernel *k, char *buf, u64 buflen) {
+    ensure_env();
     char *src = dense_source(k);
     if (!src) {
         if (buf && buflen) snprintf(buf, buflen, "not a matrix-core contraction");
@@ -660,6 +673,7 @@ int thvm_hip_dense_source(const UOpKernel *k, char *buf, u64 buflen) {
 }
 
 int thvm_hip_dense_compile_check(const UOpKernel *k, char *errbuf, u64 errlen) {
+    ensure_env();
     char *src = dense_source(k);
     if (!src) {
         if (errbuf && errlen) snprintf(errbuf, errlen, "not a matrix-core contraction");
