@@ -11,6 +11,9 @@ A step is one replay of the engine's recorded Backend calls for a workload
           TFLOP/s = GEMM FLOPs / step time.
   lenet   one LeNet-5 training step at batch 256 (forward, backward, SGD
           through ASSIGN: 54 kernels): steps/s.
+  convblock  conv3x3 64->64 pad 1, batchnorm (train), relu, maxpool 2, sum
+          loss, and the backward to dW and dX, x [64,64,56,56] ~ N(0,1)
+          (28 kernels): TFLOP/s = the three convolutions' FLOPs / step time.
 
 roofline: the dominant kernel's algorithmic bytes (or FLOPs) per launch / its
 average duration, from HIP events on the backend's stream around that one
@@ -39,6 +42,7 @@ MFMA_F32_PEAK_TFLOPS = 157.3
 METRIC = "fused-kernel HBM GB/s (% peak); f32 matmul TFLOPS; LeNet-5 train steps/sec"
 WL = os.path.join(ROOT, "tinyhvm_amd", "workloads")
 F4096 = 2 * 4096 ** 3
+FCONV = 2 * 64 * 64 * 64 * 56 * 56 * 9          # one 3x3 64->64 conv over [64,64,56,56]
 TAG_UOP, TAG_RS = 7, 8
 SKIP_READS = 1
 
@@ -89,6 +93,22 @@ WORKLOADS = {
                           "time scaled by 4; the engine's own CPU interpreter faults on the "
                           "padded convolution, so the oracle's restatement of it is timed "
                           "(1.4x slower than the engine's interpreter on the fused step)"},
+    },
+    "convblock": {
+        "trace": os.path.join(WL, "convblock_b64.trc"),
+        "step": ("conv.fwd", None),
+        "kernels": {1: ("conv.fwd", FCONV), 23: ("conv.dw", FCONV), 27: ("conv.dx", FCONV)},
+        "unit": "TFLOP/s", "bound": "mfma", "dominant": "conv.fwd",
+        "config": {"workload": "conv block f32 fwd+bwd: conv3x3 64->64 pad 1, batchnorm (train, "
+                               "eps 1e-5), relu, maxpool 2, sum loss; backward dW and dX",
+                   "batch": 64, "input": "N(0,1) [64,64,56,56]", "kernels_per_step": 28},
+        "profile": "convblock_b64.md",
+        "cpu": {"exe": "oracle/ora_replay", "kind": "port",
+                "trace": os.path.join(WL, "convblock_b1.trc"), "marks": ("conv.fwd", "-"),
+                "flops": 3 * FCONV // 64,
+                "sample": "the full step at batch 1 (the same 28 kernels; the convolutions' "
+                          "FLOPs are linear in the batch); the engine's own interpreter faults "
+                          "on the zero-pad kernel, so the oracle's restatement of it is timed"},
     },
 }
 

@@ -15,6 +15,9 @@
  *   ora_alu ...................... src/backend/cpu/dispatch.c:5-21
  *   ora_uop_exec / ora_dispatch_uop
  *                                  src/backend/cpu/uop.c:3-155
+ *   ora_dispatch_uop_exact ....... the same with SUM accumulators kept in
+ *                                  double (a checker of long sums, not a
+ *                                  restatement: the reference adds in float)
  *   ora_view_read / ora_st_read / ora_dispatch_rs
  *                                  src/backend/cpu/dispatch.c:23-282
  *   ora_contiguify ............... strided masked copy, src/ops/_.c:338-357
@@ -160,6 +163,7 @@ typedef struct {
     u32 n_leaf_ptrs;
     u32 *uv;
     f32 *fv;
+    double *dv;    /* exact mode: SUM accumulators in double, else NULL */
 } OraCtx;
 
 static int is_ftype(const UOpKernel *k, u32 id) {
@@ -201,11 +205,23 @@ static int ora_uop_exec(OraCtx *c, u32 start, u32 stop, u32 gid) {
         }
         case KOP_MASK: c->fv[i] = as_f(c, op->arg[0]) != 0.0f ? as_f(c, op->arg[1]) : 0.0f; break;
         case KOP_ALU: c->fv[i] = ora_alu(op->imm.u, op->arg[2], as_f(c, op->arg[0]), as_f(c, op->arg[1])); break;
-        case KOP_ACC_INIT: c->fv[i] = op->imm.f; break;
+        case KOP_ACC_INIT:
+            c->fv[i] = op->imm.f;
+            if (c->dv) c->dv[i] = op->imm.f;
+            break;
         case KOP_ACC: {
             u32 a = op->arg[0];
             f32 v = as_f(c, op->arg[1]);
-            if (a < k->n_ops) c->fv[a] = (op->imm.u == UOP_RMAX) ? (c->fv[a] > v ? c->fv[a] : v) : (c->fv[a] + v);
+            if (a >= k->n_ops) break;
+            if (op->imm.u == UOP_RMAX) {
+                c->fv[a] = c->fv[a] > v ? c->fv[a] : v;
+                if (c->dv) c->dv[a] = c->fv[a];
+            } else if (c->dv) {
+                c->dv[a] += (double)v;
+                c->fv[a] = (f32)c->dv[a];
+            } else {
+                c->fv[a] = c->fv[a] + v;
+            }
             break;
         }
         case KOP_RANGE: {
@@ -226,8 +242,8 @@ static int ora_uop_exec(OraCtx *c, u32 start, u32 stop, u32 gid) {
     return 1;
 }
 
-void ora_dispatch_uop(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, u32 n_leaves,
-                      const UOpKernel *k) {
+static void ora_dispatch_uop_mode(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes,
+                                  u32 n_leaves, const UOpKernel *k, int exact) {
     if (!k || !out || k->n_ops > KOP_MAX) return;
     u32 range_end[KOP_MAX], stack[KOP_MAX], sp = 0;
     for (u32 i = 0; i < KOP_MAX; i++) range_end[i] = 0xFFFFFFFFu;
@@ -241,13 +257,28 @@ void ora_dispatch_uop(void *out, u64 out_bytes, const void **leaf, const u64 *le
     if (sp != 0) return;
     u32 uv[KOP_MAX];
     f32 fv[KOP_MAX];
-    OraCtx c = {k, range_end, out, out_bytes, leaf, leaf_bytes, n_leaves, uv, fv};
+    double dv[KOP_MAX];
+    OraCtx c = {k, range_end, out, out_bytes, leaf, leaf_bytes, n_leaves, uv, fv, exact ? dv : NULL};
     u32 total = k->local_size > 0 ? k->grid[0] : k->grid[0] * k->grid[1] * k->grid[2];
     for (u32 gid = 0; gid < total; gid++) {
         memset(uv, 0, sizeof uv);
         memset(fv, 0, sizeof fv);
         if (!ora_uop_exec(&c, 0, k->n_ops, gid)) return;
     }
+}
+
+void ora_dispatch_uop(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, u32 n_leaves,
+                      const UOpKernel *k) {
+    ora_dispatch_uop_mode(out, out_bytes, leaf, leaf_bytes, n_leaves, k, 0);
+}
+
+/* The kernel with every SUM accumulated in double and rounded to float when
+ * an op reads it: the exact sum of the same float terms, to tell a reordered
+ * GPU sum's error from the float rounding of the reference's own serial one
+ * over long reductions. */
+void ora_dispatch_uop_exact(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, u32 n_leaves,
+                            const UOpKernel *k) {
+    ora_dispatch_uop_mode(out, out_bytes, leaf, leaf_bytes, n_leaves, k, 1);
 }
 
 /* ---------------- FusedOp interpreter ---------------- */

@@ -12,6 +12,10 @@
   LeNet-5 B=256     every dispatch of one training step against the oracle on
                     the GPU's own inputs (the kernel-boundary parity of
                     tests/test_gpu_parity.py at the benchmark batch).
+  conv block B=64   the same for the 28 dispatches of the conv block's forward
+                    and backward at [64,64,56,56]; the three 14.8 GFLOP
+                    convolutions are checked on a prefix of their outputs
+                    (about 1.5e8 multiply-adds of oracle work each).
 
 Inputs are the traces' generator specs materialized on the host, so the
 numpy side sees exactly the bytes the GPU was given.
@@ -121,5 +125,31 @@ def test_lenet_b256_kernel_parity(hip):
     kr, _e2e = kernel_parity(hip.thvm_hip_backend(), hip.thvm_hip_buf_read, hip.thvm_hip_synchronize,
                              ora, os.path.join(WL, "lenet_b256.trc"))
     assert len(kr) >= 54
+    bad = [r for r in kr if not r[1]]
+    assert not bad, "kernel parity: %s" % bad
+
+
+ORACLE_MACS = 150_000_000
+
+
+def _conv_prefix(k):
+    """Outputs of a contraction the oracle checks: all of them up to about
+    1.5e8 multiply-adds, else the first ORACLE_MACS / K."""
+    a = _lib.dense_analyze(k)
+    if not a:
+        return None
+    M, N, K, _splits = a
+    if M * N * K <= ORACLE_MACS:
+        return None
+    return max(1, ORACLE_MACS // K)
+
+
+@pytest.mark.timeout(600)
+def test_convblock_b64_kernel_parity(hip):
+    ora = _oracle()
+    kr, _e2e = kernel_parity(hip.thvm_hip_backend(), hip.thvm_hip_buf_read, hip.thvm_hip_synchronize,
+                             ora, os.path.join(WL, "convblock_b64.trc"), prefix_fn=_conv_prefix)
+    assert len(kr) >= 28
+    assert sum(1 for r in kr if "first" in r[2]) == 3
     bad = [r for r in kr if not r[1]]
     assert not bad, "kernel parity: %s" % bad

@@ -10,7 +10,10 @@ the oracle's under the kernel's tolerance class (the BASELINE north star):
   - 1e-6 relative per element (floor 1e-3 of the output's max): the same with
     EXP or LOG, whose last bit may differ between GPU and host libm;
   - 1e-4 normwise (max |x - y| <= 1e-4 max |y|): sums whose order differs
-    (split across a workgroup, or accumulated by matrix cores).
+    (split across a workgroup, or accumulated by matrix cores). Where the
+    reference's own serial float sum is farther than that from the exact sum
+    of the same terms (the oracle with double accumulators), the GPU result
+    must be within 1e-4 of the exact sum instead.
 End-to-end: the outputs the trace recorded from the reference CPU backend
 (SNAPSHOT records) must match the GPU run within 1e-3 normwise, the GPU's
 reordered sums propagating through whole training steps.
@@ -46,6 +49,7 @@ def _oracle():
     u64, vp = C.c_uint64, C.c_void_p
     ora.ora_dispatch_uop.argtypes = [vp, u64, C.POINTER(vp), C.POINTER(u64), C.c_uint32,
                                      C.POINTER(abi.UOpKernel)]
+    ora.ora_dispatch_uop_exact.argtypes = ora.ora_dispatch_uop.argtypes
     ora.ora_dispatch_rs.argtypes = [vp, u64, C.POINTER(vp), C.POINTER(u64),
                                     C.POINTER(C.POINTER(abi.View)),
                                     C.POINTER(C.POINTER(abi.ShapeTracker)), C.c_uint32,
@@ -187,9 +191,14 @@ def _rs_args(r):
     return keep, vptr, sptr, ops, full, red, dts
 
 
-def kernel_parity(backend, read_fn, sync_fn, ora, path, tol_fn=None):
+def kernel_parity(backend, read_fn, sync_fn, ora, path, tol_fn=None, prefix_fn=None):
     """Replays `path` against `backend`, checking every dispatch against the
-    oracle on the same inputs and every SNAPSHOT against the reference."""
+    oracle on the same inputs and every SNAPSHOT against the reference.
+
+    prefix_fn(k) -> T or None: for a kernel too large for the oracle, check
+    its first T outputs only. A lowered kernel's index arithmetic decodes the
+    flat output index from GID by constants of its own, not from the grid, so
+    the oracle run over a grid of T computes exactly those T outputs."""
     tol_fn = tol_fn or uop_tolerance
     recs = trace.read_trace(path)
     rp = tt.Replay(path, backend)
@@ -209,9 +218,17 @@ def kernel_parity(backend, read_fn, sync_fn, ora, path, tol_fn=None):
                 n = len(leaves)
                 lp = (C.c_void_p * max(n, 1))(*[C.cast(b, C.c_void_p) if m else None for b, m in leaves])
                 lb = (C.c_uint64 * max(n, 1))(*[m for _b, m in leaves])
+                cmp_n, note = out_n, ""
                 if r.tag == trace.UOP:
                     k = trace.to_uop_kernel(r)
-                    ora.ora_dispatch_uop(C.cast(out_buf, C.c_void_p), out_n, lp, lb, n, C.byref(k))
+                    T = prefix_fn(k) if prefix_fn else None
+                    kp = k
+                    if T:
+                        kp = trace.to_uop_kernel(r)
+                        kp.grid[0], kp.grid[1], kp.grid[2] = T, 1, 1
+                        cmp_n = min(out_n, T * (2 if k.out_dtype == 1 else 4))
+                        note = " [first %d outputs]" % T
+                    ora.ora_dispatch_uop(C.cast(out_buf, C.c_void_p), out_n, lp, lb, n, C.byref(kp))
                     kind, rtol = tol_fn(k)
                     dtype = k.out_dtype
                 else:
@@ -226,7 +243,17 @@ def kernel_parity(backend, read_fn, sync_fn, ora, path, tol_fn=None):
                 rp.run(i, i + 1)
                 dtype_of[out_id] = dtype
                 got, _ = host.read(out_id)
-                ok, msg = compare(bytes(got)[:out_n], bytes(out_buf)[:out_n], dtype, kind, rtol)
+                ok, msg = compare(bytes(got)[:cmp_n], bytes(out_buf)[:cmp_n], dtype, kind, rtol)
+                if not ok and kind == "norm" and r.tag == trace.UOP:
+                    # a long serial float sum in the reference can itself be
+                    # farther than the tolerance from the exact sum: then the
+                    # GPU must be within the tolerance of the exact sum
+                    exact = (C.c_uint8 * max(out_n, 4))()
+                    ora.ora_dispatch_uop_exact(C.cast(exact, C.c_void_p), out_n, lp, lb, n, C.byref(kp))
+                    ok, m_gpu = compare(bytes(got)[:cmp_n], bytes(exact)[:cmp_n], dtype, kind, rtol)
+                    _ok, m_ref = compare(bytes(out_buf)[:cmp_n], bytes(exact)[:cmp_n], dtype, kind, rtol)
+                    msg = "vs reference %s; vs the exact sum: gpu %s, reference %s" % (msg, m_gpu, m_ref)
+                msg += note
                 kernel_results.append((i, ok, msg))
                 print("  %s dispatch %d (%s): %s" % (path.split("/")[-1], i, kind, msg), flush=True)
             elif r.tag == trace.CONTIG or r.tag in trace.LEGACY:

@@ -75,3 +75,46 @@ def test_planted_mistake_is_caught():
     y = np.frombuffer(snaps[0].f["data"], dtype=np.float32)
     ok, _ = tt.close(y, y_wrong, 1e-5)
     assert not ok
+
+
+def _run_uop(fn, rec, leaves_by_id, out_elems):
+    k = trace.to_uop_kernel(rec)
+    arrs = [leaves_by_id[t] for t in rec.f["leaf_bufs"]]
+    n = len(arrs)
+    lp = (C.c_void_p * n)(*[a.ctypes.data for a in arrs])
+    lb = (C.c_uint64 * n)(*[a.nbytes for a in arrs])
+    out = np.zeros(out_elems, dtype=np.float32)
+    fn(C.c_void_p(out.ctypes.data), out.nbytes, lp, lb, n, C.byref(k))
+    return out
+
+
+@pytest.mark.parametrize("path", tt.fixtures("fused_3x1000.trc") + tt.fixtures("fused_64x256.trc"),
+                         ids=lambda p: p.split("/")[-1])
+def test_exact_accumulation_mode(path):
+    """ora_dispatch_uop_exact (the checker of long sums): the fused forward's
+    row sums equal the float64 sum of the same float32 terms rounded once, and
+    a kernel without a sum (the backward) is bit-identical to the float mode."""
+    from tests.test_gpu_parity import _oracle
+    ora = _oracle()
+    recs = trace.read_trace(path)
+    leaves = {}
+    for r in recs:
+        if r.tag == trace.WRITE:
+            f = r.f
+            if f["enc"] == trace.ENC_GEN:
+                data = trace.gen_data(f["dist"], f["dtype"], f["seed"], f["p0"], f["p1"], f["bytes"])
+            else:
+                data = f["data"]
+            leaves[f["id"]] = np.frombuffer(data, dtype=np.float32).copy()
+    ups = [r for r in recs if r.tag == trace.UOP]
+    R, Cc = ups[0].f["full_dims"][:2]
+    a, b, c = (leaves[t].reshape(R, Cc) for t in ups[0].f["leaf_bufs"][:3])
+    y = _run_uop(ora.ora_dispatch_uop_exact, ups[0], leaves, R)
+    terms = np.maximum((a * b) + c, np.float32(0))
+    want = terms.astype(np.float64).sum(axis=1).astype(np.float32)
+    assert np.array_equal(y, want)
+    y32 = _run_uop(ora.ora_dispatch_uop, ups[0], leaves, R)
+    assert not np.array_equal(y32, want) or Cc < 512   # the serial float sum rounds at each step
+    d_exact = _run_uop(ora.ora_dispatch_uop_exact, ups[1], leaves, R * Cc)
+    d_float = _run_uop(ora.ora_dispatch_uop, ups[1], leaves, R * Cc)
+    assert np.array_equal(d_exact, d_float)

@@ -90,7 +90,7 @@ static void read_dense_env(void) {
     if (hipb.gemm_bk != 16 && hipb.gemm_bk != 32) hipb.gemm_bk = 0;
     e = getenv("THVM_HIP_DENSE_TILE");
     hipb.dense_tile = e ? (u32)atoi(e) : 0;
-    if (hipb.dense_tile > 5) hipb.dense_tile = 0;
+    if (hipb.dense_tile > 7) hipb.dense_tile = 0;
 }
 
 static int hb_init(void) {

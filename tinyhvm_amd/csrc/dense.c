@@ -473,6 +473,10 @@ static const TileCfg CFG_BIG = {128, 128, 32, 2, 2, 2, 2, "128x128"};   /* large
 static const TileCfg CFG_MID = {64, 64, 32, 1, 1, 2, 2, "64x64"};       /* small GEMMs: more tiles */
 static const TileCfg CFG_TALL = {256, 32, 16, 2, 1, 4, 1, "256x32"};    /* N <= 32 (conv channels) */
 static const TileCfg CFG_WIDE = {32, 256, 16, 1, 2, 1, 4, "32x256"};    /* M <= 32 */
+/* 64 output channels: waves stacked along M, each 64x64 like the big tile;
+ * K 16 per stage keeps the stages at 42 KB of LDS (3 workgroups per CU) */
+static const TileCfg CFG_C64 = {256, 64, 16, 2, 2, 4, 1, "256x64"};
+static const TileCfg CFG_C64S = {128, 64, 32, 2, 1, 2, 2, "128x64"};
 /* Small and skinny contractions (conv channels, fc layers, weight gradients):
  * with operands that fit in L2 there is little to gain from sharing tiles
  * through LDS, and everything to gain from keeping many independent loads in
@@ -904,23 +908,30 @@ static DenseEntry *insert(u64 key, const UOpKernel *k) {
     return e;
 }
 
-/* Measured on MI355X over the LeNet-5 and 4096^3 contractions: big tiles
- * when both sides are large; the LDS-staged 256x32 (32x256) tile for very
- * tall (wide) and thin operands such as convolutions over a batch of images,
- * where its four waves share each operand stage; the direct kernel for the
- * rest (fully connected layers, weight gradients). */
-static TileCfg pick_cfg(u32 M, u32 N) {
+/* Measured on MI355X over the LeNet-5, conv-block and 4096^3 contractions:
+ * big tiles when both sides are large; the LDS-staged 256x32 (32x256) tile
+ * for very tall (wide) and thin operands such as convolutions over a batch of
+ * images, where its four waves share each operand stage; for 64 channels
+ * (33..64 columns) the 64x64 tile on a tall convolution (231 us against 282
+ * for 256x64 and 480 for the direct kernel on a 3x3 64->64 conv over
+ * [64,64,56,56]) and the 128x64 tile on a weight gradient's long K (245 us
+ * against 676); the direct kernel for the rest (fully connected layers, small
+ * weight gradients). */
+static TileCfg pick_cfg(u32 M, u32 N, u32 K) {
     u64 big_tiles = (u64)((M + 127) / 128) * ((N + 127) / 128);
     if (M >= 128 && N >= 128 && big_tiles >= 128) return CFG_BIG;
     if (N <= 32 && M >= 4096) return CFG_TALL;
     if (M <= 32 && N >= 4096) return CFG_WIDE;
+    if (N > 32 && N <= 64 && M >= 4096) return CFG_MID;
+    if (N > 32 && N <= 64 && M >= 256 && K >= 16384) return CFG_C64S;
     return CFG_DIRECT;
 }
 
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
-    static const TileCfg *forced[6] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT};
+    static const TileCfg *forced[8] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
+                                       &CFG_C64S};
     memset(pl, 0, sizeof *pl);
-    pl->cfg = hipb.dense_tile ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N);
+    pl->cfg = hipb.dense_tile ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
     /* LDS padding: a k-major operand is stored with 16 lanes along k, i.e.
      * at row stride LDA; an odd stride puts those lanes in distinct banks */
     pl->pad_a = ct->p_kmajor ? hipb.gemm_pad_k : 4;

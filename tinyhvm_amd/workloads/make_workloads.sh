@@ -8,6 +8,9 @@
 #   linear_8x4096x4096   the same with 8 rows of X (CPU-baseline slice)
 #   lenet_b256           one LeNet-5 training step at batch 256
 #   lenet_b64            the same at batch 64 (CPU-baseline sample)
+#   convblock_b64        conv3x3 64->64 pad 1 + batchnorm + relu + maxpool 2,
+#                        forward and backward, x [64,64,56,56]
+#   convblock_b1         the same at batch 1 (CPU-baseline sample)
 set -e
 HERE=$(cd "$(dirname "$0")" && pwd)
 ROOT=$(cd "$HERE/../.." && pwd)
@@ -19,3 +22,5 @@ $CAP -n linear linear_4096.trc 4096 4096 4096
 $CAP -n linear linear_8x4096x4096.trc 8 4096 4096
 $CAP -n lenet lenet_b256.trc 256 1
 $CAP -n lenet lenet_b64.trc 64 1
+$CAP -n convblock convblock_b64.trc 64 64 56
+$CAP -n convblock convblock_b1.trc 1 64 56
