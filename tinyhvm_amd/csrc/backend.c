@@ -80,6 +80,7 @@ static int env_flag(const char *name) {
 static void read_dense_env(void) {
     hipb.dense_force = env_flag("THVM_HIP_DENSE_FORCE");
     hipb.dense_nosep = env_flag("THVM_HIP_DENSE_NOSEP");
+    hipb.dense_nokperm = env_flag("THVM_HIP_DENSE_NOKPERM");
     const char *e = getenv("THVM_HIP_DENSE_SPLITS");
     hipb.dense_splits = e ? (u32)atoi(e) : 0;
     e = getenv("THVM_HIP_GEMM_PAD");

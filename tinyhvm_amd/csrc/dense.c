@@ -252,20 +252,43 @@ static int collect_gdigits(const DCtx *c, const u8 *cone, Digit *out, u32 *n, in
     return 1;
 }
 
-/* Is the first load of the cone contiguous along r (k) rather than gid? */
+/* Length of the contiguous run of an affine index along one variable: its
+ * fastest digit with coefficient 1, extended by each next digit whose
+ * coefficient equals the run so far (e.g. [y, x] of a row-major image); 0
+ * when the fastest digit is not unit-stride. Along k (var 1) the next digit
+ * must follow in k itself (divisor = the run's); along the output rows
+ * (var 0) it is the side's next gid digit, wherever the other side's digits
+ * sit between them in gid. */
+static u64 contiguous_run(const DCtx *c, const Aff *a, u8 var) {
+    u64 run = 0, div = 0;
+    for (;;) {
+        int t = -1;
+        for (u32 i = 0; i < a->n; i++) {
+            if (a->d[i].var != var) continue;
+            if (var == 1 && a->d[i].div != (div ? div : 1)) continue;
+            if (var == 0 && a->d[i].div <= div) continue;
+            if (t < 0 || a->d[i].div < a->d[t].div) t = (int)i;
+        }
+        if (t < 0 || a->coef[t] != (run ? run : 1)) break;
+        u64 ext = a->d[t].mod ? a->d[t].mod : (var_range(c, var) + a->d[t].div - 1) / a->d[t].div;
+        run = run ? run * ext : ext;
+        div = a->d[t].div;
+        if (!a->d[t].mod) break;
+        if (var == 1) div *= ext;
+        if (div > 0xFFFFFFFFull || run > 0xFFFFFFFFull) break;
+    }
+    return run;
+}
+
+/* Is the first load of the cone contiguous along r (k) rather than gid? The
+ * longer contiguous run wins: an image's rows (56 floats along the output
+ * pixels of a convolution) over the 3 taps of a kernel row along k. */
 static int cone_kmajor(const DCtx *c, const u8 *cone) {
     for (u32 i = 0; i < c->k->n_ops; i++) {
         if (!cone[i] || c->k->ops[i].type != KOP_LOAD) continue;
         const Aff *a = &c->aff[c->k->ops[i].arg[0]];
         if (!a->ok) return 1;
-        u32 coef_r = 0, coef_g = 0, best_r = 0xFFFFFFFFu, best_g = 0xFFFFFFFFu;
-        for (u32 t = 0; t < a->n; t++) {
-            if (a->d[t].var == 1 && a->d[t].div < best_r) { best_r = a->d[t].div; coef_r = a->coef[t]; }
-            if (a->d[t].var == 0 && a->d[t].div < best_g) { best_g = a->d[t].div; coef_g = a->coef[t]; }
-        }
-        if (coef_r == 1) return 1;
-        if (coef_g == 1) return 0;
-        return 1;
+        return contiguous_run(c, a, 1) >= contiguous_run(c, a, 0);
     }
     return 1;
 }
@@ -484,6 +507,27 @@ static const TileCfg CFG_C64S = {128, 64, 32, 2, 1, 2, 2, "128x64"};
  * of both MFMA operands per iteration straight into registers. */
 static const TileCfg CFG_DIRECT = {32, 32, 32, 1, 1, 1, 1, "direct32", 1};
 
+/* K-reordered affine loading of separable operands. K is split into atomic
+ * digits (the finest mixed radix both operands' k offsets decompose into);
+ * the largest digit whose extent is a multiple of the stage depth becomes the
+ * innermost, so that within a stage both offsets are a uniform base (a
+ * function of the stage's start) plus a per-lane constant. The sum visits the
+ * same (m, n, k) terms in another order. Loads are unchecked: the dispatch
+ * verifies that the largest index each side can form lies inside its buffer. */
+#define KP_MAX (4 * DG_MAX + 2)
+typedef struct {
+    int on;
+    u32 E;                       /* extent of the inner digit */
+    u32 ndig;                    /* outer digits, fastest first */
+    u32 oext[KP_MAX];
+    u32 ocoef[2][KP_MAX];
+    u32 icoef[2];                /* per side: coefficient of the inner digit */
+    u64 maxidx[2];               /* largest element index a side can form */
+    u32 buf[2];                  /* the buffer each side loads (1 + leaf) */
+    int lin[2];                  /* tile rows map to offsets linearly (no digit carry inside a tile) */
+    u32 lcoef[2];                /* the row coefficient of a linear side */
+} KPerm;
+
 typedef struct {
     char name[48];
     TileCfg cfg;
@@ -491,6 +535,7 @@ typedef struct {
     u32 splits;
     u32 kchunk;
     u32 tiles_m, tiles_n;
+    KPerm kp;
 } GemmPlan;
 
 #define GEMM_THREADS 256
@@ -665,12 +710,60 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
                "      if (m < M && n < N) {\n");
 }
 
+/* Uniform k base of one side at the stage starting at reordered index k. */
+static void emit_kbase_fn(DSB *s, const KPerm *kp, int side) {
+    dsb_put(s, "__device__ __forceinline__ u32 kbase_%c(u32 k) {\n  u32 o = k / %uu;\n  u32 u = (k %% %uu) * %uu;\n",
+            side ? 'q' : 'p', kp->E, kp->E, kp->icoef[side]);
+    for (u32 t = 0; t < kp->ndig; t++) {
+        if (t + 1 < kp->ndig)
+            dsb_put(s, "  u += (o %% %uu) * %uu; o /= %uu;\n", kp->oext[t], kp->ocoef[side][t], kp->oext[t]);
+        else
+            dsb_put(s, "  u += o * %uu;\n", kp->ocoef[side][t]);
+    }
+    dsb_put(s, "  return u;\n}\n");
+}
+
+/* K-reordered loaders (see KPerm): per-lane offsets once per tile, then one
+ * uniform base per stage and an unchecked load per element. Rows past the
+ * end of M (N) are clamped to the last row; their products are never stored. */
+static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl) {
+    const TileCfg *cf = &pl->cfg;
+    const KPerm *kp = &pl->kp;
+    const u32 EX[2] = {cf->bm * cf->bk / GEMM_THREADS, cf->bn * cf->bk / GEMM_THREADS};
+    for (int side = 0; side < 2; side++) {
+        const char S = side ? 'q' : 'p', X = side ? 'B' : 'A';
+        const char *xn = side ? "nn" : "mm";
+        const int kmaj = side ? ct->q_kmajor : ct->p_kmajor;
+        const u32 bx = side ? cf->bn : cf->bm;
+        if (kp->lin[side]) {
+            dsb_put(s, "  const u32 o%c = rowb_%c(gid_%c(%s));\n", X, S, side ? 'n' : 'm', side ? "n0" : "m0");
+        } else {
+            dsb_put(s, "  u32 o%c[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", X, EX[side], EX[side]);
+            emit_map(s, kmaj, bx, cf->bk, xn);
+            dsb_put(s, "\n    const u32 x = %s + %s;\n"
+                       "    o%c[e] = rowb_%c(gid_%c(x < %uu ? x : %uu)) + kk * %uu; }\n",
+                    side ? "n0" : "m0", xn, X, S, side ? 'n' : 'm', side ? ct->N : ct->M,
+                    (side ? ct->N : ct->M) - 1, kp->icoef[side]);
+        }
+        dsb_put(s, "  auto load%c = [&](u32 k0) {\n"
+                   "    const float* ps = (const float*)p%u + kbase_%c(k0);\n"
+                   "    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
+                X, ct->sep_buf[side], S, EX[side]);
+        emit_map(s, kmaj, bx, cf->bk, xn);
+        if (kp->lin[side])
+            dsb_put(s, "\n      r%c[e] = ps[o%c + %s * %uu + kk * %uu]; }\n  };\n", side ? 'b' : 'a', X, xn,
+                    kp->lcoef[side], kp->icoef[side]);
+        else
+            dsb_put(s, "\n      r%c[e] = ps[o%c[e]]; }\n  };\n", side ? 'b' : 'a', X);
+    }
+}
+
 static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const GemmPlan *pl, char *err,
                              size_t errlen) {
     /* the big tile evaluates its operands in place: separable row bases would
      * hold 16 more registers across its whole K loop (measured slower) */
     Contraction ctl = *ct_in;
-    if (pl->cfg.bm == 128) ctl.sep[0] = ctl.sep[1] = 0;
+    if (pl->cfg.bm == 128 && !pl->kp.on) ctl.sep[0] = ctl.sep[1] = 0;
     const Contraction *ct = &ctl;
     DSB s = {0};
     const TileCfg *cf = &pl->cfg;
@@ -682,6 +775,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         if (!ct->sep[side]) continue;
         emit_sep_fn(&s, side ? "rowb_q" : "rowb_p", &ct->sep_aff[side], 0);
         emit_sep_fn(&s, side ? "koff_q" : "koff_p", &ct->sep_aff[side], 1);
+        if (pl->kp.on) emit_kbase_fn(&s, &pl->kp, side);
     }
     static char body[1 << 16];
     for (int side = 0; side < 2; side++) {
@@ -733,17 +827,19 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
             "  const u32 kbeg = blockIdx.y * KCH;\n"
             "  const u32 kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
             "  float ra[%u], rb[%u];\n", EA, EB);
+    if (pl->kp.on) emit_kperm_loaders(&s, ct, pl);
     /* separable operands: per-row index bases, once per tile */
-    if (ct->sep[0]) {
+    if (!pl->kp.on && ct->sep[0]) {
         dsb_put(&s, "  u32 bA[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", EA, EA);
         emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
         dsb_put(&s, " (void)kk; bA[e] = rowb_p(gid_m(m0 + mm)); }\n");
     }
-    if (ct->sep[1]) {
+    if (!pl->kp.on && ct->sep[1]) {
         dsb_put(&s, "  u32 bB[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", EB, EB);
         emit_map(&s, ct->q_kmajor, cf->bn, cf->bk, "nn");
         dsb_put(&s, " (void)kk; bB[e] = rowb_q(gid_n(n0 + nn)); }\n");
     }
+    if (!pl->kp.on) {
     dsb_put(&s, "  auto loadA = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
     emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
     /* operands are evaluated unconditionally (every load is range-checked,
@@ -779,6 +875,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
     }
     dsb_put(&s, "      rb[e] = __uint_as_float(__float_as_uint(v) & ((%s && %s) ? 0xFFFFFFFFu : 0u)); }\n  };\n", gn,
             gk);
+    }
     dsb_put(&s, "  auto storeA = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
     emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
     dsb_put(&s, " As[buf][kk * LDA + mm] = ra[e]; }\n  };\n");
@@ -927,6 +1024,121 @@ static TileCfg pick_cfg(u32 M, u32 N, u32 K) {
     return CFG_DIRECT;
 }
 
+static int cmp_u64(const void *x, const void *y) {
+    u64 a = *(const u64 *)x, b = *(const u64 *)y;
+    return a < b ? -1 : a > b;
+}
+
+/* Largest value one digit of an affine index takes. */
+static u64 digit_max(const Digit *d, u64 range) {
+    if (d->mod) return d->mod - 1;
+    return (range + d->div - 1) / d->div - 1;
+}
+
+static int plan_kperm(const Contraction *ct, GemmPlan *pl) {
+    KPerm *kp = &pl->kp;
+    memset(kp, 0, sizeof *kp);
+    const TileCfg *cf = &pl->cfg;
+    if (hipb.dense_nokperm || cf->direct) return 0;
+    const u64 K = ct->K, total = (u64)ct->M * ct->N;
+    for (int s = 0; s < 2; s++)
+        if (!ct->sep[s] || ct->sep_dt[s] != DTYPE_F32 || ct->sep_buf[s] == 0) return 0;
+    /* digit boundaries of both sides' k offsets */
+    u64 b[KP_MAX + 2];
+    u32 nb = 0;
+    b[nb++] = 1;
+    b[nb++] = K;
+    for (int s = 0; s < 2; s++) {
+        const Aff *a = &ct->sep_aff[s];
+        for (u32 t = 0; t < a->n; t++) {
+            if (a->d[t].var != 1) continue;
+            if (nb + 2 > KP_MAX + 2) return 0;
+            b[nb++] = a->d[t].div;
+            b[nb++] = a->d[t].mod ? (u64)a->d[t].div * a->d[t].mod : K;
+        }
+    }
+    qsort(b, nb, sizeof b[0], cmp_u64);
+    u32 nu = 0;
+    for (u32 i = 0; i < nb; i++)
+        if (nu == 0 || b[i] != b[nu - 1]) b[nu++] = b[i];
+    if (b[nu - 1] != K) return 0;
+    u32 nd = nu - 1;                      /* atomic digit j: div b[j], extent b[j+1] / b[j] */
+    u64 ext[KP_MAX], co[2][KP_MAX];
+    for (u32 j = 0; j < nd; j++) {
+        if (b[j + 1] % b[j]) return 0;
+        ext[j] = b[j + 1] / b[j];
+        co[0][j] = co[1][j] = 0;
+    }
+    for (int s = 0; s < 2; s++) {
+        const Aff *a = &ct->sep_aff[s];
+        u64 mx = a->cst;
+        for (u32 t = 0; t < a->n; t++) {
+            const Digit *d = &a->d[t];
+            if (d->var == 0) {
+                mx += (u64)a->coef[t] * digit_max(d, total);
+                continue;
+            }
+            u64 end = d->mod ? (u64)d->div * d->mod : K;
+            for (u32 j = 0; j < nd; j++)
+                if (b[j] >= d->div && b[j + 1] <= end) co[s][j] += (u64)a->coef[t] * (b[j] / d->div);
+        }
+        for (u32 j = 0; j < nd; j++) {
+            if (co[s][j] > 0xFFFFFFFFull) return 0;
+            mx += co[s][j] * (ext[j] - 1);
+        }
+        kp->maxidx[s] = mx;
+        if (mx > 0xFFFFFFFFull) return 0;
+    }
+    /* the inner digit: the longest whose extent the stage depth divides */
+    int best = -1;
+    for (u32 j = 0; j < nd; j++)
+        if (ext[j] % cf->bk == 0 && (best < 0 || ext[j] > ext[best])) best = (int)j;
+    if (best < 0) return 0;
+    /* lanes along k stay coalesced only on a unit-stride inner digit; a
+     * strided one is fine for an operand that stays in cache (weights) */
+    for (int s = 0; s < 2; s++) {
+        int kmaj = s ? ct->q_kmajor : ct->p_kmajor;
+        if (kmaj && co[s][best] != 1 && kp->maxidx[s] * 4 > (8ull << 20)) return 0;
+    }
+    kp->E = (u32)ext[best];
+    kp->buf[0] = ct->sep_buf[0];
+    kp->buf[1] = ct->sep_buf[1];
+    for (int s = 0; s < 2; s++) kp->icoef[s] = (u32)co[s][best];
+    for (u32 j = 0; j < nd; j++) {
+        if ((int)j == best) continue;
+        kp->oext[kp->ndig] = (u32)ext[j];
+        kp->ocoef[0][kp->ndig] = (u32)co[0][j];
+        kp->ocoef[1][kp->ndig] = (u32)co[1][j];
+        kp->ndig++;
+    }
+    /* rows of a tile that never carry into the next gid digit map linearly */
+    for (int s = 0; s < 2; s++) {
+        u32 nx = s ? ct->nq : ct->np;
+        u32 fdiv = s ? ct->qdiv[nx - 1] : ct->pdiv[nx - 1];
+        u32 fext = s ? ct->qext[nx - 1] : ct->pext[nx - 1];
+        u32 bx = s ? cf->bn : cf->bm, mx = s ? ct->N : ct->M;
+        if (fext % bx || mx % bx) continue;
+        const Aff *a = &ct->sep_aff[s];
+        int ok = 1;
+        u32 lc = 0;
+        for (u32 t = 0; t < a->n; t++) {
+            const Digit *d = &a->d[t];
+            if (d->var != 0 || d->div != fdiv) continue;
+            if (d->mod && d->mod != fext) ok = 0;
+            lc = a->coef[t];
+        }
+        kp->lin[s] = ok;
+        kp->lcoef[s] = lc;
+    }
+    /* the big tile keeps no per-lane offset arrays (registers) */
+    if (cf->bm == 128 && !(kp->lin[0] && kp->lin[1])) {
+        memset(kp, 0, sizeof *kp);
+        return 0;
+    }
+    kp->on = 1;
+    return 1;
+}
+
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     static const TileCfg *forced[8] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
                                        &CFG_C64S};
@@ -936,7 +1148,7 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
      * at row stride LDA; an odd stride puts those lanes in distinct banks */
     pl->pad_a = ct->p_kmajor ? hipb.gemm_pad_k : 4;
     pl->pad_b = ct->q_kmajor ? hipb.gemm_pad_k : 4;
-    if (pl->cfg.bm == 128 && hipb.gemm_bk) pl->cfg.bk = hipb.gemm_bk;
+    if (!pl->cfg.direct && hipb.gemm_bk) pl->cfg.bk = hipb.gemm_bk;
     pl->tiles_m = (ct->M + pl->cfg.bm - 1) / pl->cfg.bm;
     pl->tiles_n = (ct->N + pl->cfg.bn - 1) / pl->cfg.bn;
     u32 tiles = pl->tiles_m * pl->tiles_n;
@@ -955,6 +1167,7 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     pl->kchunk = kch;
     pl->splits = (ct->K + kch - 1) / kch;
     snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));
+    plan_kperm(ct, pl);
 }
 
 /* Contraction analysis without a device: returns 1 and fills M/N/K when the
@@ -989,7 +1202,26 @@ char *dense_source(const UOpKernel *k) {
     return gen_gemm_source(k, &ct, &pl, err, sizeof err);
 }
 
+/* The unchecked loads of a K-reordered plan stay inside the buffers they
+ * read: every index a side can form is below that buffer's element count. */
+static int kperm_fits(const KPerm *kp, const u32 *counts) {
+    for (int s = 0; s < 2; s++)
+        if (kp->maxidx[s] >= counts[kp->buf[s]]) return 0;
+    return 1;
+}
+
 int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
+    void *ptrs[FUSE_MAX_LEAVES + 1];
+    u32 counts[FUSE_MAX_LEAVES + 1];
+    if (k->n_leaves > FUSE_MAX_LEAVES) return 0;
+    ptrs[0] = pool_ptr(out_buf);
+    counts[0] = (u32)(pool_bytes(out_buf) / (k->out_dtype == DTYPE_F16 ? 2 : 4));
+    for (u32 i = 0; i < k->n_leaves; i++) {
+        void *lp = i < n_leaves ? pool_ptr(leaf_bufs[i]) : NULL;
+        ptrs[i + 1] = lp ? lp : hipb.dummy;   /* loads index an absent buffer's element 0 */
+        u64 b = lp ? pool_bytes(leaf_bufs[i]) : 0;
+        counts[i + 1] = (u32)(b / (k->leaf_dtypes[i] == DTYPE_F16 ? 2 : 4));
+    }
     u64 key = uop_signature(k) ^ 0xD5E5E5E5D5E5E5E5ull;
     if (!key) key = 1;
     DenseEntry *e = lookup(key, k);
@@ -1000,6 +1232,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         u32 M, N, K, sp;
         if (!dense_analyze(k, &M, &N, &K, &sp) || !recognize(k, &ct)) return 0;
         make_plan(&ct, &e->plan, uop_signature(k));
+        if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts)) memset(&e->plan.kp, 0, sizeof e->plan.kp);
         char err[256] = {0};
         char *src = gen_gemm_source(k, &ct, &e->plan, err, sizeof err);
         if (!src) {
@@ -1023,10 +1256,12 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         e->N = ct.N;
         e->is_dense = 1;
         if (hipb.verbose)
-            fprintf(stderr, "tinyhvm-hip: dense %s M=%u N=%u K=%u tile %s splits=%u\n", e->plan.name, ct.M,
-                    ct.N, ct.K, e->plan.cfg.tag, e->plan.splits);
+            fprintf(stderr, "tinyhvm-hip: dense %s M=%u N=%u K=%u tile %s splits=%u kperm=%u\n", e->plan.name, ct.M,
+                    ct.N, ct.K, e->plan.cfg.tag, e->plan.splits, e->plan.kp.on ? e->plan.kp.E : 0);
     }
     if (!e->is_dense) return 0;
+    /* buffers smaller than the plan was made for: the generated kernels */
+    if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts)) return 0;
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     /* split-K workspace */
     float *ws = NULL;
@@ -1034,18 +1269,8 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         ws = scratch_reserve(&D.ws, (u64)e->plan.splits * e->M * e->N * sizeof(float));
         if (!ws) return 0;
     }
-    void *ptrs[FUSE_MAX_LEAVES + 1];
-    u32 counts[FUSE_MAX_LEAVES + 1];
     void *params[2 * (FUSE_MAX_LEAVES + 1) + 1];
     u32 nb = k->n_leaves + 1;
-    ptrs[0] = pool_ptr(out_buf);
-    counts[0] = (u32)(pool_bytes(out_buf) / (k->out_dtype == DTYPE_F16 ? 2 : 4));
-    for (u32 i = 0; i < k->n_leaves; i++) {
-        void *lp = i < n_leaves ? pool_ptr(leaf_bufs[i]) : NULL;
-        ptrs[i + 1] = lp ? lp : hipb.dummy;   /* loads index an absent buffer's element 0 */
-        u64 b = lp ? pool_bytes(leaf_bufs[i]) : 0;
-        counts[i + 1] = (u32)(b / (k->leaf_dtypes[i] == DTYPE_F16 ? 2 : 4));
-    }
     for (u32 b = 0; b < nb; b++) {
         params[b] = &ptrs[b];
         params[nb + b] = &counts[b];
