@@ -818,6 +818,8 @@ static void wl_convblock(TinyHVM *ctx, u32 B, u32 C, u32 H) {
     Term rmean = zeros(ctx, SHAPE(C), 5005);
     Term rvar = gen_tensor(ctx, SHAPE(C), DTYPE_F32, TRC_GEN_CONST, 5006, 1.f, 1.f);
     u32 N = B * H * W_;
+    /* d loss / d p = 1: an input of the step, like the weights */
+    Term ones = gen_tensor(ctx, shape_of((u32[]){B, C, H / 2, W_ / 2}, 4), DTYPE_F32, TRC_GEN_CONST, 5007, 1.f, 1.f);
     rec_mark("conv.fwd");
     Shape full = shape_of((u32[]){B, C, H, W_}, 4);
     Shape cshape = shape_of((u32[]){1, C, 1, 1}, 4);
@@ -855,8 +857,7 @@ static void wl_convblock(TinyHVM *ctx, u32 B, u32 C, u32 H) {
     Term loss = realize(ctx, thvm_sum_axes(ctx, p, (u32[]){0, 1, 2, 3}, 4));
     readback(ctx, loss);
     rec_mark("conv.bwd");
-    /* d loss / d p = 1; pool + relu backward */
-    Term ones = gen_tensor(ctx, shape_of((u32[]){B, C, H / 2, W_ / 2}, 4), DTYPE_F32, TRC_GEN_CONST, 5007, 1.f, 1.f);
+    /* pool + relu backward */
     Term dya = pool_relu_bwd(ctx, ones, p, a, B, C, H, W_);
     /* batchnorm backward (gamma = g):
      *   xhat = (c - mean) * invstd, dxhat = dy * g
