@@ -14,6 +14,8 @@ A step is one replay of the engine's recorded Backend calls for a workload
   convblock  conv3x3 64->64 pad 1, batchnorm (train), relu, maxpool 2, sum
           loss, and the backward to dW and dX, x [64,64,56,56] ~ N(0,1)
           (28 kernels): TFLOP/s = the three convolutions' FLOPs / step time.
+  mlp     2-layer MLP x [64,784] -> 128 -> 10, relu, softmax cross-entropy,
+          forward and backward to dW1, dW2 (20 kernels): steps/s (latency-bound).
 
 roofline: the dominant kernel's algorithmic bytes (or FLOPs) per launch / its
 average duration, from HIP events on the backend's stream around that one
@@ -94,6 +96,18 @@ WORKLOADS = {
                           "padded convolution, so the oracle's restatement of it is timed "
                           "(1.4x slower than the engine's interpreter on the fused step)"},
     },
+    "mlp": {
+        "trace": os.path.join(WL, "mlp_64x784x128x10.trc"),
+        "step": ("mlp.fwd", None),
+        "kernels": {},
+        "unit": "steps/s", "bound": None, "dominant": None,
+        "config": {"workload": "2-layer MLP f32 forward + backward: x [64,784] ~ N(0,1), W1 [784,128], "
+                               "W2 [128,10] Kaiming-uniform, relu, softmax cross-entropy; outputs loss, "
+                               "dW1, dW2", "batch": 64, "kernels_per_step": 20},
+        "cpu": {"exe": "oracle/_ref/ref_replay", "kind": "reference",
+                "trace": os.path.join(WL, "mlp_64x784x128x10.trc"), "marks": ("mlp.fwd", "-"), "reps": 20,
+                "sample": "the full step, 20 replays (the engine's CPU backend)"},
+    },
     "convblock": {
         "trace": os.path.join(WL, "convblock_b64.trc"),
         "step": ("conv.fwd", None),
@@ -159,7 +173,7 @@ def cpu_baseline(spec, wl):
     if not os.path.exists(exe):
         print("cpu baseline: %s is not built" % spec["exe"], file=sys.stderr)
         return None
-    cmd = [exe, spec["trace"], spec["marks"][0], spec["marks"][1], "1"]
+    cmd = [exe, spec["trace"], spec["marks"][0], spec["marks"][1], str(spec.get("reps", 1))]
     if shutil.which("taskset"):
         cmd = ["taskset", "-c", "0"] + cmd
     print("cpu baseline: %s" % " ".join(cmd), file=sys.stderr, flush=True)
@@ -298,7 +312,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workloads", default="fused,matmul,lenet,convblock",
+    ap.add_argument("--workloads", default="fused,matmul,lenet,convblock,mlp",
                     help="comma list; the first one gives the headline value")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--calibrate-copy", action="store_true",

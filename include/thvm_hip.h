@@ -75,6 +75,14 @@ void thvm_hip_op_mm(u32 dst, u32 dst_dtype, u32 a, const View *a_view, u32 a_dty
                     const View *b_view, u32 b_dtype, u32 M, u32 K, u32 N);
 void thvm_hip_op_reduce(u32 uop, u32 dst, u32 dst_numel, u32 dst_dtype, u32 src, u32 src_numel,
                         u32 src_dtype, u32 reduce_dim);
+/* Backend.adam_step (src/tinyhvm.h:1033-1035), as adam_step_direct calls it
+ * (src/nn/adam.c:103-118): param, m and v updated in place over n f32
+ * elements with the arithmetic of the engine's lazy update (src/nn/adam.c:
+ * 75-88): m' = beta1*m + (1-beta1)*g, v' = beta2*v + (1-beta2)*(g*g),
+ * p' = p - lr*((m'/bc1)/(sqrt(v'/bc2)+eps)). A buffer shorter than n elements
+ * makes the call a no-op. */
+void thvm_hip_adam_step(u32 param, u32 grad, u32 m, u32 v, f32 lr, f32 beta1, f32 beta2, f32 eps, f32 bc1,
+                        f32 bc2, u32 n);
 /* Backend.profile_report / profile_reset (src/tinyhvm.h:1044-1045). */
 void thvm_hip_profile_report(void);
 void thvm_hip_profile_reset(void);

@@ -57,6 +57,9 @@
  *             reduce_dim
  *   (the OP* records are the legacy per-op slots op_unary, op_binary, op_mm,
  *   op_reduce, src/tinyhvm.h:1004-1016)
+ *   ADAM      param, grad, m, v, f32 lr, f32 beta1, f32 beta2, f32 eps,
+ *             f32 bc1, f32 bc2, n   (the adam_step slot, src/tinyhvm.h:1033-1035,
+ *             as src/nn/adam.c:103-118 calls it)
  */
 #ifndef THVM_TRACE_H
 #define THVM_TRACE_H
@@ -81,7 +84,8 @@ enum {
     TRC_OPUN = 15,
     TRC_OPBIN = 16,
     TRC_OPMM = 17,
-    TRC_OPRED = 18
+    TRC_OPRED = 18,
+    TRC_ADAM = 19
 };
 
 enum { TRC_ENC_RAW = 0, TRC_ENC_GEN = 1 };

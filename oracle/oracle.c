@@ -22,6 +22,8 @@
  *                                  src/backend/cpu/dispatch.c:23-282
  *   ora_contiguify ............... strided masked copy, src/ops/_.c:338-357
  *   ora_op_unary/binary/mm/reduce  legacy per-op slots, src/backend/cpu/ops.c:1-130
+ *   ora_adam_step ................ the adam_step slot with the lazy update's
+ *                                  arithmetic, src/nn/adam.c:75-88
  *   pool (alloc ids, reset) ...... src/backend/cpu/pool.c:6-26
  *
  * Deliberate difference from the reference: every load and store is checked
@@ -546,6 +548,34 @@ void ora_op_reduce(u32 uop, void *dst, u64 dst_bytes, u32 dst_numel, u32 dd, con
     }
 }
 
+/* ---------------- Adam ---------------- */
+
+/* The adam_step slot (src/tinyhvm.h:1033-1035) with the arithmetic of the
+ * engine's lazy update, which is what the CPU backend computes (it has no
+ * slot): every product, quotient and sum rounded to f32 in the order of the
+ * op composition of src/nn/adam.c:75-88,
+ *   m' = beta1*m + (1-beta1)*g
+ *   v' = beta2*v + (1-beta2)*(g*g)
+ *   p' = p - lr * ((m'/bc1) / (sqrt(v'/bc2) + eps))
+ * with the engine's guarded DIV (src/backend/cpu/dispatch.c:5-21). */
+void ora_adam_step(f32 *p, const f32 *g, f32 *m, f32 *v, f32 lr, f32 beta1, f32 beta2, f32 eps, f32 bc1, f32 bc2,
+                   u32 n) {
+    const f32 omb1 = 1.0f - beta1, omb2 = 1.0f - beta2;
+    for (u32 i = 0; i < n; i++) {
+        const f32 gi = g[i];
+        f32 mi = ora_alu(UOP_ADD, 0, ora_alu(UOP_MUL, 0, beta1, m[i]), ora_alu(UOP_MUL, 0, omb1, gi));
+        f32 vi = ora_alu(UOP_ADD, 0, ora_alu(UOP_MUL, 0, beta2, v[i]),
+                         ora_alu(UOP_MUL, 0, omb2, ora_alu(UOP_MUL, 0, gi, gi)));
+        f32 m_hat = ora_alu(UOP_DIV, 0, mi, bc1);
+        f32 v_hat = ora_alu(UOP_DIV, 0, vi, bc2);
+        f32 denom = ora_alu(UOP_ADD, 0, ora_alu(UOP_SQRT, 0, v_hat, 0.0f), eps);
+        f32 step = ora_alu(UOP_MUL, 0, lr, ora_alu(UOP_DIV, 0, m_hat, denom));
+        m[i] = mi;
+        v[i] = vi;
+        p[i] = ora_alu(UOP_SUB, 0, p[i], step);
+    }
+}
+
 /* ---------------- host-memory Backend ---------------- */
 static struct {
     void **bufs;
@@ -663,6 +693,12 @@ static void ob_op_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn, u32 
     ora_op_reduce(uop, ob_ptr(dst), ob_size(dst), dn, dd, ob_ptr(src), ob_size(src), sd, rdim);
 }
 
+static void ob_adam(u32 p, u32 g, u32 m, u32 v, f32 lr, f32 b1, f32 b2, f32 eps, f32 bc1, f32 bc2, u32 n) {
+    const u64 need = (u64)n * 4;
+    if (ob_size(p) < need || ob_size(g) < need || ob_size(m) < need || ob_size(v) < need) return;
+    ora_adam_step(ob_ptr(p), ob_ptr(g), ob_ptr(m), ob_ptr(v), lr, b1, b2, eps, bc1, bc2, n);
+}
+
 Backend oracle_backend = {
     .init = ob_init,
     .shutdown = ob_shutdown,
@@ -680,6 +716,7 @@ Backend oracle_backend = {
     .contiguify = ob_contig,
     .buf_copy = ob_copy,
     .pool_reset = ob_reset,
+    .adam_step = ob_adam,
 };
 
 const Backend *oracle_backend_ptr(void) { return &oracle_backend; }

@@ -411,6 +411,27 @@ static void cap_contiguify(u32 dst, u32 numel, u32 src, const View *v) {
     rec_snapshot(dst);
 }
 
+/* adam_step's golden output. The engine's CPU backend has no adam_step slot;
+ * without one the engine updates through its lazy composition
+ * (src/nn/adam.c:52-95). The adam workload runs each step that way first and
+ * keeps the engine's results; the recorded adam_step call of the same step,
+ * on copies of the same parameter and moments, then produces exactly those
+ * bytes (SNAPSHOT source 0). */
+static void rec_adam(u32 p, u32 g, u32 m, u32 v, f32 lr, f32 b1, f32 b2, f32 eps, f32 bc1, f32 bc2, u32 n,
+                     u32 p_want, u32 m_want, u32 v_want) {
+    rb_begin();
+    rb_u32(p); rb_u32(g); rb_u32(m); rb_u32(v);
+    rb_f32(lr); rb_f32(b1); rb_f32(b2); rb_f32(eps); rb_f32(bc1); rb_f32(bc2);
+    rb_u32(n);
+    rb_emit(TRC_ADAM);
+    if (!g_exec) return;
+    const u32 dst[3] = {p, m, v}, src[3] = {p_want, m_want, v_want};
+    for (int i = 0; i < 3; i++) {
+        memcpy(cpu_pool.bufs[dst[i]], cpu_pool.bufs[src[i]], (u64)n * 4);
+        rec_snapshot(dst[i]);
+    }
+}
+
 static void install_recorder(void) {
     g_orig = cpu_backend;
     cpu_backend.init = cap_init;
@@ -881,6 +902,66 @@ static void wl_convblock(TinyHVM *ctx, u32 B, u32 C, u32 H) {
     (void)dgamma; (void)dbeta;
 }
 
+/* Adam (beta1 0.9, beta2 0.999, eps 1e-8, lr 0.01) on two parameters, [1000]
+ * and [37,111] (a length that is not a multiple of 4), for two steps. Each
+ * step runs the engine's lazy update (the path it takes when the backend has
+ * no adam_step slot, src/nn/adam.c:52-95). At this engine version that update
+ * writes the moments but not the parameter (its APP-sequenced ASSIGN of the
+ * parameter does not take effect), so the parameter's update is realized on
+ * its own, with the same op composition (src/nn/adam.c:83-88) over the new
+ * moments, and assigned. The parameters and moments are then snapshotted, and
+ * the adam_step call of the same step is recorded on copies (the slot's
+ * signature, src/tinyhvm.h:1033-1035, called as adam_step_direct does,
+ * src/nn/adam.c:103-118). */
+static void wl_adam(TinyHVM *ctx) {
+    Shape shp[2] = {SHAPE(1000), SHAPE(37, 111)};
+    u32 n[2] = {1000, 37 * 111};
+    Term P[2], G[2], Pc[2], Mc[2], Vc[2];
+    for (int i = 0; i < 2; i++) {
+        P[i] = gen_tensor(ctx, shp[i], DTYPE_F32, TRC_GEN_NORMAL, 6001 + i, 0.f, 1.f);
+        G[i] = gen_tensor(ctx, shp[i], DTYPE_F32, TRC_GEN_NORMAL, 6011 + i, 0.f, 0.1f);
+        Pc[i] = gen_tensor(ctx, shp[i], DTYPE_F32, TRC_GEN_NORMAL, 6001 + i, 0.f, 1.f);
+        Mc[i] = zeros(ctx, shp[i], 6021 + i);
+        Vc[i] = zeros(ctx, shp[i], 6031 + i);
+    }
+    Adam opt = adam_init(ctx, 0.01f, 2);
+    u32 gids[2];
+    for (int i = 0; i < 2; i++) {
+        adam_add_param(ctx, &opt, (u32)i, (u32)term_val(P[i]), n[i]);
+        gids[i] = (u32)term_val(G[i]);
+    }
+#define BUF(t) (ctx->tensors[(u32)term_val(t)].buf_id)
+#define TBUF(id) (ctx->tensors[(id)].buf_id)
+    for (int st = 0; st < 2; st++) {
+        rec_mark("adam.lazy");
+        thvm_eval(ctx, adam_step_lazy(ctx, &opt, gids));
+        f32 bc1 = 1.0f - powf(opt.beta1, (f32)opt.t);
+        f32 bc2 = 1.0f - powf(opt.beta2, (f32)opt.t);
+        rec_mark("adam.param");
+        for (int i = 0; i < 2; i++) {
+            Term m = term_new(TAG_TEN, 0, opt.m_bufs[i]);
+            Term v = term_new(TAG_TEN, 0, opt.v_bufs[i]);
+            Term m_hat = binary(ctx, UOP_DIV, m, scalar_t(ctx, bc1));
+            Term v_hat = binary(ctx, UOP_DIV, v, scalar_t(ctx, bc2));
+            Term denom = binary(ctx, UOP_ADD, unary(ctx, UOP_SQRT, v_hat), scalar_t(ctx, opt.eps));
+            Term step = binary(ctx, UOP_MUL, scalar_t(ctx, opt.lr), binary(ctx, UOP_DIV, m_hat, denom));
+            Term p_new = realize_as(ctx, binary(ctx, UOP_SUB, P[i], step), shp[i]);
+            thvm_eval(ctx, thvm_assign(ctx, P[i], p_new));
+            readback(ctx, P[i]);
+            rec_snapshot(BUF(P[i]));
+            rec_snapshot(TBUF(opt.m_bufs[i]));
+            rec_snapshot(TBUF(opt.v_bufs[i]));
+        }
+        rec_mark("adam.slot");
+        for (int i = 0; i < 2; i++)
+            rec_adam(BUF(Pc[i]), BUF(G[i]), BUF(Mc[i]), BUF(Vc[i]), opt.lr, opt.beta1, opt.beta2, opt.eps, bc1,
+                     bc2, n[i], BUF(P[i]), TBUF(opt.m_bufs[i]), TBUF(opt.v_bufs[i]));
+    }
+#undef BUF
+#undef TBUF
+    adam_free(&opt);
+}
+
 /* ASSIGN from strided views, the engine's use of contiguify
  * (src/interact/tensor_ops.c:113-120): a transpose, a broadcast, a zero-padded
  * (masked) view, a 3-D permute of i32 and a transpose of f16. Each case runs
@@ -1158,6 +1239,8 @@ int main(int argc, char **argv) {
         wl_dtypes(ctx);
     } else if (strcmp(wl, "assign") == 0) {
         wl_assign(ctx);
+    } else if (strcmp(wl, "adam") == 0) {
+        wl_adam(ctx);
     } else if (strcmp(wl, "legacy") == 0) {
         wl_legacy();
     } else if (strcmp(wl, "longreduce") == 0) {

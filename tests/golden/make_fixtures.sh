@@ -32,6 +32,8 @@ $CAP dtypes dtypes.trc
 $CAP assign assign.trc
 # the legacy per-op slots (op_unary / op_binary / op_mm / op_reduce)
 $CAP legacy legacy.trc
+# the adam_step slot against the engine's lazy Adam (src/nn/adam.c)
+$CAP adam adam.trc
 # few outputs over long axes (split group reductions)
 $CAP longreduce longreduce_4x20000.trc 4 20000
 # the engine's FusedOp fallback path (lowering disabled)

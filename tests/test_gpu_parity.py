@@ -61,6 +61,8 @@ def _oracle():
     ora.ora_op_binary.argtypes = [u32, vp, u64, PV, u32, vp, u64, PV, u32, vp, u64, PV, u32]
     ora.ora_op_mm.argtypes = [vp, u64, u32, vp, u64, PV, u32, vp, u64, PV, u32, u32, u32, u32]
     ora.ora_op_reduce.argtypes = [u32, vp, u64, u32, u32, vp, u64, u32, u32]
+    f32 = C.c_float
+    ora.ora_adam_step.argtypes = [vp, vp, vp, vp, f32, f32, f32, f32, f32, f32, u32]
     return ora
 
 
@@ -266,6 +268,20 @@ def kernel_parity(backend, read_fn, sync_fn, ora, path, tol_fn=None, prefix_fn=N
                 kernel_results.append((i, ok, msg))
                 print("  %s %s %d (%s): %s" % (path.split("/")[-1], trace.TAG_NAMES[r.tag], i, kind, msg),
                       flush=True)
+            elif r.tag == trace.ADAM:
+                f = r.f
+                nb = f["n"] * 4
+                host_in = {k: np.frombuffer(bytes(host.read(f[k])[0])[:nb], dtype=np.float32).copy()
+                           for k in ("param", "grad", "m", "v")}
+                ora.ora_adam_step(*(host_in[k].ctypes.data for k in ("param", "grad", "m", "v")),
+                                  f["lr"], f["beta1"], f["beta2"], f["eps"], f["bc1"], f["bc2"], f["n"])
+                rp.run(i, i + 1)
+                for k in ("param", "m", "v"):
+                    dtype_of[f[k]] = 0
+                    got, _ = host.read(f[k])
+                    ok, msg = compare(bytes(got)[:nb], host_in[k].tobytes(), 0, "exact", 0.0)
+                    kernel_results.append((i, ok, "%s: %s" % (k, msg)))
+                    print("  %s ADAM %d %s (exact): %s" % (path.split("/")[-1], i, k, msg), flush=True)
             elif r.tag == trace.SNAPSHOT:
                 got, n = host.read(r.f["id"])
                 dt = dtype_of.get(r.f["id"], 0)

@@ -490,6 +490,43 @@ static void hb_op_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn, u32 
     legacy_launch("thvm_op_reduce", &a, dst);
 }
 
+/* adam_step (src/tinyhvm.h:1033-1035; the engine calls it from
+ * adam_step_direct, src/nn/adam.c:103-118): one fused pass, in place, with
+ * the engine's lazy-update arithmetic. Buffers shorter than n elements make
+ * the call a no-op, as a missing slot is. */
+static void hb_adam_step(u32 param, u32 grad, u32 m, u32 v, f32 lr, f32 beta1, f32 beta2, f32 eps, f32 bc1,
+                         f32 bc2, u32 n) {
+    HipbBuf *bp = pool_get(param), *bg = pool_get(grad), *bm = pool_get(m), *bv = pool_get(v);
+    const u64 need = (u64)n * 4;
+    if (!hipb.initialized || !bp || !bg || !bm || !bv || n == 0) return;
+    if (pool_bytes(param) < need || pool_bytes(grad) < need || pool_bytes(m) < need || pool_bytes(v) < need) {
+        fprintf(stderr, "tinyhvm-hip: adam_step: buffers shorter than %u elements\n", n);
+        return;
+    }
+    legacy_guard(param, grad, m);
+    copyq_guard(v);
+    pool_sync_device(param);
+    pool_sync_device(grad);
+    pool_sync_device(m);
+    pool_sync_device(v);
+    AdamArgs a;
+    memset(&a, 0, sizeof a);
+    a.p = (u64)(uintptr_t)bp->ptr; a.g = (u64)(uintptr_t)bg->ptr;
+    a.m = (u64)(uintptr_t)bm->ptr; a.v = (u64)(uintptr_t)bv->ptr;
+    a.lr = lr; a.beta1 = beta1; a.beta2 = beta2; a.eps = eps; a.bc1 = bc1; a.bc2 = bc2;
+    a.n = n;
+    a.vec = ((a.p | a.g | a.m | a.v) & 15u) == 0;
+    hipFunction_t fn = rtc_static_fn("thvm_adam");
+    if (fn) {
+        void *params[] = {&a};
+        u64 groups = ((u64)n + 3) / 4;
+        hipb_launch(fn, (u32)((groups + 255) / 256), 1, 1, 256, params);
+    }
+    pool_mark_device_write(param);
+    pool_mark_device_write(m);
+    pool_mark_device_write(v);
+}
+
 static void hb_buf_copy(u32 dst_buf, u32 src_buf, u64 nbytes) {
     HipbBuf *d = pool_get(dst_buf), *s = pool_get(src_buf);
     if (!d || !s || nbytes == 0) return;
@@ -550,7 +587,7 @@ Backend hip_backend = {
     .contiguify = hb_contiguify,
     .buf_copy = hb_buf_copy,
     .buf_read_nosync = hb_buf_read_nosync,
-    .adam_step = NULL,
+    .adam_step = hb_adam_step,
     .pool_reset = hb_pool_reset,
     .pool_set_persistent = hb_pool_set_persistent,
     .begin_batch = hb_begin_batch,
@@ -574,6 +611,10 @@ void thvm_hip_op_mm(u32 dst, u32 dd, u32 a, const View *av, u32 ad, u32 b, const
 }
 void thvm_hip_op_reduce(u32 uop, u32 dst, u32 dn, u32 dd, u32 src, u32 sn, u32 sd, u32 rdim) {
     hb_op_reduce(uop, dst, dn, dd, src, sn, sd, rdim);
+}
+void thvm_hip_adam_step(u32 param, u32 grad, u32 m, u32 v, f32 lr, f32 beta1, f32 beta2, f32 eps, f32 bc1,
+                        f32 bc2, u32 n) {
+    hb_adam_step(param, grad, m, v, lr, beta1, beta2, eps, bc1, bc2, n);
 }
 void thvm_hip_shutdown(void) { hb_shutdown(); }
 u32  thvm_hip_buf_alloc(u64 bytes) { return hb_buf_alloc(bytes); }

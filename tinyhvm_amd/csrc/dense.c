@@ -539,7 +539,16 @@ typedef struct {
 } GemmPlan;
 
 #define GEMM_THREADS 256
-#define SUM_WAVE_MIN_SPLITS 16   /* split-K sums this long use a wavefront per output */
+#define SUM_WAVE_MIN_SPLITS 16   /* split-K sums this long use a wavefront per output, */
+#define SUM_WAVE_MAX_OUTPUTS 8192 /* unless there are enough outputs for a lane each */
+
+/* Split-K sum shape: a wavefront per output for few outputs with long sums
+ * (its lanes read one output's partials, strided), else a lane per output
+ * (consecutive lanes read consecutive partials, coalesced). Both add the
+ * splits in a fixed order. */
+static int sum_per_wave(const GemmPlan *pl, u64 outputs) {
+    return pl->splits >= SUM_WAVE_MIN_SPLITS && outputs < SUM_WAVE_MAX_OUTPUTS;
+}
 
 /* f(gid) (var 0) or g(r) (var 1) part of a separable operand index */
 static void emit_sep_fn(DSB *s, const char *name, const Aff *a, u8 var) {
@@ -596,7 +605,7 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
         dsb_put(s_, "        %s(p0, c0, gid_m(m) + gid_n(n), %s + c[v]);\n", st, fb);
     dsb_put(s_, "      }\n    }\n  }\n}\n");
     if (pl->splits <= 1) return;
-    if (pl->splits >= SUM_WAVE_MIN_SPLITS) {
+    if (sum_per_wave(pl, (u64)M * N)) {
         /* many splits: one wavefront per output; lane l adds splits l, l+64, ...
          * in order, then a fixed shuffle tree (deterministic) */
         dsb_put(s_, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
@@ -615,6 +624,7 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
                     "  if (t >= %lluull) return;\n"
                     "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
                     "  float a = 0.0f;\n"
+                    "  #pragma unroll 8\n"
                     "  for (u32 s = 0; s < %uu; s++) a = a + ws[(unsigned long long)s * %lluull + t];\n"
                     "  %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
                 pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
@@ -1281,7 +1291,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     if (e->plan.splits > 1) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};
         u64 mn = (u64)e->M * e->N;
-        u64 per_block = e->plan.splits >= SUM_WAVE_MIN_SPLITS ? 4 : 256;
+        u64 per_block = sum_per_wave(&e->plan, mn) ? 4 : 256;
         if (!hipb_launch_grid(e->fn_sum, (u32)((mn + per_block - 1) / per_block), 1, 256, p2)) return 0;
     }
     return 1;

@@ -59,4 +59,12 @@ typedef struct {
     u64 dst[COPY_BATCH_MAX], src[COPY_BATCH_MAX], bytes[COPY_BATCH_MAX];
 } CopyBatch;
 
+/* adam_step (src/tinyhvm.h:1033-1035): parameter, gradient and moment
+ * buffers of n f32 each; vec = 1 when all four are 16-byte aligned. */
+typedef struct {
+    u64 p, g, m, v;
+    f32 lr, beta1, beta2, eps, bc1, bc2;
+    u32 n, vec;
+} AdamArgs;
+
 #endif

@@ -56,6 +56,9 @@ typedef struct {
     /* OPUN / OPBIN / OPMM / OPRED (id = dst, id2 = a or src, id3 = b) */
     u32 uop, id3, dd, ad, bd, mm_m, mm_k, mm_n, dn, sn, rdim;
     View *lv;              /* dst, a, b views */
+    /* ADAM (id = param, id2 = grad, id3 = m, id4 = v, n = numel) */
+    u32 id4;
+    f32 ad_lr, ad_b1, ad_b2, ad_eps, ad_bc1, ad_bc2;
     char *text;            /* MARK */
     void *gen_cache;       /* materialized GEN data */
 } TRec;
@@ -260,6 +263,12 @@ static int parse_rec(ThvmTrace *t, TRec *r, u32 tag, const u8 *p, u64 len) {
     case TRC_OPRED:
         r->uop = c_u32(&c); r->id = c_u32(&c); r->dn = c_u32(&c); r->dd = c_u32(&c);
         r->id2 = c_u32(&c); r->sn = c_u32(&c); r->ad = c_u32(&c); r->rdim = c_u32(&c);
+        break;
+    case TRC_ADAM:
+        r->id = c_u32(&c); r->id2 = c_u32(&c); r->id3 = c_u32(&c); r->id4 = c_u32(&c);
+        r->ad_lr = c_f32(&c); r->ad_b1 = c_f32(&c); r->ad_b2 = c_f32(&c); r->ad_eps = c_f32(&c);
+        r->ad_bc1 = c_f32(&c); r->ad_bc2 = c_f32(&c);
+        r->numel = c_u32(&c);
         break;
     case TRC_MARK: {
         u32 n = c_u32(&c);
@@ -500,6 +509,14 @@ int thvm_trace_replay(ThvmTrace *t, const Backend *be, u32 lo, u32 hi, u32 flags
             break;
         case TRC_OPRED:
             if (be->op_reduce) be->op_reduce(r->uop, L(t, r->id), r->dn, r->dd, L(t, r->id2), r->sn, r->ad, r->rdim);
+            dispatched++;
+            break;
+        case TRC_ADAM:
+            /* a backend without the slot leaves the buffers as they are, as
+             * the engine's adam_step_direct does (src/nn/adam.c:108) */
+            if (be->adam_step)
+                be->adam_step(L(t, r->id), L(t, r->id2), L(t, r->id3), L(t, r->id4), r->ad_lr, r->ad_b1, r->ad_b2,
+                              r->ad_eps, r->ad_bc1, r->ad_bc2, r->numel);
             dispatched++;
             break;
         case TRC_RESET:

@@ -6,6 +6,8 @@
 //                    the legacy per-op slots (src/backend/cpu/ops.c)
 //   thvm_copy_batch  several buffer-to-buffer copies in one launch
 //   thvm_fill_u32    fill a buffer with a 32-bit pattern (graph-safe clear)
+//   thvm_adam        the adam_step slot: one fused pass over parameter,
+//                    gradient and both moments
 //
 // The rs interpreter restates the engine's CPU fallback
 // (src/backend/cpu/dispatch.c:23-282): leaves are read through their view
@@ -390,4 +392,50 @@ extern "C" __global__ __launch_bounds__(256) void thvm_copy_batch(CopyBatch B) {
 extern "C" __global__ __launch_bounds__(256) void thvm_fill_u32(u32 *dst, u32 n, u32 value) {
     const u32 t = blockIdx.x * 256u + threadIdx.x;
     if (t < n) dst[t] = value;
+}
+
+// adam_step with the arithmetic of the engine's lazy update, the CPU
+// backend's result (src/nn/adam.c:75-88): each product, quotient and sum is
+// one f32 rounding in the composition's order (no contraction: the file is
+// built with -ffp-contract=off), DIV guarded as the engine's ALU guards it.
+// One pass: reads p, g, m, v and writes p, m, v (28 bytes per element);
+// each lane owns 4 consecutive elements, with 128-bit accesses when aligned.
+__device__ __forceinline__ float adam_div(float a, float b) { return b != 0.0f ? a / b : 0.0f; }
+
+__device__ __forceinline__ void adam_one(const AdamArgs &a, float &p, float g, float &m, float &v) {
+    const float mi = a.beta1 * m + (1.0f - a.beta1) * g;
+    const float vi = a.beta2 * v + (1.0f - a.beta2) * (g * g);
+    const float m_hat = adam_div(mi, a.bc1);
+    const float v_hat = adam_div(vi, a.bc2);
+    const float denom = sqrtf(v_hat) + a.eps;
+    const float step = a.lr * adam_div(m_hat, denom);
+    m = mi;
+    v = vi;
+    p = p - step;
+}
+
+extern "C" __global__ __launch_bounds__(256) void thvm_adam(AdamArgs a) {
+    float *P = (float *)(uintptr_t)a.p, *M = (float *)(uintptr_t)a.m, *V = (float *)(uintptr_t)a.v;
+    const float *G = (const float *)(uintptr_t)a.g;
+    const unsigned long long i0 = ((unsigned long long)blockIdx.x * 256u + threadIdx.x) * 4u;
+    if (i0 >= a.n) return;
+    if (a.vec && i0 + 4u <= a.n) {
+        float4 p = *(float4 *)(P + i0), m = *(float4 *)(M + i0), v = *(float4 *)(V + i0);
+        const float4 g = *(const float4 *)(G + i0);
+        adam_one(a, p.x, g.x, m.x, v.x);
+        adam_one(a, p.y, g.y, m.y, v.y);
+        adam_one(a, p.z, g.z, m.z, v.z);
+        adam_one(a, p.w, g.w, m.w, v.w);
+        *(float4 *)(P + i0) = p;
+        *(float4 *)(M + i0) = m;
+        *(float4 *)(V + i0) = v;
+        return;
+    }
+    for (unsigned long long i = i0; i < i0 + 4u && i < a.n; i++) {
+        float p = P[i], m = M[i], v = V[i];
+        adam_one(a, p, G[i], m, v);
+        P[i] = p;
+        M[i] = m;
+        V[i] = v;
+    }
 }

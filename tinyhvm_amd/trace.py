@@ -15,14 +15,14 @@ from . import abi
 
 MAGIC = b"THVMTRC1"
 (ALLOC, FREE, INCREF, DECREF, WRITE, READ, UOP, RS, COPY, CONTIG, RESET, PERSIST,
- SNAPSHOT, MARK, OPUN, OPBIN, OPMM, OPRED) = range(1, 19)
+ SNAPSHOT, MARK, OPUN, OPBIN, OPMM, OPRED, ADAM) = range(1, 20)
 LEGACY = (OPUN, OPBIN, OPMM, OPRED)
 ENC_RAW, ENC_GEN = 0, 1
 GEN_UNIFORM, GEN_NORMAL, GEN_INT, GEN_CONST = 1, 2, 3, 4
 TAG_NAMES = {ALLOC: "ALLOC", FREE: "FREE", INCREF: "INCREF", DECREF: "DECREF", WRITE: "WRITE",
              READ: "READ", UOP: "UOP", RS: "RS", COPY: "COPY", CONTIG: "CONTIG",
              RESET: "RESET", PERSIST: "PERSIST", SNAPSHOT: "SNAPSHOT", MARK: "MARK",
-             OPUN: "OPUN", OPBIN: "OPBIN", OPMM: "OPMM", OPRED: "OPRED"}
+             OPUN: "OPUN", OPBIN: "OPBIN", OPMM: "OPMM", OPRED: "OPRED", ADAM: "ADAM"}
 
 
 @dataclass
@@ -225,6 +225,11 @@ def _parse_payload(tag, p: bytes) -> dict:
     elif tag == OPRED:
         f["uop"], f["dst"], f["dn"], f["dd"] = c.u32(), c.u32(), c.u32(), c.u32()
         f["a"], f["sn"], f["ad"], f["rdim"] = c.u32(), c.u32(), c.u32(), c.u32()
+    elif tag == ADAM:
+        f["param"], f["grad"], f["m"], f["v"] = c.u32(), c.u32(), c.u32(), c.u32()
+        for k in ("lr", "beta1", "beta2", "eps", "bc1", "bc2"):
+            f[k] = c.f32()
+        f["n"] = c.u32()
     return f
 
 

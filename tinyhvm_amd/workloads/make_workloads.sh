@@ -11,6 +11,7 @@
 #   convblock_b64        conv3x3 64->64 pad 1 + batchnorm + relu + maxpool 2,
 #                        forward and backward, x [64,64,56,56]
 #   convblock_b1         the same at batch 1 (CPU-baseline sample)
+#   mlp_64x784x128x10    2-layer MLP forward + backward at batch 64
 set -e
 HERE=$(cd "$(dirname "$0")" && pwd)
 ROOT=$(cd "$HERE/../.." && pwd)
@@ -24,3 +25,4 @@ $CAP -n lenet lenet_b256.trc 256 1
 $CAP -n lenet lenet_b64.trc 64 1
 $CAP -n convblock convblock_b64.trc 64 64 56
 $CAP -n convblock convblock_b1.trc 1 64 56
+$CAP -n mlp mlp_64x784x128x10.trc 64 784 128 10
