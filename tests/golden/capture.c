@@ -962,6 +962,183 @@ static void wl_adam(TinyHVM *ctx) {
     adam_free(&opt);
 }
 
+/* The engine's own known-answer tests, restated: the same API calls on the
+ * same inputs (in one engine context rather than one per case), each case
+ * behind a "known.<case>" mark and ending in the readback its test checks. The expected values are the tests' own:
+ *   conv        [7,9,13,15]        test/archive/test_tensor_nn_layers.m:19-36
+ *   pool        4                  test/archive/test_tensor_nn_layers.m:39-50
+ *   bn_eval     y0 1, y3 4         test/archive/test_tensor_nn_layers.m:52-67
+ *   relu_linear [0,2.6,0,5.0]      test/archive/test_readme_verify.m:22-41
+ *   multiview   160                test/archive/test_lower_multiview_kernel.m:14-33
+ *   fused_reduce 165888            test/archive/test_fused_reduce.m:9-36
+ *   mul_sum     [20,86]            test/archive/test_cpu_metal_cmp.m:12-28
+ *   mm_dup      2*colsum(x)        test/test_mm_dup_2arm.m:22-47
+ *   dup_chain   5                  test/test_dup_chain.m:26-66
+ *   readme_grad [5,7,9]            README.md:127-146
+ *   dtype_*     the printed values test/archive/test_dtype_cast.m:10-61 */
+static void known_assign_eval(TinyHVM *ctx, Term dst, Term val) {
+    u64 loc = heap_alloc(ctx, 2);
+    ctx->heap[loc] = dst;
+    ctx->heap[loc + 1] = val;
+    u64 ac = heap_alloc(ctx, 1);
+    ctx->heap[ac] = term_new(TAG_TOP, UOP_ASSIGN, loc);
+    thvm_eval(ctx, term_era());
+}
+
+static void wl_known(TinyHVM *ctx) {
+    {
+        rec_mark("known.conv");
+        f32 xdat[] = {1, 2, 3, 4, 5, 6, 7, 8, 9}, wdat[] = {1, 0, 0, 1}, bdat[] = {1};
+        Tensor x = tensor_from_f32(ctx, xdat, SHAPE(1, 1, 3, 3));
+        Tensor w = tensor_from_f32(ctx, wdat, SHAPE(1, 1, 2, 2));
+        Tensor b = tensor_from_f32(ctx, bdat, SHAPE(1));
+        u32 st[] = {1, 1}, pd[] = {0, 0, 0, 0};
+        tensor_to_host_f32(tensor_realize(tensor_conv2d(x, w, &b, 1, st, pd)));
+    }
+    {
+        rec_mark("known.pool");
+        f32 xdat[] = {1, 2, 3, 4};
+        Tensor x = tensor_from_f32(ctx, xdat, SHAPE(1, 1, 2, 2));
+        thvm_set_requires_grad(ctx, x.term);
+        u32 k[] = {2, 2}, st[] = {1, 1};
+        tensor_to_host_f32(tensor_realize(tensor_maxpool2d(x, k, st)));
+    }
+    {
+        rec_mark("known.bn_eval");
+        f32 xdat[] = {1, 2, 3, 4}, gdat[] = {1}, bdat[] = {0}, mdat[] = {0}, vdat[] = {1};
+        Tensor x = tensor_from_f32(ctx, xdat, SHAPE(1, 1, 2, 2));
+        Tensor g = tensor_from_f32(ctx, gdat, SHAPE(1));
+        Tensor b = tensor_from_f32(ctx, bdat, SHAPE(1));
+        Tensor m = tensor_from_f32(ctx, mdat, SHAPE(1));
+        Tensor v = tensor_from_f32(ctx, vdat, SHAPE(1));
+        tensor_to_host_f32(tensor_realize(tensor_batchnorm(x, g, b, m, v, 1, 1, 2, 2, 0)));
+    }
+    {
+        rec_mark("known.relu_linear");
+        f32 x_d[] = {1, 2, 3, 4, 5, 6}, w_d[] = {0.1f, -0.2f, 0.3f, 0.4f, -0.5f, 0.6f}, b_d[] = {-0.1f, 0.2f};
+        Tensor x = tensor_from_f32(ctx, x_d, SHAPE(2, 3));
+        Tensor w = tensor_from_f32(ctx, w_d, SHAPE(3, 2));
+        Tensor b = tensor_from_f32(ctx, b_d, SHAPE(1, 2));
+        Linear lin = {.weight = w, .bias = b, .has_bias = 1};
+        tensor_to_host_f32(tensor_realize(tensor_relu(linear_forward(&lin, x))));
+    }
+    {
+        rec_mark("known.multiview");
+        f32 x[] = {1, 2, 3, 4, 5, 6, 7, 8, 9};
+        Term tx = thvm_tensor(ctx, x, SHAPE(1, 1, 3, 3));
+        Term pooled = thvm_pool(ctx, tx, (u32[]){2, 2}, (u32[]){1, 1}, 2);
+        Term x_rs = thvm_reshape(ctx, pooled, shape_of((u32[]){1, 1, 1, 1, 2, 2, 2, 2}, 8));
+        Term doubled = thvm_op(ctx, UOP_ADD, x_rs, x_rs);
+        Term total = thvm_sum_axes(ctx, doubled, (u32[]){0, 1, 2, 3, 4, 5, 6, 7}, 8);
+        total = thvm_reshape(ctx, total, SHAPE(1));
+        Term out = thvm_eval(ctx, total);
+        if (term_tag(out) != TAG_TEN) out = thvm_force_tensor_term(ctx, out);
+        u32 dt = DTYPE_F32;
+        Shape os = SHAPE(1);
+        free(thvm_to_host_raw(ctx, out, &dt, &os));
+    }
+    {
+        rec_mark("known.fused_reduce");
+        u32 an = 4 * 32 * 12 * 12 * 3 * 3, bn = 32 * 3 * 3;
+        f32 *ad = malloc(an * 4), *bd = malloc(bn * 4);
+        for (u32 i = 0; i < an; i++) ad[i] = 1.f;
+        for (u32 i = 0; i < bn; i++) bd[i] = 1.f;
+        Term a = thvm_tensor(ctx, ad, shape_of((u32[]){4, 1, 32, 12, 12, 1, 3, 3}, 8));
+        Term b = thvm_tensor(ctx, bd, shape_of((u32[]){1, 1, 32, 1, 1, 1, 3, 3}, 8));
+        free(ad);
+        free(bd);
+        Term summed = thvm_sum_axes(ctx, thvm_op(ctx, UOP_MUL, a, b), (u32[]){0, 3, 4}, 3);
+        Term out = thvm_reshape(ctx, summed, shape_of((u32[]){1, 1, 32, 1, 1, 1, 3, 3}, 8));
+        Term total = thvm_reshape(ctx, thvm_sum_axes(ctx, out, (u32[]){0, 1, 2, 3, 4, 5, 6, 7}, 8), SHAPE(1));
+        f32 z = 0;
+        Term dst = thvm_tensor(ctx, &z, SHAPE(1));
+        known_assign_eval(ctx, dst, total);
+        thvm_to_host(ctx, dst);
+    }
+    {
+        rec_mark("known.mul_sum");
+        f32 a[] = {1, 2, 3, 4, 5, 6}, b[] = {2, 3, 4, 5, 6, 7};
+        Term ta = thvm_tensor(ctx, a, SHAPE(2, 3));
+        Term tb = thvm_tensor(ctx, b, SHAPE(2, 3));
+        Term out = thvm_reshape(ctx, thvm_sum_axes(ctx, thvm_op(ctx, UOP_MUL, ta, tb), (u32[]){1}, 1), SHAPE(2));
+        f32 z[2] = {0};
+        Term dst = thvm_tensor(ctx, z, SHAPE(2));
+        known_assign_eval(ctx, dst, out);
+        thvm_to_host(ctx, dst);
+    }
+    {
+        rec_mark("known.mm_dup");
+        f32 xd[] = {1.0f, 0.5f, 0.1f, -1.0f}, wd[] = {0.1f, 0.2f, 0.3f, 0.05f, 0.1f, -0.2f};
+        Term x = thvm_tensor(ctx, xd, SHAPE(2, 2));
+        Term W = thvm_tensor(ctx, wd, SHAPE(2, 3));
+        thvm_set_requires_grad(ctx, W);
+        Term logits = thvm_mm(ctx, x, W);
+        Term l0, l1;
+        thvm_dup(ctx, thvm_fresh_label(ctx), logits, &l0, &l1);
+        Term loss = thvm_op(ctx, UOP_ADD, thvm_sum_axes(ctx, l0, (u32[]){0, 1}, 2),
+                            thvm_sum_axes(ctx, l1, (u32[]){0, 1}, 2));
+        thvm_to_host(ctx, thvm_eval(ctx, thvm_grad(ctx, loss, W)));
+    }
+    {
+        rec_mark("known.dup_chain");
+        f32 wd[4] = {1.0f, -2.0f, 3.5f, -0.5f};
+        Term w = thvm_tensor(ctx, wd, SHAPE(4));
+        thvm_set_requires_grad(ctx, w);
+        Term p_fwd, w1, p_grad, w2, p_sgd, w3, p_assign, w4, p_next, p_done;
+        thvm_dup(ctx, thvm_fresh_label(ctx), w, &p_fwd, &w1);
+        thvm_dup(ctx, thvm_fresh_label(ctx), w1, &p_grad, &w2);
+        thvm_dup(ctx, thvm_fresh_label(ctx), w2, &p_sgd, &w3);
+        thvm_dup(ctx, thvm_fresh_label(ctx), w3, &p_assign, &w4);
+        thvm_dup(ctx, thvm_fresh_label(ctx), w4, &p_next, &p_done);
+        Term s[5];
+        Term arms[5] = {p_fwd, p_grad, p_sgd, p_assign, p_next};
+        for (int i = 0; i < 5; i++) s[i] = thvm_sum_axes(ctx, arms[i], (u32[]){0}, 1);
+        Term loss = thvm_op(ctx, UOP_ADD, s[0],
+                            thvm_op(ctx, UOP_ADD, s[1], thvm_op(ctx, UOP_ADD, s[2], thvm_op(ctx, UOP_ADD, s[3], s[4]))));
+        thvm_spawn_detached_era(ctx, thvm_ctr(ctx, (Term[]){p_done}, 1));
+        thvm_to_host(ctx, thvm_eval(ctx, thvm_grad(ctx, loss, w)));
+    }
+    {
+        rec_mark("known.readme_grad");
+        f32 xd[] = {1, 2, 3, 4, 5, 6}, wd[] = {0.1f, 0.2f, 0.3f};
+        Tensor x = tensor_from_f32(ctx, xd, SHAPE(2, 3));
+        Tensor w = tensor_from_f32(ctx, wd, SHAPE(3));
+        thvm_set_requires_grad(ctx, w.term);
+        Tensor loss = tensor_sum_axes(tensor_relu(tensor_mul(x, w)), (u32[]){0, 1}, 2);
+        Tensor bundle = tensor_realize(tensor_backward_keep(loss, w));
+        tensor_to_host_f32(tensor_bundle_get(bundle, 0));
+    }
+    {
+        f32 xf[] = {1.9f, -2.1f, 3.0f};
+        Term x = thvm_tensor(ctx, xf, SHAPE(3));
+        rec_mark("known.dtype_cast_i32");
+        thvm_to_host_i32(ctx, thvm_cast(ctx, x, DTYPE_I32));
+        rec_mark("known.dtype_cast_f32");
+        i32 iv[] = {3, -4};
+        thvm_to_host(ctx, thvm_cast(ctx, thvm_tensor_i32(ctx, iv, SHAPE(2)), DTYPE_F32));
+        rec_mark("known.dtype_add_i32");
+        i32 aa[] = {10, -20}, bb[] = {-3, 4};
+        Term ta = thvm_tensor_i32(ctx, aa, SHAPE(2)), tb = thvm_tensor_i32(ctx, bb, SHAPE(2));
+        thvm_to_host_i32(ctx, thvm_eval(ctx, thvm_op(ctx, UOP_ADD, ta, tb)));
+        rec_mark("known.dtype_sum_i32");
+        i32 cc[] = {1, 2, 3};
+        Term tc = thvm_tensor_i32(ctx, cc, SHAPE(3));
+        thvm_to_host_i32(ctx, thvm_eval(ctx, thvm_sum_axes(ctx, tc, (u32[]){0}, 1)));
+        rec_mark("known.dtype_cast_add_i32");
+        i32 ones[] = {1, 1, 1};
+        Term tones = thvm_tensor_i32(ctx, ones, SHAPE(3));
+        thvm_to_host_i32(ctx, thvm_eval(ctx, thvm_op(ctx, UOP_ADD, thvm_cast(ctx, x, DTYPE_I32), tones)));
+        rec_mark("known.dtype_where_i32");
+        i32 condv[] = {0, 1, 0}, thenv[] = {10, 20, 30}, elsev[] = {1, 2, 3};
+        thvm_to_host_i32(ctx, thvm_where(ctx, thvm_tensor_i32(ctx, condv, SHAPE(3)),
+                                         thvm_tensor_i32(ctx, thenv, SHAPE(3)), thvm_tensor_i32(ctx, elsev, SHAPE(3))));
+        rec_mark("known.dtype_argmax");
+        i32 logitsv[] = {1, 9, 2, 8, 7, 3};
+        thvm_to_host_u32(ctx, thvm_argmax(ctx, thvm_tensor_i32(ctx, logitsv, SHAPE(2, 3)), 2, 3));
+        rec_mark("known.end");
+    }
+}
+
 /* ASSIGN from strided views, the engine's use of contiguify
  * (src/interact/tensor_ops.c:113-120): a transpose, a broadcast, a zero-padded
  * (masked) view, a 3-D permute of i32 and a transpose of f16. Each case runs
@@ -1239,6 +1416,8 @@ int main(int argc, char **argv) {
         wl_dtypes(ctx);
     } else if (strcmp(wl, "assign") == 0) {
         wl_assign(ctx);
+    } else if (strcmp(wl, "known") == 0) {
+        wl_known(ctx);
     } else if (strcmp(wl, "adam") == 0) {
         wl_adam(ctx);
     } else if (strcmp(wl, "legacy") == 0) {

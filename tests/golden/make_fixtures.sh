@@ -34,6 +34,8 @@ $CAP assign assign.trc
 $CAP legacy legacy.trc
 # the adam_step slot against the engine's lazy Adam (src/nn/adam.c)
 $CAP adam adam.trc
+# the engine's own known-answer tests, restated
+$CAP known known.trc
 # few outputs over long axes (split group reductions)
 $CAP longreduce longreduce_4x20000.trc 4 20000
 # the engine's FusedOp fallback path (lowering disabled)
