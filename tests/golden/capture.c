@@ -427,6 +427,11 @@ static void rec_adam(u32 p, u32 g, u32 m, u32 v, f32 lr, f32 b1, f32 b2, f32 eps
     if (!g_exec) return;
     const u32 dst[3] = {p, m, v}, src[3] = {p_want, m_want, v_want};
     for (int i = 0; i < 3; i++) {
+        /* only where the ids are the CPU backend's (not when the workload
+         * runs on another backend, as tests/live/engine_live.c does) */
+        if (dst[i] >= MAX_BUFS || src[i] >= MAX_BUFS || !cpu_pool.bufs[dst[i]] || !cpu_pool.bufs[src[i]] ||
+            cpu_pool.sizes[dst[i]] < (u64)n * 4 || cpu_pool.sizes[src[i]] < (u64)n * 4)
+            continue;
         memcpy(cpu_pool.bufs[dst[i]], cpu_pool.bufs[src[i]], (u64)n * 4);
         rec_snapshot(dst[i]);
     }
@@ -1374,6 +1379,7 @@ static void wl_dtypes(TinyHVM *ctx) {
     readback(ctx, seed);
 }
 
+#ifndef CAPTURE_NO_MAIN
 int main(int argc, char **argv) {
     int ai = 1;
     while (ai < argc && argv[ai][0] == '-') {
@@ -1433,3 +1439,4 @@ int main(int argc, char **argv) {
     fclose(g_out);
     return 0;
 }
+#endif /* CAPTURE_NO_MAIN */
