@@ -17,6 +17,12 @@ A step is one replay of the engine's recorded Backend calls for a workload
   mlp     2-layer MLP x [64,784] -> 128 -> 10, relu, softmax cross-entropy,
           forward and backward to dW1, dW2 (20 kernels): steps/s (latency-bound).
 
+lenet, mlp and convblock are also captured once into a HIP graph and timed as
+graph launches (one launch = one whole step): `graph_value` beside `value`
+(the replayed step). These steps keep the GPU busy, so a graph saves little:
+it is slower for the small MLP and LeNet kernels and 4 % faster for the conv
+block.
+
 roofline: the dominant kernel's algorithmic bytes (or FLOPs) per launch / its
 average duration, from HIP events on the backend's stream around that one
 dispatch; `traffic` comes from the committed rocprofv3 counter summary.
@@ -83,7 +89,7 @@ WORKLOADS = {
         "trace": os.path.join(WL, "lenet_b256.trc"),
         "step": ("lenet.step", "lenet.end"),
         "kernels": {},
-        "unit": "steps/s", "bound": None, "dominant": None,
+        "unit": "steps/s", "bound": None, "dominant": None, "graph": True,
         "config": {"workload": "LeNet-5 training step f32 (conv5x5 pad2 -> 6, relu, maxpool2, "
                                "conv5x5 -> 16, relu, maxpool2, fc 400-120-84-10, softmax CE, "
                                "backward, SGD via ASSIGN)", "batch": 256,
@@ -100,7 +106,7 @@ WORKLOADS = {
         "trace": os.path.join(WL, "mlp_64x784x128x10.trc"),
         "step": ("mlp.fwd", None),
         "kernels": {},
-        "unit": "steps/s", "bound": None, "dominant": None,
+        "unit": "steps/s", "bound": None, "dominant": None, "graph": True,
         "config": {"workload": "2-layer MLP f32 forward + backward: x [64,784] ~ N(0,1), W1 [784,128], "
                                "W2 [128,10] Kaiming-uniform, relu, softmax cross-entropy; outputs loss, "
                                "dW1, dW2", "batch": 64, "kernels_per_step": 20},
@@ -112,7 +118,7 @@ WORKLOADS = {
         "trace": os.path.join(WL, "convblock_b64.trc"),
         "step": ("conv.fwd", None),
         "kernels": {1: ("conv.fwd", FCONV), 23: ("conv.dw", FCONV), 27: ("conv.dx", FCONV)},
-        "unit": "TFLOP/s", "bound": "mfma", "dominant": "conv.fwd",
+        "unit": "TFLOP/s", "bound": "mfma", "dominant": "conv.fwd", "graph": True,
         "config": {"workload": "conv block f32 fwd+bwd: conv3x3 64->64 pad 1, batchnorm (train, "
                                "eps 1e-5), relu, maxpool 2, sum loss; backward dW and dX",
                    "batch": 64, "input": "N(0,1) [64,64,56,56]", "kernels_per_step": 28},
@@ -244,19 +250,49 @@ def run_workload(L, name, steps, warmup, want_cpu):
                 k_ms[nm] = k_ms.get(nm, 0.0) + hip.ms(ea, eb)
         k_ms = {k: v / steps for k, v in k_ms.items()}
     assert L.thvm_hip_synchronize() == 0
+    gpu_ms_eager = gpu_ms
+    # pass 3: the step captured once into a HIP graph, launched `steps` times
+    # (each launch is a whole step on the current parameters)
+    graph_s = None
+    if wl.get("graph"):
+        g = None
+        if L.thvm_hip_graph_begin() == 0:
+            L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
+            g = L.thvm_hip_graph_end()
+        if g:
+            assert L.thvm_hip_graph_launch(g) == 0
+            assert L.thvm_hip_synchronize() == 0
+            t0 = time.perf_counter()
+            hip.record(e0)
+            for _ in range(steps):
+                assert L.thvm_hip_graph_launch(g) == 0
+            hip.record(e1)
+            assert L.thvm_hip_synchronize() == 0
+            graph_s = (time.perf_counter() - t0) / steps
+            gpu_ms = hip.ms(e0, e1)
+            L.thvm_hip_graph_destroy(g)
+        else:
+            print("%s: the step could not be captured into a graph" % name, file=sys.stderr)
     L.thvm_trace_release(t, be)
     L.thvm_trace_free(t)
     L.thvm_hip_pool_reset(0)
     res = {"value": None, "unit": wl["unit"], "ms_per_step": round(step_s * 1e3, 4),
-           "gpu_ms_per_step": round(gpu_ms / steps, 4), "config": wl["config"],
+           "gpu_ms_per_step": round(gpu_ms_eager / steps, 4), "config": wl["config"],
            "kernels_ms": {k: round(v, 4) for k, v in k_ms.items()}}
+    if graph_s is not None:
+        res["graph_ms_per_step"] = round(graph_s * 1e3, 4)
+        res["graph_gpu_ms_per_step"] = round(gpu_ms / steps, 4)
     work = sum(w for _n, w in wl["kernels"].values())
     if wl["unit"] == "GB/s":
         res["value"] = round(work / step_s / 1e9, 2)
     elif wl["unit"] == "TFLOP/s":
         res["value"] = round(work / step_s / 1e12, 3)
+        if graph_s is not None:
+            res["graph_value"] = round(work / graph_s / 1e12, 3)
     else:
         res["value"] = round(1.0 / step_s, 3)
+        if graph_s is not None:
+            res["graph_value"] = round(1.0 / graph_s, 3)
     if wl["dominant"]:
         dom = wl["dominant"]
         dom_w = next(w for nm, w in wl["kernels"].values() if nm == dom)

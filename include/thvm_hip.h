@@ -88,6 +88,25 @@ void thvm_hip_profile_report(void);
 void thvm_hip_profile_reset(void);
 
 /* ---- additions with no counterpart in the engine ---- */
+/* HIP graphs of recorded work, for callers that repeat a fixed stretch of
+ * backend calls (a training step replayed from a kernel trace): the kernel
+ * trace replay of the Metal backend's JIT record/replay role
+ * (src/backend/metal/jit.m:24-631) taken one step further.
+ *   thvm_hip_graph_begin    start capturing the stream (0, or -1)
+ *   thvm_hip_graph_end      stop; the graph, or NULL when the captured calls
+ *                           included work a graph cannot repeat (a host read
+ *                           or synchronize, a write over 16 MiB, freeing
+ *                           device memory)
+ *   thvm_hip_graph_launch   run the captured work again (0, or -1)
+ *   thvm_hip_graph_destroy  release it (waits for the stream)
+ * Capture runs nothing on the device. A launch repeats the captured kernels
+ * with their captured arguments and uploads on the current contents of the
+ * buffers they touch; those buffers must stay allocated while the graph is
+ * in use. */
+int   thvm_hip_graph_begin(void);
+void *thvm_hip_graph_end(void);
+int   thvm_hip_graph_launch(void *graph);
+void  thvm_hip_graph_destroy(void *graph);
 
 /* Wait for all enqueued work; returns 0, or -1 on a device error. */
 int  thvm_hip_synchronize(void);

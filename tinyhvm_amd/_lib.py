@@ -48,6 +48,10 @@ def lib():
                                   u32, u32]),
         "thvm_hip_op_reduce": (None, [u32, u32, u32, u32, u32, u32, u32, u32]),
         "thvm_hip_adam_step": (None, [u32, u32, u32, u32, f32, f32, f32, f32, f32, f32, u32]),
+        "thvm_hip_graph_begin": (C.c_int, []),
+        "thvm_hip_graph_end": (vp, []),
+        "thvm_hip_graph_launch": (C.c_int, [vp]),
+        "thvm_hip_graph_destroy": (None, [vp]),
         "thvm_hip_buf_copy": (None, [u32, u32, u64]),
         "thvm_hip_pool_reset": (None, [u32]),
         "thvm_hip_pool_set_persistent": (None, [u32]),
@@ -91,7 +95,8 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_buf_incref", "thvm_hip_buf_decref", "thvm_hip_buf_write", "thvm_hip_buf_read",
     "thvm_hip_buf_read_nosync", "thvm_hip_dispatch_uop_kernel", "thvm_hip_dispatch_kernel_rs",
     "thvm_hip_contiguify", "thvm_hip_op_unary", "thvm_hip_op_binary", "thvm_hip_op_mm",
-    "thvm_hip_op_reduce", "thvm_hip_adam_step", "thvm_hip_buf_copy", "thvm_hip_pool_reset",
+    "thvm_hip_op_reduce", "thvm_hip_adam_step", "thvm_hip_graph_begin", "thvm_hip_graph_end",
+    "thvm_hip_graph_launch", "thvm_hip_graph_destroy", "thvm_hip_buf_copy", "thvm_hip_pool_reset",
     "thvm_hip_pool_set_persistent", "thvm_hip_profile_report", "thvm_hip_profile_reset",
     "thvm_hip_synchronize", "thvm_hip_stream", "thvm_hip_buf_device_ptr", "thvm_hip_backend",
     "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_compile_check",

@@ -171,7 +171,7 @@ int hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params)
         fprintf(stderr, "tinyhvm-hip: launch failed: %s\n", hipGetErrorString(e));
         return 0;
     }
-    if (hipb.sync_each) {
+    if (hipb.sync_each && !hipb.capturing) {
         e = hipStreamSynchronize(hipb.stream);
         if (e != hipSuccess) {
             fprintf(stderr, "tinyhvm-hip: kernel failed: %s\n", hipGetErrorString(e));
@@ -645,6 +645,7 @@ void thvm_hip_profile_reset(void) { hb_profile_reset(); }
 
 int thvm_hip_synchronize(void) {
     if (!hipb.initialized) return -1;
+    if (pool_capture_forbids("a synchronize")) return -1;
     copyq_flush();
     hipError_t e = hipStreamSynchronize(hipb.stream);
     if (e != hipSuccess) {
@@ -734,4 +735,104 @@ int thvm_hip_compile_check(const UOpKernel *k, char *errbuf, u64 errlen) {
     int ok = rtc_compile_check(k, &cl, err, sizeof err);
     if (!ok && errbuf && errlen) snprintf(errbuf, errlen, "%s", err);
     return ok ? (int)cl : -1;
+}
+
+/* ---- HIP graphs of recorded work ----
+ * A stretch of backend calls (one training step replayed from a kernel trace,
+ * say) is captured from the stream into a HIP graph and launched again as one
+ * submission. Kernels keep the arguments they were captured with (buffer
+ * pointers, inline scalars), uploads read the graph's own pinned arena, and
+ * the graph writes the same buffers at every launch, so a launch repeats the
+ * captured step on the current contents of its persistent buffers. Capture
+ * runs nothing on the device: host writes still pending are uploaded before
+ * it starts, and the host's record of what the device holds stays
+ * conservative (a buffer a captured kernel writes is read back from the
+ * device; a host write made during the capture is uploaded again for eager
+ * use). Work a graph cannot repeat (a host read, a
+ * synchronize, a large synchronous write, freeing device memory) abandons
+ * the capture: graph_end then returns NULL. No memset is ever recorded (the
+ * dispatch path clears with kernels). */
+#define GRAPH_ARENA_BYTES (4u << 20)
+
+typedef struct {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    u8 *arena;
+} HipbGraph;
+
+static HipbGraph *g_capture;
+
+int thvm_hip_graph_begin(void) {
+    if (!hipb.initialized || hipb.capturing) return -1;
+    copyq_flush();
+    /* pending host writes reach the device now, not inside the graph */
+    pool_sync_all_device();
+    HipbGraph *g = calloc(1, sizeof *g);
+    if (!g) return -1;
+    if (hipHostMalloc((void **)&g->arena, GRAPH_ARENA_BYTES, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        free(g);
+        return -1;
+    }
+    if (hipStreamBeginCapture(hipb.stream, hipStreamCaptureModeRelaxed) != hipSuccess) {
+        (void)hipGetLastError();
+        HIPB_CHECK(hipHostFree(g->arena));
+        free(g);
+        return -1;
+    }
+    pool_capture_begin(g->arena, GRAPH_ARENA_BYTES);
+    hipb.capturing = 1;
+    hipb.capture_bad = 0;
+    g_capture = g;
+    return 0;
+}
+
+void *thvm_hip_graph_end(void) {
+    if (!hipb.capturing || !g_capture) return NULL;
+    copyq_flush();
+    HipbGraph *g = g_capture;
+    g_capture = NULL;
+    hipError_t e = hipStreamEndCapture(hipb.stream, &g->graph);
+    hipb.capturing = 0;
+    pool_capture_end();
+    if (e == hipSuccess && !hipb.capture_bad && g->graph)
+        e = hipGraphInstantiate(&g->exec, g->graph, NULL, NULL, 0);
+    if (e != hipSuccess || hipb.capture_bad || !g->exec) {
+        if (e != hipSuccess) {
+            (void)hipGetLastError();
+            fprintf(stderr, "tinyhvm-hip: graph capture failed: %s\n", hipGetErrorString(e));
+        }
+        if (g->exec) HIPB_CHECK(hipGraphExecDestroy(g->exec));
+        if (g->graph) HIPB_CHECK(hipGraphDestroy(g->graph));
+        HIPB_CHECK(hipHostFree(g->arena));
+        free(g);
+        hipb.capture_bad = 0;
+        return NULL;
+    }
+    return g;
+}
+
+int thvm_hip_graph_launch(void *handle) {
+    HipbGraph *g = handle;
+    if (!hipb.initialized || hipb.capturing || !g || !g->exec) return -1;
+    copyq_flush();
+    /* host writes since the capture reach the buffers the graph reads, and
+     * the host's copies of whatever it writes are no longer current */
+    pool_device_wrote_all();
+    hipError_t e = hipGraphLaunch(g->exec, hipb.stream);
+    if (e != hipSuccess) {
+        fprintf(stderr, "tinyhvm-hip: graph launch failed: %s\n", hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+void thvm_hip_graph_destroy(void *handle) {
+    HipbGraph *g = handle;
+    if (!g) return;
+    if (hipb.initialized) HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    if (g->exec) HIPB_CHECK(hipGraphExecDestroy(g->exec));
+    if (g->graph) HIPB_CHECK(hipGraphDestroy(g->graph));
+    if (g->arena) HIPB_CHECK(hipHostFree(g->arena));
+    free(g);
 }

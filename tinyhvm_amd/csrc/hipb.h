@@ -50,11 +50,22 @@ typedef struct {
                                 6 256x64, 7 128x64 */
     u64 n_dispatch, n_compile, n_cache_hit, n_dense;
     hipModule_t static_mod;  /* precompiled kernels */
+    int capturing;           /* a graph capture is open on the stream */
+    int capture_bad;         /* the open capture met work a graph cannot replay */
 } HipbState;
 
 extern HipbState hipb;
 
 /* ---------------- pool ---------------- */
+/* While a graph is captured, host-to-device uploads stage through a pinned
+ * arena that the graph owns (a captured copy reads its source at every
+ * replay, and the staging ring is reused); anything that would synchronize
+ * the host marks the capture unusable instead. */
+void pool_sync_all_device(void);
+void pool_device_wrote_all(void);
+void pool_capture_begin(u8 *arena, u64 bytes);
+void pool_capture_end(void);
+int  pool_capture_forbids(const char *what);
 typedef struct {
     void *ptr;        /* device pointer, NULL if free */
     u64 bytes;        /* requested bytes */
@@ -65,6 +76,7 @@ typedef struct {
     u8  dev_stale;    /* the mirror has not been copied to the device yet */
     u32 mirror_bytes; /* bytes of the mirror that were written */
     void *host_mirror;
+    u32 write_capture; /* the graph capture during which the host last wrote it (0: none) */
 } HipbBuf;
 
 int   pool_init(void);

@@ -52,7 +52,36 @@ static struct {
     u8 seg_pending[STAGE_SEGMENTS];
     u32 seg;
     u64 seg_off;
+    /* graph capture: uploads go to the capturing graph's arena */
+    u8 *arena;
+    u64 arena_cap, arena_off;
+    u32 capture_seq;      /* numbers the captures; buffers record the one they were written in */
 } P;
+
+void pool_capture_begin(u8 *arena, u64 bytes) {
+    P.capture_seq++;
+    P.arena = arena;
+    P.arena_cap = bytes;
+    P.arena_off = 0;
+}
+
+void pool_capture_end(void) {
+    /* the captured uploads did not run: mirrors written during the capture
+     * are still to be copied for eager use */
+    for (u32 i = 1; i < P.count; i++) {
+        HipbBuf *b = &P.bufs[i];
+        if (b->live && b->host_valid && b->host_mirror && b->write_capture == P.capture_seq) b->dev_stale = 1;
+    }
+    P.arena = NULL;
+    P.arena_cap = P.arena_off = 0;
+}
+
+int pool_capture_forbids(const char *what) {
+    if (!hipb.capturing) return 0;
+    if (!hipb.capture_bad && hipb.verbose) fprintf(stderr, "tinyhvm-hip: graph capture abandoned: %s\n", what);
+    hipb.capture_bad = 1;
+    return 1;
+}
 
 /* Size class of a byte count: 256 B minimum, then 4 classes per octave. */
 static u32 size_class(u64 bytes, u64 *cap_out) {
@@ -82,6 +111,7 @@ static int fl_push(FreeList *f, void *p) {
 }
 
 static void release_cache(void) {
+    if (pool_capture_forbids("device memory exhausted")) return;
     HIPB_CHECK(hipStreamSynchronize(hipb.stream));
     for (u32 c = 0; c < POOL_N_CLASSES; c++) {
         for (u32 i = 0; i < P.free[c].n; i++) HIPB_CHECK(hipFree(P.free[c].ptrs[i]));
@@ -167,7 +197,7 @@ void pool_block_put(void *ptr, u64 cap) {
     u64 c2 = 0;
     u32 c = size_class(cap, &c2);
     if (fl_push(&P.free[c], ptr)) P.cached_bytes += c2;
-    else HIPB_CHECK(hipFree(ptr));
+    else if (!pool_capture_forbids("a block free")) HIPB_CHECK(hipFree(ptr));
 }
 
 /* Device scratch outside the engine's buffer ids (kernel workspaces): grown
@@ -217,7 +247,7 @@ static void release_block(HipbBuf *b) {
     u32 c = size_class(b->cap, &cap);
     if (fl_push(&P.free[c], b->ptr)) {
         P.cached_bytes += b->cap;
-    } else {
+    } else if (!pool_capture_forbids("a block free")) {
         HIPB_CHECK(hipStreamSynchronize(hipb.stream));
         HIPB_CHECK(hipFree(b->ptr));
     }
@@ -279,6 +309,9 @@ u64 pool_bytes(u32 id) {
 int pool_host_value(u32 id, u32 dtype, u32 idx, float *out) {
     HipbBuf *b = pool_get(id);
     if (!b || !b->host_valid || !b->host_mirror) return 0;
+    /* a graph keeps an inline value for good: only for contents the captured
+     * calls wrote themselves, which every launch repeats */
+    if (hipb.capturing && b->write_capture != P.capture_seq) return 0;
     u64 es = dtype == DTYPE_F16 ? 2 : 4;
     if ((u64)idx * es + es > b->bytes) { *out = 0.0f; return 1; }
     if ((u64)idx * es + es > b->mirror_bytes) return 0;
@@ -323,9 +356,33 @@ void pool_sync_device(u32 id) {
     b->dev_stale = 0;
 }
 
+/* Every pending host mirror to the device: before work that reads buffers
+ * without a dispatch naming them (a graph launch). */
+void pool_sync_all_device(void) {
+    for (u32 i = 1; i < P.count; i++)
+        if (P.bufs[i].live && P.bufs[i].dev_stale) pool_sync_device(i);
+}
+
+/* No host mirror is current any more: after work that may write any buffer
+ * without a dispatch naming it (a graph launch). Pending uploads first. */
+void pool_device_wrote_all(void) {
+    pool_sync_all_device();
+    for (u32 i = 1; i < P.count; i++)
+        if (P.bufs[i].live) P.bufs[i].host_valid = 0;
+}
+
 /* Reserve n bytes of pinned staging; waits only if the ring wraps onto a
  * segment whose copies are still in flight. */
 static u8 *stage_reserve(u64 n) {
+    if (hipb.capturing) {
+        u64 need = (n + 255) & ~255ull;
+        if (P.arena && P.arena_off + need <= P.arena_cap) {
+            u8 *p = P.arena + P.arena_off;
+            P.arena_off += need;
+            return p;
+        }
+        pool_capture_forbids("uploads beyond the graph's staging arena");
+    }
     if (P.seg_off + n > STAGE_SEG_BYTES) {
         HIPB_CHECK(hipEventRecord(P.seg_done[P.seg], hipb.stream));
         P.seg_pending[P.seg] = 1;
@@ -344,6 +401,7 @@ static u8 *stage_reserve(u64 n) {
 void pool_write(u32 id, const void *data, u64 bytes) {
     HipbBuf *b = pool_get(id);
     if (!b || !data || bytes == 0) return;
+    b->write_capture = hipb.capturing ? P.capture_seq : 0;
     if (bytes > b->cap) {
         fprintf(stderr, "tinyhvm-hip: buf_write of %llu bytes into buffer %u of %llu bytes; truncated\n",
                 (unsigned long long)bytes, id, (unsigned long long)b->cap);
@@ -368,7 +426,7 @@ void pool_write(u32 id, const void *data, u64 bytes) {
         u8 *s = stage_reserve(bytes);
         memcpy(s, data, bytes);
         HIPB_CHECK(hipMemcpyAsync(b->ptr, s, bytes, hipMemcpyHostToDevice, hipb.stream));
-    } else {
+    } else if (!pool_capture_forbids("a write larger than the staging segment")) {
         HIPB_CHECK(hipMemcpyAsync(b->ptr, data, bytes, hipMemcpyHostToDevice, hipb.stream));
         HIPB_CHECK(hipStreamSynchronize(hipb.stream));
     }
@@ -382,7 +440,7 @@ void pool_upload(void *dst, const void *src, u64 bytes) {
         u8 *s = stage_reserve(bytes);
         memcpy(s, src, bytes);
         HIPB_CHECK(hipMemcpyAsync(dst, s, bytes, hipMemcpyHostToDevice, hipb.stream));
-    } else {
+    } else if (!pool_capture_forbids("an upload larger than the staging segment")) {
         HIPB_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, hipb.stream));
         HIPB_CHECK(hipStreamSynchronize(hipb.stream));
     }
@@ -400,6 +458,8 @@ void pool_read(u32 id, void *out, u64 bytes, int nosync) {
     if (b->host_valid && n <= b->mirror_bytes) {
         /* no device write since the host wrote it: the mirror is current */
         memcpy(out, b->host_mirror, n);
+    } else if (pool_capture_forbids("a read back to the host")) {
+        memset(out, 0, n);
     } else if (n <= STAGE_SEG_BYTES) {
         pool_sync_device(id);
         u8 *s = stage_reserve(n);
