@@ -81,11 +81,12 @@ static void read_dense_env(void) {
     hipb.dense_force = env_flag("THVM_HIP_DENSE_FORCE");
     hipb.dense_nosep = env_flag("THVM_HIP_DENSE_NOSEP");
     hipb.dense_nokperm = env_flag("THVM_HIP_DENSE_NOKPERM");
+    hipb.dense_novec = env_flag("THVM_HIP_DENSE_NOVEC");
     const char *e = getenv("THVM_HIP_DENSE_SPLITS");
     hipb.dense_splits = e ? (u32)atoi(e) : 0;
     e = getenv("THVM_HIP_GEMM_PAD");
-    hipb.gemm_pad_k = e ? (u32)atoi(e) : 4;
-    if (hipb.gemm_pad_k > 8) hipb.gemm_pad_k = 4;
+    hipb.gemm_pad_k = e ? (u32)atoi(e) : 1;
+    if (hipb.gemm_pad_k > 8) hipb.gemm_pad_k = 1;
     e = getenv("THVM_HIP_GEMM_BK");
     hipb.gemm_bk = e ? (u32)atoi(e) : 0;
     if (hipb.gemm_bk != 16 && hipb.gemm_bk != 32) hipb.gemm_bk = 0;

@@ -526,6 +526,7 @@ typedef struct {
     u32 buf[2];                  /* the buffer each side loads (1 + leaf) */
     int lin[2];                  /* tile rows map to offsets linearly (no digit carry inside a tile) */
     u32 lcoef[2];                /* the row coefficient of a linear side */
+    int vec[2];                  /* a linear side loaded 4 contiguous, 16-byte aligned elements per lane */
 } KPerm;
 
 typedef struct {
@@ -733,6 +734,18 @@ static void emit_kbase_fn(DSB *s, const KPerm *kp, int side) {
     dsb_put(s, "  return u;\n}\n");
 }
 
+/* Lane map of a 16-byte loader: each lane holds 4 contiguous elements, along
+ * k (k-major) or along the tile's rows; e counts the lane's groups of 4. */
+static void emit_map4(DSB *s, int kmajor, u32 bx, u32 bk, const char *xname) {
+    if (kmajor) {
+        const u32 g = bk / 4u;
+        dsb_put(s, "const u32 kk = (tid %% %uu) * 4u, %s = tid / %uu + %uu * e;", g, xname, g, GEMM_THREADS / g);
+    } else {
+        const u32 h = bx / 4u;
+        dsb_put(s, "const u32 %s = (tid %% %uu) * 4u, kk = tid / %uu + %uu * e;", xname, h, h, GEMM_THREADS / h);
+    }
+}
+
 /* K-reordered loaders (see KPerm): per-lane offsets once per tile, then one
  * uniform base per stage and an unchecked load per element. Rows past the
  * end of M (N) are clamped to the last row; their products are never stored. */
@@ -754,6 +767,19 @@ static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl
                        "    o%c[e] = rowb_%c(gid_%c(x < %uu ? x : %uu)) + kk * %uu; }\n",
                     side ? "n0" : "m0", xn, X, S, side ? 'n' : 'm', side ? ct->N : ct->M,
                     (side ? ct->N : ct->M) - 1, kp->icoef[side]);
+        }
+        if (kp->vec[side]) {
+            dsb_put(s, "  auto load%c = [&](u32 k0) {\n"
+                       "    const float* ps = (const float*)p%u + kbase_%c(k0);\n"
+                       "    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
+                    X, ct->sep_buf[side], S, EX[side] / 4u);
+            emit_map4(s, kmaj, bx, cf->bk, xn);
+            dsb_put(s, "\n      const float4 v = *(const float4*)(ps + o%c + %s * %uu + kk * %uu);\n"
+                       "      r%c[4u * e] = v.x; r%c[4u * e + 1u] = v.y; r%c[4u * e + 2u] = v.z; r%c[4u * e + 3u] = v.w; }\n"
+                       "  };\n",
+                    X, xn, kp->lcoef[side], kp->icoef[side], side ? 'b' : 'a', side ? 'b' : 'a', side ? 'b' : 'a',
+                    side ? 'b' : 'a');
+            continue;
         }
         dsb_put(s, "  auto load%c = [&](u32 k0) {\n"
                    "    const float* ps = (const float*)p%u + kbase_%c(k0);\n"
@@ -822,8 +848,8 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
             cf->bm, cf->bn, BK, pl->pad_a, pl->pad_b, M, N, K, pl->tiles_m, pl->tiles_n, tiles, pl->kchunk,
             cf->wm_b * 32, cf->wn_b * 32, cf->gn);
     dsb_put(&s,
-            "  __shared__ float As[2][BK * LDA];\n"
-            "  __shared__ float Bs[2][BK * LDB];\n"
+            "  __shared__ __attribute__((aligned(16))) float As[2][BK * LDA];\n"
+            "  __shared__ __attribute__((aligned(16))) float Bs[2][BK * LDB];\n"
             "  const u32 tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;\n"
             "  /* XCD-aware tile order: workgroups go round-robin over 8 XCDs; give\n"
             "   * each XCD a compact block of tiles so their operand panels share L2 */\n"
@@ -886,12 +912,28 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
     dsb_put(&s, "      rb[e] = __uint_as_float(__float_as_uint(v) & ((%s && %s) ? 0xFFFFFFFFu : 0u)); }\n  };\n", gn,
             gk);
     }
-    dsb_put(&s, "  auto storeA = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
-    emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
-    dsb_put(&s, " As[buf][kk * LDA + mm] = ra[e]; }\n  };\n");
-    dsb_put(&s, "  auto storeB = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EB);
-    emit_map(&s, ct->q_kmajor, cf->bn, cf->bk, "nn");
-    dsb_put(&s, " Bs[buf][kk * LDB + nn] = rb[e]; }\n  };\n");
+    for (int side = 0; side < 2; side++) {
+        const char X = side ? 'B' : 'A', r = side ? 'b' : 'a';
+        const char *xn = side ? "nn" : "mm", *ld = side ? "LDB" : "LDA";
+        const int kmaj = side ? ct->q_kmajor : ct->p_kmajor;
+        const u32 bx = side ? cf->bn : cf->bm, ex = side ? EB : EA;
+        if (pl->kp.on && pl->kp.vec[side]) {
+            dsb_put(&s, "  auto store%c = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", X,
+                    ex / 4u);
+            emit_map4(&s, kmaj, bx, cf->bk, xn);
+            if (kmaj)
+                dsb_put(&s, "\n      #pragma unroll\n      for (u32 j = 0; j < 4u; j++) %cs[buf][(kk + j) * %s + %s] = r%c[4u * e + j]; }\n  };\n",
+                        X, ld, xn, r);
+            else
+                dsb_put(&s, "\n      *(float4*)&%cs[buf][kk * %s + %s] = make_float4(r%c[4u * e], r%c[4u * e + 1u], "
+                            "r%c[4u * e + 2u], r%c[4u * e + 3u]); }\n  };\n",
+                        X, ld, xn, r, r, r, r);
+            continue;
+        }
+        dsb_put(&s, "  auto store%c = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", X, ex);
+        emit_map(&s, kmaj, bx, cf->bk, xn);
+        dsb_put(&s, " %cs[buf][kk * %s + %s] = r%c[e]; }\n  };\n", X, ld, xn, r);
+    }
     dsb_put(&s,
             "  f32x16 acc[%u];\n"
             "  #pragma unroll\n  for (u32 b = 0; b < %uu; b++) acc[b] = (f32x16){0};\n"
@@ -1140,6 +1182,25 @@ static int plan_kperm(const Contraction *ct, GemmPlan *pl) {
         kp->lin[s] = ok;
         kp->lcoef[s] = lc;
     }
+    /* 16-byte loads: a linear side whose lanes run along a unit-stride
+     * dimension, with every other coefficient and the constant a multiple of
+     * 4, reads 4 contiguous elements from a 16-byte aligned address (buffers
+     * start 256-byte aligned) */
+    for (int s = 0; s < 2 && !hipb.dense_novec; s++) {
+        if (!kp->lin[s]) continue;
+        const int kmaj = s ? ct->q_kmajor : ct->p_kmajor;
+        const u32 unit = kmaj ? kp->icoef[s] : kp->lcoef[s];
+        const u32 other = kmaj ? kp->lcoef[s] : kp->icoef[s];
+        const u32 nx = s ? ct->nq : ct->np;
+        const u32 fdiv = s ? ct->qdiv[nx - 1] : ct->pdiv[nx - 1];
+        const Aff *a = &ct->sep_aff[s];
+        const u32 per_lane = (s ? cf->bn : cf->bm) * cf->bk / GEMM_THREADS;
+        int ok = unit == 1 && other % 4 == 0 && a->cst % 4 == 0 && kp->E % 4 == 0 && per_lane % 4 == 0;
+        for (u32 t = 0; t < kp->ndig; t++) ok = ok && kp->ocoef[s][t] % 4 == 0;
+        for (u32 t = 0; t < a->n; t++)
+            if (a->d[t].var == 0 && a->d[t].div != fdiv) ok = ok && a->coef[t] % 4 == 0;
+        kp->vec[s] = ok;
+    }
     /* the big tile keeps no per-lane offset arrays (registers) */
     if (cf->bm == 128 && !(kp->lin[0] && kp->lin[1])) {
         memset(kp, 0, sizeof *kp);
@@ -1154,8 +1215,10 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
                                        &CFG_C64S};
     memset(pl, 0, sizeof *pl);
     pl->cfg = hipb.dense_tile ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
-    /* LDS padding: a k-major operand is stored with 16 lanes along k, i.e.
-     * at row stride LDA; an odd stride puts those lanes in distinct banks */
+    /* LDS padding: a k-major operand is stored with its lanes along k, i.e.
+     * at row stride LDA; an odd stride puts those lanes in distinct banks
+     * (1 float: 4096^3 GEMM with 16-byte loads 1.02-1.04 ms per GEMM,
+     * against 1.03-1.09 with 4) */
     pl->pad_a = ct->p_kmajor ? hipb.gemm_pad_k : 4;
     pl->pad_b = ct->q_kmajor ? hipb.gemm_pad_k : 4;
     if (!pl->cfg.direct && hipb.gemm_bk) pl->cfg.bk = hipb.gemm_bk;
@@ -1213,10 +1276,13 @@ char *dense_source(const UOpKernel *k) {
 }
 
 /* The unchecked loads of a K-reordered plan stay inside the buffers they
- * read: every index a side can form is below that buffer's element count. */
-static int kperm_fits(const KPerm *kp, const u32 *counts) {
-    for (int s = 0; s < 2; s++)
+ * read: every index a side can form is below that buffer's element count,
+ * and 16-byte loads start from 16-byte aligned buffers. */
+static int kperm_fits(const KPerm *kp, const u32 *counts, void *const *ptrs) {
+    for (int s = 0; s < 2; s++) {
         if (kp->maxidx[s] >= counts[kp->buf[s]]) return 0;
+        if (kp->vec[s] && ((uintptr_t)ptrs[kp->buf[s]] & 15u)) return 0;
+    }
     return 1;
 }
 
@@ -1242,7 +1308,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         u32 M, N, K, sp;
         if (!dense_analyze(k, &M, &N, &K, &sp) || !recognize(k, &ct)) return 0;
         make_plan(&ct, &e->plan, uop_signature(k));
-        if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts)) memset(&e->plan.kp, 0, sizeof e->plan.kp);
+        if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts, ptrs)) memset(&e->plan.kp, 0, sizeof e->plan.kp);
         char err[256] = {0};
         char *src = gen_gemm_source(k, &ct, &e->plan, err, sizeof err);
         if (!src) {
@@ -1271,7 +1337,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     }
     if (!e->is_dense) return 0;
     /* buffers smaller than the plan was made for: the generated kernels */
-    if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts)) return 0;
+    if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts, ptrs)) return 0;
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     /* split-K workspace */
     float *ws = NULL;

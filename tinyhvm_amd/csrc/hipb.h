@@ -46,6 +46,7 @@ typedef struct {
     u32 gemm_bk;             /* THVM_HIP_GEMM_BK: K per stage of the LDS tiles (0: the tile's own) */
     int dense_nosep;         /* THVM_HIP_DENSE_NOSEP: evaluate every operand through its program */
     int dense_nokperm;       /* THVM_HIP_DENSE_NOKPERM: no K-reordered affine loaders */
+    int dense_novec;         /* THVM_HIP_DENSE_NOVEC: no 16-byte operand loads */
     u32 dense_tile;          /* THVM_HIP_DENSE_TILE: 0 chosen, 1 128x128, 2 64x64, 3 256x32, 4 32x256, 5 direct,
                                 6 256x64, 7 128x64 */
     u64 n_dispatch, n_compile, n_cache_hit, n_dense;
