@@ -85,8 +85,8 @@ static void read_dense_env(void) {
     const char *e = getenv("THVM_HIP_DENSE_SPLITS");
     hipb.dense_splits = e ? (u32)atoi(e) : 0;
     e = getenv("THVM_HIP_GEMM_PAD");
-    hipb.gemm_pad_k = e ? (u32)atoi(e) : 1;
-    if (hipb.gemm_pad_k > 8) hipb.gemm_pad_k = 1;
+    hipb.gemm_pad_k = e ? (u32)atoi(e) : 0;
+    hipb.gemm_pad_k_set = e && hipb.gemm_pad_k <= 8;
     e = getenv("THVM_HIP_GEMM_BK");
     hipb.gemm_bk = e ? (u32)atoi(e) : 0;
     if (hipb.gemm_bk != 16 && hipb.gemm_bk != 32) hipb.gemm_bk = 0;

@@ -1210,17 +1210,35 @@ static int plan_kperm(const Contraction *ct, GemmPlan *pl) {
     return 1;
 }
 
+/* LDS row padding (floats). A k-major operand is stored with its lanes along
+ * k, so each store spreads over LDS rows; 32 four-byte banks serve a half
+ * wavefront at a time. 4-byte stores put 16 lanes on consecutive k and 2
+ * rows per half wavefront: a row stride of 2 mod 32 keeps all 32 in distinct
+ * banks. 16-byte loaders store 4 k-rows per lane with 8 lane groups along k
+ * and 4 rows per half wavefront: a stride of 1 mod 32. Operands stored along
+ * their rows are conflict-free at any stride; 4 keeps 16-byte alignment.
+ * (Measured: the 16-byte 4096^3 GEMM 2-6 % faster with 1 than 4; the
+ * 64-channel convolutions lost a third of their LDS cycles to conflicts with
+ * the wrong stride.) THVM_HIP_GEMM_PAD overrides the k-major padding. */
+static void plan_pads(const Contraction *ct, GemmPlan *pl) {
+    for (int s = 0; s < 2; s++) {
+        const int kmaj = s ? ct->q_kmajor : ct->p_kmajor;
+        const u32 bx = s ? pl->cfg.bn : pl->cfg.bm;
+        u32 pad = 4;
+        if (kmaj) {
+            const u32 want = pl->kp.on && pl->kp.vec[s] ? 1u : 2u;
+            pad = hipb.gemm_pad_k_set ? hipb.gemm_pad_k : (want + 32u - bx % 32u) % 32u;
+        }
+        if (s) pl->pad_b = pad;
+        else pl->pad_a = pad;
+    }
+}
+
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     static const TileCfg *forced[8] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
                                        &CFG_C64S};
     memset(pl, 0, sizeof *pl);
     pl->cfg = hipb.dense_tile ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
-    /* LDS padding: a k-major operand is stored with its lanes along k, i.e.
-     * at row stride LDA; an odd stride puts those lanes in distinct banks
-     * (1 float: 4096^3 GEMM with 16-byte loads 1.02-1.04 ms per GEMM,
-     * against 1.03-1.09 with 4) */
-    pl->pad_a = ct->p_kmajor ? hipb.gemm_pad_k : 4;
-    pl->pad_b = ct->q_kmajor ? hipb.gemm_pad_k : 4;
     if (!pl->cfg.direct && hipb.gemm_bk) pl->cfg.bk = hipb.gemm_bk;
     pl->tiles_m = (ct->M + pl->cfg.bm - 1) / pl->cfg.bm;
     pl->tiles_n = (ct->N + pl->cfg.bn - 1) / pl->cfg.bn;
@@ -1241,6 +1259,7 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     pl->splits = (ct->K + kch - 1) / kch;
     snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));
     plan_kperm(ct, pl);
+    plan_pads(ct, pl);
 }
 
 /* Contraction analysis without a device: returns 1 and fills M/N/K when the
@@ -1308,7 +1327,10 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         u32 M, N, K, sp;
         if (!dense_analyze(k, &M, &N, &K, &sp) || !recognize(k, &ct)) return 0;
         make_plan(&ct, &e->plan, uop_signature(k));
-        if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts, ptrs)) memset(&e->plan.kp, 0, sizeof e->plan.kp);
+        if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts, ptrs)) {
+            memset(&e->plan.kp, 0, sizeof e->plan.kp);
+            plan_pads(&ct, &e->plan);
+        }
         char err[256] = {0};
         char *src = gen_gemm_source(k, &ct, &e->plan, err, sizeof err);
         if (!src) {

@@ -43,6 +43,7 @@ typedef struct {
     void *dummy;             /* 256 zero bytes: the pointer argument of an absent buffer */
     u64 dummy_cap;
     u32 gemm_pad_k;          /* THVM_HIP_GEMM_PAD: LDS row padding for k-major operand stages */
+    int gemm_pad_k_set;      /* ... when set (else chosen per store layout) */
     u32 gemm_bk;             /* THVM_HIP_GEMM_BK: K per stage of the LDS tiles (0: the tile's own) */
     int dense_nosep;         /* THVM_HIP_DENSE_NOSEP: evaluate every operand through its program */
     int dense_nokperm;       /* THVM_HIP_DENSE_NOKPERM: no K-reordered affine loaders */
