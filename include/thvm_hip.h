@@ -121,6 +121,13 @@ int  thvm_hip_abi_sizes(u32 *out, u32 n);
 /* Generated HIP source for a kernel (no device needed). Returns its length,
  * or -1 with the reason in buf. mode: 0 serial, 1 group; vec: lanes per thread. */
 int  thvm_hip_kernel_source(const UOpKernel *kernel, char *buf, u64 buflen, u32 *mode, u32 *vec);
+/* The generator's vector-lane classification of a kernel's ops (no device
+ * needed), 7 words per op: kind (0 the same on every lane of a thread-vector,
+ * 1 lane v = lane 0 + off[v], 2 varying, 3 float valued), off[0..3], a divisor
+ * of the lane-0 value (0: that value is 0) and an upper bound of the value.
+ * Returns the number of ops, or -1. A diagnostic with no counterpart in the
+ * reference: it lets tests check the index analysis against the op semantics. */
+int  thvm_hip_kernel_lanes(const UOpKernel *kernel, u32 *lanes, u32 n_words, u32 *mode, u32 *vec);
 /* Generate and compile with hipRTC for gfx950, without loading (no device
  * needed). Returns the code-object size, or -1 with the reason in errbuf. */
 int  thvm_hip_compile_check(const UOpKernel *kernel, char *errbuf, u64 errlen);

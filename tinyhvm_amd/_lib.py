@@ -63,6 +63,7 @@ def lib():
         "thvm_hip_backend": (C.POINTER(abi.Backend), []),
         "thvm_hip_abi_sizes": (C.c_int, [PU32, u32]),
         "thvm_hip_kernel_source": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64, PU32, PU32]),
+        "thvm_hip_kernel_lanes": (C.c_int, [C.POINTER(abi.UOpKernel), PU32, u32, PU32, PU32]),
         "thvm_hip_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
         "thvm_hip_dense_analyze": (C.c_int, [C.POINTER(abi.UOpKernel), PU32, PU32, PU32, PU32]),
         "thvm_hip_dense_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
@@ -99,7 +100,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_graph_launch", "thvm_hip_graph_destroy", "thvm_hip_buf_copy", "thvm_hip_pool_reset",
     "thvm_hip_pool_set_persistent", "thvm_hip_profile_report", "thvm_hip_profile_reset",
     "thvm_hip_synchronize", "thvm_hip_stream", "thvm_hip_buf_device_ptr", "thvm_hip_backend",
-    "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_compile_check",
+    "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_kernel_lanes", "thvm_hip_compile_check",
     "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
@@ -155,3 +156,16 @@ def compile_check(k: abi.UOpKernel):
     if n < 0:
         raise RuntimeError(err.value.decode())
     return n
+
+
+def kernel_lanes(k: abi.UOpKernel):
+    """The generator's vector-lane classification: (mode, vec, rows), one row
+    per op (kind, off0..off3, divisor, bound); see thvm_hip_kernel_lanes."""
+    n = 7 * max(int(k.n_ops), 1)
+    buf = (C.c_uint32 * n)()
+    mode, vec = C.c_uint32(), C.c_uint32()
+    r = lib().thvm_hip_kernel_lanes(C.byref(k), buf, n, C.byref(mode), C.byref(vec))
+    if r < 0:
+        raise ValueError("kernel generation failed")
+    rows = [tuple(buf[7 * i:7 * i + 7]) for i in range(r)]
+    return mode.value, vec.value, rows

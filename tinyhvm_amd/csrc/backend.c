@@ -686,6 +686,17 @@ int thvm_hip_kernel_source(const UOpKernel *k, char *buf, u64 buflen, u32 *mode,
     return (int)n;
 }
 
+int thvm_hip_kernel_lanes(const UOpKernel *k, u32 *lanes, u32 n_words, u32 *mode, u32 *vec) {
+    char err[256] = {0};
+    KGenResult g;
+    if (!k || !lanes || n_words < 7u * k->n_ops) return -1;
+    if (!kgen_uop_lanes(k, &g, lanes, err, sizeof err)) return -1;
+    if (mode) *mode = (u32)g.mode;
+    if (vec) *vec = g.vec;
+    kgen_free(&g);
+    return (int)k->n_ops;
+}
+
 int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t errlen);
 
 /* The device-free entry points read the routing and tuning knobs once, as

@@ -125,6 +125,10 @@ typedef struct {
 } KGenResult;
 
 int  kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen);
+/* As kgen_uop; lanes (7 words per op, if not NULL) receives the vector-lane
+ * classification: kind (0 invariant, 1 lane-offset, 2 varying, 3 float),
+ * off[4], the divisor of the lane-0 value (0: the value is 0) and the bound. */
+int  kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, size_t errlen);
 void kgen_free(KGenResult *r);
 int  kgen_validate(const UOpKernel *k, char *err, size_t errlen);
 const char *kgen_prelude(void);

@@ -26,10 +26,16 @@
  *           with wavefront shuffles and LDS. SUM order differs from the CPU.
  *
  * Vectorization: inside the vector variable's scope (gid in SERIAL, the loop
- * counter in GROUP) each u32 op is classified as invariant (INV), linear
- * (value at lane v = base + v*step, with a known power-of-two alignment of
- * base) or varying. Loads whose index is linear with step 1 and aligned to 4
- * become one 128-bit load; linear step-1 stores become one 128-bit store.
+ * counter in GROUP) each u32 op is classified as invariant (INV), lane-offset
+ * (LIN: value at lane v = value at lane 0 + off[v], the offsets known when the
+ * kernel is generated) or varying. Lane-offset ops are computed once per
+ * thread-vector. The classification tracks a known divisor of the lane-0 value
+ * and an upper bound of the value over every lane: dividing or reducing a
+ * lane-offset value by d keeps it lane-offset when d divides the divisor, or
+ * when every offset is below gcd(divisor, d) (the lanes then share the
+ * quotient), as long as the bound proves the u32 arithmetic never wrapped.
+ * Loads whose offsets are 0,1,2,3 on a lane-0 index divisible by 4 become one
+ * 128-bit load (stores likewise); lanes with equal offsets share one load.
  * In GROUP mode, loads whose index is affine in the loop counter over the
  * whole loop are range-checked once per workgroup and then loaded unchecked.
  */
@@ -70,8 +76,9 @@ enum { G_INV = 0, G_LIN = 1, G_NOT = 2 };
 typedef struct {
     u8  ft;        /* float valued */
     u8  kind;      /* K_* w.r.t. the vector variable */
-    u32 step;      /* K_LIN: value(v) = value(0) + v*step */
-    u32 align;     /* power of two dividing value(0); 0 means "value is 0" */
+    u32 off[4];    /* K_LIN: value(v) = value(0) + off[v] (off[0] = 0) */
+    u32 dv;        /* a divisor of value(0); 0 means "value(0) is 0" */
+    u64 hi;        /* upper bound of the u32 value over every lane and thread */
     u8  gk;        /* G_* w.r.t. the enclosing parallel loop counter */
     u32 gs;        /* G_LIN slope */
     u8  pure;      /* value equals the parallel loop counter */
@@ -96,6 +103,8 @@ typedef struct {
     u32 per_thread;    /* SERIAL: thread-vectors per thread */
     u32 ew_block;      /* SERIAL: workgroup size (0: chosen by size) */
     u32 red_block;     /* GROUP: largest workgroup size */
+    u32 split_target;  /* split GROUP: workgroups to aim for (outputs x splits) */
+    u32 split_max;     /* split GROUP: most workgroups per output */
     u32 splits;        /* GROUP: workgroups per output (1: whole loop in one) */
     u32 split_acc;     /* GROUP split: the accumulator op */
     i32 *scal;         /* per op: index into the inline scalar list, or -1 */
@@ -121,20 +130,21 @@ static int alu_is_unary(u32 uop) {
            uop == UOP_CAST || uop == UOP_SQRT;
 }
 
-static u32 pow2_of(u32 x) {
-    if (x == 0) return 0; /* zero: divisible by anything */
-    return x & (~x + 1u);
+static u32 gcd_u32(u32 a, u32 b) {
+    while (b) { u32 t = a % b; a = b; b = t; }
+    return a;
 }
-static u32 align_min(u32 a, u32 b) {
+/* divisor facts: 0 stands for "the value is 0" (divisible by anything) */
+static u32 dv_gcd(u32 a, u32 b) {
     if (a == 0) return b;
     if (b == 0) return a;
-    return a < b ? a : b;
+    return gcd_u32(a, b);
 }
-static u32 align_mul(u32 a, u32 s) {
-    /* alignment of (value * s) where value is divisible by a */
-    if (s == 0 || a == 0) return 0;
-    u64 r = (u64)a * (u64)pow2_of(s);
-    return r >= (1ull << 31) ? (1u << 31) : (u32)r;
+static u32 dv_mul(u32 a, u32 s) {
+    /* a divisor of value*s where a divides value (no wrap: checked by the caller) */
+    if (a == 0 || s == 0) return 0;
+    u64 r = (u64)a * (u64)s;
+    return r > 0xFFFFFFFFull ? (a > s ? a : s) : (u32)r;
 }
 
 int kgen_validate(const UOpKernel *k, char *err, size_t errlen) {
@@ -263,82 +273,119 @@ static int group_ok(Gen *g, char *why, size_t wlen) {
 /* Vector classification. In SERIAL mode the vector variable is the gid; in
  * GROUP mode it is the counter of the enclosing top-level loop, and ops
  * outside top-level loops are uniform. */
+static int lin_zero(const u32 *off, u32 V) {
+    for (u32 v = 0; v < V; v++) if (off[v]) return 0;
+    return 1;
+}
+static u32 lin_max(const u32 *off, u32 V) {
+    u32 m = 0;
+    for (u32 v = 0; v < V; v++) if (off[v] > m) m = off[v];
+    return m;
+}
+/* 0,1,2,3 on a lane-0 value divisible by 4: one 128-bit access */
+static int lin_unit4(const OpI *o, u32 V) {
+    if (V != 4 || o->ft || o->kind != K_LIN || (o->dv != 0 && o->dv % 4 != 0)) return 0;
+    for (u32 v = 0; v < 4; v++) if (o->off[v] != v) return 0;
+    return 1;
+}
+
 static void analyze_vector(Gen *g) {
     const UOpKernel *k = g->k;
     u32 V = g->V;
+    const u64 U32MAX = 0xFFFFFFFFull;
     for (u32 i = 0; i < k->n_ops; i++) {
         const KOp *op = &k->ops[i];
         OpI *o = &g->oi[i];
         o->kind = K_VAR;
-        o->step = 0;
-        o->align = 1;
+        memset(o->off, 0, sizeof o->off);
+        o->dv = 1;
+        /* value bound over every gid, lane and loop counter */
+        switch (op->type) {
+        case KOP_GID:
+            o->hi = g->mode == KG_MODE_SERIAL ? ((u64)g->total + V - 1) / V * V - 1
+                                              : (g->total ? (u64)g->total - 1 : 0);
+            break;
+        case KOP_CONST_U: o->hi = op->imm.u; break;
+        case KOP_RANGE: o->hi = op->imm.u ? (u64)op->imm.u - 1 : 0; break;
+        case KOP_DIV: o->hi = op->imm.u ? g->oi[op->arg[0]].hi / op->imm.u : 0; break;
+        case KOP_MOD: {
+            u64 h = g->oi[op->arg[0]].hi;
+            o->hi = op->imm.u ? (h < (u64)op->imm.u - 1 ? h : (u64)op->imm.u - 1) : 0;
+            break;
+        }
+        case KOP_IDX: {
+            u64 h = g->oi[op->arg[0]].hi * (u64)op->imm.u + g->oi[op->arg[1]].hi;
+            o->hi = h;   /* > U32MAX: may wrap */
+            break;
+        }
+        default: o->hi = U32MAX; break;   /* float valued (f2u when used as an index) */
+        }
+        int wrap = o->hi > U32MAX;
+        if (wrap) o->hi = U32MAX;
         int inscope = (g->mode == KG_MODE_SERIAL) || (o->ploop >= 0 && o->depth > 0) ||
                       op->type == KOP_RANGE;
-        if (g->mode == KG_MODE_GROUP && !inscope) {
-            /* uniform across the workgroup */
+        if ((g->mode == KG_MODE_GROUP && !inscope) || V == 1) {
+            /* uniform across the vector */
             o->kind = K_INV;
-            if (op->type == KOP_CONST_U) o->align = pow2_of(op->imm.u);
-            continue;
-        }
-        if (V == 1) {
-            o->kind = K_INV;
-            if (op->type == KOP_CONST_U) o->align = pow2_of(op->imm.u);
+            if (op->type == KOP_CONST_U) o->dv = op->imm.u;
             continue;
         }
         switch (op->type) {
         case KOP_GID:
-            if (g->mode == KG_MODE_SERIAL) { o->kind = K_LIN; o->step = 1; o->align = V; }
-            else { o->kind = K_INV; o->align = 1; }
+            if (g->mode == KG_MODE_SERIAL) {
+                o->kind = K_LIN; o->dv = V;
+                for (u32 v = 0; v < V; v++) o->off[v] = v;
+            } else o->kind = K_INV;
             break;
         case KOP_CONST_U:
-            o->kind = K_INV; o->align = pow2_of(op->imm.u);
+            o->kind = K_INV; o->dv = op->imm.u;
             break;
         case KOP_CONST_F:
             o->kind = K_INV;
             break;
         case KOP_RANGE:
-            if (g->mode == KG_MODE_GROUP && o->depth == 0) { o->kind = K_LIN; o->step = 1; o->align = V; }
-            else { o->kind = K_INV; o->align = 1; }
+            if (g->mode == KG_MODE_GROUP && o->depth == 0) {
+                o->kind = K_LIN; o->dv = V;
+                for (u32 v = 0; v < V; v++) o->off[v] = v;
+            } else o->kind = K_INV;
             break;
         case KOP_IDX: {
             const OpI *a = &g->oi[op->arg[0]], *b = &g->oi[op->arg[1]];
-            if (a->ft || b->ft) {
-                o->kind = (a->kind == K_INV && b->kind == K_INV) ? K_INV : K_VAR;
-                o->align = 1;
+            if (a->kind == K_VAR || b->kind == K_VAR || ((a->ft || b->ft) && !(a->kind == K_INV && b->kind == K_INV))) {
+                o->kind = K_VAR;
                 break;
             }
-            if (a->kind == K_VAR || b->kind == K_VAR) { o->kind = K_VAR; break; }
-            u32 st = a->step * op->imm.u + b->step;
-            o->kind = st ? K_LIN : K_INV;
-            o->step = st;
-            o->align = align_min(align_mul(a->align, op->imm.u), b->align);
-            break;
-        }
-        case KOP_MOD: {
-            const OpI *a = &g->oi[op->arg[0]];
-            u32 m = op->imm.u;
-            if (m == 0) { o->kind = K_INV; o->align = 0; break; }
-            if (a->ft) { o->kind = a->kind == K_INV ? K_INV : K_VAR; break; }
-            if (a->kind == K_INV) { o->kind = K_INV; o->align = align_min(a->align, pow2_of(m)); break; }
-            if (a->kind == K_LIN && a->step == 1 && (a->align == 0 || a->align >= V) && pow2_of(m) >= V) {
-                o->kind = K_LIN; o->step = 1; o->align = align_min(a->align, pow2_of(m));
+            if (a->kind == K_INV && b->kind == K_INV) {
+                o->kind = K_INV;
+                o->dv = (wrap || a->ft || b->ft) ? 1 : dv_gcd(dv_mul(a->dv, op->imm.u), b->dv);
                 break;
             }
-            o->kind = K_VAR;
+            if (wrap) { o->kind = K_VAR; break; }
+            for (u32 v = 0; v < V; v++) o->off[v] = a->off[v] * op->imm.u + b->off[v];
+            o->dv = dv_gcd(dv_mul(a->dv, op->imm.u), b->dv);
+            o->kind = lin_zero(o->off, V) ? K_INV : K_LIN;
             break;
         }
-        case KOP_DIV: {
+        case KOP_MOD: case KOP_DIV: {
             const OpI *a = &g->oi[op->arg[0]];
             u32 d = op->imm.u;
-            if (d == 0) { o->kind = K_INV; o->align = 0; break; }
+            int is_mod = op->type == KOP_MOD;
+            if (d == 0) { o->kind = K_INV; o->dv = 0; break; }
             if (a->ft) { o->kind = a->kind == K_INV ? K_INV : K_VAR; break; }
-            if (a->kind == K_INV) { o->kind = K_INV; o->align = d == 1 ? a->align : 1; break; }
-            if (d == 1) { o->kind = a->kind; o->step = a->step; o->align = a->align; break; }
-            if (a->kind == K_LIN && a->step == 1 && (a->align == 0 || a->align >= V) && pow2_of(d) >= V) {
-                o->kind = K_INV; o->align = 1;
-                break;
+            if (a->kind == K_VAR) break;
+            u32 A = a->dv;
+            if (A != 0 && A % d != 0 && a->kind == K_LIN && lin_max(a->off, V) >= gcd_u32(A, d)) break;
+            /* Here either d divides A (lane values split exactly), or every
+             * offset is below G = gcd(A, d): value(0) mod d is a multiple of G
+             * and at most d - G, so no lane crosses a multiple of d. */
+            if (A == 0 || A % d == 0) {
+                for (u32 v = 0; v < V; v++) o->off[v] = is_mod ? a->off[v] % d : a->off[v] / d;
+                o->dv = is_mod ? 0 : (A == 0 ? 0 : A / d);
+            } else {
+                for (u32 v = 0; v < V; v++) o->off[v] = is_mod ? a->off[v] : 0;
+                o->dv = is_mod ? gcd_u32(A, d) : 1;
             }
-            o->kind = K_VAR;
+            o->kind = lin_zero(o->off, V) ? K_INV : K_LIN;
             break;
         }
         case KOP_LOAD:
@@ -437,8 +484,8 @@ static const char *U(Gen *g, u32 j, u32 v, char *buf) {
     }
     if (o->kind == K_INV || g->V == 1) snprintf(buf, 64, "n%u", j);
     else if (o->kind == K_LIN) {
-        if (v == 0) snprintf(buf, 64, "n%u", j);
-        else snprintf(buf, 64, "(n%u+%uu)", j, v * o->step);
+        if (o->off[v] == 0) snprintf(buf, 64, "n%u", j);
+        else snprintf(buf, 64, "(n%u+%uu)", j, o->off[v]);
     } else snprintf(buf, 64, "n%u_%u", j, v);
     return buf;
 }
@@ -585,8 +632,7 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
             U(g, op->arg[0], 0, a);
             if (unchecked) sb_put(&g->sb, "    f%u = %s_u(p%u, %s);\n", i, dt_ld(dt), bi, a);
             else sb_put(&g->sb, "    f%u = %s(p%u, c%u, %s);\n", i, dt_ld(dt), bi, bi, a);
-        } else if (V == 4 && ix->kind == K_LIN && ix->step == 1 && !ix->ft &&
-                   (ix->align == 0 || ix->align % 4 == 0) && dt == DTYPE_F32) {
+        } else if (lin_unit4(ix, V) && dt == DTYPE_F32) {
             U(g, op->arg[0], 0, a);
             const char *sfx = (g->nt & 1) ? "nt" : "";
             if (unchecked)
@@ -597,6 +643,13 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
                        sfx, bi, bi, a, i, i, i, i);
         } else {
             for (u32 v = 0; v < V; v++) {
+                u32 u = v;
+                if (ix->kind == K_LIN && !ix->ft)
+                    for (u = 0; u < v && ix->off[u] != ix->off[v]; u++) {}
+                if (u < v) {   /* same address as lane u */
+                    sb_put(&g->sb, "    f%u_%u = f%u_%u;\n", i, v, i, u);
+                    continue;
+                }
                 U(g, op->arg[0], v, a);
                 if (unchecked) sb_put(&g->sb, "    f%u_%u = %s_u(p%u, %s);\n", i, v, dt_ld(dt), bi, a);
                 else sb_put(&g->sb, "    f%u_%u = %s(p%u, c%u, %s);\n", i, v, dt_ld(dt), bi, bi, a);
@@ -650,8 +703,7 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
             sb_put(&g->sb, "    if (lane == 0) %s(p0, c0, %s, %s);\n", dt_st(k->out_dtype), a, b);
             break;
         }
-        if (V == 4 && ix->kind == K_LIN && ix->step == 1 && !ix->ft &&
-            (ix->align == 0 || ix->align % 4 == 0) && k->out_dtype == DTYPE_F32) {
+        if (lin_unit4(ix, V) && k->out_dtype == DTYPE_F32) {
             char b1[128], b2[128], b3[128];
             U(g, op->arg[0], 0, a);
             Fx(g, op->arg[1], 0, b);
@@ -971,7 +1023,7 @@ static void group_split_plan(Gen *g) {
     for (u32 i = 0; i < k->n_ops; i++)
         if (i != t && g->oi[i].acc_tgt) return;       /* one accumulator */
     u32 S = 1;
-    while (g->total * S < 512u && trip / (S * 2) >= SPLIT_MIN_CHUNK && S < 64u) S *= 2;
+    while (g->total * S < g->split_target && trip / (S * 2) >= SPLIT_MIN_CHUNK && S < g->split_max) S *= 2;
     if (S < 2) return;
     g->splits = S;
     g->split_acc = t;
@@ -1076,6 +1128,10 @@ static void emit_group_loop(Gen *g, u32 r) {
 }
 
 int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
+    return kgen_uop_lanes(k, out, NULL, err, errlen);
+}
+
+int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, size_t errlen) {
     memset(out, 0, sizeof(*out));
     if (!kgen_validate(k, err, errlen)) return 0;
     Gen G;
@@ -1094,6 +1150,10 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
         G.red_block = (e = getenv("THVM_HIP_RED_BLOCK")) ? (u32)atoi(e) : 256;
         if (G.red_block != 64 && G.red_block != 128 && G.red_block != 512 && G.red_block != 1024)
             G.red_block = 256;
+        G.split_target = (e = getenv("THVM_HIP_SPLIT_TARGET")) ? (u32)atoi(e) : 4096;
+        if (G.split_target < 1) G.split_target = 4096;
+        G.split_max = (e = getenv("THVM_HIP_SPLIT_MAX")) ? (u32)atoi(e) : 128;
+        if (G.split_max < 2 || G.split_max > 1024) G.split_max = 128;
         G.per_thread = (e = getenv("THVM_HIP_EW_PER_THREAD")) ? (u32)atoi(e) : 1;
         if (G.per_thread < 1) G.per_thread = 1;
         if (G.per_thread > 8) G.per_thread = 8;
@@ -1211,6 +1271,15 @@ int kgen_uop(const UOpKernel *k, KGenResult *out, char *err, size_t errlen) {
                out->name, total, bits, G.splits, G.splits, rmax ? "f = (f > w) ? f : w;" : "f = f + w;",
                dt_st(k->out_dtype));
     }
+    if (lanes)
+        for (u32 i = 0; i < k->n_ops; i++) {
+            const OpI *o = &G.oi[i];
+            u32 *l = lanes + 7 * i;
+            l[0] = o->ft ? 3u : o->kind;
+            for (u32 v = 0; v < 4; v++) l[1 + v] = o->off[v];
+            l[5] = o->dv;
+            l[6] = (u32)o->hi;
+        }
     free(G.oi);
     free(G.scal);
     if (!s->p) { snprintf(err, errlen, "oom"); return 0; }
