@@ -537,6 +537,8 @@ typedef struct {
     u32 kchunk;
     u32 tiles_m, tiles_n;
     KPerm kp;
+    int swap;              /* output m-contiguous: MFMA blocks computed transposed so that lanes
+                              run along m in the epilogue (coalesced stores) */
 } GemmPlan;
 
 #define GEMM_THREADS 256
@@ -600,7 +602,9 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
     const char *st;
     out_store_fn(k, ct, fb, sizeof fb, &st);
     const u32 M = ct->M, N = ct->N;
-    if (pl->splits > 1)
+    if (pl->splits > 1 && pl->swap)
+        dsb_put(s_, "        ws[((unsigned long long)blockIdx.y * N + n) * M + m] = c[v];\n");
+    else if (pl->splits > 1)
         dsb_put(s_, "        ws[((unsigned long long)blockIdx.y * M + m) * N + n] = c[v];\n");
     else
         dsb_put(s_, "        %s(p0, c0, gid_m(m) + gid_n(n), %s + c[v]);\n", st, fb);
@@ -613,22 +617,24 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
                     "  const unsigned long long t = (unsigned long long)blockIdx.x * 4u + (threadIdx.x >> 6);\n"
                     "  const u32 lane = threadIdx.x & 63u;\n"
                     "  if (t >= %lluull) return;\n"
-                    "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
+                    "  const u32 %s = (u32)(t / %uu), %s = (u32)(t %% %uu);\n"
                     "  float a = 0.0f;\n"
                     "  for (u32 s = lane; s < %uu; s += 64u) a = a + ws[(unsigned long long)s * %lluull + t];\n"
                     "  a = wsum(a);\n"
                     "  if (lane == 0u) %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
-                pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
+                pl->name, (unsigned long long)M * N, pl->swap ? "n" : "m", pl->swap ? M : N, pl->swap ? "m" : "n",
+                pl->swap ? M : N, pl->splits, (unsigned long long)M * N, st, fb);
     } else {
         dsb_put(s_, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
                     "  const unsigned long long t = (unsigned long long)blockIdx.x * 256u + threadIdx.x;\n"
                     "  if (t >= %lluull) return;\n"
-                    "  const u32 m = (u32)(t / %uu), n = (u32)(t %% %uu);\n"
+                    "  const u32 %s = (u32)(t / %uu), %s = (u32)(t %% %uu);\n"
                     "  float a = 0.0f;\n"
                     "  #pragma unroll 8\n"
                     "  for (u32 s = 0; s < %uu; s++) a = a + ws[(unsigned long long)s * %lluull + t];\n"
                     "  %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
-                pl->name, (unsigned long long)M * N, N, N, pl->splits, (unsigned long long)M * N, st, fb);
+                pl->name, (unsigned long long)M * N, pl->swap ? "n" : "m", pl->swap ? M : N, pl->swap ? "m" : "n",
+                pl->swap ? M : N, pl->splits, (unsigned long long)M * N, st, fb);
     }
 }
 
@@ -963,25 +969,29 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
             "      for (u32 i = 0; i < %uu; i++)\n"
             "        #pragma unroll\n"
             "        for (u32 j = 0; j < %uu; j++)\n"
-            "          acc[i * %uu + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[kk][i], b[kk][j], acc[i * %uu + j], 0, 0, 0);\n"
+            "          acc[i * %uu + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[i * %uu + j], 0, 0, 0);\n"
             "    /* the next stage's global loads stay in flight across the MFMAs: the\n"
             "     * LDS stores (which need them) may not move above the math */\n"
             "    __builtin_amdgcn_sched_barrier(0);\n"
             "    if (st + 1u < nst) { storeA(cur ^ 1u); storeB(cur ^ 1u); }\n"
             "    __syncthreads();\n"
             "  }\n",
-            NB, NB, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wn_b, cf->wn_b);
-    /* epilogue: D[i][j] of a 32x32 block sits in lane j + 32*((i/4)%%2), register (i%%4) + 4*(i/8) */
+            NB, NB, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wn_b,
+            pl->swap ? "b[kk][j]" : "a[kk][i]", pl->swap ? "a[kk][i]" : "b[kk][j]", cf->wn_b);
+    /* epilogue: D[i][j] of a 32x32 block sits in lane j + 32*((i/4)%%2), register (i%%4) + 4*(i/8);
+     * D is the (m, n) block, or with swap its transpose (the MFMA took B as its first operand), so
+     * that the 32 lanes of a store run along whichever output index is contiguous */
     dsb_put(&s,
             "  #pragma unroll\n"
             "  for (u32 blk = 0; blk < %uu; blk++) {\n"
             "    const f32x16 c = acc[blk];\n"
             "    const u32 bm = wm + (blk / %uu) * 32u, bn = wn + (blk %% %uu) * 32u;\n"
-            "    const u32 n = n0 + bn + (lane & 31u);\n"
             "    #pragma unroll\n"
             "    for (u32 v = 0; v < 16u; v++) {\n"
-            "      const u32 m = m0 + bm + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3u);\n"
-            "      if (m < M && n < N) {\n", NB, cf->wn_b, cf->wn_b);
+            "      const u32 %s = %s0 + b%s + (lane & 31u);\n"
+            "      const u32 %s = %s0 + b%s + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3u);\n"
+            "      if (m < M && n < N) {\n", NB, cf->wn_b, cf->wn_b, pl->swap ? "m" : "n", pl->swap ? "m" : "n",
+            pl->swap ? "m" : "n", pl->swap ? "n" : "m", pl->swap ? "n" : "m", pl->swap ? "n" : "m");
     emit_store_tail(&s, k, ct, pl);
     return s.p;
 }
@@ -1258,6 +1268,8 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     pl->kchunk = kch;
     pl->splits = (ct->K + kch - 1) / kch;
     snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));
+    pl->swap = !pl->cfg.direct && !hipb.dense_noswap && ct->np > 0 && ct->pdiv[ct->np - 1] == 1 &&
+               !(ct->nq > 0 && ct->qdiv[ct->nq - 1] == 1);
     plan_kperm(ct, pl);
     plan_pads(ct, pl);
 }
