@@ -539,6 +539,9 @@ typedef struct {
     KPerm kp;
     int swap;              /* output m-contiguous: MFMA blocks computed transposed so that lanes
                               run along m in the epilogue (coalesced stores) */
+    int pack;              /* the B side is first copied into a K x N row-major buffer in the
+                              reordered k order (a small operand with scattered loads) */
+    KPerm kpo;             /* the K-reordered plan before packing (the pack kernel's loads) */
 } GemmPlan;
 
 #define GEMM_THREADS 256
@@ -728,9 +731,9 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
 }
 
 /* Uniform k base of one side at the stage starting at reordered index k. */
-static void emit_kbase_fn(DSB *s, const KPerm *kp, int side) {
-    dsb_put(s, "__device__ __forceinline__ u32 kbase_%c(u32 k) {\n  u32 o = k / %uu;\n  u32 u = (k %% %uu) * %uu;\n",
-            side ? 'q' : 'p', kp->E, kp->E, kp->icoef[side]);
+static void emit_kbase_fn(DSB *s, const KPerm *kp, int side, const char *name) {
+    dsb_put(s, "__device__ __forceinline__ u32 %s(u32 k) {\n  u32 o = k / %uu;\n  u32 u = (k %% %uu) * %uu;\n",
+            name, kp->E, kp->E, kp->icoef[side]);
     for (u32 t = 0; t < kp->ndig; t++) {
         if (t + 1 < kp->ndig)
             dsb_put(s, "  u += (o %% %uu) * %uu; o /= %uu;\n", kp->oext[t], kp->ocoef[side][t], kp->oext[t]);
@@ -764,7 +767,9 @@ static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl
         const char *xn = side ? "nn" : "mm";
         const int kmaj = side ? ct->q_kmajor : ct->p_kmajor;
         const u32 bx = side ? cf->bn : cf->bm;
-        if (kp->lin[side]) {
+        if (side == 1 && pl->pack) {
+            dsb_put(s, "  const u32 oB = n0;\n");
+        } else if (kp->lin[side]) {
             dsb_put(s, "  const u32 o%c = rowb_%c(gid_%c(%s));\n", X, S, side ? 'n' : 'm', side ? "n0" : "m0");
         } else {
             dsb_put(s, "  u32 o%c[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", X, EX[side], EX[side]);
@@ -774,11 +779,14 @@ static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl
                     side ? "n0" : "m0", xn, X, S, side ? 'n' : 'm', side ? ct->N : ct->M,
                     (side ? ct->N : ct->M) - 1, kp->icoef[side]);
         }
+        char src[40];
+        if (side == 1 && pl->pack) snprintf(src, sizeof src, "pk");
+        else snprintf(src, sizeof src, "(const float*)p%u", ct->sep_buf[side]);
         if (kp->vec[side]) {
             dsb_put(s, "  auto load%c = [&](u32 k0) {\n"
-                       "    const float* ps = (const float*)p%u + kbase_%c(k0);\n"
+                       "    const float* ps = %s + kbase_%c(k0);\n"
                        "    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
-                    X, ct->sep_buf[side], S, EX[side] / 4u);
+                    X, src, S, EX[side] / 4u);
             emit_map4(s, kmaj, bx, cf->bk, xn);
             dsb_put(s, "\n      const float4 v = *(const float4*)(ps + o%c + %s * %uu + kk * %uu);\n"
                        "      r%c[4u * e] = v.x; r%c[4u * e + 1u] = v.y; r%c[4u * e + 2u] = v.z; r%c[4u * e + 3u] = v.w; }\n"
@@ -788,9 +796,9 @@ static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl
             continue;
         }
         dsb_put(s, "  auto load%c = [&](u32 k0) {\n"
-                   "    const float* ps = (const float*)p%u + kbase_%c(k0);\n"
+                   "    const float* ps = %s + kbase_%c(k0);\n"
                    "    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
-                X, ct->sep_buf[side], S, EX[side]);
+                X, src, S, EX[side]);
         emit_map(s, kmaj, bx, cf->bk, xn);
         if (kp->lin[side])
             dsb_put(s, "\n      r%c[e] = ps[o%c + %s * %uu + kk * %uu]; }\n  };\n", side ? 'b' : 'a', X, xn,
@@ -806,6 +814,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
      * hold 16 more registers across its whole K loop (measured slower) */
     Contraction ctl = *ct_in;
     if (pl->cfg.bm == 128 && !pl->kp.on) ctl.sep[0] = ctl.sep[1] = 0;
+    if (pl->pack) ctl.q_kmajor = 0;
     const Contraction *ct = &ctl;
     DSB s = {0};
     const TileCfg *cf = &pl->cfg;
@@ -817,7 +826,8 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         if (!ct->sep[side]) continue;
         emit_sep_fn(&s, side ? "rowb_q" : "rowb_p", &ct->sep_aff[side], 0);
         emit_sep_fn(&s, side ? "koff_q" : "koff_p", &ct->sep_aff[side], 1);
-        if (pl->kp.on) emit_kbase_fn(&s, &pl->kp, side);
+        if (pl->kp.on) emit_kbase_fn(&s, &pl->kp, side, side ? "kbase_q" : "kbase_p");
+        if (pl->pack && side == 1) emit_kbase_fn(&s, &pl->kpo, 1, "kbase_qo");
     }
     static char body[1 << 16];
     for (int side = 0; side < 2; side++) {
@@ -844,9 +854,20 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
     const u32 BK = cf->bk;
     const u32 EA = cf->bm * BK / GEMM_THREADS, EB = cf->bn * BK / GEMM_THREADS;
     const u32 NB = cf->wm_b * cf->wn_b;
+    if (pl->pack) {
+        /* B in the reordered k order, row-major K x N (n contiguous) */
+        dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(256) void %s_pack(", pl->name);
+        emit_params(&s, k->n_leaves);
+        dsb_put(&s, ", float* pk) {\n"
+                    "  const u32 t = blockIdx.x * 256u + threadIdx.x;\n"
+                    "  if (t >= %uu) return;\n"
+                    "  const u32 k = t / %uu, n = t %% %uu;\n"
+                    "  pk[t] = ld_f32(p%u, c%u, kbase_qo(k) + rowb_q(gid_n(n)));\n}\n",
+                K * N, N, N, ct->sep_buf[1], ct->sep_buf[1]);
+    }
     dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", GEMM_THREADS, pl->name);
     emit_params(&s, k->n_leaves);
-    dsb_put(&s, ", float* ws) {\n");
+    dsb_put(&s, pl->pack ? ", float* ws, const float* pk) {\n" : ", float* ws) {\n");
     dsb_put(&s,
             "  constexpr u32 BM = %u, BN = %u, BK = %u, LDA = BM + %uu, LDB = BN + %uu;\n"
             "  constexpr u32 M = %uu, N = %uu, K = %uu, TM = %uu, TN = %uu, TILES = %uu, KCH = %uu;\n"
@@ -1005,7 +1026,7 @@ typedef struct {
     u32 meta[5 + FUSE_MAX_LEAVES];
     int is_dense;                 /* 0: not a contraction (negative cache) */
     hipModule_t mod;
-    hipFunction_t fn, fn_sum;
+    hipFunction_t fn, fn_sum, fn_pack;
     GemmPlan plan;
     u32 M, N;
 } DenseEntry;
@@ -1014,6 +1035,7 @@ static struct {
     DenseEntry *tab;
     u32 cap, n;
     Scratch ws;            /* split-K partial sums */
+    Scratch pk;            /* packed B operands */
 } D;
 
 static void meta_of(const UOpKernel *k, u32 *m) {
@@ -1232,7 +1254,7 @@ static int plan_kperm(const Contraction *ct, GemmPlan *pl) {
  * the wrong stride.) THVM_HIP_GEMM_PAD overrides the k-major padding. */
 static void plan_pads(const Contraction *ct, GemmPlan *pl) {
     for (int s = 0; s < 2; s++) {
-        const int kmaj = s ? ct->q_kmajor : ct->p_kmajor;
+        const int kmaj = s ? (pl->pack ? 0 : ct->q_kmajor) : ct->p_kmajor;
         const u32 bx = s ? pl->cfg.bn : pl->cfg.bm;
         u32 pad = 4;
         if (kmaj) {
@@ -1242,6 +1264,37 @@ static void plan_pads(const Contraction *ct, GemmPlan *pl) {
         if (s) pl->pad_b = pad;
         else pl->pad_a = pad;
     }
+}
+
+/* Packing the B side. A small B (the weights of a convolution) reused by
+ * many row tiles, whose reordered-k loads are scattered (lanes along k on a
+ * strided digit: 3x3 weights put consecutive input channels 9 floats apart),
+ * costs the address unit and L1 far more than its bytes: each 64-lane load
+ * touches dozens of cache lines. A pack kernel first copies it into a K x N
+ * row-major buffer in the reordered k order; the GEMM then reads that buffer
+ * like a linear side with 16-byte loads along n. In K-reordered terms the
+ * packed side has row coefficient 1, inner coefficient N and outer digit
+ * coefficients N times the place value of each digit in k. */
+static void plan_pack(const Contraction *ct, GemmPlan *pl) {
+    KPerm *kp = &pl->kp;
+    pl->pack = 0;
+    if (!kp->on || hipb.dense_nopack || kp->vec[1] || pl->cfg.direct) return;
+    const u32 per_lane = pl->cfg.bn * pl->cfg.bk / GEMM_THREADS;
+    if ((u64)ct->K * ct->N > (4u << 20) || ct->N % 4 != 0 || ct->N % pl->cfg.bn != 0 || per_lane % 4 != 0 ||
+        pl->tiles_m < 64)
+        return;
+    pl->kpo = *kp;
+    pl->pack = 1;
+    kp->lin[1] = 1;
+    kp->lcoef[1] = 1;
+    kp->icoef[1] = ct->N;
+    u64 place = kp->E;
+    for (u32 t = 0; t < kp->ndig; t++) {
+        kp->ocoef[1][t] = (u32)(place * ct->N);
+        place *= kp->oext[t];
+    }
+    kp->vec[1] = !hipb.dense_novec;
+    kp->maxidx[1] = (u64)ct->K * ct->N - 1;
 }
 
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
@@ -1271,6 +1324,7 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     pl->swap = !pl->cfg.direct && !hipb.dense_noswap && ct->np > 0 && ct->pdiv[ct->np - 1] == 1 &&
                !(ct->nq > 0 && ct->qdiv[ct->nq - 1] == 1);
     plan_kperm(ct, pl);
+    plan_pack(ct, pl);
     plan_pads(ct, pl);
 }
 
@@ -1309,8 +1363,10 @@ char *dense_source(const UOpKernel *k) {
 /* The unchecked loads of a K-reordered plan stay inside the buffers they
  * read: every index a side can form is below that buffer's element count,
  * and 16-byte loads start from 16-byte aligned buffers. */
-static int kperm_fits(const KPerm *kp, const u32 *counts, void *const *ptrs) {
+static int kperm_fits(const GemmPlan *pl, const u32 *counts, void *const *ptrs) {
+    const KPerm *kp = &pl->kp;
     for (int s = 0; s < 2; s++) {
+        if (s == 1 && pl->pack) continue;    /* reads the pack buffer, sized K x N */
         if (kp->maxidx[s] >= counts[kp->buf[s]]) return 0;
         if (kp->vec[s] && ((uintptr_t)ptrs[kp->buf[s]] & 15u)) return 0;
     }
@@ -1339,8 +1395,9 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         u32 M, N, K, sp;
         if (!dense_analyze(k, &M, &N, &K, &sp) || !recognize(k, &ct)) return 0;
         make_plan(&ct, &e->plan, uop_signature(k));
-        if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts, ptrs)) {
+        if (e->plan.kp.on && !kperm_fits(&e->plan, counts, ptrs)) {
             memset(&e->plan.kp, 0, sizeof e->plan.kp);
+            e->plan.pack = 0;
             plan_pads(&ct, &e->plan);
         }
         char err[256] = {0};
@@ -1357,6 +1414,11 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         }
         free(src);
         if (hipModuleGetFunction(&e->fn, e->mod, e->plan.name) != hipSuccess) return 0;
+        if (e->plan.pack) {
+            char nm[64];
+            snprintf(nm, sizeof nm, "%s_pack", e->plan.name);
+            if (hipModuleGetFunction(&e->fn_pack, e->mod, nm) != hipSuccess) return 0;
+        }
         if (e->plan.splits > 1) {
             char nm[64];
             snprintf(nm, sizeof nm, "%s_sum", e->plan.name);
@@ -1371,7 +1433,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     }
     if (!e->is_dense) return 0;
     /* buffers smaller than the plan was made for: the generated kernels */
-    if (e->plan.kp.on && !kperm_fits(&e->plan.kp, counts, ptrs)) return 0;
+    if (e->plan.kp.on && !kperm_fits(&e->plan, counts, ptrs)) return 0;
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     /* split-K workspace */
     float *ws = NULL;
@@ -1379,13 +1441,27 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         ws = scratch_reserve(&D.ws, (u64)e->plan.splits * e->M * e->N * sizeof(float));
         if (!ws) return 0;
     }
-    void *params[2 * (FUSE_MAX_LEAVES + 1) + 1];
+    /* packed B side */
+    float *pk = NULL;
+    if (e->plan.pack) {
+        pk = scratch_reserve(&D.pk, (u64)e->plan.kp.maxidx[1] * sizeof(float) + sizeof(float));
+        if (!pk) return 0;
+    }
+    void *params[2 * (FUSE_MAX_LEAVES + 1) + 2];
     u32 nb = k->n_leaves + 1;
     for (u32 b = 0; b < nb; b++) {
         params[b] = &ptrs[b];
         params[nb + b] = &counts[b];
     }
     params[2 * nb] = &ws;
+    params[2 * nb + 1] = &pk;
+    if (e->plan.pack) {
+        void *pp[2 * (FUSE_MAX_LEAVES + 1) + 1];
+        for (u32 b = 0; b < 2 * nb; b++) pp[b] = params[b];
+        pp[2 * nb] = &pk;
+        const u64 kn = e->plan.kp.maxidx[1] + 1;
+        if (!hipb_launch_grid(e->fn_pack, (u32)((kn + 255) / 256), 1, 256, pp)) return 0;
+    }
     u32 tiles = e->plan.tiles_m * e->plan.tiles_n;
     if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, GEMM_THREADS, params)) return 0;
     if (e->plan.splits > 1) {
@@ -1409,5 +1485,6 @@ void dense_shutdown(void) {
         free(D.tab);
     }
     scratch_release(&D.ws);
+    scratch_release(&D.pk);
     memset(&D, 0, sizeof D);
 }
