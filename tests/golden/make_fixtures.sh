@@ -26,6 +26,8 @@ $CAP mlp mlp_64x784x128x10.trc 64 784 128 10
 $CAP lenet lenet_b2.trc 2 1
 # conv3x3 + batchnorm(train) + relu + maxpool block, forward + backward
 $CAP convblock convblock_2x4x8.trc 2 4 8
+# the same at 28x28 (image rows not a multiple of the GEMM stage depth)
+$CAP convblock convblock_2x4x28.trc 2 4 28
 # storage dtypes and casts
 $CAP dtypes dtypes.trc
 # ASSIGN from strided views (the contiguify slot)

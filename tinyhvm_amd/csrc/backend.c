@@ -92,6 +92,9 @@ static void read_dense_env(void) {
     e = getenv("THVM_HIP_GEMM_BK");
     hipb.gemm_bk = e ? (u32)atoi(e) : 0;
     if (hipb.gemm_bk != 16 && hipb.gemm_bk != 32) hipb.gemm_bk = 0;
+    e = getenv("THVM_HIP_GEMM_DEPTH");
+    hipb.gemm_depth = e ? (u32)atoi(e) : 0;
+    if (hipb.gemm_depth > 2) hipb.gemm_depth = 0;
     e = getenv("THVM_HIP_DENSE_TILE");
     hipb.dense_tile = e ? (u32)atoi(e) : 0;
     if (hipb.dense_tile > 7) hipb.dense_tile = 0;

@@ -518,6 +518,9 @@ static const TileCfg CFG_DIRECT = {32, 32, 32, 1, 1, 1, 1, "direct32", 1};
 typedef struct {
     int on;
     u32 E;                       /* extent of the inner digit */
+    u32 Ep;                      /* E rounded up to the stage depth: k runs over Ep per outer step and
+                                    the loaders zero elements whose inner index is E or more */
+    u32 Kl;                      /* the reordered K the GEMM loops over: K / E * Ep */
     u32 ndig;                    /* outer digits, fastest first */
     u32 oext[KP_MAX];
     u32 ocoef[2][KP_MAX];
@@ -534,6 +537,8 @@ typedef struct {
     TileCfg cfg;
     u32 pad_a, pad_b;      /* LDS row padding (floats) of the A and B stages */
     u32 splits;
+    u32 splits_want;       /* split count asked for; splits is what the K chunks give */
+    u32 depth;             /* stages of global loads in flight ahead of the math (1 or 2) */
     u32 kchunk;
     u32 tiles_m, tiles_n;
     KPerm kp;
@@ -606,9 +611,9 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
     out_store_fn(k, ct, fb, sizeof fb, &st);
     const u32 M = ct->M, N = ct->N;
     if (pl->splits > 1 && pl->swap)
-        dsb_put(s_, "        ws[((unsigned long long)blockIdx.y * N + n) * M + m] = c[v];\n");
+        dsb_put(s_, "        ws[((unsigned long long)spl * N + n) * M + m] = c[v];\n");
     else if (pl->splits > 1)
-        dsb_put(s_, "        ws[((unsigned long long)blockIdx.y * M + m) * N + n] = c[v];\n");
+        dsb_put(s_, "        ws[((unsigned long long)spl * M + m) * N + n] = c[v];\n");
     else
         dsb_put(s_, "        %s(p0, c0, gid_m(m) + gid_n(n), %s + c[v]);\n", st, fb);
     dsb_put(s_, "      }\n    }\n  }\n}\n");
@@ -672,7 +677,8 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
             "  const u32 blk = blockIdx.x;\n"
             "  if (blk >= BLOCKS) return;\n"
             "  const u32 m0 = (blk / TN) * 32u, n0 = (blk %% TN) * 32u;\n"
-            "  const u32 kbeg = blockIdx.y * KCH;\n"
+            "  const u32 spl = blockIdx.y;\n"
+            "  const u32 kbeg = spl * KCH;\n"
             "  const u32 kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
             "  const u32 i = lane & 31u, kh = lane >> 5;\n"
             "  const u32 ma = m0 + i, nb = n0 + i;\n",
@@ -733,7 +739,7 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
 /* Uniform k base of one side at the stage starting at reordered index k. */
 static void emit_kbase_fn(DSB *s, const KPerm *kp, int side, const char *name) {
     dsb_put(s, "__device__ __forceinline__ u32 %s(u32 k) {\n  u32 o = k / %uu;\n  u32 u = (k %% %uu) * %uu;\n",
-            name, kp->E, kp->E, kp->icoef[side]);
+            name, kp->Ep, kp->Ep, kp->icoef[side]);
     for (u32 t = 0; t < kp->ndig; t++) {
         if (t + 1 < kp->ndig)
             dsb_put(s, "  u += (o %% %uu) * %uu; o /= %uu;\n", kp->oext[t], kp->ocoef[side][t], kp->oext[t]);
@@ -762,49 +768,69 @@ static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl
     const TileCfg *cf = &pl->cfg;
     const KPerm *kp = &pl->kp;
     const u32 EX[2] = {cf->bm * cf->bk / GEMM_THREADS, cf->bn * cf->bk / GEMM_THREADS};
+    /* padded inner digit: elements whose inner index i0 + kk reaches E load
+     * as 0 from a clamped (in-range) address; lim_ = E - i0 >= 1 because i0
+     * is a multiple of the stage depth below Ep */
+    const int padded = kp->Ep != kp->E;
     for (int side = 0; side < 2; side++) {
         const char S = side ? 'q' : 'p', X = side ? 'B' : 'A';
         const char *xn = side ? "nn" : "mm";
         const int kmaj = side ? ct->q_kmajor : ct->p_kmajor;
         const u32 bx = side ? cf->bn : cf->bm;
-        if (side == 1 && pl->pack) {
+        const char rr = side ? 'b' : 'a';
+        const int packed = side == 1 && pl->pack;     /* zero rows written by the pack kernel */
+        const int mask = padded && !packed;
+        if (packed) {
             dsb_put(s, "  const u32 oB = n0;\n");
         } else if (kp->lin[side]) {
             dsb_put(s, "  const u32 o%c = rowb_%c(gid_%c(%s));\n", X, S, side ? 'n' : 'm', side ? "n0" : "m0");
         } else {
             dsb_put(s, "  u32 o%c[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", X, EX[side], EX[side]);
             emit_map(s, kmaj, bx, cf->bk, xn);
+            char kt[48] = "";
+            if (!mask) snprintf(kt, sizeof kt, " + kk * %uu", kp->icoef[side]);
             dsb_put(s, "\n    const u32 x = %s + %s;\n"
-                       "    o%c[e] = rowb_%c(gid_%c(x < %uu ? x : %uu)) + kk * %uu; }\n",
+                       "    o%c[e] = rowb_%c(gid_%c(x < %uu ? x : %uu))%s; }\n",
                     side ? "n0" : "m0", xn, X, S, side ? 'n' : 'm', side ? ct->N : ct->M,
-                    (side ? ct->N : ct->M) - 1, kp->icoef[side]);
+                    (side ? ct->N : ct->M) - 1, kt);
         }
-        char src[40];
-        if (side == 1 && pl->pack) snprintf(src, sizeof src, "pk");
+        char src[40], lim[64], kv[16];
+        if (packed) snprintf(src, sizeof src, "pk");
         else snprintf(src, sizeof src, "(const float*)p%u", ct->sep_buf[side]);
+        snprintf(lim, sizeof lim, mask ? "\n    const u32 lim_ = %uu - k0 %% %uu;" : "", kp->E, kp->Ep);
+        snprintf(kv, sizeof kv, mask ? "kv_" : "kk");
+        /* offset of one element: row base, row, and the (clamped) k */
+        char off[160];
+        if (kp->lin[side] || packed)
+            snprintf(off, sizeof off, "o%c + %s * %uu + %s * %uu", X, xn, kp->lcoef[side], kv, kp->icoef[side]);
+        else
+            snprintf(off, sizeof off, mask ? "o%c[e] + kv_ * %uu" : "o%c[e]", X, kp->icoef[side]);
         if (kp->vec[side]) {
-            dsb_put(s, "  auto load%c = [&](u32 k0) {\n"
-                       "    const float* ps = %s + kbase_%c(k0);\n"
+            dsb_put(s, "  auto load%c = [&](u32 k0, float (&r%c)[%u]) {\n"
+                       "    const float* ps = %s + kbase_%c(k0);%s\n"
                        "    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
-                    X, src, S, EX[side] / 4u);
+                    X, rr, EX[side], src, S, lim, EX[side] / 4u);
             emit_map4(s, kmaj, bx, cf->bk, xn);
-            dsb_put(s, "\n      const float4 v = *(const float4*)(ps + o%c + %s * %uu + kk * %uu);\n"
-                       "      r%c[4u * e] = v.x; r%c[4u * e + 1u] = v.y; r%c[4u * e + 2u] = v.z; r%c[4u * e + 3u] = v.w; }\n"
-                       "  };\n",
-                    X, xn, kp->lcoef[side], kp->icoef[side], side ? 'b' : 'a', side ? 'b' : 'a', side ? 'b' : 'a',
-                    side ? 'b' : 'a');
+            if (mask) dsb_put(s, "\n      const u32 kv_ = kk < lim_ ? kk : 0u;");
+            dsb_put(s, "\n      float4 v = *(const float4*)(ps + %s);\n", off);
+            if (mask) {
+                /* 16-byte groups never straddle E (E, i0 and the group start are multiples of 4) */
+                dsb_put(s, "      if (kk >= lim_) v = make_float4(0.0f, 0.0f, 0.0f, 0.0f);\n");
+            }
+            dsb_put(s, "      r%c[4u * e] = v.x; r%c[4u * e + 1u] = v.y; r%c[4u * e + 2u] = v.z; r%c[4u * e + 3u] = v.w; }\n"
+                       "  };\n", rr, rr, rr, rr);
             continue;
         }
-        dsb_put(s, "  auto load%c = [&](u32 k0) {\n"
-                   "    const float* ps = %s + kbase_%c(k0);\n"
+        dsb_put(s, "  auto load%c = [&](u32 k0, float (&r%c)[%u]) {\n"
+                   "    const float* ps = %s + kbase_%c(k0);%s\n"
                    "    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
-                X, src, S, EX[side]);
+                X, rr, EX[side], src, S, lim, EX[side]);
         emit_map(s, kmaj, bx, cf->bk, xn);
-        if (kp->lin[side])
-            dsb_put(s, "\n      r%c[e] = ps[o%c + %s * %uu + kk * %uu]; }\n  };\n", side ? 'b' : 'a', X, xn,
-                    kp->lcoef[side], kp->icoef[side]);
+        if (mask)
+            dsb_put(s, "\n      const u32 kv_ = kk < lim_ ? kk : 0u;\n"
+                       "      const float v = ps[%s];\n      r%c[e] = kk < lim_ ? v : 0.0f; }\n  };\n", off, rr);
         else
-            dsb_put(s, "\n      r%c[e] = ps[o%c[e]]; }\n  };\n", side ? 'b' : 'a', X);
+            dsb_put(s, "\n      r%c[e] = ps[%s]; }\n  };\n", rr, off);
     }
 }
 
@@ -844,7 +870,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         if (op_type_is_float(k->ops[root].type)) dsb_put(&s, "  return f%u;\n}\n", root);
         else dsb_put(&s, "  return (float)n%u;\n}\n", root);
     }
-    const u32 M = ct->M, N = ct->N, K = ct->K;
+    const u32 M = ct->M, N = ct->N, K = pl->kp.on ? pl->kp.Kl : ct->K;   /* the reordered (padded) K */
     const u32 tiles = pl->tiles_m * pl->tiles_n;
     if (cf->direct) {
         emit_direct_kernel(&s, k, ct, pl);
@@ -862,17 +888,17 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
                     "  const u32 t = blockIdx.x * 256u + threadIdx.x;\n"
                     "  if (t >= %uu) return;\n"
                     "  const u32 k = t / %uu, n = t %% %uu;\n"
-                    "  pk[t] = ld_f32(p%u, c%u, kbase_qo(k) + rowb_q(gid_n(n)));\n}\n",
-                K * N, N, N, ct->sep_buf[1], ct->sep_buf[1]);
+                    "  pk[t] = (k %% %uu < %uu) ? ld_f32(p%u, c%u, kbase_qo(k) + rowb_q(gid_n(n))) : 0.0f;\n}\n",
+                pl->kp.Kl * N, N, N, pl->kp.Ep, pl->kp.E, ct->sep_buf[1], ct->sep_buf[1]);
     }
     dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", GEMM_THREADS, pl->name);
     emit_params(&s, k->n_leaves);
     dsb_put(&s, pl->pack ? ", float* ws, const float* pk) {\n" : ", float* ws) {\n");
     dsb_put(&s,
             "  constexpr u32 BM = %u, BN = %u, BK = %u, LDA = BM + %uu, LDB = BN + %uu;\n"
-            "  constexpr u32 M = %uu, N = %uu, K = %uu, TM = %uu, TN = %uu, TILES = %uu, KCH = %uu;\n"
+            "  constexpr u32 M = %uu, N = %uu, K = %uu, TM = %uu, TN = %uu, TILES = %uu, KCH = %uu, SPLITS = %uu;\n"
             "  constexpr u32 WM = %uu, WN = %uu, GN = %uu;\n",
-            cf->bm, cf->bn, BK, pl->pad_a, pl->pad_b, M, N, K, pl->tiles_m, pl->tiles_n, tiles, pl->kchunk,
+            cf->bm, cf->bn, BK, pl->pad_a, pl->pad_b, M, N, K, pl->tiles_m, pl->tiles_n, tiles, pl->kchunk, pl->splits,
             cf->wm_b * 32, cf->wn_b * 32, cf->gn);
     dsb_put(&s,
             "  __shared__ __attribute__((aligned(16))) float As[2][BK * LDA];\n"
@@ -880,16 +906,24 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
             "  const u32 tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;\n"
             "  /* XCD-aware tile order: workgroups go round-robin over 8 XCDs; give\n"
             "   * each XCD a compact block of tiles so their operand panels share L2 */\n"
-            "  u32 bid = blockIdx.x, tile = bid;\n"
+            "  u32 bid = blockIdx.x, spl = blockIdx.y;\n"
+            "  /* split K with few tiles: every tile of one split on the same XCD\n"
+            "   * (workgroup w runs on XCD w %% 8), so the split's shared panel is\n"
+            "   * fetched into one L2 */\n"
+            "  if (SPLITS > 1u && SPLITS %% 8u == 0u && TILES %% 8u != 0u) {\n"
+            "    const u32 lin = blockIdx.y * TILES + blockIdx.x, j = lin / 8u;\n"
+            "    spl = (j / TILES) * 8u + lin %% 8u; bid = j %% TILES; }\n"
+            "  u32 tile = bid;\n"
             "  if (TILES %% 8u == 0u) tile = (bid %% 8u) * (TILES / 8u) + bid / 8u;\n"
             "  u32 tm, tn;\n"
             "  { const u32 G = 8u; const u32 grp = tile / (G * TN), first = grp * G;\n"
             "    const u32 gsz = (TM - first) < G ? (TM - first) : G;\n"
             "    tm = first + (tile %% (G * TN)) %% gsz; tn = (tile %% (G * TN)) / gsz; }\n"
             "  const u32 m0 = tm * BM, n0 = tn * BN;\n"
-            "  const u32 kbeg = blockIdx.y * KCH;\n"
+            "  const u32 kbeg = spl * KCH;\n"
             "  const u32 kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
-            "  float ra[%u], rb[%u];\n", EA, EB);
+            "  float ra0[%u], rb0[%u];\n", EA, EB);
+    if (pl->depth == 2) dsb_put(&s, "  float ra1[%u], rb1[%u];\n", EA, EB);
     if (pl->kp.on) emit_kperm_loaders(&s, ct, pl);
     /* separable operands: per-row index bases, once per tile */
     if (!pl->kp.on && ct->sep[0]) {
@@ -903,7 +937,8 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         dsb_put(&s, " (void)kk; bB[e] = rowb_q(gid_n(n0 + nn)); }\n");
     }
     if (!pl->kp.on) {
-    dsb_put(&s, "  auto loadA = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EA);
+    dsb_put(&s, "  auto loadA = [&](u32 k0, float (&ra)[%u]) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
+            EA, EA);
     emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
     /* operands are evaluated unconditionally (every load is range-checked,
      * so any (m, k) is safe) and masked after: no divergent branches */
@@ -925,7 +960,8 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
     }
     dsb_put(&s, "      ra[e] = __uint_as_float(__float_as_uint(v) & ((%s && %s) ? 0xFFFFFFFFu : 0u)); }\n  };\n", gm,
             gk);
-    dsb_put(&s, "  auto loadB = [&](u32 k0) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", EB);
+    dsb_put(&s, "  auto loadB = [&](u32 k0, float (&rb)[%u]) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
+            EB, EB);
     emit_map(&s, ct->q_kmajor, cf->bn, cf->bk, "nn");
     dsb_put(&s, "\n      const u32 n = n0 + nn, k = k0 + kk;\n");
     if (ct->sep[1]) {
@@ -945,8 +981,8 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         const int kmaj = side ? ct->q_kmajor : ct->p_kmajor;
         const u32 bx = side ? cf->bn : cf->bm, ex = side ? EB : EA;
         if (pl->kp.on && pl->kp.vec[side]) {
-            dsb_put(&s, "  auto store%c = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", X,
-                    ex / 4u);
+            dsb_put(&s, "  auto store%c = [&](u32 buf, const float (&r%c)[%u]) {\n    #pragma unroll\n"
+                        "    for (u32 e = 0; e < %uu; e++) { ", X, r, ex, ex / 4u);
             emit_map4(&s, kmaj, bx, cf->bk, xn);
             if (kmaj)
                 dsb_put(&s, "\n      #pragma unroll\n      for (u32 j = 0; j < 4u; j++) %cs[buf][(kk + j) * %s + %s] = r%c[4u * e + j]; }\n  };\n",
@@ -957,7 +993,8 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
                         X, ld, xn, r, r, r, r);
             continue;
         }
-        dsb_put(&s, "  auto store%c = [&](u32 buf) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ", X, ex);
+        dsb_put(&s, "  auto store%c = [&](u32 buf, const float (&r%c)[%u]) {\n    #pragma unroll\n"
+                    "    for (u32 e = 0; e < %uu; e++) { ", X, r, ex, ex);
         emit_map(&s, kmaj, bx, cf->bk, xn);
         dsb_put(&s, " %cs[buf][kk * %s + %s] = r%c[e]; }\n  };\n", X, ld, xn, r);
     }
@@ -965,40 +1002,64 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
             "  f32x16 acc[%u];\n"
             "  #pragma unroll\n  for (u32 b = 0; b < %uu; b++) acc[b] = (f32x16){0};\n"
             "  const u32 wm = (wave / GN) * WM, wn = (wave %% GN) * WN;\n"
-            "  const u32 nst = (kend > kbeg) ? (kend - kbeg + BK - 1u) / BK : 0u;\n"
-            "  if (nst > 0u) { loadA(kbeg); loadB(kbeg); storeA(0u); storeB(0u); }\n"
-            "  __syncthreads();\n"
-            "  for (u32 st = 0; st < nst; st++) {\n"
-            "    const u32 cur = st & 1u;\n"
-            "    if (st + 1u < nst) { loadA(kbeg + (st + 1u) * BK); loadB(kbeg + (st + 1u) * BK); }\n"
-
-            "    const float* A = As[cur];\n"
-            "    const float* B = Bs[cur];\n"
-            "    /* all of the stage's fragments first, so LDS latency overlaps MFMAs */\n"
-            "    float a[BK / 2u][%u], b[BK / 2u][%u];\n"
-            "    #pragma unroll\n"
-            "    for (u32 kk = 0; kk < BK; kk += 2u) {\n"
-            "      const u32 kr = kk + (lane >> 5);\n"
-            "      #pragma unroll\n"
-            "      for (u32 i = 0; i < %uu; i++) a[kk / 2u][i] = A[kr * LDA + wm + i * 32u + (lane & 31u)];\n"
-            "      #pragma unroll\n"
-            "      for (u32 j = 0; j < %uu; j++) b[kk / 2u][j] = B[kr * LDB + wn + j * 32u + (lane & 31u)];\n"
-            "    }\n"
-            "    #pragma unroll\n"
-            "    for (u32 kk = 0; kk < BK / 2u; kk++)\n"
-            "      #pragma unroll\n"
-            "      for (u32 i = 0; i < %uu; i++)\n"
-            "        #pragma unroll\n"
-            "        for (u32 j = 0; j < %uu; j++)\n"
-            "          acc[i * %uu + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[i * %uu + j], 0, 0, 0);\n"
-            "    /* the next stage's global loads stay in flight across the MFMAs: the\n"
-            "     * LDS stores (which need them) may not move above the math */\n"
-            "    __builtin_amdgcn_sched_barrier(0);\n"
-            "    if (st + 1u < nst) { storeA(cur ^ 1u); storeB(cur ^ 1u); }\n"
-            "    __syncthreads();\n"
-            "  }\n",
-            NB, NB, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wn_b,
-            pl->swap ? "b[kk][j]" : "a[kk][i]", pl->swap ? "a[kk][i]" : "b[kk][j]", cf->wn_b);
+            "  const u32 nst = (kend > kbeg) ? (kend - kbeg + BK - 1u) / BK : 0u;\n",
+            NB, NB);
+    /* One stage: issue the global loads of stage st + depth into a register
+     * set, multiply the current LDS buffer, then move the registers of stage
+     * st + 1 (loaded depth - 1 stages earlier) into the other buffer. With
+     * depth 2 a load has two stages of math to arrive; the loop is unrolled
+     * by two so that each register set is a fixed array. */
+    char stage[4096];
+    const char *mfma_a = pl->swap ? "b[kk][j]" : "a[kk][i]", *mfma_b = pl->swap ? "a[kk][i]" : "b[kk][j]";
+    for (u32 ph = 0; ph < pl->depth; ph++) {
+        const u32 ls = pl->depth == 2 ? ph : 0u, ss = pl->depth == 2 ? 1u - ph : 0u;
+        snprintf(stage, sizeof stage,
+                 "    {\n"
+                 "    const u32 cur = st & 1u;\n"
+                 "    if (st + %uu < nst) { loadA(kbeg + (st + %uu) * BK, ra%u); loadB(kbeg + (st + %uu) * BK, rb%u); }\n"
+                 "    const float* A = As[cur];\n"
+                 "    const float* B = Bs[cur];\n"
+                 "    /* all of the stage's fragments first, so LDS latency overlaps MFMAs */\n"
+                 "    float a[BK / 2u][%u], b[BK / 2u][%u];\n"
+                 "    #pragma unroll\n"
+                 "    for (u32 kk = 0; kk < BK; kk += 2u) {\n"
+                 "      const u32 kr = kk + (lane >> 5);\n"
+                 "      #pragma unroll\n"
+                 "      for (u32 i = 0; i < %uu; i++) a[kk / 2u][i] = A[kr * LDA + wm + i * 32u + (lane & 31u)];\n"
+                 "      #pragma unroll\n"
+                 "      for (u32 j = 0; j < %uu; j++) b[kk / 2u][j] = B[kr * LDB + wn + j * 32u + (lane & 31u)];\n"
+                 "    }\n"
+                 "    #pragma unroll\n"
+                 "    for (u32 kk = 0; kk < BK / 2u; kk++)\n"
+                 "      #pragma unroll\n"
+                 "      for (u32 i = 0; i < %uu; i++)\n"
+                 "        #pragma unroll\n"
+                 "        for (u32 j = 0; j < %uu; j++)\n"
+                 "          acc[i * %uu + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[i * %uu + j], 0, 0, 0);\n"
+                 "    /* the next stages' global loads stay in flight across the MFMAs: the\n"
+                 "     * LDS stores (which need them) may not move above the math */\n"
+                 "    __builtin_amdgcn_sched_barrier(0);\n"
+                 "    if (st + 1u < nst) { storeA(cur ^ 1u, ra%u); storeB(cur ^ 1u, rb%u); }\n"
+                 "    __syncthreads();\n"
+                 "    }\n",
+                 pl->depth, pl->depth, ls, pl->depth, ls, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b,
+                 cf->wn_b, mfma_a, mfma_b, cf->wn_b, ss, ss);
+        if (ph == 0) {
+            if (pl->depth == 2)
+                dsb_put(&s, "  if (nst > 0u) { loadA(kbeg, ra0); loadB(kbeg, rb0); storeA(0u, ra0); storeB(0u, rb0); }\n"
+                            "  if (nst > 1u) { loadA(kbeg + BK, ra1); loadB(kbeg + BK, rb1); }\n"
+                            "  __syncthreads();\n"
+                            "  for (u32 st = 0; st < nst; st += 2u) {\n");
+            else
+                dsb_put(&s, "  if (nst > 0u) { loadA(kbeg, ra0); loadB(kbeg, rb0); storeA(0u, ra0); storeB(0u, rb0); }\n"
+                            "  __syncthreads();\n"
+                            "  for (u32 st = 0; st < nst; st++) {\n");
+            dsb_put(&s, "%s", stage);
+        } else {
+            dsb_put(&s, "  if (st + 1u < nst) {\n  const u32 st1 = st + 1u;\n  { const u32 st = st1;\n%s  }\n  }\n", stage);
+        }
+    }
+    dsb_put(&s, "  }\n");
     /* epilogue: D[i][j] of a 32x32 block sits in lane j + 32*((i/4)%%2), register (i%%4) + 4*(i/8);
      * D is the (m, n) block, or with swap its transpose (the MFMA took B as its first operand), so
      * that the 32 lanes of a store run along whichever output index is contiguous */
@@ -1173,18 +1234,30 @@ static int plan_kperm(const Contraction *ct, GemmPlan *pl) {
         kp->maxidx[s] = mx;
         if (mx > 0xFFFFFFFFull) return 0;
     }
-    /* the inner digit: the longest whose extent the stage depth divides */
+    /* the inner digit: the longest whose extent the stage depth divides;
+     * lanes along k stay coalesced only on a unit-stride inner digit, and a
+     * strided one is fine only for an operand that stays in cache (weights).
+     * Failing that, a digit that is unit-stride on every k-major side, padded
+     * up to a multiple of the stage depth (at most 1/4 more work): the image
+     * rows of a weight gradient (56 -> 64) */
     int best = -1;
-    for (u32 j = 0; j < nd; j++)
-        if (ext[j] % cf->bk == 0 && (best < 0 || ext[j] > ext[best])) best = (int)j;
-    if (best < 0) return 0;
-    /* lanes along k stay coalesced only on a unit-stride inner digit; a
-     * strided one is fine for an operand that stays in cache (weights) */
-    for (int s = 0; s < 2; s++) {
-        int kmaj = s ? ct->q_kmajor : ct->p_kmajor;
-        if (kmaj && co[s][best] != 1 && kp->maxidx[s] * 4 > (8ull << 20)) return 0;
+    for (int pass = 0; pass < 2 && best < 0; pass++) {
+        for (u32 j = 0; j < nd; j++) {
+            const u64 ep = (ext[j] + cf->bk - 1) / cf->bk * cf->bk;
+            if (pass == 0 ? ext[j] % cf->bk != 0 : (ext[j] % cf->bk == 0 || ext[j] % 4 != 0 || ep * 4 > ext[j] * 5))
+                continue;
+            int ok = 1;
+            for (int s = 0; s < 2; s++) {
+                int kmaj = s ? ct->q_kmajor : ct->p_kmajor;
+                if (kmaj && co[s][j] != 1 && (pass == 1 || kp->maxidx[s] * 4 > (8ull << 20))) ok = 0;
+            }
+            if (ok && (best < 0 || ext[j] > ext[best])) best = (int)j;
+        }
     }
+    if (best < 0) return 0;
     kp->E = (u32)ext[best];
+    kp->Ep = (u32)((ext[best] + cf->bk - 1) / cf->bk * cf->bk);
+    kp->Kl = (u32)(K / kp->E * kp->Ep);
     kp->buf[0] = ct->sep_buf[0];
     kp->buf[1] = ct->sep_buf[1];
     for (int s = 0; s < 2; s++) kp->icoef[s] = (u32)co[s][best];
@@ -1233,8 +1306,8 @@ static int plan_kperm(const Contraction *ct, GemmPlan *pl) {
             if (a->d[t].var == 0 && a->d[t].div != fdiv) ok = ok && a->coef[t] % 4 == 0;
         kp->vec[s] = ok;
     }
-    /* the big tile keeps no per-lane offset arrays (registers) */
-    if (cf->bm == 128 && !(kp->lin[0] && kp->lin[1])) {
+    /* the 128x128 tile keeps no per-lane offset arrays (registers) */
+    if (cf->bm == 128 && cf->bn == 128 && !(kp->lin[0] && kp->lin[1])) {
         memset(kp, 0, sizeof *kp);
         return 0;
     }
@@ -1280,7 +1353,7 @@ static void plan_pack(const Contraction *ct, GemmPlan *pl) {
     pl->pack = 0;
     if (!kp->on || hipb.dense_nopack || kp->vec[1] || pl->cfg.direct) return;
     const u32 per_lane = pl->cfg.bn * pl->cfg.bk / GEMM_THREADS;
-    if ((u64)ct->K * ct->N > (4u << 20) || ct->N % 4 != 0 || ct->N % pl->cfg.bn != 0 || per_lane % 4 != 0 ||
+    if ((u64)kp->Kl * ct->N > (4u << 20) || ct->N % 4 != 0 || ct->N % pl->cfg.bn != 0 || per_lane % 4 != 0 ||
         pl->tiles_m < 64)
         return;
     pl->kpo = *kp;
@@ -1288,20 +1361,41 @@ static void plan_pack(const Contraction *ct, GemmPlan *pl) {
     kp->lin[1] = 1;
     kp->lcoef[1] = 1;
     kp->icoef[1] = ct->N;
-    u64 place = kp->E;
+    u64 place = kp->Ep;
     for (u32 t = 0; t < kp->ndig; t++) {
         kp->ocoef[1][t] = (u32)(place * ct->N);
         place *= kp->oext[t];
     }
     kp->vec[1] = !hipb.dense_novec;
-    kp->maxidx[1] = (u64)ct->K * ct->N - 1;
+    kp->maxidx[1] = (u64)kp->Kl * ct->N - 1;
 }
+
+/* K chunk per split, in stage multiples, over the K the kernel loops on (the
+ * padded reordered K of a K-reordered plan). */
+static void plan_chunks(const Contraction *ct, GemmPlan *pl) {
+    const u32 K = pl->kp.on ? pl->kp.Kl : ct->K, splits = pl->splits_want ? pl->splits_want : 1;
+    u32 kch = (K + splits - 1) / splits;
+    kch = (kch + pl->cfg.bk - 1) / pl->cfg.bk * pl->cfg.bk;
+    pl->kchunk = kch;
+    pl->splits = (K + kch - 1) / kch;
+}
+
+static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const TileCfg *cfg);
 
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     static const TileCfg *forced[8] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
                                        &CFG_C64S};
+    const TileCfg cfg = hipb.dense_tile ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
+    make_plan_cfg(ct, pl, sig, &cfg);
+}
+
+static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const TileCfg *cfg) {
     memset(pl, 0, sizeof *pl);
-    pl->cfg = hipb.dense_tile ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
+    pl->cfg = *cfg;
+    /* two stages of loads in flight on the 128x64 tile (the weight gradients'
+     * long K over few tiles: measured 5-7 % faster there, 3 % slower on the
+     * 64x64 convolution and the 128x128 GEMM, whose occupancy it lowers) */
+    pl->depth = hipb.gemm_depth ? hipb.gemm_depth : (cfg->bm == 128 && cfg->bn == 64) ? 2u : 1u;
     if (!pl->cfg.direct && hipb.gemm_bk) pl->cfg.bk = hipb.gemm_bk;
     pl->tiles_m = (ct->M + pl->cfg.bm - 1) / pl->cfg.bm;
     pl->tiles_n = (ct->N + pl->cfg.bn - 1) / pl->cfg.bn;
@@ -1316,16 +1410,14 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     u32 splits = 1;
     while ((u64)tiles * splits < target && ct->K / (splits * 2) >= min_chunk && splits < 1024) splits *= 2;
     if (hipb.dense_splits) splits = hipb.dense_splits;
-    u32 kch = (ct->K + splits - 1) / splits;
-    kch = (kch + pl->cfg.bk - 1) / pl->cfg.bk * pl->cfg.bk;
-    pl->kchunk = kch;
-    pl->splits = (ct->K + kch - 1) / kch;
+    pl->splits_want = splits;
     snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));
     pl->swap = !pl->cfg.direct && !hipb.dense_noswap && ct->np > 0 && ct->pdiv[ct->np - 1] == 1 &&
                !(ct->nq > 0 && ct->qdiv[ct->nq - 1] == 1);
     plan_kperm(ct, pl);
     plan_pack(ct, pl);
     plan_pads(ct, pl);
+    plan_chunks(ct, pl);
 }
 
 /* Contraction analysis without a device: returns 1 and fills M/N/K when the
@@ -1399,6 +1491,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
             memset(&e->plan.kp, 0, sizeof e->plan.kp);
             e->plan.pack = 0;
             plan_pads(&ct, &e->plan);
+            plan_chunks(&ct, &e->plan);
         }
         char err[256] = {0};
         char *src = gen_gemm_source(k, &ct, &e->plan, err, sizeof err);
