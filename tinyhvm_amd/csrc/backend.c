@@ -285,7 +285,7 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         grid_for(e->total * e->splits, e->block, &gx, &gy);
         hipb_launch(e->fn, gx, gy, 1, e->block, params);
         void *p2[] = {&ptrs[0], &counts[0], &ws};
-        hipb_launch(e->fn_fin, (u32)((e->total + 255) / 256), 1, 1, 256, p2);
+        hipb_launch(e->fn_fin, (u32)e->total, 1, 1, 256, p2);   /* a workgroup per output */
         pool_mark_device_write(out_buf);
         return;
     }

@@ -1152,8 +1152,8 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
             G.red_block = 256;
         G.split_target = (e = getenv("THVM_HIP_SPLIT_TARGET")) ? (u32)atoi(e) : 4096;
         if (G.split_target < 1) G.split_target = 4096;
-        G.split_max = (e = getenv("THVM_HIP_SPLIT_MAX")) ? (u32)atoi(e) : 128;
-        if (G.split_max < 2 || G.split_max > 1024) G.split_max = 128;
+        G.split_max = (e = getenv("THVM_HIP_SPLIT_MAX")) ? (u32)atoi(e) : 512;
+        if (G.split_max < 2 || G.split_max > 1024) G.split_max = 512;
         G.per_thread = (e = getenv("THVM_HIP_EW_PER_THREAD")) ? (u32)atoi(e) : 1;
         if (G.per_thread < 1) G.per_thread = 1;
         if (G.per_thread > 8) G.per_thread = 8;
@@ -1256,20 +1256,29 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
     }
     sb_put(s, "}\n");
     if (G.splits > 1) {
+        /* combine: one workgroup per output; lane l takes partials l, l + 256,
+         * ... in order, then a fixed shuffle/LDS tree, then the initial value */
         const KOp *init = &k->ops[G.split_acc];
         u32 bits = init->imm.u;
         int rmax = G.oi[G.split_acc].acc_type == UOP_RMAX;
         sb_put(s, "extern \"C\" __global__ __launch_bounds__(256) void %s_fin(char* p0, u32 c0, const float* ws_) {\n"
-                  "  const u32 o = blockIdx.x * 256u + threadIdx.x;\n"
+                  "  const u32 o = blockIdx.x;\n"
                   "  if (o >= %uu) return;\n"
-                  "  float f = __uint_as_float(0x%08xu);\n"
-                  "  for (u32 s = 0; s < %uu; s++) {\n"
-                  "    const float w = ws_[(unsigned long long)o * %uu + s];\n"
+                  "  __shared__ float red_[4];\n"
+                  "  float w_ = %s;\n"
+                  "  for (u32 s = threadIdx.x; s < %uu; s += 256u) {\n"
+                  "    const float x_ = ws_[(unsigned long long)o * %uu + s];\n"
                   "    %s\n"
                   "  }\n"
-                  "  %s(p0, c0, o, f);\n}\n",
-               out->name, total, bits, G.splits, G.splits, rmax ? "f = (f > w) ? f : w;" : "f = f + w;",
-               dt_st(k->out_dtype));
+                  "  w_ = %s(w_, red_);\n"
+                  "  if (threadIdx.x == 0u) {\n"
+                  "    float f = __uint_as_float(0x%08xu);\n"
+                  "    %s\n"
+                  "    %s(p0, c0, o, f);\n"
+                  "  }\n}\n",
+               out->name, total, rmax ? "__uint_as_float(0xff800000u)" : "0.0f", G.splits, G.splits,
+               rmax ? "w_ = (w_ > x_) ? w_ : x_;" : "w_ = w_ + x_;", rmax ? "bmax" : "bsum", bits,
+               rmax ? "f = (f > w_) ? f : w_;" : "f = f + w_;", dt_st(k->out_dtype));
     }
     if (lanes)
         for (u32 i = 0; i < k->n_ops; i++) {
