@@ -28,6 +28,8 @@ $CAP lenet lenet_b2.trc 2 1
 $CAP convblock convblock_2x4x8.trc 2 4 8
 # the same at 28x28 (image rows not a multiple of the GEMM stage depth)
 $CAP convblock convblock_2x4x28.trc 2 4 28
+# 64 channels at 8x8 (the convolution's weights fill a 64-wide GEMM tile: operand packing)
+$CAP convblock convblock_1x64x8.trc 1 64 8
 # storage dtypes and casts
 $CAP dtypes dtypes.trc
 # ASSIGN from strided views (the contiguify slot)

@@ -84,6 +84,7 @@ static void read_dense_env(void) {
     hipb.dense_novec = env_flag("THVM_HIP_DENSE_NOVEC");
     hipb.dense_noswap = env_flag("THVM_HIP_DENSE_NOSWAP");
     hipb.dense_nopack = env_flag("THVM_HIP_DENSE_NOPACK");
+    hipb.dense_pack = env_flag("THVM_HIP_DENSE_PACK");
     const char *e = getenv("THVM_HIP_DENSE_SPLITS");
     hipb.dense_splits = e ? (u32)atoi(e) : 0;
     e = getenv("THVM_HIP_GEMM_PAD");

@@ -1354,7 +1354,7 @@ static void plan_pack(const Contraction *ct, GemmPlan *pl) {
     if (!kp->on || hipb.dense_nopack || kp->vec[1] || pl->cfg.direct) return;
     const u32 per_lane = pl->cfg.bn * pl->cfg.bk / GEMM_THREADS;
     if ((u64)kp->Kl * ct->N > (4u << 20) || ct->N % 4 != 0 || ct->N % pl->cfg.bn != 0 || per_lane % 4 != 0 ||
-        pl->tiles_m < 64)
+        (pl->tiles_m < 64 && !hipb.dense_pack))
         return;
     pl->kpo = *kp;
     pl->pack = 1;
