@@ -1019,7 +1019,9 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
                  "    if (st + %uu < nst) { loadA(kbeg + (st + %uu) * BK, ra%u); loadB(kbeg + (st + %uu) * BK, rb%u); }\n"
                  "    const float* A = As[cur];\n"
                  "    const float* B = Bs[cur];\n"
-                 "    /* all of the stage's fragments first, so LDS latency overlaps MFMAs */\n"
+                 "    /* the stage's fragments; the compiler interleaves their reads with the\n"
+                 "     * MFMAs (measured faster than pinning every read ahead of the math, which\n"
+                 "     * costs registers and occupancy: 8-24 %% slower) */\n"
                  "    float a[BK / 2u][%u], b[BK / 2u][%u];\n"
                  "    #pragma unroll\n"
                  "    for (u32 kk = 0; kk < BK; kk += 2u) {\n"
