@@ -539,6 +539,7 @@ typedef struct {
     u32 splits;
     u32 splits_want;       /* split count asked for; splits is what the K chunks give */
     u32 depth;             /* stages of global loads in flight ahead of the math (1 or 2) */
+    u32 nw;                /* direct kernel: waves per block, each taking every nw-th K step */
     u32 kchunk;
     u32 tiles_m, tiles_n;
     KPerm kp;
@@ -668,7 +669,7 @@ static void emit_operand_expr(DSB *s, const UOpKernel *k, const Contraction *ct,
 static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
     const u32 M = ct->M, N = ct->N, K = ct->K, KU = pl->cfg.bk;
     const u32 blocks = pl->tiles_m * pl->tiles_n;
-    dsb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", GEMM_THREADS, pl->name);
+    dsb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", 64u * pl->nw, pl->name);
     emit_params(s, k->n_leaves);
     dsb_put(s, ", float* ws) {\n");
     dsb_put(s,
@@ -682,7 +683,7 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
             "  const u32 kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
             "  const u32 i = lane & 31u, kh = lane >> 5;\n"
             "  const u32 ma = m0 + i, nb = n0 + i;\n",
-            M, N, K, pl->tiles_n, blocks, pl->kchunk, KU, GEMM_THREADS / 64);
+            M, N, K, pl->tiles_n, blocks, pl->kchunk, KU, pl->nw);
     if (ct->sep[0]) dsb_put(s, "  const u32 bA = ma < M ? rowb_p(gid_m(ma)) : 0u;\n");
     if (ct->sep[1]) dsb_put(s, "  const u32 bB = nb < N ? rowb_q(gid_n(nb)) : 0u;\n");
     dsb_put(s,
@@ -1380,6 +1381,18 @@ static void plan_chunks(const Contraction *ct, GemmPlan *pl) {
     kch = (kch + pl->cfg.bk - 1) / pl->cfg.bk * pl->cfg.bk;
     pl->kchunk = kch;
     pl->splits = (K + kch - 1) / kch;
+    /* direct kernel: its waves walk the chunk's K steps in turn, each step a
+     * chain of dependent loads and MFMAs; 8 waves when an unsplit K has more
+     * than 4 steps (measured on LeNet-5's fully connected weight gradients:
+     * 7.5 -> 6.2 us; its split-K convolution weight gradients got slower, 16
+     * -> 17 us, and 16 waves were slower everywhere, 12 -> 31 us on fc1: wave
+     * 0 then adds 15 partial blocks from 60 KB of LDS) */
+    pl->nw = 4;
+    if (pl->cfg.direct) {
+        const u32 steps = (kch + pl->cfg.bk - 1) / pl->cfg.bk;
+        if (hipb.direct_waves) pl->nw = hipb.direct_waves;
+        else if (steps > 4 && pl->splits == 1) pl->nw = 8;
+    }
 }
 
 static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const TileCfg *cfg);
@@ -1558,7 +1571,8 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         if (!hipb_launch_grid(e->fn_pack, (u32)((kn + 255) / 256), 1, 256, pp)) return 0;
     }
     u32 tiles = e->plan.tiles_m * e->plan.tiles_n;
-    if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, GEMM_THREADS, params)) return 0;
+    const u32 threads = e->plan.cfg.direct ? 64u * e->plan.nw : GEMM_THREADS;
+    if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, threads, params)) return 0;
     if (e->plan.splits > 1) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};
         u64 mn = (u64)e->M * e->N;
