@@ -67,8 +67,8 @@ WORKLOADS = {
                    "dist": "N(0,1)", "kernels_per_step": 2},
         "profile": "fused_8192x8192.md",
         "cpu": {"exe": "oracle/_ref/ref_replay", "kind": "reference",
-                "trace": os.path.join(WL, "fused_8192x8192.trc"), "marks": ("fused.fwd", "-"),
-                "sample": "the full step (fwd+bwd) at [8192,8192], 1 replay"},
+                "trace": os.path.join(WL, "fused_8192x8192.trc"), "marks": ("fused.fwd", "-"), "reps": 2,
+                "sample": "the full step (fwd+bwd) at [8192,8192], 2 replays"},
     },
     "matmul": {
         "trace": os.path.join(WL, "linear_4096.trc"),
@@ -81,9 +81,9 @@ WORKLOADS = {
         "profile": "matmul_4096.md",
         "cpu": {"exe": "oracle/_ref/ref_replay", "kind": "reference",
                 "trace": os.path.join(WL, "linear_8x4096x4096.trc"),
-                "marks": ("linear.fwd", "linear.bwd.dx"), "flops": 2 * 8 * 4096 * 4096,
+                "marks": ("linear.fwd", "linear.bwd.dx"), "flops": 2 * 8 * 4096 * 4096, "reps": 3,
                 "sample": "forward (GEMM + bias + relu) on an 8-row slice of X (8x4096 @ 4096x4096), "
-                          "the same kernels; GEMM throughput is linear in the rows"},
+                          "the same kernels, 3 replays; GEMM throughput is linear in the rows"},
     },
     "lenet": {
         "trace": os.path.join(WL, "lenet_b256.trc"),
@@ -96,8 +96,8 @@ WORKLOADS = {
                    "input": "U(0,1) [256,1,28,28]", "kernels_per_step": 54},
         "cpu": {"exe": "oracle/ora_replay", "kind": "port",
                 "trace": os.path.join(WL, "lenet_b64.trc"), "marks": ("lenet.step", "lenet.end"),
-                "batch_scale": 256 / 64,
-                "sample": "one training step at batch 64 (the same kernels at 1/4 the batch), "
+                "batch_scale": 256 / 64, "reps": 2,
+                "sample": "training steps at batch 64 (the same kernels at 1/4 the batch), 2 replays, "
                           "time scaled by 4; the engine's own CPU interpreter faults on the "
                           "padded convolution, so the oracle's restatement of it is timed "
                           "(1.4x slower than the engine's interpreter on the fused step)"},
@@ -111,8 +111,8 @@ WORKLOADS = {
                                "W2 [128,10] Kaiming-uniform, relu, softmax cross-entropy; outputs loss, "
                                "dW1, dW2", "batch": 64, "kernels_per_step": 20},
         "cpu": {"exe": "oracle/_ref/ref_replay", "kind": "reference",
-                "trace": os.path.join(WL, "mlp_64x784x128x10.trc"), "marks": ("mlp.fwd", "-"), "reps": 20,
-                "sample": "the full step, 20 replays (the engine's CPU backend)"},
+                "trace": os.path.join(WL, "mlp_64x784x128x10.trc"), "marks": ("mlp.fwd", "-"), "reps": 60,
+                "sample": "the full step, 60 replays (the engine's CPU backend)"},
     },
     "convblock": {
         "trace": os.path.join(WL, "convblock_b64.trc"),
