@@ -1,0 +1,74 @@
+"""The matrix-core plans the benchmark workloads get (no device needed).
+
+The plan choices are what the measured numbers rest on; this pins them so a
+change to the planner that silently drops one shows up here:
+- the 3x3 64->64 convolution (forward and input gradient): 64x64 tiles,
+  K-reordered loaders, its weights packed, the epilogue along the pixels;
+- its weight gradient: 128x64 tiles, 128 K splits, K-reordered loaders over
+  image rows padded 56 -> 64, two stages of loads in flight;
+- the 4096^3 GEMMs: 128x128 tiles, K-reordered loaders, 16-byte loads, the
+  epilogue along n (row-major output);
+- LeNet-5's fully connected weight gradients: the direct kernel with 8 waves.
+The device-free entry points read the tuning environment once per process;
+the CPU test run exports only THVM_HIP_DENSE_FORCE (routing), which leaves
+these contractions' plans as they are.
+"""
+import os
+import re
+
+from tinyhvm_amd import _lib, trace
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+WL = os.path.join(ROOT, "tinyhvm_amd", "workloads")
+
+
+def _plans(name):
+    out = {}
+    for r in trace.read_trace(os.path.join(WL, name)):
+        if r.tag != trace.UOP:
+            continue
+        k = trace.to_uop_kernel(r)
+        a = _lib.dense_analyze(k)
+        if not a:
+            continue
+        src = _lib.dense_source(k)
+        cst = re.search(r"constexpr u32 BM = (\d+), BN = (\d+), BK = (\d+)", src)
+        nw = re.search(r"NW = (\d+)u", src)
+        out[a] = {
+            "tile": (int(cst.group(1)), int(cst.group(2))) if cst else "direct",
+            "kperm": "kbase_p(" in src,
+            "padded": "lim_" in src,
+            "packed": "_pack(" in src,
+            "transposed": "(b[kk][j], a[kk][i]" in src,
+            "vec16": "*(const float4*)(ps" in src,
+            "two_stage": "ra1[" in src,
+            "waves": int(nw.group(1)) if nw else 4,
+        }
+    return out
+
+
+def test_convolution_plans():
+    p = _plans("convblock_b64.trc")
+    fwd = p[(200704, 64, 576, 1)]
+    assert fwd["tile"] == (64, 64) and fwd["kperm"] and fwd["packed"] and fwd["transposed"]
+    assert not fwd["padded"]
+    dw = p[(576, 64, 200704, 128)]
+    assert dw["tile"] == (128, 64) and dw["kperm"] and dw["padded"] and dw["two_stage"]
+    assert not dw["packed"]
+
+
+def test_gemm_4096_plans():
+    p = _plans("linear_4096.trc")
+    assert len(p) == 1 or all(v == list(p.values())[0] for v in p.values())
+    for a, v in p.items():
+        assert a[:3] == (4096, 4096, 4096)
+        assert v["tile"] == (128, 128) and v["kperm"] and v["vec16"]
+        assert not v["transposed"] and not v["packed"] and not v["two_stage"]
+
+
+def test_lenet_fc_weight_gradients_use_eight_waves():
+    p = _plans("lenet_b256.trc")
+    for shape in [(400, 120, 256, 1), (120, 84, 256, 1), (84, 10, 256, 1)]:
+        assert p[shape]["tile"] == "direct" and p[shape]["waves"] == 8, (shape, p[shape])
+    # split-K direct kernels keep 4 waves
+    assert p[(25, 6, 200704, 483)]["waves"] == 4
