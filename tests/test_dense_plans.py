@@ -4,7 +4,7 @@ The plan choices are what the measured numbers rest on; this pins them so a
 change to the planner that silently drops one shows up here:
 - the 3x3 64->64 convolution (forward and input gradient): 64x64 tiles,
   K-reordered loaders, its weights packed, the epilogue along the pixels;
-- its weight gradient: 128x64 tiles, 128 K splits, K-reordered loaders over
+- its weight gradient: 64x64 tiles, 128 K splits, K-reordered loaders over
   image rows padded 56 -> 64, two stages of loads in flight;
 - the 4096^3 GEMMs: 128x128 tiles, K-reordered loaders, 16-byte loads, the
   epilogue along n (row-major output);
@@ -53,7 +53,7 @@ def test_convolution_plans():
     assert fwd["tile"] == (64, 64) and fwd["kperm"] and fwd["packed"] and fwd["transposed"]
     assert not fwd["padded"]
     dw = p[(576, 64, 200704, 128)]
-    assert dw["tile"] == (128, 64) and dw["kperm"] and dw["padded"] and dw["two_stage"]
+    assert dw["tile"] == (64, 64) and dw["kperm"] and dw["padded"] and dw["two_stage"]
     assert not dw["packed"]
 
 

@@ -1159,17 +1159,28 @@ static DenseEntry *insert(u64 key, const UOpKernel *k) {
  * images, where its four waves share each operand stage; for 64 channels
  * (33..64 columns) the 64x64 tile on a tall convolution (231 us against 282
  * for 256x64 and 480 for the direct kernel on a 3x3 64->64 conv over
- * [64,64,56,56]) and the 128x64 tile on a weight gradient's long K (245 us
- * against 676); the direct kernel for the rest (fully connected layers, small
- * weight gradients). */
+ * [64,64,56,56]) and also on a weight gradient's long K (see long_k); the
+ * direct kernel for the rest (fully connected layers, small weight
+ * gradients). */
 static TileCfg pick_cfg(u32 M, u32 N, u32 K) {
     u64 big_tiles = (u64)((M + 127) / 128) * ((N + 127) / 128);
     if (M >= 128 && N >= 128 && big_tiles >= 128) return CFG_BIG;
     if (N <= 32 && M >= 4096) return CFG_TALL;
     if (M <= 32 && N >= 4096) return CFG_WIDE;
     if (N > 32 && N <= 64 && M >= 4096) return CFG_MID;
-    if (N > 32 && N <= 64 && M >= 256 && K >= 16384) return CFG_C64S;
+    if (N > 32 && N <= 64 && M >= 256 && K >= 16384) return CFG_MID;
     return CFG_DIRECT;
+}
+
+/* A weight gradient's shape: few output tiles (64-channel columns, a few
+ * hundred rows) over a long K. Such a contraction is bound by each
+ * workgroup's chain of dependent stages, so it takes twice the workgroups
+ * (about 1024) and two stages of loads in flight. Measured on the 3x3 64->64
+ * weight gradient over [64,64,56,56] (576x64x200704): 64x64 tiles with 128
+ * splits 190 us + 7.5 us sum, against 200 + 7.5 for 128x64 tiles with 128
+ * splits (their fifth row tile is half empty) and 210 for 64x64 with 64. */
+static int long_k(u32 M, u32 N, u32 K) {
+    return N > 32 && N <= 64 && M >= 256 && M < 4096 && K >= 16384;
 }
 
 static int cmp_u64(const void *x, const void *y) {
@@ -1407,10 +1418,11 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
 static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const TileCfg *cfg) {
     memset(pl, 0, sizeof *pl);
     pl->cfg = *cfg;
-    /* two stages of loads in flight on the 128x64 tile (the weight gradients'
-     * long K over few tiles: measured 5-7 % faster there, 3 % slower on the
-     * 64x64 convolution and the 128x128 GEMM, whose occupancy it lowers) */
-    pl->depth = hipb.gemm_depth ? hipb.gemm_depth : (cfg->bm == 128 && cfg->bn == 64) ? 2u : 1u;
+    /* two stages of loads in flight on the 128x64 tile and for long K (the
+     * weight gradients: measured 5-7 % faster there, 3 % slower on the 64x64
+     * convolution and the 128x128 GEMM, whose occupancy it lowers) */
+    const int lk = long_k(ct->M, ct->N, ct->K) && !hipb.dense_tile;
+    pl->depth = hipb.gemm_depth ? hipb.gemm_depth : ((cfg->bm == 128 && cfg->bn == 64) || lk) ? 2u : 1u;
     if (!pl->cfg.direct && hipb.gemm_bk) pl->cfg.bk = hipb.gemm_bk;
     pl->tiles_m = (ct->M + pl->cfg.bm - 1) / pl->cfg.bm;
     pl->tiles_n = (ct->N + pl->cfg.bn - 1) / pl->cfg.bn;
@@ -1421,7 +1433,7 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
     /* direct: 4 waves per block share its K range, so a split of c gives
      * each wave c/4; keep that >= 64 and aim for ~2048 waves */
     u32 min_chunk = pl->cfg.bm == 128 ? 512 : pl->cfg.direct ? 256 : 64;
-    u64 target = pl->cfg.direct ? 512 : 512;    /* workgroups */
+    u64 target = lk ? 1024 : 512;    /* workgroups */
     u32 splits = 1;
     while ((u64)tiles * splits < target && ct->K / (splits * 2) >= min_chunk && splits < 1024) splits *= 2;
     if (hipb.dense_splits) splits = hipb.dense_splits;
