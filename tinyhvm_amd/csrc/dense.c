@@ -634,16 +634,27 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
                 pl->name, (unsigned long long)M * N, pl->swap ? "n" : "m", pl->swap ? M : N, pl->swap ? "m" : "n",
                 pl->swap ? M : N, pl->splits, (unsigned long long)M * N, st, fb);
     } else {
+        /* many outputs: a workgroup per 64 outputs, lane l of wave w adding
+         * splits w, w+4, ... of output l in order; the 4 wave sums are then
+         * added in a fixed order (four times the workgroups of a lane per
+         * output over all splits, which is bound by its serial loads) */
         dsb_put(s_, "extern \"C\" __global__ __launch_bounds__(256) void %s_sum(char* p0, u32 c0, const float* ws) {\n"
-                    "  const unsigned long long t = (unsigned long long)blockIdx.x * 256u + threadIdx.x;\n"
-                    "  if (t >= %lluull) return;\n"
-                    "  const u32 %s = (u32)(t / %uu), %s = (u32)(t %% %uu);\n"
+                    "  __shared__ float part_[3][64];\n"
+                    "  const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;\n"
+                    "  const unsigned long long t = (unsigned long long)blockIdx.x * 64u + lane;\n"
                     "  float a = 0.0f;\n"
-                    "  #pragma unroll 8\n"
-                    "  for (u32 s = 0; s < %uu; s++) a = a + ws[(unsigned long long)s * %lluull + t];\n"
+                    "  if (t < %lluull) {\n"
+                    "    #pragma unroll 4\n"
+                    "    for (u32 s = wave; s < %uu; s += 4u) a = a + ws[(unsigned long long)s * %lluull + t];\n"
+                    "  }\n"
+                    "  if (wave > 0u) part_[wave - 1u][lane] = a;\n"
+                    "  __syncthreads();\n"
+                    "  if (wave > 0u || t >= %lluull) return;\n"
+                    "  a = ((a + part_[0][lane]) + part_[1][lane]) + part_[2][lane];\n"
+                    "  const u32 %s = (u32)(t / %uu), %s = (u32)(t %% %uu);\n"
                     "  %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n}\n",
-                pl->name, (unsigned long long)M * N, pl->swap ? "n" : "m", pl->swap ? M : N, pl->swap ? "m" : "n",
-                pl->swap ? M : N, pl->splits, (unsigned long long)M * N, st, fb);
+                pl->name, (unsigned long long)M * N, pl->splits, (unsigned long long)M * N, (unsigned long long)M * N,
+                pl->swap ? "n" : "m", pl->swap ? M : N, pl->swap ? "m" : "n", pl->swap ? M : N, st, fb);
     }
 }
 
@@ -1588,7 +1599,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     if (e->plan.splits > 1) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};
         u64 mn = (u64)e->M * e->N;
-        u64 per_block = sum_per_wave(&e->plan, mn) ? 4 : 256;
+        u64 per_block = sum_per_wave(&e->plan, mn) ? 4 : 64;
         if (!hipb_launch_grid(e->fn_sum, (u32)((mn + per_block - 1) / per_block), 1, 256, p2)) return 0;
     }
     return 1;
