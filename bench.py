@@ -358,7 +358,7 @@ def main():
         copy_calibration()
         return
     if args.gpus != 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path "
+        print("bench.py measures one GPU: this backend has no multi-GPU path "
               "(use --gpus 1)", file=sys.stderr)
         sys.exit(2)
     names = [w for w in args.workloads.split(",") if w]

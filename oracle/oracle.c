@@ -2,8 +2,8 @@
  * oracle.c - CPU restatement of the TinyHVM CPU backend's kernel semantics.
  *
  * TEST INFRASTRUCTURE ONLY. Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load this library, and only as the checker
- * (or as the timed CPU baseline). The product path (tinyhvm_amd) never calls it.
+ * cpu_baseline leg of bench.py may load this library, and only as the reference
+ * results are compared against (or as the timed CPU baseline). The product path (tinyhvm_amd) never calls it.
  *
  * It exports a host-memory Backend vtable (`oracle_backend`) so that kernel
  * traces can be replayed through it exactly as through the GPU backend.

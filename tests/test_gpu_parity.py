@@ -3,7 +3,7 @@
 Kernel-boundary parity: before each dispatch the GPU's actual input buffers
 are read back and the oracle (oracle/oracle.c, the CPU restatement of the
 engine's interpreter) runs the same kernel on them; the GPU output must match
-the oracle's under the kernel's tolerance class (the BASELINE north star):
+the oracle's under the kernel's tolerance class:
   - bit-exact: kernels a single lane evaluates in the reference's own order
     (elementwise, index/view work, casts, RMAX), the FusedOp fallback, the
     legacy per-op slots, strided copies (contiguify) and buffer copies;

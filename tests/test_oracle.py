@@ -91,7 +91,7 @@ def _run_uop(fn, rec, leaves_by_id, out_elems):
 @pytest.mark.parametrize("path", tt.fixtures("fused_3x1000.trc") + tt.fixtures("fused_64x256.trc"),
                          ids=lambda p: p.split("/")[-1])
 def test_exact_accumulation_mode(path):
-    """ora_dispatch_uop_exact (the checker of long sums): the fused forward's
+    """ora_dispatch_uop_exact (the reference for long sums): the fused forward's
     row sums equal the float64 sum of the same float32 terms rounded once, and
     a kernel without a sum (the backward) is bit-identical to the float mode."""
     from tests.test_gpu_parity import _oracle
