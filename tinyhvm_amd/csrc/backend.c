@@ -92,7 +92,7 @@ static void read_dense_env(void) {
     hipb.gemm_pad_k_set = e && hipb.gemm_pad_k <= 8;
     e = getenv("THVM_HIP_GEMM_BK");
     hipb.gemm_bk = e ? (u32)atoi(e) : 0;
-    if (hipb.gemm_bk != 16 && hipb.gemm_bk != 32) hipb.gemm_bk = 0;
+    if (hipb.gemm_bk != 16 && hipb.gemm_bk != 32 && hipb.gemm_bk != 64) hipb.gemm_bk = 0;
     e = getenv("THVM_HIP_DIRECT_WAVES");
     hipb.direct_waves = e ? (u32)atoi(e) : 0;
     if (hipb.direct_waves != 4 && hipb.direct_waves != 8 && hipb.direct_waves != 16) hipb.direct_waves = 0;
