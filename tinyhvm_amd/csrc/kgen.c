@@ -270,6 +270,18 @@ static int group_ok(Gen *g, char *why, size_t wlen) {
     return 1;
 }
 
+/* At most 64 outputs, and a top-level loop of at least 64 steps.
+ * THVM_HIP_TINY_SERIAL=1 keeps such kernels serial (in the CPU's order). */
+static int tiny_long_reduce(const Gen *g, u32 total) {
+    static int keep = -1;
+    if (keep < 0) { const char *e = getenv("THVM_HIP_TINY_SERIAL"); keep = e && e[0] == '1'; }
+    if (keep || total == 0 || total > 64) return 0;
+    const UOpKernel *k = g->k;
+    for (u32 i = 0; i < k->n_ops; i++)
+        if (k->ops[i].type == KOP_RANGE && g->oi[i].depth == 0 && k->ops[i].imm.u >= 64) return 1;
+    return 0;
+}
+
 /* Vector classification. In SERIAL mode the vector variable is the gid; in
  * GROUP mode it is the counter of the enclosing top-level loop, and ops
  * outside top-level loops are uniform. */
@@ -1186,6 +1198,13 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
     char why[128] = {0};
     G.mode = KG_MODE_SERIAL;
     if (k->local_size > 0 && group_ok(&G, why, sizeof why)) G.mode = KG_MODE_GROUP;
+    else if (k->local_size == 0 && tiny_long_reduce(&G, total) && group_ok(&G, why, sizeof why)) {
+        /* a handful of outputs over a long loop (a loss summed over the batch
+         * rows) would run as one or two threads walking the loop in order;
+         * a workgroup per output splits it across lanes instead, so its sum
+         * is ordered differently (the reductions' tolerance, not bit-exact) */
+        G.mode = KG_MODE_GROUP;
+    }
     if (G.mode == KG_MODE_SERIAL) {
         for (u32 i = 0; i < k->n_ops; i++) { G.oi[i].acc_tgt = 0; G.oi[i].acc_type = 0; }
     }
