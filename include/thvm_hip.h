@@ -95,19 +95,29 @@ void thvm_hip_profile_reset(void);
  *   thvm_hip_graph_begin    start capturing the stream (0, or -1)
  *   thvm_hip_graph_end      stop; the graph, or NULL when the captured calls
  *                           included work a graph cannot repeat (a host read
- *                           or synchronize, a write over 16 MiB, freeing
- *                           device memory)
+ *                           or synchronize, a write over 16 MiB)
  *   thvm_hip_graph_launch   run the captured work again (0, or -1)
  *   thvm_hip_graph_destroy  release it (waits for the stream)
  * Capture runs nothing on the device. A launch repeats the captured kernels
  * with their captured arguments and uploads on the current contents of the
- * buffers they touch; those buffers must stay allocated while the graph is
- * in use. */
+ * device memory they touch. That memory stays reserved for the graph until
+ * it is destroyed: buffers freed during or after the capture, and outgrown
+ * workspaces, are not handed to later allocations while a graph holds them.
+ * thvm_hip_shutdown releases every graph's device resources; a handle is
+ * still destroyed with thvm_hip_graph_destroy afterwards. */
 int   thvm_hip_graph_begin(void);
 void *thvm_hip_graph_end(void);
 int   thvm_hip_graph_launch(void *graph);
 void  thvm_hip_graph_destroy(void *graph);
 
+/* Counters, for tests and the engine-driven timing (no counterpart in the
+ * reference): out[0..9] = dispatches, matrix-core dispatches, compiled
+ * programs, program cache hits, dispatches run on the KOp interpreter
+ * (programs the generator or hipRTC refused; their outputs are still
+ * written), host waits on the stream, live device bytes, hipMalloc calls,
+ * device blocks pinned by HIP graphs, released blocks held for graphs.
+ * Returns the number of counters (10). */
+int  thvm_hip_counters(u64 *out, u32 n);
 /* Wait for all enqueued work; returns 0, or -1 on a device error. */
 int  thvm_hip_synchronize(void);
 /* The hipStream_t all work is ordered on (for timing with events). */

@@ -104,7 +104,25 @@ static void read_dense_env(void) {
     if (hipb.dense_tile > 7) hipb.dense_tile = 0;
 }
 
+hipError_t hipb_stream_wait(void) {
+    hipb.n_stream_sync++;
+    return hipStreamSynchronize(hipb.stream);
+}
+
+static void hb_shutdown(void);
+static void graphs_release_all(void);
+
+/* Process exit without a shutdown call (an engine program that never calls
+ * thvm_free, a script that just ends): the backend's stream, modules, graphs
+ * and memory are released here, while the HIP runtime is still up. The
+ * handler is registered after the runtime initialised, so it runs before the
+ * runtime's own exit-time teardown. */
+static void hb_atexit(void) {
+    if (hipb.initialized) hb_shutdown();
+}
+
 static int hb_init(void) {
+    static int atexit_done = 0;
     if (hipb.initialized) return 0;
     int n = 0;
     if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) {
@@ -130,19 +148,28 @@ static int hb_init(void) {
     hipb.dump_src = env_flag("THVM_HIP_DUMP");
     hipb.no_dense = env_flag("THVM_HIP_NO_DENSE");
     hipb.verbose = env_flag("THVM_HIP_VERBOSE");
+    hipb.force_interp = env_flag("THVM_HIP_INTERP");
+    hipb.rtc_fail = env_flag("THVM_HIP_RTC_FAIL");
     read_dense_env();
     if (pool_init() != 0) return -1;
     hipb.dummy = pool_block_get(256, &hipb.dummy_cap);
     if (!hipb.dummy || hipMemset(hipb.dummy, 0, 256) != hipSuccess) return -1;
     if (rtc_init() != 0) return -1;
     hipb.initialized = 1;
+    if (!atexit_done) {
+        atexit(hb_atexit);
+        atexit_done = 1;
+    }
     return 0;
 }
 
+/* Idempotent: every graph, module, workspace and buffer goes, then the
+ * stream. */
 static void hb_shutdown(void) {
     if (!hipb.initialized) return;
     copyq_flush();
-    HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    HIPB_CHECK(hipb_stream_wait());
+    graphs_release_all();
     dense_shutdown();
     rtc_shutdown();
     scratch_release(&red_ws);
@@ -213,6 +240,66 @@ static void grid_for(u64 blocks, u32 bx, u32 *gx, u32 *gy) {
 
 static float *reduce_workspace(u64 bytes) { return scratch_reserve(&red_ws, bytes); }
 
+static int kop_is_float(u32 t) {
+    return t == KOP_CONST_F || t == KOP_LOAD || t == KOP_ALU || t == KOP_ACC_INIT || t == KOP_MASK;
+}
+
+/* The KOp interpreter (static kernel thvm_kop): the engine's CPU semantics,
+ * one lane per gid, for a program that could not be compiled. A program
+ * whose loops do not nest runs nothing, as on the reference
+ * (src/backend/cpu/uop.c:118-155). */
+static void interp_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
+    hipFunction_t fn = rtc_static_fn("thvm_kop");
+    HipbBuf *ob = pool_get(out_buf);
+    if (!fn || !ob || k->n_ops > KOP_MAX) return;
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
+    KopParams *P = calloc(1, sizeof *P);
+    if (!P) return;
+    u32 stack[KOP_MAX], sp = 0;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        P->ops[i] = k->ops[i];
+        P->ftype[i] = (u8)kop_is_float(k->ops[i].type);
+        if (k->ops[i].type == KOP_RANGE) stack[sp++] = i;
+        else if (k->ops[i].type == KOP_ENDRANGE) {
+            if (sp == 0) { free(P); return; }
+            u32 r = stack[--sp];
+            P->pair[r] = (u16)i;
+            P->pair[i] = (u16)r;
+        }
+    }
+    if (sp != 0) { free(P); return; }
+    P->n_ops = k->n_ops;
+    P->out_ptr = (u64)(uintptr_t)ob->ptr;
+    P->out_n = elem_count(out_buf, k->out_dtype);
+    P->out_dtype = k->out_dtype;
+    u32 nl = n_leaves < k->n_leaves ? n_leaves : k->n_leaves;
+    if (nl > FUSE_MAX_LEAVES) nl = FUSE_MAX_LEAVES;
+    P->n_leaves = nl;
+    for (u32 i = 0; i < nl; i++) {
+        void *lp = pool_ptr(leaf_bufs[i]);
+        P->leaf_ptr[i] = (u64)(uintptr_t)lp;
+        P->leaf_dtype[i] = k->leaf_dtypes[i];
+        P->leaf_n[i] = lp ? elem_count(leaf_bufs[i], k->leaf_dtypes[i]) : 0u;
+    }
+    /* launch total as the reference counts it (u32 arithmetic) */
+    P->total = k->local_size > 0 ? k->grid[0] : k->grid[0] * k->grid[1] * k->grid[2];
+    u64 pcap = 0;
+    void *dp = pool_block_get(sizeof *P, &pcap);
+    if (!dp) { free(P); return; }
+    pool_upload(dp, P, sizeof *P);
+    const u32 chunk = 1u << 26;   /* gids per launch: 2^20 workgroups of 64 */
+    for (u64 base = 0; base < P->total; base += chunk) {
+        u32 b32 = (u32)base;
+        u64 n = P->total - base < chunk ? P->total - base : chunk;
+        void *params[] = {&dp, &b32};
+        hipb_launch(fn, (u32)((n + 63) / 64), 1, 1, 64, params);
+    }
+    pool_block_put(dp, pcap);   /* stream order keeps the block alive for the launches above */
+    pool_mark_device_write(out_buf);
+    hipb.n_fallback++;
+    free(P);
+}
+
 static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
                                    const UOpKernel *k, u64 cache_key) {
     (void)cache_key;
@@ -230,12 +317,18 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         hipb.n_dense++;
         return;
     }
+    if (hipb.force_interp) {
+        interp_dispatch(out_buf, leaf_bufs, n_leaves, k);
+        return;
+    }
     u64 key = uop_signature(k);
     KCacheEntry *e = rtc_lookup(key, k);
     if (e) hipb.n_cache_hit++;
     else e = rtc_compile_uop(key, k);
     if (!e) {
-        for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
+        /* the generator or hipRTC refused the program: the interpreter runs
+         * it, so the output is still written (counted in n_fallback) */
+        interp_dispatch(out_buf, leaf_bufs, n_leaves, k);
         return;
     }
 
@@ -567,14 +660,16 @@ static void hb_profile_report(void) {
     pool_stats(&live, &cached, &mallocs);
     fprintf(stderr,
             "tinyhvm-hip: dispatches=%llu dense=%llu compiled=%llu cache_hits=%llu "
-            "live=%.1fMB cached=%.1fMB hipMalloc=%llu\n",
+            "interpreted=%llu host_waits=%llu live=%.1fMB cached=%.1fMB hipMalloc=%llu\n",
             (unsigned long long)hipb.n_dispatch, (unsigned long long)hipb.n_dense,
             (unsigned long long)hipb.n_compile, (unsigned long long)hipb.n_cache_hit,
+            (unsigned long long)hipb.n_fallback, (unsigned long long)hipb.n_stream_sync,
             live / 1e6, cached / 1e6, (unsigned long long)mallocs);
 }
 
 static void hb_profile_reset(void) {
     hipb.n_dispatch = hipb.n_compile = hipb.n_cache_hit = hipb.n_dense = 0;
+    hipb.n_fallback = hipb.n_stream_sync = 0;
 }
 
 Backend hip_backend = {
@@ -653,11 +748,22 @@ void thvm_hip_pool_set_persistent(u32 max_buf) { hb_pool_set_persistent(max_buf)
 void thvm_hip_profile_report(void) { hb_profile_report(); }
 void thvm_hip_profile_reset(void) { hb_profile_reset(); }
 
+int thvm_hip_counters(u64 *out, u32 n) {
+    u64 live = 0, cached = 0, mallocs = 0;
+    u32 pinned = 0, limbo = 0;
+    pool_stats(&live, &cached, &mallocs);
+    pool_pin_stats(&pinned, &limbo);
+    u64 v[10] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
+                 hipb.n_stream_sync, live, mallocs, pinned, limbo};
+    for (u32 i = 0; out && i < n && i < 10; i++) out[i] = v[i];
+    return 10;
+}
+
 int thvm_hip_synchronize(void) {
     if (!hipb.initialized) return -1;
     if (pool_capture_forbids("a synchronize")) return -1;
     copyq_flush();
-    hipError_t e = hipStreamSynchronize(hipb.stream);
+    hipError_t e = hipb_stream_wait();
     if (e != hipSuccess) {
         fprintf(stderr, "tinyhvm-hip: stream error: %s\n", hipGetErrorString(e));
         return -1;
@@ -769,19 +875,43 @@ int thvm_hip_compile_check(const UOpKernel *k, char *errbuf, u64 errlen) {
  * it starts, and the host's record of what the device holds stays
  * conservative (a buffer a captured kernel writes is read back from the
  * device; a host write made during the capture is uploaded again for eager
- * use). Work a graph cannot repeat (a host read, a
- * synchronize, a large synchronous write, freeing device memory) abandons
- * the capture: graph_end then returns NULL. No memset is ever recorded (the
- * dispatch path clears with kernels). */
+ * use). Every device block the captured work touches is pinned
+ * to the graph (pool.c): while the graph lives, such a block never returns
+ * to the free lists, even when its buffer id is freed or a workspace grows,
+ * so no later allocation can alias memory the graph writes. Work a graph
+ * cannot repeat (a host read, a synchronize, a large synchronous write)
+ * abandons the capture: graph_end then returns NULL. No memset is ever
+ * recorded (the dispatch path clears with kernels). */
 #define GRAPH_ARENA_BYTES (4u << 20)
 
-typedef struct {
+typedef struct HipbGraph {
     hipGraph_t graph;
     hipGraphExec_t exec;
     u8 *arena;
+    PoolPins pins;           /* device blocks the captured work references */
+    struct HipbGraph *next;  /* live graphs, released at shutdown */
+    int released;
 } HipbGraph;
 
 static HipbGraph *g_capture;
+static HipbGraph *g_live;
+
+/* device-side resources of a graph; the handle itself stays until destroy */
+static void graph_release(HipbGraph *g) {
+    if (g->released) return;
+    if (g->exec) HIPB_CHECK(hipGraphExecDestroy(g->exec));
+    if (g->graph) HIPB_CHECK(hipGraphDestroy(g->graph));
+    if (g->arena) HIPB_CHECK(hipHostFree(g->arena));
+    g->exec = NULL;
+    g->graph = NULL;
+    g->arena = NULL;
+    pool_pins_release(&g->pins);
+    g->released = 1;
+}
+
+static void graphs_release_all(void) {
+    for (HipbGraph *g = g_live; g; g = g->next) graph_release(g);
+}
 
 int thvm_hip_graph_begin(void) {
     if (!hipb.initialized || hipb.capturing) return -1;
@@ -801,9 +931,9 @@ int thvm_hip_graph_begin(void) {
         free(g);
         return -1;
     }
-    pool_capture_begin(g->arena, GRAPH_ARENA_BYTES);
     hipb.capturing = 1;
     hipb.capture_bad = 0;
+    pool_capture_begin(g->arena, GRAPH_ARENA_BYTES, &g->pins);
     g_capture = g;
     return 0;
 }
@@ -823,19 +953,19 @@ void *thvm_hip_graph_end(void) {
             (void)hipGetLastError();
             fprintf(stderr, "tinyhvm-hip: graph capture failed: %s\n", hipGetErrorString(e));
         }
-        if (g->exec) HIPB_CHECK(hipGraphExecDestroy(g->exec));
-        if (g->graph) HIPB_CHECK(hipGraphDestroy(g->graph));
-        HIPB_CHECK(hipHostFree(g->arena));
+        graph_release(g);
         free(g);
         hipb.capture_bad = 0;
         return NULL;
     }
+    g->next = g_live;
+    g_live = g;
     return g;
 }
 
 int thvm_hip_graph_launch(void *handle) {
     HipbGraph *g = handle;
-    if (!hipb.initialized || hipb.capturing || !g || !g->exec) return -1;
+    if (!hipb.initialized || hipb.capturing || !g || g->released || !g->exec) return -1;
     copyq_flush();
     /* host writes since the capture reach the buffers the graph reads, and
      * the host's copies of whatever it writes are no longer current */
@@ -851,9 +981,14 @@ int thvm_hip_graph_launch(void *handle) {
 void thvm_hip_graph_destroy(void *handle) {
     HipbGraph *g = handle;
     if (!g) return;
-    if (hipb.initialized) HIPB_CHECK(hipStreamSynchronize(hipb.stream));
-    if (g->exec) HIPB_CHECK(hipGraphExecDestroy(g->exec));
-    if (g->graph) HIPB_CHECK(hipGraphDestroy(g->graph));
-    if (g->arena) HIPB_CHECK(hipHostFree(g->arena));
+    if (!g->released) {
+        if (hipb.initialized) HIPB_CHECK(hipb_stream_wait());
+        graph_release(g);
+    }
+    for (HipbGraph **pp = &g_live; *pp; pp = &(*pp)->next)
+        if (*pp == g) {
+            *pp = g->next;
+            break;
+        }
     free(g);
 }

@@ -308,6 +308,10 @@ static int dense_debug(void) {
 static int recognize(const UOpKernel *k, Contraction *ct) {
     memset(ct, 0, sizeof *ct);
     if (k->n_ops == 0 || k->n_ops > KOP_MAX) REJECT("line 2");
+    /* operands name earlier ops, loops nest, types are known: the analyses
+     * below follow operand indices without further checks */
+    char verr[128];
+    if (!kgen_validate(k, verr, sizeof verr)) REJECT("invalid program");
     /* one top-level loop, no nesting */
     i32 R = -1;
     u32 E = 0;

@@ -55,7 +55,11 @@ typedef struct {
     int dense_pack;          /* THVM_HIP_DENSE_PACK: pack wherever the layout allows (tests) */
     u32 dense_tile;          /* THVM_HIP_DENSE_TILE: 0 chosen, 1 128x128, 2 64x64, 3 256x32, 4 32x256, 5 direct,
                                 6 256x64, 7 128x64 */
+    int force_interp;        /* THVM_HIP_INTERP: run generated-kernel programs on the KOp interpreter */
+    int rtc_fail;            /* THVM_HIP_RTC_FAIL: treat every program compile as failed (tests) */
     u64 n_dispatch, n_compile, n_cache_hit, n_dense;
+    u64 n_fallback;          /* dispatches run on the KOp interpreter */
+    u64 n_stream_sync;       /* host waits on the stream (buf_read, synchronize, ...) */
     hipModule_t static_mod;  /* precompiled kernels */
     int capturing;           /* a graph capture is open on the stream */
     int capture_bad;         /* the open capture met work a graph cannot replay */
@@ -70,9 +74,15 @@ extern HipbState hipb;
  * the host marks the capture unusable instead. */
 void pool_sync_all_device(void);
 void pool_device_wrote_all(void);
-void pool_capture_begin(u8 *arena, u64 bytes);
+/* the device blocks one graph references (each holds one pin) */
+typedef struct { void **ptr; u32 n, cap; } PoolPins;
+void pool_capture_begin(u8 *arena, u64 bytes, PoolPins *pins);
 void pool_capture_end(void);
 int  pool_capture_forbids(const char *what);
+void pool_pins_release(PoolPins *pins);
+void pool_pin_stats(u32 *pinned, u32 *limbo);
+/* hipStreamSynchronize on the backend's stream, counted */
+hipError_t hipb_stream_wait(void);
 typedef struct {
     void *ptr;        /* device pointer, NULL if free */
     u64 bytes;        /* requested bytes */

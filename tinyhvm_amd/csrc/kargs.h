@@ -67,4 +67,20 @@ typedef struct {
     u32 n, vec;
 } AdamArgs;
 
+/* KOp interpreter (the dispatch_uop_kernel fallback when a program cannot be
+ * compiled): the program plus its loop pairing and the buffers, copied to
+ * device memory per dispatch. pair[i] of a RANGE is its ENDRANGE and of an
+ * ENDRANGE its RANGE; ftype[i] = 1 for ops whose value is a float. */
+typedef struct {
+    u64 out_ptr;
+    u32 out_n, out_dtype;
+    u64 leaf_ptr[FUSE_MAX_LEAVES];
+    u32 leaf_n[FUSE_MAX_LEAVES];
+    u32 leaf_dtype[FUSE_MAX_LEAVES];
+    u32 n_ops, n_leaves, total, pad;
+    u16 pair[KOP_MAX];
+    u8 ftype[KOP_MAX];
+    KOp ops[KOP_MAX];
+} KopParams;
+
 #endif

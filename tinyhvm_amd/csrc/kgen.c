@@ -914,7 +914,9 @@ int kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, con
     for (u32 i = 0; i < k->n_ops; i++) {
         if (!cone[i]) continue;
         const KOp *op = &k->ops[i];
-        int fa = op_is_float(k->ops[op->arg[0]].type), fbt = op_is_float(k->ops[op->arg[1]].type);
+        /* operand types; the args of ops without operands may hold anything */
+        int fa = op->arg[0] < k->n_ops && op_is_float(k->ops[op->arg[0]].type);
+        int fbt = op->arg[1] < k->n_ops && op_is_float(k->ops[op->arg[1]].type);
 #define UA(x, ft) ((ft) ? (snprintf(a, sizeof a, "f2u(f%u)", (x)), a) : (snprintf(a, sizeof a, "n%u", (x)), a))
         switch (op->type) {
         case KOP_GID: sb_put(&sb, "  const u32 n%u = %s;\n", i, gid_expr); break;

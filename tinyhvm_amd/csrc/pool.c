@@ -14,6 +14,21 @@
  * by the host may be handed to a later dispatch without waiting: the stream
  * orders the old readers before the new writer.
  *
+ * HIP graphs: a captured graph keeps the raw device addresses of every block
+ * its work touched, and writes them again at each launch. Such a block is
+ * pinned: every block resolved while a capture is open (buffers named by the
+ * captured calls, kernel workspaces, parameter blocks) is entered in a pin
+ * table with one count per graph holding it. A pinned block that is released
+ * (its id freed or reset, a workspace outgrown) waits in limbo instead of the
+ * free list, so no later allocation can receive memory a graph still writes;
+ * when its last graph is destroyed it returns to the free list.
+ *
+ * Ids stop below 16384: the engine tracks buffer epochs for its kernel result
+ * cache only for ids under MAX_BUF_EPOCHS (src/tinyhvm.h:720), and its CPU
+ * and Metal pools hold MAX_BUFS = 16384 ids (src/backend/cpu/pool.c:4,
+ * src/backend/metal/pool.m:50). Past that, buf_alloc fails (returns 0) until
+ * a pool_reset recycles ids.
+ *
  * Host copies: writes of at most 4 KiB are kept in a host mirror and reach
  * the device only when something on the device first needs the buffer (a
  * dispatch reading or writing it, a copy, a synchronous read): the engine
@@ -33,11 +48,20 @@
 #define POOL_MIRROR_MAX 4096ull
 #define STAGE_SEGMENTS 4
 #define STAGE_SEG_BYTES (16ull << 20)
+#define POOL_MAX_IDS 16384u
 
 typedef struct {
     void **ptrs;
     u32 n, cap;
 } FreeList;
+
+/* pin table entry: a block some graph references, and how many graphs do */
+typedef struct {
+    void *ptr;
+    u64 cap;
+    u32 pins;
+    u32 seq;       /* the capture that pinned it last (one count per capture) */
+} PinEnt;
 
 static struct {
     HipbBuf *bufs;
@@ -56,13 +80,104 @@ static struct {
     u8 *arena;
     u64 arena_cap, arena_off;
     u32 capture_seq;      /* numbers the captures; buffers record the one they were written in */
+    PoolPins *capture_pins; /* blocks the open capture references */
+    /* pinned blocks (open addressing on the address) and released pinned blocks */
+    PinEnt *pin;
+    u32 pin_cap, pin_n;
+    void **limbo;
+    u64 *limbo_cap;
+    u32 limbo_n, limbo_max;
 } P;
 
-void pool_capture_begin(u8 *arena, u64 bytes) {
+static u32 pin_slot(const void *p) {
+    return (u32)((((uintptr_t)p >> 8) * 0x9E3779B97F4A7C15ull) >> 32) & (P.pin_cap - 1);
+}
+
+static PinEnt *pin_find(const void *p) {
+    if (!P.pin_cap || !p) return NULL;
+    for (u32 i = pin_slot(p);; i = (i + 1) & (P.pin_cap - 1)) {
+        if (!P.pin[i].ptr) return NULL;
+        if (P.pin[i].ptr == p) return &P.pin[i];
+    }
+}
+
+static int pin_grow(void) {
+    u32 nc = P.pin_cap ? P.pin_cap * 2 : 256;
+    PinEnt *old = P.pin, *nt = calloc(nc, sizeof(PinEnt));
+    u32 oc = P.pin_cap;
+    if (!nt) return 0;
+    P.pin = nt;
+    P.pin_cap = nc;
+    for (u32 i = 0; i < oc; i++) {
+        if (!old[i].ptr) continue;
+        u32 j = pin_slot(old[i].ptr);
+        while (P.pin[j].ptr) j = (j + 1) & (nc - 1);
+        P.pin[j] = old[i];
+    }
+    free(old);
+    return 1;
+}
+
+/* Removes slot i, shifting later entries of its probe run back into place. */
+static void pin_erase(u32 i) {
+    u32 mask = P.pin_cap - 1, j = i;
+    for (;;) {
+        j = (j + 1) & mask;
+        if (!P.pin[j].ptr) break;
+        u32 k = pin_slot(P.pin[j].ptr);
+        /* entry j may move to i unless its home slot k lies cyclically in (i, j] */
+        int stays = (i <= j) ? (k > i && k <= j) : (k > i || k <= j);
+        if (!stays) {
+            P.pin[i] = P.pin[j];
+            i = j;
+        }
+    }
+    memset(&P.pin[i], 0, sizeof(PinEnt));
+    P.pin_n--;
+}
+
+/* Records that the open capture references a block (once per capture). */
+static void capture_pin(void *ptr, u64 cap) {
+    if (!hipb.capturing || !ptr || !P.capture_pins) return;
+    PinEnt *e = pin_find(ptr);
+    if (e && e->seq == P.capture_seq) return;
+    PoolPins *pp = P.capture_pins;
+    if (pp->n == pp->cap) {
+        u32 nc = pp->cap ? pp->cap * 2 : 64;
+        void **np = realloc(pp->ptr, nc * sizeof(void *));
+        if (!np) {
+            pool_capture_forbids("pin bookkeeping out of host memory");
+            return;
+        }
+        pp->ptr = np;
+        pp->cap = nc;
+    }
+    if (!e) {
+        if ((P.pin_n + 1) * 2 > P.pin_cap && !pin_grow()) {
+            pool_capture_forbids("pin bookkeeping out of host memory");
+            return;
+        }
+        u32 j = pin_slot(ptr);
+        while (P.pin[j].ptr) j = (j + 1) & (P.pin_cap - 1);
+        e = &P.pin[j];
+        e->ptr = ptr;
+        e->cap = cap;
+        e->pins = 0;
+        P.pin_n++;
+    }
+    e->pins++;
+    e->seq = P.capture_seq;
+    pp->ptr[pp->n++] = ptr;
+}
+
+void pool_capture_begin(u8 *arena, u64 bytes, PoolPins *pins) {
     P.capture_seq++;
     P.arena = arena;
     P.arena_cap = bytes;
     P.arena_off = 0;
+    P.capture_pins = pins;
+    /* the fill block of absent buffers is in every graph's kernels */
+    capture_pin(hipb.dummy, hipb.dummy_cap);
 }
 
 void pool_capture_end(void) {
@@ -74,6 +189,7 @@ void pool_capture_end(void) {
     }
     P.arena = NULL;
     P.arena_cap = P.arena_off = 0;
+    P.capture_pins = NULL;
 }
 
 int pool_capture_forbids(const char *what) {
@@ -110,9 +226,73 @@ static int fl_push(FreeList *f, void *p) {
     return 1;
 }
 
+/* A released block: to limbo while a graph references it, else to its
+ * class's free list (or back to HIP if the list cannot grow). */
+static void block_release(void *ptr, u64 cap) {
+    if (!ptr) return;
+    if (pin_find(ptr)) {
+        if (P.limbo_n == P.limbo_max) {
+            u32 nc = P.limbo_max ? P.limbo_max * 2 : 64;
+            void **np = realloc(P.limbo, nc * sizeof(void *));
+            u64 *nq = realloc(P.limbo_cap, nc * sizeof(u64));
+            if (np) P.limbo = np;
+            if (nq) P.limbo_cap = nq;
+            if (!np || !nq) {
+                /* cannot track it: leak the block rather than reuse it */
+                fprintf(stderr, "tinyhvm-hip: out of host memory; a graph-held block is leaked\n");
+                return;
+            }
+            P.limbo_max = nc;
+        }
+        P.limbo[P.limbo_n] = ptr;
+        P.limbo_cap[P.limbo_n] = cap;
+        P.limbo_n++;
+        return;
+    }
+    u64 c2 = 0;
+    u32 c = size_class(cap, &c2);
+    if (fl_push(&P.free[c], ptr)) P.cached_bytes += c2;
+    else if (!pool_capture_forbids("a block free")) {
+        HIPB_CHECK(hipb_stream_wait());
+        HIPB_CHECK(hipFree(ptr));
+    }
+}
+
+/* A graph is gone: its blocks lose one pin each; released blocks no graph
+ * holds any more leave limbo for the free lists. */
+void pool_pins_release(PoolPins *pp) {
+    if (!pp) return;
+    for (u32 i = 0; i < pp->n; i++) {
+        PinEnt *e = pin_find(pp->ptr[i]);
+        if (!e) continue;
+        if (e->pins > 1) {
+            e->pins--;
+            continue;
+        }
+        void *ptr = e->ptr;
+        pin_erase((u32)(e - P.pin));
+        for (u32 j = 0; j < P.limbo_n; j++) {
+            if (P.limbo[j] != ptr) continue;
+            u64 cap = P.limbo_cap[j];
+            P.limbo_n--;
+            P.limbo[j] = P.limbo[P.limbo_n];
+            P.limbo_cap[j] = P.limbo_cap[P.limbo_n];
+            block_release(ptr, cap);
+            break;
+        }
+    }
+    free(pp->ptr);
+    memset(pp, 0, sizeof *pp);
+}
+
+void pool_pin_stats(u32 *pinned, u32 *limbo) {
+    if (pinned) *pinned = P.pin_n;
+    if (limbo) *limbo = P.limbo_n;
+}
+
 static void release_cache(void) {
     if (pool_capture_forbids("device memory exhausted")) return;
-    HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    HIPB_CHECK(hipb_stream_wait());
     for (u32 c = 0; c < POOL_N_CLASSES; c++) {
         for (u32 i = 0; i < P.free[c].n; i++) HIPB_CHECK(hipFree(P.free[c].ptrs[i]));
         P.free[c].n = 0;
@@ -139,12 +319,16 @@ int pool_init(void) {
 
 void pool_shutdown(void) {
     if (!P.bufs) return;
-    HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+    HIPB_CHECK(hipb_stream_wait());
     for (u32 i = 1; i < P.count; i++) {
         if (P.bufs[i].live && P.bufs[i].ptr) HIPB_CHECK(hipFree(P.bufs[i].ptr));
         free(P.bufs[i].host_mirror);
     }
     release_cache();
+    for (u32 j = 0; j < P.limbo_n; j++) HIPB_CHECK(hipFree(P.limbo[j]));
+    free(P.limbo);
+    free(P.limbo_cap);
+    free(P.pin);
     for (u32 c = 0; c < POOL_N_CLASSES; c++) free(P.free[c].ptrs);
     for (u32 s = 0; s < STAGE_SEGMENTS; s++) HIPB_CHECK(hipEventDestroy(P.seg_done[s]));
     if (P.stage) HIPB_CHECK(hipHostFree(P.stage));
@@ -187,24 +371,22 @@ void *pool_block_get(u64 bytes, u64 *cap_out) {
         P.n_mallocs++;
     }
     *cap_out = cap;
+    capture_pin(ptr, cap);
     return ptr;
 }
 
-/* Returns a block to its free list. The stream orders its last users before
- * any later owner's work. */
-void pool_block_put(void *ptr, u64 cap) {
-    if (!ptr) return;
-    u64 c2 = 0;
-    u32 c = size_class(cap, &c2);
-    if (fl_push(&P.free[c], ptr)) P.cached_bytes += c2;
-    else if (!pool_capture_forbids("a block free")) HIPB_CHECK(hipFree(ptr));
-}
+/* Returns a block to its free list (to limbo while a graph holds it). The
+ * stream orders its last users before any later owner's work. */
+void pool_block_put(void *ptr, u64 cap) { block_release(ptr, cap); }
 
 /* Device scratch outside the engine's buffer ids (kernel workspaces): grown
  * on demand, kept until released. Engine ids are never used for it, so
  * pool_reset cannot free it and the engine's id numbering is untouched. */
 void *scratch_reserve(Scratch *sc, u64 bytes) {
-    if (bytes <= sc->cap && sc->ptr) return sc->ptr;
+    if (bytes <= sc->cap && sc->ptr) {
+        capture_pin(sc->ptr, sc->cap);
+        return sc->ptr;
+    }
     pool_block_put(sc->ptr, sc->cap);
     sc->ptr = pool_block_get(bytes, &sc->cap);
     if (!sc->ptr) sc->cap = 0;
@@ -219,6 +401,11 @@ void scratch_release(Scratch *sc) {
 
 u32 pool_alloc(u64 bytes) {
     if (!hipb.initialized) return 0;
+    if (P.count >= POOL_MAX_IDS) {
+        fprintf(stderr, "tinyhvm-hip: buffer ids exhausted (%u ids; pool_reset recycles them)\n",
+                POOL_MAX_IDS - 1);
+        return 0;
+    }
     u64 cap = 0;
     void *ptr = pool_block_get(bytes, &cap);
     if (!ptr) return 0;
@@ -243,14 +430,7 @@ u32 pool_alloc(u64 bytes) {
 }
 
 static void release_block(HipbBuf *b) {
-    u64 cap = 0;
-    u32 c = size_class(b->cap, &cap);
-    if (fl_push(&P.free[c], b->ptr)) {
-        P.cached_bytes += b->cap;
-    } else if (!pool_capture_forbids("a block free")) {
-        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
-        HIPB_CHECK(hipFree(b->ptr));
-    }
+    block_release(b->ptr, b->cap);
     P.live_bytes -= b->cap;
     b->ptr = NULL;
     b->live = 0;
@@ -290,7 +470,9 @@ void pool_set_persistent(u32 max_buf) { P.persistent_floor = max_buf; }
 
 HipbBuf *pool_get(u32 id) {
     if (id == 0 || id >= P.count || !P.bufs[id].live) return NULL;
-    return &P.bufs[id];
+    HipbBuf *b = &P.bufs[id];
+    capture_pin(b->ptr, b->cap);
+    return b;
 }
 
 void *pool_ptr(u32 id) {
@@ -388,6 +570,7 @@ static u8 *stage_reserve(u64 n) {
         P.seg_pending[P.seg] = 1;
         P.seg = (P.seg + 1) % STAGE_SEGMENTS;
         if (P.seg_pending[P.seg]) {
+            hipb.n_stream_sync++;
             HIPB_CHECK(hipEventSynchronize(P.seg_done[P.seg]));
             P.seg_pending[P.seg] = 0;
         }
@@ -428,7 +611,7 @@ void pool_write(u32 id, const void *data, u64 bytes) {
         HIPB_CHECK(hipMemcpyAsync(b->ptr, s, bytes, hipMemcpyHostToDevice, hipb.stream));
     } else if (!pool_capture_forbids("a write larger than the staging segment")) {
         HIPB_CHECK(hipMemcpyAsync(b->ptr, data, bytes, hipMemcpyHostToDevice, hipb.stream));
-        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+        HIPB_CHECK(hipb_stream_wait());
     }
 }
 
@@ -442,7 +625,7 @@ void pool_upload(void *dst, const void *src, u64 bytes) {
         HIPB_CHECK(hipMemcpyAsync(dst, s, bytes, hipMemcpyHostToDevice, hipb.stream));
     } else if (!pool_capture_forbids("an upload larger than the staging segment")) {
         HIPB_CHECK(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, hipb.stream));
-        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+        HIPB_CHECK(hipb_stream_wait());
     }
 }
 
@@ -464,12 +647,12 @@ void pool_read(u32 id, void *out, u64 bytes, int nosync) {
         pool_sync_device(id);
         u8 *s = stage_reserve(n);
         HIPB_CHECK(hipMemcpyAsync(s, b->ptr, n, hipMemcpyDeviceToHost, hipb.stream));
-        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+        HIPB_CHECK(hipb_stream_wait());
         memcpy(out, s, n);
     } else {
         pool_sync_device(id);
         HIPB_CHECK(hipMemcpyAsync(out, b->ptr, n, hipMemcpyDeviceToHost, hipb.stream));
-        HIPB_CHECK(hipStreamSynchronize(hipb.stream));
+        HIPB_CHECK(hipb_stream_wait());
     }
     if (n < bytes) memset((u8 *)out + n, 0, bytes - n);
 }

@@ -210,6 +210,7 @@ int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t er
 KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
     char err[256] = {0};
     KGenResult g;
+    if (hipb.rtc_fail) return NULL;   /* test knob: every compile fails */
     if (!kgen_uop(k, &g, err, sizeof err)) {
         fprintf(stderr, "tinyhvm-hip: kernel rejected: %s\n", err);
         return NULL;

@@ -8,6 +8,10 @@
 //   thvm_fill_u32    fill a buffer with a 32-bit pattern (graph-safe clear)
 //   thvm_adam        the adam_step slot: one fused pass over parameter,
 //                    gradient and both moments
+//   thvm_kop         KOp program interpreter: the dispatch_uop_kernel path
+//                    for a program hipRTC could not compile; one lane per gid,
+//                    the reference interpreter's semantics
+//                    (src/backend/cpu/uop.c:29-155)
 //
 // The rs interpreter restates the engine's CPU fallback
 // (src/backend/cpu/dispatch.c:23-282): leaves are read through their view
@@ -438,4 +442,91 @@ extern "C" __global__ __launch_bounds__(256) void thvm_adam(AdamArgs a) {
         M[i] = m;
         V[i] = v;
     }
+}
+
+// KOp interpreter (src/backend/cpu/uop.c:29-155): lane = one gid of the
+// launch, running the whole program with its reduce loops in order, so
+// results are those of the engine's CPU backend (libm EXP/LOG aside). Like
+// the reference, each op has an unsigned slot and a float slot, zeroed per
+// gid; ftype says which one an op's value lives in. Loops: RANGE sets its
+// counter to 0 (a loop of trip 0 jumps past its ENDRANGE and leaves the
+// counter as it was); ENDRANGE steps the counter of its RANGE and jumps back
+// while it is below the trip, so after the loop the counter holds trip - 1,
+// as the reference's leaves it. The host checks that loops nest.
+__device__ __forceinline__ u32 kop_u(const KopParams *P, const u32 *uv, const float *fv, u32 id) {
+    if (id >= P->n_ops) return 0u;
+    return P->ftype[id] ? f2u(fv[id]) : uv[id];
+}
+__device__ __forceinline__ float kop_f(const KopParams *P, const u32 *uv, const float *fv, u32 id) {
+    if (id >= P->n_ops) return 0.0f;
+    return P->ftype[id] ? fv[id] : (float)uv[id];
+}
+
+extern "C" __global__ __launch_bounds__(64) void thvm_kop(const KopParams *P, u32 base) {
+    const u32 gid = base + blockIdx.x * 64u + threadIdx.x;
+    if (gid >= P->total || gid < base) return;
+    u32 uv[KOP_MAX];
+    float fv[KOP_MAX];
+    const u32 n = P->n_ops;
+    for (u32 i = 0; i < n; i++) {
+        uv[i] = 0u;
+        fv[i] = 0.0f;
+    }
+#define KU(id) kop_u(P, uv, fv, (id))
+#define KF(id) kop_f(P, uv, fv, (id))
+    u32 i = 0;
+    while (i < n) {
+        const KOp op = P->ops[i];
+        switch (op.type) {
+        case KOP_GID: uv[i] = gid; break;
+        case KOP_CONST_U: uv[i] = op.imm.u; break;
+        case KOP_CONST_F: fv[i] = op.imm.f; break;
+        case KOP_MOD: uv[i] = op.imm.u ? KU(op.arg[0]) % op.imm.u : 0u; break;
+        case KOP_DIV: uv[i] = op.imm.u ? KU(op.arg[0]) / op.imm.u : 0u; break;
+        case KOP_IDX: uv[i] = KU(op.arg[0]) * op.imm.u + KU(op.arg[1]); break;
+        case KOP_LOAD: {
+            const u32 bi = op.imm.u, idx = KU(op.arg[0]);
+            float x = 0.0f;
+            if (bi == 0u) x = load_as_f32((const void *)P->out_ptr, P->out_dtype, P->out_n, idx);
+            else if (bi - 1u < P->n_leaves)
+                x = load_as_f32((const void *)P->leaf_ptr[bi - 1u], P->leaf_dtype[bi - 1u], P->leaf_n[bi - 1u], idx);
+            fv[i] = x;
+            break;
+        }
+        case KOP_MASK: fv[i] = KF(op.arg[0]) != 0.0f ? KF(op.arg[1]) : 0.0f; break;
+        case KOP_ALU: fv[i] = alu(op.imm.u, op.arg[2], KF(op.arg[0]), KF(op.arg[1])); break;
+        case KOP_ACC_INIT: fv[i] = op.imm.f; break;
+        case KOP_ACC: {
+            const u32 a = op.arg[0];
+            if (a >= n) break;
+            const float x = KF(op.arg[1]);
+            fv[a] = op.imm.u == UOP_RMAX ? (fv[a] > x ? fv[a] : x) : fv[a] + x;
+            break;
+        }
+        case KOP_RANGE:
+            if (op.imm.u == 0u) {
+                i = (u32)P->pair[i] + 1u;
+                continue;
+            }
+            uv[i] = 0u;
+            break;
+        case KOP_ENDRANGE: {
+            const u32 s = P->pair[i];
+            const u32 r = uv[s] + 1u;
+            if (r < P->ops[s].imm.u) {
+                uv[s] = r;
+                i = s + 1u;
+                continue;
+            }
+            break;
+        }
+        case KOP_STORE:
+            store_from_f32((void *)P->out_ptr, P->out_dtype, P->out_n, KU(op.arg[0]), KF(op.arg[1]));
+            break;
+        default: break;
+        }
+        i++;
+    }
+#undef KU
+#undef KF
 }
