@@ -15,6 +15,9 @@
  *   ora_alu ...................... src/backend/cpu/dispatch.c:5-21
  *   ora_uop_exec / ora_dispatch_uop
  *                                  src/backend/cpu/uop.c:3-155
+ *   ora_dispatch_uop_gids ........ the same interpreter over a chosen list of
+ *                                  gids only (sampled checks of kernels too
+ *                                  large to interpret whole)
  *   ora_dispatch_uop_exact ....... the same with SUM accumulators kept in
  *                                  double (a checker of long sums, not a
  *                                  restatement: the reference adds in float)
@@ -245,7 +248,7 @@ static int ora_uop_exec(OraCtx *c, u32 start, u32 stop, u32 gid) {
 }
 
 static void ora_dispatch_uop_mode(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes,
-                                  u32 n_leaves, const UOpKernel *k, int exact) {
+                                  u32 n_leaves, const UOpKernel *k, int exact, const u32 *gids, u64 n_gids) {
     if (!k || !out || k->n_ops > KOP_MAX) return;
     u32 range_end[KOP_MAX], stack[KOP_MAX], sp = 0;
     for (u32 i = 0; i < KOP_MAX; i++) range_end[i] = 0xFFFFFFFFu;
@@ -262,6 +265,15 @@ static void ora_dispatch_uop_mode(void *out, u64 out_bytes, const void **leaf, c
     double dv[KOP_MAX];
     OraCtx c = {k, range_end, out, out_bytes, leaf, leaf_bytes, n_leaves, uv, fv, exact ? dv : NULL};
     u32 total = k->local_size > 0 ? k->grid[0] : k->grid[0] * k->grid[1] * k->grid[2];
+    if (gids) {
+        for (u64 j = 0; j < n_gids; j++) {
+            if (gids[j] >= total) continue;
+            memset(uv, 0, sizeof uv);
+            memset(fv, 0, sizeof fv);
+            if (!ora_uop_exec(&c, 0, k->n_ops, gids[j])) return;
+        }
+        return;
+    }
     for (u32 gid = 0; gid < total; gid++) {
         memset(uv, 0, sizeof uv);
         memset(fv, 0, sizeof fv);
@@ -271,7 +283,16 @@ static void ora_dispatch_uop_mode(void *out, u64 out_bytes, const void **leaf, c
 
 void ora_dispatch_uop(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, u32 n_leaves,
                       const UOpKernel *k) {
-    ora_dispatch_uop_mode(out, out_bytes, leaf, leaf_bytes, n_leaves, k, 0);
+    ora_dispatch_uop_mode(out, out_bytes, leaf, leaf_bytes, n_leaves, k, 0, NULL, 0);
+}
+
+/* The interpreter for the listed gids only (each runs its whole program, so
+ * its stores are exactly those of the full dispatch); gids past the launch
+ * are skipped. */
+void ora_dispatch_uop_gids(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, u32 n_leaves,
+                           const UOpKernel *k, const u32 *gids, u64 n_gids) {
+    if (!gids) return;
+    ora_dispatch_uop_mode(out, out_bytes, leaf, leaf_bytes, n_leaves, k, 0, gids, n_gids);
 }
 
 /* The kernel with every SUM accumulated in double and rounded to float when
@@ -280,7 +301,7 @@ void ora_dispatch_uop(void *out, u64 out_bytes, const void **leaf, const u64 *le
  * over long reductions. */
 void ora_dispatch_uop_exact(void *out, u64 out_bytes, const void **leaf, const u64 *leaf_bytes, u32 n_leaves,
                             const UOpKernel *k) {
-    ora_dispatch_uop_mode(out, out_bytes, leaf, leaf_bytes, n_leaves, k, 1);
+    ora_dispatch_uop_mode(out, out_bytes, leaf, leaf_bytes, n_leaves, k, 1, NULL, 0);
 }
 
 /* ---------------- FusedOp interpreter ---------------- */

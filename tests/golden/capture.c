@@ -682,6 +682,18 @@ static Term pool_relu_bwd(TinyHVM *ctx, Term dp, Term pooled, Term a, u32 B, u32
     return realize_as(ctx, g, shape_of((u32[]){B, C, H, W}, 4));
 }
 
+/* Max-pool 2x2 backward without a relu mask: dx = up(dp) * (1 - (up(pool) > x)),
+ * the engine's routing rule on any activation (negative and zero ties too). */
+static Term pool_bwd(TinyHVM *ctx, Term dp, Term pooled, Term a, u32 B, u32 C, u32 H, u32 W) {
+    Shape s6 = shape_of((u32[]){B, C, H / 2, 2, W / 2, 2}, 6);
+    Shape s1 = shape_of((u32[]){B, C, H / 2, 1, W / 2, 1}, 6);
+    Term pu = thvm_expand(ctx, thvm_reshape(ctx, pooled, s1), s6);
+    Term du = thvm_expand(ctx, thvm_reshape(ctx, dp, s1), s6);
+    Term routed = binary(ctx, UOP_SUB, scalar_t(ctx, 1.0f),
+                         binary(ctx, UOP_CMP, pu, thvm_reshape(ctx, a, s6)));
+    return realize_as(ctx, binary(ctx, UOP_MUL, du, routed), shape_of((u32[]){B, C, H, W}, 4));
+}
+
 /* Weight gradient of a stride-1 conv as one contraction:
  * dW[co,ci,kh,kw] = sum_{b,oy,ox} xp[b,ci,oy+kh,ox+kw] * dz[b,co,oy,ox],
  * with xp the already padded input (a pool view, src/nn/conv.c:20-388). */
@@ -905,6 +917,30 @@ static void wl_convblock(TinyHVM *ctx, u32 B, u32 C, u32 H) {
     readback(ctx, dW);
     readback(ctx, dx);
     (void)dgamma; (void)dbeta;
+}
+
+/* Max-pool ties: x [B,C,H,H] takes the integer values -1, 0, 1, 2, so most
+ * 2x2 windows hold their maximum more than once, at positive values too.
+ * Forward: a = relu(x), p = maxpool2(a) (src/nn/conv.c:484-514), and
+ * maxpool2(x); backward with upstream gradients g of distinct integer values
+ * 1..4: the pool+relu routing of the conv block and LeNet (every tied
+ * maximum receives the gradient, src/interact/grad.c:405-425) and the same
+ * routing on x itself. */
+static void wl_pooltie(TinyHVM *ctx, u32 B, u32 C, u32 H) {
+    Shape full = shape_of((u32[]){B, C, H, H}, 4), half = shape_of((u32[]){B, C, H / 2, H / 2}, 4);
+    Term x = gen_tensor(ctx, full, DTYPE_F32, TRC_GEN_INT, 8001, -1.f, 3.f);
+    Term g = gen_tensor(ctx, half, DTYPE_F32, TRC_GEN_INT, 8002, 1.f, 5.f);
+    rec_mark("pool.fwd");
+    Term a = realize_as(ctx, unary(ctx, UOP_RELU, x), full);
+    Term p = realize_as(ctx, thvm_maxpool2d(ctx, a, (u32[]){2, 2}, (u32[]){2, 2}), half);
+    Term px = realize_as(ctx, thvm_maxpool2d(ctx, x, (u32[]){2, 2}, (u32[]){2, 2}), half);
+    readback(ctx, p);
+    readback(ctx, px);
+    rec_mark("pool.bwd");
+    Term da = pool_relu_bwd(ctx, g, p, a, B, C, H, H);
+    Term dx = pool_bwd(ctx, g, px, x, B, C, H, H);
+    readback(ctx, da);
+    readback(ctx, dx);
 }
 
 /* Adam (beta1 0.9, beta2 0.999, eps 1e-8, lr 0.01) on two parameters, [1000]
@@ -1418,6 +1454,8 @@ int main(int argc, char **argv) {
         wl_lenet(ctx, nsz > 0 ? sz[0] : 256, nsz > 1 ? (int)sz[1] : 1);
     } else if (strcmp(wl, "convblock") == 0) {
         wl_convblock(ctx, nsz > 0 ? sz[0] : 64, nsz > 1 ? sz[1] : 64, nsz > 2 ? sz[2] : 56);
+    } else if (strcmp(wl, "pooltie") == 0) {
+        wl_pooltie(ctx, nsz > 0 ? sz[0] : 2, nsz > 1 ? sz[1] : 4, nsz > 2 ? sz[2] : 16);
     } else if (strcmp(wl, "dtypes") == 0) {
         wl_dtypes(ctx);
     } else if (strcmp(wl, "assign") == 0) {

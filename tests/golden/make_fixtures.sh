@@ -30,6 +30,8 @@ $CAP convblock convblock_2x4x8.trc 2 4 8
 $CAP convblock convblock_2x4x28.trc 2 4 28
 # 64 channels at 8x8 (the convolution's weights fill a 64-wide GEMM tile: operand packing)
 $CAP convblock convblock_1x64x8.trc 1 64 8
+# max-pool routing at tied maxima (integer-valued activations, positive ties)
+$CAP pooltie pooltie_2x4x16.trc 2 4 16
 # storage dtypes and casts
 $CAP dtypes dtypes.trc
 # ASSIGN from strided views (the contiguify slot)

@@ -128,3 +128,59 @@ def test_capture_with_a_host_read_is_refused(L):
     assert np.array_equal(out, data)
     L.thvm_hip_buf_free(buf)
     L.thvm_hip_buf_free(other)
+
+
+def test_graph_memory_is_not_handed_out_again(L):
+    """Blocks a graph writes stay reserved while it lives: the step's
+    temporaries, allocated and freed inside the capture, are not given to
+    buffers allocated after it, so launching the graph leaves those buffers
+    intact; once the graph is destroyed the blocks are reusable."""
+    from tinyhvm_amd import trace
+    recs = trace.read_trace(TRACE)
+    be = L.thvm_hip_backend()
+    t = L.thvm_trace_load(TRACE.encode())
+    assert t
+    g = None
+    extra = []
+    try:
+        lo = L.thvm_trace_find_mark(t, b"lenet.step", 0)
+        hi = L.thvm_trace_find_mark(t, b"lenet.end", lo)
+        L.thvm_trace_replay(t, be, 0, lo, 0)
+        L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
+        assert L.thvm_hip_synchronize() == 0
+        assert L.thvm_hip_graph_begin() == 0
+        L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
+        g = L.thvm_hip_graph_end()
+        assert g, "the step could not be captured"
+        cnt = (C.c_uint64 * 10)()
+        L.thvm_hip_counters(cnt, 10)
+        assert cnt[8] > 0, "no device block was pinned by the capture"
+        # buffers of every size the step allocates, each with its own pattern
+        step_sizes = [r.f["bytes"] for r in recs[lo:hi] if r.tag == trace.ALLOC]
+        assert len(step_sizes) > 20
+        for j, nb in enumerate(step_sizes):
+            b = L.thvm_hip_buf_alloc(nb)
+            assert b
+            pat = np.full((nb + 3) // 4, np.float32(1000 + j), dtype=np.float32)
+            L.thvm_hip_buf_write(b, pat.ctypes.data_as(C.c_void_p), nb)
+            extra.append((b, nb, pat))
+        assert L.thvm_hip_synchronize() == 0
+        for _ in range(2):
+            assert L.thvm_hip_graph_launch(g) == 0
+        assert L.thvm_hip_synchronize() == 0
+        for b, nb, pat in extra:
+            out = np.zeros((nb + 3) // 4, dtype=np.float32)
+            L.thvm_hip_buf_read(b, out.ctypes.data_as(C.c_void_p), nb)
+            assert np.array_equal(out[:nb // 4], pat[:nb // 4]), "a graph launch wrote a later buffer"
+        L.thvm_hip_graph_destroy(g)
+        g = None
+        L.thvm_hip_counters(cnt, 10)
+        assert cnt[8] == 0 and cnt[9] == 0, "blocks still pinned after the graph was destroyed"
+    finally:
+        if g:
+            L.thvm_hip_graph_destroy(g)
+        for b, _nb, _p in extra:
+            L.thvm_hip_buf_free(b)
+        L.thvm_trace_release(t, be)
+        L.thvm_trace_free(t)
+        L.thvm_hip_pool_reset(0)

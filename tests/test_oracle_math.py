@@ -18,9 +18,13 @@ by its iteration domain and restated in numpy float64:
 
 Sums are compared normwise within 1e-5 (f32 sequential accumulation against
 f64). A planted mistake (an unflipped kernel, a shifted window, a dropped
-relu mask) must fail the same checks. Ties at positive values, where
-ties-to-all and first-max routing differ, do not occur in random data; that
-rule is pinned by the engine's own vectors only.
+relu mask) must fail the same checks.
+
+Ties: ties at positive values, where ties-to-all and first-max routing
+differ, do not occur in random data. The pooltie fixture (integer-valued
+activations) has them in most windows; its engine snapshots of the forward
+pools and of both routings are checked bit for bit against brute force with
+the ties-to-all rule, and a first-max rule must fail the same check.
 """
 import ctypes as C
 
@@ -204,3 +208,62 @@ def test_planted_mistakes_fail():
     # relu mask zeroes the gradient: dropping it must be caught
     r, leaves, got = first["pool_bwd"]
     assert not check_dispatch(r, leaves, got, mistake="no_relu")[1]
+
+
+def _pooltie():
+    path = tt.fixtures("pooltie_2x4x16.trc")[0]
+    recs = trace.read_trace(path)
+    gens, snaps = {}, {}
+    for r in recs:
+        if r.tag == trace.WRITE and r.f["enc"] == trace.ENC_GEN:
+            f = r.f
+            gens[f["seed"]] = np.frombuffer(trace.gen_data(f["dist"], f["dtype"], f["seed"], f["p0"], f["p1"],
+                                                           f["bytes"]), dtype=np.float32)
+        if r.tag == trace.SNAPSHOT:
+            snaps[r.f["id"]] = np.frombuffer(r.f["data"], dtype=np.float32)
+    B, Cc, H = 2, 4, 16
+    x = gens[8001].reshape(B, Cc, H, H)
+    g = gens[8002].reshape(B, Cc, H // 2, H // 2)
+    return x, g, snaps
+
+
+def _first_max_bwd(dp, a):
+    """The alternative rule: only the first maximum of each window (row-major)
+    receives the gradient."""
+    B, Cc, H, W = a.shape
+    win = a.reshape(B, Cc, H // 2, 2, W // 2, 2).transpose(0, 1, 2, 4, 3, 5).reshape(B, Cc, H // 2, W // 2, 4)
+    first = np.argmax(win, axis=-1)
+    out = np.zeros_like(win)
+    np.put_along_axis(out, first[..., None], dp[..., None], axis=-1)
+    return out.reshape(B, Cc, H // 2, W // 2, 2, 2).transpose(0, 1, 2, 4, 3, 5).reshape(B, Cc, H, W)
+
+
+def test_pool_ties_fixture_has_positive_ties():
+    x, _g, _s = _pooltie()
+    a = np.maximum(x, 0)
+    win = a.reshape(2, 4, 8, 2, 8, 2).transpose(0, 1, 2, 4, 3, 5).reshape(-1, 4)
+    mx = win.max(axis=1)
+    ties = (win == mx[:, None]).sum(axis=1)
+    assert np.sum((mx > 0) & (ties >= 2)) >= 20
+    assert set(np.unique(x)) == {-1.0, 0.0, 1.0, 2.0}
+
+
+def test_pool_ties_routing_is_ties_to_all():
+    """Engine snapshots of the pooltie workload: forward pools, the pool+relu
+    routing of g and the plain routing of g, bit for bit against brute force;
+    a first-max rule differs from them."""
+    x, g, snaps = _pooltie()
+    a = np.maximum(x, np.float32(0))
+    p, px = maxpool2(a), maxpool2(x)
+    assert np.array_equal(snaps[8].reshape(p.shape), p)
+    assert np.array_equal(snaps[13].reshape(px.shape), px)
+    s6 = (2, 4, 8, 2, 8, 2)
+    da = pool_relu_bwd_ref(g, p, a.reshape(s6)).reshape(x.shape)
+    dx = pool_relu_bwd_ref(g, px, x.reshape(s6), relu_mask=False).reshape(x.shape)
+    assert np.array_equal(snaps[20].reshape(x.shape), da)
+    assert np.array_equal(snaps[28].reshape(x.shape), dx)
+    # every tied maximum got the window's gradient: the routed total per window
+    # is g times the number of maxima, not g
+    assert not np.array_equal(snaps[28].reshape(x.shape), _first_max_bwd(g, x))
+    first_relu = _first_max_bwd(g, a) * (a > 0)
+    assert not np.array_equal(snaps[20].reshape(x.shape), first_relu)
