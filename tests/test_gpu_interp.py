@@ -24,9 +24,11 @@ KNOBS = ("THVM_HIP_INTERP", "THVM_HIP_RTC_FAIL", "THVM_HIP_NO_DENSE", "THVM_HIP_
 
 
 def _init(env):
+    """A fresh backend that reads these knobs (init reads them once)."""
+    L = _lib.lib()
+    L.thvm_hip_shutdown()
     saved = {k: os.environ.pop(k, None) for k in KNOBS}
     os.environ.update(env)
-    L = _lib.lib()
     assert L.thvm_hip_init() == 0, "HIP backend failed to initialise"
     return L, saved
 
