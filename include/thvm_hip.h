@@ -110,6 +110,34 @@ void *thvm_hip_graph_end(void);
 int   thvm_hip_graph_launch(void *graph);
 void  thvm_hip_graph_destroy(void *graph);
 
+/* Dispatch without allocation. No counterpart in the reference: it is for
+ * callers that cannot allocate device memory while they dispatch (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The same work as thvm_hip_dispatch_uop_kernel, with the same kernels in the
+ * same order (so the same bits), except that every workspace its kernels use
+ * (split-K partial sums, split reduction partials, packed GEMM operands) comes
+ * from a static device array of THVM_HIP_NOALLOC_SCRATCH_BYTES per GPU,
+ * reserved when the library initialises, and that it never compiles: the
+ * program must have run once through thvm_hip_dispatch_uop_kernel. It calls
+ * no hipMalloc or hipFree. All calls on one GPU share the array; calls are
+ * ordered on the backend's single stream, so consecutive calls are safe,
+ * but calls that overlap on one GPU (from other streams or threads) race.
+ * Returns THVM_HIP_OK, or:
+ *   THVM_HIP_EINVAL     not initialised, no kernel, or an unknown output buffer
+ *   THVM_HIP_ENOTREADY  the program has not been compiled yet (or runs only on
+ *                       the KOp interpreter, which is not offered here)
+ *   THVM_HIP_ESCRATCH   its workspaces need more than THVM_HIP_NOALLOC_SCRATCH_BYTES
+ *   THVM_HIP_ENOSCRATCH the static array is not available on this device
+ * On an error nothing is launched and the output is not written. */
+#define THVM_HIP_NOALLOC_SCRATCH_BYTES (32ull << 20)
+#define THVM_HIP_OK 0
+#define THVM_HIP_EINVAL (-1)
+#define THVM_HIP_ENOTREADY (-2)
+#define THVM_HIP_ESCRATCH (-3)
+#define THVM_HIP_ENOSCRATCH (-4)
+int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
+                                          const UOpKernel *kernel);
+
 /* Counters, for tests and the engine-driven timing (no counterpart in the
  * reference): out[0..9] = dispatches, matrix-core dispatches, compiled
  * programs, program cache hits, dispatches run on the KOp interpreter

@@ -59,6 +59,7 @@ def lib():
         "thvm_hip_profile_reset": (None, []),
         "thvm_hip_synchronize": (C.c_int, []),
         "thvm_hip_counters": (C.c_int, [C.POINTER(u64), u32]),
+        "thvm_hip_dispatch_uop_kernel_noalloc": (C.c_int, [u32, PU32, u32, C.POINTER(abi.UOpKernel)]),
         "thvm_hip_stream": (vp, []),
         "thvm_hip_buf_device_ptr": (vp, [u32]),
         "thvm_hip_backend": (C.POINTER(abi.Backend), []),
@@ -100,7 +101,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_op_reduce", "thvm_hip_adam_step", "thvm_hip_graph_begin", "thvm_hip_graph_end",
     "thvm_hip_graph_launch", "thvm_hip_graph_destroy", "thvm_hip_buf_copy", "thvm_hip_pool_reset",
     "thvm_hip_pool_set_persistent", "thvm_hip_profile_report", "thvm_hip_profile_reset",
-    "thvm_hip_synchronize", "thvm_hip_counters", "thvm_hip_stream", "thvm_hip_buf_device_ptr", "thvm_hip_backend",
+    "thvm_hip_synchronize", "thvm_hip_counters", "thvm_hip_dispatch_uop_kernel_noalloc", "thvm_hip_stream", "thvm_hip_buf_device_ptr", "thvm_hip_backend",
     "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_kernel_lanes", "thvm_hip_compile_check",
     "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",

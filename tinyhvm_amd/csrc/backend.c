@@ -16,6 +16,7 @@
 #include "hipb.h"
 #include "thvm_hip.h"
 #include "kargs.h"
+#include "noalloc.h"
 
 HipbState hipb;
 
@@ -155,6 +156,9 @@ static int hb_init(void) {
     hipb.dummy = pool_block_get(256, &hipb.dummy_cap);
     if (!hipb.dummy || hipMemset(hipb.dummy, 0, 256) != hipSuccess) return -1;
     if (rtc_init() != 0) return -1;
+    /* the static workspace of the no-allocation entry point, on this device */
+    if (thvm_noalloc_scratch_init(hipb.device) == 0) hipb.noalloc_scratch = thvm_noalloc_scratch_ptr(hipb.device);
+    else fprintf(stderr, "tinyhvm-hip: static workspace unavailable; dispatch without allocation is off\n");
     hipb.initialized = 1;
     if (!atexit_done) {
         atexit(hb_atexit);
@@ -317,6 +321,11 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         hipb.n_dense++;
         return;
     }
+    if (hipb.noalloc && hipb.noalloc_err) return;
+    if (hipb.noalloc && hipb.force_interp) {
+        hipb.noalloc_err = THVM_HIP_ENOTREADY;
+        return;
+    }
     if (hipb.force_interp) {
         interp_dispatch(out_buf, leaf_bufs, n_leaves, k);
         return;
@@ -324,7 +333,10 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     u64 key = uop_signature(k);
     KCacheEntry *e = rtc_lookup(key, k);
     if (e) hipb.n_cache_hit++;
-    else e = rtc_compile_uop(key, k);
+    else if (hipb.noalloc) {
+        hipb.noalloc_err = THVM_HIP_ENOTREADY;   /* never compiles without allocating */
+        return;
+    } else e = rtc_compile_uop(key, k);
     if (!e) {
         /* the generator or hipRTC refused the program: the interpreter runs
          * it, so the output is still written (counted in n_fallback) */
@@ -390,6 +402,20 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     else grid_for((e->n_threads + e->block - 1) / e->block, e->block, &gx, &gy);
     hipb_launch(e->fn, gx, gy, 1, e->block, params);
     pool_mark_device_write(out_buf);
+}
+
+/* The same dispatch with its workspaces carved from the static array and no
+ * compilation (see thvm_hip.h). */
+int thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
+                                         const UOpKernel *k) {
+    if (!hipb.initialized || !k || !pool_get(out_buf)) return THVM_HIP_EINVAL;
+    if (!hipb.noalloc_scratch) return THVM_HIP_ENOSCRATCH;
+    hipb.noalloc = 1;
+    hipb.noalloc_off = 0;
+    hipb.noalloc_err = 0;
+    hb_dispatch_uop_kernel(out_buf, leaf_bufs, n_leaves, k, 0);
+    hipb.noalloc = 0;
+    return hipb.noalloc_err;
 }
 
 /* ---- dispatch_kernel_rs: static interpreter ---- */

@@ -38,6 +38,7 @@
 #include <string.h>
 
 #include "hipb.h"
+#include "thvm_hip.h"
 
 #define DG_MAX 8
 #define DENSE_MIN_K 16
@@ -1522,6 +1523,10 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     u64 key = uop_signature(k) ^ 0xD5E5E5E5D5E5E5E5ull;
     if (!key) key = 1;
     DenseEntry *e = lookup(key, k);
+    if (!e && hipb.noalloc) {
+        hipb.noalloc_err = THVM_HIP_ENOTREADY;   /* never compiles without allocating */
+        return 0;
+    }
     if (!e) {
         e = insert(key, k);
         if (!e) return 0;

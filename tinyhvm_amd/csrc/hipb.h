@@ -61,6 +61,10 @@ typedef struct {
     u64 n_fallback;          /* dispatches run on the KOp interpreter */
     u64 n_stream_sync;       /* host waits on the stream (buf_read, synchronize, ...) */
     hipModule_t static_mod;  /* precompiled kernels */
+    void *noalloc_scratch;   /* device address of the static workspace (noalloc.hip), or NULL */
+    int noalloc;             /* a no-allocation dispatch is running: workspaces come from it */
+    u64 noalloc_off;         /* bytes of the static workspace handed out in that dispatch */
+    int noalloc_err;         /* why that dispatch could not run (THVM_HIP_E*), or 0 */
     int capturing;           /* a graph capture is open on the stream */
     int capture_bad;         /* the open capture met work a graph cannot replay */
 } HipbState;

@@ -42,6 +42,7 @@
 #include <string.h>
 
 #include "hipb.h"
+#include "thvm_hip.h"
 
 #define POOL_MIN_CLASS_BYTES 256ull
 #define POOL_N_CLASSES 256
@@ -226,10 +227,34 @@ static int fl_push(FreeList *f, void *p) {
     return 1;
 }
 
+/* A piece of the static workspace for the running no-allocation dispatch
+ * (256-byte aligned), or NULL with the error recorded when it is full. */
+static void *noalloc_carve(u64 bytes) {
+    u64 off = (hipb.noalloc_off + 255) & ~255ull;
+    if (!hipb.noalloc_scratch) {
+        hipb.noalloc_err = THVM_HIP_ENOSCRATCH;
+        return NULL;
+    }
+    if (bytes > THVM_HIP_NOALLOC_SCRATCH_BYTES || off + bytes > THVM_HIP_NOALLOC_SCRATCH_BYTES) {
+        fprintf(stderr, "tinyhvm-hip: dispatch without allocation needs %llu bytes of workspace; "
+                "the static workspace holds %llu\n", (unsigned long long)(off + bytes),
+                (unsigned long long)THVM_HIP_NOALLOC_SCRATCH_BYTES);
+        hipb.noalloc_err = THVM_HIP_ESCRATCH;
+        return NULL;
+    }
+    hipb.noalloc_off = off + bytes;
+    return (u8 *)hipb.noalloc_scratch + off;
+}
+
+static int in_static_scratch(const void *p) {
+    const u8 *s = hipb.noalloc_scratch;
+    return s && (const u8 *)p >= s && (const u8 *)p < s + THVM_HIP_NOALLOC_SCRATCH_BYTES;
+}
+
 /* A released block: to limbo while a graph references it, else to its
  * class's free list (or back to HIP if the list cannot grow). */
 static void block_release(void *ptr, u64 cap) {
-    if (!ptr) return;
+    if (!ptr || in_static_scratch(ptr)) return;
     if (pin_find(ptr)) {
         if (P.limbo_n == P.limbo_max) {
             u32 nc = P.limbo_max ? P.limbo_max * 2 : 64;
@@ -351,6 +376,10 @@ static int ensure_cap(u32 id) {
 /* A device block of at least `bytes` from its size class's free list, or
  * hipMalloc (after releasing the cached blocks on failure). */
 void *pool_block_get(u64 bytes, u64 *cap_out) {
+    if (hipb.noalloc) {
+        *cap_out = bytes;
+        return noalloc_carve(bytes);
+    }
     u64 cap = 0;
     u32 c = size_class(bytes ? bytes : 4, &cap);
     void *ptr = NULL;
@@ -383,6 +412,7 @@ void pool_block_put(void *ptr, u64 cap) { block_release(ptr, cap); }
  * on demand, kept until released. Engine ids are never used for it, so
  * pool_reset cannot free it and the engine's id numbering is untouched. */
 void *scratch_reserve(Scratch *sc, u64 bytes) {
+    if (hipb.noalloc) return noalloc_carve(bytes);   /* the workspace it keeps stays as it is */
     if (bytes <= sc->cap && sc->ptr) {
         capture_pin(sc->ptr, sc->cap);
         return sc->ptr;
