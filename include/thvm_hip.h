@@ -143,8 +143,9 @@ int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32
  * programs, program cache hits, dispatches run on the KOp interpreter
  * (programs the generator or hipRTC refused; their outputs are still
  * written), host waits on the stream, live device bytes, hipMalloc calls,
- * device blocks pinned by HIP graphs, released blocks held for graphs.
- * Returns the number of counters (10). */
+ * device blocks pinned by HIP graphs, released blocks held for graphs,
+ * dispatches run on the window-max and run-sum kernels. Returns the number
+ * of counters (11). */
 int  thvm_hip_counters(u64 *out, u32 n);
 /* Wait for all enqueued work; returns 0, or -1 on a device error. */
 int  thvm_hip_synchronize(void);
@@ -180,6 +181,18 @@ int  thvm_hip_dense_source(const UOpKernel *kernel, char *buf, u64 buflen);
 /* Generate and compile that matrix-core kernel without loading it; returns the
  * code-object size, or -1 with the reason in errbuf. */
 int  thvm_hip_dense_compile_check(const UOpKernel *kernel, char *errbuf, u64 errlen);
+
+/* Whether a kernel is a window max (the RMAX over a pooling window that
+ * thvm_maxpool2d lowers to, src/nn/conv.c:484-514) or a run sum (a long SUM
+ * over contiguous runs into few outputs: batchnorm's per-channel statistics,
+ * src/nn/batchnorm.c:35-111, bias gradients, loss sums) that the backend runs
+ * on its dedicated kernels (no device needed). kind: 0 neither, 1 window max,
+ * 2 run sum; splits: workgroups per output. Returns 1 if so, else 0. */
+int  thvm_hip_window_analyze(const UOpKernel *kernel, u32 *kind, u32 *splits);
+/* Its generated HIP source; returns the length, or -1 with the reason in buf. */
+int  thvm_hip_window_source(const UOpKernel *kernel, char *buf, u64 buflen);
+/* Generate and compile it without loading; the code-object size, or -1. */
+int  thvm_hip_window_compile_check(const UOpKernel *kernel, char *errbuf, u64 errlen);
 
 #ifdef __cplusplus
 }

@@ -1,8 +1,10 @@
 /*
  * analyze_all.c - runs the backend's device-free program analysis over every
  * lowered kernel of the given kernel traces: the kernel generator
- * (thvm_hip_kernel_source, thvm_hip_kernel_lanes) and the matrix-core
- * recognizer (thvm_hip_dense_analyze, thvm_hip_dense_source). Built with
+ * (thvm_hip_kernel_source, thvm_hip_kernel_lanes), the matrix-core
+ * recognizer (thvm_hip_dense_analyze, thvm_hip_dense_source) and the
+ * pooling-window / run-sum recognizer (thvm_hip_window_analyze,
+ * thvm_hip_window_source). Built with
  * AddressSanitizer and UndefinedBehaviorSanitizer, it checks that parsing
  * the engine-supplied programs neither reads nor writes out of bounds nor
  * hits undefined arithmetic. No GPU is used. Also feeds each program with
@@ -22,10 +24,11 @@ static char src[1 << 20];
 static u32 lanes[7 * KOP_MAX];
 
 static void analyze(const UOpKernel *k) {
-    u32 mode = 0, vec = 0, M, N, K, S;
+    u32 mode = 0, vec = 0, M, N, K, S, kind;
     thvm_hip_kernel_source(k, src, sizeof src, &mode, &vec);
     thvm_hip_kernel_lanes(k, lanes, 7 * KOP_MAX, &mode, &vec);
     if (thvm_hip_dense_analyze(k, &M, &N, &K, &S)) thvm_hip_dense_source(k, src, sizeof src);
+    if (thvm_hip_window_analyze(k, &kind, &S)) thvm_hip_window_source(k, src, sizeof src);
 }
 
 int main(int argc, char **argv) {

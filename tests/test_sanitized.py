@@ -48,14 +48,18 @@ def test_pool_contract_sanitized(tmp_path):
 
 
 def test_program_analysis_sanitized(tmp_path):
+    from tinyhvm_amd import build
     blob = os.path.join(tt.ROOT, "_build", "static_kernels_blob.c")
     if not os.path.exists(blob):
-        from tinyhvm_amd import build
         build.build_kernels()
+    # the static-workspace object (hipcc, not instrumented: it holds no analysis code)
+    objs = [os.path.join(tt.ROOT, "_build", os.path.splitext(h)[0] + ".o") for h in build.HIP_OBJECTS]
+    if not all(os.path.exists(o) for o in objs):
+        objs = build.build_hip_objects()
     exe = str(tmp_path / "analyze_all")
-    srcs = [os.path.join(CSRC, f) for f in ("backend.c", "pool.c", "kgen.c", "rtc.c", "dense.c", "replay.c")]
-    _build(exe, srcs + [blob, os.path.join(CPU, "analyze_all.c")],
-           ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lhiprtc", "-lpthread", "-lm",
+    srcs = [os.path.join(CSRC, f) for f in ("backend.c", "pool.c", "kgen.c", "rtc.c", "affine.c", "dense.c", "window.c", "replay.c")]
+    _build(exe, srcs + [blob, os.path.join(CPU, "analyze_all.c")] + objs,
+           ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lhiprtc", "-lstdc++", "-lpthread", "-lm",
             "-Wl,-rpath," + os.path.join(ROCM, "lib")])
     traces = tt.fixtures() + sorted(
         os.path.join(tt.ROOT, "tinyhvm_amd", "workloads", f)

@@ -70,6 +70,9 @@ def lib():
         "thvm_hip_dense_analyze": (C.c_int, [C.POINTER(abi.UOpKernel), PU32, PU32, PU32, PU32]),
         "thvm_hip_dense_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
         "thvm_hip_dense_source": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
+        "thvm_hip_window_analyze": (C.c_int, [C.POINTER(abi.UOpKernel), PU32, PU32]),
+        "thvm_hip_window_source": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
+        "thvm_hip_window_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
         "thvm_trace_load": (vp, [cp]),
         "thvm_trace_free": (None, [vp]),
         "thvm_trace_count": (u32, [vp]),
@@ -104,6 +107,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_synchronize", "thvm_hip_counters", "thvm_hip_dispatch_uop_kernel_noalloc", "thvm_hip_stream", "thvm_hip_buf_device_ptr", "thvm_hip_backend",
     "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_kernel_lanes", "thvm_hip_compile_check",
     "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
+    "thvm_hip_window_analyze", "thvm_hip_window_source", "thvm_hip_window_compile_check",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
     "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",
@@ -171,3 +175,28 @@ def kernel_lanes(k: abi.UOpKernel):
         raise ValueError("kernel generation failed")
     rows = [tuple(buf[7 * i:7 * i + 7]) for i in range(r)]
     return mode.value, vec.value, rows
+
+
+def window_analyze(k: abi.UOpKernel):
+    """(kind, splits) if the backend runs this kernel on its window-max (1) or
+    run-sum (2) kernels, else None."""
+    kind, S = C.c_uint32(), C.c_uint32()
+    if lib().thvm_hip_window_analyze(C.byref(k), C.byref(kind), C.byref(S)):
+        return kind.value, S.value
+    return None
+
+
+def window_compile_check(k: abi.UOpKernel):
+    err = C.create_string_buffer(512)
+    n = lib().thvm_hip_window_compile_check(C.byref(k), err, len(err))
+    if n < 0:
+        raise RuntimeError(err.value.decode())
+    return n
+
+
+def window_source(k: abi.UOpKernel):
+    buf = C.create_string_buffer(1 << 20)
+    n = lib().thvm_hip_window_source(C.byref(k), buf, len(buf))
+    if n < 0:
+        raise ValueError(buf.value.decode())
+    return buf.value.decode()

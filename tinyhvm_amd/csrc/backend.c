@@ -105,6 +105,8 @@ static void read_dense_env(void) {
     if (hipb.dense_tile > 7) hipb.dense_tile = 0;
 }
 
+u32 hipb_resident_waves(void) { return hipb.resident_waves ? hipb.resident_waves : 256u * SINGLE_PASS_WAVES_PER_CU; }
+
 hipError_t hipb_stream_wait(void) {
     hipb.n_stream_sync++;
     return hipStreamSynchronize(hipb.stream);
@@ -139,15 +141,19 @@ static int hb_init(void) {
         return -1;
     }
     hipDeviceProp_t prop;
-    if (hipGetDeviceProperties(&prop, hipb.device) == hipSuccess &&
-        strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
-        fprintf(stderr, "tinyhvm-hip: device is %s; kernels are built for gfx950\n", prop.gcnArchName);
-        return -1;
+    if (hipGetDeviceProperties(&prop, hipb.device) == hipSuccess) {
+        if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+            fprintf(stderr, "tinyhvm-hip: device is %s; kernels are built for gfx950\n", prop.gcnArchName);
+            return -1;
+        }
+        if (prop.multiProcessorCount > 0)
+            hipb.resident_waves = (u32)prop.multiProcessorCount * SINGLE_PASS_WAVES_PER_CU;
     }
     if (hipStreamCreateWithFlags(&hipb.stream, hipStreamNonBlocking) != hipSuccess) return -1;
     hipb.sync_each = env_flag("THVM_HIP_SYNC");
     hipb.dump_src = env_flag("THVM_HIP_DUMP");
     hipb.no_dense = env_flag("THVM_HIP_NO_DENSE");
+    hipb.no_window = env_flag("THVM_HIP_NO_WINDOW");
     hipb.verbose = env_flag("THVM_HIP_VERBOSE");
     hipb.force_interp = env_flag("THVM_HIP_INTERP");
     hipb.rtc_fail = env_flag("THVM_HIP_RTC_FAIL");
@@ -156,6 +162,17 @@ static int hb_init(void) {
     hipb.dummy = pool_block_get(256, &hipb.dummy_cap);
     if (!hipb.dummy || hipMemset(hipb.dummy, 0, 256) != hipSuccess) return -1;
     if (rtc_init() != 0) return -1;
+    /* the single-pass combine area, zeroed once by a kernel */
+    {
+        u64 c1 = 0;
+        hipb.comb_slots = pool_block_get((u64)COMB_SLOTS * 8, &c1);
+        hipFunction_t fill = rtc_static_fn("thvm_fill_u32");
+        if (!hipb.comb_slots || !fill) return -1;
+        u32 n1 = COMB_SLOTS * 2, zero = 0;
+        void *a1[] = {&hipb.comb_slots, &n1, &zero};
+        hipb_launch(fill, (n1 + 255) / 256, 1, 1, 256, a1);
+        if (hipb_stream_wait() != hipSuccess) return -1;
+    }
     /* the static workspace of the no-allocation entry point, on this device */
     if (thvm_noalloc_scratch_init(hipb.device) == 0) hipb.noalloc_scratch = thvm_noalloc_scratch_ptr(hipb.device);
     else fprintf(stderr, "tinyhvm-hip: static workspace unavailable; dispatch without allocation is off\n");
@@ -175,8 +192,11 @@ static void hb_shutdown(void) {
     HIPB_CHECK(hipb_stream_wait());
     graphs_release_all();
     dense_shutdown();
+    window_shutdown();
     rtc_shutdown();
     scratch_release(&red_ws);
+    pool_block_put(hipb.comb_slots, (u64)COMB_SLOTS * 8);
+    hipb.comb_slots = NULL;
     pool_block_put(hipb.dummy, hipb.dummy_cap);
     hipb.dummy = NULL;
     pool_shutdown();
@@ -322,6 +342,12 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         return;
     }
     if (hipb.noalloc && hipb.noalloc_err) return;
+    if (!hipb.no_window && !hipb.force_interp && window_try_dispatch(out_buf, leaf_bufs, n_leaves, k)) {
+        pool_mark_device_write(out_buf);
+        hipb.n_window++;
+        return;
+    }
+    if (hipb.noalloc && hipb.noalloc_err) return;
     if (hipb.noalloc && hipb.force_interp) {
         hipb.noalloc_err = THVM_HIP_ENOTREADY;
         return;
@@ -368,7 +394,7 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     u32 nb = k->n_leaves + 1;
     void *ptrs[FUSE_MAX_LEAVES + 1];
     u32 counts[FUSE_MAX_LEAVES + 1];
-    void *params[2 * (FUSE_MAX_LEAVES + 1) + 2 + KGEN_MAX_SCALARS];
+    void *params[2 * (FUSE_MAX_LEAVES + 1) + 3 + KGEN_MAX_SCALARS];
     ptrs[0] = ob->ptr;
     counts[0] = elem_count(out_buf, k->out_dtype);
     for (u32 i = 0; i < k->n_leaves; i++) {
@@ -386,6 +412,15 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         for (u32 j = 0; j < e->n_scal; j++) params[np++] = &sv[j];
     }
     u32 gx, gy;
+    if (e->splits > 1 && !e->fn_fin) {
+        /* split group reduce, partials combined by the last workgroup of each
+         * output through the combine area */
+        params[np] = &hipb.comb_slots;
+        grid_for(e->total * e->splits, e->block, &gx, &gy);
+        hipb_launch(e->fn, gx, gy, 1, e->block, params);
+        pool_mark_device_write(out_buf);
+        return;
+    }
     if (e->splits > 1) {
         /* split group reduce: partials into the workspace, then the combine */
         float *ws = reduce_workspace((u64)e->total * e->splits * sizeof(float));
@@ -695,7 +730,7 @@ static void hb_profile_report(void) {
 
 static void hb_profile_reset(void) {
     hipb.n_dispatch = hipb.n_compile = hipb.n_cache_hit = hipb.n_dense = 0;
-    hipb.n_fallback = hipb.n_stream_sync = 0;
+    hipb.n_fallback = hipb.n_stream_sync = hipb.n_window = 0;
 }
 
 Backend hip_backend = {
@@ -779,10 +814,10 @@ int thvm_hip_counters(u64 *out, u32 n) {
     u32 pinned = 0, limbo = 0;
     pool_stats(&live, &cached, &mallocs);
     pool_pin_stats(&pinned, &limbo);
-    u64 v[10] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
-                 hipb.n_stream_sync, live, mallocs, pinned, limbo};
-    for (u32 i = 0; out && i < n && i < 10; i++) out[i] = v[i];
-    return 10;
+    u64 v[11] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
+                 hipb.n_stream_sync, live, mallocs, pinned, limbo, hipb.n_window};
+    for (u32 i = 0; out && i < n && i < 11; i++) out[i] = v[i];
+    return 11;
 }
 
 int thvm_hip_synchronize(void) {
@@ -848,6 +883,36 @@ static void ensure_env(void) {
         read_dense_env();
         env_read = 1;
     }
+}
+
+int thvm_hip_window_analyze(const UOpKernel *k, u32 *kind, u32 *splits) {
+    ensure_env();
+    return window_analyze(k, kind, splits);
+}
+
+int thvm_hip_window_source(const UOpKernel *k, char *buf, u64 buflen) {
+    char *src = window_source(k);
+    if (!src) {
+        if (buf && buflen) snprintf(buf, buflen, "not a window-max or run-sum program");
+        return -1;
+    }
+    size_t n = strlen(src);
+    if (buf && buflen) snprintf(buf, buflen, "%s", src);
+    free(src);
+    return (int)n;
+}
+
+int thvm_hip_window_compile_check(const UOpKernel *k, char *errbuf, u64 errlen) {
+    char *src = window_source(k);
+    if (!src) {
+        if (errbuf && errlen) snprintf(errbuf, errlen, "not a window-max or run-sum program");
+        return -1;
+    }
+    char err[256] = {0};
+    long n = rtc_compile_only(src, err, sizeof err);
+    free(src);
+    if (n < 0 && errbuf && errlen) snprintf(errbuf, errlen, "%s", err);
+    return (int)n;
 }
 
 int thvm_hip_dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits) {

@@ -37,6 +37,7 @@ typedef struct {
     int sync_each;           /* THVM_HIP_SYNC: synchronize after every dispatch */
     int dump_src;            /* THVM_HIP_DUMP: print generated HIP source */
     int no_dense;            /* THVM_HIP_NO_DENSE: skip dense recognizers */
+    int no_window;           /* THVM_HIP_NO_WINDOW: skip the window-max and run-sum kernels */
     int verbose;             /* THVM_HIP_VERBOSE */
     int dense_force;         /* THVM_HIP_DENSE_FORCE: matrix cores for every contraction */
     u32 dense_splits;        /* THVM_HIP_DENSE_SPLITS: fixed split-K factor (0: chosen) */
@@ -59,8 +60,11 @@ typedef struct {
     int rtc_fail;            /* THVM_HIP_RTC_FAIL: treat every program compile as failed (tests) */
     u64 n_dispatch, n_compile, n_cache_hit, n_dense;
     u64 n_fallback;          /* dispatches run on the KOp interpreter */
+    u64 n_window;            /* dispatches run on the window-max and run-sum kernels */
     u64 n_stream_sync;       /* host waits on the stream (buf_read, synchronize, ...) */
     hipModule_t static_mod;  /* precompiled kernels */
+    unsigned long long *comb_slots; /* single-pass combines: partial words (cleared after each use) */
+    u32 resident_waves;      /* waves the device holds at once for a single-pass grid */
     void *noalloc_scratch;   /* device address of the static workspace (noalloc.hip), or NULL */
     int noalloc;             /* a no-allocation dispatch is running: workspaces come from it */
     u64 noalloc_off;         /* bytes of the static workspace handed out in that dispatch */
@@ -137,7 +141,8 @@ typedef struct {
     u32 block;            /* threads per workgroup */
     u64 total;            /* serial: gids; group: outputs */
     u64 n_threads;        /* serial: number of vector lanes (ceil(total/vec)) */
-    u32 splits;           /* group: workgroups per output; > 1 adds a <name>_fin combine kernel */
+    u32 splits;           /* group: workgroups per output (> 1: partials combined in one pass) */
+    int combine_launch;   /* ... or, with splits > 1, by a separate <name>_fin kernel */
     u32 n_scal;           /* constant-index leaf loads that take an inline value (sm_, sv*) */
     u32 scal_leaf[KGEN_MAX_SCALARS], scal_index[KGEN_MAX_SCALARS];
     u32 scal_only_leaves; /* bit b: every load of leaf b is such a load */
@@ -151,8 +156,19 @@ int  kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, 
 void kgen_free(KGenResult *r);
 int  kgen_validate(const UOpKernel *k, char *err, size_t errlen);
 const char *kgen_prelude(void);
+int  kgen_alu_expr(u32 uop, u32 aux, const char *a, const char *b, char *out, size_t n);
 int  kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
                     char *out, size_t outlen);
+
+/* Single-pass combine area: one partial word per workgroup, zeroed at init;
+ * every kernel that uses it leaves it zeroed again. */
+#define COMB_SLOTS (1u << 19)
+/* A grid combines its partials in one pass only if it fits on the GPU at
+ * once (a combining workgroup waits for the others of its output): at most
+ * 16 waves per compute unit, hipb.resident_waves in all (4096 on MI355X's
+ * 256 CUs; the device's own count once initialised). */
+#define SINGLE_PASS_WAVES_PER_CU 16u
+u32 hipb_resident_waves(void);
 
 /* ---------------- rtc / cache ---------------- */
 typedef struct {
@@ -187,6 +203,13 @@ int  dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits);
 char *dense_source(const UOpKernel *k);
 void dense_reset_stats(void);
 void dense_shutdown(void);
+
+/* ---------------- pooling windows and run sums ---------------- */
+int  window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
+/* kind: 0 none, 1 window max, 2 run sum; splits: workgroups per output */
+int  window_analyze(const UOpKernel *k, u32 *kind, u32 *splits);
+char *window_source(const UOpKernel *k);
+void window_shutdown(void);
 
 /* ---------------- launch helpers ---------------- */
 int  hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params);

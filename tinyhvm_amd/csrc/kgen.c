@@ -105,6 +105,8 @@ typedef struct {
     u32 red_block;     /* GROUP: largest workgroup size */
     u32 split_target;  /* split GROUP: workgroups to aim for (outputs x splits) */
     u32 split_max;     /* split GROUP: most workgroups per output */
+    int combine_launch; /* split GROUP: partials to a workspace and a separate combine kernel */
+    int combine_mode;   /* THVM_HIP_SPLIT_COMBINE: 0 by the split count, 1 "launch", 2 "single" */
     u32 splits;        /* GROUP: workgroups per output (1: whole loop in one) */
     u32 split_acc;     /* GROUP split: the accumulator op */
     i32 *scal;         /* per op: index into the inline scalar list, or -1 */
@@ -299,6 +301,13 @@ static int lin_unit4(const OpI *o, u32 V) {
     if (V != 4 || o->ft || o->kind != K_LIN || (o->dv != 0 && o->dv % 4 != 0)) return 0;
     for (u32 v = 0; v < 4; v++) if (o->off[v] != v) return 0;
     return 1;
+}
+
+/* 0,0,1,1 on an even lane-0 value (an upsample-by-2 broadcast read with 4
+ * gids per lane): one 64-bit access serves the four lanes */
+static int lin_pair2(const OpI *o, u32 V) {
+    if (V != 4 || o->ft || o->kind != K_LIN || (o->dv != 0 && o->dv % 2 != 0)) return 0;
+    return o->off[0] == 0 && o->off[1] == 0 && o->off[2] == 1 && o->off[3] == 1;
 }
 
 static void analyze_vector(Gen *g) {
@@ -577,28 +586,35 @@ static void emit_decls(Gen *g) {
     }
 }
 
+/* The engine's ALU (src/backend/cpu/dispatch.c:5-21) on float operands a and
+ * b as one HIP expression: guarded DIV, strict-comparison MAX/CMP/RELU. */
+int kgen_alu_expr(u32 uop, u32 aux, const char *a, const char *b, char *out, size_t n) {
+    switch (uop) {
+    case UOP_ADD:  return snprintf(out, n, "%s + %s", a, b);
+    case UOP_SUB:  return snprintf(out, n, "%s - %s", a, b);
+    case UOP_MUL:  return snprintf(out, n, "%s * %s", a, b);
+    case UOP_DIV:  return snprintf(out, n, "(%s != 0.0f) ? (%s / %s) : 0.0f", b, a, b);
+    case UOP_MAX:  return snprintf(out, n, "(%s > %s) ? %s : %s", a, b, a, b);
+    case UOP_CMP:  return snprintf(out, n, "(%s > %s) ? 1.0f : 0.0f", a, b);
+    case UOP_NEG:  return snprintf(out, n, "-%s", a);
+    case UOP_RELU: return snprintf(out, n, "(%s > 0.0f) ? %s : 0.0f", a, a);
+    case UOP_EXP:  return snprintf(out, n, "expf(%s)", a);
+    case UOP_LOG:  return snprintf(out, n, "logf(%s)", a);
+    case UOP_SQRT: return snprintf(out, n, "sqrtf(%s)", a);
+    case UOP_CAST: return snprintf(out, n, "cast_f(%s, %uu)", a, aux);
+    default:       return snprintf(out, n, "%s", a);
+    }
+}
+
 static void emit_alu(Gen *g, const KOp *op, u32 i, u32 v) {
-    char a[128], b[128], d[64];
+    char a[128], b[128], d[64], x[512];
     Fx(g, op->arg[0], v, a);
     Fx(g, op->arg[1], v, b);
     const OpI *o = &g->oi[i];
     if (o->kind == K_VAR && g->V > 1) snprintf(d, sizeof d, "f%u_%u", i, v);
     else snprintf(d, sizeof d, "f%u", i);
-    switch (op->imm.u) {
-    case UOP_ADD:  sb_put(&g->sb, "    %s = %s + %s;\n", d, a, b); break;
-    case UOP_SUB:  sb_put(&g->sb, "    %s = %s - %s;\n", d, a, b); break;
-    case UOP_MUL:  sb_put(&g->sb, "    %s = %s * %s;\n", d, a, b); break;
-    case UOP_DIV:  sb_put(&g->sb, "    %s = (%s != 0.0f) ? (%s / %s) : 0.0f;\n", d, b, a, b); break;
-    case UOP_MAX:  sb_put(&g->sb, "    %s = (%s > %s) ? %s : %s;\n", d, a, b, a, b); break;
-    case UOP_CMP:  sb_put(&g->sb, "    %s = (%s > %s) ? 1.0f : 0.0f;\n", d, a, b); break;
-    case UOP_NEG:  sb_put(&g->sb, "    %s = -%s;\n", d, a); break;
-    case UOP_RELU: sb_put(&g->sb, "    %s = (%s > 0.0f) ? %s : 0.0f;\n", d, a, a); break;
-    case UOP_EXP:  sb_put(&g->sb, "    %s = expf(%s);\n", d, a); break;
-    case UOP_LOG:  sb_put(&g->sb, "    %s = logf(%s);\n", d, a); break;
-    case UOP_SQRT: sb_put(&g->sb, "    %s = sqrtf(%s);\n", d, a); break;
-    case UOP_CAST: sb_put(&g->sb, "    %s = cast_f(%s, %uu);\n", d, a, op->arg[2]); break;
-    default:       sb_put(&g->sb, "    %s = %s;\n", d, a); break;
-    }
+    kgen_alu_expr(op->imm.u, op->arg[2], a, b, x, sizeof x);
+    sb_put(&g->sb, "    %s = %s;\n", d, x);
 }
 
 /* Emit one op (all vector lanes). `fast` selects unchecked loads for indices
@@ -675,6 +691,14 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
             else
                 sb_put(&g->sb, "    { float4 t_ = ld4%s(p%u, c%u, %s); f%u_0 = t_.x; f%u_1 = t_.y; f%u_2 = t_.z; f%u_3 = t_.w; }\n",
                        sfx, bi, bi, a, i, i, i, i);
+        } else if (lin_pair2(ix, V) && dt == DTYPE_F32) {
+            U(g, op->arg[0], 0, a);
+            if (unchecked)
+                sb_put(&g->sb, "    { float2 t_ = ld2_u(p%u, %s); f%u_0 = t_.x; f%u_1 = t_.x; f%u_2 = t_.y; f%u_3 = t_.y; }\n",
+                       bi, a, i, i, i, i);
+            else
+                sb_put(&g->sb, "    { float2 t_ = ld2(p%u, c%u, %s); f%u_0 = t_.x; f%u_1 = t_.x; f%u_2 = t_.y; f%u_3 = t_.y; }\n",
+                       bi, bi, a, i, i, i, i);
         } else {
             for (u32 v = 0; v < V; v++) {
                 u32 u = v;
@@ -850,6 +874,11 @@ static const char *PRELUDE =
 "__device__ __forceinline__ float ld_i32_u(const char* p, u32 i) { return (float)((const int*)p)[i]; }\n"
 "__device__ __forceinline__ float ld_u32_u(const char* p, u32 i) { return (float)((const u32*)p)[i]; }\n"
 "__device__ __forceinline__ float4 ld4_u(const char* p, u32 i) { return *(const float4*)((const float*)p + i); }\n"
+"__device__ __forceinline__ float2 ld2_u(const char* p, u32 i) { return *(const float2*)((const float*)p + i); }\n"
+"__device__ __forceinline__ float2 ld2(const char* p, u32 n, u32 i) {\n"
+"  if (i + 1u < n && i + 1u >= i) return *(const float2*)((const float*)p + i);\n"
+"  return make_float2(ld_f32(p, n, i), ld_f32(p, n, i + 1u));\n"
+"}\n"
 "__device__ __forceinline__ float4 ld4(const char* p, u32 n, u32 i) {\n"
 "  if (i + 3u < n && i + 3u >= i) return *(const float4*)((const float*)p + i);\n"
 "  return make_float4(ld_f32(p, n, i), ld_f32(p, n, i + 1u), ld_f32(p, n, i + 2u), ld_f32(p, n, i + 3u));\n"
@@ -899,6 +928,32 @@ static const char *PRELUDE =
 "  float s = red[0];\n"
 "  for (u32 w = 1u; w < (blockDim.x >> 6); w++) { float y = red[w]; s = (s > y) ? s : y; }\n"
 "  return s;\n"
+"}\n"
+/* Single-pass combine of per-workgroup partials. Each of the S workgroups
+ * of output o but the last publishes its partial as one 64-bit word (a ready
+ * flag in the high half, the float's bits in the low half) with an
+ * agent-scope atomic store. The workgroup with split index S-1 takes the
+ * words in index order, its lanes each waiting (bounded) until their word is
+ * marked ready, clears them for the next launch, and combines them with its
+ * own partial in a fixed order. Flag and value share one word, so no fence
+ * is needed, no cache is written back and no word is contended; the result
+ * does not depend on timing. The host uses it only for grids that fit on
+ * the GPU at once (every workgroup resident together), so the waiting
+ * workgroup never holds back one it waits for. */
+"__device__ __forceinline__ void comb_put(unsigned long long* sl, u32 o, u32 sp, u32 S, float part) {\n"
+"  if (threadIdx.x == 0u)\n"
+"    __hip_atomic_store(sl + (unsigned long long)o * S + sp, (1ull << 32) | (unsigned long long)__float_as_uint(part),\n"
+"                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+"}\n"
+"__device__ __forceinline__ float comb_take(unsigned long long* sl, u32 o, u32 s, u32 S) {\n"
+"  unsigned long long* w = sl + (unsigned long long)o * S + s;\n"
+"  unsigned long long v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+"  for (u32 n = 0u; (v >> 32) == 0ull && n < (1u << 22); n++) {\n"
+"    __builtin_amdgcn_s_sleep(2);\n"
+"    v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+"  }\n"
+"  __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+"  return (v >> 32) ? __uint_as_float((u32)v) : __uint_as_float(0x7fc00000u);\n"
 "}\n";
 
 const char *kgen_prelude(void) { return PRELUDE; }
@@ -1065,6 +1120,35 @@ static void group_split_plan(Gen *g) {
     g->split_acc = t;
 }
 
+/* The end of a split workgroup (its partial t_ reduced): publish it, or, in
+ * the workgroup with the last split index, combine the output's partials in
+ * index order (lane l: partials l, l + block, ...; then the fixed
+ * shuffle/LDS tree), add the accumulator's initial value and store. */
+static void emit_single_pass(Gen *g, u32 t, int rmax) {
+    const KOp *init = &g->k->ops[t];
+    sb_put(&g->sb, "      t_ = %s(t_, red_);\n"
+                   "      if (sp_ != %uu) {\n"
+                   "        comb_put(sl_, gid, sp_, %uu, t_);\n"
+                   "      } else {\n"
+                   "        float w_ = %s;\n"
+                   "        for (u32 s_ = lane; s_ < %uu; s_ += %uu) {\n"
+                   "          const float x_ = (s_ == %uu) ? t_ : comb_take(sl_, gid, s_, %uu);\n"
+                   "          %s\n"
+                   "        }\n"
+                   "        w_ = %s(w_, red_);\n"
+                   "        if (lane == 0u) {\n"
+                   "          float f_ = __uint_as_float(0x%08xu);\n"
+                   "          %s\n"
+                   "          %s(p0, c0, gid, f_);\n"
+                   "        }\n"
+                   "      }\n"
+                   "    }\n",
+           rmax ? "bmax" : "bsum", g->splits - 1, g->splits, rmax ? "__uint_as_float(0xff800000u)" : "0.0f",
+           g->splits, g->block, g->splits - 1, g->splits, rmax ? "w_ = (w_ > x_) ? w_ : x_;" : "w_ = w_ + x_;",
+           rmax ? "bmax" : "bsum", init->imm.u, rmax ? "f_ = (f_ > w_) ? f_ : w_;" : "f_ = f_ + w_;",
+           dt_st(g->k->out_dtype));
+}
+
 /* One parallel loop of GROUP mode. */
 static void emit_group_loop(Gen *g, u32 r) {
     const UOpKernel *k = g->k;
@@ -1142,9 +1226,11 @@ static void emit_group_loop(Gen *g, u32 r) {
         if (g->oi[t].acc_type == UOP_RMAX) {
             sb_put(&g->sb, "    { float t_ = p%u_0;\n", t);
             for (u32 v = 1; v < V; v++) sb_put(&g->sb, "      t_ = (t_ > p%u_%u) ? t_ : p%u_%u;\n", t, v, t, v);
-            if (g->splits > 1)
+            if (g->splits > 1 && g->combine_launch)
                 sb_put(&g->sb, "      t_ = bmax(t_, red_);\n"
                                "      if (lane == 0) ws_[(unsigned long long)gid * %uu + sp_] = t_; }\n", g->splits);
+            else if (g->splits > 1)
+                emit_single_pass(g, t, 1);
             else
                 sb_put(&g->sb, "      f%u = bmax(t_, red_); }\n", t);
         } else {
@@ -1153,9 +1239,11 @@ static void emit_group_loop(Gen *g, u32 r) {
                 sb_put(&g->sb, "    { float t_ = p%u_0;\n", t);
                 for (u32 v = 1; v < V; v++) sb_put(&g->sb, "      t_ = t_ + p%u_%u;\n", t, v);
             }
-            if (g->splits > 1)
+            if (g->splits > 1 && g->combine_launch)
                 sb_put(&g->sb, "      t_ = bsum(t_, red_);\n"
                                "      if (lane == 0) ws_[(unsigned long long)gid * %uu + sp_] = t_; }\n", g->splits);
+            else if (g->splits > 1)
+                emit_single_pass(g, t, 0);
             else
                 sb_put(&g->sb, "      f%u = f%u + bsum(t_, red_); }\n", t, t);
         }
@@ -1190,6 +1278,8 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
         if (G.split_target < 1) G.split_target = 4096;
         G.split_max = (e = getenv("THVM_HIP_SPLIT_MAX")) ? (u32)atoi(e) : 512;
         if (G.split_max < 2 || G.split_max > 1024) G.split_max = 512;
+        e = getenv("THVM_HIP_SPLIT_COMBINE");
+        G.combine_mode = !e ? 0 : strcmp(e, "launch") == 0 ? 1 : strcmp(e, "single") == 0 ? 2 : 0;
         G.per_thread = (e = getenv("THVM_HIP_EW_PER_THREAD")) ? (u32)atoi(e) : 1;
         if (G.per_thread < 1) G.per_thread = 1;
         if (G.per_thread > 8) G.per_thread = 8;
@@ -1235,6 +1325,11 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
     }
     G.splits = 1;
     if (G.mode == KG_MODE_GROUP) group_split_plan(&G);
+    /* The partials combine in the same launch when the whole grid fits on
+     * the GPU at once; a larger grid writes them to a workspace for a
+     * combine kernel. */
+    G.combine_launch = G.combine_mode == 1 ||
+                       (G.combine_mode == 0 && (u64)G.total * G.splits * (G.block / 64) > hipb_resident_waves());
     G.scal = malloc(k->n_ops * sizeof(i32));
     if (!G.scal) { free(G.oi); snprintf(err, errlen, "oom"); return 0; }
     plan_inline_scalars(&G, out);
@@ -1259,7 +1354,7 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
     }
     sb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", G.block, out->name);
     emit_params(&G);
-    if (G.splits > 1) sb_put(s, ", float* ws_");
+    if (G.splits > 1) sb_put(s, G.combine_launch ? ", float* ws_" : ", unsigned long long* sl_");
     sb_put(s, ") {\n");
     if (G.mode == KG_MODE_SERIAL) {
         u64 nvec = ((u64)total + G.V - 1) / G.V;          /* thread-vectors */
@@ -1306,7 +1401,7 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
         out->n_threads = total;
     }
     sb_put(s, "}\n");
-    if (G.splits > 1) {
+    if (G.splits > 1 && G.combine_launch) {
         /* combine: one workgroup per output; lane l takes partials l, l + 256,
          * ... in order, then a fixed shuffle/LDS tree, then the initial value */
         const KOp *init = &k->ops[G.split_acc];
@@ -1349,6 +1444,7 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
     out->block = G.block;
     out->total = total;
     out->splits = G.splits;
+    out->combine_launch = G.splits > 1 && G.combine_launch;
     return 1;
 }
 

@@ -177,8 +177,10 @@ void pool_capture_begin(u8 *arena, u64 bytes, PoolPins *pins) {
     P.arena_cap = bytes;
     P.arena_off = 0;
     P.capture_pins = pins;
-    /* the fill block of absent buffers is in every graph's kernels */
+    /* the fill block of absent buffers and the combine area are in every
+     * graph's kernels */
     capture_pin(hipb.dummy, hipb.dummy_cap);
+    capture_pin(hipb.comb_slots, (u64)COMB_SLOTS * 8);
 }
 
 void pool_capture_end(void) {

@@ -234,7 +234,7 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
     char fin_name[48];
     snprintf(fin_name, sizeof fin_name, "%s_fin", g.name);
     if (hipModuleGetFunction(&fn, mod, g.name) != hipSuccess ||
-        (g.splits > 1 && hipModuleGetFunction(&fn_fin, mod, fin_name) != hipSuccess)) {
+        (g.combine_launch && hipModuleGetFunction(&fn_fin, mod, fin_name) != hipSuccess)) {
         fprintf(stderr, "tinyhvm-hip: kernel symbol missing\n");
         HIPB_CHECK(hipModuleUnload(mod));
         kgen_free(&g);

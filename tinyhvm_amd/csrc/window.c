@@ -1,0 +1,750 @@
+/*
+ * window.c - hand-written kernels for the pooling windows and the
+ * per-channel reductions of the engine's max-pool and batchnorm.
+ *
+ * The engine has no max-pool or batchnorm op on this path. thvm_maxpool2d
+ * (src/nn/conv.c:484-514) is an RMAX over the window axes of a pool view,
+ * and batchnorm (src/nn/batchnorm.c:35-111) is built from SUMs over axes
+ * [0,2,3] and elementwise kernels. Both reach the backend as KOp programs of
+ * the form
+ *     acc = init;  for r in [0,T): acc = acc (+|max) f(loads(gid, r));  out[gid] = acc
+ * This file recognises two such shapes, with the digit analysis of
+ * affine.c, and runs them on kernels written for them:
+ *
+ *   window max      RMAX over a small window (T <= 16): one load whose index
+ *                   is base(gid) + off(r). Each output is one lane; the
+ *                   window's elements are read with 8- or 16-byte loads
+ *                   (lanes along the output columns read contiguous memory,
+ *                   where the generated kernel's 4-byte loads sit two floats
+ *                   apart), and the maximum is taken in the engine's r order
+ *                   with its rule acc > v ? acc : v, so the result, tied and
+ *                   signed zeros and NaNs included, is the engine's bit for
+ *                   bit (src/backend/cpu/uop.c:80-88).
+ *   run sums        SUM over a long loop (T >= 4096) of an elementwise
+ *                   function of loads that either read contiguous runs along
+ *                   r (a channel's image rows, [0,2,3]: runs of H*W floats, one
+ *                   per image) or do not depend on r (a per-channel mean).
+ *                   The reduction is split over workgroups along the runs;
+ *                   lanes read 16-byte vectors and keep per-lane partials in
+ *                   sequence; a wavefront shuffle tree and an LDS tree give a
+ *                   workgroup's partial, and the last workgroup of each output
+ *                   combines the partials in index order in the same launch
+ *                   (the single-pass combine of the generator's prelude). The
+ *                   order of the sum differs from the engine's serial one:
+ *                   tolerance 1e-4 normwise.
+ *
+ * Anything else, or a dispatch whose buffers are smaller than the plan's
+ * largest index or not aligned for its vector loads, takes the generated
+ * kernels.
+ */
+#include <stdarg.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "hipb.h"
+#include "thvm_hip.h"
+#include "affine.h"
+
+#define WIN_MAX_TRIP 16          /* window max: at most this many elements per window */
+#define WIN_SUM_MIN_TRIP 4096    /* run sums: reductions at least this long */
+#define WIN_SUM_MIN_RUN 16       /* ... over contiguous runs at least this long */
+#define WIN_SUM_TARGET_WG 1024   /* workgroups to aim for in all (256 lanes each: all resident at once) */
+#define WIN_SUM_MIN_CHUNK 512    /* vectors per workgroup, at least */
+#define WIN_SUM_MAX_OUTPUTS 256  /* run sums: few outputs (more take the generated group kernels) */
+#define WIN_MAX_LOADS 16
+#define WIN_BLOCK 256u
+
+enum { WIN_NONE = 0, WIN_MAX = 1, WIN_SUM = 2 };
+
+typedef struct {
+    int kind;
+    u32 total;                   /* outputs (= gids) */
+    u32 trip;                    /* loop length */
+    u32 init_bits;               /* the accumulator's initial value */
+    u32 R, E, acc, value;        /* op indices: RANGE, ENDRANGE, ACC, accumulated value */
+    u32 n_ld;
+    u32 ld_op[WIN_MAX_LOADS];
+    Aff ld_aff[WIN_MAX_LOADS];
+    u8 ld_r[WIN_MAX_LOADS];      /* the index depends on r */
+    u64 ld_max[WIN_MAX_LOADS];   /* the largest index it forms */
+    u32 W;                       /* elements per vector load: 2 or 4 (window max), 1 or 4 (sums) */
+    /* window max */
+    u32 off[WIN_MAX_TRIP];       /* r-offset of window element r */
+    u64 cover_max;               /* the largest index its vector loads touch */
+    /* run sums */
+    u32 L;                       /* run length along r */
+    u32 n_outer;
+    u32 outer_div[DG_MAX], outer_mod[DG_MAX], outer_coef[DG_MAX];
+    u32 S;                       /* workgroups per output */
+    u32 unroll;                  /* run sums: loop unroll */
+    int launch;                  /* run sums: partials through a workspace and a combine kernel */
+    u32 U;                       /* window max: units (outputs, or pairs of outputs) per lane */
+    u32 P;                       /* window max: adjacent outputs per vector load (1 or 2) */
+    u32 c1;                      /* window max: input step between adjacent outputs */
+    u8 cone[KOP_MAX];
+} WinPlan;
+
+static u32 env_u32(const char *name, u32 dflt) {
+    const char *e = getenv(name);
+    return e && e[0] ? (u32)atoi(e) : dflt;
+}
+
+/* ---------------- recognition ---------------- */
+
+static int win_debug(void) {
+    static int v = -1;
+    if (v < 0) { const char *e = getenv("THVM_HIP_WINDOW_DEBUG"); v = e && e[0] == '1'; }
+    return v;
+}
+#define WREJECT(why) do { if (win_debug()) fprintf(stderr, "window: not recognised: %s\n", why); return 0; } while (0)
+
+static int alu_unary(u32 uop) {
+    return uop == UOP_NEG || uop == UOP_EXP || uop == UOP_LOG || uop == UOP_RELU || uop == UOP_CAST || uop == UOP_SQRT;
+}
+
+/* Index sums must not wrap in u32 (the kernel computes them in u32, the
+ * plan in u64): small coefficients and constant, and a largest value below
+ * 2^32. */
+static int aff_no_wrap(const DCtx *c, const Aff *a) {
+    if (!a->ok || a->cst >= 0x80000000u) return 0;
+    for (u32 t = 0; t < a->n; t++)
+        if (a->coef[t] >= 0x80000000u) return 0;
+    return aff_max(c, a) < 0xFFFFFFFFull;
+}
+
+static int same_r_part(const Aff *a, const Aff *b) {
+    u32 na = 0, nb = 0;
+    for (u32 t = 0; t < a->n; t++) na += a->d[t].var == 1;
+    for (u32 t = 0; t < b->n; t++) nb += b->d[t].var == 1;
+    if (na != nb) return 0;
+    for (u32 t = 0; t < a->n; t++) {
+        if (a->d[t].var != 1) continue;
+        int found = 0;
+        for (u32 u = 0; u < b->n; u++)
+            if (b->d[u].var == 1 && b->d[u].div == a->d[t].div && b->d[u].mod == a->d[t].mod &&
+                b->coef[u] == a->coef[t]) found = 1;
+        if (!found) return 0;
+    }
+    return 1;
+}
+
+static int win_recognize(const UOpKernel *k, WinPlan *p) {
+    memset(p, 0, sizeof *p);
+    char err[128];
+    if (!kgen_validate(k, err, sizeof err)) WREJECT("invalid program");
+    if (k->out_dtype != DTYPE_F32) WREJECT("output not f32");
+    i32 R = -1, E = -1;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        if (k->ops[i].type == KOP_RANGE) {
+            if (R >= 0) WREJECT("more than one loop");
+            R = (i32)i;
+        } else if (k->ops[i].type == KOP_ENDRANGE) {
+            E = (i32)i;
+        }
+    }
+    if (R < 0 || E < 0) WREJECT("no loop");
+    if ((u32)E + 2 != k->n_ops) WREJECT("ops after the store");
+    const KOp *st = &k->ops[E + 1];
+    if (st->type != KOP_STORE) WREJECT("no store after the loop");
+    u32 t = st->arg[1];
+    if (t >= (u32)R || k->ops[t].type != KOP_ACC_INIT) WREJECT("store is not the accumulator");
+    i32 acc = -1;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        if (k->ops[i].type != KOP_ACC) continue;
+        if (acc >= 0 || i <= (u32)R || i >= (u32)E || k->ops[i].arg[0] != t) WREJECT("accumulators");
+        acc = (i32)i;
+    }
+    if (acc < 0) WREJECT("no accumulation");
+    for (u32 i = 0; i < (u32)R; i++)
+        if (op_type_is_float(k->ops[i].type) && i != t) WREJECT("float work before the loop");
+    u32 value = k->ops[acc].arg[1];
+    if (value <= (u32)R || value >= (u32)acc || !op_type_is_float(k->ops[value].type)) WREJECT("accumulated value");
+    mark_cone(k, value, p->cone);
+    if (p->cone[t]) WREJECT("the accumulator feeds its own value");
+    for (u32 i = (u32)R + 1; i < (u32)E; i++) {
+        const KOp *op = &k->ops[i];
+        if (i == (u32)acc || !op_type_is_float(op->type)) continue;
+        if (!p->cone[i]) WREJECT("float work outside the accumulated value");
+        if (op->type == KOP_MASK || op->type == KOP_ACC_INIT) WREJECT("masked or nested accumulation");
+        if (op->type == KOP_ALU) {
+            if (!op_type_is_float(k->ops[op->arg[0]].type)) WREJECT("integer operand");
+            if (!alu_unary(op->imm.u) && !op_type_is_float(k->ops[op->arg[1]].type)) WREJECT("integer operand");
+        }
+        if (op->type == KOP_LOAD) {
+            u32 bi = op->imm.u;
+            if (bi == 0 || bi > k->n_leaves || k->leaf_dtypes[bi - 1] != DTYPE_F32) WREJECT("load buffer");
+            if (p->n_ld >= WIN_MAX_LOADS) WREJECT("too many loads");
+            p->ld_op[p->n_ld++] = i;
+        }
+    }
+    u64 total = k->local_size > 0 ? (u64)k->grid[0] : (u64)k->grid[0] * k->grid[1] * k->grid[2];
+    if (total == 0 || total > 0xFFFFFFFFull) WREJECT("launch size");
+    p->total = (u32)total;
+    p->trip = k->ops[R].imm.u;
+    if (p->trip == 0) WREJECT("empty loop");
+    p->init_bits = k->ops[t].imm.u;
+    p->R = (u32)R;
+    p->E = (u32)E;
+    p->acc = (u32)acc;
+    p->value = value;
+
+    Aff aff[KOP_MAX];
+    DCtx c = {k, p->total, p->trip, R, aff};
+    analyze_aff(&c);
+    const Aff *sa = &aff[st->arg[0]];
+    int is_gid = sa->ok && sa->cst == 0 &&
+                 ((sa->n == 1 && sa->coef[0] == 1 && sa->d[0].var == 0 && sa->d[0].div == 1 && sa->d[0].mod == 0) ||
+                  (sa->n == 0 && p->total == 1));   /* one output: gid is the constant 0 */
+    if (!is_gid) WREJECT("store index is not gid");
+    for (u32 j = 0; j < p->n_ld; j++) {
+        const Aff *a = &aff[k->ops[p->ld_op[j]].arg[0]];
+        if (!aff_no_wrap(&c, a)) WREJECT("load index not a bounded digit sum");
+        p->ld_aff[j] = *a;
+        p->ld_max[j] = aff_max(&c, a);
+        for (u32 q = 0; q < a->n; q++) p->ld_r[j] |= a->d[q].var == 1;
+    }
+
+    if (k->ops[acc].imm.u == UOP_RMAX) {
+        /* window max: the accumulated value is the one load itself */
+        if (p->trip > WIN_MAX_TRIP || p->n_ld != 1 || p->ld_op[0] != value) WREJECT("not a window max");
+        const Aff *a = &p->ld_aff[0];
+        for (u32 r = 0; r < p->trip; r++) p->off[r] = (u32)(aff_eval(a, 0, r) - a->cst);
+        for (u32 W = 4; W >= 2; W /= 2) {
+            int ok = a->cst % W == 0;
+            for (u32 q = 0; q < a->n; q++)
+                if (a->d[q].var == 0 && a->coef[q] % W) ok = 0;
+            /* vectors cover the window with little waste */
+            u32 groups[WIN_MAX_TRIP], ng = 0;
+            for (u32 r = 0; r < p->trip && ok; r++) {
+                u32 g = p->off[r] / W, seen = 0;
+                for (u32 x = 0; x < ng; x++) seen |= groups[x] == g;
+                if (!seen) groups[ng++] = g;
+            }
+            if (ok && ng * W <= 2 * p->trip) {
+                p->W = W;
+                u32 max_off = 0, end = 0;
+                for (u32 r = 0; r < p->trip; r++) if (p->off[r] > max_off) max_off = p->off[r];
+                for (u32 x = 0; x < ng; x++) if (groups[x] * W + W - 1 > end) end = groups[x] * W + W - 1;
+                p->cover_max = p->ld_max[0] - max_off + end;
+                break;
+            }
+        }
+        if (!p->W) WREJECT("window rows not vector aligned");
+        /* pairs of adjacent outputs in one 16-byte vector: the innermost output
+         * digit steps the input by c1, every window element and its
+         * neighbour's sit in the same aligned 4 floats */
+        p->P = 1;
+        if (env_u32("THVM_HIP_WIN_PAIR", 1)) {
+            int inner = -1, ok = a->cst % 4 == 0 && p->total % 2 == 0;
+            for (u32 q = 0; q < a->n; q++) {
+                if (a->d[q].var != 0) continue;
+                if (a->d[q].div == 1) inner = (int)q;
+                else if (a->coef[q] % 4) ok = 0;
+            }
+            if (inner < 0 || a->d[inner].mod % 2 || (2 * a->coef[inner]) % 4) ok = 0;
+            u32 c1 = inner >= 0 ? a->coef[inner] : 0;
+            for (u32 r = 0; r < p->trip && ok; r++)
+                if (p->off[r] % 4 + c1 > 3) ok = 0;
+            if (ok) {
+                p->P = 2;
+                p->W = 4;
+                p->c1 = c1;
+                u32 max_off = 0, end = 0;
+                for (u32 r = 0; r < p->trip; r++) {
+                    if (p->off[r] > max_off) max_off = p->off[r];
+                    if (p->off[r] / 4 * 4 + 3 > end) end = p->off[r] / 4 * 4 + 3;
+                }
+                /* the last output of a pair is odd: its vectors end where the even one's do */
+                p->cover_max = p->ld_max[0] - max_off - c1 + end;
+            }
+        }
+        p->U = env_u32("THVM_HIP_WIN_OUT", 2);
+        if (p->U != 1 && p->U != 2 && p->U != 4 && p->U != 8) p->U = 2;
+        p->kind = WIN_MAX;
+        return 1;
+    }
+    if (k->ops[acc].imm.u != UOP_SUM) WREJECT("reduction type");
+    if (p->trip < WIN_SUM_MIN_TRIP) WREJECT("short reduction");
+    if (p->total > WIN_SUM_MAX_OUTPUTS) WREJECT("many outputs");
+    /* run sums: every r-dependent load has the same r part, a contiguous run
+     * (digits div = run, coef = run, from run 1) and outer digits beyond it */
+    i32 first = -1;
+    for (u32 j = 0; j < p->n_ld; j++) {
+        if (!p->ld_r[j]) continue;
+        if (first < 0) first = (i32)j;
+        else if (!same_r_part(&p->ld_aff[first], &p->ld_aff[j])) WREJECT("loads with different r parts");
+    }
+    if (first < 0) WREJECT("nothing depends on r");
+    const Aff *a = &p->ld_aff[first];
+    u8 inner[DG_MAX] = {0};
+    u64 run = 1;
+    for (;;) {
+        int hit = -1;
+        for (u32 q = 0; q < a->n; q++)
+            if (a->d[q].var == 1 && !inner[q] && a->d[q].div == run && a->coef[q] == run) hit = (int)q;
+        if (hit < 0) break;
+        inner[hit] = 1;
+        if (!a->d[hit].mod) { run = p->trip; break; }
+        run *= a->d[hit].mod;
+        if (run >= p->trip) { run = p->trip; break; }
+    }
+    if (run < WIN_SUM_MIN_RUN || p->trip % run) WREJECT("no long contiguous runs");
+    p->L = (u32)run;
+    for (u32 q = 0; q < a->n; q++) {
+        if (a->d[q].var != 1 || inner[q]) continue;
+        if (a->d[q].div < p->L || a->d[q].div % p->L) WREJECT("outer digit inside a run");
+        if (p->n_outer >= DG_MAX) WREJECT("too many outer digits");
+        p->outer_div[p->n_outer] = a->d[q].div / p->L;
+        p->outer_mod[p->n_outer] = a->d[q].mod;
+        p->outer_coef[p->n_outer] = a->coef[q];
+        p->n_outer++;
+    }
+    /* 16-byte vectors when every run and every base is 4-float aligned */
+    p->W = p->L % 4 == 0 ? 4 : 1;
+    for (u32 j = 0; j < p->n_ld && p->W == 4; j++) {
+        if (!p->ld_r[j]) continue;
+        const Aff *b = &p->ld_aff[j];
+        if (b->cst % 4) p->W = 1;
+        for (u32 q = 0; q < b->n; q++)
+            if ((b->d[q].var == 0 || !(b->d[q].div < p->L)) && b->coef[q] % 4) p->W = 1;
+    }
+    u32 units = p->trip / p->W;
+    /* workgroups per output: up to the number the GPU holds at once (the
+     * combine then stays in the launch), each with at least a minimum chunk */
+    p->S = 1;
+    while (p->S < 1024 && (u64)p->total * p->S * 2 <= WIN_SUM_TARGET_WG && units / (p->S * 2) >= WIN_SUM_MIN_CHUNK)
+        p->S *= 2;
+    {
+        u32 fs = env_u32("THVM_HIP_WIN_S", 0);
+        if (fs && (fs & (fs - 1)) == 0 && fs <= 1024) p->S = fs;
+    }
+    p->unroll = env_u32("THVM_HIP_WIN_UNROLL", 2);
+    if (p->unroll < 1 || p->unroll > 16) p->unroll = 2;
+    {
+        const char *e = getenv("THVM_HIP_WIN_COMBINE");
+        if (e && strcmp(e, "single") == 0) p->launch = 0;
+        else if (e && strcmp(e, "launch") == 0) p->launch = 1;
+        else p->launch = 0;
+    }
+    /* one pass only when the whole grid is on the GPU at once */
+    if (p->S > 1 && !p->launch &&
+        ((u64)p->total * p->S > COMB_SLOTS || (u64)p->total * p->S * (WIN_BLOCK / 64) > hipb_resident_waves()))
+        p->launch = 1;
+    if ((u64)p->total * p->S > 0xFFFFFFFFull / WIN_BLOCK) WREJECT("launch size");
+    p->kind = WIN_SUM;
+    return 1;
+}
+
+/* ---------------- code generation ---------------- */
+
+typedef struct { char *p; size_t n, cap; } WSB;
+static void wsb_put(WSB *s, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
+static void wsb_put(WSB *s, const char *fmt, ...) {
+    va_list ap;
+    for (;;) {
+        size_t room = s->cap - s->n;
+        va_start(ap, fmt);
+        int w = s->p ? vsnprintf(s->p + s->n, room, fmt, ap) : -1;
+        va_end(ap);
+        if (w >= 0 && (size_t)w < room) { s->n += (size_t)w; return; }
+        size_t nc = s->cap ? s->cap * 2 : 16384;
+        while (w >= 0 && nc < s->n + (size_t)w + 1) nc *= 2;
+        char *np = realloc(s->p, nc);
+        if (!np) return;
+        s->p = np;
+        s->cap = nc;
+    }
+}
+
+/* gid part of a load's index as a u32 expression of the variable `g` */
+static void emit_base_expr(WSB *s, const Aff *a, const char *g) {
+    wsb_put(s, "%uu", a->cst);
+    for (u32 q = 0; q < a->n; q++) {
+        if (a->d[q].var != 0) continue;
+        if (a->d[q].mod) wsb_put(s, " + %uu * ((%s / %uu) %% %uu)", a->coef[q], g, a->d[q].div, a->d[q].mod);
+        else wsb_put(s, " + %uu * (%s / %uu)", a->coef[q], g, a->d[q].div);
+    }
+}
+
+/* gid part of a load's index as a u32 expression of `gid` */
+static void emit_base(WSB *s, const char *name, const Aff *a) {
+    wsb_put(s, "  const u32 %s = %uu", name, a->cst);
+    for (u32 q = 0; q < a->n; q++) {
+        if (a->d[q].var != 0) continue;
+        if (a->d[q].mod) wsb_put(s, " + %uu * ((gid / %uu) %% %uu)", a->coef[q], a->d[q].div, a->d[q].mod);
+        else wsb_put(s, " + %uu * (gid / %uu)", a->coef[q], a->d[q].div);
+    }
+    wsb_put(s, ";\n");
+}
+
+static void float_bits(char *out, size_t n, u32 bits) { snprintf(out, n, "__uint_as_float(0x%08xu)", bits); }
+
+static char *gen_window_max(const UOpKernel *k, const WinPlan *p, const char *name) {
+    WSB s = {0};
+    (void)k;
+    const u32 U = p->U, P = p->P;
+    const u64 units = (u64)p->total / P;          /* P = 2 only when total is even */
+    const u64 lanes = (units + U - 1) / U;
+    /* one vector per distinct group of W elements, in first-use order */
+    u32 groups[WIN_MAX_TRIP], ng = 0;
+    for (u32 r = 0; r < p->trip; r++) {
+        u32 g = p->off[r] / p->W, seen = 0;
+        for (u32 x = 0; x < ng; x++) seen |= groups[x] == g;
+        if (!seen) groups[ng++] = g;
+    }
+    const char *vt = p->W == 4 ? "v4f_" : "v2f_";
+    wsb_put(&s, "%s\n", kgen_prelude());
+    wsb_put(&s, "typedef float v2f_ __attribute__((ext_vector_type(2)));\n");
+    wsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(char* p0, const char* px) {\n", WIN_BLOCK, name);
+    wsb_put(&s, "  const unsigned long long t_ = ((unsigned long long)blockIdx.y * gridDim.x + blockIdx.x) * %uull + "
+                "threadIdx.x;\n", WIN_BLOCK);
+    wsb_put(&s, "  if (t_ >= %lluull) return;\n", (unsigned long long)lanes);
+    /* lane t takes units t, t + lanes, ... (a unit: P adjacent outputs); a
+     * unit past the end reads unit 0's windows (in range) and stores nothing */
+    for (u32 j = 0; j < U; j++) {
+        char g[16];
+        snprintf(g, sizeof g, "g%u_", j);
+        wsb_put(&s, "  const u32 o%u_ = (u32)t_ + %lluu;\n", j, (unsigned long long)(lanes * j));
+        wsb_put(&s, "  const u32 g%u_ = (o%u_ < %lluu) ? o%u_ * %uu : 0u;\n", j, j, (unsigned long long)units, j, P);
+        wsb_put(&s, "  const u32 b%u_ = ", j);
+        emit_base_expr(&s, &p->ld_aff[0], g);
+        wsb_put(&s, ";\n");
+    }
+    /* every unit's loads before any use: U * groups loads in flight per lane */
+    for (u32 j = 0; j < U; j++)
+        for (u32 x = 0; x < ng; x++)
+            wsb_put(&s, "  const %s v%u_%u_ = __builtin_nontemporal_load((const %s*)((const float*)px + b%u_ + %uu));\n",
+                    vt, j, x, vt, j, groups[x] * p->W);
+    char fb[64];
+    float_bits(fb, sizeof fb, p->init_bits);
+    static const char comp[4] = {'x', 'y', 'z', 'w'};
+    for (u32 j = 0; j < U; j++) {
+        wsb_put(&s, "  if (o%u_ < %lluu) {\n", j, (unsigned long long)units);
+        for (u32 q = 0; q < P; q++) {
+            wsb_put(&s, "    float a%u_ = %s;\n", q, fb);
+            for (u32 r = 0; r < p->trip; r++) {
+                u32 g = p->off[r] / p->W, x = 0;
+                while (groups[x] != g) x++;
+                wsb_put(&s, "    { const float e_ = v%u_%u_.%c; a%u_ = (a%u_ > e_) ? a%u_ : e_; }\n", j, x,
+                        comp[(p->off[r] + q * p->c1) % p->W], q, q, q);
+            }
+        }
+        if (P == 2) wsb_put(&s, "    *(float2*)((float*)p0 + g%u_) = make_float2(a0_, a1_);\n  }\n", j);
+        else wsb_put(&s, "    ((float*)p0)[g%u_] = a0_;\n  }\n", j);
+    }
+    wsb_put(&s, "}\n");
+    return s.p;
+}
+
+/* one body op for vector component v (loads were emitted before) */
+static void emit_body_op(WSB *s, const UOpKernel *k, const WinPlan *p, u32 i, u32 v) {
+    const KOp *op = &k->ops[i];
+    char a[64], b[64], x[256], fb[64];
+    switch (op->type) {
+    case KOP_CONST_F:
+        float_bits(fb, sizeof fb, op->imm.u);
+        wsb_put(s, "    const float f%u_%u = %s;\n", i, v, fb);
+        break;
+    case KOP_ALU:
+        snprintf(a, sizeof a, "f%u_%u", op->arg[0], v);
+        snprintf(b, sizeof b, "f%u_%u", alu_unary(op->imm.u) ? op->arg[0] : op->arg[1], v);
+        kgen_alu_expr(op->imm.u, op->arg[2], a, b, x, sizeof x);
+        wsb_put(s, "    const float f%u_%u = %s;\n", i, v, x);
+        break;
+    default:
+        break;
+    }
+    (void)p;
+}
+
+static char *gen_run_sum(const UOpKernel *k, const WinPlan *p, const char *name) {
+    WSB s = {0};
+    const u32 W = p->W, L4 = p->L / W, units = p->trip / W;
+    const u32 chunk = (units + p->S - 1) / p->S;
+    wsb_put(&s, "%s\n", kgen_prelude());
+    wsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(char* p0", WIN_BLOCK, name);
+    for (u32 i = 0; i < k->n_leaves; i++) wsb_put(&s, ", const char* p%u", i + 1);
+    if (p->S > 1 && p->launch) wsb_put(&s, ", float* ws_) {\n");
+    else wsb_put(&s, ", unsigned long long* sl_) {\n");
+    wsb_put(&s, "  __shared__ float red_[%u];\n", WIN_BLOCK / 64);
+    wsb_put(&s, "  const u32 gid = blockIdx.x / %uu, sp_ = blockIdx.x %% %uu;\n", p->S, p->S);
+    wsb_put(&s, "  const u32 lane = threadIdx.x;\n");
+    for (u32 j = 0; j < p->n_ld; j++) {
+        char nm[16];
+        snprintf(nm, sizeof nm, "b%u_", p->ld_op[j]);
+        emit_base(&s, nm, &p->ld_aff[j]);
+        if (!p->ld_r[j])
+            wsb_put(&s, "  const float h%u_ = ((const float*)p%u)[b%u_];\n", p->ld_op[j],
+                    k->ops[p->ld_op[j]].imm.u, p->ld_op[j]);
+    }
+    for (u32 v = 0; v < W; v++) wsb_put(&s, "  float q%u_ = 0.0f;\n", v);
+    wsb_put(&s, "  const u32 ulo_ = sp_ * %uu, uhi_ = (ulo_ + %uu < %uu) ? ulo_ + %uu : %uu;\n", chunk, chunk, units,
+            chunk, units);
+    wsb_put(&s, "  #pragma unroll %u\n  for (u32 u_ = ulo_ + lane; u_ < uhi_; u_ += %uu) {\n", p->unroll, WIN_BLOCK);
+    wsb_put(&s, "    const u32 s_ = u_ / %uu, j_ = u_ - s_ * %uu;\n", L4, L4);
+    wsb_put(&s, "    const u32 o_ = j_ * %uu", W);
+    for (u32 q = 0; q < p->n_outer; q++) {
+        if (p->outer_mod[q])
+            wsb_put(&s, " + %uu * ((s_ / %uu) %% %uu)", p->outer_coef[q], p->outer_div[q], p->outer_mod[q]);
+        else
+            wsb_put(&s, " + %uu * (s_ / %uu)", p->outer_coef[q], p->outer_div[q]);
+    }
+    wsb_put(&s, ";\n");
+    /* the body in op order, each op once per vector component */
+    for (u32 i = p->R + 1; i < p->acc; i++) {
+        if (!p->cone[i] || !op_type_is_float(k->ops[i].type)) continue;
+        if (k->ops[i].type == KOP_LOAD) {
+            u32 j = 0;
+            while (p->ld_op[j] != i) j++;
+            u32 bi = k->ops[i].imm.u;
+            if (!p->ld_r[j]) {
+                for (u32 v = 0; v < W; v++) wsb_put(&s, "    const float f%u_%u = h%u_;\n", i, v, i);
+            } else if (W == 4) {
+                wsb_put(&s, "    const float4 t%u_ = ld4nt_u(p%u, b%u_ + o_);\n", i, bi, i);
+                wsb_put(&s, "    const float f%u_0 = t%u_.x, f%u_1 = t%u_.y, f%u_2 = t%u_.z, f%u_3 = t%u_.w;\n", i, i,
+                        i, i, i, i, i, i);
+            } else {
+                wsb_put(&s, "    const float f%u_0 = ((const float*)p%u)[b%u_ + o_];\n", i, bi, i);
+            }
+            continue;
+        }
+        for (u32 v = 0; v < W; v++) emit_body_op(&s, k, p, i, v);
+    }
+    for (u32 v = 0; v < W; v++) wsb_put(&s, "    q%u_ = q%u_ + f%u_%u;\n", v, v, p->value, v);
+    wsb_put(&s, "  }\n");
+    if (W == 4) wsb_put(&s, "  float t_ = (q0_ + q1_) + (q2_ + q3_);\n");
+    else wsb_put(&s, "  float t_ = q0_;\n");
+    char fb[64];
+    float_bits(fb, sizeof fb, p->init_bits);
+    if (p->S > 1 && p->launch) {
+        /* partials to the workspace; <name>_fin: a workgroup per output, lane
+         * l adds partials l, l + 256, ... in order, then the fixed trees */
+        wsb_put(&s, "  t_ = bsum(t_, red_);\n  if (lane == 0u) ws_[(unsigned long long)gid * %uu + sp_] = t_;\n}\n", p->S);
+        wsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s_fin(char* p0, const float* ws_) {\n"
+                    "  __shared__ float red_[%u];\n"
+                    "  const u32 gid = blockIdx.x;\n"
+                    "  float w_ = 0.0f;\n"
+                    "  for (u32 s_ = threadIdx.x; s_ < %uu; s_ += %uu) w_ = w_ + ws_[(unsigned long long)gid * %uu + s_];\n"
+                    "  w_ = bsum(w_, red_);\n"
+                    "  if (threadIdx.x == 0u) ((float*)p0)[gid] = %s + w_;\n}\n",
+                WIN_BLOCK, name, WIN_BLOCK / 64, p->S, WIN_BLOCK, p->S, fb);
+    } else if (p->S > 1) {
+        wsb_put(&s, "  t_ = bsum(t_, red_);\n"
+                    "  if (sp_ != %uu) {\n"
+                    "    comb_put(sl_, gid, sp_, %uu, t_);\n"
+                    "  } else {\n"
+                    "    float w_ = 0.0f;\n"
+                    "    for (u32 s2_ = lane; s2_ < %uu; s2_ += %uu)\n"
+                    "      w_ = w_ + ((s2_ == %uu) ? t_ : comb_take(sl_, gid, s2_, %uu));\n"
+                    "    w_ = bsum(w_, red_);\n"
+                    "    if (lane == 0u) ((float*)p0)[gid] = %s + w_;\n"
+                    "  }\n}\n", p->S - 1, p->S, p->S, WIN_BLOCK, p->S - 1, p->S, fb);
+    } else {
+        wsb_put(&s, "  t_ = bsum(t_, red_);\n  if (lane == 0u) ((float*)p0)[gid] = %s + t_;\n}\n", fb);
+    }
+    return s.p;
+}
+
+static char *gen_window(const UOpKernel *k, const WinPlan *p, char *name, size_t namelen) {
+    snprintf(name, namelen, "thvm_%s_%08x", p->kind == WIN_MAX ? "wmax" : "rsum",
+             (u32)(uop_signature(k) & 0xFFFFFFFFu));
+    return p->kind == WIN_MAX ? gen_window_max(k, p, name) : gen_run_sum(k, p, name);
+}
+
+/* ---------------- cache and dispatch ---------------- */
+
+typedef struct {
+    u64 key;
+    u32 n_ops, n_leaves;
+    KOp *ops;
+    u32 meta[5];
+    u32 dts[FUSE_MAX_LEAVES];
+    int kind;                    /* WIN_NONE: a program this file does not take */
+    WinPlan plan;
+    hipModule_t mod;
+    hipFunction_t fn, fn_fin;
+} WinEntry;
+
+static Scratch win_ws;   /* run-sum partials of the combine-kernel form */
+
+static struct {
+    WinEntry *tab;
+    u32 cap, n;
+} WC;
+
+static int win_same(const WinEntry *e, const UOpKernel *k) {
+    if (e->n_ops != k->n_ops || e->n_leaves != k->n_leaves || !e->ops) return 0;
+    if (e->meta[0] != k->grid[0] || e->meta[1] != k->grid[1] || e->meta[2] != k->grid[2] ||
+        e->meta[3] != k->local_size || e->meta[4] != k->out_dtype)
+        return 0;
+    if (memcmp(e->dts, k->leaf_dtypes, (size_t)k->n_leaves * sizeof(u32)) != 0) return 0;
+    return memcmp(e->ops, k->ops, (size_t)k->n_ops * sizeof(KOp)) == 0;
+}
+
+static WinEntry *win_lookup(u64 key, const UOpKernel *k) {
+    if (!WC.tab) return NULL;
+    u32 m = WC.cap - 1;
+    for (u32 q = (u32)key & m, probes = 0; probes < WC.cap; q = (q + 1) & m, probes++) {
+        WinEntry *e = &WC.tab[q];
+        if (!e->key) return NULL;
+        if (e->key == key && win_same(e, k)) return e;
+    }
+    return NULL;
+}
+
+static WinEntry *win_insert(u64 key, const UOpKernel *k) {
+    if (!WC.tab || (WC.n + 1) * 2 > WC.cap) {
+        u32 nc = WC.cap ? WC.cap * 2 : 256;
+        WinEntry *nt = calloc(nc, sizeof(WinEntry));
+        if (!nt) return NULL;
+        for (u32 i = 0; i < WC.cap; i++) {
+            if (!WC.tab[i].key) continue;
+            u32 q = (u32)WC.tab[i].key & (nc - 1);
+            while (nt[q].key) q = (q + 1) & (nc - 1);
+            nt[q] = WC.tab[i];
+        }
+        free(WC.tab);
+        WC.tab = nt;
+        WC.cap = nc;
+    }
+    u32 m = WC.cap - 1, q = (u32)key & m;
+    while (WC.tab[q].key) q = (q + 1) & m;
+    WinEntry *e = &WC.tab[q];
+    memset(e, 0, sizeof *e);
+    e->key = key;
+    e->n_ops = k->n_ops;
+    e->n_leaves = k->n_leaves;
+    e->ops = malloc((size_t)k->n_ops * sizeof(KOp));
+    if (e->ops) memcpy(e->ops, k->ops, (size_t)k->n_ops * sizeof(KOp));
+    e->meta[0] = k->grid[0]; e->meta[1] = k->grid[1]; e->meta[2] = k->grid[2];
+    e->meta[3] = k->local_size; e->meta[4] = k->out_dtype;
+    memcpy(e->dts, k->leaf_dtypes, (size_t)k->n_leaves * sizeof(u32));
+    WC.n++;
+    return e;
+}
+
+static u64 win_key(const UOpKernel *k) {
+    u64 key = uop_signature(k) ^ 0x57494E444F57ull;
+    return key ? key : 1;
+}
+
+int window_analyze(const UOpKernel *k, u32 *kind, u32 *splits) {
+    WinPlan p;
+    if (!k || !win_recognize(k, &p)) {
+        if (kind) *kind = WIN_NONE;
+        if (splits) *splits = 0;
+        return 0;
+    }
+    if (kind) *kind = (u32)p.kind;
+    if (splits) *splits = p.kind == WIN_SUM ? p.S : 1;
+    return 1;
+}
+
+char *window_source(const UOpKernel *k) {
+    WinPlan p;
+    char name[48];
+    if (!k || !win_recognize(k, &p)) return NULL;
+    return gen_window(k, &p, name, sizeof name);
+}
+
+int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
+    if (k->n_leaves > FUSE_MAX_LEAVES) return 0;
+    u64 key = win_key(k);
+    WinEntry *e = win_lookup(key, k);
+    if (!e && hipb.noalloc) {
+        hipb.noalloc_err = THVM_HIP_ENOTREADY;   /* never compiles without allocating */
+        return 0;
+    }
+    if (!e) {
+        e = win_insert(key, k);
+        if (!e) return 0;
+        if (!win_recognize(k, &e->plan)) return 0;    /* kind stays WIN_NONE */
+        char name[48], err[256] = {0};
+        char *src = gen_window(k, &e->plan, name, sizeof name);
+        if (!src) return 0;
+        if (hipb.dump_src) fprintf(stderr, "---- window kernel ----\n%s\n", src);
+        if (!rtc_build_module(src, &e->mod, err, sizeof err)) {
+            fprintf(stderr, "tinyhvm-hip: window kernel build failed: %s\n", err);
+            free(src);
+            return 0;
+        }
+        free(src);
+        char fin[64];
+        snprintf(fin, sizeof fin, "%s_fin", name);
+        if (hipModuleGetFunction(&e->fn, e->mod, name) != hipSuccess ||
+            (e->plan.kind == WIN_SUM && e->plan.S > 1 && e->plan.launch &&
+             hipModuleGetFunction(&e->fn_fin, e->mod, fin) != hipSuccess)) {
+            HIPB_CHECK(hipModuleUnload(e->mod));
+            return 0;
+        }
+        e->kind = e->plan.kind;
+        if (hipb.verbose)
+            fprintf(stderr, "tinyhvm-hip: %s outputs=%u trip=%u W=%u run=%u splits=%u\n", name, e->plan.total,
+                    e->plan.trip, e->plan.W, e->plan.L, e->plan.S);
+    }
+    if (e->kind == WIN_NONE) return 0;
+    const WinPlan *p = &e->plan;
+    /* buffers: every index the plan forms is inside them, vector loads aligned */
+    void *ptrs[FUSE_MAX_LEAVES + 1];
+    HipbBuf *ob = pool_get(out_buf);
+    if (!ob || ob->bytes / 4 < p->total) return 0;
+    ptrs[0] = ob->ptr;
+    for (u32 i = 0; i < k->n_leaves; i++) {
+        void *lp = i < n_leaves ? pool_ptr(leaf_bufs[i]) : NULL;
+        ptrs[i + 1] = lp ? lp : hipb.dummy;
+    }
+    for (u32 j = 0; j < p->n_ld; j++) {
+        u32 bi = k->ops[p->ld_op[j]].imm.u;
+        if (bi > n_leaves || !pool_ptr(leaf_bufs[bi - 1])) return 0;
+        u64 top = p->kind == WIN_MAX ? p->cover_max : p->ld_max[j];
+        if (top >= pool_bytes(leaf_bufs[bi - 1]) / 4) return 0;
+        if (p->ld_r[j] && ((uintptr_t)ptrs[bi] & (4u * p->W - 1u))) return 0;
+    }
+    if (p->kind == WIN_MAX && p->P == 2 && ((uintptr_t)ptrs[0] & 7u)) return 0;
+    float *ws = NULL;
+    if (p->kind == WIN_SUM && p->S > 1 && p->launch) {
+        ws = scratch_reserve(&win_ws, (u64)p->total * p->S * sizeof(float));
+        if (!ws) return 0;
+    }
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
+    if (p->kind == WIN_MAX) {
+        u32 bi = k->ops[p->ld_op[0]].imm.u;
+        void *params[] = {&ptrs[0], &ptrs[bi]};
+        u64 lanes = ((u64)p->total / p->P + p->U - 1) / p->U;
+        u64 blocks = (lanes + WIN_BLOCK - 1) / WIN_BLOCK;
+        u32 gx = (u32)blocks, gy = 1;
+        if (blocks * WIN_BLOCK >= (1ull << 32)) {
+            gx = 65536;
+            gy = (u32)((blocks + 65535) / 65536);
+        }
+        if (!hipb_launch(e->fn, gx, gy, 1, WIN_BLOCK, params)) return 0;
+    } else {
+        void *params[FUSE_MAX_LEAVES + 3];
+        u32 np = 0;
+        for (u32 b = 0; b <= k->n_leaves; b++) params[np++] = &ptrs[b];
+        if (ws) {
+            params[np++] = &ws;
+        } else {
+            params[np++] = &hipb.comb_slots;
+        }
+        if (!hipb_launch(e->fn, p->total * p->S, 1, 1, WIN_BLOCK, params)) return 0;
+        if (ws) {
+            void *p2[] = {&ptrs[0], &ws};
+            if (!hipb_launch(e->fn_fin, p->total, 1, 1, WIN_BLOCK, p2)) return 0;
+        }
+    }
+    return 1;
+}
+
+void window_shutdown(void) {
+    if (WC.tab) {
+        for (u32 i = 0; i < WC.cap; i++) {
+            if (!WC.tab[i].key) continue;
+            if (WC.tab[i].kind != WIN_NONE) HIPB_CHECK(hipModuleUnload(WC.tab[i].mod));
+            free(WC.tab[i].ops);
+        }
+        free(WC.tab);
+    }
+    memset(&WC, 0, sizeof WC);
+    scratch_release(&win_ws);
+}
