@@ -95,7 +95,12 @@ static void rb_reduce(const ReduceSpec *r) {
     for (u32 d = 0; d < MAX_DIM; d++) rb_u32(r->is_reduce2[d]);
 }
 
+/* Called with each mark's text before it is recorded (a timing driver sets
+ * it to time the steps between marks). */
+static void (*g_mark_hook)(const char *text);
+
 static void rec_mark(const char *text) {
+    if (g_mark_hook) g_mark_hook(text);
     rb_begin();
     u32 n = (u32)strlen(text);
     rb_u32(n);
@@ -751,8 +756,13 @@ static void sgd(TinyHVM *ctx, Term *params, Term *grads, u32 n, f32 lr) {
 }
 
 /* 2-layer MLP: x [B,784] ~ N(0,1), W1 [784,H], W2 [H,10] Kaiming-uniform, b = 0,
- * relu, softmax cross-entropy (src/nn/loss.c:8-44); outputs loss, dW1, dW2. */
-static void wl_mlp(TinyHVM *ctx, u32 B, u32 IN, u32 H, u32 C) {
+ * relu, softmax cross-entropy (src/nn/loss.c:8-44); outputs loss, dW1, dW2.
+ * With steps > 1 the forward and backward repeat from the same inputs, each
+ * step opened by an "mlp.step" mark and closed by a reset of the step's
+ * tensors (one step records exactly as before). */
+static void wl_mlp_steps(TinyHVM *ctx, u32 B, u32 IN, u32 H, u32 C, int steps);
+static void wl_mlp(TinyHVM *ctx, u32 B, u32 IN, u32 H, u32 C) { wl_mlp_steps(ctx, B, IN, H, C, 1); }
+static void wl_mlp_steps(TinyHVM *ctx, u32 B, u32 IN, u32 H, u32 C, int steps) {
     Term x = gen_tensor(ctx, SHAPE(B, IN), DTYPE_F32, TRC_GEN_NORMAL, 1001, 0.f, 1.f);
     Term W1 = kaiming_u(ctx, SHAPE(IN, H), IN, 1002);
     Term b1 = zeros(ctx, SHAPE(H), 1003);
@@ -760,19 +770,24 @@ static void wl_mlp(TinyHVM *ctx, u32 B, u32 IN, u32 H, u32 C) {
     Term b2 = zeros(ctx, SHAPE(C), 1005);
     u8 *lab = labels_u8(B, 1006);
     Term onehot = onehot_tensor(ctx, lab, B, C);
-    rec_mark("mlp.fwd");
-    Term h = dense(ctx, x, W1, b1, 1, B, H);
-    Term logits = dense(ctx, h, W2, b2, 0, B, C);
-    Term loss = realize(ctx, cross_entropy_loss(ctx, logits, lab, B, C));
-    readback(ctx, loss);
-    rec_mark("mlp.bwd");
-    Term d2 = ce_grad(ctx, logits, onehot, B, C);
-    DenseGrads g2 = dense_bwd(ctx, h, W2, d2, B, H, C, 1);
-    Term dz1 = realize_as(ctx, binary(ctx, UOP_MUL, g2.dx, binary(ctx, UOP_CMP, h, scalar_t(ctx, 0.0f))),
-                          SHAPE(B, H));
-    DenseGrads g1 = dense_bwd(ctx, x, W1, dz1, B, IN, H, 0);
-    readback(ctx, g1.dW);
-    readback(ctx, g2.dW);
+    u32 keep = ctx->tensor_count;
+    for (int st = 0; st < steps; st++) {
+        if (steps > 1) rec_mark("mlp.step");
+        rec_mark("mlp.fwd");
+        Term h = dense(ctx, x, W1, b1, 1, B, H);
+        Term logits = dense(ctx, h, W2, b2, 0, B, C);
+        Term loss = realize(ctx, cross_entropy_loss(ctx, logits, lab, B, C));
+        readback(ctx, loss);
+        rec_mark("mlp.bwd");
+        Term d2 = ce_grad(ctx, logits, onehot, B, C);
+        DenseGrads g2 = dense_bwd(ctx, h, W2, d2, B, H, C, 1);
+        Term dz1 = realize_as(ctx, binary(ctx, UOP_MUL, g2.dx, binary(ctx, UOP_CMP, h, scalar_t(ctx, 0.0f))),
+                              SHAPE(B, H));
+        DenseGrads g1 = dense_bwd(ctx, x, W1, dz1, B, IN, H, 0);
+        readback(ctx, g1.dW);
+        readback(ctx, g2.dW);
+        if (steps > 1) thvm_reset(ctx, keep);
+    }
     free(lab);
 }
 

@@ -19,6 +19,18 @@
  * runs and compared: same sequence and sizes, values within 1e-3 normwise
  * (max |gpu - cpu| / max |cpu| per read, as float32), NaNs in the same places.
  * Prints one JSON line and exits 0 when every read agrees.
+ *
+ * Timing mode: engine_live <libthvm_hip.so> time <lenet|mlp> <steps> [sizes...]
+ * runs the workload's training steps through thvm_eval with hip_backend as
+ * the default device: two steps to warm up (kernel compilation), then
+ * <steps> timed steps, each from its "<workload>.step" mark to the next (the
+ * engine's own host work, the dispatches, and the step's read-backs of its
+ * loss and parameters or gradients). Every backend slot is wrapped to count
+ * the host's waits on the stream inside it (thvm_hip_counters): a wait may
+ * happen only inside buf_read, the engine's sync point; any other slot that
+ * waits is reported. The same steps then run on the engine's CPU backend
+ * (one step, nothing to warm up; under capture.c's recorder, as in run 0).
+ * Prints one JSON line.
  */
 #define CAPTURE_NO_MAIN
 #include "../golden/capture.c"
@@ -64,7 +76,150 @@ static int run_workload(TinyHVM *ctx, const char *wl, const u32 *sz, u32 nsz) {
     return 1;
 }
 
+/* ---- timing mode ---- */
+#define TM_MAX_STEPS 1024
+static int (*g_counters)(u64 *, u32);
+static const char *g_step_mark;
+static u32 g_nsteps;
+static double g_step_t[TM_MAX_STEPS + 1];
+static u64 g_step_waits[TM_MAX_STEPS + 1], g_step_reads[TM_MAX_STEPS + 1], g_step_disp[TM_MAX_STEPS + 1];
+static u64 g_reads_total, g_disp_total, g_waits_outside;
+static char g_waits_outside_slot[64];
+static Backend g_tm_inner;
+
+static u64 host_waits(void) {
+    u64 c[11] = {0};
+    if (g_counters) g_counters(c, 11);
+    return c[5];
+}
+
+static void tm_mark(const char *text) {
+    if (!g_step_mark || strcmp(text, g_step_mark) != 0 || g_nsteps >= TM_MAX_STEPS) return;
+    g_step_t[g_nsteps] = now_s();
+    g_step_waits[g_nsteps] = host_waits();
+    g_step_reads[g_nsteps] = g_reads_total;
+    g_step_disp[g_nsteps] = g_disp_total;
+    g_nsteps++;
+}
+
+static void tm_outside(const char *slot, u64 w0) {
+    if (host_waits() != w0) {
+        g_waits_outside++;
+        snprintf(g_waits_outside_slot, sizeof g_waits_outside_slot, "%s", slot);
+    }
+}
+#define TM_WRAP(slot, ...) do { u64 w0_ = host_waits(); g_tm_inner.slot(__VA_ARGS__); tm_outside(#slot, w0_); } while (0)
+static u32 tm_alloc(u64 b) { u64 w0 = host_waits(); u32 id = g_tm_inner.buf_alloc(b); tm_outside("buf_alloc", w0); return id; }
+static void tm_free(u32 id) { TM_WRAP(buf_free, id); }
+static void tm_incref(u32 id) { TM_WRAP(buf_incref, id); }
+static void tm_decref(u32 id) { TM_WRAP(buf_decref, id); }
+static void tm_write(u32 id, const void *d, u64 b) { TM_WRAP(buf_write, id, d, b); }
+static void tm_read(u32 id, void *o, u64 b) { g_reads_total++; g_tm_inner.buf_read(id, o, b); }
+static void tm_read_nosync(u32 id, void *o, u64 b) { g_reads_total++; g_tm_inner.buf_read_nosync(id, o, b); }
+static void tm_uop(u32 out, const u32 *l, u32 n, const UOpKernel *k, u64 key) {
+    g_disp_total++;
+    TM_WRAP(dispatch_uop_kernel, out, l, n, k, key);
+}
+static void tm_rs(u32 out, u32 *l, const View **v, const ShapeTracker *const *st, u32 n, FusedOp *ops, u32 nops,
+                  const Shape *full, const ReduceSpec *red, u32 *sb, const u32 *si, u32 ns, const u32 *dts, u32 odt) {
+    g_disp_total++;
+    TM_WRAP(dispatch_kernel_rs, out, l, v, st, n, ops, nops, full, red, sb, si, ns, dts, odt);
+}
+static void tm_copy(u32 d, u32 s_, u64 b) { TM_WRAP(buf_copy, d, s_, b); }
+static void tm_contig(u32 d, u32 n, u32 s_, const View *v) { TM_WRAP(contiguify, d, n, s_, v); }
+static void tm_reset(u32 keep) { TM_WRAP(pool_reset, keep); }
+static void tm_persist(u32 m) { TM_WRAP(pool_set_persistent, m); }
+
+static void tm_run(TinyHVM *ctx, const char *wl, u32 B, int steps) {
+    if (strcmp(wl, "lenet") == 0) wl_lenet(ctx, B, steps);
+    else wl_mlp_steps(ctx, B, 784, 128, 10, steps);
+}
+
+/* one timed run: returns the median step in seconds (0 when no step closed) */
+static double tm_steps(TinyHVM *ctx, const char *wl, u32 B, int steps, double *mean, double *waits, double *reads,
+                       double *disp) {
+    g_nsteps = 0;
+    tm_run(ctx, wl, B, steps);
+    if (g_nsteps >= TM_MAX_STEPS) return 0.0;
+    g_step_t[g_nsteps] = now_s();   /* the last step ends when the workload returns */
+    g_step_waits[g_nsteps] = host_waits();
+    g_step_reads[g_nsteps] = g_reads_total;
+    g_step_disp[g_nsteps] = g_disp_total;
+    u32 n = g_nsteps;
+    if (n == 0) return 0.0;
+    double d[TM_MAX_STEPS], sum = 0.0;
+    for (u32 i = 0; i < n; i++) {
+        d[i] = g_step_t[i + 1] - g_step_t[i];
+        sum += d[i];
+    }
+    for (u32 i = 1; i < n; i++)
+        for (u32 j = i; j > 0 && d[j - 1] > d[j]; j--) { double t = d[j]; d[j] = d[j - 1]; d[j - 1] = t; }
+    *mean = sum / n;
+    *waits = (double)(g_step_waits[n] - g_step_waits[0]) / n;
+    *reads = (double)(g_step_reads[n] - g_step_reads[0]) / n;
+    *disp = (double)(g_step_disp[n] - g_step_disp[0]) / n;
+    return d[n / 2];
+}
+
+static int time_mode(const char *lib, const char *wl, int steps, const u32 *sz, u32 nsz) {
+    if (strcmp(wl, "lenet") != 0 && strcmp(wl, "mlp") != 0) return 2;
+    u32 B = nsz > 0 ? sz[0] : (strcmp(wl, "lenet") == 0 ? 256 : 64);
+    if (steps < 1 || steps > TM_MAX_STEPS - 2) return 2;
+    g_step_mark = strcmp(wl, "lenet") == 0 ? "lenet.step" : "mlp.step";
+    g_out = fopen("/dev/null", "wb");
+    if (!g_out) return 1;
+    g_mark_hook = tm_mark;
+    void *h = dlopen(lib, RTLD_NOW | RTLD_LOCAL);
+    if (!h) {
+        fprintf(stderr, "engine_live: %s\n", dlerror());
+        return 1;
+    }
+    Backend *hb = (Backend *)dlsym(h, "hip_backend");
+    g_counters = (int (*)(u64 *, u32))dlsym(h, "thvm_hip_counters");
+    if (!hb || !g_counters || !hb->init || hb->init() != 0) {
+        fprintf(stderr, "engine_live: hip_backend unavailable\n");
+        return 1;
+    }
+    g_tm_inner = *hb;
+    static Backend tm;
+    tm = *hb;
+    tm.buf_alloc = tm_alloc; tm.buf_free = tm_free; tm.buf_incref = tm_incref; tm.buf_decref = tm_decref;
+    tm.buf_write = tm_write; tm.buf_read = tm_read; tm.buf_read_nosync = tm_read_nosync;
+    tm.dispatch_uop_kernel = tm_uop; tm.dispatch_kernel_rs = tm_rs; tm.buf_copy = tm_copy;
+    tm.contiguify = tm_contig; tm.pool_reset = tm_reset; tm.pool_set_persistent = tm_persist;
+    TinyHVM *ctx = thvm_init("cpu");
+    ctx->backends[2] = &tm;
+    if (ctx->n_backends < 3) ctx->n_backends = 3;
+    ctx->default_device = 2;
+    double mean = 0, waits = 0, reads = 0, disp = 0;
+    tm_steps(ctx, wl, B, 2, &mean, &waits, &reads, &disp);          /* warm-up: compiles every kernel */
+    g_waits_outside = 0;
+    g_waits_outside_slot[0] = 0;
+    double med = tm_steps(ctx, wl, B, steps, &mean, &waits, &reads, &disp);
+    hb->shutdown();
+    /* the engine's CPU backend, the same steps (no compilation to warm up),
+     * under the recorder so kernels whose masked loads leave their buffer run
+     * over zero-guarded leaves (the interpreter faults otherwise) */
+    install_recorder();
+    TinyHVM *cpu = thvm_init("cpu");
+    double cmean = 0, cw = 0, cr = 0, cd = 0;
+    double cmed = tm_steps(cpu, wl, B, 1, &cmean, &cw, &cr, &cd);
+    printf("{\"workload\": \"%s\", \"batch\": %u, \"steps\": %d, \"gpu\": {\"median_ms\": %.4f, "
+           "\"mean_ms\": %.4f, \"steps_per_s\": %.2f, \"host_waits_per_step\": %.2f, \"reads_per_step\": %.2f, "
+           "\"dispatches_per_step\": %.2f, \"waits_outside_reads\": %llu, \"wait_slot\": \"%s\"}, "
+           "\"cpu\": {\"seconds_per_step\": %.4f, \"steps_per_s\": %.5f}}\n",
+           wl, B, steps, med * 1e3, mean * 1e3, med > 0 ? 1.0 / med : 0.0, waits, reads, disp,
+           (unsigned long long)g_waits_outside, g_waits_outside_slot, cmed, cmed > 0 ? 1.0 / cmed : 0.0);
+    fflush(stdout);
+    return med > 0 ? 0 : 1;
+}
+
 int main(int argc, char **argv) {
+    if (argc >= 5 && strcmp(argv[2], "time") == 0) {
+        u32 tsz[8] = {0}, tn = 0;
+        for (int i = 5; i < argc && tn < 8; i++) tsz[tn++] = (u32)strtoul(argv[i], NULL, 10);
+        return time_mode(argv[1], argv[3], atoi(argv[4]), tsz, tn);
+    }
     if (argc < 3) {
         fprintf(stderr, "usage: engine_live <libthvm_hip.so> <workload> [sizes...]\n");
         return 2;
