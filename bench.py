@@ -28,13 +28,20 @@ average duration, from HIP events on the backend's stream around that one
 dispatch; `traffic` comes from the committed rocprofv3 counter summary.
 cpu_baseline: the engine's own CPU backend (oracle/_ref/ref_replay, built from
 the engine sources) on one host core, on the same trace or a stated slice;
-for LeNet the engine's interpreter faults on the padded convolution, so the
-oracle (oracle/ora_replay, the CPU restatement) is timed instead.
+LeNet and the conv block replay with every buffer in a zero-filled guard
+region, since the engine's interpreter loads masked pad elements before the
+mask discards them.
+
+lenet_engine, mlp_engine: the same training steps driven by the engine itself
+(thvm_eval with hip_backend as its default device; oracle/_ref/engine_live in
+a child process): the rate a user of the engine gets, host work included,
+with the host's stream waits per step counted beside the step's read-backs.
 """
 import argparse
 import ctypes as C
 import json
 import os
+import platform
 import shutil
 import subprocess
 import sys
@@ -94,13 +101,12 @@ WORKLOADS = {
                                "conv5x5 -> 16, relu, maxpool2, fc 400-120-84-10, softmax CE, "
                                "backward, SGD via ASSIGN)", "batch": 256,
                    "input": "U(0,1) [256,1,28,28]", "kernels_per_step": 54},
-        "cpu": {"exe": "oracle/ora_replay", "kind": "port",
-                "trace": os.path.join(WL, "lenet_b64.trc"), "marks": ("lenet.step", "lenet.end"),
-                "batch_scale": 256 / 64, "reps": 2,
-                "sample": "training steps at batch 64 (the same kernels at 1/4 the batch), 2 replays, "
-                          "time scaled by 4; the engine's own CPU interpreter faults on the "
-                          "padded convolution, so the oracle's restatement of it is timed "
-                          "(1.4x slower than the engine's interpreter on the fused step)"},
+        "cpu": {"exe": "oracle/_ref/ref_replay", "kind": "reference", "args": ["--guard"],
+                "trace": os.path.join(WL, "lenet_b256.trc"), "marks": ("lenet.step", "lenet.end"),
+                "reps": 1,
+                "sample": "one training step at batch 256 on the engine's CPU backend, its buffers "
+                          "placed in zero-filled guard regions (its interpreter loads masked pad "
+                          "elements before discarding them)"},
     },
     "mlp": {
         "trace": os.path.join(WL, "mlp_64x784x128x10.trc"),
@@ -123,12 +129,13 @@ WORKLOADS = {
                                "eps 1e-5), relu, maxpool 2, sum loss; backward dW and dX",
                    "batch": 64, "input": "N(0,1) [64,64,56,56]", "kernels_per_step": 28},
         "profile": "convblock_b64.md",
-        "cpu": {"exe": "oracle/ora_replay", "kind": "port",
+        "cpu": {"exe": "oracle/_ref/ref_replay", "kind": "reference", "args": ["--guard"],
                 "trace": os.path.join(WL, "convblock_b1.trc"), "marks": ("conv.fwd", "-"),
                 "flops": 3 * FCONV // 64,
                 "sample": "the full step at batch 1 (the same 28 kernels; the convolutions' "
-                          "FLOPs are linear in the batch); the engine's own interpreter faults "
-                          "on the zero-pad kernel, so the oracle's restatement of it is timed"},
+                          "FLOPs are linear in the batch) on the engine's CPU backend, its "
+                          "buffers placed in zero-filled guard regions (its interpreter loads "
+                          "masked pad elements before discarding them)"},
     },
 }
 
@@ -174,12 +181,31 @@ def measured_traffic(profile, kernel):
     return json.loads(block).get("traffic_bytes", {}).get(kernel)
 
 
+def host_info():
+    """The host the CPU baselines ran on: CPU model, cores visible, glibc."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        nproc = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        nproc = os.cpu_count()
+    return {"cpu": model, "nproc": nproc, "cpu_count": os.cpu_count(),
+            "glibc": "-".join(platform.libc_ver())}
+
+
 def cpu_baseline(spec, wl):
     exe = os.path.join(ROOT, spec["exe"])
     if not os.path.exists(exe):
         print("cpu baseline: %s is not built" % spec["exe"], file=sys.stderr)
         return None
-    cmd = [exe, spec["trace"], spec["marks"][0], spec["marks"][1], str(spec.get("reps", 1))]
+    cmd = [exe, spec["trace"], spec["marks"][0], spec["marks"][1], str(spec.get("reps", 1))] + spec.get("args", [])
     if shutil.which("taskset"):
         cmd = ["taskset", "-c", "0"] + cmd
     print("cpu baseline: %s" % " ".join(cmd), file=sys.stderr, flush=True)
@@ -189,7 +215,7 @@ def cpu_baseline(spec, wl):
         return None
     sec = json.loads(r.stdout.strip().splitlines()[-1])["per_rep"]
     out = {"unit": wl["unit"], "cores": 1, "kind": spec["kind"], "sample": spec["sample"],
-           "seconds": round(sec, 3)}
+           "seconds": round(sec, 3), "host": host_info()}
     if wl["unit"] == "GB/s":
         out["value"] = round(sum(b for _n, b in wl["kernels"].values()) / sec / 1e9, 4)
     elif wl["unit"] == "TFLOP/s":
@@ -309,6 +335,49 @@ def run_workload(L, name, steps, warmup, want_cpu):
     return res
 
 
+ENGINE_STEPS = {
+    "lenet_engine": ("lenet", 20, 256, "LeNet-5 training step at batch 256 through the engine"),
+    "mlp_engine": ("mlp", 50, 64, "2-layer MLP forward + backward at batch 64 through the engine"),
+}
+
+
+def engine_step(name, want_cpu):
+    """The workload's training step driven by the engine itself (thvm_eval with
+    hip_backend as the default device: scheduling, lowering, dispatch and the
+    step's read-backs, timed on the host clock), via oracle/_ref/engine_live in
+    a child process. Its CPU leg runs the same steps on the engine's CPU backend."""
+    exe = os.path.join(ROOT, "oracle", "_ref", "engine_live")
+    if not os.path.exists(exe):
+        print("engine step: oracle/_ref/engine_live is not built", file=sys.stderr)
+        return None
+    wl, steps, batch, what = ENGINE_STEPS[name]
+    cmd = [exe, os.path.join(ROOT, "tinyhvm_amd", "libthvm_hip.so"), "time", wl, str(steps), str(batch)]
+    print("engine step: %s" % " ".join(cmd), file=sys.stderr, flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+    if r.returncode != 0 or not lines:
+        sys.stderr.write(r.stderr[-2000:])
+        return None
+    e = json.loads(lines[-1])
+    g = e["gpu"]
+    res = {"value": g["steps_per_s"], "unit": "steps/s", "ms_per_step": g["median_ms"],
+           "mean_ms_per_step": g["mean_ms"],
+           "config": {"workload": what + " (thvm_eval -> hip_backend; host work, dispatches and "
+                                         "read-backs on the host clock, median of %d steps)" % steps,
+                      "batch": batch},
+           "dispatches_per_step": g["dispatches_per_step"], "reads_per_step": g["reads_per_step"],
+           "host_waits_per_step": g["host_waits_per_step"], "waits_outside_reads": g["waits_outside_reads"]}
+    if want_cpu and e["cpu"]["steps_per_s"] > 0:
+        res["cpu_baseline"] = {"value": e["cpu"]["steps_per_s"], "unit": "steps/s", "cores": 1,
+                               "kind": "reference", "seconds": e["cpu"]["seconds_per_step"],
+                               "sample": "the same step through thvm_eval on the engine's CPU "
+                                         "backend (%s)" % ("one step" if wl == "lenet" else
+                                                           "median of three steps"),
+                               "host": host_info()}
+    print("%s: %s" % (name, json.dumps(res)), file=sys.stderr, flush=True)
+    return res
+
+
 def copy_calibration(nbytes=256 << 20, reps=5):
     """A plain copy kernel of known size through the same generated-kernel
     path (out[i] = src[i]): the reference reading for the HBM byte counters."""
@@ -348,7 +417,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workloads", default="fused,matmul,lenet,convblock,mlp",
+    ap.add_argument("--workloads", default="fused,matmul,lenet,convblock,mlp,lenet_engine,mlp_engine",
                     help="comma list; the first one gives the headline value")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -363,13 +432,19 @@ def main():
         sys.exit(2)
     names = [w for w in args.workloads.split(",") if w]
     for nm in names:
-        if nm not in WORKLOADS:
-            raise SystemExit("unknown workload %r (have %s)" % (nm, ", ".join(WORKLOADS)))
+        if nm not in WORKLOADS and nm not in ENGINE_STEPS:
+            raise SystemExit("unknown workload %r (have %s)" % (nm, ", ".join(list(WORKLOADS) + list(ENGINE_STEPS))))
+    if names[0] not in WORKLOADS:
+        raise SystemExit("the first workload gives the headline value: one of %s" % ", ".join(WORKLOADS))
     L = _lib.lib()
     if L.thvm_hip_init() != 0:
         raise SystemExit("HIP backend failed to initialise")
-    results = {nm: run_workload(L, nm, args.steps, args.warmup, not args.no_cpu) for nm in names}
+    results = {nm: run_workload(L, nm, args.steps, args.warmup, not args.no_cpu) for nm in names
+               if nm in WORKLOADS}
     L.thvm_hip_shutdown()
+    for nm in names:
+        if nm in ENGINE_STEPS:
+            results[nm] = engine_step(nm, not args.no_cpu)
     head = results[names[0]]
     out = {
         "metric": METRIC,

@@ -20,7 +20,7 @@
  * (max |gpu - cpu| / max |cpu| per read, as float32), NaNs in the same places.
  * Prints one JSON line and exits 0 when every read agrees.
  *
- * Timing mode: engine_live <libthvm_hip.so> time <lenet|mlp> <steps> [sizes...]
+ * Timing mode: engine_live <libthvm_hip.so | -> time <lenet|mlp> <steps> [sizes...]
  * runs the workload's training steps through thvm_eval with hip_backend as
  * the default device: two steps to warm up (kernel compilation), then
  * <steps> timed steps, each from its "<workload>.step" mark to the next (the
@@ -29,8 +29,10 @@
  * the host's waits on the stream inside it (thvm_hip_counters): a wait may
  * happen only inside buf_read, the engine's sync point; any other slot that
  * waits is reported. The same steps then run on the engine's CPU backend
- * (one step, nothing to warm up; under capture.c's recorder, as in run 0).
- * Prints one JSON line.
+ * (one LeNet step or three MLP steps, nothing to warm up), each buffer in a
+ * zero-filled guard region (tm_guard_alloc) so that its interpreter runs the
+ * zero-padded convolutions itself. Prints one JSON line. With "-" for the
+ * library only the CPU leg runs (its GPU fields read 0).
  */
 #define CAPTURE_NO_MAIN
 #include "../golden/capture.c"
@@ -130,6 +132,38 @@ static void tm_contig(u32 d, u32 n, u32 s_, const View *v) { TM_WRAP(contiguify,
 static void tm_reset(u32 keep) { TM_WRAP(pool_reset, keep); }
 static void tm_persist(u32 m) { TM_WRAP(pool_set_persistent, m); }
 
+/* The CPU leg's buffers: each at the start of its own zero-filled, lazily
+ * mapped region spanning every u32 element index of a 4-byte type (GUARD_SPAN),
+ * placed at allocation. The engine's interpreter loads a leaf element before
+ * the mask that discards it (src/backend/cpu/uop.c:55-72); over these regions
+ * the stray loads of a zero-padded view read zeros, and the engine's CPU
+ * backend runs every kernel itself with nothing added per dispatch. */
+static u32 (*g_cpu_alloc)(u64);
+static u32 tm_guard_alloc(u64 b) {
+    u32 id = g_cpu_alloc(b);
+    void *m = mmap(NULL, GUARD_SPAN, PROT_READ | PROT_WRITE, MAP_PRIVATE | MAP_ANONYMOUS | MAP_NORESERVE, -1, 0);
+    if (m == MAP_FAILED) {
+        fprintf(stderr, "engine_live: guard mapping failed for buffer %u\n", id);
+        exit(1);
+    }
+    free(cpu_pool.bufs[id]);
+    cpu_pool.bufs[id] = m;
+    return id;
+}
+static void tm_guard_release(u32 id) {
+    if (id < MAX_BUFS && cpu_pool.bufs[id]) munmap(cpu_pool.bufs[id], GUARD_SPAN);
+    if (id < MAX_BUFS) cpu_pool.bufs[id] = NULL;
+}
+static void tm_guard_free(u32 id) { tm_guard_release(id); }
+static void tm_guard_reset(u32 keep) {
+    for (u32 i = keep + 1; i < cpu_pool.count; i++) tm_guard_release(i);
+    cpu_pool.count = keep + 1;
+}
+static void tm_guard_shutdown(void) {
+    for (u32 i = 1; i < cpu_pool.count; i++) tm_guard_release(i);
+    memset(&cpu_pool, 0, sizeof cpu_pool);
+}
+
 static void tm_run(TinyHVM *ctx, const char *wl, u32 B, int steps) {
     if (strcmp(wl, "lenet") == 0) wl_lenet(ctx, B, steps);
     else wl_mlp_steps(ctx, B, 784, 128, 10, steps);
@@ -161,24 +195,20 @@ static double tm_steps(TinyHVM *ctx, const char *wl, u32 B, int steps, double *m
     return d[n / 2];
 }
 
-static int time_mode(const char *lib, const char *wl, int steps, const u32 *sz, u32 nsz) {
-    if (strcmp(wl, "lenet") != 0 && strcmp(wl, "mlp") != 0) return 2;
-    u32 B = nsz > 0 ? sz[0] : (strcmp(wl, "lenet") == 0 ? 256 : 64);
-    if (steps < 1 || steps > TM_MAX_STEPS - 2) return 2;
-    g_step_mark = strcmp(wl, "lenet") == 0 ? "lenet.step" : "mlp.step";
-    g_out = fopen("/dev/null", "wb");
-    if (!g_out) return 1;
-    g_mark_hook = tm_mark;
+/* the hip_backend leg: returns the median step in seconds, -1 when the
+ * backend cannot be loaded or initialised */
+static double tm_hip_leg(const char *lib, const char *wl, u32 B, int steps, double *mean, double *waits,
+                         double *reads, double *disp) {
     void *h = dlopen(lib, RTLD_NOW | RTLD_LOCAL);
     if (!h) {
         fprintf(stderr, "engine_live: %s\n", dlerror());
-        return 1;
+        return -1;
     }
     Backend *hb = (Backend *)dlsym(h, "hip_backend");
     g_counters = (int (*)(u64 *, u32))dlsym(h, "thvm_hip_counters");
     if (!hb || !g_counters || !hb->init || hb->init() != 0) {
         fprintf(stderr, "engine_live: hip_backend unavailable\n");
-        return 1;
+        return -1;
     }
     g_tm_inner = *hb;
     static Backend tm;
@@ -191,19 +221,40 @@ static int time_mode(const char *lib, const char *wl, int steps, const u32 *sz, 
     ctx->backends[2] = &tm;
     if (ctx->n_backends < 3) ctx->n_backends = 3;
     ctx->default_device = 2;
-    double mean = 0, waits = 0, reads = 0, disp = 0;
-    tm_steps(ctx, wl, B, 2, &mean, &waits, &reads, &disp);          /* warm-up: compiles every kernel */
+    tm_steps(ctx, wl, B, 2, mean, waits, reads, disp);          /* warm-up: compiles every kernel */
     g_waits_outside = 0;
     g_waits_outside_slot[0] = 0;
-    double med = tm_steps(ctx, wl, B, steps, &mean, &waits, &reads, &disp);
+    double med = tm_steps(ctx, wl, B, steps, mean, waits, reads, disp);
     hb->shutdown();
+    return med;
+}
+
+static int time_mode(const char *lib, const char *wl, int steps, const u32 *sz, u32 nsz) {
+    if (strcmp(wl, "lenet") != 0 && strcmp(wl, "mlp") != 0) return 2;
+    u32 B = nsz > 0 ? sz[0] : (strcmp(wl, "lenet") == 0 ? 256 : 64);
+    if (steps < 1 || steps > TM_MAX_STEPS - 2) return 2;
+    g_step_mark = strcmp(wl, "lenet") == 0 ? "lenet.step" : "mlp.step";
+    g_out = fopen("/dev/null", "wb");
+    if (!g_out) return 1;
+    g_mark_hook = tm_mark;
+    double mean = 0, waits = 0, reads = 0, disp = 0, med = 0;
+    int cpu_only = strcmp(lib, "-") == 0;   /* "-": the CPU leg alone */
+    if (!cpu_only) {
+        med = tm_hip_leg(lib, wl, B, steps, &mean, &waits, &reads, &disp);
+        if (med < 0) return 1;
+    }
     /* the engine's CPU backend, the same steps (no compilation to warm up),
-     * under the recorder so kernels whose masked loads leave their buffer run
-     * over zero-guarded leaves (the interpreter faults otherwise) */
-    install_recorder();
+     * its buffers in guard regions */
+    g_cpu_alloc = cpu_backend.buf_alloc;
+    cpu_backend.buf_alloc = tm_guard_alloc;
+    cpu_backend.buf_free = tm_guard_free;
+    cpu_backend.pool_reset = tm_guard_reset;
+    cpu_backend.shutdown = tm_guard_shutdown;
     TinyHVM *cpu = thvm_init("cpu");
     double cmean = 0, cw = 0, cr = 0, cd = 0;
-    double cmed = tm_steps(cpu, wl, B, 1, &cmean, &cw, &cr, &cd);
+    /* the MLP marks its steps only when it runs more than one (its fixture
+     * recording is a single unmarked step), so its CPU sample is 3 steps */
+    double cmed = tm_steps(cpu, wl, B, strcmp(wl, "mlp") == 0 ? 3 : 1, &cmean, &cw, &cr, &cd);
     printf("{\"workload\": \"%s\", \"batch\": %u, \"steps\": %d, \"gpu\": {\"median_ms\": %.4f, "
            "\"mean_ms\": %.4f, \"steps_per_s\": %.2f, \"host_waits_per_step\": %.2f, \"reads_per_step\": %.2f, "
            "\"dispatches_per_step\": %.2f, \"waits_outside_reads\": %llu, \"wait_slot\": \"%s\"}, "
@@ -211,7 +262,7 @@ static int time_mode(const char *lib, const char *wl, int steps, const u32 *sz, 
            wl, B, steps, med * 1e3, mean * 1e3, med > 0 ? 1.0 / med : 0.0, waits, reads, disp,
            (unsigned long long)g_waits_outside, g_waits_outside_slot, cmed, cmed > 0 ? 1.0 / cmed : 0.0);
     fflush(stdout);
-    return med > 0 ? 0 : 1;
+    return (cpu_only || med > 0) && cmed > 0 ? 0 : 1;
 }
 
 int main(int argc, char **argv) {
