@@ -109,6 +109,61 @@ def test_graph_of_training_step_matches_eager(L):
         L.thvm_hip_pool_reset(0)
 
 
+CONV = os.path.join(ROOT, "tinyhvm_amd", "workloads", "convblock_b64.trc")
+
+
+def _out_bytes(L, t, tid, n):
+    buf = (C.c_uint8 * n)()
+    L.thvm_hip_buf_read(L.thvm_trace_live_id(t, tid), buf, n)
+    return bytes(buf)
+
+
+def test_graph_of_conv_block_matches_eager(L):
+    """The conv block step at batch 64 under graph launches (the matrix-core
+    convolutions with their packed weights and the weight gradient's split-K
+    workspace, the split reductions of batchnorm and the loss): three
+    launches, with eager steps between them, each leave the three
+    convolution outputs bit-identical to the eager step's (every sum has a
+    fixed order)."""
+    from tinyhvm_amd import trace
+    recs = trace.read_trace(CONV)
+    sizes = {r.f["id"]: r.f["bytes"] for r in recs if r.tag == trace.ALLOC}
+    be = L.thvm_hip_backend()
+    t = L.thvm_trace_load(CONV.encode())
+    assert t
+    g = None
+    try:
+        n = L.thvm_trace_count(t)
+        lo = L.thvm_trace_find_mark(t, b"conv.fwd", 0)
+        assert 0 <= lo < n
+        outs = [r.f["out"] for r in recs[lo:] if r.tag == trace.UOP]
+        watch = [outs[1], outs[23], outs[27]]          # conv forward, dW, dX
+        L.thvm_trace_replay(t, be, 0, lo, 0)
+        L.thvm_trace_replay(t, be, lo, n, SKIP_READS)      # compiles every kernel
+        assert L.thvm_hip_synchronize() == 0
+        eager = {tid: _out_bytes(L, t, tid, sizes[tid]) for tid in watch}
+        assert L.thvm_hip_graph_begin() == 0
+        L.thvm_trace_replay(t, be, lo, n, SKIP_READS)
+        g = L.thvm_hip_graph_end()
+        assert g, "the step could not be captured"
+        for rep in range(3):
+            assert L.thvm_hip_graph_launch(g) == 0
+            assert L.thvm_hip_synchronize() == 0
+            got = {tid: _out_bytes(L, t, tid, sizes[tid]) for tid in watch}
+            bad = [tid for tid in watch if got[tid] != eager[tid]]
+            assert not bad, "graph launch %d: outputs %s differ from the eager step" % (rep, bad)
+            L.thvm_trace_replay(t, be, lo, n, SKIP_READS)
+            assert L.thvm_hip_synchronize() == 0
+            again = {tid: _out_bytes(L, t, tid, sizes[tid]) for tid in watch}
+            assert again == eager, "eager step %d differs" % rep
+    finally:
+        if g:
+            L.thvm_hip_graph_destroy(g)
+        L.thvm_trace_release(t, be)
+        L.thvm_trace_free(t)
+        L.thvm_hip_pool_reset(0)
+
+
 def test_capture_with_a_host_read_is_refused(L):
     """A host read inside the captured calls cannot be repeated by a graph:
     the capture is abandoned, graph_end returns NULL, and the backend keeps

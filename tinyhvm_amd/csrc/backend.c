@@ -146,8 +146,10 @@ static int hb_init(void) {
             fprintf(stderr, "tinyhvm-hip: device is %s; kernels are built for gfx950\n", prop.gcnArchName);
             return -1;
         }
-        if (prop.multiProcessorCount > 0)
+        if (prop.multiProcessorCount > 0) {
             hipb.resident_waves = (u32)prop.multiProcessorCount * SINGLE_PASS_WAVES_PER_CU;
+            hipb.n_cu = (u32)prop.multiProcessorCount;
+        }
     }
     if (hipStreamCreateWithFlags(&hipb.stream, hipStreamNonBlocking) != hipSuccess) return -1;
     hipb.sync_each = env_flag("THVM_HIP_SYNC");

@@ -380,6 +380,12 @@ typedef struct {
 } GemmPlan;
 
 #define GEMM_THREADS 256
+/* Workgroups of the 64x64 tile a compute unit holds at once: four waves
+ * each, about 34 KB of LDS (two stages) and at most 128 VGPRs, so LDS and
+ * registers both stop at four. */
+#define GEMM_SLOTS_PER_CU 4u
+
+static u32 dense_cus(void) { return hipb.n_cu ? hipb.n_cu : 256u; }
 #define SUM_WAVE_MIN_SPLITS 16   /* split-K sums this long use a wavefront per output, */
 #define SUM_WAVE_MAX_OUTPUTS 8192 /* unless there are enough outputs for a lane each */
 
@@ -1276,6 +1282,14 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
     u64 target = lk ? 1024 : 512;    /* workgroups */
     u32 splits = 1;
     while ((u64)tiles * splits < target && ct->K / (splits * 2) >= min_chunk && splits < 1024) splits *= 2;
+    if (lk && tiles <= GEMM_SLOTS_PER_CU * dense_cus()) {
+        /* a long-K weight gradient fills the GPU's workgroup slots once: a
+         * second, mostly empty round of splits costs most of a split's time
+         * (576x64x200704 on 256 CUs: 9 tiles x 128 splits = 1152 workgroups
+         * on 1024 slots, 182 us; 9 x 112 = 1008, 160 us) */
+        splits = GEMM_SLOTS_PER_CU * dense_cus() / tiles;
+        if (splits > 1024) splits = 1024;
+    }
     if (hipb.dense_splits) splits = hipb.dense_splits;
     pl->splits_want = splits;
     snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));

@@ -65,6 +65,7 @@ typedef struct {
     hipModule_t static_mod;  /* precompiled kernels */
     unsigned long long *comb_slots; /* single-pass combines: partial words (cleared after each use) */
     u32 resident_waves;      /* waves the device holds at once for a single-pass grid */
+    u32 n_cu;                /* compute units (256 on MI355X; assumed where no device is open) */
     void *noalloc_scratch;   /* device address of the static workspace (noalloc.hip), or NULL */
     int noalloc;             /* a no-allocation dispatch is running: workspaces come from it */
     u64 noalloc_off;         /* bytes of the static workspace handed out in that dispatch */
