@@ -34,6 +34,8 @@ def _plans(name):
         src = _lib.dense_source(k)
         cst = re.search(r"constexpr u32 BM = (\d+), BN = (\d+), BK = (\d+)", src)
         nw = re.search(r"NW = (\d+)u", src)
+        kw = re.search(r"KW = (\d+)u, KCW", src)
+        ke = re.search(r"constexpr u32 E = (\d+)u, NBLK", src)
         out[a] = {
             "tile": (int(cst.group(1)), int(cst.group(2))) if cst else "direct",
             "kperm": "kbase_p(" in src,
@@ -43,6 +45,9 @@ def _plans(name):
             "vec16": "*(const float4*)(ps" in src,
             "two_stage": "ra1[" in src,
             "waves": int(nw.group(1)) if nw else 4,
+            "skinny": "KCW = " in src,
+            "skinny_waves": int(kw.group(1)) if kw else None,
+            "skinny_block": int(ke.group(1)) if ke else None,
         }
     return out
 
@@ -66,6 +71,17 @@ def test_gemm_4096_plans():
         assert a[:3] == (4096, 4096, 4096)
         assert v["tile"] == (128, 128) and v["kperm"] and v["vec16"]
         assert not v["transposed"] and not v["packed"] and not v["two_stage"]
+
+
+def test_lenet_few_channel_convolutions_are_skinny():
+    # conv1 forward (6 channels), conv2 forward (16) and conv2 dX (6): a row
+    # per lane with every column sum in registers; waves split K so that
+    # about 4096 waves run in all
+    # and K walks in blocks of the 5x5 window (25), whose offsets are constants
+    p = _plans("lenet_b256.trc")
+    for shape, waves in [((200704, 6, 25, 1), 1), ((25600, 16, 150, 1), 8), ((50176, 6, 400, 1), 4)]:
+        src = p[shape]
+        assert src["skinny"] and src["skinny_waves"] == waves and src["skinny_block"] == 25, (shape, src)
 
 
 def test_lenet_fc_weight_gradients_use_eight_waves():

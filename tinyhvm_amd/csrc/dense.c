@@ -315,7 +315,8 @@ typedef struct {
     u32 wm_b, wn_b;
     u32 gm, gn;
     const char *tag;
-    int direct;    /* no LDS: each wave owns one 32x32 block and loads its MFMA operands itself */
+    int direct;    /* no LDS: 1 = each wave owns one 32x32 block and loads its MFMA operands
+                      itself; 2 = skinny (see CFG_SKINNY) */
 } TileCfg;
 
 /* bk: K per LDS stage (32 halves the barriers per K of 16; measured 2-3%
@@ -335,6 +336,18 @@ static const TileCfg CFG_C64S = {128, 64, 32, 2, 1, 2, 2, "128x64"};
  * flight without barriers. Each wave computes one 32x32 block, loading 32 K
  * of both MFMA operands per iteration straight into registers. */
 static const TileCfg CFG_DIRECT = {32, 32, 32, 1, 1, 1, 1, "direct32", 1};
+/* Skinny contractions: at most 16 columns over many rows (the convolutions
+ * of a few channels: LeNet-5's 6 and 16). A 32-wide MFMA block would leave
+ * most of its columns empty; here each lane owns one row and keeps all N
+ * column sums in registers, reading its operand element once per k and the
+ * k-th row of the small side as wave-uniform (scalar) loads, with the
+ * workgroup's waves splitting K and adding their sums in wave order. VALU
+ * FMAs, no LDS tiles, no split-K workspace. */
+static const TileCfg CFG_SKINNY = {64, 16, 1, 1, 1, 1, 1, "skinny", 2};
+#define SKINNY_MAX_N 16
+#define SKINNY_MAX_KN 8192   /* the small side in LDS: at most 32 KB */
+#define SKINNY_MIN_M 4096
+#define SKINNY_TARGET_WAVES 4096
 
 /* K-reordered affine loading of separable operands. K is split into atomic
  * digits (the finest mixed radix both operands' k offsets decompose into);
@@ -377,6 +390,11 @@ typedef struct {
     int pack;              /* the B side is first copied into a K x N row-major buffer in the
                               reordered k order (a small operand with scattered loads) */
     KPerm kpo;             /* the K-reordered plan before packing (the pack kernel's loads) */
+    u32 ske;               /* skinny: K walked in blocks of ske (a digit boundary of both sides'
+                              k offsets), whose in-block offsets are constants; 0 = per k */
+    u64 skmax;             /* skinny: largest index the row side's loads form (unchecked loads
+                              when the buffer holds it), or ~0 */
+    u32 skbuf;             /* skinny: the buffer of the row side (1 + leaf) */
 } GemmPlan;
 
 #define GEMM_THREADS 256
@@ -505,6 +523,116 @@ static void emit_operand_expr(DSB *s, const UOpKernel *k, const Contraction *ct,
         emit_args(s, k->n_leaves);
         dsb_put(s, ")");
     }
+}
+
+/* Skinny kernel (CFG_SKINNY): lane = row m, all N column sums in registers.
+ * The small side (K x N, at most SKINNY_MAX_KN elements) is first copied by
+ * the workgroup into LDS as K rows of N, so that each k's row is a broadcast
+ * LDS read (scalar loads of it, one k at a time, each waited for, ran 5x
+ * slower). Wave w of the workgroup takes k in [w*KCW, (w+1)*KCW), its lanes
+ * loading SKU operand elements ahead of the FMAs of the previous SKU (one
+ * set of 8 loads waited for before its FMAs: 32 us on LeNet-5's conv2 dX,
+ * 50176x6x400); wave 0 then adds the other waves' sums in wave order
+ * (deterministic). */
+static void emit_skinny_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
+    const u32 M = ct->M, N = ct->N, K = ct->K, KW = pl->nw;
+    const u32 kcw = (K + KW - 1) / KW;
+    char fb[64];
+    const char *st;
+    out_store_fn(k, ct, fb, sizeof fb, &st);
+    dsb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", 64u * KW, pl->name);
+    emit_params(s, k->n_leaves);
+    dsb_put(s, ", float* ws) {\n");
+    dsb_put(s,
+            "  constexpr u32 M = %uu, N = %uu, K = %uu, KW = %uu, KCW = %uu, SKU = %uu;\n"
+            "  __shared__ float bs_[K * N];\n"
+            "  for (u32 i = threadIdx.x; i < K * N; i += 64u * KW) {\n"
+            "    const u32 k = i / N, n = i %% N;\n"
+            "    bs_[i] = ",
+            M, N, K, KW, kcw, 16u);
+    emit_operand_expr(s, k, ct, 1, "rowb_q(gid_n(n))", "n", "k");
+    dsb_put(s, ";\n"
+               "  }\n"
+               "  __syncthreads();\n"
+               "  const u32 lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n"
+               "  const u32 m = blockIdx.x * 64u + lane, ma = m < M ? m : M - 1u;\n"
+               "  const u32 kbeg = wave * KCW, kend = (kbeg + KCW < K) ? kbeg + KCW : K;\n"
+               "  float acc[N];\n"
+               "  #pragma unroll\n"
+               "  for (u32 n = 0; n < N; n++) acc[n] = 0.0f;\n");
+    if (ct->sep[0]) dsb_put(s, "  const u32 bA = rowb_p(gid_m(ma));\n");
+    if (pl->ske) {
+        /* K in blocks of E: the block's row-side offset once, the in-block
+         * offsets koff_p(i) constants; E loads in flight, then E*N FMAs with
+         * the block's rows of the small side from LDS */
+        const u32 E = pl->ske, nblk = K / E, bpw = (nblk + KW - 1) / KW;
+        char ldx[96];
+        if (pl->skmax != ~0ull)   /* the dispatch checks the buffer holds skmax */
+            snprintf(ldx, sizeof ldx, "ld_f32_u(p%u, oa + koff_p(i))", ct->sep_buf[0]);
+        else
+            snprintf(ldx, sizeof ldx, "%s(p%u, c%u, oa + koff_p(i))", ld_name(ct->sep_dt[0]), ct->sep_buf[0],
+                     ct->sep_buf[0]);
+        dsb_put(s, "  constexpr u32 E = %uu, NBLK = %uu, BPW = %uu;\n"
+                   "  const u32 bbeg = wave * BPW, bend = (bbeg + BPW < NBLK) ? bbeg + BPW : NBLK;\n"
+                   "  for (u32 bk = bbeg; bk < bend; bk++) {\n"
+                   "    const u32 kb = bk * E, oa = bA + koff_p(kb);\n"
+                   "    float a[E];\n"
+                   "    #pragma unroll\n"
+                   "    for (u32 i = 0; i < E; i++) a[i] = %s;\n"
+                   "    const float* br = bs_ + kb * N;\n"
+                   "    #pragma unroll\n"
+                   "    for (u32 i = 0; i < E; i++)\n"
+                   "      #pragma unroll\n"
+                   "      for (u32 n = 0; n < N; n++) acc[n] = fmaf(a[i], br[i * N + n], acc[n]);\n"
+                   "  }\n",
+                E, nblk, bpw, ldx);
+    } else {
+    /* two register sets of SKU operand elements: the next set's loads are
+     * issued before the current set's FMAs */
+    dsb_put(s, "  auto fetch = [&](u32 k0, float (&a)[SKU]) {\n"
+               "    #pragma unroll\n"
+               "    for (u32 u = 0; u < SKU; u++) {\n"
+               "      const u32 k = (k0 + u < kend) ? k0 + u : kbeg;\n"
+               "      const float v = ");
+    emit_operand_expr(s, k, ct, 0, "bA", "ma", "k");
+    dsb_put(s, ";\n"
+               "      a[u] = (k0 + u < kend) ? v : 0.0f;\n"
+               "    }\n"
+               "  };\n"
+               "  auto fmas = [&](u32 k0, const float (&a)[SKU]) {\n"
+               "    #pragma unroll\n"
+               "    for (u32 u = 0; u < SKU; u++) {\n"
+               "      const float* br = bs_ + ((k0 + u < kend) ? k0 + u : kbeg) * N;\n"
+               "      #pragma unroll\n"
+               "      for (u32 n = 0; n < N; n++) acc[n] = fmaf(a[u], br[n], acc[n]);\n"
+               "    }\n"
+               "  };\n"
+               "  float a0[SKU], a1[SKU];\n"
+               "  if (kbeg < kend) fetch(kbeg, a0);\n"
+               "  for (u32 k0 = kbeg; k0 < kend; k0 += 2u * SKU) {\n"
+               "    if (k0 + SKU < kend) fetch(k0 + SKU, a1);\n"
+               "    fmas(k0, a0);\n"
+               "    if (k0 + SKU >= kend) break;\n"
+               "    if (k0 + 2u * SKU < kend) fetch(k0 + 2u * SKU, a0);\n"
+               "    fmas(k0 + SKU, a1);\n"
+               "  }\n");
+    }
+    if (KW > 1)
+        dsb_put(s, "  __shared__ float part_[KW - 1u][N][64];\n"
+                   "  if (wave > 0u) {\n"
+                   "    #pragma unroll\n"
+                   "    for (u32 n = 0; n < N; n++) part_[wave - 1u][n][lane] = acc[n];\n"
+                   "  }\n"
+                   "  __syncthreads();\n"
+                   "  if (wave > 0u) return;\n"
+                   "  for (u32 w = 0; w + 1u < KW; w++)\n"
+                   "    #pragma unroll\n"
+                   "    for (u32 n = 0; n < N; n++) acc[n] = acc[n] + part_[w][n][lane];\n");
+    dsb_put(s, "  if (m < M) {\n"
+               "    #pragma unroll\n"
+               "    for (u32 n = 0; n < N; n++) %s(p0, c0, gid_m(m) + gid_n(n), %s + acc[n]);\n"
+               "  }\n"
+               "}\n", st, fb);
 }
 
 /* Direct kernel: a workgroup of 4 waves owns one 32x32 output block; the
@@ -719,6 +847,10 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
     }
     const u32 M = ct->M, N = ct->N, K = pl->kp.on ? pl->kp.Kl : ct->K;   /* the reordered (padded) K */
     const u32 tiles = pl->tiles_m * pl->tiles_n;
+    if (cf->direct == 2) {
+        emit_skinny_kernel(&s, k, ct, pl);
+        return s.p;
+    }
     if (cf->direct) {
         emit_direct_kernel(&s, k, ct, pl);
         emit_store_tail(&s, k, ct, pl);
@@ -1011,6 +1143,8 @@ static DenseEntry *insert(u64 key, const UOpKernel *k) {
 static TileCfg pick_cfg(u32 M, u32 N, u32 K) {
     u64 big_tiles = (u64)((M + 127) / 128) * ((N + 127) / 128);
     if (M >= 128 && N >= 128 && big_tiles >= 128) return CFG_BIG;
+    if (N <= SKINNY_MAX_N && M >= SKINNY_MIN_M && (u64)K * N <= SKINNY_MAX_KN && !hipb.dense_noskinny)
+        return CFG_SKINNY;
     if (N <= 32 && M >= 4096) return CFG_TALL;
     if (M <= 32 && N >= 4096) return CFG_WIDE;
     if (N > 32 && N <= 64 && M >= 4096) return CFG_MID;
@@ -1245,6 +1379,17 @@ static void plan_chunks(const Contraction *ct, GemmPlan *pl) {
      * -> 17 us, and 16 waves were slower everywhere, 12 -> 31 us on fc1: wave
      * 0 then adds 15 partial blocks from 60 KB of LDS) */
     pl->nw = 4;
+    if (pl->cfg.direct == 2) {
+        /* skinny: waves per workgroup splitting K, aiming at SKINNY_TARGET_WAVES
+         * waves in all with at least 8 k per wave */
+        const u32 rows = pl->tiles_m;
+        u32 kw = 1;
+        while (kw < 16 && (u64)rows * kw * 2 <= SKINNY_TARGET_WAVES && ct->K / (kw * 2) >= 8) kw *= 2;
+        pl->nw = hipb.direct_waves ? hipb.direct_waves : kw;
+        pl->kchunk = ct->K;
+        pl->splits = 1;
+        return;
+    }
     if (pl->cfg.direct) {
         const u32 steps = (kch + pl->cfg.bk - 1) / pl->cfg.bk;
         if (hipb.direct_waves) pl->nw = hipb.direct_waves;
@@ -1254,10 +1399,51 @@ static void plan_chunks(const Contraction *ct, GemmPlan *pl) {
 
 static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const TileCfg *cfg);
 
+/* Skinny block size: the largest E <= SKINNY_MAX_E dividing K such that no
+ * k digit of either side straddles it (each lies wholly below E or wholly at
+ * or above it), so that koff(kb + i) = koff(kb) + koff(i) for kb a multiple
+ * of E and i < E: the kernel unrolls i and every in-block offset is a
+ * constant. And the largest index the row side forms. */
+#define SKINNY_MAX_E 64
+static void plan_skinny(const Contraction *ct, GemmPlan *pl) {
+    pl->ske = 0;
+    pl->skmax = ~0ull;
+    if (pl->cfg.direct != 2) return;
+    pl->skbuf = ct->sep[0] ? ct->sep_buf[0] : 0;
+    if (ct->sep[0] && ct->sep_dt[0] == DTYPE_F32) {
+        const Aff *a = &ct->sep_aff[0];
+        u64 mx = a->cst;
+        for (u32 t = 0; t < a->n; t++)
+            mx += (u64)a->coef[t] * digit_max(&a->d[t], a->d[t].var == 0 ? (u64)ct->M * ct->N : ct->K);
+        pl->skmax = mx;
+    }
+    if (!ct->sep[0] || !ct->sep[1] || hipb.dense_noskinny_blocks) return;
+    for (u32 E = SKINNY_MAX_E < ct->K ? SKINNY_MAX_E : ct->K; E >= 2; E--) {
+        if (ct->K % E) continue;
+        int ok = 1;
+        for (int sd = 0; sd < 2 && ok; sd++) {
+            const Aff *a = &ct->sep_aff[sd];
+            for (u32 t = 0; t < a->n && ok; t++) {
+                const Digit *d = &a->d[t];
+                if (d->var != 1) continue;
+                const u64 end = d->mod ? (u64)d->div * d->mod : ct->K;
+                if (!(end <= E && E % end == 0) && !(d->div >= E && d->div % E == 0)) ok = 0;
+            }
+        }
+        if (ok) {
+            pl->ske = E;
+            return;
+        }
+    }
+}
+
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
-    static const TileCfg *forced[8] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
-                                       &CFG_C64S};
-    const TileCfg cfg = hipb.dense_tile ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
+    static const TileCfg *forced[9] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
+                                       &CFG_C64S, &CFG_SKINNY};
+    /* the skinny kernel keeps N sums per lane: forced only up to its N */
+    const int forced_ok = hipb.dense_tile &&
+                          !(hipb.dense_tile == 8 && (ct->N > SKINNY_MAX_N || (u64)ct->K * ct->N > SKINNY_MAX_KN));
+    const TileCfg cfg = forced_ok ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
     make_plan_cfg(ct, pl, sig, &cfg);
 }
 
@@ -1291,6 +1477,7 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
         if (splits > 1024) splits = 1024;
     }
     if (hipb.dense_splits) splits = hipb.dense_splits;
+    if (pl->cfg.direct == 2) splits = 1;
     pl->splits_want = splits;
     snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));
     pl->swap = !pl->cfg.direct && !hipb.dense_noswap && ct->np > 0 && ct->pdiv[ct->np - 1] == 1 &&
@@ -1299,6 +1486,7 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
     plan_pack(ct, pl);
     plan_pads(ct, pl);
     plan_chunks(ct, pl);
+    plan_skinny(ct, pl);
 }
 
 /* Contraction analysis without a device: returns 1 and fills M/N/K when the
@@ -1412,6 +1600,8 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     if (!e->is_dense) return 0;
     /* buffers smaller than the plan was made for: the generated kernels */
     if (e->plan.kp.on && !kperm_fits(&e->plan, counts, ptrs)) return 0;
+    if (e->plan.cfg.direct == 2 && e->plan.ske && e->plan.skmax != ~0ull && e->plan.skmax >= counts[e->plan.skbuf])
+        return 0;
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     /* split-K workspace */
     float *ws = NULL;

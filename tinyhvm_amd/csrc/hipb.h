@@ -53,9 +53,11 @@ typedef struct {
     int dense_novec;         /* THVM_HIP_DENSE_NOVEC: no 16-byte operand loads */
     int dense_noswap;        /* THVM_HIP_DENSE_NOSWAP: lanes along n in every GEMM epilogue */
     int dense_nopack;        /* THVM_HIP_DENSE_NOPACK: never pack a GEMM's B side */
+    int dense_noskinny;      /* THVM_HIP_DENSE_NOSKINNY: no row-per-lane kernel for N <= 16 */
+    int dense_noskinny_blocks; /* THVM_HIP_DENSE_NOSKBLK: the row-per-lane kernel walks K per k */
     int dense_pack;          /* THVM_HIP_DENSE_PACK: pack wherever the layout allows (tests) */
     u32 dense_tile;          /* THVM_HIP_DENSE_TILE: 0 chosen, 1 128x128, 2 64x64, 3 256x32, 4 32x256, 5 direct,
-                                6 256x64, 7 128x64 */
+                                6 256x64, 7 128x64, 8 skinny (where N <= 16) */
     int force_interp;        /* THVM_HIP_INTERP: run generated-kernel programs on the KOp interpreter */
     int rtc_fail;            /* THVM_HIP_RTC_FAIL: treat every program compile as failed (tests) */
     u64 n_dispatch, n_compile, n_cache_hit, n_dense;
