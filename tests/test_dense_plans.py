@@ -36,6 +36,7 @@ def _plans(name):
         nw = re.search(r"NW = (\d+)u", src)
         kw = re.search(r"KW = (\d+)u, KCW", src)
         ke = re.search(r"constexpr u32 E = (\d+)u, NBLK", src)
+        ro = re.search(r"MG = (\d+)u, V = \d+u, VP = \d+u, KCH = (\d+)u", src)
         out[a] = {
             "tile": (int(cst.group(1)), int(cst.group(2))) if cst else "direct",
             "kperm": "kbase_p(" in src,
@@ -48,6 +49,7 @@ def _plans(name):
             "skinny": "KCW = " in src,
             "skinny_waves": int(kw.group(1)) if kw else None,
             "skinny_block": int(ke.group(1)) if ke else None,
+            "outer": (int(ro.group(1)), int(ro.group(2))) if ro else None,
         }
     return out
 
@@ -84,9 +86,17 @@ def test_lenet_few_channel_convolutions_are_skinny():
         assert src["skinny"] and src["skinny_waves"] == waves and src["skinny_block"] == 25, (shape, src)
 
 
+def test_lenet_convolution_weight_gradients_are_outer_product_reductions():
+    # conv1 dW (25x6 over 200704 pixels) and conv2 dW (150x16 over 25600):
+    # a k per lane, row groups of at most 96 / N rows, K chunks of at least
+    # 8 k per lane, partials through the split-K sum
+    p = _plans("lenet_b256.trc")
+    assert p[(25, 6, 200704, 98)]["outer"] == (13, 2048)
+    assert p[(150, 16, 25600, 12)]["outer"] == (6, 2134)
+
+
 def test_lenet_fc_weight_gradients_use_eight_waves():
     p = _plans("lenet_b256.trc")
     for shape in [(400, 120, 256, 1), (120, 84, 256, 1), (84, 10, 256, 1)]:
         assert p[shape]["tile"] == "direct" and p[shape]["waves"] == 8, (shape, p[shape])
-    # split-K direct kernels keep 4 waves
-    assert p[(25, 6, 200704, 483)]["waves"] == 4
+

@@ -20,17 +20,19 @@ pytestmark = pytest.mark.gpu
 # (split-K factor, tile shape): 0 = chosen by size, 1 = 128x128, 2 = 64x64,
 # 3 = 256x32, 4 = 32x256, 5 = direct (per-wave 32x32 blocks, no LDS), 6 = 256x64,
 # 7 = 128x64, 8 = skinny (a row per lane, for at most 16 columns; wider
-# contractions keep the chosen tile)
+# contractions keep the chosen tile), 9 = outer-product reduction (a k per
+# lane, for few outputs; others keep the chosen tile)
 CONFIGS = [("1", "0"), ("2", "0"), ("1", "1"), ("3", "2"), ("1", "3"), ("2", "4"), ("1", "5"), ("3", "5"),
            ("1", "6"), ("3", "6"), ("1", "7"), ("2", "7"), ("8", "2"), ("16", "7"), ("1", "2", "pack"),
-           ("2", "7", "pack"), ("1", "8"), ("1", "8", "noskblk")]
+           ("2", "7", "pack"), ("1", "8"), ("1", "8", "noskblk"), ("1", "9")]
 
 
 @pytest.fixture(scope="module", params=CONFIGS,
                 ids=["whole-K", "split-K", "tile128x128", "tile64x64-split3", "tile256x32",
                      "tile32x256-split2", "direct", "direct-split3", "tile256x64", "tile256x64-split3",
                      "tile128x64", "tile128x64-split2", "tile64x64-split8", "tile128x64-split16",
-                     "tile64x64-packed", "tile128x64-split2-packed", "skinny", "skinny-per-k"])
+                     "tile64x64-packed", "tile128x64-split2-packed", "skinny", "skinny-per-k",
+                     "outer-product"])
 def hip_dense(request):
     saved = {k: os.environ.get(k) for k in ("THVM_HIP_DENSE_FORCE", "THVM_HIP_DENSE_SPLITS",
                                              "THVM_HIP_DENSE_TILE", "THVM_HIP_DENSE_PACK", "THVM_HIP_DENSE_NOSKBLK")}

@@ -344,6 +344,20 @@ static const TileCfg CFG_DIRECT = {32, 32, 32, 1, 1, 1, 1, "direct32", 1};
  * workgroup's waves splitting K and adding their sums in wave order. VALU
  * FMAs, no LDS tiles, no split-K workspace. */
 static const TileCfg CFG_SKINNY = {64, 16, 1, 1, 1, 1, 1, "skinny", 2};
+/* Outer-product reductions: few outputs (M*N <= RED_MAX_MN) over a long K
+ * (the weight gradients of a few-channel convolution: LeNet-5's conv1,
+ * 25x6 over 200704 pixels, and conv2, 150x16 over 25600). On MFMA blocks
+ * most of each 32x32 block is empty and the split-K chain is long. Here a
+ * lane walks k (a pixel: unit stride along the image rows) and keeps the
+ * outer products of a group of MG rows with all N columns in registers;
+ * a workgroup takes one row group and one K chunk, halves its partials
+ * across the wavefront's lanes by shuffles, adds the four waves in order, and
+ * the chunks' partials go through the split-K sum. Both sides separable. */
+static const TileCfg CFG_RED = {1, 1, 1, 1, 1, 1, 1, "outer", 3};
+#define RED_MAX_MN 4096
+#define RED_MIN_K 8192
+#define RED_MAX_ACC 96        /* MG * N */
+#define RED_K_PER_LANE 8
 #define SKINNY_MAX_N 16
 #define SKINNY_MAX_KN 8192   /* the small side in LDS: at most 32 KB */
 #define SKINNY_MIN_M 4096
@@ -395,6 +409,9 @@ typedef struct {
     u64 skmax;             /* skinny: largest index the row side's loads form (unchecked loads
                               when the buffer holds it), or ~0 */
     u32 skbuf;             /* skinny: the buffer of the row side (1 + leaf) */
+    u32 red_mg;            /* outer-product reduction: rows per group */
+    u64 red_max[2];        /* ... the largest index each side forms (unchecked loads) */
+    u32 red_buf[2];        /* ... and the buffer it reads (1 + leaf) */
 } GemmPlan;
 
 #define GEMM_THREADS 256
@@ -458,6 +475,8 @@ static void out_store_fn(const UOpKernel *k, const Contraction *ct, char *fb, si
 /* Closes the epilogue opened by the caller (inside `if (m < M && n < N) {`
  * with the accumulator value c[v]): stores the result (or the split's partial
  * into the workspace), closes the kernel, and emits the split-K sum kernel. */
+static void emit_sum_kernel(DSB *s_, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl);
+
 static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
     DSB *s_ = sp;
     char fb[64];
@@ -471,6 +490,17 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
     else
         dsb_put(s_, "        %s(p0, c0, gid_m(m) + gid_n(n), %s + c[v]);\n", st, fb);
     dsb_put(s_, "      }\n    }\n  }\n}\n");
+    emit_sum_kernel(s_, k, ct, pl);
+}
+
+/* The split-K sum kernel (<name>_sum) of a plan with splits > 1: adds the
+ * splits' partials ws[split][m][n] (or [split][n][m] with swap) per output in
+ * a fixed order and stores init + the sum. */
+static void emit_sum_kernel(DSB *s_, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
+    char fb[64];
+    const char *st;
+    out_store_fn(k, ct, fb, sizeof fb, &st);
+    const u32 M = ct->M, N = ct->N;
     if (pl->splits <= 1) return;
     if (sum_per_wave(pl, (u64)M * N)) {
         /* many splits: one wavefront per output; lane l adds splits l, l+64, ...
@@ -523,6 +553,74 @@ static void emit_operand_expr(DSB *s, const UOpKernel *k, const Contraction *ct,
         emit_args(s, k->n_leaves);
         dsb_put(s, ")");
     }
+}
+
+/* Outer-product reduction kernel (CFG_RED): workgroup (g, s) takes rows
+ * [g*MG, g*MG + MG) and k in chunk s; lane l of wave w walks k = kbeg + 64w + l,
+ * kbeg + 256 + 64w + l, ... in order. The MG*N sums of the 64 lanes are added
+ * through an LDS transpose, 32 sums at a time (lane j adds sum j over the
+ * lanes in order; a shuffle tree per value, every shuffle waited for, took
+ * 12 of 19 us on LeNet-5's conv1 dW); wave 0 then adds the four waves in
+ * order and writes the chunk's partials for the split-K sum. Loads are
+ * unchecked: the dispatch sees that both buffers hold the largest index
+ * their sides form. Deterministic. */
+static void emit_red_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
+    const u32 M = ct->M, N = ct->N, K = ct->K, MG = pl->red_mg, V = MG * N;
+    const u32 VP = (V + 63) / 64 * 64;
+    dsb_put(s, "extern \"C\" __global__ __launch_bounds__(256) void %s(", pl->name);
+    emit_params(s, k->n_leaves);
+    dsb_put(s, ", float* ws) {\n");
+    dsb_put(s,
+            "  constexpr u32 M = %uu, N = %uu, K = %uu, MG = %uu, V = %uu, VP = %uu, KCH = %uu;\n"
+            "  const u32 lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n"
+            "  const u32 m0 = blockIdx.x * MG, spl = blockIdx.y;\n"
+            "  const u32 kbeg = spl * KCH, kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
+            "  u32 rb[MG];\n"
+            "  #pragma unroll\n"
+            "  for (u32 i = 0; i < MG; i++) rb[i] = rowb_p(gid_m(m0 + i < M ? m0 + i : M - 1u));\n"
+            "  float acc[V];\n"
+            "  #pragma unroll\n"
+            "  for (u32 j = 0; j < V; j++) acc[j] = 0.0f;\n"
+            "  #pragma unroll 2\n"
+            "  for (u32 k = kbeg + wave * 64u + lane; k < kend; k += 256u) {\n"
+            "    const u32 op = koff_p(k), oq = koff_q(k);\n"
+            "    float a[MG], b[N];\n"
+            "    #pragma unroll\n"
+            "    for (u32 i = 0; i < MG; i++) a[i] = (m0 + i < M) ? ld_f32_u(p%u, rb[i] + op) : 0.0f;\n"
+            "    #pragma unroll\n"
+            "    for (u32 n = 0; n < N; n++) b[n] = ld_f32_u(p%u, rowb_q(gid_n(n)) + oq);\n"
+            "    #pragma unroll\n"
+            "    for (u32 i = 0; i < MG; i++)\n"
+            "      #pragma unroll\n"
+            "      for (u32 n = 0; n < N; n++) acc[i * N + n] = fmaf(a[i], b[n], acc[i * N + n]);\n"
+            "  }\n"
+            "  /* each chunk of 32 sums through LDS: lane l writes its 32 values as\n"
+            "   * column l, lane j < 32 adds row j over the 64 lanes in order */\n"
+            "  constexpr u32 NQ = (V + 31u) / 32u;\n"
+            "  __shared__ float tr_[4][32][65];\n"
+            "  __shared__ float tot_[4][NQ * 32u];\n"
+            "  #pragma unroll\n"
+            "  for (u32 q = 0; q < NQ; q++) {\n"
+            "    #pragma unroll\n"
+            "    for (u32 j = 0; j < 32u; j++) tr_[wave][j][lane] = (32u * q + j < V) ? acc[32u * q + j] : 0.0f;\n"
+            "    __syncthreads();\n"
+            "    if (lane < 32u) {\n"
+            "      float t = 0.0f;\n"
+            "      #pragma unroll 16\n"
+            "      for (u32 i = 0; i < 64u; i++) t = t + tr_[wave][lane][i];\n"
+            "      tot_[wave][32u * q + lane] = t;\n"
+            "    }\n"
+            "    __syncthreads();\n"
+            "  }\n"
+            "  __syncthreads();\n"
+            "  if (wave > 0u) return;\n"
+            "  for (u32 idx = lane; idx < V; idx += 64u) {\n"
+            "    const float t = ((tot_[0][idx] + tot_[1][idx]) + tot_[2][idx]) + tot_[3][idx];\n"
+            "    const u32 i = idx / N, n = idx %% N, m = m0 + i;\n"
+            "    if (m < M) ws[((unsigned long long)spl * M + m) * N + n] = t;\n"
+            "  }\n"
+            "}\n",
+            M, N, K, MG, V, VP, pl->kchunk, ct->sep_buf[0], ct->sep_buf[1]);
 }
 
 /* Skinny kernel (CFG_SKINNY): lane = row m, all N column sums in registers.
@@ -849,6 +947,11 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
     const u32 tiles = pl->tiles_m * pl->tiles_n;
     if (cf->direct == 2) {
         emit_skinny_kernel(&s, k, ct, pl);
+        return s.p;
+    }
+    if (cf->direct == 3) {
+        emit_red_kernel(&s, k, ct, pl);
+        emit_sum_kernel(&s, k, ct, pl);
         return s.p;
     }
     if (cf->direct) {
@@ -1379,6 +1482,28 @@ static void plan_chunks(const Contraction *ct, GemmPlan *pl) {
      * -> 17 us, and 16 waves were slower everywhere, 12 -> 31 us on fc1: wave
      * 0 then adds 15 partial blocks from 60 KB of LDS) */
     pl->nw = 4;
+    if (pl->cfg.direct == 3) {
+        /* row groups of at most RED_MAX_ACC / N rows, balanced; K chunks of
+         * at least RED_K_PER_LANE k per lane, about 1024 workgroups at most */
+        const u32 mgmax = RED_MAX_ACC / ct->N, ng = (ct->M + mgmax - 1) / mgmax;
+        pl->red_mg = (ct->M + ng - 1) / ng;
+        pl->tiles_m = (ct->M + pl->red_mg - 1) / pl->red_mg;
+        pl->tiles_n = 1;
+        u32 sp = ct->K / (GEMM_THREADS * RED_K_PER_LANE);
+        if (sp > 1024 / pl->tiles_m) sp = 1024 / pl->tiles_m;
+        if (sp < 2) sp = 2;
+        pl->kchunk = (ct->K + sp - 1) / sp;
+        pl->splits = (ct->K + pl->kchunk - 1) / pl->kchunk;
+        for (int sd = 0; sd < 2; sd++) {
+            const Aff *a = &ct->sep_aff[sd];
+            u64 mx = a->cst;
+            for (u32 t = 0; t < a->n; t++)
+                mx += (u64)a->coef[t] * digit_max(&a->d[t], a->d[t].var == 0 ? (u64)ct->M * ct->N : ct->K);
+            pl->red_max[sd] = mx;
+            pl->red_buf[sd] = ct->sep_buf[sd];
+        }
+        return;
+    }
     if (pl->cfg.direct == 2) {
         /* skinny: waves per workgroup splitting K, aiming at SKINNY_TARGET_WAVES
          * waves in all with at least 8 k per wave */
@@ -1438,12 +1563,18 @@ static void plan_skinny(const Contraction *ct, GemmPlan *pl) {
 }
 
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
-    static const TileCfg *forced[9] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
-                                       &CFG_C64S, &CFG_SKINNY};
-    /* the skinny kernel keeps N sums per lane: forced only up to its N */
+    static const TileCfg *forced[10] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
+                                        &CFG_C64S, &CFG_SKINNY, &CFG_RED};
+    const int red_fits = ct->sep[0] && ct->sep[1] && ct->sep_dt[0] == DTYPE_F32 && ct->sep_dt[1] == DTYPE_F32 &&
+                         ct->M >= 2 && ct->N >= 2 &&
+                         (u64)ct->M * ct->N <= RED_MAX_MN && ct->N <= RED_MAX_ACC;
+    /* the skinny kernel keeps N sums per lane and the outer-product one MG*N:
+     * forced only where they apply */
     const int forced_ok = hipb.dense_tile &&
-                          !(hipb.dense_tile == 8 && (ct->N > SKINNY_MAX_N || (u64)ct->K * ct->N > SKINNY_MAX_KN));
-    const TileCfg cfg = forced_ok ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
+                          !(hipb.dense_tile == 8 && (ct->N > SKINNY_MAX_N || (u64)ct->K * ct->N > SKINNY_MAX_KN)) &&
+                          !(hipb.dense_tile == 9 && !red_fits);
+    TileCfg cfg = forced_ok ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
+    if (!forced_ok && !hipb.dense_nored && red_fits && ct->K >= RED_MIN_K) cfg = CFG_RED;
     make_plan_cfg(ct, pl, sig, &cfg);
 }
 
@@ -1478,6 +1609,7 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
     }
     if (hipb.dense_splits) splits = hipb.dense_splits;
     if (pl->cfg.direct == 2) splits = 1;
+    if (pl->cfg.direct == 3) splits = 2;   /* the chunks are chosen with the row groups */
     pl->splits_want = splits;
     snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));
     pl->swap = !pl->cfg.direct && !hipb.dense_noswap && ct->np > 0 && ct->pdiv[ct->np - 1] == 1 &&
@@ -1602,6 +1734,9 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     if (e->plan.kp.on && !kperm_fits(&e->plan, counts, ptrs)) return 0;
     if (e->plan.cfg.direct == 2 && e->plan.ske && e->plan.skmax != ~0ull && e->plan.skmax >= counts[e->plan.skbuf])
         return 0;
+    if (e->plan.cfg.direct == 3 &&
+        (e->plan.red_max[0] >= counts[e->plan.red_buf[0]] || e->plan.red_max[1] >= counts[e->plan.red_buf[1]]))
+        return 0;
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
     /* split-K workspace */
     float *ws = NULL;
@@ -1631,7 +1766,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         if (!hipb_launch_grid(e->fn_pack, (u32)((kn + 255) / 256), 1, 256, pp)) return 0;
     }
     u32 tiles = e->plan.tiles_m * e->plan.tiles_n;
-    const u32 threads = e->plan.cfg.direct ? 64u * e->plan.nw : GEMM_THREADS;
+    const u32 threads = e->plan.cfg.direct == 3 ? GEMM_THREADS : e->plan.cfg.direct ? 64u * e->plan.nw : GEMM_THREADS;
     if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, threads, params)) return 0;
     if (e->plan.splits > 1) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};

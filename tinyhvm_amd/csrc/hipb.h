@@ -55,9 +55,11 @@ typedef struct {
     int dense_nopack;        /* THVM_HIP_DENSE_NOPACK: never pack a GEMM's B side */
     int dense_noskinny;      /* THVM_HIP_DENSE_NOSKINNY: no row-per-lane kernel for N <= 16 */
     int dense_noskinny_blocks; /* THVM_HIP_DENSE_NOSKBLK: the row-per-lane kernel walks K per k */
+    int dense_nored;         /* THVM_HIP_DENSE_NORED: no outer-product reduction kernel */
     int dense_pack;          /* THVM_HIP_DENSE_PACK: pack wherever the layout allows (tests) */
     u32 dense_tile;          /* THVM_HIP_DENSE_TILE: 0 chosen, 1 128x128, 2 64x64, 3 256x32, 4 32x256, 5 direct,
-                                6 256x64, 7 128x64, 8 skinny (where N <= 16) */
+                                6 256x64, 7 128x64, 8 skinny (where N <= 16), 9 outer-product reduction
+                                (where it applies) */
     int force_interp;        /* THVM_HIP_INTERP: run generated-kernel programs on the KOp interpreter */
     int rtc_fail;            /* THVM_HIP_RTC_FAIL: treat every program compile as failed (tests) */
     u64 n_dispatch, n_compile, n_cache_hit, n_dense;
