@@ -139,13 +139,13 @@ int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32
                                           const UOpKernel *kernel);
 
 /* Counters, for tests and the engine-driven timing (no counterpart in the
- * reference): out[0..9] = dispatches, matrix-core dispatches, compiled
+ * reference): out[0..11] = dispatches, matrix-core dispatches, compiled
  * programs, program cache hits, dispatches run on the KOp interpreter
  * (programs the generator or hipRTC refused; their outputs are still
  * written), host waits on the stream, live device bytes, hipMalloc calls,
  * device blocks pinned by HIP graphs, released blocks held for graphs,
- * dispatches run on the window-max and run-sum kernels. Returns the number
- * of counters (11). */
+ * dispatches run on the window-max and run-sum kernels, dispatches issued
+ * inside a batched launch. Returns the number of counters (12). */
 int  thvm_hip_counters(u64 *out, u32 n);
 /* Wait for all enqueued work; returns 0, or -1 on a device error. */
 int  thvm_hip_synchronize(void);

@@ -26,6 +26,8 @@ hipError_t hipb_stream_wait(void) {
     hipb.n_stream_sync++;
     return hipStreamSynchronize(hipb.stream);
 }
+/* the backend's held dispatches (none here: the pool alone is under test) */
+void hipb_before_stream(void) {}
 
 extern size_t fake_hip_limit, fake_hip_live;
 extern unsigned long fake_hip_mallocs, fake_hip_frees;

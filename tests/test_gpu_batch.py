@@ -1,0 +1,66 @@
+"""Batched launches of small independent generated kernels.
+
+A LeNet-5 training step at batch 256 ends with ten SGD updates (one small
+elementwise kernel per parameter, none reading another's output), which the
+backend holds back and issues as one launch of a batch kernel. The step is
+replayed twice from the same parameters in fresh backends, with batching on
+and with THVM_HIP_NO_BATCH=1: the ten updated parameters must be bit
+identical (the same per-element arithmetic either way), and the batched run
+must have issued at least the ten updates inside batch launches.
+"""
+import ctypes as C
+import os
+
+import pytest
+
+from tinyhvm_amd import _lib, trace
+
+pytestmark = pytest.mark.gpu
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+TRACE = os.path.join(ROOT, "tinyhvm_amd", "workloads", "lenet_b256.trc")
+PARAMS = range(2, 12)          # trace ids of W1, b1, ..., W5, b5
+
+
+def _step(no_batch):
+    old = os.environ.get("THVM_HIP_NO_BATCH")
+    os.environ["THVM_HIP_NO_BATCH"] = "1" if no_batch else "0"
+    L = _lib.lib()
+    try:
+        assert L.thvm_hip_init() == 0
+        sizes = {r.f["id"]: r.f["bytes"] for r in trace.read_trace(TRACE) if r.tag == trace.ALLOC}
+        be = L.thvm_hip_backend()
+        t = L.thvm_trace_load(TRACE.encode())
+        assert t
+        lo = L.thvm_trace_find_mark(t, b"lenet.step", 0)
+        hi = L.thvm_trace_find_mark(t, b"lenet.end", lo)
+        L.thvm_trace_replay(t, be, 0, lo, 0)
+        before = (C.c_uint64 * 12)()
+        L.thvm_hip_counters(before, 12)
+        L.thvm_trace_replay(t, be, lo, hi, 1)
+        assert L.thvm_hip_synchronize() == 0
+        after = (C.c_uint64 * 12)()
+        assert L.thvm_hip_counters(after, 12) == 12
+        out = {}
+        for tid in PARAMS:
+            buf = (C.c_uint8 * sizes[tid])()
+            L.thvm_hip_buf_read(L.thvm_trace_live_id(t, tid), buf, sizes[tid])
+            out[tid] = bytes(buf)
+        L.thvm_trace_release(t, be)
+        L.thvm_trace_free(t)
+        return out, after[11] - before[11]
+    finally:
+        L.thvm_hip_shutdown()
+        if old is None:
+            os.environ.pop("THVM_HIP_NO_BATCH", None)
+        else:
+            os.environ["THVM_HIP_NO_BATCH"] = old
+
+
+def test_batched_sgd_updates_match_single_launches():
+    single, n_single = _step(no_batch=True)
+    batched, n_batched = _step(no_batch=False)
+    assert n_single == 0
+    assert n_batched >= 10, "the ten SGD updates were not batched (%d batched)" % n_batched
+    bad = [tid for tid in PARAMS if single[tid] != batched[tid]]
+    assert not bad, "parameters %s differ between batched and single launches" % bad

@@ -71,6 +71,219 @@ static void copyq_guard_dispatch(u32 out, const u32 *leaves, u32 n) {
     for (u32 i = 0; i < n && CQ.b.n; i++) copyq_guard(leaves[i]);
 }
 
+/* Batched launches. Small serial generated kernels (at most HB_MAX_BLOCKS
+ * workgroups of 256 lanes) are held back instead of launched; while the next
+ * dispatches are such kernels too and touch no memory a held one writes (and
+ * write none a held one reads), they join it. The held dispatches then go out
+ * as one launch of a kernel that calls each one's device function on its own
+ * range of workgroups (compiled once per sequence of programs and grid
+ * sizes). The ten SGD updates of a LeNet-5 step are one launch. Any other
+ * work put on the stream issues the held dispatches first
+ * (hipb_before_stream), so the stream still sees everything in program
+ * order; dispatches in one batch are independent by construction. */
+#define HB_MAX 16
+#define HB_MAX_BLOCKS 64
+typedef struct {
+    hipFunction_t fn;
+    u64 key;
+    const char *name, *bsrc, *bparams;
+    u32 blocks;
+    u32 nb, n_scal;
+    void *ptrs[FUSE_MAX_LEAVES + 1];
+    u32 counts[FUSE_MAX_LEAVES + 1];
+    u32 sm;
+    float sv[KGEN_MAX_SCALARS];
+    u64 w_lo, w_hi;
+    u32 nr;
+    u64 r_lo[FUSE_MAX_LEAVES], r_hi[FUSE_MAX_LEAVES];
+} HbEnt;
+static struct {
+    HbEnt ent[HB_MAX];
+    u32 n;
+    int flushing;
+    struct { u64 key; hipModule_t mod; hipFunction_t fn; } cache[64];
+    u32 ncache;
+} HB;
+
+static int hb_overlap(u64 a0, u64 a1, u64 b0, u64 b1) { return a0 < b1 && b0 < a1; }
+
+/* the launch parameters of one held dispatch, in its kernel's order */
+static u32 hb_params(HbEnt *h, void **pv) {
+    u32 n = 0;
+    for (u32 b = 0; b < h->nb; b++) pv[n++] = &h->ptrs[b];
+    for (u32 b = 0; b < h->nb; b++) pv[n++] = &h->counts[b];
+    if (h->n_scal) {
+        pv[n++] = &h->sm;
+        for (u32 j = 0; j < h->n_scal; j++) pv[n++] = &h->sv[j];
+    }
+    return n;
+}
+
+static u64 hb_mix(u64 h, u64 v) {
+    h ^= v + 0x9E3779B97F4A7C15ull + (h << 6) + (h >> 2);
+    h *= 0xFF51AFD7ED558CCDull;
+    return h ^ (h >> 33);
+}
+
+/* The batch kernel for the held sequence: each program's device function
+ * once, and an entry that hands workgroup ranges to them in order. */
+static hipFunction_t hb_batch_fn(u64 key) {
+    for (u32 i = 0; i < HB.ncache; i++)
+        if (HB.cache[i].key == key) return HB.cache[i].fn;
+    if (HB.ncache >= sizeof HB.cache / sizeof HB.cache[0]) return NULL;
+    size_t cap = strlen(kgen_prelude()) + 4096;
+    for (u32 i = 0; i < HB.n; i++) cap += strlen(HB.ent[i].bsrc) + 4 * strlen(HB.ent[i].bparams) + 512;
+    char *src = malloc(cap);
+    if (!src) return NULL;
+    size_t w = (size_t)snprintf(src, cap, "%s\n", kgen_prelude());
+    for (u32 i = 0; i < HB.n; i++) {
+        int seen = 0;
+        for (u32 j = 0; j < i; j++) seen |= HB.ent[j].key == HB.ent[i].key;
+        if (!seen) w += (size_t)snprintf(src + w, cap - w, "%s\n", HB.ent[i].bsrc);
+    }
+    char name[48];
+    snprintf(name, sizeof name, "thvm_batch_%016llx", (unsigned long long)key);
+    w += (size_t)snprintf(src + w, cap - w, "extern \"C\" __global__ __launch_bounds__(256) void %s(", name);
+    /* parameters: every dispatch's list, each name prefixed q<i>_ */
+    for (u32 i = 0; i < HB.n; i++) {
+        const char *p = HB.ent[i].bparams;
+        while (*p) {
+            const char *e = strstr(p, ", ");
+            size_t len = e ? (size_t)(e - p) : strlen(p);
+            const char *sp = p + len;
+            while (sp > p && sp[-1] != ' ' && sp[-1] != '*') sp--;
+            w += (size_t)snprintf(src + w, cap - w, "%s%.*sq%u_%.*s", (i || p != HB.ent[i].bparams) ? ", " : "",
+                                  (int)(sp - p), p, i, (int)(len - (size_t)(sp - p)), sp);
+            p = e ? e + 2 : p + len;
+        }
+    }
+    w += (size_t)snprintf(src + w, cap - w, ") {\n  u32 b_ = blockIdx.x;\n");
+    for (u32 i = 0; i < HB.n; i++) {
+        w += (size_t)snprintf(src + w, cap - w, "  if (b_ < %uu) { %s_b(b_", HB.ent[i].blocks, HB.ent[i].name);
+        const char *p = HB.ent[i].bparams;
+        while (*p) {
+            const char *e = strstr(p, ", ");
+            size_t len = e ? (size_t)(e - p) : strlen(p);
+            const char *sp = p + len;
+            while (sp > p && sp[-1] != ' ' && sp[-1] != '*') sp--;
+            w += (size_t)snprintf(src + w, cap - w, ", q%u_%.*s", i, (int)(len - (size_t)(sp - p)), sp);
+            p = e ? e + 2 : p + len;
+        }
+        w += (size_t)snprintf(src + w, cap - w, "); return; }\n  b_ -= %uu;\n", HB.ent[i].blocks);
+    }
+    snprintf(src + w, cap - w, "}\n");
+    if (hipb.dump_src) fprintf(stderr, "---- batch kernel ----\n%s\n", src);
+    char err[256] = {0};
+    hipModule_t mod;
+    hipFunction_t fn = NULL;
+    if (rtc_build_module(src, &mod, err, sizeof err)) {
+        if (hipModuleGetFunction(&fn, mod, name) == hipSuccess) {
+            HB.cache[HB.ncache].key = key;
+            HB.cache[HB.ncache].mod = mod;
+            HB.cache[HB.ncache].fn = fn;
+            HB.ncache++;
+            hipb.n_compile++;
+        } else {
+            HIPB_CHECK(hipModuleUnload(mod));
+            fn = NULL;
+        }
+    } else {
+        fprintf(stderr, "tinyhvm-hip: batch kernel build failed: %s\n", err);
+    }
+    free(src);
+    return fn;
+}
+
+/* Issues the held dispatches: one alone as itself, several as their batch
+ * kernel (or one by one if it cannot be built). */
+static void hb_flush(void) {
+    if (!HB.n || HB.flushing) return;
+    HB.flushing = 1;
+    if (HB.n == 1) {
+        void *pv[2 * (FUSE_MAX_LEAVES + 1) + 1 + KGEN_MAX_SCALARS];
+        hb_params(&HB.ent[0], pv);
+        hipb_launch(HB.ent[0].fn, HB.ent[0].blocks, 1, 1, 256, pv);
+    } else {
+        u64 key = 0x626174636821ull;
+        u32 total = 0, np = 0;
+        for (u32 i = 0; i < HB.n; i++) {
+            key = hb_mix(hb_mix(key, HB.ent[i].key), HB.ent[i].blocks);
+            total += HB.ent[i].blocks;
+        }
+        hipFunction_t fn = hb_batch_fn(key);
+        if (fn) {
+            void *pv[HB_MAX * (2 * (FUSE_MAX_LEAVES + 1) + 1 + KGEN_MAX_SCALARS)];
+            for (u32 i = 0; i < HB.n; i++) np += hb_params(&HB.ent[i], pv + np);
+            hipb_launch(fn, total, 1, 1, 256, pv);
+            hipb.n_batched += HB.n;
+        } else {
+            for (u32 i = 0; i < HB.n; i++) {
+                void *pv[2 * (FUSE_MAX_LEAVES + 1) + 1 + KGEN_MAX_SCALARS];
+                hb_params(&HB.ent[i], pv);
+                hipb_launch(HB.ent[i].fn, HB.ent[i].blocks, 1, 1, 256, pv);
+            }
+        }
+    }
+    HB.n = 0;
+    HB.flushing = 0;
+}
+
+void hipb_before_stream(void) {
+    if (HB.n && !HB.flushing) hb_flush();
+}
+
+/* Holds a dispatch of a batchable kernel (returns 1), issuing the held ones
+ * first if it touches their memory; 0 when it must be launched now. */
+static int hb_hold(const KCacheEntry *e, u32 gx, u32 gy, u32 nb, void *const *ptrs, const u32 *counts, u32 sm,
+                   const float *sv, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves) {
+    if (!e->bsrc || hipb.no_batch || hipb.noalloc || hipb.sync_each || gy != 1 || gx == 0 || gx > HB_MAX_BLOCKS)
+        return 0;
+    if (nb > FUSE_MAX_LEAVES + 1 || e->n_scal > KGEN_MAX_SCALARS) return 0;
+    HbEnt h;
+    h.w_lo = (u64)(uintptr_t)ptrs[0];
+    h.w_hi = h.w_lo + pool_bytes(out_buf);
+    h.nr = 0;
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) {
+        void *lp = pool_ptr(leaf_bufs[i]);
+        if (!lp) continue;
+        h.r_lo[h.nr] = (u64)(uintptr_t)lp;
+        h.r_hi[h.nr] = h.r_lo[h.nr] + pool_bytes(leaf_bufs[i]);
+        h.nr++;
+    }
+    int clash = HB.n >= HB_MAX;
+    for (u32 i = 0; i < HB.n && !clash; i++) {
+        const HbEnt *o = &HB.ent[i];
+        if (hb_overlap(h.w_lo, h.w_hi, o->w_lo, o->w_hi)) clash = 1;
+        for (u32 r = 0; r < o->nr && !clash; r++)
+            if (hb_overlap(h.w_lo, h.w_hi, o->r_lo[r], o->r_hi[r])) clash = 1;
+        for (u32 r = 0; r < h.nr && !clash; r++)
+            if (hb_overlap(h.r_lo[r], h.r_hi[r], o->w_lo, o->w_hi)) clash = 1;
+    }
+    if (clash) hb_flush();
+    h.fn = e->fn;
+    h.key = e->key;
+    h.name = e->name;
+    h.bsrc = e->bsrc;
+    h.bparams = e->bparams;
+    h.blocks = gx;
+    h.nb = nb;
+    h.n_scal = e->n_scal;
+    for (u32 b = 0; b < nb; b++) {
+        h.ptrs[b] = ptrs[b];
+        h.counts[b] = counts[b];
+    }
+    h.sm = sm;
+    for (u32 j = 0; j < e->n_scal; j++) h.sv[j] = sv[j];
+    HB.ent[HB.n++] = h;
+    return 1;
+}
+
+static void hb_release(void) {
+    HB.n = 0;
+    for (u32 i = 0; i < HB.ncache; i++) HIPB_CHECK(hipModuleUnload(HB.cache[i].mod));
+    HB.ncache = 0;
+}
+
 static int env_flag(const char *name) {
     const char *v = getenv(name);
     return v && v[0] && strcmp(v, "0") != 0;
@@ -111,6 +324,7 @@ static void read_dense_env(void) {
 u32 hipb_resident_waves(void) { return hipb.resident_waves ? hipb.resident_waves : 256u * SINGLE_PASS_WAVES_PER_CU; }
 
 hipError_t hipb_stream_wait(void) {
+    hipb_before_stream();
     hipb.n_stream_sync++;
     return hipStreamSynchronize(hipb.stream);
 }
@@ -156,6 +370,7 @@ static int hb_init(void) {
     }
     if (hipStreamCreateWithFlags(&hipb.stream, hipStreamNonBlocking) != hipSuccess) return -1;
     hipb.sync_each = env_flag("THVM_HIP_SYNC");
+    hipb.no_batch = env_flag("THVM_HIP_NO_BATCH");
     hipb.dump_src = env_flag("THVM_HIP_DUMP");
     hipb.no_dense = env_flag("THVM_HIP_NO_DENSE");
     hipb.no_window = env_flag("THVM_HIP_NO_WINDOW");
@@ -198,6 +413,7 @@ static void hb_shutdown(void) {
     graphs_release_all();
     dense_shutdown();
     window_shutdown();
+    hb_release();
     rtc_shutdown();
     scratch_release(&red_ws);
     pool_block_put(hipb.comb_slots, (u64)COMB_SLOTS * 8);
@@ -218,7 +434,7 @@ static void hb_buf_read(u32 id, void *out, u64 bytes) { copyq_guard(id); pool_re
 static void hb_buf_read_nosync(u32 id, void *out, u64 bytes) { copyq_guard(id); pool_read(id, out, bytes, 1); }
 static void hb_mem_checkpoint(u32 *ids, u32 n) { (void)ids; (void)n; }
 static void hb_buf_mark_use(u32 id) { (void)id; }
-static void hb_pool_reset(u32 keep) { copyq_flush(); pool_reset(keep); }
+static void hb_pool_reset(u32 keep) { copyq_flush(); hipb_before_stream(); pool_reset(keep); }
 static void hb_pool_set_persistent(u32 max_buf) { pool_set_persistent(max_buf); }
 static void hb_begin_batch(void) {}
 static void hb_end_batch(void) {}
@@ -232,6 +448,7 @@ static u32 elem_count(u32 id, u32 dt) {
 }
 
 int hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params) {
+    hipb_before_stream();
     hipError_t e = hipModuleLaunchKernel(fn, gx, gy, gz, bx, 1, 1, 0, hipb.stream, params, NULL);
     if (e != hipSuccess) {
         fprintf(stderr, "tinyhvm-hip: launch failed: %s\n", hipGetErrorString(e));
@@ -440,7 +657,8 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     }
     if (e->mode == KG_MODE_GROUP) grid_for(e->total, e->block, &gx, &gy);
     else grid_for((e->n_threads + e->block - 1) / e->block, e->block, &gx, &gy);
-    hipb_launch(e->fn, gx, gy, 1, e->block, params);
+    if (e->mode != KG_MODE_SERIAL || !hb_hold(e, gx, gy, nb, ptrs, counts, sm, sv, out_buf, leaf_bufs, n_leaves))
+        hipb_launch(e->fn, gx, gy, 1, e->block, params);
     pool_mark_device_write(out_buf);
 }
 
@@ -819,10 +1037,10 @@ int thvm_hip_counters(u64 *out, u32 n) {
     u32 pinned = 0, limbo = 0;
     pool_stats(&live, &cached, &mallocs);
     pool_pin_stats(&pinned, &limbo);
-    u64 v[11] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
-                 hipb.n_stream_sync, live, mallocs, pinned, limbo, hipb.n_window};
-    for (u32 i = 0; out && i < n && i < 11; i++) out[i] = v[i];
-    return 11;
+    u64 v[12] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
+                 hipb.n_stream_sync, live, mallocs, pinned, limbo, hipb.n_window, hipb.n_batched};
+    for (u32 i = 0; out && i < n && i < 12; i++) out[i] = v[i];
+    return 12;
 }
 
 int thvm_hip_synchronize(void) {
@@ -1021,6 +1239,7 @@ int thvm_hip_graph_begin(void) {
         free(g);
         return -1;
     }
+    hipb_before_stream();
     if (hipStreamBeginCapture(hipb.stream, hipStreamCaptureModeRelaxed) != hipSuccess) {
         (void)hipGetLastError();
         HIPB_CHECK(hipHostFree(g->arena));
@@ -1037,6 +1256,7 @@ int thvm_hip_graph_begin(void) {
 void *thvm_hip_graph_end(void) {
     if (!hipb.capturing || !g_capture) return NULL;
     copyq_flush();
+    hipb_before_stream();
     HipbGraph *g = g_capture;
     g_capture = NULL;
     hipError_t e = hipStreamEndCapture(hipb.stream, &g->graph);
@@ -1066,6 +1286,7 @@ int thvm_hip_graph_launch(void *handle) {
     /* host writes since the capture reach the buffers the graph reads, and
      * the host's copies of whatever it writes are no longer current */
     pool_device_wrote_all();
+    hipb_before_stream();
     hipError_t e = hipGraphLaunch(g->exec, hipb.stream);
     if (e != hipSuccess) {
         fprintf(stderr, "tinyhvm-hip: graph launch failed: %s\n", hipGetErrorString(e));

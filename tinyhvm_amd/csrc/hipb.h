@@ -65,6 +65,8 @@ typedef struct {
     u64 n_dispatch, n_compile, n_cache_hit, n_dense;
     u64 n_fallback;          /* dispatches run on the KOp interpreter */
     u64 n_window;            /* dispatches run on the window-max and run-sum kernels */
+    u64 n_batched;           /* dispatches issued inside a batched launch */
+    int no_batch;            /* THVM_HIP_NO_BATCH: launch every dispatch on its own */
     u64 n_stream_sync;       /* host waits on the stream (buf_read, synchronize, ...) */
     hipModule_t static_mod;  /* precompiled kernels */
     unsigned long long *comb_slots; /* single-pass combines: partial words (cleared after each use) */
@@ -96,6 +98,9 @@ void pool_pins_release(PoolPins *pins);
 void pool_pin_stats(u32 *pinned, u32 *limbo);
 /* hipStreamSynchronize on the backend's stream, counted */
 hipError_t hipb_stream_wait(void);
+/* Issues the dispatches held for a batched launch; every operation put on
+ * the stream calls it first, so the stream sees work in program order. */
+void hipb_before_stream(void);
 typedef struct {
     void *ptr;        /* device pointer, NULL if free */
     u64 bytes;        /* requested bytes */
@@ -189,6 +194,11 @@ typedef struct {
     u32 n_ops, n_leaves;
     KOp *ops;             /* copy for collision checks */
     u32 meta[5 + FUSE_MAX_LEAVES]; /* grid, local_size, out_dtype, leaf dtypes */
+    char name[32];        /* the kernel's symbol */
+    /* a serial 256-lane kernel also as a device function <name>_b(u32 bk_,
+     * params), its workgroup index an argument, for launches that batch
+     * several independent dispatches (NULL: not batchable) */
+    char *bsrc, *bparams;
 } KCacheEntry;
 
 int  rtc_init(void);

@@ -92,6 +92,8 @@ void rtc_shutdown(void) {
             if (R.tab[i].key) {
                 HIPB_CHECK(hipModuleUnload(R.tab[i].mod));
                 free(R.tab[i].ops);
+                free(R.tab[i].bsrc);
+                free(R.tab[i].bparams);
             }
         }
         free(R.tab);
@@ -207,6 +209,43 @@ int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t er
     return 1;
 }
 
+/* The batch form of a serial 256-lane kernel (see KCacheEntry): its
+ * parameter list, and its text with the entry line made a device function
+ * that takes the workgroup index as bk_. Only when the kernel reads its
+ * workgroup index in the one place the generator emits it. */
+static void make_batch_form(KCacheEntry *e, const char *src, const char *name) {
+    char head[96];
+    snprintf(head, sizeof head, "extern \"C\" __global__ __launch_bounds__(256) void %s(", name);
+    const char *h = strstr(src, head);
+    if (!h) return;
+    const char *ps = h + strlen(head);
+    const char *pe = strstr(ps, ") {\n");
+    if (!pe) return;
+    static const char tpat[] = "((unsigned long long)blockIdx.y * gridDim.x + blockIdx.x)";
+    const char *t = strstr(pe, tpat);
+    if (!t || strstr(t + strlen(tpat), "blockIdx") || strstr(t + strlen(tpat), "gridDim") ||
+        strstr(pe, "__shared__") || strstr(pe, "__syncthreads"))
+        return;
+    size_t np = (size_t)(pe - ps), nb1 = (size_t)(t - (pe + 4)), nrest = strlen(t + strlen(tpat));
+    char *params = malloc(np + 1);
+    size_t cap = strlen(name) + np + nb1 + nrest + 128;
+    char *b = malloc(cap);
+    if (!params || !b) {
+        free(params);
+        free(b);
+        return;
+    }
+    memcpy(params, ps, np);
+    params[np] = 0;
+    int w = snprintf(b, cap, "__device__ __forceinline__ void %s_b(u32 bk_, %s) {\n", name, params);
+    memcpy(b + w, pe + 4, nb1);
+    w += (int)nb1;
+    w += snprintf(b + w, cap - (size_t)w, "((unsigned long long)bk_)");
+    memcpy(b + w, t + strlen(tpat), nrest + 1);
+    e->bparams = params;
+    e->bsrc = b;
+}
+
 KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
     char err[256] = {0};
     KGenResult g;
@@ -265,6 +304,9 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
     program_meta(k, e->meta);
     e->ops = malloc((size_t)k->n_ops * sizeof(KOp));
     if (e->ops) memcpy(e->ops, k->ops, (size_t)k->n_ops * sizeof(KOp));
+    snprintf(e->name, sizeof e->name, "%s", g.name);
+    e->bsrc = e->bparams = NULL;
+    if (g.mode == KG_MODE_SERIAL && g.splits <= 1 && g.block == 256) make_batch_form(e, g.src, g.name);
     hipb.n_compile++;
     kgen_free(&g);
     return e;
