@@ -51,6 +51,7 @@
 #define WIN_SUM_TARGET_WG 1024   /* workgroups to aim for in all (256 lanes each: all resident at once) */
 #define WIN_SUM_MIN_CHUNK 512    /* vectors per workgroup, at least */
 #define WIN_SUM_MAX_OUTPUTS 256  /* run sums: few outputs (more take the generated group kernels) */
+#define WIN_SUM_MAX_FIXED 16     /* run sums: vectors per lane up to which all loads are issued at once */
 #define WIN_MAX_LOADS 16
 #define WIN_BLOCK 256u
 
@@ -480,7 +481,18 @@ static char *gen_run_sum(const UOpKernel *k, const WinPlan *p, const char *name)
     for (u32 v = 0; v < W; v++) wsb_put(&s, "  float q%u_ = 0.0f;\n", v);
     wsb_put(&s, "  const u32 ulo_ = sp_ * %uu, uhi_ = (ulo_ + %uu < %uu) ? ulo_ + %uu : %uu;\n", chunk, chunk, units,
             chunk, units);
-    wsb_put(&s, "  #pragma unroll %u\n  for (u32 u_ = ulo_ + lane; u_ < uhi_; u_ += %uu) {\n", p->unroll, WIN_BLOCK);
+    /* a lane's vectors: a fixed count when it is small, every load of the
+     * lane then in flight at once (the last ones past the chunk read its
+     * first vector and add nothing); else a loop */
+    const u32 nit = (chunk + WIN_BLOCK - 1) / WIN_BLOCK;
+    const int fixed = nit <= WIN_SUM_MAX_FIXED;
+    if (fixed) {
+        wsb_put(&s, "  #pragma unroll\n  for (u32 i_ = 0; i_ < %uu; i_++) {\n", nit);
+        wsb_put(&s, "    const u32 uu_ = ulo_ + lane + i_ * %uu;\n    const bool ok_ = uu_ < uhi_;\n"
+                    "    const u32 u_ = ok_ ? uu_ : ulo_;\n", WIN_BLOCK);
+    } else {
+        wsb_put(&s, "  #pragma unroll %u\n  for (u32 u_ = ulo_ + lane; u_ < uhi_; u_ += %uu) {\n", p->unroll, WIN_BLOCK);
+    }
     wsb_put(&s, "    const u32 s_ = u_ / %uu, j_ = u_ - s_ * %uu;\n", L4, L4);
     wsb_put(&s, "    const u32 o_ = j_ * %uu", W);
     for (u32 q = 0; q < p->n_outer; q++) {
@@ -510,7 +522,8 @@ static char *gen_run_sum(const UOpKernel *k, const WinPlan *p, const char *name)
         }
         for (u32 v = 0; v < W; v++) emit_body_op(&s, k, p, i, v);
     }
-    for (u32 v = 0; v < W; v++) wsb_put(&s, "    q%u_ = q%u_ + f%u_%u;\n", v, v, p->value, v);
+    for (u32 v = 0; v < W; v++)
+        wsb_put(&s, fixed ? "    q%u_ = q%u_ + (ok_ ? f%u_%u : 0.0f);\n" : "    q%u_ = q%u_ + f%u_%u;\n", v, v, p->value, v);
     wsb_put(&s, "  }\n");
     if (W == 4) wsb_put(&s, "  float t_ = (q0_ + q1_) + (q2_ + q3_);\n");
     else wsb_put(&s, "  float t_ = q0_;\n");
