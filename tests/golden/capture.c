@@ -3,7 +3,7 @@
  * each benchmark workload, as kernel traces (include/thvm_trace.h).
  *
  * Built only in the development container, from the engine sources where
- * they lie (see oracle/ref.mk): this file includes src/tinyhvm.c and the
+ * they lie (oracle/Makefile, target `ref`): this file includes src/tinyhvm.c and the
  * engine's CPU backend (src/backend/cpu/_.c), wraps every slot of the
  * cpu_backend vtable with a recorder that forwards to the original, and
  * drives the engine's public tensor API (src/tinyhvm.h:1287-1544).
