@@ -194,6 +194,16 @@ int  thvm_hip_window_source(const UOpKernel *kernel, char *buf, u64 buflen);
 /* Generate and compile it without loading; the code-object size, or -1. */
 int  thvm_hip_window_compile_check(const UOpKernel *kernel, char *errbuf, u64 errlen);
 
+/* Independent dispatches held back and issued as one launch: the batch
+ * kernel of n generated modules (srcs[i] as the generators above return it,
+ * names[i] its main kernel, threads[i] its workgroup size, grid[2i], grid[2i+1]
+ * its grid), compiled without loading (no device needed). Returns the
+ * code-object size, or -1 with the reason in errbuf. A diagnostic with no
+ * counterpart in the reference: it checks the generated modules' device-
+ * function forms that batched launches compile. */
+int  thvm_hip_batch_compile_check(const char *const *srcs, const char *const *names, const u32 *threads,
+                                  const u32 *grid, u32 n, char *errbuf, u64 errlen);
+
 #ifdef __cplusplus
 }
 #endif

@@ -28,6 +28,7 @@ hipError_t hipb_stream_wait(void) {
 }
 /* the backend's held dispatches (none here: the pool alone is under test) */
 void hipb_before_stream(void) {}
+void hipb_before_copy(const void *dst, u64 bytes) { (void)dst; (void)bytes; }
 
 extern size_t fake_hip_limit, fake_hip_live;
 extern unsigned long fake_hip_mallocs, fake_hip_frees;

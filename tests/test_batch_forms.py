@@ -1,0 +1,51 @@
+"""Device-function forms of the generated modules (no device needed).
+
+Independent dispatches are held back and issued as one launch of a batch
+kernel that calls each generated module's kernels as device functions on
+their own workgroup ranges. Every distinct kernel of the LeNet-5 and conv-block
+traces (generated elementwise and reduction kernels, matrix-core contractions,
+window max and run sums) is put into batch kernels of eight, which must
+compile for gfx950; a module the form cannot take (none of these) would be
+launched on its own instead.
+"""
+import os
+import re
+
+import pytest
+
+from tinyhvm_amd import _lib, trace
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+WL = os.path.join(ROOT, "tinyhvm_amd", "workloads")
+MAIN = re.compile(r'extern "C" __global__ __launch_bounds__\((\d+)\) void (\w+)\(')
+
+
+def _modules(name):
+    out, seen = [], set()
+    for r in trace.read_trace(os.path.join(WL, name)):
+        if r.tag != trace.UOP:
+            continue
+        k = trace.to_uop_kernel(r)
+        if _lib.dense_analyze(k):
+            src = _lib.dense_source(k)
+        elif _lib.window_analyze(k):
+            src = _lib.window_source(k)
+        else:
+            src = _lib.kernel_source(k)[0]
+        mains = [(int(t), n) for t, n in MAIN.findall(src) if not n.endswith(("_sum", "_fin", "_pack"))]
+        assert mains, src[:2000]
+        threads, kname = mains[0]
+        if kname in seen:
+            continue
+        seen.add(kname)
+        out.append((src, kname, threads, 3, 1))
+    return out
+
+
+@pytest.mark.parametrize("name", ["lenet_b256.trc", "convblock_b64.trc"])
+def test_generated_modules_compile_as_batches(name):
+    mods = _modules(name)
+    assert len(mods) >= 10
+    for i in range(0, len(mods), 8):
+        group = mods[i:i + 8]
+        assert _lib.batch_compile_check(group) > 0, [g[1] for g in group]

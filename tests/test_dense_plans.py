@@ -50,6 +50,7 @@ def _plans(name):
             "skinny_waves": int(kw.group(1)) if kw else None,
             "skinny_block": int(ke.group(1)) if ke else None,
             "outer": (int(ro.group(1)), int(ro.group(2))) if ro else None,
+            "comb": "comb_pub(sl_" in src,
         }
     return out
 
@@ -89,10 +90,11 @@ def test_lenet_few_channel_convolutions_are_skinny():
 def test_lenet_convolution_weight_gradients_are_outer_product_reductions():
     # conv1 dW (25x6 over 200704 pixels) and conv2 dW (150x16 over 25600):
     # a k per lane, row groups of at most 96 / N rows, K chunks of at least
-    # 8 k per lane, partials through the split-K sum
+    # 8 k per lane; conv2's 12 splits combined in the same launch, conv1's 98
+    # through the split-K sum kernel
     p = _plans("lenet_b256.trc")
-    assert p[(25, 6, 200704, 98)]["outer"] == (13, 2048)
-    assert p[(150, 16, 25600, 12)]["outer"] == (6, 2134)
+    assert p[(25, 6, 200704, 98)]["outer"] == (13, 2048) and not p[(25, 6, 200704, 98)]["comb"]
+    assert p[(150, 16, 25600, 12)]["outer"] == (6, 2134) and p[(150, 16, 25600, 12)]["comb"]
 
 
 def test_lenet_fc_weight_gradients_use_eight_waves():

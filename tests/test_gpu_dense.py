@@ -21,10 +21,13 @@ pytestmark = pytest.mark.gpu
 # 3 = 256x32, 4 = 32x256, 5 = direct (per-wave 32x32 blocks, no LDS), 6 = 256x64,
 # 7 = 128x64, 8 = skinny (a row per lane, for at most 16 columns; wider
 # contractions keep the chosen tile), 9 = outer-product reduction (a k per
-# lane, for few outputs; others keep the chosen tile)
+# lane, for few outputs; others keep the chosen tile). The direct and
+# outer-product kernels combine their split-K partials in the same launch;
+# "nocomb" sends them through the workspace and the sum kernel instead.
 CONFIGS = [("1", "0"), ("2", "0"), ("1", "1"), ("3", "2"), ("1", "3"), ("2", "4"), ("1", "5"), ("3", "5"),
            ("1", "6"), ("3", "6"), ("1", "7"), ("2", "7"), ("8", "2"), ("16", "7"), ("1", "2", "pack"),
-           ("2", "7", "pack"), ("1", "8"), ("1", "8", "noskblk"), ("1", "9")]
+           ("2", "7", "pack"), ("1", "8"), ("1", "8", "noskblk"), ("1", "9"), ("8", "5"), ("3", "5", "nocomb"),
+           ("1", "9", "nocomb")]
 
 
 @pytest.fixture(scope="module", params=CONFIGS,
@@ -32,14 +35,16 @@ CONFIGS = [("1", "0"), ("2", "0"), ("1", "1"), ("3", "2"), ("1", "3"), ("2", "4"
                      "tile32x256-split2", "direct", "direct-split3", "tile256x64", "tile256x64-split3",
                      "tile128x64", "tile128x64-split2", "tile64x64-split8", "tile128x64-split16",
                      "tile64x64-packed", "tile128x64-split2-packed", "skinny", "skinny-per-k",
-                     "outer-product"])
+                     "outer-product", "direct-split8", "direct-split3-sum-kernel", "outer-product-sum-kernel"])
 def hip_dense(request):
     saved = {k: os.environ.get(k) for k in ("THVM_HIP_DENSE_FORCE", "THVM_HIP_DENSE_SPLITS",
-                                             "THVM_HIP_DENSE_TILE", "THVM_HIP_DENSE_PACK", "THVM_HIP_DENSE_NOSKBLK")}
+                                             "THVM_HIP_DENSE_TILE", "THVM_HIP_DENSE_PACK", "THVM_HIP_DENSE_NOSKBLK",
+                                             "THVM_HIP_DENSE_NOCOMB")}
     os.environ["THVM_HIP_DENSE_FORCE"] = "1"
     os.environ["THVM_HIP_DENSE_SPLITS"], os.environ["THVM_HIP_DENSE_TILE"] = request.param[:2]
     os.environ["THVM_HIP_DENSE_PACK"] = "1" if request.param[2:] == ("pack",) else "0"
     os.environ["THVM_HIP_DENSE_NOSKBLK"] = "1" if request.param[2:] == ("noskblk",) else "0"
+    os.environ["THVM_HIP_DENSE_NOCOMB"] = "1" if request.param[2:] == ("nocomb",) else "0"
     L = _lib.lib()
     assert L.thvm_hip_init() == 0
     yield L

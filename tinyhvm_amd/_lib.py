@@ -73,6 +73,8 @@ def lib():
         "thvm_hip_window_analyze": (C.c_int, [C.POINTER(abi.UOpKernel), PU32, PU32]),
         "thvm_hip_window_source": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
         "thvm_hip_window_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
+        "thvm_hip_batch_compile_check": (C.c_int, [C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), PU32, PU32, u32,
+                                                   cp, u64]),
         "thvm_trace_load": (vp, [cp]),
         "thvm_trace_free": (None, [vp]),
         "thvm_trace_count": (u32, [vp]),
@@ -108,6 +110,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_kernel_lanes", "thvm_hip_compile_check",
     "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
     "thvm_hip_window_analyze", "thvm_hip_window_source", "thvm_hip_window_compile_check",
+    "thvm_hip_batch_compile_check",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
     "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",
@@ -130,6 +133,22 @@ def kernel_source(k: abi.UOpKernel):
     if n < 0:
         raise ValueError(text)
     return text, mode.value, vec.value
+
+
+def batch_compile_check(items):
+    """Compile the batch kernel of generated modules without a device; items
+    are (source, main kernel name, workgroup size, gx, gy). Returns the
+    code-object size; raises ValueError with the compiler's reason."""
+    n = len(items)
+    srcs = (C.c_char_p * n)(*[it[0].encode() for it in items])
+    names = (C.c_char_p * n)(*[it[1].encode() for it in items])
+    threads = (C.c_uint32 * n)(*[it[2] for it in items])
+    grid = (C.c_uint32 * (2 * n))(*[v for it in items for v in (it[3], it[4])])
+    err = C.create_string_buffer(4096)
+    r = lib().thvm_hip_batch_compile_check(srcs, names, threads, grid, n, err, len(err))
+    if r < 0:
+        raise ValueError(err.value.decode())
+    return r
 
 
 def dense_analyze(k: abi.UOpKernel):

@@ -71,35 +71,40 @@ static void copyq_guard_dispatch(u32 out, const u32 *leaves, u32 n) {
     for (u32 i = 0; i < n && CQ.b.n; i++) copyq_guard(leaves[i]);
 }
 
-/* Batched launches. Small serial generated kernels (at most HB_MAX_BLOCKS
- * workgroups of 256 lanes) are held back instead of launched; while the next
- * dispatches are such kernels too and touch no memory a held one writes (and
- * write none a held one reads), they join it. The held dispatches then go out
- * as one launch of a kernel that calls each one's device function on its own
- * range of workgroups (compiled once per sequence of programs and grid
- * sizes). The ten SGD updates of a LeNet-5 step are one launch. Any other
- * work put on the stream issues the held dispatches first
- * (hipb_before_stream), so the stream still sees everything in program
- * order; dispatches in one batch are independent by construction. */
+/* Batched launches (co-launch). A generated kernel's launch of at most
+ * HB_MAX_BLOCKS workgroups is held back instead of issued; while the next
+ * dispatches are such launches too and touch no memory a held one writes
+ * (and write none a held one reads), they join it. The held launches then go
+ * out as one launch of a batch kernel that hands each one its own range of
+ * workgroups and calls its module's device function (CoForm) with its own
+ * block coordinates, so that independent kernels of a step run side by side
+ * instead of one after another: a layer's weight, bias and input gradients,
+ * a step's SGD updates. The batch kernel is compiled once per sequence of
+ * programs and grid sizes. Any other work put on the stream issues the held
+ * launches first (hipb_before_stream), so the stream still sees everything in
+ * program order; launches in one batch are independent by construction.
+ * A batch's workgroups have the largest size among its programs (a smaller
+ * program's surplus waves end at once; a wave that has ended no longer takes
+ * part in the workgroup's barriers). The batch kernel holds every program's
+ * static LDS, at most HB_MAX_LDS in all; a batch with a program whose
+ * workgroups wait for each other fits on the GPU at once, and each program
+ * that combines partials through the combine area has its own slice of it. */
 #define HB_MAX 16
-#define HB_MAX_BLOCKS 64
+#define HB_MAX_BLOCKS 512
+#define HB_MAX_LDS 65536u
+#define HB_ARG_BYTES (CO_MAX_PARAMS * 8)
 typedef struct {
+    CoForm co;             /* a copy (its strings live until shutdown) */
     hipFunction_t fn;
-    u64 key;
-    const char *name, *bsrc, *bparams;
-    u32 blocks;
-    u32 nb, n_scal;
-    void *ptrs[FUSE_MAX_LEAVES + 1];
-    u32 counts[FUSE_MAX_LEAVES + 1];
-    u32 sm;
-    float sv[KGEN_MAX_SCALARS];
-    u64 w_lo, w_hi;
-    u32 nr;
-    u64 r_lo[FUSE_MAX_LEAVES], r_hi[FUSE_MAX_LEAVES];
+    u32 gx, gy;
+    u8 args[HB_ARG_BYTES];
+    HbMem m;
+    int resident;
 } HbEnt;
 static struct {
     HbEnt ent[HB_MAX];
     u32 n;
+    u64 comb_used;         /* combine-area words given to the held launches */
     int flushing;
     struct { u64 key; hipModule_t mod; hipFunction_t fn; } cache[64];
     u32 ncache;
@@ -107,16 +112,40 @@ static struct {
 
 static int hb_overlap(u64 a0, u64 a1, u64 b0, u64 b1) { return a0 < b1 && b0 < a1; }
 
-/* the launch parameters of one held dispatch, in its kernel's order */
-static u32 hb_params(HbEnt *h, void **pv) {
-    u32 n = 0;
-    for (u32 b = 0; b < h->nb; b++) pv[n++] = &h->ptrs[b];
-    for (u32 b = 0; b < h->nb; b++) pv[n++] = &h->counts[b];
-    if (h->n_scal) {
-        pv[n++] = &h->sm;
-        for (u32 j = 0; j < h->n_scal; j++) pv[n++] = &h->sv[j];
+void hbm_add(HbMem *m, const void *p, u64 bytes, int write) {
+    if (!p || !bytes) return;
+    if (m->n >= HB_RANGES) {
+        /* out of slots: widen the last range to cover this one too */
+        u64 lo = (u64)(uintptr_t)p, hi = lo + bytes;
+        if (lo < m->lo[m->n - 1]) m->lo[m->n - 1] = lo;
+        if (hi > m->hi[m->n - 1]) m->hi[m->n - 1] = hi;
+        m->wr[m->n - 1] |= (u8)(write != 0);
+        return;
     }
-    return n;
+    m->lo[m->n] = (u64)(uintptr_t)p;
+    m->hi[m->n] = m->lo[m->n] + bytes;
+    m->wr[m->n] = (u8)(write != 0);
+    m->n++;
+}
+
+static int hbm_clash(const HbMem *a, const HbMem *b) {
+    for (u32 i = 0; i < a->n; i++)
+        for (u32 j = 0; j < b->n; j++)
+            if ((a->wr[i] || b->wr[j]) && hb_overlap(a->lo[i], a->hi[i], b->lo[j], b->hi[j])) return 1;
+    return 0;
+}
+
+static u32 hb_arg_off(u32 off, u32 sz) { return (off + sz - 1u) & ~(sz - 1u); }
+
+/* the launch parameters of one held launch, in its kernel's order */
+static u32 hb_params(HbEnt *h, void **pv) {
+    u32 off = 0;
+    for (u32 j = 0; j < h->co.np; j++) {
+        off = hb_arg_off(off, h->co.psz[j]);
+        pv[j] = h->args + off;
+        off += h->co.psz[j];
+    }
+    return h->co.np;
 }
 
 static u64 hb_mix(u64 h, u64 v) {
@@ -125,53 +154,76 @@ static u64 hb_mix(u64 h, u64 v) {
     return h ^ (h >> 33);
 }
 
-/* The batch kernel for the held sequence: each program's device function
- * once, and an entry that hands workgroup ranges to them in order. */
-static hipFunction_t hb_batch_fn(u64 key) {
-    for (u32 i = 0; i < HB.ncache; i++)
-        if (HB.cache[i].key == key) return HB.cache[i].fn;
-    if (HB.ncache >= sizeof HB.cache / sizeof HB.cache[0]) return NULL;
+static u32 hb_threads(void) {
+    u32 t = 0;
+    for (u32 i = 0; i < HB.n; i++) if (HB.ent[i].co.threads > t) t = HB.ent[i].co.threads;
+    return t;
+}
+
+/* appends a parameter list's names (or "type name"s with `decl`), each
+ * prefixed q<i>_ */
+static size_t hb_put_params(char *src, size_t w, size_t cap, const char *params, u32 i, int decl, int first) {
+    const char *p = params;
+    while (*p) {
+        const char *e = strstr(p, ", ");
+        size_t len = e ? (size_t)(e - p) : strlen(p);
+        const char *sp = p + len;
+        while (sp > p && sp[-1] != ' ' && sp[-1] != '*') sp--;
+        w += (size_t)snprintf(src + w, cap - w, "%s%.*sq%u_%.*s", first ? "" : ", ", decl ? (int)(sp - p) : 0, p, i,
+                              (int)(len - (size_t)(sp - p)), sp);
+        first = 0;
+        p = e ? e + 2 : p + len;
+    }
+    return w;
+}
+
+/* Source of the batch kernel `name` for launches ents[0..n) in order, with
+ * T lanes per workgroup: each program's module once, and an entry that hands
+ * workgroup ranges to their device functions. */
+static char *hb_batch_source(const HbEnt *ents, u32 n, u32 T, const char *name) {
     size_t cap = strlen(kgen_prelude()) + 4096;
-    for (u32 i = 0; i < HB.n; i++) cap += strlen(HB.ent[i].bsrc) + 4 * strlen(HB.ent[i].bparams) + 512;
+    for (u32 i = 0; i < n; i++) cap += strlen(ents[i].co.src) + 4 * strlen(ents[i].co.params) + 512;
     char *src = malloc(cap);
     if (!src) return NULL;
     size_t w = (size_t)snprintf(src, cap, "%s\n", kgen_prelude());
-    for (u32 i = 0; i < HB.n; i++) {
+    for (u32 i = 0; i < n; i++) {
         int seen = 0;
-        for (u32 j = 0; j < i; j++) seen |= HB.ent[j].key == HB.ent[i].key;
-        if (!seen) w += (size_t)snprintf(src + w, cap - w, "%s\n", HB.ent[i].bsrc);
+        for (u32 j = 0; j < i; j++) seen |= ents[j].co.id == ents[i].co.id;
+        if (!seen) w += (size_t)snprintf(src + w, cap - w, "%s\n", ents[i].co.src);
     }
-    char name[48];
-    snprintf(name, sizeof name, "thvm_batch_%016llx", (unsigned long long)key);
-    w += (size_t)snprintf(src + w, cap - w, "extern \"C\" __global__ __launch_bounds__(256) void %s(", name);
-    /* parameters: every dispatch's list, each name prefixed q<i>_ */
-    for (u32 i = 0; i < HB.n; i++) {
-        const char *p = HB.ent[i].bparams;
-        while (*p) {
-            const char *e = strstr(p, ", ");
-            size_t len = e ? (size_t)(e - p) : strlen(p);
-            const char *sp = p + len;
-            while (sp > p && sp[-1] != ' ' && sp[-1] != '*') sp--;
-            w += (size_t)snprintf(src + w, cap - w, "%s%.*sq%u_%.*s", (i || p != HB.ent[i].bparams) ? ", " : "",
-                                  (int)(sp - p), p, i, (int)(len - (size_t)(sp - p)), sp);
-            p = e ? e + 2 : p + len;
-        }
-    }
-    w += (size_t)snprintf(src + w, cap - w, ") {\n  u32 b_ = blockIdx.x;\n");
-    for (u32 i = 0; i < HB.n; i++) {
-        w += (size_t)snprintf(src + w, cap - w, "  if (b_ < %uu) { %s_b(b_", HB.ent[i].blocks, HB.ent[i].name);
-        const char *p = HB.ent[i].bparams;
-        while (*p) {
-            const char *e = strstr(p, ", ");
-            size_t len = e ? (size_t)(e - p) : strlen(p);
-            const char *sp = p + len;
-            while (sp > p && sp[-1] != ' ' && sp[-1] != '*') sp--;
-            w += (size_t)snprintf(src + w, cap - w, ", q%u_%.*s", i, (int)(len - (size_t)(sp - p)), sp);
-            p = e ? e + 2 : p + len;
-        }
-        w += (size_t)snprintf(src + w, cap - w, "); return; }\n  b_ -= %uu;\n", HB.ent[i].blocks);
+    w += (size_t)snprintf(src + w, cap - w, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", T, name);
+    for (u32 i = 0; i < n; i++) w = hb_put_params(src, w, cap, ents[i].co.params, i, 1, i == 0);
+    w += (size_t)snprintf(src + w, cap - w,
+                          ") {\n  u32 b_ = blockIdx.x;\n"
+                          "  const u32 wv_ = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n  (void)wv_;\n");
+    for (u32 i = 0; i < n; i++) {
+        const HbEnt *h = &ents[i];
+        w += (size_t)snprintf(src + w, cap - w, "  if (b_ < %uu) {", h->gx * h->gy);
+        if (h->co.threads < T) w += (size_t)snprintf(src + w, cap - w, " if (wv_ >= %uu) return;", h->co.threads / 64u);
+        w += (size_t)snprintf(src + w, cap - w, " co_%u::%s(b_ %% %uu, b_ / %uu, %uu, %uu", h->co.id, h->co.name, h->gx,
+                              h->gx, h->gx, h->gy);
+        w = hb_put_params(src, w, cap, h->co.params, i, 0, 0);
+        w += (size_t)snprintf(src + w, cap - w, "); return; }\n  b_ -= %uu;\n", h->gx * h->gy);
     }
     snprintf(src + w, cap - w, "}\n");
+    return src;
+}
+
+/* The batch kernel for the held sequence (compiled once per key). */
+static hipFunction_t hb_batch_fn(u64 key, u32 T) {
+    for (u32 i = 0; i < HB.ncache; i++)
+        if (HB.cache[i].key == key) return HB.cache[i].fn;
+    if (HB.ncache >= sizeof HB.cache / sizeof HB.cache[0]) return NULL;
+    char name[48];
+    snprintf(name, sizeof name, "thvm_batch_%016llx", (unsigned long long)key);
+    char *src = hb_batch_source(HB.ent, HB.n, T, name);
+    if (!src) return NULL;
+    if (hipb.verbose) {
+        fprintf(stderr, "tinyhvm-hip: %s (%u lanes):", name, T);
+        for (u32 i = 0; i < HB.n; i++)
+            fprintf(stderr, " %s[%ux%u]", HB.ent[i].co.name, HB.ent[i].gx, HB.ent[i].gy);
+        fprintf(stderr, "\n");
+    }
     if (hipb.dump_src) fprintf(stderr, "---- batch kernel ----\n%s\n", src);
     char err[256] = {0};
     hipModule_t mod;
@@ -194,37 +246,68 @@ static hipFunction_t hb_batch_fn(u64 key) {
     return fn;
 }
 
-/* Issues the held dispatches: one alone as itself, several as their batch
+/* Device-free check of the co-launch forms: the batch kernel of n generated
+ * modules (their sources, main kernel names, workgroup sizes and grids as gx,
+ * gy pairs), compiled for gfx950 without loading. Returns the code-object
+ * size, or -1 with the reason in errbuf. */
+int thvm_hip_batch_compile_check(const char *const *srcs, const char *const *names, const u32 *threads,
+                                 const u32 *grid, u32 n, char *errbuf, u64 errlen) {
+    if (!srcs || !names || !threads || !grid || n == 0 || n > HB_MAX || !errbuf || errlen == 0) return -1;
+    HbEnt *ents = calloc(n, sizeof(HbEnt));
+    if (!ents) return -1;
+    u32 T = 0, ok = 1;
+    for (u32 i = 0; i < n && ok; i++) {
+        if (!co_form_make(&ents[i].co, srcs[i], names[i], threads[i], NULL)) {
+            snprintf(errbuf, errlen, "no co-launch form for %s", names[i]);
+            ok = 0;
+            break;
+        }
+        ents[i].gx = grid[2 * i];
+        ents[i].gy = grid[2 * i + 1];
+        if (threads[i] > T) T = threads[i];
+    }
+    long r = -1;
+    char *src = ok ? hb_batch_source(ents, n, T, "thvm_batch_check") : NULL;
+    if (src) r = rtc_compile_only(src, errbuf, (size_t)errlen);
+    free(src);
+    for (u32 i = 0; i < n; i++) co_form_free(&ents[i].co);
+    free(ents);
+    return (int)r;
+}
+
+/* Issues the held launches: one alone as itself, several as their batch
  * kernel (or one by one if it cannot be built). */
 static void hb_flush(void) {
     if (!HB.n || HB.flushing) return;
     HB.flushing = 1;
     if (HB.n == 1) {
-        void *pv[2 * (FUSE_MAX_LEAVES + 1) + 1 + KGEN_MAX_SCALARS];
+        void *pv[CO_MAX_PARAMS];
         hb_params(&HB.ent[0], pv);
-        hipb_launch(HB.ent[0].fn, HB.ent[0].blocks, 1, 1, 256, pv);
+        hipb_launch(HB.ent[0].fn, HB.ent[0].gx, HB.ent[0].gy, 1, HB.ent[0].co.threads, pv);
     } else {
-        u64 key = 0x626174636821ull;
+        const u32 T = hb_threads();
+        u64 key = hb_mix(0x626174636822ull, T);
         u32 total = 0, np = 0;
         for (u32 i = 0; i < HB.n; i++) {
-            key = hb_mix(hb_mix(key, HB.ent[i].key), HB.ent[i].blocks);
-            total += HB.ent[i].blocks;
+            key = hb_mix(hb_mix(hb_mix(key, HB.ent[i].co.id), HB.ent[i].gx), HB.ent[i].gy);
+            total += HB.ent[i].gx * HB.ent[i].gy;
         }
-        hipFunction_t fn = hb_batch_fn(key);
+        hipFunction_t fn = hb_batch_fn(key, T);
         if (fn) {
-            void *pv[HB_MAX * (2 * (FUSE_MAX_LEAVES + 1) + 1 + KGEN_MAX_SCALARS)];
+            void *pv[HB_MAX * CO_MAX_PARAMS];
             for (u32 i = 0; i < HB.n; i++) np += hb_params(&HB.ent[i], pv + np);
-            hipb_launch(fn, total, 1, 1, 256, pv);
+            hipb_launch(fn, total, 1, 1, T, pv);
             hipb.n_batched += HB.n;
         } else {
             for (u32 i = 0; i < HB.n; i++) {
-                void *pv[2 * (FUSE_MAX_LEAVES + 1) + 1 + KGEN_MAX_SCALARS];
+                void *pv[CO_MAX_PARAMS];
                 hb_params(&HB.ent[i], pv);
-                hipb_launch(HB.ent[i].fn, HB.ent[i].blocks, 1, 1, 256, pv);
+                hipb_launch(HB.ent[i].fn, HB.ent[i].gx, HB.ent[i].gy, 1, HB.ent[i].co.threads, pv);
             }
         }
     }
     HB.n = 0;
+    HB.comb_used = 0;
     HB.flushing = 0;
 }
 
@@ -232,49 +315,76 @@ void hipb_before_stream(void) {
     if (HB.n && !HB.flushing) hb_flush();
 }
 
-/* Holds a dispatch of a batchable kernel (returns 1), issuing the held ones
- * first if it touches their memory; 0 when it must be launched now. */
-static int hb_hold(const KCacheEntry *e, u32 gx, u32 gy, u32 nb, void *const *ptrs, const u32 *counts, u32 sm,
-                   const float *sv, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves) {
-    if (!e->bsrc || hipb.no_batch || hipb.noalloc || hipb.sync_each || gy != 1 || gx == 0 || gx > HB_MAX_BLOCKS)
-        return 0;
-    if (nb > FUSE_MAX_LEAVES + 1 || e->n_scal > KGEN_MAX_SCALARS) return 0;
-    HbEnt h;
-    h.w_lo = (u64)(uintptr_t)ptrs[0];
-    h.w_hi = h.w_lo + pool_bytes(out_buf);
-    h.nr = 0;
-    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) {
-        void *lp = pool_ptr(leaf_bufs[i]);
-        if (!lp) continue;
-        h.r_lo[h.nr] = (u64)(uintptr_t)lp;
-        h.r_hi[h.nr] = h.r_lo[h.nr] + pool_bytes(leaf_bufs[i]);
-        h.nr++;
-    }
-    int clash = HB.n >= HB_MAX;
-    for (u32 i = 0; i < HB.n && !clash; i++) {
+void hipb_before_copy(const void *dst, u64 bytes) {
+    if (!HB.n || HB.flushing) return;
+    HbMem m;
+    m.n = 0;
+    hbm_add(&m, dst, bytes, 1);
+    for (u32 i = 0; i < HB.n; i++)
+        if (hbm_clash(&m, &HB.ent[i].m)) {
+            hb_flush();
+            return;
+        }
+}
+
+/* why h cannot join the held launches as they are (NULL: it can) */
+static const char *hb_joins(const HbEnt *h) {
+    if (HB.n >= HB_MAX) return "batch full";
+    u32 T = h->co.threads, lds = h->co.lds, blocks = h->gx * h->gy;
+    int resident = h->resident;
+    for (u32 i = 0; i < HB.n; i++) {
         const HbEnt *o = &HB.ent[i];
-        if (hb_overlap(h.w_lo, h.w_hi, o->w_lo, o->w_hi)) clash = 1;
-        for (u32 r = 0; r < o->nr && !clash; r++)
-            if (hb_overlap(h.w_lo, h.w_hi, o->r_lo[r], o->r_hi[r])) clash = 1;
-        for (u32 r = 0; r < h.nr && !clash; r++)
-            if (hb_overlap(h.r_lo[r], h.r_hi[r], o->w_lo, o->w_hi)) clash = 1;
+        if (hbm_clash(&h->m, &o->m)) return "memory";
+        if (o->co.threads > T) T = o->co.threads;
+        lds += o->co.lds;
+        blocks += o->gx * o->gy;
+        resident |= o->resident;
     }
-    if (clash) hb_flush();
-    h.fn = e->fn;
-    h.key = e->key;
-    h.name = e->name;
-    h.bsrc = e->bsrc;
-    h.bparams = e->bparams;
-    h.blocks = gx;
-    h.nb = nb;
-    h.n_scal = e->n_scal;
-    for (u32 b = 0; b < nb; b++) {
-        h.ptrs[b] = ptrs[b];
-        h.counts[b] = counts[b];
+    if (lds > HB_MAX_LDS) return "LDS";
+    if (resident && (u64)blocks * (T / 64u) > hipb_resident_waves()) return "residency";
+    return NULL;
+}
+
+int hipb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
+              int resident, int comb_param, u64 comb_words) {
+    if (!cf || !cf->src || hipb.no_batch || hipb.noalloc || hipb.sync_each || HB.flushing) return 0;
+    if (gx == 0 || gy == 0 || (u64)gx * gy > HB_MAX_BLOCKS || cf->threads == 0 || cf->threads % 64u ||
+        cf->threads > 1024u || comb_words > COMB_SLOTS || (comb_param >= 0 && ((u32)comb_param >= cf->np ||
+        cf->psz[comb_param] != 8)))
+        return 0;
+    HbEnt tmp, *h = &tmp;
+    h->co = *cf;
+    h->fn = fn;
+    h->gx = gx;
+    h->gy = gy;
+    h->m = *m;
+    h->resident = resident;
+    u32 off = 0;
+    for (u32 j = 0; j < cf->np; j++) {
+        off = hb_arg_off(off, cf->psz[j]);
+        if (off + cf->psz[j] > HB_ARG_BYTES) return 0;
+        memcpy(h->args + off, params[j], cf->psz[j]);
+        off += cf->psz[j];
     }
-    h.sm = sm;
-    for (u32 j = 0; j < e->n_scal; j++) h.sv[j] = sv[j];
-    HB.ent[HB.n++] = h;
+    const char *why = hb_joins(h);
+    if (!why && HB.comb_used + comb_words > COMB_SLOTS) why = "combine area";
+    if (why) {
+        if (hipb.verbose && HB.n)
+            fprintf(stderr, "tinyhvm-hip: %s does not join %u held launches: %s\n", cf->name, HB.n, why);
+        hb_flush();
+    }
+    if (comb_param >= 0) {
+        /* its own slice of the combine area: after the held launches' slices */
+        u32 o = 0;
+        for (u32 j = 0; j < (u32)comb_param; j++) o = hb_arg_off(o, cf->psz[j]) + cf->psz[j];
+        o = hb_arg_off(o, 8);
+        unsigned long long *base;
+        memcpy(&base, h->args + o, 8);
+        base += HB.comb_used;
+        memcpy(h->args + o, &base, 8);
+        HB.comb_used += comb_words;
+    }
+    HB.ent[HB.n++] = *h;
     return 1;
 }
 
@@ -301,6 +411,7 @@ static void read_dense_env(void) {
     hipb.dense_noskinny = env_flag("THVM_HIP_DENSE_NOSKINNY");
     hipb.dense_noskinny_blocks = env_flag("THVM_HIP_DENSE_NOSKBLK");
     hipb.dense_nored = env_flag("THVM_HIP_DENSE_NORED");
+    hipb.dense_nocomb = env_flag("THVM_HIP_DENSE_NOCOMB");
     hipb.dense_pack = env_flag("THVM_HIP_DENSE_PACK");
     const char *e = getenv("THVM_HIP_DENSE_SPLITS");
     hipb.dense_splits = e ? (u32)atoi(e) : 0;
@@ -313,6 +424,9 @@ static void read_dense_env(void) {
     e = getenv("THVM_HIP_DIRECT_WAVES");
     hipb.direct_waves = e ? (u32)atoi(e) : 0;
     if (hipb.direct_waves != 4 && hipb.direct_waves != 8 && hipb.direct_waves != 16) hipb.direct_waves = 0;
+    e = getenv("THVM_HIP_DIRECT_MIN_CHUNK");
+    hipb.direct_min_chunk = e ? (u32)atoi(e) : 0;
+    if (hipb.direct_min_chunk > 65536) hipb.direct_min_chunk = 0;
     e = getenv("THVM_HIP_GEMM_DEPTH");
     hipb.gemm_depth = e ? (u32)atoi(e) : 0;
     if (hipb.gemm_depth > 2) hipb.gemm_depth = 0;
@@ -633,13 +747,20 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
         params[np++] = &sm;
         for (u32 j = 0; j < e->n_scal; j++) params[np++] = &sv[j];
     }
+    /* the memory it touches, for holding it for a batched launch */
+    HbMem hm;
+    hm.n = 0;
+    hbm_add(&hm, ptrs[0], pool_bytes(out_buf), 1);
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++)
+        hbm_add(&hm, pool_ptr(leaf_bufs[i]), pool_bytes(leaf_bufs[i]), 0);
     u32 gx, gy;
     if (e->splits > 1 && !e->fn_fin) {
         /* split group reduce, partials combined by the last workgroup of each
          * output through the combine area */
         params[np] = &hipb.comb_slots;
         grid_for(e->total * e->splits, e->block, &gx, &gy);
-        hipb_launch(e->fn, gx, gy, 1, e->block, params);
+        if (!hipb_hold(&e->co, e->fn, gx, gy, params, &hm, 1, (int)np, e->total * e->splits))
+            hipb_launch(e->fn, gx, gy, 1, e->block, params);
         pool_mark_device_write(out_buf);
         return;
     }
@@ -657,8 +778,7 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     }
     if (e->mode == KG_MODE_GROUP) grid_for(e->total, e->block, &gx, &gy);
     else grid_for((e->n_threads + e->block - 1) / e->block, e->block, &gx, &gy);
-    if (e->mode != KG_MODE_SERIAL || !hb_hold(e, gx, gy, nb, ptrs, counts, sm, sv, out_buf, leaf_bufs, n_leaves))
-        hipb_launch(e->fn, gx, gy, 1, e->block, params);
+    if (!hipb_hold(&e->co, e->fn, gx, gy, params, &hm, 0, -1, 0)) hipb_launch(e->fn, gx, gy, 1, e->block, params);
     pool_mark_device_write(out_buf);
 }
 

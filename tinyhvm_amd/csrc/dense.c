@@ -412,6 +412,8 @@ typedef struct {
     u32 red_mg;            /* outer-product reduction: rows per group */
     u64 red_max[2];        /* ... the largest index each side forms (unchecked loads) */
     u32 red_buf[2];        /* ... and the buffer it reads (1 + leaf) */
+    int comb;              /* direct and outer-product kernels: split-K partials combined in the
+                              same launch by the last split's workgroup through the combine words */
 } GemmPlan;
 
 #define GEMM_THREADS 256
@@ -421,6 +423,11 @@ typedef struct {
 #define GEMM_SLOTS_PER_CU 4u
 
 static u32 dense_cus(void) { return hipb.n_cu ? hipb.n_cu : 256u; }
+
+/* workgroup size of a plan's main kernel */
+static u32 dense_threads(const GemmPlan *pl) {
+    return pl->cfg.direct == 3 ? GEMM_THREADS : pl->cfg.direct ? 64u * pl->nw : GEMM_THREADS;
+}
 #define SUM_WAVE_MIN_SPLITS 16   /* split-K sums this long use a wavefront per output, */
 #define SUM_WAVE_MAX_OUTPUTS 8192 /* unless there are enough outputs for a lane each */
 
@@ -483,7 +490,19 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
     const char *st;
     out_store_fn(k, ct, fb, sizeof fb, &st);
     const u32 M = ct->M, N = ct->N;
-    if (pl->splits > 1 && pl->swap)
+    if (pl->comb)
+        /* the direct kernel's in-launch combine (the words taken into cb_) */
+        dsb_put(s_, "        if (sl_ == nullptr) {\n"
+                    "          ws[((unsigned long long)spl * M + m) * N + n] = c[v];\n"
+                    "        } else if (spl != S - 1u) {\n"
+                    "          comb_pub(sl_ + (unsigned long long)spl * MN + m * N + n, c[v]);\n"
+                    "        } else {\n"
+                    "          float a_ = 0.0f;\n"
+                    "          #pragma unroll\n"
+                    "          for (u32 sp = 0; sp + 1u < S; sp++) a_ = a_ + cb_[(sp * 16u + v) * 64u + lane];\n"
+                    "          %s(p0, c0, gid_m(m) + gid_n(n), %s + (a_ + c[v]));\n"
+                    "        }\n", st, fb);
+    else if (pl->splits > 1 && pl->swap)
         dsb_put(s_, "        ws[((unsigned long long)spl * N + n) * M + m] = c[v];\n");
     else if (pl->splits > 1)
         dsb_put(s_, "        ws[((unsigned long long)spl * M + m) * N + n] = c[v];\n");
@@ -569,7 +588,7 @@ static void emit_red_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, c
     const u32 VP = (V + 63) / 64 * 64;
     dsb_put(s, "extern \"C\" __global__ __launch_bounds__(256) void %s(", pl->name);
     emit_params(s, k->n_leaves);
-    dsb_put(s, ", float* ws) {\n");
+    dsb_put(s, pl->comb ? ", float* ws, unsigned long long* sl_) {\n" : ", float* ws) {\n");
     dsb_put(s,
             "  constexpr u32 M = %uu, N = %uu, K = %uu, MG = %uu, V = %uu, VP = %uu, KCH = %uu;\n"
             "  const u32 lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n"
@@ -612,15 +631,70 @@ static void emit_red_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, c
             "    }\n"
             "    __syncthreads();\n"
             "  }\n"
-            "  __syncthreads();\n"
+            "  __syncthreads();\n",
+            M, N, K, MG, V, VP, pl->kchunk, ct->sep_buf[0], ct->sep_buf[1]);
+    if (pl->comb) {
+        char fb[64];
+        const char *st;
+        out_store_fn(k, ct, fb, sizeof fb, &st);
+        /* in-launch combine: the splits but the last publish their partials
+         * (word s*M*N + m*N + n); the last split's 256 threads take the other
+         * splits' words into LDS (the transpose buffer, free by now), all of a
+         * thread's words peeked at once and cleared after, and lane idx of wave 0
+         * adds output idx's partials in split order, its own last */
+        dsb_put(s,
+                "  constexpr u32 S = %uu, MN = M * N, NTK = (S - 1u) * V;\n"
+                "  if (sl_ != nullptr) {\n"
+                "    if (spl != S - 1u) {\n"
+                "      if (wave > 0u) return;\n"
+                "      for (u32 idx = lane; idx < V; idx += 64u) {\n"
+                "        const float t = ((tot_[0][idx] + tot_[1][idx]) + tot_[2][idx]) + tot_[3][idx];\n"
+                "        if (m0 + idx / N < M) comb_pub(sl_ + (unsigned long long)spl * MN + m0 * N + idx, t);\n"
+                "      }\n"
+                "      return;\n"
+                "    }\n"
+                "    float* cb_ = &tr_[0][0][0];\n"
+                "    constexpr u32 NB = (NTK + 255u) / 256u;\n"
+                "    unsigned long long w_[NB];\n"
+                "    #pragma unroll\n"
+                "    for (u32 u = 0; u < NB; u++) {\n"
+                "      const u32 j = threadIdx.x + 256u * u, sp = j / V, idx = j %% V;\n"
+                "      w_[u] = (j < NTK && m0 + idx / N < M) ? comb_peek(sl_ + (unsigned long long)sp * MN + m0 * N + idx)\n"
+                "                                          : (1ull << 32);\n"
+                "    }\n"
+                "    #pragma unroll\n"
+                "    for (u32 u = 0; u < NB; u++) {\n"
+                "      const u32 j = threadIdx.x + 256u * u, sp = j / V, idx = j %% V;\n"
+                "      if (j < NTK && m0 + idx / N < M) cb_[j] = comb_ready(sl_ + (unsigned long long)sp * MN + m0 * N + idx, w_[u]);\n"
+                "    }\n"
+                "    #pragma unroll\n"
+                "    for (u32 u = 0; u < NB; u++) {\n"
+                "      const u32 j = threadIdx.x + 256u * u, sp = j / V, idx = j %% V;\n"
+                "      if (j < NTK && m0 + idx / N < M) comb_clear(sl_ + (unsigned long long)sp * MN + m0 * N + idx);\n"
+                "    }\n"
+                "    __syncthreads();\n"
+                "    if (wave > 0u) return;\n"
+                "    for (u32 idx = lane; idx < V; idx += 64u) {\n"
+                "      const u32 i = idx / N, n = idx %% N, m = m0 + i;\n"
+                "      if (m >= M) continue;\n"
+                "      float a = 0.0f;\n"
+                "      #pragma unroll\n"
+                "      for (u32 sp = 0; sp + 1u < S; sp++) a = a + cb_[sp * V + idx];\n"
+                "      a = a + (((tot_[0][idx] + tot_[1][idx]) + tot_[2][idx]) + tot_[3][idx]);\n"
+                "      %s(p0, c0, gid_m(m) + gid_n(n), %s + a);\n"
+                "    }\n"
+                "    return;\n"
+                "  }\n",
+                pl->splits, st, fb);
+    }
+    dsb_put(s,
             "  if (wave > 0u) return;\n"
             "  for (u32 idx = lane; idx < V; idx += 64u) {\n"
             "    const float t = ((tot_[0][idx] + tot_[1][idx]) + tot_[2][idx]) + tot_[3][idx];\n"
             "    const u32 i = idx / N, n = idx %% N, m = m0 + i;\n"
             "    if (m < M) ws[((unsigned long long)spl * M + m) * N + n] = t;\n"
             "  }\n"
-            "}\n",
-            M, N, K, MG, V, VP, pl->kchunk, ct->sep_buf[0], ct->sep_buf[1]);
+            "}\n");
 }
 
 /* Skinny kernel (CFG_SKINNY): lane = row m, all N column sums in registers.
@@ -743,7 +817,7 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
     const u32 blocks = pl->tiles_m * pl->tiles_n;
     dsb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", 64u * pl->nw, pl->name);
     emit_params(s, k->n_leaves);
-    dsb_put(s, ", float* ws) {\n");
+    dsb_put(s, pl->comb ? ", float* ws, unsigned long long* sl_) {\n" : ", float* ws) {\n");
     dsb_put(s,
             "  constexpr u32 M = %uu, N = %uu, K = %uu, TN = %uu, BLOCKS = %uu, KCH = %uu, KU = %uu, NW = %uu;\n"
             "  const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;\n"
@@ -794,8 +868,40 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
                "    #pragma unroll\n"
                "    for (u32 v = 0; v < 16u; v++) part_[wave - 1u][v][lane] = acc[v];\n"
                "  }\n"
-               "  __syncthreads();\n"
-               "  if (wave > 0u) return;\n"
+               "  __syncthreads();\n");
+    if (pl->comb)
+        /* in-launch combine: the last split's threads take the other splits'
+         * words of the block's 1024 outputs into LDS (slot s*1024 + v*64 +
+         * lane, the output of accumulator v in lane `lane`), all of a thread's
+         * words peeked at once; the epilogue adds them in split order */
+        dsb_put(s,
+               "  constexpr u32 S = %uu, MN = M * N, NTK = (S - 1u) * 1024u;\n"
+               "  __shared__ float cb_[NTK];\n"
+               "  if (sl_ != nullptr && spl == S - 1u) {\n"
+               "    constexpr u32 NB = (NTK + NW * 64u - 1u) / (NW * 64u);\n"
+               "    unsigned long long w_[NB];\n"
+               "    u32 o_[NB];\n"
+               "    #pragma unroll\n"
+               "    for (u32 u = 0; u < NB; u++) {\n"
+               "      const u32 j = threadIdx.x + NW * 64u * u, l = j & 1023u, v = l >> 6, ln = l & 63u;\n"
+               "      const u32 m = m0 + 8u * (v >> 2) + 4u * (ln >> 5) + (v & 3u), n = n0 + (ln & 31u);\n"
+               "      o_[u] = (j < NTK && m < M && n < N) ? m * N + n : ~0u;\n"
+               "      w_[u] = o_[u] != ~0u ? comb_peek(sl_ + (unsigned long long)(j >> 10) * MN + o_[u]) : (1ull << 32);\n"
+               "    }\n"
+               "    #pragma unroll\n"
+               "    for (u32 u = 0; u < NB; u++) {\n"
+               "      const u32 j = threadIdx.x + NW * 64u * u;\n"
+               "      if (o_[u] != ~0u) cb_[j] = comb_ready(sl_ + (unsigned long long)(j >> 10) * MN + o_[u], w_[u]);\n"
+               "    }\n"
+               "    #pragma unroll\n"
+               "    for (u32 u = 0; u < NB; u++) {\n"
+               "      const u32 j = threadIdx.x + NW * 64u * u;\n"
+               "      if (o_[u] != ~0u) comb_clear(sl_ + (unsigned long long)(j >> 10) * MN + o_[u]);\n"
+               "    }\n"
+               "    __syncthreads();\n"
+               "  }\n",
+               pl->splits);
+    dsb_put(s, "  if (wave > 0u) return;\n"
                "  #pragma unroll\n"
                "  for (u32 w = 0; w < NW - 1u; w++)\n"
                "    #pragma unroll\n"
@@ -1174,6 +1280,7 @@ typedef struct {
     hipFunction_t fn, fn_sum, fn_pack;
     GemmPlan plan;
     u32 M, N;
+    CoForm co, co_sum;            /* co-launch forms of the main and split-K sum kernels */
 } DenseEntry;
 
 static struct {
@@ -1562,6 +1669,29 @@ static void plan_skinny(const Contraction *ct, GemmPlan *pl) {
     }
 }
 
+/* In-launch combine of split-K partials (direct and outer-product kernels):
+ * the splits but the last publish their partials as combine words, the last
+ * split's workgroup takes them into LDS and adds every output's partials in
+ * split order (deterministic), so no workspace and no sum kernel. It needs a
+ * word per partial in the combine area and the taken partials in LDS: the
+ * direct kernel's 1024 outputs for at most COMB_DIRECT_MAX_SPLITS - 1 splits,
+ * the outer-product kernel's within its transpose buffer. At most
+ * COMB_MAX_SPLITS splits: the last split's workgroup takes every other
+ * split's words after its own chunk, which LeNet-5's conv1 weight gradient
+ * (98 splits) paid for with 7 us over the 3 us of its sum kernel, while its
+ * conv2 weight gradient (12 splits) saved 2.5 us. */
+#define COMB_DIRECT_MAX_SPLITS 8u
+#define COMB_RED_LDS_FLOATS (4u * 32u * 65u)
+#define COMB_MAX_SPLITS 16u
+static void plan_comb(const Contraction *ct, GemmPlan *pl) {
+    pl->comb = 0;
+    if (hipb.dense_nocomb || pl->splits < 2 || pl->splits > COMB_MAX_SPLITS ||
+        (u64)pl->splits * ct->M * ct->N > COMB_SLOTS)
+        return;
+    if (pl->cfg.direct == 1) pl->comb = pl->splits <= COMB_DIRECT_MAX_SPLITS && !pl->pack;
+    else if (pl->cfg.direct == 3) pl->comb = (u64)(pl->splits - 1) * pl->red_mg * ct->N <= COMB_RED_LDS_FLOATS;
+}
+
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     static const TileCfg *forced[10] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
                                         &CFG_C64S, &CFG_SKINNY, &CFG_RED};
@@ -1595,7 +1725,7 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
      * setup is larger; 64 otherwise) */
     /* direct: 4 waves per block share its K range, so a split of c gives
      * each wave c/4; keep that >= 64 and aim for ~2048 waves */
-    u32 min_chunk = pl->cfg.bm == 128 ? 512 : pl->cfg.direct ? 256 : 64;
+    u32 min_chunk = pl->cfg.bm == 128 ? 512 : pl->cfg.direct ? (hipb.direct_min_chunk ? hipb.direct_min_chunk : 256) : 64;
     u64 target = lk ? 1024 : 512;    /* workgroups */
     u32 splits = 1;
     while ((u64)tiles * splits < target && ct->K / (splits * 2) >= min_chunk && splits < 1024) splits *= 2;
@@ -1619,6 +1749,7 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
     plan_pads(ct, pl);
     plan_chunks(ct, pl);
     plan_skinny(ct, pl);
+    plan_comb(ct, pl);
 }
 
 /* Contraction analysis without a device: returns 1 and fills M/N/K when the
@@ -1697,6 +1828,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
             e->plan.pack = 0;
             plan_pads(&ct, &e->plan);
             plan_chunks(&ct, &e->plan);
+            plan_comb(&ct, &e->plan);
         }
         char err[256] = {0};
         char *src = gen_gemm_source(k, &ct, &e->plan, err, sizeof err);
@@ -1710,18 +1842,29 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
             free(src);
             return 0;
         }
-        free(src);
-        if (hipModuleGetFunction(&e->fn, e->mod, e->plan.name) != hipSuccess) return 0;
+        if (hipModuleGetFunction(&e->fn, e->mod, e->plan.name) != hipSuccess) {
+            free(src);
+            return 0;
+        }
+        co_form_make(&e->co, src, e->plan.name, dense_threads(&e->plan), e->fn);
         if (e->plan.pack) {
             char nm[64];
             snprintf(nm, sizeof nm, "%s_pack", e->plan.name);
-            if (hipModuleGetFunction(&e->fn_pack, e->mod, nm) != hipSuccess) return 0;
+            if (hipModuleGetFunction(&e->fn_pack, e->mod, nm) != hipSuccess) {
+                free(src);
+                return 0;
+            }
         }
         if (e->plan.splits > 1) {
             char nm[64];
             snprintf(nm, sizeof nm, "%s_sum", e->plan.name);
-            if (hipModuleGetFunction(&e->fn_sum, e->mod, nm) != hipSuccess) return 0;
+            if (hipModuleGetFunction(&e->fn_sum, e->mod, nm) != hipSuccess) {
+                free(src);
+                return 0;
+            }
+            co_form_make(&e->co_sum, src, nm, 256, e->fn_sum);
         }
+        free(src);
         e->M = ct.M;
         e->N = ct.N;
         e->is_dense = 1;
@@ -1738,9 +1881,16 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         (e->plan.red_max[0] >= counts[e->plan.red_buf[0]] || e->plan.red_max[1] >= counts[e->plan.red_buf[1]]))
         return 0;
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) pool_sync_device(leaf_bufs[i]);
+    u32 tiles = e->plan.tiles_m * e->plan.tiles_n;
+    const u32 threads = dense_threads(&e->plan);
+    /* in-launch combine only when every workgroup of the grid is on the GPU at
+     * once (the last split's workgroups wait for the others' words);
+     * otherwise the partials go through the workspace and the sum kernel */
+    unsigned long long *sl = NULL;
+    if (e->plan.comb && (u64)tiles * e->plan.splits * (threads / 64u) <= hipb_resident_waves()) sl = hipb.comb_slots;
     /* split-K workspace */
     float *ws = NULL;
-    if (e->plan.splits > 1) {
+    if (e->plan.splits > 1 && !sl) {
         ws = scratch_reserve(&D.ws, (u64)e->plan.splits * e->M * e->N * sizeof(float));
         if (!ws) return 0;
     }
@@ -1757,7 +1907,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         params[nb + b] = &counts[b];
     }
     params[2 * nb] = &ws;
-    params[2 * nb + 1] = &pk;
+    params[2 * nb + 1] = e->plan.comb ? (void *)&sl : (void *)&pk;
     if (e->plan.pack) {
         void *pp[2 * (FUSE_MAX_LEAVES + 1) + 1];
         for (u32 b = 0; b < 2 * nb; b++) pp[b] = params[b];
@@ -1765,14 +1915,29 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         const u64 kn = e->plan.kp.maxidx[1] + 1;
         if (!hipb_launch_grid(e->fn_pack, (u32)((kn + 255) / 256), 1, 256, pp)) return 0;
     }
-    u32 tiles = e->plan.tiles_m * e->plan.tiles_n;
-    const u32 threads = e->plan.cfg.direct == 3 ? GEMM_THREADS : e->plan.cfg.direct ? 64u * e->plan.nw : GEMM_THREADS;
-    if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, threads, params)) return 0;
-    if (e->plan.splits > 1) {
+    /* held for a batch with the next independent dispatches (the split-K sum
+     * then joins them, its main kernel going out first) */
+    const u64 mn = (u64)e->M * e->N, wsb = (u64)e->plan.splits * mn * sizeof(float);
+    HbMem hm;
+    hm.n = 0;
+    hbm_add(&hm, ws ? (void *)ws : ptrs[0], ws ? wsb : pool_bytes(out_buf), 1);
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++)
+        hbm_add(&hm, pool_ptr(leaf_bufs[i]), pool_bytes(leaf_bufs[i]), 0);
+    if (e->plan.pack ||
+        !hipb_hold(&e->co, e->fn, tiles, e->plan.splits, params, &hm, sl != NULL, sl ? (int)(2 * nb + 1) : -1,
+                   sl ? (u64)e->plan.splits * mn : 0))
+        if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, threads, params)) return 0;
+    if (ws) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};
-        u64 mn = (u64)e->M * e->N;
-        u64 per_block = sum_per_wave(&e->plan, mn) ? 4 : 64;
-        if (!hipb_launch_grid(e->fn_sum, (u32)((mn + per_block - 1) / per_block), 1, 256, p2)) return 0;
+        const u64 per_block = sum_per_wave(&e->plan, mn) ? 4 : 64;
+        const u32 blocks = (u32)((mn + per_block - 1) / per_block);
+        HbMem hs;
+        hs.n = 0;
+        hbm_add(&hs, ptrs[0], pool_bytes(out_buf), 1);
+        hbm_add(&hs, ws, wsb, 0);
+        if (!hipb_hold(&e->co_sum, e->fn_sum, blocks, 1, p2, &hs, 0, -1, 0) &&
+            !hipb_launch_grid(e->fn_sum, blocks, 1, 256, p2))
+            return 0;
     }
     return 1;
 }
@@ -1784,6 +1949,8 @@ void dense_shutdown(void) {
         for (u32 i = 0; i < D.cap; i++) {
             if (!D.tab[i].key) continue;
             if (D.tab[i].is_dense) HIPB_CHECK(hipModuleUnload(D.tab[i].mod));
+            co_form_free(&D.tab[i].co);
+            co_form_free(&D.tab[i].co_sum);
             free(D.tab[i].ops);
         }
         free(D.tab);

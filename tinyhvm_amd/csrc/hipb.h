@@ -56,6 +56,8 @@ typedef struct {
     int dense_noskinny;      /* THVM_HIP_DENSE_NOSKINNY: no row-per-lane kernel for N <= 16 */
     int dense_noskinny_blocks; /* THVM_HIP_DENSE_NOSKBLK: the row-per-lane kernel walks K per k */
     int dense_nored;         /* THVM_HIP_DENSE_NORED: no outer-product reduction kernel */
+    int dense_nocomb;        /* THVM_HIP_DENSE_NOCOMB: split-K partials always through a sum kernel */
+    u32 direct_min_chunk;    /* THVM_HIP_DIRECT_MIN_CHUNK: shortest K chunk of a direct-kernel split (0: chosen) */
     int dense_pack;          /* THVM_HIP_DENSE_PACK: pack wherever the layout allows (tests) */
     u32 dense_tile;          /* THVM_HIP_DENSE_TILE: 0 chosen, 1 128x128, 2 64x64, 3 256x32, 4 32x256, 5 direct,
                                 6 256x64, 7 128x64, 8 skinny (where N <= 16), 9 outer-product reduction
@@ -101,6 +103,9 @@ hipError_t hipb_stream_wait(void);
 /* Issues the dispatches held for a batched launch; every operation put on
  * the stream calls it first, so the stream sees work in program order. */
 void hipb_before_stream(void);
+/* The same for a host-to-device copy into [dst, dst + bytes): only if a held
+ * dispatch touches that memory (the copy may go ahead of independent ones). */
+void hipb_before_copy(const void *dst, u64 bytes);
 typedef struct {
     void *ptr;        /* device pointer, NULL if free */
     u64 bytes;        /* requested bytes */
@@ -180,6 +185,44 @@ int  kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, co
 #define SINGLE_PASS_WAVES_PER_CU 16u
 u32 hipb_resident_waves(void);
 
+/* ---------------- co-launch ---------------- */
+/* A generated module as device functions, so that independent dispatches can
+ * go out together in one launch of a batch kernel: the module after the
+ * shared prelude, inside namespace co_<id>, each kernel a __device__ function
+ * taking its block coordinates and grid size (bx_, by_, gx_, gy_) first. */
+#define CO_MAX_PARAMS 48
+typedef struct {
+    char *src;             /* NULL: the kernel is launched on its own */
+    char *params;          /* the main kernel's parameter list */
+    char name[48];         /* the main kernel's name */
+    u32 id;                /* namespace co_<id>, unique in the process */
+    u32 threads;           /* its workgroup size */
+    u32 lds;               /* its static LDS bytes */
+    u32 np;
+    u8 psz[CO_MAX_PARAMS]; /* its parameters' sizes in bytes */
+} CoForm;
+int  co_form_make(CoForm *cf, const char *src, const char *name, u32 threads, hipFunction_t fn);
+void co_form_free(CoForm *cf);
+
+/* Memory a held dispatch touches, as address ranges (write: written, maybe
+ * also read). */
+#define HB_RANGES (FUSE_MAX_LEAVES + 4)
+typedef struct {
+    u32 n;
+    u64 lo[HB_RANGES], hi[HB_RANGES];
+    u8 wr[HB_RANGES];
+} HbMem;
+void hbm_add(HbMem *m, const void *p, u64 bytes, int write);
+/* Holds a launch of cf's kernel (returns 1) for a batch with the next
+ * independent dispatches, or returns 0: the caller launches it now.
+ * `resident`: the kernel's workgroups wait for each other (the batch must fit
+ * on the GPU at once). A kernel that combines partials through the combine
+ * area names the parameter that points there (comb_param, else -1) and the
+ * words it uses from there (comb_words): each kernel of a batch gets its own
+ * slice of the area. */
+int  hipb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
+               int resident, int comb_param, u64 comb_words);
+
 /* ---------------- rtc / cache ---------------- */
 typedef struct {
     u64 key;
@@ -195,10 +238,7 @@ typedef struct {
     KOp *ops;             /* copy for collision checks */
     u32 meta[5 + FUSE_MAX_LEAVES]; /* grid, local_size, out_dtype, leaf dtypes */
     char name[32];        /* the kernel's symbol */
-    /* a serial 256-lane kernel also as a device function <name>_b(u32 bk_,
-     * params), its workgroup index an argument, for launches that batch
-     * several independent dispatches (NULL: not batchable) */
-    char *bsrc, *bparams;
+    CoForm co;            /* its co-launch form */
 } KCacheEntry;
 
 int  rtc_init(void);

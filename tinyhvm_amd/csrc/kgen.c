@@ -929,6 +929,26 @@ static const char *PRELUDE =
 "  for (u32 w = 1u; w < (blockDim.x >> 6); w++) { float y = red[w]; s = (s > y) ? s : y; }\n"
 "  return s;\n"
 "}\n"
+/* The same with the workgroup's wave count fixed (a batched launch's
+ * workgroups can be larger than the program's) */
+"template <u32 NW> __device__ __forceinline__ float bsum_n(float x, float* red) {\n"
+"  x = wsum(x);\n"
+"  __syncthreads();\n"
+"  if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = x;\n"
+"  __syncthreads();\n"
+"  float s = red[0];\n"
+"  for (u32 w = 1u; w < NW; w++) s = s + red[w];\n"
+"  return s;\n"
+"}\n"
+"template <u32 NW> __device__ __forceinline__ float bmax_n(float x, float* red) {\n"
+"  x = wmax(x);\n"
+"  __syncthreads();\n"
+"  if ((threadIdx.x & 63u) == 0u) red[threadIdx.x >> 6] = x;\n"
+"  __syncthreads();\n"
+"  float s = red[0];\n"
+"  for (u32 w = 1u; w < NW; w++) { float y = red[w]; s = (s > y) ? s : y; }\n"
+"  return s;\n"
+"}\n"
 /* Single-pass combine of per-workgroup partials. Each of the S workgroups
  * of output o but the last publishes its partial as one 64-bit word (a ready
  * flag in the high half, the float's bits in the low half) with an
@@ -954,6 +974,29 @@ static const char *PRELUDE =
 "  }\n"
 "  __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
 "  return (v >> 32) ? __uint_as_float((u32)v) : __uint_as_float(0x7fc00000u);\n"
+"}\n"
+/* The same words for a block of partials: comb_pub publishes one,
+ * comb_peek reads one without waiting (a batch of them issued together),
+ * comb_ready waits (bounded) for a peeked word to be marked ready and
+ * returns its float (a NaN if it never became ready), comb_clear clears it
+ * for the next launch (the clears of a batch issued after all its waits, so
+ * that no wait is for a clear). */
+"__device__ __forceinline__ void comb_pub(unsigned long long* w, float x) {\n"
+"  __hip_atomic_store(w, (1ull << 32) | (unsigned long long)__float_as_uint(x), __ATOMIC_RELAXED,\n"
+"                     __HIP_MEMORY_SCOPE_AGENT);\n"
+"}\n"
+"__device__ __forceinline__ unsigned long long comb_peek(unsigned long long* w) {\n"
+"  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+"}\n"
+"__device__ __forceinline__ float comb_ready(unsigned long long* w, unsigned long long v) {\n"
+"  for (u32 n = 0u; (v >> 32) == 0ull && n < (1u << 22); n++) {\n"
+"    __builtin_amdgcn_s_sleep(2);\n"
+"    v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+"  }\n"
+"  return (v >> 32) ? __uint_as_float((u32)v) : __uint_as_float(0x7fc00000u);\n"
+"}\n"
+"__device__ __forceinline__ void comb_clear(unsigned long long* w) {\n"
+"  __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
 "}\n";
 
 const char *kgen_prelude(void) { return PRELUDE; }

@@ -564,7 +564,7 @@ static u8 *stage_reserve(u64 n);
 void pool_sync_device(u32 id) {
     HipbBuf *b = pool_get(id);
     if (!b || !b->dev_stale) return;
-    hipb_before_stream();
+    hipb_before_copy(b->ptr, b->cap);
     u8 *st = stage_reserve(b->mirror_bytes);
     memcpy(st, b->host_mirror, b->mirror_bytes);
     HIPB_CHECK(hipMemcpyAsync(b->ptr, st, b->mirror_bytes, hipMemcpyHostToDevice, hipb.stream));
@@ -589,7 +589,6 @@ void pool_device_wrote_all(void) {
 /* Reserve n bytes of pinned staging; waits only if the ring wraps onto a
  * segment whose copies are still in flight. */
 static u8 *stage_reserve(u64 n) {
-    hipb_before_stream();
     if (hipb.capturing) {
         u64 need = (n + 255) & ~255ull;
         if (P.arena && P.arena_off + need <= P.arena_cap) {
@@ -637,7 +636,7 @@ void pool_write(u32 id, const void *data, u64 bytes) {
         }
     }
     pool_sync_device(id);
-    hipb_before_stream();
+    hipb_before_copy(b->ptr, b->cap);
     b->dev_stale = 0;
     b->host_valid = 0;
     if (bytes <= STAGE_SEG_BYTES) {
@@ -654,7 +653,7 @@ void pool_write(u32 id, const void *data, u64 bytes) {
  * the caller's memory may be reused on return). */
 void pool_upload(void *dst, const void *src, u64 bytes) {
     if (!dst || !src || bytes == 0) return;
-    hipb_before_stream();
+    hipb_before_copy(dst, bytes);
     if (bytes <= STAGE_SEG_BYTES) {
         u8 *s = stage_reserve(bytes);
         memcpy(s, src, bytes);

@@ -92,8 +92,7 @@ void rtc_shutdown(void) {
             if (R.tab[i].key) {
                 HIPB_CHECK(hipModuleUnload(R.tab[i].mod));
                 free(R.tab[i].ops);
-                free(R.tab[i].bsrc);
-                free(R.tab[i].bparams);
+                co_form_free(&R.tab[i].co);
             }
         }
         free(R.tab);
@@ -209,41 +208,122 @@ int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t er
     return 1;
 }
 
-/* The batch form of a serial 256-lane kernel (see KCacheEntry): its
- * parameter list, and its text with the entry line made a device function
- * that takes the workgroup index as bk_. Only when the kernel reads its
- * workgroup index in the one place the generator emits it. */
-static void make_batch_form(KCacheEntry *e, const char *src, const char *name) {
-    char head[96];
-    snprintf(head, sizeof head, "extern \"C\" __global__ __launch_bounds__(256) void %s(", name);
-    const char *h = strstr(src, head);
-    if (!h) return;
-    const char *ps = h + strlen(head);
-    const char *pe = strstr(ps, ") {\n");
-    if (!pe) return;
-    static const char tpat[] = "((unsigned long long)blockIdx.y * gridDim.x + blockIdx.x)";
-    const char *t = strstr(pe, tpat);
-    if (!t || strstr(t + strlen(tpat), "blockIdx") || strstr(t + strlen(tpat), "gridDim") ||
-        strstr(pe, "__shared__") || strstr(pe, "__syncthreads"))
-        return;
-    size_t np = (size_t)(pe - ps), nb1 = (size_t)(t - (pe + 4)), nrest = strlen(t + strlen(tpat));
-    char *params = malloc(np + 1);
-    size_t cap = strlen(name) + np + nb1 + nrest + 128;
-    char *b = malloc(cap);
-    if (!params || !b) {
-        free(params);
-        free(b);
-        return;
+/* Co-launch form of a generated module (see CoForm): the source after the
+ * shared prelude inside namespace co_<id>, every `extern "C" __global__`
+ * kernel turned into a __device__ function whose block coordinates and grid
+ * size are its first arguments (blockIdx.x/.y and gridDim.x/.y read them).
+ * The prelude's block-wide helpers, which read blockDim, become their forms
+ * with the program's wave count fixed. Modules that use a third grid
+ * dimension, blockDim, dynamic LDS or includes keep cf->src NULL and launch
+ * on their own. */
+static u32 co_next_id;
+
+static int co_param_sizes(CoForm *cf) {
+    const char *p = cf->params;
+    cf->np = 0;
+    while (*p) {
+        while (*p == ' ' || *p == ',') p++;
+        if (!*p) break;
+        const char *e = strchr(p, ',');
+        size_t len = e ? (size_t)(e - p) : strlen(p);
+        if (cf->np >= CO_MAX_PARAMS) return 0;
+        int ptr = memchr(p, '*', len) != NULL;
+        int ll = 0;
+        for (size_t t = 0; t + 9 <= len; t++) ll |= memcmp(p + t, "long long", 9) == 0;
+        cf->psz[cf->np++] = (u8)((ptr || ll) ? 8 : 4);
+        p += len;
     }
-    memcpy(params, ps, np);
-    params[np] = 0;
-    int w = snprintf(b, cap, "__device__ __forceinline__ void %s_b(u32 bk_, %s) {\n", name, params);
-    memcpy(b + w, pe + 4, nb1);
-    w += (int)nb1;
-    w += snprintf(b + w, cap - (size_t)w, "((unsigned long long)bk_)");
-    memcpy(b + w, t + strlen(tpat), nrest + 1);
-    e->bparams = params;
-    e->bsrc = b;
+    return cf->np > 0;
+}
+
+int co_form_make(CoForm *cf, const char *src, const char *name, u32 threads, hipFunction_t fn) {
+    memset(cf, 0, sizeof *cf);
+    const char *pre = kgen_prelude();
+    const size_t pl = strlen(pre);
+    if (!src || strncmp(src, pre, pl) != 0 || strlen(name) >= sizeof cf->name) return 0;
+    const char *body = src + pl;
+    if (strstr(body, "blockIdx.z") || strstr(body, "gridDim.z") || strstr(body, "blockDim") ||
+        strstr(body, "extern __shared__") || strstr(body, "#include"))
+        return 0;
+    /* the main kernel's parameter list */
+    char head[96];
+    snprintf(head, sizeof head, " void %s(", name);
+    const char *h = strstr(body, head);
+    if (!h) return 0;
+    const char *ps = h + strlen(head), *pe = strstr(ps, ") {");
+    if (!pe) return 0;
+    cf->params = malloc((size_t)(pe - ps) + 1);
+    if (!cf->params) return 0;
+    memcpy(cf->params, ps, (size_t)(pe - ps));
+    cf->params[pe - ps] = 0;
+    if (!co_param_sizes(cf)) goto fail;
+    /* the transformed module */
+    static const char kg[] = "extern \"C\" __global__ ", lb[] = "__launch_bounds__(";
+    size_t cap = strlen(body) * 2 + 256;
+    char *o = malloc(cap);
+    if (!o) goto fail;
+    cf->id = ++co_next_id;
+    size_t w = (size_t)snprintf(o, cap, "namespace co_%u {\n", cf->id);
+    const char *q = body;
+    while (*q) {
+        if (w + 128 >= cap) {
+            char *n2 = realloc(o, cap * 2);
+            if (!n2) { free(o); goto fail; }
+            o = n2;
+            cap *= 2;
+        }
+        if (strncmp(q, kg, sizeof kg - 1) == 0) {
+            q += sizeof kg - 1;
+            if (strncmp(q, lb, sizeof lb - 1) == 0) {
+                const char *r = strchr(q, ')');
+                if (!r) { free(o); goto fail; }
+                q = r + 1;
+                while (*q == ' ') q++;
+            }
+            if (strncmp(q, "void ", 5) != 0) { free(o); goto fail; }
+            const char *par = strchr(q, '(');
+            if (!par) { free(o); goto fail; }
+            w += (size_t)snprintf(o + w, cap - w, "__device__ __forceinline__ %.*su32 bx_, u32 by_, u32 gx_, u32 gy_, ",
+                                  (int)(par + 1 - q), q);
+            q = par + 1;
+        } else if (strncmp(q, "bsum(", 5) == 0 || strncmp(q, "bmax(", 5) == 0) {
+            /* the block-wide helpers with the program's own wave count */
+            w += (size_t)snprintf(o + w, cap - w, "%.4s_n<%uu>(", q, threads / 64u);
+            q += 5;
+        } else if (strncmp(q, "blockIdx.x", 10) == 0 || strncmp(q, "blockIdx.y", 10) == 0) {
+            w += (size_t)snprintf(o + w, cap - w, "b%c_", q[9]);
+            q += 10;
+        } else if (strncmp(q, "gridDim.x", 9) == 0 || strncmp(q, "gridDim.y", 9) == 0) {
+            w += (size_t)snprintf(o + w, cap - w, "g%c_", q[8]);
+            q += 9;
+        } else {
+            o[w++] = *q++;
+        }
+    }
+    o[w] = 0;
+    if (strstr(o, "__global__") || w + 8 >= cap) { free(o); goto fail; }
+    snprintf(o + w, cap - w, "}\n");
+    cf->src = o;
+    snprintf(cf->name, sizeof cf->name, "%s", name);
+    cf->threads = threads;
+    if (fn) {   /* NULL: a device-free check */
+        int v = 0;
+        if (hipFuncGetAttribute(&v, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, fn) != hipSuccess || v < 0) goto fail_src;
+        cf->lds = (u32)v;
+    }
+    return 1;
+fail_src:
+    free(cf->src);
+fail:
+    free(cf->params);
+    memset(cf, 0, sizeof *cf);
+    return 0;
+}
+
+void co_form_free(CoForm *cf) {
+    free(cf->src);
+    free(cf->params);
+    memset(cf, 0, sizeof *cf);
 }
 
 KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
@@ -305,8 +385,8 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
     e->ops = malloc((size_t)k->n_ops * sizeof(KOp));
     if (e->ops) memcpy(e->ops, k->ops, (size_t)k->n_ops * sizeof(KOp));
     snprintf(e->name, sizeof e->name, "%s", g.name);
-    e->bsrc = e->bparams = NULL;
-    if (g.mode == KG_MODE_SERIAL && g.splits <= 1 && g.block == 256) make_batch_form(e, g.src, g.name);
+    /* split reductions with a combine kernel are two launches: not co-launched */
+    if (!g.combine_launch) co_form_make(&e->co, g.src, g.name, g.block, fn);
     hipb.n_compile++;
     kgen_free(&g);
     return e;

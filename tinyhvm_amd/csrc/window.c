@@ -576,6 +576,7 @@ typedef struct {
     WinPlan plan;
     hipModule_t mod;
     hipFunction_t fn, fn_fin;
+    CoForm co;                   /* the main kernel's co-launch form (one-launch plans) */
 } WinEntry;
 
 static Scratch win_ws;   /* run-sum partials of the combine-kernel form */
@@ -681,15 +682,18 @@ int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
             free(src);
             return 0;
         }
-        free(src);
         char fin[64];
         snprintf(fin, sizeof fin, "%s_fin", name);
         if (hipModuleGetFunction(&e->fn, e->mod, name) != hipSuccess ||
             (e->plan.kind == WIN_SUM && e->plan.S > 1 && e->plan.launch &&
              hipModuleGetFunction(&e->fn_fin, e->mod, fin) != hipSuccess)) {
             HIPB_CHECK(hipModuleUnload(e->mod));
+            free(src);
             return 0;
         }
+        if (!(e->plan.kind == WIN_SUM && e->plan.S > 1 && e->plan.launch))
+            co_form_make(&e->co, src, name, WIN_BLOCK, e->fn);
+        free(src);
         e->kind = e->plan.kind;
         if (hipb.verbose)
             fprintf(stderr, "tinyhvm-hip: %s outputs=%u trip=%u W=%u run=%u splits=%u\n", name, e->plan.total,
@@ -730,6 +734,11 @@ int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
             gx = 65536;
             gy = (u32)((blocks + 65535) / 65536);
         }
+        HbMem hm;
+        hm.n = 0;
+        hbm_add(&hm, ptrs[0], pool_bytes(out_buf), 1);
+        hbm_add(&hm, ptrs[bi], pool_bytes(leaf_bufs[bi - 1]), 0);
+        if (hipb_hold(&e->co, e->fn, gx, gy, params, &hm, 0, -1, 0)) return 1;
         if (!hipb_launch(e->fn, gx, gy, 1, WIN_BLOCK, params)) return 0;
     } else {
         void *params[FUSE_MAX_LEAVES + 3];
@@ -739,6 +748,15 @@ int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
             params[np++] = &ws;
         } else {
             params[np++] = &hipb.comb_slots;
+            /* one launch: held for a batch with the next independent dispatches */
+            HbMem hm;
+            hm.n = 0;
+            hbm_add(&hm, ptrs[0], pool_bytes(out_buf), 1);
+            for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++)
+                hbm_add(&hm, pool_ptr(leaf_bufs[i]), pool_bytes(leaf_bufs[i]), 0);
+            if (hipb_hold(&e->co, e->fn, p->total * p->S, 1, params, &hm, p->S > 1, (int)(np - 1),
+                          (u64)p->total * p->S))
+                return 1;
         }
         if (!hipb_launch(e->fn, p->total * p->S, 1, 1, WIN_BLOCK, params)) return 0;
         if (ws) {
@@ -754,6 +772,7 @@ void window_shutdown(void) {
         for (u32 i = 0; i < WC.cap; i++) {
             if (!WC.tab[i].key) continue;
             if (WC.tab[i].kind != WIN_NONE) HIPB_CHECK(hipModuleUnload(WC.tab[i].mod));
+            co_form_free(&WC.tab[i].co);
             free(WC.tab[i].ops);
         }
         free(WC.tab);
