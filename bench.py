@@ -412,6 +412,24 @@ def copy_calibration(nbytes=256 << 20, reps=5):
                       "ms_per_copy": round(ms, 4), "GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}))
 
 
+def mfma_calibration():
+    """The f32 matrix-core rate a kernel sustains on this GPU with no memory
+    traffic (thvm_hip_mfma_probe), at 4 to 32 waves per compute unit, beside
+    the published dense f32 peak the rooflines use."""
+    import ctypes as C
+    L = _lib.lib()
+    if L.thvm_hip_init() != 0:
+        raise SystemExit("HIP backend failed to initialise")
+    out = {}
+    for w in (4, 8, 16, 32):
+        t = C.c_double(0.0)
+        if L.thvm_hip_mfma_probe(w, 4000, C.byref(t)) != 0:
+            raise SystemExit("mfma probe failed")
+        out["%d_waves_per_cu" % w] = round(t.value, 1)
+    L.thvm_hip_shutdown()
+    print(json.dumps({"mfma_f32_tflops": out, "published_peak": MFMA_F32_PEAK_TFLOPS}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -422,9 +440,14 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 256 MiB copy kernel (HBM counter calibration)")
+    ap.add_argument("--calibrate-mfma", action="store_true",
+                    help="run only the f32 MFMA rate probe (register operands, no memory traffic)")
     args = ap.parse_args()
     if args.calibrate_copy:
         copy_calibration()
+        return
+    if args.calibrate_mfma:
+        mfma_calibration()
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this backend has no multi-GPU path "

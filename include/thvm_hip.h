@@ -147,6 +147,13 @@ int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32
  * dispatches run on the window-max and run-sum kernels, dispatches issued
  * inside a batched launch. Returns the number of counters (12). */
 int  thvm_hip_counters(u64 *out, u32 n);
+/* Sustained f32 MFMA rate on this GPU: a kernel of waves_per_cu waves per
+ * compute unit (a multiple of 4, at most 32), each running iters x 8
+ * v_mfma_f32_32x32x2f32 from registers with no memory traffic, timed over
+ * five launches; TFLOP/s into *tflops. Returns 0, or -1. A calibration with
+ * no counterpart in the reference: the matrix-core rate a kernel can reach
+ * at this part's sustained clock, beside the published peak. */
+int  thvm_hip_mfma_probe(u32 waves_per_cu, u32 iters, double *tflops);
 /* Wait for all enqueued work; returns 0, or -1 on a device error. */
 int  thvm_hip_synchronize(void);
 /* The hipStream_t all work is ordered on (for timing with events). */

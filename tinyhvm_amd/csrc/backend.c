@@ -1163,6 +1163,48 @@ int thvm_hip_counters(u64 *out, u32 n) {
     return 12;
 }
 
+int thvm_hip_mfma_probe(u32 waves_per_cu, u32 iters, double *tflops) {
+    if (!hipb.initialized || !tflops || waves_per_cu == 0 || waves_per_cu > 32 || iters == 0 || iters > 100000)
+        return -1;
+    hipFunction_t fn = rtc_static_fn("thvm_mfma_probe"), fill = rtc_static_fn("thvm_fill_u32");
+    const u32 cus = hipb.n_cu ? hipb.n_cu : 256u, blocks = cus * waves_per_cu / 4u;
+    u64 c_in = 0, c_out = 0;
+    float *in = pool_block_get(4096 * 4, &c_in), *out = pool_block_get((u64)blocks * 256u * 4u, &c_out);
+    hipEvent_t e0, e1;
+    int rc = -1;
+    if (!fn || !fill || !in || !out || blocks == 0) goto done;
+    if (hipEventCreate(&e0) != hipSuccess) goto done;
+    if (hipEventCreate(&e1) != hipSuccess) {
+        HIPB_CHECK(hipEventDestroy(e0));
+        goto done;
+    }
+    {
+        u32 n = 4096, one = 0x3f800000u;   /* 1.0f */
+        void *pf[] = {&in, &n, &one};
+        void *pp[] = {&in, &out, &iters};
+        hipb_launch(fill, 16, 1, 1, 256, pf);
+        hipb_launch(fn, blocks, 1, 1, 256, pp);   /* warm-up */
+        HIPB_CHECK(hipEventRecord(e0, hipb.stream));
+        for (int r = 0; r < 5; r++) hipb_launch(fn, blocks, 1, 1, 256, pp);
+        HIPB_CHECK(hipEventRecord(e1, hipb.stream));
+        if (hipEventSynchronize(e1) == hipSuccess) {
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, e0, e1) == hipSuccess && ms > 0.0f) {
+                /* 5 launches x blocks x 4 waves x iters x 8 MFMAs x 32*32*2*2 FLOP */
+                *tflops = 5.0 * blocks * 4.0 * iters * 8.0 * 4096.0 / (ms * 1e-3) / 1e12;
+                rc = 0;
+            }
+        }
+        HIPB_CHECK(hipEventDestroy(e0));
+        HIPB_CHECK(hipEventDestroy(e1));
+    }
+done:
+    HIPB_CHECK(hipb_stream_wait());
+    pool_block_put(in, c_in);
+    pool_block_put(out, c_out);
+    return rc;
+}
+
 int thvm_hip_synchronize(void) {
     if (!hipb.initialized) return -1;
     if (pool_capture_forbids("a synchronize")) return -1;
