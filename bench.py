@@ -366,7 +366,9 @@ def engine_step(name, want_cpu):
                                          "read-backs on the host clock, median of %d steps)" % steps,
                       "batch": batch},
            "dispatches_per_step": g["dispatches_per_step"], "reads_per_step": g["reads_per_step"],
-           "host_waits_per_step": g["host_waits_per_step"], "waits_outside_reads": g["waits_outside_reads"]}
+           "host_waits_per_step": g["host_waits_per_step"], "waits_outside_reads": g["waits_outside_reads"],
+           "backend_slots_ms_per_step": g.get("backend_slots_ms_per_step"),
+           "read_ms_per_step": g.get("read_ms_per_step")}
     if want_cpu and e["cpu"]["steps_per_s"] > 0:
         res["cpu_baseline"] = {"value": e["cpu"]["steps_per_s"], "unit": "steps/s", "cores": 1,
                                "kind": "reference", "seconds": e["cpu"]["seconds_per_step"],

@@ -86,6 +86,9 @@ static u32 g_nsteps;
 static double g_step_t[TM_MAX_STEPS + 1];
 static u64 g_step_waits[TM_MAX_STEPS + 1], g_step_reads[TM_MAX_STEPS + 1], g_step_disp[TM_MAX_STEPS + 1];
 static u64 g_reads_total, g_disp_total, g_waits_outside;
+/* host seconds inside the backend's slots: buf_read/buf_read_nosync (which
+ * wait for the GPU), and every other slot */
+static double g_bk_s, g_rd_s, g_step_bk[TM_MAX_STEPS + 1], g_step_rd[TM_MAX_STEPS + 1];
 static char g_waits_outside_slot[64];
 static Backend g_tm_inner;
 
@@ -101,6 +104,8 @@ static void tm_mark(const char *text) {
     g_step_waits[g_nsteps] = host_waits();
     g_step_reads[g_nsteps] = g_reads_total;
     g_step_disp[g_nsteps] = g_disp_total;
+    g_step_bk[g_nsteps] = g_bk_s;
+    g_step_rd[g_nsteps] = g_rd_s;
     g_nsteps++;
 }
 
@@ -110,14 +115,32 @@ static void tm_outside(const char *slot, u64 w0) {
         snprintf(g_waits_outside_slot, sizeof g_waits_outside_slot, "%s", slot);
     }
 }
-#define TM_WRAP(slot, ...) do { u64 w0_ = host_waits(); g_tm_inner.slot(__VA_ARGS__); tm_outside(#slot, w0_); } while (0)
-static u32 tm_alloc(u64 b) { u64 w0 = host_waits(); u32 id = g_tm_inner.buf_alloc(b); tm_outside("buf_alloc", w0); return id; }
+#define TM_WRAP(slot, ...) do { u64 w0_ = host_waits(); double t0_ = now_s(); g_tm_inner.slot(__VA_ARGS__); \
+                                   g_bk_s += now_s() - t0_; tm_outside(#slot, w0_); } while (0)
+static u32 tm_alloc(u64 b) {
+    u64 w0 = host_waits();
+    double t0 = now_s();
+    u32 id = g_tm_inner.buf_alloc(b);
+    g_bk_s += now_s() - t0;
+    tm_outside("buf_alloc", w0);
+    return id;
+}
 static void tm_free(u32 id) { TM_WRAP(buf_free, id); }
 static void tm_incref(u32 id) { TM_WRAP(buf_incref, id); }
 static void tm_decref(u32 id) { TM_WRAP(buf_decref, id); }
 static void tm_write(u32 id, const void *d, u64 b) { TM_WRAP(buf_write, id, d, b); }
-static void tm_read(u32 id, void *o, u64 b) { g_reads_total++; g_tm_inner.buf_read(id, o, b); }
-static void tm_read_nosync(u32 id, void *o, u64 b) { g_reads_total++; g_tm_inner.buf_read_nosync(id, o, b); }
+static void tm_read(u32 id, void *o, u64 b) {
+    g_reads_total++;
+    double t0 = now_s();
+    g_tm_inner.buf_read(id, o, b);
+    g_rd_s += now_s() - t0;
+}
+static void tm_read_nosync(u32 id, void *o, u64 b) {
+    g_reads_total++;
+    double t0 = now_s();
+    g_tm_inner.buf_read_nosync(id, o, b);
+    g_rd_s += now_s() - t0;
+}
 static void tm_uop(u32 out, const u32 *l, u32 n, const UOpKernel *k, u64 key) {
     g_disp_total++;
     TM_WRAP(dispatch_uop_kernel, out, l, n, k, key);
@@ -170,6 +193,7 @@ static void tm_run(TinyHVM *ctx, const char *wl, u32 B, int steps) {
 }
 
 /* one timed run: returns the median step in seconds (0 when no step closed) */
+static double g_last_bk, g_last_rd;   /* the last tm_steps: backend-slot and read seconds per step */
 static double tm_steps(TinyHVM *ctx, const char *wl, u32 B, int steps, double *mean, double *waits, double *reads,
                        double *disp) {
     g_nsteps = 0;
@@ -179,8 +203,12 @@ static double tm_steps(TinyHVM *ctx, const char *wl, u32 B, int steps, double *m
     g_step_waits[g_nsteps] = host_waits();
     g_step_reads[g_nsteps] = g_reads_total;
     g_step_disp[g_nsteps] = g_disp_total;
+    g_step_bk[g_nsteps] = g_bk_s;
+    g_step_rd[g_nsteps] = g_rd_s;
     u32 n = g_nsteps;
     if (n == 0) return 0.0;
+    g_last_bk = (g_step_bk[n] - g_step_bk[0]) / n;
+    g_last_rd = (g_step_rd[n] - g_step_rd[0]) / n;
     double d[TM_MAX_STEPS], sum = 0.0;
     for (u32 i = 0; i < n; i++) {
         d[i] = g_step_t[i + 1] - g_step_t[i];
@@ -195,6 +223,7 @@ static double tm_steps(TinyHVM *ctx, const char *wl, u32 B, int steps, double *m
     return d[n / 2];
 }
 
+static double g_hip_bk, g_hip_rd;
 /* the hip_backend leg: returns the median step in seconds, -1 when the
  * backend cannot be loaded or initialised */
 static double tm_hip_leg(const char *lib, const char *wl, u32 B, int steps, double *mean, double *waits,
@@ -225,6 +254,8 @@ static double tm_hip_leg(const char *lib, const char *wl, u32 B, int steps, doub
     g_waits_outside = 0;
     g_waits_outside_slot[0] = 0;
     double med = tm_steps(ctx, wl, B, steps, mean, waits, reads, disp);
+    g_hip_bk = g_last_bk;
+    g_hip_rd = g_last_rd;
     hb->shutdown();
     return med;
 }
@@ -257,10 +288,12 @@ static int time_mode(const char *lib, const char *wl, int steps, const u32 *sz, 
     double cmed = tm_steps(cpu, wl, B, strcmp(wl, "mlp") == 0 ? 3 : 1, &cmean, &cw, &cr, &cd);
     printf("{\"workload\": \"%s\", \"batch\": %u, \"steps\": %d, \"gpu\": {\"median_ms\": %.4f, "
            "\"mean_ms\": %.4f, \"steps_per_s\": %.2f, \"host_waits_per_step\": %.2f, \"reads_per_step\": %.2f, "
-           "\"dispatches_per_step\": %.2f, \"waits_outside_reads\": %llu, \"wait_slot\": \"%s\"}, "
+           "\"dispatches_per_step\": %.2f, \"waits_outside_reads\": %llu, \"wait_slot\": \"%s\", "
+           "\"backend_slots_ms_per_step\": %.4f, \"read_ms_per_step\": %.4f}, "
            "\"cpu\": {\"seconds_per_step\": %.4f, \"steps_per_s\": %.5f}}\n",
            wl, B, steps, med * 1e3, mean * 1e3, med > 0 ? 1.0 / med : 0.0, waits, reads, disp,
-           (unsigned long long)g_waits_outside, g_waits_outside_slot, cmed, cmed > 0 ? 1.0 / cmed : 0.0);
+           (unsigned long long)g_waits_outside, g_waits_outside_slot, g_hip_bk * 1e3, g_hip_rd * 1e3, cmed,
+           cmed > 0 ? 1.0 / cmed : 0.0);
     fflush(stdout);
     return (cpu_only || med > 0) && cmed > 0 ? 0 : 1;
 }
