@@ -143,9 +143,10 @@ WORKLOADS = {
 class Hip:
     """hipEvent timing on the backend's stream (libamdhip64 via ctypes)."""
 
-    def __init__(self, stream):
+    def __init__(self, stream, flush=None):
         self.h = C.CDLL("libamdhip64.so")
         self.stream = C.c_void_p(stream)
+        self.flush = flush
         self.h.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
         self.h.hipEventRecord.argtypes = [C.c_void_p, C.c_void_p]
         self.h.hipEventSynchronize.argtypes = [C.c_void_p]
@@ -157,6 +158,10 @@ class Hip:
         return e
 
     def record(self, e):
+        # the backend holds some launches back to batch them: issue them
+        # first, so that the event follows every earlier dispatch
+        if self.flush:
+            self.flush()
         assert self.h.hipEventRecord(e, self.stream) == 0
 
     def ms(self, a, b):
@@ -244,7 +249,7 @@ def run_workload(L, name, steps, warmup, want_cpu):
     assert L.thvm_hip_synchronize() == 0
     print("%s: setup + warmup %.1fs, step = records [%d, %d)" % (name, time.perf_counter() - t_c, lo, hi),
           file=sys.stderr, flush=True)
-    hip = Hip(L.thvm_hip_stream())
+    hip = Hip(L.thvm_hip_stream(), L.thvm_hip_flush)
     # pass 1: whole steps (the reported throughput)
     e0, e1 = hip.event(), hip.event()
     t0 = time.perf_counter()
@@ -401,7 +406,7 @@ def copy_calibration(nbytes=256 << 20, reps=5):
     leaves = (C.c_uint32 * 1)(src)
     L.thvm_hip_dispatch_uop_kernel(dst, leaves, 1, C.byref(k), 0)
     assert L.thvm_hip_synchronize() == 0
-    hip = Hip(L.thvm_hip_stream())
+    hip = Hip(L.thvm_hip_stream(), L.thvm_hip_flush)
     e0, e1 = hip.event(), hip.event()
     hip.record(e0)
     for _ in range(reps):

@@ -158,6 +158,12 @@ int  thvm_hip_mfma_probe(u32 waves_per_cu, u32 iters, double *tflops);
 int  thvm_hip_synchronize(void);
 /* The hipStream_t all work is ordered on (for timing with events). */
 void *thvm_hip_stream(void);
+/* Issues the launches the backend holds back (independent dispatches it
+ * batches, queued copies), without waiting: a caller that puts work of its
+ * own on thvm_hip_stream() (a timing event) calls it first so that the
+ * stream has every earlier dispatch ahead of that work. No counterpart in
+ * the reference (its backends issue every dispatch at once). */
+void thvm_hip_flush(void);
 /* Device address of a buffer (for tests and timing harnesses). */
 void *thvm_hip_buf_device_ptr(u32 id);
 /* The vtable, for callers that cannot read exported data symbols. */

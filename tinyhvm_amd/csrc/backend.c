@@ -1218,6 +1218,11 @@ int thvm_hip_synchronize(void) {
 }
 
 void *thvm_hip_stream(void) { return hipb.initialized ? (void *)hipb.stream : NULL; }
+void thvm_hip_flush(void) {
+    if (!hipb.initialized) return;
+    copyq_flush();
+    hipb_before_stream();
+}
 void *thvm_hip_buf_device_ptr(u32 id) { return pool_ptr(id); }
 
 const Backend *thvm_hip_backend(void) { return &hip_backend; }
