@@ -145,7 +145,9 @@ int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32
  * written), host waits on the stream, live device bytes, hipMalloc calls,
  * device blocks pinned by HIP graphs, released blocks held for graphs,
  * dispatches run on the window-max and run-sum kernels, dispatches issued
- * inside a batched launch. Returns the number of counters (12). */
+ * inside a batched launch, elementwise dispatches run as the fused epilogue
+ * of the contraction whose output they read. Returns the number of counters
+ * (13). */
 int  thvm_hip_counters(u64 *out, u32 n);
 /* Sustained f32 MFMA rate on this GPU: a kernel of waves_per_cu waves per
  * compute unit (a multiple of 4, at most 32), each running iters x 8
@@ -206,6 +208,16 @@ int  thvm_hip_window_analyze(const UOpKernel *kernel, u32 *kind, u32 *splits);
 int  thvm_hip_window_source(const UOpKernel *kernel, char *buf, u64 buflen);
 /* Generate and compile it without loading; the code-object size, or -1. */
 int  thvm_hip_window_compile_check(const UOpKernel *kernel, char *errbuf, u64 errlen);
+
+/* An elementwise dispatch that reads a matrix-core contraction's output at
+ * its own index runs in that contraction's epilogue (no launch of its own)
+ * when the contraction's launch is still held: the fused module of producer
+ * and consumer (which reads the producer's output as leaf buffer o_leaf, 1 +
+ * leaf), compiled without loading (no device needed). Returns the
+ * code-object size, or -1 with the reason in errbuf (also when the pair does
+ * not fuse). A diagnostic with no counterpart in the reference. */
+int  thvm_hip_epilogue_compile_check(const UOpKernel *producer, const UOpKernel *consumer, u32 o_leaf,
+                                     char *errbuf, u64 errlen);
 
 /* Independent dispatches held back and issued as one launch: the batch
  * kernel of n generated modules (srcs[i] as the generators above return it,

@@ -49,3 +49,35 @@ def test_generated_modules_compile_as_batches(name):
     for i in range(0, len(mods), 8):
         group = mods[i:i + 8]
         assert _lib.batch_compile_check(group) > 0, [g[1] for g in group]
+
+
+def test_lenet_epilogues_fuse_and_compile():
+    """Elementwise dispatches that read a matrix-core contraction's output at
+    their own index fuse into its epilogue: LeNet-5's five forward bias+relu
+    (or bias) kernels after conv1, conv2, fc1, fc2, fc3 and the relu mask
+    after fc2's input gradient; the fused modules compile. Consumers that
+    read the output elsewhere (the pool backward after fc1's input gradient
+    and conv2's, and the pad after the weight flip) are refused."""
+    recs = trace.read_trace(os.path.join(WL, "lenet_b256.trc"))
+    lo = next(i for i, r in enumerate(recs) if r.tag == trace.MARK and r.f["text"] == "lenet.step")
+    hi = next(i for i, r in enumerate(recs) if i > lo and r.tag == trace.MARK and r.f["text"] == "lenet.end")
+    uops = [r for r in recs[lo:hi] if r.tag == trace.UOP]
+    fused, refused = [], []
+    for p, c in zip(uops, uops[1:]):
+        kp = trace.to_uop_kernel(p)
+        a = _lib.dense_analyze(kp)
+        if not a or p.f["out"] not in c.f["leaf_bufs"]:
+            continue
+        kc = trace.to_uop_kernel(c)
+        try:
+            assert _lib.epilogue_compile_check(kp, kc, c.f["leaf_bufs"].index(p.f["out"]) + 1) > 0
+            fused.append(a[:3])
+        except ValueError as e:
+            assert "own index" in str(e), str(e)
+            refused.append(a[:3])
+    # (the CPU run routes every contraction to the matrix cores, so smaller
+    # ones fuse too)
+    for want in [(200704, 6, 25), (25600, 16, 150), (256, 120, 400), (256, 84, 120), (256, 10, 84),
+                 (256, 120, 84)]:
+        assert want in fused, (want, fused)
+    assert refused == [(256, 400, 120), (96, 25, 25), (50176, 6, 400)], refused

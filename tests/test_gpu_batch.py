@@ -1,4 +1,5 @@
-"""Batched launches of independent generated kernels.
+"""Batched launches of independent generated kernels, and elementwise
+kernels fused into the epilogue of the contraction they follow.
 
 The backend holds back launches of generated kernels and issues independent
 ones together as one launch of a batch kernel. In a LeNet-5 training step at
@@ -26,9 +27,10 @@ TRACE = os.path.join(ROOT, "tinyhvm_amd", "workloads", "lenet_b256.trc")
 PARAMS = range(2, 12)          # trace ids of W1, b1, ..., W5, b5
 
 
-def _step(no_batch):
-    old = os.environ.get("THVM_HIP_NO_BATCH")
+def _step(no_batch, no_fuse=False):
+    old = {k: os.environ.get(k) for k in ("THVM_HIP_NO_BATCH", "THVM_HIP_NO_FUSE")}
     os.environ["THVM_HIP_NO_BATCH"] = "1" if no_batch else "0"
+    os.environ["THVM_HIP_NO_FUSE"] = "1" if no_fuse else "0"
     L = _lib.lib()
     try:
         assert L.thvm_hip_init() == 0
@@ -39,12 +41,12 @@ def _step(no_batch):
         lo = L.thvm_trace_find_mark(t, b"lenet.step", 0)
         hi = L.thvm_trace_find_mark(t, b"lenet.end", lo)
         L.thvm_trace_replay(t, be, 0, lo, 0)
-        before = (C.c_uint64 * 12)()
-        L.thvm_hip_counters(before, 12)
+        before = (C.c_uint64 * 13)()
+        L.thvm_hip_counters(before, 13)
         L.thvm_trace_replay(t, be, lo, hi, 1)
         assert L.thvm_hip_synchronize() == 0
-        after = (C.c_uint64 * 12)()
-        assert L.thvm_hip_counters(after, 12) == 12
+        after = (C.c_uint64 * 13)()
+        assert L.thvm_hip_counters(after, 13) == 13
         out = {}
         for tid in PARAMS:
             buf = (C.c_uint8 * sizes[tid])()
@@ -52,19 +54,35 @@ def _step(no_batch):
             out[tid] = bytes(buf)
         L.thvm_trace_release(t, be)
         L.thvm_trace_free(t)
-        return out, after[11] - before[11]
+        return out, after[11] - before[11], after[12] - before[12]
     finally:
         L.thvm_hip_shutdown()
-        if old is None:
-            os.environ.pop("THVM_HIP_NO_BATCH", None)
-        else:
-            os.environ["THVM_HIP_NO_BATCH"] = old
+        for k, v in old.items():
+            if v is None:
+                os.environ.pop(k, None)
+            else:
+                os.environ[k] = v
 
 
 def test_batched_launches_match_single_launches():
-    single, n_single = _step(no_batch=True)
-    batched, n_batched = _step(no_batch=False)
+    single, n_single, _ = _step(no_batch=True)
+    batched, n_batched, _ = _step(no_batch=False, no_fuse=True)
     assert n_single == 0
     assert n_batched >= 20, "only %d dispatches were batched" % n_batched
     bad = [tid for tid in PARAMS if single[tid] != batched[tid]]
     assert not bad, "parameters %s differ between batched and single launches" % bad
+
+
+def test_fused_epilogues_match_separate_launches():
+    """The bias+relu (or bias) kernels after LeNet-5's two convolutions and
+    three fully connected layers, and the relu mask after fc2's input
+    gradient, run in the epilogue of the contraction whose output they read
+    (no launch of their own). The step's updated parameters are bit for bit
+    those with THVM_HIP_NO_FUSE=1 (every kernel launched on its own), and at
+    least the five forward consumers were fused."""
+    separate, _, n_sep = _step(no_batch=False, no_fuse=True)
+    fused, _, n_fused = _step(no_batch=False)
+    assert n_sep == 0
+    assert n_fused >= 5, "only %d epilogues were fused" % n_fused
+    bad = [tid for tid in PARAMS if separate[tid] != fused[tid]]
+    assert not bad, "parameters %s differ between fused and separate launches" % bad

@@ -75,6 +75,8 @@ def lib():
         "thvm_hip_window_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
         "thvm_hip_mfma_probe": (C.c_int, [u32, u32, C.POINTER(C.c_double)]),
         "thvm_hip_flush": (None, []),
+        "thvm_hip_epilogue_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), C.POINTER(abi.UOpKernel), u32, cp,
+                                                      u64]),
         "thvm_hip_batch_compile_check": (C.c_int, [C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), PU32, PU32, u32,
                                                    cp, u64]),
         "thvm_trace_load": (vp, [cp]),
@@ -112,7 +114,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_kernel_lanes", "thvm_hip_compile_check",
     "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
     "thvm_hip_window_analyze", "thvm_hip_window_source", "thvm_hip_window_compile_check",
-    "thvm_hip_batch_compile_check", "thvm_hip_mfma_probe", "thvm_hip_flush",
+    "thvm_hip_batch_compile_check", "thvm_hip_mfma_probe", "thvm_hip_flush", "thvm_hip_epilogue_compile_check",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
     "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",
@@ -148,6 +150,17 @@ def batch_compile_check(items):
     grid = (C.c_uint32 * (2 * n))(*[v for it in items for v in (it[3], it[4])])
     err = C.create_string_buffer(4096)
     r = lib().thvm_hip_batch_compile_check(srcs, names, threads, grid, n, err, len(err))
+    if r < 0:
+        raise ValueError(err.value.decode())
+    return r
+
+
+def epilogue_compile_check(producer: abi.UOpKernel, consumer: abi.UOpKernel, o_leaf: int):
+    """Code-object size of the fused module of a contraction and the
+    elementwise consumer of its output; raises ValueError with the reason
+    when the pair does not fuse or does not compile."""
+    err = C.create_string_buffer(4096)
+    r = lib().thvm_hip_epilogue_compile_check(C.byref(producer), C.byref(consumer), o_leaf, err, len(err))
     if r < 0:
         raise ValueError(err.value.decode())
     return r

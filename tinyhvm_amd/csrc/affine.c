@@ -187,3 +187,27 @@ u64 aff_max(const DCtx *c, const Aff *a) {
     }
     return v;
 }
+
+int aff_is_gid(const DCtx *c, const Aff *a) {
+    if (!a->ok || a->cst != 0 || a->n == 0 || a->n > DG_MAX) return 0;
+    /* digits of gid alone, in increasing div, each step the previous one's
+     * div * mod, the coefficient its div, the last without a mod */
+    u32 ord[DG_MAX];
+    for (u32 t = 0; t < a->n; t++) ord[t] = t;
+    for (u32 i = 1; i < a->n; i++)
+        for (u32 j = i; j > 0 && a->d[ord[j - 1]].div > a->d[ord[j]].div; j--) {
+            const u32 x = ord[j];
+            ord[j] = ord[j - 1];
+            ord[j - 1] = x;
+        }
+    u64 step = 1;
+    for (u32 i = 0; i < a->n; i++) {
+        const Digit *d = &a->d[ord[i]];
+        if (d->var != 0 || d->div != step || a->coef[ord[i]] != d->div) return 0;
+        if (i + 1 == a->n) return d->mod == 0 || (u64)d->div * d->mod >= var_range(c, 0);
+        if (d->mod == 0) return 0;
+        step = (u64)d->div * d->mod;
+        if (step > 0xFFFFFFFFull) return 0;
+    }
+    return 0;
+}

@@ -50,5 +50,7 @@ u64  contiguous_run(const DCtx *c, const Aff *a, u8 var);
 u64  aff_eval(const Aff *a, u32 gid, u32 r);
 /* the largest value an affine sum takes over its digits' ranges */
 u64  aff_max(const DCtx *c, const Aff *a);
+/* whether an affine sum is gid itself for every gid in [0, total) */
+int  aff_is_gid(const DCtx *c, const Aff *a);
 
 #endif

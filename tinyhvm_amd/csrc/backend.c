@@ -11,6 +11,7 @@
  * for the KOp program, compiled once per program and cached.
  */
 #include <stdlib.h>
+#include <time.h>
 #include <string.h>
 
 #include "hipb.h"
@@ -100,6 +101,9 @@ typedef struct {
     u8 args[HB_ARG_BYTES];
     HbMem m;
     int resident;
+    u64 fz_key;            /* a contraction an elementwise consumer may fuse into (0: none) */
+    u32 fz_serial, fz_out; /* ... its dense entry and its output buffer */
+    int solo;              /* held only for a fused epilogue: joins no batch */
 } HbEnt;
 static struct {
     HbEnt ent[HB_MAX];
@@ -330,6 +334,7 @@ void hipb_before_copy(const void *dst, u64 bytes) {
 /* why h cannot join the held launches as they are (NULL: it can) */
 static const char *hb_joins(const HbEnt *h) {
     if (HB.n >= HB_MAX) return "batch full";
+    if (h->solo || (HB.n && HB.ent[0].solo)) return "held alone";
     u32 T = h->co.threads, lds = h->co.lds, blocks = h->gx * h->gy;
     int resident = h->resident;
     for (u32 i = 0; i < HB.n; i++) {
@@ -345,15 +350,31 @@ static const char *hb_joins(const HbEnt *h) {
     return NULL;
 }
 
+static int hb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
+                   int resident, int comb_param, u64 comb_words, int solo);
+
 int hipb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
               int resident, int comb_param, u64 comb_words) {
+    return hb_hold(cf, fn, gx, gy, params, m, resident, comb_param, comb_words, 0);
+}
+
+int hipb_hold_solo(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m) {
+    if (hipb.no_fuse) return 0;
+    return hb_hold(cf, fn, gx, gy, params, m, 0, -1, 0, 1);
+}
+
+static int hb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
+                   int resident, int comb_param, u64 comb_words, int solo) {
     if (!cf || !cf->src || hipb.no_batch || hipb.noalloc || hipb.sync_each || HB.flushing) return 0;
-    if (gx == 0 || gy == 0 || (u64)gx * gy > HB_MAX_BLOCKS || cf->threads == 0 || cf->threads % 64u ||
+    if (gx == 0 || gy == 0 || (!solo && (u64)gx * gy > HB_MAX_BLOCKS) || cf->threads == 0 || cf->threads % 64u ||
         cf->threads > 1024u || comb_words > COMB_SLOTS || (comb_param >= 0 && ((u32)comb_param >= cf->np ||
         cf->psz[comb_param] != 8)))
         return 0;
     HbEnt tmp, *h = &tmp;
     h->co = *cf;
+    h->fz_key = 0;
+    h->fz_serial = h->fz_out = 0;
+    h->solo = solo;
     h->fn = fn;
     h->gx = gx;
     h->gy = gy;
@@ -388,6 +409,82 @@ int hipb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *p
     return 1;
 }
 
+void hipb_hold_tag(u64 key, u32 serial, u32 out_buf) {
+    if (!HB.n) return;
+    HbEnt *h = &HB.ent[HB.n - 1];
+    h->fz_key = key;
+    h->fz_serial = serial;
+    h->fz_out = out_buf;
+}
+
+static u32 elem_count(u32 id, u32 dtype);
+
+/* An elementwise dispatch that reads the output of a held contraction runs
+ * as that launch's fused epilogue (dense_epilogue) instead of a launch of
+ * its own: its buffers are appended to the held launch's parameters and its
+ * memory to the launch's. Only when it touches nothing another held launch
+ * writes or reads, except the contraction's output, which it reads at its
+ * own index only; writes neither that output nor its own inputs. Returns 1
+ * when it was fused. */
+static int hb_try_epilogue(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
+    if (!HB.n || hipb.no_fuse || hipb.noalloc || hipb.sync_each || HB.flushing || !k ||
+        k->n_leaves > FUSE_MAX_LEAVES || n_leaves < k->n_leaves)
+        return 0;
+    HbEnt *e = NULL;
+    u32 o_leaf = 0;
+    for (u32 i = HB.n; i-- > 0 && !e;) {
+        if (!HB.ent[i].fz_key) continue;
+        for (u32 j = 0; j < k->n_leaves; j++)
+            if (leaf_bufs[j] == HB.ent[i].fz_out) {
+                e = &HB.ent[i];
+                o_leaf = j + 1;
+                break;
+            }
+    }
+    if (!e || out_buf == e->fz_out || !pool_ptr(out_buf)) return 0;
+    for (u32 j = 0; j < k->n_leaves; j++)
+        if (leaf_bufs[j] == out_buf || (leaf_bufs[j] && !pool_ptr(leaf_bufs[j]))) return 0;
+    HbMem m;
+    m.n = 0;
+    hbm_add(&m, pool_ptr(out_buf), pool_bytes(out_buf), 1);
+    for (u32 j = 0; j < k->n_leaves; j++)
+        if (leaf_bufs[j] != e->fz_out) hbm_add(&m, pool_ptr(leaf_bufs[j]), pool_bytes(leaf_bufs[j]), 0);
+    for (u32 i = 0; i < HB.n; i++)
+        if (hbm_clash(&m, &HB.ent[i].m)) return 0;
+    hipFunction_t fn;
+    CoForm co;
+    if (!dense_epilogue(e->fz_key, e->fz_serial, k, o_leaf, &fn, &co)) return 0;
+    /* the consumer's buffers (the generated kernel's p<b>, c<b>) after the
+     * contraction's parameters */
+    u32 off = 0;
+    for (u32 j = 0; j < e->co.np; j++) off = hb_arg_off(off, e->co.psz[j]) + e->co.psz[j];
+    const u32 nb = k->n_leaves + 1;
+    if (hb_arg_off(off, 8) + 8u * nb + 4u * nb > HB_ARG_BYTES) return 0;
+    for (u32 j = 0; j < k->n_leaves; j++) pool_sync_device(leaf_bufs[j]);
+    for (u32 b = 0; b < nb; b++) {
+        void *p = b == 0 ? pool_ptr(out_buf) : leaf_bufs[b - 1] ? pool_ptr(leaf_bufs[b - 1]) : hipb.dummy;
+        off = hb_arg_off(off, 8);
+        memcpy(e->args + off, &p, 8);
+        off += 8;
+    }
+    for (u32 b = 0; b < nb; b++) {
+        const u32 c = b == 0 ? elem_count(out_buf, k->out_dtype)
+                             : leaf_bufs[b - 1] ? elem_count(leaf_bufs[b - 1], k->leaf_dtypes[b - 1]) : 0u;
+        off = hb_arg_off(off, 4);
+        memcpy(e->args + off, &c, 4);
+        off += 4;
+    }
+    e->fn = fn;
+    e->co = co;
+    for (u32 r = 0; r < m.n; r++) {
+        void *lo = (void *)(uintptr_t)m.lo[r];
+        hbm_add(&e->m, lo, m.hi[r] - m.lo[r], m.wr[r]);
+    }
+    e->fz_key = 0;
+    hipb.n_fused++;
+    return 1;
+}
+
 static void hb_release(void) {
     HB.n = 0;
     for (u32 i = 0; i < HB.ncache; i++) HIPB_CHECK(hipModuleUnload(HB.cache[i].mod));
@@ -412,6 +509,8 @@ static void read_dense_env(void) {
     hipb.dense_noskinny_blocks = env_flag("THVM_HIP_DENSE_NOSKBLK");
     hipb.dense_nored = env_flag("THVM_HIP_DENSE_NORED");
     hipb.dense_nocomb = env_flag("THVM_HIP_DENSE_NOCOMB");
+    hipb.no_fuse = env_flag("THVM_HIP_NO_FUSE");
+    hipb.host_profile = env_flag("THVM_HIP_HOST_PROFILE");
     hipb.dense_pack = env_flag("THVM_HIP_DENSE_PACK");
     const char *e = getenv("THVM_HIP_DENSE_SPLITS");
     hipb.dense_splits = e ? (u32)atoi(e) : 0;
@@ -539,11 +638,48 @@ static void hb_shutdown(void) {
     hipb.initialized = 0;
 }
 
-static u32 hb_buf_alloc(u64 bytes) { return pool_alloc(bytes); }
-static void hb_buf_free(u32 id) { copyq_guard(id); pool_free(id); }
-static void hb_buf_incref(u32 id) { pool_incref(id); }
-static void hb_buf_decref(u32 id) { copyq_guard(id); pool_decref(id); }
-static void hb_buf_write(u32 id, const void *data, u64 bytes) { copyq_guard(id); pool_write(id, data, bytes); }
+u64 hipb_hp_now(void) {
+    if (!hipb.host_profile) return 0;
+    struct timespec t;
+    clock_gettime(CLOCK_MONOTONIC, &t);
+    return (u64)t.tv_sec * 1000000000ull + (u64)t.tv_nsec;
+}
+
+void hipb_hp_add(int cat, u64 t0) {
+    if (!hipb.host_profile || cat < 0 || cat >= HP_N) return;
+    hipb.hp_ns[cat] += hipb_hp_now() - t0;
+    hipb.hp_calls[cat]++;
+}
+
+static u32 hb_buf_alloc(u64 bytes) {
+    const u64 t0 = hipb_hp_now();
+    const u32 id = pool_alloc(bytes);
+    hipb_hp_add(HP_POOL, t0);
+    return id;
+}
+static void hb_buf_free(u32 id) {
+    const u64 t0 = hipb_hp_now();
+    copyq_guard(id);
+    pool_free(id);
+    hipb_hp_add(HP_POOL, t0);
+}
+static void hb_buf_incref(u32 id) {
+    const u64 t0 = hipb_hp_now();
+    pool_incref(id);
+    hipb_hp_add(HP_POOL, t0);
+}
+static void hb_buf_decref(u32 id) {
+    const u64 t0 = hipb_hp_now();
+    copyq_guard(id);
+    pool_decref(id);
+    hipb_hp_add(HP_POOL, t0);
+}
+static void hb_buf_write(u32 id, const void *data, u64 bytes) {
+    const u64 t0 = hipb_hp_now();
+    copyq_guard(id);
+    pool_write(id, data, bytes);
+    hipb_hp_add(HP_WRITE, t0);
+}
 static void hb_buf_read(u32 id, void *out, u64 bytes) { copyq_guard(id); pool_read(id, out, bytes, 0); }
 static void hb_buf_read_nosync(u32 id, void *out, u64 bytes) { copyq_guard(id); pool_read(id, out, bytes, 1); }
 static void hb_mem_checkpoint(u32 *ids, u32 n) { (void)ids; (void)n; }
@@ -563,7 +699,9 @@ static u32 elem_count(u32 id, u32 dt) {
 
 int hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params) {
     hipb_before_stream();
+    const u64 t0 = hipb_hp_now();
     hipError_t e = hipModuleLaunchKernel(fn, gx, gy, gz, bx, 1, 1, 0, hipb.stream, params, NULL);
+    hipb_hp_add(HP_LAUNCH, t0);
     if (e != hipSuccess) {
         fprintf(stderr, "tinyhvm-hip: launch failed: %s\n", hipGetErrorString(e));
         return 0;
@@ -660,9 +798,17 @@ static void interp_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, con
     free(P);
 }
 
+static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
+
 static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
                                    const UOpKernel *k, u64 cache_key) {
     (void)cache_key;
+    const u64 t0 = hipb_hp_now();
+    hb_dispatch_uop_kernel_(out_buf, leaf_bufs, n_leaves, k);
+    hipb_hp_add(HP_DISPATCH, t0);
+}
+
+static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
     if (!hipb.initialized || !k) return;
     HipbBuf *ob = pool_get(out_buf);
     if (!ob) {
@@ -672,6 +818,10 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     hipb.n_dispatch++;
     copyq_guard_dispatch(out_buf, leaf_bufs, n_leaves < FUSE_MAX_LEAVES ? n_leaves : FUSE_MAX_LEAVES);
     pool_sync_device(out_buf);
+    if (hb_try_epilogue(out_buf, leaf_bufs, n_leaves, k)) {
+        pool_mark_device_write(out_buf);
+        return;
+    }
     if (!hipb.no_dense && dense_try_dispatch(out_buf, leaf_bufs, n_leaves, k)) {
         pool_mark_device_write(out_buf);
         hipb.n_dense++;
@@ -1069,11 +1219,21 @@ static void hb_profile_report(void) {
             (unsigned long long)hipb.n_compile, (unsigned long long)hipb.n_cache_hit,
             (unsigned long long)hipb.n_fallback, (unsigned long long)hipb.n_stream_sync,
             live / 1e6, cached / 1e6, (unsigned long long)mallocs);
+    if (hipb.host_profile) {
+        static const char *nm[HP_N] = {"dispatch_uop_kernel", "kernel launches", "program signatures",
+                                       "alloc/free/incref/decref", "buf_write"};
+        for (int c = 0; c < HP_N; c++)
+            fprintf(stderr, "tinyhvm-hip: host %-26s %10llu calls %10.3f ms %8.3f us/call\n", nm[c],
+                    (unsigned long long)hipb.hp_calls[c], hipb.hp_ns[c] / 1e6,
+                    hipb.hp_calls[c] ? hipb.hp_ns[c] / 1e3 / hipb.hp_calls[c] : 0.0);
+    }
 }
 
 static void hb_profile_reset(void) {
     hipb.n_dispatch = hipb.n_compile = hipb.n_cache_hit = hipb.n_dense = 0;
     hipb.n_fallback = hipb.n_stream_sync = hipb.n_window = 0;
+    memset(hipb.hp_ns, 0, sizeof hipb.hp_ns);
+    memset(hipb.hp_calls, 0, sizeof hipb.hp_calls);
 }
 
 Backend hip_backend = {
@@ -1157,10 +1317,10 @@ int thvm_hip_counters(u64 *out, u32 n) {
     u32 pinned = 0, limbo = 0;
     pool_stats(&live, &cached, &mallocs);
     pool_pin_stats(&pinned, &limbo);
-    u64 v[12] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
-                 hipb.n_stream_sync, live, mallocs, pinned, limbo, hipb.n_window, hipb.n_batched};
-    for (u32 i = 0; out && i < n && i < 12; i++) out[i] = v[i];
-    return 12;
+    u64 v[13] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
+                 hipb.n_stream_sync, live, mallocs, pinned, limbo, hipb.n_window, hipb.n_batched, hipb.n_fused};
+    for (u32 i = 0; out && i < n && i < 13; i++) out[i] = v[i];
+    return 13;
 }
 
 int thvm_hip_mfma_probe(u32 waves_per_cu, u32 iters, double *tflops) {
@@ -1289,6 +1449,21 @@ int thvm_hip_window_source(const UOpKernel *k, char *buf, u64 buflen) {
     size_t n = strlen(src);
     if (buf && buflen) snprintf(buf, buflen, "%s", src);
     free(src);
+    return (int)n;
+}
+
+int thvm_hip_epilogue_compile_check(const UOpKernel *producer, const UOpKernel *consumer, u32 o_leaf, char *errbuf,
+                                    u64 errlen) {
+    ensure_env();
+    char err[256] = {0};
+    char *src = producer && consumer ? dense_epilogue_source(producer, consumer, o_leaf, err, sizeof err) : NULL;
+    if (!src) {
+        if (errbuf && errlen) snprintf(errbuf, errlen, "%s", err[0] ? err : "no fused epilogue");
+        return -1;
+    }
+    long n = rtc_compile_only(src, err, sizeof err);
+    free(src);
+    if (n < 0 && errbuf && errlen) snprintf(errbuf, errlen, "%s", err);
     return (int)n;
 }
 

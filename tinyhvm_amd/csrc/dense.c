@@ -479,6 +479,23 @@ static void out_store_fn(const UOpKernel *k, const Contraction *ct, char *fb, si
           : k->out_dtype == DTYPE_U32 ? "st_u32" : "st_f32";
 }
 
+/* A fused epilogue (set only while a fused module is generated): the
+ * consumer's device function epi_, the main kernel's extra parameters for
+ * the consumer's buffers (q<b>, qc<b>) and the call made after every output
+ * store with the stored value v_ at output index o_. */
+static const char *g_epi_src, *g_epi_params, *g_epi_call;
+
+/* "st(p0, c0, idx, val);" or, with a fused epilogue, the same store followed
+ * by the consumer's epilogue for that output */
+static void emit_out_store(DSB *s, const char *indent, const char *st, const char *idx, const char *val) {
+    if (!g_epi_call) {
+        dsb_put(s, "%s%s(p0, c0, %s, %s);\n", indent, st, idx, val);
+        return;
+    }
+    dsb_put(s, "%s{ const u32 o_ = %s; const float v_ = %s; %s(p0, c0, o_, v_); %s; }\n", indent, idx, val, st,
+            g_epi_call);
+}
+
 /* Closes the epilogue opened by the caller (inside `if (m < M && n < N) {`
  * with the accumulator value c[v]): stores the result (or the split's partial
  * into the workspace), closes the kernel, and emits the split-K sum kernel. */
@@ -489,7 +506,6 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
     char fb[64];
     const char *st;
     out_store_fn(k, ct, fb, sizeof fb, &st);
-    const u32 M = ct->M, N = ct->N;
     if (pl->comb)
         /* the direct kernel's in-launch combine (the words taken into cb_) */
         dsb_put(s_, "        if (sl_ == nullptr) {\n"
@@ -506,8 +522,11 @@ static void emit_store_tail(DSB *sp, const UOpKernel *k, const Contraction *ct, 
         dsb_put(s_, "        ws[((unsigned long long)spl * N + n) * M + m] = c[v];\n");
     else if (pl->splits > 1)
         dsb_put(s_, "        ws[((unsigned long long)spl * M + m) * N + n] = c[v];\n");
-    else
-        dsb_put(s_, "        %s(p0, c0, gid_m(m) + gid_n(n), %s + c[v]);\n", st, fb);
+    else {
+        char val[96];
+        snprintf(val, sizeof val, "%s + c[v]", fb);
+        emit_out_store(s_, "        ", st, "gid_m(m) + gid_n(n)", val);
+    }
     dsb_put(s_, "      }\n    }\n  }\n}\n");
     emit_sum_kernel(s_, k, ct, pl);
 }
@@ -714,7 +733,7 @@ static void emit_skinny_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
     out_store_fn(k, ct, fb, sizeof fb, &st);
     dsb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", 64u * KW, pl->name);
     emit_params(s, k->n_leaves);
-    dsb_put(s, ", float* ws) {\n");
+    dsb_put(s, ", float* ws%s) {\n", g_epi_params ? g_epi_params : "");
     dsb_put(s,
             "  constexpr u32 M = %uu, N = %uu, K = %uu, KW = %uu, KCW = %uu, SKU = %uu;\n"
             "  __shared__ float bs_[K * N];\n"
@@ -802,9 +821,11 @@ static void emit_skinny_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
                    "    for (u32 n = 0; n < N; n++) acc[n] = acc[n] + part_[w][n][lane];\n");
     dsb_put(s, "  if (m < M) {\n"
                "    #pragma unroll\n"
-               "    for (u32 n = 0; n < N; n++) %s(p0, c0, gid_m(m) + gid_n(n), %s + acc[n]);\n"
-               "  }\n"
-               "}\n", st, fb);
+               "    for (u32 n = 0; n < N; n++)\n");
+    char val[96];
+    snprintf(val, sizeof val, "%s + acc[n]", fb);
+    emit_out_store(s, "      ", st, "gid_m(m) + gid_n(n)", val);
+    dsb_put(s, "  }\n}\n");
 }
 
 /* Direct kernel: a workgroup of 4 waves owns one 32x32 output block; the
@@ -817,7 +838,8 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
     const u32 blocks = pl->tiles_m * pl->tiles_n;
     dsb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", 64u * pl->nw, pl->name);
     emit_params(s, k->n_leaves);
-    dsb_put(s, pl->comb ? ", float* ws, unsigned long long* sl_) {\n" : ", float* ws) {\n");
+    if (pl->comb) dsb_put(s, ", float* ws, unsigned long long* sl_) {\n");
+    else dsb_put(s, ", float* ws%s) {\n", g_epi_params ? g_epi_params : "");
     dsb_put(s,
             "  constexpr u32 M = %uu, N = %uu, K = %uu, TN = %uu, BLOCKS = %uu, KCH = %uu, KU = %uu, NW = %uu;\n"
             "  const u32 lane = threadIdx.x & 63u, wave = threadIdx.x >> 6;\n"
@@ -1024,6 +1046,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
     DSB s = {0};
     const TileCfg *cf = &pl->cfg;
     dsb_put(&s, "%s\n", kgen_prelude());
+    if (g_epi_src) dsb_put(&s, "%s\n", g_epi_src);
     dsb_put(&s, "typedef float f32x16 __attribute__((ext_vector_type(16)));\n");
     emit_gid_fn(&s, "gid_m", ct->np, ct->pdiv, ct->pext);
     emit_gid_fn(&s, "gid_n", ct->nq, ct->qdiv, ct->qext);
@@ -1081,7 +1104,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
     }
     dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", GEMM_THREADS, pl->name);
     emit_params(&s, k->n_leaves);
-    dsb_put(&s, pl->pack ? ", float* ws, const float* pk) {\n" : ", float* ws) {\n");
+    dsb_put(&s, pl->pack ? ", float* ws, const float* pk%s) {\n" : ", float* ws%s) {\n", g_epi_params ? g_epi_params : "");
     dsb_put(&s,
             "  constexpr u32 BM = %u, BN = %u, BK = %u, LDA = BM + %uu, LDB = BN + %uu;\n"
             "  constexpr u32 M = %uu, N = %uu, K = %uu, TM = %uu, TN = %uu, TILES = %uu, KCH = %uu, SPLITS = %uu;\n"
@@ -1281,7 +1304,25 @@ typedef struct {
     GemmPlan plan;
     u32 M, N;
     CoForm co, co_sum;            /* co-launch forms of the main and split-K sum kernels */
+    u32 serial;                   /* unique in the process (entries move when the table grows) */
+    UOpKernel *kcopy;             /* the program, kept when its launch can take a fused epilogue */
 } DenseEntry;
+
+/* Modules of a contraction with the elementwise program that consumes its
+ * output fused into its epilogue (fn NULL: the pair was refused). */
+#define FUSED_MAX 128
+#define EPI_SOLO_MAX_LDS 8192u
+typedef struct {
+    u64 key;
+    hipModule_t mod;
+    hipFunction_t fn;
+    CoForm co;
+} FusedEntry;
+static struct {
+    FusedEntry e[FUSED_MAX];
+    u32 n;
+    u32 next_serial;
+} F;
 
 static struct {
     DenseEntry *tab;
@@ -1295,6 +1336,13 @@ static void meta_of(const UOpKernel *k, u32 *m) {
     m[0] = k->grid[0]; m[1] = k->grid[1]; m[2] = k->grid[2];
     m[3] = k->local_size; m[4] = k->out_dtype;
     for (u32 i = 0; i < k->n_leaves && i < FUSE_MAX_LEAVES; i++) m[5 + i] = k->leaf_dtypes[i];
+}
+
+/* Whether a plan's one launch writes every output once in an epilogue that
+ * can take a fused consumer: unsplit, no packed operand, f32 output, on the
+ * tiled, direct or row-per-lane kernel. */
+static int plan_takes_epilogue(const GemmPlan *pl, const UOpKernel *k) {
+    return pl->splits == 1 && !pl->comb && !pl->pack && pl->cfg.direct <= 2 && k->out_dtype == DTYPE_F32;
 }
 
 static DenseEntry *lookup(u64 key, const UOpKernel *k) {
@@ -1332,6 +1380,7 @@ static DenseEntry *insert(u64 key, const UOpKernel *k) {
     DenseEntry *e = &D.tab[p];
     memset(e, 0, sizeof *e);
     e->key = key;
+    e->serial = ++F.next_serial;
     e->n_ops = k->n_ops;
     e->n_leaves = k->n_leaves;
     meta_of(k, e->meta);
@@ -1868,6 +1917,10 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         e->M = ct.M;
         e->N = ct.N;
         e->is_dense = 1;
+        if (plan_takes_epilogue(&e->plan, k) && !hipb.no_fuse) {
+            e->kcopy = malloc(sizeof(UOpKernel));
+            if (e->kcopy) memcpy(e->kcopy, k, sizeof(UOpKernel));
+        }
         if (hipb.verbose)
             fprintf(stderr, "tinyhvm-hip: dense %s M=%u N=%u K=%u tile %s splits=%u kperm=%u\n", e->plan.name, ct.M,
                     ct.N, ct.K, e->plan.cfg.tag, e->plan.splits, e->plan.kp.on ? e->plan.kp.E : 0);
@@ -1923,10 +1976,19 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     hbm_add(&hm, ws ? (void *)ws : ptrs[0], ws ? wsb : pool_bytes(out_buf), 1);
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++)
         hbm_add(&hm, pool_ptr(leaf_bufs[i]), pool_bytes(leaf_bufs[i]), 0);
-    if (e->plan.pack ||
-        !hipb_hold(&e->co, e->fn, tiles, e->plan.splits, params, &hm, sl != NULL, sl ? (int)(2 * nb + 1) : -1,
-                   sl ? (u64)e->plan.splits * mn : 0))
+    int held = !e->plan.pack && hipb_hold(&e->co, e->fn, tiles, e->plan.splits, params, &hm, sl != NULL,
+                                          sl ? (int)(2 * nb + 1) : -1, sl ? (u64)e->plan.splits * mn : 0);
+    /* a larger launch that an elementwise consumer may still fuse into is
+     * held alone if its workgroups use little LDS (the fused module adds no
+     * LDS; big LDS tiles are the headline GEMMs, left as they are) */
+    if (!held && e->kcopy && e->co.src && e->co.lds <= EPI_SOLO_MAX_LDS)
+        held = hipb_hold_solo(&e->co, e->fn, tiles, e->plan.splits, params, &hm);
+    if (!held) {
         if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, threads, params)) return 0;
+    } else if (e->kcopy && !ws) {
+        /* held: the next dispatch may fuse into its epilogue */
+        hipb_hold_tag(key, e->serial, out_buf);
+    }
     if (ws) {
         void *p2[] = {&ptrs[0], &counts[0], &ws};
         const u64 per_block = sum_per_wave(&e->plan, mn) ? 4 : 64;
@@ -1951,11 +2013,154 @@ void dense_shutdown(void) {
             if (D.tab[i].is_dense) HIPB_CHECK(hipModuleUnload(D.tab[i].mod));
             co_form_free(&D.tab[i].co);
             co_form_free(&D.tab[i].co_sum);
+            free(D.tab[i].kcopy);
             free(D.tab[i].ops);
         }
         free(D.tab);
     }
+    for (u32 i = 0; i < F.n; i++) {
+        if (F.e[i].fn) HIPB_CHECK(hipModuleUnload(F.e[i].mod));
+        co_form_free(&F.e[i].co);
+    }
+    F.n = 0;
     scratch_release(&D.ws);
     scratch_release(&D.pk);
     memset(&D, 0, sizeof D);
+}
+
+
+/* Whether the elementwise program `c` can be the fused epilogue of a
+ * contraction with M x N outputs that it reads as leaf buffer o_leaf (1 +
+ * leaf): no loop, one STORE at gid, that leaf read only at gid and as f32,
+ * as many outputs as the contraction. */
+static int epi_fits(u32 M, u32 N, const UOpKernel *c, u32 o_leaf) {
+    if (!c || o_leaf == 0 || o_leaf > c->n_leaves || c->n_leaves > FUSE_MAX_LEAVES || c->n_ops == 0 ||
+        c->n_ops > KOP_MAX || c->leaf_dtypes[o_leaf - 1] != DTYPE_F32)
+        return 0;
+    const u32 total = c->local_size > 0 ? c->grid[0] : c->grid[0] * c->grid[1] * c->grid[2];
+    if ((u64)total != (u64)M * N) return 0;
+    Aff *aff = calloc(c->n_ops, sizeof(Aff));
+    if (!aff) return 0;
+    DCtx dc = {c, total, 1, -1, aff};
+    analyze_aff(&dc);
+    int ok = 1, stores = 0;
+    for (u32 i = 0; i < c->n_ops && ok; i++) {
+        const KOp *op = &c->ops[i];
+        if (op->type == KOP_RANGE || op->type == KOP_ENDRANGE || op->type == KOP_ACC_INIT || op->type == KOP_ACC)
+            ok = 0;
+        else if (op->type == KOP_STORE) {
+            stores++;
+            ok = op->arg[0] < c->n_ops && aff_is_gid(&dc, &aff[op->arg[0]]);
+        } else if (op->type == KOP_LOAD && op->imm.u == o_leaf)
+            ok = op->arg[0] < c->n_ops && aff_is_gid(&dc, &aff[op->arg[0]]);
+    }
+    free(aff);
+    return ok && stores == 1;
+}
+
+/* The fused module's source: the contraction's kernel (plan pl, its name
+ * replaced by `name`) with c's program, a device function over c's own
+ * buffers (the kernel's extra parameters q<b>, qc<b>), run by the lane that
+ * stores each output on the value it stores. */
+static char *epi_source(const UOpKernel *k, const Contraction *ct, const GemmPlan *pl0, const UOpKernel *c,
+                        u32 o_leaf, const char *name, char *err, size_t errlen) {
+    char *epi = malloc(65536), params[2048], call[2048];
+    if (!epi || kgen_epilogue(c, o_leaf, epi, 65536) < 0) {
+        free(epi);
+        snprintf(err, errlen, "epilogue generation failed");
+        return NULL;
+    }
+    size_t wp = 0, wc = (size_t)snprintf(call, sizeof call, "epi_(o_, v_");
+    for (u32 b = 0; b <= c->n_leaves; b++) {
+        wp += (size_t)snprintf(params + wp, sizeof params - wp, ", char* q%u", b);
+        wc += (size_t)snprintf(call + wc, sizeof call - wc, ", q%u", b);
+    }
+    for (u32 b = 0; b <= c->n_leaves; b++) {
+        wp += (size_t)snprintf(params + wp, sizeof params - wp, ", u32 qc%u", b);
+        wc += (size_t)snprintf(call + wc, sizeof call - wc, ", qc%u", b);
+    }
+    snprintf(call + wc, sizeof call - wc, ")");
+    GemmPlan pl = *pl0;
+    snprintf(pl.name, sizeof pl.name, "%s", name);
+    g_epi_src = epi;
+    g_epi_params = params;
+    g_epi_call = call;
+    char *src = gen_gemm_source(k, ct, &pl, err, errlen);
+    g_epi_src = g_epi_params = g_epi_call = NULL;
+    free(epi);
+    return src;
+}
+
+/* The contraction (key, serial) held for launch with the elementwise program
+ * `c`, which reads its output as leaf buffer o_leaf, fused into its
+ * epilogue (the same arithmetic as the two launches). Returns 1 with the
+ * fused module's function and co-launch form, 0 when the pair does not fuse
+ * (remembered, like the modules, per pair). */
+int dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunction_t *fn, CoForm *co) {
+    if (hipb.no_fuse || !c || o_leaf == 0 || o_leaf > c->n_leaves) return 0;
+    u64 fk = key ^ (uop_signature(c) * 0x9E3779B97F4A7C15ull) ^ ((u64)o_leaf << 56) ^ ((u64)serial << 40);
+    if (!fk) fk = 1;
+    for (u32 i = 0; i < F.n; i++)
+        if (F.e[i].key == fk) {
+            if (!F.e[i].fn) return 0;
+            *fn = F.e[i].fn;
+            *co = F.e[i].co;
+            return 1;
+        }
+    if (F.n >= FUSED_MAX) return 0;
+    FusedEntry *fe = &F.e[F.n++];
+    memset(fe, 0, sizeof *fe);
+    fe->key = fk;
+    DenseEntry *e = NULL;
+    for (u32 i = 0; D.tab && i < D.cap && !e; i++)
+        if (D.tab[i].key == key && D.tab[i].serial == serial && D.tab[i].is_dense && D.tab[i].kcopy) e = &D.tab[i];
+    Contraction ct;
+    if (!e || !epi_fits(e->M, e->N, c, o_leaf) || !recognize(e->kcopy, &ct)) return 0;
+    char name[48], err[256] = {0};
+    snprintf(name, sizeof name, "thvm_gemmep_%08x", (u32)(fk & 0xFFFFFFFFu));
+    char *src = epi_source(e->kcopy, &ct, &e->plan, c, o_leaf, name, err, sizeof err);
+    if (!src) return 0;
+    if (hipb.dump_src) fprintf(stderr, "---- dense kernel with fused epilogue ----\n%s\n", src);
+    if (!rtc_build_module(src, &fe->mod, err, sizeof err)) {
+        fprintf(stderr, "tinyhvm-hip: fused epilogue build failed: %s\n", err);
+        free(src);
+        return 0;
+    }
+    hipFunction_t f = NULL;
+    if (hipModuleGetFunction(&f, fe->mod, name) != hipSuccess ||
+        !co_form_make(&fe->co, src, name, dense_threads(&e->plan), f) ||
+        fe->co.np != e->co.np + 2u * (c->n_leaves + 1u)) {
+        HIPB_CHECK(hipModuleUnload(fe->mod));
+        co_form_free(&fe->co);
+        free(src);
+        return 0;
+    }
+    free(src);
+    fe->fn = f;
+    hipb.n_compile++;
+    *fn = f;
+    *co = fe->co;
+    return 1;
+}
+
+/* Device-free: the fused module of contraction k and elementwise program c
+ * (reading k's output as leaf buffer o_leaf) when the pair fuses, else NULL
+ * with the reason in err. */
+char *dense_epilogue_source(const UOpKernel *k, const UOpKernel *c, u32 o_leaf, char *err, size_t errlen) {
+    Contraction ct;
+    if (!dense_analyze(k, NULL, NULL, NULL, NULL) || !recognize(k, &ct)) {
+        snprintf(err, errlen, "not a matrix-core contraction");
+        return NULL;
+    }
+    GemmPlan pl;
+    make_plan(&ct, &pl, uop_signature(k));
+    if (!plan_takes_epilogue(&pl, k)) {
+        snprintf(err, errlen, "the contraction's plan takes no epilogue");
+        return NULL;
+    }
+    if (!epi_fits(ct.M, ct.N, c, o_leaf)) {
+        snprintf(err, errlen, "not an elementwise consumer of the output at its own index");
+        return NULL;
+    }
+    return epi_source(k, &ct, &pl, c, o_leaf, "thvm_gemmep_check", err, errlen);
 }

@@ -30,6 +30,9 @@
     } while (0)
 
 /* ---------------- global state ---------------- */
+
+/* host-time categories of THVM_HIP_HOST_PROFILE */
+enum { HP_DISPATCH = 0, HP_LAUNCH, HP_SIGNATURE, HP_POOL, HP_WRITE, HP_N };
 typedef struct {
     int initialized;
     int device;
@@ -57,6 +60,7 @@ typedef struct {
     int dense_noskinny_blocks; /* THVM_HIP_DENSE_NOSKBLK: the row-per-lane kernel walks K per k */
     int dense_nored;         /* THVM_HIP_DENSE_NORED: no outer-product reduction kernel */
     int dense_nocomb;        /* THVM_HIP_DENSE_NOCOMB: split-K partials always through a sum kernel */
+    int no_fuse;             /* THVM_HIP_NO_FUSE: no elementwise consumer fused into a contraction's epilogue */
     u32 direct_min_chunk;    /* THVM_HIP_DIRECT_MIN_CHUNK: shortest K chunk of a direct-kernel split (0: chosen) */
     int dense_pack;          /* THVM_HIP_DENSE_PACK: pack wherever the layout allows (tests) */
     u32 dense_tile;          /* THVM_HIP_DENSE_TILE: 0 chosen, 1 128x128, 2 64x64, 3 256x32, 4 32x256, 5 direct,
@@ -68,6 +72,9 @@ typedef struct {
     u64 n_fallback;          /* dispatches run on the KOp interpreter */
     u64 n_window;            /* dispatches run on the window-max and run-sum kernels */
     u64 n_batched;           /* dispatches issued inside a batched launch */
+    u64 n_fused;             /* elementwise dispatches run as a contraction's fused epilogue */
+    int host_profile;        /* THVM_HIP_HOST_PROFILE: host time per category, printed by profile_report */
+    u64 hp_ns[HP_N], hp_calls[HP_N];
     int no_batch;            /* THVM_HIP_NO_BATCH: launch every dispatch on its own */
     u64 n_stream_sync;       /* host waits on the stream (buf_read, synchronize, ...) */
     hipModule_t static_mod;  /* precompiled kernels */
@@ -100,6 +107,9 @@ void pool_pins_release(PoolPins *pins);
 void pool_pin_stats(u32 *pinned, u32 *limbo);
 /* hipStreamSynchronize on the backend's stream, counted */
 hipError_t hipb_stream_wait(void);
+/* Host clock for THVM_HIP_HOST_PROFILE (0 when it is off). */
+u64 hipb_hp_now(void);
+void hipb_hp_add(int cat, u64 t0);
 /* Issues the dispatches held for a batched launch; every operation put on
  * the stream calls it first, so the stream sees work in program order. */
 void hipb_before_stream(void);
@@ -172,6 +182,7 @@ void kgen_free(KGenResult *r);
 int  kgen_validate(const UOpKernel *k, char *err, size_t errlen);
 const char *kgen_prelude(void);
 int  kgen_alu_expr(u32 uop, u32 aux, const char *a, const char *b, char *out, size_t n);
+int  kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen);
 int  kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
                     char *out, size_t outlen);
 
@@ -222,6 +233,16 @@ void hbm_add(HbMem *m, const void *p, u64 bytes, int write);
  * slice of the area. */
 int  hipb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
                int resident, int comb_param, u64 comb_words);
+/* Holds a launch (of any grid size) only so that the next dispatch can fuse
+ * into it (hipb_hold_tag); it joins no batch. Returns 1 if held. */
+int  hipb_hold_solo(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m);
+/* Marks the launch just held as a contraction (dense entry key, serial)
+ * writing buffer out_buf that an elementwise consumer may fuse into. */
+void hipb_hold_tag(u64 key, u32 serial, u32 out_buf);
+/* dense.c: the contraction (key, serial) with the elementwise program c,
+ * which reads its output as leaf buffer o_leaf, fused into its epilogue */
+int  dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunction_t *fn, CoForm *co);
+char *dense_epilogue_source(const UOpKernel *k, const UOpKernel *c, u32 o_leaf, char *err, size_t errlen);
 
 /* ---------------- rtc / cache ---------------- */
 typedef struct {

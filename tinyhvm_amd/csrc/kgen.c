@@ -1005,8 +1005,18 @@ const char *kgen_prelude(void) { return PRELUDE; }
  * the body of a device function: GID reads `gid_expr`, the top-level RANGE
  * reads `r_expr`. Buffers are the kernel parameters p<i>/c<i>. Returns the
  * number of bytes written, or -1 if an op cannot be emitted this way. */
+static int emit_cone_subst(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
+                           u32 subst_leaf, const char *subst_expr, char *out, size_t outlen);
+
 int kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
                    char *out, size_t outlen) {
+    return emit_cone_subst(k, cone, gid_expr, r_expr, ~0u, NULL, out, outlen);
+}
+
+/* kgen_emit_cone, with every LOAD of leaf buffer subst_leaf (1 + leaf)
+ * reading subst_expr instead */
+static int emit_cone_subst(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
+                           u32 subst_leaf, const char *subst_expr, char *out, size_t outlen) {
     SB sb = {0};
     char a[96], b[96], fb[64];
     for (u32 i = 0; i < k->n_ops; i++) {
@@ -1036,6 +1046,7 @@ int kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, con
         }
         case KOP_LOAD: {
             u32 bi = op->imm.u;
+            if (bi == subst_leaf) { sb_put(&sb, "  const float f%u = %s;\n", i, subst_expr); break; }
             if (bi > k->n_leaves) { sb_put(&sb, "  const float f%u = 0.0f;\n", i); break; }
             u32 dt = bi == 0 ? k->out_dtype : k->leaf_dtypes[bi - 1];
             sb_put(&sb, "  const float f%u = %s(p%u, c%u, %s);\n", i, dt_ld(dt), bi, bi, UA(op->arg[0], fa));
@@ -1080,6 +1091,49 @@ int kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, con
         return 0;
     }
     size_t n = strlen(sb.p);
+    if (n + 1 > outlen) { free(sb.p); return -1; }
+    memcpy(out, sb.p, n + 1);
+    free(sb.p);
+    return (int)n;
+}
+
+/* An elementwise program as the epilogue of the kernel that produces one of
+ * its leaves: a device function epi_(gid_, v_, p0.., c0..) that computes the
+ * program for output gid_ with every load of leaf buffer o_leaf (1 + leaf)
+ * taking v_ (the value the producer just stored there, at gid_) and stores
+ * the result as the program's STORE does. The program has no loop and one
+ * STORE; the caller checks that its loads of o_leaf and its STORE index are
+ * gid itself. Buffers are the function's own p<b>/c<b> (0: its output).
+ * Returns the length written, or -1. */
+int kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen) {
+    u8 cone[KOP_MAX];
+    i32 st = -1;
+    if (k->n_ops == 0 || k->n_ops > KOP_MAX) return -1;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOpType t = k->ops[i].type;
+        if (t == KOP_RANGE || t == KOP_ENDRANGE || t == KOP_ACC_INIT || t == KOP_ACC) return -1;
+        if (t == KOP_STORE) {
+            if (st >= 0) return -1;
+            st = (i32)i;
+        }
+        cone[i] = t != KOP_STORE;
+    }
+    if (st < 0) return -1;
+    const KOp *so = &k->ops[st];
+    if (so->arg[0] >= k->n_ops || so->arg[1] >= k->n_ops) return -1;
+    char body[32768];
+    if (emit_cone_subst(k, cone, "gid_", "0u", o_leaf, "v_", body, sizeof body) < 0) return -1;
+    SB sb = {0};
+    sb_put(&sb, "__device__ __forceinline__ void epi_(u32 gid_, float v_");
+    for (u32 b = 0; b <= k->n_leaves; b++) sb_put(&sb, ", char* p%u", b);
+    for (u32 b = 0; b <= k->n_leaves; b++) sb_put(&sb, ", u32 c%u", b);
+    const int fv = op_is_float(k->ops[so->arg[1]].type);
+    char v[48];
+    if (fv) snprintf(v, sizeof v, "f%u", so->arg[1]);
+    else snprintf(v, sizeof v, "(float)n%u", so->arg[1]);
+    sb_put(&sb, ") {\n%s  %s(p0, c0, n%u, %s);\n}\n", body, dt_st(k->out_dtype), so->arg[0], v);
+    if (!sb.p) return -1;
+    const size_t n = strlen(sb.p);
     if (n + 1 > outlen) { free(sb.p); return -1; }
     memcpy(out, sb.p, n + 1);
     free(sb.p);

@@ -38,7 +38,16 @@ static u64 mix(u64 h, u64 v) {
     return h ^ (h >> 33);
 }
 
+static u64 uop_signature_(const UOpKernel *k);
+
 u64 uop_signature(const UOpKernel *k) {
+    const u64 t0 = hipb_hp_now();
+    const u64 h = uop_signature_(k);
+    hipb_hp_add(HP_SIGNATURE, t0);
+    return h;
+}
+
+static u64 uop_signature_(const UOpKernel *k) {
     u64 h = 0x746876686970ull;
     h = mix(h, k->n_ops);
     h = mix(h, k->n_leaves);
