@@ -444,6 +444,21 @@ static int hb_try_epilogue(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, cons
     if (!e || out_buf == e->fz_out || !pool_ptr(out_buf)) return 0;
     for (u32 j = 0; j < k->n_leaves; j++)
         if (leaf_bufs[j] == out_buf || (leaf_bufs[j] && !pool_ptr(leaf_bufs[j]))) return 0;
+    const u64 fz = e->fz_key;
+    const u32 fzs = e->fz_serial, fzo = e->fz_out;
+    hipFunction_t fn;
+    CoForm co;
+    if (!dense_epilogue(fz, fzs, k, o_leaf, &fn, &co)) return 0;
+    /* its other inputs current on the device (the epilogue reads every leaf
+     * from memory): pending host writes are copied on the stream ahead of
+     * the held launches, which do not read them (if one does, it goes out
+     * first and nothing fuses) */
+    for (u32 j = 0; j < k->n_leaves; j++)
+        if (leaf_bufs[j] != fzo) pool_sync_device(leaf_bufs[j]);
+    e = NULL;
+    for (u32 i = 0; i < HB.n && !e; i++)
+        if (HB.ent[i].fz_key == fz && HB.ent[i].fz_serial == fzs && HB.ent[i].fz_out == fzo) e = &HB.ent[i];
+    if (!e) return 0;
     HbMem m;
     m.n = 0;
     hbm_add(&m, pool_ptr(out_buf), pool_bytes(out_buf), 1);
@@ -451,16 +466,12 @@ static int hb_try_epilogue(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, cons
         if (leaf_bufs[j] != e->fz_out) hbm_add(&m, pool_ptr(leaf_bufs[j]), pool_bytes(leaf_bufs[j]), 0);
     for (u32 i = 0; i < HB.n; i++)
         if (hbm_clash(&m, &HB.ent[i].m)) return 0;
-    hipFunction_t fn;
-    CoForm co;
-    if (!dense_epilogue(e->fz_key, e->fz_serial, k, o_leaf, &fn, &co)) return 0;
     /* the consumer's buffers (the generated kernel's p<b>, c<b>) after the
      * contraction's parameters */
     u32 off = 0;
     for (u32 j = 0; j < e->co.np; j++) off = hb_arg_off(off, e->co.psz[j]) + e->co.psz[j];
     const u32 nb = k->n_leaves + 1;
     if (hb_arg_off(off, 8) + 8u * nb + 4u * nb > HB_ARG_BYTES) return 0;
-    for (u32 j = 0; j < k->n_leaves; j++) pool_sync_device(leaf_bufs[j]);
     for (u32 b = 0; b < nb; b++) {
         void *p = b == 0 ? pool_ptr(out_buf) : leaf_bufs[b - 1] ? pool_ptr(leaf_bufs[b - 1]) : hipb.dummy;
         off = hb_arg_off(off, 8);

@@ -560,7 +560,8 @@ void pool_mark_device_write(u32 id) {
 
 static u8 *stage_reserve(u64 n);
 
-/* Copy a pending host mirror to the device (stream ordered). */
+/* Copy a pending host mirror to the device (stream ordered; ahead of held
+ * launches that do not touch the buffer). */
 void pool_sync_device(u32 id) {
     HipbBuf *b = pool_get(id);
     if (!b || !b->dev_stale) return;
