@@ -59,6 +59,11 @@ WL = os.path.join(ROOT, "tinyhvm_amd", "workloads")
 F4096 = 2 * 4096 ** 3
 FCONV = 2 * 64 * 64 * 64 * 56 * 56 * 9          # one 3x3 64->64 conv over [64,64,56,56]
 TAG_UOP, TAG_RS = 7, 8
+TAG_ALLOC = 1
+# buffer ids the backend hands out before a pool_reset recycles them (the
+# engine's epoch table ends there, src/tinyhvm.h:720); every replay of a step
+# allocates its temporaries afresh
+MAX_BUFFER_IDS = 16383
 SKIP_READS = 1
 
 WORKLOADS = {
@@ -230,6 +235,12 @@ def cpu_baseline(spec, wl):
     return out
 
 
+def dispatch_count(L):
+    c = (C.c_uint64 * 13)()
+    L.thvm_hip_counters(c, 13)
+    return c[0]
+
+
 def run_workload(L, name, steps, warmup, want_cpu):
     wl = WORKLOADS[name]
     be = L.thvm_hip_backend()
@@ -240,6 +251,13 @@ def run_workload(L, name, steps, warmup, want_cpu):
     lo = L.thvm_trace_find_mark(t, wl["step"][0].encode(), 0)
     hi = n if wl["step"][1] is None else L.thvm_trace_find_mark(t, wl["step"][1].encode(), lo)
     assert 0 <= lo < hi <= n
+    allocs = sum(1 for j in range(0, hi) if L.thvm_trace_tag(t, j) == TAG_ALLOC)
+    step_allocs = sum(1 for j in range(lo, hi) if L.thvm_trace_tag(t, j) == TAG_ALLOC)
+    replays = max(warmup, 1) + 2 * steps + (1 if wl.get("graph") else 0)
+    if allocs + replays * step_allocs > MAX_BUFFER_IDS:
+        raise SystemExit("%s: %d step replays need %d buffer ids, more than the %d the backend holds without a "
+                         "pool reset; use fewer --steps" % (name, replays, allocs + replays * step_allocs,
+                                                            MAX_BUFFER_IDS))
     L.thvm_trace_replay(t, be, 0, lo, 0)           # inputs: allocate and upload (untimed)
     L.thvm_trace_drop_gen_cache(t)
     assert L.thvm_hip_synchronize() == 0
@@ -250,6 +268,8 @@ def run_workload(L, name, steps, warmup, want_cpu):
     print("%s: setup + warmup %.1fs, step = records [%d, %d)" % (name, time.perf_counter() - t_c, lo, hi),
           file=sys.stderr, flush=True)
     hip = Hip(L.thvm_hip_stream(), L.thvm_hip_flush)
+    n_disp = sum(1 for j in range(lo, hi) if L.thvm_trace_tag(t, j) in (TAG_UOP, TAG_RS))
+    d0 = dispatch_count(L)
     # pass 1: whole steps (the reported throughput)
     e0, e1 = hip.event(), hip.event()
     t0 = time.perf_counter()
@@ -259,6 +279,8 @@ def run_workload(L, name, steps, warmup, want_cpu):
     hip.record(e1)
     assert L.thvm_hip_synchronize() == 0
     wall = time.perf_counter() - t0
+    # every dispatch of every step ran (none skipped for a missing buffer)
+    assert dispatch_count(L) - d0 == steps * n_disp, "%s: dispatches skipped" % name
     gpu_ms = hip.ms(e0, e1)
     step_s = wall / steps
     # pass 2: events around each listed dispatch on the backend stream

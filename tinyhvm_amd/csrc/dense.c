@@ -2138,6 +2138,9 @@ int dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunct
     free(src);
     fe->fn = f;
     hipb.n_compile++;
+    if (hipb.verbose)
+        fprintf(stderr, "tinyhvm-hip: %s = %s + epilogue thvm_%s_%08x\n", name, e->plan.name, "ew",
+                (u32)(uop_signature(c) & 0xFFFFFFFFu));
     *fn = f;
     *co = fe->co;
     return 1;
