@@ -219,6 +219,18 @@ int  thvm_hip_window_compile_check(const UOpKernel *kernel, char *errbuf, u64 er
 int  thvm_hip_epilogue_compile_check(const UOpKernel *producer, const UOpKernel *consumer, u32 o_leaf,
                                      char *errbuf, u64 errlen);
 
+/* A loop-free dispatch that reads a held loop-free program's output at its
+ * own gid runs fused after it, as one program over both programs' buffers
+ * that writes both outputs (its STOREs name their buffer in imm.u, like the
+ * engine's KOp STORE, src/tinyhvm.h:683). The merged program of producer p
+ * (buffer ids pb: output, then leaves) and consumer c (output c_out, leaves
+ * c_leaves), as the backend builds it, without a device: returns 1 with m
+ * and its buffer ids mb (output, then m->n_leaves leaves) filled, 0 when
+ * the pair does not fuse. A diagnostic with no counterpart in the
+ * reference. */
+int  thvm_hip_chain_merge(const UOpKernel *p, const u32 *pb, const UOpKernel *c, u32 c_out, const u32 *c_leaves,
+                          UOpKernel *m, u32 *mb);
+
 /* Independent dispatches held back and issued as one launch: the batch
  * kernel of n generated modules (srcs[i] as the generators above return it,
  * names[i] its main kernel, threads[i] its workgroup size, grid[2i], grid[2i+1]

@@ -1,5 +1,6 @@
-"""Batched launches of independent generated kernels, and elementwise
-kernels fused into the epilogue of the contraction they follow.
+"""Batched launches of independent generated kernels, elementwise kernels
+fused into the epilogue of the contraction they follow, and loop-free
+kernels merged with the loop-free kernel whose output they read.
 
 The backend holds back launches of generated kernels and issues independent
 ones together as one launch of a batch kernel. In a LeNet-5 training step at
@@ -25,6 +26,50 @@ pytestmark = pytest.mark.gpu
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 TRACE = os.path.join(ROOT, "tinyhvm_amd", "workloads", "lenet_b256.trc")
 PARAMS = range(2, 12)          # trace ids of W1, b1, ..., W5, b5
+
+
+CONV = os.path.join(ROOT, "tinyhvm_amd", "workloads", "convblock_b64.trc")
+
+
+def _run_all(path, m0, m1, no_fuse):
+    """Replays [m0, m1) of a trace (the part before m0 untimed) in a fresh
+    backend; returns every buffer live at the end (trace id -> bytes) and
+    the number of dispatches fused into a held launch."""
+    old = os.environ.get("THVM_HIP_NO_FUSE")
+    os.environ["THVM_HIP_NO_FUSE"] = "1" if no_fuse else "0"
+    L = _lib.lib()
+    try:
+        assert L.thvm_hip_init() == 0
+        recs = trace.read_trace(path)
+        sizes = {r.f["id"]: r.f["bytes"] for r in recs if r.tag == trace.ALLOC}
+        be = L.thvm_hip_backend()
+        t = L.thvm_trace_load(path.encode())
+        assert t
+        lo = L.thvm_trace_find_mark(t, m0.encode(), 0)
+        hi = L.thvm_trace_find_mark(t, m1.encode(), lo) if m1 else L.thvm_trace_count(t)
+        L.thvm_trace_replay(t, be, 0, lo, 0)
+        before = (C.c_uint64 * 13)()
+        L.thvm_hip_counters(before, 13)
+        L.thvm_trace_replay(t, be, lo, hi, 1)
+        assert L.thvm_hip_synchronize() == 0
+        after = (C.c_uint64 * 13)()
+        assert L.thvm_hip_counters(after, 13) == 13
+        out = {}
+        for tid, n in sizes.items():
+            live = L.thvm_trace_live_id(t, tid)
+            if live:
+                buf = (C.c_uint8 * n)()
+                L.thvm_hip_buf_read(live, buf, n)
+                out[tid] = bytes(buf)
+        L.thvm_trace_release(t, be)
+        L.thvm_trace_free(t)
+        return out, after[12] - before[12]
+    finally:
+        L.thvm_hip_shutdown()
+        if old is None:
+            os.environ.pop("THVM_HIP_NO_FUSE", None)
+        else:
+            os.environ["THVM_HIP_NO_FUSE"] = old
 
 
 def _step(no_batch, no_fuse=False):
@@ -86,3 +131,20 @@ def test_fused_epilogues_match_separate_launches():
     assert n_fused >= 5, "only %d epilogues were fused" % n_fused
     bad = [tid for tid in PARAMS if separate[tid] != fused[tid]]
     assert not bad, "parameters %s differ between fused and separate launches" % bad
+
+
+def test_chained_elementwise_match_separate_launches():
+    """Loop-free dispatches that read a held loop-free program's output at
+    their own gid run merged with it (one launch writing both outputs): in
+    the conv block at [64,64,56,56], batchnorm's variance and inverse
+    deviation, the normalisation with its scale and shift, and the pooling
+    backward's routing with the product by the scale. Every buffer live
+    after the forward and backward step is bit for bit that of
+    THVM_HIP_NO_FUSE=1, and those three dispatches were fused."""
+    sep, n_sep = _run_all(CONV, "conv.fwd", None, no_fuse=True)
+    fused, n_fused = _run_all(CONV, "conv.fwd", None, no_fuse=False)
+    assert n_sep == 0
+    assert n_fused >= 3, "only %d dispatches were fused" % n_fused
+    assert sep.keys() == fused.keys()
+    bad = [tid for tid in sep if sep[tid] != fused[tid]]
+    assert not bad, "buffers %s differ between fused and separate launches" % bad

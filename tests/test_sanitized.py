@@ -57,7 +57,7 @@ def test_program_analysis_sanitized(tmp_path):
     if not all(os.path.exists(o) for o in objs):
         objs = build.build_hip_objects()
     exe = str(tmp_path / "analyze_all")
-    srcs = [os.path.join(CSRC, f) for f in ("backend.c", "pool.c", "kgen.c", "rtc.c", "affine.c", "dense.c", "window.c", "replay.c")]
+    srcs = [os.path.join(CSRC, f) for f in ("backend.c", "pool.c", "kgen.c", "rtc.c", "affine.c", "dense.c", "window.c", "chain.c", "replay.c")]
     _build(exe, srcs + [blob, os.path.join(CPU, "analyze_all.c")] + objs,
            ["-L" + os.path.join(ROCM, "lib"), "-lamdhip64", "-lhiprtc", "-lstdc++", "-lpthread", "-lm",
             "-Wl,-rpath," + os.path.join(ROCM, "lib")])

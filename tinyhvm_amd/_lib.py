@@ -75,6 +75,8 @@ def lib():
         "thvm_hip_window_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
         "thvm_hip_mfma_probe": (C.c_int, [u32, u32, C.POINTER(C.c_double)]),
         "thvm_hip_flush": (None, []),
+        "thvm_hip_chain_merge": (C.c_int, [C.POINTER(abi.UOpKernel), PU32, C.POINTER(abi.UOpKernel), u32,
+                                           PU32, C.POINTER(abi.UOpKernel), PU32]),
         "thvm_hip_epilogue_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), C.POINTER(abi.UOpKernel), u32, cp,
                                                       u64]),
         "thvm_hip_batch_compile_check": (C.c_int, [C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), PU32, PU32, u32,
@@ -114,7 +116,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_kernel_lanes", "thvm_hip_compile_check",
     "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
     "thvm_hip_window_analyze", "thvm_hip_window_source", "thvm_hip_window_compile_check",
-    "thvm_hip_batch_compile_check", "thvm_hip_mfma_probe", "thvm_hip_flush", "thvm_hip_epilogue_compile_check",
+    "thvm_hip_batch_compile_check", "thvm_hip_mfma_probe", "thvm_hip_flush", "thvm_hip_epilogue_compile_check", "thvm_hip_chain_merge",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
     "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",
@@ -153,6 +155,18 @@ def batch_compile_check(items):
     if r < 0:
         raise ValueError(err.value.decode())
     return r
+
+
+def chain_merge(p: abi.UOpKernel, pb, c: abi.UOpKernel, c_out: int, c_leaves):
+    """The merged program of loop-free p (buffer ids pb: output, leaves)
+    followed by c (output c_out, leaves c_leaves): (m, mb), or None when
+    the pair does not fuse."""
+    W = C.c_uint32 * (1 + abi.FUSE_MAX_LEAVES)
+    m = abi.UOpKernel()
+    mb, pbv, clv = W(), W(*pb), W(*c_leaves)
+    if not lib().thvm_hip_chain_merge(C.byref(p), pbv, C.byref(c), c_out, clv, C.byref(m), mb):
+        return None
+    return m, list(mb[:1 + m.n_leaves])
 
 
 def epilogue_compile_check(producer: abi.UOpKernel, consumer: abi.UOpKernel, o_leaf: int):

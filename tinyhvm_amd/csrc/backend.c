@@ -104,6 +104,10 @@ typedef struct {
     u64 fz_key;            /* a contraction an elementwise consumer may fuse into (0: none) */
     u32 fz_serial, fz_out; /* ... its dense entry and its output buffer */
     int solo;              /* held only for a fused epilogue: joins no batch */
+    const ChainInfo *ch;   /* a loop-free program an elementwise consumer may fuse after (NULL: none) */
+    u32 ch_bufs[1 + FUSE_MAX_LEAVES]; /* ... its buffers (output, leaves) */
+    u64 ch_seq;            /* ... the pool's host-write clock when it was held */
+    u32 ch_nb;
 } HbEnt;
 static struct {
     HbEnt ent[HB_MAX];
@@ -346,6 +350,7 @@ static const char *hb_joins(const HbEnt *h) {
         resident |= o->resident;
     }
     if (lds > HB_MAX_LDS) return "LDS";
+    if ((u64)blocks * T >= (1ull << 32)) return "grid size";
     if (resident && (u64)blocks * (T / 64u) > hipb_resident_waves()) return "residency";
     return NULL;
 }
@@ -363,10 +368,18 @@ int hipb_hold_solo(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *con
     return hb_hold(cf, fn, gx, gy, params, m, 0, -1, 0, 1);
 }
 
+/* A loop-free generated program of any grid size: held (and batched like
+ * the small ones) so that a consumer of its output can fuse after it. */
+static int hb_hold_large(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m) {
+    if (hipb.no_fuse) return 0;
+    return hb_hold(cf, fn, gx, gy, params, m, 0, -1, 0, 2);
+}
+
 static int hb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
                    int resident, int comb_param, u64 comb_words, int solo) {
     if (!cf || !cf->src || hipb.no_batch || hipb.noalloc || hipb.sync_each || HB.flushing) return 0;
-    if (gx == 0 || gy == 0 || (!solo && (u64)gx * gy > HB_MAX_BLOCKS) || cf->threads == 0 || cf->threads % 64u ||
+    if (gx == 0 || gy == 0 || (!solo && (u64)gx * gy > HB_MAX_BLOCKS) || (u64)gx * gy >= (1ull << 31) ||
+        cf->threads == 0 || cf->threads % 64u ||
         cf->threads > 1024u || comb_words > COMB_SLOTS || (comb_param >= 0 && ((u32)comb_param >= cf->np ||
         cf->psz[comb_param] != 8)))
         return 0;
@@ -374,7 +387,9 @@ static int hb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *con
     h->co = *cf;
     h->fz_key = 0;
     h->fz_serial = h->fz_out = 0;
-    h->solo = solo;
+    h->solo = solo == 1;
+    h->ch = NULL;
+    h->ch_nb = 0;
     h->fn = fn;
     h->gx = gx;
     h->gy = gy;
@@ -415,6 +430,18 @@ void hipb_hold_tag(u64 key, u32 serial, u32 out_buf) {
     h->fz_key = key;
     h->fz_serial = serial;
     h->fz_out = out_buf;
+}
+
+/* Marks the launch just held as the loop-free program ch over buffers
+ * (out_buf, leaf_bufs) that the next elementwise dispatch may fuse after. */
+static void hb_hold_chain(const ChainInfo *ch, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves) {
+    if (!HB.n || !ch || n_leaves < ch->n_leaves) return;
+    HbEnt *h = &HB.ent[HB.n - 1];
+    h->ch = ch;
+    h->ch_nb = ch->n_leaves + 1;
+    h->ch_bufs[0] = out_buf;
+    memcpy(h->ch_bufs + 1, leaf_bufs, ch->n_leaves * sizeof(u32));
+    h->ch_seq = pool_write_clock();
 }
 
 static u32 elem_count(u32 id, u32 dtype);
@@ -810,6 +837,80 @@ static void interp_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, con
 }
 
 static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
+static void hb_run_generated(KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
+
+/* A loop-free dispatch that reads the output of a held loop-free program P
+ * at its own gid runs fused after it (chain.c): P's held launch is taken
+ * back and the merged program is dispatched in its place, which writes
+ * both outputs. Only when every buffer of P is still live and unwritten by
+ * the host since P was held (P's launch would have read the old contents),
+ * and each output read is at least one launch long. The merged program
+ * goes through the usual hold, so it waits behind held launches it
+ * touches memory of and may take further consumers. Returns 1 when fused. */
+static int hb_try_chain(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
+    static UOpKernel M;
+    static u32 mb[1 + FUSE_MAX_LEAVES];
+    if (!HB.n || hipb.no_fuse || hipb.noalloc || hipb.sync_each || HB.flushing || !k || k->n_leaves > n_leaves ||
+        k->n_leaves == 0 || k->n_leaves > FUSE_MAX_LEAVES)
+        return 0;
+    i32 at = -1;
+    for (u32 i = HB.n; i-- > 0 && at < 0;) {
+        const HbEnt *h = &HB.ent[i];
+        if (!h->ch) continue;
+        for (u32 s = 0; s < h->ch->n_st && at < 0; s++)
+            for (u32 j = 0; j < k->n_leaves; j++)
+                if (leaf_bufs[j] == h->ch_bufs[h->ch->st_slot[s]]) { at = (i32)i; break; }
+    }
+    if (at < 0) return 0;
+    HbEnt *h = &HB.ent[at];
+    const ChainInfo *ch = h->ch;
+    for (u32 b = 0; b < h->ch_nb; b++) {
+        const HipbBuf *pb = h->ch_bufs[b] ? pool_get(h->ch_bufs[b]) : NULL;
+        if (h->ch_bufs[b] && (!pb || !pb->ptr || pb->wseq > h->ch_seq)) return 0;
+    }
+    for (u32 s = 0; s < ch->n_st; s++)
+        if (elem_count(h->ch_bufs[ch->st_slot[s]], DTYPE_F32) < ch->total) return 0;
+    if (!pool_ptr(out_buf) || !chain_merge(ch, h->ch_bufs, k, out_buf, leaf_bufs, n_leaves, &M, mb)) return 0;
+    static u64 refused[64];   /* merged programs the generator or hipRTC refused */
+    static u32 n_refused;
+    const u64 key = uop_signature(&M);
+    for (u32 i = 0; i < n_refused && i < 64; i++)
+        if (refused[i] == key) return 0;
+    KCacheEntry *e = rtc_lookup(key, &M);
+    if (e) hipb.n_cache_hit++;
+    else {
+        e = rtc_compile_uop(key, &M);
+        if (e && hipb.verbose)
+            fprintf(stderr, "tinyhvm-hip: %s = %s + the loop-free dispatch after it\n", e->name, h->co.name);
+    }
+    if (!e || e->splits > 1 || e->mode == KG_MODE_GROUP) {
+        refused[n_refused++ % 64] = key;
+        return 0;
+    }
+    /* the consumer's own inputs current on the device first: a copy that
+     * overlaps a held launch issues it, and then nothing fuses */
+    const u32 tag[2] = {h->ch_bufs[0], (u32)h->ch_seq};
+    for (u32 j = 0; j < k->n_leaves; j++) pool_sync_device(leaf_bufs[j]);
+    at = -1;
+    for (u32 i = 0; i < HB.n && at < 0; i++)
+        if (HB.ent[i].ch == ch && HB.ent[i].ch_bufs[0] == tag[0] && (u32)HB.ent[i].ch_seq == tag[1]) at = (i32)i;
+    if (at < 0) return 0;
+    memmove(&HB.ent[at], &HB.ent[at + 1], (HB.n - (u32)at - 1) * sizeof(HbEnt));
+    HB.n--;
+    hb_run_generated(e, mb[0], mb + 1, M.n_leaves, &M);
+    hipb.n_fused++;
+    return 1;
+}
+
+int thvm_hip_chain_merge(const UOpKernel *p, const u32 *pb, const UOpKernel *c, u32 c_out, const u32 *c_leaves,
+                         UOpKernel *m, u32 *mb) {
+    if (!p || !pb || !c || !c_leaves || !m || !mb) return 0;
+    ChainInfo *ci = chain_info_make(p, p->ops);
+    if (!ci) return 0;
+    const int r = chain_merge(ci, pb, c, c_out, c_leaves, c->n_leaves, m, mb);
+    free(ci);
+    return r;
+}
 
 static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
                                    const UOpKernel *k, u64 cache_key) {
@@ -833,6 +934,7 @@ static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_lea
         pool_mark_device_write(out_buf);
         return;
     }
+    if (!hipb.force_interp && hb_try_chain(out_buf, leaf_bufs, n_leaves, k)) return;
     if (!hipb.no_dense && dense_try_dispatch(out_buf, leaf_bufs, n_leaves, k)) {
         pool_mark_device_write(out_buf);
         hipb.n_dense++;
@@ -867,6 +969,21 @@ static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_lea
         return;
     }
 
+    hb_run_generated(e, out_buf, leaf_bufs, n_leaves, k);
+}
+
+/* The output and the leaf slots a generated program stores into hold
+ * device-written contents. */
+static void hb_mark_writes(const KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves) {
+    pool_mark_device_write(out_buf);
+    for (u32 i = 0; e->store_slots && i < n_leaves && i + 1 < 64; i++)
+        if ((e->store_slots >> (i + 1)) & 1u) pool_mark_device_write(leaf_bufs[i]);
+}
+
+/* Launches (or holds) compiled program e over its buffers. */
+static void hb_run_generated(KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
+    HipbBuf *ob = pool_get(out_buf);
+    if (!ob) return;
     /* constant-index loads of host-held leaves take their value inline; a
      * leaf read only that way is not uploaded */
     u32 sm = 0;
@@ -913,7 +1030,7 @@ static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_lea
     hm.n = 0;
     hbm_add(&hm, ptrs[0], pool_bytes(out_buf), 1);
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++)
-        hbm_add(&hm, pool_ptr(leaf_bufs[i]), pool_bytes(leaf_bufs[i]), 0);
+        hbm_add(&hm, pool_ptr(leaf_bufs[i]), pool_bytes(leaf_bufs[i]), i + 1 < 64 && ((e->store_slots >> (i + 1)) & 1u));
     u32 gx, gy;
     if (e->splits > 1 && !e->fn_fin) {
         /* split group reduce, partials combined by the last workgroup of each
@@ -922,7 +1039,7 @@ static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_lea
         grid_for(e->total * e->splits, e->block, &gx, &gy);
         if (!hipb_hold(&e->co, e->fn, gx, gy, params, &hm, 1, (int)np, e->total * e->splits))
             hipb_launch(e->fn, gx, gy, 1, e->block, params);
-        pool_mark_device_write(out_buf);
+        hb_mark_writes(e, out_buf, leaf_bufs, n_leaves);
         return;
     }
     if (e->splits > 1) {
@@ -934,13 +1051,19 @@ static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_lea
         hipb_launch(e->fn, gx, gy, 1, e->block, params);
         void *p2[] = {&ptrs[0], &counts[0], &ws};
         hipb_launch(e->fn_fin, (u32)e->total, 1, 1, 256, p2);   /* a workgroup per output */
-        pool_mark_device_write(out_buf);
+        hb_mark_writes(e, out_buf, leaf_bufs, n_leaves);
         return;
     }
     if (e->mode == KG_MODE_GROUP) grid_for(e->total, e->block, &gx, &gy);
     else grid_for((e->n_threads + e->block - 1) / e->block, e->block, &gx, &gy);
-    if (!hipb_hold(&e->co, e->fn, gx, gy, params, &hm, 0, -1, 0)) hipb_launch(e->fn, gx, gy, 1, e->block, params);
-    pool_mark_device_write(out_buf);
+    /* a loop-free program is held, alone if its grid is too large to
+     * batch, so that a consumer of its output can fuse after it */
+    if (hipb_hold(&e->co, e->fn, gx, gy, params, &hm, 0, -1, 0) ||
+        (e->chain && hb_hold_large(&e->co, e->fn, gx, gy, params, &hm)))
+        hb_hold_chain(e->chain, out_buf, leaf_bufs, n_leaves);
+    else
+        hipb_launch(e->fn, gx, gy, 1, e->block, params);
+    hb_mark_writes(e, out_buf, leaf_bufs, n_leaves);
 }
 
 /* The same dispatch with its workspaces carved from the static array and no

@@ -127,6 +127,7 @@ typedef struct {
     u32 mirror_bytes; /* bytes of the mirror that were written */
     void *host_mirror;
     u32 write_capture; /* the graph capture during which the host last wrote it (0: none) */
+    u64 wseq;          /* pool_write_clock() just after its last host write */
 } HipbBuf;
 
 int   pool_init(void);
@@ -151,6 +152,8 @@ void  pool_mark_device_write(u32 id);
 void  pool_sync_device(u32 id);
 int   pool_host_value(u32 id, u32 dtype, u32 idx, float *out);
 void  pool_write(u32 id, const void *data, u64 bytes);
+/* counts host writes (buf_write) into any buffer */
+u64   pool_write_clock(void);
 void  pool_read(u32 id, void *out, u64 bytes, int nosync);
 void  pool_stats(u64 *live_bytes, u64 *cached_bytes, u64 *n_mallocs);
 
@@ -244,6 +247,28 @@ void hipb_hold_tag(u64 key, u32 serial, u32 out_buf);
 int  dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunction_t *fn, CoForm *co);
 char *dense_epilogue_source(const UOpKernel *k, const UOpKernel *c, u32 o_leaf, char *err, size_t errlen);
 
+/* ---------------- chain.c: elementwise programs fused in sequence ---------------- */
+#define CHAIN_MAX_OPS 256     /* the generator vectorises programs up to this size */
+#define CHAIN_MAX_STORES 8
+typedef struct {
+    const KOp *ops;           /* the compiled program's copy (owned by the kernel cache) */
+    u32 n_ops, n_leaves, total, out_dtype;
+    u32 grid[3];
+    u32 leaf_dtypes[FUSE_MAX_LEAVES];
+    u32 n_st, st_slot[CHAIN_MAX_STORES], st_val[CHAIN_MAX_STORES];  /* its STOREs: buffer slot, value op */
+    u8 st_f32[CHAIN_MAX_STORES];
+} ChainInfo;
+/* A loop-free program whose STOREs all write at gid (so a consumer that
+ * reads one of its outputs at gid can take the stored value), or NULL. */
+ChainInfo *chain_info_make(const UOpKernel *k, const KOp *ops);
+/* The program M = P then C, C's loads of P's outputs taking P's stored
+ * values and C's STORE going to a new leaf slot; pb/mb are the buffer ids
+ * (output, leaves) of P and of M. Returns 0 when the pair does not fuse. */
+int chain_merge(const ChainInfo *p, const u32 *pb, const UOpKernel *c, u32 c_out, const u32 *c_leaves,
+                u32 c_nl, UOpKernel *m, u32 *mb);
+/* bit s set: the program STOREs into leaf slot s (s >= 1) */
+u64 chain_store_slots(const UOpKernel *k);
+
 /* ---------------- rtc / cache ---------------- */
 typedef struct {
     u64 key;
@@ -260,6 +285,8 @@ typedef struct {
     u32 meta[5 + FUSE_MAX_LEAVES]; /* grid, local_size, out_dtype, leaf dtypes */
     char name[32];        /* the kernel's symbol */
     CoForm co;            /* its co-launch form */
+    ChainInfo *chain;     /* set when a consumer may fuse after it */
+    u64 store_slots;      /* leaf slots it writes (chain_store_slots) */
 } KCacheEntry;
 
 int  rtc_init(void);

@@ -755,33 +755,37 @@ static void emit_op(Gen *g, u32 i, int fast, int in_ploop) {
     }
     case KOP_STORE: {
         const OpI *ix = &g->oi[op->arg[0]];
+        /* buffer imm.u: the engine's programs store to 0 (the output); a
+         * chain of fused elementwise programs also stores to leaf slots */
+        const u32 sb_ = op->imm.u <= k->n_leaves ? op->imm.u : 0u;
+        const u32 sdt = sb_ ? k->leaf_dtypes[sb_ - 1] : k->out_dtype;
         if (g->mode == KG_MODE_GROUP) {
             U(g, op->arg[0], 0, a);
             Fx(g, op->arg[1], 0, b);
-            sb_put(&g->sb, "    if (lane == 0) %s(p0, c0, %s, %s);\n", dt_st(k->out_dtype), a, b);
+            sb_put(&g->sb, "    if (lane == 0) %s(p%u, c%u, %s, %s);\n", dt_st(sdt), sb_, sb_, a, b);
             break;
         }
-        if (lin_unit4(ix, V) && k->out_dtype == DTYPE_F32) {
+        if (lin_unit4(ix, V) && sdt == DTYPE_F32) {
             char b1[128], b2[128], b3[128];
             U(g, op->arg[0], 0, a);
             Fx(g, op->arg[1], 0, b);
             Fx(g, op->arg[1], 1, b1);
             Fx(g, op->arg[1], 2, b2);
             Fx(g, op->arg[1], 3, b3);
-            sb_put(&g->sb, "    if (X0 + 3u < TOTAL) st4%s(p0, c0, %s, make_float4(%s, %s, %s, %s));\n",
-                   (g->nt & 2) ? "nt" : "", a, b, b1, b2, b3);
+            sb_put(&g->sb, "    if (X0 + 3u < TOTAL) st4%s(p%u, c%u, %s, make_float4(%s, %s, %s, %s));\n",
+                   (g->nt & 2) ? "nt" : "", sb_, sb_, a, b, b1, b2, b3);
             sb_put(&g->sb, "    else {\n");
             for (u32 v = 0; v < V; v++) {
                 U(g, op->arg[0], v, a);
                 Fx(g, op->arg[1], v, b);
-                sb_put(&g->sb, "      if (X0 + %uu < TOTAL) %s(p0, c0, %s, %s);\n", v, dt_st(k->out_dtype), a, b);
+                sb_put(&g->sb, "      if (X0 + %uu < TOTAL) %s(p%u, c%u, %s, %s);\n", v, dt_st(sdt), sb_, sb_, a, b);
             }
             sb_put(&g->sb, "    }\n");
         } else {
             for (u32 v = 0; v < V; v++) {
                 U(g, op->arg[0], v, a);
                 Fx(g, op->arg[1], v, b);
-                sb_put(&g->sb, "    if (X0 + %uu < TOTAL) %s(p0, c0, %s, %s);\n", v, dt_st(k->out_dtype), a, b);
+                sb_put(&g->sb, "    if (X0 + %uu < TOTAL) %s(p%u, c%u, %s, %s);\n", v, dt_st(sdt), sb_, sb_, a, b);
             }
         }
         break;

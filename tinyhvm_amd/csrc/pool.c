@@ -66,6 +66,7 @@ typedef struct {
 
 static struct {
     HipbBuf *bufs;
+    u64 wclock;           /* host writes so far */
     u32 cap;
     u32 count;            /* next id */
     u32 persistent_floor;
@@ -507,6 +508,8 @@ HipbBuf *pool_get(u32 id) {
     return b;
 }
 
+u64 pool_write_clock(void) { return P.wclock; }
+
 void *pool_ptr(u32 id) {
     HipbBuf *b = pool_get(id);
     return b ? b->ptr : NULL;
@@ -619,6 +622,7 @@ void pool_write(u32 id, const void *data, u64 bytes) {
     HipbBuf *b = pool_get(id);
     if (!b || !data || bytes == 0) return;
     b->write_capture = hipb.capturing ? P.capture_seq : 0;
+    b->wseq = ++P.wclock;
     if (bytes > b->cap) {
         fprintf(stderr, "tinyhvm-hip: buf_write of %llu bytes into buffer %u of %llu bytes; truncated\n",
                 (unsigned long long)bytes, id, (unsigned long long)b->cap);

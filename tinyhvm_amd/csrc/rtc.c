@@ -101,6 +101,7 @@ void rtc_shutdown(void) {
             if (R.tab[i].key) {
                 HIPB_CHECK(hipModuleUnload(R.tab[i].mod));
                 free(R.tab[i].ops);
+                free(R.tab[i].chain);
                 co_form_free(&R.tab[i].co);
             }
         }
@@ -396,6 +397,8 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
     snprintf(e->name, sizeof e->name, "%s", g.name);
     /* split reductions with a combine kernel are two launches: not co-launched */
     if (!g.combine_launch) co_form_make(&e->co, g.src, g.name, g.block, fn);
+    e->store_slots = chain_store_slots(k);
+    e->chain = (e->ops && g.mode != KG_MODE_GROUP && g.splits <= 1) ? chain_info_make(k, e->ops) : NULL;
     hipb.n_compile++;
     kgen_free(&g);
     return e;
