@@ -29,6 +29,7 @@ hipError_t hipb_stream_wait(void) {
 /* the backend's held dispatches (none here: the pool alone is under test) */
 void hipb_before_stream(void) {}
 void hipb_before_copy(const void *dst, u64 bytes) { (void)dst; (void)bytes; }
+int hipb_held_buffer(u32 id) { (void)id; return 0; }
 
 extern size_t fake_hip_limit, fake_hip_live;
 extern unsigned long fake_hip_mallocs, fake_hip_frees;

@@ -317,6 +317,15 @@ static void hb_flush(void) {
     HB.n = 0;
     HB.comb_used = 0;
     HB.flushing = 0;
+    pool_release_deferred();
+}
+
+int hipb_held_buffer(u32 id) {
+    for (u32 i = 0; i < HB.n; i++)
+        if (HB.ent[i].ch)
+            for (u32 b = 0; b < HB.ent[i].ch_nb; b++)
+                if (HB.ent[i].ch_bufs[b] == id) return 1;
+    return 0;
 }
 
 void hipb_before_stream(void) {
@@ -881,7 +890,8 @@ static int hb_try_chain(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
     else {
         e = rtc_compile_uop(key, &M);
         if (e && hipb.verbose)
-            fprintf(stderr, "tinyhvm-hip: %s = %s + the loop-free dispatch after it\n", e->name, h->co.name);
+            fprintf(stderr, "tinyhvm-hip: %s = %s + thvm_ew_%08x\n", e->name, h->co.name,
+                    (u32)(uop_signature(k) & 0xFFFFFFFFu));
     }
     if (!e || e->splits > 1 || e->mode == KG_MODE_GROUP) {
         refused[n_refused++ % 64] = key;
@@ -898,6 +908,7 @@ static int hb_try_chain(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
     memmove(&HB.ent[at], &HB.ent[at + 1], (HB.n - (u32)at - 1) * sizeof(HbEnt));
     HB.n--;
     hb_run_generated(e, mb[0], mb + 1, M.n_leaves, &M);
+    if (!HB.n) pool_release_deferred();   /* the merged launch went out at once */
     hipb.n_fused++;
     return 1;
 }

@@ -116,6 +116,10 @@ void hipb_before_stream(void);
 /* The same for a host-to-device copy into [dst, dst + bytes): only if a held
  * dispatch touches that memory (the copy may go ahead of independent ones). */
 void hipb_before_copy(const void *dst, u64 bytes);
+/* Whether a held launch that a consumer may still fuse after names buffer
+ * id (its free then waits: pool_release_deferred after the launch). */
+int  hipb_held_buffer(u32 id);
+void pool_release_deferred(void);
 typedef struct {
     void *ptr;        /* device pointer, NULL if free */
     u64 bytes;        /* requested bytes */

@@ -474,8 +474,32 @@ static void release_block(HipbBuf *b) {
     b->host_mirror = NULL;
 }
 
+/* Frees of buffers that a held launch may still be merged with (its
+ * buffers are looked up again by id when a consumer fuses after it) wait
+ * until the held launches have been issued. */
+#define POOL_DEFER_MAX 64
+static struct { u32 id[POOL_DEFER_MAX]; u32 n; } DF;
+
+static int defer_free(u32 id) {
+    for (u32 i = 0; i < DF.n; i++)
+        if (DF.id[i] == id) return 1;
+    if (DF.n >= POOL_DEFER_MAX || !hipb_held_buffer(id)) return 0;
+    DF.id[DF.n++] = id;
+    return 1;
+}
+
+void pool_release_deferred(void) {
+    const u32 n = DF.n;
+    DF.n = 0;
+    for (u32 i = 0; i < n; i++) {
+        const u32 id = DF.id[i];
+        if (id < P.count && P.bufs[id].live) release_block(&P.bufs[id]);
+    }
+}
+
 void pool_free(u32 id) {
     if (id == 0 || id >= P.count || !P.bufs[id].live) return;
+    if (defer_free(id)) return;
     release_block(&P.bufs[id]);
 }
 
@@ -488,10 +512,12 @@ void pool_decref(u32 id) {
     if (id == 0 || id >= P.count || !P.bufs[id].live) return;
     if (id <= P.persistent_floor) return;
     if (P.bufs[id].refcount > 0) P.bufs[id].refcount--;
-    if (P.bufs[id].refcount == 0) release_block(&P.bufs[id]);
+    if (P.bufs[id].refcount == 0 && !defer_free(id)) release_block(&P.bufs[id]);
 }
 
 void pool_reset(u32 keep) {
+    hipb_before_stream();   /* held launches out, deferred frees done: ids are reused from here */
+    pool_release_deferred();
     u32 first = keep + 1;
     if (first < 1) first = 1;
     for (u32 i = first; i < P.count; i++)
