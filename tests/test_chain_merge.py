@@ -8,10 +8,12 @@ recorded workloads:
 
 - the pairs that merge are the expected ones (batchnorm's variance and
   inverse deviation, normalisation then scale and shift, the pooling
-  backward's routing then the product with the scale; one pair each in
-  LeNet-5, the MLP and the linear stack), and pairs where the second does
-  not read the first's output at its own gid do not;
-- M, run by a small interpreter of loop-free KOp programs on random
+  backward's routing then the product with the scale; in LeNet-5 and the
+  MLP a softmax step and the relu mask after the last layer's input
+  gradient, whose producer is a loop each lane runs for its own gid; one
+  pair in the linear stack), and pairs where the second does not read the
+  first's output at its own gid do not;
+- M, run by a small interpreter of per-gid KOp programs on random
   inputs, leaves every buffer exactly as P followed by C does (both sides
   use the same interpreter, so this checks the merge, not the arithmetic;
   the GPU tests compare the fused launches with separate ones bit for bit);
@@ -33,15 +35,48 @@ class Skip(Exception):
 
 
 def run(k, bufs, ids):
-    """Evaluates loop-free program k over every gid, in place on bufs
-    (id -> float32 array); ids = [output, leaves...] (0: absent)."""
+    """Evaluates program k (no loop, or loops each lane runs for its own
+    gid) over every gid, in place on bufs (id -> float32 array); ids =
+    [output, leaves...] (0: absent)."""
     n = k.local_size and k.grid[0] or k.grid[0] * k.grid[1] * k.grid[2]
     gid = np.arange(n, dtype=np.uint32)
     val = {}
     isf = {}
+    end = {}
+    stack = []
     for i in range(k.n_ops):
+        if k.ops[i].type == abi.KOP_RANGE:
+            stack.append(i)
+        elif k.ops[i].type == abi.KOP_ENDRANGE:
+            end[stack.pop()] = i
+    i = 0
+    loops = []                   # [range op, r]
+    while i < k.n_ops:
         op = k.ops[i]
         t, a0, a1 = op.type, op.arg[0], op.arg[1]
+        if t == abi.KOP_RANGE:
+            if op.imm.u == 0:
+                i = end[i] + 1
+                continue
+            loops.append([i, 0])
+            val[i], isf[i] = np.zeros(n, np.uint32), False
+            i += 1
+            continue
+        if t == abi.KOP_ENDRANGE:
+            lp = loops[-1]
+            lp[1] += 1
+            if lp[1] < k.ops[lp[0]].imm.u:
+                val[lp[0]] = np.full(n, lp[1], np.uint32)
+                i = lp[0] + 1
+            else:
+                loops.pop()
+                i += 1
+            continue
+        i = step(k, i, op, t, a0, a1, n, gid, val, isf, bufs, ids)
+
+
+def step(k, i, op, t, a0, a1, n, gid, val, isf, bufs, ids):
+    if True:
 
         def f(j):
             return val[j] if isf[j] else val[j].astype(np.float32)
@@ -91,6 +126,12 @@ def run(k, bufs, ids):
             idx = u(a0)
             ok = idx < b.size
             b[idx[ok]] = f(a1)[ok]
+        elif t == abi.KOP_ACC_INIT:
+            val[i], isf[i] = np.full(n, op.imm.f, np.float32), True
+        elif t == abi.KOP_ACC:
+            x = val[a0]
+            y = val[a1] if isf[a1] else val[a1].astype(np.float32)
+            val[a0] = (np.where(x > y, x, y) if op.imm.u == abi.UOP_RMAX else x + y).astype(np.float32)
         elif t == abi.KOP_MASK:
             val[i], isf[i] = np.where(f(a0) != 0, f(a1), np.float32(0)).astype(np.float32), True
         elif t == abi.KOP_ALU:
@@ -113,6 +154,7 @@ def run(k, bufs, ids):
             val[i], isf[i] = r.astype(np.float32), True
         else:
             raise Skip("op %d" % t)
+    return i + 1
 
 
 def dispatches(name, m0=None, m1=None):
@@ -129,8 +171,11 @@ def dispatches(name, m0=None, m1=None):
 
 
 def chains(seq):
-    """Each dispatch merged into the one before when they fuse (the chain
-    continuing with the merged program): [(first, last, m, mb), ...]."""
+    """Each dispatch merged into the one before when the pair merges (the
+    chain continuing with the merged program): [(first, last, m, mb), ...].
+    The backend offers a producer only when it runs as a generated program:
+    a contraction it routes to the matrix cores takes its consumer as a
+    fused epilogue instead (the MLP's fc2 forward and its bias, 2 and 3)."""
     found = []
     prev, first = None, 0
     for n, (k, ids) in enumerate(seq):
@@ -148,9 +193,11 @@ def chains(seq):
 
 
 CASES = [
-    ("lenet_b256.trc", "lenet.step", "lenet.end", [(21, 22)]),
+    # LeNet-5: 1-2, 4-5, 9-10, 11-12 and 29-30 are contractions with their
+    # bias/relu consumers (fused epilogues in the backend)
+    ("lenet_b256.trc", "lenet.step", "lenet.end", [(1, 2), (4, 5), (9, 10), (11, 12), (21, 22), (25, 26), (29, 30)]),
     ("convblock_b64.trc", None, None, [(6, 7), (8, 9), (15, 16)]),
-    ("mlp_64x784x128x10.trc", None, None, [(12, 13)]),
+    ("mlp_64x784x128x10.trc", None, None, [(2, 3), (12, 13), (16, 17)]),
     ("linear_8x4096x4096.trc", None, None, [(1, 2)]),
 ]
 

@@ -29,6 +29,7 @@ PARAMS = range(2, 12)          # trace ids of W1, b1, ..., W5, b5
 
 
 CONV = os.path.join(ROOT, "tinyhvm_amd", "workloads", "convblock_b64.trc")
+MLP = os.path.join(ROOT, "tinyhvm_amd", "workloads", "mlp_64x784x128x10.trc")
 
 
 def _run_all(path, m0, m1, no_fuse):
@@ -146,6 +147,21 @@ def test_chained_elementwise_match_separate_launches():
     fused, n_fused = _run_all(CONV, "conv.fwd", None, no_fuse=False)
     assert n_sep == 0
     assert n_fused >= 4, "only %d dispatches were fused" % n_fused
+    assert sep.keys() == fused.keys()
+    bad = [tid for tid in sep if sep[tid] != fused[tid]]
+    assert not bad, "buffers %s differ between fused and separate launches" % bad
+
+
+def test_mlp_fusions_match_separate_launches():
+    """The MLP step: fc2's bias in the epilogue of its contraction, a
+    softmax step merged with the one before, and the relu mask merged with
+    fc2's input gradient (a generated loop that each lane runs for its own
+    gid). Every buffer live after the step is bit for bit that of
+    THVM_HIP_NO_FUSE=1."""
+    sep, n_sep = _run_all(MLP, "mlp.fwd", None, no_fuse=True)
+    fused, n_fused = _run_all(MLP, "mlp.fwd", None, no_fuse=False)
+    assert n_sep == 0
+    assert n_fused >= 3, "only %d dispatches were fused" % n_fused
     assert sep.keys() == fused.keys()
     bad = [tid for tid in sep if sep[tid] != fused[tid]]
     assert not bad, "buffers %s differ between fused and separate launches" % bad

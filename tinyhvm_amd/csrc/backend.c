@@ -104,7 +104,7 @@ typedef struct {
     u64 fz_key;            /* a contraction an elementwise consumer may fuse into (0: none) */
     u32 fz_serial, fz_out; /* ... its dense entry and its output buffer */
     int solo;              /* held only for a fused epilogue: joins no batch */
-    const ChainInfo *ch;   /* a loop-free program an elementwise consumer may fuse after (NULL: none) */
+    const ChainInfo *ch;   /* a program an elementwise consumer may fuse after (chain.c; NULL: none) */
     u32 ch_bufs[1 + FUSE_MAX_LEAVES]; /* ... its buffers (output, leaves) */
     u64 ch_seq;            /* ... the pool's host-write clock when it was held */
     u32 ch_nb;
@@ -377,7 +377,7 @@ int hipb_hold_solo(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *con
     return hb_hold(cf, fn, gx, gy, params, m, 0, -1, 0, 1);
 }
 
-/* A loop-free generated program of any grid size: held (and batched like
+/* A chainable generated program (chain.c) of any grid size: held (and batched like
  * the small ones) so that a consumer of its output can fuse after it. */
 static int hb_hold_large(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m) {
     if (hipb.no_fuse) return 0;
@@ -441,7 +441,7 @@ void hipb_hold_tag(u64 key, u32 serial, u32 out_buf) {
     h->fz_out = out_buf;
 }
 
-/* Marks the launch just held as the loop-free program ch over buffers
+/* Marks the launch just held as the chainable program ch over buffers
  * (out_buf, leaf_bufs) that the next elementwise dispatch may fuse after. */
 static void hb_hold_chain(const ChainInfo *ch, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves) {
     if (!HB.n || !ch || n_leaves < ch->n_leaves) return;
@@ -848,7 +848,7 @@ static void interp_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, con
 static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
 static void hb_run_generated(KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
 
-/* A loop-free dispatch that reads the output of a held loop-free program P
+/* A loop-free dispatch that reads the output of a held chainable program P
  * at its own gid runs fused after it (chain.c): P's held launch is taken
  * back and the merged program is dispatched in its place, which writes
  * both outputs. Only when every buffer of P is still live and unwritten by
@@ -1067,7 +1067,7 @@ static void hb_run_generated(KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, 
     }
     if (e->mode == KG_MODE_GROUP) grid_for(e->total, e->block, &gx, &gy);
     else grid_for((e->n_threads + e->block - 1) / e->block, e->block, &gx, &gy);
-    /* a loop-free program is held, alone if its grid is too large to
+    /* a chainable program is held, alone if its grid is too large to
      * batch, so that a consumer of its output can fuse after it */
     if (hipb_hold(&e->co, e->fn, gx, gy, params, &hm, 0, -1, 0) ||
         (e->chain && hb_hold_large(&e->co, e->fn, gx, gy, params, &hm)))

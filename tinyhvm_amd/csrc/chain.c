@@ -6,9 +6,10 @@
  * (src/schedule/_.c:2268-2411): batchnorm's normalisation and its scale and
  * shift, the relu after them, the routing mask of the pooling backward and
  * its product with the scale are separate launches, each reading the tensor
- * the one before wrote. When such a program P (no loop, every STORE at its
- * own gid) is held back for a batched launch and the next dispatch C (no
- * loop, one STORE at gid) reads P's output only at its own gid, the two run
+ * the one before wrote. When such a program P (no loop, or one loop that
+ * each lane runs for its own gid, every STORE after it and at its own gid)
+ * is held back for a batched launch and the next dispatch C (no loop, one
+ * STORE at gid) reads P's output only at its own gid, the two run
  * as one program M: P's ops, then C's, with each load of P's output taking
  * the value P stores there and C's STORE naming the leaf slot that holds C's
  * output (a KOp STORE names its buffer in imm.u, src/tinyhvm.h:683; the
@@ -50,6 +51,30 @@ static int loop_free(const UOpKernel *k) {
     return 1;
 }
 
+/* A producer: loop-free, or one top-level loop (the generator's serial
+ * form: each lane loops for its own gid) with every STORE after it. */
+static int producer_form(const UOpKernel *k) {
+    if (k->n_ops == 0 || k->n_ops > CHAIN_MAX_OPS || k->local_size != 0) return 0;
+    int depth = 0, loops = 0;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        const KOpType t = op->type;
+        if (t <= KOP_NOOP || t > KOP_MASK) return 0;
+        for (u32 a = 0; a < op_refs(t); a++)
+            if (op->arg[a] >= i) return 0;
+        if (t == KOP_RANGE) {
+            if (depth++ == 0) loops++;
+        } else if (t == KOP_ENDRANGE) {
+            if (--depth < 0 || op->arg[0] >= i || k->ops[op->arg[0]].type != KOP_RANGE) return 0;
+        } else if (t == KOP_ACC && (op->arg[0] >= i || k->ops[op->arg[0]].type != KOP_ACC_INIT)) {
+            return 0;
+        } else if (t == KOP_STORE && depth > 0) {
+            return 0;
+        }
+    }
+    return depth == 0 && loops <= 1;
+}
+
 static u32 slot_dtype(const UOpKernel *k, u32 slot) { return slot ? k->leaf_dtypes[slot - 1] : k->out_dtype; }
 
 u64 chain_store_slots(const UOpKernel *k) {
@@ -62,7 +87,7 @@ u64 chain_store_slots(const UOpKernel *k) {
 }
 
 ChainInfo *chain_info_make(const UOpKernel *k, const KOp *ops) {
-    if (!k || !ops || !loop_free(k) || k->n_leaves > FUSE_MAX_LEAVES) return NULL;
+    if (!k || !ops || !producer_form(k) || k->n_leaves > FUSE_MAX_LEAVES) return NULL;
     const u32 total = launch_total(k);
     if (total == 0) return NULL;
     Aff *aff = calloc(k->n_ops, sizeof(Aff));

@@ -262,8 +262,9 @@ typedef struct {
     u32 n_st, st_slot[CHAIN_MAX_STORES], st_val[CHAIN_MAX_STORES];  /* its STOREs: buffer slot, value op */
     u8 st_f32[CHAIN_MAX_STORES];
 } ChainInfo;
-/* A loop-free program whose STOREs all write at gid (so a consumer that
- * reads one of its outputs at gid can take the stored value), or NULL. */
+/* A program with no loop or one top-level loop, whose STOREs all follow
+ * the loop and write at gid (so a consumer that reads one of its outputs at
+ * gid can take the stored value), or NULL. */
 ChainInfo *chain_info_make(const UOpKernel *k, const KOp *ops);
 /* The program M = P then C, C's loads of P's outputs taking P's stored
  * values and C's STORE going to a new leaf slot; pb/mb are the buffer ids
