@@ -8,9 +8,10 @@
                 graph is destroyed, and write/read round trips; no leak at
                 shutdown.
   analyze_all   the device-free program analyses (kernel generator, lane
-                classification, matrix-core recognizer) over every lowered
-                kernel of every committed trace, plus truncated programs and
-                dangling operands.
+                classification, matrix-core and window recognizers, the merge
+                of consecutive programs) over every lowered kernel of every
+                committed trace, plus truncated programs and dangling
+                operands.
 
 Both are built with gcc (host code only; no device code is instrumented).
 """
@@ -66,5 +67,7 @@ def test_program_analysis_sanitized(tmp_path):
         for f in os.listdir(os.path.join(tt.ROOT, "tinyhvm_amd", "workloads")) if f.endswith(".trc"))
     r = subprocess.run([exe] + traces, capture_output=True, text=True, env=ENV, timeout=600)
     assert r.returncode == 0, r.stdout + r.stderr[-4000:]
-    n = int(r.stdout.split("analyze_all:")[1].split()[0])
+    words = r.stdout.split("analyze_all:")[1].split()
+    n, merged = int(words[0]), int(words[2])
     assert n > 300
+    assert merged > 10, "only %d consecutive pairs merged" % merged
