@@ -19,6 +19,7 @@ recorded workloads:
   the GPU tests compare the fused launches with separate ones bit for bit);
 - M compiles for gfx950 (hipRTC, no device).
 """
+import ctypes as C
 import os
 
 import numpy as np
@@ -261,3 +262,58 @@ def test_no_merge_without_a_gid_read():
     k10, d10 = seq[10]           # running mean, then running variance:
     k11, d11 = seq[11]           # independent of each other
     assert _lib.chain_merge(k10, d10, k11, d11[0], d11[1:]) is None
+
+
+def _with_extra_store(k, slot):
+    """A copy of loop-free producer k whose last STORE is followed by a
+    second STORE at the same index into `slot`, of the negated value."""
+    m = abi.UOpKernel()
+    C.memmove(C.byref(m), C.byref(k), C.sizeof(abi.UOpKernel))
+    st = [j for j in range(k.n_ops) if k.ops[j].type == abi.KOP_STORE][-1]
+    n = m.n_ops
+    m.ops[n].type = abi.KOP_ALU
+    m.ops[n].arg[0] = m.ops[n].arg[1] = k.ops[st].arg[1]
+    m.ops[n].imm.u = abi.UOP_NEG
+    m.ops[n + 1].type = abi.KOP_STORE
+    m.ops[n + 1].arg[0] = k.ops[st].arg[0]
+    m.ops[n + 1].arg[1] = n
+    m.ops[n + 1].imm.u = slot
+    m.n_ops = n + 2
+    return m
+
+
+def test_producer_storing_one_buffer_twice():
+    """A producer whose STOREs write one buffer twice leaves the last value
+    there. Stored twice through the same slot, it is not a producer at all;
+    through two slots that name the same buffer (its output also passed as
+    a leaf), the consumer's load takes the second, later value, as P then C
+    leaves it."""
+    seq, sizes = dispatches("convblock_b1.trc")
+    found = chains(seq)
+    assert found
+    first, _, _, _ = found[0]
+    kp, dp = seq[first]
+    kc, dc = seq[first + 1]
+    assert _lib.chain_merge(kp, dp, kc, dc[0], dc[1:]) is not None
+    twice = _with_extra_store(kp, 0)
+    assert _lib.chain_merge(twice, dp, kc, dc[0], dc[1:]) is None
+
+    # the output passed again as an extra leaf (slot kp.n_leaves + 1), stored through it last
+    alias = _with_extra_store(kp, kp.n_leaves + 1)
+    alias.leaf_dtypes[kp.n_leaves] = kp.out_dtype
+    alias.n_leaves = kp.n_leaves + 1
+    alias.n_bufs = alias.n_leaves + 1
+    ids = list(dp) + [dp[0]]
+    r = _lib.chain_merge(alias, ids, kc, dc[0], dc[1:])
+    assert r is not None
+    m, mb = r
+    rng = np.random.default_rng(11)
+    used = {i for i in ids + list(dc) + list(mb) if i}
+    init = {i: rng.standard_normal(sizes[i] // 4).astype(np.float32) for i in used}
+    a = {i: v.copy() for i, v in init.items()}
+    b = {i: v.copy() for i, v in init.items()}
+    run(alias, a, ids)
+    run(kc, a, dc)
+    run(m, b, mb)
+    for i in used:
+        assert a[i].tobytes() == b[i].tobytes(), "buffer %d differs" % i

@@ -106,6 +106,8 @@ ChainInfo *chain_info_make(const UOpKernel *k, const KOp *ops) {
         const u32 slot = op->imm.u;
         ok = ci->n_st < CHAIN_MAX_STORES && slot <= k->n_leaves && aff_is_gid(&dc, &aff[op->arg[0]]) &&
              op_type_is_float(k->ops[op->arg[1]].type);
+        /* a slot stored twice holds the last value: not a producer */
+        for (u32 s = 0; s < ci->n_st && ok; s++) ok = ci->st_slot[s] != slot;
         if (!ok) break;
         ci->st_slot[ci->n_st] = slot;
         ci->st_val[ci->n_st] = op->arg[1];
@@ -154,11 +156,10 @@ int chain_merge(const ChainInfo *p, const u32 *pb, const UOpKernel *c, u32 c_out
         const u32 id = c_leaves[j], dt = c->leaf_dtypes[j];
         sub[j] = -1;
         slot[j] = 0;
-        for (u32 s = 0; s < p->n_st && sub[j] < 0; s++)
-            if (id && pb[p->st_slot[s]] == id) {
-                ok = p->st_f32[s] && dt == DTYPE_F32;
-                sub[j] = (i32)s;
-            }
+        /* two of P's slots may name the same buffer: it holds the last store */
+        for (u32 s = 0; s < p->n_st; s++)
+            if (id && pb[p->st_slot[s]] == id) sub[j] = (i32)s;
+        if (sub[j] >= 0) ok = p->st_f32[sub[j]] && dt == DTYPE_F32;
         if (sub[j] >= 0 || !ok) continue;
         for (u32 s = 1; s <= nl && !slot[j]; s++)
             if (mb[s] == id && m->leaf_dtypes[s - 1] == dt) slot[j] = s;
