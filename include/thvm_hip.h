@@ -118,7 +118,8 @@ void  thvm_hip_graph_destroy(void *graph);
  * (split-K partial sums, split reduction partials, packed GEMM operands) comes
  * from a static device array of THVM_HIP_NOALLOC_SCRATCH_BYTES per GPU,
  * reserved when the library initialises, and that it never compiles: the
- * program must have run once through thvm_hip_dispatch_uop_kernel. It calls
+ * program must have run once through thvm_hip_dispatch_uop_kernel (also
+ * when it ran there fused into another dispatch's launch). It calls
  * no hipMalloc or hipFree. All calls on one GPU share the array; calls are
  * ordered on the backend's single stream, so consecutive calls are safe,
  * but calls that overlap on one GPU (from other streams or threads) race.
@@ -146,17 +147,14 @@ int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32
  * device blocks pinned by HIP graphs, released blocks held for graphs,
  * dispatches run on the window-max and run-sum kernels, dispatches issued
  * inside a batched launch, elementwise dispatches run as the fused epilogue
- * of the contraction whose output they read. Returns the number of counters
- * (13). */
+ * of the contraction whose output they read, host waits after which a
+ * single-pass combine was found to have given up waiting for a partial sum.
+ * Returns the number of counters (14). */
 int  thvm_hip_counters(u64 *out, u32 n);
-/* Sustained f32 MFMA rate on this GPU: a kernel of waves_per_cu waves per
- * compute unit (a multiple of 4, at most 32), each running iters x 8
- * v_mfma_f32_32x32x2f32 from registers with no memory traffic, timed over
- * five launches; TFLOP/s into *tflops. Returns 0, or -1. A calibration with
- * no counterpart in the reference: the matrix-core rate a kernel can reach
- * at this part's sustained clock, beside the published peak. */
-int  thvm_hip_mfma_probe(u32 waves_per_cu, u32 iters, double *tflops);
-/* Wait for all enqueued work; returns 0, or -1 on a device error. */
+/* Wait for all enqueued work; returns 0, or -1 on a device error or when a
+ * kernel that combines its workgroups' partial sums in one pass gave up
+ * waiting for one of them since the last call (its output then holds a
+ * NaN; buf_read reports the same on stderr and in the counters). */
 int  thvm_hip_synchronize(void);
 /* The hipStream_t all work is ordered on (for timing with events). */
 void *thvm_hip_stream(void);

@@ -67,7 +67,7 @@ def test_lenet_routes():
 
 def test_window_max_source_shape():
     recs = [r for r in trace.read_trace(os.path.join(WL, "convblock_b64.trc")) if r.tag == trace.UOP]
-    src = _lib.window_source(trace.to_uop_kernel(recs[13])).split('extern "C"')[1]
+    src = _lib.window_source(trace.to_uop_kernel(recs[13])).split('extern "C" __global__')[1]
     n_units = len(re.findall(r"const u32 o\d+_ =", src))
     # two adjacent windows per 16-byte load, two window rows per pair
     assert n_units >= 1 and src.count("(const v4f_*)") == 2 * n_units and "make_float2(a0_, a1_)" in src

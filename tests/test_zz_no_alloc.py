@@ -1,6 +1,13 @@
 """The no-allocation dispatch (thvm_hip_dispatch_uop_kernel_noalloc) against
 the allocating one, on the GPU, through the C ABI.
 
+Programs that the allocating path ran only fused into another launch (an
+elementwise consumer in a contraction's epilogue, a merged chain) are still
+accepted: a training step of LeNet-5 at batch 256 and of the 2-layer MLP is
+first replayed with no read between its dispatches (the bench's mode: held,
+batched, fused), then every program of the step goes through the
+no-allocation entry point first, and must match the allocating one.
+
 Every lowered program of two traces, one after the other: the conv block at
 its benchmark size [64,64,56,56] (matrix-core convolutions with packed
 operands and a 128-way split-K weight gradient, split batchnorm reductions,
@@ -162,5 +169,68 @@ def test_noalloc_refuses_uncompiled_and_oversized_work():
             assert L.thvm_hip_synchronize() == 0
         finally:
             rp.close()
+    finally:
+        _restore(L, saved)
+
+
+def _fused_then_noalloc(L, path, m0, m1):
+    """Replays [m0, m1) of `path` once with no reads (programs fuse), then
+    again record by record, each UOP through the no-allocation entry point
+    first and then, from the same inputs, through the allocating one."""
+    recs = trace.read_trace(path)
+    sizes = {r.f["id"]: r.f["bytes"] for r in recs if r.tag == trace.ALLOC}
+    rp = tt.Replay(path, L.thvm_hip_backend())
+    checked = 0
+    try:
+        lo = next(i for i, r in enumerate(recs) if r.tag == trace.MARK and r.f["text"] == m0)
+        hi = next(i for i, r in enumerate(recs) if i > lo and r.tag == trace.MARK and r.f["text"] == m1) \
+            if m1 else len(recs)
+        rp.run(0, lo)
+        c0 = (C.c_uint64 * 13)()
+        L.thvm_hip_counters(c0, 13)
+        rp.run(lo, hi, 1)                               # no reads: the held launches fuse
+        assert L.thvm_hip_synchronize() == 0
+        c1 = (C.c_uint64 * 13)()
+        L.thvm_hip_counters(c1, 13)
+        assert c1[12] > c0[12], "nothing fused in %s" % path
+        for i in range(lo, hi):
+            r = recs[i]
+            if r.tag != trace.UOP:
+                rp.run(i, i + 1, 1)
+                continue
+            k = rp.kernel(i)
+            out = rp.live(r.f["out"])
+            n_out = sizes[r.f["out"]]
+            nl = len(r.f["leaf_bufs"])
+            leaves = (C.c_uint32 * max(nl, 1))(*[rp.live(t) for t in r.f["leaf_bufs"]])
+            before = _read(L, out, n_out)
+            own = _reads_own_output(k, r.f["out"], r.f["leaf_bufs"])
+            fill = before if own else np.full_like(before, SENTINEL)
+            L.thvm_hip_buf_write(out, fill.ctypes.data_as(C.c_void_p), n_out)
+            m0_ = _counters(L)
+            rc = L.thvm_hip_dispatch_uop_kernel_noalloc(out, leaves, nl, C.byref(k))
+            assert rc == OK, "dispatch %d of %s (run fused before): no-allocation entry returned %d" % (
+                i, path.split("/")[-1], rc)
+            assert _counters(L)[7] == m0_[7] and _counters(L)[2] == m0_[2]
+            got = _read(L, out, n_out)
+            L.thvm_hip_buf_write(out, before.ctypes.data_as(C.c_void_p), n_out)
+            L.thvm_hip_dispatch_uop_kernel(out, leaves, nl, C.byref(k), 0)
+            want = _read(L, out, n_out)
+            assert np.array_equal(got, want), "dispatch %d of %s: %d words differ" % (
+                i, path.split("/")[-1], int(np.sum(got != want)))
+            checked += 1
+        assert L.thvm_hip_synchronize() == 0
+    finally:
+        rp.close()
+    return checked
+
+
+def test_noalloc_after_fused_step():
+    L, saved = _fresh({})
+    try:
+        n = _fused_then_noalloc(L, os.path.join(WL, "lenet_b256.trc"), "lenet.step", "lenet.end")
+        assert n >= 50
+        n = _fused_then_noalloc(L, os.path.join(WL, "mlp_64x784x128x10.trc"), "mlp.fwd", None)
+        assert n >= 15
     finally:
         _restore(L, saved)

@@ -73,7 +73,6 @@ def lib():
         "thvm_hip_window_analyze": (C.c_int, [C.POINTER(abi.UOpKernel), PU32, PU32]),
         "thvm_hip_window_source": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
         "thvm_hip_window_compile_check": (C.c_int, [C.POINTER(abi.UOpKernel), cp, u64]),
-        "thvm_hip_mfma_probe": (C.c_int, [u32, u32, C.POINTER(C.c_double)]),
         "thvm_hip_flush": (None, []),
         "thvm_hip_chain_merge": (C.c_int, [C.POINTER(abi.UOpKernel), PU32, C.POINTER(abi.UOpKernel), u32,
                                            PU32, C.POINTER(abi.UOpKernel), PU32]),
@@ -116,7 +115,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_abi_sizes", "thvm_hip_kernel_source", "thvm_hip_kernel_lanes", "thvm_hip_compile_check",
     "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
     "thvm_hip_window_analyze", "thvm_hip_window_source", "thvm_hip_window_compile_check",
-    "thvm_hip_batch_compile_check", "thvm_hip_mfma_probe", "thvm_hip_flush", "thvm_hip_epilogue_compile_check", "thvm_hip_chain_merge",
+    "thvm_hip_batch_compile_check", "thvm_hip_flush", "thvm_hip_epilogue_compile_check", "thvm_hip_chain_merge",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
     "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",

@@ -114,7 +114,7 @@ static struct {
     u32 n;
     u64 comb_used;         /* combine-area words given to the held launches */
     int flushing;
-    struct { u64 key; hipModule_t mod; hipFunction_t fn; } cache[64];
+    struct { u64 key; hipModule_t mod; hipFunction_t fn; u32 cap; } cache[64];
     u32 ncache;
 } HB;
 
@@ -217,10 +217,15 @@ static char *hb_batch_source(const HbEnt *ents, u32 n, u32 T, const char *name) 
     return src;
 }
 
-/* The batch kernel for the held sequence (compiled once per key). */
-static hipFunction_t hb_batch_fn(u64 key, u32 T) {
+/* The batch kernel for the held sequence (compiled once per key) and the
+ * workgroups of it the GPU holds at once (*cap). */
+static hipFunction_t hb_batch_fn(u64 key, u32 T, u32 *cap) {
+    *cap = 0;
     for (u32 i = 0; i < HB.ncache; i++)
-        if (HB.cache[i].key == key) return HB.cache[i].fn;
+        if (HB.cache[i].key == key) {
+            *cap = HB.cache[i].cap;
+            return HB.cache[i].fn;
+        }
     if (HB.ncache >= sizeof HB.cache / sizeof HB.cache[0]) return NULL;
     char name[48];
     snprintf(name, sizeof name, "thvm_batch_%016llx", (unsigned long long)key);
@@ -241,6 +246,7 @@ static hipFunction_t hb_batch_fn(u64 key, u32 T) {
             HB.cache[HB.ncache].key = key;
             HB.cache[HB.ncache].mod = mod;
             HB.cache[HB.ncache].fn = fn;
+            HB.cache[HB.ncache].cap = *cap = rtc_capacity(fn, T);
             HB.ncache++;
             hipb.n_compile++;
         } else {
@@ -295,12 +301,24 @@ static void hb_flush(void) {
     } else {
         const u32 T = hb_threads();
         u64 key = hb_mix(0x626174636822ull, T);
-        u32 total = 0, np = 0;
+        u32 total = 0, np = 0, cap = 0;
+        int resident = 0;
         for (u32 i = 0; i < HB.n; i++) {
             key = hb_mix(hb_mix(hb_mix(key, HB.ent[i].co.id), HB.ent[i].gx), HB.ent[i].gy);
             total += HB.ent[i].gx * HB.ent[i].gy;
+            resident |= HB.ent[i].resident;
         }
-        hipFunction_t fn = hb_batch_fn(key, T);
+        hipFunction_t fn = hb_batch_fn(key, T, &cap);
+        /* a program whose workgroups wait for each other goes in a batch only
+         * if the batch kernel's whole grid is on the GPU at once, with the
+         * batch kernel's own occupancy (its summed LDS, its registers);
+         * otherwise each launch goes out alone, as it was admitted */
+        if (fn && resident && total > cap) {
+            if (hipb.verbose)
+                fprintf(stderr, "tinyhvm-hip: batch of %u launches: %u workgroups exceed what the GPU holds at once "
+                        "(%u): launched one by one\n", HB.n, total, cap);
+            fn = NULL;
+        }
         if (fn) {
             void *pv[HB_MAX * CO_MAX_PARAMS];
             for (u32 i = 0; i < HB.n; i++) np += hb_params(&HB.ent[i], pv + np);
@@ -583,10 +601,32 @@ static void read_dense_env(void) {
 
 u32 hipb_resident_waves(void) { return hipb.resident_waves ? hipb.resident_waves : 256u * SINGLE_PASS_WAVES_PER_CU; }
 
+/* After a wait on the stream: a single-pass combine that gave up waiting
+ * for a partial (its output took a NaN) set the give-up word. It is
+ * counted, printed, and reported by the next thvm_hip_synchronize; the
+ * combine area is cleared again, since a partial published after its
+ * taker gave up would otherwise be taken by a later launch. */
+static void comb_check(void) {
+    if (!hipb.comb_err_host || !*(volatile u32 *)hipb.comb_err_host) return;
+    *(volatile u32 *)hipb.comb_err_host = 0;
+    hipb.n_comb_gaveup++;
+    hipb.comb_gaveup_pending = 1;
+    fprintf(stderr, "tinyhvm-hip: a single-pass combine gave up waiting for a partial sum; "
+                    "its output holds a NaN\n");
+    hipFunction_t fill = rtc_static_fn("thvm_fill_u32");
+    if (fill && hipb.comb_slots) {
+        u32 n1 = COMB_SLOTS * 2, zero = 0;
+        void *a1[] = {&hipb.comb_slots, &n1, &zero};
+        hipb_launch(fill, (n1 + 255) / 256, 1, 1, 256, a1);
+    }
+}
+
 hipError_t hipb_stream_wait(void) {
     hipb_before_stream();
     hipb.n_stream_sync++;
-    return hipStreamSynchronize(hipb.stream);
+    const hipError_t e = hipStreamSynchronize(hipb.stream);
+    if (e == hipSuccess) comb_check();
+    return e;
 }
 
 static void hb_shutdown(void);
@@ -611,6 +651,7 @@ static int hb_init(void) {
         return -1;
     }
     memset(&hipb, 0, sizeof(hipb));
+    kgen_prelude_reset();
     const char *dev = getenv("THVM_HIP_DEVICE");
     hipb.device = dev ? atoi(dev) : 0;
     if (hipSetDevice(hipb.device) != hipSuccess) {
@@ -641,6 +682,18 @@ static int hb_init(void) {
     if (pool_init() != 0) return -1;
     hipb.dummy = pool_block_get(256, &hipb.dummy_cap);
     if (!hipb.dummy || hipMemset(hipb.dummy, 0, 256) != hipSuccess) return -1;
+    /* the word a single-pass combine sets when it gives up waiting: host
+     * memory the GPU writes, read after each wait on the stream */
+    if (hipHostMalloc((void **)&hipb.comb_err_host, 256, hipHostMallocMapped | hipHostMallocCoherent) != hipSuccess ||
+        hipHostGetDevicePointer((void **)&hipb.comb_err_dev, hipb.comb_err_host, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        fprintf(stderr, "tinyhvm-hip: no host-mapped word for combine reports\n");
+        if (hipb.comb_err_host) HIPB_CHECK(hipHostFree(hipb.comb_err_host));
+        hipb.comb_err_host = NULL;
+        hipb.comb_err_dev = NULL;
+    } else {
+        *(volatile u32 *)hipb.comb_err_host = 0;
+    }
     if (rtc_init() != 0) return -1;
     /* the single-pass combine area, zeroed once by a kernel */
     {
@@ -680,6 +733,9 @@ static void hb_shutdown(void) {
     hipb.comb_slots = NULL;
     pool_block_put(hipb.dummy, hipb.dummy_cap);
     hipb.dummy = NULL;
+    if (hipb.comb_err_host) HIPB_CHECK(hipHostFree(hipb.comb_err_host));
+    hipb.comb_err_host = NULL;
+    hipb.comb_err_dev = NULL;
     pool_shutdown();
     HIPB_CHECK(hipStreamDestroy(hipb.stream));
     hipb.initialized = 0;
@@ -923,6 +979,22 @@ int thvm_hip_chain_merge(const UOpKernel *p, const u32 *pb, const UOpKernel *c, 
     return r;
 }
 
+/* A program that ran fused into another launch (an epilogue or a merged
+ * chain) still gets the cache entries its own dispatch would leave: the
+ * recognizers' negative entries and its compiled kernel. The dispatch
+ * without allocation, which never compiles, then runs it on its own. */
+static void hb_prepare_standalone(const UOpKernel *k) {
+    static u64 refused[64];   /* programs the generator or hipRTC refused on their own */
+    static u32 n_refused;
+    const u64 key = uop_signature(k);
+    if (rtc_lookup(key, k)) return;
+    for (u32 i = 0; i < n_refused && i < 64; i++)
+        if (refused[i] == key) return;
+    if (!hipb.no_dense) dense_note_plain(k);
+    if (!hipb.no_window) window_note_plain(k);
+    if (!rtc_compile_uop(key, k)) refused[n_refused++ % 64] = key;
+}
+
 static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
                                    const UOpKernel *k, u64 cache_key) {
     (void)cache_key;
@@ -941,12 +1013,16 @@ static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_lea
     hipb.n_dispatch++;
     copyq_guard_dispatch(out_buf, leaf_bufs, n_leaves < FUSE_MAX_LEAVES ? n_leaves : FUSE_MAX_LEAVES);
     pool_sync_device(out_buf);
-    if (hb_try_epilogue(out_buf, leaf_bufs, n_leaves, k)) {
+    if (!hipb.force_interp && hb_try_epilogue(out_buf, leaf_bufs, n_leaves, k)) {
         pool_mark_device_write(out_buf);
+        hb_prepare_standalone(k);
         return;
     }
-    if (!hipb.force_interp && hb_try_chain(out_buf, leaf_bufs, n_leaves, k)) return;
-    if (!hipb.no_dense && dense_try_dispatch(out_buf, leaf_bufs, n_leaves, k)) {
+    if (!hipb.force_interp && hb_try_chain(out_buf, leaf_bufs, n_leaves, k)) {
+        hb_prepare_standalone(k);
+        return;
+    }
+    if (!hipb.no_dense && !hipb.force_interp && dense_try_dispatch(out_buf, leaf_bufs, n_leaves, k)) {
         pool_mark_device_write(out_buf);
         hipb.n_dense++;
         return;
@@ -1462,52 +1538,11 @@ int thvm_hip_counters(u64 *out, u32 n) {
     u32 pinned = 0, limbo = 0;
     pool_stats(&live, &cached, &mallocs);
     pool_pin_stats(&pinned, &limbo);
-    u64 v[13] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
-                 hipb.n_stream_sync, live, mallocs, pinned, limbo, hipb.n_window, hipb.n_batched, hipb.n_fused};
-    for (u32 i = 0; out && i < n && i < 13; i++) out[i] = v[i];
-    return 13;
-}
-
-int thvm_hip_mfma_probe(u32 waves_per_cu, u32 iters, double *tflops) {
-    if (!hipb.initialized || !tflops || waves_per_cu == 0 || waves_per_cu > 32 || iters == 0 || iters > 100000)
-        return -1;
-    hipFunction_t fn = rtc_static_fn("thvm_mfma_probe"), fill = rtc_static_fn("thvm_fill_u32");
-    const u32 cus = hipb.n_cu ? hipb.n_cu : 256u, blocks = cus * waves_per_cu / 4u;
-    u64 c_in = 0, c_out = 0;
-    float *in = pool_block_get(4096 * 4, &c_in), *out = pool_block_get((u64)blocks * 256u * 4u, &c_out);
-    hipEvent_t e0, e1;
-    int rc = -1;
-    if (!fn || !fill || !in || !out || blocks == 0) goto done;
-    if (hipEventCreate(&e0) != hipSuccess) goto done;
-    if (hipEventCreate(&e1) != hipSuccess) {
-        HIPB_CHECK(hipEventDestroy(e0));
-        goto done;
-    }
-    {
-        u32 n = 4096, one = 0x3f800000u;   /* 1.0f */
-        void *pf[] = {&in, &n, &one};
-        void *pp[] = {&in, &out, &iters};
-        hipb_launch(fill, 16, 1, 1, 256, pf);
-        hipb_launch(fn, blocks, 1, 1, 256, pp);   /* warm-up */
-        HIPB_CHECK(hipEventRecord(e0, hipb.stream));
-        for (int r = 0; r < 5; r++) hipb_launch(fn, blocks, 1, 1, 256, pp);
-        HIPB_CHECK(hipEventRecord(e1, hipb.stream));
-        if (hipEventSynchronize(e1) == hipSuccess) {
-            float ms = 0.0f;
-            if (hipEventElapsedTime(&ms, e0, e1) == hipSuccess && ms > 0.0f) {
-                /* 5 launches x blocks x 4 waves x iters x 8 MFMAs x 32*32*2*2 FLOP */
-                *tflops = 5.0 * blocks * 4.0 * iters * 8.0 * 4096.0 / (ms * 1e-3) / 1e12;
-                rc = 0;
-            }
-        }
-        HIPB_CHECK(hipEventDestroy(e0));
-        HIPB_CHECK(hipEventDestroy(e1));
-    }
-done:
-    HIPB_CHECK(hipb_stream_wait());
-    pool_block_put(in, c_in);
-    pool_block_put(out, c_out);
-    return rc;
+    u64 v[14] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
+                 hipb.n_stream_sync, live, mallocs, pinned, limbo, hipb.n_window, hipb.n_batched, hipb.n_fused,
+                 hipb.n_comb_gaveup};
+    for (u32 i = 0; out && i < n && i < 14; i++) out[i] = v[i];
+    return 14;
 }
 
 int thvm_hip_synchronize(void) {
@@ -1517,6 +1552,10 @@ int thvm_hip_synchronize(void) {
     hipError_t e = hipb_stream_wait();
     if (e != hipSuccess) {
         fprintf(stderr, "tinyhvm-hip: stream error: %s\n", hipGetErrorString(e));
+        return -1;
+    }
+    if (hipb.comb_gaveup_pending) {
+        hipb.comb_gaveup_pending = 0;
         return -1;
     }
     return 0;

@@ -1306,6 +1306,7 @@ typedef struct {
     CoForm co, co_sum;            /* co-launch forms of the main and split-K sum kernels */
     u32 serial;                   /* unique in the process (entries move when the table grows) */
     UOpKernel *kcopy;             /* the program, kept when its launch can take a fused epilogue */
+    u32 cap;                      /* workgroups of the main kernel the GPU holds at once */
 } DenseEntry;
 
 /* Modules of a contraction with the elementwise program that consumes its
@@ -1846,6 +1847,20 @@ static int kperm_fits(const GemmPlan *pl, const u32 *counts, void *const *ptrs) 
     return 1;
 }
 
+/* Records that a program is not a contraction (the entry dense_try_dispatch
+ * would leave), without dispatching it: for a program that ran only fused
+ * into another launch, so that a later dispatch without allocation finds it.
+ * A contraction is left alone (its entry is made by its first dispatch). */
+void dense_note_plain(const UOpKernel *k) {
+    if (!k || k->n_leaves > FUSE_MAX_LEAVES) return;
+    u64 key = uop_signature(k) ^ 0xD5E5E5E5D5E5E5E5ull;
+    if (!key) key = 1;
+    if (lookup(key, k)) return;
+    u32 M, N, K, sp;
+    if (dense_analyze(k, &M, &N, &K, &sp)) return;
+    insert(key, k);
+}
+
 int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
     void *ptrs[FUSE_MAX_LEAVES + 1];
     u32 counts[FUSE_MAX_LEAVES + 1];
@@ -1896,6 +1911,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
             return 0;
         }
         co_form_make(&e->co, src, e->plan.name, dense_threads(&e->plan), e->fn);
+        e->cap = rtc_capacity(e->fn, dense_threads(&e->plan));
         if (e->plan.pack) {
             char nm[64];
             snprintf(nm, sizeof nm, "%s_pack", e->plan.name);
@@ -1940,7 +1956,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
      * once (the last split's workgroups wait for the others' words);
      * otherwise the partials go through the workspace and the sum kernel */
     unsigned long long *sl = NULL;
-    if (e->plan.comb && (u64)tiles * e->plan.splits * (threads / 64u) <= hipb_resident_waves()) sl = hipb.comb_slots;
+    if (e->plan.comb && (u64)tiles * e->plan.splits <= e->cap) sl = hipb.comb_slots;
     /* split-K workspace */
     float *ws = NULL;
     if (e->plan.splits > 1 && !sl) {

@@ -85,6 +85,11 @@ typedef struct {
     int noalloc;             /* a no-allocation dispatch is running: workspaces come from it */
     u64 noalloc_off;         /* bytes of the static workspace handed out in that dispatch */
     int noalloc_err;         /* why that dispatch could not run (THVM_HIP_E*), or 0 */
+    u32 *comb_err_host;      /* host-mapped word a single-pass combine sets when it gave up waiting */
+    u32 *comb_err_dev;       /* ... its device address, written into every loaded module */
+    u64 n_comb_gaveup;       /* waits after which such a word was found set */
+    int comb_gaveup_pending; /* ... since the last thvm_hip_synchronize */
+    int force_combine_launch; /* generate split reductions with a combine kernel (the grid does not fit at once) */
     int capturing;           /* a graph capture is open on the stream */
     int capture_bad;         /* the open capture met work a graph cannot replay */
 } HipbState;
@@ -188,6 +193,8 @@ int  kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, 
 void kgen_free(KGenResult *r);
 int  kgen_validate(const UOpKernel *k, char *err, size_t errlen);
 const char *kgen_prelude(void);
+/* rebuilt with the current knobs on the next kgen_prelude() (backend init) */
+void kgen_prelude_reset(void);
 int  kgen_alu_expr(u32 uop, u32 aux, const char *a, const char *b, char *out, size_t n);
 int  kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen);
 int  kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
@@ -301,6 +308,9 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k);
 hipFunction_t rtc_static_fn(const char *name);
 /* Compile HIP source and load it; returns the module (0 on failure). */
 int  rtc_build_module(const char *src, hipModule_t *mod, char *err, size_t errlen);
+/* Workgroups of `block` lanes of fn that the GPU holds at once (its
+ * occupancy per compute unit times the compute units), or 0. */
+u32  rtc_capacity(hipFunction_t fn, u32 block);
 /* Compile only (no device needed); returns the code size or -1. */
 long rtc_compile_only(const char *src, char *err, size_t errlen);
 u64  uop_signature(const UOpKernel *k);
@@ -310,6 +320,8 @@ int  dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
 int  dense_analyze(const UOpKernel *k, u32 *M, u32 *N, u32 *K, u32 *splits);
 char *dense_source(const UOpKernel *k);
 void dense_reset_stats(void);
+/* a program that is not a contraction gets its (negative) entry without a dispatch */
+void dense_note_plain(const UOpKernel *k);
 void dense_shutdown(void);
 
 /* ---------------- pooling windows and run sums ---------------- */
@@ -318,6 +330,8 @@ int  window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const 
 int  window_analyze(const UOpKernel *k, u32 *kind, u32 *splits);
 char *window_source(const UOpKernel *k);
 void window_shutdown(void);
+/* a program that is neither gets its (negative) entry without a dispatch */
+void window_note_plain(const UOpKernel *k);
 
 /* ---------------- launch helpers ---------------- */
 int  hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params);

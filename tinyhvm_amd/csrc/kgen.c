@@ -819,7 +819,9 @@ static void emit_range_seq(Gen *g, u32 lo, u32 hi, int fast, int in_ploop) {
     }
 }
 
-static const char *PRELUDE =
+static const char *PRELUDE_BODY =
+"#ifndef THVM_COMB_SPIN\n#define THVM_COMB_SPIN (1u << 22)\n#endif\n"
+"#ifndef THVM_COMB_WITHHOLD\n#define THVM_COMB_WITHHOLD 0\n#endif\n"
 "typedef unsigned int u32;\n"
 "typedef unsigned short u16;\n"
 "/* f16 decode (exact) */\n"
@@ -953,6 +955,14 @@ static const char *PRELUDE =
 "  for (u32 w = 1u; w < NW; w++) { float y = red[w]; s = (s > y) ? s : y; }\n"
 "  return s;\n"
 "}\n"
+/* Where a single-pass combine reports that it gave up waiting for a
+ * partial: a word of host-visible memory whose device address the host
+ * writes into every module it loads (NULL: not reported). */
+"extern \"C\" { __device__ unsigned int* thvm_comb_err_ = nullptr; }\n"
+"__device__ __forceinline__ void comb_gave_up() {\n"
+"  unsigned int* e = thvm_comb_err_;\n"
+"  if (e) __hip_atomic_store(e, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);\n"
+"}\n"
 /* Single-pass combine of per-workgroup partials. Each of the S workgroups
  * of output o but the last publishes its partial as one 64-bit word (a ready
  * flag in the high half, the float's bits in the low half) with an
@@ -963,8 +973,12 @@ static const char *PRELUDE =
  * is needed, no cache is written back and no word is contended; the result
  * does not depend on timing. The host uses it only for grids that fit on
  * the GPU at once (every workgroup resident together), so the waiting
- * workgroup never holds back one it waits for. */
+ * workgroup never holds back one it waits for. A wait that runs out
+ * (THVM_COMB_SPIN polls) takes a NaN for the partial and reports it through
+ * comb_gave_up. THVM_COMB_WITHHOLD (a test knob) keeps the partial of
+ * split 0 of output 0 unpublished, so that its wait runs out. */
 "__device__ __forceinline__ void comb_put(unsigned long long* sl, u32 o, u32 sp, u32 S, float part) {\n"
+"  if (THVM_COMB_WITHHOLD && o == 0u && sp == 0u) return;\n"
 "  if (threadIdx.x == 0u)\n"
 "    __hip_atomic_store(sl + (unsigned long long)o * S + sp, (1ull << 32) | (unsigned long long)__float_as_uint(part),\n"
 "                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
@@ -972,11 +986,12 @@ static const char *PRELUDE =
 "__device__ __forceinline__ float comb_take(unsigned long long* sl, u32 o, u32 s, u32 S) {\n"
 "  unsigned long long* w = sl + (unsigned long long)o * S + s;\n"
 "  unsigned long long v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
-"  for (u32 n = 0u; (v >> 32) == 0ull && n < (1u << 22); n++) {\n"
+"  for (u32 n = 0u; (v >> 32) == 0ull && n < THVM_COMB_SPIN; n++) {\n"
 "    __builtin_amdgcn_s_sleep(2);\n"
 "    v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
 "  }\n"
 "  __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
+"  if ((v >> 32) == 0ull) comb_gave_up();\n"
 "  return (v >> 32) ? __uint_as_float((u32)v) : __uint_as_float(0x7fc00000u);\n"
 "}\n"
 /* The same words for a block of partials: comb_pub publishes one,
@@ -993,17 +1008,41 @@ static const char *PRELUDE =
 "  return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
 "}\n"
 "__device__ __forceinline__ float comb_ready(unsigned long long* w, unsigned long long v) {\n"
-"  for (u32 n = 0u; (v >> 32) == 0ull && n < (1u << 22); n++) {\n"
+"  for (u32 n = 0u; (v >> 32) == 0ull && n < THVM_COMB_SPIN; n++) {\n"
 "    __builtin_amdgcn_s_sleep(2);\n"
 "    v = __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
 "  }\n"
+"  if ((v >> 32) == 0ull) comb_gave_up();\n"
 "  return (v >> 32) ? __uint_as_float((u32)v) : __uint_as_float(0x7fc00000u);\n"
 "}\n"
 "__device__ __forceinline__ void comb_clear(unsigned long long* w) {\n"
 "  __hip_atomic_store(w, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);\n"
 "}\n";
 
-const char *kgen_prelude(void) { return PRELUDE; }
+/* The prelude with the combine's wait bound and test knob
+ * (THVM_HIP_COMB_SPIN, THVM_HIP_COMB_WITHHOLD), read when it is first built
+ * after each kgen_prelude_reset (backend init). */
+static char *prelude_buf;
+
+void kgen_prelude_reset(void) {
+    free(prelude_buf);
+    prelude_buf = NULL;
+}
+
+const char *kgen_prelude(void) {
+    if (prelude_buf) return prelude_buf;
+    const char *e = getenv("THVM_HIP_COMB_SPIN");
+    unsigned long spin = e ? strtoul(e, NULL, 10) : 0;
+    if (spin == 0 || spin > (1ul << 24)) spin = 1ul << 22;
+    const char *w = getenv("THVM_HIP_COMB_WITHHOLD");
+    const int withhold = w && w[0] && strcmp(w, "0") != 0;
+    const size_t cap = strlen(PRELUDE_BODY) + 128;
+    char *b = malloc(cap);
+    if (!b) return PRELUDE_BODY;   /* the knobs' defaults are in the body too */
+    snprintf(b, cap, "#define THVM_COMB_SPIN %luu\n#define THVM_COMB_WITHHOLD %d\n%s", spin, withhold, PRELUDE_BODY);
+    prelude_buf = b;
+    return prelude_buf;
+}
 
 /* Scalar straight-line code for the ops flagged in `cone` (in op order), as
  * the body of a device function: GID reads `gid_expr`, the top-level RANGE
@@ -1429,7 +1468,7 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
     /* The partials combine in the same launch when the whole grid fits on
      * the GPU at once; a larger grid writes them to a workspace for a
      * combine kernel. */
-    G.combine_launch = G.combine_mode == 1 ||
+    G.combine_launch = G.combine_mode == 1 || hipb.force_combine_launch ||
                        (G.combine_mode == 0 && (u64)G.total * G.splits * (G.block / 64) > hipb_resident_waves());
     G.scal = malloc(k->n_ops * sizeof(i32));
     if (!G.scal) { free(G.oi); snprintf(err, errlen, "oom"); return 0; }
@@ -1446,7 +1485,7 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
     analyze_global(&G);
 
     SB *s = &G.sb;
-    sb_put(s, "%s\n", PRELUDE);
+    sb_put(s, "%s\n", kgen_prelude());
     {
         int has_loop = 0;
         for (u32 i = 0; i < k->n_ops; i++) if (k->ops[i].type == KOP_RANGE) has_loop = 1;

@@ -12,6 +12,7 @@
  * Compile options: gfx950, -O3, no FP contraction (a*b+c stays two rounded
  * ops, as in the x86 reference build), packed FP32 instructions disabled.
  */
+#include <pthread.h>
 #include <stdlib.h>
 #include <string.h>
 #include <hip/hiprtc.h>
@@ -154,8 +155,75 @@ static KCacheEntry *insert_slot(u64 key) {
     return &R.tab[p];
 }
 
+/* Code objects compiled in this process, by source text: a backend that is
+ * shut down and initialised again (tests, a serving process that restarts
+ * its context) loads them instead of compiling again. The whole text is
+ * compared on a hit; at most CODE_CACHE_BYTES are kept. */
+#define CODE_CACHE_BYTES (256ull << 20)
+typedef struct CodeEnt {
+    u64 h;
+    char *src;
+    char *code;
+    size_t len;
+    struct CodeEnt *next;
+} CodeEnt;
+static struct {
+    CodeEnt *bucket[1024];
+    u64 bytes;
+    pthread_mutex_t mu;
+} CC = {.mu = PTHREAD_MUTEX_INITIALIZER};
+
+static u64 text_hash(const char *s) {
+    u64 h = 0xcbf29ce484222325ull;
+    for (; *s; s++) h = (h ^ (u8)*s) * 0x100000001b3ull;
+    return h;
+}
+
+static char *code_cache_get(const char *src, u64 h, size_t *len) {
+    char *out = NULL;
+    pthread_mutex_lock(&CC.mu);
+    for (CodeEnt *e = CC.bucket[h & 1023]; e; e = e->next)
+        if (e->h == h && strcmp(e->src, src) == 0) {
+            out = malloc(e->len);
+            if (out) {
+                memcpy(out, e->code, e->len);
+                *len = e->len;
+            }
+            break;
+        }
+    pthread_mutex_unlock(&CC.mu);
+    return out;
+}
+
+static void code_cache_put(const char *src, u64 h, const char *code, size_t len) {
+    const size_t sl = strlen(src) + 1;
+    pthread_mutex_lock(&CC.mu);
+    if (CC.bytes + sl + len <= CODE_CACHE_BYTES) {
+        CodeEnt *e = malloc(sizeof *e);
+        char *s2 = e ? malloc(sl) : NULL, *c2 = s2 ? malloc(len) : NULL;
+        if (c2) {
+            memcpy(s2, src, sl);
+            memcpy(c2, code, len);
+            e->h = h;
+            e->src = s2;
+            e->code = c2;
+            e->len = len;
+            e->next = CC.bucket[h & 1023];
+            CC.bucket[h & 1023] = e;
+            CC.bytes += sl + len;
+        } else {
+            free(s2);
+            free(e);
+        }
+    }
+    pthread_mutex_unlock(&CC.mu);
+}
+
 /* Compile HIP source to a gfx950 code object. Returns malloc'd code. */
 static char *compile_source(const char *src, size_t *code_len, char *err, size_t errlen) {
+    const u64 h = text_hash(src);
+    char *hit = code_cache_get(src, h, code_len);
+    if (hit) return hit;
     hiprtcProgram prog;
     if (hiprtcCreateProgram(&prog, src, "thvm_kernel.hip", 0, NULL, NULL) != HIPRTC_SUCCESS) {
         snprintf(err, errlen, "hiprtcCreateProgram failed");
@@ -182,7 +250,31 @@ static char *compile_source(const char *src, size_t *code_len, char *err, size_t
     if (code) hiprtcGetCode(prog, code);
     hiprtcDestroyProgram(&prog);
     *code_len = cs;
+    if (code) code_cache_put(src, h, code, cs);
     return code;
+}
+
+/* A loaded module's pointer to the combine give-up word (thvm_comb_err_, in
+ * the prelude) is set to the backend's word. */
+static void module_setup(hipModule_t mod) {
+    if (!hipb.comb_err_dev) return;
+    hipDeviceptr_t p = 0;
+    size_t n = 0;
+    if (hipModuleGetGlobal(&p, &n, mod, "thvm_comb_err_") != hipSuccess || n != sizeof(void *)) {
+        (void)hipGetLastError();   /* the module has no combine: nothing to set */
+        return;
+    }
+    HIPB_CHECK(hipMemcpyHtoD(p, &hipb.comb_err_dev, sizeof(void *)));
+}
+
+u32 rtc_capacity(hipFunction_t fn, u32 block) {
+    int nb = 0;
+    if (!fn || block == 0 || hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&nb, fn, (int)block, 0) != hipSuccess ||
+        nb <= 0) {
+        (void)hipGetLastError();
+        return 0;
+    }
+    return (u32)nb * (hipb.n_cu ? hipb.n_cu : 256u);
 }
 
 int rtc_build_module(const char *src, hipModule_t *mod, char *err, size_t errlen) {
@@ -195,6 +287,7 @@ int rtc_build_module(const char *src, hipModule_t *mod, char *err, size_t errlen
         snprintf(err, errlen, "hipModuleLoadData: %s", hipGetErrorString(he));
         return 0;
     }
+    module_setup(*mod);
     hipb.n_compile++;
     return 1;
 }
@@ -340,7 +433,12 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
     char err[256] = {0};
     KGenResult g;
     if (hipb.rtc_fail) return NULL;   /* test knob: every compile fails */
-    if (!kgen_uop(k, &g, err, sizeof err)) {
+    int comb_launch = 0;
+again:
+    hipb.force_combine_launch = comb_launch;
+    const int gen_ok = kgen_uop(k, &g, err, sizeof err);
+    hipb.force_combine_launch = 0;
+    if (!gen_ok) {
         fprintf(stderr, "tinyhvm-hip: kernel rejected: %s\n", err);
         return NULL;
     }
@@ -359,6 +457,7 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
         kgen_free(&g);
         return NULL;
     }
+    module_setup(mod);
     hipFunction_t fn, fn_fin = NULL;
     char fin_name[48];
     snprintf(fin_name, sizeof fin_name, "%s_fin", g.name);
@@ -368,6 +467,18 @@ KCacheEntry *rtc_compile_uop(u64 key, const UOpKernel *k) {
         HIPB_CHECK(hipModuleUnload(mod));
         kgen_free(&g);
         return NULL;
+    }
+    /* one pass only if the whole grid is on the GPU at once with this
+     * kernel's own occupancy (registers, LDS); else the combine kernel */
+    if (g.splits > 1 && !g.combine_launch && !comb_launch &&
+        (u64)g.total * g.splits > rtc_capacity(fn, g.block)) {
+        if (hipb.verbose)
+            fprintf(stderr, "tinyhvm-hip: %s: %llu workgroups exceed what the GPU holds at once (%u): combine kernel\n",
+                    g.name, (unsigned long long)g.total * g.splits, rtc_capacity(fn, g.block));
+        HIPB_CHECK(hipModuleUnload(mod));
+        kgen_free(&g);
+        comb_launch = 1;
+        goto again;
     }
     KCacheEntry *e = insert_slot(key);
     if (!e) {

@@ -6,8 +6,6 @@
 //                    the legacy per-op slots (src/backend/cpu/ops.c)
 //   thvm_copy_batch  several buffer-to-buffer copies in one launch
 //   thvm_fill_u32    fill a buffer with a 32-bit pattern (graph-safe clear)
-//   thvm_mfma_probe  f32 MFMA issue rate with no memory traffic (a
-//                    calibration of the sustained matrix-core rate)
 //   thvm_adam        the adam_step slot: one fused pass over parameter,
 //                    gradient and both moments
 //   thvm_kop         KOp program interpreter: the dispatch_uop_kernel path
@@ -398,31 +396,6 @@ extern "C" __global__ __launch_bounds__(256) void thvm_copy_batch(CopyBatch B) {
 extern "C" __global__ __launch_bounds__(256) void thvm_fill_u32(u32 *dst, u32 n, u32 value) {
     const u32 t = blockIdx.x * 256u + threadIdx.x;
     if (t < n) dst[t] = value;
-}
-
-// Sustained f32 MFMA rate: every wave runs iters x 8 v_mfma_f32_32x32x2f32
-// on four independent accumulators from register operands (no loads in the
-// loop), then stores one value per lane so that nothing is dropped. `in`
-// holds at least 4096 floats; `out` one float per lane of the grid.
-typedef float probe_f32x16 __attribute__((ext_vector_type(16)));
-extern "C" __global__ __launch_bounds__(256) void thvm_mfma_probe(const float *in, float *out, u32 iters) {
-    const u32 t = blockIdx.x * 256u + threadIdx.x;
-    const float a0 = in[t % 4096u], a1 = in[(t + 7u) % 4096u], b0 = in[(t + 13u) % 4096u], b1 = in[(t + 29u) % 4096u];
-    probe_f32x16 c0 = {0}, c1 = {0}, c2 = {0}, c3 = {0};
-    for (u32 i = 0; i < iters; i++) {
-        c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, c0, 0, 0, 0);
-        c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, c1, 0, 0, 0);
-        c2 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, c2, 0, 0, 0);
-        c3 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, c3, 0, 0, 0);
-        c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b1, c0, 0, 0, 0);
-        c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b1, c1, 0, 0, 0);
-        c2 = __builtin_amdgcn_mfma_f32_32x32x2f32(a1, b0, c2, 0, 0, 0);
-        c3 = __builtin_amdgcn_mfma_f32_32x32x2f32(a0, b0, c3, 0, 0, 0);
-    }
-    const probe_f32x16 s = (c0 + c1) + (c2 + c3);
-    float r = 0.0f;
-    for (int i = 0; i < 16; i++) r += s[i];
-    out[t] = r;
 }
 
 // adam_step with the arithmetic of the engine's lazy update, the CPU

@@ -661,6 +661,17 @@ char *window_source(const UOpKernel *k) {
     return gen_window(k, &p, name, sizeof name);
 }
 
+/* Records that a program is neither a window max nor a run sum (the entry
+ * window_try_dispatch would leave), without dispatching it: for a program
+ * that ran only fused into another launch. */
+void window_note_plain(const UOpKernel *k) {
+    if (!k || k->n_leaves > FUSE_MAX_LEAVES) return;
+    const u64 key = win_key(k);
+    WinPlan p;
+    if (win_lookup(key, k) || win_recognize(k, &p)) return;
+    win_insert(key, k);
+}
+
 int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
     if (k->n_leaves > FUSE_MAX_LEAVES) return 0;
     u64 key = win_key(k);
@@ -674,6 +685,7 @@ int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
         if (!e) return 0;
         if (!win_recognize(k, &e->plan)) return 0;    /* kind stays WIN_NONE */
         char name[48], err[256] = {0};
+    build:;
         char *src = gen_window(k, &e->plan, name, sizeof name);
         if (!src) return 0;
         if (hipb.dump_src) fprintf(stderr, "---- window kernel ----\n%s\n", src);
@@ -690,6 +702,15 @@ int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
             HIPB_CHECK(hipModuleUnload(e->mod));
             free(src);
             return 0;
+        }
+        /* one pass only if the whole grid is on the GPU at once with this
+         * kernel's own occupancy; else partials go to a combine kernel */
+        if (e->plan.kind == WIN_SUM && e->plan.S > 1 && !e->plan.launch &&
+            (u64)e->plan.total * e->plan.S > rtc_capacity(e->fn, WIN_BLOCK)) {
+            HIPB_CHECK(hipModuleUnload(e->mod));
+            free(src);
+            e->plan.launch = 1;
+            goto build;
         }
         if (!(e->plan.kind == WIN_SUM && e->plan.S > 1 && e->plan.launch))
             co_form_make(&e->co, src, name, WIN_BLOCK, e->fn);
