@@ -33,9 +33,15 @@ region, since the engine's interpreter loads masked pad elements before the
 mask discards them.
 
 lenet_engine, mlp_engine: the same training steps driven by the engine itself
-(thvm_eval with hip_backend as its default device; oracle/_ref/engine_live in
+(thvm_eval on a context made by thvm_init("hip"); oracle/_ref/engine_live in
 a child process): the rate a user of the engine gets, host work included,
 with the host's stream waits per step counted beside the step's read-backs.
+
+lenet_engine_graph, mlp_engine_graph: such an engine-driven step captured
+once into a HIP graph and launched for every later step with new labels
+written in between (the Metal backend's JIT record/replay role): steps/s with
+the label write and the loss read, checked bit for bit against the same
+number of eager engine steps.
 """
 import argparse
 import ctypes as C
@@ -407,6 +413,47 @@ def engine_step(name, want_cpu):
     return res
 
 
+ENGINE_JIT = {
+    "lenet_engine_graph": ("lenet", 50, 256, "LeNet-5 training step at batch 256 through the engine, captured "
+                                             "once into a HIP graph and replayed"),
+    "mlp_engine_graph": ("mlp", 100, 64, "2-layer MLP training step (SGD) at batch 64 through the engine, "
+                                         "captured once into a HIP graph and replayed"),
+}
+
+
+def engine_jit(name):
+    """A training step the engine drives (thvm_eval on a context made by
+    thvm_init("hip")), captured once into a HIP graph and launched for every
+    later step, the role of the Metal backend's JIT record/replay: each step
+    writes its labels into the persistent one-hot tensor, launches the graph
+    and reads the loss back (host clock). oracle/_ref/engine_live runs the
+    same steps eagerly through the engine first and checks that every loss and
+    the final parameters agree bit for bit."""
+    exe = os.path.join(ROOT, "oracle", "_ref", "engine_live")
+    if not os.path.exists(exe):
+        print("engine jit: oracle/_ref/engine_live is not built", file=sys.stderr)
+        return None
+    wl, steps, batch, what = ENGINE_JIT[name]
+    cmd = [exe, os.path.join(ROOT, "tinyhvm_amd", "libthvm_hip.so"), "jit", wl, str(steps), str(batch)]
+    print("engine jit: %s" % " ".join(cmd), file=sys.stderr, flush=True)
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    lines = [ln for ln in r.stdout.splitlines() if ln.startswith("{")]
+    if not lines:
+        sys.stderr.write(r.stderr[-2000:])
+        return None
+    e = json.loads(lines[-1])
+    res = {"value": e["graph"]["steps_per_s"], "unit": "steps/s", "ms_per_step": e["graph"]["ms_per_step"],
+           "eager_value": e["eager"]["steps_per_s"], "eager_ms_per_step": e["eager"]["ms_per_step"],
+           "config": {"workload": what + " (label write, graph launch and loss read per step, host clock, "
+                                         "%d steps)" % steps, "batch": batch},
+           "losses_equal_eager": e["losses_equal"], "params_equal_eager": e["params_equal"],
+           "loss_first": e["loss_first"], "loss_last": e["loss_last"]}
+    if r.returncode != 0:
+        res["error"] = "graph replays differ from the engine's eager steps"
+    print("%s: %s" % (name, json.dumps(res)), file=sys.stderr, flush=True)
+    return res
+
+
 def copy_calibration(nbytes=256 << 20, reps=5):
     """A plain copy kernel of known size through the same generated-kernel
     path (out[i] = src[i]): the reference reading for the HBM byte counters."""
@@ -441,42 +488,20 @@ def copy_calibration(nbytes=256 << 20, reps=5):
                       "ms_per_copy": round(ms, 4), "GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}))
 
 
-def mfma_calibration():
-    """The f32 matrix-core rate a kernel sustains on this GPU with no memory
-    traffic (thvm_hip_mfma_probe), at 4 to 32 waves per compute unit, beside
-    the published dense f32 peak the rooflines use."""
-    import ctypes as C
-    L = _lib.lib()
-    if L.thvm_hip_init() != 0:
-        raise SystemExit("HIP backend failed to initialise")
-    out = {}
-    for w in (4, 8, 16, 32):
-        t = C.c_double(0.0)
-        if L.thvm_hip_mfma_probe(w, 4000, C.byref(t)) != 0:
-            raise SystemExit("mfma probe failed")
-        out["%d_waves_per_cu" % w] = round(t.value, 1)
-    L.thvm_hip_shutdown()
-    print(json.dumps({"mfma_f32_tflops": out, "published_peak": MFMA_F32_PEAK_TFLOPS}))
-
-
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--workloads", default="fused,matmul,lenet,convblock,mlp,lenet_engine,mlp_engine",
+    ap.add_argument("--workloads", default="fused,matmul,lenet,convblock,mlp,lenet_engine,mlp_engine,"
+                                           "lenet_engine_graph,mlp_engine_graph",
                     help="comma list; the first one gives the headline value")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baselines")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="run only a 256 MiB copy kernel (HBM counter calibration)")
-    ap.add_argument("--calibrate-mfma", action="store_true",
-                    help="run only the f32 MFMA rate probe (register operands, no memory traffic)")
     args = ap.parse_args()
     if args.calibrate_copy:
         copy_calibration()
-        return
-    if args.calibrate_mfma:
-        mfma_calibration()
         return
     if args.gpus != 1:
         print("bench.py measures one GPU: this backend has no multi-GPU path "
@@ -484,8 +509,9 @@ def main():
         sys.exit(2)
     names = [w for w in args.workloads.split(",") if w]
     for nm in names:
-        if nm not in WORKLOADS and nm not in ENGINE_STEPS:
-            raise SystemExit("unknown workload %r (have %s)" % (nm, ", ".join(list(WORKLOADS) + list(ENGINE_STEPS))))
+        if nm not in WORKLOADS and nm not in ENGINE_STEPS and nm not in ENGINE_JIT:
+            raise SystemExit("unknown workload %r (have %s)" % (
+                nm, ", ".join(list(WORKLOADS) + list(ENGINE_STEPS) + list(ENGINE_JIT))))
     if names[0] not in WORKLOADS:
         raise SystemExit("the first workload gives the headline value: one of %s" % ", ".join(WORKLOADS))
     L = _lib.lib()
@@ -497,6 +523,8 @@ def main():
     for nm in names:
         if nm in ENGINE_STEPS:
             results[nm] = engine_step(nm, not args.no_cpu)
+        elif nm in ENGINE_JIT:
+            results[nm] = engine_jit(nm)
     head = results[names[0]]
     out = {
         "metric": METRIC,

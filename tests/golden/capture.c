@@ -791,66 +791,121 @@ static void wl_mlp_steps(TinyHVM *ctx, u32 B, u32 IN, u32 H, u32 C, int steps) {
     free(lab);
 }
 
+/* The engine's cross-entropy composition (src/nn/loss.c:8-44: the row max,
+ * logsumexp, minus the label's logit, summed and scaled by 1/B) with the
+ * one-hot labels read from a persistent tensor, where the engine's
+ * cross_entropy_loss makes a new one-hot tensor from host labels at every
+ * call: the form of a step that is captured once and replayed with new
+ * labels written into the same tensor (as the engine's JIT test builds its
+ * loss from a persistent one-hot, test/archive/test_jit_dense.m:47-60).
+ * Intermediates used twice are realized (no DUP needed). [1,1]. */
+static Term ce_loss_onehot(TinyHVM *ctx, Term logits, Term onehot, u32 B, u32 C) {
+    Term mx = realize_as(ctx, thvm_rmax_axes(ctx, logits, (u32[]){1}, 1), SHAPE(B, 1));
+    Term sh = binary(ctx, UOP_SUB, logits, thvm_expand(ctx, mx, SHAPE(B, C)));
+    Term se = realize_as(ctx, thvm_sum_axes(ctx, unary(ctx, UOP_EXP, sh), (u32[]){1}, 1), SHAPE(B, 1));
+    Term lse = binary(ctx, UOP_ADD, mx, unary(ctx, UOP_LOG, se));
+    Term pick = thvm_sum_axes(ctx, binary(ctx, UOP_MUL, onehot, logits), (u32[]){1}, 1);
+    Term row = binary(ctx, UOP_SUB, lse, pick);
+    Term tot = thvm_sum_axes(ctx, row, (u32[]){0, 1}, 2);
+    return realize_as(ctx, binary(ctx, UOP_MUL, tot, scalar_t(ctx, 1.0f / (f32)B)), SHAPE(1, 1));
+}
+
+/* SGD through the engine's ASSIGN, with the loss assigned to a persistent
+ * tensor in the same evaluation (nothing read back). */
+static void sgd_keep_loss(TinyHVM *ctx, Term *params, Term *grads, u32 n, f32 lr, Term loss_out, Term loss) {
+    Term chain = thvm_assign(ctx, loss_out, loss);
+    for (u32 i = 0; i < n; i++) {
+        Term upd = binary(ctx, UOP_SUB, params[i], binary(ctx, UOP_MUL, grads[i], scalar_t(ctx, lr)));
+        chain = thvm_seq(ctx, chain, thvm_assign(ctx, params[i], upd));
+    }
+    thvm_eval(ctx, chain);
+}
+
+/* One LeNet-5 training step on persistent tensors: forward, backward, SGD
+ * (lr 0.01) through ASSIGN. With host labels `lab`, the loss is the
+ * engine's cross_entropy_loss, realized and read back after the forward;
+ * with lab NULL it is ce_loss_onehot over the persistent one-hot tensor and
+ * is assigned to loss_out with the parameter updates, nothing being read:
+ * the step a caller captures once and replays. */
+static void lenet_step(TinyHVM *ctx, u32 B, Term x, Term *params, Term onehot, const u8 *lab, Term loss_out) {
+    Term W1 = params[0], b1 = params[1], W2 = params[2], b2 = params[3], W3 = params[4], b3 = params[5];
+    Term W4 = params[6], b4 = params[7], W5 = params[8], b5 = params[9];
+    rec_mark("lenet.fwd");
+    Term xp = pad_exact(ctx, x, B, 1, 28, 28, 2);
+    Term a1 = realize_as(ctx, unary(ctx, UOP_RELU,
+                         thvm_conv2d(ctx, xp, W1, b1, 1, (u32[]){1, 1}, (u32[]){0, 0, 0, 0})),
+                         shape_of((u32[]){B, 6, 28, 28}, 4));
+    Term p1 = realize_as(ctx, thvm_maxpool2d(ctx, a1, (u32[]){2, 2}, (u32[]){2, 2}),
+                         shape_of((u32[]){B, 6, 14, 14}, 4));
+    Term a2 = realize_as(ctx, unary(ctx, UOP_RELU,
+                         thvm_conv2d(ctx, p1, W2, b2, 1, (u32[]){1, 1}, (u32[]){0, 0, 0, 0})),
+                         shape_of((u32[]){B, 16, 10, 10}, 4));
+    Term p2 = realize_as(ctx, thvm_maxpool2d(ctx, a2, (u32[]){2, 2}, (u32[]){2, 2}),
+                         shape_of((u32[]){B, 16, 5, 5}, 4));
+    Term f = alias_as(ctx, p2, SHAPE(B, 400));
+    Term h3 = dense(ctx, f, W3, b3, 1, B, 120);
+    Term h4 = dense(ctx, h3, W4, b4, 1, B, 84);
+    Term logits = dense(ctx, h4, W5, b5, 0, B, 10);
+    Term loss = term_era();
+    if (lab) {
+        loss = realize(ctx, cross_entropy_loss(ctx, logits, (u8 *)lab, B, 10));
+        readback(ctx, loss);
+    } else {
+        loss = ce_loss_onehot(ctx, logits, onehot, B, 10);
+    }
+    rec_mark("lenet.bwd");
+    Term d5 = ce_grad(ctx, logits, onehot, B, 10);
+    DenseGrads g5 = dense_bwd(ctx, h4, W5, d5, B, 84, 10, 1);
+    Term dz4 = realize_as(ctx, binary(ctx, UOP_MUL, g5.dx, binary(ctx, UOP_CMP, h4, scalar_t(ctx, 0.0f))),
+                          SHAPE(B, 84));
+    DenseGrads g4 = dense_bwd(ctx, h3, W4, dz4, B, 120, 84, 1);
+    Term dz3 = realize_as(ctx, binary(ctx, UOP_MUL, g4.dx, binary(ctx, UOP_CMP, h3, scalar_t(ctx, 0.0f))),
+                          SHAPE(B, 120));
+    DenseGrads g3 = dense_bwd(ctx, f, W3, dz3, B, 400, 120, 1);
+    Term dp2 = alias_as(ctx, g3.dx, shape_of((u32[]){B, 16, 5, 5}, 4));
+    Term dz2 = pool_relu_bwd(ctx, dp2, p2, a2, B, 16, 10, 10);
+    Term dW2 = conv_dw(ctx, p1, dz2, B, 6, 16, 5, 10, 10);
+    Term db2 = chansum(ctx, dz2, 16);
+    Term dp1 = conv_dx(ctx, dz2, W2, B, 16, 6, 5, 0, 14, 14);
+    Term dz1 = pool_relu_bwd(ctx, dp1, p1, a1, B, 6, 28, 28);
+    Term dW1 = conv_dw(ctx, xp, dz1, B, 1, 6, 5, 28, 28);
+    Term db1 = chansum(ctx, dz1, 6);
+    rec_mark("lenet.sgd");
+    Term grads[10] = {dW1, db1, dW2, db2, g3.dW, g3.db, g4.dW, g4.db, g5.dW, g5.db};
+    if (lab) sgd(ctx, params, grads, 10, 0.01f);
+    else sgd_keep_loss(ctx, params, grads, 10, 0.01f, loss_out, loss);
+}
+
+/* LeNet-5's persistent tensors: x [B,1,28,28] ~ U(0,1), the ten parameters
+ * (Kaiming-uniform weights, zero biases) in the order W1, b1, ..., W5, b5. */
+static Term lenet_params(TinyHVM *ctx, u32 B, Term *params) {
+    Term x = gen_tensor(ctx, shape_of((u32[]){B, 1, 28, 28}, 4), DTYPE_F32, TRC_GEN_UNIFORM, 4001, 0.f, 1.f);
+    params[0] = kaiming_u(ctx, shape_of((u32[]){6, 1, 5, 5}, 4), 25, 4002);
+    params[1] = zeros(ctx, SHAPE(6), 4003);
+    params[2] = kaiming_u(ctx, shape_of((u32[]){16, 6, 5, 5}, 4), 150, 4004);
+    params[3] = zeros(ctx, SHAPE(16), 4005);
+    params[4] = kaiming_u(ctx, SHAPE(400, 120), 400, 4006);
+    params[5] = zeros(ctx, SHAPE(120), 4007);
+    params[6] = kaiming_u(ctx, SHAPE(120, 84), 120, 4008);
+    params[7] = zeros(ctx, SHAPE(84), 4009);
+    params[8] = kaiming_u(ctx, SHAPE(84, 10), 84, 4010);
+    params[9] = zeros(ctx, SHAPE(10), 4011);
+    return x;
+}
+
 /* LeNet-5 training step: x [B,1,28,28] ~ U(0,1); conv5x5 -> 6 (pad 2, so that
  * the flatten is 16*5*5 = 400), relu, maxpool 2, conv5x5 -> 16, relu,
  * maxpool 2, fc 400 -> 120 -> 84 -> 10, softmax cross-entropy; backward and
  * SGD (lr 0.01) through ASSIGN. */
 static void wl_lenet(TinyHVM *ctx, u32 B, int steps) {
-    Term x = gen_tensor(ctx, shape_of((u32[]){B, 1, 28, 28}, 4), DTYPE_F32, TRC_GEN_UNIFORM, 4001, 0.f, 1.f);
-    Term W1 = kaiming_u(ctx, shape_of((u32[]){6, 1, 5, 5}, 4), 25, 4002);
-    Term b1 = zeros(ctx, SHAPE(6), 4003);
-    Term W2 = kaiming_u(ctx, shape_of((u32[]){16, 6, 5, 5}, 4), 150, 4004);
-    Term b2 = zeros(ctx, SHAPE(16), 4005);
-    Term W3 = kaiming_u(ctx, SHAPE(400, 120), 400, 4006);
-    Term b3 = zeros(ctx, SHAPE(120), 4007);
-    Term W4 = kaiming_u(ctx, SHAPE(120, 84), 120, 4008);
-    Term b4 = zeros(ctx, SHAPE(84), 4009);
-    Term W5 = kaiming_u(ctx, SHAPE(84, 10), 84, 4010);
-    Term b5 = zeros(ctx, SHAPE(10), 4011);
+    Term params[10];
+    Term x = lenet_params(ctx, B, params);
     u8 *lab = labels_u8(B, 4012);
     Term onehot = onehot_tensor(ctx, lab, B, 10);
-    Term params[10] = {W1, b1, W2, b2, W3, b3, W4, b4, W5, b5};
     u32 keep = ctx->tensor_count;
     for (int st = 0; st < steps; st++) {
         rec_mark("lenet.step");
-        rec_mark("lenet.fwd");
-        Term xp = pad_exact(ctx, x, B, 1, 28, 28, 2);
-        Term a1 = realize_as(ctx, unary(ctx, UOP_RELU,
-                             thvm_conv2d(ctx, xp, W1, b1, 1, (u32[]){1, 1}, (u32[]){0, 0, 0, 0})),
-                             shape_of((u32[]){B, 6, 28, 28}, 4));
-        Term p1 = realize_as(ctx, thvm_maxpool2d(ctx, a1, (u32[]){2, 2}, (u32[]){2, 2}),
-                             shape_of((u32[]){B, 6, 14, 14}, 4));
-        Term a2 = realize_as(ctx, unary(ctx, UOP_RELU,
-                             thvm_conv2d(ctx, p1, W2, b2, 1, (u32[]){1, 1}, (u32[]){0, 0, 0, 0})),
-                             shape_of((u32[]){B, 16, 10, 10}, 4));
-        Term p2 = realize_as(ctx, thvm_maxpool2d(ctx, a2, (u32[]){2, 2}, (u32[]){2, 2}),
-                             shape_of((u32[]){B, 16, 5, 5}, 4));
-        Term f = alias_as(ctx, p2, SHAPE(B, 400));
-        Term h3 = dense(ctx, f, W3, b3, 1, B, 120);
-        Term h4 = dense(ctx, h3, W4, b4, 1, B, 84);
-        Term logits = dense(ctx, h4, W5, b5, 0, B, 10);
-        Term loss = realize(ctx, cross_entropy_loss(ctx, logits, lab, B, 10));
-        readback(ctx, loss);
-        rec_mark("lenet.bwd");
-        Term d5 = ce_grad(ctx, logits, onehot, B, 10);
-        DenseGrads g5 = dense_bwd(ctx, h4, W5, d5, B, 84, 10, 1);
-        Term dz4 = realize_as(ctx, binary(ctx, UOP_MUL, g5.dx, binary(ctx, UOP_CMP, h4, scalar_t(ctx, 0.0f))),
-                              SHAPE(B, 84));
-        DenseGrads g4 = dense_bwd(ctx, h3, W4, dz4, B, 120, 84, 1);
-        Term dz3 = realize_as(ctx, binary(ctx, UOP_MUL, g4.dx, binary(ctx, UOP_CMP, h3, scalar_t(ctx, 0.0f))),
-                              SHAPE(B, 120));
-        DenseGrads g3 = dense_bwd(ctx, f, W3, dz3, B, 400, 120, 1);
-        Term dp2 = alias_as(ctx, g3.dx, shape_of((u32[]){B, 16, 5, 5}, 4));
-        Term dz2 = pool_relu_bwd(ctx, dp2, p2, a2, B, 16, 10, 10);
-        Term dW2 = conv_dw(ctx, p1, dz2, B, 6, 16, 5, 10, 10);
-        Term db2 = chansum(ctx, dz2, 16);
-        Term dp1 = conv_dx(ctx, dz2, W2, B, 16, 6, 5, 0, 14, 14);
-        Term dz1 = pool_relu_bwd(ctx, dp1, p1, a1, B, 6, 28, 28);
-        Term dW1 = conv_dw(ctx, xp, dz1, B, 1, 6, 5, 28, 28);
-        Term db1 = chansum(ctx, dz1, 6);
-        rec_mark("lenet.sgd");
-        Term grads[10] = {dW1, db1, dW2, db2, g3.dW, g3.db, g4.dW, g4.db, g5.dW, g5.db};
-        sgd(ctx, params, grads, 10, 0.01f);
+        lenet_step(ctx, B, x, params, onehot, lab, term_era());
         rec_mark("lenet.end");
         for (u32 i = 0; i < 10; i++) readback(ctx, params[i]);
         thvm_reset(ctx, keep);
@@ -1091,7 +1146,7 @@ static void wl_known(TinyHVM *ctx) {
         if (term_tag(out) != TAG_TEN) out = thvm_force_tensor_term(ctx, out);
         u32 dt = DTYPE_F32;
         Shape os = SHAPE(1);
-        free(thvm_to_host_raw(ctx, out, &dt, &os));
+        (void)thvm_to_host_raw(ctx, out, &dt, &os);   /* the tensor's host_ptr: thvm_free frees it */
     }
     {
         rec_mark("known.fused_reduce");

@@ -12,9 +12,11 @@
  *   run 0  on the engine's CPU backend, under capture.c's recorder in exec
  *          mode (which runs kernels whose masked loads leave their buffer over
  *          zero-guarded leaves, so the interpreter does not fault);
- *   run 1  with `hip_backend` registered as the engine's default device, as
- *          the thvm_init branch for "hip" registers it (the engine's
- *          src/ctx/init.c:23-37 does the same for Metal).
+ *   run 1  on a context made by thvm_init("hip"): the engine's thvm_init
+ *          with the branch a maintainer adds for "hip" (tests/live/hip_init.h;
+ *          src/ctx/init.c:23-37 does the same for Metal), which registers
+ *          `hip_backend` as the default device; thvm_free then shuts it
+ *          down, which the run checks (the library no longer synchronizes).
  * Every buffer the workload reads back (Backend.buf_read) is kept from both
  * runs and compared: same sequence and sizes, values within 1e-3 normwise
  * (max |gpu - cpu| / max |cpu| per read, as float32), NaNs in the same places.
@@ -37,7 +39,10 @@
 #define CAPTURE_NO_MAIN
 #include "../golden/capture.c"
 
-#include <dlfcn.h>
+/* the engine's thvm_init, compiled as thvm_init_engine, with the "hip" branch */
+#undef thvm_init
+#include "hip_init.h"
+
 #include <time.h>
 
 #define LIVE_MAX_READS 4096
@@ -228,17 +233,10 @@ static double g_hip_bk, g_hip_rd;
  * backend cannot be loaded or initialised */
 static double tm_hip_leg(const char *lib, const char *wl, u32 B, int steps, double *mean, double *waits,
                          double *reads, double *disp) {
-    void *h = dlopen(lib, RTLD_NOW | RTLD_LOCAL);
-    if (!h) {
-        fprintf(stderr, "engine_live: %s\n", dlerror());
-        return -1;
-    }
-    Backend *hb = (Backend *)dlsym(h, "hip_backend");
-    g_counters = (int (*)(u64 *, u32))dlsym(h, "thvm_hip_counters");
-    if (!hb || !g_counters || !hb->init || hb->init() != 0) {
-        fprintf(stderr, "engine_live: hip_backend unavailable\n");
-        return -1;
-    }
+    if (hip_backend_load(lib, 0) != 0) return -1;
+    Backend *hb = g_hip_backend;
+    g_counters = (int (*)(u64 *, u32))dlsym(g_hip_lib, "thvm_hip_counters");
+    if (!g_counters) return -1;
     g_tm_inner = *hb;
     static Backend tm;
     tm = *hb;
@@ -246,17 +244,19 @@ static double tm_hip_leg(const char *lib, const char *wl, u32 B, int steps, doub
     tm.buf_write = tm_write; tm.buf_read = tm_read; tm.buf_read_nosync = tm_read_nosync;
     tm.dispatch_uop_kernel = tm_uop; tm.dispatch_kernel_rs = tm_rs; tm.buf_copy = tm_copy;
     tm.contiguify = tm_contig; tm.pool_reset = tm_reset; tm.pool_set_persistent = tm_persist;
-    TinyHVM *ctx = thvm_init("cpu");
-    ctx->backends[2] = &tm;
-    if (ctx->n_backends < 3) ctx->n_backends = 3;
-    ctx->default_device = 2;
+    g_hip_backend = &tm;   /* thvm_init("hip") registers the counting wrapper */
+    TinyHVM *ctx = thvm_init("hip");
+    if (!ctx || ctx->default_device != THVM_DEV_HIP) {
+        fprintf(stderr, "engine_live: thvm_init(\"hip\") did not register hip_backend\n");
+        return -1;
+    }
     tm_steps(ctx, wl, B, 2, mean, waits, reads, disp);          /* warm-up: compiles every kernel */
     g_waits_outside = 0;
     g_waits_outside_slot[0] = 0;
     double med = tm_steps(ctx, wl, B, steps, mean, waits, reads, disp);
     g_hip_bk = g_last_bk;
     g_hip_rd = g_last_rd;
-    hb->shutdown();
+    thvm_free(ctx);
     return med;
 }
 
@@ -298,7 +298,210 @@ static int time_mode(const char *lib, const char *wl, int steps, const u32 *sz, 
     return (cpu_only || med > 0) && cmed > 0 ? 0 : 1;
 }
 
+/* ---- capture and replay of an engine-driven training step ----
+ * engine_live <libthvm_hip.so> jit <lenet|mlp> <steps> [batch]
+ *
+ * The Metal backend's JIT (src/backend/metal/jit.m:24-631, declared at
+ * src/tinyhvm.h:1294-1299, driven by test/archive/test_jit_dense.m:95-157)
+ * records the dispatches of one training step that thvm_eval issues and
+ * replays them for later steps without the engine; between replays the
+ * caller writes the next batch into the same persistent tensors. Here the
+ * same with the backend's HIP graphs: on a context made by thvm_init("hip"),
+ *   eager  2 warm-up steps (compilation), the parameters restored, then
+ *          <steps> training steps through thvm_eval, each after writing its
+ *          labels into the persistent one-hot tensor, each loss read from the
+ *          persistent tensor the step assigns it to;
+ *   graph  the parameters restored, one step through thvm_eval captured
+ *          between thvm_hip_graph_begin and thvm_hip_graph_end (nothing
+ *          runs), then <steps> launches of that graph, each after writing the
+ *          same labels as the eager step of that index, each loss read.
+ * Every loss and, at the end, every parameter must be the same bit for bit
+ * (the same kernels with the same arguments in the same order). Both legs
+ * are timed on the host clock, label write and loss read included. Prints
+ * one JSON line; exits 0 when both agree. The step (LeNet-5 as
+ * tests/golden/capture.c composes it; the 2-layer MLP with SGD on W1, b1,
+ * W2, b2) reads its labels from the one-hot tensor and assigns its loss, so
+ * a replay needs no engine work at all. */
+typedef struct {
+    int lenet;
+    u32 B, n_params, keep;
+    Term x, onehot, loss_out, params[10];
+} JNet;
+
+static void jnet_init(TinyHVM *ctx, JNet *n, int lenet, u32 B) {
+    memset(n, 0, sizeof *n);
+    n->lenet = lenet;
+    n->B = B;
+    if (lenet) {
+        n->x = lenet_params(ctx, B, n->params);
+        n->n_params = 10;
+    } else {
+        n->x = gen_tensor(ctx, SHAPE(B, 784), DTYPE_F32, TRC_GEN_NORMAL, 1001, 0.f, 1.f);
+        n->params[0] = kaiming_u(ctx, SHAPE(784, 128), 784, 1002);
+        n->params[1] = zeros(ctx, SHAPE(128), 1003);
+        n->params[2] = kaiming_u(ctx, SHAPE(128, 10), 128, 1004);
+        n->params[3] = zeros(ctx, SHAPE(10), 1005);
+        n->n_params = 4;
+    }
+    f32 *z = calloc((size_t)B * 10, sizeof(f32));
+    n->onehot = thvm_tensor(ctx, z, SHAPE(B, 10));
+    free(z);
+    f32 zero = 0.0f;
+    n->loss_out = thvm_tensor(ctx, &zero, SHAPE(1, 1));
+    n->keep = ctx->tensor_count;
+}
+
+/* the 2-layer MLP's training step, SGD (lr 0.01) on W1, b1, W2, b2 */
+static void mlp_train_step(TinyHVM *ctx, JNet *n) {
+    const u32 B = n->B;
+    Term *p = n->params;
+    Term h = dense(ctx, n->x, p[0], p[1], 1, B, 128);
+    Term logits = dense(ctx, h, p[2], p[3], 0, B, 10);
+    Term loss = ce_loss_onehot(ctx, logits, n->onehot, B, 10);
+    Term d2 = ce_grad(ctx, logits, n->onehot, B, 10);
+    DenseGrads g2 = dense_bwd(ctx, h, p[2], d2, B, 128, 10, 1);
+    Term dz1 = realize_as(ctx, binary(ctx, UOP_MUL, g2.dx, binary(ctx, UOP_CMP, h, scalar_t(ctx, 0.0f))),
+                          SHAPE(B, 128));
+    DenseGrads g1 = dense_bwd(ctx, n->x, p[0], dz1, B, 784, 128, 0);
+    Term grads[4] = {g1.dW, g1.db, g2.dW, g2.db};
+    sgd_keep_loss(ctx, p, grads, 4, 0.01f, n->loss_out, loss);
+}
+
+static void jnet_step(TinyHVM *ctx, JNet *n) {
+    if (n->lenet) lenet_step(ctx, n->B, n->x, n->params, n->onehot, NULL, n->loss_out);
+    else mlp_train_step(ctx, n);
+}
+
+static TensorMeta *jmeta(TinyHVM *ctx, Term t) { return &ctx->tensors[(u32)term_val(t)]; }
+
+/* host data into a persistent tensor through its backend, its buffer's epoch
+ * bumped as an ASSIGN bumps it (src/interact/tensor_ops.c:142-146), so that
+ * no cached kernel result that read the old contents is reused */
+static void jwrite(TinyHVM *ctx, Term t, const void *data, u64 bytes) {
+    TensorMeta *m = jmeta(ctx, t);
+    m->backend->buf_write(m->buf_id, data, bytes);
+    if (m->buf_id < MAX_BUF_EPOCHS) buf_epoch[m->buf_id]++;
+}
+
+static u64 jbytes(TinyHVM *ctx, Term t) { return (u64)jmeta(ctx, t)->view.numel * 4; }
+
+/* step t's labels (uniform integers in [0,10), seed 7000 + t) as one-hot rows */
+static void jnet_labels(TinyHVM *ctx, JNet *n, u32 t) {
+    u8 *lab = labels_u8(n->B, 7000 + t);
+    f32 *oh = calloc((size_t)n->B * 10, sizeof(f32));
+    for (u32 i = 0; i < n->B; i++) oh[i * 10 + lab[i]] = 1.0f;
+    jwrite(ctx, n->onehot, oh, (u64)n->B * 10 * sizeof(f32));
+    free(oh);
+    free(lab);
+}
+
+static f32 jloss(TinyHVM *ctx, JNet *n) {
+    f32 v = 0.0f;
+    TensorMeta *m = jmeta(ctx, n->loss_out);
+    m->backend->buf_read(m->buf_id, &v, sizeof v);
+    return v;
+}
+
+static void jparams_read(TinyHVM *ctx, JNet *n, u8 **out) {
+    for (u32 i = 0; i < n->n_params; i++) {
+        TensorMeta *m = jmeta(ctx, n->params[i]);
+        out[i] = malloc(jbytes(ctx, n->params[i]));
+        m->backend->buf_read(m->buf_id, out[i], jbytes(ctx, n->params[i]));
+    }
+}
+
+static void jparams_write(TinyHVM *ctx, JNet *n, u8 *const *in) {
+    for (u32 i = 0; i < n->n_params; i++) jwrite(ctx, n->params[i], in[i], jbytes(ctx, n->params[i]));
+}
+
+static int jit_mode(const char *lib, const char *wl, int steps, u32 B) {
+    const int lenet = strcmp(wl, "lenet") == 0;
+    if ((!lenet && strcmp(wl, "mlp") != 0) || steps < 1 || steps > 100000) return 2;
+    if (B == 0) B = lenet ? 256 : 64;
+    g_out = fopen("/dev/null", "wb");
+    if (!g_out || hip_backend_load(lib, 0) != 0) return 1;
+    int (*graph_begin)(void) = (int (*)(void))dlsym(g_hip_lib, "thvm_hip_graph_begin");
+    void *(*graph_end)(void) = (void *(*)(void))dlsym(g_hip_lib, "thvm_hip_graph_end");
+    int (*graph_launch)(void *) = (int (*)(void *))dlsym(g_hip_lib, "thvm_hip_graph_launch");
+    void (*graph_destroy)(void *) = (void (*)(void *))dlsym(g_hip_lib, "thvm_hip_graph_destroy");
+    if (!graph_begin || !graph_end || !graph_launch || !graph_destroy) return 1;
+    TinyHVM *ctx = thvm_init("hip");
+    if (!ctx || ctx->default_device != THVM_DEV_HIP) {
+        fprintf(stderr, "engine_live: thvm_init(\"hip\") did not register hip_backend\n");
+        return 1;
+    }
+    JNet n;
+    jnet_init(ctx, &n, lenet, B);
+    u8 *p0[10], *pe[10], *pg[10];
+    jparams_read(ctx, &n, p0);
+    f32 *le = calloc((size_t)steps, sizeof(f32)), *lg = calloc((size_t)steps, sizeof(f32));
+    if (!le || !lg) return 1;
+    /* warm-up: every kernel compiled, every workspace sized */
+    for (u32 w = 0; w < 2; w++) {
+        jnet_labels(ctx, &n, w);
+        jnet_step(ctx, &n);
+        (void)jloss(ctx, &n);
+        thvm_reset(ctx, n.keep);
+    }
+    /* eager leg */
+    jparams_write(ctx, &n, p0);
+    double t0 = now_s();
+    for (int t = 0; t < steps; t++) {
+        jnet_labels(ctx, &n, (u32)t);
+        jnet_step(ctx, &n);
+        le[t] = jloss(ctx, &n);
+        thvm_reset(ctx, n.keep);
+    }
+    const double t_eager = now_s() - t0;
+    jparams_read(ctx, &n, pe);
+    /* graph leg: one engine step captured, then replayed */
+    jparams_write(ctx, &n, p0);
+    jnet_labels(ctx, &n, 0);
+    if (graph_begin() != 0) {
+        fprintf(stderr, "engine_live: graph capture could not start\n");
+        return 1;
+    }
+    jnet_step(ctx, &n);
+    void *g = graph_end();
+    thvm_reset(ctx, n.keep);
+    if (!g) {
+        fprintf(stderr, "engine_live: the engine's step could not be captured\n");
+        return 1;
+    }
+    t0 = now_s();
+    int launch_err = 0;
+    for (int t = 0; t < steps; t++) {
+        jnet_labels(ctx, &n, (u32)t);
+        launch_err |= graph_launch(g) != 0;
+        lg[t] = jloss(ctx, &n);
+    }
+    const double t_graph = now_s() - t0;
+    jparams_read(ctx, &n, pg);
+    int losses_equal = memcmp(le, lg, (size_t)steps * sizeof(f32)) == 0, params_equal = 1, moved = 0;
+    for (u32 i = 0; i < n.n_params; i++) {
+        const u64 nb = jbytes(ctx, n.params[i]);
+        params_equal &= memcmp(pe[i], pg[i], nb) == 0;
+        moved |= memcmp(pe[i], p0[i], nb) != 0;
+    }
+    int finite = 1;
+    for (int t = 0; t < steps; t++) finite &= isfinite(le[t]) != 0;
+    graph_destroy(g);
+    thvm_free(ctx);
+    const int ok = losses_equal && params_equal && moved && finite && !launch_err;
+    printf("{\"workload\": \"%s\", \"batch\": %u, \"steps\": %d, \"eager\": {\"ms_per_step\": %.4f, "
+           "\"steps_per_s\": %.2f}, \"graph\": {\"ms_per_step\": %.4f, \"steps_per_s\": %.2f}, "
+           "\"losses_equal\": %s, \"params_equal\": %s, \"params_moved\": %s, \"loss_first\": %.6f, "
+           "\"loss_last\": %.6f, \"ok\": %s}\n",
+           wl, B, steps, t_eager * 1e3 / steps, steps / t_eager, t_graph * 1e3 / steps, steps / t_graph,
+           losses_equal ? "true" : "false", params_equal ? "true" : "false", moved ? "true" : "false", le[0],
+           le[steps - 1], ok ? "true" : "false");
+    fflush(stdout);
+    return ok ? 0 : 1;
+}
+
 int main(int argc, char **argv) {
+    if (argc >= 5 && strcmp(argv[2], "jit") == 0)
+        return jit_mode(argv[1], argv[3], atoi(argv[4]), argc >= 6 ? (u32)strtoul(argv[5], NULL, 10) : 0);
     if (argc >= 5 && strcmp(argv[2], "time") == 0) {
         u32 tsz[8] = {0}, tn = 0;
         for (int i = 5; i < argc && tn < 8; i++) tsz[tn++] = (u32)strtoul(argv[i], NULL, 10);
@@ -326,29 +529,27 @@ int main(int argc, char **argv) {
     }
     double t_cpu = now_s() - t0;
 
-    /* run 1: hip_backend as the engine's default device */
-    void *h = dlopen(argv[1], RTLD_NOW | RTLD_LOCAL);
-    if (!h) {
-        fprintf(stderr, "engine_live: %s\n", dlerror());
-        return 1;
-    }
-    Backend *hb = (Backend *)dlsym(h, "hip_backend");
-    if (!hb || !hb->init || hb->init() != 0) {
-        fprintf(stderr, "engine_live: hip_backend unavailable\n");
-        return 1;
-    }
+    /* run 1: thvm_init("hip") registers hip_backend as the default device */
+    if (hip_backend_load(argv[1], 0) != 0) return 1;
+    Backend *hb = g_hip_backend;
     static Backend live_hip;
     live_hip = *hb;
     g_inner_read = hb->buf_read;
     live_hip.buf_read = live_read;
+    g_hip_backend = &live_hip;
     g_run = 1;
-    TinyHVM *ctx = thvm_init("cpu");
-    ctx->backends[2] = &live_hip;
-    if (ctx->n_backends < 3) ctx->n_backends = 3;
-    ctx->default_device = 2;
+    TinyHVM *ctx = thvm_init("hip");
+    if (!ctx || ctx->default_device != THVM_DEV_HIP) {
+        fprintf(stderr, "engine_live: thvm_init(\"hip\") did not register hip_backend\n");
+        return 1;
+    }
     t0 = now_s();
     run_workload(ctx, argv[2], sz, nsz);
     double t_gpu = now_s() - t0;
+    /* thvm_free shuts every registered backend down (src/ctx/init.c:65-77) */
+    thvm_free(ctx);
+    int (*sync)(void) = (int (*)(void))dlsym(g_hip_lib, "thvm_hip_synchronize");
+    const int shut_down = sync && sync() == -1;
 
     int ok = g_nreads[0] == g_nreads[1] && g_nreads[0] > 0;
     double worst = 0.0;
@@ -376,9 +577,9 @@ int main(int argc, char **argv) {
         if (err > worst) worst = err;
         printf("%s[%llu, %.3e]", i ? ", " : "", (unsigned long long)a->n, err);
     }
-    ok = ok && worst <= 1e-3;
-    printf("], \"worst\": %.3e, \"ok\": %s}\n", worst, ok ? "true" : "false");
+    ok = ok && worst <= 1e-3 && shut_down;
+    printf("], \"worst\": %.3e, \"registered_by_thvm_init\": true, \"shut_down_by_thvm_free\": %s, "
+           "\"ok\": %s}\n", worst, shut_down ? "true" : "false", ok ? "true" : "false");
     fflush(stdout);
-    hb->shutdown();
     return ok ? 0 : 1;
 }

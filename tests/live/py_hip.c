@@ -4,29 +4,29 @@
  * py/csrc/libthvm.m:52-215) with the HIP backend as a device.
  *
  * TEST INFRASTRUCTURE. Built by `make -C oracle ref` into
- * oracle/_ref/libthvm_py.so; driven over ctypes by tests/test_gpu_pyffi.py.
+ * oracle/_ref/libthvm_py.so with -Dthvm_init=thvm_init_engine; driven over
+ * ctypes by tests/test_gpu_pyffi.py.
  *
- * py_init_hip(path) stands in for the "hip" branch a maintainer adds to
- * thvm_init (src/ctx/init.c:17-35), which this engine version does not have:
- * it loads libthvm_hip.so, initialises its `hip_backend` vtable and registers
- * it as the default device of an engine context, as the Metal branch does
- * for metal_backend. Every other py_* call is the engine's own, unchanged.
+ * The engine's thvm_init gets the "hip" branch a maintainer adds to it
+ * (tests/live/hip_init.h). py_init_hip(path) loads libthvm_hip.so and then
+ * makes exactly the engine's own py_init call for device "hip" (py_init,
+ * py/csrc/libthvm.m:52-56, is thvm_init(device) after a Metal-only path
+ * setup): thvm_init("hip") registers hip_backend as the default device, or
+ * stays on the CPU when the backend's init fails. Every other py_* call is
+ * the engine's own, unchanged; py_free reaches the backend's shutdown
+ * through thvm_free.
  */
 #include "libthvm.m"
 
+#undef thvm_init
+#include "hip_init.h"
+
 __attribute__((visibility("default")))
 TinyHVM *py_init_hip(const char *lib_path) {
-    void *h = dlopen(lib_path, RTLD_NOW | RTLD_GLOBAL);
-    if (!h) {
-        fprintf(stderr, "py_init_hip: %s\n", dlerror());
-        return NULL;
-    }
-    Backend *hb = (Backend *)dlsym(h, "hip_backend");
-    if (!hb || !hb->init || hb->init() != 0) return NULL;
-    TinyHVM *ctx = py_init("cpu");
-    if (!ctx) return NULL;
-    ctx->backends[2] = hb;
-    if (ctx->n_backends < 3) ctx->n_backends = 3;
-    ctx->default_device = 2;
-    return ctx;
+    if (hip_backend_load(lib_path, 1) != 0) return NULL;
+    return thvm_init("hip");
 }
+
+/* the engine context's default device (0 cpu, 2 hip) */
+__attribute__((visibility("default")))
+u32 py_default_device(TinyHVM *ctx) { return ctx ? ctx->default_device : 0xFFFFFFFFu; }

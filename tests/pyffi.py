@@ -48,6 +48,7 @@ def lib():
         sigs = {
             "py_init": (vp, [C.c_char_p]),
             "py_init_hip": (vp, [C.c_char_p]),
+            "py_default_device": (u32, [vp]),
             "py_free": (None, [vp]),
             "py_tensor": (u64, [vp, C.POINTER(C.c_float), pu32, u32]),
             "py_scalar": (u64, [vp, C.c_float]),
@@ -75,9 +76,13 @@ class Ctx:
     def __init__(self, device):
         L = lib()
         self.L = L
+        self.device = device
         self.ctx = L.py_init_hip(HIP.encode()) if device == "hip" else L.py_init(b"cpu")
         if not self.ctx:
             raise RuntimeError("engine context for %s unavailable" % device)
+        # thvm_init("hip") made the HIP backend the default device (2), or
+        # stayed on the CPU (0) when the backend's init failed
+        STATS.setdefault("default_device", []).append(int(L.py_default_device(self.ctx)))
 
     def tensor(self, arr):
         a = np.ascontiguousarray(arr, dtype=np.float32)
@@ -121,6 +126,12 @@ class Ctx:
 
     def free(self):
         self.L.py_free(self.ctx)
+        if self.device == "hip":
+            # thvm_free shut the registered backend down: the library no
+            # longer synchronizes
+            h = C.CDLL(HIP)
+            h.thvm_hip_synchronize.restype = C.c_int
+            STATS.setdefault("shut_down_by_free", []).append(h.thvm_hip_synchronize() == -1)
 
 
 def _gen(dist, dtype, seed, p0, p1, n):
