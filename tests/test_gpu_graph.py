@@ -1,12 +1,16 @@
 """HIP graphs of a recorded training step (thvm_hip_graph_*).
 
-One LeNet-5 training step at batch 256 (forward, backward, SGD through
-ASSIGN) is replayed from its kernel trace once eagerly and once under stream
-capture; the graph is then launched several times, each launch starting from
-the same parameters, with the program's own eager steps, host writes and
-synchronizations between the launches. Every launch must leave the ten
-parameters bit-identical to the eager step (the same kernels with the same
-arguments in the same order; every sum has a fixed order).
+For LeNet-5 at batch 256 (forward, backward, SGD through ASSIGN), the 2-layer
+MLP at batch 64 and the conv block at batch 64 ([64,64,56,56], forward and
+backward), one step is replayed from its kernel trace eagerly, and then, from
+the same state, under stream capture; the graph is then launched three times,
+each launch from that same state, with other eager work (another trace's
+kernels, host writes, synchronizations) between the launches. After every
+launch every buffer live at the end of the step (parameters, gradients,
+activations, batchnorm statistics, the loss and the step's temporaries) must
+be bit-identical to the eager step's: the same kernels with the same
+arguments in the same order, and every sum in a fixed order. For LeNet-5,
+two launches in a row must also equal two eager steps.
 """
 import ctypes as C
 import os
@@ -14,14 +18,21 @@ import os
 import numpy as np
 import pytest
 
-from tinyhvm_amd import _lib
+from tests import tracetools as tt
+from tinyhvm_amd import _lib, trace
 
 pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-TRACE = os.path.join(ROOT, "tinyhvm_amd", "workloads", "lenet_b256.trc")
+WL = os.path.join(ROOT, "tinyhvm_amd", "workloads")
+TRACE = os.path.join(WL, "lenet_b256.trc")
 PARAMS = range(2, 12)          # trace ids of W1, b1, ..., W5, b5
 SKIP_READS = 1
+STEPS = {
+    "lenet": ("lenet_b256.trc", "lenet.step", "lenet.end"),
+    "mlp": ("mlp_64x784x128x10.trc", "mlp.fwd", None),
+    "convblock": ("convblock_b64.trc", "conv.fwd", None),
+}
 
 
 @pytest.fixture(scope="module")
@@ -32,42 +43,59 @@ def L():
     L.thvm_hip_shutdown()
 
 
-def _params(L, t, sizes):
+def _live(L, t, sizes, ids=None):
     out = {}
-    for tid in PARAMS:
-        n = sizes[tid]
-        buf = (C.c_uint8 * n)()
-        L.thvm_hip_buf_read(L.thvm_trace_live_id(t, tid), buf, n)
-        out[tid] = bytes(buf)
+    for tid in (sizes if ids is None else ids):
+        live = L.thvm_trace_live_id(t, tid)
+        if live:
+            buf = (C.c_uint8 * sizes[tid])()
+            L.thvm_hip_buf_read(live, buf, sizes[tid])
+            out[tid] = bytes(buf)
     return out
 
 
-def _restore(L, t, p0):
-    for tid, data in p0.items():
+def _restore(L, t, snap):
+    for tid, data in snap.items():
         L.thvm_hip_buf_write(L.thvm_trace_live_id(t, tid), data, len(data))
 
 
-def test_graph_of_training_step_matches_eager(L):
-    from tinyhvm_amd import trace
-    sizes = {r.f["id"]: r.f["bytes"] for r in trace.read_trace(TRACE) if r.tag == trace.ALLOC}
+def _other_eager_work(L, rep):
+    """Kernels of another trace, in buffers of their own, a host write and a
+    synchronization, between two graph launches."""
+    other = tt.Replay(tt.fixtures("fused_64x256.trc")[0], L.thvm_hip_backend())
+    try:
+        other.run(0, other.n, SKIP_READS)
+        b = L.thvm_hip_buf_alloc(4096)
+        pat = np.full(1024, float(rep), dtype=np.float32)
+        L.thvm_hip_buf_write(b, pat.ctypes.data_as(C.c_void_p), 4096)
+        assert L.thvm_hip_synchronize() == 0
+        L.thvm_hip_buf_free(b)
+    finally:
+        other.close()
+
+
+@pytest.mark.parametrize("name", list(STEPS))
+def test_graph_of_step_matches_eager_on_every_buffer(L, name):
+    path = os.path.join(WL, STEPS[name][0])
+    sizes = {r.f["id"]: r.f["bytes"] for r in trace.read_trace(path) if r.tag == trace.ALLOC}
     be = L.thvm_hip_backend()
-    t = L.thvm_trace_load(TRACE.encode())
+    t = L.thvm_trace_load(path.encode())
     assert t
     g = None
     try:
-        n = L.thvm_trace_count(t)
-        lo = L.thvm_trace_find_mark(t, b"lenet.step", 0)
-        hi = L.thvm_trace_find_mark(t, b"lenet.end", lo)
-        assert 0 <= lo < hi <= n
+        lo = L.thvm_trace_find_mark(t, STEPS[name][1].encode(), 0)
+        hi = L.thvm_trace_find_mark(t, STEPS[name][2].encode(), lo) if STEPS[name][2] else L.thvm_trace_count(t)
+        assert 0 <= lo < hi
         L.thvm_trace_replay(t, be, 0, lo, 0)
+        s0 = _live(L, t, sizes)                             # the state before the step
         L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)      # compiles every kernel
         assert L.thvm_hip_synchronize() == 0
-        p0 = _params(L, t, sizes)
+        _restore(L, t, s0)
         L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
         assert L.thvm_hip_synchronize() == 0
-        eager = _params(L, t, sizes)
-        assert any(eager[k] != p0[k] for k in PARAMS), "the step did not update the parameters"
-        _restore(L, t, p0)
+        eager = _live(L, t, sizes)
+        assert len(eager) > len(s0)
+        _restore(L, t, s0)
         assert L.thvm_hip_synchronize() == 0
 
         assert L.thvm_hip_graph_begin() == 0
@@ -75,87 +103,29 @@ def test_graph_of_training_step_matches_eager(L):
         g = L.thvm_hip_graph_end()
         assert g, "the step could not be captured"
         # capture ran nothing on the device
-        assert _params(L, t, sizes) == p0
-
+        assert _live(L, t, sizes, s0) == s0
         for rep in range(3):
-            _restore(L, t, p0)
+            _restore(L, t, s0)
             assert L.thvm_hip_graph_launch(g) == 0
             assert L.thvm_hip_synchronize() == 0
-            got = _params(L, t, sizes)
-            bad = [k for k in PARAMS if got[k] != eager[k]]
-            assert not bad, "graph launch %d: parameters %s differ from the eager step" % (rep, bad)
-            # eager work between the launches: an eager step from the same state
-            _restore(L, t, p0)
-            L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
+            got = _live(L, t, sizes)
+            assert got.keys() == eager.keys()
+            bad = sorted(k for k in eager if got[k] != eager[k])
+            assert not bad, "%s, graph launch %d: buffers %s differ from the eager step" % (name, rep, bad)
+            _other_eager_work(L, rep)
+        if name == "lenet":
+            # two launches in a row are two training steps: the same parameters
+            # as a second launch from the state the first left
+            _restore(L, t, s0)
+            assert L.thvm_hip_graph_launch(g) == 0 and L.thvm_hip_graph_launch(g) == 0
             assert L.thvm_hip_synchronize() == 0
-            again = _params(L, t, sizes)
-            assert all(again[k] == eager[k] for k in PARAMS), "eager step %d differs" % rep
-        # two launches in a row are two training steps
-        _restore(L, t, p0)
-        assert L.thvm_hip_graph_launch(g) == 0 and L.thvm_hip_graph_launch(g) == 0
-        assert L.thvm_hip_synchronize() == 0
-        two = _params(L, t, sizes)
-        _restore(L, t, p0)
-        L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
-        L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
-        assert L.thvm_hip_synchronize() == 0
-        assert _params(L, t, sizes) == two
-        assert any(two[k] != eager[k] for k in PARAMS)
-    finally:
-        if g:
-            L.thvm_hip_graph_destroy(g)
-        L.thvm_trace_release(t, be)
-        L.thvm_trace_free(t)
-        L.thvm_hip_pool_reset(0)
-
-
-CONV = os.path.join(ROOT, "tinyhvm_amd", "workloads", "convblock_b64.trc")
-
-
-def _out_bytes(L, t, tid, n):
-    buf = (C.c_uint8 * n)()
-    L.thvm_hip_buf_read(L.thvm_trace_live_id(t, tid), buf, n)
-    return bytes(buf)
-
-
-def test_graph_of_conv_block_matches_eager(L):
-    """The conv block step at batch 64 under graph launches (the matrix-core
-    convolutions with their packed weights and the weight gradient's split-K
-    workspace, the split reductions of batchnorm and the loss): three
-    launches, with eager steps between them, each leave the three
-    convolution outputs bit-identical to the eager step's (every sum has a
-    fixed order)."""
-    from tinyhvm_amd import trace
-    recs = trace.read_trace(CONV)
-    sizes = {r.f["id"]: r.f["bytes"] for r in recs if r.tag == trace.ALLOC}
-    be = L.thvm_hip_backend()
-    t = L.thvm_trace_load(CONV.encode())
-    assert t
-    g = None
-    try:
-        n = L.thvm_trace_count(t)
-        lo = L.thvm_trace_find_mark(t, b"conv.fwd", 0)
-        assert 0 <= lo < n
-        outs = [r.f["out"] for r in recs[lo:] if r.tag == trace.UOP]
-        watch = [outs[1], outs[23], outs[27]]          # conv forward, dW, dX
-        L.thvm_trace_replay(t, be, 0, lo, 0)
-        L.thvm_trace_replay(t, be, lo, n, SKIP_READS)      # compiles every kernel
-        assert L.thvm_hip_synchronize() == 0
-        eager = {tid: _out_bytes(L, t, tid, sizes[tid]) for tid in watch}
-        assert L.thvm_hip_graph_begin() == 0
-        L.thvm_trace_replay(t, be, lo, n, SKIP_READS)
-        g = L.thvm_hip_graph_end()
-        assert g, "the step could not be captured"
-        for rep in range(3):
+            two = _live(L, t, sizes, PARAMS)
+            one = {k: eager[k] for k in PARAMS}
+            assert any(two[k] != one[k] for k in PARAMS), "the second launch did not update the parameters"
+            _restore(L, t, one)
             assert L.thvm_hip_graph_launch(g) == 0
             assert L.thvm_hip_synchronize() == 0
-            got = {tid: _out_bytes(L, t, tid, sizes[tid]) for tid in watch}
-            bad = [tid for tid in watch if got[tid] != eager[tid]]
-            assert not bad, "graph launch %d: outputs %s differ from the eager step" % (rep, bad)
-            L.thvm_trace_replay(t, be, lo, n, SKIP_READS)
-            assert L.thvm_hip_synchronize() == 0
-            again = {tid: _out_bytes(L, t, tid, sizes[tid]) for tid in watch}
-            assert again == eager, "eager step %d differs" % rep
+            assert _live(L, t, sizes, PARAMS) == two
     finally:
         if g:
             L.thvm_hip_graph_destroy(g)
