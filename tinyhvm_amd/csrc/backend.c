@@ -502,13 +502,35 @@ static int hb_try_epilogue(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, cons
     const u32 fzs = e->fz_serial, fzo = e->fz_out;
     hipFunction_t fn;
     CoForm co;
-    if (!dense_epilogue(fz, fzs, k, o_leaf, &fn, &co)) return 0;
-    /* its other inputs current on the device (the epilogue reads every leaf
-     * from memory): pending host writes are copied on the stream ahead of
-     * the held launches, which do not read them (if one does, it goes out
-     * first and nothing fuses) */
-    for (u32 j = 0; j < k->n_leaves; j++)
-        if (leaf_bufs[j] != fzo) pool_sync_device(leaf_bufs[j]);
+    KGenScalars sc;
+    if (!dense_epilogue(fz, fzs, k, o_leaf, &fn, &co, &sc)) return 0;
+    /* loads at a constant index of host-held leaves take their value as an
+     * argument (sm bit j set); a leaf read only that way is not uploaded */
+    u32 sm = 0;
+    float sv[KGEN_MAX_SCALARS];
+    for (u32 j = 0; j < sc.n; j++) {
+        const u32 id = leaf_bufs[sc.leaf[j]];
+        sv[j] = 0.0f;
+        if (id && id != out_buf && pool_host_value(id, k->leaf_dtypes[sc.leaf[j]], sc.index[j], &sv[j])) sm |= 1u << j;
+    }
+    /* its other inputs current on the device (the epilogue reads them from
+     * memory): pending host writes are copied on the stream ahead of the
+     * held launches, which do not read them (if one does, it goes out first
+     * and nothing fuses) */
+    for (u32 j = 0; j < k->n_leaves; j++) {
+        if (leaf_bufs[j] == fzo) continue;
+        int inline_only = 0, other = 0;
+        for (u32 q = 0; q < k->n_ops; q++)
+            if (k->ops[q].type == KOP_LOAD && k->ops[q].imm.u == j + 1) {
+                int hit = 0;
+                for (u32 t = 0; t < sc.n; t++)
+                    hit |= sc.leaf[t] == j && ((sm >> t) & 1u) && k->ops[k->ops[q].arg[0]].imm.u == sc.index[t] &&
+                           k->ops[k->ops[q].arg[0]].type == KOP_CONST_U;
+                if (hit) inline_only = 1;
+                else other = 1;
+            }
+        if (!inline_only || other) pool_sync_device(leaf_bufs[j]);
+    }
     e = NULL;
     for (u32 i = 0; i < HB.n && !e; i++)
         if (HB.ent[i].fz_key == fz && HB.ent[i].fz_serial == fzs && HB.ent[i].fz_out == fzo) e = &HB.ent[i];
@@ -525,7 +547,7 @@ static int hb_try_epilogue(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, cons
     u32 off = 0;
     for (u32 j = 0; j < e->co.np; j++) off = hb_arg_off(off, e->co.psz[j]) + e->co.psz[j];
     const u32 nb = k->n_leaves + 1;
-    if (hb_arg_off(off, 8) + 8u * nb + 4u * nb > HB_ARG_BYTES) return 0;
+    if (hb_arg_off(off, 8) + 8u * nb + 4u * nb + (sc.n ? 4u + 4u * sc.n : 0u) > HB_ARG_BYTES) return 0;
     for (u32 b = 0; b < nb; b++) {
         void *p = b == 0 ? pool_ptr(out_buf) : leaf_bufs[b - 1] ? pool_ptr(leaf_bufs[b - 1]) : hipb.dummy;
         off = hb_arg_off(off, 8);
@@ -538,6 +560,15 @@ static int hb_try_epilogue(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, cons
         off = hb_arg_off(off, 4);
         memcpy(e->args + off, &c, 4);
         off += 4;
+    }
+    if (sc.n) {
+        off = hb_arg_off(off, 4);
+        memcpy(e->args + off, &sm, 4);
+        off += 4;
+        for (u32 j = 0; j < sc.n; j++) {
+            memcpy(e->args + off, &sv[j], 4);
+            off += 4;
+        }
     }
     e->fn = fn;
     e->co = co;
@@ -903,6 +934,8 @@ static void interp_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, con
 
 static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
 static void hb_run_generated(KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k);
+static u64 hb_inline_scalars(const KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
+                             const UOpKernel *k, u32 *sm_out, float *sv);
 
 /* A loop-free dispatch that reads the output of a held chainable program P
  * at its own gid runs fused after it (chain.c): P's held launch is taken
@@ -954,9 +987,20 @@ static int hb_try_chain(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
         return 0;
     }
     /* the consumer's own inputs current on the device first: a copy that
-     * overlaps a held launch issues it, and then nothing fuses */
+     * overlaps a held launch issues it, and then nothing fuses (leaves the
+     * merged program reads only as inline scalars need no copy) */
     const u32 tag[2] = {h->ch_bufs[0], (u32)h->ch_seq};
-    for (u32 j = 0; j < k->n_leaves; j++) pool_sync_device(leaf_bufs[j]);
+    {
+        u32 sm;
+        float sv[KGEN_MAX_SCALARS];
+        const u64 only = hb_inline_scalars(e, mb[0], mb + 1, M.n_leaves, &M, &sm, sv);
+        for (u32 j = 0; j < k->n_leaves; j++) {
+            int skip = 0;
+            for (u32 s2 = 0; s2 < M.n_leaves && s2 < 32; s2++)
+                if (mb[1 + s2] == leaf_bufs[j] && ((only >> s2) & 1u)) skip = 1;
+            if (!skip) pool_sync_device(leaf_bufs[j]);
+        }
+    }
     at = -1;
     for (u32 i = 0; i < HB.n && at < 0; i++)
         if (HB.ent[i].ch == ch && HB.ent[i].ch_bufs[0] == tag[0] && (u32)HB.ent[i].ch_seq == tag[1]) at = (i32)i;
@@ -1067,6 +1111,31 @@ static void hb_mark_writes(const KCacheEntry *e, u32 out_buf, const u32 *leaf_bu
         if ((e->store_slots >> (i + 1)) & 1u) pool_mark_device_write(leaf_bufs[i]);
 }
 
+/* The inline scalars of compiled program e over these buffers: constant-
+ * index loads of host-held leaves take their value from an argument (sm bit
+ * j, value sv[j]). Returns the leaves read only that way (bit i: leaf i),
+ * which need not be uploaded. */
+static u64 hb_inline_scalars(const KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
+                             const UOpKernel *k, u32 *sm_out, float *sv) {
+    u32 sm = 0;
+    for (u32 j = 0; j < e->n_scal; j++) {
+        u32 leaf = e->scal_leaf[j];
+        u32 id = leaf < n_leaves ? leaf_bufs[leaf] : 0;
+        sv[j] = 0.0f;
+        if (id && id != out_buf && pool_host_value(id, k->leaf_dtypes[leaf], e->scal_index[j], &sv[j]))
+            sm |= 1u << j;
+    }
+    u64 only = 0;
+    for (u32 i = 0; i < n_leaves && i < 32; i++) {
+        int inline_only = (e->scal_only_leaves >> i) & 1u;
+        for (u32 j = 0; j < e->n_scal && inline_only; j++)
+            if (e->scal_leaf[j] == i && !((sm >> j) & 1u)) inline_only = 0;
+        if (inline_only) only |= 1ull << i;
+    }
+    *sm_out = sm;
+    return only;
+}
+
 /* Launches (or holds) compiled program e over its buffers. */
 static void hb_run_generated(KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
     HipbBuf *ob = pool_get(out_buf);
@@ -1075,19 +1144,9 @@ static void hb_run_generated(KCacheEntry *e, u32 out_buf, const u32 *leaf_bufs, 
      * leaf read only that way is not uploaded */
     u32 sm = 0;
     float sv[KGEN_MAX_SCALARS];
-    for (u32 j = 0; j < e->n_scal; j++) {
-        u32 leaf = e->scal_leaf[j];
-        u32 id = leaf < n_leaves ? leaf_bufs[leaf] : 0;
-        sv[j] = 0.0f;
-        if (id && id != out_buf && pool_host_value(id, k->leaf_dtypes[leaf], e->scal_index[j], &sv[j]))
-            sm |= 1u << j;
-    }
-    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++) {
-        int inline_only = i < 32 && ((e->scal_only_leaves >> i) & 1u);
-        for (u32 j = 0; j < e->n_scal && inline_only; j++)
-            if (e->scal_leaf[j] == i && !((sm >> j) & 1u)) inline_only = 0;
-        if (!inline_only) pool_sync_device(leaf_bufs[i]);
-    }
+    const u64 only = hb_inline_scalars(e, out_buf, leaf_bufs, n_leaves, k, &sm, sv);
+    for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++)
+        if (!((only >> i) & 1u)) pool_sync_device(leaf_bufs[i]);
     if (e->total == 0) return;
 
     /* kernel parameters: p0..pN (buffer pointers), c0..cN (element counts),

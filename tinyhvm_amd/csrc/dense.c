@@ -1318,6 +1318,7 @@ typedef struct {
     hipModule_t mod;
     hipFunction_t fn;
     CoForm co;
+    KGenScalars sc;    /* the consumer's inline scalars (the fused kernel's last parameters) */
 } FusedEntry;
 static struct {
     FusedEntry e[FUSED_MAX];
@@ -2079,9 +2080,9 @@ static int epi_fits(u32 M, u32 N, const UOpKernel *c, u32 o_leaf) {
  * buffers (the kernel's extra parameters q<b>, qc<b>), run by the lane that
  * stores each output on the value it stores. */
 static char *epi_source(const UOpKernel *k, const Contraction *ct, const GemmPlan *pl0, const UOpKernel *c,
-                        u32 o_leaf, const char *name, char *err, size_t errlen) {
+                        u32 o_leaf, const char *name, KGenScalars *sc, char *err, size_t errlen) {
     char *epi = malloc(65536), params[2048], call[2048];
-    if (!epi || kgen_epilogue(c, o_leaf, epi, 65536) < 0) {
+    if (!epi || kgen_epilogue(c, o_leaf, epi, 65536, sc) < 0) {
         free(epi);
         snprintf(err, errlen, "epilogue generation failed");
         return NULL;
@@ -2094,6 +2095,14 @@ static char *epi_source(const UOpKernel *k, const Contraction *ct, const GemmPla
     for (u32 b = 0; b <= c->n_leaves; b++) {
         wp += (size_t)snprintf(params + wp, sizeof params - wp, ", u32 qc%u", b);
         wc += (size_t)snprintf(call + wc, sizeof call - wc, ", qc%u", b);
+    }
+    if (sc->n) {
+        wp += (size_t)snprintf(params + wp, sizeof params - wp, ", u32 qsm_");
+        wc += (size_t)snprintf(call + wc, sizeof call - wc, ", qsm_");
+        for (u32 j = 0; j < sc->n; j++) {
+            wp += (size_t)snprintf(params + wp, sizeof params - wp, ", float qsv%u", j);
+            wc += (size_t)snprintf(call + wc, sizeof call - wc, ", qsv%u", j);
+        }
     }
     snprintf(call + wc, sizeof call - wc, ")");
     GemmPlan pl = *pl0;
@@ -2112,7 +2121,8 @@ static char *epi_source(const UOpKernel *k, const Contraction *ct, const GemmPla
  * epilogue (the same arithmetic as the two launches). Returns 1 with the
  * fused module's function and co-launch form, 0 when the pair does not fuse
  * (remembered, like the modules, per pair). */
-int dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunction_t *fn, CoForm *co) {
+int dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunction_t *fn, CoForm *co,
+                   KGenScalars *sc) {
     if (hipb.no_fuse || !c || o_leaf == 0 || o_leaf > c->n_leaves) return 0;
     u64 fk = key ^ (uop_signature(c) * 0x9E3779B97F4A7C15ull) ^ ((u64)o_leaf << 56) ^ ((u64)serial << 40);
     if (!fk) fk = 1;
@@ -2121,6 +2131,7 @@ int dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunct
             if (!F.e[i].fn) return 0;
             *fn = F.e[i].fn;
             *co = F.e[i].co;
+            *sc = F.e[i].sc;
             return 1;
         }
     if (F.n >= FUSED_MAX) return 0;
@@ -2134,7 +2145,7 @@ int dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunct
     if (!e || !epi_fits(e->M, e->N, c, o_leaf) || !recognize(e->kcopy, &ct)) return 0;
     char name[48], err[256] = {0};
     snprintf(name, sizeof name, "thvm_gemmep_%08x", (u32)(fk & 0xFFFFFFFFu));
-    char *src = epi_source(e->kcopy, &ct, &e->plan, c, o_leaf, name, err, sizeof err);
+    char *src = epi_source(e->kcopy, &ct, &e->plan, c, o_leaf, name, &fe->sc, err, sizeof err);
     if (!src) return 0;
     if (hipb.dump_src) fprintf(stderr, "---- dense kernel with fused epilogue ----\n%s\n", src);
     if (!rtc_build_module(src, &fe->mod, err, sizeof err)) {
@@ -2145,7 +2156,7 @@ int dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunct
     hipFunction_t f = NULL;
     if (hipModuleGetFunction(&f, fe->mod, name) != hipSuccess ||
         !co_form_make(&fe->co, src, name, dense_threads(&e->plan), f) ||
-        fe->co.np != e->co.np + 2u * (c->n_leaves + 1u)) {
+        fe->co.np != e->co.np + 2u * (c->n_leaves + 1u) + (fe->sc.n ? 1u + fe->sc.n : 0u)) {
         HIPB_CHECK(hipModuleUnload(fe->mod));
         co_form_free(&fe->co);
         free(src);
@@ -2159,6 +2170,7 @@ int dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunct
                 (u32)(uop_signature(c) & 0xFFFFFFFFu));
     *fn = f;
     *co = fe->co;
+    *sc = fe->sc;
     return 1;
 }
 
@@ -2181,5 +2193,6 @@ char *dense_epilogue_source(const UOpKernel *k, const UOpKernel *c, u32 o_leaf, 
         snprintf(err, errlen, "not an elementwise consumer of the output at its own index");
         return NULL;
     }
-    return epi_source(k, &ct, &pl, c, o_leaf, "thvm_gemmep_check", err, errlen);
+    KGenScalars sc;
+    return epi_source(k, &ct, &pl, c, o_leaf, "thvm_gemmep_check", &sc, err, errlen);
 }

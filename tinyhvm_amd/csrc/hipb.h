@@ -196,7 +196,10 @@ const char *kgen_prelude(void);
 /* rebuilt with the current knobs on the next kgen_prelude() (backend init) */
 void kgen_prelude_reset(void);
 int  kgen_alu_expr(u32 uop, u32 aux, const char *a, const char *b, char *out, size_t n);
-int  kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen);
+/* An elementwise program's inline scalars: its loads of leaf[j] at index[j]
+ * (constant) take argument sv<j> when bit j of sm_ is set. */
+typedef struct { u32 n, leaf[KGEN_MAX_SCALARS], index[KGEN_MAX_SCALARS]; } KGenScalars;
+int  kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen, KGenScalars *sc);
 int  kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
                     char *out, size_t outlen);
 
@@ -255,7 +258,8 @@ int  hipb_hold_solo(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *co
 void hipb_hold_tag(u64 key, u32 serial, u32 out_buf);
 /* dense.c: the contraction (key, serial) with the elementwise program c,
  * which reads its output as leaf buffer o_leaf, fused into its epilogue */
-int  dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunction_t *fn, CoForm *co);
+int  dense_epilogue(u64 key, u32 serial, const UOpKernel *c, u32 o_leaf, hipFunction_t *fn, CoForm *co,
+                    KGenScalars *sc);
 char *dense_epilogue_source(const UOpKernel *k, const UOpKernel *c, u32 o_leaf, char *err, size_t errlen);
 
 /* ---------------- chain.c: elementwise programs fused in sequence ---------------- */

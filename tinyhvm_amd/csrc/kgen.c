@@ -1049,17 +1049,18 @@ const char *kgen_prelude(void) {
  * reads `r_expr`. Buffers are the kernel parameters p<i>/c<i>. Returns the
  * number of bytes written, or -1 if an op cannot be emitted this way. */
 static int emit_cone_subst(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
-                           u32 subst_leaf, const char *subst_expr, char *out, size_t outlen);
+                           u32 subst_leaf, const char *subst_expr, const i32 *scal, char *out, size_t outlen);
 
 int kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
                    char *out, size_t outlen) {
-    return emit_cone_subst(k, cone, gid_expr, r_expr, ~0u, NULL, out, outlen);
+    return emit_cone_subst(k, cone, gid_expr, r_expr, ~0u, NULL, NULL, out, outlen);
 }
 
 /* kgen_emit_cone, with every LOAD of leaf buffer subst_leaf (1 + leaf)
- * reading subst_expr instead */
+ * reading subst_expr instead, and each LOAD i with scal[i] >= 0 taking
+ * argument sv<scal[i]> when bit scal[i] of sm_ is set (an inline scalar) */
 static int emit_cone_subst(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
-                           u32 subst_leaf, const char *subst_expr, char *out, size_t outlen) {
+                           u32 subst_leaf, const char *subst_expr, const i32 *scal, char *out, size_t outlen) {
     SB sb = {0};
     char a[96], b[96], fb[64];
     for (u32 i = 0; i < k->n_ops; i++) {
@@ -1092,7 +1093,11 @@ static int emit_cone_subst(const UOpKernel *k, const u8 *cone, const char *gid_e
             if (bi == subst_leaf) { sb_put(&sb, "  const float f%u = %s;\n", i, subst_expr); break; }
             if (bi > k->n_leaves) { sb_put(&sb, "  const float f%u = 0.0f;\n", i); break; }
             u32 dt = bi == 0 ? k->out_dtype : k->leaf_dtypes[bi - 1];
-            sb_put(&sb, "  const float f%u = %s(p%u, c%u, %s);\n", i, dt_ld(dt), bi, bi, UA(op->arg[0], fa));
+            if (scal && scal[i] >= 0)
+                sb_put(&sb, "  const float f%u = ((sm_ >> %uu) & 1u) ? sv%d : %s(p%u, c%u, %s);\n", i, (u32)scal[i],
+                       scal[i], dt_ld(dt), bi, bi, UA(op->arg[0], fa));
+            else
+                sb_put(&sb, "  const float f%u = %s(p%u, c%u, %s);\n", i, dt_ld(dt), bi, bi, UA(op->arg[0], fa));
             break;
         }
         case KOP_MASK: {
@@ -1148,10 +1153,22 @@ static int emit_cone_subst(const UOpKernel *k, const u8 *cone, const char *gid_e
  * STORE; the caller checks that its loads of o_leaf and its STORE index are
  * gid itself. Buffers are the function's own p<b>/c<b> (0: its output).
  * Returns the length written, or -1. */
-int kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen) {
+int kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen, KGenScalars *sc) {
     u8 cone[KOP_MAX];
-    i32 st = -1;
+    i32 st = -1, scal[KOP_MAX];
     if (k->n_ops == 0 || k->n_ops > KOP_MAX) return -1;
+    /* loads at a constant index of another leaf: inline scalars */
+    sc->n = 0;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        scal[i] = -1;
+        if (op->type == KOP_LOAD && op->imm.u >= 1 && op->imm.u <= k->n_leaves && op->imm.u != o_leaf &&
+            op->arg[0] < k->n_ops && k->ops[op->arg[0]].type == KOP_CONST_U && sc->n < KGEN_MAX_SCALARS) {
+            sc->leaf[sc->n] = op->imm.u - 1;
+            sc->index[sc->n] = k->ops[op->arg[0]].imm.u;
+            scal[i] = (i32)sc->n++;
+        }
+    }
     for (u32 i = 0; i < k->n_ops; i++) {
         const KOpType t = k->ops[i].type;
         if (t == KOP_RANGE || t == KOP_ENDRANGE || t == KOP_ACC_INIT || t == KOP_ACC) return -1;
@@ -1165,11 +1182,15 @@ int kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen) {
     const KOp *so = &k->ops[st];
     if (so->arg[0] >= k->n_ops || so->arg[1] >= k->n_ops) return -1;
     char body[32768];
-    if (emit_cone_subst(k, cone, "gid_", "0u", o_leaf, "v_", body, sizeof body) < 0) return -1;
+    if (emit_cone_subst(k, cone, "gid_", "0u", o_leaf, "v_", scal, body, sizeof body) < 0) return -1;
     SB sb = {0};
     sb_put(&sb, "__device__ __forceinline__ void epi_(u32 gid_, float v_");
     for (u32 b = 0; b <= k->n_leaves; b++) sb_put(&sb, ", char* p%u", b);
     for (u32 b = 0; b <= k->n_leaves; b++) sb_put(&sb, ", u32 c%u", b);
+    if (sc->n) {
+        sb_put(&sb, ", u32 sm_");
+        for (u32 j = 0; j < sc->n; j++) sb_put(&sb, ", float sv%u", j);
+    }
     const int fv = op_is_float(k->ops[so->arg[1]].type);
     char v[48];
     if (fv) snprintf(v, sizeof v, "f%u", so->arg[1]);
