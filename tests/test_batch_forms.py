@@ -17,7 +17,7 @@ from tinyhvm_amd import _lib, trace
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 WL = os.path.join(ROOT, "tinyhvm_amd", "workloads")
-MAIN = re.compile(r'extern "C" __global__ __launch_bounds__\((\d+)\) void (\w+)\(')
+MAIN = re.compile(r'extern "C" __global__ __launch_bounds__\((\d+)\) (?:__attribute__\(\(\w+\([\d, ]*\)\)\) )?void (\w+)\(')
 
 
 def _modules(name):

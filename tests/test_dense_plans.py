@@ -2,8 +2,10 @@
 
 The plan choices are what the measured numbers rest on; this pins them so a
 change to the planner that silently drops one shows up here:
-- the 3x3 64->64 convolution (forward and input gradient): 64x64 tiles,
-  K-reordered loaders, its weights packed, the epilogue along the pixels;
+- the 3x3 64->64 convolution (forward and input gradient): the LDS-free wave
+  tile (a wave per 32 pixels by 64 channels, buffer loads with scalar k
+  offsets), K-reordered loaders, its weights packed, the epilogue along the
+  pixels;
 - its weight gradient: 64x64 tiles, 128 K splits, K-reordered loaders over
   image rows padded 56 -> 64, two stages of loads in flight;
 - the 4096^3 GEMMs: 128x128 tiles, K-reordered loaders, 16-byte loads, the
@@ -42,7 +44,8 @@ def _plans(name):
             "kperm": "kbase_p(" in src,
             "padded": "lim_" in src,
             "packed": "_pack(" in src,
-            "transposed": "(b[kk][j], a[kk][i]" in src,
+            "transposed": "(b[kk][j], a[kk][i]" in src or "(rb0[q], ra[q]" in src,
+            "wave": "__amdgpu_buffer_rsrc_t rA" in src,
             "vec16": "*(const float4*)(ps" in src,
             "two_stage": "ra1[" in src,
             "waves": int(nw.group(1)) if nw else 4,
@@ -58,7 +61,7 @@ def _plans(name):
 def test_convolution_plans():
     p = _plans("convblock_b64.trc")
     fwd = p[(200704, 64, 576, 1)]
-    assert fwd["tile"] == (64, 64) and fwd["kperm"] and fwd["packed"] and fwd["transposed"]
+    assert fwd["wave"] and fwd["kperm"] and fwd["packed"] and fwd["transposed"]
     assert not fwd["padded"]
     # the weight gradient's splits fill the 1024 workgroup slots of 256 CUs
     # exactly once: 9 row tiles x 112 splits of 2048 (padded, reordered) K

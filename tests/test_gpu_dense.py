@@ -21,13 +21,15 @@ pytestmark = pytest.mark.gpu
 # 3 = 256x32, 4 = 32x256, 5 = direct (per-wave 32x32 blocks, no LDS), 6 = 256x64,
 # 7 = 128x64, 8 = skinny (a row per lane, for at most 16 columns; wider
 # contractions keep the chosen tile), 9 = outer-product reduction (a k per
-# lane, for few outputs; others keep the chosen tile). The direct and
+# lane, for few outputs; others keep the chosen tile), 11 = the wave tile (no
+# LDS, a wave per 32 rows by 64 columns; contractions of 64 columns with the
+# B side packed, others keep the 64x64 tile). The direct and
 # outer-product kernels combine their split-K partials in the same launch;
 # "nocomb" sends them through the workspace and the sum kernel instead.
 CONFIGS = [("1", "0"), ("2", "0"), ("1", "1"), ("3", "2"), ("1", "3"), ("2", "4"), ("1", "5"), ("3", "5"),
            ("1", "6"), ("3", "6"), ("1", "7"), ("2", "7"), ("8", "2"), ("16", "7"), ("1", "2", "pack"),
            ("2", "7", "pack"), ("1", "8"), ("1", "8", "noskblk"), ("1", "9"), ("8", "5"), ("3", "5", "nocomb"),
-           ("1", "9", "nocomb")]
+           ("1", "9", "nocomb"), ("1", "11", "pack")]
 
 
 @pytest.fixture(scope="module", params=CONFIGS,
@@ -35,7 +37,8 @@ CONFIGS = [("1", "0"), ("2", "0"), ("1", "1"), ("3", "2"), ("1", "3"), ("2", "4"
                      "tile32x256-split2", "direct", "direct-split3", "tile256x64", "tile256x64-split3",
                      "tile128x64", "tile128x64-split2", "tile64x64-split8", "tile128x64-split16",
                      "tile64x64-packed", "tile128x64-split2-packed", "skinny", "skinny-per-k",
-                     "outer-product", "direct-split8", "direct-split3-sum-kernel", "outer-product-sum-kernel"])
+                     "outer-product", "direct-split8", "direct-split3-sum-kernel", "outer-product-sum-kernel",
+                     "wave-tile-packed"])
 def hip_dense(request):
     saved = {k: os.environ.get(k) for k in ("THVM_HIP_DENSE_FORCE", "THVM_HIP_DENSE_SPLITS",
                                              "THVM_HIP_DENSE_TILE", "THVM_HIP_DENSE_PACK", "THVM_HIP_DENSE_NOSKBLK",

@@ -605,6 +605,7 @@ static void read_dense_env(void) {
     hipb.dense_noskinny_blocks = env_flag("THVM_HIP_DENSE_NOSKBLK");
     hipb.dense_nored = env_flag("THVM_HIP_DENSE_NORED");
     hipb.dense_nocomb = env_flag("THVM_HIP_DENSE_NOCOMB");
+    hipb.dense_nowave = env_flag("THVM_HIP_DENSE_NOWAVE");
     hipb.no_fuse = env_flag("THVM_HIP_NO_FUSE");
     hipb.host_profile = env_flag("THVM_HIP_HOST_PROFILE");
     hipb.dense_pack = env_flag("THVM_HIP_DENSE_PACK");
@@ -627,7 +628,7 @@ static void read_dense_env(void) {
     if (hipb.gemm_depth > 2) hipb.gemm_depth = 0;
     e = getenv("THVM_HIP_DENSE_TILE");
     hipb.dense_tile = e ? (u32)atoi(e) : 0;
-    if (hipb.dense_tile > 9) hipb.dense_tile = 0;
+    if (hipb.dense_tile > 11) hipb.dense_tile = 0;
 }
 
 u32 hipb_resident_waves(void) { return hipb.resident_waves ? hipb.resident_waves : 256u * SINGLE_PASS_WAVES_PER_CU; }

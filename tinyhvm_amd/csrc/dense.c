@@ -330,12 +330,24 @@ static const TileCfg CFG_WIDE = {32, 256, 16, 1, 2, 1, 4, "32x256"};    /* M <= 
  * K 16 per stage keeps the stages at 42 KB of LDS (3 workgroups per CU) */
 static const TileCfg CFG_C64 = {256, 64, 16, 2, 2, 4, 1, "256x64"};
 static const TileCfg CFG_C64S = {128, 64, 32, 2, 1, 2, 2, "128x64"};
+/* 64 output channels: four waves stacked along M, each 32 rows by all 64
+ * columns (two accumulator chains sharing each A fragment) */
+static const TileCfg CFG_C64W = {128, 64, 16, 1, 2, 4, 1, "128x64w"};
 /* Small and skinny contractions (conv channels, fc layers, weight gradients):
  * with operands that fit in L2 there is little to gain from sharing tiles
  * through LDS, and everything to gain from keeping many independent loads in
  * flight without barriers. Each wave computes one 32x32 block, loading 32 K
  * of both MFMA operands per iteration straight into registers. */
 static const TileCfg CFG_DIRECT = {32, 32, 32, 1, 1, 1, 1, "direct32", 1};
+/* 64 output channels over many rows (3x3 64->64 convolutions): no LDS and
+ * no barriers. Each wave owns 32 rows by all 64 columns (two accumulator
+ * chains sharing each A fragment) and loads its MFMA fragments straight from
+ * memory with buffer loads: a lane's row offset is fixed, the k offset is
+ * uniform (scalar), and the B side is the packed K x 64 weight matrix. A ring
+ * of k-pairs of fragments is in flight ahead of the MFMAs. Measured on the
+ * 3x3 64->64 convolution over [64,64,56,56] in a standalone probe: 141 us
+ * against 242 us for the same probe's 64x64 LDS tile. */
+static const TileCfg CFG_WAVE = {32, 64, 2, 1, 2, 1, 1, "wave32x64", 4};
 /* Skinny contractions: at most 16 columns over many rows (the convolutions
  * of a few channels: LeNet-5's 6 and 16). A 32-wide MFMA block would leave
  * most of its columns empty; here each lane owns one row and keeps all N
@@ -427,6 +439,14 @@ static u32 dense_cus(void) { return hipb.n_cu ? hipb.n_cu : 256u; }
 /* workgroup size of a plan's main kernel */
 static u32 dense_threads(const GemmPlan *pl) {
     return pl->cfg.direct == 3 ? GEMM_THREADS : pl->cfg.direct ? 64u * pl->nw : GEMM_THREADS;
+}
+
+/* wave tile: k-pairs of fragments in flight (a divisor of the K-pair count) */
+static u32 wave_ring(u32 kpairs) {
+    static const u32 pf[] = {8, 6, 4, 3, 2, 1};
+    for (u32 i = 0; i < sizeof pf / sizeof pf[0]; i++)
+        if (kpairs % pf[i] == 0) return pf[i];
+    return 1;
 }
 #define SUM_WAVE_MIN_SPLITS 16   /* split-K sums this long use a wavefront per output, */
 #define SUM_WAVE_MAX_OUTPUTS 8192 /* unless there are enough outputs for a lane each */
@@ -937,6 +957,92 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
                "      if (m < M && n < N) {\n");
 }
 
+/* The wave-tile kernel (CFG_WAVE): one wave per 32-row tile of the output,
+ * all 64 columns. A k-pair kp covers reordered k = 2kp (lanes 0-31) and
+ * 2kp + 1 (lanes 32-63), which lie in the same run of the inner digit (its
+ * extent is even): the A fragment of row m is at rowb_p(gid_m(m)) +
+ * kbase_p(2kp) + h * icoef (h the lane's half), the B fragment at packed row
+ * 2kp + h. Buffer loads take the lane's offset as a VGPR and kbase as an SGPR;
+ * loads past the buffer read 0. Rows past M are clamped to M - 1 (their
+ * products are never stored). */
+static void emit_wave_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
+    const KPerm *kp = &pl->kp;
+    const u32 M = ct->M, N = ct->N, KPAIRS = kp->Kl / 2u, PF = wave_ring(KPAIRS);
+    const u32 tiles = pl->tiles_m;
+    const char *mf_a = pl->swap ? "rb0[q]" : "ra[q]", *mf_b = pl->swap ? "ra[q]" : "rb0[q]";
+    const char *mf_a1 = pl->swap ? "rb1[q]" : "ra[q]", *mf_b1 = pl->swap ? "ra[q]" : "rb1[q]";
+    /* at least six waves per SIMD: the register budget the compiler keeps
+     * to (measured 141 against 145 us with four or five) */
+    dsb_put(s, "extern \"C\" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 8))) void %s(",
+            pl->name);
+    emit_params(s, k->n_leaves);
+    dsb_put(s, ", float* ws, const float* pk%s) {\n", g_epi_params ? g_epi_params : "");
+    dsb_put(s,
+            "  constexpr u32 M = %uu, N = %uu, KP = %uu, PF = %uu, TILES = %uu, ICA = %uu;\n"
+            "  const u32 lane = threadIdx.x & 63u, h = lane >> 5;\n"
+            "  u32 tile = blockIdx.x;\n"
+            "  if (tile >= TILES) return;\n"
+            "  /* workgroup b runs on XCD b %% 8: consecutive tiles (rows that share\n"
+            "   * their neighbourhood of A) on one XCD's L2 */\n"
+            "  if (TILES %% 8u == 0u) tile = (tile %% 8u) * (TILES / 8u) + tile / 8u;\n"
+            "  const u32 m0 = tile * 32u, n0 = 0u, wm = 0u, wn = 0u;\n"
+            "  const u32 ma = (m0 + (lane & 31u) < M) ? m0 + (lane & 31u) : M - 1u;\n"
+            "  const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)p%u, (short)0,\n"
+            "      (int)((unsigned long long)c%u * 4ull < 0xFFFFFFFFull ? c%u * 4u : 0xFFFFFFFFu), 0x00020000);\n"
+            "  const __amdgpu_buffer_rsrc_t rB = __builtin_amdgcn_make_buffer_rsrc((void*)pk, (short)0, (int)(%uu * 4u), 0x00020000);\n"
+            "  const int vA = (int)((rowb_p(gid_m(ma)) + h * ICA) * 4u);\n"
+            "  const int vB = (int)((h * N + (lane & 31u)) * 4u);\n"
+            "  float ra[PF], rb0[PF], rb1[PF];\n"
+            "  auto load = [&](u32 kp, u32 q) {\n"
+            "    const int so = (int)(kbase_p(2u * kp) * 4u);\n"
+            "    ra[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rA, vA, so, 0));\n"
+            "    rb0[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rB, vB, (int)(kp * 2u * N * 4u), 0));\n"
+            "    rb1[q] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rB, vB + 128, (int)(kp * 2u * N * 4u), 0));\n"
+            "  };\n"
+            "  f32x16 acc[2];\n"
+            "  acc[0] = (f32x16){0};\n"
+            "  acc[1] = (f32x16){0};\n"
+            "  #pragma unroll\n"
+            "  for (u32 q = 0; q < PF; q++) load(q, q);\n"
+            "  for (u32 kb = 0; kb + PF < KP; kb += PF) {\n"
+            "    #pragma unroll\n"
+            "    for (u32 q = 0; q < PF; q++) {\n"
+            "      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[0], 0, 0, 0);\n"
+            "      acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[1], 0, 0, 0);\n"
+            "      load(kb + PF + q, q);\n"
+            "      /* each step's loads go out right after its MFMAs: PF k-pairs ahead */\n"
+            "      __builtin_amdgcn_sched_barrier(0);\n"
+            "    }\n"
+            "  }\n"
+            "  #pragma unroll\n"
+            "  for (u32 q = 0; q < PF; q++) {\n"
+            "    acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[0], 0, 0, 0);\n"
+            "    acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[1], 0, 0, 0);\n"
+            "  }\n",
+            M, N, KPAIRS, PF, tiles, kp->icoef[0], ct->sep_buf[0], ct->sep_buf[0], ct->sep_buf[0],
+            kp->Kl * N, mf_a, mf_b, mf_a1, mf_b1, mf_a, mf_b, mf_a1, mf_b1);
+    /* the LDS tile's epilogue: blocks (m, n) = (0, 0) and (0, 32) of the wave's tile */
+    dsb_put(s,
+            "  #pragma unroll\n"
+            "  for (u32 blk = 0; blk < 2u; blk++) {\n"
+            "    const f32x16 c = acc[blk];\n"
+            "    const u32 bm = wm, bn = wn + blk * 32u;\n"
+            "    #pragma unroll\n"
+            "    for (u32 v = 0; v < 16u; v++) {\n"
+            "      const u32 %s = %s0 + b%s + (lane & 31u);\n"
+            "      const u32 %s = %s0 + b%s + 8u * (v >> 2) + 4u * (lane >> 5) + (v & 3u);\n"
+            "      if (m < M && n < N) {\n", pl->swap ? "m" : "n", pl->swap ? "m" : "n",
+            pl->swap ? "m" : "n", pl->swap ? "n" : "m", pl->swap ? "n" : "m", pl->swap ? "n" : "m");
+}
+
+/* Whether a plan made for CFG_WAVE can run it: K-reordered loads with an
+ * even inner digit and no padding, the B side packed as K x 64, one split. */
+static int wave_plan_ok(const Contraction *ct, const GemmPlan *pl) {
+    const KPerm *kp = &pl->kp;
+    return pl->cfg.direct == 4 && kp->on && pl->pack && kp->E == kp->Ep && kp->E % 2 == 0 && kp->Kl % 2 == 0 &&
+           ct->N == 64 && pl->splits == 1 && kp->maxidx[0] < (1ull << 30) && (u64)kp->Kl * ct->N < (1ull << 28);
+}
+
 /* Uniform k base of one side at the stage starting at reordered index k. */
 static void emit_kbase_fn(DSB *s, const KPerm *kp, int side, const char *name) {
     dsb_put(s, "__device__ __forceinline__ u32 %s(u32 k) {\n  u32 o = k / %uu;\n  u32 u = (k %% %uu) * %uu;\n",
@@ -1083,7 +1189,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         emit_sum_kernel(&s, k, ct, pl);
         return s.p;
     }
-    if (cf->direct) {
+    if (cf->direct && cf->direct != 4) {
         emit_direct_kernel(&s, k, ct, pl);
         emit_store_tail(&s, k, ct, pl);
         return s.p;
@@ -1101,6 +1207,11 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
                     "  const u32 k = t / %uu, n = t %% %uu;\n"
                     "  pk[t] = (k %% %uu < %uu) ? ld_f32(p%u, c%u, kbase_qo(k) + rowb_q(gid_n(n))) : 0.0f;\n}\n",
                 pl->kp.Kl * N, N, N, pl->kp.Ep, pl->kp.E, ct->sep_buf[1], ct->sep_buf[1]);
+    }
+    if (cf->direct == 4) {
+        emit_wave_kernel(&s, k, ct, pl);
+        emit_store_tail(&s, k, ct, pl);
+        return s.p;
     }
     dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", GEMM_THREADS, pl->name);
     emit_params(&s, k->n_leaves);
@@ -1439,7 +1550,7 @@ static int plan_kperm(const Contraction *ct, GemmPlan *pl) {
     KPerm *kp = &pl->kp;
     memset(kp, 0, sizeof *kp);
     const TileCfg *cf = &pl->cfg;
-    if (hipb.dense_nokperm || cf->direct) return 0;
+    if (hipb.dense_nokperm || (cf->direct && cf->direct != 4)) return 0;
     const u64 K = ct->K, total = (u64)ct->M * ct->N;
     for (int s = 0; s < 2; s++)
         if (!ct->sep[s] || ct->sep_dt[s] != DTYPE_F32 || ct->sep_buf[s] == 0) return 0;
@@ -1606,7 +1717,7 @@ static void plan_pads(const Contraction *ct, GemmPlan *pl) {
 static void plan_pack(const Contraction *ct, GemmPlan *pl) {
     KPerm *kp = &pl->kp;
     pl->pack = 0;
-    if (!kp->on || hipb.dense_nopack || kp->vec[1] || pl->cfg.direct) return;
+    if (!kp->on || hipb.dense_nopack || kp->vec[1] || (pl->cfg.direct && pl->cfg.direct != 4)) return;
     const u32 per_lane = pl->cfg.bn * pl->cfg.bk / GEMM_THREADS;
     if ((u64)kp->Kl * ct->N > (4u << 20) || ct->N % 4 != 0 || ct->N % pl->cfg.bn != 0 || per_lane % 4 != 0 ||
         (pl->tiles_m < 64 && !hipb.dense_pack))
@@ -1640,6 +1751,10 @@ static void plan_chunks(const Contraction *ct, GemmPlan *pl) {
      * -> 17 us, and 16 waves were slower everywhere, 12 -> 31 us on fc1: wave
      * 0 then adds 15 partial blocks from 60 KB of LDS) */
     pl->nw = 4;
+    if (pl->cfg.direct == 4) {
+        pl->nw = 1;
+        return;
+    }
     if (pl->cfg.direct == 3) {
         /* row groups of at most RED_MAX_ACC / N rows, balanced; K chunks of
          * at least RED_K_PER_LANE k per lane, about 1024 workgroups at most */
@@ -1744,8 +1859,8 @@ static void plan_comb(const Contraction *ct, GemmPlan *pl) {
 }
 
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
-    static const TileCfg *forced[10] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
-                                        &CFG_C64S, &CFG_SKINNY, &CFG_RED};
+    static const TileCfg *forced[12] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
+                                        &CFG_C64S, &CFG_SKINNY, &CFG_RED, &CFG_C64W, &CFG_WAVE};
     const int red_fits = ct->sep[0] && ct->sep[1] && ct->sep_dt[0] == DTYPE_F32 && ct->sep_dt[1] == DTYPE_F32 &&
                          ct->M >= 2 && ct->N >= 2 &&
                          (u64)ct->M * ct->N <= RED_MAX_MN && ct->N <= RED_MAX_ACC;
@@ -1756,7 +1871,13 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
                           !(hipb.dense_tile == 9 && !red_fits);
     TileCfg cfg = forced_ok ? *forced[hipb.dense_tile] : pick_cfg(ct->M, ct->N, ct->K);
     if (!forced_ok && !hipb.dense_nored && red_fits && ct->K >= RED_MIN_K) cfg = CFG_RED;
+    if (!forced_ok && !hipb.dense_nowave && ct->N == 64 && ct->M >= 4096 && !long_k(ct->M, ct->N, ct->K)) {
+        make_plan_cfg(ct, pl, sig, &CFG_WAVE);
+        if (wave_plan_ok(ct, pl)) return;
+    }
+    if (cfg.direct == 4) cfg = CFG_MID;
     make_plan_cfg(ct, pl, sig, &cfg);
+    if (pl->cfg.direct == 4 && !wave_plan_ok(ct, pl)) make_plan_cfg(ct, pl, sig, &CFG_MID);
 }
 
 static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const TileCfg *cfg) {
@@ -1789,11 +1910,11 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
         if (splits > 1024) splits = 1024;
     }
     if (hipb.dense_splits) splits = hipb.dense_splits;
-    if (pl->cfg.direct == 2) splits = 1;
+    if (pl->cfg.direct == 2 || pl->cfg.direct == 4) splits = 1;
     if (pl->cfg.direct == 3) splits = 2;   /* the chunks are chosen with the row groups */
     pl->splits_want = splits;
     snprintf(pl->name, sizeof pl->name, "thvm_gemm_%08x", (u32)(sig & 0xFFFFFFFFu));
-    pl->swap = !pl->cfg.direct && !hipb.dense_noswap && ct->np > 0 && ct->pdiv[ct->np - 1] == 1 &&
+    pl->swap = (!pl->cfg.direct || pl->cfg.direct == 4) && !hipb.dense_noswap && ct->np > 0 && ct->pdiv[ct->np - 1] == 1 &&
                !(ct->nq > 0 && ct->qdiv[ct->nq - 1] == 1);
     plan_kperm(ct, pl);
     plan_pack(ct, pl);

@@ -60,12 +60,14 @@ typedef struct {
     int dense_noskinny_blocks; /* THVM_HIP_DENSE_NOSKBLK: the row-per-lane kernel walks K per k */
     int dense_nored;         /* THVM_HIP_DENSE_NORED: no outer-product reduction kernel */
     int dense_nocomb;        /* THVM_HIP_DENSE_NOCOMB: split-K partials always through a sum kernel */
+    int dense_nowave;        /* THVM_HIP_DENSE_NOWAVE: no LDS-free wave-tile kernel for 64-column contractions */
     int no_fuse;             /* THVM_HIP_NO_FUSE: no elementwise consumer fused into a contraction's epilogue */
     u32 direct_min_chunk;    /* THVM_HIP_DIRECT_MIN_CHUNK: shortest K chunk of a direct-kernel split (0: chosen) */
     int dense_pack;          /* THVM_HIP_DENSE_PACK: pack wherever the layout allows (tests) */
     u32 dense_tile;          /* THVM_HIP_DENSE_TILE: 0 chosen, 1 128x128, 2 64x64, 3 256x32, 4 32x256, 5 direct,
                                 6 256x64, 7 128x64, 8 skinny (where N <= 16), 9 outer-product reduction
-                                (where it applies) */
+                                (where it applies), 10 128x64 of 4 waves x 32x64, 11 wave tile (where it
+                                applies) */
     int force_interp;        /* THVM_HIP_INTERP: run generated-kernel programs on the KOp interpreter */
     int rtc_fail;            /* THVM_HIP_RTC_FAIL: treat every program compile as failed (tests) */
     u64 n_dispatch, n_compile, n_cache_hit, n_dense;

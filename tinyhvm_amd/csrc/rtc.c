@@ -383,6 +383,19 @@ int co_form_make(CoForm *cf, const char *src, const char *name, u32 threads, hip
                 q = r + 1;
                 while (*q == ' ') q++;
             }
+            /* a kernel attribute (waves per SIMD) does not apply to a device function */
+            if (strncmp(q, "__attribute__((", 15) == 0) {
+                int depth = 0;
+                const char *r = q + 13;
+                do {
+                    if (*r == '(') depth++;
+                    else if (*r == ')') depth--;
+                    r++;
+                } while (*r && depth > 0);
+                if (depth != 0) { free(o); goto fail; }
+                q = r;
+                while (*q == ' ') q++;
+            }
             if (strncmp(q, "void ", 5) != 0) { free(o); goto fail; }
             const char *par = strchr(q, '(');
             if (!par) { free(o); goto fail; }
