@@ -229,6 +229,23 @@ int  thvm_hip_epilogue_compile_check(const UOpKernel *producer, const UOpKernel 
 int  thvm_hip_chain_merge(const UOpKernel *p, const u32 *pb, const UOpKernel *c, u32 c_out, const u32 *c_leaves,
                           UOpKernel *m, u32 *mb);
 
+/* Run sums of one shape that follow each other (batchnorm's sums over one
+ * tensor, src/nn/batchnorm.c:35-111) run as one launch that reads what they
+ * share once; a held elementwise program or window max whose output they
+ * read is computed inside it (and still stored), and elementwise programs
+ * over their outputs (the mean, the variance, the inverse deviation) run in
+ * the workgroup that combines each output. The group kernel of programs
+ * ks[0..n) over buffer ids bufs[i] (output, then leaves), the first the
+ * producer when `producer` is set, generated and compiled without loading
+ * (no device needed). Returns the code-object size, or -1 with the reason in
+ * errbuf (also when a program does not join). A diagnostic with no
+ * counterpart in the reference. */
+int  thvm_hip_group_compile_check(const UOpKernel *const *ks, const u32 *const *bufs, u32 n, int producer,
+                                  char *errbuf, u64 errlen);
+/* Its source (length, or -1 with the reason in buf). */
+int  thvm_hip_group_source(const UOpKernel *const *ks, const u32 *const *bufs, u32 n, int producer, char *buf,
+                           u64 buflen);
+
 /* Independent dispatches held back and issued as one launch: the batch
  * kernel of n generated modules (srcs[i] as the generators above return it,
  * names[i] its main kernel, threads[i] its workgroup size, grid[2i], grid[2i+1]

@@ -249,19 +249,44 @@ def test_merged_programs_compile():
 
 def test_no_merge_without_a_gid_read():
     """A consumer that reads the producer's output anywhere but at its own
-    gid (a padded copy) does not merge, nor one whose output is one of the
-    producer's buffers, nor one that does not read the producer's output."""
+    gid (a padded copy) does not merge, nor one whose output is a buffer the
+    producer reads at other elements than each lane's own, nor one that does
+    not read the producer's output."""
     seq, _ = dispatches("convblock_b64.trc")
     k20, d20 = seq[20]           # batchnorm backward dc
     k26, d26 = seq[26]           # the padded copy of dc: reads it shifted
     assert d20[0] in d26[1:]
     assert _lib.chain_merge(k20, d20, k26, d26[0], d26[1:]) is None
-    k8, d8 = seq[8]
+    k8, d8 = seq[8]              # xhat = c * rstd[channel]
     k9, d9 = seq[9]
-    assert _lib.chain_merge(k8, d8, k9, d8[1], d9[1:]) is None
+    assert _lib.chain_merge(k8, d8, k9, d8[2], d9[1:]) is None    # into rstd, read per channel
     k10, d10 = seq[10]           # running mean, then running variance:
     k11, d11 = seq[11]           # independent of each other
     assert _lib.chain_merge(k10, d10, k11, d11[0], d11[1:]) is None
+
+
+def test_in_place_update_merges():
+    """A consumer whose output is a buffer the producer reads only at each
+    lane's own element (ASSIGN writing an updated value back over the input
+    it came from) merges: each lane loads its element before the merged
+    store, so M leaves every buffer as P followed by C does."""
+    seq, sizes = dispatches("convblock_b1.trc")
+    k8, d8 = seq[8]              # xhat = c * rstd[channel], c read at gid
+    k9, d9 = seq[9]
+    r = _lib.chain_merge(k8, d8, k9, d8[1], d9[1:])
+    assert r is not None
+    m, mb = r
+    rng = np.random.default_rng(11)
+    ids = {i for i in list(d8) + list(d9) + list(mb) if i}
+    init = {i: rng.standard_normal(sizes[i] // 4).astype(np.float32) for i in ids}
+    a = {i: v.copy() for i, v in init.items()}
+    b = {i: v.copy() for i, v in init.items()}
+    run(k8, a, d8)
+    run(k9, a, [d8[1]] + list(d9[1:]))
+    run(m, b, mb)
+    for i in ids:
+        assert a[i].tobytes() == b[i].tobytes(), "buffer %d differs" % i
+    assert _lib.compile_check(m) > 0
 
 
 def _with_extra_store(k, slot):

@@ -80,6 +80,10 @@ def lib():
                                                       u64]),
         "thvm_hip_batch_compile_check": (C.c_int, [C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), PU32, PU32, u32,
                                                    cp, u64]),
+        "thvm_hip_group_compile_check": (C.c_int, [C.POINTER(C.POINTER(abi.UOpKernel)), C.POINTER(PU32), u32,
+                                                   C.c_int, cp, u64]),
+        "thvm_hip_group_source": (C.c_int, [C.POINTER(C.POINTER(abi.UOpKernel)), C.POINTER(PU32), u32, C.c_int,
+                                            cp, u64]),
         "thvm_trace_load": (vp, [cp]),
         "thvm_trace_free": (None, [vp]),
         "thvm_trace_count": (u32, [vp]),
@@ -116,6 +120,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
     "thvm_hip_window_analyze", "thvm_hip_window_source", "thvm_hip_window_compile_check",
     "thvm_hip_batch_compile_check", "thvm_hip_flush", "thvm_hip_epilogue_compile_check", "thvm_hip_chain_merge",
+    "thvm_hip_group_compile_check", "thvm_hip_group_source",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
     "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",
@@ -174,6 +179,37 @@ def epilogue_compile_check(producer: abi.UOpKernel, consumer: abi.UOpKernel, o_l
     when the pair does not fuse or does not compile."""
     err = C.create_string_buffer(4096)
     r = lib().thvm_hip_epilogue_compile_check(C.byref(producer), C.byref(consumer), o_leaf, err, len(err))
+    if r < 0:
+        raise ValueError(err.value.decode())
+    return r
+
+
+def _group_args(kernels, bufs):
+    n = len(kernels)
+    ks = (C.POINTER(abi.UOpKernel) * n)(*[C.pointer(k) for k in kernels])
+    arrs = [(C.c_uint32 * len(b))(*b) for b in bufs]
+    pu = C.POINTER(C.c_uint32)
+    bp = (pu * n)(*[C.cast(a, pu) for a in arrs])
+    return ks, bp, arrs
+
+
+def group_source(kernels, bufs, producer=False):
+    """Source of the run-sum group kernel of `kernels` (the first the taken-in
+    producer when `producer`) over buffer ids `bufs` (per program: output,
+    then leaves); raises ValueError with the reason when they do not group."""
+    ks, bp, _keep = _group_args(kernels, bufs)
+    buf = C.create_string_buffer(1 << 20)
+    n = lib().thvm_hip_group_source(ks, bp, len(kernels), int(producer), buf, len(buf))
+    if n < 0:
+        raise ValueError(buf.value.decode())
+    return buf.value.decode()
+
+
+def group_compile_check(kernels, bufs, producer=False):
+    """Code-object size of that kernel (compiled without a device)."""
+    ks, bp, _keep = _group_args(kernels, bufs)
+    err = C.create_string_buffer(4096)
+    r = lib().thvm_hip_group_compile_check(ks, bp, len(kernels), int(producer), err, len(err))
     if r < 0:
         raise ValueError(err.value.decode())
     return r

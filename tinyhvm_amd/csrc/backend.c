@@ -108,9 +108,16 @@ typedef struct {
     u32 ch_bufs[1 + FUSE_MAX_LEAVES]; /* ... its buffers (output, leaves) */
     u64 ch_seq;            /* ... the pool's host-write clock when it was held */
     u32 ch_nb;
+    u32 wg;                /* a run-sum group later sums and consumers may join (1 + index into HB.wg; 0: none) */
+    const void *wmax;      /* a window max a run sum over its output may take in (window.c entry; NULL: none) */
+    u32 wmax_bufs[2];      /* ... its output and input */
+    u64 hid;               /* identifies the held launch while it is held */
 } HbEnt;
 static struct {
     HbEnt ent[HB_MAX];
+    WinGroup wg[HB_MAX];
+    u8 wg_used[HB_MAX];
+    u64 next_hid;
     u32 n;
     u64 comb_used;         /* combine-area words given to the held launches */
     int flushing;
@@ -334,15 +341,20 @@ static void hb_flush(void) {
     }
     HB.n = 0;
     HB.comb_used = 0;
+    memset(HB.wg_used, 0, sizeof HB.wg_used);
     HB.flushing = 0;
     pool_release_deferred();
 }
 
 int hipb_held_buffer(u32 id) {
-    for (u32 i = 0; i < HB.n; i++)
-        if (HB.ent[i].ch)
-            for (u32 b = 0; b < HB.ent[i].ch_nb; b++)
-                if (HB.ent[i].ch_bufs[b] == id) return 1;
+    for (u32 i = 0; i < HB.n; i++) {
+        const HbEnt *h = &HB.ent[i];
+        if (h->ch)
+            for (u32 b = 0; b < h->ch_nb; b++)
+                if (h->ch_bufs[b] == id) return 1;
+        if (h->wg && window_group_uses(&HB.wg[h->wg - 1], id, 0)) return 1;
+        if (h->wmax && (h->wmax_bufs[0] == id || h->wmax_bufs[1] == id)) return 1;
+    }
     return 0;
 }
 
@@ -368,6 +380,9 @@ static const char *hb_joins(const HbEnt *h) {
     if (h->solo || (HB.n && HB.ent[0].solo)) return "held alone";
     u32 T = h->co.threads, lds = h->co.lds, blocks = h->gx * h->gy;
     int resident = h->resident;
+    /* the batch kernel holds no more waves at once than its most demanding
+     * program's kernel does (the exact count is checked when it is built) */
+    u32 cap = h->co.cap_waves ? h->co.cap_waves : hipb_resident_waves();
     for (u32 i = 0; i < HB.n; i++) {
         const HbEnt *o = &HB.ent[i];
         if (hbm_clash(&h->m, &o->m)) return "memory";
@@ -375,10 +390,12 @@ static const char *hb_joins(const HbEnt *h) {
         lds += o->co.lds;
         blocks += o->gx * o->gy;
         resident |= o->resident;
+        const u32 c = o->co.cap_waves ? o->co.cap_waves : hipb_resident_waves();
+        if (c < cap) cap = c;
     }
     if (lds > HB_MAX_LDS) return "LDS";
     if ((u64)blocks * T >= (1ull << 32)) return "grid size";
-    if (resident && (u64)blocks * (T / 64u) > hipb_resident_waves()) return "residency";
+    if (resident && (u64)blocks * (T / 64u) > cap) return "residency";
     return NULL;
 }
 
@@ -402,6 +419,12 @@ static int hb_hold_large(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, voi
     return hb_hold(cf, fn, gx, gy, params, m, 0, -1, 0, 2);
 }
 
+int hipb_hold_large(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
+                    int resident, int comb_param, u64 comb_words) {
+    if (hipb.no_fuse) return 0;
+    return hb_hold(cf, fn, gx, gy, params, m, resident, comb_param, comb_words, 2);
+}
+
 static int hb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
                    int resident, int comb_param, u64 comb_words, int solo) {
     if (!cf || !cf->src || hipb.no_batch || hipb.noalloc || hipb.sync_each || HB.flushing) return 0;
@@ -417,6 +440,9 @@ static int hb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *con
     h->solo = solo == 1;
     h->ch = NULL;
     h->ch_nb = 0;
+    h->wg = 0;
+    h->wmax = NULL;
+    h->hid = ++HB.next_hid;
     h->fn = fn;
     h->gx = gx;
     h->gy = gy;
@@ -469,6 +495,164 @@ static void hb_hold_chain(const ChainInfo *ch, u32 out_buf, const u32 *leaf_bufs
     h->ch_bufs[0] = out_buf;
     memcpy(h->ch_bufs + 1, leaf_bufs, ch->n_leaves * sizeof(u32));
     h->ch_seq = pool_write_clock();
+}
+
+/* Marks the launch just held as a run sum: a group of one that run sums of
+ * the same shape and consumers of its output may join (hb_try_group). */
+void hipb_hold_tag_sum(const void *we, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves) {
+    if (!HB.n || hipb.no_fuse) return;
+    HbEnt *h = &HB.ent[HB.n - 1];
+    for (u32 i = 0; i < HB_MAX; i++) {
+        if (HB.wg_used[i]) continue;
+        if (window_group_of_sum(&HB.wg[i], we, out_buf, leaf_bufs, n_leaves)) {
+            HB.wg_used[i] = 1;
+            h->wg = i + 1;
+        }
+        return;
+    }
+}
+
+/* Marks the launch just held as a window max that a run sum over its output
+ * may take in. */
+void hipb_hold_tag_wmax(const void *we, u32 out_buf, u32 in_buf) {
+    if (!HB.n || hipb.no_fuse) return;
+    HbEnt *h = &HB.ent[HB.n - 1];
+    h->wmax = we;
+    h->wmax_bufs[0] = out_buf;
+    h->wmax_bufs[1] = in_buf;
+    h->ch_seq = pool_write_clock();
+}
+
+static i32 hb_find(u64 hid) {
+    for (u32 i = 0; i < HB.n; i++)
+        if (HB.ent[i].hid == hid) return (i32)i;
+    return -1;
+}
+
+/* Points held launch h at kernel fn (form cf) with these parameters, in
+ * place: its own slice of the combine area after the others'. Returns 0 if
+ * they do not fit (h unchanged). */
+static int hb_set_launch(HbEnt *h, const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params,
+                         int resident, int comb_param, u64 comb_words) {
+    if (!cf || !cf->src || gx == 0 || gy == 0 || cf->np == 0 || comb_words > COMB_SLOTS ||
+        HB.comb_used + comb_words > COMB_SLOTS || (comb_param >= 0 && ((u32)comb_param >= cf->np ||
+        cf->psz[comb_param] != 8)))
+        return 0;
+    u8 args[HB_ARG_BYTES];
+    u32 off = 0;
+    for (u32 j = 0; j < cf->np; j++) {
+        off = hb_arg_off(off, cf->psz[j]);
+        if (off + cf->psz[j] > HB_ARG_BYTES) return 0;
+        memcpy(args + off, params[j], cf->psz[j]);
+        if ((i32)j == comb_param) {
+            unsigned long long *base;
+            memcpy(&base, args + off, 8);
+            base += HB.comb_used;
+            memcpy(args + off, &base, 8);
+        }
+        off += cf->psz[j];
+    }
+    if (comb_param >= 0) HB.comb_used += comb_words;
+    memcpy(h->args, args, sizeof args);
+    h->co = *cf;
+    h->fn = fn;
+    h->gx = gx;
+    h->gy = gy;
+    h->resident = resident;
+    h->solo = 0;
+    return 1;
+}
+
+/* Run-sum groups (window.c): a run sum that has the shape of a held group's
+ * sums joins it, or takes in the held elementwise program or window max
+ * whose output it reads; an elementwise consumer of a held group's output
+ * becomes one of its tails. The held launch is rebuilt in place as the
+ * group's kernel. Only when the new program's memory meets no other held
+ * launch, and a taken-in producer's buffers are unwritten by the host since
+ * it was held. Returns 1 when the dispatch joined. */
+static int hb_try_group(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
+    static WinGroup g;
+    if (!HB.n || hipb.no_fuse || hipb.no_window || hipb.noalloc || hipb.sync_each || HB.flushing || !k ||
+        k->n_leaves == 0 || k->n_leaves > n_leaves || k->n_leaves > WG_MAX_LEAVES || !pool_ptr(out_buf))
+        return 0;
+    int loop = 0;
+    for (u32 i = 0; i < k->n_ops && !loop; i++) loop = k->ops[i].type == KOP_RANGE;
+    i32 at = -1;
+    if (!loop) {
+        for (u32 i = HB.n; i-- > 0 && at < 0;) {
+            if (!HB.ent[i].wg) continue;
+            g = HB.wg[HB.ent[i].wg - 1];
+            if (window_group_add_tail(&g, k, out_buf, leaf_bufs, n_leaves)) at = (i32)i;
+        }
+    } else {
+        const void *we = window_sum_entry(k);
+        if (!we) return 0;
+        for (u32 i = HB.n; i-- > 0 && at < 0;) {
+            if (!HB.ent[i].wg) continue;
+            g = HB.wg[HB.ent[i].wg - 1];
+            if (window_group_add_sum(&g, we, out_buf, leaf_bufs, n_leaves)) at = (i32)i;
+        }
+        for (u32 i = HB.n; i-- > 0 && at < 0;) {
+            const HbEnt *h = &HB.ent[i];
+            int fresh = 1;
+            if (h->ch) {
+                for (u32 b = 0; b < h->ch_nb; b++) {
+                    const HipbBuf *pb = h->ch_bufs[b] ? pool_get(h->ch_bufs[b]) : NULL;
+                    if (h->ch_bufs[b] && (!pb || !pb->ptr || pb->wseq > h->ch_seq)) fresh = 0;
+                }
+                if (fresh && window_group_of_chain(&g, h->ch, h->ch_bufs) &&
+                    window_group_add_sum(&g, we, out_buf, leaf_bufs, n_leaves))
+                    at = (i32)i;
+            } else if (h->wmax) {
+                for (u32 b = 0; b < 2; b++) {
+                    const HipbBuf *pb = pool_get(h->wmax_bufs[b]);
+                    if (!pb || !pb->ptr || pb->wseq > h->ch_seq) fresh = 0;
+                }
+                if (fresh && window_group_of_wmax(&g, h->wmax, h->wmax_bufs[0], h->wmax_bufs[1]) &&
+                    window_group_add_sum(&g, we, out_buf, leaf_bufs, n_leaves))
+                    at = (i32)i;
+            }
+        }
+    }
+    if (at < 0 || !window_group_build(&g)) return 0;
+    HbMem m;
+    window_group_mem(&g, &m);
+    for (u32 i = 0; i < HB.n; i++)
+        if ((i32)i != at && hbm_clash(&m, &HB.ent[i].m)) return 0;
+    /* the new program's inputs current on the device (a copy that meets a
+     * held launch issues the held launches, and then nothing joins) */
+    const u64 hid = HB.ent[at].hid;
+    if (loop) {
+        for (u32 j = 0; j < k->n_leaves; j++) pool_sync_device(leaf_bufs[j]);
+    } else {
+        const u64 reads = window_group_tail_reads(&g, g.n_tail - 1);
+        for (u32 j = 0; j < k->n_leaves; j++)
+            if (j >= 64 || ((reads >> j) & 1u)) pool_sync_device(leaf_bufs[j]);
+    }
+    at = hb_find(hid);
+    if (at < 0) return 0;
+    HbEnt *h = &HB.ent[at];
+    WgArgs a;
+    void *params[CO_MAX_PARAMS + 8];
+    const u32 np = window_group_params(&g, &a, params);
+    if (np != g.co->np || !hb_set_launch(h, g.co, g.fn, g.grid, 1, params, g.resident, g.resident ? (int)np - 1 : -1,
+                                         g.comb_words))
+        return 0;
+    h->m = m;
+    h->ch = NULL;
+    h->ch_nb = 0;
+    h->wmax = NULL;
+    h->fz_key = 0;
+    if (!h->wg) {
+        for (u32 i = 0; i < HB_MAX && !h->wg; i++)
+            if (!HB.wg_used[i]) {
+                HB.wg_used[i] = 1;
+                h->wg = i + 1;
+            }
+    }
+    if (h->wg) HB.wg[h->wg - 1] = g;
+    hipb.n_fused++;
+    return 1;
 }
 
 static u32 elem_count(u32 id, u32 dtype);
@@ -1006,6 +1190,7 @@ static int hb_try_chain(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
     for (u32 i = 0; i < HB.n && at < 0; i++)
         if (HB.ent[i].ch == ch && HB.ent[i].ch_bufs[0] == tag[0] && (u32)HB.ent[i].ch_seq == tag[1]) at = (i32)i;
     if (at < 0) return 0;
+    if (HB.ent[at].wg) HB.wg_used[HB.ent[at].wg - 1] = 0;
     memmove(&HB.ent[at], &HB.ent[at + 1], (HB.n - (u32)at - 1) * sizeof(HbEnt));
     HB.n--;
     hb_run_generated(e, mb[0], mb + 1, M.n_leaves, &M);
@@ -1058,6 +1243,13 @@ static void hb_dispatch_uop_kernel_(u32 out_buf, const u32 *leaf_bufs, u32 n_lea
     hipb.n_dispatch++;
     copyq_guard_dispatch(out_buf, leaf_bufs, n_leaves < FUSE_MAX_LEAVES ? n_leaves : FUSE_MAX_LEAVES);
     pool_sync_device(out_buf);
+    if (!hipb.force_interp && hb_try_group(out_buf, leaf_bufs, n_leaves, k)) {
+        pool_mark_device_write(out_buf);
+        int loop = 0;
+        for (u32 i = 0; i < k->n_ops && !loop; i++) loop = k->ops[i].type == KOP_RANGE;
+        if (!loop) hb_prepare_standalone(k);   /* a run sum's own kernel exists already */
+        return;
+    }
     if (!hipb.force_interp && hb_try_epilogue(out_buf, leaf_bufs, n_leaves, k)) {
         pool_mark_device_write(out_buf);
         hb_prepare_standalone(k);
@@ -1465,9 +1657,54 @@ static void hb_adam_step(u32 param, u32 grad, u32 m, u32 v, f32 lr, f32 beta1, f
     pool_mark_device_write(v);
 }
 
+/* A copy of the whole f32 output of a held chainable program as one more
+ * consumer of it: the copy program (one load at gid, one store) merged into
+ * the producer (hb_try_chain), so that the producer's launch writes both
+ * buffers. ASSIGN copies each updated parameter or running statistic back
+ * right after the kernel that computed it. Returns 1 when merged. */
+static int hb_copy_as_chain(u32 dst_buf, u32 src_buf, u64 nbytes) {
+    static UOpKernel ck;
+    if (!HB.n || hipb.no_fuse || nbytes % 4 || nbytes / 4 == 0 || nbytes / 4 > 0xFFFFFFFFull ||
+        pool_bytes(src_buf) < nbytes || pool_bytes(dst_buf) < nbytes || dst_buf == src_buf)
+        return 0;
+    int held = 0;
+    for (u32 i = 0; i < HB.n && !held; i++)
+        if (HB.ent[i].ch)
+            for (u32 st = 0; st < HB.ent[i].ch->n_st; st++)
+                held |= HB.ent[i].ch_bufs[HB.ent[i].ch->st_slot[st]] == src_buf &&
+                        HB.ent[i].ch->total == (u32)(nbytes / 4) && HB.ent[i].ch->st_f32[st];
+    if (!held) return 0;
+    memset(&ck, 0, offsetof(UOpKernel, leaf_views));
+    ck.ops[0].type = KOP_GID;
+    ck.ops[1].type = KOP_LOAD;
+    ck.ops[1].arg[0] = 0;
+    ck.ops[1].imm.u = 1;
+    ck.ops[2].type = KOP_STORE;
+    ck.ops[2].arg[0] = 0;
+    ck.ops[2].arg[1] = 1;
+    ck.ops[2].imm.u = 0;
+    ck.n_ops = 3;
+    ck.n_leaves = 1;
+    ck.n_bufs = 2;
+    ck.leaf_dtypes[0] = DTYPE_F32;
+    ck.out_dtype = DTYPE_F32;
+    ck.grid[0] = (u32)(nbytes / 4);
+    ck.grid[1] = ck.grid[2] = 1;
+    ck.local_size = 0;
+    if (!hb_try_chain(dst_buf, &src_buf, 1, &ck)) return 0;
+    pool_mark_device_write(dst_buf);
+    return 1;
+}
+
 static void hb_buf_copy(u32 dst_buf, u32 src_buf, u64 nbytes) {
     HipbBuf *d = pool_get(dst_buf), *s = pool_get(src_buf);
     if (!d || !s || nbytes == 0) return;
+    /* the whole output of a held elementwise program: written by its launch */
+    if (!copyq_uses(dst_buf) && !copyq_uses(src_buf) && !d->dev_stale && nbytes <= d->cap &&
+        hb_copy_as_chain(dst_buf, src_buf, nbytes)) {
+        hipb.n_copy_fused++;
+        return;
+    }
     /* a queued copy that writes this copy's source or touches its
      * destination must land first */
     for (u32 i = 0; i < CQ.b.n; i++)
@@ -1709,6 +1946,36 @@ int thvm_hip_epilogue_compile_check(const UOpKernel *producer, const UOpKernel *
     free(src);
     if (n < 0 && errbuf && errlen) snprintf(errbuf, errlen, "%s", err);
     return (int)n;
+}
+
+int thvm_hip_group_source(const UOpKernel *const *ks, const u32 *const *bufs, u32 n, int producer, char *buf,
+                          u64 buflen) {
+    ensure_env();
+    char err[256] = {0};
+    char *src = window_group_source(ks, bufs, n, producer, err, sizeof err);
+    if (!src) {
+        if (buf && buflen) snprintf(buf, buflen, "%s", err[0] ? err : "no group");
+        return -1;
+    }
+    const size_t len = strlen(src);
+    if (buf && buflen) snprintf(buf, buflen, "%s", src);
+    free(src);
+    return (int)len;
+}
+
+int thvm_hip_group_compile_check(const UOpKernel *const *ks, const u32 *const *bufs, u32 n, int producer,
+                                 char *errbuf, u64 errlen) {
+    ensure_env();
+    char err[256] = {0};
+    char *src = window_group_source(ks, bufs, n, producer, err, sizeof err);
+    if (!src) {
+        if (errbuf && errlen) snprintf(errbuf, errlen, "%s", err[0] ? err : "no group");
+        return -1;
+    }
+    long r = rtc_compile_only(src, err, sizeof err);
+    free(src);
+    if (r < 0 && errbuf && errlen) snprintf(errbuf, errlen, "%s", err);
+    return (int)r;
 }
 
 int thvm_hip_window_compile_check(const UOpKernel *k, char *errbuf, u64 errlen) {

@@ -114,6 +114,12 @@ ChainInfo *chain_info_make(const UOpKernel *k, const KOp *ops) {
         ci->st_f32[ci->n_st] = slot_dtype(k, slot) == DTYPE_F32;
         ci->n_st++;
     }
+    ci->gid_loads = ~0ull;
+    for (u32 i = 0; i < k->n_ops && ok; i++) {
+        const KOp *op = &k->ops[i];
+        if (op->type == KOP_LOAD && op->imm.u < 64 && !aff_is_gid(&dc, &aff[op->arg[0]]))
+            ci->gid_loads &= ~(1ull << op->imm.u);
+    }
     free(aff);
     if (!ok || ci->n_st == 0) {
         free(ci);
@@ -134,9 +140,15 @@ int chain_merge(const ChainInfo *p, const u32 *pb, const UOpKernel *c, u32 c_out
     if (!p || !pb || !c || !c_leaves || !m || !mb || c->n_leaves > c_nl || c->n_leaves > FUSE_MAX_LEAVES ||
         !loop_free(c) || launch_total(c) != p->total || p->n_ops + c->n_ops > CHAIN_MAX_OPS || c_out == 0)
         return 0;
-    /* C's output is none of P's buffers and not read by C */
-    for (u32 s = 0; s <= p->n_leaves; s++)
-        if (pb[s] == c_out) return 0;
+    /* C's output is none of P's buffers, except one P only reads, each lane
+     * its own element (an in-place update: the lane's load comes before the
+     * merged store), and not read by C */
+    for (u32 s = 0; s <= p->n_leaves; s++) {
+        if (pb[s] != c_out) continue;
+        if (s == 0 || s >= 64 || !((p->gid_loads >> s) & 1u)) return 0;
+        for (u32 j = 0; j < p->n_st; j++)
+            if (p->st_slot[j] == s) return 0;
+    }
     for (u32 j = 0; j < c->n_leaves; j++)
         if (c_leaves[j] == c_out) return 0;
     Aff *aff = calloc(c->n_ops, sizeof(Aff));

@@ -19,6 +19,7 @@
 #include <hip/hip_runtime_api.h>
 
 #include "thvm_abi.h"
+#include "affine.h"
 
 #define HIPB_CHECK(expr)                                                         \
     do {                                                                         \
@@ -75,6 +76,7 @@ typedef struct {
     u64 n_window;            /* dispatches run on the window-max and run-sum kernels */
     u64 n_batched;           /* dispatches issued inside a batched launch */
     u64 n_fused;             /* elementwise dispatches run as a contraction's fused epilogue */
+    u64 n_copy_fused;        /* buffer copies written by the launch of the program that produced them */
     int host_profile;        /* THVM_HIP_HOST_PROFILE: host time per category, printed by profile_report */
     u64 hp_ns[HP_N], hp_calls[HP_N];
     int no_batch;            /* THVM_HIP_NO_BATCH: launch every dispatch on its own */
@@ -202,6 +204,17 @@ int  kgen_alu_expr(u32 uop, u32 aux, const char *a, const char *b, char *out, si
  * (constant) take argument sv<j> when bit j of sm_ is set. */
 typedef struct { u32 n, leaf[KGEN_MAX_SCALARS], index[KGEN_MAX_SCALARS]; } KGenScalars;
 int  kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen, KGenScalars *sc);
+/* the same as a device function named fname that returns the value it stores */
+int  kgen_epilogue_fn(const UOpKernel *k, u32 o_leaf, const char *fname, char *out, size_t outlen,
+                      KGenScalars *sc);
+/* A loop-free program as a device function fname(gid_, st_, r0_.., p0.., c0..)
+ * that computes it for gid_, stores its STOREs when st_ is set and returns
+ * STORE j's value in *r<j>_. */
+int  kgen_producer_fn(const UOpKernel *k, const char *fname, char *out, size_t outlen, KGenScalars *sc);
+/* the same for gids X0..X0+3 (X0 a multiple of 4, `total` gids in all) in the
+ * serial generator's vector form: fname(X0, st_, r0_.., ...), float4 values */
+int  kgen_producer4_fn(const UOpKernel *k, u32 total, const char *fname, char *out, size_t outlen,
+                       KGenScalars *sc);
 int  kgen_emit_cone(const UOpKernel *k, const u8 *cone, const char *gid_expr, const char *r_expr,
                     char *out, size_t outlen);
 
@@ -228,6 +241,7 @@ typedef struct {
     u32 id;                /* namespace co_<id>, unique in the process */
     u32 threads;           /* its workgroup size */
     u32 lds;               /* its static LDS bytes */
+    u32 cap_waves;         /* its waves the GPU holds at once (0: not known) */
     u32 np;
     u8 psz[CO_MAX_PARAMS]; /* its parameters' sizes in bytes */
 } CoForm;
@@ -252,6 +266,10 @@ void hbm_add(HbMem *m, const void *p, u64 bytes, int write);
  * slice of the area. */
 int  hipb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
                int resident, int comb_param, u64 comb_words);
+/* hipb_hold for a launch of any grid size that a later dispatch may join
+ * (a run sum, a window max: run-sum groups); only while fusion is on. */
+int  hipb_hold_large(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m,
+                     int resident, int comb_param, u64 comb_words);
 /* Holds a launch (of any grid size) only so that the next dispatch can fuse
  * into it (hipb_hold_tag); it joins no batch. Returns 1 if held. */
 int  hipb_hold_solo(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *const *params, const HbMem *m);
@@ -274,6 +292,7 @@ typedef struct {
     u32 leaf_dtypes[FUSE_MAX_LEAVES];
     u32 n_st, st_slot[CHAIN_MAX_STORES], st_val[CHAIN_MAX_STORES];  /* its STOREs: buffer slot, value op */
     u8 st_f32[CHAIN_MAX_STORES];
+    u64 gid_loads;            /* bit s: every load of leaf slot s is at gid (a lane reads only its own element) */
 } ChainInfo;
 /* A program with no loop or one top-level loop, whose STOREs all follow
  * the loop and write at gid (so a consumer that reads one of its outputs at
@@ -338,6 +357,73 @@ char *window_source(const UOpKernel *k);
 void window_shutdown(void);
 /* a program that is neither gets its (negative) entry without a dispatch */
 void window_note_plain(const UOpKernel *k);
+
+/* Run-sum groups (window.c): one launch that computes several run sums of
+ * the same shape (outputs, loop, runs, splits) over what they read, with
+ * optionally
+ *   - the producer of a tensor they read taken in: an elementwise program
+ *     or a window max, computed where the sums load the tensor and stored
+ *     there by the same lane (the sums read every element of it once), and
+ *   - elementwise consumers of the sums' outputs ("tails"), applied by the
+ *     workgroup that combines each output to the value it stores.
+ * Every value is computed by the same operations in the same order as in
+ * the separate launches, so the results are theirs bit for bit. */
+#define WG_MAX_SUMS 4
+#define WG_MAX_TAILS 4
+#define WG_MAX_LEAVES 16
+typedef struct { u32 id, cnt; void *ptr; u64 bytes; } WgBuf;
+typedef struct { u32 nb; WgBuf b[1 + WG_MAX_LEAVES]; } WgBufs;   /* output, then the leaves */
+typedef struct {
+    u32 n_sum, n_tail;
+    const void *sum[WG_MAX_SUMS];        /* the run sums (window.c cache entries) */
+    WgBufs sb[WG_MAX_SUMS];
+    int8_t sub[WG_MAX_SUMS][1 + WG_MAX_LEAVES]; /* per leaf slot: the producer STORE it reads (-1: memory) */
+    int pkind;                           /* producer: 0 none, 1 elementwise program, 2 window max */
+    const ChainInfo *pc;                 /* pkind 1 */
+    const void *pw;                      /* pkind 2: the window max (window.c cache entry) */
+    u64 psig;                            /* the producer's program signature */
+    WgBufs pb;
+    int has_canon;                       /* the index the sums read the producer's tensor at */
+    Aff canon;
+    const UOpKernel *tail[WG_MAX_TAILS]; /* window.c's copies of the consumers' programs */
+    u64 tsig[WG_MAX_TAILS];
+    WgBufs tb[WG_MAX_TAILS];
+    u32 tleaf[WG_MAX_TAILS];             /* the leaf slot (1 + leaf) that takes the value */
+    u8 tsrc[WG_MAX_TAILS];               /* that value: sum s (s < WG_MAX_SUMS) or tail WG_MAX_SUMS + t */
+    /* set by window_group_build */
+    hipFunction_t fn;
+    const CoForm *co;
+    const KGenScalars *psc, *tsc;        /* the producer's and the tails' inline scalars */
+    u32 grid, comb_words;
+    int resident;
+} WinGroup;
+/* a held run sum (window_try_dispatch) as a group of one */
+int  window_group_of_sum(WinGroup *g, const void *we, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves);
+/* an empty group around a held producer (its buffers: output, leaves) */
+int  window_group_of_chain(WinGroup *g, const ChainInfo *pc, const u32 *bufs);
+int  window_group_of_wmax(WinGroup *g, const void *we, u32 out_buf, u32 in_buf);
+/* the run-sum program's single-launch entry (compiled), or NULL */
+const void *window_sum_entry(const UOpKernel *k);
+/* g extended by run sum k / elementwise consumer k; 0: it does not join */
+int  window_group_add_sum(WinGroup *g, const void *we, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves);
+int  window_group_add_tail(WinGroup *g, const UOpKernel *k, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves);
+/* whether the group reads or writes buffer id (writes only: `writes`) */
+int  window_group_uses(const WinGroup *g, u32 id, int writes);
+/* the group's kernel (compiled once per shape): fn, co, grid, comb_words */
+int  window_group_build(WinGroup *g);
+/* its launch parameters (into the caller's storage), their count */
+typedef struct { void *ptr[160]; u32 cnt[160]; u32 sm[1 + WG_MAX_TAILS]; float sv[(1 + WG_MAX_TAILS) * KGEN_MAX_SCALARS]; } WgArgs;
+u32  window_group_params(const WinGroup *g, WgArgs *a, void **params);
+void window_group_mem(const WinGroup *g, HbMem *m);
+/* the leaves of tail t (bit i: leaf i) that are read from memory (must be current on the device) */
+u64  window_group_tail_reads(const WinGroup *g, u32 t);
+/* device-free: the group kernel of programs ks[0..n) over buffer ids (bufs[i]: output, leaves),
+ * the first a producer when `producer` is set; NULL with the reason in err */
+char *window_group_source(const UOpKernel *const *ks, const u32 *const *bufs, u32 n, int producer, char *err,
+                          size_t errlen);
+/* backend.c: the launch just held is a run sum (a group of one) or a window max a run sum may take in */
+void hipb_hold_tag_sum(const void *we, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves);
+void hipb_hold_tag_wmax(const void *we, u32 out_buf, u32 in_buf);
 
 /* ---------------- launch helpers ---------------- */
 int  hipb_launch(hipFunction_t fn, u32 gx, u32 gy, u32 gz, u32 bx, void **params);

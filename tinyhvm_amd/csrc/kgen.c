@@ -1145,30 +1145,55 @@ static int emit_cone_subst(const UOpKernel *k, const u8 *cone, const char *gid_e
     return (int)n;
 }
 
-/* An elementwise program as the epilogue of the kernel that produces one of
- * its leaves: a device function epi_(gid_, v_, p0.., c0..) that computes the
- * program for output gid_ with every load of leaf buffer o_leaf (1 + leaf)
- * taking v_ (the value the producer just stored there, at gid_) and stores
- * the result as the program's STORE does. The program has no loop and one
- * STORE; the caller checks that its loads of o_leaf and its STORE index are
- * gid itself. Buffers are the function's own p<b>/c<b> (0: its output).
- * Returns the length written, or -1. */
-int kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen, KGenScalars *sc) {
-    u8 cone[KOP_MAX];
-    i32 st = -1, scal[KOP_MAX];
-    if (k->n_ops == 0 || k->n_ops > KOP_MAX) return -1;
-    /* loads at a constant index of another leaf: inline scalars */
+/* inline scalars of an elementwise program: its loads at a constant index
+ * of a leaf other than skip_leaf (1 + leaf; ~0u: none) */
+static void find_scalars(const UOpKernel *k, u32 skip_leaf, i32 *scal, KGenScalars *sc) {
     sc->n = 0;
     for (u32 i = 0; i < k->n_ops; i++) {
         const KOp *op = &k->ops[i];
         scal[i] = -1;
-        if (op->type == KOP_LOAD && op->imm.u >= 1 && op->imm.u <= k->n_leaves && op->imm.u != o_leaf &&
+        if (op->type == KOP_LOAD && op->imm.u >= 1 && op->imm.u <= k->n_leaves && op->imm.u != skip_leaf &&
             op->arg[0] < k->n_ops && k->ops[op->arg[0]].type == KOP_CONST_U && sc->n < KGEN_MAX_SCALARS) {
             sc->leaf[sc->n] = op->imm.u - 1;
             sc->index[sc->n] = k->ops[op->arg[0]].imm.u;
             scal[i] = (i32)sc->n++;
         }
     }
+}
+
+static void put_buffer_params(SB *sb, const UOpKernel *k, const KGenScalars *sc) {
+    for (u32 b = 0; b <= k->n_leaves; b++) sb_put(sb, ", char* p%u", b);
+    for (u32 b = 0; b <= k->n_leaves; b++) sb_put(sb, ", u32 c%u", b);
+    if (sc->n) {
+        sb_put(sb, ", u32 sm_");
+        for (u32 j = 0; j < sc->n; j++) sb_put(sb, ", float sv%u", j);
+    }
+}
+
+static int sb_out(SB *sb, char *out, size_t outlen) {
+    if (!sb->p) return -1;
+    const size_t n = strlen(sb->p);
+    if (n + 1 > outlen) { free(sb->p); return -1; }
+    memcpy(out, sb->p, n + 1);
+    free(sb->p);
+    return (int)n;
+}
+
+/* An elementwise program as the epilogue of the kernel that produces one of
+ * its leaves: a device function fname(gid_, v_, p0.., c0..) that computes
+ * the program for output gid_ with every load of leaf buffer o_leaf (1 +
+ * leaf) taking v_ (the value the producer just stored there, at gid_),
+ * stores the result as the program's STORE does and returns the value it
+ * stored (before the conversion of a non-f32 output). The program has no loop
+ * and one STORE; the caller checks that its loads of o_leaf and its STORE
+ * index are gid itself. Buffers are the function's own p<b>/c<b> (0: its
+ * output). Returns the length written, or -1. */
+int kgen_epilogue_fn(const UOpKernel *k, u32 o_leaf, const char *fname, char *out, size_t outlen,
+                     KGenScalars *sc) {
+    u8 cone[KOP_MAX];
+    i32 st = -1, scal[KOP_MAX];
+    if (k->n_ops == 0 || k->n_ops > KOP_MAX) return -1;
+    find_scalars(k, o_leaf, scal, sc);
     for (u32 i = 0; i < k->n_ops; i++) {
         const KOpType t = k->ops[i].type;
         if (t == KOP_RANGE || t == KOP_ENDRANGE || t == KOP_ACC_INIT || t == KOP_ACC) return -1;
@@ -1184,24 +1209,141 @@ int kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen, KGen
     char body[32768];
     if (emit_cone_subst(k, cone, "gid_", "0u", o_leaf, "v_", scal, body, sizeof body) < 0) return -1;
     SB sb = {0};
-    sb_put(&sb, "__device__ __forceinline__ void epi_(u32 gid_, float v_");
-    for (u32 b = 0; b <= k->n_leaves; b++) sb_put(&sb, ", char* p%u", b);
-    for (u32 b = 0; b <= k->n_leaves; b++) sb_put(&sb, ", u32 c%u", b);
-    if (sc->n) {
-        sb_put(&sb, ", u32 sm_");
-        for (u32 j = 0; j < sc->n; j++) sb_put(&sb, ", float sv%u", j);
-    }
+    sb_put(&sb, "__device__ __forceinline__ float %s(u32 gid_, float v_", fname);
+    put_buffer_params(&sb, k, sc);
     const int fv = op_is_float(k->ops[so->arg[1]].type);
     char v[48];
     if (fv) snprintf(v, sizeof v, "f%u", so->arg[1]);
     else snprintf(v, sizeof v, "(float)n%u", so->arg[1]);
-    sb_put(&sb, ") {\n%s  %s(p0, c0, n%u, %s);\n}\n", body, dt_st(k->out_dtype), so->arg[0], v);
-    if (!sb.p) return -1;
-    const size_t n = strlen(sb.p);
-    if (n + 1 > outlen) { free(sb.p); return -1; }
-    memcpy(out, sb.p, n + 1);
-    free(sb.p);
-    return (int)n;
+    sb_put(&sb, ") {\n%s  %s(p0, c0, n%u, %s);\n  return %s;\n}\n", body, dt_st(k->out_dtype), so->arg[0], v, v);
+    return sb_out(&sb, out, outlen);
+}
+
+int kgen_epilogue(const UOpKernel *k, u32 o_leaf, char *out, size_t outlen, KGenScalars *sc) {
+    return kgen_epilogue_fn(k, o_leaf, "epi_", out, outlen, sc);
+}
+
+/* A loop-free elementwise program inlined where its output is read: a
+ * device function fname(gid_, st_, r0_.., p0.., c0..) that computes the
+ * program for gid_, stores each of its STOREs there when st_ is set, and
+ * returns the value of STORE j in *r<j>_ (STOREs in program order). Its
+ * STOREs must all be at gid and it must not load a buffer it stores (the
+ * caller checks both). Returns the length written, or -1. */
+int kgen_producer_fn(const UOpKernel *k, const char *fname, char *out, size_t outlen, KGenScalars *sc) {
+    u8 cone[KOP_MAX];
+    i32 scal[KOP_MAX];
+    u32 st[CHAIN_MAX_STORES], nst = 0;
+    if (k->n_ops == 0 || k->n_ops > KOP_MAX) return -1;
+    find_scalars(k, ~0u, scal, sc);
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        if (op->type == KOP_RANGE || op->type == KOP_ENDRANGE || op->type == KOP_ACC_INIT || op->type == KOP_ACC)
+            return -1;
+        if (op->type == KOP_STORE) {
+            if (nst >= CHAIN_MAX_STORES || op->arg[0] >= k->n_ops || op->arg[1] >= k->n_ops ||
+                op->imm.u > k->n_leaves)
+                return -1;
+            st[nst++] = i;
+        }
+        cone[i] = op->type != KOP_STORE;
+    }
+    if (!nst) return -1;
+    char body[32768];
+    if (emit_cone_subst(k, cone, "gid_", "0u", ~0u, NULL, scal, body, sizeof body) < 0) return -1;
+    SB sb = {0};
+    sb_put(&sb, "__device__ __forceinline__ void %s(u32 gid_, bool st_", fname);
+    for (u32 j = 0; j < nst; j++) sb_put(&sb, ", float* r%u_", j);
+    put_buffer_params(&sb, k, sc);
+    sb_put(&sb, ") {\n%s  if (st_) {\n", body);
+    for (u32 j = 0; j < nst; j++) {
+        const KOp *so = &k->ops[st[j]];
+        const u32 slot = so->imm.u, dt = slot ? k->leaf_dtypes[slot - 1] : k->out_dtype;
+        char v[48];
+        if (op_is_float(k->ops[so->arg[1]].type)) snprintf(v, sizeof v, "f%u", so->arg[1]);
+        else snprintf(v, sizeof v, "(float)n%u", so->arg[1]);
+        sb_put(&sb, "    %s(p%u, c%u, n%u, %s);\n", dt_st(dt), slot, slot, so->arg[0], v);
+    }
+    sb_put(&sb, "  }\n");
+    for (u32 j = 0; j < nst; j++) {
+        const KOp *so = &k->ops[st[j]];
+        if (op_is_float(k->ops[so->arg[1]].type)) sb_put(&sb, "  *r%u_ = f%u;\n", j, so->arg[1]);
+        else sb_put(&sb, "  *r%u_ = (float)n%u;\n", j, so->arg[1]);
+    }
+    sb_put(&sb, "}\n");
+    return sb_out(&sb, out, outlen);
+}
+
+static void plan_inline_scalars(Gen *g, KGenResult *out);
+
+/* kgen_producer_fn for four consecutive gids X0..X0+3 (X0 a multiple of 4,
+ * at most `total` gids): the serial generator's vector form of the program,
+ * so that loads along gid are 16-byte loads and values the four share are
+ * computed once. fname(X0, st_, r0_.., p0.., c0..) stores the STOREs when st_
+ * is set and returns STORE j's four values in *r<j>_ (a float4). */
+int kgen_producer4_fn(const UOpKernel *k, u32 total, const char *fname, char *out, size_t outlen,
+                      KGenScalars *sc) {
+    u32 st[CHAIN_MAX_STORES], nst = 0;
+    char err[128];
+    if (k->n_ops == 0 || k->n_ops > KOP_MAX || total == 0 || !kgen_validate(k, err, sizeof err)) return -1;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        if (op->type == KOP_RANGE || op->type == KOP_ENDRANGE || op->type == KOP_ACC_INIT || op->type == KOP_ACC)
+            return -1;
+        if (op->type == KOP_STORE) {
+            if (nst >= CHAIN_MAX_STORES || op->arg[0] >= k->n_ops || op->arg[1] >= k->n_ops ||
+                op->imm.u > k->n_leaves)
+                return -1;
+            st[nst++] = i;
+        }
+    }
+    if (!nst) return -1;
+    Gen G;
+    memset(&G, 0, sizeof G);
+    G.k = k;
+    G.mode = KG_MODE_SERIAL;
+    G.V = 4;
+    G.total = total;
+    G.block = 256;
+    G.nt = 3;
+    G.oi = calloc(k->n_ops, sizeof(OpI));
+    G.scal = malloc(k->n_ops * sizeof(i32));
+    KGenResult kr;
+    memset(&kr, 0, sizeof kr);
+    if (!G.oi || !G.scal) {
+        free(G.oi);
+        free(G.scal);
+        return -1;
+    }
+    analyze_structure(&G);
+    plan_inline_scalars(&G, &kr);
+    analyze_vector(&G);
+    analyze_global(&G);
+    sc->n = kr.n_scal;
+    for (u32 j = 0; j < kr.n_scal; j++) {
+        sc->leaf[j] = kr.scal_leaf[j];
+        sc->index[j] = kr.scal_index[j];
+    }
+    SB *s = &G.sb;
+    sb_put(s, "__device__ __forceinline__ void %s(u32 X0, bool st_", fname);
+    for (u32 j = 0; j < nst; j++) sb_put(s, ", float4* r%u_", j);
+    put_buffer_params(s, k, sc);
+    sb_put(s, ") {\n  const u32 TOTAL = %uu;\n", total);
+    emit_decls(&G);
+    for (u32 i = 0; i < k->n_ops; i++)
+        if (k->ops[i].type != KOP_STORE) emit_op(&G, i, 0, 0);
+    sb_put(s, "  if (st_) {\n");
+    for (u32 j = 0; j < nst; j++) emit_op(&G, st[j], 0, 0);
+    sb_put(s, "  }\n");
+    for (u32 j = 0; j < nst; j++) {
+        const u32 val = k->ops[st[j]].arg[1];
+        char a[4][128];
+        for (u32 v = 0; v < 4; v++) Fx(&G, val, v, a[v]);
+        sb_put(s, "  *r%u_ = make_float4(%s, %s, %s, %s);\n", j, a[0], a[1], a[2], a[3]);
+    }
+    sb_put(s, "}\n");
+    free(G.oi);
+    free(G.scal);
+    return sb_out(s, out, outlen);
 }
 
 static void emit_params(Gen *g) {

@@ -426,6 +426,7 @@ int co_form_make(CoForm *cf, const char *src, const char *name, u32 threads, hip
         int v = 0;
         if (hipFuncGetAttribute(&v, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, fn) != hipSuccess || v < 0) goto fail_src;
         cf->lds = (u32)v;
+        cf->cap_waves = rtc_capacity(fn, threads) * (threads / 64u);
     }
     return 1;
 fail_src:

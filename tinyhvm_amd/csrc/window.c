@@ -577,6 +577,8 @@ typedef struct {
     hipModule_t mod;
     hipFunction_t fn, fn_fin;
     CoForm co;                   /* the main kernel's co-launch form (one-launch plans) */
+    u32 cov_n[WIN_MAX_LOADS];    /* run sums: the tensor size each load was checked to tile (0: not yet) */
+    u8 cov_ok[WIN_MAX_LOADS];    /* ... and the answer */
 } WinEntry;
 
 static Scratch win_ws;   /* run-sum partials of the combine-kernel form */
@@ -642,6 +644,8 @@ static u64 win_key(const UOpKernel *k) {
     return key ? key : 1;
 }
 
+static u64 win_key_of(const WinEntry *e) { return e->key; }
+
 int window_analyze(const UOpKernel *k, u32 *kind, u32 *splits) {
     WinPlan p;
     if (!k || !win_recognize(k, &p)) {
@@ -672,55 +676,62 @@ void window_note_plain(const UOpKernel *k) {
     win_insert(key, k);
 }
 
-int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
-    if (k->n_leaves > FUSE_MAX_LEAVES) return 0;
+/* The program's entry: looked up, or recognised and compiled on first
+ * sight (kind WIN_NONE: a program this file does not take). NULL only when
+ * no entry could be made. */
+static WinEntry *win_entry(const UOpKernel *k) {
+    if (k->n_leaves > FUSE_MAX_LEAVES) return NULL;
     u64 key = win_key(k);
     WinEntry *e = win_lookup(key, k);
-    if (!e && hipb.noalloc) {
+    if (e) return e;
+    if (hipb.noalloc) {
         hipb.noalloc_err = THVM_HIP_ENOTREADY;   /* never compiles without allocating */
-        return 0;
+        return NULL;
     }
-    if (!e) {
-        e = win_insert(key, k);
-        if (!e) return 0;
-        if (!win_recognize(k, &e->plan)) return 0;    /* kind stays WIN_NONE */
-        char name[48], err[256] = {0};
-    build:;
-        char *src = gen_window(k, &e->plan, name, sizeof name);
-        if (!src) return 0;
-        if (hipb.dump_src) fprintf(stderr, "---- window kernel ----\n%s\n", src);
-        if (!rtc_build_module(src, &e->mod, err, sizeof err)) {
-            fprintf(stderr, "tinyhvm-hip: window kernel build failed: %s\n", err);
-            free(src);
-            return 0;
-        }
-        char fin[64];
-        snprintf(fin, sizeof fin, "%s_fin", name);
-        if (hipModuleGetFunction(&e->fn, e->mod, name) != hipSuccess ||
-            (e->plan.kind == WIN_SUM && e->plan.S > 1 && e->plan.launch &&
-             hipModuleGetFunction(&e->fn_fin, e->mod, fin) != hipSuccess)) {
-            HIPB_CHECK(hipModuleUnload(e->mod));
-            free(src);
-            return 0;
-        }
-        /* one pass only if the whole grid is on the GPU at once with this
-         * kernel's own occupancy; else partials go to a combine kernel */
-        if (e->plan.kind == WIN_SUM && e->plan.S > 1 && !e->plan.launch &&
-            (u64)e->plan.total * e->plan.S > rtc_capacity(e->fn, WIN_BLOCK)) {
-            HIPB_CHECK(hipModuleUnload(e->mod));
-            free(src);
-            e->plan.launch = 1;
-            goto build;
-        }
-        if (!(e->plan.kind == WIN_SUM && e->plan.S > 1 && e->plan.launch))
-            co_form_make(&e->co, src, name, WIN_BLOCK, e->fn);
+    e = win_insert(key, k);
+    if (!e) return NULL;
+    if (!win_recognize(k, &e->plan)) return e;    /* kind stays WIN_NONE */
+    char name[48], err[256] = {0};
+build:;
+    char *src = gen_window(k, &e->plan, name, sizeof name);
+    if (!src) return e;
+    if (hipb.dump_src) fprintf(stderr, "---- window kernel ----\n%s\n", src);
+    if (!rtc_build_module(src, &e->mod, err, sizeof err)) {
+        fprintf(stderr, "tinyhvm-hip: window kernel build failed: %s\n", err);
         free(src);
-        e->kind = e->plan.kind;
-        if (hipb.verbose)
-            fprintf(stderr, "tinyhvm-hip: %s outputs=%u trip=%u W=%u run=%u splits=%u\n", name, e->plan.total,
-                    e->plan.trip, e->plan.W, e->plan.L, e->plan.S);
+        return e;
     }
-    if (e->kind == WIN_NONE) return 0;
+    char fin[64];
+    snprintf(fin, sizeof fin, "%s_fin", name);
+    if (hipModuleGetFunction(&e->fn, e->mod, name) != hipSuccess ||
+        (e->plan.kind == WIN_SUM && e->plan.S > 1 && e->plan.launch &&
+         hipModuleGetFunction(&e->fn_fin, e->mod, fin) != hipSuccess)) {
+        HIPB_CHECK(hipModuleUnload(e->mod));
+        free(src);
+        return e;
+    }
+    /* one pass only if the whole grid is on the GPU at once with this
+     * kernel's own occupancy; else partials go to a combine kernel */
+    if (e->plan.kind == WIN_SUM && e->plan.S > 1 && !e->plan.launch &&
+        (u64)e->plan.total * e->plan.S > rtc_capacity(e->fn, WIN_BLOCK)) {
+        HIPB_CHECK(hipModuleUnload(e->mod));
+        free(src);
+        e->plan.launch = 1;
+        goto build;
+    }
+    if (!(e->plan.kind == WIN_SUM && e->plan.S > 1 && e->plan.launch))
+        co_form_make(&e->co, src, name, WIN_BLOCK, e->fn);
+    free(src);
+    e->kind = e->plan.kind;
+    if (hipb.verbose)
+        fprintf(stderr, "tinyhvm-hip: %s outputs=%u trip=%u W=%u run=%u splits=%u\n", name, e->plan.total,
+                e->plan.trip, e->plan.W, e->plan.L, e->plan.S);
+    return e;
+}
+
+int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UOpKernel *k) {
+    WinEntry *e = win_entry(k);
+    if (!e || e->kind == WIN_NONE) return 0;
     const WinPlan *p = &e->plan;
     /* buffers: every index the plan forms is inside them, vector loads aligned */
     void *ptrs[FUSE_MAX_LEAVES + 1];
@@ -759,7 +770,11 @@ int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
         hm.n = 0;
         hbm_add(&hm, ptrs[0], pool_bytes(out_buf), 1);
         hbm_add(&hm, ptrs[bi], pool_bytes(leaf_bufs[bi - 1]), 0);
-        if (hipb_hold(&e->co, e->fn, gx, gy, params, &hm, 0, -1, 0)) return 1;
+        if (hipb_hold(&e->co, e->fn, gx, gy, params, &hm, 0, -1, 0) ||
+            (gy == 1 && hipb_hold_large(&e->co, e->fn, gx, gy, params, &hm, 0, -1, 0))) {
+            hipb_hold_tag_wmax(e, out_buf, leaf_bufs[bi - 1]);
+            return 1;
+        }
         if (!hipb_launch(e->fn, gx, gy, 1, WIN_BLOCK, params)) return 0;
     } else {
         void *params[FUSE_MAX_LEAVES + 3];
@@ -776,8 +791,12 @@ int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
             for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++)
                 hbm_add(&hm, pool_ptr(leaf_bufs[i]), pool_bytes(leaf_bufs[i]), 0);
             if (hipb_hold(&e->co, e->fn, p->total * p->S, 1, params, &hm, p->S > 1, (int)(np - 1),
-                          (u64)p->total * p->S))
+                          (u64)p->total * p->S) ||
+                hipb_hold_large(&e->co, e->fn, p->total * p->S, 1, params, &hm, p->S > 1, (int)(np - 1),
+                                (u64)p->total * p->S)) {
+                hipb_hold_tag_sum(e, out_buf, leaf_bufs, n_leaves);
                 return 1;
+            }
         }
         if (!hipb_launch(e->fn, p->total * p->S, 1, 1, WIN_BLOCK, params)) return 0;
         if (ws) {
@@ -786,6 +805,906 @@ int window_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const U
         }
     }
     return 1;
+}
+
+/* ---------------- run-sum groups ---------------- */
+
+/* The generated group kernels, one per shape (the key names the programs
+ * and which of their loads take the producer's values); fn NULL: refused. */
+#define WG_CACHE 128
+typedef struct {
+    u64 key;
+    hipModule_t mod;
+    hipFunction_t fn;
+    CoForm co;
+    KGenScalars psc, tsc[WG_MAX_TAILS];
+    u32 cap;                     /* workgroups resident at once */
+} WgEntry;
+static struct {
+    WgEntry e[WG_CACHE];
+    u32 n;
+    UOpKernel *tail[64];         /* the consumers' programs (copies, by signature) */
+    u64 tail_sig[64];
+    u32 n_tail;
+} WGC;
+
+static u64 wg_mix(u64 h, u64 v) {
+    h ^= v + 0x9E3779B97F4A7C15ull + (h << 6) + (h >> 2);
+    h *= 0xFF51AFD7ED558CCDull;
+    return h ^ (h >> 33);
+}
+
+static u32 launch_total_of(const UOpKernel *k) {
+    return k->local_size > 0 ? k->grid[0] : k->grid[0] * k->grid[1] * k->grid[2];
+}
+
+/* a cached entry's program as a UOpKernel (heap) */
+static UOpKernel *win_kernel(const WinEntry *e) {
+    UOpKernel *k = calloc(1, sizeof *k);
+    if (!k) return NULL;
+    memcpy(k->ops, e->ops, (size_t)e->n_ops * sizeof(KOp));
+    k->n_ops = e->n_ops;
+    k->n_leaves = e->n_leaves;
+    k->n_bufs = e->n_leaves + 1;
+    k->grid[0] = e->meta[0]; k->grid[1] = e->meta[1]; k->grid[2] = e->meta[2];
+    k->local_size = e->meta[3];
+    k->out_dtype = e->meta[4];
+    memcpy(k->leaf_dtypes, e->dts, (size_t)e->n_leaves * sizeof(u32));
+    return k;
+}
+
+static UOpKernel *chain_kernel(const ChainInfo *c) {
+    UOpKernel *k = calloc(1, sizeof *k);
+    if (!k) return NULL;
+    memcpy(k->ops, c->ops, (size_t)c->n_ops * sizeof(KOp));
+    k->n_ops = c->n_ops;
+    k->n_leaves = c->n_leaves;
+    k->n_bufs = c->n_leaves + 1;
+    memcpy(k->grid, c->grid, sizeof k->grid);
+    k->out_dtype = c->out_dtype;
+    memcpy(k->leaf_dtypes, c->leaf_dtypes, sizeof c->leaf_dtypes);
+    return k;
+}
+
+static int aff_same(const Aff *a, const Aff *b) {
+    if (!a->ok || !b->ok || a->cst != b->cst || a->n != b->n) return 0;
+    for (u32 t = 0; t < a->n; t++) {
+        int found = 0;
+        for (u32 u = 0; u < b->n && !found; u++)
+            found = a->d[t].var == b->d[u].var && a->d[t].div == b->d[u].div && a->d[t].mod == b->d[u].mod &&
+                    a->coef[t] == b->coef[u];
+        if (!found) return 0;
+    }
+    return 1;
+}
+
+/* whether the run sum's load at `a` reads each element of [0, n) exactly
+ * once over the launch: its runs, laid out for every output and outer
+ * digit, tile the tensor (checked by marking them) */
+static int wg_covers(const WinPlan *p, const Aff *a, u32 n) {
+    if ((u64)p->total * p->trip != n) return 0;
+    u8 *seen = calloc(n, 1);
+    if (!seen) return 0;
+    int ok = 1;
+    const u32 runs = p->trip / p->L;
+    for (u32 g = 0; g < p->total && ok; g++)
+        for (u32 r = 0; r < runs && ok; r++) {
+            const u64 st = aff_eval(a, g, r * p->L);
+            if (st + p->L > n) { ok = 0; break; }
+            for (u32 j = 0; j < p->L && ok; j++) ok = !seen[st + j]++;
+        }
+    free(seen);
+    return ok;
+}
+
+static void wg_buf(WgBuf *b, u32 id, u32 dtype) {
+    b->id = id;
+    b->ptr = id ? pool_ptr(id) : NULL;
+    b->bytes = id ? pool_bytes(id) : 0;
+    b->cnt = (u32)(b->bytes / (dtype == DTYPE_F16 ? 2u : 4u));
+}
+
+static void wg_bufs(WgBufs *w, u32 out, u32 out_dt, const u32 *leaves, const u32 *dts, u32 nl) {
+    w->nb = nl + 1;
+    wg_buf(&w->b[0], out, out_dt);
+    for (u32 i = 0; i < nl; i++) wg_buf(&w->b[i + 1], leaves[i], dts[i]);
+}
+
+/* same buffer: the id and, where the device is up, the memory */
+static int wg_is(const WgBuf *b, u32 id) { return b->id && b->id == id && (!b->ptr || b->ptr == pool_ptr(id)); }
+
+int window_group_uses(const WinGroup *g, u32 id, int writes) {
+    if (!id) return 0;
+    for (u32 s = 0; s < g->n_sum; s++)
+        for (u32 b = 0; b < (writes ? 1u : g->sb[s].nb); b++)
+            if (wg_is(&g->sb[s].b[b], id)) return 1;
+    for (u32 t = 0; t < g->n_tail; t++)
+        for (u32 b = 0; b < (writes ? 1u : g->tb[t].nb); b++)
+            if (wg_is(&g->tb[t].b[b], id)) return 1;
+    if (g->pkind == 1) {
+        for (u32 b = 0; b < g->pb.nb; b++) {
+            int st = 0;
+            for (u32 j = 0; j < g->pc->n_st; j++) st |= g->pc->st_slot[j] == b;
+            if ((!writes || st) && wg_is(&g->pb.b[b], id)) return 1;
+        }
+    } else if (g->pkind == 2) {
+        if (wg_is(&g->pb.b[0], id) || (!writes && wg_is(&g->pb.b[1], id))) return 1;
+    }
+    return 0;
+}
+
+/* the producer STORE whose buffer id is (-1: none) */
+static int wg_prod_store(const WinGroup *g, u32 id) {
+    if (g->pkind == 1) {
+        for (u32 j = 0; j < g->pc->n_st; j++)
+            if (wg_is(&g->pb.b[g->pc->st_slot[j]], id)) return (int)j;
+    } else if (g->pkind == 2 && wg_is(&g->pb.b[0], id)) {
+        return 0;
+    }
+    return -1;
+}
+
+static u32 wg_prod_total(const WinGroup *g) {
+    return g->pkind == 1 ? g->pc->total : g->pkind == 2 ? ((const WinEntry *)g->pw)->plan.total : 0;
+}
+
+static int wg_same_shape(const WinPlan *a, const WinPlan *b) {
+    if (a->total != b->total || a->trip != b->trip || a->L != b->L || a->W != b->W || a->S != b->S ||
+        a->unroll != b->unroll || a->launch != b->launch || a->n_outer != b->n_outer)
+        return 0;
+    for (u32 q = 0; q < a->n_outer; q++)
+        if (a->outer_div[q] != b->outer_div[q] || a->outer_mod[q] != b->outer_mod[q] ||
+            a->outer_coef[q] != b->outer_coef[q])
+            return 0;
+    return 1;
+}
+
+static void wg_clear(WinGroup *g) { memset(g, 0, sizeof *g); }
+
+const void *window_sum_entry(const UOpKernel *k) {
+    if (!k || k->n_leaves > WG_MAX_LEAVES) return NULL;
+    const WinEntry *e = win_entry(k);
+    if (!e || e->kind != WIN_SUM || (e->plan.S > 1 && e->plan.launch)) return NULL;
+    return e;
+}
+
+/* The checks window_try_dispatch makes before a launch: every index a
+ * memory load forms inside its buffer, vector loads aligned, the output
+ * large enough (a load the producer's value replaces reads no memory). */
+static int wg_sum_fits(const WinEntry *e, const int8_t *sub, u32 out_buf, const u32 *leaf_bufs) {
+    const WinPlan *p = &e->plan;
+    if (!pool_ptr(out_buf)) return 1;   /* no device: a source check */
+    if (pool_bytes(out_buf) / 4 < p->total) return 0;
+    for (u32 j = 0; j < p->n_ld; j++) {
+        const u32 bi = e->ops[p->ld_op[j]].imm.u;
+        if (sub[bi] >= 0) continue;
+        const void *lp = pool_ptr(leaf_bufs[bi - 1]);
+        if (!lp || p->ld_max[j] >= pool_bytes(leaf_bufs[bi - 1]) / 4) return 0;
+        if (p->ld_r[j] && ((uintptr_t)lp & (4u * p->W - 1u))) return 0;
+    }
+    return 1;
+}
+
+int window_group_add_sum(WinGroup *g, const void *we, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves) {
+    const WinEntry *e = we;
+    if (!e || e->kind != WIN_SUM || g->n_sum >= WG_MAX_SUMS || e->n_leaves > WG_MAX_LEAVES ||
+        n_leaves < e->n_leaves || (e->plan.S > 1 && e->plan.launch) || !out_buf)
+        return 0;
+    const WinPlan *p = &e->plan;
+    if (g->n_sum && !wg_same_shape(&((const WinEntry *)g->sum[0])->plan, p)) return 0;
+    if (g->n_tail) return 0;     /* consumers run after every sum's combine: sums first */
+    if (window_group_uses(g, out_buf, 0)) return 0;
+    for (u32 i = 0; i < e->n_leaves; i++)
+        if (leaf_bufs[i] == out_buf) return 0;
+    const u32 s = g->n_sum;
+    int reads = 0;
+    for (u32 b = 1; b <= e->n_leaves; b++) {
+        const u32 id = leaf_bufs[b - 1];
+        const int K = g->pkind ? wg_prod_store(g, id) : -1;
+        g->sub[s][b] = (int8_t)K;
+        if (K < 0) {
+            if (window_group_uses(g, id, 1)) return 0;   /* another output of the group */
+            continue;
+        }
+        if (g->pkind == 1 && !g->pc->st_f32[K]) return 0;
+        /* every load of it: along r, at the index the group reads the tensor at */
+        for (u32 j = 0; j < p->n_ld; j++) {
+            if (e->ops[p->ld_op[j]].imm.u != b) continue;
+            if (!p->ld_r[j]) return 0;
+            if (!g->has_canon) {
+                const u32 pn = wg_prod_total(g);
+                WinEntry *me = (WinEntry *)e;
+                if (me->cov_n[j] != pn) {   /* checked once per load and size */
+                    me->cov_ok[j] = (u8)wg_covers(p, &p->ld_aff[j], pn);
+                    me->cov_n[j] = pn;
+                }
+                if (!me->cov_ok[j]) return 0;
+                g->canon = p->ld_aff[j];
+                g->has_canon = 1;
+            } else if (!aff_same(&g->canon, &p->ld_aff[j])) {
+                return 0;
+            }
+            reads = 1;
+        }
+    }
+    if (g->pkind && s == 0 && !reads) return 0;
+    if (!wg_sum_fits(e, g->sub[s], out_buf, leaf_bufs)) return 0;
+    g->sum[s] = e;
+    wg_bufs(&g->sb[s], out_buf, e->meta[4], leaf_bufs, e->dts, e->n_leaves);
+    g->n_sum++;
+    return 1;
+}
+
+int window_group_of_sum(WinGroup *g, const void *we, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves) {
+    wg_clear(g);
+    return window_group_add_sum(g, we, out_buf, leaf_bufs, n_leaves);
+}
+
+int window_group_of_chain(WinGroup *g, const ChainInfo *pc, const u32 *bufs) {
+    wg_clear(g);
+    if (!pc || pc->n_leaves > WG_MAX_LEAVES || pc->n_ops > KOP_MAX) return 0;
+    /* loop-free, and reads no buffer it stores */
+    for (u32 i = 0; i < pc->n_ops; i++) {
+        const KOp *op = &pc->ops[i];
+        if (op->type == KOP_RANGE || op->type == KOP_ACC) return 0;
+        if (op->type == KOP_LOAD)
+            for (u32 j = 0; j < pc->n_st; j++)
+                if (op->imm.u == pc->st_slot[j] || (op->imm.u <= pc->n_leaves && bufs[op->imm.u] &&
+                                                    bufs[op->imm.u] == bufs[pc->st_slot[j]]))
+                    return 0;
+    }
+    g->pkind = 1;
+    g->pc = pc;
+    UOpKernel *k = chain_kernel(pc);
+    if (!k) return 0;
+    g->psig = uop_signature(k);
+    free(k);
+    wg_bufs(&g->pb, bufs[0], pc->out_dtype, bufs + 1, pc->leaf_dtypes, pc->n_leaves);
+    return 1;
+}
+
+int window_group_of_wmax(WinGroup *g, const void *we, u32 out_buf, u32 in_buf) {
+    wg_clear(g);
+    const WinEntry *e = we;
+    if (!e || e->kind != WIN_MAX || !out_buf || !in_buf || out_buf == in_buf) return 0;
+    /* its loads (one element at a time here) and stores inside the buffers */
+    if (pool_ptr(out_buf) && (pool_bytes(out_buf) / 4 < e->plan.total || !pool_ptr(in_buf) ||
+                              e->plan.ld_max[0] >= pool_bytes(in_buf) / 4))
+        return 0;
+    g->pkind = 2;
+    g->pw = e;
+    g->psig = win_key_of(e);
+    const u32 dts[1] = {DTYPE_F32};
+    wg_bufs(&g->pb, out_buf, DTYPE_F32, &in_buf, dts, 1);
+    return 1;
+}
+
+static const UOpKernel *wg_tail_copy(const UOpKernel *k, u64 sig) {
+    for (u32 i = 0; i < WGC.n_tail; i++)
+        if (WGC.tail_sig[i] == sig && WGC.tail[i]->n_ops == k->n_ops &&
+            memcmp(WGC.tail[i]->ops, k->ops, (size_t)k->n_ops * sizeof(KOp)) == 0)
+            return WGC.tail[i];
+    if (WGC.n_tail >= 64) return NULL;
+    UOpKernel *c = malloc(sizeof *c);
+    if (!c) return NULL;
+    memcpy(c, k, sizeof *c);
+    WGC.tail[WGC.n_tail] = c;
+    WGC.tail_sig[WGC.n_tail++] = sig;
+    return c;
+}
+
+int window_group_add_tail(WinGroup *g, const UOpKernel *k, u32 out_buf, const u32 *leaf_bufs, u32 n_leaves) {
+    if (!g->n_sum || g->n_tail >= WG_MAX_TAILS || !k || k->n_leaves == 0 || k->n_leaves > WG_MAX_LEAVES ||
+        n_leaves < k->n_leaves || k->out_dtype != DTYPE_F32 || k->n_ops == 0 || k->n_ops > KOP_MAX || !out_buf)
+        return 0;
+    const u32 total = ((const WinEntry *)g->sum[0])->plan.total;
+    if (launch_total_of(k) != total || window_group_uses(g, out_buf, 0)) return 0;
+    /* the one leaf slot that holds a value of the group */
+    u32 slot = 0;
+    int src = -1;
+    for (u32 b = 1; b <= k->n_leaves; b++) {
+        const u32 id = leaf_bufs[b - 1];
+        if (id == out_buf) return 0;
+        int v = -1;
+        for (u32 s = 0; s < g->n_sum && v < 0; s++)
+            if (wg_is(&g->sb[s].b[0], id)) v = (int)s;
+        for (u32 t = 0; t < g->n_tail && v < 0; t++)
+            if (wg_is(&g->tb[t].b[0], id)) v = WG_MAX_SUMS + (int)t;
+        if (v >= 0) {
+            if (slot) return 0;
+            slot = b;
+            src = v;
+        } else if (window_group_uses(g, id, 1)) {
+            return 0;
+        }
+    }
+    if (!slot) return 0;
+    /* loop-free, one STORE, loads of that slot and the STORE at gid */
+    Aff *aff = calloc(k->n_ops, sizeof(Aff));
+    if (!aff) return 0;
+    DCtx dc = {k, total, 1, -1, aff};
+    analyze_aff(&dc);
+    int ok = 1, stores = 0;
+    for (u32 i = 0; i < k->n_ops && ok; i++) {
+        const KOp *op = &k->ops[i];
+        if (op->type == KOP_RANGE || op->type == KOP_ENDRANGE || op->type == KOP_ACC_INIT || op->type == KOP_ACC)
+            ok = 0;
+        else if (op->type == KOP_STORE)
+            ok = stores++ == 0 && op->imm.u == 0 && op->arg[0] < k->n_ops && aff_is_gid(&dc, &aff[op->arg[0]]) &&
+                 op->arg[1] < k->n_ops && op_type_is_float(k->ops[op->arg[1]].type);
+        else if (op->type == KOP_LOAD && op->imm.u == slot)
+            ok = op->arg[0] < k->n_ops && aff_is_gid(&dc, &aff[op->arg[0]]);
+        else if (op->type == KOP_LOAD && op->imm.u == 0)
+            ok = 0;
+    }
+    free(aff);
+    if (!ok || stores != 1 || k->leaf_dtypes[slot - 1] != DTYPE_F32) return 0;
+    const u64 sig = uop_signature(k);
+    const UOpKernel *c = wg_tail_copy(k, sig);
+    if (!c) return 0;
+    const u32 t = g->n_tail;
+    g->tail[t] = c;
+    g->tsig[t] = sig;
+    g->tleaf[t] = slot;
+    g->tsrc[t] = (u8)src;
+    wg_bufs(&g->tb[t], out_buf, k->out_dtype, leaf_bufs, k->leaf_dtypes, k->n_leaves);
+    g->n_tail++;
+    return 1;
+}
+
+static u64 wg_key(const WinGroup *g) {
+    u64 h = wg_mix(0x5347524F5550ull, ((u64)g->n_sum << 8) | ((u64)g->n_tail << 4) | (u64)g->pkind);
+    for (u32 s = 0; s < g->n_sum; s++) {
+        const WinEntry *e = g->sum[s];
+        h = wg_mix(h, e->key);
+        for (u32 b = 1; b <= e->n_leaves; b++) h = wg_mix(h, (u64)(u8)g->sub[s][b]);
+    }
+    if (g->pkind) {
+        h = wg_mix(h, g->psig);
+        for (u32 q = 0; q < g->canon.n; q++)
+            h = wg_mix(h, ((u64)g->canon.d[q].var << 60) ^ ((u64)g->canon.d[q].div << 32) ^ g->canon.coef[q] ^
+                              ((u64)g->canon.d[q].mod << 16));
+        h = wg_mix(h, g->canon.cst);
+    }
+    for (u32 t = 0; t < g->n_tail; t++) h = wg_mix(wg_mix(h, g->tsig[t]), ((u64)g->tleaf[t] << 8) | g->tsrc[t]);
+    return h ? h : 1;
+}
+
+/* the sum whose combine a value (sum s, or tail WG_MAX_SUMS + t) belongs to */
+static u32 wg_root(const WinGroup *g, u32 v) {
+    while (v >= WG_MAX_SUMS) v = g->tsrc[v - WG_MAX_SUMS];
+    return v;
+}
+
+/* body op i of member m for component v (loads were emitted before) */
+static void emit_member_op(WSB *s, const UOpKernel *k, u32 m, u32 i, u32 v) {
+    const KOp *op = &k->ops[i];
+    char a[64], b[64], x[256], fb[64];
+    switch (op->type) {
+    case KOP_CONST_F:
+        float_bits(fb, sizeof fb, op->imm.u);
+        wsb_put(s, "    const float m%u_f%u_%u = %s;\n", m, i, v, fb);
+        break;
+    case KOP_ALU:
+        snprintf(a, sizeof a, "m%u_f%u_%u", m, op->arg[0], v);
+        snprintf(b, sizeof b, "m%u_f%u_%u", m, alu_unary(op->imm.u) ? op->arg[0] : op->arg[1], v);
+        kgen_alu_expr(op->imm.u, op->arg[2], a, b, x, sizeof x);
+        wsb_put(s, "    const float m%u_f%u_%u = %s;\n", m, i, v, x);
+        break;
+    default:
+        break;
+    }
+}
+
+/* A window-max producer read four outputs at a time as two of its pairs:
+ * the plan pairs adjacent outputs in 16-byte vectors, and its input is
+ * aligned for them and holds every element they read. */
+static int wg_wmax_vec(const WinGroup *g) {
+    const WinEntry *e = g->pw;
+    if (g->pkind != 2 || !e || e->plan.P != 2 || e->plan.W != 4) return 0;
+    if (!g->pb.b[1].ptr) return 1;    /* no device: a source check */
+    return ((uintptr_t)g->pb.b[1].ptr & 15u) == 0 && ((uintptr_t)g->pb.b[0].ptr & 15u) == 0 &&
+           e->plan.cover_max < g->pb.b[1].bytes / 4;
+}
+
+/* The group's kernel source: the run sums' loop (their shared geometry),
+ * each sum's body in its own names, the producer's device function called
+ * once per element at the group's index, each sum's combine, and the tails
+ * in the lane that stores the sum. */
+static char *gen_group(const WinGroup *g, const char *name, u32 unroll, KGenScalars *psc, KGenScalars *tsc,
+                       char *err, size_t errlen) {
+    const WinEntry *e0 = g->sum[0];
+    const WinPlan *p = &e0->plan;
+    const u32 W = p->W, L4 = p->L / W, units = p->trip / W, S = p->S, total = p->total;
+    const u32 chunk = (units + S - 1) / S;
+    const u32 nit = (chunk + WIN_BLOCK - 1) / WIN_BLOCK;
+    const int fixed = nit <= WIN_SUM_MAX_FIXED;
+    UOpKernel *ks[WG_MAX_SUMS] = {0}, *pk = NULL;
+    char *fnbuf = malloc(65536);
+    WSB s = {0};
+    int ok = fnbuf != NULL;
+    for (u32 m = 0; m < g->n_sum && ok; m++) ok = (ks[m] = win_kernel(g->sum[m])) != NULL;
+    u32 nst = 0;
+    memset(psc, 0, sizeof *psc);
+    if (ok) wsb_put(&s, "%s\n", kgen_prelude());
+    /* four consecutive elements per call */
+    const int vec_prod = (g->pkind == 1 || (g->pkind == 2 && wg_wmax_vec(g))) && W == 4;
+    if (ok && g->pkind == 1) {
+        nst = g->pc->n_st;
+        ok = (pk = chain_kernel(g->pc)) != NULL &&
+             (vec_prod ? kgen_producer4_fn(pk, g->pc->total, "prod_", fnbuf, 65536, psc)
+                       : kgen_producer_fn(pk, "prod_", fnbuf, 65536, psc)) >= 0;
+        if (ok) wsb_put(&s, "%s", fnbuf);
+        else snprintf(err, errlen, "producer generation failed");
+    } else if (ok && g->pkind == 2 && W == 4 && wg_wmax_vec(g)) {
+        /* four adjacent outputs as two pairs, each pair's window rows read
+         * as 16-byte vectors (the window-max kernel's loads), the maximum in
+         * the engine's order */
+        const WinPlan *w = &((const WinEntry *)g->pw)->plan;
+        u32 groups[WIN_MAX_TRIP], ng = 0;
+        for (u32 r = 0; r < w->trip; r++) {
+            u32 gq = w->off[r] / 4, seen = 0;
+            for (u32 x = 0; x < ng; x++) seen |= groups[x] == gq;
+            if (!seen) groups[ng++] = gq;
+        }
+        char fb[64];
+        nst = 1;
+        float_bits(fb, sizeof fb, w->init_bits);
+        wsb_put(&s, "__device__ __forceinline__ void prod_(u32 X0, bool st_, float4* r0_, char* p0, const char* p1) {\n"
+                    "  float a_[4];\n");
+        for (u32 q = 0; q < 2; q++) {
+            char gx[32];
+            snprintf(gx, sizeof gx, "(X0 + %uu)", 2 * q);
+            wsb_put(&s, "  {\n    const u32 b_ = ");
+            emit_base_expr(&s, &w->ld_aff[0], gx);
+            wsb_put(&s, ";\n");
+            for (u32 x = 0; x < ng; x++)
+                wsb_put(&s, "    const v4f_ v%u_ = __builtin_nontemporal_load((const v4f_*)((const float*)p1 + b_ + %uu));\n",
+                        x, groups[x] * 4);
+            for (u32 t = 0; t < 2; t++) {
+                wsb_put(&s, "    a_[%u] = %s;\n", 2 * q + t, fb);
+                for (u32 r = 0; r < w->trip; r++) {
+                    u32 x = 0;
+                    while (groups[x] != w->off[r] / 4) x++;
+                    wsb_put(&s, "    { const float e_ = v%u_.%c; a_[%u] = (a_[%u] > e_) ? a_[%u] : e_; }\n", x,
+                            "xyzw"[(w->off[r] + t * w->c1) % 4], 2 * q + t, 2 * q + t, 2 * q + t);
+                }
+            }
+            wsb_put(&s, "  }\n");
+        }
+        wsb_put(&s, "  if (st_) {\n    *(float2*)((float*)p0 + X0) = make_float2(a_[0], a_[1]);\n"
+                    "    *(float2*)((float*)p0 + X0 + 2u) = make_float2(a_[2], a_[3]);\n  }\n"
+                    "  *r0_ = make_float4(a_[0], a_[1], a_[2], a_[3]);\n}\n");
+    } else if (ok && g->pkind == 2) {
+        const WinPlan *w = &((const WinEntry *)g->pw)->plan;
+        char fb[64];
+        nst = 1;
+        float_bits(fb, sizeof fb, w->init_bits);
+        wsb_put(&s, "__device__ __forceinline__ void prod_(u32 gid_, bool st_, float* r0_, char* p0, const char* p1) {\n"
+                    "  const u32 b_ = ");
+        emit_base_expr(&s, &w->ld_aff[0], "gid_");
+        wsb_put(&s, ";\n  float a_ = %s;\n", fb);
+        for (u32 r = 0; r < w->trip; r++)
+            wsb_put(&s, "  { const float e_ = ((const float*)p1)[b_ + %uu]; a_ = (a_ > e_) ? a_ : e_; }\n", w->off[r]);
+        wsb_put(&s, "  if (st_) ((float*)p0)[gid_] = a_;\n  *r0_ = a_;\n}\n");
+    }
+    for (u32 t = 0; t < g->n_tail && ok; t++) {
+        char fname[16];
+        snprintf(fname, sizeof fname, "tl%u_", t);
+        ok = kgen_epilogue_fn(g->tail[t], g->tleaf[t], fname, fnbuf, 65536, &tsc[t]) >= 0;
+        if (ok) wsb_put(&s, "%s", fnbuf);
+        else snprintf(err, errlen, "consumer generation failed");
+    }
+    if (!ok) goto out;
+    /* parameters */
+    wsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", WIN_BLOCK, name);
+    for (u32 m = 0; m < g->n_sum; m++)
+        for (u32 b = 0; b <= ks[m]->n_leaves; b++)
+            wsb_put(&s, "%s%s m%u_p%u", m || b ? ", " : "", b ? "const char*" : "char*", m, b);
+    if (g->pkind == 1) {
+        for (u32 b = 0; b <= pk->n_leaves; b++) wsb_put(&s, ", char* g_p%u", b);
+        for (u32 b = 0; b <= pk->n_leaves; b++) wsb_put(&s, ", u32 g_c%u", b);
+        if (psc->n) {
+            wsb_put(&s, ", u32 g_sm");
+            for (u32 j = 0; j < psc->n; j++) wsb_put(&s, ", float g_sv%u", j);
+        }
+    } else if (g->pkind == 2) {
+        wsb_put(&s, ", char* g_p0, const char* g_p1");
+    }
+    for (u32 t = 0; t < g->n_tail; t++) {
+        for (u32 b = 0; b <= g->tail[t]->n_leaves; b++) wsb_put(&s, ", char* t%u_p%u", t, b);
+        for (u32 b = 0; b <= g->tail[t]->n_leaves; b++) wsb_put(&s, ", u32 t%u_c%u", t, b);
+        if (tsc[t].n) {
+            wsb_put(&s, ", u32 t%u_sm", t);
+            for (u32 j = 0; j < tsc[t].n; j++) wsb_put(&s, ", float t%u_sv%u", t, j);
+        }
+    }
+    wsb_put(&s, ", unsigned long long* sl_) {\n");
+    wsb_put(&s, "  __shared__ float red_[%u];\n", WIN_BLOCK / 64);
+    wsb_put(&s, "  const u32 gid = blockIdx.x / %uu, sp_ = blockIdx.x %% %uu;\n", S, S);
+    wsb_put(&s, "  const u32 lane = threadIdx.x;\n");
+    for (u32 m = 0; m < g->n_sum; m++) {
+        const WinPlan *q = &((const WinEntry *)g->sum[m])->plan;
+        for (u32 j = 0; j < q->n_ld; j++) {
+            const u32 op = q->ld_op[j], bi = ks[m]->ops[op].imm.u;
+            if (g->sub[m][bi] >= 0) continue;
+            char nm[24];
+            snprintf(nm, sizeof nm, "m%u_b%u_", m, op);
+            emit_base(&s, nm, &q->ld_aff[j]);
+            if (!q->ld_r[j]) wsb_put(&s, "  const float m%u_h%u_ = ((const float*)m%u_p%u)[m%u_b%u_];\n", m, op, m, bi, m, op);
+        }
+        for (u32 v = 0; v < W; v++) wsb_put(&s, "  float m%u_q%u_ = 0.0f;\n", m, v);
+    }
+    if (g->pkind) emit_base(&s, "pb_", &g->canon);
+    wsb_put(&s, "  const u32 ulo_ = sp_ * %uu, uhi_ = (ulo_ + %uu < %uu) ? ulo_ + %uu : %uu;\n", chunk, chunk, units,
+            chunk, units);
+    /* the lane's vectors in order (the order of its partial sums); how far
+     * the loop is unrolled changes only how many loads are in flight */
+    if (fixed) {
+        if (unroll) wsb_put(&s, "  #pragma unroll %u\n", unroll);
+        else wsb_put(&s, "  #pragma unroll\n");
+        wsb_put(&s, "  for (u32 i_ = 0; i_ < %uu; i_++) {\n", nit);
+        wsb_put(&s, "    const u32 uu_ = ulo_ + lane + i_ * %uu;\n    const bool ok_ = uu_ < uhi_;\n"
+                    "    const u32 u_ = ok_ ? uu_ : ulo_;\n", WIN_BLOCK);
+    } else {
+        wsb_put(&s, "  #pragma unroll %u\n  for (u32 u_ = ulo_ + lane; u_ < uhi_; u_ += %uu) {\n",
+                unroll ? unroll : p->unroll, WIN_BLOCK);
+    }
+    wsb_put(&s, "    const u32 s_ = u_ / %uu, j_ = u_ - s_ * %uu;\n", L4, L4);
+    wsb_put(&s, "    const u32 o_ = j_ * %uu", W);
+    for (u32 q = 0; q < p->n_outer; q++) {
+        if (p->outer_mod[q])
+            wsb_put(&s, " + %uu * ((s_ / %uu) %% %uu)", p->outer_coef[q], p->outer_div[q], p->outer_mod[q]);
+        else
+            wsb_put(&s, " + %uu * (s_ / %uu)", p->outer_coef[q], p->outer_div[q]);
+    }
+    wsb_put(&s, ";\n");
+    /* the producer's values at the group's index, stored by this lane */
+    if (vec_prod) {
+        wsb_put(&s, "    float4");
+        for (u32 j = 0; j < nst; j++) wsb_put(&s, "%s pv%u_", j ? "," : "", j);
+        wsb_put(&s, ";\n    prod_(pb_ + o_, %s", fixed ? "ok_" : "true");
+        for (u32 j = 0; j < nst; j++) wsb_put(&s, ", &pv%u_", j);
+        if (g->pkind == 2) {
+            wsb_put(&s, ", g_p0, g_p1");
+        } else {
+            for (u32 b = 0; b <= pk->n_leaves; b++) wsb_put(&s, ", g_p%u", b);
+            for (u32 b = 0; b <= pk->n_leaves; b++) wsb_put(&s, ", g_c%u", b);
+            if (psc->n) {
+                wsb_put(&s, ", g_sm");
+                for (u32 j = 0; j < psc->n; j++) wsb_put(&s, ", g_sv%u", j);
+            }
+        }
+        wsb_put(&s, ");\n");
+        for (u32 j = 0; j < nst; j++)
+            wsb_put(&s, "    const float pv%u_0 = pv%u_.x, pv%u_1 = pv%u_.y, pv%u_2 = pv%u_.z, pv%u_3 = pv%u_.w;\n", j, j,
+                    j, j, j, j, j, j);
+    }
+    for (u32 v = 0; v < W && g->pkind && !vec_prod; v++) {
+        wsb_put(&s, "    float");
+        for (u32 j = 0; j < nst; j++) wsb_put(&s, "%s pv%u_%u", j ? "," : "", j, v);
+        wsb_put(&s, ";\n    prod_(pb_ + o_ + %uu, %s", v, fixed ? "ok_" : "true");
+        for (u32 j = 0; j < nst; j++) wsb_put(&s, ", &pv%u_%u", j, v);
+        if (g->pkind == 1) {
+            for (u32 b = 0; b <= pk->n_leaves; b++) wsb_put(&s, ", g_p%u", b);
+            for (u32 b = 0; b <= pk->n_leaves; b++) wsb_put(&s, ", g_c%u", b);
+            if (psc->n) {
+                wsb_put(&s, ", g_sm");
+                for (u32 j = 0; j < psc->n; j++) wsb_put(&s, ", g_sv%u", j);
+            }
+        } else {
+            wsb_put(&s, ", g_p0, g_p1");
+        }
+        wsb_put(&s, ");\n");
+    }
+    /* each sum's body in op order, each op once per vector component */
+    for (u32 m = 0; m < g->n_sum; m++) {
+        const WinPlan *q = &((const WinEntry *)g->sum[m])->plan;
+        const UOpKernel *k = ks[m];
+        for (u32 i = q->R + 1; i < q->acc; i++) {
+            if (!q->cone[i] || !op_type_is_float(k->ops[i].type)) continue;
+            if (k->ops[i].type == KOP_LOAD) {
+                u32 j = 0;
+                while (q->ld_op[j] != i) j++;
+                const u32 bi = k->ops[i].imm.u;
+                if (g->sub[m][bi] >= 0) {
+                    for (u32 v = 0; v < W; v++) wsb_put(&s, "    const float m%u_f%u_%u = pv%d_%u;\n", m, i, v, g->sub[m][bi], v);
+                } else if (!q->ld_r[j]) {
+                    for (u32 v = 0; v < W; v++) wsb_put(&s, "    const float m%u_f%u_%u = m%u_h%u_;\n", m, i, v, m, i);
+                } else if (W == 4) {
+                    wsb_put(&s, "    const float4 m%u_t%u_ = ld4nt_u(m%u_p%u, m%u_b%u_ + o_);\n", m, i, m, bi, m, i);
+                    for (u32 v = 0; v < 4; v++)
+                        wsb_put(&s, "    const float m%u_f%u_%u = m%u_t%u_.%c;\n", m, i, v, m, i, "xyzw"[v]);
+                } else {
+                    wsb_put(&s, "    const float m%u_f%u_0 = ((const float*)m%u_p%u)[m%u_b%u_ + o_];\n", m, i, m, bi, m, i);
+                }
+                continue;
+            }
+            for (u32 v = 0; v < W; v++) emit_member_op(&s, k, m, i, v);
+        }
+        for (u32 v = 0; v < W; v++)
+            wsb_put(&s, fixed ? "    m%u_q%u_ = m%u_q%u_ + (ok_ ? m%u_f%u_%u : 0.0f);\n" : "    m%u_q%u_ = m%u_q%u_ + m%u_f%u_%u;\n",
+                    m, v, m, v, m, q->value, v);
+    }
+    wsb_put(&s, "  }\n");
+    for (u32 m = 0; m < g->n_sum; m++) {
+        if (W == 4) wsb_put(&s, "  float m%u_t_ = (m%u_q0_ + m%u_q1_) + (m%u_q2_ + m%u_q3_);\n", m, m, m, m, m);
+        else wsb_put(&s, "  float m%u_t_ = m%u_q0_;\n", m, m);
+        wsb_put(&s, "  m%u_t_ = bsum(m%u_t_, red_);\n", m, m);
+    }
+    if (S > 1) {
+        wsb_put(&s, "  if (sp_ != %uu) {\n", S - 1);
+        for (u32 m = 0; m < g->n_sum; m++) wsb_put(&s, "    comb_put(sl_, gid + %uu, sp_, %uu, m%u_t_);\n", m * total, S, m);
+        wsb_put(&s, "    return;\n  }\n");
+    }
+    for (u32 m = 0; m < g->n_sum; m++) {
+        char fb[64];
+        float_bits(fb, sizeof fb, ((const WinEntry *)g->sum[m])->plan.init_bits);
+        if (S > 1)
+            wsb_put(&s, "  {\n    float w_ = 0.0f;\n"
+                        "    for (u32 s2_ = lane; s2_ < %uu; s2_ += %uu)\n"
+                        "      w_ = w_ + ((s2_ == %uu) ? m%u_t_ : comb_take(sl_, gid + %uu, s2_, %uu));\n"
+                        "    w_ = bsum(w_, red_);\n", S, WIN_BLOCK, S - 1, m, m * total, S);
+        else
+            wsb_put(&s, "  {\n    const float w_ = m%u_t_;\n", m);
+        wsb_put(&s, "    if (lane == 0u) {\n      const float v%u_ = %s + w_;\n      ((float*)m%u_p0)[gid] = v%u_;\n", m, fb, m, m);
+        for (u32 t = 0; t < g->n_tail; t++) {
+            if (wg_root(g, WG_MAX_SUMS + t) != m) continue;
+            char in[16];
+            if (g->tsrc[t] < WG_MAX_SUMS) snprintf(in, sizeof in, "v%u_", g->tsrc[t]);
+            else snprintf(in, sizeof in, "u%u_", g->tsrc[t] - WG_MAX_SUMS);
+            wsb_put(&s, "      const float u%u_ = tl%u_(gid, %s", t, t, in);
+            for (u32 b = 0; b <= g->tail[t]->n_leaves; b++) wsb_put(&s, ", t%u_p%u", t, b);
+            for (u32 b = 0; b <= g->tail[t]->n_leaves; b++) wsb_put(&s, ", t%u_c%u", t, b);
+            if (tsc[t].n) {
+                wsb_put(&s, ", t%u_sm", t);
+                for (u32 j = 0; j < tsc[t].n; j++) wsb_put(&s, ", t%u_sv%u", t, j);
+            }
+            wsb_put(&s, ");\n      (void)u%u_;\n", t);
+        }
+        wsb_put(&s, "    }\n  }\n");
+    }
+    wsb_put(&s, "}\n");
+out:
+    for (u32 m = 0; m < WG_MAX_SUMS; m++) free(ks[m]);
+    free(pk);
+    free(fnbuf);
+    if (!ok) {
+        free(s.p);
+        return NULL;
+    }
+    return s.p;
+}
+
+int window_group_build(WinGroup *g) {
+    if (!g->n_sum || (g->n_sum == 1 && !g->pkind && !g->n_tail)) return 0;
+    const WinPlan *p = &((const WinEntry *)g->sum[0])->plan;
+    const u64 key = wg_key(g);
+    WgEntry *w = NULL;
+    for (u32 i = 0; i < WGC.n && !w; i++)
+        if (WGC.e[i].key == key) w = &WGC.e[i];
+    if (!w) {
+        if (WGC.n >= WG_CACHE || hipb.noalloc) return 0;
+        w = &WGC.e[WGC.n++];
+        memset(w, 0, sizeof *w);
+        w->key = key;
+        char name[48], err[256] = {0};
+        snprintf(name, sizeof name, "thvm_rsg_%08x", (u32)(key & 0xFFFFFFFFu));
+        /* every workgroup of an output waits for the others, so the whole
+         * grid must be resident: the loop is unrolled less until the
+         * kernel's registers allow that */
+        static const u32 unrolls[] = {0, 8, 4, 2, 1};
+        hipFunction_t f = NULL;
+        for (u32 a = 0; a < sizeof unrolls / sizeof unrolls[0] && !f; a++) {
+            char *src = gen_group(g, name, unrolls[a], &w->psc, w->tsc, err, sizeof err);
+            if (!src) return 0;
+            if (hipb.dump_src) fprintf(stderr, "---- run-sum group kernel ----\n%s\n", src);
+            if (!rtc_build_module(src, &w->mod, err, sizeof err)) {
+                fprintf(stderr, "tinyhvm-hip: run-sum group build failed: %s\n", err);
+                free(src);
+                return 0;
+            }
+            if (hipModuleGetFunction(&f, w->mod, name) != hipSuccess ||
+                !co_form_make(&w->co, src, name, WIN_BLOCK, f)) {
+                HIPB_CHECK(hipModuleUnload(w->mod));
+                co_form_free(&w->co);
+                w->mod = NULL;
+                free(src);
+                return 0;
+            }
+            free(src);
+            w->cap = rtc_capacity(f, WIN_BLOCK);
+            if (p->S > 1 && (u64)p->total * p->S > w->cap) {
+                if (hipb.verbose)
+                    fprintf(stderr, "tinyhvm-hip: %s (unroll %u): grid does not fit at once\n", name, unrolls[a]);
+                co_form_free(&w->co);
+                HIPB_CHECK(hipModuleUnload(w->mod));
+                w->mod = NULL;
+                f = NULL;
+            }
+        }
+        if (!f) return 0;
+        w->fn = f;
+        hipb.n_compile++;
+        if (hipb.verbose) {
+            fprintf(stderr, "tinyhvm-hip: %s: %u sums", name, g->n_sum);
+            if (g->pkind) fprintf(stderr, ", producer %s", g->pkind == 1 ? "elementwise" : "window max");
+            fprintf(stderr, ", %u consumers\n", g->n_tail);
+        }
+    }
+    if (!w->fn) return 0;
+    g->fn = w->fn;
+    g->co = &w->co;
+    g->psc = &w->psc;
+    g->tsc = w->tsc;
+    g->grid = p->total * p->S;
+    g->comb_words = p->S > 1 ? p->total * p->S * g->n_sum : 0;
+    g->resident = p->S > 1;
+    return 1;
+}
+
+static void wg_scalars(const KGenScalars *sc, const WgBufs *b, const u32 *dts, u32 *sm, float *sv) {
+    *sm = 0;
+    for (u32 j = 0; j < sc->n; j++) {
+        const u32 id = b->b[1 + sc->leaf[j]].id;
+        sv[j] = 0.0f;
+        if (id && id != b->b[0].id && pool_host_value(id, dts[sc->leaf[j]], sc->index[j], &sv[j])) *sm |= 1u << j;
+    }
+}
+
+u32 window_group_params(const WinGroup *g, WgArgs *a, void **params) {
+    u32 np = 0, nptr = 0, ncnt = 0, nsv = 0;
+    for (u32 m = 0; m < g->n_sum; m++)
+        for (u32 b = 0; b < g->sb[m].nb; b++) {
+            a->ptr[nptr] = g->sb[m].b[b].ptr ? g->sb[m].b[b].ptr : hipb.dummy;
+            params[np++] = &a->ptr[nptr++];
+        }
+    if (g->pkind == 1) {
+        for (u32 b = 0; b < g->pb.nb; b++) {
+            a->ptr[nptr] = g->pb.b[b].ptr ? g->pb.b[b].ptr : hipb.dummy;
+            params[np++] = &a->ptr[nptr++];
+        }
+        for (u32 b = 0; b < g->pb.nb; b++) {
+            a->cnt[ncnt] = g->pb.b[b].ptr ? g->pb.b[b].cnt : 0u;
+            params[np++] = &a->cnt[ncnt++];
+        }
+        if (g->psc->n) {
+            wg_scalars(g->psc, &g->pb, g->pc->leaf_dtypes, &a->sm[0], &a->sv[nsv]);
+            params[np++] = &a->sm[0];
+            for (u32 j = 0; j < g->psc->n; j++) params[np++] = &a->sv[nsv++];
+        }
+    } else if (g->pkind == 2) {
+        for (u32 b = 0; b < 2; b++) {
+            a->ptr[nptr] = g->pb.b[b].ptr;
+            params[np++] = &a->ptr[nptr++];
+        }
+    }
+    for (u32 t = 0; t < g->n_tail; t++) {
+        for (u32 b = 0; b < g->tb[t].nb; b++) {
+            a->ptr[nptr] = g->tb[t].b[b].ptr ? g->tb[t].b[b].ptr : hipb.dummy;
+            params[np++] = &a->ptr[nptr++];
+        }
+        for (u32 b = 0; b < g->tb[t].nb; b++) {
+            a->cnt[ncnt] = g->tb[t].b[b].ptr ? g->tb[t].b[b].cnt : 0u;
+            params[np++] = &a->cnt[ncnt++];
+        }
+        if (g->tsc[t].n) {
+            wg_scalars(&g->tsc[t], &g->tb[t], g->tail[t]->leaf_dtypes, &a->sm[1 + t], &a->sv[nsv]);
+            params[np++] = &a->sm[1 + t];
+            for (u32 j = 0; j < g->tsc[t].n; j++) params[np++] = &a->sv[nsv++];
+        }
+    }
+    params[np++] = &hipb.comb_slots;
+    return np;
+}
+
+void window_group_mem(const WinGroup *g, HbMem *m) {
+    m->n = 0;
+    for (u32 s = 0; s < g->n_sum; s++)
+        for (u32 b = 0; b < g->sb[s].nb; b++)
+            hbm_add(m, g->sb[s].b[b].ptr, g->sb[s].b[b].bytes, b == 0);
+    for (u32 b = 0; b < g->pb.nb && g->pkind; b++) {
+        int wr = g->pkind == 2 ? b == 0 : 0;
+        for (u32 j = 0; g->pkind == 1 && j < g->pc->n_st; j++) wr |= g->pc->st_slot[j] == b;
+        hbm_add(m, g->pb.b[b].ptr, g->pb.b[b].bytes, wr);
+    }
+    for (u32 t = 0; t < g->n_tail; t++)
+        for (u32 b = 0; b < g->tb[t].nb; b++)
+            hbm_add(m, g->tb[t].b[b].ptr, g->tb[t].b[b].bytes, b == 0);
+}
+
+u64 window_group_tail_reads(const WinGroup *g, u32 t) {
+    const UOpKernel *k = g->tail[t];
+    u32 sm;
+    float sv[KGEN_MAX_SCALARS];
+    wg_scalars(&g->tsc[t], &g->tb[t], k->leaf_dtypes, &sm, sv);
+    u64 reads = 0;
+    for (u32 i = 0; i < k->n_ops; i++) {
+        const KOp *op = &k->ops[i];
+        if (op->type != KOP_LOAD || op->imm.u == 0 || op->imm.u > k->n_leaves || op->imm.u == g->tleaf[t]) continue;
+        int inl = 0;
+        for (u32 j = 0; j < g->tsc[t].n && !inl; j++)
+            inl = g->tsc[t].leaf[j] == op->imm.u - 1 && ((sm >> j) & 1u) && k->ops[op->arg[0]].type == KOP_CONST_U &&
+                  k->ops[op->arg[0]].imm.u == g->tsc[t].index[j];
+        if (!inl && op->imm.u - 1 < 64) reads |= 1ull << (op->imm.u - 1);
+    }
+    return reads;
+}
+
+/* a recognised program's entry outside the cache (not compiled), or NULL */
+static WinEntry *wg_temp_entry(const UOpKernel *k) {
+    WinEntry *e = calloc(1, sizeof *e);
+    if (!e) return NULL;
+    e->key = win_key(k);
+    e->n_ops = k->n_ops;
+    e->n_leaves = k->n_leaves;
+    e->ops = malloc((size_t)k->n_ops * sizeof(KOp) + 1);
+    if (!e->ops || k->n_leaves > FUSE_MAX_LEAVES || !win_recognize(k, &e->plan)) {
+        free(e->ops);
+        free(e);
+        return NULL;
+    }
+    memcpy(e->ops, k->ops, (size_t)k->n_ops * sizeof(KOp));
+    e->meta[0] = k->grid[0]; e->meta[1] = k->grid[1]; e->meta[2] = k->grid[2];
+    e->meta[3] = k->local_size; e->meta[4] = k->out_dtype;
+    memcpy(e->dts, k->leaf_dtypes, (size_t)k->n_leaves * sizeof(u32));
+    e->kind = e->plan.kind;
+    return e;
+}
+
+char *window_group_source(const UOpKernel *const *ks, const u32 *const *bufs, u32 n, int producer, char *err,
+                          size_t errlen) {
+    static WinGroup g;
+    ChainInfo *pc = NULL;
+    WinEntry *tmp[1 + WG_MAX_SUMS] = {0};
+    u32 ntmp = 0;
+    char *src = NULL;
+    wg_clear(&g);
+    if (!ks || !bufs || n < 2) { snprintf(err, errlen, "need at least two programs"); return NULL; }
+    u32 i = 0;
+    if (producer) {
+        WinEntry *we = wg_temp_entry(ks[0]);
+        if (we && we->kind == WIN_MAX) {
+            tmp[ntmp++] = we;
+            if (!window_group_of_wmax(&g, we, bufs[0][0], bufs[0][ks[0]->ops[we->plan.ld_op[0]].imm.u])) {
+                snprintf(err, errlen, "window max producer refused");
+                goto out;
+            }
+        } else {
+            if (we) { free(we->ops); free(we); }
+            pc = chain_info_make(ks[0], ks[0]->ops);
+            if (!pc || !window_group_of_chain(&g, pc, bufs[0])) {
+                snprintf(err, errlen, "producer refused");
+                goto out;
+            }
+        }
+        i = 1;
+    }
+    for (; i < n; i++) {
+        int loop = 0;
+        for (u32 q = 0; q < ks[i]->n_ops; q++) loop |= ks[i]->ops[q].type == KOP_RANGE;
+        if (loop) {
+            WinEntry *we = ntmp <= WG_MAX_SUMS ? wg_temp_entry(ks[i]) : NULL;
+            if (!we) { snprintf(err, errlen, "program %u not a run sum", i); goto out; }
+            tmp[ntmp++] = we;
+            if (we->kind != WIN_SUM || !window_group_add_sum(&g, we, bufs[i][0], bufs[i] + 1, ks[i]->n_leaves)) {
+                snprintf(err, errlen, "run sum %u does not join", i);
+                goto out;
+            }
+        } else if (!window_group_add_tail(&g, ks[i], bufs[i][0], bufs[i] + 1, ks[i]->n_leaves)) {
+            snprintf(err, errlen, "consumer %u does not join", i);
+            goto out;
+        }
+    }
+    {
+        KGenScalars psc, tsc[WG_MAX_TAILS];
+        src = gen_group(&g, "thvm_rsg_check", 0, &psc, tsc, err, errlen);
+    }
+out:
+    free(pc);
+    for (u32 q = 0; q < ntmp; q++) { free(tmp[q]->ops); free(tmp[q]); }
+    wg_clear(&g);
+    return src;
 }
 
 void window_shutdown(void) {
@@ -800,4 +1719,10 @@ void window_shutdown(void) {
     }
     memset(&WC, 0, sizeof WC);
     scratch_release(&win_ws);
+    for (u32 i = 0; i < WGC.n; i++) {
+        if (WGC.e[i].fn) HIPB_CHECK(hipModuleUnload(WGC.e[i].mod));
+        co_form_free(&WGC.e[i].co);
+    }
+    for (u32 i = 0; i < WGC.n_tail; i++) free(WGC.tail[i]);
+    memset(&WGC, 0, sizeof WGC);
 }
