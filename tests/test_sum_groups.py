@@ -91,7 +91,9 @@ def test_backward_group(conv):
     # the second pair of sums over the pooling backward's output: siblings
     ks, bs, pr = _group(conv, [21, 22])
     main = _lib.group_source(ks, bs, pr).split('extern "C" __global__')[1]
-    assert main.count("ld4nt_u(") == 3            # dyp and xhat for one sum, dyp for the other
+    # dyp and xhat loaded once each: the second sum takes the first's dyp values
+    assert main.count("ld4nt_u(") == 2
+    assert re.search(r"const float m1_f\d+_0 = m0_f\d+_0;", main)
     assert "comb_put(sl_, gid + 64u" in main      # the second sum's partials after the first's
     assert _lib.group_compile_check(ks, bs, pr) > 0
 
@@ -109,10 +111,13 @@ def test_sequences_that_do_not_group(conv):
     # the sum must read the producer's output: sum(y) does not read c
     with pytest.raises(ValueError, match="does not join"):
         _lib.group_source(*_group(conv, [4, 2], producer=True))
-    # a sum that reads the producer's tensor but not every element once: the
-    # window max's output summed with a shifted index would skip elements
+    # the loss sum over a tensor the window max does not write
     k14, b14 = conv[14]
     ks, bs, pr = _group(conv, [13, 14], producer=True)
-    bs2 = [bs[0], [b14[0], 999]]                   # the loss sum over another tensor
     with pytest.raises(ValueError, match="does not join"):
-        _lib.group_source(ks, bs2, pr)
+        _lib.group_source(ks, [bs[0], [b14[0], 999]], pr)
+    # a sum that does not read every element of the producer's tensor once:
+    # sum(y) over the pooled output (a quarter of its loop's elements exist)
+    k2, b2 = conv[2]
+    with pytest.raises(ValueError, match="does not join"):
+        _lib.group_source([ks[0], k2], [bs[0], [b2[0], bs[0][0]]], pr)

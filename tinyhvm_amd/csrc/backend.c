@@ -1225,10 +1225,42 @@ static void hb_prepare_standalone(const UOpKernel *k) {
     if (!rtc_compile_uop(key, k)) refused[n_refused++ % 64] = key;
 }
 
+/* Loads of two leaf slots that name the same buffer (of one dtype, neither
+ * stored into) read it through the first slot, so that the generated code
+ * loads each element once: the engine passes a tensor once per use in an
+ * expression (the pooling backward's input and its comparison operand).
+ * Returns k itself when no slots repeat. */
+static const UOpKernel *hb_dedup_slots(const UOpKernel *k, const u32 *leaf_bufs, u32 n_leaves) {
+    static UOpKernel dk;
+    const u32 n = k->n_leaves < n_leaves ? k->n_leaves : n_leaves;
+    if (n < 2 || n >= 64) return k;
+    const u64 stored = chain_store_slots(k);
+    u8 map[64];
+    int any = 0;
+    for (u32 s = 1; s <= n; s++) {
+        map[s] = (u8)s;
+        if (!leaf_bufs[s - 1] || ((stored >> s) & 1u)) continue;
+        for (u32 t = 1; t < s; t++)
+            if (leaf_bufs[t - 1] == leaf_bufs[s - 1] && !((stored >> t) & 1u) &&
+                k->leaf_dtypes[t - 1] == k->leaf_dtypes[s - 1]) {
+                map[s] = (u8)t;
+                any = 1;
+                break;
+            }
+    }
+    if (!any) return k;
+    memcpy(&dk, k, sizeof dk);
+    for (u32 i = 0; i < dk.n_ops; i++)
+        if (dk.ops[i].type == KOP_LOAD && dk.ops[i].imm.u >= 1 && dk.ops[i].imm.u <= n)
+            dk.ops[i].imm.u = map[dk.ops[i].imm.u];
+    return &dk;
+}
+
 static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves,
                                    const UOpKernel *k, u64 cache_key) {
     (void)cache_key;
     const u64 t0 = hipb_hp_now();
+    if (k && leaf_bufs) k = hb_dedup_slots(k, leaf_bufs, n_leaves);
     hb_dispatch_uop_kernel_(out_buf, leaf_bufs, n_leaves, k);
     hipb_hp_add(HP_DISPATCH, t0);
 }

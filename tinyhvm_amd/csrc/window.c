@@ -1152,12 +1152,38 @@ int window_group_add_tail(WinGroup *g, const UOpKernel *k, u32 out_buf, const u3
     return 1;
 }
 
+/* An earlier member's memory load that member m's load j repeats (the same
+ * buffer at the same index): its value is taken instead of loading again.
+ * Returns 1 with that member and load. */
+static int wg_shared_load(const WinGroup *g, u32 m, u32 j, u32 *pm, u32 *pj) {
+    const WinEntry *e = g->sum[m];
+    const u32 bi = e->ops[e->plan.ld_op[j]].imm.u;
+    if (!e->plan.ld_r[j] || g->sub[m][bi] >= 0) return 0;
+    for (u32 m2 = 0; m2 < m; m2++) {
+        const WinEntry *e2 = g->sum[m2];
+        for (u32 j2 = 0; j2 < e2->plan.n_ld; j2++) {
+            const u32 b2 = e2->ops[e2->plan.ld_op[j2]].imm.u;
+            if (!e2->plan.ld_r[j2] || g->sub[m2][b2] >= 0 || g->sb[m2].b[b2].id != g->sb[m].b[bi].id ||
+                !aff_same(&e2->plan.ld_aff[j2], &e->plan.ld_aff[j]))
+                continue;
+            *pm = m2;
+            *pj = j2;
+            return 1;
+        }
+    }
+    return 0;
+}
+
 static u64 wg_key(const WinGroup *g) {
     u64 h = wg_mix(0x5347524F5550ull, ((u64)g->n_sum << 8) | ((u64)g->n_tail << 4) | (u64)g->pkind);
     for (u32 s = 0; s < g->n_sum; s++) {
         const WinEntry *e = g->sum[s];
         h = wg_mix(h, e->key);
         for (u32 b = 1; b <= e->n_leaves; b++) h = wg_mix(h, (u64)(u8)g->sub[s][b]);
+        for (u32 j = 0; j < e->plan.n_ld; j++) {
+            u32 pm, pj;
+            if (wg_shared_load(g, s, j, &pm, &pj)) h = wg_mix(h, 0x5348ull ^ ((u64)j << 16) ^ ((u64)pm << 32) ^ ((u64)pj << 40));
+        }
     }
     if (g->pkind) {
         h = wg_mix(h, g->psig);
@@ -1407,8 +1433,12 @@ static char *gen_group(const WinGroup *g, const char *name, u32 unroll, KGenScal
                 u32 j = 0;
                 while (q->ld_op[j] != i) j++;
                 const u32 bi = k->ops[i].imm.u;
+                u32 pm, pj;
                 if (g->sub[m][bi] >= 0) {
                     for (u32 v = 0; v < W; v++) wsb_put(&s, "    const float m%u_f%u_%u = pv%d_%u;\n", m, i, v, g->sub[m][bi], v);
+                } else if (wg_shared_load(g, m, j, &pm, &pj)) {
+                    const u32 i2 = ((const WinEntry *)g->sum[pm])->plan.ld_op[pj];
+                    for (u32 v = 0; v < W; v++) wsb_put(&s, "    const float m%u_f%u_%u = m%u_f%u_%u;\n", m, i, v, pm, i2, v);
                 } else if (!q->ld_r[j]) {
                     for (u32 v = 0; v < W; v++) wsb_put(&s, "    const float m%u_f%u_%u = m%u_h%u_;\n", m, i, v, m, i);
                 } else if (W == 4) {
