@@ -120,3 +120,70 @@ def test_combine_give_up_is_reported(no_window):
         else:
             assert rcs[i] == 0 and gave[i] == 0, (i, rcs[i], gave[i])
             assert got[i].tobytes() == ref[i].tobytes(), "dispatch %d differs" % i
+
+
+def _long_sum(trip):
+    """One output summing `trip` consecutive floats of its leaf: a run sum
+    the backend splits over up to 1024 workgroups."""
+    k = abi.UOpKernel()
+    ops = [(abi.KOP_GID, (0, 0, 0), None), (abi.KOP_ACC_INIT, (0, 0, 0), 0.0), (abi.KOP_RANGE, (0, 0, 0), trip),
+           (abi.KOP_LOAD, (2, 0, 0), 1), (abi.KOP_ACC, (1, 3, 0), abi.UOP_SUM), (abi.KOP_ENDRANGE, (2, 0, 0), 0),
+           (abi.KOP_STORE, (0, 1, 0), 0)]
+    for j, (t, a, imm) in enumerate(ops):
+        k.ops[j].type = t
+        for q in range(3):
+            k.ops[j].arg[q] = a[q]
+        if isinstance(imm, float):
+            k.ops[j].imm.f = imm
+        elif imm is not None:
+            k.ops[j].imm.u = imm
+    k.n_ops, k.n_leaves, k.n_bufs = len(ops), 1, 2
+    k.leaf_dtypes[0] = abi.DTYPE_F32
+    k.out_dtype = abi.DTYPE_F32
+    k.grid[0], k.grid[1], k.grid[2] = 1, 1, 1
+    k.local_size, k.reduce_numel = 256, trip
+    return k
+
+
+def _sum_once(k, x, env):
+    L = _lib.lib()
+    L.thvm_hip_shutdown()
+    saved = {n: os.environ.pop(n, None) for n in KNOBS}
+    os.environ.update(env)
+    try:
+        assert L.thvm_hip_init() == 0
+        xb, ob = L.thvm_hip_buf_alloc(x.nbytes), L.thvm_hip_buf_alloc(4)
+        L.thvm_hip_buf_write(xb, x.ctypes.data_as(C.c_void_p), x.nbytes)
+        c0 = (C.c_uint64 * 14)()
+        L.thvm_hip_counters(c0, 14)
+        leaves = (C.c_uint32 * 1)(xb)
+        L.thvm_hip_dispatch_uop_kernel(ob, leaves, 1, C.byref(k), 0)
+        rc = L.thvm_hip_synchronize()
+        c1 = (C.c_uint64 * 14)()
+        L.thvm_hip_counters(c1, 14)
+        out = np.zeros(1, dtype=np.float32)
+        L.thvm_hip_buf_read(ob, out.ctypes.data_as(C.c_void_p), 4)
+        return out[0], rc, c1[13] - c0[13]
+    finally:
+        L.thvm_hip_shutdown()
+        for n in KNOBS:
+            os.environ.pop(n, None)
+            if saved[n] is not None:
+                os.environ[n] = saved[n]
+
+
+def test_give_up_with_several_partials_per_lane():
+    """A sum split over more workgroups than a workgroup has lanes (1024
+    here): the combining workgroup reads all of a lane's partial words first
+    and then waits for each. A withheld partial is still a NaN, reported
+    once, and the sum without the knob is the plain one."""
+    trip = 1 << 21
+    k = _long_sum(trip)
+    w = _lib.window_analyze(k)
+    assert w == (2, 1024), w
+    x = np.random.default_rng(5).standard_normal(trip).astype(np.float32)
+    ref, rc, gave = _sum_once(k, x, {})
+    assert rc == 0 and gave == 0
+    assert abs(float(ref) - float(x.astype(np.float64).sum())) <= 1e-4 * float(np.abs(x).astype(np.float64).sum())
+    got, rc, gave = _sum_once(k, x, {"THVM_HIP_COMB_WITHHOLD": "1", "THVM_HIP_COMB_SPIN": "4096"})
+    assert rc == -1 and gave == 1 and np.isnan(got), (got, rc, gave)

@@ -458,6 +458,34 @@ static void emit_body_op(WSB *s, const UOpKernel *k, const WinPlan *p, u32 i, u3
     (void)p;
 }
 
+/* The combining workgroup's sum of an output's S partials into w_: lane l
+ * adds partials l, l + 256, ... in that order (its own, t, in place of the
+ * last one). With more than one per lane, all of the lane's words are read
+ * first and then waited for (one round trip instead of one per word) and
+ * cleared after every wait. */
+static void emit_take_all(WSB *s, u32 S, const char *t, const char *o_expr) {
+    if (S <= WIN_BLOCK) {
+        wsb_put(s, "    float w_ = 0.0f;\n"
+                   "    for (u32 s2_ = lane; s2_ < %uu; s2_ += %uu)\n"
+                   "      w_ = w_ + ((s2_ == %uu) ? %s : comb_take(sl_, %s, s2_, %uu));\n",
+                S, WIN_BLOCK, S - 1, t, o_expr, S);
+        return;
+    }
+    const u32 nq = (S + WIN_BLOCK - 1) / WIN_BLOCK;
+    wsb_put(s, "    float w_ = 0.0f;\n    {\n      unsigned long long* const w0_ = sl_ + (unsigned long long)(%s) * %uu;\n",
+            o_expr, S);
+    for (u32 q = 0; q < nq; q++)
+        wsb_put(s, "      const u32 s%u_ = lane + %uu;\n"
+                   "      const unsigned long long k%u_ = (s%u_ < %uu && s%u_ != %uu) ? comb_peek(w0_ + s%u_) : 0ull;\n",
+                q, q * WIN_BLOCK, q, q, S, q, S - 1, q);
+    for (u32 q = 0; q < nq; q++)
+        wsb_put(s, "      if (s%u_ < %uu) w_ = w_ + ((s%u_ == %uu) ? %s : comb_ready(w0_ + s%u_, k%u_));\n", q, S, q,
+                S - 1, t, q, q);
+    for (u32 q = 0; q < nq; q++)
+        wsb_put(s, "      if (s%u_ < %uu && s%u_ != %uu) comb_clear(w0_ + s%u_);\n", q, S, q, S - 1, q);
+    wsb_put(s, "    }\n");
+}
+
 static char *gen_run_sum(const UOpKernel *k, const WinPlan *p, const char *name) {
     WSB s = {0};
     const u32 W = p->W, L4 = p->L / W, units = p->trip / W;
@@ -545,13 +573,11 @@ static char *gen_run_sum(const UOpKernel *k, const WinPlan *p, const char *name)
         wsb_put(&s, "  t_ = bsum(t_, red_);\n"
                     "  if (sp_ != %uu) {\n"
                     "    comb_put(sl_, gid, sp_, %uu, t_);\n"
-                    "  } else {\n"
-                    "    float w_ = 0.0f;\n"
-                    "    for (u32 s2_ = lane; s2_ < %uu; s2_ += %uu)\n"
-                    "      w_ = w_ + ((s2_ == %uu) ? t_ : comb_take(sl_, gid, s2_, %uu));\n"
-                    "    w_ = bsum(w_, red_);\n"
+                    "  } else {\n", p->S - 1, p->S);
+        emit_take_all(&s, p->S, "t_", "gid");
+        wsb_put(&s, "    w_ = bsum(w_, red_);\n"
                     "    if (lane == 0u) ((float*)p0)[gid] = %s + w_;\n"
-                    "  }\n}\n", p->S - 1, p->S, p->S, WIN_BLOCK, p->S - 1, p->S, fb);
+                    "  }\n}\n", fb);
     } else {
         wsb_put(&s, "  t_ = bsum(t_, red_);\n  if (lane == 0u) ((float*)p0)[gid] = %s + t_;\n}\n", fb);
     }
@@ -577,6 +603,7 @@ typedef struct {
     hipModule_t mod;
     hipFunction_t fn, fn_fin;
     CoForm co;                   /* the main kernel's co-launch form (one-launch plans) */
+    char name[32];               /* its kernel's name */
     u32 cov_n[WIN_MAX_LOADS];    /* run sums: the tensor size each load was checked to tile (0: not yet) */
     u8 cov_ok[WIN_MAX_LOADS];    /* ... and the answer */
 } WinEntry;
@@ -723,6 +750,7 @@ build:;
         co_form_make(&e->co, src, name, WIN_BLOCK, e->fn);
     free(src);
     e->kind = e->plan.kind;
+    snprintf(e->name, sizeof e->name, "%s", name);
     if (hipb.verbose)
         fprintf(stderr, "tinyhvm-hip: %s outputs=%u trip=%u W=%u run=%u splits=%u\n", name, e->plan.total,
                 e->plan.trip, e->plan.W, e->plan.L, e->plan.S);
@@ -1470,12 +1498,14 @@ static char *gen_group(const WinGroup *g, const char *name, u32 unroll, KGenScal
     for (u32 m = 0; m < g->n_sum; m++) {
         char fb[64];
         float_bits(fb, sizeof fb, ((const WinEntry *)g->sum[m])->plan.init_bits);
-        if (S > 1)
-            wsb_put(&s, "  {\n    float w_ = 0.0f;\n"
-                        "    for (u32 s2_ = lane; s2_ < %uu; s2_ += %uu)\n"
-                        "      w_ = w_ + ((s2_ == %uu) ? m%u_t_ : comb_take(sl_, gid + %uu, s2_, %uu));\n"
-                        "    w_ = bsum(w_, red_);\n", S, WIN_BLOCK, S - 1, m, m * total, S);
-        else
+        if (S > 1) {
+            char t[16], o[32];
+            snprintf(t, sizeof t, "m%u_t_", m);
+            snprintf(o, sizeof o, "gid + %uu", m * total);
+            wsb_put(&s, "  {\n");
+            emit_take_all(&s, S, t, o);
+            wsb_put(&s, "    w_ = bsum(w_, red_);\n");
+        } else
             wsb_put(&s, "  {\n    const float w_ = m%u_t_;\n", m);
         wsb_put(&s, "    if (lane == 0u) {\n      const float v%u_ = %s + w_;\n      ((float*)m%u_p0)[gid] = v%u_;\n", m, fb, m, m);
         for (u32 t = 0; t < g->n_tail; t++) {
@@ -1557,9 +1587,14 @@ int window_group_build(WinGroup *g) {
         w->fn = f;
         hipb.n_compile++;
         if (hipb.verbose) {
-            fprintf(stderr, "tinyhvm-hip: %s: %u sums", name, g->n_sum);
-            if (g->pkind) fprintf(stderr, ", producer %s", g->pkind == 1 ? "elementwise" : "window max");
-            fprintf(stderr, ", %u consumers\n", g->n_tail);
+            /* its parts by the names of their own kernels, in dispatch order */
+            fprintf(stderr, "tinyhvm-hip: %s =", name);
+            if (g->pkind == 1) fprintf(stderr, " thvm_ew_%08x +", (u32)(g->psig & 0xFFFFFFFFu));
+            if (g->pkind == 2) fprintf(stderr, " %s +", ((const WinEntry *)g->pw)->name);
+            for (u32 m = 0; m < g->n_sum; m++)
+                fprintf(stderr, "%s %s", m ? " +" : "", ((const WinEntry *)g->sum[m])->name);
+            for (u32 t = 0; t < g->n_tail; t++) fprintf(stderr, " + thvm_ew_%08x", (u32)(g->tsig[t] & 0xFFFFFFFFu));
+            fprintf(stderr, "\n");
         }
     }
     if (!w->fn) return 0;
