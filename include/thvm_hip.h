@@ -140,7 +140,7 @@ int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32
                                           const UOpKernel *kernel);
 
 /* Counters, for tests and the engine-driven timing (no counterpart in the
- * reference): out[0..11] = dispatches, matrix-core dispatches, compiled
+ * reference): out[0..14] = dispatches, matrix-core dispatches, compiled
  * programs, program cache hits, dispatches run on the KOp interpreter
  * (programs the generator or hipRTC refused; their outputs are still
  * written), host waits on the stream, live device bytes, hipMalloc calls,
@@ -148,8 +148,9 @@ int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32
  * dispatches run on the window-max and run-sum kernels, dispatches issued
  * inside a batched launch, elementwise dispatches run as the fused epilogue
  * of the contraction whose output they read, host waits after which a
- * single-pass combine was found to have given up waiting for a partial sum.
- * Returns the number of counters (14). */
+ * single-pass combine was found to have given up waiting for a partial sum,
+ * host uploads copied by an upload kernel held with other launches.
+ * Returns the number of counters (15). */
 int  thvm_hip_counters(u64 *out, u32 n);
 /* Wait for all enqueued work; returns 0, or -1 on a device error or when a
  * kernel that combines its workgroups' partial sums in one pass gave up
@@ -245,6 +246,12 @@ int  thvm_hip_group_compile_check(const UOpKernel *const *ks, const u32 *const *
 /* Its source (length, or -1 with the reason in buf). */
 int  thvm_hip_group_source(const UOpKernel *const *ks, const u32 *const *bufs, u32 n, int producer, char *buf,
                            u64 buflen);
+
+/* Source of the upload kernel (main kernel thvm_upload, 256 lanes): host
+ * writes of at most 64 KiB reach the device through it, read from pinned
+ * coherent host memory, and it joins a batch launch with independent held
+ * work. Length, or -1. A diagnostic with no counterpart in the reference. */
+int  thvm_hip_upload_source(char *buf, u64 buflen);
 
 /* Independent dispatches held back and issued as one launch: the batch
  * kernel of n generated modules (srcs[i] as the generators above return it,

@@ -46,6 +46,13 @@ hipError_t hipHostMalloc(void **p, size_t n, unsigned int flags) {
     return *p ? hipSuccess : hipErrorOutOfMemory;
 }
 
+/* host memory stands for device memory here */
+hipError_t hipHostGetDevicePointer(void **dev, void *host, unsigned int flags) {
+    (void)flags;
+    *dev = host;
+    return hipSuccess;
+}
+
 hipError_t hipHostFree(void *p) {
     free(p);
     return hipSuccess;

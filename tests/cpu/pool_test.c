@@ -30,6 +30,17 @@ hipError_t hipb_stream_wait(void) {
 void hipb_before_stream(void) {}
 void hipb_before_copy(const void *dst, u64 bytes) { (void)dst; (void)bytes; }
 int hipb_held_buffer(u32 id) { (void)id; return 0; }
+int hipb_holding(void) { return 0; }
+/* an upload kernel run at once, on every other upload (the others take the
+ * copy path) */
+static u64 uploads_held;
+int hipb_hold_upload(void *dst, u64 dst_bytes, const void *src_dev, u64 bytes) {
+    static int turn;
+    if (bytes > dst_bytes || (turn++ & 1)) return 0;
+    memmove(dst, src_dev, bytes);
+    uploads_held++;
+    return 1;
+}
 
 extern size_t fake_hip_limit, fake_hip_live;
 extern unsigned long fake_hip_mallocs, fake_hip_frees;
@@ -180,6 +191,27 @@ static void test_write_read(void) {
     pool_reset(0);
 }
 
+/* Small writes reach the device through the upload ring: held as upload
+ * kernels or copied, across several wraps of the ring's segments. */
+static void test_uploads(void) {
+    pool_reset(0);
+    u32 a = pool_alloc(16384), b = pool_alloc(100);
+    u8 src[16384];
+    const u64 held0 = uploads_held;
+    for (u32 r = 0; r < 600; r++) {
+        for (u32 i = 0; i < sizeof src; i++) src[i] = (u8)(i * 31 + r);
+        const u32 n = r % 3 == 0 ? 16384 : 4096 + r;
+        pool_write(a, src, n);
+        pool_sync_device(a);
+        CHECK(memcmp(pool_ptr(a), src, n) == 0);
+        pool_write(b, src + r, 100);
+        pool_sync_device(b);
+        CHECK(memcmp(pool_ptr(b), src + r, 100) == 0);
+    }
+    CHECK(uploads_held > held0);
+    pool_reset(0);
+}
+
 int main(void) {
     memset(&hipb, 0, sizeof hipb);
     if (pool_init() != 0) {
@@ -193,6 +225,7 @@ int main(void) {
     test_oom();
     test_graph_pins();
     test_write_read();
+    test_uploads();
     pool_block_put(hipb.dummy, hipb.dummy_cap);
     pool_shutdown();
     CHECK(fake_hip_live == 0);                 /* everything went back */

@@ -81,3 +81,15 @@ def test_lenet_epilogues_fuse_and_compile():
                  (256, 120, 84)]:
         assert want in fused, (want, fused)
     assert refused == [(256, 400, 120), (96, 25, 25), (50176, 6, 400)], refused
+
+
+def test_upload_kernel_compiles_in_a_batch():
+    """Host writes of at most 64 KiB are copied by the upload kernel, read
+    from pinned coherent host memory, so that the copy goes out in one batch
+    launch with independent held work instead of as a copy of its own: its
+    module compiles alone and batched with generated modules."""
+    src = _lib.upload_source()
+    assert 'void thvm_upload(' in src and "__launch_bounds__(256)" in src
+    mods = _modules("lenet_b256.trc")[:3]
+    assert _lib.batch_compile_check([(src, "thvm_upload", 256, 3, 1)]) > 0
+    assert _lib.batch_compile_check([(src, "thvm_upload", 256, 3, 1)] + mods) > 0

@@ -346,6 +346,8 @@ static void hb_flush(void) {
     pool_release_deferred();
 }
 
+int hipb_holding(void) { return HB.n > 0; }
+
 int hipb_held_buffer(u32 id) {
     for (u32 i = 0; i < HB.n; i++) {
         const HbEnt *h = &HB.ent[i];
@@ -495,6 +497,74 @@ static void hb_hold_chain(const ChainInfo *ch, u32 out_buf, const u32 *leaf_bufs
     h->ch_bufs[0] = out_buf;
     memcpy(h->ch_bufs + 1, leaf_bufs, ch->n_leaves * sizeof(u32));
     h->ch_seq = pool_write_clock();
+}
+
+/* The upload kernel: 16 bytes per lane from device-readable host memory,
+ * the tail bytes by the first workgroup's lanes. Compiled once. */
+static struct { hipModule_t mod; hipFunction_t fn; CoForm co; } UPK;
+
+static const char UPLOAD_SRC[] =
+    "extern \"C\" __global__ __launch_bounds__(256) void thvm_upload(char* dst, const char* src, u32 n16, u32 n) {\n"
+    "  const u32 i = blockIdx.x * 256u + threadIdx.x;\n"
+    "  if (i < n16) ((uint4*)dst)[i] = ((const uint4*)src)[i];\n"
+    "  if (blockIdx.x == 0u && threadIdx.x < (n & 15u)) dst[n16 * 16u + threadIdx.x] = src[n16 * 16u + threadIdx.x];\n"
+    "}\n";
+
+/* prelude + the upload kernel (malloc'd) */
+static char *upload_source(void) {
+    const char *pre = kgen_prelude();
+    char *src = malloc(strlen(pre) + sizeof UPLOAD_SRC + 2);
+    if (src) sprintf(src, "%s\n%s", pre, UPLOAD_SRC);
+    return src;
+}
+
+int hipb_hold_upload(void *dst, u64 dst_bytes, const void *src_dev, u64 bytes) {
+    if (hipb.no_batch || hipb.noalloc || hipb.sync_each || HB.flushing || !hipb.initialized || !dst || !src_dev ||
+        bytes == 0 || bytes > dst_bytes || bytes > 0xFFFFFFFFull || ((uintptr_t)dst & 15u) || ((uintptr_t)src_dev & 15u))
+        return 0;
+    /* a launch held for a fused epilogue joins no batch: the copy then goes on
+     * the stream ahead of it, as before */
+    if ((HB.n && HB.ent[0].solo) || !UPK.fn) return 0;
+    const u32 n16 = (u32)(bytes / 16u), n = (u32)bytes;
+    u32 gx = (n16 + 255u) / 256u;
+    if (gx == 0) gx = 1;
+    void *d = dst;
+    const void *sp = src_dev;
+    u32 a = n16, b = n;
+    void *params[] = {&d, &sp, &a, &b};
+    HbMem m;
+    m.n = 0;
+    hbm_add(&m, dst, dst_bytes, 1);
+    if (!hipb_hold(&UPK.co, UPK.fn, gx, 1, params, &m, 0, -1, 0)) return 0;
+    hipb.n_upload_held++;
+    return 1;
+}
+
+/* at backend init (a module cannot be set up inside a graph capture);
+ * without it uploads are copies */
+static void upload_prepare(void) {
+    if (UPK.fn || hipb.no_batch) return;
+    char *src = upload_source();
+    char err[256] = {0};
+    if (!src) return;
+    if (rtc_build_module(src, &UPK.mod, err, sizeof err)) {
+        if (hipModuleGetFunction(&UPK.fn, UPK.mod, "thvm_upload") != hipSuccess ||
+            !co_form_make(&UPK.co, src, "thvm_upload", 256, UPK.fn)) {
+            (void)hipGetLastError();
+            HIPB_CHECK(hipModuleUnload(UPK.mod));
+            co_form_free(&UPK.co);
+            UPK.fn = NULL;
+        }
+    } else if (hipb.verbose) {
+        fprintf(stderr, "tinyhvm-hip: no upload kernel: %s\n", err);
+    }
+    free(src);
+}
+
+static void upload_release(void) {
+    if (UPK.fn) HIPB_CHECK(hipModuleUnload(UPK.mod));
+    co_form_free(&UPK.co);
+    memset(&UPK, 0, sizeof UPK);
 }
 
 /* Marks the launch just held as a run sum: a group of one that run sums of
@@ -886,6 +956,7 @@ static int hb_init(void) {
         }
     }
     if (hipStreamCreateWithFlags(&hipb.stream, hipStreamNonBlocking) != hipSuccess) return -1;
+    if (hipStreamCreateWithFlags(&hipb.setup_stream, hipStreamNonBlocking) != hipSuccess) return -1;
     hipb.sync_each = env_flag("THVM_HIP_SYNC");
     hipb.no_batch = env_flag("THVM_HIP_NO_BATCH");
     hipb.dump_src = env_flag("THVM_HIP_DUMP");
@@ -922,6 +993,7 @@ static int hb_init(void) {
         hipb_launch(fill, (n1 + 255) / 256, 1, 1, 256, a1);
         if (hipb_stream_wait() != hipSuccess) return -1;
     }
+    upload_prepare();
     /* the static workspace of the no-allocation entry point, on this device */
     if (thvm_noalloc_scratch_init(hipb.device) == 0) hipb.noalloc_scratch = thvm_noalloc_scratch_ptr(hipb.device);
     else fprintf(stderr, "tinyhvm-hip: static workspace unavailable; dispatch without allocation is off\n");
@@ -943,6 +1015,7 @@ static void hb_shutdown(void) {
     dense_shutdown();
     window_shutdown();
     hb_release();
+    upload_release();
     rtc_shutdown();
     scratch_release(&red_ws);
     pool_block_put(hipb.comb_slots, (u64)COMB_SLOTS * 8);
@@ -954,6 +1027,7 @@ static void hb_shutdown(void) {
     hipb.comb_err_dev = NULL;
     pool_shutdown();
     HIPB_CHECK(hipStreamDestroy(hipb.stream));
+    HIPB_CHECK(hipStreamDestroy(hipb.setup_stream));
     hipb.initialized = 0;
 }
 
@@ -1867,11 +1941,11 @@ int thvm_hip_counters(u64 *out, u32 n) {
     u32 pinned = 0, limbo = 0;
     pool_stats(&live, &cached, &mallocs);
     pool_pin_stats(&pinned, &limbo);
-    u64 v[14] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
+    u64 v[15] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
                  hipb.n_stream_sync, live, mallocs, pinned, limbo, hipb.n_window, hipb.n_batched, hipb.n_fused,
-                 hipb.n_comb_gaveup};
-    for (u32 i = 0; out && i < n && i < 14; i++) out[i] = v[i];
-    return 14;
+                 hipb.n_comb_gaveup, hipb.n_upload_held};
+    for (u32 i = 0; out && i < n && i < 15; i++) out[i] = v[i];
+    return 15;
 }
 
 int thvm_hip_synchronize(void) {
@@ -1978,6 +2052,16 @@ int thvm_hip_epilogue_compile_check(const UOpKernel *producer, const UOpKernel *
     free(src);
     if (n < 0 && errbuf && errlen) snprintf(errbuf, errlen, "%s", err);
     return (int)n;
+}
+
+int thvm_hip_upload_source(char *buf, u64 buflen) {
+    ensure_env();
+    char *src = upload_source();
+    if (!src) return -1;
+    const size_t len = strlen(src);
+    if (buf && buflen) snprintf(buf, buflen, "%s", src);
+    free(src);
+    return (int)len;
 }
 
 int thvm_hip_group_source(const UOpKernel *const *ks, const u32 *const *bufs, u32 n, int producer, char *buf,
@@ -2119,7 +2203,9 @@ int thvm_hip_graph_begin(void) {
     pool_sync_all_device();
     HipbGraph *g = calloc(1, sizeof *g);
     if (!g) return -1;
-    if (hipHostMalloc((void **)&g->arena, GRAPH_ARENA_BYTES, 0) != hipSuccess) {
+    /* coherent: upload kernels in the graph read it directly */
+    if (hipHostMalloc((void **)&g->arena, GRAPH_ARENA_BYTES, hipHostMallocMapped | hipHostMallocCoherent) !=
+        hipSuccess) {
         (void)hipGetLastError();
         free(g);
         return -1;

@@ -38,6 +38,7 @@ typedef struct {
     int initialized;
     int device;
     hipStream_t stream;
+    hipStream_t setup_stream; /* module set-up copies (legal while the main stream is captured) */
     int sync_each;           /* THVM_HIP_SYNC: synchronize after every dispatch */
     int dump_src;            /* THVM_HIP_DUMP: print generated HIP source */
     int no_dense;            /* THVM_HIP_NO_DENSE: skip dense recognizers */
@@ -77,6 +78,7 @@ typedef struct {
     u64 n_batched;           /* dispatches issued inside a batched launch */
     u64 n_fused;             /* elementwise dispatches run as a contraction's fused epilogue */
     u64 n_copy_fused;        /* buffer copies written by the launch of the program that produced them */
+    u64 n_upload_held;       /* host uploads copied by a held upload kernel */
     int host_profile;        /* THVM_HIP_HOST_PROFILE: host time per category, printed by profile_report */
     u64 hp_ns[HP_N], hp_calls[HP_N];
     int no_batch;            /* THVM_HIP_NO_BATCH: launch every dispatch on its own */
@@ -125,9 +127,16 @@ void hipb_before_stream(void);
 /* The same for a host-to-device copy into [dst, dst + bytes): only if a held
  * dispatch touches that memory (the copy may go ahead of independent ones). */
 void hipb_before_copy(const void *dst, u64 bytes);
+/* Holds a copy of `bytes` from device-readable host memory src_dev into the
+ * device buffer at dst (dst_bytes long) as a launch of the upload kernel, so
+ * that it goes out with independent held launches. Returns 0 when it is not
+ * held (the caller copies with hipMemcpyAsync). */
+int  hipb_hold_upload(void *dst, u64 dst_bytes, const void *src_dev, u64 bytes);
 /* Whether a held launch that a consumer may still fuse after names buffer
  * id (its free then waits: pool_release_deferred after the launch). */
 int  hipb_held_buffer(u32 id);
+/* launches are held (not yet issued) */
+int  hipb_holding(void);
 void pool_release_deferred(void);
 typedef struct {
     void *ptr;        /* device pointer, NULL if free */

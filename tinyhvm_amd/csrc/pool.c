@@ -46,9 +46,17 @@
 
 #define POOL_MIN_CLASS_BYTES 256ull
 #define POOL_N_CLASSES 256
-#define POOL_MIRROR_MAX 4096ull
+#define POOL_MIRROR_MAX 16384ull
 #define STAGE_SEGMENTS 4
 #define STAGE_SEG_BYTES (16ull << 20)
+/* Host writes of more than UP_EAGER_MIN and at most POOL_MIRROR_MAX bytes
+ * are copied by a kernel that reads them from pinned, coherent host memory
+ * (an upload ring of UP_SEGMENTS segments), so that the copy can go out in
+ * one launch with independent held work. */
+#define UP_SEGMENTS 2
+#define UP_SEG_BYTES (2ull << 20)
+#define UP_MAX (64ull << 10)
+#define UP_EAGER_MIN 256ull
 #define POOL_MAX_IDS 16384u
 
 typedef struct {
@@ -78,8 +86,15 @@ static struct {
     u8 seg_pending[STAGE_SEGMENTS];
     u32 seg;
     u64 seg_off;
+    /* upload ring (host pointer, device pointer) */
+    u8 *up, *up_dev;
+    hipEvent_t up_done[UP_SEGMENTS];
+    u8 up_pending[UP_SEGMENTS];
+    u32 up_seg;
+    i32 up_closing;       /* segment whose event waits for the held launches to go out, or -1 */
+    u64 up_off;
     /* graph capture: uploads go to the capturing graph's arena */
-    u8 *arena;
+    u8 *arena, *arena_dev;
     u64 arena_cap, arena_off;
     u32 capture_seq;      /* numbers the captures; buffers record the one they were written in */
     PoolPins *capture_pins; /* blocks the open capture references */
@@ -175,6 +190,11 @@ static void capture_pin(void *ptr, u64 cap) {
 void pool_capture_begin(u8 *arena, u64 bytes, PoolPins *pins) {
     P.capture_seq++;
     P.arena = arena;
+    P.arena_dev = NULL;
+    if (arena && hipHostGetDevicePointer((void **)&P.arena_dev, arena, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        P.arena_dev = NULL;
+    }
     P.arena_cap = bytes;
     P.arena_off = 0;
     P.capture_pins = pins;
@@ -191,7 +211,7 @@ void pool_capture_end(void) {
         HipbBuf *b = &P.bufs[i];
         if (b->live && b->host_valid && b->host_mirror && b->write_capture == P.capture_seq) b->dev_stale = 1;
     }
-    P.arena = NULL;
+    P.arena = P.arena_dev = NULL;
     P.arena_cap = P.arena_off = 0;
     P.capture_pins = NULL;
 }
@@ -342,6 +362,17 @@ int pool_init(void) {
     for (u32 s = 0; s < STAGE_SEGMENTS; s++) {
         if (hipEventCreateWithFlags(&P.seg_done[s], hipEventDisableTiming) != hipSuccess) return -1;
     }
+    /* the upload ring: optional (uploads fall back to copies without it) */
+    P.up_closing = -1;
+    if (hipHostMalloc((void **)&P.up, UP_SEGMENTS * UP_SEG_BYTES, hipHostMallocMapped | hipHostMallocCoherent) !=
+            hipSuccess ||
+        hipHostGetDevicePointer((void **)&P.up_dev, P.up, 0) != hipSuccess) {
+        (void)hipGetLastError();
+        if (P.up) HIPB_CHECK(hipHostFree(P.up));
+        P.up = P.up_dev = NULL;
+    }
+    for (u32 s = 0; s < UP_SEGMENTS && P.up; s++)
+        if (hipEventCreateWithFlags(&P.up_done[s], hipEventDisableTiming) != hipSuccess) return -1;
     return 0;
 }
 
@@ -360,6 +391,10 @@ void pool_shutdown(void) {
     for (u32 c = 0; c < POOL_N_CLASSES; c++) free(P.free[c].ptrs);
     for (u32 s = 0; s < STAGE_SEGMENTS; s++) HIPB_CHECK(hipEventDestroy(P.seg_done[s]));
     if (P.stage) HIPB_CHECK(hipHostFree(P.stage));
+    if (P.up) {
+        for (u32 s = 0; s < UP_SEGMENTS; s++) HIPB_CHECK(hipEventDestroy(P.up_done[s]));
+        HIPB_CHECK(hipHostFree(P.up));
+    }
     free(P.bufs);
     memset(&P, 0, sizeof(P));
 }
@@ -489,6 +524,11 @@ static int defer_free(u32 id) {
 }
 
 void pool_release_deferred(void) {
+    if (P.up_closing >= 0) {   /* the held launches are out: the segment left before is done after them */
+        HIPB_CHECK(hipEventRecord(P.up_done[P.up_closing], hipb.stream));
+        P.up_pending[P.up_closing] = 1;
+        P.up_closing = -1;
+    }
     const u32 n = DF.n;
     DF.n = 0;
     for (u32 i = 0; i < n; i++) {
@@ -589,6 +629,57 @@ void pool_mark_device_write(u32 id) {
 
 static u8 *stage_reserve(u64 n);
 
+/* n bytes of device-readable pinned memory for an upload kernel to read:
+ * the capturing graph's arena, else the upload ring (a segment is reused once
+ * the work issued before it moved on has finished). NULL if there is none. */
+static u8 *up_reserve(u64 n, u8 **dev) {
+    if (hipb.capturing) {
+        if (!P.arena_dev) return NULL;
+        u8 *h = stage_reserve(n);
+        if (!h) return NULL;
+        *dev = P.arena_dev + (h - P.arena);
+        return h;
+    }
+    if (!P.up || n > UP_MAX) return NULL;
+    if (P.up_off + n > UP_SEG_BYTES) {
+        /* the segment left is done once the work issued after its last
+         * upload has finished: its event is recorded now, or, while launches
+         * (upload kernels reading it among them) are held, once they go out,
+         * so that the ring never decides which launches go out together */
+        const u32 next = (P.up_seg + 1) % UP_SEGMENTS;
+        if (P.up_closing == (i32)next) hipb_before_stream();   /* records it */
+        if (hipb_holding()) {
+            P.up_closing = (i32)P.up_seg;
+        } else {
+            HIPB_CHECK(hipEventRecord(P.up_done[P.up_seg], hipb.stream));
+            P.up_pending[P.up_seg] = 1;
+        }
+        P.up_seg = next;
+        if (P.up_pending[P.up_seg]) {
+            hipb.n_stream_sync++;
+            HIPB_CHECK(hipEventSynchronize(P.up_done[P.up_seg]));
+            P.up_pending[P.up_seg] = 0;
+        }
+        P.up_off = 0;
+    }
+    const u64 o = (u64)P.up_seg * UP_SEG_BYTES + P.up_off;
+    P.up_off += (n + 255) & ~255ull;
+    *dev = P.up_dev + o;
+    return P.up + o;
+}
+
+/* A host write of the whole buffer, just taken into the mirror, held as an
+ * upload kernel: it goes out in one launch with the independent launches
+ * held now, instead of as a copy of its own when a consumer needs it (that
+ * copy would precede the consumer's launch and split no batch, but costs a
+ * copy per write). Stays pending if it cannot be held. */
+static void up_eager(u32 id, HipbBuf *b) {
+    u8 *dev = NULL, *h = up_reserve(b->mirror_bytes, &dev);
+    if (!h) return;
+    memcpy(h, b->host_mirror, b->mirror_bytes);
+    if (hipb_hold_upload(b->ptr, pool_bytes(id), dev, b->mirror_bytes)) b->dev_stale = 0;
+}
+
 /* Copy a pending host mirror to the device (stream ordered; ahead of held
  * launches that do not touch the buffer). */
 void pool_sync_device(u32 id) {
@@ -663,6 +754,9 @@ void pool_write(u32 id, const void *data, u64 bytes) {
             if (bytes >= b->bytes) b->mirror_bytes = (u32)bytes;
             b->host_valid = 1;
             b->dev_stale = 1;
+            /* small buffers (scalars, shapes) stay pending: their readers
+             * often take them inline, and then they are never uploaded */
+            if (bytes >= b->bytes && bytes > UP_EAGER_MIN) up_eager(id, b);
             return;
         }
     }

@@ -255,7 +255,9 @@ static char *compile_source(const char *src, size_t *code_len, char *err, size_t
 }
 
 /* A loaded module's pointer to the combine give-up word (thvm_comb_err_, in
- * the prelude) is set to the backend's word. */
+ * the prelude) is set to the backend's word, by a copy on a stream of its
+ * own: a module first built while the main stream is captured into a graph
+ * (a batch of launches first seen there) is set up the same way. */
 static void module_setup(hipModule_t mod) {
     if (!hipb.comb_err_dev) return;
     hipDeviceptr_t p = 0;
@@ -264,7 +266,8 @@ static void module_setup(hipModule_t mod) {
         (void)hipGetLastError();   /* the module has no combine: nothing to set */
         return;
     }
-    HIPB_CHECK(hipMemcpyHtoD(p, &hipb.comb_err_dev, sizeof(void *)));
+    HIPB_CHECK(hipMemcpyHtoDAsync(p, &hipb.comb_err_dev, sizeof(void *), hipb.setup_stream));
+    HIPB_CHECK(hipStreamSynchronize(hipb.setup_stream));
 }
 
 u32 rtc_capacity(hipFunction_t fn, u32 block) {
