@@ -424,6 +424,8 @@ typedef struct {
     u32 red_mg;            /* outer-product reduction: rows per group */
     u64 red_max[2];        /* ... the largest index each side forms (unchecked loads) */
     u32 red_buf[2];        /* ... and the buffer it reads (1 + leaf) */
+    int dvec[2];           /* direct kernel: side s read 4 consecutive k per lane with one 16-byte load */
+    u32 dvec_buf[2];       /* ... from this buffer (p<b>) */
     int comb;              /* direct and outer-product kernels: split-K partials combined in the
                               same launch by the last split's workgroup through the combine words */
 } GemmPlan;
@@ -853,6 +855,27 @@ static void emit_skinny_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
  * keeping 4 independent accumulator chains and loading the next step's
  * operands before it multiplies the current ones. The 4 waves' partial blocks
  * are summed through LDS in a fixed order. */
+/* Direct kernel: a side whose k offset is k itself (one loop digit, unit
+ * coefficient, no wrap below K) and whose row bases are multiples of 4 reads
+ * 4 consecutive k per lane as one 16-byte load, for K a multiple of 4 (then
+ * a group of 4 never straddles the end of K or of a split's chunk). The
+ * buffer's 16-byte alignment is checked when the kernel is dispatched. */
+static int direct_vec_side(const Contraction *ct, int side) {
+    if (!ct->sep[side] || ct->sep_dt[side] != DTYPE_F32 || ct->K % 4u || hipb.dense_novec) return 0;
+    const Aff *a = &ct->sep_aff[side];
+    if (a->cst % 4u) return 0;
+    u32 nr = 0;
+    for (u32 t = 0; t < a->n; t++) {
+        if (a->d[t].var == 1) {
+            if (a->d[t].div != 1u || a->coef[t] != 1u || (a->d[t].mod && a->d[t].mod < ct->K)) return 0;
+            nr++;
+        } else if (a->coef[t] % 4u) {
+            return 0;
+        }
+    }
+    return nr == 1;
+}
+
 static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
     const u32 M = ct->M, N = ct->N, K = ct->K, KU = pl->cfg.bk;
     const u32 blocks = pl->tiles_m * pl->tiles_n;
@@ -874,19 +897,54 @@ static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
             M, N, K, pl->tiles_n, blocks, pl->kchunk, KU, pl->nw);
     if (ct->sep[0]) dsb_put(s, "  const u32 bA = ma < M ? rowb_p(gid_m(ma)) : 0u;\n");
     if (ct->sep[1]) dsb_put(s, "  const u32 bB = nb < N ? rowb_q(gid_n(nb)) : 0u;\n");
-    dsb_put(s,
-            "  float a[KU / 2u], b[KU / 2u];\n"
-            "  auto fetch = [&](u32 k0) {\n"
-            "    #pragma unroll\n"
-            "    for (u32 q = 0; q < KU / 2u; q++) {\n"
-            "      const u32 k = k0 + 2u * q + kh;\n"
-            "      const float va = ");
-    emit_operand_expr(s, k, ct, 0, "bA", "ma", "k");
-    dsb_put(s, ";\n      const float vb = ");
-    emit_operand_expr(s, k, ct, 1, "bB", "nb", "k");
-    dsb_put(s, ";\n      a[q] = __uint_as_float(__float_as_uint(va) & ((ma < M && k < kend) ? 0xFFFFFFFFu : 0u));\n"
-               "      b[q] = __uint_as_float(__float_as_uint(vb) & ((nb < N && k < kend) ? 0xFFFFFFFFu : 0u));\n    }\n  };\n"
-               "  f32x16 acc0 = {0}, acc1 = {0}, acc2 = {0}, acc3 = {0};\n"
+    if (pl->dvec[0] || pl->dvec[1]) {
+        /* MFMA step q = 4j + t takes k = k0 + 8j + 4h + t in the lanes of
+         * half h: a lane's 4 k of a group of 8 are consecutive */
+        dsb_put(s,
+                "  float a[KU / 2u], b[KU / 2u];\n"
+                "  auto fetch = [&](u32 k0) {\n"
+                "    #pragma unroll\n"
+                "    for (u32 j = 0; j < KU / 8u; j++) {\n"
+                "      const u32 kk = k0 + 8u * j + 4u * kh;\n");
+        for (int side = 0; side < 2; side++) {
+            const char *arr = side ? "b" : "a", *base = side ? "bB" : "bA", *x = side ? "nb" : "ma",
+                       *lim = side ? "N" : "M";
+            if (pl->dvec[side]) {
+                dsb_put(s,
+                        "      {\n"
+                        "        float4 v4 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);\n"
+                        "        if (%s < %s && kk < kend) v4 = ld4(p%u, c%u, %s + kk);\n"
+                        "        %s[4u * j] = v4.x; %s[4u * j + 1u] = v4.y; %s[4u * j + 2u] = v4.z; %s[4u * j + 3u] = v4.w;\n"
+                        "      }\n",
+                        x, lim, ct->sep_buf[side], ct->sep_buf[side], base, arr, arr, arr, arr);
+            } else {
+                dsb_put(s,
+                        "      #pragma unroll\n"
+                        "      for (u32 t = 0; t < 4u; t++) {\n"
+                        "        const u32 k = kk + t;\n"
+                        "        const float v = ");
+                emit_operand_expr(s, k, ct, side, base, x, "k");
+                dsb_put(s, ";\n        %s[4u * j + t] = __uint_as_float(__float_as_uint(v) & ((%s < %s && k < kend) ? "
+                           "0xFFFFFFFFu : 0u));\n      }\n", arr, x, lim);
+            }
+        }
+        dsb_put(s, "    }\n  };\n");
+    } else {
+        dsb_put(s,
+                "  float a[KU / 2u], b[KU / 2u];\n"
+                "  auto fetch = [&](u32 k0) {\n"
+                "    #pragma unroll\n"
+                "    for (u32 q = 0; q < KU / 2u; q++) {\n"
+                "      const u32 k = k0 + 2u * q + kh;\n"
+                "      const float va = ");
+        emit_operand_expr(s, k, ct, 0, "bA", "ma", "k");
+        dsb_put(s, ";\n      const float vb = ");
+        emit_operand_expr(s, k, ct, 1, "bB", "nb", "k");
+        dsb_put(s, ";\n      a[q] = __uint_as_float(__float_as_uint(va) & ((ma < M && k < kend) ? 0xFFFFFFFFu : 0u));\n"
+                   "      b[q] = __uint_as_float(__float_as_uint(vb) & ((nb < N && k < kend) ? 0xFFFFFFFFu : 0u));\n"
+                   "    }\n  };\n");
+    }
+    dsb_put(s, "  f32x16 acc0 = {0}, acc1 = {0}, acc2 = {0}, acc3 = {0};\n"
                "  u32 k0 = kbeg + wave * KU;\n"
                "  if (k0 < kend) fetch(k0);\n"
                "  while (k0 < kend) {\n"
@@ -1922,6 +1980,11 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
     plan_chunks(ct, pl);
     plan_skinny(ct, pl);
     plan_comb(ct, pl);
+    if (pl->cfg.direct == 1 && pl->cfg.bk % 8u == 0)
+        for (int side = 0; side < 2; side++) {
+            pl->dvec[side] = direct_vec_side(ct, side);
+            pl->dvec_buf[side] = ct->sep_buf[side];
+        }
 }
 
 /* Contraction analysis without a device: returns 1 and fills M/N/K when the
@@ -2066,6 +2129,8 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     if (!e->is_dense) return 0;
     /* buffers smaller than the plan was made for: the generated kernels */
     if (e->plan.kp.on && !kperm_fits(&e->plan, counts, ptrs)) return 0;
+    for (int side = 0; side < 2; side++)
+        if (e->plan.dvec[side] && ((uintptr_t)ptrs[e->plan.dvec_buf[side]] & 15u)) return 0;
     if (e->plan.cfg.direct == 2 && e->plan.ske && e->plan.skmax != ~0ull && e->plan.skmax >= counts[e->plan.skbuf])
         return 0;
     if (e->plan.cfg.direct == 3 &&
