@@ -850,11 +850,6 @@ static void emit_skinny_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
     dsb_put(s, "  }\n}\n");
 }
 
-/* Direct kernel: a workgroup of 4 waves owns one 32x32 output block; the
- * waves take alternate KU-long steps of the workgroup's K range, each wave
- * keeping 4 independent accumulator chains and loading the next step's
- * operands before it multiplies the current ones. The 4 waves' partial blocks
- * are summed through LDS in a fixed order. */
 /* Direct kernel: a side whose k offset is k itself (one loop digit, unit
  * coefficient, no wrap below K) and whose row bases are multiples of 4 reads
  * 4 consecutive k per lane as one 16-byte load, for K a multiple of 4 (then
@@ -876,6 +871,11 @@ static int direct_vec_side(const Contraction *ct, int side) {
     return nr == 1;
 }
 
+/* Direct kernel: a workgroup of 4 waves owns one 32x32 output block; the
+ * waves take alternate KU-long steps of the workgroup's K range, each wave
+ * keeping 4 independent accumulator chains and loading the next step's
+ * operands before it multiplies the current ones. The 4 waves' partial blocks
+ * are summed through LDS in a fixed order. */
 static void emit_direct_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, const GemmPlan *pl) {
     const u32 M = ct->M, N = ct->N, K = ct->K, KU = pl->cfg.bk;
     const u32 blocks = pl->tiles_m * pl->tiles_n;
