@@ -780,8 +780,9 @@ static void emit_skinny_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
          * the block's rows of the small side from LDS */
         const u32 E = pl->ske, nblk = K / E, bpw = (nblk + KW - 1) / KW;
         char ldx[96];
-        if (pl->skmax != ~0ull)   /* the dispatch checks the buffer holds skmax */
-            snprintf(ldx, sizeof ldx, "ld_f32_u(p%u, oa + koff_p(i))", ct->sep_buf[0]);
+        if (pl->skmax != ~0ull)   /* the dispatch checks the buffer holds skmax; the block's
+                                   * 64-bit base once, its loads at constant offsets from it */
+            snprintf(ldx, sizeof ldx, "pa_[koff_p(i)]");
         else
             snprintf(ldx, sizeof ldx, "%s(p%u, c%u, oa + koff_p(i))", ld_name(ct->sep_dt[0]), ct->sep_buf[0],
                      ct->sep_buf[0]);
@@ -789,6 +790,7 @@ static void emit_skinny_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
                    "  const u32 bbeg = wave * BPW, bend = (bbeg + BPW < NBLK) ? bbeg + BPW : NBLK;\n"
                    "  for (u32 bk = bbeg; bk < bend; bk++) {\n"
                    "    const u32 kb = bk * E, oa = bA + koff_p(kb);\n"
+                   "    const float* pa_ = (const float*)p%u + oa;\n"
                    "    float a[E];\n"
                    "    #pragma unroll\n"
                    "    for (u32 i = 0; i < E; i++) a[i] = %s;\n"
@@ -798,7 +800,7 @@ static void emit_skinny_kernel(DSB *s, const UOpKernel *k, const Contraction *ct
                    "      #pragma unroll\n"
                    "      for (u32 n = 0; n < N; n++) acc[n] = fmaf(a[i], br[i * N + n], acc[n]);\n"
                    "  }\n",
-                E, nblk, bpw, ldx);
+                E, nblk, bpw, ct->sep_buf[0], ldx);
     } else {
     /* two register sets of SKU operand elements: the next set's loads are
      * issued before the current set's FMAs */
