@@ -81,11 +81,12 @@ def test_gemm_4096_plans():
 
 def test_lenet_few_channel_convolutions_are_skinny():
     # conv1 forward (6 channels), conv2 forward (16) and conv2 dX (6): a row
-    # per lane with every column sum in registers; waves split K so that
-    # about 4096 waves run in all
-    # and K walks in blocks of the 5x5 window (25), whose offsets are constants
+    # per lane with every column sum in registers; K walks in blocks of the
+    # 5x5 window (25), whose offsets are constants, and the waves of a row
+    # group split the blocks evenly, as many as keep the grid at most 8192
+    # waves (conv2: its 6 blocks on 6 waves; conv2 dX: 16 blocks on 8)
     p = _plans("lenet_b256.trc")
-    for shape, waves in [((200704, 6, 25, 1), 1), ((25600, 16, 150, 1), 8), ((50176, 6, 400, 1), 4)]:
+    for shape, waves in [((200704, 6, 25, 1), 1), ((25600, 16, 150, 1), 6), ((50176, 6, 400, 1), 8)]:
         src = p[shape]
         assert src["skinny"] and src["skinny_waves"] == waves and src["skinny_block"] == 25, (shape, src)
 

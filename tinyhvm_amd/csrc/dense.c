@@ -374,6 +374,7 @@ static const TileCfg CFG_RED = {1, 1, 1, 1, 1, 1, 1, "outer", 3};
 #define SKINNY_MAX_KN 8192   /* the small side in LDS: at most 32 KB */
 #define SKINNY_MIN_M 4096
 #define SKINNY_TARGET_WAVES 4096
+#define SKINNY_TARGET_WAVES_BLK 8192
 
 /* K-reordered affine loading of separable operands. K is split into atomic
  * digits (the finest mixed radix both operands' k offsets decompose into);
@@ -1890,6 +1891,18 @@ static void plan_skinny(const Contraction *ct, GemmPlan *pl) {
         }
         if (ok) {
             pl->ske = E;
+            /* waves per row group: a divisor of the block count (no wave
+             * without a block, every wave the same number of blocks), the
+             * largest with at most SKINNY_TARGET_WAVES_BLK waves in all
+             * (LeNet-5's conv2 input gradient: 16 blocks over 8 waves
+             * instead of 4, conv2: 6 blocks over 6 waves instead of 8) */
+            const u32 nblk = ct->K / E, rows = pl->tiles_m;
+            if (!hipb.direct_waves) {
+                u32 kw = 1;
+                for (u32 w = 1; w <= 16 && w <= nblk; w++)
+                    if (nblk % w == 0 && (u64)rows * w <= SKINNY_TARGET_WAVES_BLK) kw = w;
+                pl->nw = kw;
+            }
             return;
         }
     }
