@@ -631,10 +631,29 @@ static void emit_red_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, c
     dsb_put(s, "extern \"C\" __global__ __launch_bounds__(256) void %s(", pl->name);
     emit_params(s, k->n_leaves);
     dsb_put(s, pl->comb ? ", float* ws, unsigned long long* sl_) {\n" : ", float* ws) {\n");
+    /* the loads as buffer loads: the lane's k offset in a VGPR and the
+     * row's base (uniform) in an SGPR, so that no load needs a 64-bit
+     * address of its own; the byte offsets fit 32 bits (the dispatch checks
+     * that the buffers hold every index formed) */
+    const int bufld = pl->red_max[0] < (1ull << 30) && pl->red_max[1] < (1ull << 30);
     dsb_put(s,
             "  constexpr u32 M = %uu, N = %uu, K = %uu, MG = %uu, V = %uu, VP = %uu, KCH = %uu;\n"
             "  const u32 lane = threadIdx.x & 63u, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n"
-            "  const u32 m0 = blockIdx.x * MG, spl = blockIdx.y;\n"
+            "  const u32 m0 = blockIdx.x * MG, spl = blockIdx.y;\n",
+            M, N, K, MG, V, VP, pl->kchunk);
+    for (int sd = 0; sd < 2; sd++) {
+        const u32 b = ct->sep_buf[sd];
+        const char S = sd ? 'Q' : 'P';
+        if (bufld)
+            dsb_put(s, "  const __amdgpu_buffer_rsrc_t r%c_ = __builtin_amdgcn_make_buffer_rsrc((void*)p%u, (short)0,\n"
+                       "      (int)((unsigned long long)c%u * 4ull < 0xFFFFFFFFull ? c%u * 4u : 0xFFFFFFFFu), 0x00020000);\n"
+                       "  auto LD%c_ = [&](u32 base, u32 off) {\n"
+                       "    return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r%c_, (int)(off * 4u), (int)(base * 4u), 0));\n"
+                       "  };\n", S, b, b, b, S, S);
+        else
+            dsb_put(s, "  auto LD%c_ = [&](u32 base, u32 off) { return ld_f32_u(p%u, base + off); };\n", S, b);
+    }
+    dsb_put(s,
             "  const u32 kbeg = spl * KCH, kend = (kbeg + KCH < K) ? kbeg + KCH : K;\n"
             "  u32 rb[MG];\n"
             "  #pragma unroll\n"
@@ -647,9 +666,9 @@ static void emit_red_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, c
             "    const u32 op = koff_p(k), oq = koff_q(k);\n"
             "    float a[MG], b[N];\n"
             "    #pragma unroll\n"
-            "    for (u32 i = 0; i < MG; i++) a[i] = (m0 + i < M) ? ld_f32_u(p%u, rb[i] + op) : 0.0f;\n"
+            "    for (u32 i = 0; i < MG; i++) a[i] = (m0 + i < M) ? LDP_(rb[i], op) : 0.0f;\n"
             "    #pragma unroll\n"
-            "    for (u32 n = 0; n < N; n++) b[n] = ld_f32_u(p%u, rowb_q(gid_n(n)) + oq);\n"
+            "    for (u32 n = 0; n < N; n++) b[n] = LDQ_(rowb_q(gid_n(n)), oq);\n"
             "    #pragma unroll\n"
             "    for (u32 i = 0; i < MG; i++)\n"
             "      #pragma unroll\n"
@@ -673,8 +692,7 @@ static void emit_red_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, c
             "    }\n"
             "    __syncthreads();\n"
             "  }\n"
-            "  __syncthreads();\n",
-            M, N, K, MG, V, VP, pl->kchunk, ct->sep_buf[0], ct->sep_buf[1]);
+            "  __syncthreads();\n");
     if (pl->comb) {
         char fb[64];
         const char *st;
