@@ -860,6 +860,7 @@ static void read_dense_env(void) {
     hipb.dense_nored = env_flag("THVM_HIP_DENSE_NORED");
     hipb.dense_nocomb = env_flag("THVM_HIP_DENSE_NOCOMB");
     hipb.dense_nowave = env_flag("THVM_HIP_DENSE_NOWAVE");
+    hipb.dense_notail = env_flag("THVM_HIP_DENSE_NOTAIL");
     hipb.no_fuse = env_flag("THVM_HIP_NO_FUSE");
     hipb.host_profile = env_flag("THVM_HIP_HOST_PROFILE");
     hipb.dense_pack = env_flag("THVM_HIP_DENSE_PACK");

@@ -425,6 +425,10 @@ typedef struct {
     u32 red_mg;            /* outer-product reduction: rows per group */
     u64 red_max[2];        /* ... the largest index each side forms (unchecked loads) */
     u32 red_buf[2];        /* ... and the buffer it reads (1 + leaf) */
+    u32 tail_full;         /* wave tile: tiles run whole, tail_s per workgroup (a multiple of the SIMD
+                              count); each of the rest is split over the tail_s waves of a workgroup */
+    u32 tail_s;            /* ... in K chunks, added through LDS; 0 = one wave per workgroup, no split */
+    u32 tail_pf;           /* ... whose k-pairs go through a ring of tail_pf loads */
     int dvec[2];           /* direct kernel: side s read 4 consecutive k per lane with one 16-byte load */
     u32 dvec_buf[2];       /* ... from this buffer (p<b>) */
     int comb;              /* direct and outer-product kernels: split-K partials combined in the
@@ -441,6 +445,7 @@ static u32 dense_cus(void) { return hipb.n_cu ? hipb.n_cu : 256u; }
 
 /* workgroup size of a plan's main kernel */
 static u32 dense_threads(const GemmPlan *pl) {
+    if (pl->cfg.direct == 4) return 64u * (pl->tail_s ? pl->tail_s : 1u);
     return pl->cfg.direct == 3 ? GEMM_THREADS : pl->cfg.direct ? 64u * pl->nw : GEMM_THREADS;
 }
 
@@ -1052,18 +1057,35 @@ static void emit_wave_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, 
     const char *mf_a1 = pl->swap ? "rb1[q]" : "ra[q]", *mf_b1 = pl->swap ? "ra[q]" : "rb1[q]";
     /* at least six waves per SIMD: the register budget the compiler keeps
      * to (measured 141 against 145 us with four or five) */
-    dsb_put(s, "extern \"C\" __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(6, 8))) void %s(",
-            pl->name);
+    const u32 S = pl->tail_s ? pl->tail_s : 1u;
+    dsb_put(s, "extern \"C\" __global__ __launch_bounds__(%u) __attribute__((amdgpu_waves_per_eu(6, 8))) void %s(",
+            64u * S, pl->name);
     emit_params(s, k->n_leaves);
     dsb_put(s, ", float* ws, const float* pk%s) {\n", g_epi_params ? g_epi_params : "");
     dsb_put(s,
             "  constexpr u32 M = %uu, N = %uu, KP = %uu, PF = %uu, TILES = %uu, ICA = %uu;\n"
+            "  constexpr u32 S = %uu, FULL = %uu, NFW = FULL / S, KPC = KP / S, PFT = %uu;\n"
             "  const u32 lane = threadIdx.x & 63u, h = lane >> 5;\n"
-            "  u32 tile = blockIdx.x;\n"
-            "  if (tile >= TILES) return;\n"
-            "  /* workgroup b runs on XCD b %% 8: consecutive tiles (rows that share\n"
-            "   * their neighbourhood of A) on one XCD's L2 */\n"
-            "  if (TILES %% 8u == 0u) tile = (tile %% 8u) * (TILES / 8u) + tile / 8u;\n"
+            "  const u32 wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n"
+            "  u32 tile = blockIdx.x, kp0 = 0u;\n"
+            "  bool tail = false;\n"
+            "  if (S > 1u && tile >= NFW) {\n"
+            "    /* the tiles past FULL (fewer than one per SIMD): each split over\n"
+            "     * the S waves of one workgroup in K chunks of KPC k-pairs, so that\n"
+            "     * no SIMD gets a whole extra tile */\n"
+            "    tile = FULL + (tile - NFW);\n"
+            "    if (tile >= TILES) return;\n"
+            "    kp0 = wave * KPC;\n"
+            "    tail = true;\n"
+            "  } else if (S > 1u) {\n"
+            "    /* workgroup b runs on XCD b %% 8: consecutive tiles (rows that share\n"
+            "     * their neighbourhood of A) on one XCD's L2 */\n"
+            "    if (NFW %% 8u == 0u) tile = (tile %% 8u) * (NFW / 8u) + tile / 8u;\n"
+            "    tile = tile * S + wave;\n"
+            "  } else {\n"
+            "    if (tile >= TILES) return;\n"
+            "    if (TILES %% 8u == 0u) tile = (tile %% 8u) * (TILES / 8u) + tile / 8u;\n"
+            "  }\n"
             "  const u32 m0 = tile * 32u, n0 = 0u, wm = 0u, wn = 0u;\n"
             "  const u32 ma = (m0 + (lane & 31u) < M) ? m0 + (lane & 31u) : M - 1u;\n"
             "  const __amdgpu_buffer_rsrc_t rA = __builtin_amdgcn_make_buffer_rsrc((void*)p%u, (short)0,\n"
@@ -1081,25 +1103,67 @@ static void emit_wave_kernel(DSB *s, const UOpKernel *k, const Contraction *ct, 
             "  f32x16 acc[2];\n"
             "  acc[0] = (f32x16){0};\n"
             "  acc[1] = (f32x16){0};\n"
-            "  #pragma unroll\n"
-            "  for (u32 q = 0; q < PF; q++) load(q, q);\n"
-            "  for (u32 kb = 0; kb + PF < KP; kb += PF) {\n"
+            "  if (!tail) {\n"
+            "    #pragma unroll\n"
+            "    for (u32 q = 0; q < PF; q++) load(q, q);\n"
+            "    for (u32 kb = 0; kb + PF < KP; kb += PF) {\n"
+            "      #pragma unroll\n"
+            "      for (u32 q = 0; q < PF; q++) {\n"
+            "        acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[0], 0, 0, 0);\n"
+            "        acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[1], 0, 0, 0);\n"
+            "        load(kb + PF + q, q);\n"
+            "        /* each step's loads go out right after its MFMAs: PF k-pairs ahead */\n"
+            "        __builtin_amdgcn_sched_barrier(0);\n"
+            "      }\n"
+            "    }\n"
             "    #pragma unroll\n"
             "    for (u32 q = 0; q < PF; q++) {\n"
             "      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[0], 0, 0, 0);\n"
             "      acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[1], 0, 0, 0);\n"
-            "      load(kb + PF + q, q);\n"
-            "      /* each step's loads go out right after its MFMAs: PF k-pairs ahead */\n"
-            "      __builtin_amdgcn_sched_barrier(0);\n"
             "    }\n"
-            "  }\n"
-            "  #pragma unroll\n"
-            "  for (u32 q = 0; q < PF; q++) {\n"
-            "    acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[0], 0, 0, 0);\n"
-            "    acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[1], 0, 0, 0);\n"
             "  }\n",
-            M, N, KPAIRS, PF, tiles, kp->icoef[0], ct->sep_buf[0], ct->sep_buf[0], ct->sep_buf[0],
+            M, N, KPAIRS, PF, tiles, kp->icoef[0], S, pl->tail_full, pl->tail_pf ? pl->tail_pf : 1u,
+            ct->sep_buf[0], ct->sep_buf[0], ct->sep_buf[0],
             kp->Kl * N, mf_a, mf_b, mf_a1, mf_b1, mf_a, mf_b, mf_a1, mf_b1);
+    if (S > 1u)
+        /* a tail chunk: its KPC k-pairs through the first PFT slots of the
+         * ring; then waves 1..S-1 hand their partials to wave 0 through LDS
+         * one after the other, and wave 0 adds them in wave (chunk) order
+         * and makes the stores */
+        dsb_put(s,
+                "  __shared__ float tl_[32][64];\n"
+                "  if (tail) {\n"
+                "    #pragma unroll\n"
+                "    for (u32 q = 0; q < PFT; q++) load(kp0 + q, q);\n"
+                "    for (u32 kb = kp0; kb + PFT < kp0 + KPC; kb += PFT) {\n"
+                "      #pragma unroll\n"
+                "      for (u32 q = 0; q < PFT; q++) {\n"
+                "        acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[0], 0, 0, 0);\n"
+                "        acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[1], 0, 0, 0);\n"
+                "        load(kb + PFT + q, q);\n"
+                "        __builtin_amdgcn_sched_barrier(0);\n"
+                "      }\n"
+                "    }\n"
+                "    #pragma unroll\n"
+                "    for (u32 q = 0; q < PFT; q++) {\n"
+                "      acc[0] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[0], 0, 0, 0);\n"
+                "      acc[1] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[1], 0, 0, 0);\n"
+                "    }\n"
+                "    for (u32 j = 1u; j < S; j++) {\n"
+                "      if (wave == j) {\n"
+                "        #pragma unroll\n"
+                "        for (u32 v = 0; v < 16u; v++) { tl_[v][lane] = acc[0][v]; tl_[16u + v][lane] = acc[1][v]; }\n"
+                "      }\n"
+                "      __syncthreads();\n"
+                "      if (wave == 0u) {\n"
+                "        #pragma unroll\n"
+                "        for (u32 v = 0; v < 16u; v++) { acc[0][v] = acc[0][v] + tl_[v][lane]; acc[1][v] = acc[1][v] + tl_[16u + v][lane]; }\n"
+                "      }\n"
+                "      __syncthreads();\n"
+                "    }\n"
+                "    if (wave != 0u) return;\n"
+                "  }\n",
+                mf_a, mf_b, mf_a1, mf_b1, mf_a, mf_b, mf_a1, mf_b1);
     /* the LDS tile's epilogue: blocks (m, n) = (0, 0) and (0, 32) of the wave's tile */
     dsb_put(s,
             "  #pragma unroll\n"
@@ -1949,6 +2013,34 @@ static void plan_comb(const Contraction *ct, GemmPlan *pl) {
     else if (pl->cfg.direct == 3) pl->comb = (u64)(pl->splits - 1) * pl->red_mg * ct->N <= COMB_RED_LDS_FLOATS;
 }
 
+/* Wave tile: its grid is one wave per 32-row tile, and the waves of a SIMD
+ * share its matrix pipe, so the kernel takes as long as the SIMD with the
+ * most tiles. With S waves per workgroup, the tiles up to the largest
+ * multiple of the SIMD count run whole (S per workgroup) and each of the
+ * rest (fewer than one per SIMD) is split over the S waves of a workgroup in
+ * K chunks, added through LDS in chunk order: on the 3x3 64->64 convolution
+ * at batch 64, 6272 tiles on 1024 SIMDs are 6144 whole tiles and 128 tiles in
+ * 4 chunks, at most 6.25 tiles of work per SIMD instead of 7. */
+static void plan_wave_tail(GemmPlan *pl) {
+    pl->tail_full = pl->tail_s = pl->tail_pf = 0;
+    if (hipb.dense_notail) return;
+    const u32 simds = 4u * dense_cus(), tiles = pl->tiles_m * pl->tiles_n, kpairs = pl->kp.Kl / 2u;
+    const u32 full = tiles / simds * simds, rem = tiles - full;
+    if (!full || !rem) return;
+    for (u32 S = 4u; S >= 2u; S /= 2u) {
+        if (full % (8u * S) || kpairs % S) continue;
+        const u32 kpc = kpairs / S;
+        u32 pft = 0;
+        for (u32 d = wave_ring(kpairs); d >= 2u && !pft; d--)
+            if (kpc % d == 0) pft = d;
+        if (!pft) continue;
+        pl->tail_full = full;
+        pl->tail_s = S;
+        pl->tail_pf = pft;
+        return;
+    }
+}
+
 static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     static const TileCfg *forced[12] = {NULL, &CFG_BIG, &CFG_MID, &CFG_TALL, &CFG_WIDE, &CFG_DIRECT, &CFG_C64,
                                         &CFG_C64S, &CFG_SKINNY, &CFG_RED, &CFG_C64W, &CFG_WAVE};
@@ -1964,11 +2056,15 @@ static void make_plan(const Contraction *ct, GemmPlan *pl, u64 sig) {
     if (!forced_ok && !hipb.dense_nored && red_fits && ct->K >= RED_MIN_K) cfg = CFG_RED;
     if (!forced_ok && !hipb.dense_nowave && ct->N == 64 && ct->M >= 4096 && !long_k(ct->M, ct->N, ct->K)) {
         make_plan_cfg(ct, pl, sig, &CFG_WAVE);
-        if (wave_plan_ok(ct, pl)) return;
+        if (wave_plan_ok(ct, pl)) {
+            plan_wave_tail(pl);
+            return;
+        }
     }
     if (cfg.direct == 4) cfg = CFG_MID;
     make_plan_cfg(ct, pl, sig, &cfg);
     if (pl->cfg.direct == 4 && !wave_plan_ok(ct, pl)) make_plan_cfg(ct, pl, sig, &CFG_MID);
+    if (pl->cfg.direct == 4) plan_wave_tail(pl);
 }
 
 static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const TileCfg *cfg) {
@@ -2220,7 +2316,10 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     if (!held && e->kcopy && e->co.src && e->co.lds <= EPI_SOLO_MAX_LDS)
         held = hipb_hold_solo(&e->co, e->fn, tiles, e->plan.splits, params, &hm);
     if (!held) {
-        if (!hipb_launch_grid(e->fn, tiles, e->plan.splits, threads, params)) return 0;
+        /* wave tile with split tail tiles: S whole tiles per workgroup, then a
+         * workgroup per split tile */
+        const u32 gx = e->plan.tail_s ? e->plan.tail_full / e->plan.tail_s + (tiles - e->plan.tail_full) : tiles;
+        if (!hipb_launch_grid(e->fn, gx, e->plan.splits, threads, params)) return 0;
     } else if (e->kcopy && !ws) {
         /* held: the next dispatch may fuse into its epilogue */
         hipb_hold_tag(key, e->serial, out_buf);

@@ -63,6 +63,7 @@ typedef struct {
     int dense_nored;         /* THVM_HIP_DENSE_NORED: no outer-product reduction kernel */
     int dense_nocomb;        /* THVM_HIP_DENSE_NOCOMB: split-K partials always through a sum kernel */
     int dense_nowave;        /* THVM_HIP_DENSE_NOWAVE: no LDS-free wave-tile kernel for 64-column contractions */
+    int dense_notail;        /* THVM_HIP_DENSE_NOTAIL: the wave tile's last tiles are not split */
     int no_fuse;             /* THVM_HIP_NO_FUSE: no elementwise consumer fused into a contraction's epilogue */
     u32 direct_min_chunk;    /* THVM_HIP_DIRECT_MIN_CHUNK: shortest K chunk of a direct-kernel split (0: chosen) */
     int dense_pack;          /* THVM_HIP_DENSE_PACK: pack wherever the layout allows (tests) */
