@@ -19,13 +19,15 @@ A step is one replay of the engine's recorded Backend calls for a workload
 
 lenet, mlp and convblock are also captured once into a HIP graph and timed as
 graph launches (one launch = one whole step): `graph_value` beside `value`
-(the replayed step). These steps keep the GPU busy, so a graph saves little:
-it is slower for the small MLP and LeNet kernels and 4 % faster for the conv
-block.
+(the replayed step).
 
 roofline: the dominant kernel's algorithmic bytes (or FLOPs) per launch / its
-average duration, from HIP events on the backend's stream around that one
-dispatch; `traffic` comes from the committed rocprofv3 counter summary.
+average duration, from HIP events on the backend's stream: around that one
+dispatch for the HBM-bound kernels, around the contraction's main kernel
+alone for the matrix-core ones (thvm_hip_time_contraction; the kernel that
+rocprof's statistics name, without the operand pack or split-K sum kernel of
+the same dispatch, which `kernels_ms` includes and `main_kernels_ms` does
+not); `traffic` comes from the committed rocprofv3 counter summary.
 cpu_baseline: the engine's own CPU backend (oracle/_ref/ref_replay, built from
 the engine sources) on one host core, on the same trace or a stated slice;
 LeNet and the conv block replay with every buffer in a zero-filled guard
@@ -291,23 +293,35 @@ def run_workload(L, name, steps, warmup, want_cpu):
     step_s = wall / steps
     # pass 2: events around each listed dispatch on the backend stream
     disp = [j for j in range(lo, hi) if L.thvm_trace_tag(t, j) in (TAG_UOP, TAG_RS)]
-    k_ms = {}
+    k_ms, km_ms = {}, {}
     if wl["kernels"]:
         ev = {o: (hip.event(), hip.event()) for o in wl["kernels"]}
+        # matrix-core workloads: a second pair of events right around each
+        # contraction's main kernel (thvm_hip_time_contraction), the kernel
+        # the roofline and the rocprof statistics name; the dispatch's pair
+        # also holds its pack or split-K sum kernel
+        evm = {o: (hip.event(), hip.event()) for o in wl["kernels"]} if wl["bound"] == "mfma" else {}
         for _ in range(steps):
             prev = lo
             for o in sorted(ev):
                 u = disp[o]
                 L.thvm_trace_replay(t, be, prev, u, SKIP_READS)
                 hip.record(ev[o][0])
+                if o in evm:
+                    L.thvm_hip_time_contraction(evm[o][0], evm[o][1])
                 L.thvm_trace_replay(t, be, u, u + 1, SKIP_READS)
+                if o in evm:
+                    assert L.thvm_hip_time_contraction(None, None) == 1, "%s: dispatch %d is no contraction" % (name, o)
                 hip.record(ev[o][1])
                 prev = u + 1
             L.thvm_trace_replay(t, be, prev, hi, SKIP_READS)
             for o, (ea, eb) in ev.items():
                 nm = wl["kernels"][o][0]
                 k_ms[nm] = k_ms.get(nm, 0.0) + hip.ms(ea, eb)
+                if o in evm:
+                    km_ms[nm] = km_ms.get(nm, 0.0) + hip.ms(*evm[o])
         k_ms = {k: v / steps for k, v in k_ms.items()}
+        km_ms = {k: v / steps for k, v in km_ms.items()}
     assert L.thvm_hip_synchronize() == 0
     gpu_ms_eager = gpu_ms
     # pass 3: the step captured once into a HIP graph, launched `steps` times
@@ -338,6 +352,8 @@ def run_workload(L, name, steps, warmup, want_cpu):
     res = {"value": None, "unit": wl["unit"], "ms_per_step": round(step_s * 1e3, 4),
            "gpu_ms_per_step": round(gpu_ms_eager / steps, 4), "config": wl["config"],
            "kernels_ms": {k: round(v, 4) for k, v in k_ms.items()}}
+    if km_ms:
+        res["main_kernels_ms"] = {k: round(v, 4) for k, v in km_ms.items()}
     if graph_s is not None:
         res["graph_ms_per_step"] = round(graph_s * 1e3, 4)
         res["graph_gpu_ms_per_step"] = round(gpu_ms / steps, 4)
@@ -358,7 +374,7 @@ def run_workload(L, name, steps, warmup, want_cpu):
         if wl["bound"] == "hbm":
             ach, peak, unit = dom_w / (k_ms[dom] * 1e-3) / 1e9, HBM_PEAK_GBS, "GB/s"
         else:
-            ach, peak, unit = dom_w / (k_ms[dom] * 1e-3) / 1e12, MFMA_F32_PEAK_TFLOPS, "TFLOP/s"
+            ach, peak, unit = dom_w / (km_ms.get(dom, k_ms[dom]) * 1e-3) / 1e12, MFMA_F32_PEAK_TFLOPS, "TFLOP/s"
         res["roofline"] = {"bound": wl["bound"], "achieved": round(ach, 2), "peak": peak,
                            "unit": unit, "frac": round(ach / peak, 4),
                            "traffic": measured_traffic(wl.get("profile"), dom), "kernel": dom}
@@ -545,6 +561,8 @@ def main():
         "kernels_ms": head.get("kernels_ms"),
         "workloads": {nm: r for nm, r in results.items() if nm != names[0]},
     }
+    if head.get("main_kernels_ms"):
+        out["main_kernels_ms"] = head["main_kernels_ms"]
     print(json.dumps(out))
 
 

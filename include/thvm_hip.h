@@ -247,6 +247,16 @@ int  thvm_hip_group_compile_check(const UOpKernel *const *ks, const u32 *const *
 int  thvm_hip_group_source(const UOpKernel *const *ks, const u32 *const *bufs, u32 n, int producer, char *buf,
                            u64 buflen);
 
+/* Timing of one matrix-core kernel: with two hipEvent_t, the next
+ * contraction dispatch records ev_begin on the backend stream right before
+ * its main kernel and ev_end right after it (the kernel then goes out on its
+ * own instead of in a batch; a pack or split-K sum kernel of the same
+ * dispatch stays outside the pair). NULL, NULL disarms. Returns 1 if the
+ * previous pair was recorded, 0 if not, -1 before thvm_hip_init. For
+ * benchmarks (the rocprof kernel statistics name the same kernel); no
+ * counterpart in the reference. */
+int  thvm_hip_time_contraction(void *ev_begin, void *ev_end);
+
 /* Source of the upload kernel (main kernel thvm_upload, 256 lanes): host
  * writes of at most 64 KiB reach the device through it, read from pinned
  * coherent host memory, and it joins a batch launch with independent held

@@ -82,6 +82,7 @@ def lib():
                                                    cp, u64]),
         "thvm_hip_group_compile_check": (C.c_int, [C.POINTER(C.POINTER(abi.UOpKernel)), C.POINTER(PU32), u32,
                                                    C.c_int, cp, u64]),
+        "thvm_hip_time_contraction": (C.c_int, [vp, vp]),
         "thvm_hip_upload_source": (C.c_int, [cp, u64]),
         "thvm_hip_group_source": (C.c_int, [C.POINTER(C.POINTER(abi.UOpKernel)), C.POINTER(PU32), u32, C.c_int,
                                             cp, u64]),
@@ -121,7 +122,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_dense_analyze", "thvm_hip_dense_compile_check", "thvm_hip_dense_source",
     "thvm_hip_window_analyze", "thvm_hip_window_source", "thvm_hip_window_compile_check",
     "thvm_hip_batch_compile_check", "thvm_hip_flush", "thvm_hip_epilogue_compile_check", "thvm_hip_chain_merge",
-    "thvm_hip_group_compile_check", "thvm_hip_group_source", "thvm_hip_upload_source",
+    "thvm_hip_group_compile_check", "thvm_hip_group_source", "thvm_hip_upload_source", "thvm_hip_time_contraction",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
     "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",

@@ -861,6 +861,11 @@ static void read_dense_env(void) {
     hipb.dense_nocomb = env_flag("THVM_HIP_DENSE_NOCOMB");
     hipb.dense_nowave = env_flag("THVM_HIP_DENSE_NOWAVE");
     hipb.dense_notail = env_flag("THVM_HIP_DENSE_NOTAIL");
+    {
+        const char *ts = getenv("THVM_HIP_WAVE_TAIL_S");
+        const long v = ts ? strtol(ts, NULL, 10) : 0;
+        hipb.wave_tail_s = (v == 2 || v == 4 || v == 8) ? (u32)v : 0u;
+    }
     hipb.no_fuse = env_flag("THVM_HIP_NO_FUSE");
     hipb.host_profile = env_flag("THVM_HIP_HOST_PROFILE");
     hipb.dense_pack = env_flag("THVM_HIP_DENSE_PACK");
@@ -2053,6 +2058,15 @@ int thvm_hip_epilogue_compile_check(const UOpKernel *producer, const UOpKernel *
     free(src);
     if (n < 0 && errbuf && errlen) snprintf(errbuf, errlen, "%s", err);
     return (int)n;
+}
+
+int thvm_hip_time_contraction(void *ev_begin, void *ev_end) {
+    if (!hipb.initialized) return -1;
+    const int fired = hipb.time_fired;
+    hipb.time_fired = 0;
+    hipb.time_ev[0] = ev_begin && ev_end ? ev_begin : NULL;
+    hipb.time_ev[1] = ev_begin && ev_end ? ev_end : NULL;
+    return fired;
 }
 
 int thvm_hip_upload_source(char *buf, u64 buflen) {

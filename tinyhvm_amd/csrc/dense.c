@@ -2027,7 +2027,7 @@ static void plan_wave_tail(GemmPlan *pl) {
     const u32 simds = 4u * dense_cus(), tiles = pl->tiles_m * pl->tiles_n, kpairs = pl->kp.Kl / 2u;
     const u32 full = tiles / simds * simds, rem = tiles - full;
     if (!full || !rem) return;
-    for (u32 S = 4u; S >= 2u; S /= 2u) {
+    for (u32 S = hipb.wave_tail_s ? hipb.wave_tail_s : 4u; S >= 2u; S /= 2u) {
         if (full % (8u * S) || kpairs % S) continue;
         const u32 kpc = kpairs / S;
         u32 pft = 0;
@@ -2308,18 +2308,31 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
     hbm_add(&hm, ws ? (void *)ws : ptrs[0], ws ? wsb : pool_bytes(out_buf), 1);
     for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++)
         hbm_add(&hm, pool_ptr(leaf_bufs[i]), pool_bytes(leaf_bufs[i]), 0);
-    int held = !e->plan.pack && hipb_hold(&e->co, e->fn, tiles, e->plan.splits, params, &hm, sl != NULL,
-                                          sl ? (int)(2 * nb + 1) : -1, sl ? (u64)e->plan.splits * mn : 0);
+    /* a timed contraction (thvm_hip_time_contraction) goes out on its own,
+     * between its two events */
+    const int timed = hipb.time_ev[0] != NULL;
+    int held = !timed && !e->plan.pack && hipb_hold(&e->co, e->fn, tiles, e->plan.splits, params, &hm, sl != NULL,
+                                                    sl ? (int)(2 * nb + 1) : -1, sl ? (u64)e->plan.splits * mn : 0);
     /* a larger launch that an elementwise consumer may still fuse into is
      * held alone if its workgroups use little LDS (the fused module adds no
      * LDS; big LDS tiles are the headline GEMMs, left as they are) */
-    if (!held && e->kcopy && e->co.src && e->co.lds <= EPI_SOLO_MAX_LDS)
+    if (!held && !timed && e->kcopy && e->co.src && e->co.lds <= EPI_SOLO_MAX_LDS)
         held = hipb_hold_solo(&e->co, e->fn, tiles, e->plan.splits, params, &hm);
     if (!held) {
         /* wave tile with split tail tiles: S whole tiles per workgroup, then a
          * workgroup per split tile */
         const u32 gx = e->plan.tail_s ? e->plan.tail_full / e->plan.tail_s + (tiles - e->plan.tail_full) : tiles;
-        if (!hipb_launch_grid(e->fn, gx, e->plan.splits, threads, params)) return 0;
+        if (timed) {
+            hipb_before_stream();
+            HIPB_CHECK(hipEventRecord((hipEvent_t)hipb.time_ev[0], hipb.stream));
+        }
+        const int ok = hipb_launch_grid(e->fn, gx, e->plan.splits, threads, params);
+        if (timed) {
+            HIPB_CHECK(hipEventRecord((hipEvent_t)hipb.time_ev[1], hipb.stream));
+            hipb.time_ev[0] = hipb.time_ev[1] = NULL;
+            hipb.time_fired = 1;
+        }
+        if (!ok) return 0;
     } else if (e->kcopy && !ws) {
         /* held: the next dispatch may fuse into its epilogue */
         hipb_hold_tag(key, e->serial, out_buf);

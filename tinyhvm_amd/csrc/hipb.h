@@ -64,6 +64,7 @@ typedef struct {
     int dense_nocomb;        /* THVM_HIP_DENSE_NOCOMB: split-K partials always through a sum kernel */
     int dense_nowave;        /* THVM_HIP_DENSE_NOWAVE: no LDS-free wave-tile kernel for 64-column contractions */
     int dense_notail;        /* THVM_HIP_DENSE_NOTAIL: the wave tile's last tiles are not split */
+    u32 wave_tail_s;         /* THVM_HIP_WAVE_TAIL_S: waves per workgroup of the split (2, 4, 8; 0 = 4) */
     int no_fuse;             /* THVM_HIP_NO_FUSE: no elementwise consumer fused into a contraction's epilogue */
     u32 direct_min_chunk;    /* THVM_HIP_DIRECT_MIN_CHUNK: shortest K chunk of a direct-kernel split (0: chosen) */
     int dense_pack;          /* THVM_HIP_DENSE_PACK: pack wherever the layout allows (tests) */
@@ -90,6 +91,8 @@ typedef struct {
     u32 n_cu;                /* compute units (256 on MI355X; assumed where no device is open) */
     void *noalloc_scratch;   /* device address of the static workspace (noalloc.hip), or NULL */
     int noalloc;             /* a no-allocation dispatch is running: workspaces come from it */
+    void *time_ev[2];        /* events to record around the next contraction's main kernel, or NULL */
+    int time_fired;          /* they were recorded */
     u64 noalloc_off;         /* bytes of the static workspace handed out in that dispatch */
     int noalloc_err;         /* why that dispatch could not run (THVM_HIP_E*), or 0 */
     u32 *comb_err_host;      /* host-mapped word a single-pass combine sets when it gave up waiting */
