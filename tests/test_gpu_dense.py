@@ -74,3 +74,65 @@ def test_trace_parity_matrix_cores(hip_dense, path):
     assert not bad, "kernel parity: %s" % bad
     bad_e2e = [r for r in e2e if not r[1]]
     assert not bad_e2e, "end-to-end vs reference: %s" % bad_e2e
+
+
+def test_contraction_timing_events():
+    """thvm_hip_time_contraction: armed with two events, the next contraction
+    dispatch records them on the backend stream around its main kernel (it
+    reports 1 when disarmed after it, and the pair measures a positive
+    time); a dispatch that is no contraction leaves them unrecorded (0). The
+    buffers after the step match a run without the events bit for bit."""
+    import ctypes as C
+    from tinyhvm_amd import trace
+    path = os.path.join(tt.ROOT, "tests", "golden", "mlp_64x784x128x10.trc")
+    sizes = {r.f["id"]: r.f["bytes"] for r in trace.read_trace(path) if r.tag == trace.ALLOC}
+    hip = C.CDLL("libamdhip64.so")
+    hip.hipEventCreate.argtypes = [C.POINTER(C.c_void_p)]
+    hip.hipEventSynchronize.argtypes = [C.c_void_p]
+    hip.hipEventElapsedTime.argtypes = [C.POINTER(C.c_float), C.c_void_p, C.c_void_p]
+    hip.hipEventDestroy.argtypes = [C.c_void_p]
+    L = _lib.lib()
+
+    def run(timed):
+        L.thvm_hip_shutdown()
+        assert L.thvm_hip_init() == 0
+        rp = tt.Replay(path, L.thvm_hip_backend())
+        fired, ms = [], []
+        try:
+            for i in range(rp.n):
+                k = rp.kernel(i) if rp.tag(i) == trace.UOP else None
+                if not (timed and k is not None):
+                    rp.run(i, i + 1)
+                    continue
+                ea, eb = C.c_void_p(), C.c_void_p()
+                assert hip.hipEventCreate(C.byref(ea)) == 0 and hip.hipEventCreate(C.byref(eb)) == 0
+                assert L.thvm_hip_time_contraction(ea, eb) == 0
+                rp.run(i, i + 1)
+                f = L.thvm_hip_time_contraction(None, None)
+                fired.append((bool(_lib.dense_analyze(k)), f))
+                if f == 1:
+                    assert hip.hipEventSynchronize(eb) == 0
+                    t = C.c_float()
+                    assert hip.hipEventElapsedTime(C.byref(t), ea, eb) == 0
+                    ms.append(t.value)
+                hip.hipEventDestroy(ea)
+                hip.hipEventDestroy(eb)
+            assert L.thvm_hip_synchronize() == 0
+            outs = {}
+            for tid, n in sizes.items():
+                live = rp.live(tid)
+                if live:
+                    buf = (C.c_uint8 * n)()
+                    L.thvm_hip_buf_read(live, buf, n)
+                    outs[tid] = bytes(buf)
+            return fired, ms, outs
+        finally:
+            rp.close()
+
+    fired, ms, got = run(True)
+    _f, _m, want = run(False)
+    L.thvm_hip_shutdown()
+    assert any(c for c, _ in fired) and any(not c for c, _ in fired), fired
+    assert all(f == (1 if c else 0) for c, f in fired), fired
+    assert ms and all(t > 0.0 for t in ms), ms
+    assert got.keys() == want.keys() and got == want

@@ -543,11 +543,15 @@ int hipb_hold_upload(void *dst, u64 dst_bytes, const void *src_dev, u64 bytes) {
 /* at backend init (a module cannot be set up inside a graph capture);
  * without it uploads are copies */
 static void upload_prepare(void) {
-    if (UPK.fn || hipb.no_batch) return;
+    if (UPK.fn || hipb.no_batch || hipb.rtc_fail) return;
     char *src = upload_source();
     char err[256] = {0};
     if (!src) return;
-    if (rtc_build_module(src, &UPK.mod, err, sizeof err)) {
+    /* backend machinery, not a dispatched program: not in the compile count */
+    const u64 n_compile = hipb.n_compile;
+    const int built = rtc_build_module(src, &UPK.mod, err, sizeof err);
+    hipb.n_compile = n_compile;
+    if (built) {
         if (hipModuleGetFunction(&UPK.fn, UPK.mod, "thvm_upload") != hipSuccess ||
             !co_form_make(&UPK.co, src, "thvm_upload", 256, UPK.fn)) {
             (void)hipGetLastError();
