@@ -39,6 +39,7 @@ def _plans(name):
         kw = re.search(r"KW = (\d+)u, KCW", src)
         ke = re.search(r"constexpr u32 E = (\d+)u, NBLK", src)
         ro = re.search(r"MG = (\d+)u, V = \d+u, VP = \d+u, KCH = (\d+)u", src)
+        tl = re.search(r"constexpr u32 S = (\d+)u, FULL = (\d+)u, NFW = FULL / S, KPC = KP / S, PFT = (\d+)u", src)
         out[a] = {
             "tile": (int(cst.group(1)), int(cst.group(2))) if cst else "direct",
             "kperm": "kbase_p(" in src,
@@ -54,6 +55,7 @@ def _plans(name):
             "skinny_block": int(ke.group(1)) if ke else None,
             "outer": (int(ro.group(1)), int(ro.group(2))) if ro else None,
             "comb": "comb_pub(sl_" in src,
+            "tail": (int(tl.group(2)), int(tl.group(1)), int(tl.group(3))) if tl else None,
         }
     return out
 
@@ -106,3 +108,13 @@ def test_lenet_fc_weight_gradients_use_eight_waves():
     for shape in [(400, 120, 256, 1), (120, 84, 256, 1), (84, 10, 256, 1)]:
         assert p[shape]["tile"] == "direct" and p[shape]["waves"] == 8, (shape, p[shape])
 
+
+
+def test_conv_wave_tile_splits_its_last_tiles():
+    # the 3x3 64->64 convolution at batch 64 (forward and dX): 6272 wave
+    # tiles on 1024 SIMDs; 6144 run whole, 4 to a workgroup, and the last
+    # 128 are split over the 4 waves of a workgroup in K chunks of 72
+    # k-pairs (a ring of 8 loads), so that no SIMD gets a seventh tile
+    p = _plans("convblock_b64.trc")
+    hit = [v for a, v in p.items() if a[:3] == (200704, 64, 576)]
+    assert hit and all(v["tail"] == (6144, 4, 8) for v in hit), hit
