@@ -93,3 +93,24 @@ def test_upload_kernel_compiles_in_a_batch():
     mods = _modules("lenet_b256.trc")[:3]
     assert _lib.batch_compile_check([(src, "thvm_upload", 256, 3, 1)]) > 0
     assert _lib.batch_compile_check([(src, "thvm_upload", 256, 3, 1)] + mods) > 0
+
+
+def test_weight_pack_kernels_compile_in_a_batch():
+    """The B-operand pack kernel of a contraction (the 3x3 convolutions'
+    weights packed K x N) is held like a generated kernel, so that it goes
+    out in one launch with the independent work before it: its module
+    compiles batched with generated modules."""
+    packs = []
+    for r in trace.read_trace(os.path.join(WL, "convblock_b64.trc")):
+        if r.tag != trace.UOP:
+            continue
+        k = trace.to_uop_kernel(r)
+        if not _lib.dense_analyze(k):
+            continue
+        src = _lib.dense_source(k)
+        m = re.search(r'void (thvm_gemm_[0-9a-f]+_pack)\(', src)
+        if m and all(m.group(1) != p[1] for p in packs):
+            packs.append((src, m.group(1), 256, 144, 1))
+    assert packs
+    mods = _modules("convblock_b64.trc")[:2]
+    assert _lib.batch_compile_check(packs + mods) > 0

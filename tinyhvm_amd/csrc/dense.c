@@ -1557,7 +1557,7 @@ typedef struct {
     hipFunction_t fn, fn_sum, fn_pack;
     GemmPlan plan;
     u32 M, N;
-    CoForm co, co_sum;            /* co-launch forms of the main and split-K sum kernels */
+    CoForm co, co_sum, co_pack;   /* co-launch forms of the main, split-K sum and pack kernels */
     u32 serial;                   /* unique in the process (entries move when the table grows) */
     UOpKernel *kcopy;             /* the program, kept when its launch can take a fused epilogue */
     u32 cap;                      /* workgroups of the main kernel the GPU holds at once */
@@ -2233,6 +2233,7 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
                 free(src);
                 return 0;
             }
+            co_form_make(&e->co_pack, src, nm, 256, e->fn_pack);
         }
         if (e->plan.splits > 1) {
             char nm[64];
@@ -2298,7 +2299,17 @@ int dense_try_dispatch(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, const UO
         for (u32 b = 0; b < 2 * nb; b++) pp[b] = params[b];
         pp[2 * nb] = &pk;
         const u64 kn = e->plan.kp.maxidx[1] + 1;
-        if (!hipb_launch_grid(e->fn_pack, (u32)((kn + 255) / 256), 1, 256, pp)) return 0;
+        /* held: it goes out in one launch with the independent work held
+         * before it (the forward convolution's pack with the padding of its
+         * input), and the main kernel's launch below issues it first */
+        HbMem hp;
+        hp.n = 0;
+        hbm_add(&hp, pk, kn * sizeof(float), 1);
+        for (u32 i = 0; i < n_leaves && i < FUSE_MAX_LEAVES; i++)
+            hbm_add(&hp, pool_ptr(leaf_bufs[i]), pool_bytes(leaf_bufs[i]), 0);
+        if (!hipb_hold(&e->co_pack, e->fn_pack, (u32)((kn + 255) / 256), 1, pp, &hp, 0, -1, 0) &&
+            !hipb_launch_grid(e->fn_pack, (u32)((kn + 255) / 256), 1, 256, pp))
+            return 0;
     }
     /* held for a batch with the next independent dispatches (the split-K sum
      * then joins them, its main kernel going out first) */
@@ -2361,6 +2372,7 @@ void dense_shutdown(void) {
             if (D.tab[i].is_dense) HIPB_CHECK(hipModuleUnload(D.tab[i].mod));
             co_form_free(&D.tab[i].co);
             co_form_free(&D.tab[i].co_sum);
+            co_form_free(&D.tab[i].co_pack);
             free(D.tab[i].kcopy);
             free(D.tab[i].ops);
         }
