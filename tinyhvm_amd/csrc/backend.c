@@ -1345,7 +1345,16 @@ static void hb_dispatch_uop_kernel(u32 out_buf, const u32 *leaf_bufs, u32 n_leav
     (void)cache_key;
     const u64 t0 = hipb_hp_now();
     if (k && leaf_bufs) k = hb_dedup_slots(k, leaf_bufs, n_leaves);
+    /* the dispatched program's signature is computed once for the dispatch
+     * (the lookups of every path ask for it); programs built during the
+     * dispatch (merged, fused, copies) live elsewhere and are hashed anew */
+    const UOpKernel *sk = hipb.sig_k;
+    const u64 sh = hipb.sig_h;
+    hipb.sig_k = k;
+    hipb.sig_h = 0;
     hb_dispatch_uop_kernel_(out_buf, leaf_bufs, n_leaves, k);
+    hipb.sig_k = sk;
+    hipb.sig_h = sh;
     hipb_hp_add(HP_DISPATCH, t0);
 }
 

@@ -92,6 +92,8 @@ typedef struct {
     void *noalloc_scratch;   /* device address of the static workspace (noalloc.hip), or NULL */
     int noalloc;             /* a no-allocation dispatch is running: workspaces come from it */
     void *time_ev[2];        /* events to record around the next contraction's main kernel, or NULL */
+    const UOpKernel *sig_k;  /* the program being dispatched, and its signature once computed (0: not yet) */
+    u64 sig_h;
     int time_fired;          /* they were recorded */
     u64 noalloc_off;         /* bytes of the static workspace handed out in that dispatch */
     int noalloc_err;         /* why that dispatch could not run (THVM_HIP_E*), or 0 */

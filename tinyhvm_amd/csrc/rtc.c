@@ -42,9 +42,11 @@ static u64 mix(u64 h, u64 v) {
 static u64 uop_signature_(const UOpKernel *k);
 
 u64 uop_signature(const UOpKernel *k) {
+    if (k && k == hipb.sig_k && hipb.sig_h) return hipb.sig_h;
     const u64 t0 = hipb_hp_now();
     const u64 h = uop_signature_(k);
     hipb_hp_add(HP_SIGNATURE, t0);
+    if (k && k == hipb.sig_k) hipb.sig_h = h;
     return h;
 }
 
