@@ -140,7 +140,7 @@ int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32
                                           const UOpKernel *kernel);
 
 /* Counters, for tests and the engine-driven timing (no counterpart in the
- * reference): out[0..14] = dispatches, matrix-core dispatches, compiled
+ * reference): out[0..15] = dispatches, matrix-core dispatches, compiled
  * programs, program cache hits, dispatches run on the KOp interpreter
  * (programs the generator or hipRTC refused; their outputs are still
  * written), host waits on the stream, live device bytes, hipMalloc calls,
@@ -149,8 +149,9 @@ int  thvm_hip_dispatch_uop_kernel_noalloc(u32 out_buf, const u32 *leaf_bufs, u32
  * inside a batched launch, elementwise dispatches run as the fused epilogue
  * of the contraction whose output they read, host waits after which a
  * single-pass combine was found to have given up waiting for a partial sum,
- * host uploads copied by an upload kernel held with other launches.
- * Returns the number of counters (15). */
+ * host uploads copied by an upload kernel held with other launches,
+ * dispatches issued as steps of a sequence kernel (dependent small launches
+ * run in order by one workgroup). Returns the number of counters (16). */
 int  thvm_hip_counters(u64 *out, u32 n);
 /* Wait for all enqueued work; returns 0, or -1 on a device error or when a
  * kernel that combines its workgroups' partial sums in one pass gave up
@@ -272,6 +273,13 @@ int  thvm_hip_upload_source(char *buf, u64 buflen);
  * function forms that batched launches compile. */
 int  thvm_hip_batch_compile_check(const char *const *srcs, const char *const *names, const u32 *threads,
                                   const u32 *grid, u32 n, char *errbuf, u64 errlen);
+/* The same for the sequence kernel of dependent small launches (the programs
+ * run in order by one 256-lane workgroup); -1 also when a program cannot be
+ * a step of a sequence (more than 4 workgroups, more than 256 lanes, or
+ * workgroup barriers or LDS of its own). A diagnostic with no counterpart in
+ * the reference. */
+int  thvm_hip_seq_compile_check(const char *const *srcs, const char *const *names, const u32 *threads,
+                                const u32 *grid, u32 n, char *errbuf, u64 errlen);
 
 #ifdef __cplusplus
 }

@@ -114,3 +114,44 @@ def test_weight_pack_kernels_compile_in_a_batch():
     assert packs
     mods = _modules("convblock_b64.trc")[:2]
     assert _lib.batch_compile_check(packs + mods) > 0
+
+
+def _region(name, mark, lo, hi):
+    """(source, main kernel, lanes, gx, gy) of dispatches lo..hi-1 after mark
+    (the generated and window-max programs; grids as the backend launches them)"""
+    recs = trace.read_trace(os.path.join(WL, name))
+    start = next(i for i, r in enumerate(recs) if r.tag == trace.MARK and r.f["text"] == mark)
+    out, n = [], 0
+    for r in recs[start:]:
+        if r.tag != trace.UOP:
+            continue
+        if lo <= n < hi:
+            k = trace.to_uop_kernel(r)
+            assert not _lib.dense_analyze(k)
+            src = _lib.window_source(k) if _lib.window_analyze(k) else _lib.kernel_source(k)[0]
+            mains = [(int(t), nm) for t, nm in MAIN.findall(src) if not nm.endswith(("_sum", "_fin", "_pack"))]
+            out.append((src, mains[0][1], mains[0][0], 1, 1))
+        n += 1
+        if n >= hi:
+            break
+    return out
+
+
+@pytest.mark.parametrize("name,mark,parts", [
+    ("lenet_b256.trc", "lenet.step", [(13, 16), (17, 23)]),
+    ("mlp_64x784x128x10.trc", "mlp.fwd", [(4, 7), (8, 14)]),
+])
+def test_softmax_steps_compile_as_sequences(name, mark, parts):
+    """The softmax cross-entropy and its gradient on [batch, 10] are tiny
+    dependent programs: the backend holds them as steps of a sequence and
+    issues each run of them as one launch of a sequence kernel (one
+    workgroup runs the programs in order, a barrier after each). The runs
+    around the one group reduction (64 lanes with workgroup barriers, which
+    cannot be a step) compile as sequence kernels."""
+    for lo, hi in parts:
+        items = _region(name, mark, lo, hi)
+        assert len(items) == hi - lo
+        assert _lib.seq_compile_check(items) > 0, [it[1] for it in items]
+    red = _region(name, mark, parts[0][1], parts[0][1] + 1)
+    with pytest.raises(ValueError, match="cannot be a step"):
+        _lib.seq_compile_check(red)

@@ -41,11 +41,12 @@ SKIP_READS = 1
 KNOBS = ("THVM_HIP_NO_BATCH", "THVM_HIP_NO_FUSE")
 
 # name -> trace, first mark of the step, mark after it (None: the trace's end),
-# least dispatches batched and fused in the shipped mode
+# least dispatches batched, fused and issued as sequence steps (the softmax
+# and its gradient: two runs of dependent small programs) in the shipped mode
 STEPS = {
-    "lenet": ("lenet_b256.trc", "lenet.step", "lenet.end", 20, 5),
-    "mlp": ("mlp_64x784x128x10.trc", "mlp.fwd", None, 2, 3),
-    "convblock": ("convblock_b64.trc", "conv.fwd", None, 2, 4),
+    "lenet": ("lenet_b256.trc", "lenet.step", "lenet.end", 20, 5, 6),
+    "mlp": ("mlp_64x784x128x10.trc", "mlp.fwd", None, 2, 3, 6),
+    "convblock": ("convblock_b64.trc", "conv.fwd", None, 2, 4, 0),
 }
 MODES = {
     "single": {"THVM_HIP_NO_BATCH": "1", "THVM_HIP_NO_FUSE": "1"},
@@ -93,8 +94,8 @@ def _step(name, mode):
             hi = L.thvm_trace_find_mark(t, m1.encode(), lo) if m1 else L.thvm_trace_count(t)
             assert 0 <= lo < hi
             L.thvm_trace_replay(t, be, 0, lo, 0)
-            before = (C.c_uint64 * 14)()
-            after = (C.c_uint64 * 14)()
+            before = (C.c_uint64 * 16)()
+            after = (C.c_uint64 * 16)()
             if mode == "graph":
                 s0 = _live(L, t, sizes)
                 L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)      # compiles every kernel
@@ -105,20 +106,20 @@ def _step(name, mode):
                 g = L.thvm_hip_graph_end()
                 assert g, "the step could not be captured"
                 _restore(L, t, s0)
-                L.thvm_hip_counters(before, 14)
+                L.thvm_hip_counters(before, 16)
                 assert L.thvm_hip_graph_launch(g) == 0
             else:
-                L.thvm_hip_counters(before, 14)
+                L.thvm_hip_counters(before, 16)
                 L.thvm_trace_replay(t, be, lo, hi, SKIP_READS)
             assert L.thvm_hip_synchronize() == 0
-            assert L.thvm_hip_counters(after, 14) >= 13
+            assert L.thvm_hip_counters(after, 16) >= 16
             out = _live(L, t, sizes)
         finally:
             if g:
                 L.thvm_hip_graph_destroy(g)
             L.thvm_trace_release(t, be)
             L.thvm_trace_free(t)
-        return out, after[11] - before[11], after[12] - before[12]
+        return out, after[11] - before[11], after[12] - before[12], after[15] - before[15]
     finally:
         L.thvm_hip_shutdown()
         for k in KNOBS:
@@ -134,17 +135,19 @@ _single = {}
 @pytest.mark.parametrize("name", list(STEPS))
 def test_step_matches_single_launches(name, mode):
     if name not in _single:
-        ref, nb, nf = _step(name, "single")
-        assert nb == 0 and nf == 0
+        ref, nb, nf, ns = _step(name, "single")
+        assert nb == 0 and nf == 0 and ns == 0
         _single[name] = ref
     ref = _single[name]
-    got, n_batched, n_fused = _step(name, mode)
-    print("%s %s: %d buffers, %d dispatches batched, %d fused" % (name, mode, len(got), n_batched, n_fused))
+    got, n_batched, n_fused, n_seq = _step(name, mode)
+    print("%s %s: %d buffers, %d dispatches batched (%d as sequence steps), %d fused" %
+          (name, mode, len(got), n_batched, n_seq, n_fused))
     assert got.keys() == ref.keys()
     bad = sorted(tid for tid in ref if got[tid] != ref[tid])
     assert not bad, "%s, %s mode: buffers %s differ from single launches" % (name, mode, bad)
     if mode == "shipped":
         assert n_batched >= STEPS[name][3], "only %d dispatches were batched" % n_batched
         assert n_fused >= STEPS[name][4], "only %d dispatches were fused" % n_fused
+        assert n_seq >= STEPS[name][5], "only %d dispatches were sequence steps" % n_seq
     if mode == "batched":
         assert n_batched >= STEPS[name][3] and n_fused == 0, (n_batched, n_fused)

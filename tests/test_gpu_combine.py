@@ -78,7 +78,7 @@ def _run(env, fix=None):
                 L.thvm_hip_counters(c0, 14)
                 rcs[i] = L.thvm_hip_synchronize()
                 c1 = (C.c_uint64 * 14)()
-                assert L.thvm_hip_counters(c1, 14) == 15
+                assert L.thvm_hip_counters(c1, 14) == 16
                 gave[i] = c1[13] - c0[13]
                 n = sizes[r.f["out"]]
                 buf = np.zeros(n // 4, dtype=np.float32)

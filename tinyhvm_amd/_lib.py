@@ -80,6 +80,8 @@ def lib():
                                                       u64]),
         "thvm_hip_batch_compile_check": (C.c_int, [C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), PU32, PU32, u32,
                                                    cp, u64]),
+        "thvm_hip_seq_compile_check": (C.c_int, [C.POINTER(C.c_char_p), C.POINTER(C.c_char_p), PU32, PU32, u32,
+                                                 cp, u64]),
         "thvm_hip_group_compile_check": (C.c_int, [C.POINTER(C.POINTER(abi.UOpKernel)), C.POINTER(PU32), u32,
                                                    C.c_int, cp, u64]),
         "thvm_hip_time_contraction": (C.c_int, [vp, vp]),
@@ -123,6 +125,7 @@ EXPORTED = ["hip_backend"] + [
     "thvm_hip_window_analyze", "thvm_hip_window_source", "thvm_hip_window_compile_check",
     "thvm_hip_batch_compile_check", "thvm_hip_flush", "thvm_hip_epilogue_compile_check", "thvm_hip_chain_merge",
     "thvm_hip_group_compile_check", "thvm_hip_group_source", "thvm_hip_upload_source", "thvm_hip_time_contraction",
+    "thvm_hip_seq_compile_check",
     "thvm_trace_load", "thvm_trace_free", "thvm_trace_count", "thvm_trace_tag",
     "thvm_trace_rec_id", "thvm_trace_rec_bytes", "thvm_trace_rec_data", "thvm_trace_rec_kernel",
     "thvm_trace_find_mark", "thvm_trace_replay", "thvm_trace_live_id", "thvm_trace_release",
@@ -158,6 +161,22 @@ def batch_compile_check(items):
     grid = (C.c_uint32 * (2 * n))(*[v for it in items for v in (it[3], it[4])])
     err = C.create_string_buffer(4096)
     r = lib().thvm_hip_batch_compile_check(srcs, names, threads, grid, n, err, len(err))
+    if r < 0:
+        raise ValueError(err.value.decode())
+    return r
+
+
+def seq_compile_check(items):
+    """Compile the sequence kernel of generated modules without a device
+    (items as for batch_compile_check). Returns the code-object size; raises
+    ValueError with the reason."""
+    n = len(items)
+    srcs = (C.c_char_p * n)(*[it[0].encode() for it in items])
+    names = (C.c_char_p * n)(*[it[1].encode() for it in items])
+    threads = (C.c_uint32 * n)(*[it[2] for it in items])
+    grid = (C.c_uint32 * (2 * n))(*[v for it in items for v in (it[3], it[4])])
+    err = C.create_string_buffer(4096)
+    r = lib().thvm_hip_seq_compile_check(srcs, names, threads, grid, n, err, len(err))
     if r < 0:
         raise ValueError(err.value.decode())
     return r

@@ -90,6 +90,23 @@ static void copyq_guard_dispatch(u32 out, const u32 *leaves, u32 n) {
  * static LDS, at most HB_MAX_LDS in all; a batch with a program whose
  * workgroups wait for each other fits on the GPU at once, and each program
  * that combines partials through the combine area has its own slice of it. */
+/* Sequences. Launches of a few workgroups each (the softmax and loss of a
+ * training step: row maxima, exponentials, sums, logarithms on [batch, 10])
+ * that depend on each other are held too: each one that touches memory an
+ * earlier held launch writes (or writes what one reads) starts a new step,
+ * and they go out as one launch of a sequence kernel whose single workgroup
+ * runs every program's workgroups in program order, a workgroup barrier
+ * after each (which also makes the global writes before it visible to the
+ * whole workgroup). Every program's code is its own device function, so the
+ * results are those of separate launches bit for bit; the launches saved
+ * are what a step of tiny dependent kernels pays for. A sequence holds only
+ * programs of at most HB_SEQ_MAX_BLOCKS workgroups of at most 256 lanes,
+ * without workgroup barriers or LDS of their own, none resident or held
+ * alone; if one no longer qualifies when the sequence goes out (a fusion
+ * grew it), the held launches go out one by one in order. */
+#define HB_SEQ_MAX_BLOCKS 4u
+#define HB_SEQ_MAX_VBLOCKS 24u
+#define HB_SEQ_THREADS 256u
 #define HB_MAX 16
 #define HB_MAX_BLOCKS 512
 #define HB_MAX_LDS 65536u
@@ -112,6 +129,8 @@ typedef struct {
     const void *wmax;      /* a window max a run sum over its output may take in (window.c entry; NULL: none) */
     u32 wmax_bufs[2];      /* ... its output and input */
     u64 hid;               /* identifies the held launch while it is held */
+    int seq_start;         /* reads or writes what an earlier held launch touches: starts a new step of
+                              the held sequence */
 } HbEnt;
 static struct {
     HbEnt ent[HB_MAX];
@@ -121,9 +140,12 @@ static struct {
     u32 n;
     u64 comb_used;         /* combine-area words given to the held launches */
     int flushing;
+    int seq;               /* the held launches are a sequence of dependent steps (hb_seq_*) */
     struct { u64 key; hipModule_t mod; hipFunction_t fn; u32 cap; } cache[64];
     u32 ncache;
 } HB;
+
+static int hb_seq_eligible(const HbEnt *h);
 
 static int hb_overlap(u64 a0, u64 a1, u64 b0, u64 b1) { return a0 < b1 && b0 < a1; }
 
@@ -195,6 +217,36 @@ static size_t hb_put_params(char *src, size_t w, size_t cap, const char *params,
 /* Source of the batch kernel `name` for launches ents[0..n) in order, with
  * T lanes per workgroup: each program's module once, and an entry that hands
  * workgroup ranges to their device functions. */
+/* The sequence kernel of n held launches: one workgroup of T lanes runs each
+ * program's workgroups in order, a barrier after each (see Sequences above). */
+static char *hb_seq_source(const HbEnt *ents, u32 n, u32 T, const char *name) {
+    size_t cap = strlen(kgen_prelude()) + 4096;
+    for (u32 i = 0; i < n; i++) cap += strlen(ents[i].co.src) + 4 * strlen(ents[i].co.params) + 512;
+    char *src = malloc(cap);
+    if (!src) return NULL;
+    size_t w = (size_t)snprintf(src, cap, "%s\n", kgen_prelude());
+    for (u32 i = 0; i < n; i++) {
+        int seen = 0;
+        for (u32 j = 0; j < i; j++) seen |= ents[j].co.id == ents[i].co.id;
+        if (!seen) w += (size_t)snprintf(src + w, cap - w, "%s\n", ents[i].co.src);
+    }
+    w += (size_t)snprintf(src + w, cap - w, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", T, name);
+    for (u32 i = 0; i < n; i++) w = hb_put_params(src, w, cap, ents[i].co.params, i, 1, i == 0);
+    w += (size_t)snprintf(src + w, cap - w,
+                          ") {\n  const u32 wv_ = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n  (void)wv_;\n");
+    for (u32 i = 0; i < n; i++) {
+        const HbEnt *h = &ents[i];
+        w += (size_t)snprintf(src + w, cap - w, "  for (u32 b_ = 0; b_ < %uu; b_++) {\n    ", h->gx * h->gy);
+        if (h->co.threads < T) w += (size_t)snprintf(src + w, cap - w, "if (wv_ < %uu) ", h->co.threads / 64u);
+        w += (size_t)snprintf(src + w, cap - w, "co_%u::%s(b_ %% %uu, b_ / %uu, %uu, %uu", h->co.id, h->co.name, h->gx,
+                              h->gx, h->gx, h->gy);
+        w = hb_put_params(src, w, cap, h->co.params, i, 0, 0);
+        w += (size_t)snprintf(src + w, cap - w, ");\n    __syncthreads();\n  }\n");
+    }
+    snprintf(src + w, cap - w, "}\n");
+    return src;
+}
+
 static char *hb_batch_source(const HbEnt *ents, u32 n, u32 T, const char *name) {
     size_t cap = strlen(kgen_prelude()) + 4096;
     for (u32 i = 0; i < n; i++) cap += strlen(ents[i].co.src) + 4 * strlen(ents[i].co.params) + 512;
@@ -226,7 +278,7 @@ static char *hb_batch_source(const HbEnt *ents, u32 n, u32 T, const char *name) 
 
 /* The batch kernel for the held sequence (compiled once per key) and the
  * workgroups of it the GPU holds at once (*cap). */
-static hipFunction_t hb_batch_fn(u64 key, u32 T, u32 *cap) {
+static hipFunction_t hb_batch_fn(u64 key, u32 T, u32 *cap, int seq) {
     *cap = 0;
     for (u32 i = 0; i < HB.ncache; i++)
         if (HB.cache[i].key == key) {
@@ -235,8 +287,8 @@ static hipFunction_t hb_batch_fn(u64 key, u32 T, u32 *cap) {
         }
     if (HB.ncache >= sizeof HB.cache / sizeof HB.cache[0]) return NULL;
     char name[48];
-    snprintf(name, sizeof name, "thvm_batch_%016llx", (unsigned long long)key);
-    char *src = hb_batch_source(HB.ent, HB.n, T, name);
+    snprintf(name, sizeof name, "thvm_%s_%016llx", seq ? "seq" : "batch", (unsigned long long)key);
+    char *src = seq ? hb_seq_source(HB.ent, HB.n, T, name) : hb_batch_source(HB.ent, HB.n, T, name);
     if (!src) return NULL;
     if (hipb.verbose) {
         fprintf(stderr, "tinyhvm-hip: %s (%u lanes):", name, T);
@@ -296,15 +348,69 @@ int thvm_hip_batch_compile_check(const char *const *srcs, const char *const *nam
     return (int)r;
 }
 
+/* Device-free check of the sequence kernel of n generated modules (as for
+ * thvm_hip_batch_compile_check; the programs run in order by one workgroup
+ * of HB_SEQ_THREADS lanes). */
+int thvm_hip_seq_compile_check(const char *const *srcs, const char *const *names, const u32 *threads,
+                               const u32 *grid, u32 n, char *errbuf, u64 errlen) {
+    if (!srcs || !names || !threads || !grid || n == 0 || n > HB_MAX || !errbuf || errlen == 0) return -1;
+    HbEnt *ents = calloc(n, sizeof(HbEnt));
+    if (!ents) return -1;
+    u32 ok = 1;
+    for (u32 i = 0; i < n && ok; i++) {
+        if (!co_form_make(&ents[i].co, srcs[i], names[i], threads[i], NULL)) {
+            snprintf(errbuf, errlen, "no co-launch form for %s", names[i]);
+            ok = 0;
+            break;
+        }
+        ents[i].gx = grid[2 * i];
+        ents[i].gy = grid[2 * i + 1];
+        if (!hb_seq_eligible(&ents[i])) {
+            snprintf(errbuf, errlen, "%s cannot be a step of a sequence", names[i]);
+            ok = 0;
+        }
+    }
+    long r = -1;
+    char *src = ok ? hb_seq_source(ents, n, HB_SEQ_THREADS, "thvm_seq_check") : NULL;
+    if (src) r = rtc_compile_only(src, errbuf, (size_t)errlen);
+    free(src);
+    for (u32 i = 0; i < n; i++) co_form_free(&ents[i].co);
+    free(ents);
+    return (int)r;
+}
+
 /* Issues the held launches: one alone as itself, several as their batch
  * kernel (or one by one if it cannot be built). */
 static void hb_flush(void) {
     if (!HB.n || HB.flushing) return;
     HB.flushing = 1;
+    int seq_ok = HB.seq && HB.n > 1;
+    for (u32 i = 0; i < HB.n && seq_ok; i++) seq_ok = hb_seq_eligible(&HB.ent[i]);
     if (HB.n == 1) {
         void *pv[CO_MAX_PARAMS];
         hb_params(&HB.ent[0], pv);
         hipb_launch(HB.ent[0].fn, HB.ent[0].gx, HB.ent[0].gy, 1, HB.ent[0].co.threads, pv);
+    } else if (HB.seq) {
+        /* dependent steps: the sequence kernel, or each launch alone in order */
+        u64 key = hb_mix(0x73657175656e6365ull, HB_SEQ_THREADS);
+        for (u32 i = 0; i < HB.n; i++)
+            key = hb_mix(hb_mix(hb_mix(key, HB.ent[i].co.id), HB.ent[i].gx), HB.ent[i].gy);
+        u32 cap = 0;
+        hipFunction_t fn = seq_ok ? hb_batch_fn(key, HB_SEQ_THREADS, &cap, 1) : NULL;
+        if (fn) {
+            void *pv[HB_MAX * CO_MAX_PARAMS];
+            u32 np = 0;
+            for (u32 i = 0; i < HB.n; i++) np += hb_params(&HB.ent[i], pv + np);
+            hipb_launch(fn, 1, 1, 1, HB_SEQ_THREADS, pv);
+            hipb.n_batched += HB.n;
+            hipb.n_seq += HB.n;
+        } else {
+            for (u32 i = 0; i < HB.n; i++) {
+                void *pv[CO_MAX_PARAMS];
+                hb_params(&HB.ent[i], pv);
+                hipb_launch(HB.ent[i].fn, HB.ent[i].gx, HB.ent[i].gy, 1, HB.ent[i].co.threads, pv);
+            }
+        }
     } else {
         const u32 T = hb_threads();
         u64 key = hb_mix(0x626174636822ull, T);
@@ -315,7 +421,7 @@ static void hb_flush(void) {
             total += HB.ent[i].gx * HB.ent[i].gy;
             resident |= HB.ent[i].resident;
         }
-        hipFunction_t fn = hb_batch_fn(key, T, &cap);
+        hipFunction_t fn = hb_batch_fn(key, T, &cap, 0);
         /* a program whose workgroups wait for each other goes in a batch only
          * if the batch kernel's whole grid is on the GPU at once, with the
          * batch kernel's own occupancy (its summed LDS, its registers);
@@ -340,6 +446,7 @@ static void hb_flush(void) {
         }
     }
     HB.n = 0;
+    HB.seq = 0;
     HB.comb_used = 0;
     memset(HB.wg_used, 0, sizeof HB.wg_used);
     HB.flushing = 0;
@@ -374,6 +481,33 @@ void hipb_before_copy(const void *dst, u64 bytes) {
             hb_flush();
             return;
         }
+}
+
+/* whether a held launch may be a step of a held sequence */
+static int hb_seq_eligible(const HbEnt *h) {
+    if (hipb.no_seq || h->solo || h->resident || !h->co.src || h->gx * h->gy > HB_SEQ_MAX_BLOCKS ||
+        h->co.threads == 0 || h->co.threads > HB_SEQ_THREADS || h->co.threads % 64u)
+        return 0;
+    /* no workgroup barriers or LDS of its own: then the sequence's barriers
+     * are the only ones, and every wave reaches each of them (a wave whose
+     * lanes leave a program early goes on to the barrier after it) */
+    return !strstr(h->co.src, "__syncthreads") && !strstr(h->co.src, "bsum_n<") &&
+           !strstr(h->co.src, "bmax_n<") && !strstr(h->co.src, "__shared__");
+}
+
+/* whether h may follow the held launches as a new step of a sequence */
+static int hb_seq_join(const HbEnt *h) {
+    if (HB.n == 0 || HB.n >= HB_MAX || !hb_seq_eligible(h)) return 0;
+    u32 vb = h->gx * h->gy, lds = h->co.lds;
+    for (u32 i = 0; i < HB.n; i++) {
+        const HbEnt *o = &HB.ent[i];
+        if (!hb_seq_eligible(o)) return 0;
+        vb += o->gx * o->gy;
+        int seen = o->co.id == h->co.id;
+        for (u32 j = 0; j < i && !seen; j++) seen = HB.ent[j].co.id == o->co.id;
+        if (!seen) lds += o->co.lds;
+    }
+    return vb <= HB_SEQ_MAX_VBLOCKS && lds <= HB_MAX_LDS;
 }
 
 /* why h cannot join the held launches as they are (NULL: it can) */
@@ -457,8 +591,16 @@ static int hb_hold(const CoForm *cf, hipFunction_t fn, u32 gx, u32 gy, void *con
         memcpy(h->args + off, params[j], cf->psz[j]);
         off += cf->psz[j];
     }
+    h->seq_start = 0;
     const char *why = hb_joins(h);
     if (!why && HB.comb_used + comb_words > COMB_SLOTS) why = "combine area";
+    if (!why && HB.seq && !hb_seq_join(h)) why = "sequence";
+    if (why && strcmp(why, "memory") == 0 && comb_param < 0 && hb_seq_join(h)) {
+        /* depends on a held launch: the next step of a held sequence */
+        h->seq_start = 1;
+        HB.seq = 1;
+        why = NULL;
+    }
     if (why) {
         if (hipb.verbose && HB.n)
             fprintf(stderr, "tinyhvm-hip: %s does not join %u held launches: %s\n", cf->name, HB.n, why);
@@ -841,6 +983,7 @@ static int hb_try_epilogue(u32 out_buf, const u32 *leaf_bufs, u32 n_leaves, cons
 
 static void hb_release(void) {
     HB.n = 0;
+    HB.seq = 0;
     for (u32 i = 0; i < HB.ncache; i++) HIPB_CHECK(hipModuleUnload(HB.cache[i].mod));
     HB.ncache = 0;
 }
@@ -969,6 +1112,7 @@ static int hb_init(void) {
     if (hipStreamCreateWithFlags(&hipb.setup_stream, hipStreamNonBlocking) != hipSuccess) return -1;
     hipb.sync_each = env_flag("THVM_HIP_SYNC");
     hipb.no_batch = env_flag("THVM_HIP_NO_BATCH");
+    hipb.no_seq = env_flag("THVM_HIP_NO_SEQ");
     hipb.dump_src = env_flag("THVM_HIP_DUMP");
     hipb.no_dense = env_flag("THVM_HIP_NO_DENSE");
     hipb.no_window = env_flag("THVM_HIP_NO_WINDOW");
@@ -1960,11 +2104,11 @@ int thvm_hip_counters(u64 *out, u32 n) {
     u32 pinned = 0, limbo = 0;
     pool_stats(&live, &cached, &mallocs);
     pool_pin_stats(&pinned, &limbo);
-    u64 v[15] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
+    u64 v[16] = {hipb.n_dispatch, hipb.n_dense, hipb.n_compile, hipb.n_cache_hit, hipb.n_fallback,
                  hipb.n_stream_sync, live, mallocs, pinned, limbo, hipb.n_window, hipb.n_batched, hipb.n_fused,
-                 hipb.n_comb_gaveup, hipb.n_upload_held};
-    for (u32 i = 0; out && i < n && i < 15; i++) out[i] = v[i];
-    return 15;
+                 hipb.n_comb_gaveup, hipb.n_upload_held, hipb.n_seq};
+    for (u32 i = 0; out && i < n && i < 16; i++) out[i] = v[i];
+    return 16;
 }
 
 int thvm_hip_synchronize(void) {

@@ -81,9 +81,11 @@ typedef struct {
     u64 n_fused;             /* elementwise dispatches run as a contraction's fused epilogue */
     u64 n_copy_fused;        /* buffer copies written by the launch of the program that produced them */
     u64 n_upload_held;       /* host uploads copied by a held upload kernel */
+    u64 n_seq;               /* dispatches issued as steps of a sequence kernel */
     int host_profile;        /* THVM_HIP_HOST_PROFILE: host time per category, printed by profile_report */
     u64 hp_ns[HP_N], hp_calls[HP_N];
     int no_batch;            /* THVM_HIP_NO_BATCH: launch every dispatch on its own */
+    int no_seq;              /* THVM_HIP_NO_SEQ: no sequence kernels for dependent small launches */
     u64 n_stream_sync;       /* host waits on the stream (buf_read, synchronize, ...) */
     hipModule_t static_mod;  /* precompiled kernels */
     unsigned long long *comb_slots; /* single-pass combines: partial words (cleared after each use) */
