@@ -137,21 +137,20 @@ def _region(name, mark, lo, hi):
     return out
 
 
-@pytest.mark.parametrize("name,mark,parts", [
-    ("lenet_b256.trc", "lenet.step", [(13, 16), (17, 23)]),
-    ("mlp_64x784x128x10.trc", "mlp.fwd", [(4, 7), (8, 14)]),
+@pytest.mark.parametrize("name,mark,lo,hi", [
+    ("lenet_b256.trc", "lenet.step", 13, 23),
+    ("mlp_64x784x128x10.trc", "mlp.fwd", 4, 14),
 ])
-def test_softmax_steps_compile_as_sequences(name, mark, parts):
+def test_softmax_steps_compile_as_sequences(name, mark, lo, hi):
     """The softmax cross-entropy and its gradient on [batch, 10] are tiny
     dependent programs: the backend holds them as steps of a sequence and
     issues each run of them as one launch of a sequence kernel (one
-    workgroup runs the programs in order, a barrier after each). The runs
-    around the one group reduction (64 lanes with workgroup barriers, which
-    cannot be a step) compile as sequence kernels."""
-    for lo, hi in parts:
-        items = _region(name, mark, lo, hi)
-        assert len(items) == hi - lo
-        assert _lib.seq_compile_check(items) > 0, [it[1] for it in items]
-    red = _region(name, mark, parts[0][1], parts[0][1] + 1)
-    with pytest.raises(ValueError, match="cannot be a step"):
-        _lib.seq_compile_check(red)
+    workgroup runs the programs in order, a barrier after each). The group
+    reduction among them runs one wave per output and reduces in registers
+    (no LDS, no barrier), so the whole run compiles as one sequence."""
+    items = _region(name, mark, lo, hi)
+    assert len(items) == hi - lo
+    reds = [it for it in items if it[1].startswith("thvm_red_")]
+    assert len(reds) == 1 and reds[0][2] == 64
+    assert "__shared__" not in reds[0][0].split(reds[0][1])[1] and "wsum0(" in reds[0][0]
+    assert _lib.seq_compile_check(items) > 0, [it[1] for it in items]

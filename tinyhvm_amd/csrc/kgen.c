@@ -917,6 +917,10 @@ static const char *PRELUDE_BODY =
 "  for (int o = 32; o > 0; o >>= 1) { float y = __shfl_xor(x, o, 64); x = (x > y) ? x : y; }\n"
 "  return x;\n"
 "}\n"
+/* a single-wave workgroup's total, lane 0's value in every lane (the same
+ * bits a block-wide helper returns, without LDS or barriers) */
+"__device__ __forceinline__ float wsum0(float x) { return __shfl(wsum(x), 0, 64); }\n"
+"__device__ __forceinline__ float wmax0(float x) { return __shfl(wmax(x), 0, 64); }\n"
 "__device__ __forceinline__ float bsum(float x, float* red) {\n"
 "  x = wsum(x);\n"
 "  __syncthreads();\n"
@@ -1535,7 +1539,7 @@ static void emit_group_loop(Gen *g, u32 r) {
             else if (g->splits > 1)
                 emit_single_pass(g, t, 1);
             else
-                sb_put(&g->sb, "      f%u = bmax(t_, red_); }\n", t);
+                sb_put(&g->sb, g->block == 64 ? "      f%u = wmax0(t_); }\n" : "      f%u = bmax(t_, red_); }\n", t);
         } else {
             if (V == 4) sb_put(&g->sb, "    { float t_ = (p%u_0 + p%u_1) + (p%u_2 + p%u_3);\n", t, t, t, t);
             else {
@@ -1548,7 +1552,7 @@ static void emit_group_loop(Gen *g, u32 r) {
             else if (g->splits > 1)
                 emit_single_pass(g, t, 0);
             else
-                sb_put(&g->sb, "      f%u = f%u + bsum(t_, red_); }\n", t, t);
+                sb_put(&g->sb, g->block == 64 ? "      f%u = f%u + wsum0(t_); }\n" : "      f%u = f%u + bsum(t_, red_); }\n", t, t);
         }
     }
     sb_put(&g->sb, "  }\n");
@@ -1688,7 +1692,8 @@ int kgen_uop_lanes(const UOpKernel *k, KGenResult *out, u32 *lanes, char *err, s
         }
         sb_put(s, "  if (gid >= %uu) return;\n", total);
         sb_put(s, "  const u32 lane = threadIdx.x;\n");
-        sb_put(s, "  __shared__ float red_[%u];\n", G.block / 64);
+        /* a one-wave workgroup without splits reduces in registers */
+        if (G.block > 64 || G.splits > 1) sb_put(s, "  __shared__ float red_[%u];\n", G.block / 64);
         emit_decls(&G);
         for (u32 i = 0; i < k->n_ops; i++) {
             const KOp *op = &k->ops[i];
