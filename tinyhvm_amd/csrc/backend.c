@@ -95,17 +95,17 @@ static void copyq_guard_dispatch(u32 out, const u32 *leaves, u32 n) {
  * that depend on each other are held too: each one that touches memory an
  * earlier held launch writes (or writes what one reads) starts a new step,
  * and they go out as one launch of a sequence kernel whose single workgroup
- * runs every program's workgroups in program order, a workgroup barrier
- * after each (which also makes the global writes before it visible to the
- * whole workgroup). Every program's code is its own device function, so the
- * results are those of separate launches bit for bit; the launches saved
- * are what a step of tiny dependent kernels pays for. A sequence holds only
- * programs of at most HB_SEQ_MAX_BLOCKS workgroups of at most 256 lanes,
- * without workgroup barriers or LDS of their own, none resident or held
- * alone; if one no longer qualifies when the sequence goes out (a fusion
- * grew it), the held launches go out one by one in order. */
+ * runs the programs in order, each program's workgroups side by side on
+ * their own waves, a workgroup barrier after each program (which also makes
+ * the global writes before it visible to the whole workgroup). Every
+ * program's code is its own device function, so the results are those of
+ * separate launches bit for bit; the launches saved are what a step of tiny
+ * dependent kernels pays for. A sequence holds only programs of at most
+ * HB_SEQ_MAX_BLOCKS workgroups of at most HB_SEQ_THREADS lanes, without
+ * workgroup barriers or LDS of their own, none resident or held alone; if
+ * one no longer qualifies when the sequence goes out (a fusion grew it), the
+ * held launches go out one by one in order. */
 #define HB_SEQ_MAX_BLOCKS 4u
-#define HB_SEQ_MAX_VBLOCKS 24u
 #define HB_SEQ_THREADS 256u
 #define HB_MAX 16
 #define HB_MAX_BLOCKS 512
@@ -217,8 +217,20 @@ static size_t hb_put_params(char *src, size_t w, size_t cap, const char *params,
 /* Source of the batch kernel `name` for launches ents[0..n) in order, with
  * T lanes per workgroup: each program's module once, and an entry that hands
  * workgroup ranges to their device functions. */
-/* The sequence kernel of n held launches: one workgroup of T lanes runs each
- * program's workgroups in order, a barrier after each (see Sequences above). */
+/* Lanes of the sequence kernel of n held launches: the most any one program
+ * takes with all its workgroups side by side (at most 1024). */
+static u32 hb_seq_threads(const HbEnt *ents, u32 n) {
+    u32 T = 64;
+    for (u32 i = 0; i < n; i++) {
+        const u32 t = ents[i].gx * ents[i].gy * ents[i].co.threads;
+        if (t > T) T = t;
+    }
+    return T;
+}
+
+/* The sequence kernel of n held launches: one workgroup of T lanes runs the
+ * programs in order, workgroup b of a program of W waves on waves
+ * [b W, (b + 1) W), a barrier after each program (see Sequences above). */
 static char *hb_seq_source(const HbEnt *ents, u32 n, u32 T, const char *name) {
     size_t cap = strlen(kgen_prelude()) + 4096;
     for (u32 i = 0; i < n; i++) cap += strlen(ents[i].co.src) + 4 * strlen(ents[i].co.params) + 512;
@@ -236,12 +248,15 @@ static char *hb_seq_source(const HbEnt *ents, u32 n, u32 T, const char *name) {
                           ") {\n  const u32 wv_ = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);\n  (void)wv_;\n");
     for (u32 i = 0; i < n; i++) {
         const HbEnt *h = &ents[i];
-        w += (size_t)snprintf(src + w, cap - w, "  for (u32 b_ = 0; b_ < %uu; b_++) {\n    ", h->gx * h->gy);
-        if (h->co.threads < T) w += (size_t)snprintf(src + w, cap - w, "if (wv_ < %uu) ", h->co.threads / 64u);
-        w += (size_t)snprintf(src + w, cap - w, "co_%u::%s(b_ %% %uu, b_ / %uu, %uu, %uu", h->co.id, h->co.name, h->gx,
-                              h->gx, h->gx, h->gy);
+        const u32 W = h->co.threads / 64u, G = h->gx * h->gy;
+        w += (size_t)snprintf(src + w, cap - w, "  ");
+        if (G * W * 64u < T) w += (size_t)snprintf(src + w, cap - w, "if (wv_ < %uu) ", G * W);
+        w += (size_t)snprintf(src + w, cap - w,
+                              "{\n    const u32 b_ = wv_ / %uu;\n    co_%u::%s(b_ %% %uu, b_ / %uu, %uu, %uu, "
+                              "threadIdx.x - b_ * %uu",
+                              W, h->co.id, h->co.name, h->gx, h->gx, h->gx, h->gy, h->co.threads);
         w = hb_put_params(src, w, cap, h->co.params, i, 0, 0);
-        w += (size_t)snprintf(src + w, cap - w, ");\n    __syncthreads();\n  }\n");
+        w += (size_t)snprintf(src + w, cap - w, ");\n  }\n  __syncthreads();\n");
     }
     snprintf(src + w, cap - w, "}\n");
     return src;
@@ -267,8 +282,8 @@ static char *hb_batch_source(const HbEnt *ents, u32 n, u32 T, const char *name) 
         const HbEnt *h = &ents[i];
         w += (size_t)snprintf(src + w, cap - w, "  if (b_ < %uu) {", h->gx * h->gy);
         if (h->co.threads < T) w += (size_t)snprintf(src + w, cap - w, " if (wv_ >= %uu) return;", h->co.threads / 64u);
-        w += (size_t)snprintf(src + w, cap - w, " co_%u::%s(b_ %% %uu, b_ / %uu, %uu, %uu", h->co.id, h->co.name, h->gx,
-                              h->gx, h->gx, h->gy);
+        w += (size_t)snprintf(src + w, cap - w, " co_%u::%s(b_ %% %uu, b_ / %uu, %uu, %uu, threadIdx.x", h->co.id,
+                              h->co.name, h->gx, h->gx, h->gx, h->gy);
         w = hb_put_params(src, w, cap, h->co.params, i, 0, 0);
         w += (size_t)snprintf(src + w, cap - w, "); return; }\n  b_ -= %uu;\n", h->gx * h->gy);
     }
@@ -349,8 +364,8 @@ int thvm_hip_batch_compile_check(const char *const *srcs, const char *const *nam
 }
 
 /* Device-free check of the sequence kernel of n generated modules (as for
- * thvm_hip_batch_compile_check; the programs run in order by one workgroup
- * of HB_SEQ_THREADS lanes). */
+ * thvm_hip_batch_compile_check; the programs run in order by one
+ * workgroup, each program's workgroups side by side). */
 int thvm_hip_seq_compile_check(const char *const *srcs, const char *const *names, const u32 *threads,
                                const u32 *grid, u32 n, char *errbuf, u64 errlen) {
     if (!srcs || !names || !threads || !grid || n == 0 || n > HB_MAX || !errbuf || errlen == 0) return -1;
@@ -371,7 +386,7 @@ int thvm_hip_seq_compile_check(const char *const *srcs, const char *const *names
         }
     }
     long r = -1;
-    char *src = ok ? hb_seq_source(ents, n, HB_SEQ_THREADS, "thvm_seq_check") : NULL;
+    char *src = ok ? hb_seq_source(ents, n, hb_seq_threads(ents, n), "thvm_seq_check") : NULL;
     if (src) r = rtc_compile_only(src, errbuf, (size_t)errlen);
     free(src);
     for (u32 i = 0; i < n; i++) co_form_free(&ents[i].co);
@@ -392,16 +407,17 @@ static void hb_flush(void) {
         hipb_launch(HB.ent[0].fn, HB.ent[0].gx, HB.ent[0].gy, 1, HB.ent[0].co.threads, pv);
     } else if (HB.seq) {
         /* dependent steps: the sequence kernel, or each launch alone in order */
-        u64 key = hb_mix(0x73657175656e6365ull, HB_SEQ_THREADS);
+        const u32 T = hb_seq_threads(HB.ent, HB.n);
+        u64 key = hb_mix(0x73657175656e6365ull, T);
         for (u32 i = 0; i < HB.n; i++)
             key = hb_mix(hb_mix(hb_mix(key, HB.ent[i].co.id), HB.ent[i].gx), HB.ent[i].gy);
         u32 cap = 0;
-        hipFunction_t fn = seq_ok ? hb_batch_fn(key, HB_SEQ_THREADS, &cap, 1) : NULL;
+        hipFunction_t fn = seq_ok ? hb_batch_fn(key, T, &cap, 1) : NULL;
         if (fn) {
             void *pv[HB_MAX * CO_MAX_PARAMS];
             u32 np = 0;
             for (u32 i = 0; i < HB.n; i++) np += hb_params(&HB.ent[i], pv + np);
-            hipb_launch(fn, 1, 1, 1, HB_SEQ_THREADS, pv);
+            hipb_launch(fn, 1, 1, 1, T, pv);
             hipb.n_batched += HB.n;
             hipb.n_seq += HB.n;
         } else {
@@ -498,16 +514,15 @@ static int hb_seq_eligible(const HbEnt *h) {
 /* whether h may follow the held launches as a new step of a sequence */
 static int hb_seq_join(const HbEnt *h) {
     if (HB.n == 0 || HB.n >= HB_MAX || !hb_seq_eligible(h)) return 0;
-    u32 vb = h->gx * h->gy, lds = h->co.lds;
+    u32 lds = h->co.lds;
     for (u32 i = 0; i < HB.n; i++) {
         const HbEnt *o = &HB.ent[i];
         if (!hb_seq_eligible(o)) return 0;
-        vb += o->gx * o->gy;
         int seen = o->co.id == h->co.id;
         for (u32 j = 0; j < i && !seen; j++) seen = HB.ent[j].co.id == o->co.id;
         if (!seen) lds += o->co.lds;
     }
-    return vb <= HB_SEQ_MAX_VBLOCKS && lds <= HB_MAX_LDS;
+    return lds <= HB_MAX_LDS;
 }
 
 /* why h cannot join the held launches as they are (NULL: it can) */

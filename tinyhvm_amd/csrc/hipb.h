@@ -249,7 +249,8 @@ u32 hipb_resident_waves(void);
 /* A generated module as device functions, so that independent dispatches can
  * go out together in one launch of a batch kernel: the module after the
  * shared prelude, inside namespace co_<id>, each kernel a __device__ function
- * taking its block coordinates and grid size (bx_, by_, gx_, gy_) first. */
+ * taking its block coordinates, grid size and lane within its own workgroup
+ * (bx_, by_, gx_, gy_, tx_) first. */
 #define CO_MAX_PARAMS 48
 typedef struct {
     char *src;             /* NULL: the kernel is launched on its own */

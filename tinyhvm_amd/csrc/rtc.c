@@ -318,12 +318,13 @@ int rtc_compile_check(const UOpKernel *k, size_t *code_len, char *err, size_t er
 
 /* Co-launch form of a generated module (see CoForm): the source after the
  * shared prelude inside namespace co_<id>, every `extern "C" __global__`
- * kernel turned into a __device__ function whose block coordinates and grid
- * size are its first arguments (blockIdx.x/.y and gridDim.x/.y read them).
- * The prelude's block-wide helpers, which read blockDim, become their forms
- * with the program's wave count fixed. Modules that use a third grid
- * dimension, blockDim, dynamic LDS or includes keep cf->src NULL and launch
- * on their own. */
+ * kernel turned into a __device__ function whose block coordinates, grid
+ * size and lane are its first arguments (blockIdx.x/.y, gridDim.x/.y and
+ * threadIdx.x read them), so that a caller may run several of its workgroups
+ * side by side in one larger workgroup. The prelude's block-wide helpers,
+ * which read blockDim, become their forms with the program's wave count
+ * fixed. Modules that use a third grid or thread dimension, blockDim,
+ * dynamic LDS or includes keep cf->src NULL and launch on their own. */
 static u32 co_next_id;
 
 static int co_param_sizes(CoForm *cf) {
@@ -351,6 +352,7 @@ int co_form_make(CoForm *cf, const char *src, const char *name, u32 threads, hip
     if (!src || strncmp(src, pre, pl) != 0 || strlen(name) >= sizeof cf->name) return 0;
     const char *body = src + pl;
     if (strstr(body, "blockIdx.z") || strstr(body, "gridDim.z") || strstr(body, "blockDim") ||
+        strstr(body, "threadIdx.y") || strstr(body, "threadIdx.z") ||
         strstr(body, "extern __shared__") || strstr(body, "#include"))
         return 0;
     /* the main kernel's parameter list */
@@ -404,13 +406,17 @@ int co_form_make(CoForm *cf, const char *src, const char *name, u32 threads, hip
             if (strncmp(q, "void ", 5) != 0) { free(o); goto fail; }
             const char *par = strchr(q, '(');
             if (!par) { free(o); goto fail; }
-            w += (size_t)snprintf(o + w, cap - w, "__device__ __forceinline__ %.*su32 bx_, u32 by_, u32 gx_, u32 gy_, ",
+            w += (size_t)snprintf(o + w, cap - w, "__device__ __forceinline__ %.*su32 bx_, u32 by_, u32 gx_, u32 gy_, u32 tx_, ",
                                   (int)(par + 1 - q), q);
             q = par + 1;
         } else if (strncmp(q, "bsum(", 5) == 0 || strncmp(q, "bmax(", 5) == 0) {
             /* the block-wide helpers with the program's own wave count */
             w += (size_t)snprintf(o + w, cap - w, "%.4s_n<%uu>(", q, threads / 64u);
             q += 5;
+        } else if (strncmp(q, "threadIdx.x", 11) == 0) {
+            /* the lane within the program's own workgroup */
+            w += (size_t)snprintf(o + w, cap - w, "tx_");
+            q += 11;
         } else if (strncmp(q, "blockIdx.x", 10) == 0 || strncmp(q, "blockIdx.y", 10) == 0) {
             w += (size_t)snprintf(o + w, cap - w, "b%c_", q[9]);
             q += 10;
