@@ -507,8 +507,7 @@ static int hb_seq_eligible(const HbEnt *h) {
     /* no workgroup barriers or LDS of its own: then the sequence's barriers
      * are the only ones, and every wave reaches each of them (a wave whose
      * lanes leave a program early goes on to the barrier after it) */
-    return !strstr(h->co.src, "__syncthreads") && !strstr(h->co.src, "bsum_n<") &&
-           !strstr(h->co.src, "bmax_n<") && !strstr(h->co.src, "__shared__");
+    return h->co.no_sync;
 }
 
 /* whether h may follow the held launches as a new step of a sequence */

@@ -262,6 +262,7 @@ typedef struct {
     u32 cap_waves;         /* its waves the GPU holds at once (0: not known) */
     u32 np;
     u8 psz[CO_MAX_PARAMS]; /* its parameters' sizes in bytes */
+    u8 no_sync;            /* no workgroup barrier or LDS of its own */
 } CoForm;
 int  co_form_make(CoForm *cf, const char *src, const char *name, u32 threads, hipFunction_t fn);
 void co_form_free(CoForm *cf);

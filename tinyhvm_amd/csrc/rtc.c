@@ -433,6 +433,8 @@ int co_form_make(CoForm *cf, const char *src, const char *name, u32 threads, hip
     cf->src = o;
     snprintf(cf->name, sizeof cf->name, "%s", name);
     cf->threads = threads;
+    cf->no_sync = !strstr(o, "__syncthreads") && !strstr(o, "bsum_n<") && !strstr(o, "bmax_n<") &&
+                  !strstr(o, "__shared__");
     if (fn) {   /* NULL: a device-free check */
         int v = 0;
         if (hipFuncGetAttribute(&v, HIP_FUNC_ATTRIBUTE_SHARED_SIZE_BYTES, fn) != hipSuccess || v < 0) goto fail_src;
