@@ -443,10 +443,14 @@ typedef struct {
 
 static u32 dense_cus(void) { return hipb.n_cu ? hipb.n_cu : 256u; }
 
+/* lanes of an LDS tile's workgroup: one wave per gm x gn position (the
+ * kernels without LDS tiles plan their loaders against GEMM_THREADS) */
+static u32 lds_threads(const TileCfg *cf) { return cf->direct ? GEMM_THREADS : 64u * cf->gm * cf->gn; }
+
 /* workgroup size of a plan's main kernel */
 static u32 dense_threads(const GemmPlan *pl) {
     if (pl->cfg.direct == 4) return 64u * (pl->tail_s ? pl->tail_s : 1u);
-    return pl->cfg.direct == 3 ? GEMM_THREADS : pl->cfg.direct ? 64u * pl->nw : GEMM_THREADS;
+    return pl->cfg.direct == 3 ? GEMM_THREADS : pl->cfg.direct ? 64u * pl->nw : lds_threads(&pl->cfg);
 }
 
 /* wave tile: k-pairs of fragments in flight (a divisor of the K-pair count) */
@@ -485,17 +489,18 @@ static const char *ld_name(u32 dt) {
 /* Loader lane map for one operand: x in [0, BX) along the tile's M or N side,
  * k in [0, BK). k-major operands put 16 consecutive lanes on consecutive k,
  * the others put consecutive lanes on consecutive x (coalesced either way). */
-static void emit_map(DSB *s, int kmajor, u32 bx, u32 bk, const char *xname) {
+static void emit_map(DSB *s, int kmajor, u32 bx, const TileCfg *cf, const char *xname) {
+    const u32 bk = cf->bk, T = lds_threads(cf);
     if (kmajor) {
         if (bk == 16)
-            dsb_put(s, "const u32 kk = tid & 15u, %s = (tid >> 4) + e * 16u;", xname);
+            dsb_put(s, "const u32 kk = tid & 15u, %s = (tid >> 4) + e * %uu;", xname, T / 16u);
         else
-            dsb_put(s, "const u32 kk = (tid & 15u) + (e %% %uu) * 16u, %s = (tid >> 4) + (e / %uu) * 16u;", bk / 16,
-                    xname, bk / 16);
-    } else if (bx >= GEMM_THREADS) {
+            dsb_put(s, "const u32 kk = (tid & 15u) + (e %% %uu) * 16u, %s = (tid >> 4) + (e / %uu) * %uu;", bk / 16,
+                    xname, bk / 16, T / 16u);
+    } else if (bx == T) {
         dsb_put(s, "const u32 %s = tid, kk = e;", xname);
     } else {
-        dsb_put(s, "const u32 %s = tid %% %uu, kk = tid / %uu + e * %uu;", xname, bx, bx, GEMM_THREADS / bx);
+        dsb_put(s, "const u32 %s = tid %% %uu, kk = tid / %uu + e * %uu;", xname, bx, bx, T / bx);
     }
 }
 
@@ -1201,13 +1206,14 @@ static void emit_kbase_fn(DSB *s, const KPerm *kp, int side, const char *name) {
 
 /* Lane map of a 16-byte loader: each lane holds 4 contiguous elements, along
  * k (k-major) or along the tile's rows; e counts the lane's groups of 4. */
-static void emit_map4(DSB *s, int kmajor, u32 bx, u32 bk, const char *xname) {
+static void emit_map4(DSB *s, int kmajor, u32 bx, const TileCfg *cf, const char *xname) {
+    const u32 T = lds_threads(cf);
     if (kmajor) {
-        const u32 g = bk / 4u;
-        dsb_put(s, "const u32 kk = (tid %% %uu) * 4u, %s = tid / %uu + %uu * e;", g, xname, g, GEMM_THREADS / g);
+        const u32 g = cf->bk / 4u;
+        dsb_put(s, "const u32 kk = (tid %% %uu) * 4u, %s = tid / %uu + %uu * e;", g, xname, g, T / g);
     } else {
         const u32 h = bx / 4u;
-        dsb_put(s, "const u32 %s = (tid %% %uu) * 4u, kk = tid / %uu + %uu * e;", xname, h, h, GEMM_THREADS / h);
+        dsb_put(s, "const u32 %s = (tid %% %uu) * 4u, kk = tid / %uu + %uu * e;", xname, h, h, T / h);
     }
 }
 
@@ -1217,7 +1223,7 @@ static void emit_map4(DSB *s, int kmajor, u32 bx, u32 bk, const char *xname) {
 static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl) {
     const TileCfg *cf = &pl->cfg;
     const KPerm *kp = &pl->kp;
-    const u32 EX[2] = {cf->bm * cf->bk / GEMM_THREADS, cf->bn * cf->bk / GEMM_THREADS};
+    const u32 EX[2] = {cf->bm * cf->bk / lds_threads(cf), cf->bn * cf->bk / lds_threads(cf)};
     /* padded inner digit: elements whose inner index i0 + kk reaches E load
      * as 0 from a clamped (in-range) address; lim_ = E - i0 >= 1 because i0
      * is a multiple of the stage depth below Ep */
@@ -1236,7 +1242,7 @@ static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl
             dsb_put(s, "  const u32 o%c = rowb_%c(gid_%c(%s));\n", X, S, side ? 'n' : 'm', side ? "n0" : "m0");
         } else {
             dsb_put(s, "  u32 o%c[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", X, EX[side], EX[side]);
-            emit_map(s, kmaj, bx, cf->bk, xn);
+            emit_map(s, kmaj, bx, cf, xn);
             char kt[48] = "";
             if (!mask) snprintf(kt, sizeof kt, " + kk * %uu", kp->icoef[side]);
             dsb_put(s, "\n    const u32 x = %s + %s;\n"
@@ -1260,7 +1266,7 @@ static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl
                        "    const float* ps = %s + kbase_%c(k0);%s\n"
                        "    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
                     X, rr, EX[side], src, S, lim, EX[side] / 4u);
-            emit_map4(s, kmaj, bx, cf->bk, xn);
+            emit_map4(s, kmaj, bx, cf, xn);
             if (mask) dsb_put(s, "\n      const u32 kv_ = kk < lim_ ? kk : 0u;");
             dsb_put(s, "\n      float4 v = *(const float4*)(ps + %s);\n", off);
             if (mask) {
@@ -1275,7 +1281,7 @@ static void emit_kperm_loaders(DSB *s, const Contraction *ct, const GemmPlan *pl
                    "    const float* ps = %s + kbase_%c(k0);%s\n"
                    "    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
                 X, rr, EX[side], src, S, lim, EX[side]);
-        emit_map(s, kmaj, bx, cf->bk, xn);
+        emit_map(s, kmaj, bx, cf, xn);
         if (mask)
             dsb_put(s, "\n      const u32 kv_ = kk < lim_ ? kk : 0u;\n"
                        "      const float v = ps[%s];\n      r%c[e] = kk < lim_ ? v : 0.0f; }\n  };\n", off, rr);
@@ -1338,7 +1344,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         return s.p;
     }
     const u32 BK = cf->bk;
-    const u32 EA = cf->bm * BK / GEMM_THREADS, EB = cf->bn * BK / GEMM_THREADS;
+    const u32 EA = cf->bm * BK / lds_threads(cf), EB = cf->bn * BK / lds_threads(cf);
     const u32 NB = cf->wm_b * cf->wn_b;
     if (pl->pack) {
         /* B in the reordered k order, row-major K x N (n contiguous) */
@@ -1356,7 +1362,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         emit_store_tail(&s, k, ct, pl);
         return s.p;
     }
-    dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", GEMM_THREADS, pl->name);
+    dsb_put(&s, "extern \"C\" __global__ __launch_bounds__(%u) void %s(", lds_threads(cf), pl->name);
     emit_params(&s, k->n_leaves);
     dsb_put(&s, pl->pack ? ", float* ws, const float* pk%s) {\n" : ", float* ws%s) {\n", g_epi_params ? g_epi_params : "");
     dsb_put(&s,
@@ -1393,18 +1399,18 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
     /* separable operands: per-row index bases, once per tile */
     if (!pl->kp.on && ct->sep[0]) {
         dsb_put(&s, "  u32 bA[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", EA, EA);
-        emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
+        emit_map(&s, ct->p_kmajor, cf->bm, cf, "mm");
         dsb_put(&s, " (void)kk; bA[e] = rowb_p(gid_m(m0 + mm)); }\n");
     }
     if (!pl->kp.on && ct->sep[1]) {
         dsb_put(&s, "  u32 bB[%u];\n  #pragma unroll\n  for (u32 e = 0; e < %uu; e++) { ", EB, EB);
-        emit_map(&s, ct->q_kmajor, cf->bn, cf->bk, "nn");
+        emit_map(&s, ct->q_kmajor, cf->bn, cf, "nn");
         dsb_put(&s, " (void)kk; bB[e] = rowb_q(gid_n(n0 + nn)); }\n");
     }
     if (!pl->kp.on) {
     dsb_put(&s, "  auto loadA = [&](u32 k0, float (&ra)[%u]) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
             EA, EA);
-    emit_map(&s, ct->p_kmajor, cf->bm, cf->bk, "mm");
+    emit_map(&s, ct->p_kmajor, cf->bm, cf, "mm");
     /* operands are evaluated unconditionally (every load is range-checked,
      * so any (m, k) is safe) and masked after: no divergent branches */
     dsb_put(&s, "\n      const u32 m = m0 + mm, k = k0 + kk;\n");
@@ -1427,7 +1433,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
             gk);
     dsb_put(&s, "  auto loadB = [&](u32 k0, float (&rb)[%u]) {\n    #pragma unroll\n    for (u32 e = 0; e < %uu; e++) { ",
             EB, EB);
-    emit_map(&s, ct->q_kmajor, cf->bn, cf->bk, "nn");
+    emit_map(&s, ct->q_kmajor, cf->bn, cf, "nn");
     dsb_put(&s, "\n      const u32 n = n0 + nn, k = k0 + kk;\n");
     if (ct->sep[1]) {
         dsb_put(&s, "      const float v = %s(p%u, c%u, bB[e] + koff_q(k));\n",
@@ -1448,7 +1454,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         if (pl->kp.on && pl->kp.vec[side]) {
             dsb_put(&s, "  auto store%c = [&](u32 buf, const float (&r%c)[%u]) {\n    #pragma unroll\n"
                         "    for (u32 e = 0; e < %uu; e++) { ", X, r, ex, ex / 4u);
-            emit_map4(&s, kmaj, bx, cf->bk, xn);
+            emit_map4(&s, kmaj, bx, cf, xn);
             if (kmaj)
                 dsb_put(&s, "\n      #pragma unroll\n      for (u32 j = 0; j < 4u; j++) %cs[buf][(kk + j) * %s + %s] = r%c[4u * e + j]; }\n  };\n",
                         X, ld, xn, r);
@@ -1460,7 +1466,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
         }
         dsb_put(&s, "  auto store%c = [&](u32 buf, const float (&r%c)[%u]) {\n    #pragma unroll\n"
                     "    for (u32 e = 0; e < %uu; e++) { ", X, r, ex, ex);
-        emit_map(&s, kmaj, bx, cf->bk, xn);
+        emit_map(&s, kmaj, bx, cf, xn);
         dsb_put(&s, " %cs[buf][kk * %s + %s] = r%c[e]; }\n  };\n", X, ld, xn, r);
     }
     dsb_put(&s,
@@ -1808,7 +1814,7 @@ static int plan_kperm(const Contraction *ct, GemmPlan *pl) {
         const u32 nx = s ? ct->nq : ct->np;
         const u32 fdiv = s ? ct->qdiv[nx - 1] : ct->pdiv[nx - 1];
         const Aff *a = &ct->sep_aff[s];
-        const u32 per_lane = (s ? cf->bn : cf->bm) * cf->bk / GEMM_THREADS;
+        const u32 per_lane = (s ? cf->bn : cf->bm) * cf->bk / lds_threads(cf);
         int ok = unit == 1 && other % 4 == 0 && a->cst % 4 == 0 && kp->E % 4 == 0 && per_lane % 4 == 0;
         for (u32 t = 0; t < kp->ndig; t++) ok = ok && kp->ocoef[s][t] % 4 == 0;
         for (u32 t = 0; t < a->n; t++)
@@ -1861,7 +1867,7 @@ static void plan_pack(const Contraction *ct, GemmPlan *pl) {
     KPerm *kp = &pl->kp;
     pl->pack = 0;
     if (!kp->on || hipb.dense_nopack || kp->vec[1] || (pl->cfg.direct && pl->cfg.direct != 4)) return;
-    const u32 per_lane = pl->cfg.bn * pl->cfg.bk / GEMM_THREADS;
+    const u32 per_lane = pl->cfg.bn * pl->cfg.bk / lds_threads(&pl->cfg);
     if ((u64)kp->Kl * ct->N > (4u << 20) || ct->N % 4 != 0 || ct->N % pl->cfg.bn != 0 || per_lane % 4 != 0 ||
         (pl->tiles_m < 64 && !hipb.dense_pack))
         return;
