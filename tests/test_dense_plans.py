@@ -56,6 +56,7 @@ def _plans(name):
             "outer": (int(ro.group(1)), int(ro.group(2))) if ro else None,
             "comb": "comb_pub(sl_" in src,
             "tail": (int(tl.group(2)), int(tl.group(1)), int(tl.group(3))) if tl else None,
+            "prio": "__builtin_amdgcn_s_setprio(1)" in src,
         }
     return out
 
@@ -70,6 +71,9 @@ def test_convolution_plans():
     dw = p[(576, 64, 200704, 112)]
     assert dw["tile"] == (64, 64) and dw["kperm"] and dw["padded"] and dw["two_stage"]
     assert not dw["packed"]
+    # the long-K weight gradient raises a wave's priority over its math; the
+    # forward (wave tile) has no stages to do so
+    assert dw["prio"] and not fwd["prio"]
 
 
 def test_gemm_4096_plans():
@@ -78,7 +82,7 @@ def test_gemm_4096_plans():
     for a, v in p.items():
         assert a[:3] == (4096, 4096, 4096)
         assert v["tile"] == (128, 128) and v["kperm"] and v["vec16"]
-        assert not v["transposed"] and not v["packed"] and not v["two_stage"]
+        assert not v["transposed"] and not v["packed"] and not v["two_stage"] and not v["prio"]
 
 
 def test_lenet_few_channel_convolutions_are_skinny():

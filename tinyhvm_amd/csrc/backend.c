@@ -1044,6 +1044,9 @@ static void read_dense_env(void) {
     e = getenv("THVM_HIP_DIRECT_MIN_CHUNK");
     hipb.direct_min_chunk = e ? (u32)atoi(e) : 0;
     if (hipb.direct_min_chunk > 65536) hipb.direct_min_chunk = 0;
+    e = getenv("THVM_HIP_GEMM_PRIO");
+    hipb.gemm_prio = e ? (u32)atoi(e) : 0;
+    if (hipb.gemm_prio > 2) hipb.gemm_prio = 0;
     e = getenv("THVM_HIP_GEMM_DEPTH");
     hipb.gemm_depth = e ? (u32)atoi(e) : 0;
     if (hipb.gemm_depth > 2) hipb.gemm_depth = 0;

@@ -433,6 +433,8 @@ typedef struct {
     u32 dvec_buf[2];       /* ... from this buffer (p<b>) */
     int comb;              /* direct and outer-product kernels: split-K partials combined in the
                               same launch by the last split's workgroup through the combine words */
+    int prio;              /* LDS tiles: the wave's priority raised over its stage's fragment reads
+                              and MFMAs */
 } GemmPlan;
 
 #define GEMM_THREADS 256
@@ -1482,6 +1484,8 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
      * by two so that each register set is a fixed array. */
     char stage[4096];
     const char *mfma_a = pl->swap ? "b[kk][j]" : "a[kk][i]", *mfma_b = pl->swap ? "a[kk][i]" : "b[kk][j]";
+    const char *prio_on = pl->prio ? "    __builtin_amdgcn_s_setprio(1);\n" : "";
+    const char *prio_off = pl->prio ? "    __builtin_amdgcn_s_setprio(0);\n" : "";
     for (u32 ph = 0; ph < pl->depth; ph++) {
         const u32 ls = pl->depth == 2 ? ph : 0u, ss = pl->depth == 2 ? 1u - ph : 0u;
         snprintf(stage, sizeof stage,
@@ -1493,6 +1497,7 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
                  "    /* the stage's fragments; the compiler interleaves their reads with the\n"
                  "     * MFMAs (measured faster than pinning every read ahead of the math, which\n"
                  "     * costs registers and occupancy: 8-24 %% slower) */\n"
+                 "%s"
                  "    float a[BK / 2u][%u], b[BK / 2u][%u];\n"
                  "    #pragma unroll\n"
                  "    for (u32 kk = 0; kk < BK; kk += 2u) {\n"
@@ -1509,14 +1514,15 @@ static char *gen_gemm_source(const UOpKernel *k, const Contraction *ct_in, const
                  "        #pragma unroll\n"
                  "        for (u32 j = 0; j < %uu; j++)\n"
                  "          acc[i * %uu + j] = __builtin_amdgcn_mfma_f32_32x32x2f32(%s, %s, acc[i * %uu + j], 0, 0, 0);\n"
+                 "%s"
                  "    /* the next stages' global loads stay in flight across the MFMAs: the\n"
                  "     * LDS stores (which need them) may not move above the math */\n"
                  "    __builtin_amdgcn_sched_barrier(0);\n"
                  "    if (st + 1u < nst) { storeA(cur ^ 1u, ra%u); storeB(cur ^ 1u, rb%u); }\n"
                  "    __syncthreads();\n"
                  "    }\n",
-                 pl->depth, pl->depth, ls, pl->depth, ls, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b,
-                 cf->wn_b, mfma_a, mfma_b, cf->wn_b, ss, ss);
+                 pl->depth, pl->depth, ls, pl->depth, ls, prio_on, cf->wm_b, cf->wn_b, cf->wm_b, cf->wn_b, cf->wm_b,
+                 cf->wn_b, cf->wn_b, mfma_a, mfma_b, cf->wn_b, prio_off, ss, ss);
         if (ph == 0) {
             if (pl->depth == 2)
                 dsb_put(&s, "  if (nst > 0u) { loadA(kbeg, ra0); loadB(kbeg, rb0); storeA(0u, ra0); storeB(0u, rb0); }\n"
@@ -2081,6 +2087,10 @@ static void make_plan_cfg(const Contraction *ct, GemmPlan *pl, u64 sig, const Ti
      * convolution and the 128x128 GEMM, whose occupancy it lowers) */
     const int lk = long_k(ct->M, ct->N, ct->K) && !hipb.dense_tile;
     pl->depth = hipb.gemm_depth ? hipb.gemm_depth : ((cfg->bm == 128 && cfg->bn == 64) || lk) ? 2u : 1u;
+    /* a wave's priority raised over its stage's math (the SIMD's other wave
+     * then issues its loads and LDS stores around it): the long-K weight
+     * gradient 162 -> 158 us, the 4096^3 GEMM 4 % slower */
+    pl->prio = hipb.gemm_prio == 1 || (hipb.gemm_prio == 0 && lk);
     if (!pl->cfg.direct && hipb.gemm_bk) pl->cfg.bk = hipb.gemm_bk;
     pl->tiles_m = (ct->M + pl->cfg.bm - 1) / pl->cfg.bm;
     pl->tiles_n = (ct->N + pl->cfg.bn - 1) / pl->cfg.bn;

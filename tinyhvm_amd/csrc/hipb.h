@@ -52,6 +52,9 @@ typedef struct {
     int gemm_pad_k_set;      /* ... when set (else chosen per store layout) */
     u32 gemm_bk;             /* THVM_HIP_GEMM_BK: K per stage of the LDS tiles (0: the tile's own) */
     u32 gemm_depth;          /* THVM_HIP_GEMM_DEPTH: stages of loads in flight, 1 or 2 (0: chosen) */
+    u32 gemm_prio;           /* THVM_HIP_GEMM_PRIO: a wave's priority raised over its stage's math on
+                                the LDS tiles: 0 = chosen (the long-K weight gradients), 1 = on every
+                                tile, 2 = on none */
     u32 direct_waves;        /* THVM_HIP_DIRECT_WAVES: waves per direct-kernel block, 4, 8 or 16 (0: chosen) */
     int dense_nosep;         /* THVM_HIP_DENSE_NOSEP: evaluate every operand through its program */
     int dense_nokperm;       /* THVM_HIP_DENSE_NOKPERM: no K-reordered affine loaders */
